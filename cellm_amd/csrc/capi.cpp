@@ -1,0 +1,552 @@
+// C ABI of libcellm_hip.so (declarations and contracts in include/cellm_hip.h).
+//
+// Host-side structure mirrors MetalOps (crates/cellm-kernels/src/metal.rs:637-1267):
+// a context owns the device, a stream, a name-keyed weight cache and scratch
+// buffers grown on demand (ensure_buf_f32, metal.rs:1247-1253), all behind one
+// mutex; kernels are launched asynchronously, and the sync logits_* wrappers
+// copy x in, launch, and copy y back.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "../../include/cellm_hip.h"
+#include "common.hpp"
+#include "kernels.hpp"
+
+using namespace cellm;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int32_t set_error(int32_t code, const char* fmt, ...)
+{
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int32_t hip_error(hipError_t e, const char* what)
+{
+    if (e == hipErrorOutOfMemory) return set_error(CELLM_HIP_ERR_OUT_OF_MEMORY, "%s: %s", what, hipGetErrorString(e));
+    return set_error(CELLM_HIP_ERR_DEVICE, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define HIP_TRY(expr, what)                     \
+    do {                                        \
+        hipError_t e_ = (expr);                 \
+        if (e_ != hipSuccess) return hip_error(e_, what); \
+    } while (0)
+
+struct DeviceBuffer {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+
+bool valid_dtype(int32_t d) { return d == DT_F32 || d == DT_F16 || d == DT_BF16; }
+size_t dtype_size(int32_t d) { return d == DT_F32 ? 4 : 2; }
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+struct cellm_hip_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::recursive_mutex mu;
+    std::unordered_map<std::string, DeviceBuffer> weights;
+    size_t weight_bytes = 0;
+    DeviceBuffer x_buf, y_buf;
+    std::unordered_map<hipStream_t, DeviceBuffer> workspaces;  // split-K partials, one per stream
+};
+
+namespace {
+
+// Grow `b` to at least `bytes` (contents not preserved).
+int32_t ensure_buffer(DeviceBuffer& b, size_t bytes)
+{
+    if (b.bytes >= bytes) return CELLM_HIP_OK;
+    if (b.ptr) {
+        hipError_t e = hipFree(b.ptr);
+        b.ptr = nullptr;
+        b.bytes = 0;
+        if (e != hipSuccess) return hip_error(e, "hipFree(scratch)");
+    }
+    HIP_TRY(hipMalloc(&b.ptr, bytes), "hipMalloc(scratch)");
+    b.bytes = bytes;
+    return CELLM_HIP_OK;
+}
+
+// RAII: make ctx->device current for the duration of a call, restore after.
+struct DeviceGuard {
+    int prev = -1;
+    bool ok = true;
+    explicit DeviceGuard(int dev)
+    {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (prev != dev) ok = hipSetDevice(dev) == hipSuccess;
+    }
+    ~DeviceGuard()
+    {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+};
+
+hipStream_t pick_stream(cellm_hip_ctx* ctx, void* stream)
+{
+    return stream ? reinterpret_cast<hipStream_t>(stream) : ctx->stream;
+}
+
+int32_t check_ctx(cellm_hip_ctx* ctx)
+{
+    if (!ctx) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null context");
+    return CELLM_HIP_OK;
+}
+
+int32_t check_dims(int64_t m, int64_t n, int64_t k)
+{
+    if (m < 0 || n < 0 || k < 0) return set_error(CELLM_HIP_ERR_INVALID_ARG, "negative dimension m=%lld n=%lld k=%lld",
+                                                  (long long)m, (long long)n, (long long)k);
+    if (m > INT32_MAX || n > INT32_MAX || k > INT32_MAX || m * k > (int64_t)1 << 40 || n * k > (int64_t)1 << 40)
+        return set_error(CELLM_HIP_ERR_INVALID_ARG, "dimension too large m=%lld n=%lld k=%lld", (long long)m,
+                         (long long)n, (long long)k);
+    return CELLM_HIP_OK;
+}
+
+int32_t check_group(int64_t group)
+{
+    if (group < 8 || group > (1 << 20) || (group & (group - 1)) != 0)
+        return set_error(CELLM_HIP_ERR_INVALID_ARG, "group size %lld must be a power of two >= 8", (long long)group);
+    return CELLM_HIP_OK;
+}
+
+// Workspace for split-K on `st`, sized for this call; nullptr if not needed.
+int32_t get_workspace(cellm_hip_ctx* ctx, hipStream_t st, int M, int N, int K, float** out)
+{
+    *out = nullptr;
+    const size_t need = qgemm_workspace_bytes(M, N, K);
+    if (need == 0) return CELLM_HIP_OK;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    DeviceBuffer& b = ctx->workspaces[st];
+    if (b.bytes < need) {
+        // The old buffer may still be read by queued work on this stream.
+        HIP_TRY(hipStreamSynchronize(st), "hipStreamSynchronize(workspace grow)");
+    }
+    int32_t rc = ensure_buffer(b, need);
+    if (rc) return rc;
+    *out = reinterpret_cast<float*>(b.ptr);
+    return CELLM_HIP_OK;
+}
+
+int32_t qgemv_i8_impl(cellm_hip_ctx* ctx, const int8_t* w, const void* scales, int32_t sdt, int64_t n_scales,
+                      const void* x, int32_t xdt, const float* bias, float* y, int64_t m, int64_t n, int64_t k,
+                      hipStream_t st, bool force_gemm)
+{
+    if (int32_t rc = check_dims(m, n, k)) return rc;
+    if (!valid_dtype(sdt) || !valid_dtype(xdt)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "bad dtype");
+    if (m == 0 || n == 0) return CELLM_HIP_OK;
+    if (!w && k > 0) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null weight pointer");
+    if (!scales || !y || (!x && k > 0)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null scale/x/y pointer");
+    if (n_scales < 1) return set_error(CELLM_HIP_ERR_INVALID_ARG, "n_scales must be >= 1");
+    const int per_channel = n_scales >= n ? 1 : 0;
+    const bool gemm_ok = xdt == DT_F16 && k > 0 && (k % 64) == 0 && aligned16(w) && aligned16(x);
+    if ((force_gemm || m > 4) && gemm_ok) {
+        float* ws = nullptr;
+        if (int32_t rc = get_workspace(ctx, st, (int)m, (int)n, (int)k, &ws)) return rc;
+        HIP_TRY(launch_qgemm_i8_ws(w, scales, sdt, per_channel, reinterpret_cast<const _Float16*>(x), bias, y, (int)m,
+                                   (int)n, (int)k, ws, st),
+                "qgemm_i8 launch");
+        return CELLM_HIP_OK;
+    }
+    if (force_gemm) return set_error(CELLM_HIP_ERR_UNSUPPORTED, "qgemm_i8 needs f16 x, k %% 64 == 0, 16-byte alignment");
+    HIP_TRY(launch_qgemv_i8(w, scales, sdt, per_channel, x, xdt, bias, y, (int)m, (int)n, (int)k, st, k == 0),
+            "qgemv_i8 launch");
+    return CELLM_HIP_OK;
+}
+
+int32_t qgemv_q4_impl(cellm_hip_ctx* ctx, const uint32_t* wq, const void* scales, const void* biases, int32_t sbt,
+                      int64_t group, const void* x, int32_t xdt, float* y, int64_t m, int64_t n, int64_t k,
+                      hipStream_t st, bool force_gemm)
+{
+    if (int32_t rc = check_dims(m, n, k)) return rc;
+    if (int32_t rc = check_group(group)) return rc;
+    if (!valid_dtype(sbt) || !valid_dtype(xdt)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "bad dtype");
+    if (k % 8 != 0) return set_error(CELLM_HIP_ERR_INVALID_ARG, "k=%lld must be a multiple of 8 (u32 nibble words)",
+                                     (long long)k);
+    if (m == 0 || n == 0) return CELLM_HIP_OK;
+    if (k > 0 && (!wq || !scales || !biases || !x)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null input pointer");
+    if (!y) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null output pointer");
+    const bool gemm_ok = xdt == DT_F16 && k > 0 && (k % 64) == 0 && group >= 32 && aligned16(wq) && aligned16(x);
+    if ((force_gemm || m > 4) && gemm_ok) {
+        float* ws = nullptr;
+        if (int32_t rc = get_workspace(ctx, st, (int)m, (int)n, (int)k, &ws)) return rc;
+        HIP_TRY(launch_qgemm_q4_affine_ws(wq, scales, biases, sbt, (int)group, reinterpret_cast<const _Float16*>(x), y,
+                                          (int)m, (int)n, (int)k, ws, st),
+                "qgemm_q4_affine launch");
+        return CELLM_HIP_OK;
+    }
+    if (force_gemm)
+        return set_error(CELLM_HIP_ERR_UNSUPPORTED, "qgemm_q4_affine needs f16 x, k %% 64 == 0, group >= 32, alignment");
+    HIP_TRY(launch_qgemv_q4_affine(wq, scales, biases, sbt, (int)group, x, xdt, y, (int)m, (int)n, (int)k, st, k == 0),
+            "qgemv_q4_affine launch");
+    return CELLM_HIP_OK;
+}
+
+int32_t upload_locked(cellm_hip_ctx* ctx, const std::string& key, const void* host, size_t nbytes, const void** out)
+{
+    auto it = ctx->weights.find(key);
+    if (it != ctx->weights.end()) {
+        if (it->second.bytes != nbytes)
+            return set_error(CELLM_HIP_ERR_INVALID_ARG, "weight '%s' cached with %zu bytes, upload has %zu",
+                             key.c_str(), it->second.bytes, nbytes);
+        *out = it->second.ptr;
+        return CELLM_HIP_OK;
+    }
+    if (!host && nbytes) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null host pointer for '%s'", key.c_str());
+    DeviceBuffer b;
+    HIP_TRY(hipMalloc(&b.ptr, nbytes ? nbytes : 1), "hipMalloc(weight)");
+    b.bytes = nbytes;
+    if (nbytes) {
+        hipError_t e = hipMemcpyAsync(b.ptr, host, nbytes, hipMemcpyHostToDevice, ctx->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) {
+            (void)hipFree(b.ptr);
+            return hip_error(e, "upload weight");
+        }
+    }
+    ctx->weights.emplace(key, b);
+    ctx->weight_bytes += nbytes;
+    *out = b.ptr;
+    return CELLM_HIP_OK;
+}
+
+// Shared tail of the logits_* wrappers: x (f32 host) in, launch, y (f32 host) out.
+template <typename Launch>
+int32_t run_logits(cellm_hip_ctx* ctx, const float* x, size_t cols, size_t rows, float* out, Launch&& launch)
+{
+    if (int32_t rc = ensure_buffer(ctx->x_buf, (cols ? cols : 1) * sizeof(float))) return rc;
+    if (int32_t rc = ensure_buffer(ctx->y_buf, (rows ? rows : 1) * sizeof(float))) return rc;
+    if (cols) HIP_TRY(hipMemcpyAsync(ctx->x_buf.ptr, x, cols * sizeof(float), hipMemcpyHostToDevice, ctx->stream), "copy x");
+    if (int32_t rc = launch(reinterpret_cast<const float*>(ctx->x_buf.ptr), reinterpret_cast<float*>(ctx->y_buf.ptr)))
+        return rc;
+    if (rows)
+        HIP_TRY(hipMemcpyAsync(out, ctx->y_buf.ptr, rows * sizeof(float), hipMemcpyDeviceToHost, ctx->stream), "copy y");
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize(logits)");
+    return CELLM_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t cellm_hip_last_error_message(char* buf, size_t buf_len)
+{
+    const size_t n = g_last_error.size();
+    if (buf && buf_len) {
+        const size_t c = n < buf_len - 1 ? n : buf_len - 1;
+        memcpy(buf, g_last_error.data(), c);
+        buf[c] = '\0';
+    }
+    return n;
+}
+
+int32_t cellm_hip_device_count(int32_t* out_count)
+{
+    if (!out_count) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null out_count");
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e == hipErrorNoDevice) n = 0;
+    else if (e != hipSuccess) return hip_error(e, "hipGetDeviceCount");
+    *out_count = n;
+    return CELLM_HIP_OK;
+}
+
+int32_t cellm_hip_smoke_test(int32_t device)
+{
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count == 0) return set_error(CELLM_HIP_ERR_DEVICE, "no HIP device available");
+    if (device < 0 || device >= count) return set_error(CELLM_HIP_ERR_INVALID_ARG, "device %d out of range", device);
+    DeviceGuard g(device);
+    if (!g.ok) return set_error(CELLM_HIP_ERR_DEVICE, "hipSetDevice(%d) failed", device);
+    const int n = 1024;
+    std::vector<float> a(n), b(n), c(n, 0.0f);
+    for (int i = 0; i < n; ++i) {
+        a[i] = (float)i;
+        b[i] = (float)(2 * i);
+    }
+    float *da = nullptr, *db = nullptr, *dc = nullptr;
+    int32_t rc = CELLM_HIP_OK;
+    if (hipMalloc(&da, n * 4) != hipSuccess || hipMalloc(&db, n * 4) != hipSuccess || hipMalloc(&dc, n * 4) != hipSuccess) {
+        rc = set_error(CELLM_HIP_ERR_OUT_OF_MEMORY, "smoke test allocation failed");
+    } else if (hipMemcpy(da, a.data(), n * 4, hipMemcpyHostToDevice) != hipSuccess ||
+               hipMemcpy(db, b.data(), n * 4, hipMemcpyHostToDevice) != hipSuccess ||
+               launch_add_f32(da, db, dc, n, nullptr) != hipSuccess ||
+               hipMemcpy(c.data(), dc, n * 4, hipMemcpyDeviceToHost) != hipSuccess) {
+        rc = set_error(CELLM_HIP_ERR_DEVICE, "smoke test kernel failed");
+    } else {
+        for (int i = 0; i < n; ++i)
+            if (c[i] != (float)(3 * i)) {
+                rc = set_error(CELLM_HIP_ERR_DEVICE, "smoke test mismatch at %d: %f", i, c[i]);
+                break;
+            }
+    }
+    if (da) (void)hipFree(da);
+    if (db) (void)hipFree(db);
+    if (dc) (void)hipFree(dc);
+    return rc;
+}
+
+int32_t cellm_hip_create(int32_t device, cellm_hip_ctx_t** out_ctx)
+{
+    if (!out_ctx) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null out_ctx");
+    *out_ctx = nullptr;
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || count == 0) return set_error(CELLM_HIP_ERR_DEVICE, "no HIP device available");
+    if (device < 0 || device >= count) return set_error(CELLM_HIP_ERR_INVALID_ARG, "device %d out of range", device);
+    DeviceGuard g(device);
+    if (!g.ok) return set_error(CELLM_HIP_ERR_DEVICE, "hipSetDevice(%d) failed", device);
+    auto* ctx = new (std::nothrow) cellm_hip_ctx();
+    if (!ctx) return set_error(CELLM_HIP_ERR_OUT_OF_MEMORY, "context allocation failed");
+    ctx->device = device;
+    e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete ctx;
+        return hip_error(e, "hipStreamCreate");
+    }
+    *out_ctx = ctx;
+    return CELLM_HIP_OK;
+}
+
+void cellm_hip_destroy(cellm_hip_ctx_t* ctx)
+{
+    if (!ctx) return;
+    DeviceGuard g(ctx->device);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    for (auto& kv : ctx->workspaces) {
+        (void)hipStreamSynchronize(kv.first);
+        if (kv.second.ptr) (void)hipFree(kv.second.ptr);
+    }
+    for (auto& kv : ctx->weights)
+        if (kv.second.ptr) (void)hipFree(kv.second.ptr);
+    if (ctx->x_buf.ptr) (void)hipFree(ctx->x_buf.ptr);
+    if (ctx->y_buf.ptr) (void)hipFree(ctx->y_buf.ptr);
+    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+}
+
+int32_t cellm_hip_synchronize(cellm_hip_ctx_t* ctx)
+{
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    DeviceGuard g(ctx->device);
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    return CELLM_HIP_OK;
+}
+
+int32_t cellm_hip_get_stream(cellm_hip_ctx_t* ctx, void** out_stream)
+{
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    if (!out_stream) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null out_stream");
+    *out_stream = reinterpret_cast<void*>(ctx->stream);
+    return CELLM_HIP_OK;
+}
+
+int32_t cellm_hip_weight_upload(cellm_hip_ctx_t* ctx, const char* key, const void* host, size_t nbytes,
+                                const void** out_dev)
+{
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    if (!key || !out_dev) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null key or out_dev");
+    DeviceGuard g(ctx->device);
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    return upload_locked(ctx, key, host, nbytes, out_dev);
+}
+
+int32_t cellm_hip_weight_lookup(cellm_hip_ctx_t* ctx, const char* key, const void** out_dev, size_t* out_nbytes)
+{
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    if (!key) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null key");
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    auto it = ctx->weights.find(key);
+    if (it == ctx->weights.end()) return set_error(CELLM_HIP_ERR_NOT_FOUND, "weight '%s' not cached", key);
+    if (out_dev) *out_dev = it->second.ptr;
+    if (out_nbytes) *out_nbytes = it->second.bytes;
+    return CELLM_HIP_OK;
+}
+
+int32_t cellm_hip_weight_evict(cellm_hip_ctx_t* ctx, const char* key)
+{
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    if (!key) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null key");
+    DeviceGuard g(ctx->device);
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    auto it = ctx->weights.find(key);
+    if (it == ctx->weights.end()) return set_error(CELLM_HIP_ERR_NOT_FOUND, "weight '%s' not cached", key);
+    // queued kernels on any stream may still read it
+    HIP_TRY(hipDeviceSynchronize(), "hipDeviceSynchronize(evict)");
+    HIP_TRY(hipFree(it->second.ptr), "hipFree(weight)");
+    ctx->weight_bytes -= it->second.bytes;
+    ctx->weights.erase(it);
+    return CELLM_HIP_OK;
+}
+
+int32_t cellm_hip_weight_cache_stats(cellm_hip_ctx_t* ctx, size_t* out_entries, size_t* out_bytes)
+{
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    if (out_entries) *out_entries = ctx->weights.size();
+    if (out_bytes) *out_bytes = ctx->weight_bytes;
+    return CELLM_HIP_OK;
+}
+
+int32_t cellm_hip_qgemv_i8(cellm_hip_ctx_t* ctx, const int8_t* w, const void* scales, int32_t scale_dtype,
+                           int64_t n_scales, const void* x, int32_t x_dtype, const float* bias, float* y, int64_t m,
+                           int64_t n, int64_t k, void* stream)
+{
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    DeviceGuard g(ctx->device);
+    return qgemv_i8_impl(ctx, w, scales, scale_dtype, n_scales, x, x_dtype, bias, y, m, n, k, pick_stream(ctx, stream),
+                         false);
+}
+
+int32_t cellm_hip_qgemv_q4_affine(cellm_hip_ctx_t* ctx, const uint32_t* wq, const void* scales, const void* biases,
+                                  int32_t sb_dtype, int64_t group, const void* x, int32_t x_dtype, float* y,
+                                  int64_t m, int64_t n, int64_t k, void* stream)
+{
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    DeviceGuard g(ctx->device);
+    return qgemv_q4_impl(ctx, wq, scales, biases, sb_dtype, group, x, x_dtype, y, m, n, k, pick_stream(ctx, stream),
+                         false);
+}
+
+int32_t cellm_hip_qgemv_i4_sym(cellm_hip_ctx_t* ctx, const uint8_t* w, const uint16_t* scales_f16, int64_t n_scales,
+                               int64_t gs, const void* x, int32_t x_dtype, float* y, int64_t m, int64_t n, int64_t k,
+                               void* stream)
+{
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    if (int32_t rc = check_dims(m, n, k)) return rc;
+    if (!valid_dtype(x_dtype)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "bad dtype");
+    if (m == 0 || n == 0) return CELLM_HIP_OK;
+    if (gs < 1) return set_error(CELLM_HIP_ERR_INVALID_ARG, "gs must be >= 1");
+    const int64_t spr = n_scales / n;
+    if (spr < 1) return set_error(CELLM_HIP_ERR_INVALID_ARG, "n_scales=%lld < n=%lld", (long long)n_scales, (long long)n);
+    if (k > 0 && (k - 1) / gs >= spr)
+        return set_error(CELLM_HIP_ERR_INVALID_ARG, "scale index (k-1)/gs=%lld out of range spr=%lld",
+                         (long long)((k - 1) / gs), (long long)spr);
+    if ((k > 0 && (!w || !scales_f16 || !x)) || !y) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null pointer");
+    DeviceGuard g(ctx->device);
+    HIP_TRY(launch_qgemv_i4_sym(w, scales_f16, (int)spr, (int)gs, x, x_dtype, y, (int)m, (int)n, (int)k,
+                                pick_stream(ctx, stream)),
+            "qgemv_i4_sym launch");
+    return CELLM_HIP_OK;
+}
+
+int32_t cellm_hip_qgemm_q4_affine(cellm_hip_ctx_t* ctx, const uint32_t* wq, const void* scales, const void* biases,
+                                  int32_t sb_dtype, int64_t group, const uint16_t* x_f16, float* y, int64_t m,
+                                  int64_t n, int64_t k, void* stream)
+{
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    DeviceGuard g(ctx->device);
+    return qgemv_q4_impl(ctx, wq, scales, biases, sb_dtype, group, x_f16, DT_F16, y, m, n, k, pick_stream(ctx, stream),
+                         true);
+}
+
+int32_t cellm_hip_qgemm_i8(cellm_hip_ctx_t* ctx, const int8_t* w, const void* scales, int32_t scale_dtype,
+                           int64_t n_scales, const uint16_t* x_f16, const float* bias, float* y, int64_t m, int64_t n,
+                           int64_t k, void* stream)
+{
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    DeviceGuard g(ctx->device);
+    return qgemv_i8_impl(ctx, w, scales, scale_dtype, n_scales, x_f16, DT_F16, bias, y, m, n, k,
+                         pick_stream(ctx, stream), true);
+}
+
+int32_t cellm_hip_dequant_q4_affine(cellm_hip_ctx_t* ctx, const uint32_t* wq, const void* scales, const void* biases,
+                                    int32_t sb_dtype, int64_t group, void* out, int32_t out_dtype, int64_t n,
+                                    int64_t k, void* stream)
+{
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    if (int32_t rc = check_dims(1, n, k)) return rc;
+    if (int32_t rc = check_group(group)) return rc;
+    if (!valid_dtype(sb_dtype) || (out_dtype != DT_F32 && out_dtype != DT_F16))
+        return set_error(CELLM_HIP_ERR_INVALID_ARG, "bad dtype");
+    if (k % 8 != 0) return set_error(CELLM_HIP_ERR_INVALID_ARG, "k must be a multiple of 8");
+    if (n == 0 || k == 0) return CELLM_HIP_OK;
+    if (!wq || !scales || !biases || !out) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null pointer");
+    if (!aligned16(out)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "output must be 16-byte aligned");
+    DeviceGuard g(ctx->device);
+    HIP_TRY(launch_dequant_q4_affine(wq, scales, biases, sb_dtype, (int)group, out, out_dtype, (int)n, (int)k,
+                                     pick_stream(ctx, stream)),
+            "dequant launch");
+    return CELLM_HIP_OK;
+}
+
+int32_t cellm_hip_logits_i8(cellm_hip_ctx_t* ctx, const float* x, const int8_t* w, const uint16_t* scales_f16,
+                            size_t rows, size_t cols, const char* cache_key, float* out)
+{
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    if (!cache_key || (!x && cols) || (!out && rows)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null argument");
+    DeviceGuard g(ctx->device);
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    const void *dw = nullptr, *ds = nullptr;
+    const std::string key = cache_key;
+    if (int32_t rc = upload_locked(ctx, "logits.w." + key, w, rows * cols, &dw)) return rc;
+    if (int32_t rc = upload_locked(ctx, "logits.s." + key, scales_f16, rows * 2, &ds)) return rc;
+    return run_logits(ctx, x, cols, rows, out, [&](const float* dx, float* dy) {
+        return qgemv_i8_impl(ctx, reinterpret_cast<const int8_t*>(dw), ds, DT_F16, (int64_t)rows, dx, DT_F32, nullptr,
+                             dy, 1, (int64_t)rows, (int64_t)cols, ctx->stream, false);
+    });
+}
+
+int32_t cellm_hip_logits_i4(cellm_hip_ctx_t* ctx, const float* x, const uint8_t* w, const uint16_t* scales_f16,
+                            size_t n_scales, size_t rows, size_t cols, size_t gs, const char* cache_key, float* out)
+{
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    if (!cache_key || (!x && cols) || (!out && rows)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null argument");
+    DeviceGuard g(ctx->device);
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    const void *dw = nullptr, *ds = nullptr;
+    const std::string key = cache_key;
+    if (int32_t rc = upload_locked(ctx, "logits.w." + key, w, rows * ((cols + 1) / 2), &dw)) return rc;
+    if (int32_t rc = upload_locked(ctx, "logits.s." + key, scales_f16, n_scales * 2, &ds)) return rc;
+    return run_logits(ctx, x, cols, rows, out, [&](const float* dx, float* dy) {
+        return cellm_hip_qgemv_i4_sym(ctx, reinterpret_cast<const uint8_t*>(dw), reinterpret_cast<const uint16_t*>(ds),
+                                      (int64_t)n_scales, (int64_t)gs, dx, DT_F32, dy, 1, (int64_t)rows, (int64_t)cols,
+                                      ctx->stream);
+    });
+}
+
+int32_t cellm_hip_logits_q4_affine(cellm_hip_ctx_t* ctx, const float* x, const uint32_t* wq, const void* scales,
+                                   const void* biases, int32_t sb_dtype, size_t rows, size_t cols,
+                                   const char* cache_key, float* out)
+{
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    if (!cache_key || (!x && cols) || (!out && rows)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null argument");
+    if (!valid_dtype(sb_dtype)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "bad dtype");
+    if (cols % 8 != 0) return set_error(CELLM_HIP_ERR_INVALID_ARG, "cols must be a multiple of 8");
+    DeviceGuard g(ctx->device);
+    std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+    const size_t groups = (cols + 63) / 64;
+    const size_t sb_bytes = rows * groups * dtype_size(sb_dtype);
+    const void *dw = nullptr, *ds = nullptr, *db = nullptr;
+    const std::string key = cache_key;
+    if (int32_t rc = upload_locked(ctx, "logits.w." + key, wq, rows * cols / 2, &dw)) return rc;
+    if (int32_t rc = upload_locked(ctx, "logits.s." + key, scales, sb_bytes, &ds)) return rc;
+    if (int32_t rc = upload_locked(ctx, "logits.b." + key, biases, sb_bytes, &db)) return rc;
+    return run_logits(ctx, x, cols, rows, out, [&](const float* dx, float* dy) {
+        return qgemv_q4_impl(ctx, reinterpret_cast<const uint32_t*>(dw), ds, db, sb_dtype, 64, dx, DT_F32, dy, 1,
+                             (int64_t)rows, (int64_t)cols, ctx->stream, false);
+    });
+}
+
+}  // extern "C"

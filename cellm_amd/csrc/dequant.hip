@@ -1,0 +1,142 @@
+// Bit-exact dequantization of MLX 4-bit affine weights, the symmetric-i4 GEMV
+// and the device smoke-test kernel.
+//
+// Dequant semantics:
+//   f32 out: w = f32(q) * s + b, multiply and add rounded separately
+//            (crates/cellm-model/src/lfm.rs:1014-1025)
+//   f16 out: h = RNE_f16(f32(q) * s + b)   (tools/convert/src/main.rs:4430-4436)
+// Contraction into v_fma_f32 would round once instead of twice, so this file
+// turns contraction off for the element formula.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace cellm {
+
+namespace {
+
+constexpr int kBlock = 256;
+
+__device__ __forceinline__ float affine_elem(uint32_t q, float s, float b)
+{
+#pragma clang fp contract(off)
+    const float t = (float)q * s;
+    return t + b;
+}
+
+// One thread per u32 word (8 elements).  Rows have K/8 words; groups of
+// `gsize` elements share a scale/bias; g = min(i/gsize, groups-1).
+template <int SBT, int OUT_F16>
+__global__ __launch_bounds__(kBlock) void dequant_q4_affine_kernel(const uint32_t* __restrict__ wq,
+                                                                   const void* __restrict__ S,
+                                                                   const void* __restrict__ B, void* __restrict__ out,
+                                                                   int N, int K, int gsize)
+{
+    const int P = K >> 3;
+    const size_t total = (size_t)N * P;
+    const int groups = (K + gsize - 1) / gsize;
+    for (size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x; i < total; i += (size_t)gridDim.x * kBlock) {
+        const int n = (int)(i / P);
+        const int p = (int)(i - (size_t)n * P);
+        const uint32_t w = wq[i];
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            int g = (p * 8 + k) / gsize;
+            g = g < groups - 1 ? g : groups - 1;
+            const float s = load_f32<SBT>(S, (size_t)n * groups + g);
+            const float b = load_f32<SBT>(B, (size_t)n * groups + g);
+            v[k] = affine_elem((w >> (4 * k)) & 0xFu, s, b);
+        }
+        if constexpr (OUT_F16) {
+            h8_t h;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) h[k] = (_Float16)v[k];  // v_cvt_f16_f32: round to nearest even
+            reinterpret_cast<h8_t*>(out)[i] = h;
+        } else {
+            float* o = reinterpret_cast<float*>(out) + i * 8;
+            *reinterpret_cast<f4_t*>(o) = f4_t{v[0], v[1], v[2], v[3]};
+            *reinterpret_cast<f4_t*>(o + 4) = f4_t{v[4], v[5], v[6], v[7]};
+        }
+    }
+}
+
+// Symmetric i4, one wave per output row; element formula of
+// cpu_kernels.rs:234-240: w = (nib - 8) * scale[j / gs] (exact in f32).
+template <int XT>
+__global__ __launch_bounds__(kBlock) void qgemv_i4_sym_kernel(const uint8_t* __restrict__ w,
+                                                              const uint16_t* __restrict__ S, int spr, int gs,
+                                                              const void* __restrict__ x, float* __restrict__ y,
+                                                              int M, int N, int K)
+{
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int n = blockIdx.x * (kBlock / 64) + wave;
+    if (n >= N) return;
+    const int row_stride = (K + 1) >> 1;
+    const uint8_t* row = w + (size_t)n * row_stride;
+    const uint16_t* rs = S + (size_t)n * spr;
+    for (int m = 0; m < M; ++m) {
+        float acc = 0.0f;
+        for (int bi = lane; bi < row_stride; bi += 64) {
+            const uint32_t byte = row[bi];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int j = 2 * bi + h;
+                if (j < K) {
+                    const int q = (int)((byte >> (4 * h)) & 0xFu) - 8;
+                    const float s = load_f32<DT_F16>(rs, (size_t)(j / gs));
+                    acc = __builtin_fmaf((float)q * s, load_f32<XT>(x, (size_t)m * K + j), acc);
+                }
+            }
+        }
+        acc = group_sum<64>(acc);
+        if (lane == 0) y[(size_t)m * N + n] = acc;
+    }
+}
+
+__global__ void add_f32_kernel(const float* a, const float* b, float* out, int n)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = a[i] + b[i];
+}
+
+}  // namespace
+
+hipError_t launch_dequant_q4_affine(const uint32_t* wq, const void* S, const void* B, int sbt, int group_size,
+                                    void* out, int out_dt, int N, int K, hipStream_t st)
+{
+    const size_t total = (size_t)N * (size_t)(K >> 3);
+    size_t blocks = (total + kBlock - 1) / kBlock;
+    if (blocks > 65536) blocks = 65536;
+    if (blocks == 0) return hipSuccess;
+    const dim3 grid((unsigned)blocks);
+#define CELLM_DQ(SBT_, F16_)                                                                                    \
+    hipLaunchKernelGGL((dequant_q4_affine_kernel<SBT_, F16_>), grid, dim3(kBlock), 0, st, wq, S, B, out, N, K, \
+                       group_size)
+    const bool f16 = out_dt == DT_F16;
+    if (sbt == DT_F32) { if (f16) CELLM_DQ(DT_F32, 1); else CELLM_DQ(DT_F32, 0); }
+    else if (sbt == DT_F16) { if (f16) CELLM_DQ(DT_F16, 1); else CELLM_DQ(DT_F16, 0); }
+    else { if (f16) CELLM_DQ(DT_BF16, 1); else CELLM_DQ(DT_BF16, 0); }
+#undef CELLM_DQ
+    return hipGetLastError();
+}
+
+hipError_t launch_qgemv_i4_sym(const uint8_t* w, const uint16_t* S, int spr, int gs, const void* x, int xdt, float* y,
+                               int M, int N, int K, hipStream_t st)
+{
+    const dim3 grid((N + 3) / 4);
+    if (xdt == DT_F32)
+        hipLaunchKernelGGL((qgemv_i4_sym_kernel<DT_F32>), grid, dim3(kBlock), 0, st, w, S, spr, gs, x, y, M, N, K);
+    else if (xdt == DT_F16)
+        hipLaunchKernelGGL((qgemv_i4_sym_kernel<DT_F16>), grid, dim3(kBlock), 0, st, w, S, spr, gs, x, y, M, N, K);
+    else
+        hipLaunchKernelGGL((qgemv_i4_sym_kernel<DT_BF16>), grid, dim3(kBlock), 0, st, w, S, spr, gs, x, y, M, N, K);
+    return hipGetLastError();
+}
+
+hipError_t launch_add_f32(const float* a, const float* b, float* out, int n, hipStream_t st)
+{
+    hipLaunchKernelGGL(add_f32_kernel, dim3((n + 255) / 256), dim3(256), 0, st, a, b, out, n);
+    return hipGetLastError();
+}
+
+}  // namespace cellm

@@ -1,0 +1,45 @@
+// Host-side launchers for the cellm HIP kernels.  All pointers are device
+// pointers; all launches are asynchronous on `st`.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace cellm {
+
+// Decode GEMV, int8 weights with one scale per output row (per_channel=1) or
+// one scale for the tensor (per_channel=0).  M <= 4 and K % 16 == 0 take the
+// fast kernels; anything else runs the generic one-wave-per-row kernel.
+hipError_t launch_qgemv_i8(const int8_t* w, const void* S, int sdt, int per_channel, const void* x, int xdt,
+                           const float* bias, float* y, int M, int N, int K, hipStream_t st, int force_generic);
+
+// Decode GEMV, MLX 4-bit affine weights (u32 words, 8 nibbles; scale+bias per group).
+hipError_t launch_qgemv_q4_affine(const uint32_t* wq, const void* S, const void* B, int sbt, int group_size,
+                                  const void* x, int xdt, float* y, int M, int N, int K, hipStream_t st,
+                                  int force_generic);
+int qgemv_q4_lds_bytes(int M, int K);
+
+// Symmetric i4 (u8 bytes, low nibble = even element, (nib-8)*scale).
+hipError_t launch_qgemv_i4_sym(const uint8_t* w, const uint16_t* S, int spr, int gs, const void* x, int xdt, float* y,
+                               int M, int N, int K, hipStream_t st);
+
+// Bit-exact dequant of MLX affine weights: out_dt f32 (lfm.rs order) or f16
+// (converter RNE).
+hipError_t launch_dequant_q4_affine(const uint32_t* wq, const void* S, const void* B, int sbt, int group_size,
+                                    void* out, int out_dt, int N, int K, hipStream_t st);
+
+// Prefill / batched qGEMM on MFMA: Y[M,N] = X[M,K] . dequant(W)[N,K]^T with
+// W tiles dequantized to f16 in LDS and f32 accumulation.  Requires K % 64 == 0
+// and 16-byte aligned W and X.  `workspace` (qgemm_workspace_bytes) enables
+// split-K; nullptr runs without it.
+int qgemm_splits(int M, int N, int K);
+size_t qgemm_workspace_bytes(int M, int N, int K);
+hipError_t launch_qgemm_q4_affine_ws(const uint32_t* wq, const void* S, const void* B, int sbt, int group_size,
+                                     const _Float16* x, float* y, int M, int N, int K, float* workspace,
+                                     hipStream_t st);
+hipError_t launch_qgemm_i8_ws(const int8_t* w, const void* S, int sdt, int per_channel, const _Float16* x,
+                              const float* bias, float* y, int M, int N, int K, float* workspace, hipStream_t st);
+
+// Device smoke test kernel: out[i] = a[i] + b[i].
+hipError_t launch_add_f32(const float* a, const float* b, float* out, int n, hipStream_t st);
+
+}  // namespace cellm

@@ -1,0 +1,274 @@
+// Quantized-weight GEMM on MFMA for prefill and batched decode (gfx950).
+//
+//   Y[M,N] = X[M,K] . dequant(W)[N,K]^T        (f16 X, f32 accumulate, f32 Y)
+//
+// Reference: there is no batched or GEMM path in cellm (prefill runs the GEMV
+// token by token, crates/cellm-model/src/llama.rs:214-233).  The per-element
+// oracle is cpu_kernels::matmul_f32 (cpu_kernels.rs:36-63) over the dequantized
+// weight, summed over k ascending.
+//
+// Weight tiles are dequantized into LDS as f16 with the converter's rounding,
+// h = RNE_f16(f32(q)*s + b) (tools/convert/src/main.rs:4435-4436).  For f16 or
+// bf16 scales, f32(q)*s is exact in f32, so fma(q, s, b) rounds exactly as the
+// reference's mul-then-add does; f32 scales take a separate mul and add.
+// int8 weights are exact in f16; their per-row scale is applied in the epilogue
+// (y = acc * s, cpu_kernels.rs:130).
+//
+// Tiling: 256 threads = 4 waves in a 2x2 grid; block tile 128x128, wave tile
+// 64x64 = 4x4 v_mfma_f32_16x16x32_f16 tiles; BK = 64 per LDS stage.  The next
+// stage's global data is prefetched into registers during the MFMA loop.
+// Split-K over blockIdx.z writes f32 partials to a workspace that a second
+// kernel sums in a fixed order (deterministic).
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace cellm {
+
+namespace {
+
+constexpr int BM = 128, BN = 128, BK = 64;
+constexpr int LDS_STRIDE = BK + 8;  // halves; 144-byte rows break LDS bank aliasing
+constexpr int kThreads = 256;
+
+template <int SBT>
+__device__ __forceinline__ h8_t dequant_word_f16(uint32_t w, float s, float b)
+{
+    h8_t h;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const float q = (float)((w >> (4 * k)) & 0xFu);
+        float v;
+        if constexpr (SBT == DT_F32) {
+#pragma clang fp contract(off)
+            const float t = q * s;
+            v = t + b;
+        } else {
+            v = __builtin_fmaf(q, s, b);  // q*s exact: same bits as mul-then-add
+        }
+        h[k] = (_Float16)v;
+    }
+    return h;
+}
+
+__device__ __forceinline__ h8_t int8_to_f16x8(u2_t w)
+{
+    const uint32_t mlo = 0x00FF00FFu, magic = 0x64006400u;
+    const h2_t off = {(_Float16)1152.0f, (_Float16)1152.0f};
+    uint32_t b0 = w[0] ^ 0x80808080u, b1 = w[1] ^ 0x80808080u;
+    // (1152+w0, 1152+w2), (1152+w1, 1152+w3): exact in f16; subtracting 1152 is exact
+    h2_t a0 = as_h2(and_or(b0, mlo, magic)) - off;
+    h2_t a1 = as_h2(and_or(b0 >> 8, mlo, magic)) - off;
+    h2_t a2 = as_h2(and_or(b1, mlo, magic)) - off;
+    h2_t a3 = as_h2(and_or(b1 >> 8, mlo, magic)) - off;
+    h8_t h = {a0[0], a1[0], a0[1], a1[1], a2[0], a3[0], a2[1], a3[1]};
+    return h;
+}
+
+// WT: 0 = q4 affine (u32 words), 1 = int8.
+template <int WT, int SBT>
+__global__ __launch_bounds__(kThreads) void qgemm_kernel(const void* __restrict__ W, const void* __restrict__ S,
+                                                         const void* __restrict__ Bz, int group_size,
+                                                         const _Float16* __restrict__ X, float* __restrict__ Y,
+                                                         int M, int N, int K, int k_per_split, int per_channel)
+{
+    __shared__ __align__(16) _Float16 xs[BM * LDS_STRIDE];
+    __shared__ __align__(16) _Float16 ws[BN * LDS_STRIDE];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int kbeg = blockIdx.z * k_per_split;
+    const int kend = min(K, kbeg + k_per_split);
+
+    // global -> register staging assignment
+    const int ld_row = tid >> 1;        // 0..127
+    const int ld_half = tid & 1;        // which 32-element half of the 64-wide K stage
+    const int xm = m0 + ld_row, wn_row = n0 + ld_row;
+    const int gpr = (K + group_size - 1) / group_size;
+
+    u4_t xr[4];
+    u4_t wr;      // q4: 4 words (32 nibbles); int8: 2 x u2 (32 bytes) -> use wr and wr2
+    u4_t wr2;
+    float sc = 0.0f, bi = 0.0f;
+
+    auto load_stage = [&](int k0) {
+        const int kc = k0 + ld_half * 32;
+        const bool kin = kc < kend;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            xr[i] = (xm < M && kin) ? *reinterpret_cast<const u4_t*>(X + (size_t)xm * K + kc + i * 8)
+                                    : u4_t{0u, 0u, 0u, 0u};
+        }
+        if constexpr (WT == 0) {
+            const u4_t* w4 = reinterpret_cast<const u4_t*>(W);
+            const bool ok = wn_row < N && kin;
+            wr = ok ? __builtin_nontemporal_load(w4 + ((size_t)wn_row * K + kc) / 32) : u4_t{0u, 0u, 0u, 0u};
+            if (ok) {
+                const int g = kc / group_size;
+                sc = load_f32<SBT>(S, (size_t)wn_row * gpr + g);
+                bi = load_f32<SBT>(Bz, (size_t)wn_row * gpr + g);
+            } else {
+                sc = 0.0f;
+                bi = 0.0f;
+            }
+        } else {
+            const u4_t* w4 = reinterpret_cast<const u4_t*>(W);
+            const bool ok = wn_row < N && kin;
+            wr = ok ? __builtin_nontemporal_load(w4 + ((size_t)wn_row * K + kc) / 16) : u4_t{0u, 0u, 0u, 0u};
+            wr2 = ok ? __builtin_nontemporal_load(w4 + ((size_t)wn_row * K + kc) / 16 + 1) : u4_t{0u, 0u, 0u, 0u};
+        }
+    };
+
+    auto store_stage = [&]() {
+        _Float16* xd = xs + ld_row * LDS_STRIDE + ld_half * 32;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) *reinterpret_cast<u4_t*>(xd + i * 8) = xr[i];
+        _Float16* wd = ws + ld_row * LDS_STRIDE + ld_half * 32;
+        if constexpr (WT == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) *reinterpret_cast<h8_t*>(wd + i * 8) = dequant_word_f16<SBT>(wr[i], sc, bi);
+        } else {
+            *reinterpret_cast<h8_t*>(wd + 0) = int8_to_f16x8(u2_t{wr[0], wr[1]});
+            *reinterpret_cast<h8_t*>(wd + 8) = int8_to_f16x8(u2_t{wr[2], wr[3]});
+            *reinterpret_cast<h8_t*>(wd + 16) = int8_to_f16x8(u2_t{wr2[0], wr2[1]});
+            *reinterpret_cast<h8_t*>(wd + 24) = int8_to_f16x8(u2_t{wr2[2], wr2[3]});
+        }
+    };
+
+    f4_t acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f4_t{0.f, 0.f, 0.f, 0.f};
+
+    const int frag_row = lane & 15;
+    const int frag_k = (lane >> 4) * 8;
+
+    load_stage(kbeg);
+    for (int k0 = kbeg; k0 < kend; k0 += BK) {
+        __syncthreads();  // previous stage fully consumed
+        store_stage();
+        __syncthreads();
+        if (k0 + BK < kend) load_stage(k0 + BK);
+#pragma unroll
+        for (int kk = 0; kk < BK; kk += 32) {
+            h8_t a[4], b[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                a[i] = *reinterpret_cast<const h8_t*>(xs + (wm * 64 + i * 16 + frag_row) * LDS_STRIDE + kk + frag_k);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                b[j] = *reinterpret_cast<const h8_t*>(ws + (wn * 64 + j * 16 + frag_row) * LDS_STRIDE + kk + frag_k);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+    }
+
+    // C fragment: lane holds rows 4*(lane/16)+e, column lane%16 of each 16x16 tile.
+    float* out = Y + (size_t)blockIdx.z * M * N;
+    const int crow = (lane >> 4) * 4;
+    const int ccol = lane & 15;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int n = n0 + wn * 64 + j * 16 + ccol;
+        if (n >= N) continue;
+        float s = 1.0f;
+        if constexpr (WT == 1) s = load_f32<SBT>(S, per_channel ? (size_t)n : 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int m = m0 + wm * 64 + i * 16 + crow + e;
+                if (m < M) out[(size_t)m * N + n] = acc[i][j][e] * s;
+            }
+        }
+    }
+}
+
+// Sum split-K partials [splits][M*N] in split order, then add the optional bias.
+__global__ void splitk_reduce_kernel(const float* __restrict__ part, float* __restrict__ y, const float* __restrict__ bias,
+                                     int splits, int M, int N)
+{
+    const size_t total = (size_t)M * N;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+        float v = part[i];
+        for (int s = 1; s < splits; ++s) v += part[(size_t)s * total + i];
+        if (bias) v += bias[i % N];
+        y[i] = v;
+    }
+}
+
+__global__ void add_bias_kernel(float* __restrict__ y, const float* __restrict__ bias, int M, int N)
+{
+    const size_t total = (size_t)M * N;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x)
+        y[i] += bias[i % N];
+}
+
+}  // namespace
+
+// Choose the split-K factor so the grid covers the chip: 256 CUs.
+int qgemm_splits(int M, int N, int K)
+{
+    const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    const int ksteps = (K + BK - 1) / BK;
+    int splits = 1;
+    while (tiles * splits * 2 <= 320 && ksteps / (splits * 2) >= 4) splits *= 2;
+    return splits;
+}
+
+size_t qgemm_workspace_bytes(int M, int N, int K)
+{
+    const int splits = qgemm_splits(M, N, K);
+    return splits > 1 ? (size_t)splits * M * N * sizeof(float) : 0;
+}
+
+template <int WT>
+static hipError_t launch_qgemm_common(const void* W, const void* S, const void* B, int sbt, int group_size,
+                                      int per_channel, const _Float16* X, float* Y, const float* bias, int M, int N,
+                                      int K, float* workspace, hipStream_t st)
+{
+    const int splits = workspace ? qgemm_splits(M, N, K) : 1;
+    const int ksteps = (K + BK - 1) / BK;
+    const int k_per_split = ((ksteps + splits - 1) / splits) * BK;
+    const dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM, splits);
+    float* out = splits > 1 ? workspace : Y;
+#define CELLM_QGEMM(SBT_)                                                                                          \
+    hipLaunchKernelGGL((qgemm_kernel<WT, SBT_>), grid, dim3(kThreads), 0, st, W, S, B, group_size, X, out, M, N, K, \
+                       k_per_split, per_channel)
+    if (sbt == DT_F32) CELLM_QGEMM(DT_F32);
+    else if (sbt == DT_F16) CELLM_QGEMM(DT_F16);
+    else CELLM_QGEMM(DT_BF16);
+#undef CELLM_QGEMM
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const size_t total = (size_t)M * N;
+    unsigned blocks = (unsigned)((total + 255) / 256);
+    if (blocks > 4096) blocks = 4096;
+    if (splits > 1) {
+        hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, st, workspace, Y, bias, splits, M, N);
+        e = hipGetLastError();
+    } else if (bias) {
+        hipLaunchKernelGGL(add_bias_kernel, dim3(blocks), dim3(256), 0, st, Y, bias, M, N);
+        e = hipGetLastError();
+    }
+    return e;
+}
+
+hipError_t launch_qgemm_q4_affine_ws(const uint32_t* wq, const void* S, const void* B, int sbt, int group_size,
+                                     const _Float16* x, float* y, int M, int N, int K, float* workspace,
+                                     hipStream_t st)
+{
+    return launch_qgemm_common<0>(wq, S, B, sbt, group_size, 1, x, y, nullptr, M, N, K, workspace, st);
+}
+
+hipError_t launch_qgemm_i8_ws(const int8_t* w, const void* S, int sdt, int per_channel, const _Float16* x,
+                              const float* bias, float* y, int M, int N, int K, float* workspace, hipStream_t st)
+{
+    return launch_qgemm_common<1>(w, S, nullptr, sdt, 64, per_channel, x, y, bias, M, N, K, workspace, st);
+}
+
+}  // namespace cellm

@@ -1,0 +1,681 @@
+// Quantized-weight decode GEMV for gfx950 (wave64, 256-thread workgroups).
+//
+//   int8 per-row:   y[m,n] = (sum_k W[n,k] * x[m,k]) * s[n] (+ bias[n])
+//                   crates/cellm-kernels/src/cpu_kernels.rs:66-133 (matmul_i8_f32),
+//                   crates/cellm-kernels/src/metal.rs:365-385 (mv_i8)
+//   MLX q4 affine:  y[m,n] = sum_k (q[n,k] * S[n,k/64] + B[n,k/64]) * x[m,k]
+//                   crates/cellm-model/src/lfm.rs:985-1066 (linear_i4_out_in)
+//
+// Work decomposition.  A "team" of LPR lanes (8..64, always inside one wave)
+// owns R consecutive output rows.  The packed row is cut into 16-byte chunks
+// (32 nibbles for q4, 16 bytes for int8); lane l of a team reads chunks
+// l, l+LPR, ... with one global_load_dwordx4 each, so a team streams its rows
+// as contiguous 16-byte segments and a wave reads whole rows back to back.
+// All weight loads of a lane are issued before the activation vector is staged
+// into LDS, so the x staging overlaps the HBM round trip.
+//
+// Activations live in LDS, pre-arranged as the half2 pairs the unpacked
+// weights meet in v_dot2_f32_f16:
+//   q4:   v_and_or_b32(w, 0x000F000F, 0x64006400) gives the half pair
+//         (1024+q0, 1024+q4); the same mask on the 0x00F0 nibbles gives
+//         (1024+16*q1, 1024+16*q5), met by (x1/16, x5/16).  One shift by 8
+//         covers nibbles 2,6 and 3,7.  The 1024 offsets are removed by
+//         starting each chunk's dot at -corr, corr = 1024 * sum(staged x),
+//         so a 32-element chunk costs 4 shifts + 16 and_or + 16 dot2 per row.
+//   int8: w ^ 0x80808080 turns int8 into u8 = w+128; v_and_or_b32 with
+//         0x00FF00FF / 0x64006400 gives (1152+w0, 1152+w2) and, after a
+//         shift, (1152+w1, 1152+w3); corr = 1152 * sum(x).
+// Products of f16 values are exact in f32 and every sum is f32, so the only
+// difference from the reference is summation order (checked to 1e-3 relative
+// against the reference CPU order in tests/).
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace cellm {
+
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kUnroll = 4;  // chunks per lane held in registers per pass
+
+// ---------------------------------------------------------------------------
+// q4 affine, f16 activations
+// ---------------------------------------------------------------------------
+
+// Stage x[M,K] (f16) into LDS as dot2 pairs plus per-chunk (corr, xsum).
+// xq layout: [MT][CPR][16] uint32; cx layout: [MT][CPR] float2.
+template <int MT>
+__device__ void stage_x_q4(const _Float16* __restrict__ x, int M, int K, uint32_t* xq, float2* cx)
+{
+    const int CPR = K >> 5;
+    const int words = CPR * 4;  // 8-element words per activation row
+    const int total = MT * words;
+    const uint32_t tid = threadIdx.x;
+    for (int base = 0; base < total; base += kBlock) {
+        const int idx = base + (int)tid;
+        const bool valid = idx < total;
+        const int m = valid ? idx / words : 0;
+        const int wdx = valid ? idx - m * words : 0;  // word within the row
+        uint4 raw = make_uint4(0, 0, 0, 0);
+        if (valid && m < M) raw = *reinterpret_cast<const uint4*>(x + (size_t)m * K + (size_t)wdx * 8);
+        h8_t v = __builtin_bit_cast(h8_t, raw);
+        // pairs (x0,x4), (x1/16,x5/16), (x2,x6), (x3/16,x7/16)
+        const _Float16 inv16 = (_Float16)0.0625f;
+        h2_t p0 = {v[0], v[4]};
+        h2_t p1 = {v[1] * inv16, v[5] * inv16};
+        h2_t p2 = {v[2], v[6]};
+        h2_t p3 = {v[3] * inv16, v[7] * inv16};
+        float corr = ((float)p0[0] + (float)p0[1]) + ((float)p1[0] + (float)p1[1]) +
+                     ((float)p2[0] + (float)p2[1]) + ((float)p3[0] + (float)p3[1]);
+        float xs = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xs += (float)v[i];
+        if (valid) {
+            uint4 o = make_uint4(as_u32(p0), as_u32(p1), as_u32(p2), as_u32(p3));
+            *reinterpret_cast<uint4*>(xq + (size_t)idx * 4) = o;
+        }
+        // four consecutive words form one chunk; they sit in four adjacent lanes
+        corr = group_sum<4>(corr);
+        xs = group_sum<4>(xs);
+        if (valid && (wdx & 3) == 0) cx[idx >> 2] = make_float2(1024.0f * corr, xs);
+    }
+}
+
+template <int LPR, int R, int MT, int SBT>
+__global__ __launch_bounds__(kBlock) void qgemv_q4_f16x_kernel(
+    const u4_t* __restrict__ wq, const void* __restrict__ S, const void* __restrict__ B,
+    const _Float16* __restrict__ x, float* __restrict__ y, int M, int N, int K, int gshift)
+{
+    extern __shared__ __align__(16) uint32_t lds[];
+    const int CPR = K >> 5;
+    uint32_t* xq = lds;
+    float2* cx = reinterpret_cast<float2*>(lds + (size_t)MT * CPR * 16);
+
+    const int team = threadIdx.x / LPR;
+    const int lane = threadIdx.x % LPR;
+    const int row0 = (blockIdx.x * (kBlock / LPR) + team) * R;
+    const int gpr = (K + (1 << gshift) - 1) >> gshift;  // groups per row
+
+    // Issue the first pass of weight loads before staging x.
+    u4_t wv[kUnroll][R];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const int c = lane + u * LPR;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int n = row0 + r;
+            wv[u][r] = (c < CPR && n < N) ? __builtin_nontemporal_load(wq + (size_t)n * CPR + c)
+                                          : u4_t{0u, 0u, 0u, 0u};
+        }
+    }
+
+    stage_x_q4<MT>(x, M, K, xq, cx);
+    __syncthreads();
+    if (row0 >= N) return;
+
+    float acc[R][MT];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[r][m] = 0.0f;
+
+    const uint32_t m0f = 0x000F000Fu, m1f = 0x00F000F0u, magic = 0x64006400u;
+    for (int cbase = 0; cbase < CPR; cbase += kUnroll * LPR) {
+        if (cbase != 0) {
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) {
+                const int c = cbase + lane + u * LPR;
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const int n = row0 + r;
+                    wv[u][r] = (c < CPR && n < N) ? __builtin_nontemporal_load(wq + (size_t)n * CPR + c)
+                                                  : u4_t{0u, 0u, 0u, 0u};
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const int c = cbase + lane + u * LPR;
+            if (c < CPR) {
+                const int g = (c << 5) >> gshift;
+                float sc[R], bi[R];
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const int n = min(row0 + r, N - 1);
+                    sc[r] = load_f32<SBT>(S, (size_t)n * gpr + g);
+                    bi[r] = load_f32<SBT>(B, (size_t)n * gpr + g);
+                }
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    const uint4* xp = reinterpret_cast<const uint4*>(xq + ((size_t)m * CPR + c) * 16);
+                    const uint4 xa = xp[0], xb = xp[1], xc = xp[2], xd = xp[3];
+                    const float2 cc = cx[(size_t)m * CPR + c];
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        const u4_t w = wv[u][r];
+                        float d = -cc.x;
+                        uint32_t h;
+                        d = dot2(and_or(w[0], m0f, magic), xa.x, d);
+                        d = dot2(and_or(w[0], m1f, magic), xa.y, d);
+                        h = w[0] >> 8;
+                        d = dot2(and_or(h, m0f, magic), xa.z, d);
+                        d = dot2(and_or(h, m1f, magic), xa.w, d);
+                        d = dot2(and_or(w[1], m0f, magic), xb.x, d);
+                        d = dot2(and_or(w[1], m1f, magic), xb.y, d);
+                        h = w[1] >> 8;
+                        d = dot2(and_or(h, m0f, magic), xb.z, d);
+                        d = dot2(and_or(h, m1f, magic), xb.w, d);
+                        d = dot2(and_or(w[2], m0f, magic), xc.x, d);
+                        d = dot2(and_or(w[2], m1f, magic), xc.y, d);
+                        h = w[2] >> 8;
+                        d = dot2(and_or(h, m0f, magic), xc.z, d);
+                        d = dot2(and_or(h, m1f, magic), xc.w, d);
+                        d = dot2(and_or(w[3], m0f, magic), xd.x, d);
+                        d = dot2(and_or(w[3], m1f, magic), xd.y, d);
+                        h = w[3] >> 8;
+                        d = dot2(and_or(h, m0f, magic), xd.z, d);
+                        d = dot2(and_or(h, m1f, magic), xd.w, d);
+                        acc[r][m] += sc[r] * d + bi[r] * cc.y;
+                    }
+                }
+            }
+        }
+    }
+
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[r][m] = group_sum<LPR>(acc[r][m]);
+
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int n = row0 + r;
+            if (n < N) {
+#pragma unroll
+                for (int m = 0; m < MT; ++m)
+                    if (m < M) y[(size_t)m * N + n] = acc[r][m];
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// int8 per-row scale
+// ---------------------------------------------------------------------------
+
+// f16 activations: xq[MT][CPR][8] uint32 pairs (x0,x2),(x1,x3) per word; cx[MT][CPR] = 1152*sum(x)
+template <int MT>
+__device__ void stage_x_i8_f16(const _Float16* __restrict__ x, int M, int K, uint32_t* xq, float* cx)
+{
+    const int CPR = K >> 4;
+    const int quads = CPR * 2;  // 8-element units; 2 per 16-byte chunk
+    const int total = MT * quads;
+    const uint32_t tid = threadIdx.x;
+    for (int base = 0; base < total; base += kBlock) {
+        const int idx = base + (int)tid;
+        const bool valid = idx < total;
+        const int m = valid ? idx / quads : 0;
+        const int q = valid ? idx - m * quads : 0;
+        uint4 raw = make_uint4(0, 0, 0, 0);
+        if (valid && m < M) raw = *reinterpret_cast<const uint4*>(x + (size_t)m * K + (size_t)q * 8);
+        h8_t v = __builtin_bit_cast(h8_t, raw);
+        h2_t p0 = {v[0], v[2]}, p1 = {v[1], v[3]}, p2 = {v[4], v[6]}, p3 = {v[5], v[7]};
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s += (float)v[i];
+        if (valid) {
+            uint4 o = make_uint4(as_u32(p0), as_u32(p1), as_u32(p2), as_u32(p3));
+            *reinterpret_cast<uint4*>(xq + (size_t)idx * 4) = o;
+        }
+        s = group_sum<2>(s);
+        if (valid && (q & 1) == 0) cx[idx >> 1] = 1152.0f * s;
+    }
+}
+
+template <int LPR, int R, int MT>
+__global__ __launch_bounds__(kBlock) void qgemv_i8_f16x_kernel(
+    const u4_t* __restrict__ w8, const void* __restrict__ S, int sdt, int per_channel,
+    const _Float16* __restrict__ x, const float* __restrict__ bias, float* __restrict__ y, int M, int N, int K)
+{
+    extern __shared__ __align__(16) uint32_t lds[];
+    const int CPR = K >> 4;
+    uint32_t* xq = lds;
+    float* cx = reinterpret_cast<float*>(lds + (size_t)MT * CPR * 8);
+
+    const int team = threadIdx.x / LPR;
+    const int lane = threadIdx.x % LPR;
+    const int row0 = (blockIdx.x * (kBlock / LPR) + team) * R;
+
+    u4_t wv[kUnroll][R];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const int c = lane + u * LPR;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int n = row0 + r;
+            wv[u][r] = (c < CPR && n < N) ? __builtin_nontemporal_load(w8 + (size_t)n * CPR + c)
+                                          : u4_t{0u, 0u, 0u, 0u};
+        }
+    }
+
+    stage_x_i8_f16<MT>(x, M, K, xq, cx);
+    __syncthreads();
+    if (row0 >= N) return;
+
+    float acc[R][MT];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[r][m] = 0.0f;
+
+    const uint32_t mlo = 0x00FF00FFu, magic = 0x64006400u;
+    for (int cbase = 0; cbase < CPR; cbase += kUnroll * LPR) {
+        if (cbase != 0) {
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) {
+                const int c = cbase + lane + u * LPR;
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const int n = row0 + r;
+                    wv[u][r] = (c < CPR && n < N) ? __builtin_nontemporal_load(w8 + (size_t)n * CPR + c)
+                                                  : u4_t{0u, 0u, 0u, 0u};
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const int c = cbase + lane + u * LPR;
+            if (c < CPR) {
+                uint32_t lo[R][4], hi[R][4];
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const uint32_t wd[4] = {wv[u][r][0], wv[u][r][1], wv[u][r][2], wv[u][r][3]};
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        const uint32_t b = wd[t] ^ 0x80808080u;
+                        lo[r][t] = and_or(b, mlo, magic);
+                        hi[r][t] = and_or(b >> 8, mlo, magic);
+                    }
+                }
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    const uint4* xp = reinterpret_cast<const uint4*>(xq + ((size_t)m * CPR + c) * 8);
+                    const uint4 xa = xp[0], xb = xp[1];
+                    const float corr = cx[(size_t)m * CPR + c];
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        float d = acc[r][m] - corr;
+                        d = dot2(lo[r][0], xa.x, d);
+                        d = dot2(hi[r][0], xa.y, d);
+                        d = dot2(lo[r][1], xa.z, d);
+                        d = dot2(hi[r][1], xa.w, d);
+                        d = dot2(lo[r][2], xb.x, d);
+                        d = dot2(hi[r][2], xb.y, d);
+                        d = dot2(lo[r][3], xb.z, d);
+                        d = dot2(hi[r][3], xb.w, d);
+                        acc[r][m] = d;
+                    }
+                }
+            }
+        }
+    }
+
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[r][m] = group_sum<LPR>(acc[r][m]);
+
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int n = row0 + r;
+            if (n < N) {
+                const size_t si = per_channel ? (size_t)n : 0;
+                const float s = sdt == DT_F32 ? load_f32<DT_F32>(S, si)
+                              : sdt == DT_F16 ? load_f32<DT_F16>(S, si)
+                                              : load_f32<DT_BF16>(S, si);
+                const float bv = bias ? bias[n] : 0.0f;
+#pragma unroll
+                for (int m = 0; m < MT; ++m)
+                    if (m < M) {
+                        float v = acc[r][m] * s;
+                        if (bias) v += bv;
+                        y[(size_t)m * N + n] = v;
+                    }
+            }
+        }
+    }
+}
+
+// f32 activations: exact int8 -> f32 conversion (v_cvt_f32_i32 with byte select) and f32 FMA.
+template <int LPR, int R, int MT>
+__global__ __launch_bounds__(kBlock) void qgemv_i8_f32x_kernel(
+    const u4_t* __restrict__ w8, const void* __restrict__ S, int sdt, int per_channel,
+    const float* __restrict__ x, const float* __restrict__ bias, float* __restrict__ y, int M, int N, int K)
+{
+    extern __shared__ __align__(16) uint32_t lds[];
+    float* xs = reinterpret_cast<float*>(lds);  // [MT][K]
+    const int CPR = K >> 4;
+
+    const int team = threadIdx.x / LPR;
+    const int lane = threadIdx.x % LPR;
+    const int row0 = (blockIdx.x * (kBlock / LPR) + team) * R;
+
+    u4_t wv[kUnroll][R];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const int c = lane + u * LPR;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int n = row0 + r;
+            wv[u][r] = (c < CPR && n < N) ? __builtin_nontemporal_load(w8 + (size_t)n * CPR + c)
+                                          : u4_t{0u, 0u, 0u, 0u};
+        }
+    }
+
+    for (int i = threadIdx.x; i < MT * (K >> 2); i += kBlock) {
+        const int m = i / (K >> 2);
+        const int q = i - m * (K >> 2);
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (m < M) v = *reinterpret_cast<const float4*>(x + (size_t)m * K + (size_t)q * 4);
+        *reinterpret_cast<float4*>(xs + (size_t)m * K + (size_t)q * 4) = v;
+    }
+    __syncthreads();
+    if (row0 >= N) return;
+
+    float acc[R][MT];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[r][m] = 0.0f;
+
+    for (int cbase = 0; cbase < CPR; cbase += kUnroll * LPR) {
+        if (cbase != 0) {
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) {
+                const int c = cbase + lane + u * LPR;
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const int n = row0 + r;
+                    wv[u][r] = (c < CPR && n < N) ? __builtin_nontemporal_load(w8 + (size_t)n * CPR + c)
+                                                  : u4_t{0u, 0u, 0u, 0u};
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const int c = cbase + lane + u * LPR;
+            if (c < CPR) {
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    const float4* xp = reinterpret_cast<const float4*>(xs + (size_t)m * K + (size_t)c * 16);
+                    const float4 x0 = xp[0], x1 = xp[1], x2 = xp[2], x3 = xp[3];
+                    const float xv[16] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w,
+                                          x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        const uint32_t wd[4] = {wv[u][r][0], wv[u][r][1], wv[u][r][2], wv[u][r][3]};
+                        float d = acc[r][m];
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) {
+#pragma unroll
+                            for (int b = 0; b < 4; ++b)
+                                d = __builtin_fmaf((float)(int8_t)(wd[t] >> (8 * b)), xv[t * 4 + b], d);
+                        }
+                        acc[r][m] = d;
+                    }
+                }
+            }
+        }
+    }
+
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[r][m] = group_sum<LPR>(acc[r][m]);
+
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int n = row0 + r;
+            if (n < N) {
+                const size_t si = per_channel ? (size_t)n : 0;
+                const float s = sdt == DT_F32 ? load_f32<DT_F32>(S, si)
+                              : sdt == DT_F16 ? load_f32<DT_F16>(S, si)
+                                              : load_f32<DT_BF16>(S, si);
+                const float bv = bias ? bias[n] : 0.0f;
+#pragma unroll
+                for (int m = 0; m < MT; ++m)
+                    if (m < M) {
+                        float v = acc[r][m] * s;
+                        if (bias) v += bv;
+                        y[(size_t)m * N + n] = v;
+                    }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Generic fallback: any K % 8 == 0, any activation dtype, one wave per row.
+// Same element formulas as the reference, f32 arithmetic throughout.
+// ---------------------------------------------------------------------------
+
+template <int XT, int SBT>
+__global__ __launch_bounds__(kBlock) void qgemv_q4_generic_kernel(
+    const uint32_t* __restrict__ wq, const void* __restrict__ S, const void* __restrict__ B, const void* __restrict__ x,
+    float* __restrict__ y, int M, int N, int K, int gshift)
+{
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int n = blockIdx.x * (kBlock / 64) + wave;
+    if (n >= N) return;
+    const int P = K >> 3;
+    const int gpr = (K + (1 << gshift) - 1) >> gshift;
+    for (int m = 0; m < M; ++m) {
+        float acc = 0.0f;
+        for (int p = lane; p < P; p += 64) {
+            const uint32_t w = wq[(size_t)n * P + p];
+            const int g = (p << 3) >> gshift;
+            const float s = load_f32<SBT>(S, (size_t)n * gpr + g);
+            const float b = load_f32<SBT>(B, (size_t)n * gpr + g);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                const float wv = __fadd_rn(__fmul_rn((float)((w >> (4 * k)) & 0xFu), s), b);
+                acc = __builtin_fmaf(wv, load_f32<XT>(x, (size_t)m * K + (size_t)p * 8 + k), acc);
+            }
+        }
+        acc = group_sum<64>(acc);
+        if (lane == 0) y[(size_t)m * N + n] = acc;
+    }
+}
+
+template <int XT>
+__global__ __launch_bounds__(kBlock) void qgemv_i8_generic_kernel(
+    const int8_t* __restrict__ w, const void* __restrict__ S, int sdt, int per_channel, const void* __restrict__ x,
+    const float* __restrict__ bias, float* __restrict__ y, int M, int N, int K)
+{
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int n = blockIdx.x * (kBlock / 64) + wave;
+    if (n >= N) return;
+    const size_t si = per_channel ? (size_t)n : 0;
+    const float s = sdt == DT_F32 ? load_f32<DT_F32>(S, si) : sdt == DT_F16 ? load_f32<DT_F16>(S, si)
+                                                                            : load_f32<DT_BF16>(S, si);
+    for (int m = 0; m < M; ++m) {
+        float acc = 0.0f;
+        for (int k = lane; k < K; k += 64)
+            acc = __builtin_fmaf((float)w[(size_t)n * K + k], load_f32<XT>(x, (size_t)m * K + k), acc);
+        acc = group_sum<64>(acc);
+        if (lane == 0) {
+            float v = acc * s;
+            if (bias) v += bias[n];
+            y[(size_t)m * N + n] = v;
+        }
+    }
+}
+
+// Pick lanes-per-row: single pass (<= kUnroll chunks per lane) if possible,
+// best lane utilisation, enough waves to cover the chip.
+int pick_lpr(int cpr, int n_rows, int R)
+{
+    const int cand[4] = {8, 16, 32, 64};
+    int best = 64;
+    double best_score = -1.0;
+    for (int i = 0; i < 4; ++i) {
+        const int lpr = cand[i];
+        const int c = (cpr + lpr - 1) / lpr;
+        if (c > kUnroll && lpr != 64) continue;
+        const double eff = (double)cpr / ((double)lpr * c);
+        const double waves = (double)((n_rows + R - 1) / R) * lpr / 64.0;
+        const double fill = waves >= 2048.0 ? 1.0 : waves / 2048.0;
+        const double score = eff * (0.5 + 0.5 * fill);
+        if (score > best_score + 1e-9) {
+            best_score = score;
+            best = lpr;
+        }
+    }
+    return best;
+}
+
+template <int LPR, int R, int MT>
+hipError_t launch_q4_f16x_sbt(int sbt, const uint32_t* wq, const void* S, const void* B, const _Float16* x, float* y,
+                              int M, int N, int K, int gshift, hipStream_t st)
+{
+    const int CPR = K >> 5;
+    const size_t lds = (size_t)MT * CPR * 16 * 4 + (size_t)MT * CPR * 8;
+    const int rows_per_block = (kBlock / LPR) * R;
+    const dim3 grid((N + rows_per_block - 1) / rows_per_block);
+    const u4_t* w4 = reinterpret_cast<const u4_t*>(wq);
+    if (sbt == DT_F16)
+        hipLaunchKernelGGL((qgemv_q4_f16x_kernel<LPR, R, MT, DT_F16>), grid, dim3(kBlock), lds, st, w4, S, B, x, y, M,
+                           N, K, gshift);
+    else if (sbt == DT_F32)
+        hipLaunchKernelGGL((qgemv_q4_f16x_kernel<LPR, R, MT, DT_F32>), grid, dim3(kBlock), lds, st, w4, S, B, x, y, M,
+                           N, K, gshift);
+    else
+        hipLaunchKernelGGL((qgemv_q4_f16x_kernel<LPR, R, MT, DT_BF16>), grid, dim3(kBlock), lds, st, w4, S, B, x, y,
+                           M, N, K, gshift);
+    return hipGetLastError();
+}
+
+template <int R, int MT>
+hipError_t launch_q4_f16x_lpr(int lpr, int sbt, const uint32_t* wq, const void* S, const void* B, const _Float16* x,
+                              float* y, int M, int N, int K, int gshift, hipStream_t st)
+{
+    switch (lpr) {
+    case 8: return launch_q4_f16x_sbt<8, R, MT>(sbt, wq, S, B, x, y, M, N, K, gshift, st);
+    case 16: return launch_q4_f16x_sbt<16, R, MT>(sbt, wq, S, B, x, y, M, N, K, gshift, st);
+    case 32: return launch_q4_f16x_sbt<32, R, MT>(sbt, wq, S, B, x, y, M, N, K, gshift, st);
+    default: return launch_q4_f16x_sbt<64, R, MT>(sbt, wq, S, B, x, y, M, N, K, gshift, st);
+    }
+}
+
+template <int LPR, int R, int MT>
+hipError_t launch_i8_lpr_fixed(int xdt, const int8_t* w, const void* S, int sdt, int per_channel, const void* x,
+                               const float* bias, float* y, int M, int N, int K, hipStream_t st)
+{
+    const int CPR = K >> 4;
+    const int rows_per_block = (kBlock / LPR) * R;
+    const dim3 grid((N + rows_per_block - 1) / rows_per_block);
+    const u4_t* w4 = reinterpret_cast<const u4_t*>(w);
+    if (xdt == DT_F16) {
+        const size_t lds = (size_t)MT * CPR * 8 * 4 + (size_t)MT * CPR * 4;
+        hipLaunchKernelGGL((qgemv_i8_f16x_kernel<LPR, R, MT>), grid, dim3(kBlock), lds, st, w4, S, sdt, per_channel,
+                           reinterpret_cast<const _Float16*>(x), bias, y, M, N, K);
+    } else {
+        const size_t lds = (size_t)MT * K * 4;
+        hipLaunchKernelGGL((qgemv_i8_f32x_kernel<LPR, R, MT>), grid, dim3(kBlock), lds, st, w4, S, sdt, per_channel,
+                           reinterpret_cast<const float*>(x), bias, y, M, N, K);
+    }
+    return hipGetLastError();
+}
+
+template <int R, int MT>
+hipError_t launch_i8_lpr(int lpr, int xdt, const int8_t* w, const void* S, int sdt, int per_channel, const void* x,
+                         const float* bias, float* y, int M, int N, int K, hipStream_t st)
+{
+    switch (lpr) {
+    case 8: return launch_i8_lpr_fixed<8, R, MT>(xdt, w, S, sdt, per_channel, x, bias, y, M, N, K, st);
+    case 16: return launch_i8_lpr_fixed<16, R, MT>(xdt, w, S, sdt, per_channel, x, bias, y, M, N, K, st);
+    case 32: return launch_i8_lpr_fixed<32, R, MT>(xdt, w, S, sdt, per_channel, x, bias, y, M, N, K, st);
+    default: return launch_i8_lpr_fixed<64, R, MT>(xdt, w, S, sdt, per_channel, x, bias, y, M, N, K, st);
+    }
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+int qgemv_q4_lds_bytes(int M, int K)
+{
+    const int MT = M <= 1 ? 1 : (M <= 2 ? 2 : 4);
+    const int CPR = K >> 5;
+    return MT * CPR * 16 * 4 + MT * CPR * 8;
+}
+
+hipError_t launch_qgemv_q4_affine(const uint32_t* wq, const void* S, const void* B, int sbt, int group_size,
+                                  const void* x, int xdt, float* y, int M, int N, int K, hipStream_t st,
+                                  int force_generic)
+{
+    const int gshift = __builtin_ctz((unsigned)group_size);
+    const bool fast = !force_generic && xdt == DT_F16 && M <= 4 && (K % 32) == 0 && group_size >= 32 &&
+                      aligned16(wq) && aligned16(x) && qgemv_q4_lds_bytes(M, K) <= 64 * 1024;
+    if (fast) {
+        const int CPR = K >> 5;
+        const int R = 2;
+        const int lpr = pick_lpr(CPR, N, R);
+        const _Float16* xh = reinterpret_cast<const _Float16*>(x);
+        if (M == 1) return launch_q4_f16x_lpr<2, 1>(lpr, sbt, wq, S, B, xh, y, M, N, K, gshift, st);
+        if (M == 2) return launch_q4_f16x_lpr<2, 2>(lpr, sbt, wq, S, B, xh, y, M, N, K, gshift, st);
+        return launch_q4_f16x_lpr<2, 4>(lpr, sbt, wq, S, B, xh, y, M, N, K, gshift, st);
+    }
+    const dim3 grid((N + 3) / 4);
+#define CELLM_Q4_GENERIC(XT_, SBT_)                                                                              \
+    hipLaunchKernelGGL((qgemv_q4_generic_kernel<XT_, SBT_>), grid, dim3(kBlock), 0, st, wq, S, B, x, y, M, N, K, \
+                       gshift)
+    if (xdt == DT_F32) {
+        if (sbt == DT_F32) CELLM_Q4_GENERIC(DT_F32, DT_F32);
+        else if (sbt == DT_F16) CELLM_Q4_GENERIC(DT_F32, DT_F16);
+        else CELLM_Q4_GENERIC(DT_F32, DT_BF16);
+    } else if (xdt == DT_F16) {
+        if (sbt == DT_F32) CELLM_Q4_GENERIC(DT_F16, DT_F32);
+        else if (sbt == DT_F16) CELLM_Q4_GENERIC(DT_F16, DT_F16);
+        else CELLM_Q4_GENERIC(DT_F16, DT_BF16);
+    } else {
+        if (sbt == DT_F32) CELLM_Q4_GENERIC(DT_BF16, DT_F32);
+        else if (sbt == DT_F16) CELLM_Q4_GENERIC(DT_BF16, DT_F16);
+        else CELLM_Q4_GENERIC(DT_BF16, DT_BF16);
+    }
+#undef CELLM_Q4_GENERIC
+    return hipGetLastError();
+}
+
+hipError_t launch_qgemv_i8(const int8_t* w, const void* S, int sdt, int per_channel, const void* x, int xdt,
+                           const float* bias, float* y, int M, int N, int K, hipStream_t st, int force_generic)
+{
+    const int MT = M <= 1 ? 1 : (M <= 2 ? 2 : 4);
+    const size_t lds = xdt == DT_F16 ? (size_t)MT * (K >> 4) * 36 : (size_t)MT * K * 4;
+    const bool fast = !force_generic && (xdt == DT_F16 || xdt == DT_F32) && M <= 4 && (K % 16) == 0 &&
+                      aligned16(w) && aligned16(x) && lds <= 64 * 1024;
+    if (fast) {
+        const int CPR = K >> 4;
+        const int R = 2;
+        const int lpr = pick_lpr(CPR, N, R);
+        if (M == 1) return launch_i8_lpr<2, 1>(lpr, xdt, w, S, sdt, per_channel, x, bias, y, M, N, K, st);
+        if (M == 2) return launch_i8_lpr<2, 2>(lpr, xdt, w, S, sdt, per_channel, x, bias, y, M, N, K, st);
+        return launch_i8_lpr<2, 4>(lpr, xdt, w, S, sdt, per_channel, x, bias, y, M, N, K, st);
+    }
+    const dim3 grid((N + 3) / 4);
+    if (xdt == DT_F32)
+        hipLaunchKernelGGL((qgemv_i8_generic_kernel<DT_F32>), grid, dim3(kBlock), 0, st, w, S, sdt, per_channel, x,
+                           bias, y, M, N, K);
+    else if (xdt == DT_F16)
+        hipLaunchKernelGGL((qgemv_i8_generic_kernel<DT_F16>), grid, dim3(kBlock), 0, st, w, S, sdt, per_channel, x,
+                           bias, y, M, N, K);
+    else
+        hipLaunchKernelGGL((qgemv_i8_generic_kernel<DT_BF16>), grid, dim3(kBlock), 0, st, w, S, sdt, per_channel, x,
+                           bias, y, M, N, K);
+    return hipGetLastError();
+}
+
+}  // namespace cellm

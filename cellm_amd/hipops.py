@@ -1,0 +1,215 @@
+"""HipOps: the host-side mirror of cellm's MetalOps over libcellm_hip.so.
+
+Method names and argument meaning follow MetalOps
+(crates/cellm-kernels/src/metal.rs): `logits_*` take host arrays and a cache
+key and return host results (metal.rs:1017-1204); `encode_*` take device
+tensors and queue work on a stream (metal.rs:813-1176).  Errors raise
+CellmHipError, the analogue of the anyhow::Result the Rust methods return.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from . import _lib
+from ._lib import DTYPE_BF16, DTYPE_F16, DTYPE_F32, check
+
+_NP_DT = {np.dtype(np.float32): DTYPE_F32, np.dtype(np.float16): DTYPE_F16}
+
+
+def _np_ptr(a: np.ndarray):
+    if not a.flags["C_CONTIGUOUS"]:
+        raise ValueError("arrays passed to HipOps must be C-contiguous")
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def _torch_dtype_code(t) -> int:
+    import torch
+
+    if t.dtype == torch.float32:
+        return DTYPE_F32
+    if t.dtype == torch.float16:
+        return DTYPE_F16
+    if t.dtype == torch.bfloat16:
+        return DTYPE_BF16
+    raise TypeError(f"unsupported tensor dtype {t.dtype}")
+
+
+def _dev_ptr(t):
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError("encode_* expects device tensors")
+    if not t.is_contiguous():
+        raise ValueError("encode_* expects contiguous tensors")
+    return C.c_void_p(t.data_ptr())
+
+
+def _stream_ptr(stream):
+    if stream is None:
+        return None
+    if isinstance(stream, int):
+        return C.c_void_p(stream)
+    return C.c_void_p(stream.cuda_stream)
+
+
+def device_count() -> int:
+    lib = _lib.load()
+    n = C.c_int32(0)
+    check(lib.cellm_hip_device_count(C.byref(n)))
+    return n.value
+
+
+def smoke_test(device: int = 0) -> None:
+    """MetalKernels::smoke_test_add_f32 analogue (metal.rs:33-93)."""
+    check(_lib.load().cellm_hip_smoke_test(device))
+
+
+class HipOps:
+    """One device context: stream, name-keyed weight cache, scratch buffers."""
+
+    def __init__(self, device: int = 0):
+        self._lib = _lib.load()
+        h = C.c_void_p()
+        check(self._lib.cellm_hip_create(device, C.byref(h)))
+        self._h = h
+        self.device = device
+
+    @classmethod
+    def create(cls, device: int = 0) -> "HipOps":
+        return cls(device)
+
+    def close(self) -> None:
+        if getattr(self, "_h", None) and self._h.value:
+            self._lib.cellm_hip_destroy(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    @property
+    def handle(self):
+        return self._h
+
+    def synchronize(self) -> None:
+        check(self._lib.cellm_hip_synchronize(self._h))
+
+    def stream(self) -> int:
+        s = C.c_void_p()
+        check(self._lib.cellm_hip_get_stream(self._h, C.byref(s)))
+        return s.value or 0
+
+    # -- weight cache -------------------------------------------------------------
+    def weight_upload(self, key: str, host: np.ndarray) -> int:
+        out = C.c_void_p()
+        check(self._lib.cellm_hip_weight_upload(self._h, key.encode(), _np_ptr(host), host.nbytes, C.byref(out)))
+        return out.value
+
+    def weight_lookup(self, key: str):
+        out, nb = C.c_void_p(), C.c_size_t()
+        check(self._lib.cellm_hip_weight_lookup(self._h, key.encode(), C.byref(out), C.byref(nb)))
+        return out.value, nb.value
+
+    def weight_evict(self, key: str) -> None:
+        check(self._lib.cellm_hip_weight_evict(self._h, key.encode()))
+
+    def weight_cache_stats(self):
+        e, b = C.c_size_t(), C.c_size_t()
+        check(self._lib.cellm_hip_weight_cache_stats(self._h, C.byref(e), C.byref(b)))
+        return e.value, b.value
+
+    # -- sync: MetalOps::logits_* -----------------------------------------------
+    def logits_i8(self, x: np.ndarray, w_i8: np.ndarray, scales_f16_bits: np.ndarray, vocab: int, hidden: int,
+                  cache_key: str, out: np.ndarray | None = None) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        w = np.ascontiguousarray(w_i8, np.int8)
+        s = np.ascontiguousarray(scales_f16_bits, np.uint16)
+        if x.size != hidden or w.size != vocab * hidden or s.size != vocab:
+            raise ValueError("logits_i8: shape mismatch")
+        out = np.empty(vocab, np.float32) if out is None else out
+        check(self._lib.cellm_hip_logits_i8(self._h, _np_ptr(x), _np_ptr(w), _np_ptr(s), vocab, hidden,
+                                            cache_key.encode(), _np_ptr(out)))
+        return out
+
+    def logits_i4(self, x: np.ndarray, w_u8: np.ndarray, scales_f16_bits: np.ndarray, vocab: int, hidden: int,
+                  gs: int, cache_key: str, out: np.ndarray | None = None) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        w = np.ascontiguousarray(w_u8, np.uint8)
+        s = np.ascontiguousarray(scales_f16_bits, np.uint16)
+        if x.size != hidden or w.size != vocab * ((hidden + 1) // 2):
+            raise ValueError("logits_i4: shape mismatch")
+        out = np.empty(vocab, np.float32) if out is None else out
+        check(self._lib.cellm_hip_logits_i4(self._h, _np_ptr(x), _np_ptr(w), _np_ptr(s), s.size, vocab, hidden, gs,
+                                            cache_key.encode(), _np_ptr(out)))
+        return out
+
+    def logits_q4_affine(self, x: np.ndarray, wq: np.ndarray, scales: np.ndarray, biases: np.ndarray, rows: int,
+                         cols: int, cache_key: str, out: np.ndarray | None = None) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32)
+        wq = np.ascontiguousarray(wq, np.uint32)
+        scales = np.ascontiguousarray(scales)
+        biases = np.ascontiguousarray(biases, scales.dtype)
+        dt = _NP_DT.get(scales.dtype, DTYPE_BF16 if scales.dtype == np.uint16 else None)
+        if dt is None:
+            raise TypeError(f"unsupported scale dtype {scales.dtype}")
+        out = np.empty(rows, np.float32) if out is None else out
+        check(self._lib.cellm_hip_logits_q4_affine(self._h, _np_ptr(x), _np_ptr(wq), _np_ptr(scales), _np_ptr(biases),
+                                                   dt, rows, cols, cache_key.encode(), _np_ptr(out)))
+        return out
+
+    # -- async: MetalOps::encode_* over torch device tensors ------------------------
+    def encode_qgemv_i8(self, w, scales, x, y, bias=None, stream=None) -> None:
+        """y[m,n] = (W[n,:] . x[m,:]) * s[n] (+ bias[n]); W int8 [n,k]."""
+        n, k = w.shape
+        m = x.numel() // k
+        check(self._lib.cellm_hip_qgemv_i8(self._h, _dev_ptr(w), _dev_ptr(scales), _torch_dtype_code(scales),
+                                           scales.numel(), _dev_ptr(x), _torch_dtype_code(x), _dev_ptr(bias),
+                                           _dev_ptr(y), m, n, k, _stream_ptr(stream)))
+
+    def encode_qgemv_q4_affine(self, wq, scales, biases, x, y, group: int = 64, stream=None) -> None:
+        """MLX affine; wq int32/uint32 words [n, k/8], scales/biases [n, ceil(k/group)]."""
+        n = wq.shape[0]
+        k = wq.shape[1] * 8
+        m = x.numel() // k
+        check(self._lib.cellm_hip_qgemv_q4_affine(self._h, _dev_ptr(wq), _dev_ptr(scales), _dev_ptr(biases),
+                                                  _torch_dtype_code(scales), group, _dev_ptr(x), _torch_dtype_code(x),
+                                                  _dev_ptr(y), m, n, k, _stream_ptr(stream)))
+
+    def encode_qgemv_i4_sym(self, w_u8, scales_f16, gs: int, x, y, k: int, stream=None) -> None:
+        n = w_u8.shape[0]
+        m = x.numel() // k
+        check(self._lib.cellm_hip_qgemv_i4_sym(self._h, _dev_ptr(w_u8), _dev_ptr(scales_f16), scales_f16.numel(), gs,
+                                               _dev_ptr(x), _torch_dtype_code(x), _dev_ptr(y), m, n, k,
+                                               _stream_ptr(stream)))
+
+    def encode_qgemm_q4_affine(self, wq, scales, biases, x_f16, y, group: int = 64, stream=None) -> None:
+        n = wq.shape[0]
+        k = wq.shape[1] * 8
+        m = x_f16.numel() // k
+        check(self._lib.cellm_hip_qgemm_q4_affine(self._h, _dev_ptr(wq), _dev_ptr(scales), _dev_ptr(biases),
+                                                  _torch_dtype_code(scales), group, _dev_ptr(x_f16), _dev_ptr(y), m, n,
+                                                  k, _stream_ptr(stream)))
+
+    def encode_qgemm_i8(self, w, scales, x_f16, y, bias=None, stream=None) -> None:
+        n, k = w.shape
+        m = x_f16.numel() // k
+        check(self._lib.cellm_hip_qgemm_i8(self._h, _dev_ptr(w), _dev_ptr(scales), _torch_dtype_code(scales),
+                                           scales.numel(), _dev_ptr(x_f16), _dev_ptr(bias), _dev_ptr(y), m, n, k,
+                                           _stream_ptr(stream)))
+
+    def encode_dequant_q4_affine(self, wq, scales, biases, out, group: int = 64, stream=None) -> None:
+        n = wq.shape[0]
+        k = wq.shape[1] * 8
+        check(self._lib.cellm_hip_dequant_q4_affine(self._h, _dev_ptr(wq), _dev_ptr(scales), _dev_ptr(biases),
+                                                    _torch_dtype_code(scales), group, _dev_ptr(out),
+                                                    _torch_dtype_code(out), n, k, _stream_ptr(stream)))

@@ -1,0 +1,171 @@
+/*
+ * cellm_hip.h -- C ABI of the MI355X (gfx950) quantized-weight matmul library.
+ *
+ * This is the drop-in boundary for cellm's quantized projection path: a Rust
+ * `HipOps` (the sibling of `MetalOps`, crates/cellm-kernels/src/metal.rs:637-661)
+ * binds these functions one-to-one and a `BackendKind::Hip` selects it.
+ * Each declaration cites the reference interface it replaces.
+ *
+ * Conventions (mirroring crates/cellm-sdk/include/cellm.h:19-26 and ffi.rs:21-52):
+ *   - every function returns int32_t: 0 (CELLM_HIP_OK) on success, < 0 on error;
+ *   - on error a message is stored per calling thread and read with
+ *     cellm_hip_last_error_message();
+ *   - no CPU fallback exists: an entry point either runs on the GPU or fails.
+ *
+ * Layouts (all row-major, "HF linear weight: [out, in]", llama.rs:770-776):
+ *   int8:       W [n, k] int8; scales [n] (per row) or [1] (per tensor)
+ *   q4 affine:  Wq [n, k/8] uint32, nibble j of word p = element 8p+j;
+ *               scales, biases [n, ceil(k/group)] ; w = q*scale + bias
+ *   i4 sym:     W [n, ceil(k/2)] uint8, low nibble = even element;
+ *               scales f16 [n * spr], spr = n_scales / n, w = (nib-8)*scale[j/gs]
+ *   x [m, k], y [m, n] (f32).
+ *
+ * Async entry points take device pointers and a stream (a hipStream_t passed
+ * as void*; NULL selects the context's own stream) and return as soon as the
+ * work is queued, like MetalOps::encode_* (metal.rs:813-1176).  Sync entry
+ * points take host pointers, cache the weights on the device under a name
+ * key, and return after the result is back in host memory, like
+ * MetalOps::logits_* (metal.rs:1017-1204).
+ */
+#ifndef CELLM_HIP_H
+#define CELLM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CELLM_HIP_OK 0
+#define CELLM_HIP_ERR_INVALID_ARG (-1)
+#define CELLM_HIP_ERR_DEVICE (-2)
+#define CELLM_HIP_ERR_OUT_OF_MEMORY (-3)
+#define CELLM_HIP_ERR_NOT_FOUND (-4)
+#define CELLM_HIP_ERR_UNSUPPORTED (-5)
+
+/* Element type of scales, biases and activations. */
+typedef enum {
+    CELLM_HIP_DTYPE_F32 = 0,
+    CELLM_HIP_DTYPE_F16 = 1,
+    CELLM_HIP_DTYPE_BF16 = 2
+} cellm_hip_dtype_t;
+
+typedef struct cellm_hip_ctx cellm_hip_ctx_t;
+
+/* ---- errors, devices, lifetime ------------------------------------------ */
+
+/* Copies the calling thread's last error message (NUL-terminated, truncated to
+ * buf_len) and returns its full length; buf may be NULL to query the length.
+ * Replaces cellm_last_error_message (crates/cellm-sdk/include/cellm.h:24-26). */
+size_t cellm_hip_last_error_message(char* buf, size_t buf_len);
+
+/* Number of visible HIP devices. */
+int32_t cellm_hip_device_count(int32_t* out_count);
+
+/* Launches out = a + b on `device` and checks the result on the host.
+ * Replaces MetalKernels::smoke_test_add_f32 (metal.rs:33-93), the probe that
+ * select_backend runs (tools/infer/src/main.rs:591-615). */
+int32_t cellm_hip_smoke_test(int32_t device);
+
+/* Creates a context bound to `device`: an owned stream, a name-keyed device
+ * weight cache and scratch buffers.  Replaces MetalOps::create (metal.rs:705-746). */
+int32_t cellm_hip_create(int32_t device, cellm_hip_ctx_t** out_ctx);
+
+/* Frees every cached weight and scratch buffer, then the context. */
+void cellm_hip_destroy(cellm_hip_ctx_t* ctx);
+
+/* Waits for all work queued on the context's own stream. */
+int32_t cellm_hip_synchronize(cellm_hip_ctx_t* ctx);
+
+/* Returns the context's own stream (a hipStream_t) in *out_stream. */
+int32_t cellm_hip_get_stream(cellm_hip_ctx_t* ctx, void** out_stream);
+
+/* ---- device weight cache (MetalOps::tensor_cache, metal.rs:660,1045-1050) - */
+
+/* Uploads `nbytes` from host memory once under `key`; a second upload of the
+ * same key returns the existing buffer.  *out_dev receives the device pointer
+ * (256-byte aligned), owned by the context. */
+int32_t cellm_hip_weight_upload(cellm_hip_ctx_t* ctx, const char* key, const void* host, size_t nbytes,
+                                const void** out_dev);
+
+/* Looks up a cached weight; CELLM_HIP_ERR_NOT_FOUND if absent. */
+int32_t cellm_hip_weight_lookup(cellm_hip_ctx_t* ctx, const char* key, const void** out_dev, size_t* out_nbytes);
+
+/* Frees one cached weight; CELLM_HIP_ERR_NOT_FOUND if absent. */
+int32_t cellm_hip_weight_evict(cellm_hip_ctx_t* ctx, const char* key);
+
+/* Number of cached weights and their total bytes. */
+int32_t cellm_hip_weight_cache_stats(cellm_hip_ctx_t* ctx, size_t* out_entries, size_t* out_bytes);
+
+/* ---- async entry points (device pointers) ------------------------------- */
+
+/* int8 per-row-scaled GEMV / GEMM:
+ *   y[i, r] = (sum_j W[r, j] * x[i, j]) * scale[per_row ? r : 0]  (+ bias[r] if bias != NULL)
+ * scale applied after the sum as in cpu_kernels::matmul_i8_f32
+ * (crates/cellm-kernels/src/cpu_kernels.rs:66-133); per-tensor scale when
+ * n_scales < n as MetalOps::encode_mv_i8_bias decides (metal.rs:891-904).
+ * scale_dtype: F32/F16/BF16; x_dtype: F32/F16/BF16.  m <= 4 runs the decode
+ * GEMV; larger m with f16 x and k % 64 == 0 runs the MFMA GEMM. */
+int32_t cellm_hip_qgemv_i8(cellm_hip_ctx_t* ctx, const int8_t* w, const void* scales, int32_t scale_dtype,
+                           int64_t n_scales, const void* x, int32_t x_dtype, const float* bias, float* y, int64_t m,
+                           int64_t n, int64_t k, void* stream);
+
+/* MLX 4-bit affine GEMV / GEMM:
+ *   y[i, r] = sum_j (q[r, j] * S[r, j/group] + B[r, j/group]) * x[i, j]
+ * Replaces LfmRunner::linear_i4_out_in (crates/cellm-model/src/lfm.rs:985-1066)
+ * and its dequant -> MetalOps::logits_f32 route (lfm.rs:1049-1054).
+ * k % 8 == 0; group a power of two >= 8 (MLX uses 64). */
+int32_t cellm_hip_qgemv_q4_affine(cellm_hip_ctx_t* ctx, const uint32_t* wq, const void* scales, const void* biases,
+                                  int32_t sb_dtype, int64_t group, const void* x, int32_t x_dtype, float* y,
+                                  int64_t m, int64_t n, int64_t k, void* stream);
+
+/* Symmetric i4 GEMV: y[i, r] = sum_j ((nib - 8) * scale[r*spr + j/gs]) * x[i, j],
+ * spr = n_scales / n.  Replaces cpu_kernels::matmul_i4_f32 (cpu_kernels.rs:219-243)
+ * and MetalOps::encode_mv_i4 (metal.rs:1167-1176). */
+int32_t cellm_hip_qgemv_i4_sym(cellm_hip_ctx_t* ctx, const uint8_t* w, const uint16_t* scales_f16, int64_t n_scales,
+                               int64_t gs, const void* x, int32_t x_dtype, float* y, int64_t m, int64_t n, int64_t k,
+                               void* stream);
+
+/* Prefill qGEMM on MFMA: Y[m, n] = X[m, k] . dequant(Wq)^T, X f16, Y f32,
+ * weight tiles dequantized to f16 as tools/convert/src/main.rs:4349-4444 does.
+ * No reference counterpart (prefill is token-by-token, llama.rs:214-233);
+ * its oracle is cpu_kernels::matmul_f32 (cpu_kernels.rs:36-63). k % 64 == 0. */
+int32_t cellm_hip_qgemm_q4_affine(cellm_hip_ctx_t* ctx, const uint32_t* wq, const void* scales, const void* biases,
+                                  int32_t sb_dtype, int64_t group, const uint16_t* x_f16, float* y, int64_t m,
+                                  int64_t n, int64_t k, void* stream);
+
+/* int8 qGEMM on MFMA (exact int8 -> f16 tiles, per-row scale in the epilogue). */
+int32_t cellm_hip_qgemm_i8(cellm_hip_ctx_t* ctx, const int8_t* w, const void* scales, int32_t scale_dtype,
+                           int64_t n_scales, const uint16_t* x_f16, const float* bias, float* y, int64_t m, int64_t n,
+                           int64_t k, void* stream);
+
+/* Bit-exact dequant of MLX affine weights to f32 (lfm.rs:1014-1025 rounding)
+ * or f16 (RNE of the f32 value, tools/convert/src/main.rs:4430-4436). */
+int32_t cellm_hip_dequant_q4_affine(cellm_hip_ctx_t* ctx, const uint32_t* wq, const void* scales, const void* biases,
+                                    int32_t sb_dtype, int64_t group, void* out, int32_t out_dtype, int64_t n,
+                                    int64_t k, void* stream);
+
+/* ---- sync entry points (host pointers, weights cached by key) ----------- */
+
+/* MetalOps::logits_i8 (metal.rs:1044-1066): x f32 [cols], w int8 [rows, cols],
+ * scales f16 [rows], out f32 [rows]. */
+int32_t cellm_hip_logits_i8(cellm_hip_ctx_t* ctx, const float* x, const int8_t* w, const uint16_t* scales_f16,
+                            size_t rows, size_t cols, const char* cache_key, float* out);
+
+/* MetalOps::logits_i4 (metal.rs:1178-1204) with the CPU reference's scale
+ * indexing (spr = n_scales / rows, cpu_kernels.rs:228-229). */
+int32_t cellm_hip_logits_i4(cellm_hip_ctx_t* ctx, const float* x, const uint8_t* w, const uint16_t* scales_f16,
+                            size_t n_scales, size_t rows, size_t cols, size_t gs, const char* cache_key, float* out);
+
+/* The LFM affine linear (lfm.rs:985-1066) without the f32 dequant cache:
+ * x f32 [cols], Wq [rows, cols/8], scales/biases [rows, ceil(cols/64)]. */
+int32_t cellm_hip_logits_q4_affine(cellm_hip_ctx_t* ctx, const float* x, const uint32_t* wq, const void* scales,
+                                   const void* biases, int32_t sb_dtype, size_t rows, size_t cols,
+                                   const char* cache_key, float* out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CELLM_HIP_H */

@@ -1,0 +1,309 @@
+"""GPU parity: the HIP path (through the C ABI) against the CPU oracle.
+
+Bars:
+  * unpack / dequant: bit-exact;
+  * GEMV/GEMM with f32 accumulation of exact products: normwise relative error
+    max|y - ref| / max|ref| <= 1e-3 against the reference CPU order;
+  * GEMM over f16 dequantized tiles: <= 2e-2 against the reference f32 path,
+    and <= 1e-3 against the same f16 tiles summed by the oracle.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from tests._util import make_i8, make_q4, rel_err, seed
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-3
+TOL_F16_TILE = 2e-2
+
+
+def _t(a, dtype=None):
+    import torch
+
+    if a.dtype == np.uint32:
+        a = a.view(np.int32)
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    return t.to("cuda")
+
+
+def _sb_tensor(a):
+    import torch
+
+    if a.dtype == np.uint16:  # bf16 bits
+        return torch.from_numpy(a.view(np.int16)).to("cuda").view(torch.bfloat16)
+    return _t(a)
+
+
+def _run_q4(ops, wq, s, b, x, group=64, gemm=False):
+    import torch
+
+    n, k = wq.shape[0], wq.shape[1] * 8
+    m = x.shape[0]
+    y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    if gemm:
+        ops.encode_qgemm_q4_affine(_t(wq), _sb_tensor(s), _sb_tensor(b), _t(x), y, group=group)
+    else:
+        ops.encode_qgemv_q4_affine(_t(wq), _sb_tensor(s), _sb_tensor(b), _t(x), y, group=group)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+def _run_i8(ops, w, s, x, bias=None, gemm=False):
+    import torch
+
+    n, k = w.shape
+    m = x.shape[0]
+    y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    bt = _t(bias) if bias is not None else None
+    if gemm:
+        ops.encode_qgemm_i8(_t(w), _t(s), _t(x), y, bias=bt)
+    else:
+        ops.encode_qgemv_i8(_t(w), _t(s), _t(x), y, bias=bt)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+def test_smoke(ops):
+    from cellm_amd import smoke_test
+
+    smoke_test(0)
+
+
+# ---------------------------------------------------------------- dequant ----
+
+@pytest.mark.parametrize("sb", [np.float16, np.float32, "bf16"])
+@pytest.mark.parametrize("n,k,group", [(64, 896, 64), (7, 128, 64), (5, 96, 64), (9, 256, 32), (3, 512, 128)])
+def test_dequant_bit_exact(ops, sb, n, k, group):
+    import torch
+
+    wq, s, b, _ = make_q4(n, k, 1, sb_dtype=sb, group=group, salt=n + k)
+    out16 = torch.empty((n, k), dtype=torch.float16, device="cuda")
+    ops.encode_dequant_q4_affine(_t(wq), _sb_tensor(s), _sb_tensor(b), out16, group=group)
+    out32 = torch.empty((n, k), dtype=torch.float32, device="cuda")
+    ops.encode_dequant_q4_affine(_t(wq), _sb_tensor(s), _sb_tensor(b), out32, group=group)
+    torch.cuda.synchronize()
+    ref16 = oracle.dequant_q4_affine_f16(wq, s, b, k, group)
+    ref32 = oracle.q4_affine_dequant_f32(wq, s, b, k, group)
+    np.testing.assert_array_equal(out16.cpu().numpy().view(np.uint16), ref16)
+    np.testing.assert_array_equal(out32.cpu().numpy().view(np.uint32), ref32.view(np.uint32))
+
+
+# ------------------------------------------------------------- q4 affine GEMV ----
+
+QWEN_SHAPES = [(896, 1152), (896, 896), (896, 9728), (4864, 896)]  # (K, N), config 2
+
+
+@pytest.mark.parametrize("k,n", QWEN_SHAPES)
+def test_q4_gemv_qwen_shapes(ops, k, n):
+    wq, s, b, x = make_q4(n, k, 1)
+    y = _run_q4(ops, wq, s, b, x)
+    ref = oracle.qgemv_q4_affine(wq, s, b, x, k)
+    assert rel_err(y, ref) <= TOL_F32, rel_err(y, ref)
+
+
+def test_q4_gemv_qwen_lm_head(ops):
+    k, n = 896, 151936
+    wq, s, b, x = make_q4(n, k, 1, salt=1)
+    y = _run_q4(ops, wq, s, b, x)
+    ref = oracle.qgemv_q4_affine(wq, s, b, x, k)
+    assert rel_err(y, ref) <= TOL_F32
+    assert int(np.argmax(y[0])) == int(np.argmax(ref[0]))
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+@pytest.mark.parametrize("sb", [np.float16, np.float32, "bf16"])
+def test_q4_gemv_batched_small_m(ops, m, sb):
+    k, n = 1152, 1000  # N not a multiple of any rows-per-block
+    wq, s, b, x = make_q4(n, k, m, cfg=3, sb_dtype=sb, salt=m)
+    y = _run_q4(ops, wq, s, b, x)
+    ref = oracle.qgemv_q4_affine(wq, s, b, x, k)
+    assert rel_err(y, ref) <= TOL_F32
+
+
+@pytest.mark.parametrize("k,n,group", [(40, 33, 64), (96, 17, 64), (256, 50, 32), (512, 31, 128)])
+def test_q4_gemv_ragged_and_groups(ops, k, n, group):
+    wq, s, b, x = make_q4(n, k, 1, group=group, salt=k)
+    y = _run_q4(ops, wq, s, b, x, group=group)
+    ref = oracle.qgemv_q4_affine(wq, s, b, x, k, group)
+    assert rel_err(y, ref) <= TOL_F32
+
+
+def test_q4_logits_sync_f32_reference_dtypes(ops):
+    """The LFM layout as converted by convert_lfm.py: f32 scales/biases, f32 x."""
+    k, n = 1024, 2048
+    wq, s, b, x = make_q4(n, k, 1, sb_dtype=np.float32, x_dtype=np.float32, salt=7)
+    y = ops.logits_q4_affine(x[0], wq, s, b, n, k, "test.lfm.q4")
+    ref = oracle.qgemv_q4_affine(wq, s, b, x, k)[0]
+    assert rel_err(y, ref) <= TOL_F32
+    # second call hits the weight cache
+    y2 = ops.logits_q4_affine(x[0], wq, s, b, n, k, "test.lfm.q4")
+    np.testing.assert_array_equal(y, y2)
+
+
+# ------------------------------------------------------------------ int8 GEMV ----
+
+@pytest.mark.parametrize("n", [576, 1536])
+def test_i8_gemv_smollm_config1(ops, n):
+    k = 576
+    w, s, x = make_i8(n, k, 1)
+    y = _run_i8(ops, w, s, x)
+    ref = oracle.qgemv_i8(w, s, x)
+    assert rel_err(y, ref) <= TOL_F32
+
+
+@pytest.mark.parametrize("k,n", [(1152, 1536), (1024, 1152)])
+@pytest.mark.parametrize("m", [1, 4])
+def test_i8_gemv_gemma_attn_f16x(ops, k, n, m):
+    w, s, x = make_i8(n, k, m, cfg=3, x_dtype=np.float16, salt=m)
+    y = _run_i8(ops, w, s, x)
+    ref = oracle.qgemv_i8(w, s, x)
+    assert rel_err(y, ref) <= TOL_F32
+
+
+def test_i8_logits_sync_reference_dtypes(ops):
+    """MetalOps::logits_i8 contract: f16 scales, f32 x, host in/out."""
+    k, n = 960, 2560
+    w, s, x = make_i8(n, k, 1, cfg=5, scale_dtype=np.float16)
+    sbits = s.view(np.uint16)
+    y = ops.logits_i8(x[0], w, sbits, n, k, "test.i8.logits")
+    ref = oracle.matmul_i8_f32(w, sbits, x[0])
+    assert rel_err(y, ref) <= TOL_F32
+
+
+def test_i8_bias_and_per_tensor_scale(ops):
+    import torch
+
+    k, n = 256, 300
+    w, s, x = make_i8(n, k, 2, salt=3)
+    bias = oracle.gen_normal((n,), seed(1, 5), 0.0, 1.0)
+    y = _run_i8(ops, w, s, x, bias=bias)
+    ref = oracle.qgemv_i8(w, s, x) + bias[None, :]
+    assert rel_err(y, ref) <= TOL_F32
+    # per-tensor scale: n_scales < n uses scale[0] (metal.rs:900)
+    s1 = s[:1].copy()
+    yt = torch.empty((2, n), dtype=torch.float32, device="cuda")
+    ops.encode_qgemv_i8(_t(w), _t(s1), _t(x), yt)
+    torch.cuda.synchronize()
+    ref1 = oracle.qgemv_i8(w, np.full(n, s1[0], np.float32), x)
+    assert rel_err(yt.cpu().numpy(), ref1) <= TOL_F32
+
+
+def test_i8_ragged_k(ops):
+    k, n = 40, 19  # k % 16 != 0 -> generic kernel
+    w, s, x = make_i8(n, k, 1, salt=9)
+    y = _run_i8(ops, w, s, x)
+    ref = oracle.qgemv_i8(w, s, x)
+    assert rel_err(y, ref) <= TOL_F32
+
+
+# ------------------------------------------------------------- batched / GEMM ----
+
+@pytest.mark.parametrize("m", [16, 64])
+def test_i8_batched_gemma_lm_head_slice(ops, m):
+    k, n = 1152, 8192  # slice of the 262144-row Gemma lm_head
+    w, s, x = make_i8(n, k, m, cfg=3, x_dtype=np.float16, salt=m)
+    y = _run_i8(ops, w, s, x)
+    ref = oracle.qgemv_i8(w, s, x)
+    assert rel_err(y, ref) <= TOL_F32  # int8 is exact in f16: f32-accumulation bar
+
+
+@pytest.mark.parametrize("m", [16, 64])
+def test_q4_batched_gemma_mlp(ops, m):
+    k, n = 1152, 13824
+    wq, s, b, x = make_q4(n, k, m, cfg=3, salt=m)
+    y = _run_q4(ops, wq, s, b, x)
+    ref32 = oracle.qgemv_q4_affine(wq, s, b, x, k)
+    assert rel_err(y, ref32) <= TOL_F16_TILE
+    w16 = oracle.f16_bits_to_f32(oracle.dequant_q4_affine_f16(wq, s, b, k))
+    ref16 = oracle.gemm_xwT(x, w16)
+    assert rel_err(y, ref16) <= TOL_F32
+
+
+@pytest.mark.parametrize("k,n", [(896, 4864), (4864, 896)])
+def test_q4_prefill_qgemm_m512(ops, k, n):
+    m = 512
+    wq, s, b, x = make_q4(n, k, m, cfg=4)
+    y = _run_q4(ops, wq, s, b, x, gemm=True)
+    w16 = oracle.f16_bits_to_f32(oracle.dequant_q4_affine_f16(wq, s, b, k))
+    ref16 = oracle.gemm_xwT(x, w16)
+    assert rel_err(y, ref16) <= TOL_F32
+    w32 = oracle.q4_affine_dequant_f32(wq, s, b, k)
+    ref32 = oracle.gemm_xwT(x, w32)
+    assert rel_err(y, ref32) <= TOL_F16_TILE
+
+
+def test_qgemm_ragged_m_n(ops):
+    m, k, n = 37, 192, 77
+    wq, s, b, x = make_q4(n, k, m, cfg=4, salt=5)
+    y = _run_q4(ops, wq, s, b, x, gemm=True)
+    w16 = oracle.f16_bits_to_f32(oracle.dequant_q4_affine_f16(wq, s, b, k))
+    assert rel_err(y, oracle.gemm_xwT(x, w16)) <= TOL_F32
+
+
+# ------------------------------------------------------------------- i4 sym ----
+
+def test_i4_sym_logits(ops):
+    k, n, gs = 512, 700, 128
+    w = oracle.gen_i8((n, k // 2), seed(6, 0)).view(np.uint8)
+    s = oracle.gen_uniform((n * (k // gs),), seed(6, 1), 1e-3, 2e-2).astype(np.float16).view(np.uint16)
+    x = oracle.gen_normal((k,), seed(6, 2), 0.0, 1.0)
+    y = ops.logits_i4(x, w, s, n, k, gs, "test.i4")
+    ref = oracle.matmul_i4_f32(w, s, n, k, gs, x)
+    assert rel_err(y, ref) <= TOL_F32
+
+
+# -------------------------------------------------------------- edge cases ----
+
+def test_empty_inputs_are_noops(ops):
+    import torch
+
+    w = torch.zeros((0, 64), dtype=torch.int8, device="cuda")
+    s = torch.ones(1, dtype=torch.float32, device="cuda")
+    x = torch.zeros((1, 64), dtype=torch.float32, device="cuda")
+    y = torch.zeros((1, 0), dtype=torch.float32, device="cuda")
+    ops.encode_qgemv_i8(w, s, x, y)
+    torch.cuda.synchronize()
+
+
+def test_k_zero_gives_zero(ops):
+    import torch
+
+    n = 10
+    w = torch.zeros((n, 0), dtype=torch.int8, device="cuda")
+    s = torch.ones(n, dtype=torch.float32, device="cuda")
+    x = torch.zeros((1, 0), dtype=torch.float32, device="cuda")
+    y = torch.full((1, n), 7.0, dtype=torch.float32, device="cuda")
+    from cellm_amd._lib import load
+    import ctypes as C
+
+    lib = load()
+    def ptr(t):
+        return C.c_void_p(t.data_ptr()) if t.data_ptr() else None
+
+    rc = lib.cellm_hip_qgemv_i8(ops.handle, ptr(w), ptr(s), 0, n, ptr(x), 0, None, ptr(y), 1, n, 0, None)
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert float(y.abs().max()) == 0.0
+
+
+def test_bad_k_is_rejected(ops):
+    import torch
+    from cellm_amd import CellmHipError
+
+    wq = torch.zeros((4, 1), dtype=torch.int32, device="cuda")
+    s = torch.ones((4, 1), dtype=torch.float16, device="cuda")
+    x = torch.zeros((1, 12), dtype=torch.float16, device="cuda")
+    y = torch.zeros((1, 4), dtype=torch.float32, device="cuda")
+    import ctypes as C
+    from cellm_amd._lib import load, last_error
+
+    rc = load().cellm_hip_qgemv_q4_affine(ops.handle, C.c_void_p(wq.data_ptr()), C.c_void_p(s.data_ptr()),
+                                          C.c_void_p(s.data_ptr()), 1, 64, C.c_void_p(x.data_ptr()), 1,
+                                          C.c_void_p(y.data_ptr()), 1, 4, 12, None)
+    assert rc == -1 and "multiple of 8" in last_error()
+    with pytest.raises(CellmHipError):
+        ops.weight_lookup("no.such.key")
