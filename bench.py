@@ -1,0 +1,294 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized-weight matmul path on one MI355X.
+
+A step is one decode pass (batch 1) over the five Qwen2.5-0.5B-shape MLX 4-bit
+affine projections of BASELINE.json configs[1]: 896->1152 (fused QKV),
+896->896, 896->9728 (gate+up), 4864->896, 896->151936 (lm_head), fp16 x,
+fp16 group-64 scales/biases.  Every step reads a different copy of the weights
+(copies total > 512 MB, twice the 256 MB Infinity Cache), so weights stream
+from HBM.  `value` = algorithmic bytes of the step / step time (GB/s).
+
+Extra keys report the other BASELINE configs (int8 GEMV, Gemma batched decode,
+M=512 prefill qGEMM) and the roofline of the dominant kernel (the lm_head GEMV),
+whose per-launch duration is measured with HIP events on the launch stream.
+cpu_baseline times the CPU oracle (a restatement of the reference CPU kernels)
+on a bounded sample of the same workload on the host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, published
+BASELINE_METRIC = "int4/int8 qGEMV µs & HBM GB/s (% peak); M=512 qGEMM TFLOP/s (% MFMA)"
+
+QWEN_SHAPES = [("qkv", 896, 1152), ("o", 896, 896), ("gate_up", 896, 9728), ("down", 4864, 896),
+               ("lm_head", 896, 151936)]
+
+
+def q4_bytes(m: int, n: int, k: int) -> int:
+    """Algorithmic bytes of one q4-affine g64 call: packed W + f16 S,B + f16 x + f32 y."""
+    return n * k // 2 + 4 * n * ((k + 63) // 64) + 2 * m * k + 4 * m * n
+
+
+def i8_bytes(m: int, n: int, k: int, x_bytes: int, s_bytes: int = 4) -> int:
+    return n * k + s_bytes * n + x_bytes * m * k + 4 * m * n
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-extra", action="store_true", help="skip the extra configs")
+    return ap.parse_args()
+
+
+class Q4Weights:
+    def __init__(self, torch, n: int, k: int, gen):
+        self.n, self.k = n, k
+        g = (k + 63) // 64
+        self.wq = torch.randint(-2**31, 2**31 - 1, (n, k // 8), dtype=torch.int32, device="cuda", generator=gen)
+        self.s = (torch.randn((n, g), device="cuda", generator=gen) * 0.005 + 0.02).abs_().to(torch.float16)
+        self.b = (torch.randn((n, g), device="cuda", generator=gen) * 0.05).to(torch.float16)
+
+
+def time_launches(torch, fn, reps: int, stream):
+    """Per-launch HIP-event timing on `stream`; returns mean ms per launch."""
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    for i in range(reps):
+        starts[i].record(stream)
+        fn(i)
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    return sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / reps
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 (sharding is described in "
+                                   "DESIGN.md, not implemented)"}))
+        sys.exit(2)
+
+    import torch
+
+    from cellm_amd import HipOps
+
+    assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    ops = HipOps(0)
+    stream = torch.cuda.current_stream()
+    sptr = stream.cuda_stream
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0xCE11)
+
+    # ---- the step -------------------------------------------------
+    step_bytes = sum(q4_bytes(1, n, k) for _, k, n in QWEN_SHAPES)
+    w_bytes_per_set = sum(n * k // 2 + 4 * n * ((k + 63) // 64) for _, k, n in QWEN_SHAPES)
+    copies = max(2, -(-512 * 2**20 // w_bytes_per_set) + 1)
+    sets = [[Q4Weights(torch, n, k, gen) for _, k, n in QWEN_SHAPES] for _ in range(copies)]
+    xs = [torch.randn((1, k), device="cuda", generator=gen).to(torch.float16) for _, k, _ in QWEN_SHAPES]
+    ys = [torch.empty((1, n), dtype=torch.float32, device="cuda") for _, _, n in QWEN_SHAPES]
+
+    def step(i):
+        ws = sets[i % copies]
+        for j in range(len(QWEN_SHAPES)):
+            w = ws[j]
+            ops.encode_qgemv_q4_affine(w.wq, w.s, w.b, xs[j], ys[j], stream=sptr)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for i in range(args.steps):
+        step(i)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_total = ev0.elapsed_time(ev1)
+    ms_per_step = ms_total / args.steps
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+
+    # ---- per-shape latency (rotating copies) and the dominant kernel's roofline --
+    per_shape = {}
+    for j, (name, k, n) in enumerate(QWEN_SHAPES):
+        def one(i, j=j):
+            w = sets[i % copies][j]
+            ops.encode_qgemv_q4_affine(w.wq, w.s, w.b, xs[j], ys[j], stream=sptr)
+        one(0)
+        ms = time_launches(torch, one, 100, stream)
+        gbs = q4_bytes(1, n, k) / (ms * 1e-3) / 1e9
+        per_shape[f"{name}_{k}x{n}"] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
+                                        "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+    dom = per_shape["lm_head_896x151936"]
+    traffic = None
+    tfile = ROOT / "profiles" / "traffic_q4_gemv_lm_head.json"
+    if tfile.exists():
+        try:
+            traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+        except Exception:
+            traffic = None
+    roofline = {"bound": "hbm", "achieved": dom["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(dom["GB/s"] / HBM_PEAK_GBS, 4), "traffic": traffic,
+                "kernel": "qgemv_q4_f16x_kernel (896->151936 lm_head, M=1)",
+                "algorithmic_bytes": q4_bytes(1, 151936, 896)}
+    del sets
+    torch.cuda.empty_cache()
+
+    extra = {}
+    if not args.no_extra:
+        extra = extra_configs(torch, ops, stream, gen)
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline()
+
+    out = {
+        "metric": BASELINE_METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u4*f16->f32",
+        "data": "synthetic (seeded random weights/activations of the config shapes)",
+        "config": {"workload": "qwen2.5-0.5b-shape q4-affine g64 decode GEMV set, batch 1: "
+                               "896->1152, 896->896, 896->9728, 4864->896, 896->151936",
+                   "weight_copies_rotated": copies, "bytes_per_step": step_bytes,
+                   "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4), "wall_s": round(wall, 3)},
+        "per_shape": per_shape,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(out))
+    ops.close()
+
+
+def extra_configs(torch, ops, stream, gen):
+    """configs[0], [2], [3]: int8 GEMV, Gemma batched decode, M=512 prefill qGEMM."""
+    sptr = stream.cuda_stream
+    res = {}
+
+    # SmolLM2-135M int8, fp32 scale, fp32 x, K=576
+    for n in (576, 1536):
+        k = 576
+        copies = max(2, -(-512 * 2**20 // (n * k)) + 1)
+        w = torch.randint(-127, 128, (copies, n, k), dtype=torch.int8, device="cuda", generator=gen)
+        s = torch.rand((n,), device="cuda", generator=gen) * 0.019 + 0.001
+        x = torch.randn((1, k), device="cuda", generator=gen)
+        y = torch.empty((1, n), dtype=torch.float32, device="cuda")
+        fn = lambda i: ops.encode_qgemv_i8(w[i % copies], s, x, y, stream=sptr)
+        fn(0)
+        ms = time_launches(torch, fn, 200, stream)
+        b = i8_bytes(1, n, k, 4)
+        res[f"cfg1_i8_576x{n}"] = {"us": round(ms * 1e3, 3), "GB/s": round(b / (ms * 1e-3) / 1e9, 1)}
+        del w
+
+    # Gemma-3-1B int8 lm_head 1152->262144 and q4 gate+up 1152->13824 at M in {1,4,16,64}
+    k, n = 1152, 262144
+    copies = 2
+    w = torch.randint(-127, 128, (copies, n, k), dtype=torch.int8, device="cuda", generator=gen)
+    s = torch.rand((n,), device="cuda", generator=gen) * 0.019 + 0.001
+    for m in (1, 4, 16, 64):
+        x = torch.randn((m, k), device="cuda", generator=gen).to(torch.float16)
+        y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        fn = lambda i: ops.encode_qgemv_i8(w[i % copies], s, x, y, stream=sptr)
+        fn(0)
+        ms = time_launches(torch, fn, 20, stream)
+        b = i8_bytes(m, n, k, 2)
+        res[f"cfg3_i8_lm_head_1152x262144_m{m}"] = {"us": round(ms * 1e3, 2), "GB/s": round(b / (ms * 1e-3) / 1e9, 1),
+                                                    "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    del w
+    k, n = 1152, 13824
+    wset = [Q4Weights(torch, n, k, gen) for _ in range(64)]
+    for m in (1, 4, 16, 64):
+        x = torch.randn((m, k), device="cuda", generator=gen).to(torch.float16)
+        y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        fn = lambda i: ops.encode_qgemv_q4_affine(wset[i % 64].wq, wset[i % 64].s, wset[i % 64].b, x, y, stream=sptr)
+        fn(0)
+        ms = time_launches(torch, fn, 100, stream)
+        b = q4_bytes(m, n, k)
+        res[f"cfg3_q4_gate_up_1152x13824_m{m}"] = {"us": round(ms * 1e3, 2), "GB/s": round(b / (ms * 1e-3) / 1e9, 1),
+                                                   "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    del wset
+
+    # M=512 prefill qGEMM (MFMA)
+    m = 512
+    for k, n in ((896, 4864), (4864, 896)):
+        w = Q4Weights(torch, n, k, gen)
+        x = torch.randn((m, k), device="cuda", generator=gen).to(torch.float16)
+        y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        fn = lambda i: ops.encode_qgemm_q4_affine(w.wq, w.s, w.b, x, y, stream=sptr)
+        fn(0)
+        ms = time_launches(torch, fn, 100, stream)
+        tflops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+        res[f"cfg4_qgemm_m512_{k}x{n}"] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tflops, 1),
+                                           "frac_mfma_f16": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
+    return res
+
+
+def cpu_baseline():
+    """The CPU oracle timed on the host cores on a bounded sample of the step.
+
+    Reference CPU work per decode token for configs[1] (LfmRunner, lfm.rs):
+    the four linear projections hit the f32 dequant cache and run the f32 row
+    GEMV (lfm.rs:1056-1063, 'warm'); the tied lm_head dequantizes on the fly
+    (lfm.rs:700-741).  Timed over a few such passes.
+    """
+    import numpy as np
+
+    import oracle
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
+    rng = np.random.default_rng(0xCE11)
+    lin = []
+    for name, k, n in QWEN_SHAPES[:-1]:
+        wq = rng.integers(0, 2**32, (n, k // 8), dtype=np.uint32)
+        s = (np.abs(rng.normal(0.02, 0.005, (n, k // 64)))).astype(np.float32)
+        b = rng.normal(0.0, 0.05, (n, k // 64)).astype(np.float32)
+        lin.append((oracle.q4_affine_dequant_f32(wq, s, b, k), rng.normal(size=k).astype(np.float32)))
+    k, n = 896, 151936
+    wq = rng.integers(0, 2**32, (n, k // 8), dtype=np.uint32)
+    s = (np.abs(rng.normal(0.02, 0.005, (n, k // 64)))).astype(np.float32)
+    b = rng.normal(0.0, 0.05, (n, k // 64)).astype(np.float32)
+    x = rng.normal(size=k).astype(np.float32)
+
+    def one_pass():
+        for w32, xv in lin:
+            oracle.matmul_f32(w32, xv.reshape(-1, 1))
+        oracle.lfm_lm_head_q4_affine(wq, s, b, x, n, k)
+
+    one_pass()
+    times = []
+    t_end = time.perf_counter() + 10.0
+    while time.perf_counter() < t_end and len(times) < 50:
+        t0 = time.perf_counter()
+        one_pass()
+        times.append(time.perf_counter() - t0)
+    med = sorted(times)[len(times) // 2]
+    step_bytes = sum(q4_bytes(1, n_, k_) for _, k_, n_ in QWEN_SHAPES)
+    return {"value": round(step_bytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "ms_per_step": round(med * 1e3, 3),
+            "sample": f"{len(times)} decode passes over the 5 configs[1] projections (4 warm f32-cache GEMVs + "
+                      "on-the-fly affine lm_head, lfm.rs:700-741,1056-1063), median; C oracle, OpenMP over rows"}
+
+
+if __name__ == "__main__":
+    main()

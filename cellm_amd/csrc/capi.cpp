@@ -102,10 +102,10 @@ struct DeviceGuard {
     }
 };
 
-hipStream_t pick_stream(cellm_hip_ctx* ctx, void* stream)
-{
-    return stream ? reinterpret_cast<hipStream_t>(stream) : ctx->stream;
-}
+// Async entry points take the caller's stream as is: NULL is HIP's default
+// (null) stream, as in the HIP API.  The context's own stream is only used by
+// the sync logits_* wrappers (and is available via cellm_hip_get_stream).
+hipStream_t pick_stream(cellm_hip_ctx* /*ctx*/, void* stream) { return reinterpret_cast<hipStream_t>(stream); }
 
 int32_t check_ctx(cellm_hip_ctx* ctx)
 {

@@ -34,6 +34,32 @@ __device__ __forceinline__ float load_f32(const void* p, size_t i)
     }
 }
 
+// Split load/convert: load_raw issues the memory access and returns the
+// stored bits; raw_to_f32 widens them at the point of use.  Keeping the
+// conversion away from the load lets the compiler leave the load in flight
+// (a conversion right after a load forces an s_waitcnt on every earlier load).
+template <int DT>
+__device__ __forceinline__ uint32_t load_raw(const void* p, size_t i)
+{
+    if constexpr (DT == DT_F32) {
+        return reinterpret_cast<const uint32_t*>(p)[i];
+    } else {
+        return (uint32_t)reinterpret_cast<const uint16_t*>(p)[i];
+    }
+}
+
+template <int DT>
+__device__ __forceinline__ float raw_to_f32(uint32_t r)
+{
+    if constexpr (DT == DT_F32) {
+        return __builtin_bit_cast(float, r);
+    } else if constexpr (DT == DT_F16) {
+        return (float)__builtin_bit_cast(_Float16, (uint16_t)r);
+    } else {
+        return __builtin_bit_cast(float, r << 16);
+    }
+}
+
 // v_and_or_b32: (a & mask) | bits in one VOP3 op.  gfx9 VOP3 can encode
 // neither a literal nor more than one SGPR operand, so the mask comes from an
 // SGPR and the OR constant from a VGPR the compiler hoists out of the loops.

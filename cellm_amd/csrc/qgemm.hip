@@ -84,39 +84,31 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(const void* __restrict_
     // global -> register staging assignment
     const int ld_row = tid >> 1;        // 0..127
     const int ld_half = tid & 1;        // which 32-element half of the 64-wide K stage
-    const int xm = m0 + ld_row, wn_row = n0 + ld_row;
-    const int gpr = (K + group_size - 1) / group_size;
+    // Rows past M or N are clamped to the last valid row: their loads stay in
+    // bounds without a branch and their results are never stored.
+    const int xm = min(m0 + ld_row, M - 1), wn_row = min(n0 + ld_row, N - 1);
+    const int gshift = __builtin_ctz((unsigned)group_size);
+    const int gpr = (K + group_size - 1) >> gshift;
 
     u4_t xr[4];
-    u4_t wr;      // q4: 4 words (32 nibbles); int8: 2 x u2 (32 bytes) -> use wr and wr2
+    u4_t wr;      // q4: 4 words (32 nibbles); int8: 16 bytes (wr) + 16 bytes (wr2)
     u4_t wr2;
-    float sc = 0.0f, bi = 0.0f;
+    uint32_t sraw = 0, braw = 0;  // scale/bias bits, converted when the tile is stored
 
+    // K % 64 == 0 and k_per_split % 64 == 0, so every stage lies inside [kbeg, kend).
     auto load_stage = [&](int k0) {
         const int kc = k0 + ld_half * 32;
-        const bool kin = kc < kend;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            xr[i] = (xm < M && kin) ? *reinterpret_cast<const u4_t*>(X + (size_t)xm * K + kc + i * 8)
-                                    : u4_t{0u, 0u, 0u, 0u};
-        }
+        for (int i = 0; i < 4; ++i) xr[i] = *reinterpret_cast<const u4_t*>(X + (size_t)xm * K + kc + i * 8);
+        const u4_t* w4 = reinterpret_cast<const u4_t*>(W);
         if constexpr (WT == 0) {
-            const u4_t* w4 = reinterpret_cast<const u4_t*>(W);
-            const bool ok = wn_row < N && kin;
-            wr = ok ? __builtin_nontemporal_load(w4 + ((size_t)wn_row * K + kc) / 32) : u4_t{0u, 0u, 0u, 0u};
-            if (ok) {
-                const int g = kc / group_size;
-                sc = load_f32<SBT>(S, (size_t)wn_row * gpr + g);
-                bi = load_f32<SBT>(Bz, (size_t)wn_row * gpr + g);
-            } else {
-                sc = 0.0f;
-                bi = 0.0f;
-            }
+            wr = __builtin_nontemporal_load(w4 + ((size_t)wn_row * K + kc) / 32);
+            const size_t gi = (size_t)wn_row * gpr + (kc >> gshift);
+            sraw = load_raw<SBT>(S, gi);
+            braw = load_raw<SBT>(Bz, gi);
         } else {
-            const u4_t* w4 = reinterpret_cast<const u4_t*>(W);
-            const bool ok = wn_row < N && kin;
-            wr = ok ? __builtin_nontemporal_load(w4 + ((size_t)wn_row * K + kc) / 16) : u4_t{0u, 0u, 0u, 0u};
-            wr2 = ok ? __builtin_nontemporal_load(w4 + ((size_t)wn_row * K + kc) / 16 + 1) : u4_t{0u, 0u, 0u, 0u};
+            wr = __builtin_nontemporal_load(w4 + ((size_t)wn_row * K + kc) / 16);
+            wr2 = __builtin_nontemporal_load(w4 + ((size_t)wn_row * K + kc) / 16 + 1);
         }
     };
 
@@ -126,6 +118,7 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(const void* __restrict_
         for (int i = 0; i < 4; ++i) *reinterpret_cast<u4_t*>(xd + i * 8) = xr[i];
         _Float16* wd = ws + ld_row * LDS_STRIDE + ld_half * 32;
         if constexpr (WT == 0) {
+            const float sc = raw_to_f32<SBT>(sraw), bi = raw_to_f32<SBT>(braw);
 #pragma unroll
             for (int i = 0; i < 4; ++i) *reinterpret_cast<h8_t*>(wd + i * 8) = dequant_word_f16<SBT>(wr[i], sc, bi);
         } else {

@@ -38,50 +38,129 @@ namespace {
 constexpr int kBlock = 256;
 constexpr int kUnroll = 4;  // chunks per lane held in registers per pass
 
+// Load order inside every kernel below: (1) this thread's activation words,
+// (2) all weight chunks and their scale/bias bits for the first pass, (3)
+// stage the activations into LDS.  Loads retire in issue order, so (3) waits
+// only for (1) and the weight stream stays in flight while x is staged; the
+// scale/bias bits are converted at their use, never right after the load.
+
 // ---------------------------------------------------------------------------
 // q4 affine, f16 activations
 // ---------------------------------------------------------------------------
 
-// Stage x[M,K] (f16) into LDS as dot2 pairs plus per-chunk (corr, xsum).
+// One 8-element activation word -> LDS as the pairs (x0,x4), (x1/16,x5/16),
+// (x2,x6), (x3/16,x7/16), plus per-chunk (corr, xsum) summed over the four
+// words of a chunk, which sit in four adjacent lanes.
 // xq layout: [MT][CPR][16] uint32; cx layout: [MT][CPR] float2.
-template <int MT>
-__device__ void stage_x_q4(const _Float16* __restrict__ x, int M, int K, uint32_t* xq, float2* cx)
+__device__ __forceinline__ void stage_word_q4(u4_t raw, int idx, bool valid, uint32_t* xq, float2* cx)
 {
-    const int CPR = K >> 5;
-    const int words = CPR * 4;  // 8-element words per activation row
-    const int total = MT * words;
-    const uint32_t tid = threadIdx.x;
-    for (int base = 0; base < total; base += kBlock) {
-        const int idx = base + (int)tid;
-        const bool valid = idx < total;
-        const int m = valid ? idx / words : 0;
-        const int wdx = valid ? idx - m * words : 0;  // word within the row
-        uint4 raw = make_uint4(0, 0, 0, 0);
-        if (valid && m < M) raw = *reinterpret_cast<const uint4*>(x + (size_t)m * K + (size_t)wdx * 8);
-        h8_t v = __builtin_bit_cast(h8_t, raw);
-        // pairs (x0,x4), (x1/16,x5/16), (x2,x6), (x3/16,x7/16)
-        const _Float16 inv16 = (_Float16)0.0625f;
-        h2_t p0 = {v[0], v[4]};
-        h2_t p1 = {v[1] * inv16, v[5] * inv16};
-        h2_t p2 = {v[2], v[6]};
-        h2_t p3 = {v[3] * inv16, v[7] * inv16};
-        float corr = ((float)p0[0] + (float)p0[1]) + ((float)p1[0] + (float)p1[1]) +
-                     ((float)p2[0] + (float)p2[1]) + ((float)p3[0] + (float)p3[1]);
-        float xs = 0.0f;
+    h8_t v = __builtin_bit_cast(h8_t, raw);
+    const _Float16 inv16 = (_Float16)0.0625f;
+    h2_t p0 = {v[0], v[4]};
+    h2_t p1 = {v[1] * inv16, v[5] * inv16};
+    h2_t p2 = {v[2], v[6]};
+    h2_t p3 = {v[3] * inv16, v[7] * inv16};
+    float corr = ((float)p0[0] + (float)p0[1]) + ((float)p1[0] + (float)p1[1]) +
+                 ((float)p2[0] + (float)p2[1]) + ((float)p3[0] + (float)p3[1]);
+    float xs = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) xs += (float)v[i];
-        if (valid) {
-            uint4 o = make_uint4(as_u32(p0), as_u32(p1), as_u32(p2), as_u32(p3));
-            *reinterpret_cast<uint4*>(xq + (size_t)idx * 4) = o;
+    for (int i = 0; i < 8; ++i) xs += (float)v[i];
+    if (valid) *reinterpret_cast<u4_t*>(xq + (size_t)idx * 4) = u4_t{as_u32(p0), as_u32(p1), as_u32(p2), as_u32(p3)};
+    corr = group_sum<4>(corr);
+    xs = group_sum<4>(xs);
+    if (valid && (idx & 3) == 0) cx[idx >> 2] = make_float2(1024.0f * corr, xs);
+}
+
+template <int XW>
+__device__ __forceinline__ void load_x_words(const _Float16* __restrict__ x, int M, int K, int total, u4_t (&xr)[XW])
+{
+    const int words = K >> 3;
+#pragma unroll
+    for (int j = 0; j < XW; ++j) {
+        // clamped, branch-free: padding rows m >= M and words past `total`
+        // read valid data whose results are never stored
+        const int idx = min((int)threadIdx.x + j * kBlock, total - 1);
+        const int m = idx / words;
+        const int mc = min(m, M - 1);
+        xr[j] = *reinterpret_cast<const u4_t*>(x + (size_t)mc * K + (size_t)(idx - m * words) * 8);
+    }
+}
+
+template <int LPR, int R, int SBT>
+__device__ __forceinline__ void load_pass_q4(const u4_t* __restrict__ wq, const void* __restrict__ S,
+                                             const void* __restrict__ B, int row0, int c0, int N, int CPR, int gpr,
+                                             int gshift, u4_t (&wv)[kUnroll][R], uint32_t (&sr)[kUnroll][R],
+                                             uint32_t (&br)[kUnroll][R])
+{
+    // Addresses are clamped into the matrix instead of branching around the
+    // loads: a lane whose chunk or row is out of range loads a valid element
+    // and its result is never used (compute skips c >= CPR, rows >= N are not
+    // stored).  Branch-free loads keep every conversion away from its load.
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const int c = min(c0 + u * LPR, CPR - 1);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int n = min(row0 + r, N - 1);
+            wv[u][r] = __builtin_nontemporal_load(wq + (size_t)n * CPR + c);
+            const size_t gi = (size_t)n * gpr + ((c << 5) >> gshift);
+            sr[u][r] = load_raw<SBT>(S, gi);
+            br[u][r] = load_raw<SBT>(B, gi);
         }
-        // four consecutive words form one chunk; they sit in four adjacent lanes
-        corr = group_sum<4>(corr);
-        xs = group_sum<4>(xs);
-        if (valid && (wdx & 3) == 0) cx[idx >> 2] = make_float2(1024.0f * corr, xs);
     }
 }
 
 template <int LPR, int R, int MT, int SBT>
+__device__ __forceinline__ void compute_pass_q4(int c0, int CPR, const uint32_t* xq, const float2* cx,
+                                                const u4_t (&wv)[kUnroll][R], const uint32_t (&sr)[kUnroll][R],
+                                                const uint32_t (&br)[kUnroll][R], float (&acc)[R][MT])
+{
+    const uint32_t m0f = 0x000F000Fu, m1f = 0x00F000F0u, magic = 0x64006400u;
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const int c = c0 + u * LPR;
+        if (c < CPR) {
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                const u4_t* xp = reinterpret_cast<const u4_t*>(xq + ((size_t)m * CPR + c) * 16);
+                const u4_t xa = xp[0], xb = xp[1], xc = xp[2], xd = xp[3];
+                const float2 cc = cx[(size_t)m * CPR + c];
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const u4_t w = wv[u][r];
+                    float d = -cc.x;
+                    uint32_t h;
+                    d = dot2(and_or(w[0], m0f, magic), xa[0], d);
+                    d = dot2(and_or(w[0], m1f, magic), xa[1], d);
+                    h = w[0] >> 8;
+                    d = dot2(and_or(h, m0f, magic), xa[2], d);
+                    d = dot2(and_or(h, m1f, magic), xa[3], d);
+                    d = dot2(and_or(w[1], m0f, magic), xb[0], d);
+                    d = dot2(and_or(w[1], m1f, magic), xb[1], d);
+                    h = w[1] >> 8;
+                    d = dot2(and_or(h, m0f, magic), xb[2], d);
+                    d = dot2(and_or(h, m1f, magic), xb[3], d);
+                    d = dot2(and_or(w[2], m0f, magic), xc[0], d);
+                    d = dot2(and_or(w[2], m1f, magic), xc[1], d);
+                    h = w[2] >> 8;
+                    d = dot2(and_or(h, m0f, magic), xc[2], d);
+                    d = dot2(and_or(h, m1f, magic), xc[3], d);
+                    d = dot2(and_or(w[3], m0f, magic), xd[0], d);
+                    d = dot2(and_or(w[3], m1f, magic), xd[1], d);
+                    h = w[3] >> 8;
+                    d = dot2(and_or(h, m0f, magic), xd[2], d);
+                    d = dot2(and_or(h, m1f, magic), xd[3], d);
+                    acc[r][m] += raw_to_f32<SBT>(sr[u][r]) * d + raw_to_f32<SBT>(br[u][r]) * cc.y;
+                }
+            }
+        }
+    }
+}
+
+// MP: rows need more than one pass of kUnroll chunks per lane; the next pass
+// is prefetched into a second register set (ping-pong) before the current one
+// is consumed.
+template <int LPR, int R, int MT, int SBT, bool MP>
 __global__ __launch_bounds__(kBlock) void qgemv_q4_f16x_kernel(
     const u4_t* __restrict__ wq, const void* __restrict__ S, const void* __restrict__ B,
     const _Float16* __restrict__ x, float* __restrict__ y, int M, int N, int K, int gshift)
@@ -94,22 +173,31 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_f16x_kernel(
     const int team = threadIdx.x / LPR;
     const int lane = threadIdx.x % LPR;
     const int row0 = (blockIdx.x * (kBlock / LPR) + team) * R;
-    const int gpr = (K + (1 << gshift) - 1) >> gshift;  // groups per row
+    const int gpr = (K + (1 << gshift) - 1) >> gshift;
+    const int total = MT * (K >> 3);
 
-    // Issue the first pass of weight loads before staging x.
-    u4_t wv[kUnroll][R];
+    constexpr int XW = MT == 1 ? 4 : 8;
+    u4_t xr[XW];
+    load_x_words<XW>(x, M, K, total, xr);
+
+    u4_t wa[kUnroll][R];
+    uint32_t sa[kUnroll][R], ba[kUnroll][R];
+    load_pass_q4<LPR, R, SBT>(wq, S, B, row0, lane, N, CPR, gpr, gshift, wa, sa, ba);
+
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-        const int c = lane + u * LPR;
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int n = row0 + r;
-            wv[u][r] = (c < CPR && n < N) ? __builtin_nontemporal_load(wq + (size_t)n * CPR + c)
-                                          : u4_t{0u, 0u, 0u, 0u};
-        }
+    for (int j = 0; j < XW; ++j) {
+        const int idx = (int)threadIdx.x + j * kBlock;
+        stage_word_q4(xr[j], idx, idx < total, xq, cx);
     }
-
-    stage_x_q4<MT>(x, M, K, xq, cx);
+    for (int base = XW * kBlock; base < total; base += kBlock) {  // large M*K only
+        const int idx = base + (int)threadIdx.x;
+        const int words = K >> 3;
+        const int m = idx / words;
+        u4_t raw = (idx < total && m < M)
+                       ? *reinterpret_cast<const u4_t*>(x + (size_t)m * K + (size_t)(idx - m * words) * 8)
+                       : u4_t{0u, 0u, 0u, 0u};
+        stage_word_q4(raw, idx, idx < total, xq, cx);
+    }
     __syncthreads();
     if (row0 >= N) return;
 
@@ -119,66 +207,19 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_f16x_kernel(
 #pragma unroll
         for (int m = 0; m < MT; ++m) acc[r][m] = 0.0f;
 
-    const uint32_t m0f = 0x000F000Fu, m1f = 0x00F000F0u, magic = 0x64006400u;
-    for (int cbase = 0; cbase < CPR; cbase += kUnroll * LPR) {
-        if (cbase != 0) {
-#pragma unroll
-            for (int u = 0; u < kUnroll; ++u) {
-                const int c = cbase + lane + u * LPR;
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const int n = row0 + r;
-                    wv[u][r] = (c < CPR && n < N) ? __builtin_nontemporal_load(wq + (size_t)n * CPR + c)
-                                                  : u4_t{0u, 0u, 0u, 0u};
-                }
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            const int c = cbase + lane + u * LPR;
-            if (c < CPR) {
-                const int g = (c << 5) >> gshift;
-                float sc[R], bi[R];
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const int n = min(row0 + r, N - 1);
-                    sc[r] = load_f32<SBT>(S, (size_t)n * gpr + g);
-                    bi[r] = load_f32<SBT>(B, (size_t)n * gpr + g);
-                }
-#pragma unroll
-                for (int m = 0; m < MT; ++m) {
-                    const uint4* xp = reinterpret_cast<const uint4*>(xq + ((size_t)m * CPR + c) * 16);
-                    const uint4 xa = xp[0], xb = xp[1], xc = xp[2], xd = xp[3];
-                    const float2 cc = cx[(size_t)m * CPR + c];
-#pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        const u4_t w = wv[u][r];
-                        float d = -cc.x;
-                        uint32_t h;
-                        d = dot2(and_or(w[0], m0f, magic), xa.x, d);
-                        d = dot2(and_or(w[0], m1f, magic), xa.y, d);
-                        h = w[0] >> 8;
-                        d = dot2(and_or(h, m0f, magic), xa.z, d);
-                        d = dot2(and_or(h, m1f, magic), xa.w, d);
-                        d = dot2(and_or(w[1], m0f, magic), xb.x, d);
-                        d = dot2(and_or(w[1], m1f, magic), xb.y, d);
-                        h = w[1] >> 8;
-                        d = dot2(and_or(h, m0f, magic), xb.z, d);
-                        d = dot2(and_or(h, m1f, magic), xb.w, d);
-                        d = dot2(and_or(w[2], m0f, magic), xc.x, d);
-                        d = dot2(and_or(w[2], m1f, magic), xc.y, d);
-                        h = w[2] >> 8;
-                        d = dot2(and_or(h, m0f, magic), xc.z, d);
-                        d = dot2(and_or(h, m1f, magic), xc.w, d);
-                        d = dot2(and_or(w[3], m0f, magic), xd.x, d);
-                        d = dot2(and_or(w[3], m1f, magic), xd.y, d);
-                        h = w[3] >> 8;
-                        d = dot2(and_or(h, m0f, magic), xd.z, d);
-                        d = dot2(and_or(h, m1f, magic), xd.w, d);
-                        acc[r][m] += sc[r] * d + bi[r] * cc.y;
-                    }
-                }
-            }
+    if constexpr (!MP) {
+        compute_pass_q4<LPR, R, MT, SBT>(lane, CPR, xq, cx, wa, sa, ba, acc);
+    } else {
+        constexpr int P = kUnroll * LPR;
+        u4_t wb[kUnroll][R];
+        uint32_t sb[kUnroll][R], bb[kUnroll][R];
+        for (int c0 = lane; c0 < CPR + lane; c0 += 2 * P) {
+            if (c0 - lane + P < CPR) load_pass_q4<LPR, R, SBT>(wq, S, B, row0, c0 + P, N, CPR, gpr, gshift, wb, sb, bb);
+            compute_pass_q4<LPR, R, MT, SBT>(c0, CPR, xq, cx, wa, sa, ba, acc);
+            if (c0 - lane + P >= CPR) break;
+            if (c0 - lane + 2 * P < CPR)
+                load_pass_q4<LPR, R, SBT>(wq, S, B, row0, c0 + 2 * P, N, CPR, gpr, gshift, wa, sa, ba);
+            compute_pass_q4<LPR, R, MT, SBT>(c0 + P, CPR, xq, cx, wb, sb, bb, acc);
         }
     }
 
@@ -204,182 +245,179 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_f16x_kernel(
 // int8 per-row scale
 // ---------------------------------------------------------------------------
 
-// f16 activations: xq[MT][CPR][8] uint32 pairs (x0,x2),(x1,x3) per word; cx[MT][CPR] = 1152*sum(x)
-template <int MT>
-__device__ void stage_x_i8_f16(const _Float16* __restrict__ x, int M, int K, uint32_t* xq, float* cx)
+// f16 activations, 8 elements per unit: pairs (x0,x2),(x1,x3),(x4,x6),(x5,x7);
+// xq [MT][CPR][8] uint32, cx [MT][CPR] = 1152*sum(x) over the 16-element chunk
+// (two units in adjacent lanes).
+__device__ __forceinline__ void stage_unit_i8(u4_t raw, int idx, bool valid, uint32_t* xq, float* cx)
 {
-    const int CPR = K >> 4;
-    const int quads = CPR * 2;  // 8-element units; 2 per 16-byte chunk
-    const int total = MT * quads;
-    const uint32_t tid = threadIdx.x;
-    for (int base = 0; base < total; base += kBlock) {
-        const int idx = base + (int)tid;
-        const bool valid = idx < total;
-        const int m = valid ? idx / quads : 0;
-        const int q = valid ? idx - m * quads : 0;
-        uint4 raw = make_uint4(0, 0, 0, 0);
-        if (valid && m < M) raw = *reinterpret_cast<const uint4*>(x + (size_t)m * K + (size_t)q * 8);
-        h8_t v = __builtin_bit_cast(h8_t, raw);
-        h2_t p0 = {v[0], v[2]}, p1 = {v[1], v[3]}, p2 = {v[4], v[6]}, p3 = {v[5], v[7]};
-        float s = 0.0f;
+    h8_t v = __builtin_bit_cast(h8_t, raw);
+    h2_t p0 = {v[0], v[2]}, p1 = {v[1], v[3]}, p2 = {v[4], v[6]}, p3 = {v[5], v[7]};
+    float s = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) s += (float)v[i];
-        if (valid) {
-            uint4 o = make_uint4(as_u32(p0), as_u32(p1), as_u32(p2), as_u32(p3));
-            *reinterpret_cast<uint4*>(xq + (size_t)idx * 4) = o;
+    for (int i = 0; i < 8; ++i) s += (float)v[i];
+    if (valid) *reinterpret_cast<u4_t*>(xq + (size_t)idx * 4) = u4_t{as_u32(p0), as_u32(p1), as_u32(p2), as_u32(p3)};
+    s = group_sum<2>(s);
+    if (valid && (idx & 1) == 0) cx[idx >> 1] = 1152.0f * s;
+}
+
+template <int LPR, int R>
+__device__ __forceinline__ void load_pass_i8(const u4_t* __restrict__ w8, int row0, int c0, int N, int CPR,
+                                             u4_t (&wv)[kUnroll][R])
+{
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const int c = min(c0 + u * LPR, CPR - 1);  // clamped, branch-free (see load_pass_q4)
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int n = min(row0 + r, N - 1);
+            wv[u][r] = __builtin_nontemporal_load(w8 + (size_t)n * CPR + c);
         }
-        s = group_sum<2>(s);
-        if (valid && (q & 1) == 0) cx[idx >> 1] = 1152.0f * s;
     }
 }
 
 template <int LPR, int R, int MT>
-__global__ __launch_bounds__(kBlock) void qgemv_i8_f16x_kernel(
-    const u4_t* __restrict__ w8, const void* __restrict__ S, int sdt, int per_channel,
-    const _Float16* __restrict__ x, const float* __restrict__ bias, float* __restrict__ y, int M, int N, int K)
+__device__ __forceinline__ void compute_pass_i8_f16x(int c0, int CPR, const uint32_t* xq, const float* cx,
+                                                     const u4_t (&wv)[kUnroll][R], float (&acc)[R][MT])
 {
-    extern __shared__ __align__(16) uint32_t lds[];
-    const int CPR = K >> 4;
-    uint32_t* xq = lds;
-    float* cx = reinterpret_cast<float*>(lds + (size_t)MT * CPR * 8);
-
-    const int team = threadIdx.x / LPR;
-    const int lane = threadIdx.x % LPR;
-    const int row0 = (blockIdx.x * (kBlock / LPR) + team) * R;
-
-    u4_t wv[kUnroll][R];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-        const int c = lane + u * LPR;
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int n = row0 + r;
-            wv[u][r] = (c < CPR && n < N) ? __builtin_nontemporal_load(w8 + (size_t)n * CPR + c)
-                                          : u4_t{0u, 0u, 0u, 0u};
-        }
-    }
-
-    stage_x_i8_f16<MT>(x, M, K, xq, cx);
-    __syncthreads();
-    if (row0 >= N) return;
-
-    float acc[R][MT];
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int m = 0; m < MT; ++m) acc[r][m] = 0.0f;
-
     const uint32_t mlo = 0x00FF00FFu, magic = 0x64006400u;
-    for (int cbase = 0; cbase < CPR; cbase += kUnroll * LPR) {
-        if (cbase != 0) {
 #pragma unroll
-            for (int u = 0; u < kUnroll; ++u) {
-                const int c = cbase + lane + u * LPR;
+    for (int u = 0; u < kUnroll; ++u) {
+        const int c = c0 + u * LPR;
+        if (c < CPR) {
+            uint32_t lo[R][4], hi[R][4];
 #pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const int n = row0 + r;
-                    wv[u][r] = (c < CPR && n < N) ? __builtin_nontemporal_load(w8 + (size_t)n * CPR + c)
-                                                  : u4_t{0u, 0u, 0u, 0u};
+            for (int r = 0; r < R; ++r) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const uint32_t b = wv[u][r][t] ^ 0x80808080u;
+                    lo[r][t] = and_or(b, mlo, magic);
+                    hi[r][t] = and_or(b >> 8, mlo, magic);
                 }
             }
-        }
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            const int c = cbase + lane + u * LPR;
-            if (c < CPR) {
-                uint32_t lo[R][4], hi[R][4];
+            for (int m = 0; m < MT; ++m) {
+                const u4_t* xp = reinterpret_cast<const u4_t*>(xq + ((size_t)m * CPR + c) * 8);
+                const u4_t xa = xp[0], xb = xp[1];
+                const float corr = cx[(size_t)m * CPR + c];
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
-                    const uint32_t wd[4] = {wv[u][r][0], wv[u][r][1], wv[u][r][2], wv[u][r][3]};
-#pragma unroll
-                    for (int t = 0; t < 4; ++t) {
-                        const uint32_t b = wd[t] ^ 0x80808080u;
-                        lo[r][t] = and_or(b, mlo, magic);
-                        hi[r][t] = and_or(b >> 8, mlo, magic);
-                    }
+                    float d = acc[r][m] - corr;
+                    d = dot2(lo[r][0], xa[0], d);
+                    d = dot2(hi[r][0], xa[1], d);
+                    d = dot2(lo[r][1], xa[2], d);
+                    d = dot2(hi[r][1], xa[3], d);
+                    d = dot2(lo[r][2], xb[0], d);
+                    d = dot2(hi[r][2], xb[1], d);
+                    d = dot2(lo[r][3], xb[2], d);
+                    d = dot2(hi[r][3], xb[3], d);
+                    acc[r][m] = d;
                 }
-#pragma unroll
-                for (int m = 0; m < MT; ++m) {
-                    const uint4* xp = reinterpret_cast<const uint4*>(xq + ((size_t)m * CPR + c) * 8);
-                    const uint4 xa = xp[0], xb = xp[1];
-                    const float corr = cx[(size_t)m * CPR + c];
-#pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        float d = acc[r][m] - corr;
-                        d = dot2(lo[r][0], xa.x, d);
-                        d = dot2(hi[r][0], xa.y, d);
-                        d = dot2(lo[r][1], xa.z, d);
-                        d = dot2(hi[r][1], xa.w, d);
-                        d = dot2(lo[r][2], xb.x, d);
-                        d = dot2(hi[r][2], xb.y, d);
-                        d = dot2(lo[r][3], xb.z, d);
-                        d = dot2(hi[r][3], xb.w, d);
-                        acc[r][m] = d;
-                    }
-                }
-            }
-        }
-    }
-
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int m = 0; m < MT; ++m) acc[r][m] = group_sum<LPR>(acc[r][m]);
-
-    if (lane == 0) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int n = row0 + r;
-            if (n < N) {
-                const size_t si = per_channel ? (size_t)n : 0;
-                const float s = sdt == DT_F32 ? load_f32<DT_F32>(S, si)
-                              : sdt == DT_F16 ? load_f32<DT_F16>(S, si)
-                                              : load_f32<DT_BF16>(S, si);
-                const float bv = bias ? bias[n] : 0.0f;
-#pragma unroll
-                for (int m = 0; m < MT; ++m)
-                    if (m < M) {
-                        float v = acc[r][m] * s;
-                        if (bias) v += bv;
-                        y[(size_t)m * N + n] = v;
-                    }
             }
         }
     }
 }
 
-// f32 activations: exact int8 -> f32 conversion (v_cvt_f32_i32 with byte select) and f32 FMA.
 template <int LPR, int R, int MT>
-__global__ __launch_bounds__(kBlock) void qgemv_i8_f32x_kernel(
+__device__ __forceinline__ void compute_pass_i8_f32x(int c0, int CPR, int K, const float* xs,
+                                                     const u4_t (&wv)[kUnroll][R], float (&acc)[R][MT])
+{
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const int c = c0 + u * LPR;
+        if (c < CPR) {
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                const f4_t* xp = reinterpret_cast<const f4_t*>(xs + (size_t)m * K + (size_t)c * 16);
+                const f4_t x0 = xp[0], x1 = xp[1], x2 = xp[2], x3 = xp[3];
+                const float xv[16] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3],
+                                      x2[0], x2[1], x2[2], x2[3], x3[0], x3[1], x3[2], x3[3]};
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    float d = acc[r][m];
+#pragma unroll
+                    for (int t = 0; t < 4; ++t)
+#pragma unroll
+                        for (int b = 0; b < 4; ++b)
+                            d = __builtin_fmaf((float)(int8_t)(wv[u][r][t] >> (8 * b)), xv[t * 4 + b], d);
+                    acc[r][m] = d;
+                }
+            }
+        }
+    }
+}
+
+// XT: DT_F16 (dot2 path) or DT_F32 (exact int8->f32 conversion + f32 FMA).
+template <int LPR, int R, int MT, int XT, bool MP>
+__global__ __launch_bounds__(kBlock) void qgemv_i8_kernel(
     const u4_t* __restrict__ w8, const void* __restrict__ S, int sdt, int per_channel,
-    const float* __restrict__ x, const float* __restrict__ bias, float* __restrict__ y, int M, int N, int K)
+    const void* __restrict__ xv, const float* __restrict__ bias, float* __restrict__ y, int M, int N, int K)
 {
     extern __shared__ __align__(16) uint32_t lds[];
-    float* xs = reinterpret_cast<float*>(lds);  // [MT][K]
     const int CPR = K >> 4;
-
     const int team = threadIdx.x / LPR;
     const int lane = threadIdx.x % LPR;
     const int row0 = (blockIdx.x * (kBlock / LPR) + team) * R;
 
-    u4_t wv[kUnroll][R];
+    // (1) activations: f16 in 8-element units, f32 in 4-element units
+    constexpr int XW = MT == 1 ? 4 : 8;
+    const int unit = XT == DT_F16 ? 8 : 4;
+    const int units = K / unit;
+    const int total = MT * units;
+    u4_t xr[XW];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-        const int c = lane + u * LPR;
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int n = row0 + r;
-            wv[u][r] = (c < CPR && n < N) ? __builtin_nontemporal_load(w8 + (size_t)n * CPR + c)
-                                          : u4_t{0u, 0u, 0u, 0u};
-        }
+    for (int j = 0; j < XW; ++j) {
+        const int idx = min((int)threadIdx.x + j * kBlock, total - 1);  // clamped, branch-free
+        const int m = idx / units;
+        const int mc = min(m, M - 1);
+        const char* base = reinterpret_cast<const char*>(xv) + ((size_t)mc * K + (size_t)(idx - m * units) * unit) *
+                                                                   (XT == DT_F16 ? 2 : 4);
+        xr[j] = *reinterpret_cast<const u4_t*>(base);
     }
-
-    for (int i = threadIdx.x; i < MT * (K >> 2); i += kBlock) {
-        const int m = i / (K >> 2);
-        const int q = i - m * (K >> 2);
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (m < M) v = *reinterpret_cast<const float4*>(x + (size_t)m * K + (size_t)q * 4);
-        *reinterpret_cast<float4*>(xs + (size_t)m * K + (size_t)q * 4) = v;
+    // (2) weights for the first pass and this team's per-row scale / bias
+    u4_t wa[kUnroll][R];
+    load_pass_i8<LPR, R>(w8, row0, lane, N, CPR, wa);
+    uint32_t sraw[R];
+    float bv[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int n = min(row0 + r, N - 1);
+        const size_t si = per_channel ? (size_t)n : 0;
+        sraw[r] = sdt == DT_F32 ? load_raw<DT_F32>(S, si) : load_raw<DT_F16>(S, si);
+        bv[r] = bias ? bias[n] : 0.0f;
+    }
+    // (3) stage activations
+    uint32_t* xq = lds;
+    if constexpr (XT == DT_F16) {
+        float* cx = reinterpret_cast<float*>(lds + (size_t)MT * CPR * 8);
+#pragma unroll
+        for (int j = 0; j < XW; ++j) {
+            const int idx = (int)threadIdx.x + j * kBlock;
+            stage_unit_i8(xr[j], idx, idx < total, xq, cx);
+        }
+        for (int b0 = XW * kBlock; b0 < total; b0 += kBlock) {
+            const int idx = b0 + (int)threadIdx.x;
+            const int m = idx / units;
+            const _Float16* xh = reinterpret_cast<const _Float16*>(xv);
+            u4_t raw = (idx < total && m < M)
+                           ? *reinterpret_cast<const u4_t*>(xh + (size_t)m * K + (size_t)(idx - m * units) * 8)
+                           : u4_t{0u, 0u, 0u, 0u};
+            stage_unit_i8(raw, idx, idx < total, xq, cx);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < XW; ++j) {
+            const int idx = (int)threadIdx.x + j * kBlock;
+            if (idx < total) *reinterpret_cast<u4_t*>(xq + (size_t)idx * 4) = xr[j];
+        }
+        for (int b0 = XW * kBlock; b0 < total; b0 += kBlock) {
+            const int idx = b0 + (int)threadIdx.x;
+            const int m = idx / units;
+            const float* xf = reinterpret_cast<const float*>(xv);
+            if (idx < total)
+                *reinterpret_cast<u4_t*>(xq + (size_t)idx * 4) =
+                    m < M ? *reinterpret_cast<const u4_t*>(xf + (size_t)m * K + (size_t)(idx - m * units) * 4)
+                          : u4_t{0u, 0u, 0u, 0u};
+        }
     }
     __syncthreads();
     if (row0 >= N) return;
@@ -390,43 +428,24 @@ __global__ __launch_bounds__(kBlock) void qgemv_i8_f32x_kernel(
 #pragma unroll
         for (int m = 0; m < MT; ++m) acc[r][m] = 0.0f;
 
-    for (int cbase = 0; cbase < CPR; cbase += kUnroll * LPR) {
-        if (cbase != 0) {
-#pragma unroll
-            for (int u = 0; u < kUnroll; ++u) {
-                const int c = cbase + lane + u * LPR;
-#pragma unroll
-                for (int r = 0; r < R; ++r) {
-                    const int n = row0 + r;
-                    wv[u][r] = (c < CPR && n < N) ? __builtin_nontemporal_load(w8 + (size_t)n * CPR + c)
-                                                  : u4_t{0u, 0u, 0u, 0u};
-                }
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < kUnroll; ++u) {
-            const int c = cbase + lane + u * LPR;
-            if (c < CPR) {
-#pragma unroll
-                for (int m = 0; m < MT; ++m) {
-                    const float4* xp = reinterpret_cast<const float4*>(xs + (size_t)m * K + (size_t)c * 16);
-                    const float4 x0 = xp[0], x1 = xp[1], x2 = xp[2], x3 = xp[3];
-                    const float xv[16] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w,
-                                          x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
-#pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        const uint32_t wd[4] = {wv[u][r][0], wv[u][r][1], wv[u][r][2], wv[u][r][3]};
-                        float d = acc[r][m];
-#pragma unroll
-                        for (int t = 0; t < 4; ++t) {
-#pragma unroll
-                            for (int b = 0; b < 4; ++b)
-                                d = __builtin_fmaf((float)(int8_t)(wd[t] >> (8 * b)), xv[t * 4 + b], d);
-                        }
-                        acc[r][m] = d;
-                    }
-                }
-            }
+    auto compute = [&](int c0, const u4_t(&wv)[kUnroll][R]) {
+        if constexpr (XT == DT_F16)
+            compute_pass_i8_f16x<LPR, R, MT>(c0, CPR, xq, reinterpret_cast<const float*>(lds + (size_t)MT * CPR * 8),
+                                             wv, acc);
+        else
+            compute_pass_i8_f32x<LPR, R, MT>(c0, CPR, K, reinterpret_cast<const float*>(lds), wv, acc);
+    };
+    if constexpr (!MP) {
+        compute(lane, wa);
+    } else {
+        constexpr int P = kUnroll * LPR;
+        u4_t wb[kUnroll][R];
+        for (int c0 = lane; c0 < CPR + lane; c0 += 2 * P) {
+            if (c0 - lane + P < CPR) load_pass_i8<LPR, R>(w8, row0, c0 + P, N, CPR, wb);
+            compute(c0, wa);
+            if (c0 - lane + P >= CPR) break;
+            if (c0 - lane + 2 * P < CPR) load_pass_i8<LPR, R>(w8, row0, c0 + 2 * P, N, CPR, wa);
+            compute(c0 + P, wb);
         }
     }
 
@@ -440,16 +459,14 @@ __global__ __launch_bounds__(kBlock) void qgemv_i8_f32x_kernel(
         for (int r = 0; r < R; ++r) {
             const int n = row0 + r;
             if (n < N) {
-                const size_t si = per_channel ? (size_t)n : 0;
-                const float s = sdt == DT_F32 ? load_f32<DT_F32>(S, si)
-                              : sdt == DT_F16 ? load_f32<DT_F16>(S, si)
-                                              : load_f32<DT_BF16>(S, si);
-                const float bv = bias ? bias[n] : 0.0f;
+                const float s = sdt == DT_F32 ? raw_to_f32<DT_F32>(sraw[r])
+                              : sdt == DT_F16 ? raw_to_f32<DT_F16>(sraw[r])
+                                              : raw_to_f32<DT_BF16>(sraw[r]);
 #pragma unroll
                 for (int m = 0; m < MT; ++m)
                     if (m < M) {
                         float v = acc[r][m] * s;
-                        if (bias) v += bv;
+                        if (bias) v += bv[r];
                         y[(size_t)m * N + n] = v;
                     }
             }
@@ -537,7 +554,7 @@ int pick_lpr(int cpr, int n_rows, int R)
     return best;
 }
 
-template <int LPR, int R, int MT>
+template <int LPR, int R, int MT, bool MP>
 hipError_t launch_q4_f16x_sbt(int sbt, const uint32_t* wq, const void* S, const void* B, const _Float16* x, float* y,
                               int M, int N, int K, int gshift, hipStream_t st)
 {
@@ -547,15 +564,23 @@ hipError_t launch_q4_f16x_sbt(int sbt, const uint32_t* wq, const void* S, const 
     const dim3 grid((N + rows_per_block - 1) / rows_per_block);
     const u4_t* w4 = reinterpret_cast<const u4_t*>(wq);
     if (sbt == DT_F16)
-        hipLaunchKernelGGL((qgemv_q4_f16x_kernel<LPR, R, MT, DT_F16>), grid, dim3(kBlock), lds, st, w4, S, B, x, y, M,
-                           N, K, gshift);
-    else if (sbt == DT_F32)
-        hipLaunchKernelGGL((qgemv_q4_f16x_kernel<LPR, R, MT, DT_F32>), grid, dim3(kBlock), lds, st, w4, S, B, x, y, M,
-                           N, K, gshift);
-    else
-        hipLaunchKernelGGL((qgemv_q4_f16x_kernel<LPR, R, MT, DT_BF16>), grid, dim3(kBlock), lds, st, w4, S, B, x, y,
+        hipLaunchKernelGGL((qgemv_q4_f16x_kernel<LPR, R, MT, DT_F16, MP>), grid, dim3(kBlock), lds, st, w4, S, B, x, y,
                            M, N, K, gshift);
+    else if (sbt == DT_F32)
+        hipLaunchKernelGGL((qgemv_q4_f16x_kernel<LPR, R, MT, DT_F32, MP>), grid, dim3(kBlock), lds, st, w4, S, B, x, y,
+                           M, N, K, gshift);
+    else
+        hipLaunchKernelGGL((qgemv_q4_f16x_kernel<LPR, R, MT, DT_BF16, MP>), grid, dim3(kBlock), lds, st, w4, S, B, x,
+                           y, M, N, K, gshift);
     return hipGetLastError();
+}
+
+template <int LPR, int R, int MT>
+hipError_t launch_q4_f16x_mp(int sbt, const uint32_t* wq, const void* S, const void* B, const _Float16* x, float* y,
+                             int M, int N, int K, int gshift, hipStream_t st)
+{
+    if ((K >> 5) > kUnroll * LPR) return launch_q4_f16x_sbt<LPR, R, MT, true>(sbt, wq, S, B, x, y, M, N, K, gshift, st);
+    return launch_q4_f16x_sbt<LPR, R, MT, false>(sbt, wq, S, B, x, y, M, N, K, gshift, st);
 }
 
 template <int R, int MT>
@@ -563,31 +588,37 @@ hipError_t launch_q4_f16x_lpr(int lpr, int sbt, const uint32_t* wq, const void* 
                               float* y, int M, int N, int K, int gshift, hipStream_t st)
 {
     switch (lpr) {
-    case 8: return launch_q4_f16x_sbt<8, R, MT>(sbt, wq, S, B, x, y, M, N, K, gshift, st);
-    case 16: return launch_q4_f16x_sbt<16, R, MT>(sbt, wq, S, B, x, y, M, N, K, gshift, st);
-    case 32: return launch_q4_f16x_sbt<32, R, MT>(sbt, wq, S, B, x, y, M, N, K, gshift, st);
-    default: return launch_q4_f16x_sbt<64, R, MT>(sbt, wq, S, B, x, y, M, N, K, gshift, st);
+    case 8: return launch_q4_f16x_mp<8, R, MT>(sbt, wq, S, B, x, y, M, N, K, gshift, st);
+    case 16: return launch_q4_f16x_mp<16, R, MT>(sbt, wq, S, B, x, y, M, N, K, gshift, st);
+    case 32: return launch_q4_f16x_mp<32, R, MT>(sbt, wq, S, B, x, y, M, N, K, gshift, st);
+    default: return launch_q4_f16x_mp<64, R, MT>(sbt, wq, S, B, x, y, M, N, K, gshift, st);
     }
+}
+
+template <int LPR, int R, int MT, int XT>
+hipError_t launch_i8_xt(const int8_t* w, const void* S, int sdt, int per_channel, const void* x, const float* bias,
+                        float* y, int M, int N, int K, hipStream_t st)
+{
+    const int CPR = K >> 4;
+    const int rows_per_block = (kBlock / LPR) * R;
+    const dim3 grid((N + rows_per_block - 1) / rows_per_block);
+    const u4_t* w4 = reinterpret_cast<const u4_t*>(w);
+    const size_t lds = XT == DT_F16 ? (size_t)MT * CPR * 8 * 4 + (size_t)MT * CPR * 4 : (size_t)MT * K * 4;
+    if (CPR > kUnroll * LPR)
+        hipLaunchKernelGGL((qgemv_i8_kernel<LPR, R, MT, XT, true>), grid, dim3(kBlock), lds, st, w4, S, sdt,
+                           per_channel, x, bias, y, M, N, K);
+    else
+        hipLaunchKernelGGL((qgemv_i8_kernel<LPR, R, MT, XT, false>), grid, dim3(kBlock), lds, st, w4, S, sdt,
+                           per_channel, x, bias, y, M, N, K);
+    return hipGetLastError();
 }
 
 template <int LPR, int R, int MT>
 hipError_t launch_i8_lpr_fixed(int xdt, const int8_t* w, const void* S, int sdt, int per_channel, const void* x,
                                const float* bias, float* y, int M, int N, int K, hipStream_t st)
 {
-    const int CPR = K >> 4;
-    const int rows_per_block = (kBlock / LPR) * R;
-    const dim3 grid((N + rows_per_block - 1) / rows_per_block);
-    const u4_t* w4 = reinterpret_cast<const u4_t*>(w);
-    if (xdt == DT_F16) {
-        const size_t lds = (size_t)MT * CPR * 8 * 4 + (size_t)MT * CPR * 4;
-        hipLaunchKernelGGL((qgemv_i8_f16x_kernel<LPR, R, MT>), grid, dim3(kBlock), lds, st, w4, S, sdt, per_channel,
-                           reinterpret_cast<const _Float16*>(x), bias, y, M, N, K);
-    } else {
-        const size_t lds = (size_t)MT * K * 4;
-        hipLaunchKernelGGL((qgemv_i8_f32x_kernel<LPR, R, MT>), grid, dim3(kBlock), lds, st, w4, S, sdt, per_channel,
-                           reinterpret_cast<const float*>(x), bias, y, M, N, K);
-    }
-    return hipGetLastError();
+    if (xdt == DT_F16) return launch_i8_xt<LPR, R, MT, DT_F16>(w, S, sdt, per_channel, x, bias, y, M, N, K, st);
+    return launch_i8_xt<LPR, R, MT, DT_F32>(w, S, sdt, per_channel, x, bias, y, M, N, K, st);
 }
 
 template <int R, int MT>

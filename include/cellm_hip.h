@@ -21,8 +21,9 @@
  *   x [m, k], y [m, n] (f32).
  *
  * Async entry points take device pointers and a stream (a hipStream_t passed
- * as void*; NULL selects the context's own stream) and return as soon as the
- * work is queued, like MetalOps::encode_* (metal.rs:813-1176).  Sync entry
+ * as void*; NULL is HIP's default stream, as in the HIP API) and return as
+ * soon as the work is queued, like MetalOps::encode_* (metal.rs:813-1176).
+ * The context's own stream (cellm_hip_get_stream) serves the sync calls.  Sync entry
  * points take host pointers, cache the weights on the device under a name
  * key, and return after the result is back in host memory, like
  * MetalOps::logits_* (metal.rs:1017-1204).
