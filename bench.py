@@ -63,15 +63,17 @@ class Q4Weights:
 
 
 def time_launches(torch, fn, reps: int, stream):
-    """Per-launch HIP-event timing on `stream`; returns mean ms per launch."""
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
-    ends = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
-    for i in range(reps):
-        starts[i].record(stream)
-        fn(i)
-        ends[i].record(stream)
+    """HIP events on `stream` around `reps` back-to-back launches; mean ms per
+    launch (kernel time plus the inter-launch gap of a busy stream)."""
+    fn(0)
     torch.cuda.synchronize()
-    return sum(s.elapsed_time(e) for s, e in zip(starts, ends)) / reps
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(reps):
+        fn(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
 
 
 def main():

@@ -36,7 +36,10 @@ namespace cellm {
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kUnroll = 4;  // chunks per lane held in registers per pass
+#ifndef CELLM_GEMV_UNROLL
+#define CELLM_GEMV_UNROLL 4
+#endif
+constexpr int kUnroll = CELLM_GEMV_UNROLL;  // chunks per lane held in registers per pass
 
 // Load order inside every kernel below: (1) this thread's activation words,
 // (2) all weight chunks and their scale/bias bits for the first pass, (3)
@@ -531,10 +534,21 @@ __global__ __launch_bounds__(kBlock) void qgemv_i8_generic_kernel(
     }
 }
 
-// Pick lanes-per-row: single pass (<= kUnroll chunks per lane) if possible,
-// best lane utilisation, enough waves to cover the chip.
-int pick_lpr(int cpr, int n_rows, int R)
+// Launch shape (lanes per row, rows per team).  Chosen from a sweep on
+// MI355X (4-byte and 16-byte chunk rows, M=1):
+//   * large N (>= 32768 rows): 8 lanes per row; weight streaming dominates and
+//     narrow teams minimise reduction and staging cost per byte; rows longer
+//     than one pass use the ping-pong multi-pass kernel;
+//   * otherwise: the narrowest team whose row fits in one pass while keeping
+//     >= 512 waves in flight, weighted by lane utilisation.
+struct GemvShape {
+    int lpr;
+    int rows;
+};
+
+GemvShape pick_shape(int cpr, int n_rows, bool q4)
 {
+    if (n_rows >= 32768) return {8, q4 && cpr <= 4 * 8 ? 2 : 1};
     const int cand[4] = {8, 16, 32, 64};
     int best = 64;
     double best_score = -1.0;
@@ -543,15 +557,15 @@ int pick_lpr(int cpr, int n_rows, int R)
         const int c = (cpr + lpr - 1) / lpr;
         if (c > kUnroll && lpr != 64) continue;
         const double eff = (double)cpr / ((double)lpr * c);
-        const double waves = (double)((n_rows + R - 1) / R) * lpr / 64.0;
-        const double fill = waves >= 2048.0 ? 1.0 : waves / 2048.0;
-        const double score = eff * (0.5 + 0.5 * fill);
+        const double waves = (double)n_rows * lpr / 64.0;
+        const double fill = waves >= 512.0 ? 1.0 : waves / 512.0;
+        const double score = eff * fill;
         if (score > best_score + 1e-9) {
             best_score = score;
             best = lpr;
         }
     }
-    return best;
+    return {best, 1};
 }
 
 template <int LPR, int R, int MT, bool MP>
@@ -652,13 +666,16 @@ hipError_t launch_qgemv_q4_affine(const uint32_t* wq, const void* S, const void*
     const bool fast = !force_generic && xdt == DT_F16 && M <= 4 && (K % 32) == 0 && group_size >= 32 &&
                       aligned16(wq) && aligned16(x) && qgemv_q4_lds_bytes(M, K) <= 64 * 1024;
     if (fast) {
-        const int CPR = K >> 5;
-        const int R = 2;
-        const int lpr = pick_lpr(CPR, N, R);
+        const GemvShape sh = pick_shape(K >> 5, N, true);
         const _Float16* xh = reinterpret_cast<const _Float16*>(x);
-        if (M == 1) return launch_q4_f16x_lpr<2, 1>(lpr, sbt, wq, S, B, xh, y, M, N, K, gshift, st);
-        if (M == 2) return launch_q4_f16x_lpr<2, 2>(lpr, sbt, wq, S, B, xh, y, M, N, K, gshift, st);
-        return launch_q4_f16x_lpr<2, 4>(lpr, sbt, wq, S, B, xh, y, M, N, K, gshift, st);
+        if (sh.rows == 2) {
+            if (M == 1) return launch_q4_f16x_lpr<2, 1>(sh.lpr, sbt, wq, S, B, xh, y, M, N, K, gshift, st);
+            if (M == 2) return launch_q4_f16x_lpr<2, 2>(sh.lpr, sbt, wq, S, B, xh, y, M, N, K, gshift, st);
+            return launch_q4_f16x_lpr<2, 4>(sh.lpr, sbt, wq, S, B, xh, y, M, N, K, gshift, st);
+        }
+        if (M == 1) return launch_q4_f16x_lpr<1, 1>(sh.lpr, sbt, wq, S, B, xh, y, M, N, K, gshift, st);
+        if (M == 2) return launch_q4_f16x_lpr<1, 2>(sh.lpr, sbt, wq, S, B, xh, y, M, N, K, gshift, st);
+        return launch_q4_f16x_lpr<1, 4>(sh.lpr, sbt, wq, S, B, xh, y, M, N, K, gshift, st);
     }
     const dim3 grid((N + 3) / 4);
 #define CELLM_Q4_GENERIC(XT_, SBT_)                                                                              \
@@ -689,12 +706,10 @@ hipError_t launch_qgemv_i8(const int8_t* w, const void* S, int sdt, int per_chan
     const bool fast = !force_generic && (xdt == DT_F16 || xdt == DT_F32) && M <= 4 && (K % 16) == 0 &&
                       aligned16(w) && aligned16(x) && lds <= 64 * 1024;
     if (fast) {
-        const int CPR = K >> 4;
-        const int R = 2;
-        const int lpr = pick_lpr(CPR, N, R);
-        if (M == 1) return launch_i8_lpr<2, 1>(lpr, xdt, w, S, sdt, per_channel, x, bias, y, M, N, K, st);
-        if (M == 2) return launch_i8_lpr<2, 2>(lpr, xdt, w, S, sdt, per_channel, x, bias, y, M, N, K, st);
-        return launch_i8_lpr<2, 4>(lpr, xdt, w, S, sdt, per_channel, x, bias, y, M, N, K, st);
+        const GemvShape sh = pick_shape(K >> 4, N, false);
+        if (M == 1) return launch_i8_lpr<1, 1>(sh.lpr, xdt, w, S, sdt, per_channel, x, bias, y, M, N, K, st);
+        if (M == 2) return launch_i8_lpr<1, 2>(sh.lpr, xdt, w, S, sdt, per_channel, x, bias, y, M, N, K, st);
+        return launch_i8_lpr<1, 4>(sh.lpr, xdt, w, S, sdt, per_channel, x, bias, y, M, N, K, st);
     }
     const dim3 grid((N + 3) / 4);
     if (xdt == DT_F32)

@@ -1,0 +1,334 @@
+"""Pins of the CPU oracle (oracle/cellm_oracle.c) without the reference.
+
+The reference is Rust (no toolchain here) and ships no tests or fixtures for
+these kernels, so each oracle function is checked against something the
+mathematics fixes, built from different primitives than the oracle's C loops:
+  * IEEE-754 conversions from numpy (exhaustive over f16);
+  * strict left-to-right f32 sums via np.add.accumulate (sequential in numpy),
+    which is the order the reference's x86 loops use;
+  * integer closed forms where every partial sum is exact;
+  * fp64 error bounds gamma_K * sum|w x|;
+  * known-answer nibble/byte words and brute force on tiny shapes.
+Each test names the plausible mistake it catches.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+
+U = 2.0 ** -24
+
+
+def seq_sum_f32(p: np.ndarray) -> np.float32:
+    """Strict left-to-right f32 sum (np.add.accumulate does not reassociate)."""
+    p = np.asarray(p, np.float32)
+    if p.size == 0:
+        return np.float32(0.0)
+    return np.add.accumulate(p, dtype=np.float32)[-1]
+
+
+def gamma(k: int) -> float:
+    return k * U / (1 - k * U)
+
+
+# ------------------------------------------------------------ conversions ----
+
+def test_f16_to_f32_exhaustive():
+    bits = np.arange(65536, dtype=np.uint16)
+    ours = oracle.f16_bits_to_f32(bits)
+    ref = bits.view(np.float16).astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(ours), nan)
+    assert np.array_equal(ours[~nan].view(np.uint32), ref[~nan].view(np.uint32))  # signed zeros too
+
+
+def test_f32_to_f16_rne_matches_numpy():
+    rng = np.random.default_rng(1)
+    vals = [rng.standard_normal(200000).astype(np.float32) * s for s in (1e-6, 1e-3, 1.0, 1e3, 6e4)]
+    # every f16 value, the midpoints between neighbours (ties) and one ulp either side
+    h = np.arange(0, 0x7c00, dtype=np.uint16).view(np.float16).astype(np.float64)
+    mids = ((h[:-1] + h[1:]) / 2).astype(np.float32)
+    vals += [h.astype(np.float32), mids, np.nextafter(mids, np.float32(np.inf)), np.nextafter(mids, np.float32(0))]
+    vals += [np.array([65504.0, 65519.99, 65520.0, 1e9, 2.0 ** -25, 2.0 ** -26, 3 * 2.0 ** -26, 0.0, -0.0, np.inf,
+                       -np.inf], np.float32)]
+    x = np.concatenate(vals).astype(np.float32)
+    x = np.concatenate([x, -x])
+    ours = oracle.f32_to_f16_bits(x)
+    with np.errstate(over="ignore"):
+        ref = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(ours, ref)
+
+
+def test_f32_to_f16_nan_is_quiet():
+    out = oracle.f32_to_f16_bits(np.array([np.nan], np.float32))
+    assert out[0] & 0x7c00 == 0x7c00 and out[0] & 0x3ff
+
+
+# ------------------------------------------------------------------ LCG ----
+
+def test_lcg_deterministic_and_in_range():
+    a = oracle.lcg_fill(1000, 0xA11CE, 0.8)
+    b = oracle.lcg_fill(1000, 0xA11CE, 0.8)
+    assert np.array_equal(a, b) and np.all(np.abs(a) <= 0.8)
+    # first draw by exact integer arithmetic: s1 = seed*6364136223846793005 + 1 mod 2^64
+    s1 = (0xA11CE * 6364136223846793005 + 1) % 2 ** 64
+    u = np.float32(np.float32(s1 >> 32) / np.float32(2 ** 32 - 1))
+    assert a[0] == np.float32((u * np.float32(2.0) - np.float32(1.0)) * np.float32(0.8))
+    w = oracle.gen_q4_words((4096,), 3)
+    nib = (w[:, None] >> (4 * np.arange(8, dtype=np.uint32))) & 0xF
+    assert set(np.unique(nib)) == set(range(16))
+    q = oracle.gen_i8((100000,), 5)
+    assert q.min() == -127 and q.max() == 127
+    s = oracle.gen_normal((10000,), 9, 0.02, 0.005, positive_only=True)
+    assert s.min() > 0 and abs(float(s.mean()) - 0.02) < 5e-4
+
+
+# ------------------------------------------------------ a1: int8 per-row ----
+
+def test_i8_closed_form_exact_integers():
+    """Integer x in [-4,4], power-of-two scales, K <= 4096: every partial sum is
+    exact, so any order gives the integer dot * scale (catches a dropped or
+    per-element-misplaced scale, wrong row/column indexing)."""
+    rng = np.random.default_rng(2)
+    n, k = 37, 4096
+    w = rng.integers(-127, 128, (n, k)).astype(np.int8)
+    x = rng.integers(-4, 5, k).astype(np.float32)
+    e = rng.integers(-12, -4, n)
+    s = (2.0 ** e).astype(np.float16)
+    y = oracle.matmul_i8_f32(w, s.view(np.uint16), x)
+    exact = (w.astype(np.int64) @ x.astype(np.int64)).astype(np.float64) * s.astype(np.float64)
+    assert np.array_equal(y.astype(np.float64), exact)
+
+
+def test_i8_sequential_order_bit_exact():
+    """x86 branch: acc += f32(w)*x left to right, then * scale."""
+    rng = np.random.default_rng(3)
+    n, k = 9, 577
+    w = rng.integers(-127, 128, (n, k)).astype(np.int8)
+    x = rng.standard_normal(k).astype(np.float32)
+    s = rng.uniform(1e-3, 2e-2, n).astype(np.float16)
+    y = oracle.matmul_i8_f32(w, s.view(np.uint16), x)
+    for r in range(n):
+        acc = seq_sum_f32(w[r].astype(np.float32) * x)
+        assert y[r] == np.float32(acc * np.float32(s[r]))
+
+
+def test_i8_fp64_bound_and_batched_rows():
+    rng = np.random.default_rng(4)
+    n, k, m = 50, 1152, 3
+    w = rng.integers(-127, 128, (n, k)).astype(np.int8)
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    s = rng.uniform(1e-3, 2e-2, n).astype(np.float32)
+    y = oracle.qgemv_i8(w, s, x)
+    ref = (x.astype(np.float64) @ w.astype(np.float64).T) * s[None, :]
+    bound = gamma(k + 1) * (np.abs(x.astype(np.float64)) @ np.abs(w.astype(np.float64)).T) * s[None, :]
+    assert np.all(np.abs(y - ref) <= bound + 1e-30)
+    # batched form = the reference row GEMV on each activation row
+    for i in range(m):
+        yi = oracle.qgemv_i8(w, s, x[i:i + 1])
+        assert np.array_equal(yi[0], y[i])
+
+
+def test_llama_lm_head_i8_per_element_scale_and_nonfinite():
+    """llama.rs:602-643: acc += x * (f32(w) * scale); non-finite -> -inf."""
+    rng = np.random.default_rng(5)
+    v, h = 6, 64
+    w = rng.integers(-127, 128, (v, h)).astype(np.int8)
+    s = rng.uniform(1e-3, 2e-2, v).astype(np.float16)
+    x = rng.standard_normal(h).astype(np.float32)
+    y = oracle.llama_lm_head_i8(x, w, s.view(np.uint16))
+    for r in range(v):
+        assert y[r] == seq_sum_f32(x * (w[r].astype(np.float32) * np.float32(s[r])))
+    x[3] = np.inf
+    w[0, 3] = 5   # +inf -> -inf
+    w[1, 3] = -5  # -inf stays -inf
+    w[2, 3] = 0   # inf * 0 = nan -> -inf
+    y = oracle.llama_lm_head_i8(x, w, s.view(np.uint16))
+    assert np.all(np.isneginf(y))
+
+
+# ------------------------------------------------------------- a2: i4 sym ----
+
+def test_i4_known_answer_and_order():
+    """byte 0x8F -> elements [7, 0] (low nibble even, q = nib - 8)."""
+    w = np.array([[0x8F, 0x08]], np.uint8)  # elements: 7, 0, 0, -8
+    s = np.array([1.0], np.float16).view(np.uint16)
+    x = np.array([1.0, 10.0, 100.0, 1000.0], np.float32)
+    y = oracle.matmul_i4_f32(w, s, 1, 4, 4, x)
+    assert y[0] == np.float32(7.0 - 8000.0)
+    rng = np.random.default_rng(6)
+    n, k, gs = 5, 256, 64
+    w = rng.integers(0, 256, (n, k // 2)).astype(np.uint8)
+    s = rng.uniform(1e-3, 2e-2, n * (k // gs)).astype(np.float16)
+    x = rng.standard_normal(k).astype(np.float32)
+    y = oracle.matmul_i4_f32(w, s.view(np.uint16), n, k, gs, x)
+    q = np.empty((n, k), np.float32)
+    q[:, 0::2] = (w & 0xF).astype(np.int32) - 8
+    q[:, 1::2] = (w >> 4).astype(np.int32) - 8
+    for r in range(n):
+        sc = np.repeat(s[r * (k // gs):(r + 1) * (k // gs)].astype(np.float32), gs)
+        assert y[r] == seq_sum_f32((q[r] * sc) * x)
+
+
+# --------------------------------------------------------- a3/a4/a5: affine ----
+
+def _unpack(wq: np.ndarray) -> np.ndarray:
+    return ((wq[..., None] >> (4 * np.arange(8, dtype=np.uint32))) & 0xF).reshape(wq.shape[0], -1)
+
+
+def test_affine_nibble_order_known_answer():
+    """u32 0x76543210 -> q = 0..7 and 0xFEDCBA98 -> 8..15 (nibble j = bits 4j..4j+3)."""
+    wq = np.array([[0x76543210, 0xFEDCBA98] * 4], np.uint32)  # K = 64, one group
+    s = np.array([[1.0]], np.float32)
+    b = np.array([[0.0]], np.float32)
+    w = oracle.q4_affine_dequant_f32(wq, s, b, 64)
+    assert np.array_equal(w[0, :16], np.arange(16, dtype=np.float32))
+    # exhaustive 16-value sweep through scale and bias
+    s = np.array([[0.37]], np.float32)
+    b = np.array([[-1.25]], np.float32)
+    w = oracle.q4_affine_dequant_f32(wq, s, b, 64)
+    qs = np.arange(16, dtype=np.float32)
+    assert np.array_equal(w[0, :16], (qs * np.float32(0.37)) + np.float32(-1.25))
+
+
+def test_affine_dequant_two_roundings_and_groups():
+    rng = np.random.default_rng(7)
+    n, k = 6, 320  # 5 groups
+    wq = rng.integers(0, 2 ** 32, (n, k // 8), dtype=np.uint64).astype(np.uint32)
+    s = rng.standard_normal((n, 5)).astype(np.float32)
+    b = rng.standard_normal((n, 5)).astype(np.float32)
+    w = oracle.q4_affine_dequant_f32(wq, s, b, k)
+    q = _unpack(wq).astype(np.float32)
+    sg, bg = np.repeat(s, 64, axis=1), np.repeat(b, 64, axis=1)
+    assert np.array_equal(w, (q * sg) + bg)  # numpy rounds each op in f32: mul then add
+    fused = (q.astype(np.float64) * sg + bg).astype(np.float32)  # one rounding
+    assert not np.array_equal(w, fused), "data should separate one and two roundings"
+
+
+def test_affine_gemv_sequential_bit_exact_and_lm_head_equal():
+    rng = np.random.default_rng(8)
+    n, k, m = 11, 896, 2
+    wq = rng.integers(0, 2 ** 32, (n, k // 8), dtype=np.uint64).astype(np.uint32)
+    s = np.abs(rng.normal(0.02, 0.005, (n, k // 64))).astype(np.float16)
+    b = rng.normal(0, 0.05, (n, k // 64)).astype(np.float16)
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    y = oracle.qgemv_q4_affine(wq, s, b, x, k)
+    w = oracle.q4_affine_dequant_f32(wq, s, b, k)
+    for i in range(m):
+        for r in range(n):
+            assert y[i, r] == seq_sum_f32(w[r] * x[i].astype(np.float32))
+    # a4 (lfm.rs:700-741) with f32 scale/bias files gives the same bits as a3
+    s32, b32 = s.astype(np.float32), b.astype(np.float32)
+    lm = oracle.lfm_lm_head_q4_affine(wq, s32, b32, x[0].astype(np.float32), n, k)
+    assert np.array_equal(lm, oracle.qgemv_q4_affine(wq, s32, b32, x[0:1].astype(np.float32), k)[0])
+
+
+def test_affine_gemv_fp64_bound_brute_force_tiny():
+    rng = np.random.default_rng(9)
+    for k in (8, 16, 64, 128):
+        for n in range(1, 8):
+            wq = rng.integers(0, 2 ** 32, (n, k // 8), dtype=np.uint64).astype(np.uint32)
+            g = (k + 63) // 64
+            s = rng.uniform(0.01, 0.03, (n, g)).astype(np.float32)
+            b = rng.normal(0, 0.05, (n, g)).astype(np.float32)
+            x = rng.standard_normal((1, k)).astype(np.float32)
+            y = oracle.qgemv_q4_affine(wq, s, b, x, k)[0]
+            q = _unpack(wq).astype(np.float64)
+            w64 = q * np.repeat(s, 64, axis=1)[:, :k] + np.repeat(b, 64, axis=1)[:, :k]
+            ref = w64 @ x[0].astype(np.float64)
+            bound = (gamma(k) + 3 * U) * (np.abs(w64) @ np.abs(x[0].astype(np.float64)))
+            assert np.all(np.abs(y - ref) <= bound + 1e-30), (k, n)
+
+
+def test_dequant_f16_rne_and_double_rounding():
+    rng = np.random.default_rng(10)
+    n, k = 8, 256
+    wq = rng.integers(0, 2 ** 32, (n, k // 8), dtype=np.uint64).astype(np.uint32)
+    for dt in (np.float32, np.float16):
+        s = rng.normal(0.02, 0.005, (n, 4)).astype(dt)
+        b = rng.normal(0, 0.05, (n, 4)).astype(dt)
+        h = oracle.dequant_q4_affine_f16(wq, s, b, k)
+        w32 = oracle.q4_affine_dequant_f32(wq, s, b, k)
+        assert np.array_equal(h, w32.astype(np.float16).view(np.uint16))
+    # q=3, s = 1+2^-10 (an f16), b = -2^-24: q*s = 3.0029296875 is an f16 midpoint;
+    # f32 rounding of q*s+b lands back on it and RNE picks the even neighbour, the
+    # reference's double rounding; a single rounding would pick the lower value.
+    wq1 = np.array([[3]], np.uint32)
+    s1 = np.array([[1 + 2 ** -10]], np.float16)
+    b1 = np.array([[-(2.0 ** -24)]], np.float16)
+    h1 = oracle.dequant_q4_affine_f16(wq1, s1, b1, 8, 64)[0, 0]
+    single = np.float16(np.float64(3) * np.float64(s1[0, 0]) + np.float64(b1[0, 0])).view(np.uint16)
+    double = np.float16(np.float32(3) * np.float32(s1[0, 0]) + np.float32(b1[0, 0])).view(np.uint16)
+    assert h1 == double and h1 != single
+
+
+# --------------------------------------------------------------- a6: dense ----
+
+def test_matmul_f32_accumulates_into_out_sequentially():
+    rng = np.random.default_rng(11)
+    m, k, n = 3, 17, 5
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    bm = rng.standard_normal((k, n)).astype(np.float32)
+    out0 = rng.standard_normal((m, n)).astype(np.float32)
+    out = oracle.matmul_f32(a, bm, out0.copy())
+    for i in range(m):
+        for j in range(n):
+            p = np.concatenate([[out0[i, j]], a[i] * bm[:, j]]).astype(np.float32)
+            assert out[i, j] == seq_sum_f32(p)
+    # n == 1 path: row dot
+    v = oracle.matmul_f32(a, bm[:, :1].copy())
+    for i in range(m):
+        assert v[i] == seq_sum_f32(a[i] * bm[:, 0])
+
+
+def test_gemm_xwT_equals_matmul_over_transposed_weight():
+    rng = np.random.default_rng(12)
+    m, k, n = 7, 128, 9
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    w = rng.standard_normal((n, k)).astype(np.float32)
+    y = oracle.gemm_xwT(x, w)
+    ref = oracle.matmul_f32(x.astype(np.float32), np.ascontiguousarray(w.T))
+    assert np.array_equal(y, ref)
+
+
+# ------------------------------------------------- a9: decode-step helpers ----
+
+def test_rms_norm_closed_form():
+    x = np.full(64, 3.0, np.float32)
+    w = np.linspace(0.5, 1.5, 64).astype(np.float32)
+    y = oracle.rms_norm(x, w, 1e-5)
+    inv = np.float32(1.0) / np.sqrt(np.float32(9.0) + np.float32(1e-5))
+    assert np.allclose(y, (x * inv) * w, rtol=0, atol=1e-6)
+
+
+def test_rope_identity_at_zero_and_rotation():
+    rng = np.random.default_rng(13)
+    x = rng.standard_normal(4 * 64).astype(np.float32)
+    y = oracle.rope_half_(x.copy(), 4, 64, 0, 10000.0)
+    assert np.array_equal(x, y)
+    y = oracle.rope_half_(x.copy(), 4, 64, 37, 10000.0)
+    nx = np.linalg.norm(x.reshape(4, 2, 32), axis=1)
+    ny = np.linalg.norm(y.reshape(4, 2, 32), axis=1)
+    assert np.allclose(nx, ny, rtol=1e-5)
+    # head_dim 2, pos 1: angle 1 rad
+    z = oracle.rope_half_(np.array([1.0, 0.0], np.float32), 1, 2, 1, 10000.0)
+    assert np.allclose(z, [np.cos(1.0), np.sin(1.0)], atol=1e-6)
+
+
+def test_softmax_attention_argmax():
+    s = oracle.softmax_(np.full(8, 2.5, np.float32))
+    assert np.allclose(s, 1 / 8)
+    # one token: attention returns v exactly (weight 1)
+    hd, nh, nkv = 8, 4, 2
+    v = np.arange(nkv * hd, dtype=np.float32).astype(np.float16)
+    kc = np.ones(nkv * hd, np.float16)
+    out = oracle.attention_gqa_f16kv(kc.view(np.uint16), v.view(np.uint16), [0], np.ones(nh * hd, np.float32), nh,
+                                     nkv, hd)
+    expect = np.concatenate([v[(h // 2) * hd:(h // 2 + 1) * hd] for h in range(nh)]).astype(np.float32)
+    assert np.array_equal(out, expect)
+    assert oracle.argmax_first(np.array([1.0, 3.0, 3.0, 2.0], np.float32)) == 1
+    g = np.array([0.0, 1.0], np.float32)
+    oracle.silu_mul_(g, np.array([2.0, 2.0], np.float32))
+    assert g[0] == 0.0 and np.isclose(g[1], 2.0 / (1.0 + np.exp(-1.0)))
