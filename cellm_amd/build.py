@@ -20,6 +20,7 @@ PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 BUILD_DIR = PKG_DIR / "_build"
 LIB_PATH = PKG_DIR / "libcellm_hip.so"
+STEP_LIB_PATH = PKG_DIR / "libcellm_llama_step.so"
 REPO_ROOT = PKG_DIR.parent
 
 SOURCES = ["qgemv.hip", "qgemm.hip", "dequant.hip", "capi.cpp"]
@@ -78,7 +79,25 @@ def build_library(verbose: bool = False, jobs: int = 4) -> Path:
     if res.returncode != 0:
         raise RuntimeError("link failed:\n" + res.stderr)
     os.replace(tmp, LIB_PATH)
+    build_step_library(verbose)
     return LIB_PATH
+
+
+def build_step_library(verbose: bool = False) -> Path:
+    """The host-side decode-step runner over libcellm_hip.so (pure C++, CPU
+    parts compiled without FP contraction so they round as the reference)."""
+    cxx = os.environ.get("CXX", "g++")
+    tmp = STEP_LIB_PATH.with_suffix(".so.tmp")
+    cmd = [cxx, "-O3", "-std=c++17", "-fPIC", "-shared", "-ffp-contract=off", "-fno-fast-math", "-fno-math-errno",
+           "-Wall", "-o", str(tmp), str(CSRC / "llama_step.cpp"), f"-L{PKG_DIR}", "-lcellm_hip",
+           "-Wl,-rpath,$ORIGIN"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError("decode-step library build failed:\n" + res.stderr)
+    os.replace(tmp, STEP_LIB_PATH)
+    return STEP_LIB_PATH
 
 
 if __name__ == "__main__":

@@ -1,0 +1,83 @@
+/*
+ * cellm_llama_step.h -- host-side Llama decode step whose projections run on
+ * libcellm_hip.so (the config-5 harness).
+ *
+ * This is the runner side of the boundary, above the C ABI of cellm_hip.h:
+ * it mirrors LlamaRunner::step_topk / step_inner
+ * (crates/cellm-model/src/llama.rs:189-212, 235-647) with every int8
+ * projection (q, k, v, o, gate, up, down, tied lm_head) issued to the HIP
+ * qGEMV, while embedding, RMSNorm, RoPE, the paged f16 KV cache and GQA
+ * attention stay on the CPU ("the existing path", as a Rust runner with a
+ * HipOps would keep them).  Greedy top-1 follows topk_from_logits
+ * (llama.rs:1049-1078).
+ *
+ * Status codes are those of cellm_hip.h; this library's own messages are
+ * read with cellm_llama_last_error_message (errors raised inside
+ * libcellm_hip.so are copied there too).
+ */
+#ifndef CELLM_LLAMA_STEP_H
+#define CELLM_LLAMA_STEP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Model shape (ModelConfig, crates/cellm-model/src/lib.rs; .cellm header). */
+typedef struct {
+    int32_t n_layers;
+    int32_t hidden;
+    int32_t n_heads;
+    int32_t n_kv_heads;
+    int32_t head_dim;
+    int32_t intermediate;
+    int32_t vocab;
+    float rms_norm_eps;
+    float rope_theta;
+    int32_t tokens_per_block; /* KvCacheLayout::tokens_per_block */
+    int32_t total_blocks;     /* KvCacheLayout::total_blocks */
+} cellm_llama_config_t;
+
+/* One layer's host tensors: int8 [out, in] weights with f16 per-row scales
+ * (".qscale"), f16 RMSNorm weights.  Order: q, k, v, o, gate, up, down. */
+typedef struct {
+    const int8_t* w[7];
+    const uint16_t* scale_f16[7];
+    const uint16_t* input_layernorm_f16;
+    const uint16_t* post_attention_layernorm_f16;
+} cellm_llama_layer_t;
+
+typedef struct cellm_llama cellm_llama_t;
+
+/* Copies the calling thread's last error message; returns its full length. */
+size_t cellm_llama_last_error_message(char* buf, size_t buf_len);
+
+/* Builds the runner on `device`, uploading every projection weight once into
+ * the HIP weight cache.  embed_i8 [vocab, hidden] with f16 row scales is also
+ * the tied lm_head.  Host arrays may be freed after the call. */
+int32_t cellm_llama_create(const cellm_llama_config_t* cfg, const cellm_llama_layer_t* layers,
+                           const int8_t* embed_i8, const uint16_t* embed_scale_f16,
+                           const uint16_t* final_norm_f16, int32_t device, cellm_llama_t** out);
+
+void cellm_llama_destroy(cellm_llama_t* m);
+
+/* The CPU paged KV cache: K and V are f16 arrays of
+ * total_blocks * n_layers * tokens_per_block * n_kv_heads * head_dim elements,
+ * laid out as KvCacheLayout::token_base_elem (crates/cellm-core/src/kv_cache.rs:62-73).
+ * Returned pointers stay valid until destroy; callers may seed them. */
+int32_t cellm_llama_kv_cache(cellm_llama_t* m, uint16_t** k_f16, uint16_t** v_f16, size_t* n_elems);
+
+/* One decode step of one session (LlamaRunner::step_topk with top_k = 1):
+ * embeds `token`, writes this position's K/V into block
+ * block_table[pos / tokens_per_block], attends over positions 0..pos, and
+ * returns the greedy id and its logit.  logits_out (vocab floats) is optional. */
+int32_t cellm_llama_step(cellm_llama_t* m, uint32_t token, size_t pos, const uint32_t* block_table,
+                         size_t n_blocks, uint32_t* out_token, float* out_logit, float* logits_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CELLM_LLAMA_STEP_H */

@@ -13,10 +13,10 @@ ROOT = Path(__file__).resolve().parent.parent
 HEADER = ROOT / "include" / "cellm_hip.h"
 
 
-def declared_symbols() -> set[str]:
-    text = HEADER.read_text()
+def declared_symbols(header: Path = HEADER, prefix: str = "cellm_hip_") -> set[str]:
+    text = header.read_text()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return set(re.findall(r"\b(cellm_hip_\w+)\s*\(", text))
+    return set(re.findall(r"\b(" + prefix + r"\w+)\s*\(", text))
 
 
 def test_library_exports_every_declared_symbol():
@@ -86,3 +86,19 @@ def test_product_does_not_import_oracle():
     for p in list(pkg.rglob("*.py")) + list(pkg.rglob("*.cpp")) + list(pkg.rglob("*.hip")) + list(pkg.rglob("*.hpp")):
         text = p.read_text()
         assert "import oracle" not in text and "from oracle" not in text and "liboracle" not in text, p
+
+
+def test_step_library_exports_its_header():
+    from cellm_amd import build
+
+    assert build.STEP_LIB_PATH.exists(), "libcellm_llama_step.so not built"
+    out = subprocess.run(["nm", "-D", "--defined-only", str(build.STEP_LIB_PATH)], capture_output=True, text=True,
+                         check=True)
+    exported = set(re.findall(r"\bT (cellm_llama_\w+)", out.stdout))
+    declared = declared_symbols(ROOT / "include" / "cellm_llama_step.h", "cellm_llama_")
+    assert declared and not (declared - exported), sorted(declared - exported)
+
+
+def test_every_header_is_checked():
+    headers = {p.name for p in (ROOT / "include").glob("*.h")}
+    assert headers == {"cellm_hip.h", "cellm_llama_step.h"}, headers

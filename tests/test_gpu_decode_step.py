@@ -1,0 +1,177 @@
+"""Config 5: a full random-init SmolLM2-360M-shape decode step.
+
+32 layers, hidden 960, 15 q / 5 kv heads, head_dim 64, intermediate 2560,
+vocab 49152, int8 per-row weights.  Context 512 of seeded f16 KV, 4 sessions
+decoded one at a time (crates/cellm-sdk/src/lib.rs:622-680).
+
+The HIP side is libcellm_llama_step.so: projections on the HIP qGEMV,
+embedding/RMSNorm/RoPE/paged KV/attention on the CPU.  The reference side is
+the all-CPU oracle step (LlamaRunner::step_inner, llama.rs:235-647, with the
+i8 lm_head loop of llama.rs:602-643).  Greedy ids must be identical.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+L, HID, NH, NKV, HD, INTER, VOCAB = 32, 960, 15, 5, 64, 2560, 49152
+EPS, THETA, TPB, CTX, SESSIONS = 1e-5, 100000.0, 16, 512, 4
+KVD = NKV * HD
+BLOCKS_PER_SESSION = CTX // TPB
+TOTAL_BLOCKS = SESSIONS * BLOCKS_PER_SESSION
+
+
+class Config(C.Structure):
+    _fields_ = [("n_layers", C.c_int32), ("hidden", C.c_int32), ("n_heads", C.c_int32), ("n_kv_heads", C.c_int32),
+                ("head_dim", C.c_int32), ("intermediate", C.c_int32), ("vocab", C.c_int32),
+                ("rms_norm_eps", C.c_float), ("rope_theta", C.c_float), ("tokens_per_block", C.c_int32),
+                ("total_blocks", C.c_int32)]
+
+
+class Layer(C.Structure):
+    _fields_ = [("w", C.c_void_p * 7), ("scale_f16", C.c_void_p * 7), ("input_layernorm_f16", C.c_void_p),
+                ("post_attention_layernorm_f16", C.c_void_p)]
+
+
+def _shapes():
+    return [(HID, HID), (KVD, HID), (KVD, HID), (HID, HID), (INTER, HID), (INTER, HID), (HID, INTER)]
+
+
+def make_model():
+    """Seeded int8 weights with variance-preserving f16 row scales."""
+    layers = []
+    for l in range(L):
+        ws, ss = [], []
+        for j, (o, i) in enumerate(_shapes()):
+            sd = 0xC5000000 + l * 64 + j * 4
+            ws.append(oracle.gen_i8((o, i), sd))
+            base = 1.0 / (73.3 * np.sqrt(i))
+            ss.append((oracle.gen_uniform((o,), sd + 1, 0.5, 1.5) * base).astype(np.float16).view(np.uint16))
+        n1 = (1.0 + 0.1 * oracle.lcg_fill(HID, 0xC5100000 + l, 1.0)).astype(np.float16).view(np.uint16)
+        n2 = (1.0 + 0.1 * oracle.lcg_fill(HID, 0xC5200000 + l, 1.0)).astype(np.float16).view(np.uint16)
+        layers.append((ws, ss, n1, n2))
+    embed = oracle.gen_i8((VOCAB, HID), 0xC5300000)
+    escale = (oracle.gen_uniform((VOCAB,), 0xC5300001, 0.5, 1.5) / 127.0).astype(np.float16).view(np.uint16)
+    fnorm = (1.0 + 0.1 * oracle.lcg_fill(HID, 0xC5300002, 1.0)).astype(np.float16).view(np.uint16)
+    return layers, embed, escale, fnorm
+
+
+def make_kv():
+    """Seeded f16 K/V for positions 0..CTX-2 of every session (the step writes CTX-1)."""
+    n = TOTAL_BLOCKS * L * TPB * KVD
+    k = oracle.gen_normal((n,), 0xC5400000, 0.0, 1.0).astype(np.float16).view(np.uint16)
+    v = oracle.gen_normal((n,), 0xC5400001, 0.0, 1.0).astype(np.float16).view(np.uint16)
+    return k, v
+
+
+def block_table(s):
+    # interleave sessions across blocks so pages are not contiguous per session
+    return np.array([b * SESSIONS + s for b in range(BLOCKS_PER_SESSION)], np.uint32)
+
+
+def base_of(bt, tpos, layer):
+    return int(bt[tpos // TPB]) * (L * TPB * KVD) + layer * (TPB * KVD) + (tpos % TPB) * KVD
+
+
+def oracle_step(model, kcache, vcache, token, pos, bt):
+    layers, embed, escale, fnorm = model
+    t = token % VOCAB
+    x = (embed[t].astype(np.float32) * np.float32(oracle.f16_bits_to_f32(escale[t:t + 1])[0])).astype(np.float32)
+    bases = np.array([base_of(bt, tp, 0) for tp in range(pos + 1)], np.uint64)
+    for l in range(L):
+        ws, ss, n1, n2 = layers[l]
+        xn = oracle.rms_norm(x, oracle.f16_bits_to_f32(n1), EPS)
+        q = oracle.matmul_i8_f32(ws[0], ss[0], xn)
+        k = oracle.matmul_i8_f32(ws[1], ss[1], xn)
+        v = oracle.matmul_i8_f32(ws[2], ss[2], xn)
+        oracle.rope_half_(q, NH, HD, pos, THETA)
+        oracle.rope_half_(k, NKV, HD, pos, THETA)
+        wb = base_of(bt, pos, l)
+        kcache[wb:wb + KVD] = k.astype(np.float16).view(np.uint16)
+        vcache[wb:wb + KVD] = v.astype(np.float16).view(np.uint16)
+        lb = bases + np.uint64(l * TPB * KVD)
+        attn = oracle.attention_gqa_f16kv(kcache, vcache, lb, q, NH, NKV, HD)
+        x = x + oracle.matmul_i8_f32(ws[3], ss[3], attn)
+        xn = oracle.rms_norm(x, oracle.f16_bits_to_f32(n2), EPS)
+        g = oracle.matmul_i8_f32(ws[4], ss[4], xn)
+        u = oracle.matmul_i8_f32(ws[5], ss[5], xn)
+        oracle.silu_mul_(g, u)
+        x = x + oracle.matmul_i8_f32(ws[6], ss[6], g)
+    xf = oracle.rms_norm(x, oracle.f16_bits_to_f32(fnorm), EPS)
+    logits = oracle.llama_lm_head_i8(xf, embed, escale)
+    return oracle.argmax_first(logits), logits
+
+
+def test_decode_step_greedy_ids_match_cpu_reference():
+    from cellm_amd import build
+    from cellm_amd._lib import load
+
+    load()  # libcellm_hip first, loudly
+    lib = C.CDLL(str(build.STEP_LIB_PATH))
+    lib.cellm_llama_create.argtypes = [C.POINTER(Config), C.POINTER(Layer), C.c_void_p, C.c_void_p, C.c_void_p,
+                                       C.c_int32, C.POINTER(C.c_void_p)]
+    lib.cellm_llama_kv_cache.argtypes = [C.c_void_p, C.POINTER(C.c_void_p), C.POINTER(C.c_void_p),
+                                         C.POINTER(C.c_size_t)]
+    lib.cellm_llama_step.argtypes = [C.c_void_p, C.c_uint32, C.c_size_t, C.c_void_p, C.c_size_t,
+                                     C.POINTER(C.c_uint32), C.POINTER(C.c_float), C.c_void_p]
+    lib.cellm_llama_destroy.argtypes = [C.c_void_p]
+    lib.cellm_llama_last_error_message.restype = C.c_size_t
+    lib.cellm_llama_last_error_message.argtypes = [C.c_char_p, C.c_size_t]
+
+    def err():
+        b = C.create_string_buffer(1024)
+        lib.cellm_llama_last_error_message(b, 1024)
+        return b.value.decode()
+
+    model = make_model()
+    layers, embed, escale, fnorm = model
+    cl = (Layer * L)()
+    for l, (ws, ss, n1, n2) in enumerate(layers):
+        for j in range(7):
+            cl[l].w[j] = ws[j].ctypes.data
+            cl[l].scale_f16[j] = ss[j].ctypes.data
+        cl[l].input_layernorm_f16 = n1.ctypes.data
+        cl[l].post_attention_layernorm_f16 = n2.ctypes.data
+    cfg = Config(L, HID, NH, NKV, HD, INTER, VOCAB, EPS, THETA, TPB, TOTAL_BLOCKS)
+    h = C.c_void_p()
+    rc = lib.cellm_llama_create(C.byref(cfg), cl, embed.ctypes.data, escale.ctypes.data, fnorm.ctypes.data, 0,
+                                C.byref(h))
+    assert rc == 0, err()
+    try:
+        kptr, vptr, n = C.c_void_p(), C.c_void_p(), C.c_size_t()
+        assert lib.cellm_llama_kv_cache(h, C.byref(kptr), C.byref(vptr), C.byref(n)) == 0
+        k0, v0 = make_kv()
+        assert n.value == k0.size
+        hk = np.ctypeslib.as_array(C.cast(kptr, C.POINTER(C.c_uint16)), shape=(n.value,))
+        hv = np.ctypeslib.as_array(C.cast(vptr, C.POINTER(C.c_uint16)), shape=(n.value,))
+        hk[:] = k0
+        hv[:] = v0
+        ok, ov = k0.copy(), v0.copy()
+        pos = CTX - 1
+        margins = []
+        for s in range(SESSIONS):
+            token = int(1000 + 7919 * s) % VOCAB
+            bt = block_table(s)
+            tok, logit = C.c_uint32(), C.c_float()
+            hip_logits = np.empty(VOCAB, np.float32)
+            rc = lib.cellm_llama_step(h, token, pos, bt.ctypes.data, bt.size, C.byref(tok), C.byref(logit),
+                                      hip_logits.ctypes.data)
+            assert rc == 0, err()
+            ref_id, ref_logits = oracle_step(model, ok, ov, token, pos, bt)
+            top2 = np.sort(ref_logits)[-2:]
+            margins.append(float(top2[1] - top2[0]))
+            rel = float(np.max(np.abs(hip_logits - ref_logits)) / np.max(np.abs(ref_logits)))
+            print(f"session {s}: token {token} -> hip {tok.value} ref {ref_id} "
+                  f"top2 margin {margins[-1]:.4g} logits rel err {rel:.2e}")
+            assert tok.value == ref_id
+            assert rel <= 1e-3
+        # the step wrote the same K/V row on both sides (f16 RNE of each projection)
+        assert np.array_equal(np.flatnonzero(hk != k0), np.flatnonzero(ok != k0))
+    finally:
+        lib.cellm_llama_destroy(h)
