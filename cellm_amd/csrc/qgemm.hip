@@ -29,6 +29,7 @@ namespace {
 constexpr int BM = 128, BN = 128, BK = 64;
 constexpr int LDS_STRIDE = BK + 8;  // halves; 144-byte rows break LDS bank aliasing
 constexpr int kThreads = 256;
+constexpr int kStages = 4;  // register prefetch depth (K stages of 64 in flight)
 
 template <int SBT>
 __device__ __forceinline__ h8_t dequant_word_f16(uint32_t w, float s, float b)
@@ -45,6 +46,10 @@ __device__ __forceinline__ h8_t dequant_word_f16(uint32_t w, float s, float b)
         } else {
             v = __builtin_fmaf(q, s, b);  // q*s exact: same bits as mul-then-add
         }
+        // Keep the f32 rounding: without this barrier the compiler folds the
+        // fma and the f16 narrowing into one v_fma_mix*_f16, which rounds once
+        // instead of the reference's twice (f32, then f16).
+        asm volatile("" : "+v"(v));
         h[k] = (_Float16)v;
     }
     return h;
@@ -64,15 +69,26 @@ __device__ __forceinline__ h8_t int8_to_f16x8(u2_t w)
     return h;
 }
 
-// WT: 0 = q4 affine (u32 words), 1 = int8.
-template <int WT, int SBT>
+// One K stage (BK = 64) of global data held in registers by one thread:
+// its 32-element halves of one X row and one W row, plus the W row's scale
+// and bias bits for that group (raw, converted when the tile is stored).
+struct StageRegs {
+    u4_t x[4];
+    u4_t w0, w1;  // q4: w0 = 32 nibbles; int8: w0, w1 = 32 bytes
+    uint32_t s, b;
+};
+
+// WT: 0 = q4 affine (u32 words), 1 = int8.  NS = register prefetch depth.
+template <int WT, int SBT, int NS>
 __global__ __launch_bounds__(kThreads) void qgemm_kernel(const void* __restrict__ W, const void* __restrict__ S,
                                                          const void* __restrict__ Bz, int group_size,
                                                          const _Float16* __restrict__ X, float* __restrict__ Y,
                                                          int M, int N, int K, int k_per_split, int per_channel)
 {
-    __shared__ __align__(16) _Float16 xs[BM * LDS_STRIDE];
-    __shared__ __align__(16) _Float16 ws[BN * LDS_STRIDE];
+    // two LDS buffers: stage s is stored into buffer s&1 while no wave can
+    // still read it (every wave passed the barrier after its compute of s-2)
+    __shared__ __align__(16) _Float16 xs[2][BM * LDS_STRIDE];
+    __shared__ __align__(16) _Float16 ws[2][BN * LDS_STRIDE];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -80,52 +96,47 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(const void* __restrict_
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
     const int kbeg = blockIdx.z * k_per_split;
     const int kend = min(K, kbeg + k_per_split);
+    const int nsteps = kend > kbeg ? (kend - kbeg) / BK : 0;  // K % 64 == 0, k_per_split % 64 == 0
 
-    // global -> register staging assignment
-    const int ld_row = tid >> 1;        // 0..127
-    const int ld_half = tid & 1;        // which 32-element half of the 64-wide K stage
+    // global -> register assignment: thread = (row, 32-element half of the stage)
+    const int ld_row = tid >> 1;
+    const int ld_half = tid & 1;
     // Rows past M or N are clamped to the last valid row: their loads stay in
     // bounds without a branch and their results are never stored.
     const int xm = min(m0 + ld_row, M - 1), wn_row = min(n0 + ld_row, N - 1);
     const int gshift = __builtin_ctz((unsigned)group_size);
     const int gpr = (K + group_size - 1) >> gshift;
+    const u4_t* w4 = reinterpret_cast<const u4_t*>(W);
 
-    u4_t xr[4];
-    u4_t wr;      // q4: 4 words (32 nibbles); int8: 16 bytes (wr) + 16 bytes (wr2)
-    u4_t wr2;
-    uint32_t sraw = 0, braw = 0;  // scale/bias bits, converted when the tile is stored
-
-    // K % 64 == 0 and k_per_split % 64 == 0, so every stage lies inside [kbeg, kend).
-    auto load_stage = [&](int k0) {
-        const int kc = k0 + ld_half * 32;
+    auto load_stage = [&](int step, StageRegs& r) {
+        const int kc = kbeg + min(step, nsteps - 1) * BK + ld_half * 32;  // clamped: tail slots reload the last stage
 #pragma unroll
-        for (int i = 0; i < 4; ++i) xr[i] = *reinterpret_cast<const u4_t*>(X + (size_t)xm * K + kc + i * 8);
-        const u4_t* w4 = reinterpret_cast<const u4_t*>(W);
+        for (int i = 0; i < 4; ++i) r.x[i] = *reinterpret_cast<const u4_t*>(X + (size_t)xm * K + kc + i * 8);
         if constexpr (WT == 0) {
-            wr = __builtin_nontemporal_load(w4 + ((size_t)wn_row * K + kc) / 32);
+            r.w0 = __builtin_nontemporal_load(w4 + ((size_t)wn_row * K + kc) / 32);
             const size_t gi = (size_t)wn_row * gpr + (kc >> gshift);
-            sraw = load_raw<SBT>(S, gi);
-            braw = load_raw<SBT>(Bz, gi);
+            r.s = load_raw<SBT>(S, gi);
+            r.b = load_raw<SBT>(Bz, gi);
         } else {
-            wr = __builtin_nontemporal_load(w4 + ((size_t)wn_row * K + kc) / 16);
-            wr2 = __builtin_nontemporal_load(w4 + ((size_t)wn_row * K + kc) / 16 + 1);
+            r.w0 = __builtin_nontemporal_load(w4 + ((size_t)wn_row * K + kc) / 16);
+            r.w1 = __builtin_nontemporal_load(w4 + ((size_t)wn_row * K + kc) / 16 + 1);
         }
     };
 
-    auto store_stage = [&]() {
-        _Float16* xd = xs + ld_row * LDS_STRIDE + ld_half * 32;
+    auto store_stage = [&](const StageRegs& r, int buf) {
+        _Float16* xd = xs[buf] + ld_row * LDS_STRIDE + ld_half * 32;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) *reinterpret_cast<u4_t*>(xd + i * 8) = xr[i];
-        _Float16* wd = ws + ld_row * LDS_STRIDE + ld_half * 32;
+        for (int i = 0; i < 4; ++i) *reinterpret_cast<u4_t*>(xd + i * 8) = r.x[i];
+        _Float16* wd = ws[buf] + ld_row * LDS_STRIDE + ld_half * 32;
         if constexpr (WT == 0) {
-            const float sc = raw_to_f32<SBT>(sraw), bi = raw_to_f32<SBT>(braw);
+            const float sc = raw_to_f32<SBT>(r.s), bi = raw_to_f32<SBT>(r.b);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) *reinterpret_cast<h8_t*>(wd + i * 8) = dequant_word_f16<SBT>(wr[i], sc, bi);
+            for (int i = 0; i < 4; ++i) *reinterpret_cast<h8_t*>(wd + i * 8) = dequant_word_f16<SBT>(r.w0[i], sc, bi);
         } else {
-            *reinterpret_cast<h8_t*>(wd + 0) = int8_to_f16x8(u2_t{wr[0], wr[1]});
-            *reinterpret_cast<h8_t*>(wd + 8) = int8_to_f16x8(u2_t{wr[2], wr[3]});
-            *reinterpret_cast<h8_t*>(wd + 16) = int8_to_f16x8(u2_t{wr2[0], wr2[1]});
-            *reinterpret_cast<h8_t*>(wd + 24) = int8_to_f16x8(u2_t{wr2[2], wr2[3]});
+            *reinterpret_cast<h8_t*>(wd + 0) = int8_to_f16x8(u2_t{r.w0[0], r.w0[1]});
+            *reinterpret_cast<h8_t*>(wd + 8) = int8_to_f16x8(u2_t{r.w0[2], r.w0[3]});
+            *reinterpret_cast<h8_t*>(wd + 16) = int8_to_f16x8(u2_t{r.w1[0], r.w1[1]});
+            *reinterpret_cast<h8_t*>(wd + 24) = int8_to_f16x8(u2_t{r.w1[2], r.w1[3]});
         }
     };
 
@@ -137,26 +148,53 @@ __global__ __launch_bounds__(kThreads) void qgemm_kernel(const void* __restrict_
 
     const int frag_row = lane & 15;
     const int frag_k = (lane >> 4) * 8;
-
-    load_stage(kbeg);
-    for (int k0 = kbeg; k0 < kend; k0 += BK) {
-        __syncthreads();  // previous stage fully consumed
-        store_stage();
-        __syncthreads();
-        if (k0 + BK < kend) load_stage(k0 + BK);
+    auto compute = [&](int buf) {
 #pragma unroll
         for (int kk = 0; kk < BK; kk += 32) {
             h8_t a[4], b[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                a[i] = *reinterpret_cast<const h8_t*>(xs + (wm * 64 + i * 16 + frag_row) * LDS_STRIDE + kk + frag_k);
+                a[i] = *reinterpret_cast<const h8_t*>(xs[buf] + (wm * 64 + i * 16 + frag_row) * LDS_STRIDE + kk + frag_k);
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                b[j] = *reinterpret_cast<const h8_t*>(ws + (wn * 64 + j * 16 + frag_row) * LDS_STRIDE + kk + frag_k);
+                b[j] = *reinterpret_cast<const h8_t*>(ws[buf] + (wn * 64 + j * 16 + frag_row) * LDS_STRIDE + kk + frag_k);
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+        }
+    };
+
+    if (nsteps > 0) {
+        // Software pipeline.  Stage s is in LDS buffer s&1 when step s starts;
+        // step s dequantizes and stores stage s+1 into the other buffer while
+        // its own MFMAs run (same basic block, so VALU issues in the MFMA
+        // shadow), then one barrier, then the freed ring slot is refilled with
+        // stage s+1+NS.  Buffer (s+1)&1 last held stage s-1, which every wave
+        // finished reading before the barrier that ended step s-1.
+        StageRegs ring[NS];
+#pragma unroll
+        for (int j = 0; j < NS; ++j) load_stage(j, ring[j]);
+        store_stage(ring[0], 0);
+        __syncthreads();
+        load_stage(NS, ring[0]);
+        for (int s0 = 0; s0 < nsteps; s0 += NS) {
+#pragma unroll
+            for (int j = 0; j < NS; ++j) {
+                const int s = s0 + j;
+                if (s < nsteps) {
+                    // past the end this stores a clamped copy of the last stage
+                    // into the idle buffer; nobody reads it
+                    store_stage(ring[(j + 1) % NS], (s + 1) & 1);
+                    compute(s & 1);
+                }
+                // The barrier and the reload run on every path (s is block-uniform and
+                // the reload is clamped), so each unrolled step issues the same loads
+                // and the compiler's vmcnt stays partial across the loop back edge.
+                __syncthreads();
+                load_stage(s + 1 + NS, ring[(j + 1) % NS]);
+            }
         }
     }
 
@@ -209,7 +247,9 @@ int qgemm_splits(int M, int N, int K)
     const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
     const int ksteps = (K + BK - 1) / BK;
     int splits = 1;
-    while (tiles * splits * 2 <= 320 && ksteps / (splits * 2) >= 4) splits *= 2;
+    // one round of blocks on 256 CUs; each split keeps >= 8 stages so the
+    // prefetch ring has something to overlap
+    while (tiles * splits * 2 <= 256 && ksteps / (splits * 2) >= 8) splits *= 2;
     return splits;
 }
 
@@ -230,7 +270,7 @@ static hipError_t launch_qgemm_common(const void* W, const void* S, const void* 
     const dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM, splits);
     float* out = splits > 1 ? workspace : Y;
 #define CELLM_QGEMM(SBT_)                                                                                          \
-    hipLaunchKernelGGL((qgemm_kernel<WT, SBT_>), grid, dim3(kThreads), 0, st, W, S, B, group_size, X, out, M, N, K, \
+    hipLaunchKernelGGL((qgemm_kernel<WT, SBT_, kStages>), grid, dim3(kThreads), 0, st, W, S, B, group_size, X, out, M, N, K, \
                        k_per_split, per_channel)
     if (sbt == DT_F32) CELLM_QGEMM(DT_F32);
     else if (sbt == DT_F16) CELLM_QGEMM(DT_F16);

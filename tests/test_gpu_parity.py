@@ -236,6 +236,26 @@ def test_q4_prefill_qgemm_m512(ops, k, n):
     assert rel_err(y, ref32) <= TOL_F16_TILE
 
 
+@pytest.mark.parametrize("sb", [np.float16, "bf16", np.float32])
+def test_qgemm_tiles_are_the_converter_f16_dequant(ops, sb):
+    """X = identity makes Y[m, n] = W_tile[n, m]: one exact product, zeros
+    elsewhere, so the GEMM output exposes the f16 tile values bit for bit.
+    Row 0 carries the double-rounding case of the oracle pins (q=3,
+    s=1+2^-10, b=-2^-24), where one rounding of q*s+b would differ."""
+    import torch
+
+    k, n = 256, 64
+    wq, s, b, _ = make_q4(n, k, 1, cfg=4, sb_dtype=sb, salt=77)
+    if sb == np.float16:
+        wq[0, 0] = (wq[0, 0] & ~np.uint32(0xF)) | np.uint32(3)
+        s[0, 0] = np.float16(1 + 2 ** -10)
+        b[0, 0] = np.float16(-(2.0 ** -24))
+    x = np.eye(k, dtype=np.float16)
+    y = _run_q4(ops, wq, s, b, x, gemm=True)
+    ref16 = oracle.f16_bits_to_f32(oracle.dequant_q4_affine_f16(wq, s, b, k))
+    np.testing.assert_array_equal(y.T.view(np.uint32), ref16.view(np.uint32))
+
+
 def test_qgemm_ragged_m_n(ops):
     m, k, n = 37, 192, 77
     wq, s, b, x = make_q4(n, k, m, cfg=4, salt=5)
