@@ -160,6 +160,13 @@ int32_t qgemv_i8_impl(cellm_hip_ctx* ctx, const int8_t* w, const void* scales, i
     if (n_scales < 1) return set_error(CELLM_HIP_ERR_INVALID_ARG, "n_scales must be >= 1");
     const int per_channel = n_scales >= n ? 1 : 0;
     const bool gemm_ok = xdt == DT_F16 && k > 0 && (k % 64) == 0 && aligned16(w) && aligned16(x);
+    // 2..64 activation rows: weights streamed once into MFMA operands (exact for int8)
+    if (!force_gemm && gemm_ok && qgemv_mfma_supported(1, (int)m, (int)k, 0)) {
+        HIP_TRY(launch_qgemv_mfma_i8(w, scales, sdt, per_channel, reinterpret_cast<const _Float16*>(x), bias, y,
+                                     (int)m, (int)n, (int)k, st),
+                "qgemv_mfma_i8 launch");
+        return CELLM_HIP_OK;
+    }
     if ((force_gemm || m > 4) && gemm_ok) {
         float* ws = nullptr;
         if (int32_t rc = get_workspace(ctx, st, (int)m, (int)n, (int)k, &ws)) return rc;
@@ -187,6 +194,14 @@ int32_t qgemv_q4_impl(cellm_hip_ctx* ctx, const uint32_t* wq, const void* scales
     if (k > 0 && (!wq || !scales || !biases || !x)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null input pointer");
     if (!y) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null output pointer");
     const bool gemm_ok = xdt == DT_F16 && k > 0 && (k % 64) == 0 && group >= 32 && aligned16(wq) && aligned16(x);
+    // 5..64 activation rows: f16 MFMA tiles dequantized in registers (M <= 4
+    // keeps the f32-accumulating VALU GEMV)
+    if (!force_gemm && m > 4 && gemm_ok && qgemv_mfma_supported(0, (int)m, (int)k, (int)group)) {
+        HIP_TRY(launch_qgemv_mfma_q4(wq, scales, biases, sbt, (int)group, reinterpret_cast<const _Float16*>(x), y,
+                                     (int)m, (int)n, (int)k, st),
+                "qgemv_mfma_q4 launch");
+        return CELLM_HIP_OK;
+    }
     if ((force_gemm || m > 4) && gemm_ok) {
         float* ws = nullptr;
         if (int32_t rc = get_workspace(ctx, st, (int)m, (int)n, (int)k, &ws)) return rc;

@@ -39,6 +39,14 @@ hipError_t launch_qgemm_q4_affine_ws(const uint32_t* wq, const void* S, const vo
 hipError_t launch_qgemm_i8_ws(const int8_t* w, const void* S, int sdt, int per_channel, const _Float16* x,
                               const float* bias, float* y, int M, int N, int K, float* workspace, hipStream_t st);
 
+// Batched decode on MFMA (2 <= M <= 64, f16 x): int8 needs K % 64 == 0,
+// q4 K % 128 == 0 and group >= 32; 16-byte aligned W and x.
+bool qgemv_mfma_supported(int wt, int M, int K, int group_size);
+hipError_t launch_qgemv_mfma_i8(const int8_t* w, const void* S, int sdt, int per_channel, const _Float16* x,
+                                const float* bias, float* y, int M, int N, int K, hipStream_t st);
+hipError_t launch_qgemv_mfma_q4(const uint32_t* wq, const void* S, const void* B, int sbt, int group_size,
+                                const _Float16* x, float* y, int M, int N, int K, hipStream_t st);
+
 // Device smoke test kernel: out[i] = a[i] + b[i].
 hipError_t launch_add_f32(const float* a, const float* b, float* out, int n, hipStream_t st);
 

@@ -1,0 +1,409 @@
+// Batched decode GEMV on MFMA (2 <= M <= 64 activation rows, f16 x).
+//
+//   int8:  y[m,n] = (sum_k W[n,k] x[m,k]) * s[n] (+ bias[n])
+//          (crates/cellm-kernels/src/cpu_kernels.rs:66-133, one row per call)
+//   q4:    y[m,n] = sum_k (q S + B)[n,k] x[m,k]   (crates/cellm-model/src/lfm.rs:985-1066)
+//
+// The reference decodes sessions one at a time (crates/cellm-sdk/src/lib.rs:622-680);
+// batching M sessions reads every weight once for all of them.  At M <= 64
+// the work is still HBM-bound (<= 128 flop per int8 weight byte), but a VALU
+// dot product would need 2*M ops per weight, so the multiply runs on
+// v_mfma_f32_16x16x32_f16 with A = X (M padded to 16-row tiles) and B = W.
+//
+// Each wave owns NT 16-row tiles of W.  W streams from HBM with 16-byte loads
+// straight into B-operand registers -- no LDS for W, no sharing, each weight
+// is read once.  A lane (row n = lane%16, slot group g = lane/16) holds one
+// 16-byte chunk of its row per K block:
+//   int8: 16 weights, k = kb + 16g .. +16, two MFMA k-steps (t = 0,1: 8 each);
+//   q4:   32 weights (one group), k = kb + 32g .. +32, four k-steps.
+// The MFMA contracts over whatever k each slot carries as long as A and B
+// agree, so X is staged in LDS per 8-k word in the order the unpacked weight
+// pairs come out (int8: 0,2,1,3,4,6,5,7; q4: 0,4,1,5,2,6,3,7).
+//
+// Dequant into the f16 B operand:
+//   int8: u8 = w ^ 0x80 is exact in f16 as (1152 + w) - 1152 (v_and_or_b32 +
+//         v_pk_add_f16), so products are exact and the result differs from
+//         the reference only by summation order; the row scale is applied
+//         after the sum, as in the reference.
+//   q4:   exact q (magic 0x6400 nibble trick, pk_add), then one packed f16
+//         FMA per pair: w = RN_f16(q*s + b).  One f16 rounding per weight
+//         (the fp16-tile tolerance of the MFMA paths); the odd nibbles come
+//         out as 16q and meet s/16, which is exact.
+#include <algorithm>
+#include <mutex>
+#include <vector>
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace cellm {
+
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kRowRor8 = 0x128;  // DPP control: rotate by 8 within each 16-lane row
+
+// Permutation of one 8-element x word into the unpack order.
+template <int WT>
+__device__ __forceinline__ h8_t permute_word(h8_t v)
+{
+    if constexpr (WT == 1) return h8_t{v[0], v[2], v[1], v[3], v[4], v[6], v[5], v[7]};
+    else return h8_t{v[0], v[4], v[1], v[5], v[2], v[6], v[3], v[7]};
+}
+
+// int8 word pair (8 weights) -> f16 x8 in order 0,2,1,3,4,6,5,7 (exact).
+__device__ __forceinline__ h8_t i8x8_to_f16(uint32_t w0, uint32_t w1)
+{
+    const uint32_t mlo = 0x00FF00FFu, magic = 0x64006400u;
+    const h2_t off = {(_Float16)1152.0f, (_Float16)1152.0f};
+    const uint32_t b0 = w0 ^ 0x80808080u, b1 = w1 ^ 0x80808080u;
+    const h2_t a0 = as_h2(and_or(b0, mlo, magic)) - off;       // (w0, w2)
+    const h2_t a1 = as_h2(and_or(b0 >> 8, mlo, magic)) - off;  // (w1, w3)
+    const h2_t a2 = as_h2(and_or(b1, mlo, magic)) - off;       // (w4, w6)
+    const h2_t a3 = as_h2(and_or(b1 >> 8, mlo, magic)) - off;  // (w5, w7)
+    return h8_t{a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
+}
+
+// q4 word (8 nibbles) -> f16 x8 in order 0,4,1,5,2,6,3,7: RN_f16(q*s + b).
+__device__ __forceinline__ h8_t q4_to_f16(uint32_t w, h2_t s2, h2_t s16, h2_t b2)
+{
+    const uint32_t m0f = 0x000F000Fu, m1f = 0x00F000F0u, magic = 0x64006400u;
+    const h2_t off = {(_Float16)1024.0f, (_Float16)1024.0f};
+    const uint32_t h = w >> 8;
+    const h2_t q04 = as_h2(and_or(w, m0f, magic)) - off;    // (q0, q4)
+    const h2_t q15 = as_h2(and_or(w, m1f, magic)) - off;    // (16 q1, 16 q5)
+    const h2_t q26 = as_h2(and_or(h, m0f, magic)) - off;    // (q2, q6)
+    const h2_t q37 = as_h2(and_or(h, m1f, magic)) - off;    // (16 q3, 16 q7)
+    const h2_t r0 = q04 * s2 + b2;
+    const h2_t r1 = q15 * s16 + b2;
+    const h2_t r2 = q26 * s2 + b2;
+    const h2_t r3 = q37 * s16 + b2;
+    return h8_t{r0[0], r0[1], r1[0], r1[1], r2[0], r2[1], r3[0], r3[1]};
+}
+
+// Persistent streaming kernel.  WT: 0 = q4 affine, 1 = int8.  MS = 16-row
+// tiles of X (ceil(M/16)); NT = 16-row tiles of W per wave; DEPTH = pairs of
+// K blocks a wave loads per group; SBT = scale (and q4 bias) dtype; CHUNKED: X
+// does not fit LDS whole and is staged per K chunk of KC columns (KC a
+// multiple of a group's columns).
+//
+// A block owns tiles of ROWS = 4*NT*16 weight rows: tile, tile+grid, ...  Each
+// wave walks its rows in groups of DEPTH block pairs (128 B of every row per
+// pair): it issues the whole group's loads (8 KB per wave), waits once, then
+// runs the group's MFMAs.  Memory stays busy through the other waves of the
+// CU (8-16 per CU), so no cross-iteration register ring is needed -- the
+// compiler counts outstanding loads exactly only through straight-line code,
+// and a ring that crosses tile boundaries would wait on every load anyway.
+template <int WT, int MS, int NT, int DEPTH, int SBT, bool CHUNKED>
+__global__ __launch_bounds__(kBlock) void qgemv_mfma_kernel(
+    const void* __restrict__ W, const void* __restrict__ S, const void* __restrict__ Bz, int per_channel, int gshift,
+    const _Float16* __restrict__ X, const float* __restrict__ bias, float* __restrict__ Y, int M, int N, int K, int KC,
+    int ntiles)
+{
+    extern __shared__ __align__(16) _Float16 xs[];  // [MS*16][KC + 8]
+    constexpr int KB = WT == 1 ? 64 : 128;  // K per block: 64 bytes of every row
+    constexpr int TSTEPS = KB / 32;         // MFMA k-steps per block
+    constexpr int ROWS = (kBlock / 64) * NT * 16;
+    const int stride = KC + 8;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int rl = lane & 15, g = lane >> 4;
+    const int nkb = K / KB;
+    const int gpr = (K + (1 << gshift) - 1) >> gshift;
+    const size_t row_bytes = WT == 1 ? (size_t)K : (size_t)K / 2;
+    const char* wb = reinterpret_cast<const char*>(W);
+    const int row_in_tile = wave * NT * 16 + rl;
+
+    // ---- X staging: columns [k0, k0 + kcl) in unpack order, rows >= M zero.
+    // Loads are unconditional (clamped) so they issue back to back.
+    auto stage = [&](int k0, int kcl) {
+        const int words = kcl >> 3, total = MS * 16 * words;
+        for (int base = threadIdx.x; base < total; base += 4 * kBlock) {
+            u4_t r[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int idx = min(base + u * kBlock, total - 1);
+                const int m = idx / words, wd = idx - m * words;
+                r[u] = *reinterpret_cast<const u4_t*>(X + (size_t)min(m, M - 1) * K + k0 + wd * 8);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int idx = base + u * kBlock;
+                const int m = idx / words, wd = idx - m * words;
+                const u4_t v = m < M ? r[u] : u4_t{0u, 0u, 0u, 0u};
+                if (idx < total)
+                    *reinterpret_cast<h8_t*>(xs + (size_t)m * stride + wd * 8) =
+                        permute_word<WT>(__builtin_bit_cast(h8_t, v));
+            }
+        }
+    };
+    if constexpr (!CHUNKED) {
+        stage(0, K);
+        __syncthreads();
+    }
+
+    // One block's B operands + MFMAs: w[t] is this lane's 16 bytes of row
+    // (lane%16) of W tile t at the block's k slot 16*(lane/16) bytes; kx is the
+    // block's first column in the staged X.
+    f4_t acc[MS][NT];
+    auto mma_block = [&](const u4_t(&w)[NT], const uint32_t(&s)[NT], const uint32_t(&b)[NT], int kx) {
+        h8_t bf[NT][TSTEPS];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            if constexpr (WT == 1) {
+                bf[t][0] = i8x8_to_f16(w[t][0], w[t][1]);
+                bf[t][1] = i8x8_to_f16(w[t][2], w[t][3]);
+            } else {
+                const float sc = raw_to_f32<SBT>(s[t]), bi = raw_to_f32<SBT>(b[t]);
+                const h2_t s2 = {(_Float16)sc, (_Float16)sc};
+                const h2_t s16 = {(_Float16)(sc * 0.0625f), (_Float16)(sc * 0.0625f)};
+                const h2_t b2 = {(_Float16)bi, (_Float16)bi};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) bf[t][q] = q4_to_f16(w[t][q], s2, s16, b2);
+            }
+        }
+#pragma unroll
+        for (int st = 0; st < TSTEPS; ++st) {
+            const int kof = kx + g * (KB / 4) + st * 8;
+#pragma unroll
+            for (int i = 0; i < MS; ++i) {
+                const h8_t a = *reinterpret_cast<const h8_t*>(xs + (size_t)(i * 16 + rl) * stride + kof);
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+                    acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bf[t][st], acc[i][t], 0, 0, 0);
+            }
+        }
+    };
+    // stage the X chunk that starts at column kcol, if one does; returns the
+    // column's offset in the staged X
+    auto chunk_at = [&](int kcol) {
+        if constexpr (CHUNKED) {
+            const int c = kcol / KC, off = kcol - c * KC;
+            if (off == 0) {
+                __syncthreads();  // every wave is done with the previous chunk
+                stage(c * KC, min(KC, K - c * KC));
+                __syncthreads();
+            }
+            return off;
+        } else {
+            return kcol;
+        }
+    };
+
+    // Weights load as full 128-byte row segments (two K blocks): load h of a
+    // pair covers rows 8h..8h+7 of a 16-row tile, lane (rl, g) taking row
+    // (rl & 7) + 8h at byte 16g + 64*((rl >> 3) ^ h).  Then, per lane,
+    //   block 0 = rl < 8 ? load0 : load1                (row rl, byte 16g)
+    //   block 1 = row_ror:8 of (rl < 8 ? load1 : load0) (row rl, byte 64 + 16g)
+    // which is the MFMA B layout.  A 16-row x 64-byte load per block (the
+    // layout itself) splits every cache line over two instructions and streams
+    // about a quarter slower.
+    const bool low8 = (rl & 8) == 0;
+    const int npairs = nkb >> 1;
+    for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+        // rows past N read row N-1 and are never stored
+        const char* wpair[NT][2];
+        const char* wtail[NT];
+        size_t sbrow[NT];
+        uint32_t sc_raw[NT];
+        float bv[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const int base = tile * ROWS + wave * NT * 16 + t * 16;
+            const int r = min(base + rl, N - 1);
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                wpair[t][h] = wb + (size_t)min(base + (rl & 7) + 8 * h, N - 1) * row_bytes + 16 * g +
+                              64 * ((rl >> 3) ^ h);
+            wtail[t] = wb + (size_t)r * row_bytes + 16 * g;
+            sbrow[t] = (size_t)r * gpr;
+            sc_raw[t] = 0;
+            bv[t] = 0.0f;
+            if constexpr (WT == 1) {
+                sc_raw[t] = load_raw<SBT>(S, per_channel ? (size_t)r : 0);
+                if (bias) bv[t] = bias[r];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < MS; ++i)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) acc[i][t] = f4_t{0.f, 0.f, 0.f, 0.f};
+
+        for (int p0 = 0; p0 < npairs; p0 += DEPTH) {
+            // the group's weights (and q4 group scale/bias) in one burst
+            u4_t ld[DEPTH][NT][2];
+            uint32_t sr[DEPTH][2][NT], br[DEPTH][2][NT];
+#pragma unroll
+            for (int d = 0; d < DEPTH; ++d) {
+                if (p0 + d < npairs) {
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) {
+#pragma unroll
+                        for (int h = 0; h < 2; ++h)
+                            ld[d][t][h] = __builtin_nontemporal_load(
+                                reinterpret_cast<const u4_t*>(wpair[t][h] + (size_t)(p0 + d) * 128));
+                        if constexpr (WT == 0) {
+#pragma unroll
+                            for (int h = 0; h < 2; ++h) {
+                                const size_t gi = sbrow[t] + ((((p0 + d) * 2 + h) * KB + 32 * g) >> gshift);
+                                sr[d][h][t] = load_raw<SBT>(S, gi);
+                                br[d][h][t] = load_raw<SBT>(Bz, gi);
+                            }
+                        }
+                    }
+                }
+            }
+            const int kx0 = chunk_at(p0 * 2 * KB);
+#pragma unroll
+            for (int d = 0; d < DEPTH; ++d) {
+                if (p0 + d < npairs) {
+                    u4_t w0[NT], w1[NT];
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) {
+                        const u4_t a = ld[d][t][0], b = ld[d][t][1];
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            w0[t][j] = low8 ? a[j] : b[j];
+                            w1[t][j] = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(low8 ? b[j] : a[j]), kRowRor8,
+                                                                             0xF, 0xF, false);
+                        }
+                    }
+                    mma_block(w0, sr[d][0], br[d][0], kx0 + d * 2 * KB);
+                    mma_block(w1, sr[d][1], br[d][1], kx0 + d * 2 * KB + KB);
+                }
+            }
+        }
+        if (nkb & 1) {
+            // odd last block: 16 rows x 64 bytes, already in the B layout
+            u4_t w[NT];
+            uint32_t s[NT], b[NT];
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                w[t] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(wtail[t] + (size_t)(nkb - 1) * 64));
+                if constexpr (WT == 0) {
+                    const size_t gi = sbrow[t] + (((nkb - 1) * KB + 32 * g) >> gshift);
+                    s[t] = load_raw<SBT>(S, gi);
+                    b[t] = load_raw<SBT>(Bz, gi);
+                }
+            }
+            mma_block(w, s, b, chunk_at((nkb - 1) * KB));
+        }
+
+        // C tile: lane holds activation rows 4*(lane/16)+e, weight row lane%16
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const int n = tile * ROWS + row_in_tile + t * 16;
+            const float s = WT == 1 ? raw_to_f32<SBT>(sc_raw[t]) : 1.0f;
+#pragma unroll
+            for (int i = 0; i < MS; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int m = i * 16 + g * 4 + e;
+                    if (n < N && m < M) Y[(size_t)m * N + n] = acc[i][t][e] * s + bv[t];
+                }
+        }
+    }
+}
+
+// Blocks of one instantiation that fit a CU at this LDS size, times the CU
+// count (cached per device and LDS size): the persistent grid.
+template <typename Kern>
+int resident_blocks(Kern kern, size_t lds)
+{
+    struct Entry {
+        const void* kern;
+        int dev;
+        size_t lds;
+        int blocks;
+    };
+    static std::mutex mu;
+    static std::vector<Entry> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 1;
+    const void* key = reinterpret_cast<const void*>(kern);
+    std::lock_guard<std::mutex> lk(mu);
+    for (const Entry& e : cache)
+        if (e.kern == key && e.dev == dev && e.lds == lds) return e.blocks;
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kBlock, lds) != hipSuccess || per_cu < 1)
+        per_cu = 1;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 1;
+    cache.push_back({key, dev, lds, per_cu * cus});
+    return per_cu * cus;
+}
+
+template <int WT, int MS, int NT, int SBT>
+hipError_t launch_mfma_nt(const void* W, const void* S, const void* B, int per_channel, int gshift, const _Float16* X,
+                          const float* bias, float* Y, int M, int N, int K, hipStream_t st)
+{
+    constexpr int KB = WT == 1 ? 64 : 128;
+    constexpr int DEPTH = 4 / NT;  // block pairs per group: 8 KB of weights per wave
+    constexpr int ROWS = (kBlock / 64) * NT * 16;
+    // X in LDS: at most 80 KB per block so two blocks share a CU; the whole K
+    // when it fits, else chunks of KC columns (a multiple of the K block)
+    int KC = std::max(1, (80 * 1024 / (MS * 16 * 2) - 8) / (2 * DEPTH * KB)) * (2 * DEPTH * KB);
+    if (KC >= K) KC = K;
+    const size_t lds = (size_t)MS * 16 * (KC + 8) * 2;
+    const int ntiles = (N + ROWS - 1) / ROWS;
+    if (KC < K) {
+        auto kern = qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, true>;
+        const int grid = std::min(ntiles, resident_blocks(kern, lds));
+        hipLaunchKernelGGL(kern, dim3(grid), dim3(kBlock), lds, st, W, S, B, per_channel, gshift, X, bias, Y, M, N, K,
+                           KC, ntiles);
+    } else {
+        auto kern = qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, false>;
+        const int grid = std::min(ntiles, resident_blocks(kern, lds));
+        hipLaunchKernelGGL(kern, dim3(grid), dim3(kBlock), lds, st, W, S, B, per_channel, gshift, X, bias, Y, M, N, K,
+                           KC, ntiles);
+    }
+    return hipGetLastError();
+}
+
+template <int WT, int MS, int SBT>
+hipError_t launch_mfma_ms(const void* W, const void* S, const void* B, int per_channel, int gshift, const _Float16* X,
+                          const float* bias, float* Y, int M, int N, int K, hipStream_t st)
+{
+    // two 16-row W tiles per wave when there are rows enough to fill the chip
+    if (N >= 128 * 512)
+        return launch_mfma_nt<WT, MS, 2, SBT>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, st);
+    return launch_mfma_nt<WT, MS, 1, SBT>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, st);
+}
+
+template <int WT, int SBT>
+hipError_t launch_mfma(const void* W, const void* S, const void* B, int per_channel, int gshift, const _Float16* X,
+                       const float* bias, float* Y, int M, int N, int K, hipStream_t st)
+{
+    switch ((M + 15) / 16) {
+    case 1: return launch_mfma_ms<WT, 1, SBT>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, st);
+    case 2: return launch_mfma_ms<WT, 2, SBT>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, st);
+    case 3: return launch_mfma_ms<WT, 3, SBT>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, st);
+    default: return launch_mfma_ms<WT, 4, SBT>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, st);
+    }
+}
+
+}  // namespace
+
+bool qgemv_mfma_supported(int wt, int M, int K, int group_size)
+{
+    if (M < 2 || M > 64 || K <= 0) return false;
+    if (wt == 1) return K % 64 == 0;
+    return K % 128 == 0 && group_size >= 32;
+}
+
+hipError_t launch_qgemv_mfma_i8(const int8_t* w, const void* S, int sdt, int per_channel, const _Float16* x,
+                                const float* bias, float* y, int M, int N, int K, hipStream_t st)
+{
+    if (sdt == DT_F16) return launch_mfma<1, DT_F16>(w, S, nullptr, per_channel, 0, x, bias, y, M, N, K, st);
+    if (sdt == DT_F32) return launch_mfma<1, DT_F32>(w, S, nullptr, per_channel, 0, x, bias, y, M, N, K, st);
+    return launch_mfma<1, DT_BF16>(w, S, nullptr, per_channel, 0, x, bias, y, M, N, K, st);
+}
+
+hipError_t launch_qgemv_mfma_q4(const uint32_t* wq, const void* S, const void* B, int sbt, int group_size,
+                                const _Float16* x, float* y, int M, int N, int K, hipStream_t st)
+{
+    const int gshift = __builtin_ctz((unsigned)group_size);
+    if (sbt == DT_F16) return launch_mfma<0, DT_F16>(wq, S, B, 1, gshift, x, nullptr, y, M, N, K, st);
+    if (sbt == DT_F32) return launch_mfma<0, DT_F32>(wq, S, B, 1, gshift, x, nullptr, y, M, N, K, st);
+    return launch_mfma<0, DT_BF16>(wq, S, B, 1, gshift, x, nullptr, y, M, N, K, st);
+}
+
+}  // namespace cellm

@@ -223,6 +223,27 @@ def test_q4_batched_gemma_mlp(ops, m):
     assert rel_err(y, ref16) <= TOL_F32
 
 
+@pytest.mark.parametrize("m", [2, 3, 7, 33])
+def test_i8_batched_mfma_small_m_and_k_chunks(ops, m):
+    """2..64 rows take the MFMA batched path; K=6912 spans several LDS chunks,
+    K=960 and 576 end on an odd 64-column block (576 at m=33: the odd block
+    opens a fresh X chunk)."""
+    for k, n in ((1152, 1000), (6912, 300), (960, 333), (576, 700)):
+        w, s, x = make_i8(n, k, m, cfg=3, x_dtype=np.float16, salt=m + k)
+        y = _run_i8(ops, w, s, x)
+        assert rel_err(y, oracle.qgemv_i8(w, s, x)) <= TOL_F32, (m, k)
+
+
+@pytest.mark.parametrize("m", [5, 17, 64])
+def test_q4_batched_mfma_k_chunks(ops, m):
+    k, n = 6912, 1152  # Gemma down projection: several X chunks in LDS
+    wq, s, b, x = make_q4(n, k, m, cfg=3, salt=m)
+    y = _run_q4(ops, wq, s, b, x)
+    assert rel_err(y, oracle.qgemv_q4_affine(wq, s, b, x, k)) <= TOL_F16_TILE
+    w16 = oracle.f16_bits_to_f32(oracle.dequant_q4_affine_f16(wq, s, b, k))
+    assert rel_err(y, oracle.gemm_xwT(x, w16)) <= TOL_F32
+
+
 @pytest.mark.parametrize("k,n", [(896, 4864), (4864, 896)])
 def test_q4_prefill_qgemm_m512(ops, k, n):
     m = 512
