@@ -131,10 +131,9 @@ int32_t check_group(int64_t group)
 }
 
 // Workspace for split-K on `st`, sized for this call; nullptr if not needed.
-int32_t get_workspace(cellm_hip_ctx* ctx, hipStream_t st, int M, int N, int K, float** out)
+int32_t get_workspace(cellm_hip_ctx* ctx, hipStream_t st, size_t need, float** out)
 {
     *out = nullptr;
-    const size_t need = qgemm_workspace_bytes(M, N, K);
     if (need == 0) return CELLM_HIP_OK;
     std::lock_guard<std::recursive_mutex> lk(ctx->mu);
     DeviceBuffer& b = ctx->workspaces[st];
@@ -169,7 +168,8 @@ int32_t qgemv_i8_impl(cellm_hip_ctx* ctx, const int8_t* w, const void* scales, i
     }
     if ((force_gemm || m > 4) && gemm_ok) {
         float* ws = nullptr;
-        if (int32_t rc = get_workspace(ctx, st, (int)m, (int)n, (int)k, &ws)) return rc;
+        const size_t need = qgemm_workspace_bytes(1, (int)m, (int)n, (int)k, 64, sdt);
+        if (int32_t rc = get_workspace(ctx, st, need, &ws)) return rc;
         HIP_TRY(launch_qgemm_i8_ws(w, scales, sdt, per_channel, reinterpret_cast<const _Float16*>(x), bias, y, (int)m,
                                    (int)n, (int)k, ws, st),
                 "qgemm_i8 launch");
@@ -204,7 +204,8 @@ int32_t qgemv_q4_impl(cellm_hip_ctx* ctx, const uint32_t* wq, const void* scales
     }
     if ((force_gemm || m > 4) && gemm_ok) {
         float* ws = nullptr;
-        if (int32_t rc = get_workspace(ctx, st, (int)m, (int)n, (int)k, &ws)) return rc;
+        const size_t need = qgemm_workspace_bytes(0, (int)m, (int)n, (int)k, (int)group, sbt);
+        if (int32_t rc = get_workspace(ctx, st, need, &ws)) return rc;
         HIP_TRY(launch_qgemm_q4_affine_ws(wq, scales, biases, sbt, (int)group, reinterpret_cast<const _Float16*>(x), y,
                                           (int)m, (int)n, (int)k, ws, st),
                 "qgemm_q4_affine launch");

@@ -29,10 +29,10 @@ hipError_t launch_dequant_q4_affine(const uint32_t* wq, const void* S, const voi
 
 // Prefill / batched qGEMM on MFMA: Y[M,N] = X[M,K] . dequant(W)[N,K]^T with
 // W tiles dequantized to f16 in LDS and f32 accumulation.  Requires K % 64 == 0
-// and 16-byte aligned W and X.  `workspace` (qgemm_workspace_bytes) enables
-// split-K; nullptr runs without it.
+// and 16-byte aligned W and X.  `workspace` (qgemm_workspace_bytes: wt 0 = q4
+// affine, 1 = int8) enables split-K; nullptr runs without it.
 int qgemm_splits(int M, int N, int K);
-size_t qgemm_workspace_bytes(int M, int N, int K);
+size_t qgemm_workspace_bytes(int wt, int M, int N, int K, int group_size, int sbt);
 hipError_t launch_qgemm_q4_affine_ws(const uint32_t* wq, const void* S, const void* B, int sbt, int group_size,
                                      const _Float16* x, float* y, int M, int N, int K, float* workspace,
                                      hipStream_t st);

@@ -19,6 +19,8 @@
 // stage's global data is prefetched into registers during the MFMA loop.
 // Split-K over blockIdx.z writes f32 partials to a workspace that a second
 // kernel sums in a fixed order (deterministic).
+#include <atomic>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -239,6 +241,237 @@ __global__ void add_bias_kernel(float* __restrict__ y, const float* __restrict__
         y[i] += bias[i % N];
 }
 
+
+// ---------------------------------------------------------------------------
+// q4 affine qGEMM, direct-to-LDS pipeline (K % 128 == 0).
+//
+// 512 threads = 8 waves in a 2 (M) x 4 (N) grid of 64x32 wave tiles over a
+// 128x128 block tile; BK = 128 per stage; v_mfma_f32_32x32x16_f16 (its 32x32
+// accumulator keeps the loop free of AGPR<->VGPR moves, which the 16x16
+// form's 16 small accumulators provoke).  Per k-step:
+//   * X[128 rows, 128 k] f16 and the raw nibbles W[128 cols, 128 k] go
+//     global -> LDS with global_load_lds_dwordx4 (no register staging), one
+//     stage ahead of use (two stages);
+//   * each thread dequantizes 32 weights of the next step from the raw LDS
+//     tile into a double-buffered f16 tile with the converter's rounding
+//     (same arithmetic as dequant_word_f16);
+//   * X and W fragments are read from LDS tiles stored in 16 chunks of 8
+//     halves per row, chunk position XOR-swizzled by (row & 15) so that the
+//     16 rows a fragment read touches fall in 16 distinct 4-bank groups.
+// The DMA loads are issued from inline asm with the LDS base in M0 and are
+// waited for with explicit s_waitcnt before each barrier: the compiler treats
+// LDS DMA as aliasing every LDS read and would otherwise wait for all of them
+// (including the stage just issued) before each fragment read.  The loop
+// therefore contains no compiler-visible global memory access; scales and
+// biases of the block's columns are preloaded into LDS once.
+// ---------------------------------------------------------------------------
+namespace dma {
+
+constexpr int BK = 128;
+constexpr int kThreads = 512;
+constexpr int kStageHalves = BM * BK;       // one f16 X or W tile
+constexpr int kRawWords = BN * BK / 8;      // one raw q4 W tile (u32 words)
+constexpr size_t kFixedLds = (2 * (size_t)kStageHalves + 2 * (size_t)kStageHalves) * 2 + 2 * (size_t)kRawWords * 4;
+constexpr size_t kMaxLds = 160 * 1024;
+
+__device__ __forceinline__ int slot(int r, int c) { return r * 16 + (c ^ (r & 15)); }
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p)
+{
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
+}
+
+// 16 bytes per lane, global -> LDS; lane i lands at lds + 16 i (checked on gfx950)
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds)
+{
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(__builtin_amdgcn_readfirstlane(lds))
+                 : "memory", "m0");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt()
+{
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <int SBT>
+__global__ __launch_bounds__(kThreads) void qgemm_q4_dma_kernel(const uint32_t* __restrict__ W,
+                                                                const void* __restrict__ S,
+                                                                const void* __restrict__ Bz, int gshift,
+                                                                const _Float16* __restrict__ X, float* __restrict__ out,
+                                                                int M, int N, int K, int k_per_split)
+{
+    extern __shared__ __align__(16) unsigned char smem[];
+    _Float16* xs = reinterpret_cast<_Float16*>(smem);             // 2 stages of X
+    _Float16* ws = xs + 2 * kStageHalves;                           // 2 f16 W tiles
+    uint32_t* wraw = reinterpret_cast<uint32_t*>(ws + 2 * kStageHalves);  // 2 raw W tiles
+    uint32_t* sbl = wraw + 2 * kRawWords;                            // [BN][groups]: f16/bf16 (s | b << 16), f32 pairs
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave & 1, wn = wave >> 1;
+    const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+    const int kbeg = blockIdx.z * k_per_split;
+    const int kend = min(K, kbeg + k_per_split);
+    const int nsteps = (kend - kbeg) / BK;
+    float* o = out + (size_t)blockIdx.z * M * N;
+    if (nsteps <= 0) return;  // the launcher never makes an empty split
+    const int last = nsteps - 1;
+    const int kwords = K >> 3;
+    const int gpr = (K + (1 << gshift) - 1) >> gshift;
+    const int g0 = kbeg >> gshift;
+    const int ng = ((kend - 1) >> gshift) - g0 + 1;
+
+    // X DMA: wave issues 4 per stage, load j covers tile rows (wave*4+j)*4 .. +4
+    // (16 lanes per 256-byte row, lane -> chunk position, global chunk swizzled)
+    const _Float16* xsrc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int r = (wave * 4 + j) * 4 + (lane >> 4);
+        const int c = (lane & 15) ^ (r & 15);
+        xsrc[j] = X + (size_t)min(m0 + r, M - 1) * K + kbeg + 8 * c;
+    }
+    const uint32_t xs_lds = lds_addr(xs) + wave * 4 * 1024;
+    // raw W DMA and dequant: thread -> column tid/4, words 4(tid&3)..+4 (32 k) of a step
+    const int wcol = tid >> 2, wq4 = tid & 3;
+    const uint32_t* wsrc = W + (size_t)min(n0 + wcol, N - 1) * kwords + (kbeg >> 3) + 4 * wq4;
+    const uint32_t wr_lds = lds_addr(wraw) + wave * 1024;
+    // one group of loads per step: 4 X + 1 W per wave (tail steps re-read the last step)
+    auto issue = [&](int xstep, int wstep, int xst, int wst) {
+        const int xc = min(xstep, last), wc = min(wstep, last);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dma16(xsrc[j] + (size_t)xc * BK, xs_lds + xst * kStageHalves * 2 + j * 1024);
+        dma16(wsrc + (size_t)wc * (BK / 8), wr_lds + wst * kRawWords * 4);
+    };
+
+    dma16(wsrc, wr_lds);  // W(0)
+    issue(0, 1, 0, 1);    // X(0), W(1)
+    {
+        // scales/biases of this split's groups, loads batched before any use
+        constexpr int PB = 8;
+        const int total = BN * ng;
+        for (int base = tid; base < total; base += PB * kThreads) {
+            uint32_t sv[PB], bv[PB];
+#pragma unroll
+            for (int u = 0; u < PB; ++u) {
+                const int i = min(base + u * kThreads, total - 1);
+                const int col = i / ng, gi = i - col * ng;
+                const size_t idx = (size_t)min(n0 + col, N - 1) * gpr + g0 + gi;
+                sv[u] = load_raw<SBT>(S, idx);
+                bv[u] = load_raw<SBT>(Bz, idx);
+            }
+#pragma unroll
+            for (int u = 0; u < PB; ++u) {
+                const int i = base + u * kThreads;
+                if (i < total) {
+                    if constexpr (SBT == DT_F32) {
+                        sbl[2 * i] = sv[u];
+                        sbl[2 * i + 1] = bv[u];
+                    } else {
+                        sbl[i] = sv[u] | (bv[u] << 16);
+                    }
+                }
+            }
+        }
+    }
+    wait_vmcnt<0>();
+    __syncthreads();
+
+    // dequantize step `step` (raw tile wst) into f16 tile `buf`
+    auto dequant_step = [&](int step, int wst, int buf) {
+        const u4_t w = *reinterpret_cast<const u4_t*>(wraw + wst * kRawWords + tid * 4);
+        const int gi = ((kbeg + min(step, last) * BK + 32 * wq4) >> gshift) - g0;
+        float s, b;
+        if constexpr (SBT == DT_F32) {
+            s = __builtin_bit_cast(float, sbl[2 * (wcol * ng + gi)]);
+            b = __builtin_bit_cast(float, sbl[2 * (wcol * ng + gi) + 1]);
+        } else {
+            const uint32_t sb = sbl[wcol * ng + gi];
+            s = raw_to_f32<SBT>(sb & 0xFFFFu);
+            b = raw_to_f32<SBT>(sb >> 16);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<h8_t*>(ws + buf * kStageHalves + slot(wcol, 4 * wq4 + q) * 8) =
+                dequant_word_f16<SBT>(w[q], s, b);
+    };
+    dequant_step(0, 0, 0);
+
+    f16v_t acc[2];
+    acc[0] = f16v_t{};
+    acc[1] = f16v_t{};
+    const int r32 = lane & 31, h32 = lane >> 5;
+    for (int s = 0; s < nsteps; ++s) {
+        const int cur = s & 1, nxt = cur ^ 1;
+        // X(s), W(s+1) were the last group issued: nothing may stay in flight
+        wait_vmcnt<0>();
+        __syncthreads();  // stage s complete everywhere; stage s-1 and f16 tile (s+1)&1 free
+        issue(s + 1, s + 2, nxt, cur);        // X(s+1) -> stage nxt, W(s+2) -> raw tile of W(s)
+        dequant_step(s + 1, nxt, nxt);       // W(s+1): raw tile nxt -> f16 tile nxt
+        const _Float16* xa = xs + cur * kStageHalves;
+        const _Float16* wb = ws + cur * kStageHalves;
+#pragma unroll
+        for (int ks = 0; ks < BK / 16; ++ks) {
+            // 32x32x16: lane carries row/column lane%32, k chunk 2*ks + lane/32
+            h8_t a[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                a[i] = *reinterpret_cast<const h8_t*>(xa + slot(wm * 64 + i * 32 + r32, 2 * ks + h32) * 8);
+            const h8_t b = *reinterpret_cast<const h8_t*>(wb + slot(wn * 32 + r32, 2 * ks + h32) * 8);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b, acc[i], 0, 0, 0);
+        }
+    }
+    // drain the trailing (re-read) DMA before the workgroup's LDS is released
+    wait_vmcnt<0>();
+
+    // register r of a 32x32 tile: row (r/4)*8 + (lane/32)*4 + r%4, column lane%32;
+    // a store writes two full 128-byte row pieces
+    const int n = n0 + wn * 32 + r32;
+    if (n < N) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int m = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + h32 * 4 + (r & 3);
+                if (m < M) o[(size_t)m * N + n] = acc[i][r];
+            }
+    }
+}
+
+struct Plan {
+    int splits;
+    int k_per_split;
+    size_t lds;
+};
+
+// Split-K so the grid covers the 256 CUs (each split >= 4 steps), and enough
+// splits that a split's scales/biases fit the LDS left by the tiles.
+Plan plan(int M, int N, int K, int group, int sbt)
+{
+    Plan p{0, 0, 0};
+    if (K <= 0 || K % BK != 0 || group < 32) return p;
+    const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    const int steps = K / BK;
+    int splits = 1;
+    while (tiles * splits * 2 <= 256 && steps / (splits * 2) >= 4) splits *= 2;
+    const size_t sb_bytes = sbt == DT_F32 ? 8 : 4;
+    for (;;) {
+        const int sps = (steps + splits - 1) / splits;
+        const int kps = sps * BK;
+        const int ng = (kps + group - 1) / group + 1;  // + 1: a split may start mid-group
+        const size_t lds = kFixedLds + (size_t)BN * ng * sb_bytes;
+        if (lds <= kMaxLds) {
+            p.splits = (steps + sps - 1) / sps;  // no empty split
+            p.k_per_split = kps;
+            p.lds = lds;
+            return p;
+        }
+        if (sps == 1) return Plan{0, 0, 0};
+        ++splits;
+    }
+}
+
+}  // namespace dma
+
 }  // namespace
 
 // Choose the split-K factor so the grid covers the chip: 256 CUs.
@@ -253,10 +486,43 @@ int qgemm_splits(int M, int N, int K)
     return splits;
 }
 
-size_t qgemm_workspace_bytes(int M, int N, int K)
+size_t qgemm_workspace_bytes(int wt, int M, int N, int K, int group_size, int sbt)
 {
+    if (wt == 0) {
+        const dma::Plan p = dma::plan(M, N, K, group_size, sbt);
+        if (p.splits > 0) return p.splits > 1 ? (size_t)p.splits * M * N * sizeof(float) : 0;
+    }
     const int splits = qgemm_splits(M, N, K);
     return splits > 1 ? (size_t)splits * M * N * sizeof(float) : 0;
+}
+
+// Dynamic LDS above 64 KB needs the per-function limit raised once per device.
+template <typename Kern>
+static hipError_t allow_lds(Kern kern, size_t bytes)
+{
+    static std::atomic<uint64_t> done{0};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const uint64_t bit = 1ull << (dev & 63);
+    if (done.load(std::memory_order_acquire) & bit) return hipSuccess;
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)dma::kMaxLds);
+    if (e == hipSuccess) done.fetch_or(bit, std::memory_order_acq_rel);
+    (void)bytes;
+    return e;
+}
+
+template <int SBT>
+static hipError_t launch_q4_dma(const dma::Plan& p, const uint32_t* wq, const void* S, const void* B, int gshift,
+                                const _Float16* x, float* out, int M, int N, int K, hipStream_t st)
+{
+    auto kern = dma::qgemm_q4_dma_kernel<SBT>;
+    hipError_t e = allow_lds(kern, p.lds);
+    if (e != hipSuccess) return e;
+    const dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM, p.splits);
+    hipLaunchKernelGGL(kern, grid, dim3(dma::kThreads), p.lds, st, wq, S, B, gshift, x, out, M, N, K, p.k_per_split);
+    return hipGetLastError();
 }
 
 template <int WT>
@@ -295,6 +561,21 @@ hipError_t launch_qgemm_q4_affine_ws(const uint32_t* wq, const void* S, const vo
                                      const _Float16* x, float* y, int M, int N, int K, float* workspace,
                                      hipStream_t st)
 {
+    const dma::Plan p = dma::plan(M, N, K, group_size, sbt);
+    if (p.splits > 0 && (p.splits == 1 || workspace)) {
+        const int gshift = __builtin_ctz((unsigned)group_size);
+        float* out = p.splits > 1 ? workspace : y;
+        hipError_t e = sbt == DT_F16   ? launch_q4_dma<DT_F16>(p, wq, S, B, gshift, x, out, M, N, K, st)
+                       : sbt == DT_F32 ? launch_q4_dma<DT_F32>(p, wq, S, B, gshift, x, out, M, N, K, st)
+                                       : launch_q4_dma<DT_BF16>(p, wq, S, B, gshift, x, out, M, N, K, st);
+        if (e != hipSuccess || p.splits == 1) return e;
+        const size_t total = (size_t)M * N;
+        unsigned blocks = (unsigned)((total + 255) / 256);
+        if (blocks > 4096) blocks = 4096;
+        hipLaunchKernelGGL(splitk_reduce_kernel, dim3(blocks), dim3(256), 0, st, workspace, y, nullptr, p.splits, M,
+                           N);
+        return hipGetLastError();
+    }
     return launch_qgemm_common<0>(wq, S, B, sbt, group_size, 1, x, y, nullptr, M, N, K, workspace, st);
 }
 

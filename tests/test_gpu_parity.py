@@ -277,11 +277,17 @@ def test_qgemm_tiles_are_the_converter_f16_dequant(ops, sb):
     np.testing.assert_array_equal(y.T.view(np.uint32), ref16.view(np.uint32))
 
 
-def test_qgemm_ragged_m_n(ops):
-    m, k, n = 37, 192, 77
-    wq, s, b, x = make_q4(n, k, m, cfg=4, salt=5)
-    y = _run_q4(ops, wq, s, b, x, gemm=True)
-    w16 = oracle.f16_bits_to_f32(oracle.dequant_q4_affine_f16(wq, s, b, k))
+@pytest.mark.parametrize("m,k,n,group,sb", [
+    (37, 192, 77, 64, np.float16),      # K % 128 != 0: register-staged kernel
+    (37, 256, 77, 64, np.float16),      # direct-to-LDS kernel, ragged M and N
+    (300, 640, 1000, 128, "bf16"),
+    (130, 4864, 200, 64, np.float32),   # split-K through the workspace
+    (64, 256, 96, 32, np.float16),
+])
+def test_qgemm_ragged_m_n(ops, m, k, n, group, sb):
+    wq, s, b, x = make_q4(n, k, m, cfg=4, sb_dtype=sb, group=group, salt=5 + k)
+    y = _run_q4(ops, wq, s, b, x, group=group, gemm=True)
+    w16 = oracle.f16_bits_to_f32(oracle.dequant_q4_affine_f16(wq, s, b, k, gs=group))
     assert rel_err(y, oracle.gemm_xwT(x, w16)) <= TOL_F32
 
 
