@@ -28,6 +28,8 @@
 // Products of f16 values are exact in f32 and every sum is f32, so the only
 // difference from the reference is summation order (checked to 1e-3 relative
 // against the reference CPU order in tests/).
+#include <algorithm>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -89,22 +91,22 @@ __device__ __forceinline__ void load_x_words(const _Float16* __restrict__ x, int
     }
 }
 
-template <int LPR, int R, int SBT>
+template <int LPR, int R, int SBT, int U = kUnroll>
 __device__ __forceinline__ void load_pass_q4(const u4_t* __restrict__ wq, const void* __restrict__ S,
-                                             const void* __restrict__ B, int row0, int c0, int N, int CPR, int gpr,
-                                             int gshift, u4_t (&wv)[kUnroll][R], uint32_t (&sr)[kUnroll][R],
-                                             uint32_t (&br)[kUnroll][R])
+                                             const void* __restrict__ B, int row0, int rstride, int c0, int N, int CPR,
+                                             int gpr, int gshift, u4_t (&wv)[U][R], uint32_t (&sr)[U][R],
+                                             uint32_t (&br)[U][R])
 {
     // Addresses are clamped into the matrix instead of branching around the
     // loads: a lane whose chunk or row is out of range loads a valid element
     // and its result is never used (compute skips c >= CPR, rows >= N are not
     // stored).  Branch-free loads keep every conversion away from its load.
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
+    for (int u = 0; u < U; ++u) {
         const int c = min(c0 + u * LPR, CPR - 1);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
-            const int n = min(row0 + r, N - 1);
+            const int n = min(row0 + r * rstride, N - 1);
             wv[u][r] = __builtin_nontemporal_load(wq + (size_t)n * CPR + c);
             const size_t gi = (size_t)n * gpr + ((c << 5) >> gshift);
             sr[u][r] = load_raw<SBT>(S, gi);
@@ -113,14 +115,14 @@ __device__ __forceinline__ void load_pass_q4(const u4_t* __restrict__ wq, const 
     }
 }
 
-template <int LPR, int R, int MT, int SBT>
+template <int LPR, int R, int MT, int SBT, int U = kUnroll>
 __device__ __forceinline__ void compute_pass_q4(int c0, int CPR, const uint32_t* xq, const float2* cx,
-                                                const u4_t (&wv)[kUnroll][R], const uint32_t (&sr)[kUnroll][R],
-                                                const uint32_t (&br)[kUnroll][R], float (&acc)[R][MT])
+                                                const u4_t (&wv)[U][R], const uint32_t (&sr)[U][R],
+                                                const uint32_t (&br)[U][R], float (&acc)[R][MT])
 {
     const uint32_t m0f = 0x000F000Fu, m1f = 0x00F000F0u, magic = 0x64006400u;
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
+    for (int u = 0; u < U; ++u) {
         const int c = c0 + u * LPR;
         if (c < CPR) {
 #pragma unroll
@@ -185,7 +187,7 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_f16x_kernel(
 
     u4_t wa[kUnroll][R];
     uint32_t sa[kUnroll][R], ba[kUnroll][R];
-    load_pass_q4<LPR, R, SBT>(wq, S, B, row0, lane, N, CPR, gpr, gshift, wa, sa, ba);
+    load_pass_q4<LPR, R, SBT>(wq, S, B, row0, 1, lane, N, CPR, gpr, gshift, wa, sa, ba);
 
 #pragma unroll
     for (int j = 0; j < XW; ++j) {
@@ -217,11 +219,11 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_f16x_kernel(
         u4_t wb[kUnroll][R];
         uint32_t sb[kUnroll][R], bb[kUnroll][R];
         for (int c0 = lane; c0 < CPR + lane; c0 += 2 * P) {
-            if (c0 - lane + P < CPR) load_pass_q4<LPR, R, SBT>(wq, S, B, row0, c0 + P, N, CPR, gpr, gshift, wb, sb, bb);
+            if (c0 - lane + P < CPR) load_pass_q4<LPR, R, SBT>(wq, S, B, row0, 1, c0 + P, N, CPR, gpr, gshift, wb, sb, bb);
             compute_pass_q4<LPR, R, MT, SBT>(c0, CPR, xq, cx, wa, sa, ba, acc);
             if (c0 - lane + P >= CPR) break;
             if (c0 - lane + 2 * P < CPR)
-                load_pass_q4<LPR, R, SBT>(wq, S, B, row0, c0 + 2 * P, N, CPR, gpr, gshift, wa, sa, ba);
+                load_pass_q4<LPR, R, SBT>(wq, S, B, row0, 1, c0 + 2 * P, N, CPR, gpr, gshift, wa, sa, ba);
             compute_pass_q4<LPR, R, MT, SBT>(c0 + P, CPR, xq, cx, wb, sb, bb, acc);
         }
     }
@@ -241,6 +243,82 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_f16x_kernel(
                     if (m < M) y[(size_t)m * N + n] = acc[r][m];
             }
         }
+    }
+}
+
+// Persistent single-row (M = 1) variant for long outputs (lm_head): a block
+// stages x once, then walks tiles tile, tile+grid, ... of ROWS rows.  The next
+// tile's weights are loaded while the current one is computed (two register
+// sets, loop unrolled by two), and each team's sums go to LDS; the block
+// writes them out after its last tile, so the loop holds no global store and
+// the compiler's in-order load counting stays exact.  A wave's teams own rows
+// interleaved by team (row = base + r*TPW + team), so one load instruction
+// covers TPW consecutive rows.  Requires CPR <= U*LPR (one pass per row).
+template <int LPR, int R, int U, int SBT>
+__global__ __launch_bounds__(kBlock) void qgemv_q4_persist_kernel(
+    const u4_t* __restrict__ wq, const void* __restrict__ S, const void* __restrict__ B,
+    const _Float16* __restrict__ x, float* __restrict__ y, int N, int K, int gshift, int ntiles)
+{
+    extern __shared__ __align__(16) uint32_t lds[];
+    constexpr int TPW = 64 / LPR;
+    constexpr int ROWS = (kBlock / LPR) * R;
+    const int CPR = K >> 5;
+    uint32_t* xq = lds;
+    float2* cx = reinterpret_cast<float2*>(lds + (size_t)CPR * 16);
+    float* yl = reinterpret_cast<float*>(lds + (size_t)CPR * 16 + (size_t)CPR * 2);  // [tiles of this block][ROWS]
+    const int lane = threadIdx.x % LPR;
+    const int rbase = (int)(threadIdx.x >> 6) * TPW * R + (int)((threadIdx.x & 63) / LPR);
+    const int gpr = (K + (1 << gshift) - 1) >> gshift;
+    const int total = K >> 3;
+    const int grid = gridDim.x;
+
+    u4_t xr[4];
+    load_x_words<4>(x, 1, K, total, xr);
+    u4_t wa[U][R], wb[U][R];
+    uint32_t sa[U][R], ba[U][R], sb[U][R], bb[U][R];
+    int t = blockIdx.x;
+    load_pass_q4<LPR, R, SBT, U>(wq, S, B, t * ROWS + rbase, TPW, lane, N, CPR, gpr, gshift, wa, sa, ba);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int idx = (int)threadIdx.x + j * kBlock;
+        stage_word_q4(xr[j], idx, idx < total, xq, cx);
+    }
+    for (int base = 4 * kBlock; base < total; base += kBlock) {
+        const int idx = base + (int)threadIdx.x;
+        const u4_t raw = idx < total ? *reinterpret_cast<const u4_t*>(x + (size_t)idx * 8) : u4_t{0u, 0u, 0u, 0u};
+        stage_word_q4(raw, idx, idx < total, xq, cx);
+    }
+    __syncthreads();
+
+    // one tile: prefetch the next into (wn, sn, bn), compute (wc, sc, bc)
+    int it = 0;
+    auto tile_step = [&](u4_t(&wn)[U][R], uint32_t(&sn)[U][R], uint32_t(&bn)[U][R], const u4_t(&wc)[U][R],
+                         const uint32_t(&sc)[U][R], const uint32_t(&bc)[U][R]) {
+        const int tn = t + grid;
+        // past the last tile: re-read tile 0 (cache resident), never used
+        const int tl = tn < ntiles ? tn : 0;
+        load_pass_q4<LPR, R, SBT, U>(wq, S, B, tl * ROWS + rbase, TPW, lane, N, CPR, gpr, gshift, wn, sn, bn);
+        float acc[R][1];
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r][0] = 0.0f;
+        compute_pass_q4<LPR, R, 1, SBT, U>(lane, CPR, xq, cx, wc, sc, bc, acc);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float v = group_sum<LPR>(acc[r][0]);
+            if (lane == 0) yl[it * ROWS + rbase + r * TPW] = v;
+        }
+        ++it;
+        t = tn;
+        return t < ntiles;
+    };
+    for (;;) {
+        if (!tile_step(wb, sb, bb, wa, sa, ba)) break;
+        if (!tile_step(wa, sa, ba, wb, sb, bb)) break;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < it * ROWS; i += kBlock) {
+        const int n = (blockIdx.x + (i / ROWS) * grid) * ROWS + (i % ROWS);
+        if (n < N) y[n] = yl[i];
     }
 }
 
@@ -658,6 +736,21 @@ int qgemv_q4_lds_bytes(int M, int K)
     return MT * CPR * 16 * 4 + MT * CPR * 8;
 }
 
+// Persistent grid: 4 blocks per CU (measured best for the lm_head shape).
+static int persist_grid()
+{
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    int& c = cached[dev & 63];
+    if (c == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 256;
+        c = 4 * cus;
+    }
+    return c;
+}
+
 hipError_t launch_qgemv_q4_affine(const uint32_t* wq, const void* S, const void* B, int sbt, int group_size,
                                   const void* x, int xdt, float* y, int M, int N, int K, hipStream_t st,
                                   int force_generic)
@@ -665,6 +758,26 @@ hipError_t launch_qgemv_q4_affine(const uint32_t* wq, const void* S, const void*
     const int gshift = __builtin_ctz((unsigned)group_size);
     const bool fast = !force_generic && xdt == DT_F16 && M <= 4 && (K % 32) == 0 && group_size >= 32 &&
                       aligned16(wq) && aligned16(x) && qgemv_q4_lds_bytes(M, K) <= 64 * 1024;
+    if (fast && M == 1 && N >= 32768 && (K >> 5) <= 32) {
+        // long single-row outputs: persistent kernel, 32 lanes per row, 2 rows per team
+        constexpr int LPR = 32, R = 2, ROWS = (kBlock / LPR) * R;
+        const int ntiles = (N + ROWS - 1) / ROWS;
+        const int grid = std::min(ntiles, persist_grid());
+        const int tiles_per_block = (ntiles + grid - 1) / grid;
+        const size_t lds = (size_t)qgemv_q4_lds_bytes(1, K) + (size_t)tiles_per_block * ROWS * 4;
+        if (lds <= 64 * 1024) {
+            const u4_t* w4 = reinterpret_cast<const u4_t*>(wq);
+            const _Float16* xh = reinterpret_cast<const _Float16*>(x);
+#define CELLM_Q4_PERSIST(SBT_)                                                                                   \
+    hipLaunchKernelGGL((qgemv_q4_persist_kernel<LPR, R, 1, SBT_>), dim3(grid), dim3(kBlock), lds, st, w4, S, B, xh, y, \
+                       N, K, gshift, ntiles)
+            if (sbt == DT_F16) CELLM_Q4_PERSIST(DT_F16);
+            else if (sbt == DT_F32) CELLM_Q4_PERSIST(DT_F32);
+            else CELLM_Q4_PERSIST(DT_BF16);
+#undef CELLM_Q4_PERSIST
+            return hipGetLastError();
+        }
+    }
     if (fast) {
         const GemvShape sh = pick_shape(K >> 5, N, true);
         const _Float16* xh = reinterpret_cast<const _Float16*>(x);

@@ -114,6 +114,17 @@ def test_q4_gemv_qwen_lm_head(ops):
     assert int(np.argmax(y[0])) == int(np.argmax(ref[0]))
 
 
+@pytest.mark.parametrize("k,n,group,sb", [
+    (1024, 40000, 64, "bf16"),      # persistent single-row kernel, 32 chunks per row
+    (512, 33001, 128, np.float32),  # ragged last tile
+    (256, 32768, 32, np.float16),
+])
+def test_q4_gemv_long_output_persistent(ops, k, n, group, sb):
+    wq, s, b, x = make_q4(n, k, 1, sb_dtype=sb, group=group, salt=k + n)
+    y = _run_q4(ops, wq, s, b, x, group=group)
+    assert rel_err(y, oracle.qgemv_q4_affine(wq, s, b, x, k, gs=group)) <= TOL_F32
+
+
 @pytest.mark.parametrize("m", [1, 2, 3, 4])
 @pytest.mark.parametrize("sb", [np.float16, np.float32, "bf16"])
 def test_q4_gemv_batched_small_m(ops, m, sb):
