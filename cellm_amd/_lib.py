@@ -21,6 +21,15 @@ DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 
 _vp, _sz, _i32, _i64 = C.c_void_p, C.c_size_t, C.c_int32, C.c_int64
 
+OP_QGEMV_I8, OP_QGEMV_Q4_AFFINE = 0, 1
+
+
+class QgemvOp(C.Structure):
+    """cellm_hip_qgemv_op_t (include/cellm_hip.h)."""
+    _fields_ = [("kind", _i32), ("sb_dtype", _i32), ("x_dtype", _i32), ("group", _i32), ("w", _vp), ("scales", _vp),
+                ("biases", _vp), ("n_scales", _i64), ("x", _vp), ("bias", _vp), ("y", _vp), ("m", _i64), ("n", _i64),
+                ("k", _i64)]
+
 # name -> (restype, argtypes); the same set include/cellm_hip.h declares
 SIGNATURES = {
     "cellm_hip_last_error_message": (_sz, [C.c_char_p, _sz]),
@@ -36,6 +45,7 @@ SIGNATURES = {
     "cellm_hip_weight_cache_stats": (_i32, [_vp, C.POINTER(_sz), C.POINTER(_sz)]),
     "cellm_hip_qgemv_i8": (_i32, [_vp, _vp, _vp, _i32, _i64, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _vp]),
     "cellm_hip_qgemv_q4_affine": (_i32, [_vp, _vp, _vp, _vp, _i32, _i64, _vp, _i32, _vp, _i64, _i64, _i64, _vp]),
+    "cellm_hip_qgemv_batch": (_i32, [_vp, C.POINTER(QgemvOp), _i64, _vp]),
     "cellm_hip_qgemv_i4_sym": (_i32, [_vp, _vp, _vp, _i64, _i64, _vp, _i32, _vp, _i64, _i64, _i64, _vp]),
     "cellm_hip_qgemm_q4_affine": (_i32, [_vp, _vp, _vp, _vp, _i32, _i64, _vp, _vp, _i64, _i64, _i64, _vp]),
     "cellm_hip_qgemm_i8": (_i32, [_vp, _vp, _vp, _i32, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),

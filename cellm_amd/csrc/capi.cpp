@@ -445,6 +445,28 @@ int32_t cellm_hip_qgemv_q4_affine(cellm_hip_ctx_t* ctx, const uint32_t* wq, cons
                          false);
 }
 
+int32_t cellm_hip_qgemv_batch(cellm_hip_ctx_t* ctx, const cellm_hip_qgemv_op_t* ops, int64_t n_ops, void* stream)
+{
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    if (n_ops < 0 || (n_ops > 0 && !ops)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null or negative op list");
+    DeviceGuard g(ctx->device);
+    hipStream_t st = pick_stream(ctx, stream);
+    for (int64_t i = 0; i < n_ops; ++i) {
+        const cellm_hip_qgemv_op_t& o = ops[i];
+        int32_t rc;
+        if (o.kind == CELLM_HIP_OP_QGEMV_I8)
+            rc = qgemv_i8_impl(ctx, static_cast<const int8_t*>(o.w), o.scales, o.sb_dtype, o.n_scales, o.x, o.x_dtype,
+                               o.bias, o.y, o.m, o.n, o.k, st, false);
+        else if (o.kind == CELLM_HIP_OP_QGEMV_Q4_AFFINE)
+            rc = qgemv_q4_impl(ctx, static_cast<const uint32_t*>(o.w), o.scales, o.biases, o.sb_dtype, o.group, o.x,
+                               o.x_dtype, o.y, o.m, o.n, o.k, st, false);
+        else
+            rc = set_error(CELLM_HIP_ERR_INVALID_ARG, "op %lld: unknown kind %d", (long long)i, (int)o.kind);
+        if (rc) return rc;
+    }
+    return CELLM_HIP_OK;
+}
+
 int32_t cellm_hip_qgemv_i4_sym(cellm_hip_ctx_t* ctx, const uint8_t* w, const uint16_t* scales_f16, int64_t n_scales,
                                int64_t gs, const void* x, int32_t x_dtype, float* y, int64_t m, int64_t n, int64_t k,
                                void* stream)

@@ -185,6 +185,30 @@ class HipOps:
                                                   _torch_dtype_code(scales), group, _dev_ptr(x), _torch_dtype_code(x),
                                                   _dev_ptr(y), m, n, k, _stream_ptr(stream)))
 
+    @staticmethod
+    def qgemv_op_i8(w, scales, x, y, bias=None) -> "_lib.QgemvOp":
+        """One cellm_hip_qgemv_op_t of kind int8 (arguments as encode_qgemv_i8)."""
+        n, k = w.shape
+        return _lib.QgemvOp(kind=_lib.OP_QGEMV_I8, sb_dtype=_torch_dtype_code(scales), x_dtype=_torch_dtype_code(x),
+                            group=0, w=_dev_ptr(w), scales=_dev_ptr(scales), biases=None, n_scales=scales.numel(),
+                            x=_dev_ptr(x), bias=_dev_ptr(bias), y=_dev_ptr(y), m=x.numel() // k, n=n, k=k)
+
+    @staticmethod
+    def qgemv_op_q4_affine(wq, scales, biases, x, y, group: int = 64) -> "_lib.QgemvOp":
+        """One cellm_hip_qgemv_op_t of kind q4 affine (arguments as encode_qgemv_q4_affine)."""
+        n, k = wq.shape[0], wq.shape[1] * 8
+        return _lib.QgemvOp(kind=_lib.OP_QGEMV_Q4_AFFINE, sb_dtype=_torch_dtype_code(scales),
+                            x_dtype=_torch_dtype_code(x), group=group, w=_dev_ptr(wq), scales=_dev_ptr(scales),
+                            biases=_dev_ptr(biases), n_scales=0, x=_dev_ptr(x), bias=None, y=_dev_ptr(y),
+                            m=x.numel() // k, n=n, k=k)
+
+    def encode_qgemv_batch(self, ops, stream=None) -> None:
+        """Enqueue a list of qgemv ops (qgemv_op_*) in order with one call; a
+        ctypes array built once may be passed again to re-enqueue it."""
+        if not isinstance(ops, C.Array):
+            ops = (_lib.QgemvOp * len(ops))(*ops)
+        check(self._lib.cellm_hip_qgemv_batch(self._h, ops, len(ops), _stream_ptr(stream)))
+
     def encode_qgemv_i4_sym(self, w_u8, scales_f16, gs: int, x, y, k: int, stream=None) -> None:
         n = w_u8.shape[0]
         m = x.numel() // k

@@ -121,6 +121,38 @@ int32_t cellm_hip_qgemv_q4_affine(cellm_hip_ctx_t* ctx, const uint32_t* wq, cons
                                   int32_t sb_dtype, int64_t group, const void* x, int32_t x_dtype, float* y,
                                   int64_t m, int64_t n, int64_t k, void* stream);
 
+/* One projection of a batch (cellm_hip_qgemv_batch).  kind
+ * CELLM_HIP_OP_QGEMV_I8 takes the arguments of cellm_hip_qgemv_i8 (w int8,
+ * scales, sb_dtype = scale dtype, n_scales, bias; biases and group unused);
+ * kind CELLM_HIP_OP_QGEMV_Q4_AFFINE those of cellm_hip_qgemv_q4_affine (w =
+ * u32 words, scales, biases, sb_dtype, group; n_scales and bias unused). */
+#define CELLM_HIP_OP_QGEMV_I8 0
+#define CELLM_HIP_OP_QGEMV_Q4_AFFINE 1
+typedef struct {
+    int32_t kind;
+    int32_t sb_dtype;
+    int32_t x_dtype;
+    int32_t group;
+    const void* w;
+    const void* scales;
+    const void* biases;
+    int64_t n_scales;
+    const void* x;
+    const float* bias;
+    float* y;
+    int64_t m;
+    int64_t n;
+    int64_t k;
+} cellm_hip_qgemv_op_t;
+
+/* Enqueues ops[0..n_ops) in order on one stream with one call, as the
+ * reference's fused decode graphs encode consecutive projections on one Metal
+ * command encoder (crates/cellm-model/src/llama_graph.rs:245-336: encode_qkv_i8,
+ * encode_mv_i8 for o / gate / up / down).  Each op is checked and launched as
+ * its single-op entry point does; the first failing op's status is returned
+ * and the ops before it stay enqueued. */
+int32_t cellm_hip_qgemv_batch(cellm_hip_ctx_t* ctx, const cellm_hip_qgemv_op_t* ops, int64_t n_ops, void* stream);
+
 /* Symmetric i4 GEMV: y[i, r] = sum_j ((nib - 8) * scale[r*spr + j/gs]) * x[i, j],
  * spr = n_scales / n.  Replaces cpu_kernels::matmul_i4_f32 (cpu_kernels.rs:219-243)
  * and MetalOps::encode_mv_i4 (metal.rs:1167-1176). */

@@ -365,3 +365,68 @@ def test_bad_k_is_rejected(ops):
     assert rc == -1 and "multiple of 8" in last_error()
     with pytest.raises(CellmHipError):
         ops.weight_lookup("no.such.key")
+
+
+# ------------------------------------------------------------- HIP graphs ----
+
+def test_graph_replays_match_eager(ops):
+    """Each path captured in a HIP graph, replayed several times with eager
+    work in between; every replay equals the eager result bit for bit."""
+    import torch
+
+    cases = []
+    a = [_t(v) if i != 1 and i != 2 else _sb_tensor(v) for i, v in enumerate(make_q4(40000, 896, 1, salt=11))]
+    cases.append(lambda y, st: ops.encode_qgemv_q4_affine(a[0], a[1], a[2], a[3], y, stream=st))  # persistent GEMV
+    c = [_t(v) for v in make_i8(3000, 1152, 16, cfg=3, x_dtype=np.float16, salt=12)]
+    cases.append(lambda y, st: ops.encode_qgemv_i8(c[0], c[1], c[2], y, stream=st))  # batched MFMA decode
+    e = [_t(v) if i != 1 and i != 2 else _sb_tensor(v) for i, v in enumerate(make_q4(896, 4864, 512, cfg=4, salt=13))]
+    cases.append(lambda y, st: ops.encode_qgemm_q4_affine(e[0], e[1], e[2], e[3], y, stream=st))  # split-K qGEMM
+    shapes = [(1, 40000), (16, 3000), (512, 896)]
+    cap = torch.cuda.Stream()
+    for fn, (m, n) in zip(cases, shapes):
+        ref = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        fn(ref, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        y = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+        with torch.cuda.stream(cap):
+            fn(y, cap.cuda_stream)  # warm-up on the capture stream (per-stream scratch)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=cap):
+            fn(y, cap.cuda_stream)
+        for rep in range(3):
+            y.fill_(float("nan"))
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(y, ref), (m, n, rep)
+            _ = (ref * 2).sum().item()  # eager work between replays
+
+
+def test_qgemv_batch_matches_single_calls(ops):
+    """cellm_hip_qgemv_batch enqueues each op as its single-op entry point does."""
+    import torch
+
+    from cellm_amd._lib import CellmHipError, QgemvOp
+
+    q = [_t(v) if i not in (1, 2) else _sb_tensor(v) for i, v in enumerate(make_q4(1000, 1152, 1, cfg=3, salt=21))]
+    e = [_t(v) for v in make_i8(700, 576, 4, x_dtype=np.float16, salt=22)]
+    g = [_t(v) if i not in (1, 2) else _sb_tensor(v) for i, v in enumerate(make_q4(300, 896, 16, cfg=3, salt=23))]
+    outs = [torch.empty(shape, dtype=torch.float32, device="cuda") for shape in ((1, 1000), (4, 700), (16, 300))]
+    refs = [torch.empty_like(o) for o in outs]
+    ops.encode_qgemv_q4_affine(q[0], q[1], q[2], q[3], refs[0])
+    ops.encode_qgemv_i8(e[0], e[1], e[2], refs[1])
+    ops.encode_qgemv_q4_affine(g[0], g[1], g[2], g[3], refs[2])
+    ops.encode_qgemv_batch([ops.qgemv_op_q4_affine(q[0], q[1], q[2], q[3], outs[0]),
+                            ops.qgemv_op_i8(e[0], e[1], e[2], outs[1]),
+                            ops.qgemv_op_q4_affine(g[0], g[1], g[2], g[3], outs[2])])
+    torch.cuda.synchronize()
+    for o, r in zip(outs, refs):
+        assert torch.equal(o, r)
+    # an unknown op kind fails with its own status after the ops before it
+    outs[0].zero_()
+    bad = QgemvOp(kind=9)
+    with pytest.raises(CellmHipError, match="unknown kind"):
+        ops.encode_qgemv_batch([ops.qgemv_op_q4_affine(q[0], q[1], q[2], q[3], outs[0]), bad])
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], refs[0])
