@@ -53,7 +53,34 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="skip the extra configs")
+    ap.add_argument("--pmc-sample", action="store_true",
+                    help="run only a 256 MiB device copy (counter calibration) and 20 lm_head GEMVs, for "
+                         "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes")
     return ap.parse_args()
+
+
+def pmc_sample(torch, ops, stream, gen):
+    """Workload of the traffic measurement: the plain copy whose counters
+    calibrate FETCH_SIZE / WRITE_SIZE against known bytes, then the dominant
+    kernel on rotating weight copies."""
+    nbytes = 256 * 2**20
+    src = torch.randn(nbytes // 4, device="cuda", generator=gen)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    k, n = 896, 151936
+    copies = 8
+    ws = [Q4Weights(torch, n, k, gen) for _ in range(copies)]
+    x = torch.randn((1, k), device="cuda", generator=gen).to(torch.float16)
+    y = torch.empty((1, n), dtype=torch.float32, device="cuda")
+    arr = op_array([ops.qgemv_op_q4_affine(ws[i % copies].wq, ws[i % copies].s, ws[i % copies].b, x, y)
+                    for i in range(20)])
+    ops.encode_qgemv_batch(arr, stream=stream.cuda_stream)
+    torch.cuda.synchronize()
+    print(json.dumps({"pmc_sample": {"copy_bytes_read": nbytes, "copy_bytes_written": nbytes, "copy_launches": 3,
+                                     "gemv": "q4 affine 896->151936, M=1", "gemv_launches": 20,
+                                     "gemv_algorithmic_bytes": q4_bytes(1, n, k)}}))
 
 
 class Q4Weights:
@@ -116,6 +143,10 @@ def main():
     sptr = stream.cuda_stream
     gen = torch.Generator(device="cuda")
     gen.manual_seed(0xCE11)
+    if args.pmc_sample:
+        pmc_sample(torch, ops, stream, gen)
+        ops.close()
+        return
 
     # ---- the step -------------------------------------------------
     step_bytes = sum(q4_bytes(1, n, k) for _, k, n in QWEN_SHAPES)
@@ -166,7 +197,7 @@ def main():
             traffic = None
     roofline = {"bound": "hbm", "achieved": dom["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(dom["GB/s"] / HBM_PEAK_GBS, 4), "traffic": traffic,
-                "kernel": "qgemv_q4_f16x_kernel (896->151936 lm_head, M=1)",
+                "kernel": "qgemv_q4_persist_kernel (896->151936 lm_head, M=1)",
                 "algorithmic_bytes": q4_bytes(1, 151936, 896)}
     del sets
     torch.cuda.empty_cache()
@@ -207,8 +238,17 @@ def main():
 
 
 def extra_configs(torch, ops, stream, gen):
-    """configs[0], [2], [3]: int8 GEMV, Gemma batched decode, M=512 prefill qGEMM."""
+    """configs[0], [2], [3]: int8 GEMV, Gemma batched decode, M=512 prefill qGEMM;
+    plus a measured device-to-device copy as the box's practical HBM figure."""
     res = {}
+
+    # plain 512 MiB device copy: read + write bytes over time
+    nbytes = 512 * 2**20
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    ms = time_calls(torch, lambda i: dst.copy_(src), 20, stream)
+    res["hbm_copy_512MiB"] = {"us": round(ms * 1e3, 1), "GB/s_read_plus_write": round(2 * nbytes / (ms * 1e-3) / 1e9, 1)}
+    del src, dst
 
     # configs[0]: SmolLM2-135M int8, fp32 scale, fp32 x, K=576
     for n in (576, 1536):

@@ -147,6 +147,11 @@ int32_t get_workspace(cellm_hip_ctx* ctx, hipStream_t st, size_t need, float** o
     return CELLM_HIP_OK;
 }
 
+// Output rows from which the MFMA batched-decode kernel beats the VALU GEMV at
+// 2..4 activation rows (measured on MI355X: 1152->13824 q4 at m=4 7.6 vs 10.3 us;
+// 960->2560 int8 at m=4 7.2 vs 4.6 us).
+constexpr int64_t kMfmaMinRows = 8192;
+
 int32_t qgemv_i8_impl(cellm_hip_ctx* ctx, const int8_t* w, const void* scales, int32_t sdt, int64_t n_scales,
                       const void* x, int32_t xdt, const float* bias, float* y, int64_t m, int64_t n, int64_t k,
                       hipStream_t st, bool force_gemm)
@@ -159,8 +164,10 @@ int32_t qgemv_i8_impl(cellm_hip_ctx* ctx, const int8_t* w, const void* scales, i
     if (n_scales < 1) return set_error(CELLM_HIP_ERR_INVALID_ARG, "n_scales must be >= 1");
     const int per_channel = n_scales >= n ? 1 : 0;
     const bool gemm_ok = xdt == DT_F16 && k > 0 && (k % 64) == 0 && aligned16(w) && aligned16(x);
-    // 2..64 activation rows: weights streamed once into MFMA operands (exact for int8)
-    if (!force_gemm && gemm_ok && qgemv_mfma_supported(1, (int)m, (int)k, 0)) {
+    // 2..64 activation rows: weights streamed once into MFMA operands (exact for
+    // int8).  At m <= 4 the VALU GEMV wins until there are rows enough to fill
+    // the chip with MFMA tiles.
+    if (!force_gemm && gemm_ok && (m > 4 || n >= kMfmaMinRows) && qgemv_mfma_supported(1, (int)m, (int)k, 0)) {
         HIP_TRY(launch_qgemv_mfma_i8(w, scales, sdt, per_channel, reinterpret_cast<const _Float16*>(x), bias, y,
                                      (int)m, (int)n, (int)k, st),
                 "qgemv_mfma_i8 launch");
@@ -194,9 +201,10 @@ int32_t qgemv_q4_impl(cellm_hip_ctx* ctx, const uint32_t* wq, const void* scales
     if (k > 0 && (!wq || !scales || !biases || !x)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null input pointer");
     if (!y) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null output pointer");
     const bool gemm_ok = xdt == DT_F16 && k > 0 && (k % 64) == 0 && group >= 32 && aligned16(wq) && aligned16(x);
-    // 5..64 activation rows: f16 MFMA tiles dequantized in registers (M <= 4
-    // keeps the f32-accumulating VALU GEMV)
-    if (!force_gemm && m > 4 && gemm_ok && qgemv_mfma_supported(0, (int)m, (int)k, (int)group)) {
+    // 2..64 activation rows: f16 MFMA tiles dequantized in registers; at m <= 4
+    // only for long outputs (else the f32-accumulating VALU GEMV is faster)
+    if (!force_gemm && (m > 4 || n >= kMfmaMinRows) && gemm_ok &&
+        qgemv_mfma_supported(0, (int)m, (int)k, (int)group)) {
         HIP_TRY(launch_qgemv_mfma_q4(wq, scales, biases, sbt, (int)group, reinterpret_cast<const _Float16*>(x), y,
                                      (int)m, (int)n, (int)k, st),
                 "qgemv_mfma_q4 launch");

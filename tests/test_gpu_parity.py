@@ -236,18 +236,20 @@ def test_q4_batched_gemma_mlp(ops, m):
 
 @pytest.mark.parametrize("m", [2, 3, 7, 33])
 def test_i8_batched_mfma_small_m_and_k_chunks(ops, m):
-    """2..64 rows take the MFMA batched path; K=6912 spans several LDS chunks,
-    K=960 and 576 end on an odd 64-column block (576 at m=33: the odd block
-    opens a fresh X chunk)."""
-    for k, n in ((1152, 1000), (6912, 300), (960, 333), (576, 700)):
+    """5..64 rows (and 2..4 rows with >= 8192 outputs) take the MFMA batched
+    path; K=6912 spans several LDS chunks, K=960 and 576 end on an odd
+    64-column block (576 at m=33: the odd block opens a fresh X chunk)."""
+    for k, n in ((1152, 1000), (6912, 300), (960, 333), (576, 700), (1152, 8200)):
         w, s, x = make_i8(n, k, m, cfg=3, x_dtype=np.float16, salt=m + k)
         y = _run_i8(ops, w, s, x)
         assert rel_err(y, oracle.qgemv_i8(w, s, x)) <= TOL_F32, (m, k)
 
 
-@pytest.mark.parametrize("m", [5, 17, 64])
-def test_q4_batched_mfma_k_chunks(ops, m):
-    k, n = 6912, 1152  # Gemma down projection: several X chunks in LDS
+@pytest.mark.parametrize("m,k,n", [(5, 6912, 1152), (17, 6912, 1152), (64, 6912, 1152), (2, 1152, 8200),
+                                   (4, 1152, 8200)])
+def test_q4_batched_mfma_k_chunks(ops, m, k, n):
+    """Gemma down projection (several X chunks in LDS) at 5..64 rows; 2..4
+    rows take the MFMA path only for >= 8192 outputs."""
     wq, s, b, x = make_q4(n, k, m, cfg=3, salt=m)
     y = _run_q4(ops, wq, s, b, x)
     assert rel_err(y, oracle.qgemv_q4_affine(wq, s, b, x, k)) <= TOL_F16_TILE
