@@ -67,6 +67,7 @@ struct cellm_hip_ctx {
     size_t weight_bytes = 0;
     DeviceBuffer x_buf, y_buf;
     std::unordered_map<hipStream_t, DeviceBuffer> workspaces;  // split-K partials, one per stream
+    std::unordered_map<hipStream_t, DeviceBuffer> aux;         // unfused gate/up: the up rows, one per stream
 };
 
 namespace {
@@ -131,12 +132,13 @@ int32_t check_group(int64_t group)
 }
 
 // Workspace for split-K on `st`, sized for this call; nullptr if not needed.
-int32_t get_workspace(cellm_hip_ctx* ctx, hipStream_t st, size_t need, float** out)
+int32_t get_stream_buffer(cellm_hip_ctx* ctx, std::unordered_map<hipStream_t, DeviceBuffer>& map, hipStream_t st,
+                          size_t need, float** out)
 {
     *out = nullptr;
     if (need == 0) return CELLM_HIP_OK;
     std::lock_guard<std::recursive_mutex> lk(ctx->mu);
-    DeviceBuffer& b = ctx->workspaces[st];
+    DeviceBuffer& b = map[st];
     if (b.bytes < need) {
         // The old buffer may still be read by queued work on this stream.
         HIP_TRY(hipStreamSynchronize(st), "hipStreamSynchronize(workspace grow)");
@@ -151,6 +153,11 @@ int32_t get_workspace(cellm_hip_ctx* ctx, hipStream_t st, size_t need, float** o
 // 2..4 activation rows (measured on MI355X: 1152->13824 q4 at m=4 7.6 vs 10.3 us;
 // 960->2560 int8 at m=4 7.2 vs 4.6 us).
 constexpr int64_t kMfmaMinRows = 8192;
+
+int32_t get_workspace(cellm_hip_ctx* ctx, hipStream_t st, size_t need, float** out)
+{
+    return get_stream_buffer(ctx, ctx->workspaces, st, need, out);
+}
 
 int32_t qgemv_i8_impl(cellm_hip_ctx* ctx, const int8_t* w, const void* scales, int32_t sdt, int64_t n_scales,
                       const void* x, int32_t xdt, const float* bias, float* y, int64_t m, int64_t n, int64_t k,
@@ -223,6 +230,74 @@ int32_t qgemv_q4_impl(cellm_hip_ctx* ctx, const uint32_t* wq, const void* scales
         return set_error(CELLM_HIP_ERR_UNSUPPORTED, "qgemm_q4_affine needs f16 x, k %% 64 == 0, group >= 32, alignment");
     HIP_TRY(launch_qgemv_q4_affine(wq, scales, biases, sbt, (int)group, x, xdt, y, (int)m, (int)n, (int)k, st, k == 0),
             "qgemv_q4_affine launch");
+    return CELLM_HIP_OK;
+}
+
+// Fused projections (one launch for M <= 4); other shapes run the single-op
+// paths, plus the elementwise SiLU * up for gate/up.
+int32_t qkv_i8_impl(cellm_hip_ctx* ctx, const int8_t* const w[3], const void* const s[3], const int64_t n_s[3],
+                    const float* const b[3], int32_t sdt, const void* x, int32_t xdt, float* const y[3], int64_t m,
+                    const int64_t rows[3], int64_t k, hipStream_t st)
+{
+    for (int i = 0; i < 3; ++i)
+        if (int32_t rc = check_dims(m, rows[i], k)) return rc;
+    if (!valid_dtype(sdt) || !valid_dtype(xdt)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "bad dtype");
+    if (m == 0 || rows[0] + rows[1] + rows[2] == 0) return CELLM_HIP_OK;
+    for (int i = 0; i < 3; ++i) {
+        if (rows[i] == 0) continue;
+        if ((!w[i] && k > 0) || !s[i] || !y[i] || (!x && k > 0))
+            return set_error(CELLM_HIP_ERR_INVALID_ARG, "null pointer in projection %d", i);
+        if (n_s[i] < 1) return set_error(CELLM_HIP_ERR_INVALID_ARG, "n_scales must be >= 1 (projection %d)", i);
+    }
+    I8FusedSeg segs[3];
+    for (int i = 0; i < 3; ++i)
+        segs[i] = I8FusedSeg{w[i], s[i], b[i], y[i], (int)rows[i], n_s[i] >= rows[i] ? 1 : 0};
+    if (k > 0 && qgemv_i8_fused_supported(xdt, (int)m, (int)k, x, segs, 3)) {
+        HIP_TRY(launch_qgemv_i8_fused(segs, 3, false, sdt, x, xdt, (int)m, (int)k, st), "qgemv_i8_qkv launch");
+        return CELLM_HIP_OK;
+    }
+    for (int i = 0; i < 3; ++i)
+        if (rows[i] > 0)
+            if (int32_t rc = qgemv_i8_impl(ctx, w[i], s[i], sdt, n_s[i], x, xdt, b[i], y[i], m, rows[i], k, st, false))
+                return rc;
+    return CELLM_HIP_OK;
+}
+
+int32_t gate_up_i8_impl(cellm_hip_ctx* ctx, const int8_t* wg, const void* sg, int64_t n_sg, const float* bg,
+                        const int8_t* wu, const void* su, int64_t n_su, const float* bu, int32_t sdt, const void* x,
+                        int32_t xdt, float* h, int64_t m, int64_t n, int64_t k, hipStream_t st)
+{
+    if (int32_t rc = check_dims(m, n, k)) return rc;
+    if (!valid_dtype(sdt) || !valid_dtype(xdt)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "bad dtype");
+    if (m == 0 || n == 0) return CELLM_HIP_OK;
+    if ((k > 0 && (!wg || !wu || !x)) || !sg || !su || !h) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null pointer");
+    if (n_sg < 1 || n_su < 1) return set_error(CELLM_HIP_ERR_INVALID_ARG, "n_scales must be >= 1");
+    I8FusedSeg segs[2] = {I8FusedSeg{wg, sg, bg, h, (int)n, n_sg >= n ? 1 : 0},
+                          I8FusedSeg{wu, su, bu, nullptr, (int)n, n_su >= n ? 1 : 0}};
+    if (k > 0 && qgemv_i8_fused_supported(xdt, (int)m, (int)k, x, segs, 2)) {
+        HIP_TRY(launch_qgemv_i8_fused(segs, 2, true, sdt, x, xdt, (int)m, (int)k, st), "qgemv_i8_gate_up_silu launch");
+        return CELLM_HIP_OK;
+    }
+    float* up = nullptr;
+    if (int32_t rc = get_stream_buffer(ctx, ctx->aux, st, (size_t)m * n * sizeof(float), &up)) return rc;
+    if (int32_t rc = qgemv_i8_impl(ctx, wg, sg, sdt, n_sg, x, xdt, bg, h, m, n, k, st, false)) return rc;
+    if (int32_t rc = qgemv_i8_impl(ctx, wu, su, sdt, n_su, x, xdt, bu, up, m, n, k, st, false)) return rc;
+    HIP_TRY(launch_silu_mul(h, up, (size_t)m * n, st), "silu_mul launch");
+    return CELLM_HIP_OK;
+}
+
+int32_t gate_up_q4_impl(cellm_hip_ctx* ctx, const uint32_t* wg, const void* sg, const void* bg, const uint32_t* wu,
+                        const void* su, const void* bu, int32_t sbt, int64_t group, const void* x, int32_t xdt,
+                        float* h, int64_t m, int64_t n, int64_t k, hipStream_t st)
+{
+    if (int32_t rc = check_dims(m, n, k)) return rc;
+    if (m == 0 || n == 0) return CELLM_HIP_OK;
+    if (!h) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null output pointer");
+    float* up = nullptr;
+    if (int32_t rc = get_stream_buffer(ctx, ctx->aux, st, (size_t)m * n * sizeof(float), &up)) return rc;
+    if (int32_t rc = qgemv_q4_impl(ctx, wg, sg, bg, sbt, group, x, xdt, h, m, n, k, st, false)) return rc;
+    if (int32_t rc = qgemv_q4_impl(ctx, wu, su, bu, sbt, group, x, xdt, up, m, n, k, st, false)) return rc;
+    HIP_TRY(launch_silu_mul(h, up, (size_t)m * n, st), "silu_mul launch");
     return CELLM_HIP_OK;
 }
 
@@ -358,10 +433,11 @@ void cellm_hip_destroy(cellm_hip_ctx_t* ctx)
     if (!ctx) return;
     DeviceGuard g(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
-    for (auto& kv : ctx->workspaces) {
-        (void)hipStreamSynchronize(kv.first);
-        if (kv.second.ptr) (void)hipFree(kv.second.ptr);
-    }
+    for (auto* map : {&ctx->workspaces, &ctx->aux})
+        for (auto& kv : *map) {
+            (void)hipStreamSynchronize(kv.first);
+            if (kv.second.ptr) (void)hipFree(kv.second.ptr);
+        }
     for (auto& kv : ctx->weights)
         if (kv.second.ptr) (void)hipFree(kv.second.ptr);
     if (ctx->x_buf.ptr) (void)hipFree(ctx->x_buf.ptr);
@@ -473,6 +549,45 @@ int32_t cellm_hip_qgemv_batch(cellm_hip_ctx_t* ctx, const cellm_hip_qgemv_op_t* 
         if (rc) return rc;
     }
     return CELLM_HIP_OK;
+}
+
+int32_t cellm_hip_qgemv_i8_qkv(cellm_hip_ctx_t* ctx, const int8_t* wq, const void* sq, int64_t n_sq, const float* bq,
+                               const int8_t* wk, const void* sk, int64_t n_sk, const float* bk, const int8_t* wv,
+                               const void* sv, int64_t n_sv, const float* bv, int32_t scale_dtype, const void* x,
+                               int32_t x_dtype, float* q, float* k_out, float* v, int64_t m, int64_t rows_q,
+                               int64_t rows_kv, int64_t cols, void* stream)
+{
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    DeviceGuard g(ctx->device);
+    const int8_t* w[3] = {wq, wk, wv};
+    const void* s[3] = {sq, sk, sv};
+    const int64_t n_s[3] = {n_sq, n_sk, n_sv};
+    const float* b[3] = {bq, bk, bv};
+    float* y[3] = {q, k_out, v};
+    const int64_t rows[3] = {rows_q, rows_kv, rows_kv};
+    return qkv_i8_impl(ctx, w, s, n_s, b, scale_dtype, x, x_dtype, y, m, rows, cols, pick_stream(ctx, stream));
+}
+
+int32_t cellm_hip_qgemv_i8_gate_up_silu(cellm_hip_ctx_t* ctx, const int8_t* wg, const void* sg, int64_t n_sg,
+                                        const float* bg, const int8_t* wu, const void* su, int64_t n_su,
+                                        const float* bu, int32_t scale_dtype, const void* x, int32_t x_dtype, float* h,
+                                        int64_t m, int64_t n, int64_t k, void* stream)
+{
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    DeviceGuard g(ctx->device);
+    return gate_up_i8_impl(ctx, wg, sg, n_sg, bg, wu, su, n_su, bu, scale_dtype, x, x_dtype, h, m, n, k,
+                           pick_stream(ctx, stream));
+}
+
+int32_t cellm_hip_qgemv_q4_affine_gate_up_silu(cellm_hip_ctx_t* ctx, const uint32_t* wg, const void* sg,
+                                               const void* bg, const uint32_t* wu, const void* su, const void* bu,
+                                               int32_t sb_dtype, int64_t group, const void* x, int32_t x_dtype,
+                                               float* h, int64_t m, int64_t n, int64_t k, void* stream)
+{
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    DeviceGuard g(ctx->device);
+    return gate_up_q4_impl(ctx, wg, sg, bg, wu, su, bu, sb_dtype, group, x, x_dtype, h, m, n, k,
+                           pick_stream(ctx, stream));
 }
 
 int32_t cellm_hip_qgemv_i4_sym(cellm_hip_ctx_t* ctx, const uint8_t* w, const uint16_t* scales_f16, int64_t n_scales,

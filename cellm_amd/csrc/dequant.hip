@@ -99,6 +99,17 @@ __global__ void add_f32_kernel(const float* a, const float* b, float* out, int n
     if (i < n) out[i] = a[i] + b[i];
 }
 
+// g[i] = silu(g[i]) * u[i], silu(g) = g / (1 + exp(-g)) as silu_mul_f32_inplace
+// (crates/cellm-kernels/src/metal.rs:235-245) and llama.rs:477-484
+__global__ void silu_mul_kernel(float* __restrict__ g, const float* __restrict__ u, size_t n)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
+        const float x = g[i];
+        const float sig = 1.0f / (1.0f + expf(-x));
+        g[i] = (x * sig) * u[i];
+    }
+}
+
 }  // namespace
 
 hipError_t launch_dequant_q4_affine(const uint32_t* wq, const void* S, const void* B, int sbt, int group_size,
@@ -130,6 +141,15 @@ hipError_t launch_qgemv_i4_sym(const uint8_t* w, const uint16_t* S, int spr, int
         hipLaunchKernelGGL((qgemv_i4_sym_kernel<DT_F16>), grid, dim3(kBlock), 0, st, w, S, spr, gs, x, y, M, N, K);
     else
         hipLaunchKernelGGL((qgemv_i4_sym_kernel<DT_BF16>), grid, dim3(kBlock), 0, st, w, S, spr, gs, x, y, M, N, K);
+    return hipGetLastError();
+}
+
+hipError_t launch_silu_mul(float* g, const float* u, size_t count, hipStream_t st)
+{
+    if (count == 0) return hipSuccess;
+    size_t blocks = (count + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)blocks), dim3(256), 0, st, g, u, count);
     return hipGetLastError();
 }
 

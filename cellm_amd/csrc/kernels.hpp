@@ -27,6 +27,25 @@ hipError_t launch_qgemv_i4_sym(const uint8_t* w, const uint16_t* S, int spr, int
 hipError_t launch_dequant_q4_affine(const uint32_t* wq, const void* S, const void* B, int sbt, int group_size,
                                     void* out, int out_dt, int N, int K, hipStream_t st);
 
+// Fused multi-output int8 GEMV (qgemv.hip): nseg (1..3) matrices sharing x
+// in one launch, or (silu) seg 0 = gate, seg 1 = up with h = silu(g) * u
+// written to seg 0's y.  Requires M <= 4, f16/f32 x, K % 16 == 0 and 16-byte
+// aligned W and x (qgemv_i8_fused_supported).
+struct I8FusedSeg {
+    const int8_t* w;
+    const void* s;
+    const float* bias;
+    float* y;
+    int n;
+    int per_channel;
+};
+bool qgemv_i8_fused_supported(int xdt, int M, int K, const void* x, const I8FusedSeg* segs, int nseg);
+hipError_t launch_qgemv_i8_fused(const I8FusedSeg* segs, int nseg, bool silu, int sdt, const void* x, int xdt, int M,
+                                 int K, hipStream_t st);
+
+// h[i] = silu(g[i]) * u[i] in place on g (dequant.hip), silu(g) = g / (1 + exp(-g)).
+hipError_t launch_silu_mul(float* g, const float* u, size_t count, hipStream_t st);
+
 // Prefill / batched qGEMM on MFMA: Y[M,N] = X[M,K] . dequant(W)[N,K]^T with
 // W tiles dequantized to f16 in LDS and f32 accumulation.  Requires K % 64 == 0
 // and 16-byte aligned W and X.  `workspace` (qgemm_workspace_bytes: wt 0 = q4

@@ -341,6 +341,19 @@ __device__ __forceinline__ void stage_unit_i8(u4_t raw, int idx, bool valid, uin
     if (valid && (idx & 1) == 0) cx[idx >> 1] = 1152.0f * s;
 }
 
+// Same pass with one row pointer per team row (rows of different matrices).
+template <int LPR, int R>
+__device__ __forceinline__ void load_pass_i8_rows(const u4_t* const (&rp)[R], int c0, int CPR,
+                                                  u4_t (&wv)[kUnroll][R])
+{
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+        const int c = min(c0 + u * LPR, CPR - 1);
+#pragma unroll
+        for (int r = 0; r < R; ++r) wv[u][r] = __builtin_nontemporal_load(rp[r] + c);
+    }
+}
+
 template <int LPR, int R>
 __device__ __forceinline__ void load_pass_i8(const u4_t* __restrict__ w8, int row0, int c0, int N, int CPR,
                                              u4_t (&wv)[kUnroll][R])
@@ -427,46 +440,35 @@ __device__ __forceinline__ void compute_pass_i8_f32x(int c0, int CPR, int K, con
     }
 }
 
-// XT: DT_F16 (dot2 path) or DT_F32 (exact int8->f32 conversion + f32 FMA).
-template <int LPR, int R, int MT, int XT, bool MP>
-__global__ __launch_bounds__(kBlock) void qgemv_i8_kernel(
-    const u4_t* __restrict__ w8, const void* __restrict__ S, int sdt, int per_channel,
-    const void* __restrict__ xv, const float* __restrict__ bias, float* __restrict__ y, int M, int N, int K)
+// int8 kernels' activation staging.  i8_load_x issues this thread's first
+// XW activation words (clamped, branch-free); i8_stage_x stores them (and any
+// further words of a large M*K) into LDS: f16 x as the dot2 pairs plus the
+// 1152*sum(x) offsets (stage_unit_i8), f32 x as is.
+template <int MT, int XT, int XW>
+__device__ __forceinline__ void i8_load_x(const void* __restrict__ xv, int M, int K, u4_t (&xr)[XW])
 {
-    extern __shared__ __align__(16) uint32_t lds[];
-    const int CPR = K >> 4;
-    const int team = threadIdx.x / LPR;
-    const int lane = threadIdx.x % LPR;
-    const int row0 = (blockIdx.x * (kBlock / LPR) + team) * R;
-
-    // (1) activations: f16 in 8-element units, f32 in 4-element units
-    constexpr int XW = MT == 1 ? 4 : 8;
     const int unit = XT == DT_F16 ? 8 : 4;
     const int units = K / unit;
     const int total = MT * units;
-    u4_t xr[XW];
 #pragma unroll
     for (int j = 0; j < XW; ++j) {
-        const int idx = min((int)threadIdx.x + j * kBlock, total - 1);  // clamped, branch-free
+        const int idx = min((int)threadIdx.x + j * kBlock, total - 1);
         const int m = idx / units;
         const int mc = min(m, M - 1);
         const char* base = reinterpret_cast<const char*>(xv) + ((size_t)mc * K + (size_t)(idx - m * units) * unit) *
                                                                    (XT == DT_F16 ? 2 : 4);
         xr[j] = *reinterpret_cast<const u4_t*>(base);
     }
-    // (2) weights for the first pass and this team's per-row scale / bias
-    u4_t wa[kUnroll][R];
-    load_pass_i8<LPR, R>(w8, row0, lane, N, CPR, wa);
-    uint32_t sraw[R];
-    float bv[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const int n = min(row0 + r, N - 1);
-        const size_t si = per_channel ? (size_t)n : 0;
-        sraw[r] = sdt == DT_F32 ? load_raw<DT_F32>(S, si) : load_raw<DT_F16>(S, si);
-        bv[r] = bias ? bias[n] : 0.0f;
-    }
-    // (3) stage activations
+}
+
+template <int MT, int XT, int XW>
+__device__ __forceinline__ void i8_stage_x(const u4_t (&xr)[XW], const void* __restrict__ xv, int M, int K,
+                                           uint32_t* lds)
+{
+    const int CPR = K >> 4;
+    const int unit = XT == DT_F16 ? 8 : 4;
+    const int units = K / unit;
+    const int total = MT * units;
     uint32_t* xq = lds;
     if constexpr (XT == DT_F16) {
         float* cx = reinterpret_cast<float*>(lds + (size_t)MT * CPR * 8);
@@ -500,6 +502,38 @@ __global__ __launch_bounds__(kBlock) void qgemv_i8_kernel(
                           : u4_t{0u, 0u, 0u, 0u};
         }
     }
+}
+
+// XT: DT_F16 (dot2 path) or DT_F32 (exact int8->f32 conversion + f32 FMA).
+template <int LPR, int R, int MT, int XT, bool MP>
+__global__ __launch_bounds__(kBlock) void qgemv_i8_kernel(
+    const u4_t* __restrict__ w8, const void* __restrict__ S, int sdt, int per_channel,
+    const void* __restrict__ xv, const float* __restrict__ bias, float* __restrict__ y, int M, int N, int K)
+{
+    extern __shared__ __align__(16) uint32_t lds[];
+    const int CPR = K >> 4;
+    const int team = threadIdx.x / LPR;
+    const int lane = threadIdx.x % LPR;
+    const int row0 = (blockIdx.x * (kBlock / LPR) + team) * R;
+
+    // (1) activations: f16 in 8-element units, f32 in 4-element units
+    constexpr int XW = MT == 1 ? 4 : 8;
+    u4_t xr[XW];
+    i8_load_x<MT, XT, XW>(xv, M, K, xr);
+    // (2) weights for the first pass and this team's per-row scale / bias
+    u4_t wa[kUnroll][R];
+    load_pass_i8<LPR, R>(w8, row0, lane, N, CPR, wa);
+    uint32_t sraw[R];
+    float bv[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int n = min(row0 + r, N - 1);
+        const size_t si = per_channel ? (size_t)n : 0;
+        sraw[r] = sdt == DT_F32 ? load_raw<DT_F32>(S, si) : load_raw<DT_F16>(S, si);
+        bv[r] = bias ? bias[n] : 0.0f;
+    }
+    // (3) stage activations
+    i8_stage_x<MT, XT, XW>(xr, xv, M, K, lds);
     __syncthreads();
     if (row0 >= N) return;
 
@@ -511,7 +545,7 @@ __global__ __launch_bounds__(kBlock) void qgemv_i8_kernel(
 
     auto compute = [&](int c0, const u4_t(&wv)[kUnroll][R]) {
         if constexpr (XT == DT_F16)
-            compute_pass_i8_f16x<LPR, R, MT>(c0, CPR, xq, reinterpret_cast<const float*>(lds + (size_t)MT * CPR * 8),
+            compute_pass_i8_f16x<LPR, R, MT>(c0, CPR, lds, reinterpret_cast<const float*>(lds + (size_t)MT * CPR * 8),
                                              wv, acc);
         else
             compute_pass_i8_f32x<LPR, R, MT>(c0, CPR, K, reinterpret_cast<const float*>(lds), wv, acc);
@@ -551,6 +585,150 @@ __global__ __launch_bounds__(kBlock) void qgemv_i8_kernel(
                         y[(size_t)m * N + n] = v;
                     }
             }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Fused multi-output int8 GEMV: up to three int8 matrices that share x in one
+// launch (QKV, metal.rs:387-439 mv_qkv_i8), or gate and up with the SiLU * up
+// epilogue (llama_graph.rs:320-327: mv_i8 x2 + silu_mul_f32_inplace,
+// metal.rs:235-245).  Each team holds R = 2 rows:
+//   * segments (SILU = false): consecutive rows of the concatenation
+//     [seg0 rows; seg1 rows; seg2 rows], each row reading its own matrix,
+//     scale, bias and output;
+//   * SILU: row n of seg0 (gate) and row n of seg1 (up);
+//     h[n] = silu(g) * u with g, u the scaled (and biased) row results and
+//     silu(g) = g / (1 + exp(-g)), written to seg0's output.
+// ---------------------------------------------------------------------------
+using I8Seg = I8FusedSeg;
+
+struct I8Segs {
+    I8Seg g0, g1, g2;
+};
+
+__device__ __forceinline__ I8Seg seg_of(const I8Segs& t, int i)
+{
+    I8Seg r = t.g0;
+    if (i == 1) r = t.g1;
+    if (i == 2) r = t.g2;
+    return r;
+}
+
+template <int LPR, int MT, int XT, bool MP, bool SILU>
+__global__ __launch_bounds__(kBlock) void qgemv_i8_fused_kernel(I8Segs segs, int sdt, const void* __restrict__ xv,
+                                                                int M, int total_rows, int K)
+{
+    constexpr int R = 2;
+    extern __shared__ __align__(16) uint32_t lds[];
+    const int CPR = K >> 4;
+    const int team = threadIdx.x / LPR;
+    const int lane = threadIdx.x % LPR;
+    // SILU: team -> one row index of both matrices; else two consecutive rows
+    const int first = SILU ? blockIdx.x * (kBlock / LPR) + team : (blockIdx.x * (kBlock / LPR) + team) * R;
+
+    constexpr int XW = MT == 1 ? 4 : 8;
+    u4_t xr[XW];
+    i8_load_x<MT, XT, XW>(xv, M, K, xr);
+
+    // row -> (segment, local row); rows past the end repeat the last row and are not stored
+    int segi[R], loc[R];
+    const u4_t* rp[R];
+    uint32_t sraw[R];
+    float bv[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        if constexpr (SILU) {
+            segi[r] = r;
+            loc[r] = min(first, total_rows - 1);
+        } else {
+            int v = min(first + r, total_rows - 1);
+            int i = 0;
+            if (v >= segs.g0.n) {
+                v -= segs.g0.n;
+                i = 1;
+                if (v >= segs.g1.n) {
+                    v -= segs.g1.n;
+                    i = 2;
+                }
+            }
+            segi[r] = i;
+            loc[r] = v;
+        }
+        const I8Seg sg = seg_of(segs, segi[r]);
+        rp[r] = reinterpret_cast<const u4_t*>(sg.w) + (size_t)loc[r] * CPR;
+        const size_t si = sg.per_channel ? (size_t)loc[r] : 0;
+        sraw[r] = sdt == DT_F32 ? load_raw<DT_F32>(sg.s, si) : load_raw<DT_F16>(sg.s, si);
+        bv[r] = sg.bias ? sg.bias[loc[r]] : 0.0f;
+    }
+    u4_t wa[kUnroll][R];
+    load_pass_i8_rows<LPR, R>(rp, lane, CPR, wa);
+    i8_stage_x<MT, XT, XW>(xr, xv, M, K, lds);
+    __syncthreads();
+    if (first >= total_rows) return;
+
+    float acc[R][MT];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[r][m] = 0.0f;
+    auto compute = [&](int c0, const u4_t(&wv)[kUnroll][R]) {
+        if constexpr (XT == DT_F16)
+            compute_pass_i8_f16x<LPR, R, MT>(c0, CPR, lds, reinterpret_cast<const float*>(lds + (size_t)MT * CPR * 8),
+                                             wv, acc);
+        else
+            compute_pass_i8_f32x<LPR, R, MT>(c0, CPR, K, reinterpret_cast<const float*>(lds), wv, acc);
+    };
+    if constexpr (!MP) {
+        compute(lane, wa);
+    } else {
+        constexpr int P = kUnroll * LPR;
+        u4_t wb[kUnroll][R];
+        for (int c0 = lane; c0 < CPR + lane; c0 += 2 * P) {
+            if (c0 - lane + P < CPR) load_pass_i8_rows<LPR, R>(rp, c0 + P, CPR, wb);
+            compute(c0, wa);
+            if (c0 - lane + P >= CPR) break;
+            if (c0 - lane + 2 * P < CPR) load_pass_i8_rows<LPR, R>(rp, c0 + 2 * P, CPR, wa);
+            compute(c0 + P, wb);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[r][m] = group_sum<LPR>(acc[r][m]);
+    if (lane != 0) return;
+
+    float val[R][MT];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const float s = sdt == DT_F32 ? raw_to_f32<DT_F32>(sraw[r])
+                      : sdt == DT_F16 ? raw_to_f32<DT_F16>(sraw[r])
+                                      : raw_to_f32<DT_BF16>(sraw[r]);
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            float v = acc[r][m] * s;
+            if (seg_of(segs, segi[r]).bias) v += bv[r];
+            val[r][m] = v;
+        }
+    }
+    if constexpr (SILU) {
+        float* h = segs.g0.y;
+        const int n = segs.g0.n;
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+            if (m < M) {
+                const float g = val[0][m];
+                const float sig = 1.0f / (1.0f + expf(-g));
+                h[(size_t)m * n + first] = (g * sig) * val[1][m];
+            }
+    } else {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            if (first + r >= total_rows) continue;
+            const I8Seg sg = seg_of(segs, segi[r]);
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+                if (m < M) sg.y[(size_t)m * sg.n + loc[r]] = val[r][m];
         }
     }
 }
@@ -725,6 +903,43 @@ hipError_t launch_i8_lpr(int lpr, int xdt, const int8_t* w, const void* S, int s
     }
 }
 
+template <int LPR, int MT, int XT, bool SILU>
+hipError_t launch_i8_fused_lpr(const I8Segs& t, int total_rows, int sdt, const void* x, int M, int K, hipStream_t st)
+{
+    const int CPR = K >> 4;
+    const int rows_per_block = (kBlock / LPR) * (SILU ? 1 : 2);
+    const dim3 grid((total_rows + rows_per_block - 1) / rows_per_block);
+    const size_t lds = XT == DT_F16 ? (size_t)MT * CPR * 8 * 4 + (size_t)MT * CPR * 4 : (size_t)MT * K * 4;
+    if (CPR > kUnroll * LPR)
+        hipLaunchKernelGGL((qgemv_i8_fused_kernel<LPR, MT, XT, true, SILU>), grid, dim3(kBlock), lds, st, t, sdt, x, M,
+                           total_rows, K);
+    else
+        hipLaunchKernelGGL((qgemv_i8_fused_kernel<LPR, MT, XT, false, SILU>), grid, dim3(kBlock), lds, st, t, sdt, x,
+                           M, total_rows, K);
+    return hipGetLastError();
+}
+
+template <int MT, int XT, bool SILU>
+hipError_t launch_i8_fused_mt(int lpr, const I8Segs& t, int total_rows, int sdt, const void* x, int M, int K,
+                              hipStream_t st)
+{
+    switch (lpr) {
+    case 8: return launch_i8_fused_lpr<8, MT, XT, SILU>(t, total_rows, sdt, x, M, K, st);
+    case 16: return launch_i8_fused_lpr<16, MT, XT, SILU>(t, total_rows, sdt, x, M, K, st);
+    case 32: return launch_i8_fused_lpr<32, MT, XT, SILU>(t, total_rows, sdt, x, M, K, st);
+    default: return launch_i8_fused_lpr<64, MT, XT, SILU>(t, total_rows, sdt, x, M, K, st);
+    }
+}
+
+template <int XT, bool SILU>
+hipError_t launch_i8_fused_xt(int lpr, const I8Segs& t, int total_rows, int sdt, const void* x, int M, int K,
+                              hipStream_t st)
+{
+    if (M == 1) return launch_i8_fused_mt<1, XT, SILU>(lpr, t, total_rows, sdt, x, M, K, st);
+    if (M == 2) return launch_i8_fused_mt<2, XT, SILU>(lpr, t, total_rows, sdt, x, M, K, st);
+    return launch_i8_fused_mt<4, XT, SILU>(lpr, t, total_rows, sdt, x, M, K, st);
+}
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
@@ -835,6 +1050,37 @@ hipError_t launch_qgemv_i8(const int8_t* w, const void* S, int sdt, int per_chan
         hipLaunchKernelGGL((qgemv_i8_generic_kernel<DT_BF16>), grid, dim3(kBlock), 0, st, w, S, sdt, per_channel, x,
                            bias, y, M, N, K);
     return hipGetLastError();
+}
+
+bool qgemv_i8_fused_supported(int xdt, int M, int K, const void* x, const I8FusedSeg* segs, int nseg)
+{
+    if (!(xdt == DT_F16 || xdt == DT_F32) || M < 1 || M > 4 || K <= 0 || (K % 16) != 0 || !aligned16(x)) return false;
+    const int MT = M <= 1 ? 1 : (M <= 2 ? 2 : 4);
+    const size_t lds = xdt == DT_F16 ? (size_t)MT * (K >> 4) * 36 : (size_t)MT * K * 4;
+    if (lds > 64 * 1024) return false;
+    for (int i = 0; i < nseg; ++i)
+        if (!aligned16(segs[i].w)) return false;
+    return true;
+}
+
+hipError_t launch_qgemv_i8_fused(const I8FusedSeg* segs, int nseg, bool silu, int sdt, const void* x, int xdt, int M,
+                                 int K, hipStream_t st)
+{
+    I8Segs t;
+    t.g0 = segs[0];
+    t.g1 = nseg > 1 ? segs[1] : segs[0];
+    t.g2 = nseg > 2 ? segs[2] : segs[0];
+    if (nseg < 2) t.g1.n = 0;
+    if (nseg < 3) t.g2.n = 0;
+    const int total_rows = silu ? segs[0].n : t.g0.n + t.g1.n + t.g2.n;
+    if (total_rows <= 0) return hipSuccess;
+    const GemvShape sh = pick_shape(K >> 4, silu ? 2 * total_rows : total_rows, false);
+    if (silu) {
+        if (xdt == DT_F16) return launch_i8_fused_xt<DT_F16, true>(sh.lpr, t, total_rows, sdt, x, M, K, st);
+        return launch_i8_fused_xt<DT_F32, true>(sh.lpr, t, total_rows, sdt, x, M, K, st);
+    }
+    if (xdt == DT_F16) return launch_i8_fused_xt<DT_F16, false>(sh.lpr, t, total_rows, sdt, x, M, K, st);
+    return launch_i8_fused_xt<DT_F32, false>(sh.lpr, t, total_rows, sdt, x, M, K, st);
 }
 
 }  // namespace cellm

@@ -185,6 +185,40 @@ class HipOps:
                                                   _torch_dtype_code(scales), group, _dev_ptr(x), _torch_dtype_code(x),
                                                   _dev_ptr(y), m, n, k, _stream_ptr(stream)))
 
+    def encode_qkv_i8(self, wq, sq, wk, sk, wv, sv, x, q, k_out, v, bq=None, bk=None, bv=None,
+                      stream=None) -> None:
+        """MetalOps::encode_qkv_i8(_bias): three int8 projections of one x in one launch."""
+        rows_q, cols = wq.shape
+        rows_kv = wk.shape[0]
+        m = x.numel() // cols
+        if sq.dtype != sk.dtype or sq.dtype != sv.dtype:
+            raise TypeError("q/k/v scales must share a dtype")
+        check(self._lib.cellm_hip_qgemv_i8_qkv(
+            self._h, _dev_ptr(wq), _dev_ptr(sq), sq.numel(), _dev_ptr(bq), _dev_ptr(wk), _dev_ptr(sk), sk.numel(),
+            _dev_ptr(bk), _dev_ptr(wv), _dev_ptr(sv), sv.numel(), _dev_ptr(bv), _torch_dtype_code(sq), _dev_ptr(x),
+            _torch_dtype_code(x), _dev_ptr(q), _dev_ptr(k_out), _dev_ptr(v), m, rows_q, rows_kv, cols,
+            _stream_ptr(stream)))
+
+    def encode_gate_up_silu_i8(self, wg, sg, wu, su, x, h, bg=None, bu=None, stream=None) -> None:
+        """h = silu(Wg.x * sg (+bg)) * (Wu.x * su (+bu)); int8 gate/up."""
+        n, k = wg.shape
+        m = x.numel() // k
+        if sg.dtype != su.dtype:
+            raise TypeError("gate/up scales must share a dtype")
+        check(self._lib.cellm_hip_qgemv_i8_gate_up_silu(
+            self._h, _dev_ptr(wg), _dev_ptr(sg), sg.numel(), _dev_ptr(bg), _dev_ptr(wu), _dev_ptr(su), su.numel(),
+            _dev_ptr(bu), _torch_dtype_code(sg), _dev_ptr(x), _torch_dtype_code(x), _dev_ptr(h), m, n, k,
+            _stream_ptr(stream)))
+
+    def encode_gate_up_silu_q4_affine(self, wg, sg, bg, wu, su, bu, x, h, group: int = 64, stream=None) -> None:
+        """h = silu(dequant(Wg).x) * (dequant(Wu).x); MLX 4-bit affine gate/up."""
+        n, k = wg.shape[0], wg.shape[1] * 8
+        m = x.numel() // k
+        check(self._lib.cellm_hip_qgemv_q4_affine_gate_up_silu(
+            self._h, _dev_ptr(wg), _dev_ptr(sg), _dev_ptr(bg), _dev_ptr(wu), _dev_ptr(su), _dev_ptr(bu),
+            _torch_dtype_code(sg), group, _dev_ptr(x), _torch_dtype_code(x), _dev_ptr(h), m, n, k,
+            _stream_ptr(stream)))
+
     @staticmethod
     def qgemv_op_i8(w, scales, x, y, bias=None) -> "_lib.QgemvOp":
         """One cellm_hip_qgemv_op_t of kind int8 (arguments as encode_qgemv_i8)."""

@@ -121,6 +121,40 @@ int32_t cellm_hip_qgemv_q4_affine(cellm_hip_ctx_t* ctx, const uint32_t* wq, cons
                                   int32_t sb_dtype, int64_t group, const void* x, int32_t x_dtype, float* y,
                                   int64_t m, int64_t n, int64_t k, void* stream);
 
+/* Fused QKV, one launch for m <= 4 (f16/f32 x, cols % 16 == 0, 16-byte
+ * aligned W and x; other shapes run three cellm_hip_qgemv_i8 launches):
+ *   q = (Wq . x) * sq (+ bq), k and v likewise with rows_kv rows each.
+ * Each projection has its own scales (per row when n_s >= rows, else scale[0])
+ * and optional bias (NULL = none); all scales share scale_dtype.  Replaces
+ * MetalOps::encode_qkv_i8 / encode_qkv_i8_bias (crates/cellm-kernels/src/metal.rs:923-945,
+ * 1153-1160; kernel mv_qkv_i8 metal.rs:387-439). */
+int32_t cellm_hip_qgemv_i8_qkv(cellm_hip_ctx_t* ctx, const int8_t* wq, const void* sq, int64_t n_sq, const float* bq,
+                               const int8_t* wk, const void* sk, int64_t n_sk, const float* bk, const int8_t* wv,
+                               const void* sv, int64_t n_sv, const float* bv, int32_t scale_dtype, const void* x,
+                               int32_t x_dtype, float* q, float* k_out, float* v, int64_t m, int64_t rows_q,
+                               int64_t rows_kv, int64_t cols, void* stream);
+
+/* Gate and up projections with the SiLU * up epilogue:
+ *   h = silu((Wg . x) * sg (+ bg)) * ((Wu . x) * su (+ bu)),  silu(g) = g / (1 + exp(-g)).
+ * One launch for m <= 4 under the conditions of cellm_hip_qgemv_i8_qkv; other
+ * shapes run two GEMVs and an elementwise kernel.  Replaces the gate/up
+ * encode_mv_i8(_bias) pair plus encode_silu_mul_f32_inplace of the decode
+ * graphs (crates/cellm-model/src/llama_graph.rs:318-327,
+ * crates/cellm-model/src/qwen.rs:1445-1453; metal.rs:235-245, 956), and the
+ * CPU loop of llama.rs:477-484. */
+int32_t cellm_hip_qgemv_i8_gate_up_silu(cellm_hip_ctx_t* ctx, const int8_t* wg, const void* sg, int64_t n_sg,
+                                        const float* bg, const int8_t* wu, const void* su, int64_t n_su,
+                                        const float* bu, int32_t scale_dtype, const void* x, int32_t x_dtype, float* h,
+                                        int64_t m, int64_t n, int64_t k, void* stream);
+
+/* The same for MLX 4-bit affine gate/up weights (two cellm_hip_qgemv_q4_affine
+ * launches, then the SiLU * up kernel); sg/bg and su/bu are the affine
+ * scales/biases of each matrix. */
+int32_t cellm_hip_qgemv_q4_affine_gate_up_silu(cellm_hip_ctx_t* ctx, const uint32_t* wg, const void* sg,
+                                               const void* bg, const uint32_t* wu, const void* su, const void* bu,
+                                               int32_t sb_dtype, int64_t group, const void* x, int32_t x_dtype,
+                                               float* h, int64_t m, int64_t n, int64_t k, void* stream);
+
 /* One projection of a batch (cellm_hip_qgemv_batch).  kind
  * CELLM_HIP_OP_QGEMV_I8 takes the arguments of cellm_hip_qgemv_i8 (w int8,
  * scales, sb_dtype = scale dtype, n_scales, bias; biases and group unused);

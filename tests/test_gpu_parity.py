@@ -432,3 +432,60 @@ def test_qgemv_batch_matches_single_calls(ops):
         ops.encode_qgemv_batch([ops.qgemv_op_q4_affine(q[0], q[1], q[2], q[3], outs[0]), bad])
     torch.cuda.synchronize()
     assert torch.equal(outs[0], refs[0])
+
+
+# ----------------------------------------------------- fused multi-output ----
+
+@pytest.mark.parametrize("m,xdt", [(1, np.float32), (4, np.float16), (8, np.float16), (3, np.float32)])
+def test_qkv_i8_fused(ops, m, xdt):
+    """SmolLM2-360M attention: q 960 rows, k/v 320 rows, hidden 960; biases,
+    and a per-tensor scale on v.  m <= 4 is one launch, m = 8 the fallback."""
+    import torch
+
+    k, rq, rkv = 960, 960, 320
+    wq, sq, x = make_i8(rq, k, m, cfg=5, scale_dtype=np.float16, x_dtype=xdt, salt=31)
+    wk, sk, _ = make_i8(rkv, k, m, cfg=5, scale_dtype=np.float16, salt=32)
+    wv, sv, _ = make_i8(rkv, k, m, cfg=5, scale_dtype=np.float16, salt=33)
+    sv = sv[:1].copy()  # per-tensor
+    bq = oracle.gen_normal((rq,), seed(5, 8, 1), 0.0, 1.0)
+    bk = oracle.gen_normal((rkv,), seed(5, 8, 2), 0.0, 1.0)
+    outs = [torch.empty((m, n), dtype=torch.float32, device="cuda") for n in (rq, rkv, rkv)]
+    ops.encode_qkv_i8(_t(wq), _t(sq), _t(wk), _t(sk), _t(wv), _t(sv), _t(x), *outs, bq=_t(bq), bk=_t(bk))
+    torch.cuda.synchronize()
+    refs = [oracle.qgemv_i8(wq, sq, x) + bq[None, :], oracle.qgemv_i8(wk, sk, x) + bk[None, :],
+            oracle.qgemv_i8(wv, np.full(rkv, sv[0], np.float16), x)]
+    for o, r in zip(outs, refs):
+        assert rel_err(o.cpu().numpy(), r) <= TOL_F32
+
+
+@pytest.mark.parametrize("m,xdt", [(1, np.float32), (4, np.float16), (8, np.float16)])
+def test_gate_up_silu_i8(ops, m, xdt):
+    """SmolLM2-360M MLP: h = silu(Wg.x*sg + bg) * (Wu.x*su) for 2560 rows."""
+    import torch
+
+    k, n = 960, 2560
+    wg, sg, x = make_i8(n, k, m, cfg=5, scale_dtype=np.float16, x_dtype=xdt, salt=41)
+    wu, su, _ = make_i8(n, k, m, cfg=5, scale_dtype=np.float16, salt=42)
+    bg = oracle.gen_normal((n,), seed(5, 9, 1), 0.0, 0.5)
+    h = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    ops.encode_gate_up_silu_i8(_t(wg), _t(sg), _t(wu), _t(su), _t(x), h, bg=_t(bg))
+    torch.cuda.synchronize()
+    g = np.ascontiguousarray(oracle.qgemv_i8(wg, sg, x) + bg[None, :], np.float32)
+    ref = oracle.silu_mul_(g, oracle.qgemv_i8(wu, su, x))
+    assert rel_err(h.cpu().numpy(), ref) <= TOL_F32
+
+
+def test_gate_up_silu_q4(ops):
+    """Qwen2.5-0.5B MLP halves (896 -> 4864 each), q4 affine g64."""
+    import torch
+
+    k, n = 896, 4864
+    wg, sg, bg, x = make_q4(n, k, 1, salt=51)
+    wu, su, bu, _ = make_q4(n, k, 1, salt=52)
+    h = torch.empty((1, n), dtype=torch.float32, device="cuda")
+    ops.encode_gate_up_silu_q4_affine(_t(wg), _sb_tensor(sg), _sb_tensor(bg), _t(wu), _sb_tensor(su),
+                                      _sb_tensor(bu), _t(x), h)
+    torch.cuda.synchronize()
+    g = np.ascontiguousarray(oracle.qgemv_q4_affine(wg, sg, bg, x, k), np.float32)
+    ref = oracle.silu_mul_(g, oracle.qgemv_q4_affine(wu, su, bu, x, k))
+    assert rel_err(h.cpu().numpy(), ref) <= TOL_F32
