@@ -197,7 +197,7 @@ def main():
             traffic = None
     roofline = {"bound": "hbm", "achieved": dom["GB/s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(dom["GB/s"] / HBM_PEAK_GBS, 4), "traffic": traffic,
-                "kernel": "qgemv_q4_persist_kernel (896->151936 lm_head, M=1)",
+                "kernel": "qgemv_q4_ring_kernel (896->151936 lm_head, M=1)",
                 "algorithmic_bytes": q4_bytes(1, 151936, 896)}
     del sets
     torch.cuda.empty_cache()

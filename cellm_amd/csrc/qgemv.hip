@@ -322,6 +322,119 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_persist_kernel(
     }
 }
 
+// Batched-row variant for long single-row outputs (M = 1, N % 16 == 0, K <= 1024).
+// A wave owns batches of 16 consecutive rows, b = wave, wave + waves, ...; a
+// step is one row pair (lanes 0-31 row 2s, lanes 32-63 row 2s+1, lane = 16-byte
+// chunk of the row, its x chunk held in registers).  Every lane keeps the 8
+// steps of the next batch in flight (a register ring), and the batch's scale
+// and bias rows, contiguous in S and B, arrive with one 16-byte load per array
+// a batch ahead and are parked in LDS.  The 8 per-step partial sums of a lane
+// are reduced across the row's 32 lanes with a halving butterfly (9 exchanges
+// per 8 rows instead of 5 per row).
+constexpr int kRingThreads = 512;
+constexpr int kRingSteps = 8;
+
+template <int SBT>
+__global__ __launch_bounds__(kRingThreads) void qgemv_q4_ring_kernel(const u4_t* __restrict__ wq,
+                                                                    const void* __restrict__ S,
+                                                                    const void* __restrict__ Bz,
+                                                                    const _Float16* __restrict__ x,
+                                                                    float* __restrict__ y, int N, int K, int gshift)
+{
+    constexpr int P = kRingSteps;
+    constexpr int SBB = SBT == DT_F32 ? 4 : 2;
+    extern __shared__ __align__(16) uint32_t lds[];
+    const int CPR = K >> 5;
+    uint32_t* xq = lds;
+    float2* cx = reinterpret_cast<float2*>(lds + (size_t)CPR * 16);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // per wave: S rows at +0, B rows at +1024 (16 rows, <= 32 bytes each), 16-byte aligned
+    unsigned char* sbw = reinterpret_cast<unsigned char*>(lds) + ((CPR * 72 + 15) & ~15) + wave * 2048;
+    const int h = lane >> 5, c = lane & 31;
+    const int gpr = (K + (1 << gshift) - 1) >> gshift;
+    const int sbrow = gpr * SBB;        // bytes of S (and of B) per row
+    const int sbv = sbrow;              // 16-byte vectors per batch per array: 16 rows * sbrow / 16
+    const int NB = N >> 4;
+    const int gw = blockIdx.x * (kRingThreads / 64) + wave, GW = gridDim.x * (kRingThreads / 64);
+    const int nb = gw < NB ? (NB - 1 - gw) / GW + 1 : 0;  // batches of this wave
+    const int cc = min(c, CPR - 1);  // lanes past the row re-read its last chunk; x is zero there
+    const int gi = (cc << 5) >> gshift;
+
+    u4_t wr[P];
+    auto load_w = [&](int bi, int s) {
+        const int b = min(gw + GW * bi, NB - 1);  // past the end: a clamped re-read, never used
+        wr[s] = __builtin_nontemporal_load(wq + (size_t)(16 * b + 2 * s + h) * CPR + cc);
+    };
+    u4_t sbr;
+    auto load_sb = [&](int bi) {
+        const int b = min(gw + GW * bi, NB - 1);
+        const int v = lane < sbv ? lane : min(lane - sbv, sbv - 1);
+        const unsigned char* base = reinterpret_cast<const unsigned char*>(lane < sbv ? S : Bz);
+        sbr = *reinterpret_cast<const u4_t*>(base + (size_t)b * 16 * sbrow + (size_t)v * 16);
+    };
+    // loads first, then the x staging (its wait covers them; nothing is computed before both)
+#pragma unroll
+    for (int s = 0; s < P; ++s) load_w(0, s);
+    load_sb(0);
+    for (int idx = threadIdx.x; idx < (K >> 3); idx += kRingThreads) {
+        const u4_t raw = *reinterpret_cast<const u4_t*>(x + idx * 8);
+        stage_word_q4(raw, idx, true, xq, cx);
+    }
+    __syncthreads();
+    u4_t xa[4];
+    float2 xc = make_float2(0.f, 0.f);
+    {
+        const u4_t* xp = reinterpret_cast<const u4_t*>(xq + cc * 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xa[i] = c < CPR ? xp[i] : u4_t{0u, 0u, 0u, 0u};
+        if (c < CPR) xc = cx[cc];
+    }
+    const uint32_t m0f = 0x000F000Fu, m1f = 0x00F000F0u, magic = 0x64006400u;
+    for (int bi = 0; bi < nb; ++bi) {
+        // this batch's scale/bias rows -> LDS (loaded a batch ago); next batch's load
+        if (lane < 2 * sbv) *reinterpret_cast<u4_t*>(sbw + (lane < sbv ? lane * 16 : 1024 + (lane - sbv) * 16)) = sbr;
+        load_sb(bi + 1);
+        float v[P];
+#pragma unroll
+        for (int s = 0; s < P; ++s) {
+            const u4_t w = wr[s];
+            const int row = 2 * s + h;
+            float sc, bb;
+            if constexpr (SBT == DT_F32) {
+                sc = *reinterpret_cast<const float*>(sbw + row * sbrow + gi * 4);
+                bb = *reinterpret_cast<const float*>(sbw + 1024 + row * sbrow + gi * 4);
+            } else {
+                sc = raw_to_f32<SBT>(*reinterpret_cast<const uint16_t*>(sbw + row * sbrow + gi * 2));
+                bb = raw_to_f32<SBT>(*reinterpret_cast<const uint16_t*>(sbw + 1024 + row * sbrow + gi * 2));
+            }
+            float d = -xc.x;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                d = dot2(and_or(w[e], m0f, magic), xa[e][0], d);
+                d = dot2(and_or(w[e], m1f, magic), xa[e][1], d);
+                const uint32_t t = w[e] >> 8;
+                d = dot2(and_or(t, m0f, magic), xa[e][2], d);
+                d = dot2(and_or(t, m1f, magic), xa[e][3], d);
+            }
+            v[s] = sc * d + bb * xc.y;
+            load_w(bi + 1, s);
+        }
+        // halving butterfly over the 32 lanes of a row: 8 partials -> one row sum per lane
+        const bool b16 = c & 16, b8 = c & 8, b4 = c & 4;
+        float a4[4], a2[2], a1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a4[i] = (b16 ? v[i + 4] : v[i]) + __shfl_xor(b16 ? v[i] : v[i + 4], 16, 32);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) a2[i] = (b8 ? a4[i + 2] : a4[i]) + __shfl_xor(b8 ? a4[i] : a4[i + 2], 8, 32);
+        a1 = (b4 ? a2[1] : a2[0]) + __shfl_xor(b4 ? a2[0] : a2[1], 4, 32);
+        a1 += __shfl_xor(a1, 2, 32);
+        a1 += __shfl_xor(a1, 1, 32);
+        // the lane now holds step s = 4*b16 + 2*b8 + b4 of the batch
+        const int s = (b16 ? 4 : 0) + (b8 ? 2 : 0) + (b4 ? 1 : 0);
+        if ((c & 3) == 0) y[16 * (gw + GW * bi) + 2 * s + h] = a1;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // int8 per-row scale
 // ---------------------------------------------------------------------------
@@ -973,6 +1086,25 @@ hipError_t launch_qgemv_q4_affine(const uint32_t* wq, const void* S, const void*
     const int gshift = __builtin_ctz((unsigned)group_size);
     const bool fast = !force_generic && xdt == DT_F16 && M <= 4 && (K % 32) == 0 && group_size >= 32 &&
                       aligned16(wq) && aligned16(x) && qgemv_q4_lds_bytes(M, K) <= 64 * 1024;
+    const int sbrow = ((K + group_size - 1) / group_size) * (sbt == DT_F32 ? 4 : 2);
+    if (fast && M == 1 && N >= 32768 && (N % 16) == 0 && (K >> 5) <= 32 && sbrow <= 32 && aligned16(S) &&
+        aligned16(B)) {
+        // long single-row outputs, whole 16-row batches: batched-row ring kernel, one block per CU
+        const int grid = std::max(1, persist_grid() / 4);
+        const size_t lds = (size_t)(((K >> 5) * 72 + 15) & ~15) + (size_t)(kRingThreads / 64) * 2048;
+        const u4_t* w4 = reinterpret_cast<const u4_t*>(wq);
+        const _Float16* xh = reinterpret_cast<const _Float16*>(x);
+        if (sbt == DT_F16)
+            hipLaunchKernelGGL((qgemv_q4_ring_kernel<DT_F16>), dim3(grid), dim3(kRingThreads), lds, st, w4, S, B, xh, y,
+                               N, K, gshift);
+        else if (sbt == DT_F32)
+            hipLaunchKernelGGL((qgemv_q4_ring_kernel<DT_F32>), dim3(grid), dim3(kRingThreads), lds, st, w4, S, B, xh, y,
+                               N, K, gshift);
+        else
+            hipLaunchKernelGGL((qgemv_q4_ring_kernel<DT_BF16>), dim3(grid), dim3(kRingThreads), lds, st, w4, S, B, xh,
+                               y, N, K, gshift);
+        return hipGetLastError();
+    }
     if (fast && M == 1 && N >= 32768 && (K >> 5) <= 32) {
         // long single-row outputs: persistent kernel, 32 lanes per row, 2 rows per team
         constexpr int LPR = 32, R = 2, ROWS = (kBlock / LPR) * R;

@@ -115,11 +115,13 @@ def test_q4_gemv_qwen_lm_head(ops):
 
 
 @pytest.mark.parametrize("k,n,group,sb", [
-    (1024, 40000, 64, "bf16"),      # persistent single-row kernel, 32 chunks per row
-    (512, 33001, 128, np.float32),  # ragged last tile
-    (256, 32768, 32, np.float16),
+    (1024, 40000, 64, "bf16"),      # batched-row ring kernel, 32 chunks per row
+    (960, 49152, 64, np.float16),   # ring kernel, 30 of 32 lanes per row (SmolLM2-360M lm_head shape)
+    (256, 32768, 32, np.float16),   # ring kernel, 8 chunks per row
+    (512, 33001, 128, np.float32),  # N % 16 != 0: persistent kernel, ragged last tile
+    (896, 65536, 64, np.float32),   # f32 scale rows of 56 bytes: persistent kernel
 ])
-def test_q4_gemv_long_output_persistent(ops, k, n, group, sb):
+def test_q4_gemv_long_output(ops, k, n, group, sb):
     wq, s, b, x = make_q4(n, k, 1, sb_dtype=sb, group=group, salt=k + n)
     y = _run_q4(ops, wq, s, b, x, group=group)
     assert rel_err(y, oracle.qgemv_q4_affine(wq, s, b, x, k, gs=group)) <= TOL_F32
