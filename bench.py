@@ -291,6 +291,8 @@ def extra_configs(torch, ops, stream, gen):
                                                    "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     del wset
 
+    res.update(decode_step_cfg5())
+
     # M=512 prefill qGEMM (MFMA)
     m = 512
     for k, n in ((896, 4864), (4864, 896)):
@@ -302,6 +304,79 @@ def extra_configs(torch, ops, stream, gen):
         tflops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
         res[f"cfg4_qgemm_m512_{k}x{n}"] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tflops, 1),
                                            "frac_mfma_f16": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
+    return res
+
+
+CFG5_SESSIONS, CFG5_CTX, CFG5_TPB = 4, 512, 16
+
+
+def cfg5_runner():
+    """a random-init SmolLM2-360M-shape int8 model on the device
+    runner (cellm_llama_dev_*): 32 layers, hidden 960, 15/5 heads of 64,
+    intermediate 2560, vocab 49152, 4 sessions with context 512 of seeded f16
+    K/V on interleaved pages.  Returns (runner, shape, block tables)."""
+    import numpy as np
+
+    from cellm_amd.llama_step import LlamaDevice, LlamaShape
+
+    sessions, ctx, tpb = CFG5_SESSIONS, CFG5_CTX, CFG5_TPB
+    shape = LlamaShape(32, 960, 15, 5, 64, 2560, 49152, 1e-5, 100000.0, tpb, sessions * ctx // tpb)
+    rng = np.random.default_rng(0xC5)
+    layers = []
+    for _ in range(shape.n_layers):
+        ws, ss = [], []
+        for o, i in shape.proj_shapes():
+            ws.append(rng.integers(-127, 128, (o, i), dtype=np.int8))
+            ss.append((rng.uniform(0.5, 1.5, o) / (73.3 * np.sqrt(i))).astype(np.float16))
+        n1 = (1.0 + 0.1 * rng.standard_normal(shape.hidden)).astype(np.float16)
+        n2 = (1.0 + 0.1 * rng.standard_normal(shape.hidden)).astype(np.float16)
+        layers.append((ws, ss, n1, n2))
+    embed = rng.integers(-127, 128, (shape.vocab, shape.hidden), dtype=np.int8)
+    escale = (rng.uniform(0.5, 1.5, shape.vocab) / 127.0).astype(np.float16)
+    fnorm = (1.0 + 0.1 * rng.standard_normal(shape.hidden)).astype(np.float16)
+    dev = LlamaDevice(shape, layers, embed, escale, fnorm, 0, max_rows=sessions, max_blocks=ctx // tpb)
+    del layers, embed
+    kv = shape.kv_elems()
+    dev.kv_upload(rng.standard_normal(kv, dtype=np.float32).astype(np.float16),
+                  rng.standard_normal(kv, dtype=np.float32).astype(np.float16))
+    bts = np.array([[b * sessions + s for b in range(ctx // tpb)] for s in range(sessions)], np.uint32)
+    return dev, shape, bts
+
+
+def decode_step_cfg5():
+    """The configs[4] decode step: host ids in -> greedy ids out (input/output
+    copies and the final synchronisation included), timed on the host clock,
+    replaying the captured graph and, for comparison, launching eagerly.
+    Bytes per step: every int8 weight and scale once, plus each session's K/V
+    over its context."""
+    import numpy as np
+
+    dev, shape, bts = cfg5_runner()
+    sessions, ctx = CFG5_SESSIONS, CFG5_CTX
+    kvd = shape.n_kv_heads * shape.head_dim
+    res = {}
+    for rows in (sessions, 1):
+        tokens = np.array([(1000 + 7919 * s) % shape.vocab for s in range(rows)], np.uint32)
+        pos = np.full(rows, ctx - 1, np.int32)
+        step_bytes = shape.weight_bytes() + rows * ctx * shape.n_layers * kvd * 2 * 2
+        entry = {"sessions": rows, "context": ctx, "bytes_per_step": step_bytes}
+        for mode, graphs in (("graph", True), ("eager", False)):
+            dev.set_graphs(graphs)
+            for _ in range(3):
+                dev.step(tokens, pos, bts[:rows])
+            n = 50
+            t0 = time.perf_counter()
+            for _ in range(n):
+                ids, _ = dev.step(tokens, pos, bts[:rows])
+            us = (time.perf_counter() - t0) / n * 1e6
+            if graphs:
+                entry.update({"us_per_step": round(us, 1), "tokens_per_s": round(rows * 1e6 / us, 1),
+                              "GB/s": round(step_bytes / (us * 1e-6) / 1e9, 1),
+                              "frac_hbm": round(step_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+            else:
+                entry["eager_us_per_step"] = round(us, 1)
+        res[f"cfg5_llama360m_i8_decode_step_{rows}sessions"] = entry
+    dev.close()
     return res
 
 

@@ -59,6 +59,18 @@ SIGNATURES = {
     "cellm_hip_logits_i8": (_i32, [_vp, _vp, _vp, _vp, _sz, _sz, C.c_char_p, _vp]),
     "cellm_hip_logits_i4": (_i32, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, C.c_char_p, _vp]),
     "cellm_hip_logits_q4_affine": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _sz, _sz, C.c_char_p, _vp]),
+    "cellm_hip_embed_i8": (_i32, [_vp, _vp, _i64, _vp, _vp, _i64, _i64, _vp, _vp]),
+    "cellm_hip_rms_norm": (_i32, [_vp, _vp, _vp, _i32, _i64, _i64, C.c_float, _vp, _vp]),
+    "cellm_hip_add_rms_norm": (_i32, [_vp, _vp, _vp, _vp, _i32, _i64, _i64, C.c_float, _vp, _vp]),
+    "cellm_hip_rope_half_f32": (_i32, [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp]),
+    "cellm_hip_rope_kv_write_f16": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp,
+                                           _i64, _i64, _i64, _i64, _i64, _vp]),
+    "cellm_hip_kv_write_f16": (_i32, [_vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
+                                      _vp]),
+    "cellm_hip_attention_gqa_f16kv": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64,
+                                             _i64, _i64, _vp, _vp]),
+    "cellm_hip_add_f32_inplace": (_i32, [_vp, _vp, _vp, _i64, _vp]),
+    "cellm_hip_argmax_f32": (_i32, [_vp, _vp, _i64, _i64, _vp, _vp, _vp]),
 }
 
 _lib = None

@@ -23,7 +23,7 @@ LIB_PATH = PKG_DIR / "libcellm_hip.so"
 STEP_LIB_PATH = PKG_DIR / "libcellm_llama_step.so"
 REPO_ROOT = PKG_DIR.parent
 
-SOURCES = ["qgemv.hip", "qgemv_mfma.hip", "qgemm.hip", "dequant.hip", "capi.cpp"]
+SOURCES = ["qgemv.hip", "qgemv_mfma.hip", "qgemm.hip", "dequant.hip", "decode.hip", "capi.cpp"]
 HEADERS = ["common.hpp", "kernels.hpp"]
 ARCH = os.environ.get("CELLM_HIP_ARCH", "gfx950")
 
@@ -84,13 +84,16 @@ def build_library(verbose: bool = False, jobs: int = 4) -> Path:
 
 
 def build_step_library(verbose: bool = False) -> Path:
-    """The host-side decode-step runner over libcellm_hip.so (pure C++, CPU
-    parts compiled without FP contraction so they round as the reference)."""
+    """The host-side decode-step runners over libcellm_hip.so (C++; the CPU
+    parts compiled without FP contraction so they round as the reference; the
+    device runner also calls the HIP runtime for its own buffers)."""
     cxx = os.environ.get("CXX", "g++")
     tmp = STEP_LIB_PATH.with_suffix(".so.tmp")
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
     cmd = [cxx, "-O3", "-std=c++17", "-fPIC", "-shared", "-ffp-contract=off", "-fno-fast-math", "-fno-math-errno",
-           "-Wall", "-o", str(tmp), str(CSRC / "llama_step.cpp"), f"-L{PKG_DIR}", "-lcellm_hip",
-           "-Wl,-rpath,$ORIGIN"]
+           "-Wall", "-D__HIP_PLATFORM_AMD__", f"-I{rocm}/include", "-o", str(tmp), str(CSRC / "llama_step.cpp"),
+           str(CSRC / "llama_device.cpp"), f"-L{PKG_DIR}", "-lcellm_hip", f"-L{rocm}/lib", "-lamdhip64",
+           "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{rocm}/lib"]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

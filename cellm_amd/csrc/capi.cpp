@@ -68,6 +68,7 @@ struct cellm_hip_ctx {
     DeviceBuffer x_buf, y_buf;
     std::unordered_map<hipStream_t, DeviceBuffer> workspaces;  // split-K partials, one per stream
     std::unordered_map<hipStream_t, DeviceBuffer> aux;         // unfused gate/up: the up rows, one per stream
+    std::unordered_map<hipStream_t, DeviceBuffer> attn;        // split-sequence attention partials, one per stream
 };
 
 namespace {
@@ -433,7 +434,7 @@ void cellm_hip_destroy(cellm_hip_ctx_t* ctx)
     if (!ctx) return;
     DeviceGuard g(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
-    for (auto* map : {&ctx->workspaces, &ctx->aux})
+    for (auto* map : {&ctx->workspaces, &ctx->aux, &ctx->attn})
         for (auto& kv : *map) {
             (void)hipStreamSynchronize(kv.first);
             if (kv.second.ptr) (void)hipFree(kv.second.ptr);
@@ -708,6 +709,193 @@ int32_t cellm_hip_logits_q4_affine(cellm_hip_ctx_t* ctx, const float* x, const u
         return qgemv_q4_impl(ctx, reinterpret_cast<const uint32_t*>(dw), ds, db, sb_dtype, 64, dx, DT_F32, dy, 1,
                              (int64_t)rows, (int64_t)cols, ctx->stream, false);
     });
+}
+
+}  // extern "C"
+
+// ---- decode-step ops (decode.hip): MetalOps::encode_rms_norm_f16w,
+// encode_rope_half_f32, encode_add_f32_inplace and MetalKvStorage's
+// encode_write_token_f32 / encode_attention (metal.rs, kvcache.rs) ---------
+
+namespace {
+
+int32_t check_paged(int64_t rows, int64_t max_blocks, int64_t total_blocks, int64_t n_layers, int64_t tpb,
+                    int64_t layer)
+{
+    if (rows < 0 || rows > 4096 || max_blocks < 1 || total_blocks < 1 || n_layers < 1 || tpb < 1 || layer < 0 ||
+        layer >= n_layers || max_blocks * tpb > INT32_MAX || total_blocks * n_layers * tpb > ((int64_t)1 << 40))
+        return set_error(CELLM_HIP_ERR_INVALID_ARG,
+                         "bad paged-cache geometry rows=%lld max_blocks=%lld total_blocks=%lld layers=%lld tpb=%lld "
+                         "layer=%lld",
+                         (long long)rows, (long long)max_blocks, (long long)total_blocks, (long long)n_layers,
+                         (long long)tpb, (long long)layer);
+    return CELLM_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t cellm_hip_embed_i8(cellm_hip_ctx_t* ctx, const uint32_t* tokens, int64_t rows, const int8_t* embed_i8,
+                           const uint16_t* scales_f16, int64_t vocab, int64_t hidden, float* out, void* stream)
+{
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    if (int32_t rc = check_dims(rows, vocab, hidden)) return rc;
+    if (rows == 0 || hidden == 0) return CELLM_HIP_OK;
+    if (vocab < 1) return set_error(CELLM_HIP_ERR_INVALID_ARG, "vocab must be >= 1");
+    if (!tokens || !embed_i8 || !scales_f16 || !out) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null pointer");
+    DeviceGuard g(ctx->device);
+    HIP_TRY(launch_embed_i8(tokens, (int)rows, embed_i8, scales_f16, (int)vocab, (int)hidden, out,
+                            pick_stream(ctx, stream)),
+            "embed_i8 launch");
+    return CELLM_HIP_OK;
+}
+
+int32_t cellm_hip_rms_norm(cellm_hip_ctx_t* ctx, const float* x, const void* weight, int32_t weight_dtype,
+                           int64_t rows, int64_t n, float eps, float* out, void* stream)
+{
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    if (int32_t rc = check_dims(rows, n, 1)) return rc;
+    if (!valid_dtype(weight_dtype)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "bad dtype");
+    if (rows == 0 || n == 0) return CELLM_HIP_OK;
+    if (!x || !weight || !out) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null pointer");
+    DeviceGuard g(ctx->device);
+    HIP_TRY(launch_rms_norm(x, weight, weight_dtype, (int)rows, (int)n, eps, out, pick_stream(ctx, stream)),
+            "rms_norm launch");
+    return CELLM_HIP_OK;
+}
+
+int32_t cellm_hip_add_rms_norm(cellm_hip_ctx_t* ctx, float* x, const float* y, const void* weight,
+                               int32_t weight_dtype, int64_t rows, int64_t n, float eps, float* out, void* stream)
+{
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    if (int32_t rc = check_dims(rows, n, 1)) return rc;
+    if (!valid_dtype(weight_dtype)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "bad dtype");
+    if (rows == 0 || n == 0) return CELLM_HIP_OK;
+    if (!x || !y || !weight || !out) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null pointer");
+    DeviceGuard g(ctx->device);
+    HIP_TRY(launch_add_rms_norm(x, y, weight, weight_dtype, (int)rows, (int)n, eps, out, pick_stream(ctx, stream)),
+            "add_rms_norm launch");
+    return CELLM_HIP_OK;
+}
+
+int32_t cellm_hip_rope_half_f32(cellm_hip_ctx_t* ctx, float* x, int64_t rows, int64_t n_heads, int64_t head_dim,
+                                const int32_t* positions, const float* cos_sin, int64_t table_positions, void* stream)
+{
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    if (int32_t rc = check_dims(rows, n_heads, head_dim)) return rc;
+    if (rows == 0 || n_heads == 0 || head_dim == 0) return CELLM_HIP_OK;
+    if (head_dim % 2 != 0) return set_error(CELLM_HIP_ERR_INVALID_ARG, "head_dim must be even");
+    if (table_positions < 1 || table_positions > INT32_MAX)
+        return set_error(CELLM_HIP_ERR_INVALID_ARG, "table_positions must be >= 1");
+    if (rows * n_heads * head_dim > INT32_MAX) return set_error(CELLM_HIP_ERR_INVALID_ARG, "tensor too large");
+    if (!x || !positions || !cos_sin) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null pointer");
+    DeviceGuard g(ctx->device);
+    HIP_TRY(launch_rope_half(x, (int)rows, (int)n_heads, (int)head_dim, positions, cos_sin, (int)table_positions,
+                             pick_stream(ctx, stream)),
+            "rope_half launch");
+    return CELLM_HIP_OK;
+}
+
+int32_t cellm_hip_kv_write_f16(cellm_hip_ctx_t* ctx, const float* k, const float* v, int64_t rows, int64_t kv_dim,
+                               const int32_t* positions, uint16_t* kcache, uint16_t* vcache,
+                               const uint32_t* block_tables, int64_t max_blocks, int64_t total_blocks,
+                               int64_t n_layers, int64_t tokens_per_block, int64_t layer, void* stream)
+{
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    if (int32_t rc = check_paged(rows, max_blocks, total_blocks, n_layers, tokens_per_block, layer)) return rc;
+    if (kv_dim < 1 || rows * kv_dim > INT32_MAX) return set_error(CELLM_HIP_ERR_INVALID_ARG, "bad kv_dim");
+    if (rows == 0) return CELLM_HIP_OK;
+    if (!k || !v || !positions || !kcache || !vcache || !block_tables)
+        return set_error(CELLM_HIP_ERR_INVALID_ARG, "null pointer");
+    DeviceGuard g(ctx->device);
+    HIP_TRY(launch_kv_write_f16(k, v, (int)rows, (int)kv_dim, positions, kcache, vcache, block_tables, (int)max_blocks,
+                                (int)total_blocks, (int)n_layers, (int)tokens_per_block, (int)layer,
+                                pick_stream(ctx, stream)),
+            "kv_write launch");
+    return CELLM_HIP_OK;
+}
+
+int32_t cellm_hip_rope_kv_write_f16(cellm_hip_ctx_t* ctx, float* q, float* k, const float* v, int64_t rows,
+                                    int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, const int32_t* positions,
+                                    const float* cos_sin, int64_t table_positions, uint16_t* kcache, uint16_t* vcache,
+                                    const uint32_t* block_tables, int64_t max_blocks, int64_t total_blocks,
+                                    int64_t n_layers, int64_t tokens_per_block, int64_t layer, void* stream)
+{
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    if (int32_t rc = check_paged(rows, max_blocks, total_blocks, n_layers, tokens_per_block, layer)) return rc;
+    if (n_heads < 1 || n_kv_heads < 1 || head_dim < 2 || head_dim % 2 != 0 ||
+        rows * (n_heads + n_kv_heads) * head_dim > INT32_MAX)
+        return set_error(CELLM_HIP_ERR_INVALID_ARG, "bad head geometry %lld/%lld/%lld", (long long)n_heads,
+                         (long long)n_kv_heads, (long long)head_dim);
+    if (table_positions < 1 || table_positions > INT32_MAX)
+        return set_error(CELLM_HIP_ERR_INVALID_ARG, "table_positions must be >= 1");
+    if (rows == 0) return CELLM_HIP_OK;
+    if (!q || !k || !v || !positions || !cos_sin || !kcache || !vcache || !block_tables)
+        return set_error(CELLM_HIP_ERR_INVALID_ARG, "null pointer");
+    DeviceGuard g(ctx->device);
+    HIP_TRY(launch_rope_kv_write_f16(q, k, v, (int)rows, (int)n_heads, (int)n_kv_heads, (int)head_dim, positions,
+                                     cos_sin, (int)table_positions, kcache, vcache, block_tables, (int)max_blocks,
+                                     (int)total_blocks, (int)n_layers, (int)tokens_per_block, (int)layer,
+                                     pick_stream(ctx, stream)),
+            "rope_kv_write launch");
+    return CELLM_HIP_OK;
+}
+
+int32_t cellm_hip_attention_gqa_f16kv(cellm_hip_ctx_t* ctx, const float* q, const uint16_t* kcache,
+                                      const uint16_t* vcache, const uint32_t* block_tables, int64_t max_blocks,
+                                      int64_t total_blocks, const int32_t* positions, int64_t rows, int64_t n_heads,
+                                      int64_t n_kv_heads, int64_t head_dim, int64_t n_layers, int64_t tokens_per_block,
+                                      int64_t layer, float* out, void* stream)
+{
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    if (int32_t rc = check_paged(rows, max_blocks, total_blocks, n_layers, tokens_per_block, layer)) return rc;
+    if (n_heads < 1 || n_kv_heads < 1 || head_dim < 1 || n_heads > 4096 ||
+        !attention_supported((int)n_heads, (int)n_kv_heads, (int)head_dim, (int)(max_blocks * tokens_per_block)))
+        return set_error(CELLM_HIP_ERR_UNSUPPORTED,
+                         "attention needs n_heads %% n_kv_heads == 0, <= 8 query heads per kv head, head_dim 64 or "
+                         "128 and max_blocks * tokens_per_block <= 32768 (got %lld/%lld/%lld, %lld positions)",
+                         (long long)n_heads, (long long)n_kv_heads, (long long)head_dim,
+                         (long long)(max_blocks * tokens_per_block));
+    if (rows == 0) return CELLM_HIP_OK;
+    if (!q || !kcache || !vcache || !block_tables || !positions || !out)
+        return set_error(CELLM_HIP_ERR_INVALID_ARG, "null pointer");
+    if (!aligned16(kcache) || !aligned16(vcache)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "K/V must be 16-byte aligned");
+    DeviceGuard g(ctx->device);
+    const hipStream_t st = pick_stream(ctx, stream);
+    float* ws = nullptr;
+    const size_t need = attention_workspace_bytes((int)rows, (int)n_heads, (int)n_kv_heads, (int)head_dim,
+                                                  (int)(max_blocks * tokens_per_block));
+    if (int32_t rc = get_stream_buffer(ctx, ctx->attn, st, need, &ws)) return rc;
+    HIP_TRY(launch_attention_gqa_f16kv(q, kcache, vcache, block_tables, (int)max_blocks, (int)total_blocks, positions,
+                                       (int)rows, (int)n_heads, (int)n_kv_heads, (int)head_dim, (int)n_layers,
+                                       (int)tokens_per_block, (int)layer, out, ws, st),
+            "attention launch");
+    return CELLM_HIP_OK;
+}
+
+int32_t cellm_hip_add_f32_inplace(cellm_hip_ctx_t* ctx, float* x, const float* y, int64_t n, void* stream)
+{
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    if (n < 0 || n > INT32_MAX) return set_error(CELLM_HIP_ERR_INVALID_ARG, "bad length");
+    if (n == 0) return CELLM_HIP_OK;
+    if (!x || !y) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null pointer");
+    DeviceGuard g(ctx->device);
+    HIP_TRY(launch_add_f32(x, y, x, (int)n, pick_stream(ctx, stream)), "add launch");
+    return CELLM_HIP_OK;
+}
+
+int32_t cellm_hip_argmax_f32(cellm_hip_ctx_t* ctx, const float* logits, int64_t rows, int64_t n, int32_t* out_index,
+                             float* out_value, void* stream)
+{
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    if (int32_t rc = check_dims(rows, n, 1)) return rc;
+    if (rows == 0) return CELLM_HIP_OK;
+    if (n == 0) return set_error(CELLM_HIP_ERR_INVALID_ARG, "empty logits");
+    if (!logits || !out_index || !out_value) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null pointer");
+    DeviceGuard g(ctx->device);
+    HIP_TRY(launch_argmax(logits, (int)rows, (int)n, out_index, out_value, pick_stream(ctx, stream)), "argmax launch");
+    return CELLM_HIP_OK;
 }
 
 }  // extern "C"

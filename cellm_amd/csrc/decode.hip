@@ -1,0 +1,588 @@
+// Decode-step kernels around the projections (gfx950): the device side of a
+// Llama decode step, as the reference's fused Metal graph encodes it
+// (crates/cellm-model/src/llama_graph.rs:140-405).  Every kernel takes `rows`
+// independent sessions (one activation row each) so that a step for several
+// sessions reads every projection weight once.
+//
+//   embed_i8       x = f32(E[tok % vocab]) * f32(scale)        llama.rs:676-701
+//   rms_norm       out = x * (1/sqrt(mean(x^2)+eps)) * w        cpu_kernels.rs:17-34
+//   add_rms_norm   x += y (residual, llama.rs:440,494), then rms_norm
+//   rope_half      rotate-half RoPE from a cos/sin table        cpu_kernels.rs:264-277
+//   kv_write_f16   f32 -> f16 (RNE) into the paged cache        kvcache.rs:589-615
+//   rope_kv_write  rope_half on q and k, then kv_write_f16, in one launch
+//   attention      single-token GQA over f16 K/V pages          kvcache.rs:710-789
+//   argmax         first maximum, non-finite -> -inf            llama.rs:1049-1092
+//
+// Where the reference rounds a product and a sum separately, so do these
+// kernels: FP contraction is off for this file (hipcc contracts a*b+c into
+// an FMA by default; HIP's __fmul_rn is an inline a*b from a header outside
+// this pragma, so it would still be fused: plain operators are used here).
+// Sums over a vector are tree-shaped here and sequential there; softmax uses
+// the device expf.
+// Paged addressing is KvCacheLayout::token_base_elem
+// (crates/cellm-core/src/kv_cache.rs:62-73):
+//   base(t, layer) = block[t / tpb] * (L * tpb * kvd) + layer * (tpb * kvd) + (t % tpb) * kvd
+#include <algorithm>
+#include <cmath>
+#include <type_traits>
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+#pragma clang fp contract(off)
+
+namespace cellm {
+
+namespace {
+
+constexpr int kNormThreads = 256;
+constexpr int kAttnChunk = 64;        // positions per partial-attention block
+constexpr int kAttnThreads = 256;
+constexpr int kAttnGMax = 8;          // query heads per kv head
+constexpr int kAttnMaxChunks = 512;   // positions per sequence <= 32768
+
+__device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+__global__ void embed_i8_kernel(const uint32_t* __restrict__ tokens, const int8_t* __restrict__ emb,
+                                const uint16_t* __restrict__ scale, int vocab, int hidden, float* __restrict__ x)
+{
+    const int r = blockIdx.y;
+    const size_t t = tokens[r] % (uint32_t)vocab;
+    const float s = h2f(scale[t]);
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < hidden; i += gridDim.x * blockDim.x)
+        x[(size_t)r * hidden + i] = (float)emb[t * hidden + i] * s;
+}
+
+template <int WDT>
+__global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const float* __restrict__ x, const void* __restrict__ w,
+                                                               float* __restrict__ out, int n, float eps)
+{
+    __shared__ float part[kNormThreads / 64];
+    const int r = blockIdx.x;
+    const float* xr = x + (size_t)r * n;
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < n; i += kNormThreads) s = s + xr[i] * xr[i];
+    s = group_sum<64>(s);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kNormThreads / 64; ++i) tot = tot + part[i];
+    const float mean = tot / (float)n;
+    const float inv = 1.0f / sqrtf(mean + eps);
+    for (int i = threadIdx.x; i < n; i += kNormThreads)
+        out[(size_t)r * n + i] = xr[i] * inv * load_f32<WDT>(w, i);
+}
+
+// x += y, then out = rms_norm(x) * w: the residual add of the previous
+// sub-layer and the next RMSNorm in one pass; per element the same
+// arithmetic, and the same reduction tree, as add_f32 followed by rms_norm.
+template <int WDT>
+__global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(float* __restrict__ x, const float* __restrict__ y,
+                                                                   const void* __restrict__ w, float* __restrict__ out,
+                                                                   int n, float eps)
+{
+    __shared__ float part[kNormThreads / 64];
+    const int r = blockIdx.x;
+    float* xr = x + (size_t)r * n;
+    const float* yr = y + (size_t)r * n;
+    float s = 0.0f;
+    for (int i = threadIdx.x; i < n; i += kNormThreads) {
+        const float v = xr[i] + yr[i];
+        xr[i] = v;
+        s = s + v * v;
+    }
+    s = group_sum<64>(s);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kNormThreads / 64; ++i) tot = tot + part[i];
+    const float mean = tot / (float)n;
+    const float inv = 1.0f / sqrtf(mean + eps);
+    for (int i = threadIdx.x; i < n; i += kNormThreads)
+        out[(size_t)r * n + i] = xr[i] * inv * load_f32<WDT>(w, i);
+}
+
+// One thread per (row, head, i < half).  cs[p][i] = (cos, sin) of position p.
+__global__ void rope_half_kernel(float* __restrict__ x, int rows, int n_heads, int head_dim,
+                                 const int32_t* __restrict__ pos, const float2* __restrict__ cs, int table_positions)
+{
+    const int half = head_dim >> 1;
+    const int total = rows * n_heads * half;
+    for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += gridDim.x * blockDim.x) {
+        const int i = idx % half, rh = idx / half;
+        const int r = rh / n_heads;
+        const int p = min(max(pos[r], 0), table_positions - 1);
+        const float2 c = cs[(size_t)p * half + i];
+        float* head = x + (size_t)rh * head_dim;
+        const float x0 = head[i], x1 = head[half + i];
+        head[i] = x0 * c.x - x1 * c.y;
+        head[half + i] = x1 * c.x + x0 * c.y;
+    }
+}
+
+struct PagedKv {
+    const uint32_t* bt;  // [rows][max_blocks]
+    int max_blocks, total_blocks, n_layers, tpb, kvd;
+
+    // element base of (row, token t) in `layer`, or -1 when the page is out of range
+    __device__ __forceinline__ long long base(int r, int t, int layer) const
+    {
+        const int b = t / tpb;
+        if (b >= max_blocks) return -1;
+        const uint32_t blk = bt[(size_t)r * max_blocks + b];
+        if (blk >= (uint32_t)total_blocks) return -1;
+        return ((long long)blk * n_layers + layer) * (long long)tpb * kvd + (long long)(t % tpb) * kvd;
+    }
+};
+
+__global__ void kv_write_kernel(const float* __restrict__ k, const float* __restrict__ v, int rows,
+                                const int32_t* __restrict__ pos, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
+                                PagedKv kv, int layer)
+{
+    const int total = rows * kv.kvd;
+    for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += gridDim.x * blockDim.x) {
+        const int r = idx / kv.kvd, j = idx - r * kv.kvd;
+        const long long b = pos[r] >= 0 ? kv.base(r, pos[r], layer) : -1;
+        if (b < 0) continue;
+        kc[b + j] = __builtin_bit_cast(uint16_t, (_Float16)k[idx]);
+        vc[b + j] = __builtin_bit_cast(uint16_t, (_Float16)v[idx]);
+    }
+}
+
+// RoPE on q and k, then k and v into the paged cache as f16: the same
+// arithmetic as rope_half on q and on k followed by kv_write_f16, in one
+// launch.  Work item (row, j): j < n_heads * half rotates the q pair
+// (i, i + half) of head j / half; the rest rotate the k pair of one kv head,
+// write it back to k, and store that pair of k and of v in the cache.
+__global__ void rope_kv_write_kernel(float* __restrict__ q, float* __restrict__ k, const float* __restrict__ v,
+                                     int rows, int n_heads, int n_kv_heads, int head_dim,
+                                     const int32_t* __restrict__ pos, const float2* __restrict__ cs,
+                                     int table_positions, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
+                                     PagedKv kv, int layer)
+{
+    const int half = head_dim >> 1;
+    const int nq = n_heads * half, per_row = nq + n_kv_heads * half;
+    const int total = rows * per_row;
+    for (int idx = blockIdx.x * blockDim.x + threadIdx.x; idx < total; idx += gridDim.x * blockDim.x) {
+        const int r = idx / per_row, j = idx - r * per_row;
+        const int p = min(max(pos[r], 0), table_positions - 1);
+        if (j < nq) {
+            const int i = j % half;
+            const float2 c = cs[(size_t)p * half + i];
+            float* head = q + ((size_t)r * n_heads + j / half) * head_dim;
+            const float x0 = head[i], x1 = head[half + i];
+            head[i] = x0 * c.x - x1 * c.y;
+            head[half + i] = x1 * c.x + x0 * c.y;
+        } else {
+            const int jk = j - nq, kh = jk / half, i = jk % half;
+            const float2 c = cs[(size_t)p * half + i];
+            const size_t off = ((size_t)r * n_kv_heads + kh) * head_dim;
+            const float x0 = k[off + i], x1 = k[off + half + i];
+            const float k0 = x0 * c.x - x1 * c.y;
+            const float k1 = x1 * c.x + x0 * c.y;
+            k[off + i] = k0;
+            k[off + half + i] = k1;
+            const long long b = pos[r] >= 0 ? kv.base(r, pos[r], layer) : -1;
+            if (b < 0) continue;
+            const size_t e = (size_t)b + (size_t)kh * head_dim;
+            kc[e + i] = __builtin_bit_cast(uint16_t, (_Float16)k0);
+            kc[e + half + i] = __builtin_bit_cast(uint16_t, (_Float16)k1);
+            vc[e + i] = __builtin_bit_cast(uint16_t, (_Float16)v[off + i]);
+            vc[e + half + i] = __builtin_bit_cast(uint16_t, (_Float16)v[off + half + i]);
+        }
+    }
+}
+
+// Partial attention over positions [64c, 64c+64) for one (row, kv head) and
+// its G query heads; part layout [row][kvh][chunk][G][HD + 2]: HD weighted-V
+// sums, the chunk max and the chunk sum of exp(score - max).  Every K and V
+// load of the chunk is issued before any arithmetic (one memory latency):
+//   Q.K: thread t -> position t / 4, dims (t % 4) * HD/4 .. + HD/4 (16-B loads)
+//   P.V: thread t -> dims (t % 64) * HD/64 .. + HD/64, positions 16 (t / 64) .. + 16
+// so wave w owns positions 16w .. 16w + 15 in both phases.
+template <int HD, int G>
+__global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
+    const float* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
+    const int32_t* __restrict__ pos, PagedKv kv, int layer, int n_kv_heads, float scale, float* __restrict__ part,
+    int nch_max)
+{
+    constexpr int KD = HD / 4;                             // Q.K dims per thread
+    constexpr int KL = KD / 8;                             // 16-byte K loads per thread
+    constexpr int VD = HD / 64;                            // P.V dims per thread (1 or 2)
+    constexpr int VP = kAttnChunk / 4;                     // P.V positions per thread
+    constexpr int QL = (G * HD + kAttnThreads - 1) / kAttnThreads;  // q elements per thread
+    using vword_t = typename std::conditional<VD == 1, uint16_t, uint32_t>::type;
+    const int n_heads = G * n_kv_heads;
+    __shared__ float qs[G * HD];
+    __shared__ float ps[G][kAttnChunk];
+    __shared__ long long bases[kAttnChunk];
+    __shared__ float wmax[4][G], wsum[4][G];
+    __shared__ float accs[4][G * HD];
+    const int r = blockIdx.x / n_kv_heads, kvh = blockIdx.x % n_kv_heads, ch = blockIdx.y;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int t0 = ch * kAttnChunk;
+    // position, q and this chunk's page entries: independent loads, issued together
+    // (addresses clamped in range so that no load sits behind a branch)
+    const int p_r = pos[r];
+    const float* qr = q + ((size_t)r * n_heads + (size_t)kvh * G) * HD;
+    float qv[QL];
+#pragma unroll
+    for (int j = 0; j < QL; ++j) qv[j] = qr[min(t + j * kAttnThreads, G * HD - 1)];
+    const int tt = t0 + lane, blk_i = tt / kv.tpb;
+    const uint32_t blk = kv.bt[(size_t)r * kv.max_blocks + min(blk_i, kv.max_blocks - 1)];
+    const int seq = min(p_r + 1, kv.max_blocks * kv.tpb);
+    if (t0 >= seq) return;  // the same for the whole block
+    const int nt = min(kAttnChunk, seq - t0);
+#pragma unroll
+    for (int j = 0; j < QL; ++j)
+        if (t + j * kAttnThreads < G * HD) qs[t + j * kAttnThreads] = qv[j];
+    if (t < kAttnChunk)
+        bases[t] = (t < nt && blk_i < kv.max_blocks && blk < (uint32_t)kv.total_blocks)
+                       ? ((long long)blk * kv.n_layers + layer) * (long long)kv.tpb * kv.kvd +
+                             (long long)(tt % kv.tpb) * kv.kvd
+                       : -1;
+    __syncthreads();
+
+    // every K and V load of the chunk (a missing page reads element 0 and is zeroed)
+    const int kp = t >> 2, kq = t & 3;
+    const long long kb = bases[kp];
+    const u4_t* ksrc = reinterpret_cast<const u4_t*>(kc + (kb >= 0 ? kb + (long long)kvh * HD + kq * KD : 0));
+    u4_t kraw[KL];
+#pragma unroll
+    for (int j = 0; j < KL; ++j) kraw[j] = ksrc[j];
+    vword_t vraw[VP];
+    bool vok[VP];
+#pragma unroll
+    for (int i = 0; i < VP; ++i) {
+        const long long vb = bases[wave * VP + i];
+        vok[i] = vb >= 0;
+        vraw[i] = *reinterpret_cast<const vword_t*>(vc + (vb >= 0 ? vb + (long long)kvh * HD + lane * VD : 0));
+    }
+    if (kb < 0) {
+#pragma unroll
+        for (int j = 0; j < KL; ++j) kraw[j] = u4_t{0, 0, 0, 0};
+    }
+
+    // scores: a partial dot over this thread's dims, summed over the 4 threads of the position
+    float dot[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) dot[g] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < KL; ++j) {
+        const h8_t kh = __builtin_bit_cast(h8_t, kraw[j]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float kf = (float)kh[e];
+            const int d = kq * KD + j * 8 + e;
+#pragma unroll
+            for (int g = 0; g < G; ++g) dot[g] = dot[g] + qs[g * HD + d] * kf;
+        }
+    }
+    const bool valid = kp < nt;
+    float sc[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        float d = dot[g];
+        d = d + __shfl_xor(d, 1);
+        d = d + __shfl_xor(d, 2);
+        sc[g] = valid ? d * scale : -INFINITY;
+        float m = sc[g];
+        m = fmaxf(m, __shfl_xor(m, 4));
+        m = fmaxf(m, __shfl_xor(m, 8));
+        m = fmaxf(m, __shfl_xor(m, 16));
+        m = fmaxf(m, __shfl_xor(m, 32));
+        if (lane == 0) wmax[wave][g] = m;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const float m = fmaxf(fmaxf(wmax[0][g], wmax[1][g]), fmaxf(wmax[2][g], wmax[3][g]));
+        const float e = valid ? expf(sc[g] - m) : 0.0f;
+        if (kq == 0) ps[g][kp] = e;
+        float l = e;
+        l = l + __shfl_xor(l, 4);
+        l = l + __shfl_xor(l, 8);
+        l = l + __shfl_xor(l, 16);
+        l = l + __shfl_xor(l, 32);
+        if (lane == 0) wsum[wave][g] = l;
+    }
+    __syncthreads();
+
+    // weighted V over this wave's 16 positions, then over the 4 waves
+    float acc[G][VD];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int d = 0; d < VD; ++d) acc[g][d] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VP; ++i) {
+        const vword_t w = vok[i] ? vraw[i] : vword_t(0);
+        float vf[VD];
+        if constexpr (VD == 1) {
+            vf[0] = h2f(w);
+        } else {
+            vf[0] = h2f((uint16_t)(w & 0xffffu));
+            vf[1] = h2f((uint16_t)(w >> 16));
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+                const float pg = ps[g][wave * VP + i];
+#pragma unroll
+            for (int d = 0; d < VD; ++d) acc[g][d] = acc[g][d] + pg * vf[d];
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+        for (int d = 0; d < VD; ++d) accs[wave][g * HD + lane * VD + d] = acc[g][d];
+    }
+    __syncthreads();
+    float* out = part + ((((size_t)r * n_kv_heads + kvh) * nch_max + ch) * G) * (HD + 2);
+    for (int i = t; i < G * HD; i += kAttnThreads)
+        out[(size_t)(i / HD) * (HD + 2) + i % HD] = (accs[0][i] + accs[1][i]) + (accs[2][i] + accs[3][i]);
+    if (t < G) {
+        out[(size_t)t * (HD + 2) + HD] = fmaxf(fmaxf(wmax[0][t], wmax[1][t]), fmaxf(wmax[2][t], wmax[3][t]));
+        out[(size_t)t * (HD + 2) + HD + 1] = (wsum[0][t] + wsum[1][t]) + (wsum[2][t] + wsum[3][t]);
+    }
+}
+
+// One block per (row, kv head): its G query heads.
+//   out[h][i] = (sum_c acc_c[i] e^(m_c - M)) / (sum_c l_c e^(m_c - M)),  M = max_c m_c
+// The chunk maxima and sums go to LDS, together with each thread's first
+// kCombinePre partials of its first output (one memory latency for up to
+// kCombinePre chunks); wave w then weighs the chunks of heads w and w + 4.
+template <int HD, int G>
+__global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(const float* __restrict__ part,
+                                                                   const int32_t* __restrict__ pos, PagedKv kv,
+                                                                   int n_kv_heads, int nch_max,
+                                                                   float* __restrict__ out)
+{
+    constexpr int kCombinePre = 16;
+    const int n_heads = G * n_kv_heads;
+    __shared__ float cm[G][kAttnMaxChunks];  // chunk maxima, then the weights e^(m_c - M)
+    __shared__ float cl[G][kAttnMaxChunks];  // chunk exp-sums
+    __shared__ float invl[G];
+    const int r = blockIdx.x / n_kv_heads, kvh = blockIdx.x % n_kv_heads;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int seq = min(pos[r] + 1, kv.max_blocks * kv.tpb);
+    const int nch = seq > 0 ? (seq + kAttnChunk - 1) / kAttnChunk : 0;
+    if (nch == 0) return;
+    const size_t cstride = (size_t)G * (HD + 2);
+    const float* p = part + ((size_t)r * n_kv_heads + kvh) * nch_max * cstride;
+    // this thread's first output and its first partials
+    const int i0 = min(t, G * HD - 1);
+    const float* pc0 = p + (size_t)(i0 / HD) * (HD + 2) + i0 % HD;
+    float pre[kCombinePre];
+#pragma unroll
+    for (int c = 0; c < kCombinePre; ++c) pre[c] = pc0[(size_t)min(c, nch - 1) * cstride];
+    for (int j = t; j < G * nch; j += kAttnThreads) {
+        const int g = j % G, c = j / G;
+        cm[g][c] = p[c * cstride + (size_t)g * (HD + 2) + HD];
+        cl[g][c] = p[c * cstride + (size_t)g * (HD + 2) + HD + 1];
+    }
+    __syncthreads();
+    for (int g = wave; g < G; g += 4) {
+        float m = -INFINITY;
+        for (int c = lane; c < nch; c += 64) m = fmaxf(m, cm[g][c]);
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+        float l = 0.0f;
+        for (int c = lane; c < nch; c += 64) {
+            const float w = expf(cm[g][c] - m);
+            cm[g][c] = w;
+            l = l + cl[g][c] * w;
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) l = l + __shfl_xor(l, off);
+        if (lane == 0) invl[g] = l > 0.0f ? 1.0f / l : 0.0f;
+    }
+    __syncthreads();
+    for (int i = t; i < G * HD; i += kAttnThreads) {
+        const int g = i / HD, d = i % HD;
+        const float* pc = p + (size_t)g * (HD + 2) + d;
+        float acc = 0.0f;
+        int c = 0;
+        if (i == t) {
+#pragma unroll
+            for (; c < kCombinePre; ++c)
+                if (c < nch) acc = acc + pre[c] * cm[g][c];
+        }
+#pragma unroll 8
+        for (; c < nch; ++c) acc = acc + pc[c * cstride] * cm[g][c];
+        out[((size_t)r * n_heads + (size_t)kvh * G + g) * HD + d] = acc * invl[g];
+    }
+}
+
+__global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ logits, int n, int32_t* __restrict__ idx,
+                                                     float* __restrict__ val)
+{
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    const int r = blockIdx.x;
+    const float* z = logits + (size_t)r * n;
+    float best = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int i = threadIdx.x; i < n; i += 256) {
+        float v = z[i];
+        if (!isfinite(v)) v = -INFINITY;  // llama.rs:1081-1092
+        if (v > best || bi == 0x7fffffff) {  // strictly greater keeps the first maximum
+            best = v;
+            bi = i;
+        }
+    }
+    // (value, index) max with the lowest index among equal values: the first maximum
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(best, off);
+        const int oi = __shfl_xor(bi, off);
+        if (ov > best || (ov == best && oi < bi)) {
+            best = ov;
+            bi = oi;
+        }
+    }
+    if ((threadIdx.x & 63) == 0) {
+        sv[threadIdx.x >> 6] = best;
+        si[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; ++w)
+            if (sv[w] > best || (sv[w] == best && si[w] < bi)) {
+                best = sv[w];
+                bi = si[w];
+            }
+        idx[r] = bi == 0x7fffffff ? 0 : bi;
+        val[r] = best;
+    }
+}
+
+}  // namespace
+
+hipError_t launch_embed_i8(const uint32_t* tokens, int rows, const int8_t* emb, const uint16_t* scale, int vocab,
+                           int hidden, float* x, hipStream_t st)
+{
+    const dim3 grid((unsigned)std::min((hidden + 255) / 256, 64), (unsigned)rows);
+    hipLaunchKernelGGL(embed_i8_kernel, grid, dim3(256), 0, st, tokens, emb, scale, vocab, hidden, x);
+    return hipGetLastError();
+}
+
+hipError_t launch_rms_norm(const float* x, const void* w, int wdt, int rows, int n, float eps, float* out,
+                           hipStream_t st)
+{
+    if (wdt == DT_F32)
+        hipLaunchKernelGGL((rms_norm_kernel<DT_F32>), dim3(rows), dim3(kNormThreads), 0, st, x, w, out, n, eps);
+    else if (wdt == DT_F16)
+        hipLaunchKernelGGL((rms_norm_kernel<DT_F16>), dim3(rows), dim3(kNormThreads), 0, st, x, w, out, n, eps);
+    else
+        hipLaunchKernelGGL((rms_norm_kernel<DT_BF16>), dim3(rows), dim3(kNormThreads), 0, st, x, w, out, n, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_add_rms_norm(float* x, const float* y, const void* w, int wdt, int rows, int n, float eps,
+                               float* out, hipStream_t st)
+{
+    if (wdt == DT_F32)
+        hipLaunchKernelGGL((add_rms_norm_kernel<DT_F32>), dim3(rows), dim3(kNormThreads), 0, st, x, y, w, out, n, eps);
+    else if (wdt == DT_F16)
+        hipLaunchKernelGGL((add_rms_norm_kernel<DT_F16>), dim3(rows), dim3(kNormThreads), 0, st, x, y, w, out, n, eps);
+    else
+        hipLaunchKernelGGL((add_rms_norm_kernel<DT_BF16>), dim3(rows), dim3(kNormThreads), 0, st, x, y, w, out, n,
+                           eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_kv_write_f16(float* q, float* k, const float* v, int rows, int n_heads, int n_kv_heads,
+                                    int head_dim, const int32_t* pos, const float* cos_sin, int table_positions,
+                                    uint16_t* kcache, uint16_t* vcache, const uint32_t* block_tables, int max_blocks,
+                                    int total_blocks, int n_layers, int tokens_per_block, int layer, hipStream_t st)
+{
+    const PagedKv kv{block_tables, max_blocks, total_blocks, n_layers, tokens_per_block, n_kv_heads * head_dim};
+    const int total = rows * (n_heads + n_kv_heads) * (head_dim / 2);
+    const int blocks = std::max(1, std::min((total + 255) / 256, 1024));
+    hipLaunchKernelGGL(rope_kv_write_kernel, dim3(blocks), dim3(256), 0, st, q, k, v, rows, n_heads, n_kv_heads,
+                       head_dim, pos, reinterpret_cast<const float2*>(cos_sin), table_positions, kcache, vcache, kv,
+                       layer);
+    return hipGetLastError();
+}
+
+hipError_t launch_rope_half(float* x, int rows, int n_heads, int head_dim, const int32_t* pos, const float* cos_sin,
+                            int table_positions, hipStream_t st)
+{
+    const int total = rows * n_heads * (head_dim / 2);
+    const int blocks = std::max(1, std::min((total + 255) / 256, 1024));
+    hipLaunchKernelGGL(rope_half_kernel, dim3(blocks), dim3(256), 0, st, x, rows, n_heads, head_dim, pos,
+                       reinterpret_cast<const float2*>(cos_sin), table_positions);
+    return hipGetLastError();
+}
+
+hipError_t launch_kv_write_f16(const float* k, const float* v, int rows, int kv_dim, const int32_t* pos,
+                               uint16_t* kcache, uint16_t* vcache, const uint32_t* block_tables, int max_blocks,
+                               int total_blocks, int n_layers, int tokens_per_block, int layer, hipStream_t st)
+{
+    const PagedKv kv{block_tables, max_blocks, total_blocks, n_layers, tokens_per_block, kv_dim};
+    const int total = rows * kv_dim;
+    const int blocks = std::max(1, std::min((total + 255) / 256, 1024));
+    hipLaunchKernelGGL(kv_write_kernel, dim3(blocks), dim3(256), 0, st, k, v, rows, pos, kcache, vcache, kv, layer);
+    return hipGetLastError();
+}
+
+bool attention_supported(int n_heads, int n_kv_heads, int head_dim, int max_seq)
+{
+    return n_kv_heads > 0 && n_heads % n_kv_heads == 0 && n_heads / n_kv_heads <= kAttnGMax &&
+           (head_dim == 64 || head_dim == 128) && max_seq >= 1 && max_seq <= kAttnMaxChunks * kAttnChunk;
+}
+
+size_t attention_workspace_bytes(int rows, int n_heads, int n_kv_heads, int head_dim, int max_seq)
+{
+    const int nch = (max_seq + kAttnChunk - 1) / kAttnChunk;
+    return (size_t)rows * n_heads * nch * (head_dim + 2) * sizeof(float);
+}
+
+hipError_t launch_attention_gqa_f16kv(const float* q, const uint16_t* kcache, const uint16_t* vcache,
+                                      const uint32_t* block_tables, int max_blocks, int total_blocks,
+                                      const int32_t* pos, int rows, int n_heads, int n_kv_heads, int head_dim,
+                                      int n_layers, int tokens_per_block, int layer, float* out, float* workspace,
+                                      hipStream_t st)
+{
+    const PagedKv kv{block_tables, max_blocks, total_blocks, n_layers, tokens_per_block, n_kv_heads * head_dim};
+    const int nch = (max_blocks * tokens_per_block + kAttnChunk - 1) / kAttnChunk;
+    if (nch > kAttnMaxChunks) return hipErrorInvalidValue;
+    // scale = 1 / sqrt(head_dim) in f32, as kvcache.rs computes it
+    const float scale = 1.0f / std::sqrt((float)head_dim);
+    const dim3 pgrid((unsigned)(rows * n_kv_heads), (unsigned)nch);
+    const dim3 cgrid((unsigned)(rows * n_kv_heads));
+    const int G = n_heads / n_kv_heads;
+    auto go = [&](auto hd, auto g) {
+        constexpr int HD = decltype(hd)::value, GG = decltype(g)::value;
+        hipLaunchKernelGGL((attn_partial_kernel<HD, GG>), pgrid, dim3(kAttnThreads), 0, st, q, kcache, vcache, pos, kv,
+                           layer, n_kv_heads, scale, workspace, nch);
+        hipLaunchKernelGGL((attn_combine_kernel<HD, GG>), cgrid, dim3(kAttnThreads), 0, st, workspace, pos, kv,
+                           n_kv_heads, nch, out);
+    };
+    auto by_g = [&](auto hd) {
+        switch (G) {
+        case 1: go(hd, std::integral_constant<int, 1>{}); break;
+        case 2: go(hd, std::integral_constant<int, 2>{}); break;
+        case 3: go(hd, std::integral_constant<int, 3>{}); break;
+        case 4: go(hd, std::integral_constant<int, 4>{}); break;
+        case 5: go(hd, std::integral_constant<int, 5>{}); break;
+        case 6: go(hd, std::integral_constant<int, 6>{}); break;
+        case 7: go(hd, std::integral_constant<int, 7>{}); break;
+        default: go(hd, std::integral_constant<int, 8>{}); break;
+        }
+    };
+    if (head_dim == 64)
+        by_g(std::integral_constant<int, 64>{});
+    else
+        by_g(std::integral_constant<int, 128>{});
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax(const float* logits, int rows, int n, int32_t* idx, float* val, hipStream_t st)
+{
+    hipLaunchKernelGGL(argmax_kernel, dim3(rows), dim3(256), 0, st, logits, n, idx, val);
+    return hipGetLastError();
+}
+
+}  // namespace cellm

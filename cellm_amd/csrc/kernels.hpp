@@ -66,6 +66,33 @@ hipError_t launch_qgemv_mfma_i8(const int8_t* w, const void* S, int sdt, int per
 hipError_t launch_qgemv_mfma_q4(const uint32_t* wq, const void* S, const void* B, int sbt, int group_size,
                                 const _Float16* x, float* y, int M, int N, int K, hipStream_t st);
 
+// Decode-step kernels (decode.hip).  `rows` sessions, one activation row each;
+// positions and block tables are device arrays ([rows] int32, [rows][max_blocks]
+// uint32); K/V caches are f16 pages laid out as KvCacheLayout::token_base_elem.
+hipError_t launch_embed_i8(const uint32_t* tokens, int rows, const int8_t* emb, const uint16_t* scale, int vocab,
+                           int hidden, float* x, hipStream_t st);
+hipError_t launch_rms_norm(const float* x, const void* w, int wdt, int rows, int n, float eps, float* out,
+                           hipStream_t st);
+hipError_t launch_add_rms_norm(float* x, const float* y, const void* w, int wdt, int rows, int n, float eps,
+                               float* out, hipStream_t st);
+hipError_t launch_rope_kv_write_f16(float* q, float* k, const float* v, int rows, int n_heads, int n_kv_heads,
+                                    int head_dim, const int32_t* pos, const float* cos_sin, int table_positions,
+                                    uint16_t* kcache, uint16_t* vcache, const uint32_t* block_tables, int max_blocks,
+                                    int total_blocks, int n_layers, int tokens_per_block, int layer, hipStream_t st);
+hipError_t launch_rope_half(float* x, int rows, int n_heads, int head_dim, const int32_t* pos, const float* cos_sin,
+                            int table_positions, hipStream_t st);
+hipError_t launch_kv_write_f16(const float* k, const float* v, int rows, int kv_dim, const int32_t* pos,
+                               uint16_t* kcache, uint16_t* vcache, const uint32_t* block_tables, int max_blocks,
+                               int total_blocks, int n_layers, int tokens_per_block, int layer, hipStream_t st);
+bool attention_supported(int n_heads, int n_kv_heads, int head_dim, int max_seq);
+size_t attention_workspace_bytes(int rows, int n_heads, int n_kv_heads, int head_dim, int max_seq);
+hipError_t launch_attention_gqa_f16kv(const float* q, const uint16_t* kcache, const uint16_t* vcache,
+                                      const uint32_t* block_tables, int max_blocks, int total_blocks,
+                                      const int32_t* pos, int rows, int n_heads, int n_kv_heads, int head_dim,
+                                      int n_layers, int tokens_per_block, int layer, float* out, float* workspace,
+                                      hipStream_t st);
+hipError_t launch_argmax(const float* logits, int rows, int n, int32_t* idx, float* val, hipStream_t st);
+
 // Device smoke test kernel: out[i] = a[i] + b[i].
 hipError_t launch_add_f32(const float* a, const float* b, float* out, int n, hipStream_t st);
 

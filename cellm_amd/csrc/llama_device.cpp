@@ -1,0 +1,497 @@
+// Device-resident Llama decode step over libcellm_hip.so (declared in
+// include/cellm_llama_step.h): the HIP counterpart of the fused Metal decode
+// graph LlamaGraphState::step_fused (crates/cellm-model/src/llama_graph.rs:140-405).
+// Weights are uploaded once into the context's name-keyed weight cache
+// (preload_weight, llama_graph.rs:92-99); the paged f16 K/V cache, the RoPE
+// table and the activations live on the device; a step is one stream of
+// launches through the C ABI and one small copy back.
+//
+// Unlike the reference, which decodes sessions one at a time
+// (crates/cellm-sdk/src/lib.rs:581-599), a step takes up to max_rows sessions
+// at once: every projection runs as one GEMV over all their activation rows,
+// so each weight byte is read once per step, not once per session.
+//
+// The host parts (validation, the RoPE cos/sin table) are compiled without FP
+// contraction so the table holds exactly the f32 values the CPU reference
+// computes (cpu_kernels.rs:264-277).
+#include <hip/hip_runtime_api.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/cellm_hip.h"
+#include "../../include/cellm_llama_step.h"
+
+namespace cellm_step {
+extern thread_local std::string g_err;  // llama_step.cpp: read by cellm_llama_last_error_message
+}
+
+namespace {
+
+using cellm_step::g_err;
+
+int32_t fail(int32_t code, const char* fmt, ...)
+{
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int32_t from_hip_lib(int32_t rc, const char* what)
+{
+    char buf[512];
+    cellm_hip_last_error_message(buf, sizeof(buf));
+    return fail(rc, "%s: %s", what, buf);
+}
+
+int32_t from_runtime(hipError_t e, const char* what)
+{
+    return fail(e == hipErrorOutOfMemory ? CELLM_HIP_ERR_OUT_OF_MEMORY : CELLM_HIP_ERR_DEVICE, "%s: %s", what,
+                hipGetErrorString(e));
+}
+
+#define RT_TRY(expr, what)                                 \
+    do {                                                   \
+        hipError_t e_ = (expr);                            \
+        if (e_ != hipSuccess) return from_runtime(e_, what); \
+    } while (0)
+#define LIB_TRY(expr, what)                          \
+    do {                                             \
+        int32_t rc_ = (expr);                        \
+        if (rc_ != CELLM_HIP_OK) return from_hip_lib(rc_, what); \
+    } while (0)
+
+const char* kNames[7] = {"self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
+                         "mlp.gate_proj",    "mlp.up_proj",      "mlp.down_proj"};
+
+// f16::from_bits(h).to_f32() (exact)
+float h2f(uint16_t h)
+{
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    const uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+    uint32_t u;
+    if (e == 0) {
+        if (m == 0) {
+            u = sign;
+        } else {
+            const float v = (float)m * 5.9604644775390625e-08f;
+            return sign ? -v : v;
+        }
+    } else if (e == 31) {
+        u = sign | 0x7f800000u | (m << 13);
+    } else {
+        u = sign | ((e + 112u) << 23) | (m << 13);
+    }
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+struct DevBuf {
+    void* p = nullptr;
+    ~DevBuf()
+    {
+        if (p) (void)hipFree(p);
+    }
+    int32_t alloc(size_t bytes, const char* what)
+    {
+        RT_TRY(hipMalloc(&p, bytes ? bytes : 1), what);
+        return CELLM_HIP_OK;
+    }
+    template <typename T>
+    T* as() const
+    {
+        return reinterpret_cast<T*>(p);
+    }
+};
+
+}  // namespace
+
+struct cellm_llama_dev {
+    cellm_llama_config_t cfg{};
+    int32_t max_rows = 0, max_blocks = 0, table_positions = 0;
+    int device = 0;
+    cellm_hip_ctx_t* hip = nullptr;
+    void* stream = nullptr;
+    size_t kvd = 0, kv_elems = 0;
+    // device views of the cached weights, per layer: 7 int8 matrices and their f16 row scales
+    std::vector<const int8_t*> w;
+    std::vector<const uint16_t*> s;
+    std::vector<const float*> attn_norm, mlp_norm;
+    const int8_t* embed = nullptr;
+    const uint16_t* embed_scale = nullptr;
+    const float* final_norm = nullptr;
+    DevBuf kcache, vcache, rope, x, xn, q, k, v, attn, proj, h, logits, io;
+    // io: [tokens u32 | positions i32 | block tables u32 | argmax idx i32 | argmax val f32]
+    void* host_io = nullptr;  // pinned mirror of io
+    size_t io_tokens = 0, io_pos = 0, io_bt = 0, io_idx = 0, io_val = 0, io_bytes = 0;
+    // one captured graph per row count (index rows - 1): the step's launches
+    // from the embedding to the argmax, replayed with one hipGraphLaunch
+    hipGraph_t graph[4] = {};
+    hipGraphExec_t graph_exec[4] = {};
+    bool use_graphs = false;
+};
+
+namespace {
+
+int32_t upload(cellm_llama_dev* m, const std::string& key, const void* host, size_t bytes, const void** dev)
+{
+    LIB_TRY(cellm_hip_weight_upload(m->hip, key.c_str(), host, bytes, dev), key.c_str());
+    return CELLM_HIP_OK;
+}
+
+int32_t upload_norm(cellm_llama_dev* m, const std::string& key, const uint16_t* f16, size_t n, const float** dev)
+{
+    std::vector<float> f(n);
+    for (size_t i = 0; i < n; ++i) f[i] = h2f(f16[i]);  // rmsnorm_weight (llama.rs:728-741)
+    const void* d = nullptr;
+    if (int32_t rc = upload(m, key, f.data(), n * sizeof(float), &d)) return rc;
+    *dev = reinterpret_cast<const float*>(d);
+    return CELLM_HIP_OK;
+}
+
+void out_in(const cellm_llama_config_t& c, int j, size_t* out, size_t* in)
+{
+    const size_t hid = (size_t)c.hidden, kv = (size_t)c.n_kv_heads * c.head_dim, inter = (size_t)c.intermediate;
+    const size_t o[7] = {hid, kv, kv, hid, inter, inter, hid};
+    const size_t i[7] = {hid, hid, hid, hid, hid, hid, inter};
+    *out = o[j];
+    *in = i[j];
+}
+
+
+// The step's device work for `rows` sessions, enqueued on the runner's stream:
+// inputs are read from io (tokens, positions, block tables), the greedy ids
+// and logits are left in io and m->logits.  Only kernel launches: no
+// allocation, copy or synchronisation, so the sequence can be captured.
+int32_t enqueue_step(cellm_llama_dev* m, int32_t rows)
+{
+    const cellm_llama_config_t& c = m->cfg;
+    const int64_t tpb = c.tokens_per_block, MB = m->max_blocks;
+    unsigned char* dio = m->io.as<unsigned char>();
+    const uint32_t* d_tok = reinterpret_cast<const uint32_t*>(dio + m->io_tokens);
+    const int32_t* d_pos = reinterpret_cast<const int32_t*>(dio + m->io_pos);
+    const uint32_t* d_bt = reinterpret_cast<const uint32_t*>(dio + m->io_bt);
+    int32_t* d_idx = reinterpret_cast<int32_t*>(dio + m->io_idx);
+    float* d_val = reinterpret_cast<float*>(dio + m->io_val);
+
+    const int64_t R = rows, hid = c.hidden, kvd = (int64_t)m->kvd, inter = c.intermediate, vocab = c.vocab;
+    const int64_t L = c.n_layers;
+    float *x = m->x.as<float>(), *xn = m->xn.as<float>(), *q = m->q.as<float>(), *k = m->k.as<float>();
+    float *v = m->v.as<float>(), *attn = m->attn.as<float>(), *proj = m->proj.as<float>(), *h = m->h.as<float>();
+    uint16_t *kc = m->kcache.as<uint16_t>(), *vc = m->vcache.as<uint16_t>();
+    cellm_hip_ctx_t* H = m->hip;
+    void* S = m->stream;
+    const float eps = c.rms_norm_eps;
+
+    LIB_TRY(cellm_hip_embed_i8(H, d_tok, R, m->embed, m->embed_scale, vocab, hid, x, S), "embed");
+    LIB_TRY(cellm_hip_rms_norm(H, x, m->attn_norm[0], CELLM_HIP_DTYPE_F32, R, hid, eps, xn, S), "input_layernorm");
+    for (int64_t l = 0; l < L; ++l) {
+        const int8_t* const* W = &m->w[l * 7];
+        const uint16_t* const* Sc = &m->s[l * 7];
+        // xn = input_layernorm(x), from the previous layer's residual add (or the embedding)
+        LIB_TRY(cellm_hip_qgemv_i8_qkv(H, W[0], Sc[0], hid, nullptr, W[1], Sc[1], kvd, nullptr, W[2], Sc[2], kvd, nullptr,
+                                       CELLM_HIP_DTYPE_F16, xn, CELLM_HIP_DTYPE_F32, q, k, v, R, hid, kvd, hid, S),
+                "qkv");
+        LIB_TRY(cellm_hip_rope_kv_write_f16(H, q, k, v, R, c.n_heads, c.n_kv_heads, c.head_dim, d_pos,
+                                            m->rope.as<float>(), m->table_positions, kc, vc, d_bt, MB, c.total_blocks,
+                                            L, tpb, l, S),
+                "rope + kv write");
+        LIB_TRY(cellm_hip_attention_gqa_f16kv(H, q, kc, vc, d_bt, MB, c.total_blocks, d_pos, R, c.n_heads,
+                                              c.n_kv_heads, c.head_dim, L, tpb, l, attn, S),
+                "attention");
+        LIB_TRY(cellm_hip_qgemv_i8(H, W[3], Sc[3], CELLM_HIP_DTYPE_F16, hid, attn, CELLM_HIP_DTYPE_F32, nullptr, proj, R,
+                                   hid, hid, S),
+                "o_proj");
+        LIB_TRY(cellm_hip_add_rms_norm(H, x, proj, m->mlp_norm[l], CELLM_HIP_DTYPE_F32, R, hid, eps, xn, S),
+                "residual + post_attention_layernorm");
+        LIB_TRY(cellm_hip_qgemv_i8_gate_up_silu(H, W[4], Sc[4], inter, nullptr, W[5], Sc[5], inter, nullptr,
+                                                CELLM_HIP_DTYPE_F16, xn, CELLM_HIP_DTYPE_F32, h, R, inter, hid, S),
+                "gate/up");
+        LIB_TRY(cellm_hip_qgemv_i8(H, W[6], Sc[6], CELLM_HIP_DTYPE_F16, hid, h, CELLM_HIP_DTYPE_F32, nullptr, proj, R,
+                                   hid, inter, S),
+                "down_proj");
+        // residual, then the next layer's input_layernorm (the final norm after the last layer)
+        const float* next_norm = l + 1 < L ? m->attn_norm[l + 1] : m->final_norm;
+        LIB_TRY(cellm_hip_add_rms_norm(H, x, proj, next_norm, CELLM_HIP_DTYPE_F32, R, hid, eps, xn, S),
+                "residual + norm");
+    }
+    // tied lm_head through the int8 GEMV (llama.rs:549-567), greedy id on the device
+    float* lg = m->logits.as<float>();
+    LIB_TRY(cellm_hip_qgemv_i8(H, m->embed, m->embed_scale, CELLM_HIP_DTYPE_F16, vocab, xn, CELLM_HIP_DTYPE_F32, nullptr, lg, R,
+                               vocab, hid, S),
+            "lm_head");
+    LIB_TRY(cellm_hip_argmax_f32(H, lg, R, vocab, d_idx, d_val, S), "argmax");
+    return CELLM_HIP_OK;
+}
+
+// Size every scratch buffer of the HIP context for all row counts, then
+// capture one graph per row count.  The context grows a per-stream scratch
+// buffer (split-K partials, attention partials) on the first call that needs
+// more and never shrinks it, so after one eager step at each row count no
+// later step reallocates, and the captured kernel arguments stay valid.  The
+// eager steps run at position 0 on block 0 and the K/V cache is cleared
+// afterwards.
+int32_t prepare_graphs(cellm_llama_dev* m)
+{
+    const hipStream_t st = reinterpret_cast<hipStream_t>(m->stream);
+    memset(m->host_io, 0, m->io_bytes);
+    RT_TRY(hipMemcpyAsync(m->io.p, m->host_io, m->io_bytes, hipMemcpyHostToDevice, st), "clear step io");
+    for (int32_t r = 1; r <= m->max_rows; ++r)
+        if (int32_t rc = enqueue_step(m, r)) return rc;
+    RT_TRY(hipStreamSynchronize(st), "warm-up steps");
+    RT_TRY(hipMemsetAsync(m->kcache.p, 0, m->kv_elems * 2, st), "clear K cache");
+    RT_TRY(hipMemsetAsync(m->vcache.p, 0, m->kv_elems * 2, st), "clear V cache");
+    RT_TRY(hipStreamSynchronize(st), "clear K/V cache");
+    for (int32_t r = 1; r <= m->max_rows; ++r) {
+        RT_TRY(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+        const int32_t rc = enqueue_step(m, r);
+        hipGraph_t g = nullptr;
+        const hipError_t e = hipStreamEndCapture(st, &g);
+        if (rc) {
+            if (g) (void)hipGraphDestroy(g);
+            return rc;
+        }
+        if (e != hipSuccess) return from_runtime(e, "hipStreamEndCapture");
+        m->graph[r - 1] = g;
+        RT_TRY(hipGraphInstantiate(&m->graph_exec[r - 1], g, nullptr, nullptr, 0), "hipGraphInstantiate");
+    }
+    m->use_graphs = true;
+    return CELLM_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t cellm_llama_rope_table(float theta, int32_t head_dim, int32_t positions, float* out)
+{
+    if (!out || head_dim <= 0 || head_dim % 2 || positions <= 0)
+        return fail(CELLM_HIP_ERR_INVALID_ARG, "bad rope table arguments");
+    const int32_t half = head_dim / 2;
+    for (int32_t p = 0; p < positions; ++p)
+        for (int32_t i = 0; i < half; ++i) {
+            // rope_non_interleaved_inplace_f32 (cpu_kernels.rs:264-277), f32 throughout
+            const float inv_freq = std::pow(theta, -(2.0f * (float)i) / (float)head_dim);
+            const float angle = (float)p * inv_freq;
+            out[((size_t)p * half + i) * 2] = std::cos(angle);
+            out[((size_t)p * half + i) * 2 + 1] = std::sin(angle);
+        }
+    return CELLM_HIP_OK;
+}
+
+int32_t cellm_llama_dev_create(const cellm_llama_config_t* cfg, const cellm_llama_layer_t* layers,
+                               const int8_t* embed_i8, const uint16_t* embed_scale_f16,
+                               const uint16_t* final_norm_f16, int32_t device, int32_t max_rows, int32_t max_blocks,
+                               cellm_llama_dev_t** out)
+{
+    if (!cfg || !layers || !embed_i8 || !embed_scale_f16 || !final_norm_f16 || !out)
+        return fail(CELLM_HIP_ERR_INVALID_ARG, "null argument");
+    *out = nullptr;
+    const cellm_llama_config_t& c = *cfg;
+    if (c.n_layers <= 0 || c.hidden <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 || c.head_dim <= 0 ||
+        c.intermediate <= 0 || c.vocab <= 0 || c.tokens_per_block <= 0 || c.total_blocks <= 0)
+        return fail(CELLM_HIP_ERR_INVALID_ARG, "non-positive dimension in config");
+    if (c.head_dim * c.n_heads != c.hidden)  // llama.rs:285-289
+        return fail(CELLM_HIP_ERR_INVALID_ARG, "hidden_size must equal num_heads * head_dim");
+    if (c.n_heads % c.n_kv_heads != 0) return fail(CELLM_HIP_ERR_INVALID_ARG, "n_heads %% n_kv_heads != 0");
+    if (max_rows < 1 || max_rows > 4) return fail(CELLM_HIP_ERR_INVALID_ARG, "max_rows must be 1..4");
+    if (max_blocks < 1 || max_blocks > c.total_blocks)
+        return fail(CELLM_HIP_ERR_INVALID_ARG, "max_blocks must be 1..total_blocks");
+    auto* m = new cellm_llama_dev();
+    m->cfg = c;
+    m->max_rows = max_rows;
+    m->max_blocks = max_blocks;
+    m->device = device;
+    m->kvd = (size_t)c.n_kv_heads * c.head_dim;
+    m->table_positions = max_blocks * c.tokens_per_block;
+    auto bail = [&](int32_t rc) {
+        cellm_llama_dev_destroy(m);
+        return rc;
+    };
+    int32_t rc = cellm_hip_create(device, &m->hip);
+    if (rc) {
+        m->hip = nullptr;
+        return bail(from_hip_lib(rc, "cellm_hip_create"));
+    }
+    if ((rc = cellm_hip_get_stream(m->hip, &m->stream))) return bail(from_hip_lib(rc, "cellm_hip_get_stream"));
+    int prev = 0;
+    if (hipGetDevice(&prev) != hipSuccess || hipSetDevice(device) != hipSuccess)
+        return bail(fail(CELLM_HIP_ERR_DEVICE, "hipSetDevice(%d) failed", device));
+    const size_t hid = (size_t)c.hidden, L = (size_t)c.n_layers;
+    m->w.resize(L * 7);
+    m->s.resize(L * 7);
+    for (size_t l = 0; l < L; ++l) {
+        const std::string pre = "model.layers." + std::to_string(l) + ".";
+        for (int j = 0; j < 7; ++j) {
+            size_t o, i;
+            out_in(c, j, &o, &i);
+            if (!layers[l].w[j] || !layers[l].scale_f16[j])
+                return bail(fail(CELLM_HIP_ERR_INVALID_ARG, "layer %zu tensor %s missing", l, kNames[j]));
+            const void *dw = nullptr, *ds = nullptr;
+            if ((rc = upload(m, pre + kNames[j] + ".weight", layers[l].w[j], o * i, &dw)) ||
+                (rc = upload(m, pre + kNames[j] + ".weight.qscale", layers[l].scale_f16[j], o * 2, &ds)))
+                return bail(rc);
+            m->w[l * 7 + j] = reinterpret_cast<const int8_t*>(dw);
+            m->s[l * 7 + j] = reinterpret_cast<const uint16_t*>(ds);
+        }
+        const float *a = nullptr, *b = nullptr;
+        if ((rc = upload_norm(m, pre + "input_layernorm.weight", layers[l].input_layernorm_f16, hid, &a)) ||
+            (rc = upload_norm(m, pre + "post_attention_layernorm.weight", layers[l].post_attention_layernorm_f16, hid,
+                              &b)))
+            return bail(rc);
+        m->attn_norm.push_back(a);
+        m->mlp_norm.push_back(b);
+    }
+    const void *de = nullptr, *des = nullptr;
+    if ((rc = upload(m, "model.embed_tokens.weight", embed_i8, (size_t)c.vocab * hid, &de)) ||
+        (rc = upload(m, "model.embed_tokens.weight.qscale", embed_scale_f16, (size_t)c.vocab * 2, &des)) ||
+        (rc = upload_norm(m, "model.norm.weight", final_norm_f16, hid, &m->final_norm)))
+        return bail(rc);
+    m->embed = reinterpret_cast<const int8_t*>(de);
+    m->embed_scale = reinterpret_cast<const uint16_t*>(des);
+
+    // paged K/V (KvCacheLayout: total_blocks x layers x tokens_per_block x kv_dim), zeroed
+    m->kv_elems = (size_t)c.total_blocks * L * c.tokens_per_block * m->kvd;
+    const size_t R = (size_t)max_rows, inter = (size_t)c.intermediate;
+    if ((rc = m->kcache.alloc(m->kv_elems * 2, "hipMalloc(K cache)")) ||
+        (rc = m->vcache.alloc(m->kv_elems * 2, "hipMalloc(V cache)")) ||
+        (rc = m->rope.alloc((size_t)m->table_positions * c.head_dim * sizeof(float), "hipMalloc(rope table)")) ||
+        (rc = m->x.alloc(R * hid * 4, "hipMalloc(x)")) || (rc = m->xn.alloc(R * hid * 4, "hipMalloc(xn)")) ||
+        (rc = m->q.alloc(R * hid * 4, "hipMalloc(q)")) || (rc = m->k.alloc(R * m->kvd * 4, "hipMalloc(k)")) ||
+        (rc = m->v.alloc(R * m->kvd * 4, "hipMalloc(v)")) || (rc = m->attn.alloc(R * hid * 4, "hipMalloc(attn)")) ||
+        (rc = m->proj.alloc(R * hid * 4, "hipMalloc(proj)")) || (rc = m->h.alloc(R * inter * 4, "hipMalloc(h)")) ||
+        (rc = m->logits.alloc(R * (size_t)c.vocab * 4, "hipMalloc(logits)")))
+        return bail(rc);
+    hipError_t e = hipMemset(m->kcache.p, 0, m->kv_elems * 2);
+    if (e == hipSuccess) e = hipMemset(m->vcache.p, 0, m->kv_elems * 2);
+    if (e != hipSuccess) return bail(from_runtime(e, "hipMemset(K/V cache)"));
+    {
+        std::vector<float> table((size_t)m->table_positions * c.head_dim);
+        if ((rc = cellm_llama_rope_table(c.rope_theta, c.head_dim, m->table_positions, table.data()))) return bail(rc);
+        e = hipMemcpy(m->rope.p, table.data(), table.size() * sizeof(float), hipMemcpyHostToDevice);
+        if (e != hipSuccess) return bail(from_runtime(e, "upload rope table"));
+    }
+    auto align = [](size_t v) { return (v + 255) & ~(size_t)255; };
+    m->io_tokens = 0;
+    m->io_pos = align(R * 4);
+    m->io_bt = m->io_pos + align(R * 4);
+    m->io_idx = m->io_bt + align(R * (size_t)max_blocks * 4);
+    m->io_val = m->io_idx + align(R * 4);
+    m->io_bytes = m->io_val + align(R * 4);
+    if ((rc = m->io.alloc(m->io_bytes, "hipMalloc(step io)"))) return bail(rc);
+    e = hipHostMalloc(&m->host_io, m->io_bytes, hipHostMallocDefault);
+    if (e != hipSuccess) {
+        m->host_io = nullptr;
+        return bail(from_runtime(e, "hipHostMalloc(step io)"));
+    }
+    if ((rc = prepare_graphs(m))) return bail(rc);
+    (void)hipSetDevice(prev);
+    *out = m;
+    return CELLM_HIP_OK;
+}
+
+void cellm_llama_dev_destroy(cellm_llama_dev_t* m)
+{
+    if (!m) return;
+    if (m->hip) (void)cellm_hip_synchronize(m->hip);
+    for (int r = 0; r < 4; ++r) {
+        if (m->graph_exec[r]) (void)hipGraphExecDestroy(m->graph_exec[r]);
+        if (m->graph[r]) (void)hipGraphDestroy(m->graph[r]);
+    }
+    if (m->host_io) (void)hipHostFree(m->host_io);
+    m->host_io = nullptr;
+    // device buffers free themselves; the weight cache goes with the context
+    cellm_hip_ctx_t* hip = m->hip;
+    delete m;
+    if (hip) cellm_hip_destroy(hip);
+}
+
+int32_t cellm_llama_dev_set_graphs(cellm_llama_dev_t* m, int32_t enable)
+{
+    if (!m) return fail(CELLM_HIP_ERR_INVALID_ARG, "null argument");
+    for (int32_t r = 0; enable && r < m->max_rows; ++r)
+        if (!m->graph_exec[r]) return fail(CELLM_HIP_ERR_UNSUPPORTED, "no captured graph for %d rows", r + 1);
+    m->use_graphs = enable != 0;
+    return CELLM_HIP_OK;
+}
+
+int32_t cellm_llama_dev_kv_upload(cellm_llama_dev_t* m, const uint16_t* k_f16, const uint16_t* v_f16, size_t n_elems)
+{
+    if (!m || !k_f16 || !v_f16) return fail(CELLM_HIP_ERR_INVALID_ARG, "null argument");
+    if (n_elems != m->kv_elems) return fail(CELLM_HIP_ERR_INVALID_ARG, "K/V have %zu elements, not %zu", n_elems,
+                                            m->kv_elems);
+    RT_TRY(hipSetDevice(m->device), "hipSetDevice");
+    RT_TRY(hipMemcpy(m->kcache.p, k_f16, n_elems * 2, hipMemcpyHostToDevice), "upload K");
+    RT_TRY(hipMemcpy(m->vcache.p, v_f16, n_elems * 2, hipMemcpyHostToDevice), "upload V");
+    return CELLM_HIP_OK;
+}
+
+int32_t cellm_llama_dev_kv_download(cellm_llama_dev_t* m, uint16_t* k_f16, uint16_t* v_f16, size_t n_elems)
+{
+    if (!m || !k_f16 || !v_f16) return fail(CELLM_HIP_ERR_INVALID_ARG, "null argument");
+    if (n_elems != m->kv_elems) return fail(CELLM_HIP_ERR_INVALID_ARG, "K/V have %zu elements, not %zu", n_elems,
+                                            m->kv_elems);
+    RT_TRY(hipSetDevice(m->device), "hipSetDevice");
+    LIB_TRY(cellm_hip_synchronize(m->hip), "synchronize");
+    RT_TRY(hipMemcpy(k_f16, m->kcache.p, n_elems * 2, hipMemcpyDeviceToHost), "download K");
+    RT_TRY(hipMemcpy(v_f16, m->vcache.p, n_elems * 2, hipMemcpyDeviceToHost), "download V");
+    return CELLM_HIP_OK;
+}
+
+int32_t cellm_llama_dev_step(cellm_llama_dev_t* m, int32_t rows, const uint32_t* tokens, const int32_t* positions,
+                             const uint32_t* block_tables, uint32_t* out_tokens, float* out_logits, float* logits_out)
+{
+    if (!m || !tokens || !positions || !block_tables || !out_tokens)
+        return fail(CELLM_HIP_ERR_INVALID_ARG, "null argument");
+    const cellm_llama_config_t& c = m->cfg;
+    if (rows < 1 || rows > m->max_rows) return fail(CELLM_HIP_ERR_INVALID_ARG, "rows must be 1..%d", m->max_rows);
+    const int64_t tpb = c.tokens_per_block, MB = m->max_blocks;
+    for (int32_t r = 0; r < rows; ++r) {
+        const int32_t p = positions[r];
+        if (p < 0 || p >= m->table_positions)
+            return fail(CELLM_HIP_ERR_INVALID_ARG, "row %d: position %d outside 0..%d", r, p, m->table_positions - 1);
+        for (int64_t b = 0; b <= p / tpb; ++b)
+            if (block_tables[r * MB + b] >= (uint32_t)c.total_blocks)
+                return fail(CELLM_HIP_ERR_INVALID_ARG, "row %d: block %u out of range", r, block_tables[r * MB + b]);
+    }
+    RT_TRY(hipSetDevice(m->device), "hipSetDevice");
+    const hipStream_t st = reinterpret_cast<hipStream_t>(m->stream);
+    // inputs: one pinned staging copy
+    unsigned char* hio = reinterpret_cast<unsigned char*>(m->host_io);
+    memcpy(hio + m->io_tokens, tokens, (size_t)rows * 4);
+    memcpy(hio + m->io_pos, positions, (size_t)rows * 4);
+    memcpy(hio + m->io_bt, block_tables, (size_t)rows * MB * 4);
+    RT_TRY(hipMemcpyAsync(m->io.p, m->host_io, m->io_idx, hipMemcpyHostToDevice, st), "upload step inputs");
+    if (m->use_graphs) {
+        RT_TRY(hipGraphLaunch(m->graph_exec[rows - 1], st), "hipGraphLaunch(step)");
+    } else if (int32_t rc = enqueue_step(m, rows)) {
+        return rc;
+    }
+    unsigned char* dio = m->io.as<unsigned char>();
+    const float* lg = m->logits.as<float>();
+    RT_TRY(hipMemcpyAsync(hio + m->io_idx, dio + m->io_idx, m->io_bytes - m->io_idx, hipMemcpyDeviceToHost, st),
+           "download ids");
+    if (logits_out)
+        RT_TRY(hipMemcpyAsync(logits_out, lg, (size_t)rows * c.vocab * 4, hipMemcpyDeviceToHost, st), "download logits");
+    RT_TRY(hipStreamSynchronize(st), "step");
+    for (int32_t r = 0; r < rows; ++r) {
+        int32_t id;
+        float val;
+        memcpy(&id, hio + m->io_idx + (size_t)r * 4, 4);
+        memcpy(&val, hio + m->io_val + (size_t)r * 4, 4);
+        out_tokens[r] = (uint32_t)id;
+        if (out_logits) out_logits[r] = val;
+    }
+    return CELLM_HIP_OK;
+}
+
+}  // extern "C"

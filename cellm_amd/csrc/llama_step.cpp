@@ -17,9 +17,13 @@
 #include "../../include/cellm_hip.h"
 #include "../../include/cellm_llama_step.h"
 
+namespace cellm_step {
+thread_local std::string g_err;  // shared with llama_device.cpp
+}
+
 namespace {
 
-thread_local std::string g_err;
+using cellm_step::g_err;
 
 int32_t fail(int32_t code, const char* fmt, ...)
 {

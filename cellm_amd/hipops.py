@@ -271,3 +271,64 @@ class HipOps:
         check(self._lib.cellm_hip_dequant_q4_affine(self._h, _dev_ptr(wq), _dev_ptr(scales), _dev_ptr(biases),
                                                     _torch_dtype_code(scales), group, _dev_ptr(out),
                                                     _torch_dtype_code(out), n, k, _stream_ptr(stream)))
+
+    # ---- decode-step ops (MetalOps::encode_rms_norm_f16w / encode_rope_half_f32 /
+    # encode_add_f32_inplace, MetalKvStorage::encode_write_token_f32 / encode_attention)
+
+    def encode_embed_i8(self, tokens_u32, embed_i8, scales_f16, out, stream=None) -> None:
+        vocab, hidden = embed_i8.shape
+        check(self._lib.cellm_hip_embed_i8(self._h, _dev_ptr(tokens_u32), tokens_u32.numel(), _dev_ptr(embed_i8),
+                                           _dev_ptr(scales_f16), vocab, hidden, _dev_ptr(out), _stream_ptr(stream)))
+
+    def encode_rms_norm(self, x, weight, out, eps: float, stream=None) -> None:
+        n = weight.numel()
+        check(self._lib.cellm_hip_rms_norm(self._h, _dev_ptr(x), _dev_ptr(weight), _torch_dtype_code(weight),
+                                           x.numel() // n, n, eps, _dev_ptr(out), _stream_ptr(stream)))
+
+    def encode_add_rms_norm(self, x, y, weight, out, eps: float, stream=None) -> None:
+        n = weight.numel()
+        check(self._lib.cellm_hip_add_rms_norm(self._h, _dev_ptr(x), _dev_ptr(y), _dev_ptr(weight),
+                                               _torch_dtype_code(weight), x.numel() // n, n, eps, _dev_ptr(out),
+                                               _stream_ptr(stream)))
+
+    def encode_rope_kv_write(self, q, k, v, n_heads: int, n_kv_heads: int, head_dim: int, positions_i32, cos_sin,
+                             kcache, vcache, block_tables, total_blocks: int, n_layers: int, tokens_per_block: int,
+                             layer: int, stream=None) -> None:
+        rows = positions_i32.numel()
+        check(self._lib.cellm_hip_rope_kv_write_f16(self._h, _dev_ptr(q), _dev_ptr(k), _dev_ptr(v), rows, n_heads,
+                                                    n_kv_heads, head_dim, _dev_ptr(positions_i32), _dev_ptr(cos_sin),
+                                                    cos_sin.shape[0], _dev_ptr(kcache), _dev_ptr(vcache),
+                                                    _dev_ptr(block_tables), block_tables.shape[-1], total_blocks,
+                                                    n_layers, tokens_per_block, layer, _stream_ptr(stream)))
+
+    def encode_rope_half(self, x, n_heads: int, head_dim: int, positions_i32, cos_sin, stream=None) -> None:
+        rows = positions_i32.numel()
+        check(self._lib.cellm_hip_rope_half_f32(self._h, _dev_ptr(x), rows, n_heads, head_dim,
+                                                _dev_ptr(positions_i32), _dev_ptr(cos_sin), cos_sin.shape[0],
+                                                _stream_ptr(stream)))
+
+    def encode_kv_write(self, k, v, positions_i32, kcache, vcache, block_tables, total_blocks: int, n_layers: int,
+                        tokens_per_block: int, layer: int, stream=None) -> None:
+        rows = positions_i32.numel()
+        check(self._lib.cellm_hip_kv_write_f16(self._h, _dev_ptr(k), _dev_ptr(v), rows, k.numel() // rows,
+                                               _dev_ptr(positions_i32), _dev_ptr(kcache), _dev_ptr(vcache),
+                                               _dev_ptr(block_tables), block_tables.shape[-1], total_blocks, n_layers,
+                                               tokens_per_block, layer, _stream_ptr(stream)))
+
+    def encode_attention(self, q, kcache, vcache, block_tables, positions_i32, out, n_heads: int, n_kv_heads: int,
+                         head_dim: int, total_blocks: int, n_layers: int, tokens_per_block: int, layer: int,
+                         stream=None) -> None:
+        rows = positions_i32.numel()
+        check(self._lib.cellm_hip_attention_gqa_f16kv(self._h, _dev_ptr(q), _dev_ptr(kcache), _dev_ptr(vcache),
+                                                      _dev_ptr(block_tables), block_tables.shape[-1], total_blocks,
+                                                      _dev_ptr(positions_i32), rows, n_heads, n_kv_heads, head_dim,
+                                                      n_layers, tokens_per_block, layer, _dev_ptr(out),
+                                                      _stream_ptr(stream)))
+
+    def encode_add_inplace(self, x, y, stream=None) -> None:
+        check(self._lib.cellm_hip_add_f32_inplace(self._h, _dev_ptr(x), _dev_ptr(y), x.numel(), _stream_ptr(stream)))
+
+    def encode_argmax(self, logits, out_index_i32, out_value, stream=None) -> None:
+        rows = out_index_i32.numel()
+        check(self._lib.cellm_hip_argmax_f32(self._h, _dev_ptr(logits), rows, logits.numel() // rows,
+                                             _dev_ptr(out_index_i32), _dev_ptr(out_value), _stream_ptr(stream)))

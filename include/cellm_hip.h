@@ -231,6 +231,83 @@ int32_t cellm_hip_logits_q4_affine(cellm_hip_ctx_t* ctx, const float* x, const u
                                    const void* biases, int32_t sb_dtype, size_t rows, size_t cols,
                                    const char* cache_key, float* out);
 
+/* ---- decode-step ops around the projections (async, device pointers) ----
+ * The device side of the fused Metal decode graph
+ * (crates/cellm-model/src/llama_graph.rs:140-405).  `rows` sessions, one
+ * activation row each; `positions` is a device int32[rows]; a paged K/V cache
+ * is an f16 array addressed as KvCacheLayout::token_base_elem
+ * (crates/cellm-core/src/kv_cache.rs:62-73):
+ *   base = block * (n_layers * tokens_per_block * kv_dim)
+ *        + layer * (tokens_per_block * kv_dim) + (pos % tokens_per_block) * kv_dim
+ * with block = block_tables[row * max_blocks + pos / tokens_per_block]
+ * (device uint32).  Pages with block >= total_blocks are skipped. */
+
+/* embed_token, i8 branch (crates/cellm-model/src/llama.rs:676-701):
+ * out[r] = f32(embed_i8[t]) * f32(scales_f16[t]), t = tokens[r] % vocab. */
+int32_t cellm_hip_embed_i8(cellm_hip_ctx_t* ctx, const uint32_t* tokens, int64_t rows, const int8_t* embed_i8,
+                           const uint16_t* scales_f16, int64_t vocab, int64_t hidden, float* out, void* stream);
+
+/* MetalOps::encode_rms_norm_f16w (metal.rs) / rms_norm_f32 (cpu_kernels.rs:17-34)
+ * per row: out = x * (1 / sqrt(mean(x^2) + eps)) * weight; weight f32/f16/bf16 [n]. */
+int32_t cellm_hip_rms_norm(cellm_hip_ctx_t* ctx, const float* x, const void* weight, int32_t weight_dtype,
+                           int64_t rows, int64_t n, float eps, float* out, void* stream);
+
+/* The residual add of a sub-layer (x[i] += y[i], llama.rs:440 and :494)
+ * followed by the next RMSNorm (cellm_hip_rms_norm) in one launch:
+ * x += y in place, then out = rms_norm(x) * weight.  Same results as
+ * cellm_hip_add_f32_inplace followed by cellm_hip_rms_norm. */
+int32_t cellm_hip_add_rms_norm(cellm_hip_ctx_t* ctx, float* x, const float* y, const void* weight,
+                               int32_t weight_dtype, int64_t rows, int64_t n, float eps, float* out, void* stream);
+
+/* MetalOps::encode_rope_half_f32 with rotary_dim = head_dim
+ * (rope_non_interleaved_inplace_f32, cpu_kernels.rs:264-277), in place on
+ * x [rows][n_heads][head_dim].  cos_sin [table_positions][head_dim/2][2] holds
+ * (cos, sin) of pos * theta^(-2i/head_dim), computed by the caller as the
+ * reference does in f32; positions are clamped to the table. */
+int32_t cellm_hip_rope_half_f32(cellm_hip_ctx_t* ctx, float* x, int64_t rows, int64_t n_heads, int64_t head_dim,
+                                const int32_t* positions, const float* cos_sin, int64_t table_positions, void* stream);
+
+/* MetalKvStorage::encode_write_token_f32 / write_token_f32 (kvcache.rs:589-615):
+ * k, v [rows][kv_dim] f32 -> f16 (RNE) at each row's position in `layer`. */
+int32_t cellm_hip_kv_write_f16(cellm_hip_ctx_t* ctx, const float* k, const float* v, int64_t rows, int64_t kv_dim,
+                               const int32_t* positions, uint16_t* kcache, uint16_t* vcache,
+                               const uint32_t* block_tables, int64_t max_blocks, int64_t total_blocks,
+                               int64_t n_layers, int64_t tokens_per_block, int64_t layer, void* stream);
+
+/* The step's q/k rotation and K/V write in one launch
+ * (llama_graph.rs:273-281 encodes them as three): RoPE in place on q
+ * [rows][n_heads][head_dim] and k [rows][n_kv_heads][head_dim], then the
+ * rotated k and v written as f16 at each row's position in `layer`.  Same
+ * results as cellm_hip_rope_half_f32 on q and on k followed by
+ * cellm_hip_kv_write_f16. */
+int32_t cellm_hip_rope_kv_write_f16(cellm_hip_ctx_t* ctx, float* q, float* k, const float* v, int64_t rows,
+                                    int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, const int32_t* positions,
+                                    const float* cos_sin, int64_t table_positions, uint16_t* kcache, uint16_t* vcache,
+                                    const uint32_t* block_tables, int64_t max_blocks, int64_t total_blocks,
+                                    int64_t n_layers, int64_t tokens_per_block, int64_t layer, void* stream);
+
+/* MetalKvStorage::encode_attention / attention_single_token_gqa_f32
+ * (kvcache.rs:710-789, 1377-1439): each row attends over positions
+ * 0..positions[r] of `layer`; q and out [rows][n_heads][head_dim] f32, query
+ * head h reads kv head h / (n_heads / n_kv_heads).  Needs n_heads %
+ * n_kv_heads == 0, at most 8 query heads per kv head, head_dim 64 or 128,
+ * max_blocks * tokens_per_block <= 32768.  Split over the sequence in chunks
+ * of 64 positions whose softmax partials are combined in a second pass
+ * (workspace owned by the context, per stream). */
+int32_t cellm_hip_attention_gqa_f16kv(cellm_hip_ctx_t* ctx, const float* q, const uint16_t* kcache,
+                                      const uint16_t* vcache, const uint32_t* block_tables, int64_t max_blocks,
+                                      int64_t total_blocks, const int32_t* positions, int64_t rows, int64_t n_heads,
+                                      int64_t n_kv_heads, int64_t head_dim, int64_t n_layers, int64_t tokens_per_block,
+                                      int64_t layer, float* out, void* stream);
+
+/* MetalOps::encode_add_f32_inplace: x[i] += y[i]. */
+int32_t cellm_hip_add_f32_inplace(cellm_hip_ctx_t* ctx, float* x, const float* y, int64_t n, void* stream);
+
+/* topk_from_logits(..)[0] (llama.rs:1049-1078) after the non-finite -> -inf
+ * sanitize (llama.rs:1081-1092), per row: the first index of the maximum. */
+int32_t cellm_hip_argmax_f32(cellm_hip_ctx_t* ctx, const float* logits, int64_t rows, int64_t n, int32_t* out_index,
+                             float* out_value, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,9 +1,10 @@
 /*
- * cellm_llama_step.h -- host-side Llama decode step whose projections run on
- * libcellm_hip.so (the config-5 harness).
+ * cellm_llama_step.h -- Llama decode steps over libcellm_hip.so: a host-side
+ * step whose projections run on the HIP qGEMV (cellm_llama_*), and a
+ * device-resident step (cellm_llama_dev_*, below).
  *
- * This is the runner side of the boundary, above the C ABI of cellm_hip.h:
- * it mirrors LlamaRunner::step_topk / step_inner
+ * This is the runner side of the boundary, above the C ABI of cellm_hip.h.
+ * The host-side step mirrors LlamaRunner::step_topk / step_inner
  * (crates/cellm-model/src/llama.rs:189-212, 235-647) with every int8
  * projection (q, k, v, o, gate, up, down, tied lm_head) issued to the HIP
  * qGEMV, while embedding, RMSNorm, RoPE, the paged f16 KV cache and GQA
@@ -75,6 +76,50 @@ int32_t cellm_llama_kv_cache(cellm_llama_t* m, uint16_t** k_f16, uint16_t** v_f1
  * returns the greedy id and its logit.  logits_out (vocab floats) is optional. */
 int32_t cellm_llama_step(cellm_llama_t* m, uint32_t token, size_t pos, const uint32_t* block_table,
                          size_t n_blocks, uint32_t* out_token, float* out_logit, float* logits_out);
+
+/* ---- device-resident step ------------------------------------------------
+ * The HIP counterpart of the fused Metal decode graph
+ * LlamaGraphState::step_fused (crates/cellm-model/src/llama_graph.rs:140-405):
+ * weights in the HIP weight cache, a paged f16 K/V cache on the device
+ * (same layout as cellm_llama_kv_cache), RMSNorm, RoPE, the K/V write, GQA
+ * attention and the greedy id on the device (cellm_hip.h decode-step ops).
+ * A step decodes up to max_rows (1..4) sessions together: one GEMV per
+ * projection over all their rows, instead of the reference's one session at
+ * a time (crates/cellm-sdk/src/lib.rs:581-599). */
+typedef struct cellm_llama_dev cellm_llama_dev_t;
+
+/* Weights as for cellm_llama_create.  max_blocks: entries per block table
+ * (positions up to max_blocks * tokens_per_block - 1).  The K/V cache starts
+ * zeroed.  The step's launches are captured as one HIP graph per row count
+ * (1..max_rows) here, and steps replay them. */
+int32_t cellm_llama_dev_create(const cellm_llama_config_t* cfg, const cellm_llama_layer_t* layers,
+                               const int8_t* embed_i8, const uint16_t* embed_scale_f16,
+                               const uint16_t* final_norm_f16, int32_t device, int32_t max_rows, int32_t max_blocks,
+                               cellm_llama_dev_t** out);
+
+void cellm_llama_dev_destroy(cellm_llama_dev_t* m);
+
+/* enable = 0: steps enqueue their launches one by one instead of replaying
+ * the captured graph (same kernels, same arguments); 1: replay (default). */
+int32_t cellm_llama_dev_set_graphs(cellm_llama_dev_t* m, int32_t enable);
+
+/* Copy the whole K and V caches (n_elems f16 each, cellm_llama_kv_cache layout)
+ * to / from the device. */
+int32_t cellm_llama_dev_kv_upload(cellm_llama_dev_t* m, const uint16_t* k_f16, const uint16_t* v_f16,
+                                  size_t n_elems);
+int32_t cellm_llama_dev_kv_download(cellm_llama_dev_t* m, uint16_t* k_f16, uint16_t* v_f16, size_t n_elems);
+
+/* One decode step for `rows` sessions: tokens[rows], positions[rows],
+ * block_tables[rows * max_blocks].  Each session writes its K/V at its
+ * position and attends over 0..position.  Returns each greedy id (and its
+ * logit in out_logits, optional); logits_out [rows * vocab] is optional. */
+int32_t cellm_llama_dev_step(cellm_llama_dev_t* m, int32_t rows, const uint32_t* tokens, const int32_t* positions,
+                             const uint32_t* block_tables, uint32_t* out_tokens, float* out_logits, float* logits_out);
+
+/* The RoPE table of the device step: out[p][i] = (cos, sin) of
+ * p * theta^(-2i/head_dim) for p < positions, i < head_dim / 2, in f32 as
+ * rope_non_interleaved_inplace_f32 computes them (cpu_kernels.rs:264-277). */
+int32_t cellm_llama_rope_table(float theta, int32_t head_dim, int32_t positions, float* out);
 
 #ifdef __cplusplus
 }

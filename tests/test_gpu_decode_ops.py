@@ -1,0 +1,253 @@
+"""Decode-step ops on the device (cellm_hip.h: embed, RMSNorm, RoPE, K/V write,
+paged GQA attention, residual add, greedy argmax) against the CPU oracle.
+
+- embed, K/V write, add, argmax, RoPE: bit-exact (RoPE angles come from
+  cellm_llama_rope_table, the same glibc f32 math the oracle's rope uses).
+- RMSNorm: the sum of squares is a tree here and sequential in the reference:
+  relative error <= 1e-6.
+- attention: softmax with the device expf, split-sequence partials combined
+  with rescaling: relative error <= 1e-5 of max|out|.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from _util import rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ops():
+    from cellm_amd import HipOps
+
+    o = HipOps(0)
+    yield o
+    o.close()
+
+
+@pytest.fixture(scope="module")
+def steplib():
+    from cellm_amd import build
+    from cellm_amd._lib import load
+
+    load()
+    lib = C.CDLL(str(build.STEP_LIB_PATH))
+    lib.cellm_llama_rope_table.argtypes = [C.c_float, C.c_int32, C.c_int32, C.c_void_p]
+    return lib
+
+
+def dev(a: np.ndarray):
+    if a.dtype == np.uint32:
+        return torch.from_numpy(a.view(np.int32)).cuda()
+    if a.dtype == np.uint16:
+        return torch.from_numpy(a.view(np.int16)).cuda()
+    return torch.from_numpy(a).cuda()
+
+
+def rope_table(lib, theta, hd, positions):
+    t = np.empty((positions, hd // 2, 2), np.float32)
+    assert lib.cellm_llama_rope_table(theta, hd, positions, t.ctypes.data) == 0
+    return t
+
+
+def test_embed_i8(ops):
+    vocab, hid = 1000, 960
+    emb = oracle.gen_i8((vocab, hid), 0xD0000001)
+    sc = (oracle.gen_uniform((vocab,), 0xD0000002, 0.5, 1.5) / 127).astype(np.float16).view(np.uint16)
+    toks = np.array([3, 999, 1000 + 5, 0], np.uint32)  # token % vocab, as embed_token does
+    out = torch.empty((4, hid), dtype=torch.float32, device="cuda")
+    ops.encode_embed_i8(dev(toks), dev(emb), dev(sc), out)
+    torch.cuda.synchronize()
+    ref = np.stack([emb[t % vocab].astype(np.float32) * oracle.f16_bits_to_f32(sc[t % vocab:t % vocab + 1])[0]
+                    for t in toks])
+    np.testing.assert_array_equal(out.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("wdt", ["f32", "f16"])
+@pytest.mark.parametrize("n", [960, 1152, 7])
+def test_rms_norm(ops, n, wdt):
+    rows = 3
+    x = np.stack([oracle.gen_normal((n,), 0xD0000010 + r, 0.0, 2.0) for r in range(rows)]).astype(np.float32)
+    w = (1.0 + 0.1 * oracle.lcg_fill(n, 0xD0000020, 1.0)).astype(np.float16)
+    wd = w.astype(np.float32) if wdt == "f32" else w
+    out = torch.empty((rows, n), dtype=torch.float32, device="cuda")
+    ops.encode_rms_norm(dev(x), dev(wd), out, 1e-5)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    for r in range(rows):
+        ref = oracle.rms_norm(x[r], w.astype(np.float32), 1e-5)
+        assert rel_err(got[r], ref) <= 1e-6
+
+
+@pytest.mark.parametrize("heads,hd", [(15, 64), (5, 64), (8, 128)])
+def test_rope_half_bit_exact(ops, steplib, heads, hd):
+    positions = np.array([0, 1, 511, 2047], np.int32)
+    theta = 100000.0
+    table = rope_table(steplib, theta, hd, 2048)
+    x = np.stack([oracle.gen_normal((heads * hd,), 0xD0000030 + i, 0.0, 1.0) for i in range(4)]).astype(np.float32)
+    xd = dev(x.copy())
+    ops.encode_rope_half(xd, heads, hd, dev(positions), dev(table))
+    torch.cuda.synchronize()
+    got = xd.cpu().numpy()
+    for r, p in enumerate(positions):
+        ref = oracle.rope_half_(x[r].copy(), heads, hd, int(p), theta)
+        np.testing.assert_array_equal(got[r], ref)
+
+
+def paged_setup(L, tpb, nkv, hd, rows, blocks_per_row, seed):
+    total = rows * blocks_per_row + 3
+    kvd = nkv * hd
+    n = total * L * tpb * kvd
+    k = oracle.gen_normal((n,), seed, 0.0, 1.0).astype(np.float16).view(np.uint16)
+    v = oracle.gen_normal((n,), seed + 1, 0.0, 1.0).astype(np.float16).view(np.uint16)
+    # interleaved, non-contiguous pages per row
+    bt = np.array([[b * rows + r + 3 for b in range(blocks_per_row)] for r in range(rows)], np.uint32)
+    return total, k, v, bt
+
+
+def base_of(bt_row, t, layer, L, tpb, kvd):
+    return int(bt_row[t // tpb]) * (L * tpb * kvd) + layer * (tpb * kvd) + (t % tpb) * kvd
+
+
+def test_kv_write_f16(ops):
+    L, tpb, nkv, hd, rows = 4, 16, 5, 64, 3
+    kvd = nkv * hd
+    total, k0, v0, bt = paged_setup(L, tpb, nkv, hd, rows, 8, 0xD0000040)
+    pos = np.array([0, 17, 127], np.int32)
+    layer = 2
+    kn = np.stack([oracle.gen_normal((kvd,), 0xD0000050 + r, 0.0, 3.0) for r in range(rows)]).astype(np.float32)
+    vn = np.stack([oracle.gen_normal((kvd,), 0xD0000060 + r, 0.0, 3.0) for r in range(rows)]).astype(np.float32)
+    kd, vd = dev(k0.copy()), dev(v0.copy())
+    ops.encode_kv_write(dev(kn), dev(vn), dev(pos), kd, vd, dev(bt), total, L, tpb, layer)
+    torch.cuda.synchronize()
+    k_ref, v_ref = k0.copy(), v0.copy()
+    for r in range(rows):
+        b = base_of(bt[r], int(pos[r]), layer, L, tpb, kvd)
+        k_ref[b:b + kvd] = kn[r].astype(np.float16).view(np.uint16)  # write_token_f32: f16 RNE
+        v_ref[b:b + kvd] = vn[r].astype(np.float16).view(np.uint16)
+    np.testing.assert_array_equal(kd.cpu().numpy().view(np.uint16), k_ref)
+    np.testing.assert_array_equal(vd.cpu().numpy().view(np.uint16), v_ref)
+
+
+@pytest.mark.parametrize("nh,nkv,hd,blocks,pos", [
+    (15, 5, 64, 34, (0, 31, 64, 543)),      # G 3: seq 1, half a chunk, chunk + 1, 9 chunks
+    (8, 8, 128, 34, (63, 64, 127, 543)),    # G 1, head_dim 128
+    (14, 2, 64, 34, (0, 100, 200, 543)),    # G 7
+    (8, 4, 64, 8, (5, 127, 0, 64)),         # G 2, a short table
+    (16, 2, 128, 132, (2099, 1024, 1, 700)),  # G 8: 33 chunks, past the combine's preloaded 16
+])
+def test_attention_gqa_f16kv(ops, nh, nkv, hd, blocks, pos):
+    L, tpb, rows = 3, 16, 4
+    kvd = nkv * hd
+    total, k, v, bt = paged_setup(L, tpb, nkv, hd, rows, blocks, 0xD0000070 + nh)
+    pos = np.array(pos, np.int32)
+    layer = 1
+    q = np.stack([oracle.gen_normal((nh * hd,), 0xD0000080 + r, 0.0, 1.0) for r in range(rows)]).astype(np.float32)
+    out = torch.empty((rows, nh * hd), dtype=torch.float32, device="cuda")
+    ops.encode_attention(dev(q), dev(k), dev(v), dev(bt), dev(pos), out, nh, nkv, hd, total, L, tpb, layer)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    for r in range(rows):
+        seq = int(pos[r]) + 1
+        bases = np.array([base_of(bt[r], t, layer, L, tpb, kvd) for t in range(seq)], np.uint64)
+        ref = oracle.attention_gqa_f16kv(k, v, bases, q[r], nh, nkv, hd)
+        assert rel_err(got[r], ref) <= 1e-5, (r, rel_err(got[r], ref))
+
+
+def test_attention_rejects_unsupported_head_dim(ops):
+    from cellm_amd._lib import CellmHipError
+
+    z = torch.zeros(64, dtype=torch.float32, device="cuda")
+    with pytest.raises(CellmHipError):
+        ops.encode_attention(z, z, z, torch.zeros((1, 1), dtype=torch.int32, device="cuda"),
+                             torch.zeros(1, dtype=torch.int32, device="cuda"), z, 1, 1, 96, 1, 1, 16, 0)
+
+
+def test_argmax_first_and_non_finite(ops):
+    n = 49152
+    rows = np.stack([oracle.gen_normal((n,), 0xD0000090 + r, 0.0, 1.0) for r in range(4)]).astype(np.float32)
+    rows[1, 100] = rows[1, 40000] = 50.0          # a tie: the first index wins
+    rows[2, 7] = np.nan                           # NaN -> -inf
+    rows[2, 9] = np.inf                           # +inf -> -inf too (not finite)
+    rows[3, :] = -np.inf                          # all -inf: index 0
+    idx = torch.empty(4, dtype=torch.int32, device="cuda")
+    val = torch.empty(4, dtype=torch.float32, device="cuda")
+    ops.encode_argmax(dev(rows), idx, val)
+    torch.cuda.synchronize()
+    got = idx.cpu().numpy()
+    for r in range(4):
+        z = rows[r].copy()
+        z[~np.isfinite(z)] = -np.inf
+        assert got[r] == oracle.argmax_first(z), r
+    assert got[1] == 100
+
+
+def test_add_inplace(ops):
+    a = oracle.gen_normal((5000,), 0xD00000A0, 0.0, 1.0).astype(np.float32)
+    b = oracle.gen_normal((5000,), 0xD00000A1, 0.0, 1.0).astype(np.float32)
+    ad = dev(a.copy())
+    ops.encode_add_inplace(ad, dev(b))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(ad.cpu().numpy(), a + b)
+
+
+@pytest.mark.parametrize("wdt", ["f32", "f16"])
+def test_add_rms_norm(ops, wdt):
+    """x += y, then rms_norm(x): x is exactly a + b; out is what add followed by
+    rms_norm gives (the same kernel arithmetic), within 1e-6 of the oracle."""
+    rows, n = 4, 960
+    a = np.stack([oracle.gen_normal((n,), 0xD00000B0 + r, 0.0, 2.0) for r in range(rows)]).astype(np.float32)
+    b = np.stack([oracle.gen_normal((n,), 0xD00000C0 + r, 0.0, 1.0) for r in range(rows)]).astype(np.float32)
+    w = (1.0 + 0.1 * oracle.lcg_fill(n, 0xD00000D0, 1.0)).astype(np.float16)
+    wd = dev(w.astype(np.float32) if wdt == "f32" else w)
+    xd = dev(a.copy())
+    out = torch.empty((rows, n), dtype=torch.float32, device="cuda")
+    ops.encode_add_rms_norm(xd, dev(b), wd, out, 1e-5)
+    x2 = dev(a.copy())
+    ops.encode_add_inplace(x2, dev(b))
+    out2 = torch.empty_like(out)
+    ops.encode_rms_norm(x2, wd, out2, 1e-5)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(xd.cpu().numpy(), a + b)
+    np.testing.assert_array_equal(out.cpu().numpy(), out2.cpu().numpy())
+    got = out.cpu().numpy()
+    for r in range(rows):
+        assert rel_err(got[r], oracle.rms_norm(a[r] + b[r], w.astype(np.float32), 1e-5)) <= 1e-6
+
+
+@pytest.mark.parametrize("nh,nkv,hd", [(15, 5, 64), (16, 2, 128)])
+def test_rope_kv_write_matches_rope_then_write(ops, steplib, nh, nkv, hd):
+    """One launch = rope on q, rope on k, then the K/V write: q and k bit-exact
+    against the oracle's RoPE, the cache rows bit-exact against f16(k), f16(v),
+    every other cache element untouched; a negative position writes nothing."""
+    L, tpb, rows, layer, theta = 3, 16, 4, 1, 10000.0
+    kvd = nkv * hd
+    total, k0, v0, bt = paged_setup(L, tpb, nkv, hd, rows, 8, 0xD00000E0 + nh)
+    pos = np.array([0, 17, 127, -1], np.int32)
+    table = rope_table(steplib, theta, hd, 8 * tpb)
+    q = np.stack([oracle.gen_normal((nh * hd,), 0xD00000F0 + r, 0.0, 1.0) for r in range(rows)]).astype(np.float32)
+    k = np.stack([oracle.gen_normal((kvd,), 0xD0000100 + r, 0.0, 1.0) for r in range(rows)]).astype(np.float32)
+    v = np.stack([oracle.gen_normal((kvd,), 0xD0000110 + r, 0.0, 1.0) for r in range(rows)]).astype(np.float32)
+    qd, kd, vd = dev(q.copy()), dev(k.copy()), dev(v.copy())
+    kc, vc = dev(k0.copy()), dev(v0.copy())
+    ops.encode_rope_kv_write(qd, kd, vd, nh, nkv, hd, dev(pos), dev(table), kc, vc, dev(bt), total, L, tpb, layer)
+    torch.cuda.synchronize()
+    gq, gk = qd.cpu().numpy(), kd.cpu().numpy()
+    k_ref, v_ref = k0.copy(), v0.copy()
+    for r in range(rows):
+        p = max(int(pos[r]), 0)
+        np.testing.assert_array_equal(gq[r], oracle.rope_half_(q[r].copy(), nh, hd, p, theta))
+        kr = oracle.rope_half_(k[r].copy(), nkv, hd, p, theta)
+        np.testing.assert_array_equal(gk[r], kr)
+        if pos[r] >= 0:
+            b = base_of(bt[r], int(pos[r]), layer, L, tpb, kvd)
+            k_ref[b:b + kvd] = kr.astype(np.float16).view(np.uint16)
+            v_ref[b:b + kvd] = v[r].astype(np.float16).view(np.uint16)
+    np.testing.assert_array_equal(kc.cpu().numpy().view(np.uint16), k_ref)
+    np.testing.assert_array_equal(vc.cpu().numpy().view(np.uint16), v_ref)

@@ -4,8 +4,10 @@
 vocab 49152, int8 per-row weights.  Context 512 of seeded f16 KV, 4 sessions
 decoded one at a time (crates/cellm-sdk/src/lib.rs:622-680).
 
-The HIP side is libcellm_llama_step.so: projections on the HIP qGEMV,
-embedding/RMSNorm/RoPE/paged KV/attention on the CPU.  The reference side is
+Two HIP runners in libcellm_llama_step.so: cellm_llama_step (projections on
+the HIP qGEMV, embedding/RMSNorm/RoPE/paged KV/attention on the CPU) and
+cellm_llama_dev_step (the whole step on the device, several sessions per pass
+over the weights, replayed from a captured HIP graph).  The reference side is
 the all-CPU oracle step (LlamaRunner::step_inner, llama.rs:235-647, with the
 i8 lm_head loop of llama.rs:602-643).  Greedy ids must be identical.
 """
@@ -175,3 +177,150 @@ def test_decode_step_greedy_ids_match_cpu_reference():
         assert np.array_equal(np.flatnonzero(hk != k0), np.flatnonzero(ok != k0))
     finally:
         lib.cellm_llama_destroy(h)
+
+
+def dev_lib():
+    from cellm_amd import build
+    from cellm_amd._lib import load
+
+    load()
+    lib = C.CDLL(str(build.STEP_LIB_PATH))
+    lib.cellm_llama_dev_create.argtypes = [C.POINTER(Config), C.POINTER(Layer), C.c_void_p, C.c_void_p, C.c_void_p,
+                                           C.c_int32, C.c_int32, C.c_int32, C.POINTER(C.c_void_p)]
+    lib.cellm_llama_dev_kv_upload.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t]
+    lib.cellm_llama_dev_kv_download.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_size_t]
+    lib.cellm_llama_dev_step.argtypes = [C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                         C.c_void_p, C.c_void_p]
+    lib.cellm_llama_dev_set_graphs.argtypes = [C.c_void_p, C.c_int32]
+    lib.cellm_llama_dev_destroy.argtypes = [C.c_void_p]
+    lib.cellm_llama_last_error_message.restype = C.c_size_t
+    lib.cellm_llama_last_error_message.argtypes = [C.c_char_p, C.c_size_t]
+    return lib
+
+
+def lib_err(lib):
+    b = C.create_string_buffer(1024)
+    lib.cellm_llama_last_error_message(b, 1024)
+    return b.value.decode()
+
+
+def dev_create(lib, model, max_rows):
+    layers, embed, escale, fnorm = model
+    cl = (Layer * L)()
+    for l, (ws, ss, n1, n2) in enumerate(layers):
+        for j in range(7):
+            cl[l].w[j] = ws[j].ctypes.data
+            cl[l].scale_f16[j] = ss[j].ctypes.data
+        cl[l].input_layernorm_f16 = n1.ctypes.data
+        cl[l].post_attention_layernorm_f16 = n2.ctypes.data
+    cfg = Config(L, HID, NH, NKV, HD, INTER, VOCAB, EPS, THETA, TPB, TOTAL_BLOCKS)
+    h = C.c_void_p()
+    rc = lib.cellm_llama_dev_create(C.byref(cfg), cl, embed.ctypes.data, escale.ctypes.data, fnorm.ctypes.data, 0,
+                                    max_rows, BLOCKS_PER_SESSION, C.byref(h))
+    assert rc == 0, lib_err(lib)
+    return h
+
+
+def dev_step(lib, h, tokens, positions, bts):
+    rows = len(tokens)
+    out_tok = np.empty(rows, np.uint32)
+    out_logit = np.empty(rows, np.float32)
+    logits = np.empty((rows, VOCAB), np.float32)
+    rc = lib.cellm_llama_dev_step(h, rows, tokens.ctypes.data, positions.ctypes.data, bts.ctypes.data,
+                                  out_tok.ctypes.data, out_logit.ctypes.data, logits.ctypes.data)
+    assert rc == 0, lib_err(lib)
+    return out_tok, out_logit, logits
+
+
+def test_device_step_batched_sessions_match_cpu_reference():
+    """cellm_llama_dev_step: the whole step on the device (RMSNorm, RoPE, K/V
+    write, attention, greedy id in HIP), the 4 sessions decoded together in one
+    pass over the weights; two consecutive steps so the second reads the K/V
+    rows the first wrote.  Greedy ids must equal the CPU reference's."""
+    lib = dev_lib()
+    model = make_model()
+    h = dev_create(lib, model, SESSIONS)
+    err = lambda: lib_err(lib)  # noqa: E731
+    try:
+        k0, v0 = make_kv()
+        assert lib.cellm_llama_dev_kv_upload(h, k0.ctypes.data, v0.ctypes.data, k0.size) == 0, err()
+        ok, ov = k0.copy(), v0.copy()
+        bts = np.stack([block_table(s) for s in range(SESSIONS)]).astype(np.uint32)
+        tokens = np.array([(1000 + 7919 * s) % VOCAB for s in range(SESSIONS)], np.uint32)
+        for pos in (CTX - 2, CTX - 1):
+            positions = np.full(SESSIONS, pos, np.int32)
+            out_tok, out_logit, logits = dev_step(lib, h, tokens, positions, bts)
+            for s in range(SESSIONS):
+                ref_id, ref_logits = oracle_step(model, ok, ov, int(tokens[s]), pos, bts[s])
+                rel = float(np.max(np.abs(logits[s] - ref_logits)) / np.max(np.abs(ref_logits)))
+                top2 = np.sort(ref_logits)[-2:]
+                print(f"pos {pos} session {s}: token {tokens[s]} -> device {out_tok[s]} ref {ref_id} "
+                      f"top2 margin {float(top2[1] - top2[0]):.4g} logits rel err {rel:.2e}")
+                assert out_tok[s] == ref_id
+                assert out_logit[s] == logits[s, out_tok[s]]
+                assert rel <= 1e-3
+            tokens = out_tok.copy()
+        # K/V: the rows of positions CTX-2 and CTX-1 of every session and layer were written, nothing
+        # else changed; the written values are within f16 rounding of the reference's (the projections
+        # sum in a different order)
+        hk = np.empty_like(k0)
+        hv = np.empty_like(v0)
+        assert lib.cellm_llama_dev_kv_download(h, hk.ctypes.data, hv.ctypes.data, hk.size) == 0, err()
+        written = np.zeros(k0.size, bool)
+        for s in range(SESSIONS):
+            for layer in range(L):
+                for pos in (CTX - 2, CTX - 1):
+                    b = base_of(bts[s], pos, layer)
+                    written[b:b + KVD] = True
+        for got, init, ref in ((hk, k0, ok), (hv, v0, ov)):
+            np.testing.assert_array_equal(got[~written], init[~written])
+            d = np.abs(oracle.f16_bits_to_f32(got[written]) - oracle.f16_bits_to_f32(ref[written]))
+            assert float(d.max()) <= 1e-2 * float(np.abs(oracle.f16_bits_to_f32(ref[written])).max())
+    finally:
+        lib.cellm_llama_dev_destroy(h)
+
+
+def test_device_step_graph_replays_match_eager_launches():
+    """The captured graph and the eager launch sequence give bit-identical ids,
+    logits and K/V, on several replays of each row count with eager steps in
+    between (a step rewrites the same K/V row with the same values, so
+    repeating it leaves the state unchanged)."""
+    lib = dev_lib()
+    model = make_model()
+    h = dev_create(lib, model, SESSIONS)
+    try:
+        k0, v0 = make_kv()
+        assert lib.cellm_llama_dev_kv_upload(h, k0.ctypes.data, v0.ctypes.data, k0.size) == 0, lib_err(lib)
+        bts = np.stack([block_table(s) for s in range(SESSIONS)]).astype(np.uint32)
+        for rows in (4, 1, 3, 4):
+            tokens = np.array([(31 + 977 * s + rows) % VOCAB for s in range(rows)], np.uint32)
+            positions = np.array([CTX - 1 - 37 * s for s in range(rows)], np.int32)
+            b = np.ascontiguousarray(bts[:rows])
+            assert lib.cellm_llama_dev_set_graphs(h, 0) == 0, lib_err(lib)
+            e_tok, e_logit, e_logits = dev_step(lib, h, tokens, positions, b)
+            assert lib.cellm_llama_dev_set_graphs(h, 1) == 0, lib_err(lib)
+            for rep in range(3):
+                g_tok, g_logit, g_logits = dev_step(lib, h, tokens, positions, b)
+                np.testing.assert_array_equal(g_tok, e_tok)
+                np.testing.assert_array_equal(g_logit, e_logit)
+                np.testing.assert_array_equal(g_logits, e_logits)
+            print(f"rows {rows}: ids {e_tok.tolist()} identical over 3 graph replays")
+        hk = np.empty_like(k0)
+        hv = np.empty_like(v0)
+        assert lib.cellm_llama_dev_kv_download(h, hk.ctypes.data, hv.ctypes.data, hk.size) == 0, lib_err(lib)
+        assert lib.cellm_llama_dev_set_graphs(h, 0) == 0, lib_err(lib)
+        tokens = np.array([5], np.uint32)
+        positions = np.array([CTX - 1], np.int32)
+        dev_step(lib, h, tokens, positions, np.ascontiguousarray(bts[:1]))
+        hk2 = np.empty_like(k0)
+        hv2 = np.empty_like(v0)
+        assert lib.cellm_llama_dev_kv_download(h, hk2.ctypes.data, hv2.ctypes.data, hk.size) == 0, lib_err(lib)
+        # an eager step with other inputs changes only its own K/V rows
+        allowed = np.zeros(k0.size, bool)
+        for layer in range(L):
+            bb = base_of(bts[0], CTX - 1, layer)
+            allowed[bb:bb + KVD] = True
+        assert not np.any(((hk2 != hk) | (hv2 != hv)) & ~allowed)
+        assert np.any(hk2[allowed] != hk[allowed])
+    finally:
+        lib.cellm_llama_dev_destroy(h)
