@@ -82,26 +82,58 @@ __global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(float* __res
                                                                    const void* __restrict__ w, float* __restrict__ out,
                                                                    int n, float eps)
 {
+    constexpr int kRegs = 8;  // rows up to kRegs * kNormThreads stay in registers: one memory latency
     __shared__ float part[kNormThreads / 64];
-    const int r = blockIdx.x;
+    const int r = blockIdx.x, t = threadIdx.x;
     float* xr = x + (size_t)r * n;
     const float* yr = y + (size_t)r * n;
+    float* orow = out + (size_t)r * n;
     float s = 0.0f;
-    for (int i = threadIdx.x; i < n; i += kNormThreads) {
-        const float v = xr[i] + yr[i];
-        xr[i] = v;
-        s = s + v * v;
+    const bool in_regs = n <= kRegs * kNormThreads;
+    float xv[kRegs], wv[kRegs];
+    if (in_regs) {
+        float yv[kRegs];
+#pragma unroll
+        for (int u = 0; u < kRegs; ++u) {
+            const int i = min(t + u * kNormThreads, n - 1);
+            xv[u] = xr[i];
+            yv[u] = yr[i];
+            wv[u] = load_f32<WDT>(w, i);
+        }
+#pragma unroll
+        for (int u = 0; u < kRegs; ++u) {
+            const int i = t + u * kNormThreads;
+            if (i < n) {
+                const float v = xv[u] + yv[u];
+                xv[u] = v;
+                xr[i] = v;
+                s = s + v * v;
+            }
+        }
+    } else {
+        for (int i = t; i < n; i += kNormThreads) {
+            const float v = xr[i] + yr[i];
+            xr[i] = v;
+            s = s + v * v;
+        }
     }
     s = group_sum<64>(s);
-    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = s;
+    if ((t & 63) == 0) part[t >> 6] = s;
     __syncthreads();
     float tot = 0.0f;
 #pragma unroll
     for (int i = 0; i < kNormThreads / 64; ++i) tot = tot + part[i];
     const float mean = tot / (float)n;
     const float inv = 1.0f / sqrtf(mean + eps);
-    for (int i = threadIdx.x; i < n; i += kNormThreads)
-        out[(size_t)r * n + i] = xr[i] * inv * load_f32<WDT>(w, i);
+    if (in_regs) {
+#pragma unroll
+        for (int u = 0; u < kRegs; ++u) {
+            const int i = t + u * kNormThreads;
+            if (i < n) orow[i] = xv[u] * inv * wv[u];
+        }
+    } else {
+        for (int i = t; i < n; i += kNormThreads) orow[i] = xr[i] * inv * load_f32<WDT>(w, i);
+    }
 }
 
 // One thread per (row, head, i < half).  cs[p][i] = (cos, sin) of position p.
@@ -415,22 +447,50 @@ __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(const float*
     }
 }
 
-__global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ logits, int n, int32_t* __restrict__ idx,
-                                                     float* __restrict__ val)
+__device__ __forceinline__ void argmax_take(float v, int i, float& best, int& bi)
 {
-    __shared__ float sv[4];
-    __shared__ int si[4];
-    const int r = blockIdx.x;
+    if (!isfinite(v)) v = -INFINITY;          // llama.rs:1081-1092
+    if (v > best || bi == 0x7fffffff) {       // strictly greater keeps the first maximum
+        best = v;
+        bi = i;
+    }
+}
+
+// One block per row.  Each thread visits its elements in increasing index
+// order; with 16-byte rows it first loads up to kArgmaxUnroll float4 at once
+// (one memory latency for a 64K-entry row), addresses clamped in range.
+constexpr int kArgmaxThreads = 1024;
+constexpr int kArgmaxUnroll = 16;
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __restrict__ logits, int n,
+                                                                int32_t* __restrict__ idx, float* __restrict__ val)
+{
+    __shared__ float sv[kArgmaxThreads / 64];
+    __shared__ int si[kArgmaxThreads / 64];
+    const int r = blockIdx.x, t = threadIdx.x;
     const float* z = logits + (size_t)r * n;
     float best = -INFINITY;
     int bi = 0x7fffffff;
-    for (int i = threadIdx.x; i < n; i += 256) {
-        float v = z[i];
-        if (!isfinite(v)) v = -INFINITY;  // llama.rs:1081-1092
-        if (v > best || bi == 0x7fffffff) {  // strictly greater keeps the first maximum
-            best = v;
-            bi = i;
+    if ((n & 3) == 0 && (reinterpret_cast<uintptr_t>(z) & 15) == 0) {
+        const float4* z4 = reinterpret_cast<const float4*>(z);
+        const int n4 = n >> 2;
+        for (int j0 = t; j0 < n4; j0 += kArgmaxUnroll * kArgmaxThreads) {
+            float4 a[kArgmaxUnroll];
+#pragma unroll
+            for (int u = 0; u < kArgmaxUnroll; ++u) a[u] = z4[min(j0 + u * kArgmaxThreads, n4 - 1)];
+#pragma unroll
+            for (int u = 0; u < kArgmaxUnroll; ++u) {
+                const int j = j0 + u * kArgmaxThreads;
+                if (j < n4) {
+                    argmax_take(a[u].x, 4 * j, best, bi);
+                    argmax_take(a[u].y, 4 * j + 1, best, bi);
+                    argmax_take(a[u].z, 4 * j + 2, best, bi);
+                    argmax_take(a[u].w, 4 * j + 3, best, bi);
+                }
+            }
         }
+    } else {
+        for (int i = t; i < n; i += kArgmaxThreads) argmax_take(z[i], i, best, bi);
     }
     // (value, index) max with the lowest index among equal values: the first maximum
     for (int off = 32; off > 0; off >>= 1) {
@@ -441,13 +501,13 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ l
             bi = oi;
         }
     }
-    if ((threadIdx.x & 63) == 0) {
-        sv[threadIdx.x >> 6] = best;
-        si[threadIdx.x >> 6] = bi;
+    if ((t & 63) == 0) {
+        sv[t >> 6] = best;
+        si[t >> 6] = bi;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int w = 1; w < 4; ++w)
+    if (t == 0) {
+        for (int w = 1; w < kArgmaxThreads / 64; ++w)
             if (sv[w] > best || (sv[w] == best && si[w] < bi)) {
                 best = sv[w];
                 bi = si[w];
@@ -581,7 +641,7 @@ hipError_t launch_attention_gqa_f16kv(const float* q, const uint16_t* kcache, co
 
 hipError_t launch_argmax(const float* logits, int rows, int n, int32_t* idx, float* val, hipStream_t st)
 {
-    hipLaunchKernelGGL(argmax_kernel, dim3(rows), dim3(256), 0, st, logits, n, idx, val);
+    hipLaunchKernelGGL(argmax_kernel, dim3(rows), dim3(kArgmaxThreads), 0, st, logits, n, idx, val);
     return hipGetLastError();
 }
 

@@ -169,8 +169,8 @@ def test_attention_rejects_unsupported_head_dim(ops):
                              torch.zeros(1, dtype=torch.int32, device="cuda"), z, 1, 1, 96, 1, 1, 16, 0)
 
 
-def test_argmax_first_and_non_finite(ops):
-    n = 49152
+@pytest.mark.parametrize("n", [49152, 49151, 131072])
+def test_argmax_first_and_non_finite(ops, n):
     rows = np.stack([oracle.gen_normal((n,), 0xD0000090 + r, 0.0, 1.0) for r in range(4)]).astype(np.float32)
     rows[1, 100] = rows[1, 40000] = 50.0          # a tie: the first index wins
     rows[2, 7] = np.nan                           # NaN -> -inf
@@ -198,10 +198,12 @@ def test_add_inplace(ops):
 
 
 @pytest.mark.parametrize("wdt", ["f32", "f16"])
-def test_add_rms_norm(ops, wdt):
+@pytest.mark.parametrize("n", [960, 2048, 2049, 5])
+def test_add_rms_norm(ops, wdt, n):
     """x += y, then rms_norm(x): x is exactly a + b; out is what add followed by
-    rms_norm gives (the same kernel arithmetic), within 1e-6 of the oracle."""
-    rows, n = 4, 960
+    rms_norm gives (the same kernel arithmetic), within 1e-6 of the oracle.
+    n 2048 is the largest row kept in registers, 2049 takes the loop."""
+    rows = 4
     a = np.stack([oracle.gen_normal((n,), 0xD00000B0 + r, 0.0, 2.0) for r in range(rows)]).astype(np.float32)
     b = np.stack([oracle.gen_normal((n,), 0xD00000C0 + r, 0.0, 1.0) for r in range(rows)]).astype(np.float32)
     w = (1.0 + 0.1 * oracle.lcg_fill(n, 0xD00000D0, 1.0)).astype(np.float16)
