@@ -21,7 +21,7 @@ DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 
 _vp, _sz, _i32, _i64 = C.c_void_p, C.c_size_t, C.c_int32, C.c_int64
 
-OP_QGEMV_I8, OP_QGEMV_Q4_AFFINE = 0, 1
+OP_QGEMV_I8, OP_QGEMV_Q4_AFFINE, OP_QGEMV_F16, OP_QGEMV_I2, OP_QGEMV_Q1_0_G128 = 0, 1, 2, 3, 4
 
 
 class QgemvOp(C.Structure):
@@ -61,6 +61,9 @@ SIGNATURES = {
     "cellm_hip_logits_q4_affine": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _sz, _sz, C.c_char_p, _vp]),
     "cellm_hip_embed_i8": (_i32, [_vp, _vp, _i64, _vp, _vp, _i64, _i64, _vp, _vp]),
     "cellm_hip_rms_norm": (_i32, [_vp, _vp, _vp, _i32, _i64, _i64, C.c_float, _vp, _vp]),
+    "cellm_hip_qgemv_f16": (_i32, [_vp, _vp, _vp, _i32, _vp, _i64, _i64, _i64, _vp]),
+    "cellm_hip_qgemv_i2": (_i32, [_vp, _vp, _vp, _i32, _vp, _i32, _vp, _i64, _i64, _i64, _vp]),
+    "cellm_hip_qgemv_q1_0_g128": (_i32, [_vp, _vp, _vp, _i32, _vp, _i64, _i64, _i64, _vp]),
     "cellm_hip_add_rms_norm": (_i32, [_vp, _vp, _vp, _vp, _i32, _i64, _i64, C.c_float, _vp, _vp]),
     "cellm_hip_rope_half_f32": (_i32, [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp]),
     "cellm_hip_rope_kv_write_f16": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp,

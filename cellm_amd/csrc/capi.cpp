@@ -196,6 +196,30 @@ int32_t qgemv_i8_impl(cellm_hip_ctx* ctx, const int8_t* w, const void* scales, i
     return CELLM_HIP_OK;
 }
 
+// f16 / i2 / q1_0_g128 row GEMVs (lowbit.hip)
+int32_t qgemv_lowbit_impl(int fmt, const void* w, const uint16_t* scales_f16, int32_t scale_mode, const void* x,
+                          int32_t xdt, float* y, int64_t m, int64_t n, int64_t k, hipStream_t st)
+{
+    if (int32_t rc = check_dims(m, n, k)) return rc;
+    if (!valid_dtype(xdt)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "bad dtype");
+    if (fmt == LB_Q1 && k % 128 != 0)
+        return set_error(CELLM_HIP_ERR_INVALID_ARG, "q1_0_g128 needs k %% 128 == 0 (k=%lld)", (long long)k);
+    if (fmt == LB_I2 && scale_mode != 0 && scale_mode != 1)
+        return set_error(CELLM_HIP_ERR_INVALID_ARG, "i2 scale_mode must be 0 (at the end) or 1 (per element)");
+    if (m == 0 || n == 0) return CELLM_HIP_OK;
+    if ((k > 0 && (!w || !x)) || !y || (fmt == LB_I2 && !scales_f16))
+        return set_error(CELLM_HIP_ERR_INVALID_ARG, "null pointer");
+    if (fmt == LB_F16 && (reinterpret_cast<uintptr_t>(w) & 1))
+        return set_error(CELLM_HIP_ERR_INVALID_ARG, "f16 weights must be 2-byte aligned");
+    if (k == 0) {
+        HIP_TRY(hipMemsetAsync(y, 0, (size_t)m * n * sizeof(float), st), "hipMemsetAsync(y)");
+        return CELLM_HIP_OK;
+    }
+    HIP_TRY(launch_qgemv_lowbit(fmt, w, scales_f16, scale_mode, x, xdt, y, (int)m, (int)n, (int)k, st),
+            "qgemv lowbit launch");
+    return CELLM_HIP_OK;
+}
+
 int32_t qgemv_q4_impl(cellm_hip_ctx* ctx, const uint32_t* wq, const void* scales, const void* biases, int32_t sbt,
                       int64_t group, const void* x, int32_t xdt, float* y, int64_t m, int64_t n, int64_t k,
                       hipStream_t st, bool force_gemm)
@@ -545,6 +569,13 @@ int32_t cellm_hip_qgemv_batch(cellm_hip_ctx_t* ctx, const cellm_hip_qgemv_op_t* 
         else if (o.kind == CELLM_HIP_OP_QGEMV_Q4_AFFINE)
             rc = qgemv_q4_impl(ctx, static_cast<const uint32_t*>(o.w), o.scales, o.biases, o.sb_dtype, o.group, o.x,
                                o.x_dtype, o.y, o.m, o.n, o.k, st, false);
+        else if (o.kind == CELLM_HIP_OP_QGEMV_F16)
+            rc = qgemv_lowbit_impl(LB_F16, o.w, nullptr, 0, o.x, o.x_dtype, o.y, o.m, o.n, o.k, st);
+        else if (o.kind == CELLM_HIP_OP_QGEMV_I2)
+            rc = qgemv_lowbit_impl(LB_I2, o.w, static_cast<const uint16_t*>(o.scales), o.group, o.x, o.x_dtype, o.y,
+                                   o.m, o.n, o.k, st);
+        else if (o.kind == CELLM_HIP_OP_QGEMV_Q1_0_G128)
+            rc = qgemv_lowbit_impl(LB_Q1, o.w, nullptr, 0, o.x, o.x_dtype, o.y, o.m, o.n, o.k, st);
         else
             rc = set_error(CELLM_HIP_ERR_INVALID_ARG, "op %lld: unknown kind %d", (long long)i, (int)o.kind);
         if (rc) return rc;
@@ -611,6 +642,30 @@ int32_t cellm_hip_qgemv_i4_sym(cellm_hip_ctx_t* ctx, const uint8_t* w, const uin
                                 pick_stream(ctx, stream)),
             "qgemv_i4_sym launch");
     return CELLM_HIP_OK;
+}
+
+int32_t cellm_hip_qgemv_f16(cellm_hip_ctx_t* ctx, const uint16_t* w_f16, const void* x, int32_t x_dtype, float* y,
+                            int64_t m, int64_t n, int64_t k, void* stream)
+{
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    DeviceGuard g(ctx->device);
+    return qgemv_lowbit_impl(LB_F16, w_f16, nullptr, 0, x, x_dtype, y, m, n, k, pick_stream(ctx, stream));
+}
+
+int32_t cellm_hip_qgemv_i2(cellm_hip_ctx_t* ctx, const uint8_t* w, const uint16_t* scales_f16, int32_t scale_mode,
+                           const void* x, int32_t x_dtype, float* y, int64_t m, int64_t n, int64_t k, void* stream)
+{
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    DeviceGuard g(ctx->device);
+    return qgemv_lowbit_impl(LB_I2, w, scales_f16, scale_mode, x, x_dtype, y, m, n, k, pick_stream(ctx, stream));
+}
+
+int32_t cellm_hip_qgemv_q1_0_g128(cellm_hip_ctx_t* ctx, const uint8_t* w, const void* x, int32_t x_dtype, float* y,
+                                  int64_t m, int64_t n, int64_t k, void* stream)
+{
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    DeviceGuard g(ctx->device);
+    return qgemv_lowbit_impl(LB_Q1, w, nullptr, 0, x, x_dtype, y, m, n, k, pick_stream(ctx, stream));
 }
 
 int32_t cellm_hip_qgemm_q4_affine(cellm_hip_ctx_t* ctx, const uint32_t* wq, const void* scales, const void* biases,

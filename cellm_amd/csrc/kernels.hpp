@@ -93,6 +93,13 @@ hipError_t launch_attention_gqa_f16kv(const float* q, const uint16_t* kcache, co
                                       hipStream_t st);
 hipError_t launch_argmax(const float* logits, int rows, int n, int32_t* idx, float* val, hipStream_t st);
 
+// Remaining .cellm weight formats (lowbit.hip): f16 rows, i2 (2-bit per-row
+// symmetric, scale_mode 0 = scale at the end, 1 = per element), q1_0_g128.
+enum { LB_F16 = 0, LB_I2 = 1, LB_Q1 = 2 };
+size_t lowbit_row_bytes(int fmt, int K);
+hipError_t launch_qgemv_lowbit(int fmt, const void* w, const uint16_t* S, int scale_mode, const void* x, int xdt,
+                               float* y, int M, int N, int K, hipStream_t st);
+
 // Device smoke test kernel: out[i] = a[i] + b[i].
 hipError_t launch_add_f32(const float* a, const float* b, float* out, int n, hipStream_t st);
 

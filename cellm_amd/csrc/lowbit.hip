@@ -1,0 +1,301 @@
+// Row GEMVs for the remaining .cellm weight formats (gfx950):
+//
+//   f16        W [N][K] f16                         cpu_kernels.rs:135-214 (matmul_f16_f32)
+//   i2         W [N][ceil(K/4)] u8, 2-bit codes low bits first, one f16 scale per row;
+//              value = centroid(code) in {-1.5, -0.5, 0.5, 1.5}
+//                scale mode 0 (Qwen, qwen.rs:1591-1606):   y = (sum x * c) * s
+//                scale mode 1 (Gemma, gemma.rs:1673-1687): y = sum x * (c * s)
+//   q1_0_g128  W [N][K/128 blocks of 18 B]: f16 d (little endian) + 128 sign bits,
+//              element 8b+j = bit j of byte b, value d if set else -d
+//              (qwen.rs:1004-1022, metal.rs:542-570)
+//
+// Layout of the fast kernel: a team of LPR lanes per output row; each lane
+// streams whole units of the row (16 bytes: 8 f16 or 64 i2 codes; one 18-byte
+// q1 block of 128 elements) and multiplies them with the matching activations
+// staged in LDS as f32 for up to MT activation rows.  The lanes of a team read
+// x at a stride of one unit (64 or 128 elements for i2 / q1), which would put
+// every lane on the same LDS banks, so each unit of x is followed by 4 floats
+// of padding.  Sums are per-lane then a team butterfly, compared with the
+// reference's sequential sums at a relative tolerance.  Shapes the fast kernel
+// does not take (unaligned rows, K that is not a whole number of units, rows
+// too long for LDS) use a one-wave-per-row kernel that reads x from memory.
+#include <algorithm>
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace cellm {
+
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kPad = 4;  // floats of LDS padding after each unit of x
+
+template <int FMT>
+struct LowbitFmt;
+template <>
+struct LowbitFmt<LB_F16> {
+    static constexpr int kElems = 8;  // elements per 16-byte unit
+};
+template <>
+struct LowbitFmt<LB_I2> {
+    static constexpr int kElems = 64;
+};
+template <>
+struct LowbitFmt<LB_Q1> {
+    static constexpr int kElems = 128;  // one 18-byte block
+};
+
+__device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+// i2 centroid table: t[c] for code c (mode 1 folds the row scale in)
+struct I2Table {
+    float t0, t1, t2, t3;
+    __device__ __forceinline__ float operator()(uint32_t c) const
+    {
+        const float lo = (c & 1u) ? t1 : t0;
+        const float hi = (c & 1u) ? t3 : t2;
+        return (c & 2u) ? hi : lo;
+    }
+};
+
+__device__ __forceinline__ I2Table i2_table(float s, int mode)
+{
+    if (mode == 0) return I2Table{-1.5f, -0.5f, 0.5f, 1.5f};
+    return I2Table{-1.5f * s, -0.5f * s, 0.5f * s, 1.5f * s};
+}
+
+template <int FMT, int LPR, int MT, int XT>
+__global__ __launch_bounds__(kBlock) void lowbit_gemv_kernel(const uint8_t* __restrict__ w,
+                                                             const uint16_t* __restrict__ S, int scale_mode,
+                                                             const void* __restrict__ x, float* __restrict__ y, int M,
+                                                             int N, int K, size_t row_bytes)
+{
+    constexpr int UE = LowbitFmt<FMT>::kElems;
+    extern __shared__ __align__(16) float xs[];  // [MT][units][UE + kPad]
+    const int units = K / UE;
+    const int xstride = units * (UE + kPad);
+    const int team = threadIdx.x / LPR, lane = threadIdx.x % LPR;
+    const int n = blockIdx.x * (kBlock / LPR) + team;
+    const bool active = n < N;
+    const uint8_t* row = w + (size_t)min(n, N - 1) * row_bytes;
+    float scale = 1.0f;
+    if constexpr (FMT == LB_I2) scale = h2f(S[min(n, N - 1)]);
+
+    for (int m0 = 0; m0 < M; m0 += MT) {
+        const int mt = min(MT, M - m0);
+        for (int i = threadIdx.x; i < mt * K; i += kBlock) {
+            const int m = i / K, k = i - m * K;
+            xs[m * xstride + (k / UE) * (UE + kPad) + k % UE] = load_f32<XT>(x, (size_t)(m0 + m) * K + k);
+        }
+        __syncthreads();
+        float acc[MT];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
+        if (active) {
+            for (int u = lane; u < units; u += LPR) {
+                const float* xu = xs + u * (UE + kPad);
+                if constexpr (FMT == LB_F16) {
+                    const h8_t wh = __builtin_bit_cast(h8_t, *reinterpret_cast<const u4_t*>(row + (size_t)u * 16));
+#pragma unroll
+                    for (int m = 0; m < MT; ++m) {
+                        const f4_t a = *reinterpret_cast<const f4_t*>(xu + m * xstride);
+                        const f4_t b = *reinterpret_cast<const f4_t*>(xu + m * xstride + 4);
+                        float s = acc[m];
+                        s = __builtin_fmaf((float)wh[0], a[0], s);
+                        s = __builtin_fmaf((float)wh[1], a[1], s);
+                        s = __builtin_fmaf((float)wh[2], a[2], s);
+                        s = __builtin_fmaf((float)wh[3], a[3], s);
+                        s = __builtin_fmaf((float)wh[4], b[0], s);
+                        s = __builtin_fmaf((float)wh[5], b[1], s);
+                        s = __builtin_fmaf((float)wh[6], b[2], s);
+                        s = __builtin_fmaf((float)wh[7], b[3], s);
+                        acc[m] = s;
+                    }
+                } else if constexpr (FMT == LB_I2) {
+                    const u4_t raw = *reinterpret_cast<const u4_t*>(row + (size_t)u * 16);
+                    const I2Table tab = i2_table(scale, scale_mode);
+#pragma unroll
+                    for (int wd = 0; wd < 4; ++wd) {
+                        const uint32_t word = raw[wd];
+#pragma unroll
+                        for (int q4 = 0; q4 < 4; ++q4) {
+                            float v[4];
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) v[e] = tab((word >> (2 * (4 * q4 + e))) & 3u);
+#pragma unroll
+                            for (int m = 0; m < MT; ++m) {
+                                const f4_t a = *reinterpret_cast<const f4_t*>(xu + m * xstride + wd * 16 + q4 * 4);
+                                float s = acc[m];
+                                s = __builtin_fmaf(v[0], a[0], s);
+                                s = __builtin_fmaf(v[1], a[1], s);
+                                s = __builtin_fmaf(v[2], a[2], s);
+                                s = __builtin_fmaf(v[3], a[3], s);
+                                acc[m] = s;
+                            }
+                        }
+                    }
+                } else {
+                    // 18-byte block: 9 little-endian u16 words (2-byte aligned)
+                    const uint16_t* blk = reinterpret_cast<const uint16_t*>(row + (size_t)u * 18);
+                    uint16_t hw[9];
+#pragma unroll
+                    for (int i = 0; i < 9; ++i) hw[i] = blk[i];
+                    const float d = h2f(hw[0]);
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) {
+                        const uint32_t bits = hw[1 + t];
+#pragma unroll
+                        for (int q4 = 0; q4 < 4; ++q4) {
+                            float v[4];
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) v[e] = (bits >> (4 * q4 + e)) & 1u ? d : -d;
+#pragma unroll
+                            for (int m = 0; m < MT; ++m) {
+                                const f4_t a = *reinterpret_cast<const f4_t*>(xu + m * xstride + t * 16 + q4 * 4);
+                                float s = acc[m];
+                                s = __builtin_fmaf(v[0], a[0], s);
+                                s = __builtin_fmaf(v[1], a[1], s);
+                                s = __builtin_fmaf(v[2], a[2], s);
+                                s = __builtin_fmaf(v[3], a[3], s);
+                                acc[m] = s;
+                            }
+                        }
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[m] = group_sum<LPR>(acc[m]);
+        if (active && lane == 0) {
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+                if (m < mt) {
+                    float v = acc[m];
+                    if (FMT == LB_I2 && scale_mode == 0) v = v * scale;
+                    y[(size_t)(m0 + m) * N + n] = v;
+                }
+        }
+        __syncthreads();
+    }
+}
+
+// Any shape: one wave per output row, x read from memory, elements strided
+// over the lanes.
+template <int FMT, int XT>
+__global__ __launch_bounds__(kBlock) void lowbit_gemv_generic_kernel(const uint8_t* __restrict__ w,
+                                                                     const uint16_t* __restrict__ S, int scale_mode,
+                                                                     const void* __restrict__ x,
+                                                                     float* __restrict__ y, int M, int N, int K,
+                                                                     size_t row_bytes)
+{
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int n = blockIdx.x * (kBlock / 64) + wave;
+    if (n >= N) return;
+    const uint8_t* row = w + (size_t)n * row_bytes;
+    float scale = 1.0f;
+    if constexpr (FMT == LB_I2) scale = h2f(S[n]);
+    const I2Table tab = i2_table(scale, scale_mode);
+    for (int m = 0; m < M; ++m) {
+        float acc = 0.0f;
+        for (int j = lane; j < K; j += 64) {
+            float v;
+            if constexpr (FMT == LB_F16) {
+                v = h2f(reinterpret_cast<const uint16_t*>(row)[j]);
+            } else if constexpr (FMT == LB_I2) {
+                v = tab((row[j >> 2] >> (2 * (j & 3))) & 3u);
+            } else {
+                const uint8_t* blk = row + (size_t)(j >> 7) * 18;
+                const float d = h2f((uint16_t)(blk[0] | (blk[1] << 8)));
+                const int e = j & 127;
+                v = (blk[2 + (e >> 3)] >> (e & 7)) & 1u ? d : -d;
+            }
+            acc = __builtin_fmaf(v, load_f32<XT>(x, (size_t)m * K + j), acc);
+        }
+        acc = group_sum<64>(acc);
+        if (lane == 0) y[(size_t)m * N + n] = (FMT == LB_I2 && scale_mode == 0) ? acc * scale : acc;
+    }
+}
+
+template <int FMT, int LPR, int MT>
+hipError_t launch_fast(const uint8_t* w, const uint16_t* S, int mode, const void* x, int xdt, float* y, int M, int N,
+                       int K, size_t row_bytes, size_t lds, hipStream_t st)
+{
+    const dim3 grid((N + kBlock / LPR - 1) / (kBlock / LPR));
+    if (xdt == DT_F32)
+        hipLaunchKernelGGL((lowbit_gemv_kernel<FMT, LPR, MT, DT_F32>), grid, dim3(kBlock), lds, st, w, S, mode, x, y,
+                           M, N, K, row_bytes);
+    else if (xdt == DT_F16)
+        hipLaunchKernelGGL((lowbit_gemv_kernel<FMT, LPR, MT, DT_F16>), grid, dim3(kBlock), lds, st, w, S, mode, x, y,
+                           M, N, K, row_bytes);
+    else
+        hipLaunchKernelGGL((lowbit_gemv_kernel<FMT, LPR, MT, DT_BF16>), grid, dim3(kBlock), lds, st, w, S, mode, x, y,
+                           M, N, K, row_bytes);
+    return hipGetLastError();
+}
+
+template <int FMT, int MT>
+hipError_t launch_fast_lpr(int lpr, const uint8_t* w, const uint16_t* S, int mode, const void* x, int xdt, float* y,
+                           int M, int N, int K, size_t row_bytes, size_t lds, hipStream_t st)
+{
+    switch (lpr) {
+    case 4: return launch_fast<FMT, 4, MT>(w, S, mode, x, xdt, y, M, N, K, row_bytes, lds, st);
+    case 8: return launch_fast<FMT, 8, MT>(w, S, mode, x, xdt, y, M, N, K, row_bytes, lds, st);
+    case 16: return launch_fast<FMT, 16, MT>(w, S, mode, x, xdt, y, M, N, K, row_bytes, lds, st);
+    case 32: return launch_fast<FMT, 32, MT>(w, S, mode, x, xdt, y, M, N, K, row_bytes, lds, st);
+    default: return launch_fast<FMT, 64, MT>(w, S, mode, x, xdt, y, M, N, K, row_bytes, lds, st);
+    }
+}
+
+template <int FMT>
+hipError_t launch_fmt(const uint8_t* w, const uint16_t* S, int mode, const void* x, int xdt, float* y, int M, int N,
+                      int K, size_t row_bytes, hipStream_t st)
+{
+    constexpr int UE = LowbitFmt<FMT>::kElems;
+    const bool unit_ok =
+        K % UE == 0 && (reinterpret_cast<uintptr_t>(w) & (FMT == LB_Q1 ? 1u : 15u)) == 0;
+    const size_t per_row = (size_t)(K / UE) * (UE + kPad) * sizeof(float);
+    int MT = M >= 4 ? 4 : (M >= 2 ? 2 : 1);
+    while (MT > 1 && MT * per_row > 64 * 1024) MT >>= 1;
+    if (unit_ok && K > 0 && per_row <= 64 * 1024) {
+        const int units = K / UE;
+        int lpr = 4;
+        while (lpr < 64 && lpr < units) lpr <<= 1;
+        const size_t lds = (size_t)MT * per_row;
+        if (MT == 4) return launch_fast_lpr<FMT, 4>(lpr, w, S, mode, x, xdt, y, M, N, K, row_bytes, lds, st);
+        if (MT == 2) return launch_fast_lpr<FMT, 2>(lpr, w, S, mode, x, xdt, y, M, N, K, row_bytes, lds, st);
+        return launch_fast_lpr<FMT, 1>(lpr, w, S, mode, x, xdt, y, M, N, K, row_bytes, lds, st);
+    }
+    const dim3 grid((N + 3) / 4);
+    if (xdt == DT_F32)
+        hipLaunchKernelGGL((lowbit_gemv_generic_kernel<FMT, DT_F32>), grid, dim3(kBlock), 0, st, w, S, mode, x, y, M,
+                           N, K, row_bytes);
+    else if (xdt == DT_F16)
+        hipLaunchKernelGGL((lowbit_gemv_generic_kernel<FMT, DT_F16>), grid, dim3(kBlock), 0, st, w, S, mode, x, y, M,
+                           N, K, row_bytes);
+    else
+        hipLaunchKernelGGL((lowbit_gemv_generic_kernel<FMT, DT_BF16>), grid, dim3(kBlock), 0, st, w, S, mode, x, y, M,
+                           N, K, row_bytes);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+size_t lowbit_row_bytes(int fmt, int K)
+{
+    if (fmt == LB_F16) return (size_t)K * 2;
+    if (fmt == LB_I2) return (size_t)(K + 3) / 4;
+    return (size_t)(K / 128) * 18;
+}
+
+hipError_t launch_qgemv_lowbit(int fmt, const void* w, const uint16_t* S, int scale_mode, const void* x, int xdt,
+                               float* y, int M, int N, int K, hipStream_t st)
+{
+    const uint8_t* wb = reinterpret_cast<const uint8_t*>(w);
+    const size_t rb = lowbit_row_bytes(fmt, K);
+    if (fmt == LB_F16) return launch_fmt<LB_F16>(wb, S, scale_mode, x, xdt, y, M, N, K, rb, st);
+    if (fmt == LB_I2) return launch_fmt<LB_I2>(wb, S, scale_mode, x, xdt, y, M, N, K, rb, st);
+    return launch_fmt<LB_Q1>(wb, S, scale_mode, x, xdt, y, M, N, K, rb, st);
+}
+
+}  // namespace cellm

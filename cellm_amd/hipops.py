@@ -236,6 +236,28 @@ class HipOps:
                             biases=_dev_ptr(biases), n_scales=0, x=_dev_ptr(x), bias=None, y=_dev_ptr(y),
                             m=x.numel() // k, n=n, k=k)
 
+    @staticmethod
+    def qgemv_op_f16(w_f16, x, y) -> "_lib.QgemvOp":
+        """One cellm_hip_qgemv_op_t of kind f16 (arguments as encode_qgemv_f16)."""
+        n, k = w_f16.shape
+        return _lib.QgemvOp(kind=_lib.OP_QGEMV_F16, sb_dtype=0, x_dtype=_torch_dtype_code(x), group=0,
+                            w=_dev_ptr(w_f16), scales=None, biases=None, n_scales=0, x=_dev_ptr(x), bias=None,
+                            y=_dev_ptr(y), m=x.numel() // k, n=n, k=k)
+
+    @staticmethod
+    def qgemv_op_i2(w_u8, scales_f16, scale_mode: int, x, y, k: int) -> "_lib.QgemvOp":
+        """One cellm_hip_qgemv_op_t of kind i2 (group carries scale_mode)."""
+        return _lib.QgemvOp(kind=_lib.OP_QGEMV_I2, sb_dtype=1, x_dtype=_torch_dtype_code(x), group=scale_mode,
+                            w=_dev_ptr(w_u8), scales=_dev_ptr(scales_f16), biases=None, n_scales=scales_f16.numel(),
+                            x=_dev_ptr(x), bias=None, y=_dev_ptr(y), m=x.numel() // k, n=w_u8.shape[0], k=k)
+
+    @staticmethod
+    def qgemv_op_q1_0_g128(w_u8, x, y, k: int) -> "_lib.QgemvOp":
+        """One cellm_hip_qgemv_op_t of kind q1_0_g128."""
+        return _lib.QgemvOp(kind=_lib.OP_QGEMV_Q1_0_G128, sb_dtype=0, x_dtype=_torch_dtype_code(x), group=0,
+                            w=_dev_ptr(w_u8), scales=None, biases=None, n_scales=0, x=_dev_ptr(x), bias=None,
+                            y=_dev_ptr(y), m=x.numel() // k, n=w_u8.shape[0], k=k)
+
     def encode_qgemv_batch(self, ops, stream=None) -> None:
         """Enqueue a list of qgemv ops (qgemv_op_*) in order with one call; a
         ctypes array built once may be passed again to re-enqueue it."""
@@ -249,6 +271,23 @@ class HipOps:
         check(self._lib.cellm_hip_qgemv_i4_sym(self._h, _dev_ptr(w_u8), _dev_ptr(scales_f16), scales_f16.numel(), gs,
                                                _dev_ptr(x), _torch_dtype_code(x), _dev_ptr(y), m, n, k,
                                                _stream_ptr(stream)))
+
+    def encode_qgemv_f16(self, w_f16, x, y, stream=None) -> None:
+        """y[m, n] = sum_k f32(W[n, k]) * x[m, k]; W [n][k] float16 (or int16 holding f16 bits)."""
+        n, k = w_f16.shape
+        check(self._lib.cellm_hip_qgemv_f16(self._h, _dev_ptr(w_f16), _dev_ptr(x), _torch_dtype_code(x), _dev_ptr(y),
+                                            x.numel() // k, n, k, _stream_ptr(stream)))
+
+    def encode_qgemv_i2(self, w_u8, scales_f16, scale_mode: int, x, y, k: int, stream=None) -> None:
+        """i2 rows of ceil(k/4) bytes, one f16 scale per row; scale_mode 0 = at the end (Qwen), 1 = per element (Gemma)."""
+        check(self._lib.cellm_hip_qgemv_i2(self._h, _dev_ptr(w_u8), _dev_ptr(scales_f16), scale_mode, _dev_ptr(x),
+                                           _torch_dtype_code(x), _dev_ptr(y), x.numel() // k, w_u8.shape[0], k,
+                                           _stream_ptr(stream)))
+
+    def encode_qgemv_q1_0_g128(self, w_u8, x, y, k: int, stream=None) -> None:
+        """q1_0_g128 rows of k/128 blocks of 18 bytes."""
+        check(self._lib.cellm_hip_qgemv_q1_0_g128(self._h, _dev_ptr(w_u8), _dev_ptr(x), _torch_dtype_code(x),
+                                                  _dev_ptr(y), x.numel() // k, w_u8.shape[0], k, _stream_ptr(stream)))
 
     def encode_qgemm_q4_affine(self, wq, scales, biases, x_f16, y, group: int = 64, stream=None) -> None:
         n = wq.shape[0]

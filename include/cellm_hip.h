@@ -159,9 +159,16 @@ int32_t cellm_hip_qgemv_q4_affine_gate_up_silu(cellm_hip_ctx_t* ctx, const uint3
  * CELLM_HIP_OP_QGEMV_I8 takes the arguments of cellm_hip_qgemv_i8 (w int8,
  * scales, sb_dtype = scale dtype, n_scales, bias; biases and group unused);
  * kind CELLM_HIP_OP_QGEMV_Q4_AFFINE those of cellm_hip_qgemv_q4_affine (w =
- * u32 words, scales, biases, sb_dtype, group; n_scales and bias unused). */
+ * u32 words, scales, biases, sb_dtype, group; n_scales and bias unused);
+ * kind CELLM_HIP_OP_QGEMV_F16 those of cellm_hip_qgemv_f16 (w only);
+ * kind CELLM_HIP_OP_QGEMV_I2 those of cellm_hip_qgemv_i2 (w, scales = f16 row
+ * scales, group = scale_mode); kind CELLM_HIP_OP_QGEMV_Q1_0_G128 those of
+ * cellm_hip_qgemv_q1_0_g128 (w only).  Unused fields are ignored. */
 #define CELLM_HIP_OP_QGEMV_I8 0
 #define CELLM_HIP_OP_QGEMV_Q4_AFFINE 1
+#define CELLM_HIP_OP_QGEMV_F16 2
+#define CELLM_HIP_OP_QGEMV_I2 3
+#define CELLM_HIP_OP_QGEMV_Q1_0_G128 4
 typedef struct {
     int32_t kind;
     int32_t sb_dtype;
@@ -193,6 +200,30 @@ int32_t cellm_hip_qgemv_batch(cellm_hip_ctx_t* ctx, const cellm_hip_qgemv_op_t* 
 int32_t cellm_hip_qgemv_i4_sym(cellm_hip_ctx_t* ctx, const uint8_t* w, const uint16_t* scales_f16, int64_t n_scales,
                                int64_t gs, const void* x, int32_t x_dtype, float* y, int64_t m, int64_t n, int64_t k,
                                void* stream);
+
+/* f16-weight GEMV: y[i, r] = sum_j f32(W[r, j]) * x[i, j], W [n][k] f16
+ * (2-byte aligned).  Replaces cpu_kernels::matmul_f16_f32
+ * (cpu_kernels.rs:135-214) in the runners' "f16" linear arms (qwen.rs:1073,
+ * llama.rs:898) and MetalOps::encode_mv_f16 / mv_f16 (metal.rs:347-363,
+ * 1089). */
+int32_t cellm_hip_qgemv_f16(cellm_hip_ctx_t* ctx, const uint16_t* w_f16, const void* x, int32_t x_dtype, float* y,
+                            int64_t m, int64_t n, int64_t k, void* stream);
+
+/* i2 GEMV: W [n][ceil(k/4)] bytes, element j = bits 2(j%4)..2(j%4)+1 of byte
+ * j/4, code c -> centroid {-1.5, -0.5, 0.5, 1.5}[c] (dequant_i2,
+ * qwen.rs:1582-1589); one f16 scale per row.  scale_mode 0 applies the scale
+ * to the row sum (Qwen dot_i2_scaled_row, qwen.rs:1591-1606); scale_mode 1
+ * to each element (Gemma dot_i2_scaled_row, gemma.rs:1673-1687). */
+int32_t cellm_hip_qgemv_i2(cellm_hip_ctx_t* ctx, const uint8_t* w, const uint16_t* scales_f16, int32_t scale_mode,
+                           const void* x, int32_t x_dtype, float* y, int64_t m, int64_t n, int64_t k, void* stream);
+
+/* q1_0_g128 GEMV: each row is k/128 blocks of 18 bytes, a little-endian f16
+ * d then 16 bytes of sign bits (element 8b+j = bit j of byte b; value d when
+ * set, -d otherwise).  Replaces the "q1_0_g128" arm of Qwen's dot_row
+ * (qwen.rs:1004-1022) and MetalOps::encode_mv_q1 / mv_q1_0_g128
+ * (metal.rs:542-570).  k % 128 == 0. */
+int32_t cellm_hip_qgemv_q1_0_g128(cellm_hip_ctx_t* ctx, const uint8_t* w, const void* x, int32_t x_dtype, float* y,
+                                  int64_t m, int64_t n, int64_t k, void* stream);
 
 /* Prefill qGEMM on MFMA: Y[m, n] = X[m, k] . dequant(Wq)^T, X f16, Y f32,
  * weight tiles dequantized to f16 as tools/convert/src/main.rs:4349-4444 does.

@@ -51,6 +51,9 @@ def _declare(L):
         "oracle_llama_lm_head_i8": (None, [vp, vp, vp, sz, sz, vp]),
         "oracle_matmul_i4_f32": (None, [vp, vp, sz, sz, sz, sz, vp, vp]),
         "oracle_qgemv_i4_sym": (None, [vp, vp, sz, sz, vp, i32, sz, sz, sz, vp]),
+        "oracle_qgemv_f16": (None, [vp, vp, i32, sz, sz, sz, vp]),
+        "oracle_qgemv_i2": (None, [vp, vp, i32, vp, i32, sz, sz, sz, vp]),
+        "oracle_qgemv_q1_0_g128": (None, [vp, vp, i32, sz, sz, sz, vp]),
         "oracle_q4_affine_dequant_f32": (None, [vp, vp, vp, i32, sz, sz, sz, vp]),
         "oracle_qgemv_q4_affine": (None, [vp, vp, vp, i32, vp, i32, sz, sz, sz, sz, vp]),
         "oracle_lfm_lm_head_q4_affine": (None, [vp, sz, vp, vp, sz, vp, sz, sz, vp]),
@@ -183,6 +186,36 @@ def qgemv_i4_sym(w_u8, scales_f16_bits, gs, x, n, k):
     y = np.empty((m, n), np.float32)
     lib().oracle_qgemv_i4_sym(_p(np.ascontiguousarray(w_u8, np.uint8)), _p(s), s.size, gs, _p(x2), _dt(x2), m, n, k,
                               _p(y))
+    return y
+
+
+# --- f16, i2, q1_0_g128 --------------------------------------------------------
+
+def qgemv_f16(w_f16_bits: np.ndarray, x: np.ndarray) -> np.ndarray:
+    """y[m, n] = sum_k f32(W[n, k]) * x[m, k] (matmul_f16_f32, cpu_kernels.rs:135-214)."""
+    n, k = w_f16_bits.shape
+    x2 = np.ascontiguousarray(x.reshape(-1, k))
+    y = np.empty((x2.shape[0], n), np.float32)
+    lib().oracle_qgemv_f16(_p(np.ascontiguousarray(w_f16_bits, np.uint16)), _p(x2), _dt(x2), x2.shape[0], n, k, _p(y))
+    return y
+
+
+def qgemv_i2(w_u8: np.ndarray, scales_f16_bits: np.ndarray, x: np.ndarray, k: int, scale_mode: int) -> np.ndarray:
+    """i2 rows of ceil(k/4) bytes; scale_mode 0 = Qwen (scale at the end), 1 = Gemma (per element)."""
+    n = w_u8.shape[0]
+    x2 = np.ascontiguousarray(x.reshape(-1, k))
+    y = np.empty((x2.shape[0], n), np.float32)
+    lib().oracle_qgemv_i2(_p(np.ascontiguousarray(w_u8, np.uint8)), _p(np.ascontiguousarray(scales_f16_bits, np.uint16)),
+                          scale_mode, _p(x2), _dt(x2), x2.shape[0], n, k, _p(y))
+    return y
+
+
+def qgemv_q1_0_g128(w_u8: np.ndarray, x: np.ndarray, k: int) -> np.ndarray:
+    """q1_0_g128 rows of k/128 blocks of 18 bytes (f16 d + 128 sign bits)."""
+    n = w_u8.shape[0]
+    x2 = np.ascontiguousarray(x.reshape(-1, k))
+    y = np.empty((x2.shape[0], n), np.float32)
+    lib().oracle_qgemv_q1_0_g128(_p(np.ascontiguousarray(w_u8, np.uint8)), _p(x2), _dt(x2), x2.shape[0], n, k, _p(y))
     return y
 
 

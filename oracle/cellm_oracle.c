@@ -304,6 +304,100 @@ void oracle_qgemv_i4_sym(const uint8_t* w, const uint16_t* scales_f16, size_t n_
 }
 
 /* ------------------------------------------------------------------------ */
+/* Rank-4 dtypes: f16 weights, i2 (2-bit per-row symmetric), q1_0_g128.      */
+/* ------------------------------------------------------------------------ */
+
+/* cpu_kernels::matmul_f16_f32, x86 branch (cpu_kernels.rs:135-214, :205-211):
+ * acc += f32(w[kk]) * b[kk], sequential, product and sum rounded apart.
+ * Batched/dtype form: x [M][K] widened from f32/f16/bf16, y [M][N]. */
+void oracle_qgemv_f16(const uint16_t* w, const void* x, int x_dtype, size_t M, size_t N, size_t K, float* y)
+{
+    for (size_t mi = 0; mi < M; ++mi) {
+#pragma omp parallel for schedule(static)
+        for (size_t n = 0; n < N; ++n) {
+            const uint16_t* row = w + n * K;
+            float acc = 0.0f;
+            for (size_t kk = 0; kk < K; ++kk) {
+                const float p = oracle_f16_to_f32(row[kk]) * load_as_f32(x, x_dtype, mi * K + kk);
+                acc = acc + p;
+            }
+            y[mi * N + n] = acc;
+        }
+    }
+}
+
+/* dequant_i2 (qwen.rs:1582-1589, gemma.rs:2220-2227): 2-bit code -> centroid. */
+static inline float i2_centroid(unsigned q)
+{
+    switch (q & 3u) {
+    case 0: return -1.5f;
+    case 1: return -0.5f;
+    case 2: return 0.5f;
+    default: return 1.5f;
+    }
+}
+
+/* i2 row GEMV, row_stride = ceil(K/4) bytes, element j = bits 2(j%4)..+1 of
+ * byte j/4 (low bits first), one f16 scale per row (".qscale").
+ * scale_mode 0: Qwen dot_i2_scaled_row (qwen.rs:1591-1606, used by the linear
+ *   fallback qwen.rs:1092-1101): acc += x * dq; result acc * scale.
+ * scale_mode 1: Gemma dot_i2_scaled_row (gemma.rs:1673-1687):
+ *   acc += x * (dq * scale). */
+void oracle_qgemv_i2(const uint8_t* w, const uint16_t* scales_f16, int scale_mode, const void* x, int x_dtype,
+                     size_t M, size_t N, size_t K, float* y)
+{
+    const size_t row_stride = (K + 3) / 4;
+    for (size_t mi = 0; mi < M; ++mi) {
+#pragma omp parallel for schedule(static)
+        for (size_t n = 0; n < N; ++n) {
+            const uint8_t* row = w + n * row_stride;
+            const float scale = oracle_f16_to_f32(scales_f16[n]);
+            float acc = 0.0f;
+            for (size_t j = 0; j < K; ++j) {
+                const float dq = i2_centroid((unsigned)(row[j / 4] >> (2 * (j % 4))));
+                const float xv = load_as_f32(x, x_dtype, mi * K + j);
+                if (scale_mode == 0) {
+                    const float p = xv * dq;
+                    acc = acc + p;
+                } else {
+                    const float wv = dq * scale;
+                    const float p = xv * wv;
+                    acc = acc + p;
+                }
+            }
+            y[mi * N + n] = scale_mode == 0 ? acc * scale : acc;
+        }
+    }
+}
+
+/* q1_0_g128 row GEMV (qwen.rs:1004-1022; metal.rs:542-570 mv_q1_0_g128):
+ * a row is K/128 blocks of 18 bytes: f16 d (little endian) then 16 bytes of
+ * sign bits, element b*8+j of the block = bit j of byte b; value d if the bit
+ * is set, else -d; acc += value * x, sequential.  K % 128 == 0. */
+void oracle_qgemv_q1_0_g128(const uint8_t* w, const void* x, int x_dtype, size_t M, size_t N, size_t K, float* y)
+{
+    const size_t nblk = K / 128, row_stride = nblk * 18;
+    for (size_t mi = 0; mi < M; ++mi) {
+#pragma omp parallel for schedule(static)
+        for (size_t n = 0; n < N; ++n) {
+            const uint8_t* row = w + n * row_stride;
+            float acc = 0.0f;
+            for (size_t i = 0; i < nblk; ++i) {
+                const uint8_t* blk = row + i * 18;
+                const float d = oracle_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+                for (int b = 0; b < 16; ++b)
+                    for (int j = 0; j < 8; ++j) {
+                        const float v = (blk[2 + b] >> j) & 1 ? d : -d;
+                        const float p = v * load_as_f32(x, x_dtype, mi * K + i * 128 + (size_t)b * 8 + j);
+                        acc = acc + p;
+                    }
+            }
+            y[mi * N + n] = acc;
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
 /* a3/a4: MLX 4-bit affine (u32 words, 8 nibbles, per-64-group scale+bias). */
 /* ------------------------------------------------------------------------ */
 

@@ -332,3 +332,105 @@ def test_softmax_attention_argmax():
     g = np.array([0.0, 1.0], np.float32)
     oracle.silu_mul_(g, np.array([2.0, 2.0], np.float32))
     assert g[0] == 0.0 and np.isclose(g[1], 2.0 / (1.0 + np.exp(-1.0)))
+
+
+# ------------------------------------------------------- f16, i2, q1_0_g128 ----
+
+def test_f16_gemv_known_answer_and_sequential_order():
+    """f16 weights: 1.0, -2.0, 0.5 (bits 0x3C00, 0xC000, 0x3800) against x =
+    1, 10, 100 is exactly 31; random rows equal the strict left-to-right sum of
+    f32(w) * x (catches a transposed weight, a reordered or fused sum)."""
+    w = np.array([[0x3C00, 0xC000, 0x3800]], np.uint16)
+    assert oracle.qgemv_f16(w, np.array([1.0, 10.0, 100.0], np.float32))[0, 0] == np.float32(31.0)
+    rng = np.random.default_rng(21)
+    n, k = 7, 300
+    wf = rng.standard_normal((n, k)).astype(np.float16)
+    x = rng.standard_normal((2, k)).astype(np.float32)
+    y = oracle.qgemv_f16(wf.view(np.uint16), x)
+    for m in range(2):
+        for r in range(n):
+            assert y[m, r] == seq_sum_f32(wf[r].astype(np.float32) * x[m])
+    # an f16 x is widened exactly
+    xh = x.astype(np.float16)
+    np.testing.assert_array_equal(oracle.qgemv_f16(wf.view(np.uint16), xh),
+                                  oracle.qgemv_f16(wf.view(np.uint16), xh.astype(np.float32)))
+
+
+def _i2_codes(w: np.ndarray, k: int) -> np.ndarray:
+    """numpy decode: element j = bits 2(j%4)..2(j%4)+1 of byte j/4."""
+    q = (w[:, :, None] >> (2 * np.arange(4, dtype=np.uint8))) & 3
+    return q.reshape(w.shape[0], -1)[:, :k]
+
+
+I2_CENTROIDS = np.array([-1.5, -0.5, 0.5, 1.5], np.float32)
+
+
+def test_i2_known_answer_bit_order():
+    """byte 0xE4 = codes 0, 1, 2, 3 (low bits first) = -1.5, -0.5, 0.5, 1.5;
+    against x = 1, 10, 100, 1000 that is 1543.5, exact in both scale modes,
+    times 2 for a scale of 2 (catches reversed lanes or centroids)."""
+    w = np.array([[0xE4]], np.uint8)
+    x = np.array([1.0, 10.0, 100.0, 1000.0], np.float32)
+    for mode in (0, 1):
+        assert oracle.qgemv_i2(w, np.array([1.0], np.float16).view(np.uint16), x, 4, mode)[0, 0] == np.float32(1543.5)
+        assert oracle.qgemv_i2(w, np.array([2.0], np.float16).view(np.uint16), x, 4, mode)[0, 0] == np.float32(3087.0)
+
+
+def test_i2_scale_modes_and_ragged_rows():
+    """Mode 0 (Qwen) = (left-to-right sum of x * dq) * scale; mode 1 (Gemma) =
+    left-to-right sum of x * (dq * scale); the two differ for a scale that is
+    not a power of two (catches swapped modes).  K = 1023 leaves the last byte
+    partly used: codes past K are ignored."""
+    rng = np.random.default_rng(22)
+    n, k = 6, 1023
+    w = rng.integers(0, 256, (n, (k + 3) // 4)).astype(np.uint8)
+    s = rng.uniform(0.01, 0.05, n).astype(np.float16)
+    x = rng.standard_normal(k).astype(np.float32)
+    dq = I2_CENTROIDS[_i2_codes(w, k)]
+    y0 = oracle.qgemv_i2(w, s.view(np.uint16), x, k, 0)[0]
+    y1 = oracle.qgemv_i2(w, s.view(np.uint16), x, k, 1)[0]
+    for r in range(n):
+        sc = np.float32(s[r])
+        assert y0[r] == np.float32(seq_sum_f32(x * dq[r]) * sc)
+        assert y1[r] == seq_sum_f32(x * (dq[r] * sc))
+    assert np.any(y0 != y1)
+    # the unused high code bits of the last byte do not matter
+    w2 = w.copy()
+    w2[:, -1] ^= 0xC0
+    np.testing.assert_array_equal(oracle.qgemv_i2(w2, s.view(np.uint16), x, k, 0)[0], y0)
+
+
+def _q1_values(w: np.ndarray, k: int) -> np.ndarray:
+    """numpy decode of q1_0_g128 rows: little-endian f16 d, then 128 bits (bit j of byte b = element 8b+j)."""
+    n = w.shape[0]
+    blk = w.reshape(n, k // 128, 18)
+    d = blk[:, :, :2].copy().view(np.float16).astype(np.float32)[:, :, 0]
+    bits = np.unpackbits(blk[:, :, 2:], axis=2, bitorder="little").astype(bool)
+    return np.where(bits, d[:, :, None], -d[:, :, None]).reshape(n, k)
+
+
+def test_q1_known_answer_bit_and_byte_order():
+    """d = 1.0 as bytes 00 3C; only bit 3 of sign byte 5 set: element 43 is +1,
+    the other 127 are -1, so y = 2 x[43] - sum(x), exact for integer x
+    (catches a big-endian d, a reversed bit order or a block offset)."""
+    w = np.zeros((1, 18), np.uint8)
+    w[0, 0], w[0, 1] = 0x00, 0x3C
+    w[0, 2 + 5] = 1 << 3
+    x = np.arange(128, dtype=np.float32) - 40.0
+    assert oracle.qgemv_q1_0_g128(w, x, 128)[0, 0] == np.float32(2 * x[43] - x.sum())
+
+
+def test_q1_sequential_order_random():
+    """Random blocks: y = left-to-right sum of value * x over the row, values
+    from numpy's own unpacking."""
+    rng = np.random.default_rng(23)
+    n, k = 5, 512
+    w = rng.integers(0, 256, (n, k // 128 * 18)).astype(np.uint8)
+    d = rng.uniform(0.01, 0.1, (n, k // 128)).astype(np.float16)
+    w.reshape(n, k // 128, 18)[:, :, :2] = d.view(np.uint8).reshape(n, k // 128, 2)
+    x = rng.standard_normal((3, k)).astype(np.float32)
+    y = oracle.qgemv_q1_0_g128(w, x, k)
+    v = _q1_values(w, k)
+    for m in range(3):
+        for r in range(n):
+            assert y[m, r] == seq_sum_f32(v[r] * x[m])
