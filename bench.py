@@ -292,6 +292,7 @@ def extra_configs(torch, ops, stream, gen):
     del wset
 
     res.update(decode_step_cfg5())
+    res.update(lowbit_gemvs(torch, ops, stream, gen))
 
     # M=512 prefill qGEMM (MFMA)
     m = 512
@@ -304,6 +305,43 @@ def extra_configs(torch, ops, stream, gen):
         tflops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
         res[f"cfg4_qgemm_m512_{k}x{n}"] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tflops, 1),
                                            "frac_mfma_f16": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
+    return res
+
+
+def lowbit_gemvs(torch, ops, stream, gen):
+    """The remaining .cellm weight formats at batch 1 (f16 x): f16 896->4864
+    (Qwen2.5-0.5B gate), i2 1152->6912 (Gemma-3-1B MLP), q1_0_g128
+    1152->6912 and 1152->262144 (a Gemma-3-1B-size lm_head).  Weight copies
+    rotate past 512 MB so that they stream from HBM.  Bytes per call: weights
+    and row scales + x + y."""
+    res = {}
+    cases = [("f16", 896, 4864), ("i2", 1152, 6912), ("q1_0_g128", 1152, 6912), ("q1_0_g128", 1152, 262144)]
+    for fmt, k, n in cases:
+        if fmt == "f16":
+            wbytes, sbytes = n * k * 2, 0
+        elif fmt == "i2":
+            wbytes, sbytes = n * k // 4, 2 * n
+        else:
+            wbytes, sbytes = n * (k // 128) * 18, 0
+        copies = max(2, -(-512 * 2**20 // wbytes) + 1)
+        w = torch.randint(0, 256, (copies, wbytes), dtype=torch.uint8, device="cuda", generator=gen)
+        if fmt == "q1_0_g128":  # finite d in every block
+            d = torch.full((copies, n * (k // 128), 1), 0.05, dtype=torch.float16, device="cuda").view(torch.uint8)
+            w.view(copies, n * (k // 128), 18)[:, :, :2] = d
+        s = (torch.rand((n,), device="cuda", generator=gen) * 0.04 + 0.01).to(torch.float16)
+        x = torch.randn((1, k), device="cuda", generator=gen).to(torch.float16)
+        y = torch.empty((1, n), dtype=torch.float32, device="cuda")
+        if fmt == "f16":
+            arr = op_array([ops.qgemv_op_f16(w[i % copies].view(torch.float16).view(n, k), x, y) for i in range(100)])
+        elif fmt == "i2":
+            arr = op_array([ops.qgemv_op_i2(w[i % copies].view(n, k // 4), s, 0, x, y, k) for i in range(100)])
+        else:
+            arr = op_array([ops.qgemv_op_q1_0_g128(w[i % copies].view(n, -1), x, y, k) for i in range(100)])
+        ms = time_batch(torch, ops, arr, stream)
+        b = wbytes + sbytes + 2 * k + 4 * n
+        res[f"lowbit_{fmt}_{k}x{n}"] = {"us": round(ms * 1e3, 2), "GB/s": round(b / (ms * 1e-3) / 1e9, 1),
+                                         "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        del w
     return res
 
 

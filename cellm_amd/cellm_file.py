@@ -1,0 +1,144 @@
+"""ctypes binding of the .cellm file API of libcellm_hip.so (include/cellm_hip.h,
+cellm_file_*), the host side of CellmFile (crates/cellm-model/src/cellm_file.rs).
+
+`CellmFile(path)` maps and validates a file; `.config` holds the model fields
+of the header, `.tensors` the tensor index in header order, `.tensor_bytes`
+returns a zero-copy numpy view of the mapped bytes, and `.upload(ops)` puts
+the tensors into a HipOps context's name-keyed device weight cache.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import numpy as np
+
+from ._lib import CellmHipError, load
+
+
+class FileConfig(C.Structure):
+    _fields_ = [("model_type", C.c_char * 64), ("vocab_size", C.c_int64), ("hidden_dim", C.c_int64),
+                ("intermediate_size", C.c_int64), ("num_layers", C.c_int64), ("num_heads", C.c_int64),
+                ("num_kv_heads", C.c_int64), ("head_dim", C.c_int64), ("bos_token_id", C.c_int64),
+                ("eos_token_id", C.c_int64), ("max_position_embeddings", C.c_int64),
+                ("rms_norm_eps", C.c_float), ("rope_theta", C.c_float), ("tie_word_embeddings", C.c_int32)]
+
+
+class FileTensor(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("dtype", C.c_char_p), ("shape", C.c_int64 * 8), ("ndim", C.c_int32),
+                ("offset_bytes", C.c_uint64), ("nbytes", C.c_uint64)]
+
+
+@dataclass(frozen=True)
+class TensorInfo:
+    name: str
+    dtype: str
+    shape: tuple
+    offset_bytes: int
+    nbytes: int
+
+
+_bound = None
+
+
+def _lib():
+    global _bound
+    if _bound is not None:
+        return _bound
+    lib = load()
+    vp = C.c_void_p
+    sig = {
+        "cellm_file_open": (C.c_int32, [C.c_char_p, C.POINTER(vp)]),
+        "cellm_file_close": (None, [vp]),
+        "cellm_file_config": (C.c_int32, [vp, C.POINTER(FileConfig)]),
+        "cellm_file_header_json": (C.c_int32, [vp, C.POINTER(C.c_char_p), C.POINTER(C.c_size_t)]),
+        "cellm_file_tensor_count": (C.c_int64, [vp]),
+        "cellm_file_tensor_at": (C.c_int32, [vp, C.c_int64, C.POINTER(FileTensor)]),
+        "cellm_file_find": (C.c_int32, [vp, C.c_char_p, C.POINTER(FileTensor)]),
+        "cellm_file_tensor_bytes": (C.c_int32, [vp, C.c_char_p, C.POINTER(vp), C.POINTER(C.c_size_t)]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _bound = lib
+    return lib
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        from ._lib import last_error
+
+        raise CellmHipError(rc, f"{what}: {last_error()}")
+
+
+class CellmFile:
+    def __init__(self, path):
+        self._lib = _lib()
+        h = C.c_void_p()
+        _check(self._lib.cellm_file_open(str(path).encode(), C.byref(h)), f"cellm_file_open({path})")
+        self._h = h
+        cfg = FileConfig()
+        _check(self._lib.cellm_file_config(h, C.byref(cfg)), "cellm_file_config")
+        self.config = {f: getattr(cfg, f) for f, _ in FileConfig._fields_}
+        self.config["model_type"] = cfg.model_type.decode()
+        self.tensors = []
+        t = FileTensor()
+        for i in range(self._lib.cellm_file_tensor_count(h)):
+            _check(self._lib.cellm_file_tensor_at(h, i, C.byref(t)), "cellm_file_tensor_at")
+            self.tensors.append(TensorInfo(t.name.decode(), t.dtype.decode(), tuple(t.shape[:t.ndim]),
+                                           int(t.offset_bytes), int(t.nbytes)))
+        self._by_name = {ti.name: ti for ti in self.tensors}
+
+    @property
+    def handle(self):
+        return self._h
+
+    def header_json(self) -> str:
+        p = C.c_char_p()
+        n = C.c_size_t()
+        _check(self._lib.cellm_file_header_json(self._h, C.byref(p), C.byref(n)), "cellm_file_header_json")
+        return C.string_at(p, n.value).decode()
+
+    def has_tensor(self, name: str) -> bool:
+        return name in self._by_name
+
+    def tensor(self, name: str) -> TensorInfo:
+        t = FileTensor()
+        _check(self._lib.cellm_file_find(self._h, name.encode(), C.byref(t)), f"cellm_file_find({name})")
+        return self._by_name[name]
+
+    def tensor_bytes(self, name: str) -> np.ndarray:
+        """The mapped bytes of a tensor as a read-only uint8 view (valid while the file is open)."""
+        p = C.c_void_p()
+        n = C.c_size_t()
+        _check(self._lib.cellm_file_tensor_bytes(self._h, name.encode(), C.byref(p), C.byref(n)),
+               f"cellm_file_tensor_bytes({name})")
+        if n.value == 0:
+            return np.zeros(0, np.uint8)
+        buf = (C.c_uint8 * n.value).from_address(p.value)
+        a = np.frombuffer(buf, dtype=np.uint8)
+        a.flags.writeable = False
+        return a
+
+    def upload(self, ops, name_prefix: str | None = None) -> tuple[int, int]:
+        """All tensors (or those under name_prefix) into ops' device weight cache; (count, bytes)."""
+        count = C.c_int64()
+        nbytes = C.c_size_t()
+        _check(ops._lib.cellm_hip_upload_cellm_file(ops._h, self._h, name_prefix.encode() if name_prefix else None,
+                                                    C.byref(count), C.byref(nbytes)), "cellm_hip_upload_cellm_file")
+        return count.value, nbytes.value
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self._lib.cellm_file_close(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        self.close()

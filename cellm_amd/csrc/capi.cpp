@@ -25,6 +25,20 @@ namespace {
 
 thread_local std::string g_last_error;
 
+}  // namespace
+
+namespace cellm {
+// Lets the other translation units of the library (cellm_file.cpp) report
+// through cellm_hip_last_error_message.
+int32_t set_error_external(int32_t code, const std::string& msg)
+{
+    g_last_error = msg;
+    return code;
+}
+}  // namespace cellm
+
+namespace {
+
 int32_t set_error(int32_t code, const char* fmt, ...)
 {
     char buf[1024];

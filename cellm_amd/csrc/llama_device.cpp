@@ -128,6 +128,8 @@ struct cellm_llama_dev {
     std::vector<const float*> attn_norm, mlp_norm;
     const int8_t* embed = nullptr;
     const uint16_t* embed_scale = nullptr;
+    const int8_t* lm_w = nullptr;  // the tied embedding unless the model has its own lm_head
+    const uint16_t* lm_s = nullptr;
     const float* final_norm = nullptr;
     DevBuf kcache, vcache, rope, x, xn, q, k, v, attn, proj, h, logits, io;
     // io: [tokens u32 | positions i32 | block tables u32 | argmax idx i32 | argmax val f32]
@@ -224,9 +226,9 @@ int32_t enqueue_step(cellm_llama_dev* m, int32_t rows)
         LIB_TRY(cellm_hip_add_rms_norm(H, x, proj, next_norm, CELLM_HIP_DTYPE_F32, R, hid, eps, xn, S),
                 "residual + norm");
     }
-    // tied lm_head through the int8 GEMV (llama.rs:549-567), greedy id on the device
+    // lm_head (tied embedding or lm_head.weight, llama.rs:522-567) through the int8 GEMV, greedy id on the device
     float* lg = m->logits.as<float>();
-    LIB_TRY(cellm_hip_qgemv_i8(H, m->embed, m->embed_scale, CELLM_HIP_DTYPE_F16, vocab, xn, CELLM_HIP_DTYPE_F32, nullptr, lg, R,
+    LIB_TRY(cellm_hip_qgemv_i8(H, m->lm_w, m->lm_s, CELLM_HIP_DTYPE_F16, vocab, xn, CELLM_HIP_DTYPE_F32, nullptr, lg, R,
                                vocab, hid, S),
             "lm_head");
     LIB_TRY(cellm_hip_argmax_f32(H, lg, R, vocab, d_idx, d_val, S), "argmax");
@@ -268,6 +270,11 @@ int32_t prepare_graphs(cellm_llama_dev* m)
     return CELLM_HIP_OK;
 }
 
+int32_t dev_create_impl(const cellm_llama_config_t* cfg, const cellm_llama_layer_t* layers, const int8_t* embed_i8,
+                        const uint16_t* embed_scale_f16, const int8_t* lm_i8, const uint16_t* lm_scale_f16,
+                        const uint16_t* final_norm_f16, int32_t device, int32_t max_rows, int32_t max_blocks,
+                        cellm_llama_dev_t** out);
+
 }  // namespace
 
 extern "C" {
@@ -292,6 +299,19 @@ int32_t cellm_llama_dev_create(const cellm_llama_config_t* cfg, const cellm_llam
                                const int8_t* embed_i8, const uint16_t* embed_scale_f16,
                                const uint16_t* final_norm_f16, int32_t device, int32_t max_rows, int32_t max_blocks,
                                cellm_llama_dev_t** out)
+{
+    return dev_create_impl(cfg, layers, embed_i8, embed_scale_f16, nullptr, nullptr, final_norm_f16, device, max_rows,
+                           max_blocks, out);
+}
+
+}  // extern "C"
+
+namespace {
+
+int32_t dev_create_impl(const cellm_llama_config_t* cfg, const cellm_llama_layer_t* layers, const int8_t* embed_i8,
+                        const uint16_t* embed_scale_f16, const int8_t* lm_i8, const uint16_t* lm_scale_f16,
+                        const uint16_t* final_norm_f16, int32_t device, int32_t max_rows, int32_t max_blocks,
+                        cellm_llama_dev_t** out)
 {
     if (!cfg || !layers || !embed_i8 || !embed_scale_f16 || !final_norm_f16 || !out)
         return fail(CELLM_HIP_ERR_INVALID_ARG, "null argument");
@@ -358,6 +378,16 @@ int32_t cellm_llama_dev_create(const cellm_llama_config_t* cfg, const cellm_llam
         return bail(rc);
     m->embed = reinterpret_cast<const int8_t*>(de);
     m->embed_scale = reinterpret_cast<const uint16_t*>(des);
+    m->lm_w = m->embed;
+    m->lm_s = m->embed_scale;
+    if (lm_i8) {
+        const void *dl = nullptr, *dls = nullptr;
+        if ((rc = upload(m, "lm_head.weight", lm_i8, (size_t)c.vocab * hid, &dl)) ||
+            (rc = upload(m, "lm_head.weight.qscale", lm_scale_f16, (size_t)c.vocab * 2, &dls)))
+            return bail(rc);
+        m->lm_w = reinterpret_cast<const int8_t*>(dl);
+        m->lm_s = reinterpret_cast<const uint16_t*>(dls);
+    }
 
     // paged K/V (KvCacheLayout: total_blocks x layers x tokens_per_block x kv_dim), zeroed
     m->kv_elems = (size_t)c.total_blocks * L * c.tokens_per_block * m->kvd;
@@ -399,6 +429,10 @@ int32_t cellm_llama_dev_create(const cellm_llama_config_t* cfg, const cellm_llam
     return CELLM_HIP_OK;
 }
 
+}  // namespace
+
+extern "C" {
+
 void cellm_llama_dev_destroy(cellm_llama_dev_t* m)
 {
     if (!m) return;
@@ -413,6 +447,108 @@ void cellm_llama_dev_destroy(cellm_llama_dev_t* m)
     cellm_hip_ctx_t* hip = m->hip;
     delete m;
     if (hip) cellm_hip_destroy(hip);
+}
+
+int32_t cellm_llama_dev_create_from_file(const char* path, int32_t device, int32_t max_rows, int32_t max_blocks,
+                                         int32_t tokens_per_block, int32_t total_blocks, cellm_llama_dev_t** out)
+{
+    if (!path || !out) return fail(CELLM_HIP_ERR_INVALID_ARG, "null argument");
+    *out = nullptr;
+    cellm_file_t* f = nullptr;
+    if (int32_t rc = cellm_file_open(path, &f)) return from_hip_lib(rc, "cellm_file_open");
+    struct Closer {
+        cellm_file_t* f;
+        ~Closer() { cellm_file_close(f); }
+    } closer{f};
+    cellm_file_config_t fc;
+    if (int32_t rc = cellm_file_config(f, &fc)) return from_hip_lib(rc, "cellm_file_config");
+    // LlamaRunner::load (llama.rs:39-53): head_dim defaults to hidden / heads
+    const int64_t head_dim = fc.head_dim > 0 ? fc.head_dim : (fc.num_heads > 0 ? fc.hidden_dim / fc.num_heads : 0);
+    const int64_t dims[] = {fc.num_layers, fc.hidden_dim, fc.num_heads, fc.num_kv_heads, head_dim,
+                            fc.intermediate_size, fc.vocab_size};
+    for (int64_t d : dims)
+        if (d <= 0 || d > INT32_MAX) return fail(CELLM_HIP_ERR_INVALID_ARG, "cellm header: bad model dimension");
+    cellm_llama_config_t c{};
+    c.n_layers = (int32_t)fc.num_layers;
+    c.hidden = (int32_t)fc.hidden_dim;
+    c.n_heads = (int32_t)fc.num_heads;
+    c.n_kv_heads = (int32_t)fc.num_kv_heads;
+    c.head_dim = (int32_t)head_dim;
+    c.intermediate = (int32_t)fc.intermediate_size;
+    c.vocab = (int32_t)fc.vocab_size;
+    c.rms_norm_eps = fc.rms_norm_eps;
+    c.rope_theta = fc.rope_theta;
+    c.tokens_per_block = tokens_per_block;
+    c.total_blocks = total_blocks;
+
+    // detect_llama_prefix (llama.rs:1094-1113)
+    std::string prefix;
+    {
+        bool found = false;
+        for (const char* p : {"", "language_model."}) {
+            const std::string e = std::string(p) + "model.embed_tokens.weight", n = std::string(p) + "model.norm.weight";
+            if (cellm_file_find(f, e.c_str(), nullptr) == CELLM_HIP_OK &&
+                cellm_file_find(f, n.c_str(), nullptr) == CELLM_HIP_OK) {
+                prefix = p;
+                found = true;
+                break;
+            }
+        }
+        if (!found)
+            return fail(CELLM_HIP_ERR_NOT_FOUND,
+                        "missing required llama tensors: model.embed_tokens.weight/model.norm.weight");
+    }
+    // a tensor of the given dtype and shape ([d0] when d1 < 0), as mapped bytes
+    auto tensor = [&](const std::string& name, const char* dtype, int64_t d0, int64_t d1, const void** p) -> int32_t {
+        cellm_file_tensor_t t;
+        if (cellm_file_find(f, name.c_str(), &t) != CELLM_HIP_OK)
+            return fail(CELLM_HIP_ERR_NOT_FOUND, "tensor %s missing", name.c_str());
+        if (strcmp(t.dtype, dtype) != 0)
+            return fail(CELLM_HIP_ERR_UNSUPPORTED, "tensor %s is %s; the device step takes %s", name.c_str(), t.dtype,
+                        dtype);
+        const int64_t elem = strcmp(dtype, "f16") == 0 ? 2 : 1;
+        const bool shape_ok = d1 < 0 ? (t.ndim == 1 && t.shape[0] == d0)
+                                     : (t.ndim == 2 && t.shape[0] == d0 && t.shape[1] == d1);
+        if (!shape_ok || t.nbytes != (uint64_t)(d0 * (d1 < 0 ? 1 : d1) * elem))
+            return fail(CELLM_HIP_ERR_INVALID_ARG, "tensor %s has shape/bytes that do not match the config",
+                        name.c_str());
+        return cellm_file_tensor_bytes(f, name.c_str(), p, nullptr) == CELLM_HIP_OK
+                   ? CELLM_HIP_OK
+                   : fail(CELLM_HIP_ERR_INVALID_ARG, "tensor %s unreadable", name.c_str());
+    };
+    std::vector<cellm_llama_layer_t> layers((size_t)c.n_layers);
+    for (int32_t l = 0; l < c.n_layers; ++l) {
+        const std::string pre = prefix + "model.layers." + std::to_string(l) + ".";
+        for (int j = 0; j < 7; ++j) {
+            size_t o, i;
+            out_in(c, j, &o, &i);
+            const std::string w = pre + kNames[j] + ".weight";
+            const void *pw = nullptr, *ps = nullptr;
+            if (int32_t rc = tensor(w, "i8", (int64_t)o, (int64_t)i, &pw)) return rc;
+            if (int32_t rc = tensor(w + ".qscale", "f16", (int64_t)o, -1, &ps)) return rc;
+            layers[l].w[j] = static_cast<const int8_t*>(pw);
+            layers[l].scale_f16[j] = static_cast<const uint16_t*>(ps);
+        }
+        const void *n1 = nullptr, *n2 = nullptr;
+        if (int32_t rc = tensor(pre + "input_layernorm.weight", "f16", c.hidden, -1, &n1)) return rc;
+        if (int32_t rc = tensor(pre + "post_attention_layernorm.weight", "f16", c.hidden, -1, &n2)) return rc;
+        layers[l].input_layernorm_f16 = static_cast<const uint16_t*>(n1);
+        layers[l].post_attention_layernorm_f16 = static_cast<const uint16_t*>(n2);
+    }
+    const void *emb = nullptr, *embs = nullptr, *fn = nullptr, *lm = nullptr, *lms = nullptr;
+    if (int32_t rc = tensor(prefix + "model.embed_tokens.weight", "i8", c.vocab, c.hidden, &emb)) return rc;
+    if (int32_t rc = tensor(prefix + "model.embed_tokens.weight.qscale", "f16", c.vocab, -1, &embs)) return rc;
+    if (int32_t rc = tensor(prefix + "model.norm.weight", "f16", c.hidden, -1, &fn)) return rc;
+    // lm_head.weight when the file has one, else the tied embedding (llama.rs:522-532)
+    for (const std::string& name : {prefix + "lm_head.weight", std::string("lm_head.weight")}) {
+        if (cellm_file_find(f, name.c_str(), nullptr) != CELLM_HIP_OK) continue;
+        if (int32_t rc = tensor(name, "i8", c.vocab, c.hidden, &lm)) return rc;
+        if (int32_t rc = tensor(name + ".qscale", "f16", c.vocab, -1, &lms)) return rc;
+        break;
+    }
+    return dev_create_impl(&c, layers.data(), static_cast<const int8_t*>(emb), static_cast<const uint16_t*>(embs),
+                           static_cast<const int8_t*>(lm), static_cast<const uint16_t*>(lms),
+                           static_cast<const uint16_t*>(fn), device, max_rows, max_blocks, out);
 }
 
 int32_t cellm_llama_dev_set_graphs(cellm_llama_dev_t* m, int32_t enable)

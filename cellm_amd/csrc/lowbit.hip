@@ -31,19 +31,42 @@ namespace {
 constexpr int kBlock = 256;
 constexpr int kPad = 4;  // floats of LDS padding after each unit of x
 
+struct Q1Block {
+    uint16_t h[9];  // f16 d, then 8 words of sign bits (little endian)
+};
+
 template <int FMT>
 struct LowbitFmt;
 template <>
 struct LowbitFmt<LB_F16> {
     static constexpr int kElems = 8;  // elements per 16-byte unit
+    using unit_t = u4_t;
+    __device__ __forceinline__ static unit_t load(const uint8_t* row, int u)
+    {
+        return *reinterpret_cast<const u4_t*>(row + (size_t)u * 16);
+    }
 };
 template <>
 struct LowbitFmt<LB_I2> {
     static constexpr int kElems = 64;
+    using unit_t = u4_t;
+    __device__ __forceinline__ static unit_t load(const uint8_t* row, int u)
+    {
+        return *reinterpret_cast<const u4_t*>(row + (size_t)u * 16);
+    }
 };
 template <>
 struct LowbitFmt<LB_Q1> {
-    static constexpr int kElems = 128;  // one 18-byte block
+    static constexpr int kElems = 128;  // one 18-byte block, 2-byte aligned
+    using unit_t = Q1Block;
+    __device__ __forceinline__ static unit_t load(const uint8_t* row, int u)
+    {
+        const uint16_t* b = reinterpret_cast<const uint16_t*>(row + (size_t)u * 18);
+        Q1Block q;
+#pragma unroll
+        for (int i = 0; i < 9; ++i) q.h[i] = b[i];
+        return q;
+    }
 };
 
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
@@ -82,6 +105,15 @@ __global__ __launch_bounds__(kBlock) void lowbit_gemv_kernel(const uint8_t* __re
     float scale = 1.0f;
     if constexpr (FMT == LB_I2) scale = h2f(S[min(n, N - 1)]);
 
+    // the lane's first two units are loaded before x is staged (one memory latency for both)
+    using unit_t = typename LowbitFmt<FMT>::unit_t;
+    unit_t pre[2];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        const int u = min(lane + p * LPR, units - 1);
+        pre[p] = LowbitFmt<FMT>::load(row, u);
+    }
+
     for (int m0 = 0; m0 < M; m0 += MT) {
         const int mt = min(MT, M - m0);
         for (int i = threadIdx.x; i < mt * K; i += kBlock) {
@@ -93,10 +125,12 @@ __global__ __launch_bounds__(kBlock) void lowbit_gemv_kernel(const uint8_t* __re
 #pragma unroll
         for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
         if (active) {
-            for (int u = lane; u < units; u += LPR) {
+            int p = 0;
+            for (int u = lane; u < units; u += LPR, ++p) {
+                const unit_t raw = (m0 == 0 && p < 2) ? (p == 0 ? pre[0] : pre[1]) : LowbitFmt<FMT>::load(row, u);
                 const float* xu = xs + u * (UE + kPad);
                 if constexpr (FMT == LB_F16) {
-                    const h8_t wh = __builtin_bit_cast(h8_t, *reinterpret_cast<const u4_t*>(row + (size_t)u * 16));
+                    const h8_t wh = __builtin_bit_cast(h8_t, raw);
 #pragma unroll
                     for (int m = 0; m < MT; ++m) {
                         const f4_t a = *reinterpret_cast<const f4_t*>(xu + m * xstride);
@@ -113,7 +147,6 @@ __global__ __launch_bounds__(kBlock) void lowbit_gemv_kernel(const uint8_t* __re
                         acc[m] = s;
                     }
                 } else if constexpr (FMT == LB_I2) {
-                    const u4_t raw = *reinterpret_cast<const u4_t*>(row + (size_t)u * 16);
                     const I2Table tab = i2_table(scale, scale_mode);
 #pragma unroll
                     for (int wd = 0; wd < 4; ++wd) {
@@ -136,15 +169,10 @@ __global__ __launch_bounds__(kBlock) void lowbit_gemv_kernel(const uint8_t* __re
                         }
                     }
                 } else {
-                    // 18-byte block: 9 little-endian u16 words (2-byte aligned)
-                    const uint16_t* blk = reinterpret_cast<const uint16_t*>(row + (size_t)u * 18);
-                    uint16_t hw[9];
-#pragma unroll
-                    for (int i = 0; i < 9; ++i) hw[i] = blk[i];
-                    const float d = h2f(hw[0]);
+                    const float d = h2f(raw.h[0]);
 #pragma unroll
                     for (int t = 0; t < 8; ++t) {
-                        const uint32_t bits = hw[1 + t];
+                        const uint32_t bits = raw.h[1 + t];
 #pragma unroll
                         for (int q4 = 0; q4 < 4; ++q4) {
                             float v[4];

@@ -80,6 +80,8 @@ def _load():
     lib.cellm_llama_dev_step.argtypes = [C.c_void_p, C.c_int32, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                          C.c_void_p, C.c_void_p]
     lib.cellm_llama_dev_set_graphs.argtypes = [C.c_void_p, C.c_int32]
+    lib.cellm_llama_dev_create_from_file.argtypes = [C.c_char_p, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
+                                                     C.c_int32, C.POINTER(C.c_void_p)]
     lib.cellm_llama_dev_destroy.argtypes = [C.c_void_p]
     lib.cellm_llama_last_error_message.restype = C.c_size_t
     lib.cellm_llama_last_error_message.argtypes = [C.c_char_p, C.c_size_t]
@@ -137,6 +139,32 @@ class LlamaDevice:
                                                          fn.ctypes.data, device, max_rows, self.max_blocks,
                                                          C.byref(h)), "cellm_llama_dev_create")
         self.h = h
+
+    @classmethod
+    def from_file(cls, path, device: int = 0, max_rows: int = 4, max_blocks: int = 64, tokens_per_block: int = 16,
+                  total_blocks: int | None = None) -> "LlamaDevice":
+        """A runner over an int8 .cellm model (cellm_llama_dev_create_from_file); the shape comes from
+        the file's header, the paged K/V cache from the arguments (total_blocks defaults to
+        max_rows * max_blocks)."""
+        from .cellm_file import CellmFile
+
+        with CellmFile(path) as f:
+            c = f.config
+        total = total_blocks if total_blocks is not None else max_rows * max_blocks
+        head_dim = c["head_dim"] if c["head_dim"] > 0 else c["hidden_dim"] // c["num_heads"]
+        self = cls.__new__(cls)
+        self.lib = _load()
+        self.shape = LlamaShape(c["num_layers"], c["hidden_dim"], c["num_heads"], c["num_kv_heads"], head_dim,
+                                c["intermediate_size"], c["vocab_size"], c["rms_norm_eps"], c["rope_theta"],
+                                tokens_per_block, total)
+        self.max_rows = max_rows
+        self.max_blocks = max_blocks
+        h = C.c_void_p()
+        _check(self.lib, self.lib.cellm_llama_dev_create_from_file(str(path).encode(), device, max_rows, max_blocks,
+                                                                   tokens_per_block, total, C.byref(h)),
+               "cellm_llama_dev_create_from_file")
+        self.h = h
+        return self
 
     def close(self) -> None:
         if getattr(self, "h", None):

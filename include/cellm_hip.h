@@ -339,6 +339,71 @@ int32_t cellm_hip_add_f32_inplace(cellm_hip_ctx_t* ctx, float* x, const float* y
 int32_t cellm_hip_argmax_f32(cellm_hip_ctx_t* ctx, const float* logits, int64_t rows, int64_t n, int32_t* out_index,
                              float* out_value, void* stream);
 
+/* ---- .cellm model files -----------------------------------------------------
+ * CellmFile (crates/cellm-model/src/cellm_file.rs:58-146): "CELLM", version 1,
+ * u32 little-endian header length, JSON header whose "tensors" list gives
+ * each tensor's name, absolute offset_bytes, nbytes, shape and dtype string
+ * ("f32", "f16", "bf16", "i8", "u8", "u32", "i4", "i2", "q1_0_g128", ...;
+ * int8 / i4 / i2 weights have an f16 "<name>.qscale" companion, MLX affine
+ * u32 weights ".scales" / ".biases").  The file is memory-mapped read-only
+ * and every tensor range is checked at open.  These calls touch no device. */
+typedef struct cellm_file cellm_file_t;
+
+/* The model fields of CellmHeader (cellm_file.rs:20-48) a runner needs;
+ * optional counts the header omits are -1, tie_word_embeddings -1 if absent. */
+typedef struct {
+    char model_type[64];
+    int64_t vocab_size;
+    int64_t hidden_dim;
+    int64_t intermediate_size;
+    int64_t num_layers;
+    int64_t num_heads;
+    int64_t num_kv_heads;
+    int64_t head_dim;
+    int64_t bos_token_id;
+    int64_t eos_token_id;
+    int64_t max_position_embeddings;
+    float rms_norm_eps;
+    float rope_theta;
+    int32_t tie_word_embeddings;
+} cellm_file_config_t;
+
+/* One entry of the header's tensor list (CellmTensorIndex, cellm_file.rs:11-18);
+ * name and dtype stay valid until cellm_file_close. */
+typedef struct {
+    const char* name;
+    const char* dtype;
+    int64_t shape[8];
+    int32_t ndim;
+    uint64_t offset_bytes;
+    uint64_t nbytes;
+} cellm_file_tensor_t;
+
+/* CellmFile::load: map, validate, parse; pages are touched once (the
+ * reference's pre-warm, cellm_file.rs:91-105). */
+int32_t cellm_file_open(const char* path, cellm_file_t** out);
+void cellm_file_close(cellm_file_t* f);
+int32_t cellm_file_config(const cellm_file_t* f, cellm_file_config_t* out);
+/* The raw JSON header text (not NUL-terminated), valid until close. */
+int32_t cellm_file_header_json(const cellm_file_t* f, const char** out_text, size_t* out_len);
+int64_t cellm_file_tensor_count(const cellm_file_t* f);
+/* The index-th tensor of the header, in header order. */
+int32_t cellm_file_tensor_at(const cellm_file_t* f, int64_t index, cellm_file_tensor_t* out);
+/* tensor_index / has_tensor: CELLM_HIP_ERR_NOT_FOUND if the name is absent
+ * (out may be NULL to test presence). */
+int32_t cellm_file_find(const cellm_file_t* f, const char* name, cellm_file_tensor_t* out);
+/* tensor_bytes (cellm_file.rs:138-146): the mapped bytes of a tensor. */
+int32_t cellm_file_tensor_bytes(const cellm_file_t* f, const char* name, const void** out_host, size_t* out_nbytes);
+
+/* Device-resident weights from a file: every tensor whose name starts with
+ * name_prefix (NULL or "" = all) goes into ctx's weight cache under its own
+ * name, one host-to-device copy each, as the Metal graphs preload every
+ * tensor of the file once (preload_weight, llama_graph.rs:92-110, gemma_graph.rs:145;
+ * called from llama.rs:146).  Returns how many tensors and bytes were
+ * uploaded; look them up with cellm_hip_weight_lookup. */
+int32_t cellm_hip_upload_cellm_file(cellm_hip_ctx_t* ctx, const cellm_file_t* f, const char* name_prefix,
+                                    int64_t* out_count, size_t* out_bytes);
+
 #ifdef __cplusplus
 }
 #endif

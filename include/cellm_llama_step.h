@@ -97,6 +97,17 @@ int32_t cellm_llama_dev_create(const cellm_llama_config_t* cfg, const cellm_llam
                                const uint16_t* final_norm_f16, int32_t device, int32_t max_rows, int32_t max_blocks,
                                cellm_llama_dev_t** out);
 
+/* The same runner from a .cellm file (LlamaRunner::load, llama.rs:39-75): the
+ * model shape from the header (head_dim defaults to hidden / heads), the
+ * tensor prefix "" or "language_model." (detect_llama_prefix,
+ * llama.rs:1094-1113), int8 projection weights with f16 ".qscale" row scales,
+ * f16 norms, the int8 embedding as the lm_head unless the file has an int8
+ * lm_head.weight (llama.rs:522-532).  Other dtypes are
+ * CELLM_HIP_ERR_UNSUPPORTED.  tokens_per_block / total_blocks size the paged
+ * K/V cache; the file is closed before this returns. */
+int32_t cellm_llama_dev_create_from_file(const char* path, int32_t device, int32_t max_rows, int32_t max_blocks,
+                                         int32_t tokens_per_block, int32_t total_blocks, cellm_llama_dev_t** out);
+
 void cellm_llama_dev_destroy(cellm_llama_dev_t* m);
 
 /* enable = 0: steps enqueue their launches one by one instead of replaying

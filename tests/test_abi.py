@@ -19,6 +19,16 @@ def declared_symbols(header: Path = HEADER, prefix: str = "cellm_hip_") -> set[s
     return set(re.findall(r"\b(" + prefix + r"\w+)\s*\(", text))
 
 
+def test_library_exports_the_cellm_file_api():
+    from cellm_amd import _lib
+
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True, text=True,
+                         check=True)
+    exported = set(re.findall(r"\bT (cellm_file_\w+)", out.stdout))
+    declared = declared_symbols(prefix="cellm_file_")
+    assert declared and declared <= exported, sorted(declared - exported)
+
+
 def test_library_exports_every_declared_symbol():
     from cellm_amd import _lib
 

@@ -1,0 +1,175 @@
+"""A .cellm file to device-resident weights (cellm_hip_upload_cellm_file) and
+to the device decode runner (cellm_llama_dev_create_from_file).
+
+- every uploaded tensor's device bytes equal the file's bytes;
+- a runner built from a file decodes bit-identically (ids, logits, K/V) to
+  one built from the same tensors in memory;
+- with an untied int8 lm_head.weight whose rows are the embedding's rows
+  permuted, the logits come out permuted the same way, exactly (each logit
+  row depends only on its own weight row).
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle
+from _cellm_writer import llama_header, write_cellm
+
+pytestmark = pytest.mark.gpu
+
+L, HID, NH, NKV, HD, INTER, VOCAB = 2, 960, 15, 5, 64, 2560, 49152
+TPB, CTX, ROWS = 16, 512, 4
+KVD = NKV * HD
+NAMES = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj", "mlp.gate_proj",
+         "mlp.up_proj", "mlp.down_proj")
+
+
+def shapes():
+    return [(HID, HID), (KVD, HID), (KVD, HID), (HID, HID), (INTER, HID), (INTER, HID), (HID, INTER)]
+
+
+def make_model():
+    layers = []
+    for l in range(L):
+        ws, ss = [], []
+        for j, (o, i) in enumerate(shapes()):
+            sd = 0xCF000000 + l * 64 + j * 4
+            ws.append(oracle.gen_i8((o, i), sd))
+            ss.append((oracle.gen_uniform((o,), sd + 1, 0.5, 1.5) / (73.3 * np.sqrt(i))).astype(np.float16))
+        n1 = (1.0 + 0.1 * oracle.lcg_fill(HID, 0xCF100000 + l, 1.0)).astype(np.float16)
+        n2 = (1.0 + 0.1 * oracle.lcg_fill(HID, 0xCF200000 + l, 1.0)).astype(np.float16)
+        layers.append((ws, ss, n1, n2))
+    embed = oracle.gen_i8((VOCAB, HID), 0xCF300000)
+    escale = (oracle.gen_uniform((VOCAB,), 0xCF300001, 0.5, 1.5) / 127.0).astype(np.float16)
+    fnorm = (1.0 + 0.1 * oracle.lcg_fill(HID, 0xCF300002, 1.0)).astype(np.float16)
+    return layers, embed, escale, fnorm
+
+
+def file_tensors(model, prefix="", lm_head=None):
+    layers, embed, escale, fnorm = model
+    ts = []
+    for l, (ws, ss, n1, n2) in enumerate(layers):
+        pre = f"{prefix}model.layers.{l}."
+        for j, name in enumerate(NAMES):
+            ts.append((pre + name + ".weight", ws[j], "i8", ws[j].shape))
+            ts.append((pre + name + ".weight.qscale", ss[j], "f16", ss[j].shape))
+        ts.append((pre + "input_layernorm.weight", n1, "f16", n1.shape))
+        ts.append((pre + "post_attention_layernorm.weight", n2, "f16", n2.shape))
+    ts.append((prefix + "model.embed_tokens.weight", embed, "i8", embed.shape))
+    ts.append((prefix + "model.embed_tokens.weight.qscale", escale, "f16", escale.shape))
+    ts.append((prefix + "model.norm.weight", fnorm, "f16", fnorm.shape))
+    if lm_head is not None:
+        ts.append(("lm_head.weight", lm_head[0], "i8", lm_head[0].shape))
+        ts.append(("lm_head.weight.qscale", lm_head[1], "f16", lm_head[1].shape))
+    return ts
+
+
+def header(tied=True):
+    return llama_header(L, HID, NH, NKV, INTER, VOCAB, eps=1e-5, theta=100000.0, tie_word_embeddings=tied)
+
+
+@pytest.fixture(scope="module")
+def model():
+    return make_model()
+
+
+def kv_state():
+    total = ROWS * CTX // TPB
+    n = total * L * TPB * KVD
+    k = oracle.gen_normal((n,), 0xCF400000, 0.0, 1.0).astype(np.float16)
+    v = oracle.gen_normal((n,), 0xCF400001, 0.0, 1.0).astype(np.float16)
+    bts = np.array([[b * ROWS + s for b in range(CTX // TPB)] for s in range(ROWS)], np.uint32)
+    return k, v, bts
+
+
+def run(dev, k, v, bts):
+    dev.kv_upload(k, v)
+    tokens = np.array([(100 + 7919 * s) % VOCAB for s in range(ROWS)], np.uint32)
+    pos = np.array([CTX - 1, 300, 64, 0], np.int32)
+    ids, vals, logits = dev.step(tokens, pos, bts, want_logits=True)
+    kk, vv = dev.kv_download()
+    return ids, logits, kk, vv
+
+
+def test_upload_puts_file_bytes_on_the_device(tmp_path, model):
+    from cellm_amd import HipOps
+    from cellm_amd.cellm_file import CellmFile
+
+    p = tmp_path / "m.cellm"
+    ts = file_tensors(model)
+    write_cellm(p, header(), ts)
+    hip = C.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_int]
+    ops = HipOps(0)
+    try:
+        with CellmFile(p) as f:
+            count, nbytes = f.upload(ops, "model.layers.1.")
+            assert count == 7 * 2 + 2
+            count2, nbytes2 = f.upload(ops)
+            assert count2 == len(ts) and nbytes2 == sum(a.nbytes for _, a, _, _ in ts)
+        for name, a, _, _ in ts:
+            ptr, nb = ops.weight_lookup(name)
+            assert nb == a.nbytes
+            host = np.empty(a.nbytes, np.uint8)
+            assert hip.hipMemcpy(host.ctypes.data, ptr, nb, 2) == 0  # device to host
+            np.testing.assert_array_equal(host, np.frombuffer(a.tobytes(), np.uint8))
+    finally:
+        ops.close()
+
+
+@pytest.mark.parametrize("prefix", ["", "language_model."])
+def test_runner_from_file_equals_runner_from_memory(tmp_path, model, prefix):
+    from cellm_amd.llama_step import LlamaDevice, LlamaShape
+
+    layers, embed, escale, fnorm = model
+    p = tmp_path / "m.cellm"
+    write_cellm(p, header(), file_tensors(model, prefix))
+    k, v, bts = kv_state()
+    shape = LlamaShape(L, HID, NH, NKV, HD, INTER, VOCAB, 1e-5, 100000.0, TPB, ROWS * CTX // TPB)
+    mem = LlamaDevice(shape, layers, embed, escale, fnorm, 0, max_rows=ROWS, max_blocks=CTX // TPB)
+    try:
+        a = run(mem, k, v, bts)
+    finally:
+        mem.close()
+    dev = LlamaDevice.from_file(p, 0, max_rows=ROWS, max_blocks=CTX // TPB, tokens_per_block=TPB)
+    try:
+        b = run(dev, k, v, bts)
+    finally:
+        dev.close()
+    for x, y in zip(a, b):
+        np.testing.assert_array_equal(x, y)
+    print("ids", a[0].tolist())
+
+
+def test_untied_lm_head_from_file(tmp_path, model):
+    from cellm_amd.llama_step import LlamaDevice
+
+    layers, embed, escale, fnorm = model
+    perm = np.random.default_rng(5).permutation(VOCAB)
+    k, v, bts = kv_state()
+    p1, p2 = tmp_path / "tied.cellm", tmp_path / "untied.cellm"
+    write_cellm(p1, header(), file_tensors(model))
+    write_cellm(p2, header(tied=False), file_tensors(model, lm_head=(embed[perm], escale[perm])))
+    outs = []
+    for p in (p1, p2):
+        dev = LlamaDevice.from_file(p, 0, max_rows=ROWS, max_blocks=CTX // TPB, tokens_per_block=TPB)
+        try:
+            outs.append(run(dev, k, v, bts))
+        finally:
+            dev.close()
+    np.testing.assert_array_equal(outs[1][1], outs[0][1][:, perm])
+
+
+def test_runner_from_file_rejects_other_dtypes(tmp_path, model):
+    from cellm_amd._lib import CellmHipError
+    from cellm_amd.llama_step import LlamaDevice
+
+    ts = file_tensors(model)
+    ts = [(n, a, "f16" if n == "model.layers.0.self_attn.q_proj.weight" else d, s) for n, a, d, s in ts]
+    p = tmp_path / "bad.cellm"
+    write_cellm(p, header(), ts)
+    with pytest.raises(CellmHipError, match="q_proj.weight is f16"):
+        LlamaDevice.from_file(p, 0, max_rows=ROWS, max_blocks=CTX // TPB, tokens_per_block=TPB)
