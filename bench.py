@@ -52,6 +52,9 @@ def parse():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--eager-decode-step", action="store_true",
+                    help="time the configs[4] decode step with eager launches only (the same kernels without "
+                         "HIP graph replay; for runs under rocprofv3, whose kernel tracer fails on graph launches)")
     ap.add_argument("--no-extra", action="store_true", help="skip the extra configs")
     ap.add_argument("--pmc-sample", action="store_true",
                     help="run only a 256 MiB device copy (counter calibration) and 20 lm_head GEMVs, for "
@@ -204,7 +207,7 @@ def main():
 
     extra = {}
     if not args.no_extra:
-        extra = extra_configs(torch, ops, stream, gen)
+        extra = extra_configs(torch, ops, stream, gen, graphs=not args.eager_decode_step)
 
     cpu = None
     if not args.no_cpu:
@@ -237,7 +240,7 @@ def main():
     ops.close()
 
 
-def extra_configs(torch, ops, stream, gen):
+def extra_configs(torch, ops, stream, gen, graphs: bool = True):
     """configs[0], [2], [3]: int8 GEMV, Gemma batched decode, M=512 prefill qGEMM;
     plus a measured device-to-device copy as the box's practical HBM figure."""
     res = {}
@@ -291,7 +294,7 @@ def extra_configs(torch, ops, stream, gen):
                                                    "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     del wset
 
-    res.update(decode_step_cfg5())
+    res.update(decode_step_cfg5(graphs))
     res.update(lowbit_gemvs(torch, ops, stream, gen))
 
     # M=512 prefill qGEMM (MFMA)
@@ -381,7 +384,7 @@ def cfg5_runner():
     return dev, shape, bts
 
 
-def decode_step_cfg5():
+def decode_step_cfg5(graphs: bool = True):
     """The configs[4] decode step: host ids in -> greedy ids out (input/output
     copies and the final synchronisation included), timed on the host clock,
     replaying the captured graph and, for comparison, launching eagerly.
@@ -397,9 +400,10 @@ def decode_step_cfg5():
         tokens = np.array([(1000 + 7919 * s) % shape.vocab for s in range(rows)], np.uint32)
         pos = np.full(rows, ctx - 1, np.int32)
         step_bytes = shape.weight_bytes() + rows * ctx * shape.n_layers * kvd * 2 * 2
-        entry = {"sessions": rows, "context": ctx, "bytes_per_step": step_bytes}
-        for mode, graphs in (("graph", True), ("eager", False)):
-            dev.set_graphs(graphs)
+        entry = {"sessions": rows, "context": ctx, "bytes_per_step": step_bytes,
+                 "launch": "captured HIP graph" if graphs else "eager launches"}
+        for replay in ((True, False) if graphs else (False,)):
+            dev.set_graphs(replay)
             for _ in range(3):
                 dev.step(tokens, pos, bts[:rows])
             n = 50
@@ -407,7 +411,7 @@ def decode_step_cfg5():
             for _ in range(n):
                 ids, _ = dev.step(tokens, pos, bts[:rows])
             us = (time.perf_counter() - t0) / n * 1e6
-            if graphs:
+            if replay or not graphs:
                 entry.update({"us_per_step": round(us, 1), "tokens_per_s": round(rows * 1e6 / us, 1),
                               "GB/s": round(step_bytes / (us * 1e-6) / 1e9, 1),
                               "frac_hbm": round(step_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
