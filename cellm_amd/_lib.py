@@ -65,6 +65,11 @@ SIGNATURES = {
     "cellm_hip_qgemv_i2": (_i32, [_vp, _vp, _vp, _i32, _vp, _i32, _vp, _i64, _i64, _i64, _vp]),
     "cellm_hip_qgemv_q1_0_g128": (_i32, [_vp, _vp, _vp, _i32, _vp, _i64, _i64, _i64, _vp]),
     "cellm_hip_upload_cellm_file": (_i32, [_vp, _vp, C.c_char_p, _vp, _vp]),
+    "cellm_hip_decode_qkv_rope_kv": (_i32, [_vp, _vp, _vp, _vp, _vp, C.c_float, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
+                                            _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64,
+                                            _i64, _i64, _i64, _vp]),
+    "cellm_hip_decode_gate_up_silu": (_i32, [_vp, _vp, _vp, _vp, _vp, C.c_float, _vp, _vp, _vp, _vp, _i64, _i64,
+                                             _i64, _vp, _vp]),
     "cellm_hip_add_rms_norm": (_i32, [_vp, _vp, _vp, _vp, _i32, _i64, _i64, C.c_float, _vp, _vp]),
     "cellm_hip_rope_half_f32": (_i32, [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp]),
     "cellm_hip_rope_kv_write_f16": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp,

@@ -911,6 +911,69 @@ int32_t cellm_hip_rope_kv_write_f16(cellm_hip_ctx_t* ctx, float* q, float* k, co
     return CELLM_HIP_OK;
 }
 
+int32_t cellm_hip_decode_qkv_rope_kv(cellm_hip_ctx_t* ctx, const float* x_prev, const float* y, float* x_out,
+                                     const float* norm_w, float eps, const int8_t* wq, const uint16_t* sq,
+                                     const int8_t* wk, const uint16_t* sk, const int8_t* wv, const uint16_t* sv,
+                                     int64_t rows, int64_t hidden, int64_t n_heads, int64_t n_kv_heads,
+                                     int64_t head_dim, const int32_t* positions, const float* cos_sin,
+                                     int64_t table_positions, float* q_out, uint16_t* kcache, uint16_t* vcache,
+                                     const uint32_t* block_tables, int64_t max_blocks, int64_t total_blocks,
+                                     int64_t n_layers, int64_t tokens_per_block, int64_t layer, void* stream)
+{
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    if (int32_t rc = check_paged(rows, max_blocks, total_blocks, n_layers, tokens_per_block, layer)) return rc;
+    if (rows == 0) return CELLM_HIP_OK;
+    if (hidden > INT32_MAX || !decode_fused_supported((int)rows, (int)hidden) || hidden > 4096)
+        return set_error(CELLM_HIP_ERR_UNSUPPORTED, "fused decode QKV needs 1..4 rows and hidden %% 16 == 0, <= 4096 "
+                                                    "(got rows=%lld hidden=%lld)", (long long)rows, (long long)hidden);
+    if (n_heads < 1 || n_kv_heads < 1 || head_dim < 2 || head_dim % 2 != 0 || n_heads > 4096 || n_kv_heads > 4096 ||
+        head_dim > 4096)
+        return set_error(CELLM_HIP_ERR_INVALID_ARG, "bad head geometry %lld/%lld/%lld", (long long)n_heads,
+                         (long long)n_kv_heads, (long long)head_dim);
+    if (table_positions < 1 || table_positions > INT32_MAX)
+        return set_error(CELLM_HIP_ERR_INVALID_ARG, "table_positions must be >= 1");
+    if (!x_prev || !x_out || !norm_w || !wq || !sq || !wk || !sk || !wv || !sv || !positions || !cos_sin || !q_out ||
+        !kcache || !vcache || !block_tables)
+        return set_error(CELLM_HIP_ERR_INVALID_ARG, "null pointer");
+    if (x_out == x_prev || x_out == y)
+        return set_error(CELLM_HIP_ERR_INVALID_ARG, "x_out must not alias x_prev or y (other blocks still read them)");
+    if (!aligned16(wq) || !aligned16(wk) || !aligned16(wv))
+        return set_error(CELLM_HIP_ERR_INVALID_ARG, "weights must be 16-byte aligned");
+    DeviceGuard g(ctx->device);
+    const int8_t* w[3] = {wq, wk, wv};
+    const uint16_t* sc[3] = {sq, sk, sv};
+    HIP_TRY(launch_decode_qkv(x_prev, y, x_out, norm_w, eps, w, sc, (int)rows, (int)hidden, (int)n_heads,
+                              (int)n_kv_heads, (int)head_dim, positions, cos_sin, (int)table_positions, q_out, kcache,
+                              vcache, block_tables, (int)max_blocks, (int)total_blocks, (int)n_layers,
+                              (int)tokens_per_block, (int)layer, pick_stream(ctx, stream)),
+            "decode_qkv launch");
+    return CELLM_HIP_OK;
+}
+
+int32_t cellm_hip_decode_gate_up_silu(cellm_hip_ctx_t* ctx, const float* x_prev, const float* y, float* x_out,
+                                      const float* norm_w, float eps, const int8_t* wg, const uint16_t* sg,
+                                      const int8_t* wu, const uint16_t* su, int64_t rows, int64_t hidden,
+                                      int64_t inter, float* h, void* stream)
+{
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    if (rows == 0) return CELLM_HIP_OK;
+    if (rows < 0 || hidden > INT32_MAX || !decode_fused_supported((int)rows, (int)hidden) || hidden > 4096)
+        return set_error(CELLM_HIP_ERR_UNSUPPORTED, "fused decode gate/up needs 1..4 rows and hidden %% 16 == 0, "
+                                                    "<= 4096 (got rows=%lld hidden=%lld)", (long long)rows,
+                         (long long)hidden);
+    if (inter < 1 || inter > INT32_MAX) return set_error(CELLM_HIP_ERR_INVALID_ARG, "bad intermediate size");
+    if (!x_prev || !x_out || !norm_w || !wg || !sg || !wu || !su || !h)
+        return set_error(CELLM_HIP_ERR_INVALID_ARG, "null pointer");
+    if (x_out == x_prev || x_out == y)
+        return set_error(CELLM_HIP_ERR_INVALID_ARG, "x_out must not alias x_prev or y (other blocks still read them)");
+    if (!aligned16(wg) || !aligned16(wu)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "weights must be 16-byte aligned");
+    DeviceGuard g(ctx->device);
+    HIP_TRY(launch_decode_gate_up(x_prev, y, x_out, norm_w, eps, wg, sg, wu, su, (int)rows, (int)hidden, (int)inter, h,
+                                  pick_stream(ctx, stream)),
+            "decode_gate_up launch");
+    return CELLM_HIP_OK;
+}
+
 int32_t cellm_hip_attention_gqa_f16kv(cellm_hip_ctx_t* ctx, const float* q, const uint16_t* kcache,
                                       const uint16_t* vcache, const uint32_t* block_tables, int64_t max_blocks,
                                       int64_t total_blocks, const int32_t* positions, int64_t rows, int64_t n_heads,

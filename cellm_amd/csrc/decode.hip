@@ -447,6 +447,256 @@ __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(const float*
     }
 }
 
+// ---- fused decode-step GEMVs ------------------------------------------------
+// One launch replaces "residual add + RMSNorm, int8 GEMV(s), epilogue op":
+//   decode_qkv_kernel:     xn = rms_norm(x_prev + y) * w;  q, k, v = W xn;
+//                          RoPE on q and k; k and v into the paged cache
+//   decode_gate_up_kernel: xn = rms_norm(x_prev + y) * w;  h = silu(Wg xn) * (Wu xn)
+// Every block stages the whole normalised row(s) in LDS (each needs all of
+// xn); block 0 also writes x_prev + y to x_out, the next residual stream, a
+// different buffer from x_prev so that no block reads a row another has
+// already overwritten.  The add, sum of squares, reduction tree and scaling
+// are those of add_rms_norm_kernel, so xn has the same bits.  A team of LPR
+// lanes computes two output rows; each lane owns C 16-byte chunks of both,
+// loaded before the prologue so that their memory latency overlaps it.  x is
+// stored with 4 floats of padding after every 16 (lanes read it at a stride of
+// 16 floats, which would put 4 lanes on each bank group).
+
+__host__ __device__ __forceinline__ int xpad(int k) { return k + (k >> 4) * 4; }
+
+// x rows [rows][H] -> LDS xs[MT][xpad(H)] = rms_norm(x_prev + y) * w; block 0
+// writes x_prev + y to x_out (y may be null: x_prev as is).  KR * kNormThreads >= H.
+template <int MT, int KR, bool HASY>
+__device__ __forceinline__ void stage_add_norm(const float* __restrict__ x_prev, const float* __restrict__ y,
+                                               float* __restrict__ x_out, const float* __restrict__ w, int rows,
+                                               int H, float eps, float* xs, float (*red)[MT])
+{
+    const int t = threadIdx.x;
+    const int xst = xpad(H);
+    // every load first (addresses clamped in range, no branch between them), then the adds
+    float v[MT][KR], yv[MT][KR], wv[KR];
+#pragma unroll
+    for (int u = 0; u < KR; ++u) {
+        const int i = min(t + u * kNormThreads, H - 1);
+        wv[u] = w[i];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            const int mm = min(m, rows - 1);
+            v[m][u] = x_prev[(size_t)mm * H + i];
+            if constexpr (HASY) yv[m][u] = y[(size_t)mm * H + i];
+        }
+    }
+    if constexpr (HASY) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int u = 0; u < KR; ++u) v[m][u] = v[m][u] + yv[m][u];
+    }
+    float s[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        s[m] = 0.0f;
+#pragma unroll
+        for (int u = 0; u < KR; ++u) {
+            const int i = t + u * kNormThreads;
+            if (i < H && m < rows) {
+                if (blockIdx.x == 0) x_out[(size_t)m * H + i] = v[m][u];
+                s[m] = s[m] + v[m][u] * v[m][u];
+            }
+        }
+        s[m] = group_sum<64>(s[m]);
+        if ((t & 63) == 0) red[t >> 6][m] = s[m];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        if (m >= rows) break;
+        float tot = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kNormThreads / 64; ++i) tot = tot + red[i][m];
+        const float mean = tot / (float)H;
+        const float inv = 1.0f / sqrtf(mean + eps);
+#pragma unroll
+        for (int u = 0; u < KR; ++u) {
+            const int i = t + u * kNormThreads;
+            if (i < H) xs[m * xst + xpad(i)] = v[m][u] * inv * wv[u];
+        }
+    }
+    __syncthreads();
+}
+
+// This lane's C chunks of rows r0 and r1 (row bytes H), chunk index clamped.
+template <int C>
+__device__ __forceinline__ void load_rows_i8(const int8_t* __restrict__ w0, const int8_t* __restrict__ w1, int lane,
+                                             int LPR, int nchunk, u4_t (&a)[C], u4_t (&b)[C])
+{
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        const int ch = min(lane + c * LPR, nchunk - 1);
+        a[c] = reinterpret_cast<const u4_t*>(w0)[ch];
+        b[c] = reinterpret_cast<const u4_t*>(w1)[ch];
+    }
+}
+
+// acc0/acc1[m] += sum over this lane's chunks of w * xn[m]
+template <int MT, int C>
+__device__ __forceinline__ void dot_rows_i8(const u4_t (&a)[C], const u4_t (&b)[C], int lane, int LPR, int nchunk,
+                                            const float* xs, int xst, int rows, float (&acc0)[MT],
+                                            float (&acc1)[MT])
+{
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        const int ch = lane + c * LPR;
+        if (ch >= nchunk) break;
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            if (m >= rows) break;
+            const f4_t* xp = reinterpret_cast<const f4_t*>(xs + m * xst + ch * 20);
+            const f4_t xq[4] = {xp[0], xp[1], xp[2], xp[3]};
+            float d0 = acc0[m], d1 = acc1[m];
+#pragma unroll
+            for (int wd = 0; wd < 4; ++wd)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float xe = xq[wd][e];
+                    d0 = __builtin_fmaf((float)(int8_t)(a[c][wd] >> (8 * e)), xe, d0);
+                    d1 = __builtin_fmaf((float)(int8_t)(b[c][wd] >> (8 * e)), xe, d1);
+                }
+            acc0[m] = d0;
+            acc1[m] = d1;
+        }
+    }
+}
+
+struct DecodeQkvArgs {
+    const float* x_prev;
+    const float* y;
+    float* x_out;
+    const float* norm_w;
+    float eps;
+    const int8_t* w[3];    // q, k, v [rows_out][H]
+    const uint16_t* s[3];  // f16 row scales
+    int rows, H, n_heads, n_kv_heads, head_dim;
+    const int32_t* pos;
+    const float2* cs;
+    int table_positions;
+    float* q_out;
+    uint16_t* kc;
+    uint16_t* vc;
+    PagedKv kv;
+    int layer;
+};
+
+// Team -> one (head, i < head_dim/2) pair: rows i and i + head_dim/2 of a q,
+// k or v head, the two operands of one RoPE rotation.
+template <int LPR, int C, int MT, int KR, bool HASY>
+__global__ __launch_bounds__(256) void decode_qkv_kernel(DecodeQkvArgs a)
+{
+    extern __shared__ __align__(16) float xs[];
+    __shared__ float red[kNormThreads / 64][MT];
+    const int H = a.H, half = a.head_dim >> 1, nchunk = H >> 4;
+    const int team = threadIdx.x / LPR, lane = threadIdx.x % LPR;
+    const int pairs = (a.n_heads + 2 * a.n_kv_heads) * half;
+    const int p = min((int)(blockIdx.x * (256 / LPR) + team), pairs - 1);
+    const bool active = (int)(blockIdx.x * (256 / LPR) + team) < pairs;
+    const int hh = p / half, i = p - hh * half;
+    const int which = hh < a.n_heads ? 0 : (hh < a.n_heads + a.n_kv_heads ? 1 : 2);
+    const int head = which == 0 ? hh : (which == 1 ? hh - a.n_heads : hh - a.n_heads - a.n_kv_heads);
+    const int r0 = head * a.head_dim + i, r1 = r0 + half;
+    const int8_t* wm = which == 0 ? a.w[0] : (which == 1 ? a.w[1] : a.w[2]);
+    const uint16_t* sm = which == 0 ? a.s[0] : (which == 1 ? a.s[1] : a.s[2]);
+    u4_t w0[C], w1[C];
+    load_rows_i8<C>(wm + (size_t)r0 * H, wm + (size_t)r1 * H, lane, LPR, nchunk, w0, w1);
+    const float s0 = h2f(sm[r0]), s1 = h2f(sm[r1]);
+
+    stage_add_norm<MT, KR, HASY>(a.x_prev, a.y, a.x_out, a.norm_w, a.rows, H, a.eps, xs, red);
+
+    float acc0[MT], acc1[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc0[m] = acc1[m] = 0.0f;
+    dot_rows_i8<MT, C>(w0, w1, lane, LPR, nchunk, xs, xpad(H), a.rows, acc0, acc1);
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        acc0[m] = group_sum<LPR>(acc0[m]);
+        acc1[m] = group_sum<LPR>(acc1[m]);
+    }
+    if (!active) return;
+    // lane m writes session m: y = acc * scale (matmul_i8_f32), then the epilogue op
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        if (m != lane || m >= a.rows) continue;
+        const float v0 = acc0[m] * s0, v1 = acc1[m] * s1;
+        const int pr = a.pos[m];
+        const float2 c = a.cs[(size_t)min(max(pr, 0), a.table_positions - 1) * half + i];
+        if (which == 0) {
+            float* q = a.q_out + ((size_t)m * a.n_heads + head) * a.head_dim;
+            q[i] = v0 * c.x - v1 * c.y;
+            q[half + i] = v1 * c.x + v0 * c.y;
+            continue;
+        }
+        const long long b = pr >= 0 ? a.kv.base(m, pr, a.layer) : -1;
+        if (b < 0) continue;
+        const size_t e = (size_t)b + (size_t)head * a.head_dim;
+        if (which == 1) {
+            a.kc[e + i] = __builtin_bit_cast(uint16_t, (_Float16)(v0 * c.x - v1 * c.y));
+            a.kc[e + half + i] = __builtin_bit_cast(uint16_t, (_Float16)(v1 * c.x + v0 * c.y));
+        } else {
+            a.vc[e + i] = __builtin_bit_cast(uint16_t, (_Float16)v0);
+            a.vc[e + half + i] = __builtin_bit_cast(uint16_t, (_Float16)v1);
+        }
+    }
+}
+
+struct DecodeGateUpArgs {
+    const float* x_prev;
+    const float* y;
+    float* x_out;
+    const float* norm_w;
+    float eps;
+    const int8_t* wg;
+    const uint16_t* sg;
+    const int8_t* wu;
+    const uint16_t* su;
+    int rows, H, N;
+    float* h;  // [rows][N]
+};
+
+// Team -> row n of gate and of up; h = silu(g) * u as silu_mul_f32_inplace
+// (metal.rs:235-245): (g * (1 / (1 + exp(-g)))) * u.
+template <int LPR, int C, int MT, int KR, bool HASY>
+__global__ __launch_bounds__(256) void decode_gate_up_kernel(DecodeGateUpArgs a)
+{
+    extern __shared__ __align__(16) float xs[];
+    __shared__ float red[kNormThreads / 64][MT];
+    const int H = a.H, nchunk = H >> 4;
+    const int team = threadIdx.x / LPR, lane = threadIdx.x % LPR;
+    const int n_raw = blockIdx.x * (256 / LPR) + team;
+    const int n = min(n_raw, a.N - 1);
+    u4_t w0[C], w1[C];
+    load_rows_i8<C>(a.wg + (size_t)n * H, a.wu + (size_t)n * H, lane, LPR, nchunk, w0, w1);
+    const float sg = h2f(a.sg[n]), su = h2f(a.su[n]);
+
+    stage_add_norm<MT, KR, HASY>(a.x_prev, a.y, a.x_out, a.norm_w, a.rows, H, a.eps, xs, red);
+
+    float acc0[MT], acc1[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc0[m] = acc1[m] = 0.0f;
+    dot_rows_i8<MT, C>(w0, w1, lane, LPR, nchunk, xs, xpad(H), a.rows, acc0, acc1);
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        acc0[m] = group_sum<LPR>(acc0[m]);
+        acc1[m] = group_sum<LPR>(acc1[m]);
+    }
+    if (n_raw >= a.N) return;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        if (m != lane || m >= a.rows) continue;
+        const float g = acc0[m] * sg, u = acc1[m] * su;
+        const float sig = 1.0f / (1.0f + expf(-g));
+        a.h[(size_t)m * a.N + n] = (g * sig) * u;
+    }
+}
+
 __device__ __forceinline__ void argmax_take(float v, int i, float& best, int& bi)
 {
     if (!isfinite(v)) v = -INFINITY;          // llama.rs:1081-1092
@@ -637,6 +887,117 @@ hipError_t launch_attention_gqa_f16kv(const float* q, const uint16_t* kcache, co
     else
         by_g(std::integral_constant<int, 128>{});
     return hipGetLastError();
+}
+
+// Host-side geometry of the fused decode GEMVs: LPR = 64 lanes per row pair
+// while a row has at least 64 chunks of 16 bytes, fewer otherwise; C chunks
+// per lane; KR registers per thread of the staged row; MT activation rows.
+bool decode_fused_supported(int rows, int H)
+{
+    return rows >= 1 && rows <= 4 && H >= 16 && H % 16 == 0 && H <= 8 * kNormThreads;
+}
+
+size_t decode_fused_lds_bytes(int rows, int H)
+{
+    const int MT = rows <= 1 ? 1 : (rows <= 2 ? 2 : 4);
+    return (size_t)MT * xpad(H) * sizeof(float);
+}
+
+namespace {
+
+template <int LPR, int C, int MT, int KR, bool QKV, class Args>
+hipError_t launch_decode_fixed(const Args& a, int teams_total, size_t lds, hipStream_t st)
+{
+    const dim3 grid((unsigned)((teams_total + 256 / LPR - 1) / (256 / LPR)));
+    if constexpr (QKV) {
+        if (a.y)
+            hipLaunchKernelGGL((decode_qkv_kernel<LPR, C, MT, KR, true>), grid, dim3(256), lds, st, a);
+        else
+            hipLaunchKernelGGL((decode_qkv_kernel<LPR, C, MT, KR, false>), grid, dim3(256), lds, st, a);
+    } else {
+        if (a.y)
+            hipLaunchKernelGGL((decode_gate_up_kernel<LPR, C, MT, KR, true>), grid, dim3(256), lds, st, a);
+        else
+            hipLaunchKernelGGL((decode_gate_up_kernel<LPR, C, MT, KR, false>), grid, dim3(256), lds, st, a);
+    }
+    return hipGetLastError();
+}
+
+template <int LPR, int C, int MT, bool QKV, class Args>
+hipError_t launch_decode_kr(int H, const Args& a, int teams_total, size_t lds, hipStream_t st)
+{
+    const int kr = (H + kNormThreads - 1) / kNormThreads;
+    if (kr <= 1) return launch_decode_fixed<LPR, C, MT, 1, QKV>(a, teams_total, lds, st);
+    if (kr <= 2) return launch_decode_fixed<LPR, C, MT, 2, QKV>(a, teams_total, lds, st);
+    if (kr <= 4) return launch_decode_fixed<LPR, C, MT, 4, QKV>(a, teams_total, lds, st);
+    return launch_decode_fixed<LPR, C, MT, 8, QKV>(a, teams_total, lds, st);
+}
+
+template <int LPR, int C, bool QKV, class Args>
+hipError_t launch_decode_mt(int rows, int H, const Args& a, int teams_total, hipStream_t st)
+{
+    const size_t lds = decode_fused_lds_bytes(rows, H);
+    if (rows <= 1) return launch_decode_kr<LPR, C, 1, QKV>(H, a, teams_total, lds, st);
+    if (rows <= 2) return launch_decode_kr<LPR, C, 2, QKV>(H, a, teams_total, lds, st);
+    return launch_decode_kr<LPR, C, 4, QKV>(H, a, teams_total, lds, st);
+}
+
+// chunks per row nchunk = H / 16: LPR 64 with C = ceil(nchunk / 64) (up to 8)
+template <bool QKV, class Args>
+hipError_t launch_decode(int rows, int H, const Args& a, int teams_total, hipStream_t st)
+{
+    const int nchunk = H >> 4;
+    if (nchunk <= 16) return launch_decode_mt<16, 1, QKV>(rows, H, a, teams_total, st);
+    if (nchunk <= 32) return launch_decode_mt<32, 1, QKV>(rows, H, a, teams_total, st);
+    if (nchunk <= 64) return launch_decode_mt<64, 1, QKV>(rows, H, a, teams_total, st);
+    if (nchunk <= 128) return launch_decode_mt<64, 2, QKV>(rows, H, a, teams_total, st);
+    return launch_decode_mt<64, 4, QKV>(rows, H, a, teams_total, st);
+}
+
+}  // namespace
+
+hipError_t launch_decode_qkv(const float* x_prev, const float* y, float* x_out, const float* norm_w, float eps,
+                             const int8_t* const w[3], const uint16_t* const s[3], int rows, int H, int n_heads,
+                             int n_kv_heads, int head_dim, const int32_t* pos, const float* cos_sin,
+                             int table_positions, float* q_out, uint16_t* kcache, uint16_t* vcache,
+                             const uint32_t* block_tables, int max_blocks, int total_blocks, int n_layers,
+                             int tokens_per_block, int layer, hipStream_t st)
+{
+    DecodeQkvArgs a{};
+    a.x_prev = x_prev;
+    a.y = y;
+    a.x_out = x_out;
+    a.norm_w = norm_w;
+    a.eps = eps;
+    for (int j = 0; j < 3; ++j) {
+        a.w[j] = w[j];
+        a.s[j] = s[j];
+    }
+    a.rows = rows;
+    a.H = H;
+    a.n_heads = n_heads;
+    a.n_kv_heads = n_kv_heads;
+    a.head_dim = head_dim;
+    a.pos = pos;
+    a.cs = reinterpret_cast<const float2*>(cos_sin);
+    a.table_positions = table_positions;
+    a.q_out = q_out;
+    a.kc = kcache;
+    a.vc = vcache;
+    a.kv = PagedKv{block_tables, max_blocks, total_blocks, n_layers, tokens_per_block, n_kv_heads * head_dim};
+    a.layer = layer;
+    const int pairs = (n_heads + 2 * n_kv_heads) * (head_dim / 2);
+    if (H > 64 * 16 * 4) return hipErrorInvalidValue;
+    return launch_decode<true>(rows, H, a, pairs, st);
+}
+
+hipError_t launch_decode_gate_up(const float* x_prev, const float* y, float* x_out, const float* norm_w, float eps,
+                                 const int8_t* wg, const uint16_t* sg, const int8_t* wu, const uint16_t* su, int rows,
+                                 int H, int N, float* h, hipStream_t st)
+{
+    DecodeGateUpArgs a{x_prev, y, x_out, norm_w, eps, wg, sg, wu, su, rows, H, N, h};
+    if (H > 64 * 16 * 4) return hipErrorInvalidValue;
+    return launch_decode<false>(rows, H, a, N, st);
 }
 
 hipError_t launch_argmax(const float* logits, int rows, int n, int32_t* idx, float* val, hipStream_t st)

@@ -92,6 +92,19 @@ hipError_t launch_attention_gqa_f16kv(const float* q, const uint16_t* kcache, co
                                       int n_layers, int tokens_per_block, int layer, float* out, float* workspace,
                                       hipStream_t st);
 hipError_t launch_argmax(const float* logits, int rows, int n, int32_t* idx, float* val, hipStream_t st);
+// Fused decode-step GEMVs (decode.hip): residual add + RMSNorm prologue, int8
+// GEMV of two rows per team, RoPE + K/V write or SiLU * up epilogue.
+bool decode_fused_supported(int rows, int H);
+size_t decode_fused_lds_bytes(int rows, int H);
+hipError_t launch_decode_qkv(const float* x_prev, const float* y, float* x_out, const float* norm_w, float eps,
+                             const int8_t* const w[3], const uint16_t* const s[3], int rows, int H, int n_heads,
+                             int n_kv_heads, int head_dim, const int32_t* pos, const float* cos_sin,
+                             int table_positions, float* q_out, uint16_t* kcache, uint16_t* vcache,
+                             const uint32_t* block_tables, int max_blocks, int total_blocks, int n_layers,
+                             int tokens_per_block, int layer, hipStream_t st);
+hipError_t launch_decode_gate_up(const float* x_prev, const float* y, float* x_out, const float* norm_w, float eps,
+                                 const int8_t* wg, const uint16_t* sg, const int8_t* wu, const uint16_t* su, int rows,
+                                 int H, int N, float* h, hipStream_t st);
 
 // Remaining .cellm weight formats (lowbit.hip): f16 rows, i2 (2-bit per-row
 // symmetric, scale_mode 0 = scale at the end, 1 = per element), q1_0_g128.

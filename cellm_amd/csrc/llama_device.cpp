@@ -131,7 +131,8 @@ struct cellm_llama_dev {
     const int8_t* lm_w = nullptr;  // the tied embedding unless the model has its own lm_head
     const uint16_t* lm_s = nullptr;
     const float* final_norm = nullptr;
-    DevBuf kcache, vcache, rope, x, xn, q, k, v, attn, proj, h, logits, io;
+    DevBuf kcache, vcache, rope, x, x2, xn, q, k, v, attn, proj, h, logits, io;
+    bool fused = false;  // fused add+norm+GEMV launches (rows <= 4, hidden % 16 == 0, hidden <= 4096)
     // io: [tokens u32 | positions i32 | block tables u32 | argmax idx i32 | argmax val f32]
     void* host_io = nullptr;  // pinned mirror of io
     size_t io_tokens = 0, io_pos = 0, io_bt = 0, io_idx = 0, io_val = 0, io_bytes = 0;
@@ -195,6 +196,33 @@ int32_t enqueue_step(cellm_llama_dev* m, int32_t rows)
     const float eps = c.rms_norm_eps;
 
     LIB_TRY(cellm_hip_embed_i8(H, d_tok, R, m->embed, m->embed_scale, vocab, hid, x, S), "embed");
+    if (m->fused) {
+        // 5 launches per layer; the residual stream alternates between x and x2
+        float* x2 = m->x2.as<float>();
+        for (int64_t l = 0; l < L; ++l) {
+            const int8_t* const* W = &m->w[l * 7];
+            const uint16_t* const* Sc = &m->s[l * 7];
+            LIB_TRY(cellm_hip_decode_qkv_rope_kv(H, x, l == 0 ? nullptr : proj, x2, m->attn_norm[l], eps, W[0], Sc[0],
+                                                 W[1], Sc[1], W[2], Sc[2], R, hid, c.n_heads, c.n_kv_heads,
+                                                 c.head_dim, d_pos, m->rope.as<float>(), m->table_positions, q, kc, vc,
+                                                 d_bt, MB, c.total_blocks, L, tpb, l, S),
+                    "residual + input_layernorm + qkv + rope + kv write");
+            LIB_TRY(cellm_hip_attention_gqa_f16kv(H, q, kc, vc, d_bt, MB, c.total_blocks, d_pos, R, c.n_heads,
+                                                  c.n_kv_heads, c.head_dim, L, tpb, l, attn, S),
+                    "attention");
+            LIB_TRY(cellm_hip_qgemv_i8(H, W[3], Sc[3], CELLM_HIP_DTYPE_F16, hid, attn, CELLM_HIP_DTYPE_F32, nullptr,
+                                       proj, R, hid, hid, S),
+                    "o_proj");
+            LIB_TRY(cellm_hip_decode_gate_up_silu(H, x2, proj, x, m->mlp_norm[l], eps, W[4], Sc[4], W[5], Sc[5], R, hid,
+                                                  inter, h, S),
+                    "residual + post_attention_layernorm + gate/up");
+            LIB_TRY(cellm_hip_qgemv_i8(H, W[6], Sc[6], CELLM_HIP_DTYPE_F16, hid, h, CELLM_HIP_DTYPE_F32, nullptr, proj,
+                                       R, hid, inter, S),
+                    "down_proj");
+        }
+        LIB_TRY(cellm_hip_add_rms_norm(H, x, proj, m->final_norm, CELLM_HIP_DTYPE_F32, R, hid, eps, xn, S),
+                "residual + norm");
+    } else {
     LIB_TRY(cellm_hip_rms_norm(H, x, m->attn_norm[0], CELLM_HIP_DTYPE_F32, R, hid, eps, xn, S), "input_layernorm");
     for (int64_t l = 0; l < L; ++l) {
         const int8_t* const* W = &m->w[l * 7];
@@ -225,6 +253,7 @@ int32_t enqueue_step(cellm_llama_dev* m, int32_t rows)
         const float* next_norm = l + 1 < L ? m->attn_norm[l + 1] : m->final_norm;
         LIB_TRY(cellm_hip_add_rms_norm(H, x, proj, next_norm, CELLM_HIP_DTYPE_F32, R, hid, eps, xn, S),
                 "residual + norm");
+    }
     }
     // lm_head (tied embedding or lm_head.weight, llama.rs:522-567) through the int8 GEMV, greedy id on the device
     float* lg = m->logits.as<float>();
@@ -395,7 +424,8 @@ int32_t dev_create_impl(const cellm_llama_config_t* cfg, const cellm_llama_layer
     if ((rc = m->kcache.alloc(m->kv_elems * 2, "hipMalloc(K cache)")) ||
         (rc = m->vcache.alloc(m->kv_elems * 2, "hipMalloc(V cache)")) ||
         (rc = m->rope.alloc((size_t)m->table_positions * c.head_dim * sizeof(float), "hipMalloc(rope table)")) ||
-        (rc = m->x.alloc(R * hid * 4, "hipMalloc(x)")) || (rc = m->xn.alloc(R * hid * 4, "hipMalloc(xn)")) ||
+        (rc = m->x.alloc(R * hid * 4, "hipMalloc(x)")) || (rc = m->x2.alloc(R * hid * 4, "hipMalloc(x2)")) ||
+        (rc = m->xn.alloc(R * hid * 4, "hipMalloc(xn)")) ||
         (rc = m->q.alloc(R * hid * 4, "hipMalloc(q)")) || (rc = m->k.alloc(R * m->kvd * 4, "hipMalloc(k)")) ||
         (rc = m->v.alloc(R * m->kvd * 4, "hipMalloc(v)")) || (rc = m->attn.alloc(R * hid * 4, "hipMalloc(attn)")) ||
         (rc = m->proj.alloc(R * hid * 4, "hipMalloc(proj)")) || (rc = m->h.alloc(R * inter * 4, "hipMalloc(h)")) ||
@@ -410,6 +440,7 @@ int32_t dev_create_impl(const cellm_llama_config_t* cfg, const cellm_llama_layer
         e = hipMemcpy(m->rope.p, table.data(), table.size() * sizeof(float), hipMemcpyHostToDevice);
         if (e != hipSuccess) return bail(from_runtime(e, "upload rope table"));
     }
+    m->fused = (c.hidden % 16) == 0 && c.hidden <= 4096 && c.head_dim % 2 == 0;
     auto align = [](size_t v) { return (v + 255) & ~(size_t)255; };
     m->io_tokens = 0;
     m->io_pos = align(R * 4);

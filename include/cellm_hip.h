@@ -317,6 +317,32 @@ int32_t cellm_hip_rope_kv_write_f16(cellm_hip_ctx_t* ctx, float* q, float* k, co
                                     const uint32_t* block_tables, int64_t max_blocks, int64_t total_blocks,
                                     int64_t n_layers, int64_t tokens_per_block, int64_t layer, void* stream);
 
+/* One launch for "residual add + input_layernorm, q/k/v projections, RoPE,
+ * K/V write" of a decode layer (llama_graph.rs:245-292 encodes them as
+ * separate dispatches): x_out = x_prev + y (y may be NULL: x_prev as is),
+ * xn = rms_norm(x_out) * norm_w (f32 weights), q = RoPE(Wq xn) into q_out
+ * [rows][n_heads][head_dim], k = RoPE(Wk xn) and v = Wv xn written as f16 at
+ * each row's position in `layer` of the paged cache.  int8 weights [out][hidden]
+ * with f16 row scales.  x_out must be a different buffer from x_prev and y.
+ * rows 1..4, hidden % 16 == 0 and <= 4096; otherwise CELLM_HIP_ERR_UNSUPPORTED
+ * (use the separate calls). */
+int32_t cellm_hip_decode_qkv_rope_kv(cellm_hip_ctx_t* ctx, const float* x_prev, const float* y, float* x_out,
+                                     const float* norm_w, float eps, const int8_t* wq, const uint16_t* sq,
+                                     const int8_t* wk, const uint16_t* sk, const int8_t* wv, const uint16_t* sv,
+                                     int64_t rows, int64_t hidden, int64_t n_heads, int64_t n_kv_heads,
+                                     int64_t head_dim, const int32_t* positions, const float* cos_sin,
+                                     int64_t table_positions, float* q_out, uint16_t* kcache, uint16_t* vcache,
+                                     const uint32_t* block_tables, int64_t max_blocks, int64_t total_blocks,
+                                     int64_t n_layers, int64_t tokens_per_block, int64_t layer, void* stream);
+
+/* The same for "residual add + post_attention_layernorm, gate/up, SiLU * up"
+ * (llama_graph.rs:310-327): x_out = x_prev + y, xn = rms_norm(x_out) * norm_w,
+ * h [rows][inter] = silu(Wg xn) * (Wu xn).  Same limits as above. */
+int32_t cellm_hip_decode_gate_up_silu(cellm_hip_ctx_t* ctx, const float* x_prev, const float* y, float* x_out,
+                                      const float* norm_w, float eps, const int8_t* wg, const uint16_t* sg,
+                                      const int8_t* wu, const uint16_t* su, int64_t rows, int64_t hidden,
+                                      int64_t inter, float* h, void* stream);
+
 /* MetalKvStorage::encode_attention / attention_single_token_gqa_f32
  * (kvcache.rs:710-789, 1377-1439): each row attends over positions
  * 0..positions[r] of `layer`; q and out [rows][n_heads][head_dim] f32, query

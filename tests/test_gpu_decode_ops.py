@@ -253,3 +253,101 @@ def test_rope_kv_write_matches_rope_then_write(ops, steplib, nh, nkv, hd):
             v_ref[b:b + kvd] = v[r].astype(np.float16).view(np.uint16)
     np.testing.assert_array_equal(kc.cpu().numpy().view(np.uint16), k_ref)
     np.testing.assert_array_equal(vc.cpu().numpy().view(np.uint16), v_ref)
+
+
+def _i8_layer(out_dims, k, seed):
+    ws, ss = [], []
+    for j, o in enumerate(out_dims):
+        ws.append(oracle.gen_i8((o, k), seed + 4 * j))
+        ss.append((oracle.gen_uniform((o,), seed + 4 * j + 1, 0.5, 1.5) / (73.3 * np.sqrt(k))).astype(np.float16))
+    return ws, ss
+
+
+@pytest.mark.parametrize("rows,with_y", [(4, True), (1, True), (3, False)])
+def test_decode_qkv_matches_separate_ops(ops, steplib, rows, with_y):
+    """cellm_hip_decode_qkv_rope_kv against add_rms_norm + three int8 GEMVs +
+    rope_kv_write: the residual exactly, q within 1e-5 (the GEMV sums its row
+    in another order), the written K/V rows within f16 rounding, no other
+    cache element touched."""
+    H, nh, nkv, hd, L, tpb, layer = 960, 15, 5, 64, 3, 16, 2
+    kvd = nkv * hd
+    total, k0, v0, bt = paged_setup(L, tpb, nkv, hd, rows, 8, 0xD0000200)
+    pos = np.array([127, 0, 64, 17][:rows], np.int32)
+    table = rope_table(steplib, 100000.0, hd, 8 * tpb)
+    xp = np.stack([oracle.gen_normal((H,), 0xD0000210 + r, 0.0, 1.0) for r in range(rows)]).astype(np.float32)
+    y = np.stack([oracle.gen_normal((H,), 0xD0000220 + r, 0.0, 0.5) for r in range(rows)]).astype(np.float32)
+    nw = (1.0 + 0.1 * oracle.lcg_fill(H, 0xD0000230, 1.0)).astype(np.float32)
+    (wq, wk, wv), (sq, sk, sv) = _i8_layer([nh * hd, kvd, kvd], H, 0xD0000240)
+    d = [dev(a) for a in (wq, sq.view(np.uint16), wk, sk.view(np.uint16), wv, sv.view(np.uint16))]
+    d = [t.view(torch.float16) if t.dtype == torch.int16 else t for t in d]
+    # separate ops
+    x_sep = dev(xp.copy())
+    xn = torch.empty((rows, H), dtype=torch.float32, device="cuda")
+    if with_y:
+        ops.encode_add_rms_norm(x_sep, dev(y), dev(nw), xn, 1e-5)
+    else:
+        ops.encode_rms_norm(x_sep, dev(nw), xn, 1e-5)
+    q = torch.empty((rows, nh * hd), dtype=torch.float32, device="cuda")
+    k = torch.empty((rows, kvd), dtype=torch.float32, device="cuda")
+    v = torch.empty((rows, kvd), dtype=torch.float32, device="cuda")
+    ops.encode_qgemv_i8(d[0], d[1], xn, q)
+    ops.encode_qgemv_i8(d[2], d[3], xn, k)
+    ops.encode_qgemv_i8(d[4], d[5], xn, v)
+    kc1, vc1 = dev(k0.copy()), dev(v0.copy())
+    ops.encode_rope_kv_write(q, k, v, nh, nkv, hd, dev(pos), dev(table), kc1, vc1, dev(bt), total, L, tpb, layer)
+    # fused
+    x_out = torch.full((rows, H), np.nan, dtype=torch.float32, device="cuda")
+    q2 = torch.empty_like(q)
+    kc2, vc2 = dev(k0.copy()), dev(v0.copy())
+    ops.encode_decode_qkv(dev(xp), dev(y) if with_y else None, x_out, dev(nw), 1e-5, d[0], d[1], d[2], d[3], d[4],
+                          d[5], nh, nkv, hd, dev(pos), dev(table), q2, kc2, vc2, dev(bt), total, L, tpb, layer)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(x_out.cpu().numpy(), x_sep.cpu().numpy())
+    assert rel_err(q2.cpu().numpy(), q.cpu().numpy()) <= 1e-5
+    for got, ref, init in ((kc2, kc1, k0), (vc2, vc1, v0)):
+        g = got.cpu().numpy().view(np.uint16)
+        r = ref.cpu().numpy().view(np.uint16)
+        changed = r != init
+        np.testing.assert_array_equal(g[~changed], init[~changed])
+        gf, rf = oracle.f16_bits_to_f32(g[changed]), oracle.f16_bits_to_f32(r[changed])
+        assert np.max(np.abs(gf - rf)) <= 2e-3 * np.max(np.abs(rf))
+
+
+@pytest.mark.parametrize("rows", [4, 2, 1])
+def test_decode_gate_up_matches_separate_ops(ops, rows):
+    H, N = 960, 2560
+    xp = np.stack([oracle.gen_normal((H,), 0xD0000300 + r, 0.0, 1.0) for r in range(rows)]).astype(np.float32)
+    y = np.stack([oracle.gen_normal((H,), 0xD0000310 + r, 0.0, 0.5) for r in range(rows)]).astype(np.float32)
+    nw = (1.0 + 0.1 * oracle.lcg_fill(H, 0xD0000320, 1.0)).astype(np.float32)
+    (wg, wu), (sg, su) = _i8_layer([N, N], H, 0xD0000330)
+    wgd, wud = dev(wg), dev(wu)
+    sgd, sud = dev(sg.view(np.uint16)).view(torch.float16), dev(su.view(np.uint16)).view(torch.float16)
+    x_sep = dev(xp.copy())
+    xn = torch.empty((rows, H), dtype=torch.float32, device="cuda")
+    ops.encode_add_rms_norm(x_sep, dev(y), dev(nw), xn, 1e-5)
+    h = torch.empty((rows, N), dtype=torch.float32, device="cuda")
+    ops.encode_gate_up_silu_i8(wgd, sgd, wud, sud, xn, h)
+    x_out = torch.empty((rows, H), dtype=torch.float32, device="cuda")
+    h2 = torch.empty_like(h)
+    ops.encode_decode_gate_up(dev(xp), dev(y), x_out, dev(nw), 1e-5, wgd, sgd, wud, sud, h2)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(x_out.cpu().numpy(), x_sep.cpu().numpy())
+    assert rel_err(h2.cpu().numpy(), h.cpu().numpy()) <= 1e-5
+
+
+def test_decode_fused_rejects_aliasing_and_unsupported(ops):
+    from cellm_amd._lib import CellmHipError
+
+    H = 960
+    x = torch.zeros((1, H), dtype=torch.float32, device="cuda")
+    nw = torch.ones(H, dtype=torch.float32, device="cuda")
+    w = torch.zeros((64, H), dtype=torch.int8, device="cuda")
+    s = torch.ones(64, dtype=torch.float16, device="cuda")
+    h = torch.zeros((1, 64), dtype=torch.float32, device="cuda")
+    with pytest.raises(CellmHipError, match="alias"):
+        ops.encode_decode_gate_up(x, None, x, nw, 1e-5, w, s, w, s, h)
+    xb = torch.zeros((1, 5000), dtype=torch.float32, device="cuda")
+    with pytest.raises(CellmHipError, match="4096"):
+        ops.encode_decode_gate_up(xb, None, xb.clone(), torch.ones(5000, dtype=torch.float32, device="cuda"), 1e-5,
+                                  torch.zeros((64, 5000), dtype=torch.int8, device="cuda"), s,
+                                  torch.zeros((64, 5000), dtype=torch.int8, device="cuda"), s, h)

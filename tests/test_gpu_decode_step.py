@@ -324,3 +324,70 @@ def test_device_step_graph_replays_match_eager_launches():
         assert np.any(hk2[allowed] != hk[allowed])
     finally:
         lib.cellm_llama_dev_destroy(h)
+
+
+def test_device_step_unfused_path_matches_cpu_reference():
+    """hidden 4160 is past the fused decode kernels' 4096 limit, so the runner
+    takes its separate-launch sequence (RMSNorm, QKV, RoPE + K/V write,
+    attention, o_proj, add + RMSNorm, gate/up, down): greedy ids of 2
+    sessions equal the CPU reference's, logits within 1e-3."""
+    from cellm_amd.llama_step import LlamaDevice, LlamaShape
+
+    Lx, H, nh, nkv, hd, inter, vocab, tpb, ctx, rows = 1, 4160, 65, 13, 64, 512, 2000, 16, 64, 2
+    kvd = nkv * hd
+    dims = [(H, H), (kvd, H), (kvd, H), (H, H), (inter, H), (inter, H), (H, inter)]
+    ws, ss = [], []
+    for j, (o, i) in enumerate(dims):
+        ws.append(oracle.gen_i8((o, i), 0xC6000000 + 4 * j))
+        ss.append((oracle.gen_uniform((o,), 0xC6000001 + 4 * j, 0.5, 1.5) / (73.3 * np.sqrt(i))).astype(np.float16))
+    n1 = (1.0 + 0.1 * oracle.lcg_fill(H, 0xC6100000, 1.0)).astype(np.float16)
+    n2 = (1.0 + 0.1 * oracle.lcg_fill(H, 0xC6200000, 1.0)).astype(np.float16)
+    embed = oracle.gen_i8((vocab, H), 0xC6300000)
+    escale = (oracle.gen_uniform((vocab,), 0xC6300001, 0.5, 1.5) / 127.0).astype(np.float16)
+    fnorm = (1.0 + 0.1 * oracle.lcg_fill(H, 0xC6300002, 1.0)).astype(np.float16)
+    total = rows * ctx // tpb
+    shape = LlamaShape(Lx, H, nh, nkv, hd, inter, vocab, EPS, THETA, tpb, total)
+    n = total * Lx * tpb * kvd
+    k0 = oracle.gen_normal((n,), 0xC6400000, 0.0, 1.0).astype(np.float16).view(np.uint16)
+    v0 = oracle.gen_normal((n,), 0xC6400001, 0.0, 1.0).astype(np.float16).view(np.uint16)
+    bts = np.array([[b * rows + s for b in range(ctx // tpb)] for s in range(rows)], np.uint32)
+    tokens = np.array([17, 1234], np.uint32)
+    pos = np.array([ctx - 1, 20], np.int32)
+    dev = LlamaDevice(shape, [(ws, [s.view(np.uint16) for s in ss], n1.view(np.uint16), n2.view(np.uint16))],
+                      embed, escale.view(np.uint16), fnorm.view(np.uint16), 0, max_rows=rows, max_blocks=ctx // tpb)
+    try:
+        dev.kv_upload(k0, v0)
+        ids, _, logits = dev.step(tokens, pos, bts, want_logits=True)
+    finally:
+        dev.close()
+
+    def base(bt, t):
+        return int(bt[t // tpb]) * (Lx * tpb * kvd) + (t % tpb) * kvd
+
+    for r in range(rows):
+        kc, vc = k0.copy(), v0.copy()
+        t = int(tokens[r]) % vocab
+        x = (embed[t].astype(np.float32) * np.float32(escale[t])).astype(np.float32)
+        xn = oracle.rms_norm(x, n1.astype(np.float32), EPS)
+        q = oracle.matmul_i8_f32(ws[0], ss[0].view(np.uint16), xn)
+        k = oracle.matmul_i8_f32(ws[1], ss[1].view(np.uint16), xn)
+        v = oracle.matmul_i8_f32(ws[2], ss[2].view(np.uint16), xn)
+        oracle.rope_half_(q, nh, hd, int(pos[r]), THETA)
+        oracle.rope_half_(k, nkv, hd, int(pos[r]), THETA)
+        wb = base(bts[r], int(pos[r]))
+        kc[wb:wb + kvd] = k.astype(np.float16).view(np.uint16)
+        vc[wb:wb + kvd] = v.astype(np.float16).view(np.uint16)
+        bases = np.array([base(bts[r], tp) for tp in range(int(pos[r]) + 1)], np.uint64)
+        attn = oracle.attention_gqa_f16kv(kc, vc, bases, q, nh, nkv, hd)
+        x = x + oracle.matmul_i8_f32(ws[3], ss[3].view(np.uint16), attn)
+        xn = oracle.rms_norm(x, n2.astype(np.float32), EPS)
+        g = oracle.matmul_i8_f32(ws[4], ss[4].view(np.uint16), xn)
+        u = oracle.matmul_i8_f32(ws[5], ss[5].view(np.uint16), xn)
+        oracle.silu_mul_(g, u)
+        x = x + oracle.matmul_i8_f32(ws[6], ss[6].view(np.uint16), g)
+        xf = oracle.rms_norm(x, fnorm.astype(np.float32), EPS)
+        ref = oracle.llama_lm_head_i8(xf, embed, escale.view(np.uint16))
+        rel = float(np.max(np.abs(logits[r] - ref)) / np.max(np.abs(ref)))
+        print(f"session {r}: device {ids[r]} ref {oracle.argmax_first(ref)} logits rel err {rel:.2e}")
+        assert ids[r] == oracle.argmax_first(ref)
+        assert rel <= 1e-3
