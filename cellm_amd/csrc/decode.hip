@@ -455,8 +455,9 @@ __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(const float*
 // Every block stages the whole normalised row(s) in LDS (each needs all of
 // xn); block 0 also writes x_prev + y to x_out, the next residual stream, a
 // different buffer from x_prev so that no block reads a row another has
-// already overwritten.  The add, sum of squares, reduction tree and scaling
-// are those of add_rms_norm_kernel, so xn has the same bits.  A team of LPR
+// already overwritten.  The add and the scaling are those of
+// add_rms_norm_kernel; the sum of squares is a tree of another shape (each
+// thread sums 4 neighbouring elements first).  A team of LPR
 // lanes computes two output rows; each lane owns C 16-byte chunks of both,
 // loaded before the prologue so that their memory latency overlaps it.  x is
 // stored with 4 floats of padding after every 16 (lanes read it at a stride of
@@ -465,32 +466,37 @@ __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(const float*
 __host__ __device__ __forceinline__ int xpad(int k) { return k + (k >> 4) * 4; }
 
 // x rows [rows][H] -> LDS xs[MT][xpad(H)] = rms_norm(x_prev + y) * w; block 0
-// writes x_prev + y to x_out (y may be null: x_prev as is).  KR * kNormThreads >= H.
+// writes x_prev + y to x_out (HASY false: x_prev as is).  Thread t handles the
+// float4 groups t, t + 256, ... (KR of them: KR * 1024 >= H); its sum of
+// squares runs over its groups in order, then the same wave and block tree as
+// add_rms_norm_kernel.
 template <int MT, int KR, bool HASY>
 __device__ __forceinline__ void stage_add_norm(const float* __restrict__ x_prev, const float* __restrict__ y,
                                                float* __restrict__ x_out, const float* __restrict__ w, int rows,
                                                int H, float eps, float* xs, float (*red)[MT])
 {
     const int t = threadIdx.x;
-    const int xst = xpad(H);
+    const int xst = xpad(H), H4 = H >> 2;
     // every load first (addresses clamped in range, no branch between them), then the adds
-    float v[MT][KR], yv[MT][KR], wv[KR];
+    f4_t v[MT][KR], yv[MT][KR], wv[KR];
 #pragma unroll
     for (int u = 0; u < KR; ++u) {
-        const int i = min(t + u * kNormThreads, H - 1);
-        wv[u] = w[i];
+        const int g = min(t + u * kNormThreads, H4 - 1);
+        wv[u] = reinterpret_cast<const f4_t*>(w)[g];
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
             const int mm = min(m, rows - 1);
-            v[m][u] = x_prev[(size_t)mm * H + i];
-            if constexpr (HASY) yv[m][u] = y[(size_t)mm * H + i];
+            v[m][u] = reinterpret_cast<const f4_t*>(x_prev + (size_t)mm * H)[g];
+            if constexpr (HASY) yv[m][u] = reinterpret_cast<const f4_t*>(y + (size_t)mm * H)[g];
         }
     }
     if constexpr (HASY) {
 #pragma unroll
         for (int m = 0; m < MT; ++m)
 #pragma unroll
-            for (int u = 0; u < KR; ++u) v[m][u] = v[m][u] + yv[m][u];
+            for (int u = 0; u < KR; ++u)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[m][u][e] = v[m][u][e] + yv[m][u][e];
     }
     float s[MT];
 #pragma unroll
@@ -498,10 +504,11 @@ __device__ __forceinline__ void stage_add_norm(const float* __restrict__ x_prev,
         s[m] = 0.0f;
 #pragma unroll
         for (int u = 0; u < KR; ++u) {
-            const int i = t + u * kNormThreads;
-            if (i < H && m < rows) {
-                if (blockIdx.x == 0) x_out[(size_t)m * H + i] = v[m][u];
-                s[m] = s[m] + v[m][u] * v[m][u];
+            const int g = t + u * kNormThreads;
+            if (g < H4 && m < rows) {
+                if (blockIdx.x == 0) reinterpret_cast<f4_t*>(x_out + (size_t)m * H)[g] = v[m][u];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) s[m] = s[m] + v[m][u][e] * v[m][u][e];
             }
         }
         s[m] = group_sum<64>(s[m]);
@@ -518,8 +525,13 @@ __device__ __forceinline__ void stage_add_norm(const float* __restrict__ x_prev,
         const float inv = 1.0f / sqrtf(mean + eps);
 #pragma unroll
         for (int u = 0; u < KR; ++u) {
-            const int i = t + u * kNormThreads;
-            if (i < H) xs[m * xst + xpad(i)] = v[m][u] * inv * wv[u];
+            const int g = t + u * kNormThreads;
+            if (g < H4) {
+                f4_t o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[e] = v[m][u][e] * inv * wv[u][e];
+                *reinterpret_cast<f4_t*>(xs + m * xst + xpad(4 * g)) = o;  // 4 | 16: a group never straddles padding
+            }
         }
     }
     __syncthreads();
@@ -894,7 +906,7 @@ hipError_t launch_attention_gqa_f16kv(const float* q, const uint16_t* kcache, co
 // per lane; KR registers per thread of the staged row; MT activation rows.
 bool decode_fused_supported(int rows, int H)
 {
-    return rows >= 1 && rows <= 4 && H >= 16 && H % 16 == 0 && H <= 8 * kNormThreads;
+    return rows >= 1 && rows <= 4 && H >= 16 && H % 16 == 0 && H <= 4 * 4 * kNormThreads;
 }
 
 size_t decode_fused_lds_bytes(int rows, int H)
@@ -926,11 +938,10 @@ hipError_t launch_decode_fixed(const Args& a, int teams_total, size_t lds, hipSt
 template <int LPR, int C, int MT, bool QKV, class Args>
 hipError_t launch_decode_kr(int H, const Args& a, int teams_total, size_t lds, hipStream_t st)
 {
-    const int kr = (H + kNormThreads - 1) / kNormThreads;
+    const int kr = (H / 4 + kNormThreads - 1) / kNormThreads;  // float4 groups per thread
     if (kr <= 1) return launch_decode_fixed<LPR, C, MT, 1, QKV>(a, teams_total, lds, st);
     if (kr <= 2) return launch_decode_fixed<LPR, C, MT, 2, QKV>(a, teams_total, lds, st);
-    if (kr <= 4) return launch_decode_fixed<LPR, C, MT, 4, QKV>(a, teams_total, lds, st);
-    return launch_decode_fixed<LPR, C, MT, 8, QKV>(a, teams_total, lds, st);
+    return launch_decode_fixed<LPR, C, MT, 4, QKV>(a, teams_total, lds, st);
 }
 
 template <int LPR, int C, bool QKV, class Args>
@@ -948,8 +959,7 @@ hipError_t launch_decode(int rows, int H, const Args& a, int teams_total, hipStr
 {
     const int nchunk = H >> 4;
     if (nchunk <= 16) return launch_decode_mt<16, 1, QKV>(rows, H, a, teams_total, st);
-    if (nchunk <= 32) return launch_decode_mt<32, 1, QKV>(rows, H, a, teams_total, st);
-    if (nchunk <= 64) return launch_decode_mt<64, 1, QKV>(rows, H, a, teams_total, st);
+    if (nchunk <= 64) return launch_decode_mt<32, 2, QKV>(rows, H, a, teams_total, st);
     if (nchunk <= 128) return launch_decode_mt<64, 2, QKV>(rows, H, a, teams_total, st);
     return launch_decode_mt<64, 4, QKV>(rows, H, a, teams_total, st);
 }

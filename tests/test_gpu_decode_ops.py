@@ -351,3 +351,33 @@ def test_decode_fused_rejects_aliasing_and_unsupported(ops):
         ops.encode_decode_gate_up(xb, None, xb.clone(), torch.ones(5000, dtype=torch.float32, device="cuda"), 1e-5,
                                   torch.zeros((64, 5000), dtype=torch.int8, device="cuda"), s,
                                   torch.zeros((64, 5000), dtype=torch.int8, device="cuda"), s, h)
+
+
+def test_attention_workspace_growth():
+    """A fresh context whose attention workspace grows through 1, 2, 3 and 4
+    rows (a grow frees and reallocates, possibly at the same address) gives
+    correct results at every size, twice."""
+    from cellm_amd import HipOps
+
+    nh, nkv, hd, L, tpb, layer = 15, 5, 64, 2, 16, 1
+    kvd = nkv * hd
+    total, k, v, bt = paged_setup(L, tpb, nkv, hd, 4, 34, 0xD0000400)
+    o = HipOps(0)
+    try:
+        for rep in range(2):
+            for rows in (1, 2, 3, 4):
+                pos = np.array([543, 0, 64, 300][:rows][::-1], np.int32)
+                q = np.stack([oracle.gen_normal((nh * hd,), 0xD0000410 + r, 0.0, 1.0) for r in range(rows)])
+                q = q.astype(np.float32)
+                out = torch.empty((rows, nh * hd), dtype=torch.float32, device="cuda")
+                o.encode_attention(dev(q), dev(k), dev(v), dev(np.ascontiguousarray(bt[:rows])), dev(pos), out, nh,
+                                   nkv, hd, total, L, tpb, layer)
+                torch.cuda.synchronize()
+                got = out.cpu().numpy()
+                for r in range(rows):
+                    bases = np.array([base_of(bt[r], t, layer, L, tpb, kvd) for t in range(int(pos[r]) + 1)],
+                                     np.uint64)
+                    ref = oracle.attention_gqa_f16kv(k, v, bases, q[r], nh, nkv, hd)
+                    assert rel_err(got[r], ref) <= 1e-5, (rep, rows, r)
+    finally:
+        o.close()
