@@ -208,6 +208,158 @@ __global__ __launch_bounds__(kBlock) void lowbit_gemv_kernel(const uint8_t* __re
     }
 }
 
+// f16 x, i2 / q1 weights: the pair-packed form.  x is staged in LDS as half
+// pairs in the order the weight bits meet them, with a per-unit correction,
+// and each pair of weights becomes a half pair for v_dot2_f32_f16 (products
+// of halves are exact in the f32 accumulate):
+//   i2: word W of a unit holds codes 16w..16w+15; v_and_or(W >> 2j, 0x00030003,
+//       0x64006400) = (1024 + q_j, 1024 + q_{j+8}).  Since the centroid is
+//       q - 1.5, the unit's dot starts at -1025.5 * sum(x of the unit).
+//   q1: word W = sign bits of elements 32w..32w+31;
+//       ((~W << (15 - k)) & 0x80008000) | 0x3C003C00 = (+-1, +-1) for
+//       elements k and k + 16 (sign set when the bit is clear); the block's
+//       dot starts at 0 and is scaled by d.
+// About 1.5 instructions per element instead of 4-6; the products are
+// exact, the sums are f32 trees, and the i2 row scale is applied to the row
+// sum in both scale modes (the modes differ only in rounding).
+template <int FMT>
+struct PairFmt;
+template <>
+struct PairFmt<LB_I2> {
+    static constexpr int kPairs = 32;             // half pairs per unit (64 elements)
+    static constexpr int kStride = 36;            // dwords per unit in LDS: 32 pairs + corr + pad (36 % 32 = 4)
+    __device__ __forceinline__ static int pair_of(int e) { return (e >> 4) * 8 + (e & 7); }   // element -> pair
+    __device__ __forceinline__ static int half_of(int e) { return (e >> 3) & 1; }              // low / high half
+    static constexpr float kCorr = 1025.5f;
+};
+template <>
+struct PairFmt<LB_Q1> {
+    static constexpr int kPairs = 64;             // 128 elements
+    static constexpr int kStride = 68;
+    __device__ __forceinline__ static int pair_of(int e) { return (e >> 5) * 16 + (e & 15); }
+    __device__ __forceinline__ static int half_of(int e) { return (e >> 4) & 1; }
+    static constexpr float kCorr = 0.0f;
+};
+
+__device__ __forceinline__ float dot2h(uint32_t a, uint32_t b, float c)
+{
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, a), __builtin_bit_cast(h2_t, b), c, false);
+}
+
+template <int FMT, int LPR, int MT>
+__global__ __launch_bounds__(kBlock) void lowbit_pair_kernel(const uint8_t* __restrict__ w,
+                                                             const uint16_t* __restrict__ S,
+                                                             const _Float16* __restrict__ x, float* __restrict__ y,
+                                                             int M, int N, int K, size_t row_bytes, int rows_per_team)
+{
+    using P = PairFmt<FMT>;
+    constexpr int UE = LowbitFmt<FMT>::kElems;
+    constexpr int kTeams = kBlock / LPR;
+    extern __shared__ __align__(16) uint32_t xl[];  // [MT][units][kStride]: pairs, then the correction
+    const int units = K / UE;
+    const int xstride = units * P::kStride;
+    const int team = threadIdx.x / LPR, lane = threadIdx.x % LPR;
+    // the block's rows: base + team + r * kTeams for r < rows_per_team (staging x once for all of them)
+    const int base = blockIdx.x * kTeams * rows_per_team;
+    using unit_t = typename LowbitFmt<FMT>::unit_t;
+    unit_t pre[2];
+    {
+        const uint8_t* row0 = w + (size_t)min(base + team, N - 1) * row_bytes;
+#pragma unroll
+        for (int p = 0; p < 2; ++p) pre[p] = LowbitFmt<FMT>::load(row0, min(lane + p * LPR, units - 1));
+    }
+
+    for (int m0 = 0; m0 < M; m0 += MT) {
+        const int mt = min(MT, M - m0);
+        // pairs: thread -> one half of one pair
+        uint16_t* xh = reinterpret_cast<uint16_t*>(xl);
+        for (int i = threadIdx.x; i < mt * K; i += kBlock) {
+            const int m = i / K, k = i - m * K, u = k / UE, e = k - u * UE;
+            xh[2 * (m * xstride + u * P::kStride + P::pair_of(e)) + P::half_of(e)] =
+                __builtin_bit_cast(uint16_t, x[(size_t)(m0 + m) * K + k]);
+        }
+        __syncthreads();
+        // the correction: -kCorr * sum of the unit's x (f32), from the staged pairs
+        if constexpr (FMT == LB_I2) {
+            for (int j = threadIdx.x; j < mt * units; j += kBlock) {
+                const int m = j / units, u = j - m * units;
+                const uint32_t* xu = xl + m * xstride + u * P::kStride;
+                float sum = 0.0f;
+#pragma unroll 8
+                for (int q = 0; q < P::kPairs; ++q) {
+                    const h2_t h = __builtin_bit_cast(h2_t, xu[q]);
+                    sum += (float)h[0] + (float)h[1];
+                }
+                reinterpret_cast<float*>(xl)[m * xstride + u * P::kStride + P::kPairs] = -P::kCorr * sum;
+            }
+            __syncthreads();
+        }
+        for (int r = 0; r < rows_per_team; ++r) {
+        const int n = base + team + r * kTeams;
+        if (n >= N) break;  // the same for the whole team
+        const uint8_t* row = w + (size_t)n * row_bytes;
+        float scale = 1.0f;
+        if constexpr (FMT == LB_I2) scale = h2f(S[n]);
+        float acc[MT];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
+        {
+            int p = 0;
+            for (int u = lane; u < units; u += LPR, ++p) {
+                const unit_t raw = (m0 == 0 && r == 0 && p < 2) ? (p == 0 ? pre[0] : pre[1])
+                                                                : LowbitFmt<FMT>::load(row, u);
+#pragma unroll
+                for (int m = 0; m < MT; ++m) {
+                    if (m >= mt) break;
+                    const uint32_t* xu = xl + m * xstride + u * P::kStride;
+                    if constexpr (FMT == LB_I2) {
+                        float d = reinterpret_cast<const float*>(xu)[P::kPairs];
+#pragma unroll
+                        for (int wd = 0; wd < 4; ++wd) {
+                            const u4_t xa = *reinterpret_cast<const u4_t*>(xu + wd * 8);
+                            const u4_t xb = *reinterpret_cast<const u4_t*>(xu + wd * 8 + 4);
+                            const uint32_t W = raw[wd];
+#pragma unroll
+                            for (int j = 0; j < 8; ++j) {
+                                const uint32_t h = ((W >> (2 * j)) & 0x00030003u) | 0x64006400u;
+                                d = dot2h(h, j < 4 ? xa[j] : xb[j - 4], d);
+                            }
+                        }
+                        acc[m] += d;
+                    } else {
+                        const float dscale = h2f(raw.h[0]);
+                        float d = 0.0f;
+#pragma unroll
+                        for (int wd = 0; wd < 4; ++wd) {
+                            const uint32_t Wn = ~((uint32_t)raw.h[1 + 2 * wd] | ((uint32_t)raw.h[2 + 2 * wd] << 16));
+#pragma unroll
+                            for (int q = 0; q < 4; ++q) {
+                                const u4_t xq = *reinterpret_cast<const u4_t*>(xu + wd * 16 + q * 4);
+#pragma unroll
+                                for (int j = 0; j < 4; ++j) {
+                                    const int k = q * 4 + j;
+                                    const uint32_t h = ((Wn << (15 - k)) & 0x80008000u) | 0x3C003C00u;
+                                    d = dot2h(h, xq[j], d);
+                                }
+                            }
+                        }
+                        acc[m] = __builtin_fmaf(dscale, d, acc[m]);
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[m] = group_sum<LPR>(acc[m]);
+        if (lane == 0) {
+#pragma unroll
+            for (int m = 0; m < MT; ++m)
+                if (m < mt) y[(size_t)(m0 + m) * N + n] = FMT == LB_I2 ? acc[m] * scale : acc[m];
+        }
+        }
+        __syncthreads();
+    }
+}
+
 // Any shape: one wave per output row, x read from memory, elements strided
 // over the lanes.
 template <int FMT, int XT>
@@ -275,11 +427,55 @@ hipError_t launch_fast_lpr(int lpr, const uint8_t* w, const uint16_t* S, int mod
     }
 }
 
+template <int FMT, int LPR, int MT>
+hipError_t launch_pair(const uint8_t* w, const uint16_t* S, const void* x, float* y, int M, int N, int K,
+                       size_t row_bytes, size_t lds, hipStream_t st)
+{
+    // rows per team: as many as keep about 1024 blocks (the x staging of a block is shared by all its rows)
+    constexpr int kTeams = kBlock / LPR;
+    const int rpt = std::max(1, std::min(16, N / (kTeams * 1024)));
+    const dim3 grid((N + kTeams * rpt - 1) / (kTeams * rpt));
+    hipLaunchKernelGGL((lowbit_pair_kernel<FMT, LPR, MT>), grid, dim3(kBlock), lds, st, w, S,
+                       reinterpret_cast<const _Float16*>(x), y, M, N, K, row_bytes, rpt);
+    return hipGetLastError();
+}
+
+template <int FMT, int MT>
+hipError_t launch_pair_lpr(int lpr, const uint8_t* w, const uint16_t* S, const void* x, float* y, int M, int N, int K,
+                           size_t row_bytes, size_t lds, hipStream_t st)
+{
+    switch (lpr) {
+    case 4: return launch_pair<FMT, 4, MT>(w, S, x, y, M, N, K, row_bytes, lds, st);
+    case 8: return launch_pair<FMT, 8, MT>(w, S, x, y, M, N, K, row_bytes, lds, st);
+    case 16: return launch_pair<FMT, 16, MT>(w, S, x, y, M, N, K, row_bytes, lds, st);
+    case 32: return launch_pair<FMT, 32, MT>(w, S, x, y, M, N, K, row_bytes, lds, st);
+    default: return launch_pair<FMT, 64, MT>(w, S, x, y, M, N, K, row_bytes, lds, st);
+    }
+}
+
 template <int FMT>
 hipError_t launch_fmt(const uint8_t* w, const uint16_t* S, int mode, const void* x, int xdt, float* y, int M, int N,
                       int K, size_t row_bytes, hipStream_t st)
 {
     constexpr int UE = LowbitFmt<FMT>::kElems;
+    if constexpr (FMT != LB_F16) {
+        // f16 x: the pair-packed dot2 kernel (the i2 scale is applied to the row sum in both modes)
+        const bool unit_ok = K > 0 && K % UE == 0 &&
+                             (reinterpret_cast<uintptr_t>(w) & (FMT == LB_Q1 ? 1u : 15u)) == 0;
+        const size_t per_row = (size_t)(K / UE) * PairFmt<FMT>::kStride * 4;
+        if (xdt == DT_F16 && unit_ok && per_row <= 64 * 1024) {
+            // q1 keeps its 64 sign pairs of a block live across the rows: at most 2 rows per pass
+            int MT = M >= 4 && FMT == LB_I2 ? 4 : (M >= 2 ? 2 : 1);
+            while (MT > 1 && MT * per_row > 64 * 1024) MT >>= 1;
+            int lpr = 4;
+            while (lpr < 64 && lpr < K / UE) lpr <<= 1;
+            const size_t lds = (size_t)MT * per_row;
+            if constexpr (FMT == LB_I2)
+                if (MT == 4) return launch_pair_lpr<FMT, 4>(lpr, w, S, x, y, M, N, K, row_bytes, lds, st);
+            if (MT == 2) return launch_pair_lpr<FMT, 2>(lpr, w, S, x, y, M, N, K, row_bytes, lds, st);
+            return launch_pair_lpr<FMT, 1>(lpr, w, S, x, y, M, N, K, row_bytes, lds, st);
+        }
+    }
     const bool unit_ok =
         K % UE == 0 && (reinterpret_cast<uintptr_t>(w) & (FMT == LB_Q1 ? 1u : 15u)) == 0;
     const size_t per_row = (size_t)(K / UE) * (UE + kPad) * sizeof(float);

@@ -114,7 +114,8 @@ def test_f16_gemv_exact_integers(ops, k, n, m):
 
 
 I2_CASES = [(1152, 1536, 1, np.float32), (2048, 1000, 4, np.float16), (6912, 256, 2, np.float32),
-            (1023, 77, 3, np.float32), (20000, 40, 1, np.float32)]
+            (1023, 77, 3, np.float32), (20000, 40, 1, np.float32), (1152, 6912, 1, np.float16),
+            (1152, 700, 3, np.float16)]
 
 
 @pytest.mark.parametrize("mode", [0, 1])
@@ -129,13 +130,16 @@ def test_i2_gemv_random(ops, k, n, m, xdt, mode):
     within_bound(y.cpu().numpy(), ref, absprod, k + 1)
 
 
+@pytest.mark.parametrize("xdt", [np.float32, np.float16])
 @pytest.mark.parametrize("mode", [0, 1])
-def test_i2_gemv_exact_integers(ops, mode):
+def test_i2_gemv_exact_integers(ops, mode, xdt):
+    """f16 x takes the pair-packed dot2 kernel: (1024 + q) * x and the
+    -1025.5 * sum(x) correction stay exact integers (or halves) here."""
     k, n, m = 1024, 500, 4
     rng = np.random.default_rng(0x12E)
     w = rng.integers(0, 256, (n, k // 4)).astype(np.uint8)
     s = np.full(n, 0.5, np.float16)
-    x = rng.integers(-4, 5, (m, k)).astype(np.float32)
+    x = rng.integers(-4, 5, (m, k)).astype(xdt)
     y = out(m, n)
     ops.encode_qgemv_i2(dev(w), dev(s.view(np.uint16)), mode, dev(x), y, k)
     torch.cuda.synchronize()
@@ -143,7 +147,8 @@ def test_i2_gemv_exact_integers(ops, mode):
 
 
 Q1_CASES = [(1152, 1536, 1, np.float32), (2048, 1000, 4, np.float16), (4096, 300, 2, np.float32),
-            (128, 9, 3, np.float32), (20480, 40, 1, np.float32)]
+            (128, 9, 3, np.float32), (20480, 40, 1, np.float32), (1152, 6912, 1, np.float16),
+            (1152, 700, 3, np.float16)]
 
 
 @pytest.mark.parametrize("k,n,m,xdt", Q1_CASES)
@@ -157,15 +162,17 @@ def test_q1_gemv_random(ops, k, n, m, xdt):
     within_bound(y.cpu().numpy(), ref, absprod, k)
 
 
-def test_q1_gemv_exact_integers_odd_row_offset(ops):
+@pytest.mark.parametrize("xdt", [np.float32, np.float16])
+def test_q1_gemv_exact_integers_odd_row_offset(ops, xdt):
     """d = 0.25 everywhere, integer x: exact; the tensor starts 2 bytes into
-    an allocation, so the 18-byte blocks sit on 2-byte boundaries only."""
+    an allocation, so the 18-byte blocks sit on 2-byte boundaries only.  f16 x
+    takes the pair-packed dot2 kernel."""
     k, n, m = 1024, 333, 4
     rng = np.random.default_rng(0x1AE)
     w = rng.integers(0, 256, (n, k // 128 * 18)).astype(np.uint8)
     d = np.full((n, k // 128), 0.25, np.float16)
     w.reshape(n, k // 128, 18)[:, :, :2] = d.view(np.uint8).reshape(n, k // 128, 2)
-    x = rng.integers(-4, 5, (m, k)).astype(np.float32)
+    x = rng.integers(-4, 5, (m, k)).astype(xdt)
     buf = torch.zeros(w.size + 16, dtype=torch.uint8, device="cuda")
     buf[2:2 + w.size] = torch.from_numpy(w.reshape(-1)).cuda()
     y = out(m, n)
