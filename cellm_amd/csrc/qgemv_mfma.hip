@@ -85,7 +85,11 @@ __device__ __forceinline__ h8_t q4_to_f16(uint32_t w, h2_t s2, h2_t s16, h2_t b2
 // tiles of X (ceil(M/16)); NT = 16-row tiles of W per wave; DEPTH = pairs of
 // K blocks a wave loads per group; SBT = scale (and q4 bias) dtype; CHUNKED: X
 // does not fit LDS whole and is staged per K chunk of KC columns (KC a
-// multiple of a group's columns).
+// multiple of a group's columns); BT = threads per block.  BT = 1024 is the
+// one-block-per-CU form of the int8 kernel for an X of 80-152 KB (M = 49..64):
+// the whole X stays in LDS (up to 160 KB per CU on gfx950) and 16 waves stream
+// W, instead of restaging X chunks for every tile.  (The q4 form needs more
+// than the 128 registers per lane a 1024-thread block leaves.)
 //
 // A block owns tiles of ROWS = 4*NT*16 weight rows: tile, tile+grid, ...  Each
 // wave walks its rows in groups of DEPTH block pairs (128 B of every row per
@@ -94,8 +98,8 @@ __device__ __forceinline__ h8_t q4_to_f16(uint32_t w, h2_t s2, h2_t s16, h2_t b2
 // CU (8-16 per CU), so no cross-iteration register ring is needed -- the
 // compiler counts outstanding loads exactly only through straight-line code,
 // and a ring that crosses tile boundaries would wait on every load anyway.
-template <int WT, int MS, int NT, int DEPTH, int SBT, bool CHUNKED>
-__global__ __launch_bounds__(kBlock) void qgemv_mfma_kernel(
+template <int WT, int MS, int NT, int DEPTH, int SBT, bool CHUNKED, int BT = kBlock>
+__global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
     const void* __restrict__ W, const void* __restrict__ S, const void* __restrict__ Bz, int per_channel, int gshift,
     const _Float16* __restrict__ X, const float* __restrict__ bias, float* __restrict__ Y, int M, int N, int K, int KC,
     int ntiles)
@@ -103,7 +107,7 @@ __global__ __launch_bounds__(kBlock) void qgemv_mfma_kernel(
     extern __shared__ __align__(16) _Float16 xs[];  // [MS*16][KC + 8]
     constexpr int KB = WT == 1 ? 64 : 128;  // K per block: 64 bytes of every row
     constexpr int TSTEPS = KB / 32;         // MFMA k-steps per block
-    constexpr int ROWS = (kBlock / 64) * NT * 16;
+    constexpr int ROWS = (BT / 64) * NT * 16;
     const int stride = KC + 8;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int rl = lane & 15, g = lane >> 4;
@@ -117,17 +121,17 @@ __global__ __launch_bounds__(kBlock) void qgemv_mfma_kernel(
     // Loads are unconditional (clamped) so they issue back to back.
     auto stage = [&](int k0, int kcl) {
         const int words = kcl >> 3, total = MS * 16 * words;
-        for (int base = threadIdx.x; base < total; base += 4 * kBlock) {
+        for (int base = threadIdx.x; base < total; base += 4 * BT) {
             u4_t r[4];
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                const int idx = min(base + u * kBlock, total - 1);
+                const int idx = min(base + u * BT, total - 1);
                 const int m = idx / words, wd = idx - m * words;
                 r[u] = *reinterpret_cast<const u4_t*>(X + (size_t)min(m, M - 1) * K + k0 + wd * 8);
             }
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                const int idx = base + u * kBlock;
+                const int idx = base + u * BT;
                 const int m = idx / words, wd = idx - m * words;
                 const u4_t v = m < M ? r[u] : u4_t{0u, 0u, 0u, 0u};
                 if (idx < total)
@@ -331,11 +335,52 @@ int resident_blocks(Kern kern, size_t lds)
     return per_cu * cus;
 }
 
+// Raises the dynamic LDS limit of one kernel, once per device.
+template <typename Kern>
+hipError_t allow_big_lds(Kern kern, int bytes)
+{
+    static std::mutex mu;
+    static std::vector<std::pair<int, int>> done;  // (device, bytes)
+    int dev = 0;
+    if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
+    std::lock_guard<std::mutex> lk(mu);
+    for (const auto& d : done)
+        if (d.first == dev && d.second >= bytes) return hipSuccess;
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       bytes);
+    if (e == hipSuccess) done.emplace_back(dev, bytes);
+    return e;
+}
+
+constexpr size_t kWholeXLds = 152 * 1024;  // the BT = 1024 form holds X up to this size
+
 template <int WT, int MS, int NT, int SBT>
 hipError_t launch_mfma_nt(const void* W, const void* S, const void* B, int per_channel, int gshift, const _Float16* X,
                           const float* bias, float* Y, int M, int N, int K, hipStream_t st)
 {
     constexpr int KB = WT == 1 ? 64 : 128;
+    if constexpr (WT == 1 && MS == 4 && NT == 1) {
+        // X too big for two blocks per CU but within one CU's LDS: one 1024-thread block per CU keeps it
+        // whole; 16 waves of one W tile each (two tiles per wave need more than the 128 registers per
+        // lane a 1024-thread block leaves, and 8 waves of two tiles stream 12 % slower: measured)
+        const size_t whole = (size_t)MS * 16 * (K + 8) * 2;
+        if (whole > 80 * 1024 && whole <= kWholeXLds) {
+            constexpr int BT = 1024, DEPTH = 2, ROWS = (BT / 64) * NT * 16;
+            auto kern = qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, false, BT>;
+            if (hipError_t e = allow_big_lds(kern, (int)kWholeXLds); e != hipSuccess) return e;
+            const int ntiles = (N + ROWS - 1) / ROWS;
+            int per_cu = 0, cus = 0, dev = 0;
+            (void)hipGetDevice(&dev);
+            if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+                cus = 1;
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, BT, whole) != hipSuccess || per_cu < 1)
+                per_cu = 1;
+            const int grid = std::min(ntiles, per_cu * cus);
+            hipLaunchKernelGGL(kern, dim3(grid), dim3(BT), whole, st, W, S, B, per_channel, gshift, X, bias, Y, M, N, K,
+                               K, ntiles);
+            return hipGetLastError();
+        }
+    }
     constexpr int DEPTH = 4 / NT;  // block pairs per group: 8 KB of weights per wave
     constexpr int ROWS = (kBlock / 64) * NT * 16;
     // X in LDS: at most 80 KB per block so two blocks share a CU; the whole K
@@ -362,8 +407,11 @@ template <int WT, int MS, int SBT>
 hipError_t launch_mfma_ms(const void* W, const void* S, const void* B, int per_channel, int gshift, const _Float16* X,
                           const float* bias, float* Y, int M, int N, int K, hipStream_t st)
 {
-    // two 16-row W tiles per wave when there are rows enough to fill the chip
-    if (N >= 128 * 512)
+    // two 16-row W tiles per wave when there are rows enough to fill the chip, unless X needs the
+    // one-block-per-CU form (one tile per wave there)
+    const size_t whole = (size_t)MS * 16 * (K + 8) * 2;
+    const bool whole_x = WT == 1 && MS == 4 && whole > 80 * 1024 && whole <= kWholeXLds;
+    if (N >= 128 * 512 && !whole_x)
         return launch_mfma_nt<WT, MS, 2, SBT>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, st);
     return launch_mfma_nt<WT, MS, 1, SBT>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, st);
 }

@@ -224,6 +224,17 @@ def test_i8_batched_gemma_lm_head_slice(ops, m):
     assert rel_err(y, ref) <= TOL_F32  # int8 is exact in f16: f32-accumulation bar
 
 
+@pytest.mark.parametrize("m,k,n", [(64, 1152, 1000), (49, 1024, 4099), (64, 704, 300), (64, 1216, 2000),
+                                   (57, 1152, 262)])
+def test_i8_batched_whole_x_in_lds(ops, m, k, n):
+    """49..64 rows whose X is 80-152 KB run one 1024-thread block per CU with
+    the whole X in LDS (ragged tile counts, a CU count above the tile count);
+    K = 1216 is past 152 KB and takes the chunked form."""
+    w, s, x = make_i8(n, k, m, cfg=3, x_dtype=np.float16, salt=m + k)
+    y = _run_i8(ops, w, s, x)
+    assert rel_err(y, oracle.qgemv_i8(w, s, x)) <= TOL_F32
+
+
 @pytest.mark.parametrize("m", [16, 64])
 def test_q4_batched_gemma_mlp(ops, m):
     k, n = 1152, 13824
