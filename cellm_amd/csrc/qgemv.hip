@@ -330,7 +330,8 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_persist_kernel(
 // and bias rows, contiguous in S and B, arrive with one 16-byte load per array
 // a batch ahead and are parked in LDS.  The 8 per-step partial sums of a lane
 // are reduced across the row's 32 lanes with a halving butterfly (9 exchanges
-// per 8 rows instead of 5 per row).
+// per 8 rows instead of 5 per row).  Row sums are parked in LDS until the last
+// batch (a store inside the loop turns every weight-load wait into vmcnt(0)).
 constexpr int kRingThreads = 512;
 constexpr int kRingSteps = 8;
 
@@ -339,7 +340,8 @@ __global__ __launch_bounds__(kRingThreads) void qgemv_q4_ring_kernel(const u4_t*
                                                                     const void* __restrict__ S,
                                                                     const void* __restrict__ Bz,
                                                                     const _Float16* __restrict__ x,
-                                                                    float* __restrict__ y, int N, int K, int gshift)
+                                                                    float* __restrict__ y, int N, int K, int gshift,
+                                                                    int nbmax)
 {
     constexpr int P = kRingSteps;
     constexpr int SBB = SBT == DT_F32 ? 4 : 2;
@@ -348,8 +350,10 @@ __global__ __launch_bounds__(kRingThreads) void qgemv_q4_ring_kernel(const u4_t*
     uint32_t* xq = lds;
     float2* cx = reinterpret_cast<float2*>(lds + (size_t)CPR * 16);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    // per wave: S rows at +0, B rows at +1024 (16 rows, <= 32 bytes each), 16-byte aligned
-    unsigned char* sbw = reinterpret_cast<unsigned char*>(lds) + ((CPR * 72 + 15) & ~15) + wave * 2048;
+    // per wave: S rows at +0, B rows at +1024 (16 rows, <= 32 bytes each), 16-byte aligned; then the
+    // parked row sums (16 per batch, nbmax batches)
+    unsigned char* sbw = reinterpret_cast<unsigned char*>(lds) + ((CPR * 72 + 15) & ~15) + wave * (2048 + 64 * nbmax);
+    float* park = reinterpret_cast<float*>(sbw + 2048);
     const int h = lane >> 5, c = lane & 31;
     const int gpr = (K + (1 << gshift) - 1) >> gshift;
     const int sbrow = gpr * SBB;        // bytes of S (and of B) per row
@@ -372,10 +376,11 @@ __global__ __launch_bounds__(kRingThreads) void qgemv_q4_ring_kernel(const u4_t*
         const unsigned char* base = reinterpret_cast<const unsigned char*>(lane < sbv ? S : Bz);
         sbr = *reinterpret_cast<const u4_t*>(base + (size_t)b * 16 * sbrow + (size_t)v * 16);
     };
-    // loads first, then the x staging (its wait covers them; nothing is computed before both)
+    // loads first, then the x staging (its wait covers them; nothing is computed before both); the
+    // scale/bias load first, in the loop's order (else its wait in the loop becomes a full drain)
+    load_sb(0);
 #pragma unroll
     for (int s = 0; s < P; ++s) load_w(0, s);
-    load_sb(0);
     for (int idx = threadIdx.x; idx < (K >> 3); idx += kRingThreads) {
         const u4_t raw = *reinterpret_cast<const u4_t*>(x + idx * 8);
         stage_word_q4(raw, idx, true, xq, cx);
@@ -431,8 +436,147 @@ __global__ __launch_bounds__(kRingThreads) void qgemv_q4_ring_kernel(const u4_t*
         a1 += __shfl_xor(a1, 1, 32);
         // the lane now holds step s = 4*b16 + 2*b8 + b4 of the batch
         const int s = (b16 ? 4 : 0) + (b8 ? 2 : 0) + (b4 ? 1 : 0);
-        if ((c & 3) == 0) y[16 * (gw + GW * bi) + 2 * s + h] = a1;
+        if ((c & 3) == 0) park[16 * bi + 2 * s + h] = a1;
     }
+    __builtin_amdgcn_wave_barrier();
+    for (int i = lane; i < 16 * nb; i += 64) y[16 * (gw + GW * (i >> 4)) + (i & 15)] = park[i];
+}
+
+// Flat-batch variant for rows of 4J whole 16-byte chunks (K = 128 J, J = 4..8).
+// A 16-row batch is 16 * 4J = 64 J chunks, contiguous in memory, so a wave
+// reads it with J full-width loads (lane l of load j takes chunk 64 j + l of
+// the batch): every load covers 1 KB of whole 128-byte lines and no lane
+// idles, where the row-pair steps above leave 4 of 32 lanes idle at K = 896
+// and split lines between two loads.  The chunk -> (row, k chunk) map is the
+// same in every batch, so each lane keeps its J x chunks in registers.  The J
+// per-chunk sums of a lane go to a per-wave LDS slot (row stride 4J + 1) and
+// four lanes per row add up its 4J chunks.  D batches of loads are in flight.
+// Row sums are parked in LDS and stored after the last batch: on gfx9 stores
+// count in vmcnt with the loads, and a store inside the loop makes every wait
+// for a weight load a full drain (vmcnt(0)) of the batches in flight.
+constexpr int kFlatThreads = 512;
+#ifndef CELLM_Q4_FLAT_DEPTH
+#define CELLM_Q4_FLAT_DEPTH 1
+#endif
+constexpr int kFlatDepth = CELLM_Q4_FLAT_DEPTH;
+
+__host__ __device__ constexpr int flat_wave_bytes(int J, int nbmax) { return 1024 + 16 * (4 * J + 1) * 4 + 64 * nbmax; }
+
+template <int SBT, int J, int D>
+__global__ __launch_bounds__(kFlatThreads) void qgemv_q4_flat_kernel(const u4_t* __restrict__ wq,
+                                                                    const void* __restrict__ S,
+                                                                    const void* __restrict__ Bz,
+                                                                    const _Float16* __restrict__ x,
+                                                                    float* __restrict__ y, int N, int gshift,
+                                                                    int nbmax)
+{
+    constexpr int CPR = 4 * J, K = 32 * CPR, RS = CPR + 1;
+    constexpr int SBB = SBT == DT_F32 ? 4 : 2;
+    extern __shared__ __align__(16) uint32_t lds[];
+    uint32_t* xq = lds;
+    float2* cx = reinterpret_cast<float2*>(lds + CPR * 16);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // per wave: 16 S rows at +0, 16 B rows at +512 (<= 32 bytes each), chunk sums at +1024, then
+    // the parked row sums (16 per batch, nbmax batches)
+    unsigned char* sbw =
+        reinterpret_cast<unsigned char*>(lds) + ((CPR * 72 + 15) & ~15) + wave * flat_wave_bytes(J, nbmax);
+    float* red = reinterpret_cast<float*>(sbw + 1024);
+    float* park = red + 16 * RS;
+    const int gpr = (K + (1 << gshift) - 1) >> gshift;
+    const int sbrow = gpr * SBB;  // bytes of S (and of B) per row; 16 rows = sbrow 16-byte vectors
+    const int NB = N >> 4;
+    const int gw = blockIdx.x * (kFlatThreads / 64) + wave, GW = gridDim.x * (kFlatThreads / 64);
+    const int nb = gw < NB ? (NB - 1 - gw) / GW + 1 : 0;
+
+    u4_t wr[D][J];
+    auto load_w = [&](int bi, int slot, int j) {
+        const int b = min(gw + GW * bi, NB - 1);  // past the end: a clamped re-read, never used
+        wr[slot][j] = __builtin_nontemporal_load(wq + (size_t)b * (64 * J) + 64 * j + lane);
+    };
+    u4_t sbr;
+    auto load_sb = [&](int bi) {
+        const int b = min(gw + GW * bi, NB - 1);
+        const int v = lane < sbrow ? lane : min(lane - sbrow, sbrow - 1);
+        const unsigned char* base = reinterpret_cast<const unsigned char*>(lane < sbrow ? S : Bz);
+        sbr = *reinterpret_cast<const u4_t*>(base + (size_t)b * 16 * sbrow + (size_t)v * 16);
+    };
+    // loads first, then the x staging (its wait covers them; nothing is computed before both).  The
+    // scale/bias load goes before the weights, in the order the loop issues them: were it the newest
+    // load on the way into the loop, the compiler's wait for it would become a full vmcnt(0) drain.
+    load_sb(0);
+#pragma unroll
+    for (int d = 0; d < D; ++d)
+#pragma unroll
+        for (int j = 0; j < J; ++j) load_w(d, d, j);
+    for (int idx = threadIdx.x; idx < (K >> 3); idx += kFlatThreads) {
+        const u4_t raw = *reinterpret_cast<const u4_t*>(x + idx * 8);
+        stage_word_q4(raw, idx, true, xq, cx);
+    }
+    __syncthreads();
+    u4_t xa[J][4];
+    float2 xc[J];
+    int soff[J], roff[J];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int f = 64 * j + lane, r = f / CPR, kc = f - r * CPR;
+        const u4_t* xp = reinterpret_cast<const u4_t*>(xq + kc * 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) xa[j][i] = xp[i];
+        xc[j] = cx[kc];
+        soff[j] = r * sbrow + ((kc << 5) >> gshift) * SBB;
+        roff[j] = r * RS + kc;
+    }
+    const uint32_t m0f = 0x000F000Fu, m1f = 0x00F000F0u, magic = 0x64006400u;
+    const int rr = lane >> 2, q = lane & 3;
+    auto batch = [&](int bi, int slot) {
+        // this batch's scale/bias rows -> LDS (loaded a batch ago); next batch's load.  Lanes past the
+        // rows write the spare last 16 bytes of the S slot (free whenever such lanes exist): a store
+        // under a branch made the compiler wait for every load in flight.
+        *reinterpret_cast<u4_t*>(sbw + (lane < sbrow ? lane * 16 : (lane < 2 * sbrow ? 512 + (lane - sbrow) * 16 : 496))) =
+            sbr;
+        load_sb(bi + 1);
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const u4_t w = wr[slot][j];
+            float sc, bb;
+            if constexpr (SBT == DT_F32) {
+                sc = *reinterpret_cast<const float*>(sbw + soff[j]);
+                bb = *reinterpret_cast<const float*>(sbw + 512 + soff[j]);
+            } else {
+                sc = raw_to_f32<SBT>(*reinterpret_cast<const uint16_t*>(sbw + soff[j]));
+                bb = raw_to_f32<SBT>(*reinterpret_cast<const uint16_t*>(sbw + 512 + soff[j]));
+            }
+            float d = -xc[j].x;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                d = dot2(and_or(w[e], m0f, magic), xa[j][e][0], d);
+                d = dot2(and_or(w[e], m1f, magic), xa[j][e][1], d);
+                const uint32_t t = w[e] >> 8;
+                d = dot2(and_or(t, m0f, magic), xa[j][e][2], d);
+                d = dot2(and_or(t, m1f, magic), xa[j][e][3], d);
+            }
+            red[roff[j]] = sc * d + bb * xc[j].y;
+            load_w(bi + D, slot, j);
+        }
+        // LDS operations of a wave complete in order: the reads below see every lane's writes
+        __builtin_amdgcn_wave_barrier();
+        float s = 0.0f;
+#pragma unroll
+        for (int t = 0; t < J; ++t) s += red[rr * RS + q + 4 * t];
+        s += __shfl_xor(s, 1);
+        s += __shfl_xor(s, 2);
+        if (q == 0) park[16 * bi + rr] = s;
+        __builtin_amdgcn_wave_barrier();
+    };
+    static_assert(D == 1 || D == 2, "one or two batches in flight");
+    for (int bi = 0; bi < nb; bi += D) {
+        batch(bi, 0);
+        if constexpr (D == 2) {
+            if (bi + 1 < nb) batch(bi + 1, 1);
+        }
+    }
+    for (int i = lane; i < 16 * nb; i += 64) y[16 * (gw + GW * (i >> 4)) + (i & 15)] = park[i];
 }
 
 // ---------------------------------------------------------------------------
@@ -1064,6 +1208,23 @@ int qgemv_q4_lds_bytes(int M, int K)
     return MT * CPR * 16 * 4 + MT * CPR * 8;
 }
 
+static int persist_grid();
+
+// The flat-batch kernel parks every row sum of a wave in LDS (64 bytes per batch).
+static bool flat_lds_fits(int N, int K)
+{
+    const int GW = std::max(1, persist_grid() / 4) * (kFlatThreads / 64), nbmax = ((N >> 4) + GW - 1) / GW;
+    return (size_t)(((K >> 5) * 72 + 15) & ~15) + (size_t)(kFlatThreads / 64) * flat_wave_bytes(K >> 7, nbmax) <=
+           64 * 1024;
+}
+
+// The ring kernel parks every row sum of a wave in LDS too.
+static bool ring_lds_fits(int N, int K)
+{
+    const int GW = std::max(1, persist_grid() / 4) * (kRingThreads / 64), nbmax = ((N >> 4) + GW - 1) / GW;
+    return (size_t)(((K >> 5) * 72 + 15) & ~15) + (size_t)(kRingThreads / 64) * (2048 + 64 * nbmax) <= 64 * 1024;
+}
+
 // Persistent grid: 4 blocks per CU (measured best for the lm_head shape).
 static int persist_grid()
 {
@@ -1087,22 +1248,55 @@ hipError_t launch_qgemv_q4_affine(const uint32_t* wq, const void* S, const void*
     const bool fast = !force_generic && xdt == DT_F16 && M <= 4 && (K % 32) == 0 && group_size >= 32 &&
                       aligned16(wq) && aligned16(x) && qgemv_q4_lds_bytes(M, K) <= 64 * 1024;
     const int sbrow = ((K + group_size - 1) / group_size) * (sbt == DT_F32 ? 4 : 2);
+    if (fast && M == 1 && N >= 32768 && (N % 16) == 0 && (K % 128) == 0 && K >= 512 && K <= 1024 &&
+        sbrow <= 32 && aligned16(S) && aligned16(B) && flat_lds_fits(N, K)) {
+        // long single-row outputs, rows of 16..32 chunks in groups of 4: flat-batch kernel, one block per CU
+        const int grid = std::max(1, persist_grid() / 4);
+        const int J = K >> 7;
+        const int GW = grid * (kFlatThreads / 64), nbmax = ((N >> 4) + GW - 1) / GW;
+        const size_t lds =
+            (size_t)(((K >> 5) * 72 + 15) & ~15) + (size_t)(kFlatThreads / 64) * flat_wave_bytes(J, nbmax);
+        const u4_t* w4 = reinterpret_cast<const u4_t*>(wq);
+        const _Float16* xh = reinterpret_cast<const _Float16*>(x);
+#define CELLM_Q4_FLAT(SBT_, J_)                                                                                   \
+    hipLaunchKernelGGL((qgemv_q4_flat_kernel<SBT_, J_, kFlatDepth>), dim3(grid), dim3(kFlatThreads), lds, st, w4, S, \
+                       B, xh, y, N, gshift, nbmax)
+#define CELLM_Q4_FLAT_J(SBT_)                 \
+    switch (J) {                              \
+        case 4: CELLM_Q4_FLAT(SBT_, 4); break; \
+        case 5: CELLM_Q4_FLAT(SBT_, 5); break; \
+        case 6: CELLM_Q4_FLAT(SBT_, 6); break; \
+        case 7: CELLM_Q4_FLAT(SBT_, 7); break; \
+        default: CELLM_Q4_FLAT(SBT_, 8); break; \
+    }
+        if (sbt == DT_F16) {
+            CELLM_Q4_FLAT_J(DT_F16)
+        } else if (sbt == DT_F32) {
+            CELLM_Q4_FLAT_J(DT_F32)
+        } else {
+            CELLM_Q4_FLAT_J(DT_BF16)
+        }
+#undef CELLM_Q4_FLAT_J
+#undef CELLM_Q4_FLAT
+        return hipGetLastError();
+    }
     if (fast && M == 1 && N >= 32768 && (N % 16) == 0 && (K >> 5) <= 32 && sbrow <= 32 && aligned16(S) &&
-        aligned16(B)) {
+        aligned16(B) && ring_lds_fits(N, K)) {
         // long single-row outputs, whole 16-row batches: batched-row ring kernel, one block per CU
         const int grid = std::max(1, persist_grid() / 4);
-        const size_t lds = (size_t)(((K >> 5) * 72 + 15) & ~15) + (size_t)(kRingThreads / 64) * 2048;
+        const int GW = grid * (kRingThreads / 64), nbmax = ((N >> 4) + GW - 1) / GW;
+        const size_t lds = (size_t)(((K >> 5) * 72 + 15) & ~15) + (size_t)(kRingThreads / 64) * (2048 + 64 * nbmax);
         const u4_t* w4 = reinterpret_cast<const u4_t*>(wq);
         const _Float16* xh = reinterpret_cast<const _Float16*>(x);
         if (sbt == DT_F16)
             hipLaunchKernelGGL((qgemv_q4_ring_kernel<DT_F16>), dim3(grid), dim3(kRingThreads), lds, st, w4, S, B, xh, y,
-                               N, K, gshift);
+                               N, K, gshift, nbmax);
         else if (sbt == DT_F32)
             hipLaunchKernelGGL((qgemv_q4_ring_kernel<DT_F32>), dim3(grid), dim3(kRingThreads), lds, st, w4, S, B, xh, y,
-                               N, K, gshift);
+                               N, K, gshift, nbmax);
         else
             hipLaunchKernelGGL((qgemv_q4_ring_kernel<DT_BF16>), dim3(grid), dim3(kRingThreads), lds, st, w4, S, B, xh,
-                               y, N, K, gshift);
+                               y, N, K, gshift, nbmax);
         return hipGetLastError();
     }
     if (fast && M == 1 && N >= 32768 && (K >> 5) <= 32) {

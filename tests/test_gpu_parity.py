@@ -115,8 +115,12 @@ def test_q4_gemv_qwen_lm_head(ops):
 
 
 @pytest.mark.parametrize("k,n,group,sb", [
-    (1024, 40000, 64, "bf16"),      # batched-row ring kernel, 32 chunks per row
-    (960, 49152, 64, np.float16),   # ring kernel, 30 of 32 lanes per row (SmolLM2-360M lm_head shape)
+    (1024, 40000, 64, "bf16"),      # flat-batch kernel, 8 loads per 16-row batch
+    (512, 32768, 64, np.float32),   # flat, 4 loads per batch, f32 scale rows of 32 bytes
+    (640, 40000, 64, np.float16),   # flat, 5 loads per batch
+    (768, 65536, 128, "bf16"),      # flat, 6 loads per batch, group 128
+    (512, 1048576, 32, np.float16), # flat, group 32, 32 batches parked per wave
+    (960, 49152, 64, np.float16),   # batched-row ring kernel, 30 of 32 lanes per row (SmolLM2-360M lm_head shape)
     (256, 32768, 32, np.float16),   # ring kernel, 8 chunks per row
     (512, 33001, 128, np.float32),  # N % 16 != 0: persistent kernel, ragged last tile
     (896, 65536, 64, np.float32),   # f32 scale rows of 56 bytes: persistent kernel
