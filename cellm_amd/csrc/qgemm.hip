@@ -7,10 +7,12 @@
 // oracle is cpu_kernels::matmul_f32 (cpu_kernels.rs:36-63) over the dequantized
 // weight, summed over k ascending.
 //
-// Weight tiles are dequantized into LDS as f16 with the converter's rounding,
-// h = RNE_f16(f32(q)*s + b) (tools/convert/src/main.rs:4435-4436).  For f16 or
-// bf16 scales, f32(q)*s is exact in f32, so fma(q, s, b) rounds exactly as the
-// reference's mul-then-add does; f32 scales take a separate mul and add.
+// Weights are dequantized to f16 with the converter's rounding,
+// h = RNE_f16(f32(q)*s + b) (tools/convert/src/main.rs:4435-4436): into LDS
+// tiles by qgemm_kernel, in registers right before each MFMA by the q4 kernel
+// for K % 128 == 0.  For f16 or bf16 scales, f32(q)*s is exact in f32, so
+// fma(q, s, b) rounds exactly as the reference's mul-then-add does; f32
+// scales take a separate mul and add.
 // int8 weights are exact in f16; their per-row scale is applied in the epilogue
 // (y = acc * s, cpu_kernels.rs:130).
 //
@@ -243,35 +245,18 @@ __global__ void add_bias_kernel(float* __restrict__ y, const float* __restrict__
 
 
 // ---------------------------------------------------------------------------
-// q4 affine qGEMM, direct-to-LDS pipeline (K % 128 == 0).
-//
-// 512 threads = 8 waves in a 2 (M) x 4 (N) grid of 64x32 wave tiles over a
-// 128x128 block tile; BK = 128 per stage; v_mfma_f32_32x32x16_f16 (its 32x32
-// accumulator keeps the loop free of AGPR<->VGPR moves, which the 16x16
-// form's 16 small accumulators provoke).  Per k-step:
-//   * X[128 rows, 128 k] f16 and the raw nibbles W[128 cols, 128 k] go
-//     global -> LDS with global_load_lds_dwordx4 (no register staging), one
-//     stage ahead of use (two stages);
-//   * each thread dequantizes 32 weights of the next step from the raw LDS
-//     tile into a double-buffered f16 tile with the converter's rounding
-//     (same arithmetic as dequant_word_f16);
-//   * X and W fragments are read from LDS tiles stored in 16 chunks of 8
-//     halves per row, chunk position XOR-swizzled by (row & 15) so that the
-//     16 rows a fragment read touches fall in 16 distinct 4-bank groups.
+// Direct-to-LDS helpers for the q4 qGEMM below (K % 128 == 0): LDS tiles hold
+// rows of 16 chunks of 8 halves, chunk position XOR-swizzled by (row & 15) so
+// that the 16 rows a fragment read touches fall in 16 distinct 4-bank groups.
 // The DMA loads are issued from inline asm with the LDS base in M0 and are
-// waited for with explicit s_waitcnt before each barrier: the compiler treats
-// LDS DMA as aliasing every LDS read and would otherwise wait for all of them
-// (including the stage just issued) before each fragment read.  The loop
-// therefore contains no compiler-visible global memory access; scales and
-// biases of the block's columns are preloaded into LDS once.
+// waited for with explicit s_waitcnt counts: the compiler treats LDS DMA as
+// aliasing every LDS read and would otherwise wait for all of them (including
+// the stage just issued) before each fragment read.
 // ---------------------------------------------------------------------------
 namespace dma {
 
 constexpr int BK = 128;
-constexpr int kThreads = 512;
 constexpr int kStageHalves = BM * BK;       // one f16 X or W tile
-constexpr int kRawWords = BN * BK / 8;      // one raw q4 W tile (u32 words)
-constexpr size_t kFixedLds = (2 * (size_t)kStageHalves + 2 * (size_t)kStageHalves) * 2 + 2 * (size_t)kRawWords * 4;
 constexpr size_t kMaxLds = 160 * 1024;
 
 __device__ __forceinline__ int slot(int r, int c) { return r * 16 + (c ^ (r & 15)); }
@@ -288,26 +273,112 @@ __device__ __forceinline__ void dma16(const void* g, uint32_t lds)
                  : "memory", "m0");
 }
 
+// Same with a uniform 64-bit base in SGPRs and a per-lane 32-bit byte offset: a loop that only changes
+// the base never rewrites the VGPR operand (the compiler's wait pass treats an asm's VGPR operands as
+// pending after it, and rewriting them cost a vmcnt(0) drain per iteration).
+__device__ __forceinline__ void dma16_s(uint32_t voff, const void* sbase, uint32_t lds)
+{
+    asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase),
+                 "s"(__builtin_amdgcn_readfirstlane(lds))
+                 : "memory", "m0");
+}
+
 template <int N>
 __device__ __forceinline__ void wait_vmcnt()
 {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// ---------------------------------------------------------------------------
+// q4 affine qGEMM, dequant at the MFMA (K % 128 == 0).
+//
+// 256 threads = 4 waves; block tile 128 (M) x 128 (N), wave tile 128 x 32:
+// four v_mfma_f32_32x32x16_f16 accumulators per wave.  X (f16) and the raw
+// nibbles of W go global -> LDS by global_load_lds_dwordx4 through a ring of
+// three stages (stage = one 128-wide k-step: X 128 x 128 halves, swizzled as
+// above, and W 128 columns x 64 bytes), issued two steps ahead; the f16
+// weights never touch LDS.  Lane (r32 = lane % 32, h32 = lane / 32) of wave
+// wn owns column n0 + 32 wn + r32 and, in each k-step, the 64 k starting at
+// 64 h32 (32 bytes of nibbles, two LDS reads).  The MFMA's k order is free as
+// long as X and W agree, so k-slot group h32 of substep ks is
+// k = 64 h32 + 8 ks + 0..7: one nibble word of the lane, dequantized right
+// before its MFMA, and chunk 8 h32 + ks of the X row.
+// Per k-step a CU moves ~170 KB through LDS instead of ~280 KB for the kernel
+// above (no f16 W tile written and re-read by fragment loads), and every
+// weight is dequantized once, by the lane that multiplies it.
+// Dequant: bytes of (w & 0x0F0F0F0F) and ((w >> 4) & 0x0F0F0F0F) convert with
+// v_cvt_f32_ubyteN, then fma(q, s, b) in f32 (mul then add for f32 scales)
+// and a round-to-nearest-even pack to f16: the converter's
+// RNE_f16(f32(q) * s + b).
+// The loop holds no compiler-visible global access (the DMA is inline asm
+// waited for by explicit counts): a register prefetch of W made the compiler
+// copy the loaded registers between iterations behind a vmcnt(0), which
+// drained every load in flight at each step.
+// ---------------------------------------------------------------------------
+constexpr int kRegThreads = 256;
+constexpr int kRegStages = 3;
+constexpr int kRawStepBytes = BN * BK / 2;                           // W nibbles of one k-step
+constexpr int kRegStageBytes = kStageHalves * 2 + kRawStepBytes;    // 40 KB
+constexpr size_t kRegFixedLds = (size_t)kRegStages * kRegStageBytes;
+
+// v_cvt_f32_ubyteN: byte N of a register to f32.  Spelled out because the compiler folds
+// (float)((x >> 8N) & 0xFF) of a masked word back into one v_bfe_u32 per nibble plus a convert.
+template <int N>
+__device__ __forceinline__ float cvt_ubyte(uint32_t x)
+{
+    float f;
+    if constexpr (N == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(f) : "v"(x));
+    else if constexpr (N == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(f) : "v"(x));
+    else if constexpr (N == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(f) : "v"(x));
+    else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(f) : "v"(x));
+    return f;
+}
+
 template <int SBT>
-__global__ __launch_bounds__(kThreads) void qgemm_q4_dma_kernel(const uint32_t* __restrict__ W,
-                                                                const void* __restrict__ S,
-                                                                const void* __restrict__ Bz, int gshift,
-                                                                const _Float16* __restrict__ X, float* __restrict__ out,
-                                                                int M, int N, int K, int k_per_split)
+__device__ __forceinline__ h8_t dequant_word_bytes(uint32_t w, float s, float b)
+{
+    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+    const float q[8] = {cvt_ubyte<0>(lo), cvt_ubyte<0>(hi), cvt_ubyte<1>(lo), cvt_ubyte<1>(hi),
+                        cvt_ubyte<2>(lo), cvt_ubyte<2>(hi), cvt_ubyte<3>(lo), cvt_ubyte<3>(hi)};
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float q0 = q[2 * i], q1 = q[2 * i + 1];  // nibbles 2i, 2i + 1
+        if constexpr (SBT == DT_F32) {
+#pragma clang fp contract(off)
+            const float t0 = q0 * s, t1 = q1 * s;
+            v[2 * i] = t0 + b;
+            v[2 * i + 1] = t1 + b;
+        } else {
+            v[2 * i] = __builtin_fmaf(q0, s, b);  // q*s exact: same bits as mul-then-add
+            v[2 * i + 1] = __builtin_fmaf(q1, s, b);
+        }
+    }
+    h8_t h;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        // Keep the f32 rounding (no fused v_fma_mix*_f16 with a single rounding).  Not volatile: a
+        // volatile asm is a scheduling barrier.
+        asm("" : "+v"(v[k]));
+        h[k] = (_Float16)v[k];
+    }
+    return h;
+}
+
+template <int SBT>
+__global__ __launch_bounds__(kRegThreads) void qgemm_q4_regw_kernel(const uint32_t* __restrict__ W,
+                                                                   const void* __restrict__ S,
+                                                                   const void* __restrict__ Bz, int gshift,
+                                                                   const _Float16* __restrict__ X,
+                                                                   float* __restrict__ out, int M, int N, int K,
+                                                                   int k_per_split)
 {
     extern __shared__ __align__(16) unsigned char smem[];
-    _Float16* xs = reinterpret_cast<_Float16*>(smem);             // 2 stages of X
-    _Float16* ws = xs + 2 * kStageHalves;                           // 2 f16 W tiles
-    uint32_t* wraw = reinterpret_cast<uint32_t*>(ws + 2 * kStageHalves);  // 2 raw W tiles
-    uint32_t* sbl = wraw + 2 * kRawWords;                            // [BN][groups]: f16/bf16 (s | b << 16), f32 pairs
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave & 1, wn = wave >> 1;
+    // stage t: X tile at t * kRegStageBytes, W raw at + kStageHalves * 2; then the scales/biases
+    uint32_t* sbl = reinterpret_cast<uint32_t*>(smem + kRegFixedLds);  // [BN][groups] as in the DMA kernel
+    // wn through readfirstlane: the DMA's LDS bases derived from it stay scalar arithmetic
+    const int tid = threadIdx.x, lane = tid & 63, wn = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r32 = lane & 31, h32 = lane >> 5;
     const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
     const int kbeg = blockIdx.z * k_per_split;
     const int kend = min(K, kbeg + k_per_split);
@@ -315,44 +386,51 @@ __global__ __launch_bounds__(kThreads) void qgemm_q4_dma_kernel(const uint32_t* 
     float* o = out + (size_t)blockIdx.z * M * N;
     if (nsteps <= 0) return;  // the launcher never makes an empty split
     const int last = nsteps - 1;
-    const int kwords = K >> 3;
     const int gpr = (K + (1 << gshift) - 1) >> gshift;
     const int g0 = kbeg >> gshift;
     const int ng = ((kend - 1) >> gshift) - g0 + 1;
 
-    // X DMA: wave issues 4 per stage, load j covers tile rows (wave*4+j)*4 .. +4
-    // (16 lanes per 256-byte row, lane -> chunk position, global chunk swizzled)
-    const _Float16* xsrc[4];
+    // X DMA: 8 per wave per stage, load j covers tile rows (wn * 8 + j) * 4 .. +4; byte offsets from
+    // X + 2 kbeg (the launcher keeps M K 2 below 2^32)
+    uint32_t xoff[8];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int r = (wave * 4 + j) * 4 + (lane >> 4);
+    for (int j = 0; j < 8; ++j) {
+        const int r = (wn * 8 + j) * 4 + (lane >> 4);
         const int c = (lane & 15) ^ (r & 15);
-        xsrc[j] = X + (size_t)min(m0 + r, M - 1) * K + kbeg + 8 * c;
+        xoff[j] = (uint32_t)((size_t)min(m0 + r, M - 1) * K * 2 + 16 * c);
     }
-    const uint32_t xs_lds = lds_addr(xs) + wave * 4 * 1024;
-    // raw W DMA and dequant: thread -> column tid/4, words 4(tid&3)..+4 (32 k) of a step
-    const int wcol = tid >> 2, wq4 = tid & 3;
-    const uint32_t* wsrc = W + (size_t)min(n0 + wcol, N - 1) * kwords + (kbeg >> 3) + 4 * wq4;
-    const uint32_t wr_lds = lds_addr(wraw) + wave * 1024;
-    // one group of loads per step: 4 X + 1 W per wave (tail steps re-read the last step)
-    auto issue = [&](int xstep, int wstep, int xst, int wst) {
-        const int xc = min(xstep, last), wc = min(wstep, last);
+    // W DMA: 2 per wave per stage, load j covers columns (wn * 2 + j) * 16 .. +16, 64 bytes each
+    // (columns past N re-read the last one: computed, never stored); byte offsets from W + kbeg / 2
+    uint32_t woff[2];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) dma16(xsrc[j] + (size_t)xc * BK, xs_lds + xst * kStageHalves * 2 + j * 1024);
-        dma16(wsrc + (size_t)wc * (BK / 8), wr_lds + wst * kRawWords * 4);
+    for (int j = 0; j < 2; ++j) {
+        const int col = min(n0 + (wn * 2 + j) * 16 + (lane >> 2), N - 1);
+        woff[j] = (uint32_t)((size_t)col * (K / 2) + 16 * (lane & 3));
+    }
+    const unsigned char* xbase = reinterpret_cast<const unsigned char*>(X) + (size_t)kbeg * 2;
+    const unsigned char* wbase = reinterpret_cast<const unsigned char*>(W) + kbeg / 2;
+    const uint32_t lds0 = lds_addr(smem);
+    auto issue = [&](int step) {
+        const int sc = min(step, last), st = step % kRegStages;
+        const uint32_t base = lds0 + st * kRegStageBytes;
+        const unsigned char* xs_ = xbase + (size_t)sc * BK * 2;
+        const unsigned char* ws_ = wbase + (size_t)sc * (BK / 2);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dma16_s(xoff[j], xs_, base + (wn * 8 + j) * 1024);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) dma16_s(woff[j], ws_, base + kStageHalves * 2 + (wn * 2 + j) * 1024);
     };
 
-    dma16(wsrc, wr_lds);  // W(0)
-    issue(0, 1, 0, 1);    // X(0), W(1)
+    issue(0);
     {
         // scales/biases of this split's groups, loads batched before any use
         constexpr int PB = 8;
         const int total = BN * ng;
-        for (int base = tid; base < total; base += PB * kThreads) {
+        for (int base = tid; base < total; base += PB * kRegThreads) {
             uint32_t sv[PB], bv[PB];
 #pragma unroll
             for (int u = 0; u < PB; ++u) {
-                const int i = min(base + u * kThreads, total - 1);
+                const int i = min(base + u * kRegThreads, total - 1);
                 const int col = i / ng, gi = i - col * ng;
                 const size_t idx = (size_t)min(n0 + col, N - 1) * gpr + g0 + gi;
                 sv[u] = load_raw<SBT>(S, idx);
@@ -360,79 +438,84 @@ __global__ __launch_bounds__(kThreads) void qgemm_q4_dma_kernel(const uint32_t* 
             }
 #pragma unroll
             for (int u = 0; u < PB; ++u) {
-                const int i = base + u * kThreads;
-                if (i < total) {
-                    if constexpr (SBT == DT_F32) {
-                        sbl[2 * i] = sv[u];
-                        sbl[2 * i + 1] = bv[u];
-                    } else {
-                        sbl[i] = sv[u] | (bv[u] << 16);
-                    }
+                // unconditional (slots past the end rewrite the last one with its own value): a load
+                // consumed only under a branch stays pending for the compiler on the other path, and
+                // the first reuse of its register inside the k-loop became a vmcnt(0) drain per step
+                const int i = min(base + u * kRegThreads, total - 1);
+                if constexpr (SBT == DT_F32) {
+                    sbl[2 * i] = sv[u];
+                    sbl[2 * i + 1] = bv[u];
+                } else {
+                    sbl[i] = sv[u] | (bv[u] << 16);
                 }
             }
         }
     }
-    wait_vmcnt<0>();
     __syncthreads();
+    issue(1);
 
-    // dequantize step `step` (raw tile wst) into f16 tile `buf`
-    auto dequant_step = [&](int step, int wst, int buf) {
-        const u4_t w = *reinterpret_cast<const u4_t*>(wraw + wst * kRawWords + tid * 4);
-        const int gi = ((kbeg + min(step, last) * BK + 32 * wq4) >> gshift) - g0;
-        float s, b;
+    const int lcol = wn * 32 + r32;
+    auto scale_bias = [&](int k) {
+        const int gi = ((kbeg + k) >> gshift) - g0;
+        float sc, bi;
         if constexpr (SBT == DT_F32) {
-            s = __builtin_bit_cast(float, sbl[2 * (wcol * ng + gi)]);
-            b = __builtin_bit_cast(float, sbl[2 * (wcol * ng + gi) + 1]);
+            sc = __builtin_bit_cast(float, sbl[2 * (lcol * ng + gi)]);
+            bi = __builtin_bit_cast(float, sbl[2 * (lcol * ng + gi) + 1]);
         } else {
-            const uint32_t sb = sbl[wcol * ng + gi];
-            s = raw_to_f32<SBT>(sb & 0xFFFFu);
-            b = raw_to_f32<SBT>(sb >> 16);
+            const uint32_t sb = sbl[lcol * ng + gi];
+            sc = raw_to_f32<SBT>(sb & 0xFFFFu);
+            bi = raw_to_f32<SBT>(sb >> 16);
         }
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            *reinterpret_cast<h8_t*>(ws + buf * kStageHalves + slot(wcol, 4 * wq4 + q) * 8) =
-                dequant_word_f16<SBT>(w[q], s, b);
+        return make_float2(sc, bi);
     };
-    dequant_step(0, 0, 0);
 
-    f16v_t acc[2];
-    acc[0] = f16v_t{};
-    acc[1] = f16v_t{};
-    const int r32 = lane & 31, h32 = lane >> 5;
+    f16v_t acc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = f16v_t{};
     for (int s = 0; s < nsteps; ++s) {
-        const int cur = s & 1, nxt = cur ^ 1;
-        // X(s), W(s+1) were the last group issued: nothing may stay in flight
-        wait_vmcnt<0>();
-        __syncthreads();  // stage s complete everywhere; stage s-1 and f16 tile (s+1)&1 free
-        issue(s + 1, s + 2, nxt, cur);        // X(s+1) -> stage nxt, W(s+2) -> raw tile of W(s)
-        dequant_step(s + 1, nxt, nxt);       // W(s+1): raw tile nxt -> f16 tile nxt
-        const _Float16* xa = xs + cur * kStageHalves;
-        const _Float16* wb = ws + cur * kStageHalves;
+        // Stage s was issued two steps ago; only stage s + 1 (10 loads per thread) may stay in flight.
+        // A bare s_barrier: __syncthreads()'s release fence waits for vmcnt(0), i.e. for every DMA in
+        // flight.  The asm waits carry memory clobbers, so no LDS access moves across them.
+        wait_vmcnt<10>();
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();  // stage s complete everywhere; stage s - 1 no longer read
+        issue(s + 2);                  // into the ring slot of stage s - 1
+        const unsigned char* sbase = smem + (s % kRegStages) * kRegStageBytes;
+        const _Float16* xa = reinterpret_cast<const _Float16*>(sbase);
+        const u4_t* wraw = reinterpret_cast<const u4_t*>(sbase + kStageHalves * 2 + lcol * 64 + 32 * h32);
+        const u4_t w0 = wraw[0], w1 = wraw[1];
+        const float2 sb0 = scale_bias(s * BK + 64 * h32), sb1 = scale_bias(s * BK + 64 * h32 + 32);
+        // A fragments are read one substep ahead of their MFMAs: with one wave per SIMD nothing
+        // else hides the LDS latency
+        h8_t a[2][4];
+        auto read_a = [&](int ks, h8_t (&dst)[4]) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                dst[i] = *reinterpret_cast<const h8_t*>(xa + slot(i * 32 + r32, 8 * h32 + ks) * 8);
+        };
+        read_a(0, a[0]);
 #pragma unroll
         for (int ks = 0; ks < BK / 16; ++ks) {
-            // 32x32x16: lane carries row/column lane%32, k chunk 2*ks + lane/32
-            h8_t a[2];
+            if (ks + 1 < BK / 16) read_a(ks + 1, a[(ks + 1) & 1]);
+            const uint32_t word = ks < 4 ? w0[ks] : w1[ks - 4];
+            const float2 sb = ks < 4 ? sb0 : sb1;
+            const h8_t b = dequant_word_bytes<SBT>(word, sb.x, sb.y);
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
-                a[i] = *reinterpret_cast<const h8_t*>(xa + slot(wm * 64 + i * 32 + r32, 2 * ks + h32) * 8);
-            const h8_t b = *reinterpret_cast<const h8_t*>(wb + slot(wn * 32 + r32, 2 * ks + h32) * 8);
-#pragma unroll
-            for (int i = 0; i < 2; ++i) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], b, acc[i], 0, 0, 0);
+            for (int i = 0; i < 4; ++i) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[ks & 1][i], b, acc[i], 0, 0, 0);
         }
     }
     // drain the trailing (re-read) DMA before the workgroup's LDS is released
     wait_vmcnt<0>();
 
-    // register r of a 32x32 tile: row (r/4)*8 + (lane/32)*4 + r%4, column lane%32;
-    // a store writes two full 128-byte row pieces
-    const int n = n0 + wn * 32 + r32;
-    if (n < N) {
+    // register r of a 32x32 tile: row (r/4)*8 + (lane/32)*4 + r%4, column lane%32
+    const int ncol = n0 + lcol;
+    if (ncol < N) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int m = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + h32 * 4 + (r & 3);
-                if (m < M) o[(size_t)m * N + n] = acc[i][r];
+                const int m = m0 + i * 32 + (r >> 2) * 8 + h32 * 4 + (r & 3);
+                if (m < M) o[(size_t)m * N + ncol] = acc[i][r];
             }
     }
 }
@@ -445,7 +528,7 @@ struct Plan {
 
 // Split-K so the grid covers the 256 CUs (each split >= 4 steps), and enough
 // splits that a split's scales/biases fit the LDS left by the tiles.
-Plan plan(int M, int N, int K, int group, int sbt)
+Plan plan(int M, int N, int K, int group, int sbt, size_t fixed_lds)
 {
     Plan p{0, 0, 0};
     if (K <= 0 || K % BK != 0 || group < 32) return p;
@@ -458,7 +541,7 @@ Plan plan(int M, int N, int K, int group, int sbt)
         const int sps = (steps + splits - 1) / splits;
         const int kps = sps * BK;
         const int ng = (kps + group - 1) / group + 1;  // + 1: a split may start mid-group
-        const size_t lds = kFixedLds + (size_t)BN * ng * sb_bytes;
+        const size_t lds = fixed_lds + (size_t)BN * ng * sb_bytes;
         if (lds <= kMaxLds) {
             p.splits = (steps + sps - 1) / sps;  // no empty split
             p.k_per_split = kps;
@@ -489,7 +572,7 @@ int qgemm_splits(int M, int N, int K)
 size_t qgemm_workspace_bytes(int wt, int M, int N, int K, int group_size, int sbt)
 {
     if (wt == 0) {
-        const dma::Plan p = dma::plan(M, N, K, group_size, sbt);
+        const dma::Plan p = dma::plan(M, N, K, group_size, sbt, dma::kRegFixedLds);
         if (p.splits > 0) return p.splits > 1 ? (size_t)p.splits * M * N * sizeof(float) : 0;
     }
     const int splits = qgemm_splits(M, N, K);
@@ -514,14 +597,15 @@ static hipError_t allow_lds(Kern kern, size_t bytes)
 }
 
 template <int SBT>
-static hipError_t launch_q4_dma(const dma::Plan& p, const uint32_t* wq, const void* S, const void* B, int gshift,
-                                const _Float16* x, float* out, int M, int N, int K, hipStream_t st)
+static hipError_t launch_q4_regw(const dma::Plan& p, const uint32_t* wq, const void* S, const void* B, int gshift,
+                                 const _Float16* x, float* out, int M, int N, int K, hipStream_t st)
 {
-    auto kern = dma::qgemm_q4_dma_kernel<SBT>;
+    auto kern = dma::qgemm_q4_regw_kernel<SBT>;
     hipError_t e = allow_lds(kern, p.lds);
     if (e != hipSuccess) return e;
     const dim3 grid((N + BN - 1) / BN, (M + BM - 1) / BM, p.splits);
-    hipLaunchKernelGGL(kern, grid, dim3(dma::kThreads), p.lds, st, wq, S, B, gshift, x, out, M, N, K, p.k_per_split);
+    hipLaunchKernelGGL(kern, grid, dim3(dma::kRegThreads), p.lds, st, wq, S, B, gshift, x, out, M, N, K,
+                       p.k_per_split);
     return hipGetLastError();
 }
 
@@ -561,13 +645,14 @@ hipError_t launch_qgemm_q4_affine_ws(const uint32_t* wq, const void* S, const vo
                                      const _Float16* x, float* y, int M, int N, int K, float* workspace,
                                      hipStream_t st)
 {
-    const dma::Plan p = dma::plan(M, N, K, group_size, sbt);
-    if (p.splits > 0 && (p.splits == 1 || workspace)) {
+    const dma::Plan p = dma::plan(M, N, K, group_size, sbt, dma::kRegFixedLds);
+    const bool offsets_fit = (uint64_t)M * K * 2 < (1ull << 32) && (uint64_t)N * K / 2 < (1ull << 32);
+    if (p.splits > 0 && (p.splits == 1 || workspace) && offsets_fit) {
         const int gshift = __builtin_ctz((unsigned)group_size);
         float* out = p.splits > 1 ? workspace : y;
-        hipError_t e = sbt == DT_F16   ? launch_q4_dma<DT_F16>(p, wq, S, B, gshift, x, out, M, N, K, st)
-                       : sbt == DT_F32 ? launch_q4_dma<DT_F32>(p, wq, S, B, gshift, x, out, M, N, K, st)
-                                       : launch_q4_dma<DT_BF16>(p, wq, S, B, gshift, x, out, M, N, K, st);
+        hipError_t e = sbt == DT_F16   ? launch_q4_regw<DT_F16>(p, wq, S, B, gshift, x, out, M, N, K, st)
+                       : sbt == DT_F32 ? launch_q4_regw<DT_F32>(p, wq, S, B, gshift, x, out, M, N, K, st)
+                                       : launch_q4_regw<DT_BF16>(p, wq, S, B, gshift, x, out, M, N, K, st);
         if (e != hipSuccess || p.splits == 1) return e;
         const size_t total = (size_t)M * N;
         unsigned blocks = (unsigned)((total + 255) / 256);

@@ -309,7 +309,7 @@ def test_qgemm_tiles_are_the_converter_f16_dequant(ops, sb):
 
 @pytest.mark.parametrize("m,k,n,group,sb", [
     (37, 192, 77, 64, np.float16),      # K % 128 != 0: register-staged kernel
-    (37, 256, 77, 64, np.float16),      # direct-to-LDS kernel, ragged M and N
+    (37, 256, 77, 64, np.float16),      # K % 128 == 0: dequant-at-the-MFMA kernel, ragged M and N
     (300, 640, 1000, 128, "bf16"),
     (130, 4864, 200, 64, np.float32),   # split-K through the workspace
     (64, 256, 96, 32, np.float16),
