@@ -22,6 +22,7 @@
 // Split-K over blockIdx.z writes f32 partials to a workspace that a second
 // kernel sums in a fixed order (deterministic).
 #include <atomic>
+#include <type_traits>
 
 #include "common.hpp"
 #include "kernels.hpp"
@@ -292,20 +293,20 @@ __device__ __forceinline__ void wait_vmcnt()
 // ---------------------------------------------------------------------------
 // q4 affine qGEMM, dequant at the MFMA (K % 128 == 0).
 //
-// 256 threads = 4 waves; block tile 128 (M) x 128 (N), wave tile 128 x 32:
-// four v_mfma_f32_32x32x16_f16 accumulators per wave.  X (f16) and the raw
-// nibbles of W go global -> LDS by global_load_lds_dwordx4 through a ring of
-// three stages (stage = one 128-wide k-step: X 128 x 128 halves, swizzled as
-// above, and W 128 columns x 64 bytes), issued two steps ahead; the f16
-// weights never touch LDS.  Lane (r32 = lane % 32, h32 = lane / 32) of wave
-// wn owns column n0 + 32 wn + r32 and, in each k-step, the 64 k starting at
-// 64 h32 (32 bytes of nibbles, two LDS reads).  The MFMA's k order is free as
-// long as X and W agree, so k-slot group h32 of substep ks is
-// k = 64 h32 + 8 ks + 0..7: one nibble word of the lane, dequantized right
-// before its MFMA, and chunk 8 h32 + ks of the X row.
-// Per k-step a CU moves ~170 KB through LDS instead of ~280 KB for the kernel
-// above (no f16 W tile written and re-read by fragment loads), and every
-// weight is dequantized once, by the lane that multiplies it.
+// 512 threads = 8 waves, two per SIMD; block tile 128 (M) x 128 (N).  Wave
+// (kh, ns) owns a 128 x 32 tile (four v_mfma_f32_32x32x16_f16 accumulators)
+// over k half kh of every 128-wide k-step; the two halves are added through
+// LDS after the loop.  X (f16) and the raw nibbles of W go global -> LDS by
+// global_load_lds_dwordx4 through a ring of three stages (stage = one k-step:
+// X 128 x 128 halves, swizzled as above, and W 128 columns x 64 bytes),
+// issued two steps ahead; the f16 weights never touch LDS.  Lane
+// (r32 = lane % 32, h32 = lane / 32) owns column n0 + 32 ns + r32 and the 32 k
+// starting at 64 kh + 32 h32 of each step (16 bytes of nibbles, one LDS read).
+// The MFMA's k order is free as long as X and W agree, so k-slot group h32 of
+// substep ks is k = 64 kh + 32 h32 + 8 ks + 0..7: one nibble word of the lane,
+// dequantized right before its MFMAs, and chunk 8 kh + 4 h32 + ks of the X row.
+// Every weight is dequantized once, by the lane that multiplies it, and LDS
+// carries no f16 weight tile.
 // Dequant: bytes of (w & 0x0F0F0F0F) and ((w >> 4) & 0x0F0F0F0F) convert with
 // v_cvt_f32_ubyteN, then fma(q, s, b) in f32 (mul then add for f32 scales)
 // and a round-to-nearest-even pack to f16: the converter's
@@ -313,13 +314,17 @@ __device__ __forceinline__ void wait_vmcnt()
 // The loop holds no compiler-visible global access (the DMA is inline asm
 // waited for by explicit counts): a register prefetch of W made the compiler
 // copy the loaded registers between iterations behind a vmcnt(0), which
-// drained every load in flight at each step.
+// drained every load in flight at each step.  Measured per k-step on the box:
+// X fragment reads plus DMA (~170 KB of LDS traffic per CU) 0.48 us, with the
+// MFMAs 0.82 us, everything 1.04 us; one wave per SIMD (4 waves, 128 x 32
+// tiles over the whole step) took 1.36 us.
 // ---------------------------------------------------------------------------
-constexpr int kRegThreads = 256;
+constexpr int kRegThreads = 512;
 constexpr int kRegStages = 3;
 constexpr int kRawStepBytes = BN * BK / 2;                           // W nibbles of one k-step
 constexpr int kRegStageBytes = kStageHalves * 2 + kRawStepBytes;    // 40 KB
 constexpr size_t kRegFixedLds = (size_t)kRegStages * kRegStageBytes;
+constexpr size_t kRegExchangeBytes = 8 * 2 * 16 * 64 * 4;  // k-half exchange after the loop (64 KB)
 
 // v_cvt_f32_ubyteN: byte N of a register to f32.  Spelled out because the compiler folds
 // (float)((x >> 8N) & 0xFF) of a masked word back into one v_bfe_u32 per nibble plus a convert.
@@ -376,8 +381,10 @@ __global__ __launch_bounds__(kRegThreads) void qgemm_q4_regw_kernel(const uint32
     extern __shared__ __align__(16) unsigned char smem[];
     // stage t: X tile at t * kRegStageBytes, W raw at + kStageHalves * 2; then the scales/biases
     uint32_t* sbl = reinterpret_cast<uint32_t*>(smem + kRegFixedLds);  // [BN][groups] as in the DMA kernel
-    // wn through readfirstlane: the DMA's LDS bases derived from it stay scalar arithmetic
+    // wn through readfirstlane: the DMA's LDS bases derived from it stay scalar arithmetic.  Wave
+    // wn = (kh, ns): k half kh of every step, 32-column slice ns of the tile.
     const int tid = threadIdx.x, lane = tid & 63, wn = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int kh = wn >> 2, ns = wn & 3;
     const int r32 = lane & 31, h32 = lane >> 5;
     const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
     const int kbeg = blockIdx.z * k_per_split;
@@ -390,23 +397,19 @@ __global__ __launch_bounds__(kRegThreads) void qgemm_q4_regw_kernel(const uint32
     const int g0 = kbeg >> gshift;
     const int ng = ((kend - 1) >> gshift) - g0 + 1;
 
-    // X DMA: 8 per wave per stage, load j covers tile rows (wn * 8 + j) * 4 .. +4; byte offsets from
+    // X DMA: 4 per wave per stage, load j covers tile rows (wn * 4 + j) * 4 .. +4; byte offsets from
     // X + 2 kbeg (the launcher keeps M K 2 below 2^32)
-    uint32_t xoff[8];
+    uint32_t xoff[4];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int r = (wn * 8 + j) * 4 + (lane >> 4);
+    for (int j = 0; j < 4; ++j) {
+        const int r = (wn * 4 + j) * 4 + (lane >> 4);
         const int c = (lane & 15) ^ (r & 15);
         xoff[j] = (uint32_t)((size_t)min(m0 + r, M - 1) * K * 2 + 16 * c);
     }
-    // W DMA: 2 per wave per stage, load j covers columns (wn * 2 + j) * 16 .. +16, 64 bytes each
-    // (columns past N re-read the last one: computed, never stored); byte offsets from W + kbeg / 2
-    uint32_t woff[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int col = min(n0 + (wn * 2 + j) * 16 + (lane >> 2), N - 1);
-        woff[j] = (uint32_t)((size_t)col * (K / 2) + 16 * (lane & 3));
-    }
+    // W DMA: 1 per wave per stage, covering columns wn * 16 .. +16, 64 bytes each (columns past N
+    // re-read the last one: computed, never stored); byte offsets from W + kbeg / 2
+    const uint32_t woff =
+        (uint32_t)((size_t)min(n0 + wn * 16 + (lane >> 2), N - 1) * (K / 2) + 16 * (lane & 3));
     const unsigned char* xbase = reinterpret_cast<const unsigned char*>(X) + (size_t)kbeg * 2;
     const unsigned char* wbase = reinterpret_cast<const unsigned char*>(W) + kbeg / 2;
     const uint32_t lds0 = lds_addr(smem);
@@ -416,9 +419,8 @@ __global__ __launch_bounds__(kRegThreads) void qgemm_q4_regw_kernel(const uint32
         const unsigned char* xs_ = xbase + (size_t)sc * BK * 2;
         const unsigned char* ws_ = wbase + (size_t)sc * (BK / 2);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) dma16_s(xoff[j], xs_, base + (wn * 8 + j) * 1024);
-#pragma unroll
-        for (int j = 0; j < 2; ++j) dma16_s(woff[j], ws_, base + kStageHalves * 2 + (wn * 2 + j) * 1024);
+        for (int j = 0; j < 4; ++j) dma16_s(xoff[j], xs_, base + (wn * 4 + j) * 1024);
+        dma16_s(woff, ws_, base + kStageHalves * 2 + wn * 1024);
     };
 
     issue(0);
@@ -454,7 +456,7 @@ __global__ __launch_bounds__(kRegThreads) void qgemm_q4_regw_kernel(const uint32
     __syncthreads();
     issue(1);
 
-    const int lcol = wn * 32 + r32;
+    const int lcol = ns * 32 + r32;
     auto scale_bias = [&](int k) {
         const int gi = ((kbeg + k) >> gshift) - g0;
         float sc, bi;
@@ -473,51 +475,70 @@ __global__ __launch_bounds__(kRegThreads) void qgemm_q4_regw_kernel(const uint32
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[i] = f16v_t{};
     for (int s = 0; s < nsteps; ++s) {
-        // Stage s was issued two steps ago; only stage s + 1 (10 loads per thread) may stay in flight.
+        // Stage s was issued two steps ago; only stage s + 1 (5 loads per thread) may stay in flight.
         // A bare s_barrier: __syncthreads()'s release fence waits for vmcnt(0), i.e. for every DMA in
         // flight.  The asm waits carry memory clobbers, so no LDS access moves across them.
-        wait_vmcnt<10>();
+        wait_vmcnt<5>();
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();  // stage s complete everywhere; stage s - 1 no longer read
         issue(s + 2);                  // into the ring slot of stage s - 1
         const unsigned char* sbase = smem + (s % kRegStages) * kRegStageBytes;
         const _Float16* xa = reinterpret_cast<const _Float16*>(sbase);
-        const u4_t* wraw = reinterpret_cast<const u4_t*>(sbase + kStageHalves * 2 + lcol * 64 + 32 * h32);
-        const u4_t w0 = wraw[0], w1 = wraw[1];
-        const float2 sb0 = scale_bias(s * BK + 64 * h32), sb1 = scale_bias(s * BK + 64 * h32 + 32);
-        // A fragments are read one substep ahead of their MFMAs: with one wave per SIMD nothing
-        // else hides the LDS latency
+        // this lane's 32 k of the step: k = 64 kh + 32 h32 + 8 ks + 0..7 (substep ks = 0..3)
+        const u4_t w = *reinterpret_cast<const u4_t*>(sbase + kStageHalves * 2 + lcol * 64 + 32 * kh + 16 * h32);
+        const float2 sb = scale_bias(s * BK + 64 * kh + 32 * h32);
+        // A fragments are read one substep ahead of their MFMAs
         h8_t a[2][4];
         auto read_a = [&](int ks, h8_t (&dst)[4]) {
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                dst[i] = *reinterpret_cast<const h8_t*>(xa + slot(i * 32 + r32, 8 * h32 + ks) * 8);
+                dst[i] = *reinterpret_cast<const h8_t*>(xa + slot(i * 32 + r32, 8 * kh + 4 * h32 + ks) * 8);
         };
         read_a(0, a[0]);
 #pragma unroll
-        for (int ks = 0; ks < BK / 16; ++ks) {
-            if (ks + 1 < BK / 16) read_a(ks + 1, a[(ks + 1) & 1]);
-            const uint32_t word = ks < 4 ? w0[ks] : w1[ks - 4];
-            const float2 sb = ks < 4 ? sb0 : sb1;
-            const h8_t b = dequant_word_bytes<SBT>(word, sb.x, sb.y);
+        for (int ks = 0; ks < 4; ++ks) {
+            if (ks + 1 < 4) read_a(ks + 1, a[(ks + 1) & 1]);
+            const h8_t b = dequant_word_bytes<SBT>(w[ks], sb.x, sb.y);
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[ks & 1][i], b, acc[i], 0, 0, 0);
         }
     }
-    // drain the trailing (re-read) DMA before the workgroup's LDS is released
+    // drain the trailing (re-read) DMA before the stage memory is reused
     wait_vmcnt<0>();
+    __syncthreads();
 
-    // register r of a 32x32 tile: row (r/4)*8 + (lane/32)*4 + r%4, column lane%32
+    // The two k halves meet through LDS: wave (kh, ns) hands the row tiles the other half keeps to
+    // its partner (kh = 0 keeps rows 0..63, kh = 1 rows 64..127) and adds what it receives; lane l
+    // exchanges with lane l of the partner, 8 KB per wave.  All partner values are read before any
+    // add or store (one LDS round trip instead of one per store).
+    float* xch = reinterpret_cast<float*>(smem);
     const int ncol = n0 + lcol;
-    if (ncol < N) {
+    auto finish = [&](auto keep_c) {
+        constexpr int KEEP = decltype(keep_c)::value, GIVE = 2 - KEEP;  // constant indices: no scratch
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) xch[(((wn * 2 + t) * 16 + r) * 64) + lane] = acc[GIVE + t][r];
+        __syncthreads();
+        float other[2][16];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) other[t][r] = xch[((((wn ^ 4) * 2 + t) * 16 + r) * 64) + lane];
+        if (ncol >= N) return;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int m = m0 + i * 32 + (r >> 2) * 8 + h32 * 4 + (r & 3);
-                if (m < M) o[(size_t)m * N + ncol] = acc[i][r];
+                // register r of a 32x32 tile: row (r/4)*8 + (lane/32)*4 + r%4, column lane%32
+                const int m = m0 + (KEEP + t) * 32 + (r >> 2) * 8 + h32 * 4 + (r & 3);
+                if (m < M) o[(size_t)m * N + ncol] = acc[KEEP + t][r] + other[t][r];
             }
-    }
+    };
+    if (kh == 0)
+        finish(std::integral_constant<int, 0>{});
+    else
+        finish(std::integral_constant<int, 2>{});
 }
 
 struct Plan {
@@ -645,7 +666,8 @@ hipError_t launch_qgemm_q4_affine_ws(const uint32_t* wq, const void* S, const vo
                                      const _Float16* x, float* y, int M, int N, int K, float* workspace,
                                      hipStream_t st)
 {
-    const dma::Plan p = dma::plan(M, N, K, group_size, sbt, dma::kRegFixedLds);
+    dma::Plan p = dma::plan(M, N, K, group_size, sbt, dma::kRegFixedLds);
+    p.lds = std::max(p.lds, dma::kRegExchangeBytes);
     const bool offsets_fit = (uint64_t)M * K * 2 < (1ull << 32) && (uint64_t)N * K / 2 < (1ull << 32);
     if (p.splits > 0 && (p.splits == 1 || workspace) && offsets_fit) {
         const int gshift = __builtin_ctz((unsigned)group_size);
