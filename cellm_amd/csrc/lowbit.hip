@@ -453,11 +453,171 @@ hipError_t launch_pair_lpr(int lpr, const uint8_t* w, const uint16_t* S, const v
     }
 }
 
+// ---------------------------------------------------------------------------
+// q1_0_g128 with one activation row and long outputs: a sign-sum table.
+//
+// Byte j of block b holds the signs of elements 8 (16 b + j) + 0..7, so the
+// byte's contribution to the row is T[16 b + j][byte] with
+// T[g][v] = sum_i (bit i of v ? x[8 g + i] : -x[8 g + i]).  Each CU builds T
+// for all K / 8 groups once (256 floats per group, 144 KB at K = 1152) and
+// then spends one LDS lookup and one add per 8 weights, instead of building
+// +-1 pairs and a dot2 per 2 weights.  T[g][v] = A[v & 15] + B[v >> 4], with
+// A and B the 16 signed sums of elements 0..3 and 4..7 of the group.
+// Lane = (row, block): a wave takes 64 / blocks-per-row rows at a time (7 at
+// K = 1152, 63 of 64 lanes busy), each lane one 18-byte block (nine 2-byte
+// loads, the next row group's issued before the current one is used); the
+// blocks of a row meet in a per-wave LDS slot.
+// ---------------------------------------------------------------------------
+constexpr int kLutThreads = 512;
+constexpr int kQ1Depth = 4;  // row groups in flight per wave
+constexpr size_t kLutMaxBytes = (size_t)(1152 / 8) * 256 * 4;  // K <= 1152 (at most 9 blocks per row)
+
+template <int XT>
+__global__ __launch_bounds__(kLutThreads) void q1_lut_kernel(const uint8_t* __restrict__ w, const void* __restrict__ x,
+                                                            float* __restrict__ y, int N, int K, int row_bytes,
+                                                            int park_per_wave)
+{
+    extern __shared__ __align__(16) float lut[];  // [K / 8][256], 64 floats per wave, parked row sums
+    const int G = K >> 3, nblk = K >> 7;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float* slot = lut + (size_t)G * 256 + wave * 64;
+    // the table: four threads per group, 64 entries each
+    for (int u = tid; u < G * 4; u += kLutThreads) {
+        const int g = u >> 2, part = u & 3;
+        float xv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) xv[i] = load_f32<XT>(x, (size_t)g * 8 + i);
+        float a[16], b[4];
+#pragma unroll
+        for (int c = 0; c < 16; ++c)
+            a[c] = (((c & 1) ? xv[0] : -xv[0]) + ((c & 2) ? xv[1] : -xv[1])) + (((c & 4) ? xv[2] : -xv[2]) + ((c & 8) ? xv[3] : -xv[3]));
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+            const int c = part * 4 + h;
+            b[h] = (((c & 1) ? xv[4] : -xv[4]) + ((c & 2) ? xv[5] : -xv[5])) + (((c & 4) ? xv[6] : -xv[6]) + ((c & 8) ? xv[7] : -xv[7]));
+        }
+        float4* dst = reinterpret_cast<float4*>(lut + (size_t)g * 256 + part * 64);
+#pragma unroll
+        for (int h = 0; h < 4; ++h)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                dst[h * 4 + q] = make_float4(a[4 * q] + b[h], a[4 * q + 1] + b[h], a[4 * q + 2] + b[h], a[4 * q + 3] + b[h]);
+    }
+    __syncthreads();
+
+    const int R = 64 / nblk;  // rows per wave step
+    const int r = lane / nblk, bk = lane - r * nblk;
+    const int ngroups = (N + R - 1) / R;
+    const int gw = blockIdx.x * (kLutThreads / 64) + wave, GW = gridDim.x * (kLutThreads / 64);
+    const int my_groups = gw < ngroups ? (ngroups - 1 - gw) / GW + 1 : 0;
+    float* park = lut + (size_t)G * 256 + (kLutThreads / 64) * 64 + (size_t)wave * park_per_wave;
+    auto load = [&](int i, uint16_t (&dst)[9]) {
+        // clamped: idle lanes and rows past N read a valid block whose result is never stored
+        const int grp = min(gw + i * GW, ngroups - 1);
+        const int row = min(grp * R + min(r, R - 1), N - 1);
+        const uint16_t* p = reinterpret_cast<const uint16_t*>(w + (size_t)row * row_bytes + (size_t)bk * 18);
+#pragma unroll
+        for (int k = 0; k < 9; ++k) dst[k] = p[k];
+    };
+    const float* tb = lut + (size_t)bk * 16 * 256;
+    auto group = [&](int i, const uint16_t (&c)[9]) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const uint32_t byte = (c[1 + (j >> 1)] >> (8 * (j & 1))) & 0xFFu;
+            sum += tb[j * 256 + byte];
+        }
+        slot[lane] = raw_to_f32<DT_F16>(c[0]) * sum;
+        __builtin_amdgcn_wave_barrier();  // LDS operations of a wave complete in order
+        if (lane < R) {
+            // all (up to 9) block sums read at once, clamped, then added in block order
+            float v9[9];
+#pragma unroll
+            for (int k = 0; k < 9; ++k) v9[k] = slot[lane * nblk + min(k, nblk - 1)];
+            float t = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 9; ++k) t += k < nblk ? v9[k] : 0.0f;
+            park[i * R + lane] = t;
+        }
+        __builtin_amdgcn_wave_barrier();
+    };
+    // kQ1Depth row groups in flight per wave; results parked in LDS until the end (a store in the loop
+    // would turn every load wait into a full vmcnt(0) drain)
+    uint16_t h[kQ1Depth][9];
+#pragma unroll
+    for (int p = 0; p < kQ1Depth; ++p) load(p, h[p]);
+    for (int i0 = 0; i0 < my_groups; i0 += kQ1Depth) {
+        // uniform control flow: every slot reloads (clamped past the end) and only the work is guarded;
+        // an early exit from the unrolled slots made the compiler's merged waits full drains
+#pragma unroll
+        for (int p = 0; p < kQ1Depth; ++p) {
+            const int i = i0 + p;
+            uint16_t c[9];
+#pragma unroll
+            for (int k = 0; k < 9; ++k) c[k] = h[p][k];
+            load(i + kQ1Depth, h[p]);
+            if (i < my_groups) group(i, c);
+        }
+    }
+    for (int k = lane; k < my_groups * R; k += 64) {
+        const int row = (gw + (k / R) * GW) * R + k % R;
+        if (row < N) y[row] = park[k];
+    }
+}
+
+static int lut_cus()
+{
+    static int cus = 0;
+    if (cus == 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+            cus = 256;
+    }
+    return cus;
+}
+
+// LDS of the table kernel: the table, a 64-float slot per wave and each wave's parked row sums
+// (0 if it exceeds one CU's 160 KB)
+static size_t q1_lut_lds(int N, int K, int* park_per_wave)
+{
+    const int nblk = K >> 7, R = 64 / nblk;
+    const int ngroups = (N + R - 1) / R, GW = lut_cus() * (kLutThreads / 64);
+    *park_per_wave = ((ngroups + GW - 1) / GW) * R;
+    const size_t lds = ((size_t)(K >> 3) * 256 + (kLutThreads / 64) * 64 + (size_t)(kLutThreads / 64) * *park_per_wave) * 4;
+    return lds <= 160 * 1024 ? lds : 0;
+}
+
+template <int XT>
+hipError_t launch_q1_lut(const uint8_t* w, const void* x, float* y, int N, int K, int row_bytes, size_t lds,
+                         int park_per_wave, hipStream_t st)
+{
+    auto kern = q1_lut_kernel<XT>;
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(kern, dim3(lut_cus()), dim3(kLutThreads), lds, st, w, x, y, N, K, row_bytes, park_per_wave);
+    return hipGetLastError();
+}
+
 template <int FMT>
 hipError_t launch_fmt(const uint8_t* w, const uint16_t* S, int mode, const void* x, int xdt, float* y, int M, int N,
                       int K, size_t row_bytes, hipStream_t st)
 {
     constexpr int UE = LowbitFmt<FMT>::kElems;
+    if constexpr (FMT == LB_Q1) {
+        int park = 0;
+        const size_t lut_lds = M == 1 && N >= 32768 && K % 128 == 0 && K > 0 &&
+                                       (size_t)(K >> 3) * 256 * 4 <= kLutMaxBytes &&
+                                       (reinterpret_cast<uintptr_t>(w) & 1u) == 0
+                                   ? q1_lut_lds(N, K, &park)
+                                   : 0;
+        if (lut_lds > 0) {
+            if (xdt == DT_F16) return launch_q1_lut<DT_F16>(w, x, y, N, K, (int)row_bytes, lut_lds, park, st);
+            if (xdt == DT_F32) return launch_q1_lut<DT_F32>(w, x, y, N, K, (int)row_bytes, lut_lds, park, st);
+            return launch_q1_lut<DT_BF16>(w, x, y, N, K, (int)row_bytes, lut_lds, park, st);
+        }
+    }
     if constexpr (FMT != LB_F16) {
         // f16 x: the pair-packed dot2 kernel (the i2 scale is applied to the row sum in both modes)
         const bool unit_ok = K > 0 && K % UE == 0 &&

@@ -541,6 +541,11 @@ __global__ __launch_bounds__(kRegThreads) void qgemm_q4_regw_kernel(const uint32
         finish(std::integral_constant<int, 2>{});
 }
 
+#ifndef CELLM_QGEMM_MIN_SPLIT_STEPS
+#define CELLM_QGEMM_MIN_SPLIT_STEPS 4
+#endif
+constexpr int kMinSplitSteps = CELLM_QGEMM_MIN_SPLIT_STEPS;  // k-steps per split at least
+
 struct Plan {
     int splits;
     int k_per_split;
@@ -556,7 +561,7 @@ Plan plan(int M, int N, int K, int group, int sbt, size_t fixed_lds)
     const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
     const int steps = K / BK;
     int splits = 1;
-    while (tiles * splits * 2 <= 256 && steps / (splits * 2) >= 4) splits *= 2;
+    while (tiles * splits * 2 <= 256 && steps / (splits * 2) >= kMinSplitSteps) splits *= 2;
     const size_t sb_bytes = sbt == DT_F32 ? 8 : 4;
     for (;;) {
         const int sps = (steps + splits - 1) / splits;

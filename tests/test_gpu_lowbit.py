@@ -148,7 +148,10 @@ def test_i2_gemv_exact_integers(ops, mode, xdt):
 
 Q1_CASES = [(1152, 1536, 1, np.float32), (2048, 1000, 4, np.float16), (4096, 300, 2, np.float32),
             (128, 9, 3, np.float32), (20480, 40, 1, np.float32), (1152, 6912, 1, np.float16),
-            (1152, 700, 3, np.float16)]
+            (1152, 700, 3, np.float16),
+            # one row, N >= 32768, K <= 1152: the sign-sum table kernel (9, 8, 5 and 1 blocks per row)
+            (1152, 40000, 1, np.float32), (1024, 32768, 1, np.float16), (640, 50000, 1, np.float16),
+            (128, 65536, 1, np.float32)]
 
 
 @pytest.mark.parametrize("k,n,m,xdt", Q1_CASES)
@@ -177,6 +180,24 @@ def test_q1_gemv_exact_integers_odd_row_offset(ops, xdt):
     buf[2:2 + w.size] = torch.from_numpy(w.reshape(-1)).cuda()
     y = out(m, n)
     ops.encode_qgemv_q1_0_g128(buf[2:2 + w.size].view(n, -1), dev(x), y, k)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(y.cpu().numpy(), oracle.qgemv_q1_0_g128(w, x, k))
+
+
+@pytest.mark.parametrize("xdt", [np.float32, np.float16])
+def test_q1_table_kernel_exact_integers(ops, xdt):
+    """One row, N >= 32768: the sign-sum table path.  d = 0.25 and integer x
+    keep every table entry and partial sum an exact integer (or quarter), so
+    the result must equal the oracle bit for bit; N = 33001 leaves a ragged
+    last row group (7 rows per group at K = 1152)."""
+    k, n = 1152, 33001
+    rng = np.random.default_rng(0x1AB)
+    w = rng.integers(0, 256, (n, k // 128 * 18)).astype(np.uint8)
+    d = np.full((n, k // 128), 0.25, np.float16)
+    w.reshape(n, k // 128, 18)[:, :, :2] = d.view(np.uint8).reshape(n, k // 128, 2)
+    x = rng.integers(-4, 5, (1, k)).astype(xdt)
+    y = out(1, n)
+    ops.encode_qgemv_q1_0_g128(dev(w), dev(x), y, k)
     torch.cuda.synchronize()
     np.testing.assert_array_equal(y.cpu().numpy(), oracle.qgemv_q1_0_g128(w, x, k))
 
