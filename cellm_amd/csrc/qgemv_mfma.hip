@@ -359,13 +359,14 @@ hipError_t launch_mfma_nt(const void* W, const void* S, const void* B, int per_c
                           const float* bias, float* Y, int M, int N, int K, hipStream_t st)
 {
     constexpr int KB = WT == 1 ? 64 : 128;
-    if constexpr (WT == 1 && MS == 4 && NT == 1) {
-        // X too big for two blocks per CU but within one CU's LDS: one 1024-thread block per CU keeps it
-        // whole; 16 waves of one W tile each (two tiles per wave need more than the 128 registers per
-        // lane a 1024-thread block leaves, and 8 waves of two tiles stream 12 % slower: measured)
+    if constexpr (MS == 4 && NT == 1) {
+        // X too big for two blocks per CU but within one CU's LDS: one block per CU keeps it whole.
+        // int8: 1024 threads, 16 waves of one W tile each (two tiles per wave need more than the 128
+        // registers per lane a 1024-thread block leaves, and 8 waves of two tiles stream 12 % slower:
+        // measured).  q4 (its dequant needs more registers): 512 threads.
         const size_t whole = (size_t)MS * 16 * (K + 8) * 2;
         if (whole > 80 * 1024 && whole <= kWholeXLds) {
-            constexpr int BT = 1024, DEPTH = 2, ROWS = (BT / 64) * NT * 16;
+            constexpr int BT = WT == 1 ? 1024 : 512, DEPTH = 2, ROWS = (BT / 64) * NT * 16;
             auto kern = qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, false, BT>;
             if (hipError_t e = allow_big_lds(kern, (int)kWholeXLds); e != hipSuccess) return e;
             const int ntiles = (N + ROWS - 1) / ROWS;
@@ -410,7 +411,7 @@ hipError_t launch_mfma_ms(const void* W, const void* S, const void* B, int per_c
     // two 16-row W tiles per wave when there are rows enough to fill the chip, unless X needs the
     // one-block-per-CU form (one tile per wave there)
     const size_t whole = (size_t)MS * 16 * (K + 8) * 2;
-    const bool whole_x = WT == 1 && MS == 4 && whole > 80 * 1024 && whole <= kWholeXLds;
+    const bool whole_x = MS == 4 && whole > 80 * 1024 && whole <= kWholeXLds;
     if (N >= 128 * 512 && !whole_x)
         return launch_mfma_nt<WT, MS, 2, SBT>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, st);
     return launch_mfma_nt<WT, MS, 1, SBT>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, st);

@@ -239,6 +239,19 @@ def test_i8_batched_whole_x_in_lds(ops, m, k, n):
     assert rel_err(y, oracle.qgemv_i8(w, s, x)) <= TOL_F32
 
 
+@pytest.mark.parametrize("m,k,n,sb", [(64, 1152, 1000, np.float16), (49, 1024, 4099, "bf16"),
+                                      (57, 1152, 262, np.float32), (64, 1280, 300, np.float16)])
+def test_q4_batched_whole_x_in_lds(ops, m, k, n, sb):
+    """q4 at 49..64 rows whose X is 80-152 KB: one 512-thread block per CU
+    with the whole X in LDS (ragged tile counts); K = 1280 is past 152 KB and
+    takes the chunked form."""
+    wq, s, b, x = make_q4(n, k, m, cfg=3, sb_dtype=sb, salt=m + k)
+    y = _run_q4(ops, wq, s, b, x)
+    assert rel_err(y, oracle.qgemv_q4_affine(wq, s, b, x, k)) <= TOL_F16_TILE
+    w16 = oracle.f16_bits_to_f32(oracle.dequant_q4_affine_f16(wq, s, b, k))
+    assert rel_err(y, oracle.gemm_xwT(x, w16)) <= TOL_F32
+
+
 @pytest.mark.parametrize("m", [16, 64])
 def test_q4_batched_gemma_mlp(ops, m):
     k, n = 1152, 13824
