@@ -538,7 +538,11 @@ __global__ __launch_bounds__(kFlatThreads) void qgemv_q4_flat_kernel(const u4_t*
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
         for (int j = 0; j < J; ++j) {
-            const u4_t w = wr[slot][j];
+            // copy the chunk and reissue its ring slot before the arithmetic: the opaque copy lets
+            // the next batch's load leave ahead of this chunk's dot instead of after it
+            u4_t w = wr[slot][j];
+            asm("" : "+v"(w));
+            load_w(bi + D, slot, j);
             float sc, bb;
             if constexpr (SBT == DT_F32) {
                 sc = *reinterpret_cast<const float*>(sbw + soff[j]);
@@ -557,7 +561,6 @@ __global__ __launch_bounds__(kFlatThreads) void qgemv_q4_flat_kernel(const u4_t*
                 d = dot2(and_or(t, m1f, magic), xa[j][e][3], d);
             }
             red[roff[j]] = sc * d + bb * xc[j].y;
-            load_w(bi + D, slot, j);
         }
         // LDS operations of a wave complete in order: the reads below see every lane's writes
         __builtin_amdgcn_wave_barrier();
