@@ -565,16 +565,19 @@ __global__ __launch_bounds__(kLutThreads) void q1_lut_kernel(const uint8_t* __re
     }
 }
 
+// CU count of the current device (cached per device)
 static int lut_cus()
 {
-    static int cus = 0;
-    if (cus == 0) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
-            cus = 256;
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    int& c = cached[dev & 63];
+    if (c == 0) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 256;
+        c = cus;
     }
-    return cus;
+    return c;
 }
 
 // LDS of the table kernel: the table, a 64-float slot per wave and each wave's parked row sums
