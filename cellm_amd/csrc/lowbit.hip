@@ -20,6 +20,7 @@
 // does not take (unaligned rows, K that is not a whole number of units, rows
 // too long for LDS) use a one-wave-per-row kernel that reads x from memory.
 #include <algorithm>
+#include <atomic>
 
 #include "common.hpp"
 #include "kernels.hpp"
@@ -596,9 +597,17 @@ hipError_t launch_q1_lut(const uint8_t* w, const void* x, float* y, int N, int K
                          int park_per_wave, hipStream_t st)
 {
     auto kern = q1_lut_kernel<XT>;
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    if (e != hipSuccess) return e;
+    // the dynamic LDS limit is raised once per device and kernel
+    static std::atomic<uint64_t> done{0};
+    int dev = 0;
+    if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
+    const uint64_t bit = 1ull << (dev & 63);
+    if (!(done.load(std::memory_order_acquire) & bit)) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        if (e != hipSuccess) return e;
+        done.fetch_or(bit, std::memory_order_acq_rel);
+    }
     hipLaunchKernelGGL(kern, dim3(lut_cus()), dim3(kLutThreads), lds, st, w, x, y, N, K, row_bytes, park_per_wave);
     return hipGetLastError();
 }

@@ -21,7 +21,9 @@
 // stage's global data is prefetched into registers during the MFMA loop.
 // Split-K over blockIdx.z writes f32 partials to a workspace that a second
 // kernel sums in a fixed order (deterministic).
-#include <atomic>
+#include <mutex>
+#include <utility>
+#include <vector>
 #include <type_traits>
 
 #include "common.hpp"
@@ -605,19 +607,22 @@ size_t qgemm_workspace_bytes(int wt, int M, int N, int K, int group_size, int sb
     return splits > 1 ? (size_t)splits * M * N * sizeof(float) : 0;
 }
 
-// Dynamic LDS above 64 KB needs the per-function limit raised once per device.
+// Dynamic LDS above 64 KB needs the per-function limit raised once per device and kernel (keyed by the
+// kernel itself: every instantiation of a kernel template has the same pointer type).
 template <typename Kern>
 static hipError_t allow_lds(Kern kern, size_t bytes)
 {
-    static std::atomic<uint64_t> done{0};
+    static std::mutex mu;
+    static std::vector<std::pair<int, const void*>> done;
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
-    const uint64_t bit = 1ull << (dev & 63);
-    if (done.load(std::memory_order_acquire) & bit) return hipSuccess;
-    e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)dma::kMaxLds);
-    if (e == hipSuccess) done.fetch_or(bit, std::memory_order_acq_rel);
+    const void* fn = reinterpret_cast<const void*>(kern);
+    std::lock_guard<std::mutex> lk(mu);
+    for (const auto& d : done)
+        if (d.first == dev && d.second == fn) return hipSuccess;
+    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)dma::kMaxLds);
+    if (e == hipSuccess) done.emplace_back(dev, fn);
     (void)bytes;
     return e;
 }

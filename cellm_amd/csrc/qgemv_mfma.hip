@@ -339,16 +339,22 @@ int resident_blocks(Kern kern, size_t lds)
 template <typename Kern>
 hipError_t allow_big_lds(Kern kern, int bytes)
 {
+    // keyed by (device, kernel): every instantiation of a kernel template has the same pointer type
+    struct Done {
+        int dev;
+        const void* fn;
+        int bytes;
+    };
     static std::mutex mu;
-    static std::vector<std::pair<int, int>> done;  // (device, bytes)
+    static std::vector<Done> done;
     int dev = 0;
     if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
+    const void* fn = reinterpret_cast<const void*>(kern);
     std::lock_guard<std::mutex> lk(mu);
     for (const auto& d : done)
-        if (d.first == dev && d.second >= bytes) return hipSuccess;
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       bytes);
-    if (e == hipSuccess) done.emplace_back(dev, bytes);
+        if (d.dev == dev && d.fn == fn && d.bytes >= bytes) return hipSuccess;
+    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (e == hipSuccess) done.push_back(Done{dev, fn, bytes});
     return e;
 }
 
