@@ -143,8 +143,8 @@ def op_array(ops_list):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 (sharding is described in "
-                                   "DESIGN.md, not implemented)"}))
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 (multi-GPU sharding of the "
+                                   "path is designed, not implemented)"}))
         sys.exit(2)
 
     import torch
