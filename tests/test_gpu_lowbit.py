@@ -184,7 +184,7 @@ def test_q1_gemv_exact_integers_odd_row_offset(ops, xdt):
     np.testing.assert_array_equal(y.cpu().numpy(), oracle.qgemv_q1_0_g128(w, x, k))
 
 
-@pytest.mark.parametrize("xdt", [np.float32, np.float16])
+@pytest.mark.parametrize("xdt", [np.float32, np.float16, "bf16"])
 def test_q1_table_kernel_exact_integers(ops, xdt):
     """One row, N >= 32768: the sign-sum table path.  d = 0.25 and integer x
     keep every table entry and partial sum an exact integer (or quarter), so
@@ -195,9 +195,10 @@ def test_q1_table_kernel_exact_integers(ops, xdt):
     w = rng.integers(0, 256, (n, k // 128 * 18)).astype(np.uint8)
     d = np.full((n, k // 128), 0.25, np.float16)
     w.reshape(n, k // 128, 18)[:, :, :2] = d.view(np.uint8).reshape(n, k // 128, 2)
-    x = rng.integers(-4, 5, (1, k)).astype(xdt)
+    x = rng.integers(-4, 5, (1, k)).astype(np.float32 if xdt == "bf16" else xdt)
     y = out(1, n)
-    ops.encode_qgemv_q1_0_g128(dev(w), dev(x), y, k)
+    xd = dev(x).to(torch.bfloat16) if xdt == "bf16" else dev(x)  # small integers are exact in bf16
+    ops.encode_qgemv_q1_0_g128(dev(w), xd, y, k)
     torch.cuda.synchronize()
     np.testing.assert_array_equal(y.cpu().numpy(), oracle.qgemv_q1_0_g128(w, x, k))
 
