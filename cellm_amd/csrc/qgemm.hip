@@ -534,7 +534,7 @@ __global__ __launch_bounds__(kRegThreads) void qgemm_q4_regw_kernel(const uint32
             for (int r = 0; r < 16; ++r) {
                 // register r of a 32x32 tile: row (r/4)*8 + (lane/32)*4 + r%4, column lane%32
                 const int m = m0 + (KEEP + t) * 32 + (r >> 2) * 8 + h32 * 4 + (r & 3);
-                if (m < M) o[(size_t)m * N + ncol] = acc[KEEP + t][r] + other[t][r];
+                if (m < M) __builtin_nontemporal_store(acc[KEEP + t][r] + other[t][r], o + (size_t)m * N + ncol);
             }
     };
     if (kh == 0)
