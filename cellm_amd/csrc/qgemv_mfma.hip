@@ -302,7 +302,15 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int m = i * 16 + g * 4 + e;
-                    if (n < N && m < M) Y[(size_t)m * N + n] = acc[i][t][e] * s + bv[t];
+                    if (n < N && m < M) {
+                        // many rows: up to 64 MB of logits that nothing re-reads soon, stored past the
+                        // caches (measured ~3 % faster at M = 64, 5 % slower at M = 4)
+                        const float v = acc[i][t][e] * s + bv[t];
+                        if (M > 8)
+                            __builtin_nontemporal_store(v, Y + (size_t)m * N + n);
+                        else
+                            Y[(size_t)m * N + n] = v;
+                    }
                 }
         }
     }
