@@ -77,7 +77,7 @@ SIGNATURES = {
     "cellm_hip_kv_write_f16": (_i32, [_vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
                                       _vp]),
     "cellm_hip_attention_gqa_f16kv": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64,
-                                             _i64, _i64, _vp, _vp]),
+                                             _i64, _i64, C.c_float, C.c_float, _vp, _vp]),
     "cellm_hip_add_f32_inplace": (_i32, [_vp, _vp, _vp, _i64, _vp]),
     "cellm_hip_argmax_f32": (_i32, [_vp, _vp, _i64, _i64, _vp, _vp, _vp]),
 }
@@ -110,11 +110,12 @@ def load(path: str | os.PathLike | None = None) -> C.CDLL:
 
 
 def last_error() -> str:
+    """Takes the calling thread's last error message (it is cleared, as
+    cellm_last_error_message does, crates/cellm-sdk/src/ffi.rs:126-138)."""
     lib = load()
-    n = lib.cellm_hip_last_error_message(None, 0)
-    buf = C.create_string_buffer(n + 1)
-    lib.cellm_hip_last_error_message(buf, n + 1)
-    return buf.value.decode(errors="replace")
+    buf = C.create_string_buffer(2048)
+    n = lib.cellm_hip_last_error_message(buf, len(buf))
+    return buf.raw[:n].decode(errors="replace")
 
 
 def check(rc: int) -> None:

@@ -7,6 +7,8 @@
 // copy x in, launch, and copy y back.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -16,6 +18,7 @@
 #include <vector>
 
 #include "../../include/cellm_hip.h"
+#include "api_guard.hpp"
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -23,16 +26,30 @@ using namespace cellm;
 
 namespace {
 
-thread_local std::string g_last_error;
+// The calling thread's last error (cellm.h:24-26 documents the reference's as
+// thread-local).  A fixed buffer: recording an error never allocates.
+thread_local ErrorSlot g_last_error = {};
+
+void store_error(const char* msg, size_t len) { g_last_error.store(msg, len); }
 
 }  // namespace
 
 namespace cellm {
-// Lets the other translation units of the library (cellm_file.cpp) report
-// through cellm_hip_last_error_message.
+// Lets the other translation units of the library (cellm_file.cpp,
+// llama_device.cpp) report through cellm_hip_last_error_message.
 int32_t set_error_external(int32_t code, const std::string& msg)
 {
-    g_last_error = msg;
+    store_error(msg.data(), msg.size());
+    return code;
+}
+
+// The CELLM_API_END report of this library: records "internal error: <what>"
+// without allocating.
+int32_t report_exception(int32_t code, const char* what)
+{
+    char buf[sizeof(g_last_error.msg)];
+    const int n = snprintf(buf, sizeof(buf), "internal error: %s", what ? what : "");
+    store_error(buf, n < 0 ? 0 : std::min((size_t)n, sizeof(buf) - 1));
     return code;
 }
 }  // namespace cellm
@@ -41,12 +58,12 @@ namespace {
 
 int32_t set_error(int32_t code, const char* fmt, ...)
 {
-    char buf[1024];
+    char buf[sizeof(g_last_error.msg)];
     va_list ap;
     va_start(ap, fmt);
-    vsnprintf(buf, sizeof(buf), fmt, ap);
+    int n = vsnprintf(buf, sizeof(buf), fmt, ap);
     va_end(ap);
-    g_last_error = buf;
+    store_error(buf, n < 0 ? 0 : std::min((size_t)n, sizeof(buf) - 1));
     return code;
 }
 
@@ -146,7 +163,21 @@ int32_t check_group(int64_t group)
     return CELLM_HIP_OK;
 }
 
-// Workspace for split-K on `st`, sized for this call; nullptr if not needed.
+// int8 scale counts: one per tensor, or one per output row (the reference's
+// per_channel = "the scale buffer covers every row", metal.rs:900,938-941).
+// Counts in between would silently use scale[0] there and are refused here.
+int32_t check_n_scales(int64_t n_scales, int64_t n, const char* what)
+{
+    if (n_scales == 1 || n_scales >= n) return CELLM_HIP_OK;
+    return set_error(CELLM_HIP_ERR_INVALID_ARG, "n_scales=%lld%s must be 1 (per tensor) or >= n=%lld (per row)",
+                     (long long)n_scales, what, (long long)n);
+}
+
+// Per-stream scratch (split-K partials, unfused gate/up rows, attention
+// partials), grown on demand.  The caller holds ctx->mu from this call until
+// every kernel that uses the buffer is enqueued: calls on one stream then
+// queue their scratch users back to back, and a grow (which waits for the
+// stream, then frees) cannot happen between a get and its launches.
 int32_t get_stream_buffer(cellm_hip_ctx* ctx, std::unordered_map<hipStream_t, DeviceBuffer>& map, hipStream_t st,
                           size_t need, float** out)
 {
@@ -183,7 +214,7 @@ int32_t qgemv_i8_impl(cellm_hip_ctx* ctx, const int8_t* w, const void* scales, i
     if (m == 0 || n == 0) return CELLM_HIP_OK;
     if (!w && k > 0) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null weight pointer");
     if (!scales || !y || (!x && k > 0)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null scale/x/y pointer");
-    if (n_scales < 1) return set_error(CELLM_HIP_ERR_INVALID_ARG, "n_scales must be >= 1");
+    if (int32_t rc = check_n_scales(n_scales, n, "")) return rc;
     const int per_channel = n_scales >= n ? 1 : 0;
     const bool gemm_ok = xdt == DT_F16 && k > 0 && (k % 64) == 0 && aligned16(w) && aligned16(x);
     // 2..64 activation rows: weights streamed once into MFMA operands (exact for
@@ -286,7 +317,7 @@ int32_t qkv_i8_impl(cellm_hip_ctx* ctx, const int8_t* const w[3], const void* co
         if (rows[i] == 0) continue;
         if ((!w[i] && k > 0) || !s[i] || !y[i] || (!x && k > 0))
             return set_error(CELLM_HIP_ERR_INVALID_ARG, "null pointer in projection %d", i);
-        if (n_s[i] < 1) return set_error(CELLM_HIP_ERR_INVALID_ARG, "n_scales must be >= 1 (projection %d)", i);
+        if (int32_t rc = check_n_scales(n_s[i], rows[i], i == 0 ? " (q)" : i == 1 ? " (k)" : " (v)")) return rc;
     }
     I8FusedSeg segs[3];
     for (int i = 0; i < 3; ++i)
@@ -310,7 +341,8 @@ int32_t gate_up_i8_impl(cellm_hip_ctx* ctx, const int8_t* wg, const void* sg, in
     if (!valid_dtype(sdt) || !valid_dtype(xdt)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "bad dtype");
     if (m == 0 || n == 0) return CELLM_HIP_OK;
     if ((k > 0 && (!wg || !wu || !x)) || !sg || !su || !h) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null pointer");
-    if (n_sg < 1 || n_su < 1) return set_error(CELLM_HIP_ERR_INVALID_ARG, "n_scales must be >= 1");
+    if (int32_t rc = check_n_scales(n_sg, n, " (gate)")) return rc;
+    if (int32_t rc = check_n_scales(n_su, n, " (up)")) return rc;
     I8FusedSeg segs[2] = {I8FusedSeg{wg, sg, bg, h, (int)n, n_sg >= n ? 1 : 0},
                           I8FusedSeg{wu, su, bu, nullptr, (int)n, n_su >= n ? 1 : 0}};
     if (k > 0 && qgemv_i8_fused_supported(xdt, (int)m, (int)k, x, segs, 2)) {
@@ -387,19 +419,11 @@ int32_t run_logits(cellm_hip_ctx* ctx, const float* x, size_t cols, size_t rows,
 
 extern "C" {
 
-size_t cellm_hip_last_error_message(char* buf, size_t buf_len)
-{
-    const size_t n = g_last_error.size();
-    if (buf && buf_len) {
-        const size_t c = n < buf_len - 1 ? n : buf_len - 1;
-        memcpy(buf, g_last_error.data(), c);
-        buf[c] = '\0';
-    }
-    return n;
-}
+size_t cellm_hip_last_error_message(char* buf, size_t buf_len) { return g_last_error.take(buf, buf_len); }
 
 int32_t cellm_hip_device_count(int32_t* out_count)
 {
+    CELLM_API_BEGIN
     if (!out_count) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null out_count");
     int n = 0;
     hipError_t e = hipGetDeviceCount(&n);
@@ -407,10 +431,12 @@ int32_t cellm_hip_device_count(int32_t* out_count)
     else if (e != hipSuccess) return hip_error(e, "hipGetDeviceCount");
     *out_count = n;
     return CELLM_HIP_OK;
+    CELLM_API_END(report_exception)
 }
 
 int32_t cellm_hip_smoke_test(int32_t device)
 {
+    CELLM_API_BEGIN
     int count = 0;
     hipError_t e = hipGetDeviceCount(&count);
     if (e != hipSuccess || count == 0) return set_error(CELLM_HIP_ERR_DEVICE, "no HIP device available");
@@ -443,10 +469,12 @@ int32_t cellm_hip_smoke_test(int32_t device)
     if (db) (void)hipFree(db);
     if (dc) (void)hipFree(dc);
     return rc;
+    CELLM_API_END(report_exception)
 }
 
 int32_t cellm_hip_create(int32_t device, cellm_hip_ctx_t** out_ctx)
 {
+    CELLM_API_BEGIN
     if (!out_ctx) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null out_ctx");
     *out_ctx = nullptr;
     int count = 0;
@@ -465,10 +493,12 @@ int32_t cellm_hip_create(int32_t device, cellm_hip_ctx_t** out_ctx)
     }
     *out_ctx = ctx;
     return CELLM_HIP_OK;
+    CELLM_API_END(report_exception)
 }
 
 void cellm_hip_destroy(cellm_hip_ctx_t* ctx)
 {
+    CELLM_API_BEGIN
     if (!ctx) return;
     DeviceGuard g(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
@@ -483,36 +513,44 @@ void cellm_hip_destroy(cellm_hip_ctx_t* ctx)
     if (ctx->y_buf.ptr) (void)hipFree(ctx->y_buf.ptr);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
+    CELLM_API_END_VOID
 }
 
 int32_t cellm_hip_synchronize(cellm_hip_ctx_t* ctx)
 {
+    CELLM_API_BEGIN
     if (int32_t rc = check_ctx(ctx)) return rc;
     DeviceGuard g(ctx->device);
     HIP_TRY(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
     return CELLM_HIP_OK;
+    CELLM_API_END(report_exception)
 }
 
 int32_t cellm_hip_get_stream(cellm_hip_ctx_t* ctx, void** out_stream)
 {
+    CELLM_API_BEGIN
     if (int32_t rc = check_ctx(ctx)) return rc;
     if (!out_stream) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null out_stream");
     *out_stream = reinterpret_cast<void*>(ctx->stream);
     return CELLM_HIP_OK;
+    CELLM_API_END(report_exception)
 }
 
 int32_t cellm_hip_weight_upload(cellm_hip_ctx_t* ctx, const char* key, const void* host, size_t nbytes,
                                 const void** out_dev)
 {
+    CELLM_API_BEGIN
     if (int32_t rc = check_ctx(ctx)) return rc;
     if (!key || !out_dev) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null key or out_dev");
     DeviceGuard g(ctx->device);
     std::lock_guard<std::recursive_mutex> lk(ctx->mu);
     return upload_locked(ctx, key, host, nbytes, out_dev);
+    CELLM_API_END(report_exception)
 }
 
 int32_t cellm_hip_weight_lookup(cellm_hip_ctx_t* ctx, const char* key, const void** out_dev, size_t* out_nbytes)
 {
+    CELLM_API_BEGIN
     if (int32_t rc = check_ctx(ctx)) return rc;
     if (!key) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null key");
     std::lock_guard<std::recursive_mutex> lk(ctx->mu);
@@ -521,10 +559,12 @@ int32_t cellm_hip_weight_lookup(cellm_hip_ctx_t* ctx, const char* key, const voi
     if (out_dev) *out_dev = it->second.ptr;
     if (out_nbytes) *out_nbytes = it->second.bytes;
     return CELLM_HIP_OK;
+    CELLM_API_END(report_exception)
 }
 
 int32_t cellm_hip_weight_evict(cellm_hip_ctx_t* ctx, const char* key)
 {
+    CELLM_API_BEGIN
     if (int32_t rc = check_ctx(ctx)) return rc;
     if (!key) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null key");
     DeviceGuard g(ctx->device);
@@ -537,42 +577,53 @@ int32_t cellm_hip_weight_evict(cellm_hip_ctx_t* ctx, const char* key)
     ctx->weight_bytes -= it->second.bytes;
     ctx->weights.erase(it);
     return CELLM_HIP_OK;
+    CELLM_API_END(report_exception)
 }
 
 int32_t cellm_hip_weight_cache_stats(cellm_hip_ctx_t* ctx, size_t* out_entries, size_t* out_bytes)
 {
+    CELLM_API_BEGIN
     if (int32_t rc = check_ctx(ctx)) return rc;
     std::lock_guard<std::recursive_mutex> lk(ctx->mu);
     if (out_entries) *out_entries = ctx->weights.size();
     if (out_bytes) *out_bytes = ctx->weight_bytes;
     return CELLM_HIP_OK;
+    CELLM_API_END(report_exception)
 }
 
 int32_t cellm_hip_qgemv_i8(cellm_hip_ctx_t* ctx, const int8_t* w, const void* scales, int32_t scale_dtype,
                            int64_t n_scales, const void* x, int32_t x_dtype, const float* bias, float* y, int64_t m,
                            int64_t n, int64_t k, void* stream)
 {
+    CELLM_API_BEGIN
     if (int32_t rc = check_ctx(ctx)) return rc;
     DeviceGuard g(ctx->device);
+    const std::lock_guard<std::recursive_mutex> lk(ctx->mu);  // held until the scratch users are enqueued
     return qgemv_i8_impl(ctx, w, scales, scale_dtype, n_scales, x, x_dtype, bias, y, m, n, k, pick_stream(ctx, stream),
                          false);
+    CELLM_API_END(report_exception)
 }
 
 int32_t cellm_hip_qgemv_q4_affine(cellm_hip_ctx_t* ctx, const uint32_t* wq, const void* scales, const void* biases,
                                   int32_t sb_dtype, int64_t group, const void* x, int32_t x_dtype, float* y,
                                   int64_t m, int64_t n, int64_t k, void* stream)
 {
+    CELLM_API_BEGIN
     if (int32_t rc = check_ctx(ctx)) return rc;
     DeviceGuard g(ctx->device);
+    const std::lock_guard<std::recursive_mutex> lk(ctx->mu);  // held until the scratch users are enqueued
     return qgemv_q4_impl(ctx, wq, scales, biases, sb_dtype, group, x, x_dtype, y, m, n, k, pick_stream(ctx, stream),
                          false);
+    CELLM_API_END(report_exception)
 }
 
 int32_t cellm_hip_qgemv_batch(cellm_hip_ctx_t* ctx, const cellm_hip_qgemv_op_t* ops, int64_t n_ops, void* stream)
 {
+    CELLM_API_BEGIN
     if (int32_t rc = check_ctx(ctx)) return rc;
     if (n_ops < 0 || (n_ops > 0 && !ops)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null or negative op list");
     DeviceGuard g(ctx->device);
+    const std::lock_guard<std::recursive_mutex> lk(ctx->mu);  // held until the scratch users are enqueued
     hipStream_t st = pick_stream(ctx, stream);
     for (int64_t i = 0; i < n_ops; ++i) {
         const cellm_hip_qgemv_op_t& o = ops[i];
@@ -595,6 +646,7 @@ int32_t cellm_hip_qgemv_batch(cellm_hip_ctx_t* ctx, const cellm_hip_qgemv_op_t* 
         if (rc) return rc;
     }
     return CELLM_HIP_OK;
+    CELLM_API_END(report_exception)
 }
 
 int32_t cellm_hip_qgemv_i8_qkv(cellm_hip_ctx_t* ctx, const int8_t* wq, const void* sq, int64_t n_sq, const float* bq,
@@ -603,8 +655,10 @@ int32_t cellm_hip_qgemv_i8_qkv(cellm_hip_ctx_t* ctx, const int8_t* wq, const voi
                                int32_t x_dtype, float* q, float* k_out, float* v, int64_t m, int64_t rows_q,
                                int64_t rows_kv, int64_t cols, void* stream)
 {
+    CELLM_API_BEGIN
     if (int32_t rc = check_ctx(ctx)) return rc;
     DeviceGuard g(ctx->device);
+    const std::lock_guard<std::recursive_mutex> lk(ctx->mu);  // held until the scratch users are enqueued
     const int8_t* w[3] = {wq, wk, wv};
     const void* s[3] = {sq, sk, sv};
     const int64_t n_s[3] = {n_sq, n_sk, n_sv};
@@ -612,6 +666,7 @@ int32_t cellm_hip_qgemv_i8_qkv(cellm_hip_ctx_t* ctx, const int8_t* wq, const voi
     float* y[3] = {q, k_out, v};
     const int64_t rows[3] = {rows_q, rows_kv, rows_kv};
     return qkv_i8_impl(ctx, w, s, n_s, b, scale_dtype, x, x_dtype, y, m, rows, cols, pick_stream(ctx, stream));
+    CELLM_API_END(report_exception)
 }
 
 int32_t cellm_hip_qgemv_i8_gate_up_silu(cellm_hip_ctx_t* ctx, const int8_t* wg, const void* sg, int64_t n_sg,
@@ -619,10 +674,13 @@ int32_t cellm_hip_qgemv_i8_gate_up_silu(cellm_hip_ctx_t* ctx, const int8_t* wg, 
                                         const float* bu, int32_t scale_dtype, const void* x, int32_t x_dtype, float* h,
                                         int64_t m, int64_t n, int64_t k, void* stream)
 {
+    CELLM_API_BEGIN
     if (int32_t rc = check_ctx(ctx)) return rc;
     DeviceGuard g(ctx->device);
+    const std::lock_guard<std::recursive_mutex> lk(ctx->mu);  // held until the scratch users are enqueued
     return gate_up_i8_impl(ctx, wg, sg, n_sg, bg, wu, su, n_su, bu, scale_dtype, x, x_dtype, h, m, n, k,
                            pick_stream(ctx, stream));
+    CELLM_API_END(report_exception)
 }
 
 int32_t cellm_hip_qgemv_q4_affine_gate_up_silu(cellm_hip_ctx_t* ctx, const uint32_t* wg, const void* sg,
@@ -630,16 +688,20 @@ int32_t cellm_hip_qgemv_q4_affine_gate_up_silu(cellm_hip_ctx_t* ctx, const uint3
                                                int32_t sb_dtype, int64_t group, const void* x, int32_t x_dtype,
                                                float* h, int64_t m, int64_t n, int64_t k, void* stream)
 {
+    CELLM_API_BEGIN
     if (int32_t rc = check_ctx(ctx)) return rc;
     DeviceGuard g(ctx->device);
+    const std::lock_guard<std::recursive_mutex> lk(ctx->mu);  // held until the scratch users are enqueued
     return gate_up_q4_impl(ctx, wg, sg, bg, wu, su, bu, sb_dtype, group, x, x_dtype, h, m, n, k,
                            pick_stream(ctx, stream));
+    CELLM_API_END(report_exception)
 }
 
 int32_t cellm_hip_qgemv_i4_sym(cellm_hip_ctx_t* ctx, const uint8_t* w, const uint16_t* scales_f16, int64_t n_scales,
                                int64_t gs, const void* x, int32_t x_dtype, float* y, int64_t m, int64_t n, int64_t k,
                                void* stream)
 {
+    CELLM_API_BEGIN
     if (int32_t rc = check_ctx(ctx)) return rc;
     if (int32_t rc = check_dims(m, n, k)) return rc;
     if (!valid_dtype(x_dtype)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "bad dtype");
@@ -656,56 +718,70 @@ int32_t cellm_hip_qgemv_i4_sym(cellm_hip_ctx_t* ctx, const uint8_t* w, const uin
                                 pick_stream(ctx, stream)),
             "qgemv_i4_sym launch");
     return CELLM_HIP_OK;
+    CELLM_API_END(report_exception)
 }
 
 int32_t cellm_hip_qgemv_f16(cellm_hip_ctx_t* ctx, const uint16_t* w_f16, const void* x, int32_t x_dtype, float* y,
                             int64_t m, int64_t n, int64_t k, void* stream)
 {
+    CELLM_API_BEGIN
     if (int32_t rc = check_ctx(ctx)) return rc;
     DeviceGuard g(ctx->device);
     return qgemv_lowbit_impl(LB_F16, w_f16, nullptr, 0, x, x_dtype, y, m, n, k, pick_stream(ctx, stream));
+    CELLM_API_END(report_exception)
 }
 
 int32_t cellm_hip_qgemv_i2(cellm_hip_ctx_t* ctx, const uint8_t* w, const uint16_t* scales_f16, int32_t scale_mode,
                            const void* x, int32_t x_dtype, float* y, int64_t m, int64_t n, int64_t k, void* stream)
 {
+    CELLM_API_BEGIN
     if (int32_t rc = check_ctx(ctx)) return rc;
     DeviceGuard g(ctx->device);
     return qgemv_lowbit_impl(LB_I2, w, scales_f16, scale_mode, x, x_dtype, y, m, n, k, pick_stream(ctx, stream));
+    CELLM_API_END(report_exception)
 }
 
 int32_t cellm_hip_qgemv_q1_0_g128(cellm_hip_ctx_t* ctx, const uint8_t* w, const void* x, int32_t x_dtype, float* y,
                                   int64_t m, int64_t n, int64_t k, void* stream)
 {
+    CELLM_API_BEGIN
     if (int32_t rc = check_ctx(ctx)) return rc;
     DeviceGuard g(ctx->device);
     return qgemv_lowbit_impl(LB_Q1, w, nullptr, 0, x, x_dtype, y, m, n, k, pick_stream(ctx, stream));
+    CELLM_API_END(report_exception)
 }
 
 int32_t cellm_hip_qgemm_q4_affine(cellm_hip_ctx_t* ctx, const uint32_t* wq, const void* scales, const void* biases,
                                   int32_t sb_dtype, int64_t group, const uint16_t* x_f16, float* y, int64_t m,
                                   int64_t n, int64_t k, void* stream)
 {
+    CELLM_API_BEGIN
     if (int32_t rc = check_ctx(ctx)) return rc;
     DeviceGuard g(ctx->device);
+    const std::lock_guard<std::recursive_mutex> lk(ctx->mu);  // held until the scratch users are enqueued
     return qgemv_q4_impl(ctx, wq, scales, biases, sb_dtype, group, x_f16, DT_F16, y, m, n, k, pick_stream(ctx, stream),
                          true);
+    CELLM_API_END(report_exception)
 }
 
 int32_t cellm_hip_qgemm_i8(cellm_hip_ctx_t* ctx, const int8_t* w, const void* scales, int32_t scale_dtype,
                            int64_t n_scales, const uint16_t* x_f16, const float* bias, float* y, int64_t m, int64_t n,
                            int64_t k, void* stream)
 {
+    CELLM_API_BEGIN
     if (int32_t rc = check_ctx(ctx)) return rc;
     DeviceGuard g(ctx->device);
+    const std::lock_guard<std::recursive_mutex> lk(ctx->mu);  // held until the scratch users are enqueued
     return qgemv_i8_impl(ctx, w, scales, scale_dtype, n_scales, x_f16, DT_F16, bias, y, m, n, k,
                          pick_stream(ctx, stream), true);
+    CELLM_API_END(report_exception)
 }
 
 int32_t cellm_hip_dequant_q4_affine(cellm_hip_ctx_t* ctx, const uint32_t* wq, const void* scales, const void* biases,
                                     int32_t sb_dtype, int64_t group, void* out, int32_t out_dtype, int64_t n,
                                     int64_t k, void* stream)
 {
+    CELLM_API_BEGIN
     if (int32_t rc = check_ctx(ctx)) return rc;
     if (int32_t rc = check_dims(1, n, k)) return rc;
     if (int32_t rc = check_group(group)) return rc;
@@ -720,11 +796,13 @@ int32_t cellm_hip_dequant_q4_affine(cellm_hip_ctx_t* ctx, const uint32_t* wq, co
                                      pick_stream(ctx, stream)),
             "dequant launch");
     return CELLM_HIP_OK;
+    CELLM_API_END(report_exception)
 }
 
 int32_t cellm_hip_logits_i8(cellm_hip_ctx_t* ctx, const float* x, const int8_t* w, const uint16_t* scales_f16,
                             size_t rows, size_t cols, const char* cache_key, float* out)
 {
+    CELLM_API_BEGIN
     if (int32_t rc = check_ctx(ctx)) return rc;
     if (!cache_key || (!x && cols) || (!out && rows)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null argument");
     DeviceGuard g(ctx->device);
@@ -737,11 +815,13 @@ int32_t cellm_hip_logits_i8(cellm_hip_ctx_t* ctx, const float* x, const int8_t* 
         return qgemv_i8_impl(ctx, reinterpret_cast<const int8_t*>(dw), ds, DT_F16, (int64_t)rows, dx, DT_F32, nullptr,
                              dy, 1, (int64_t)rows, (int64_t)cols, ctx->stream, false);
     });
+    CELLM_API_END(report_exception)
 }
 
 int32_t cellm_hip_logits_i4(cellm_hip_ctx_t* ctx, const float* x, const uint8_t* w, const uint16_t* scales_f16,
                             size_t n_scales, size_t rows, size_t cols, size_t gs, const char* cache_key, float* out)
 {
+    CELLM_API_BEGIN
     if (int32_t rc = check_ctx(ctx)) return rc;
     if (!cache_key || (!x && cols) || (!out && rows)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null argument");
     DeviceGuard g(ctx->device);
@@ -755,12 +835,14 @@ int32_t cellm_hip_logits_i4(cellm_hip_ctx_t* ctx, const float* x, const uint8_t*
                                       (int64_t)n_scales, (int64_t)gs, dx, DT_F32, dy, 1, (int64_t)rows, (int64_t)cols,
                                       ctx->stream);
     });
+    CELLM_API_END(report_exception)
 }
 
 int32_t cellm_hip_logits_q4_affine(cellm_hip_ctx_t* ctx, const float* x, const uint32_t* wq, const void* scales,
                                    const void* biases, int32_t sb_dtype, size_t rows, size_t cols,
                                    const char* cache_key, float* out)
 {
+    CELLM_API_BEGIN
     if (int32_t rc = check_ctx(ctx)) return rc;
     if (!cache_key || (!x && cols) || (!out && rows)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null argument");
     if (!valid_dtype(sb_dtype)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "bad dtype");
@@ -778,6 +860,7 @@ int32_t cellm_hip_logits_q4_affine(cellm_hip_ctx_t* ctx, const float* x, const u
         return qgemv_q4_impl(ctx, reinterpret_cast<const uint32_t*>(dw), ds, db, sb_dtype, 64, dx, DT_F32, dy, 1,
                              (int64_t)rows, (int64_t)cols, ctx->stream, false);
     });
+    CELLM_API_END(report_exception)
 }
 
 }  // extern "C"
@@ -808,6 +891,7 @@ extern "C" {
 int32_t cellm_hip_embed_i8(cellm_hip_ctx_t* ctx, const uint32_t* tokens, int64_t rows, const int8_t* embed_i8,
                            const uint16_t* scales_f16, int64_t vocab, int64_t hidden, float* out, void* stream)
 {
+    CELLM_API_BEGIN
     if (int32_t rc = check_ctx(ctx)) return rc;
     if (int32_t rc = check_dims(rows, vocab, hidden)) return rc;
     if (rows == 0 || hidden == 0) return CELLM_HIP_OK;
@@ -818,11 +902,13 @@ int32_t cellm_hip_embed_i8(cellm_hip_ctx_t* ctx, const uint32_t* tokens, int64_t
                             pick_stream(ctx, stream)),
             "embed_i8 launch");
     return CELLM_HIP_OK;
+    CELLM_API_END(report_exception)
 }
 
 int32_t cellm_hip_rms_norm(cellm_hip_ctx_t* ctx, const float* x, const void* weight, int32_t weight_dtype,
                            int64_t rows, int64_t n, float eps, float* out, void* stream)
 {
+    CELLM_API_BEGIN
     if (int32_t rc = check_ctx(ctx)) return rc;
     if (int32_t rc = check_dims(rows, n, 1)) return rc;
     if (!valid_dtype(weight_dtype)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "bad dtype");
@@ -832,11 +918,13 @@ int32_t cellm_hip_rms_norm(cellm_hip_ctx_t* ctx, const float* x, const void* wei
     HIP_TRY(launch_rms_norm(x, weight, weight_dtype, (int)rows, (int)n, eps, out, pick_stream(ctx, stream)),
             "rms_norm launch");
     return CELLM_HIP_OK;
+    CELLM_API_END(report_exception)
 }
 
 int32_t cellm_hip_add_rms_norm(cellm_hip_ctx_t* ctx, float* x, const float* y, const void* weight,
                                int32_t weight_dtype, int64_t rows, int64_t n, float eps, float* out, void* stream)
 {
+    CELLM_API_BEGIN
     if (int32_t rc = check_ctx(ctx)) return rc;
     if (int32_t rc = check_dims(rows, n, 1)) return rc;
     if (!valid_dtype(weight_dtype)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "bad dtype");
@@ -846,11 +934,13 @@ int32_t cellm_hip_add_rms_norm(cellm_hip_ctx_t* ctx, float* x, const float* y, c
     HIP_TRY(launch_add_rms_norm(x, y, weight, weight_dtype, (int)rows, (int)n, eps, out, pick_stream(ctx, stream)),
             "add_rms_norm launch");
     return CELLM_HIP_OK;
+    CELLM_API_END(report_exception)
 }
 
 int32_t cellm_hip_rope_half_f32(cellm_hip_ctx_t* ctx, float* x, int64_t rows, int64_t n_heads, int64_t head_dim,
                                 const int32_t* positions, const float* cos_sin, int64_t table_positions, void* stream)
 {
+    CELLM_API_BEGIN
     if (int32_t rc = check_ctx(ctx)) return rc;
     if (int32_t rc = check_dims(rows, n_heads, head_dim)) return rc;
     if (rows == 0 || n_heads == 0 || head_dim == 0) return CELLM_HIP_OK;
@@ -864,6 +954,7 @@ int32_t cellm_hip_rope_half_f32(cellm_hip_ctx_t* ctx, float* x, int64_t rows, in
                              pick_stream(ctx, stream)),
             "rope_half launch");
     return CELLM_HIP_OK;
+    CELLM_API_END(report_exception)
 }
 
 int32_t cellm_hip_kv_write_f16(cellm_hip_ctx_t* ctx, const float* k, const float* v, int64_t rows, int64_t kv_dim,
@@ -871,6 +962,7 @@ int32_t cellm_hip_kv_write_f16(cellm_hip_ctx_t* ctx, const float* k, const float
                                const uint32_t* block_tables, int64_t max_blocks, int64_t total_blocks,
                                int64_t n_layers, int64_t tokens_per_block, int64_t layer, void* stream)
 {
+    CELLM_API_BEGIN
     if (int32_t rc = check_ctx(ctx)) return rc;
     if (int32_t rc = check_paged(rows, max_blocks, total_blocks, n_layers, tokens_per_block, layer)) return rc;
     if (kv_dim < 1 || rows * kv_dim > INT32_MAX) return set_error(CELLM_HIP_ERR_INVALID_ARG, "bad kv_dim");
@@ -883,6 +975,7 @@ int32_t cellm_hip_kv_write_f16(cellm_hip_ctx_t* ctx, const float* k, const float
                                 pick_stream(ctx, stream)),
             "kv_write launch");
     return CELLM_HIP_OK;
+    CELLM_API_END(report_exception)
 }
 
 int32_t cellm_hip_rope_kv_write_f16(cellm_hip_ctx_t* ctx, float* q, float* k, const float* v, int64_t rows,
@@ -891,6 +984,7 @@ int32_t cellm_hip_rope_kv_write_f16(cellm_hip_ctx_t* ctx, float* q, float* k, co
                                     const uint32_t* block_tables, int64_t max_blocks, int64_t total_blocks,
                                     int64_t n_layers, int64_t tokens_per_block, int64_t layer, void* stream)
 {
+    CELLM_API_BEGIN
     if (int32_t rc = check_ctx(ctx)) return rc;
     if (int32_t rc = check_paged(rows, max_blocks, total_blocks, n_layers, tokens_per_block, layer)) return rc;
     if (n_heads < 1 || n_kv_heads < 1 || head_dim < 2 || head_dim % 2 != 0 ||
@@ -909,6 +1003,7 @@ int32_t cellm_hip_rope_kv_write_f16(cellm_hip_ctx_t* ctx, float* q, float* k, co
                                      pick_stream(ctx, stream)),
             "rope_kv_write launch");
     return CELLM_HIP_OK;
+    CELLM_API_END(report_exception)
 }
 
 int32_t cellm_hip_decode_qkv_rope_kv(cellm_hip_ctx_t* ctx, const float* x_prev, const float* y, float* x_out,
@@ -920,6 +1015,7 @@ int32_t cellm_hip_decode_qkv_rope_kv(cellm_hip_ctx_t* ctx, const float* x_prev, 
                                      const uint32_t* block_tables, int64_t max_blocks, int64_t total_blocks,
                                      int64_t n_layers, int64_t tokens_per_block, int64_t layer, void* stream)
 {
+    CELLM_API_BEGIN
     if (int32_t rc = check_ctx(ctx)) return rc;
     if (int32_t rc = check_paged(rows, max_blocks, total_blocks, n_layers, tokens_per_block, layer)) return rc;
     if (rows == 0) return CELLM_HIP_OK;
@@ -948,6 +1044,7 @@ int32_t cellm_hip_decode_qkv_rope_kv(cellm_hip_ctx_t* ctx, const float* x_prev, 
                               (int)tokens_per_block, (int)layer, pick_stream(ctx, stream)),
             "decode_qkv launch");
     return CELLM_HIP_OK;
+    CELLM_API_END(report_exception)
 }
 
 int32_t cellm_hip_decode_gate_up_silu(cellm_hip_ctx_t* ctx, const float* x_prev, const float* y, float* x_out,
@@ -955,6 +1052,7 @@ int32_t cellm_hip_decode_gate_up_silu(cellm_hip_ctx_t* ctx, const float* x_prev,
                                       const int8_t* wu, const uint16_t* su, int64_t rows, int64_t hidden,
                                       int64_t inter, float* h, void* stream)
 {
+    CELLM_API_BEGIN
     if (int32_t rc = check_ctx(ctx)) return rc;
     if (rows == 0) return CELLM_HIP_OK;
     if (rows < 0 || hidden > INT32_MAX || !decode_fused_supported((int)rows, (int)hidden) || hidden > 4096)
@@ -972,14 +1070,16 @@ int32_t cellm_hip_decode_gate_up_silu(cellm_hip_ctx_t* ctx, const float* x_prev,
                                   pick_stream(ctx, stream)),
             "decode_gate_up launch");
     return CELLM_HIP_OK;
+    CELLM_API_END(report_exception)
 }
 
 int32_t cellm_hip_attention_gqa_f16kv(cellm_hip_ctx_t* ctx, const float* q, const uint16_t* kcache,
                                       const uint16_t* vcache, const uint32_t* block_tables, int64_t max_blocks,
                                       int64_t total_blocks, const int32_t* positions, int64_t rows, int64_t n_heads,
                                       int64_t n_kv_heads, int64_t head_dim, int64_t n_layers, int64_t tokens_per_block,
-                                      int64_t layer, float* out, void* stream)
+                                      int64_t layer, float attn_scale, float soft_cap, float* out, void* stream)
 {
+    CELLM_API_BEGIN
     if (int32_t rc = check_ctx(ctx)) return rc;
     if (int32_t rc = check_paged(rows, max_blocks, total_blocks, n_layers, tokens_per_block, layer)) return rc;
     if (n_heads < 1 || n_kv_heads < 1 || head_dim < 1 || n_heads > 4096 ||
@@ -989,11 +1089,14 @@ int32_t cellm_hip_attention_gqa_f16kv(cellm_hip_ctx_t* ctx, const float* q, cons
                          "128 and max_blocks * tokens_per_block <= 32768 (got %lld/%lld/%lld, %lld positions)",
                          (long long)n_heads, (long long)n_kv_heads, (long long)head_dim,
                          (long long)(max_blocks * tokens_per_block));
+    if (!(attn_scale >= 0.0f) || !(soft_cap >= 0.0f) || std::isinf(attn_scale) || std::isinf(soft_cap))
+        return set_error(CELLM_HIP_ERR_INVALID_ARG, "attn_scale and soft_cap must be finite and >= 0 (0 = none)");
     if (rows == 0) return CELLM_HIP_OK;
     if (!q || !kcache || !vcache || !block_tables || !positions || !out)
         return set_error(CELLM_HIP_ERR_INVALID_ARG, "null pointer");
     if (!aligned16(kcache) || !aligned16(vcache)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "K/V must be 16-byte aligned");
     DeviceGuard g(ctx->device);
+    const std::lock_guard<std::recursive_mutex> lk(ctx->mu);  // held until the scratch users are enqueued
     const hipStream_t st = pick_stream(ctx, stream);
     float* ws = nullptr;
     const size_t need = attention_workspace_bytes((int)rows, (int)n_heads, (int)n_kv_heads, (int)head_dim,
@@ -1001,13 +1104,15 @@ int32_t cellm_hip_attention_gqa_f16kv(cellm_hip_ctx_t* ctx, const float* q, cons
     if (int32_t rc = get_stream_buffer(ctx, ctx->attn, st, need, &ws)) return rc;
     HIP_TRY(launch_attention_gqa_f16kv(q, kcache, vcache, block_tables, (int)max_blocks, (int)total_blocks, positions,
                                        (int)rows, (int)n_heads, (int)n_kv_heads, (int)head_dim, (int)n_layers,
-                                       (int)tokens_per_block, (int)layer, out, ws, st),
+                                       (int)tokens_per_block, (int)layer, attn_scale, soft_cap, out, ws, st),
             "attention launch");
     return CELLM_HIP_OK;
+    CELLM_API_END(report_exception)
 }
 
 int32_t cellm_hip_add_f32_inplace(cellm_hip_ctx_t* ctx, float* x, const float* y, int64_t n, void* stream)
 {
+    CELLM_API_BEGIN
     if (int32_t rc = check_ctx(ctx)) return rc;
     if (n < 0 || n > INT32_MAX) return set_error(CELLM_HIP_ERR_INVALID_ARG, "bad length");
     if (n == 0) return CELLM_HIP_OK;
@@ -1015,11 +1120,13 @@ int32_t cellm_hip_add_f32_inplace(cellm_hip_ctx_t* ctx, float* x, const float* y
     DeviceGuard g(ctx->device);
     HIP_TRY(launch_add_f32(x, y, x, (int)n, pick_stream(ctx, stream)), "add launch");
     return CELLM_HIP_OK;
+    CELLM_API_END(report_exception)
 }
 
 int32_t cellm_hip_argmax_f32(cellm_hip_ctx_t* ctx, const float* logits, int64_t rows, int64_t n, int32_t* out_index,
                              float* out_value, void* stream)
 {
+    CELLM_API_BEGIN
     if (int32_t rc = check_ctx(ctx)) return rc;
     if (int32_t rc = check_dims(rows, n, 1)) return rc;
     if (rows == 0) return CELLM_HIP_OK;
@@ -1028,6 +1135,7 @@ int32_t cellm_hip_argmax_f32(cellm_hip_ctx_t* ctx, const float* logits, int64_t 
     DeviceGuard g(ctx->device);
     HIP_TRY(launch_argmax(logits, (int)rows, (int)n, out_index, out_value, pick_stream(ctx, stream)), "argmax launch");
     return CELLM_HIP_OK;
+    CELLM_API_END(report_exception)
 }
 
 }  // extern "C"

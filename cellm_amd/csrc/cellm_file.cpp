@@ -35,9 +35,11 @@
 #include <hip/hip_runtime.h>
 
 #include "../../include/cellm_hip.h"
+#include "api_guard.hpp"
 
 namespace cellm {
 int32_t set_error_external(int32_t code, const std::string& msg);  // capi.cpp: the thread's last error
+int32_t report_exception(int32_t code, const char* what);           // capi.cpp: the same, without allocating
 }
 
 namespace {
@@ -362,6 +364,7 @@ extern "C" {
 
 int32_t cellm_file_open(const char* path, cellm_file_t** out)
 {
+    CELLM_API_BEGIN
     if (!path || !out) return fail(CELLM_HIP_ERR_INVALID_ARG, "null argument");
     *out = nullptr;
     std::unique_ptr<cellm_file> f(new cellm_file());
@@ -428,57 +431,69 @@ int32_t cellm_file_open(const char* path, cellm_file_t** out)
     (void)sink;
     *out = f.release();
     return CELLM_HIP_OK;
+    CELLM_API_END(cellm::report_exception)
 }
 
 void cellm_file_close(cellm_file_t* f) { delete f; }
 
 int32_t cellm_file_config(const cellm_file_t* f, cellm_file_config_t* out)
 {
+    CELLM_API_BEGIN
     if (!f || !out) return fail(CELLM_HIP_ERR_INVALID_ARG, "null argument");
     *out = f->config;
     return CELLM_HIP_OK;
+    CELLM_API_END(cellm::report_exception)
 }
 
 int32_t cellm_file_header_json(const cellm_file_t* f, const char** out_text, size_t* out_len)
 {
+    CELLM_API_BEGIN
     if (!f || !out_text || !out_len) return fail(CELLM_HIP_ERR_INVALID_ARG, "null argument");
     *out_text = f->header_text.data();
     *out_len = f->header_text.size();
     return CELLM_HIP_OK;
+    CELLM_API_END(cellm::report_exception)
 }
 
 int64_t cellm_file_tensor_count(const cellm_file_t* f) { return f ? (int64_t)f->tensors.size() : -1; }
 
 int32_t cellm_file_tensor_at(const cellm_file_t* f, int64_t index, cellm_file_tensor_t* out)
 {
+    CELLM_API_BEGIN
     if (!f || !out) return fail(CELLM_HIP_ERR_INVALID_ARG, "null argument");
     if (index < 0 || index >= (int64_t)f->tensors.size())
         return fail(CELLM_HIP_ERR_INVALID_ARG, "tensor index %lld out of range", (long long)index);
     *out = f->tensors[(size_t)index];
     return CELLM_HIP_OK;
+    CELLM_API_END(cellm::report_exception)
 }
 
 int32_t cellm_file_find(const cellm_file_t* f, const char* name, cellm_file_tensor_t* out)
 {
+    CELLM_API_BEGIN
     if (!f || !name) return fail(CELLM_HIP_ERR_INVALID_ARG, "null argument");
     auto it = f->by_name.find(name);
     if (it == f->by_name.end()) return fail(CELLM_HIP_ERR_NOT_FOUND, "cellm: unknown tensor %s", name);
     if (out) *out = f->tensors[it->second];
     return CELLM_HIP_OK;
+    CELLM_API_END(cellm::report_exception)
 }
 
 int32_t cellm_file_tensor_bytes(const cellm_file_t* f, const char* name, const void** out_host, size_t* out_nbytes)
 {
+    CELLM_API_BEGIN
     cellm_file_tensor_t t;
     if (int32_t rc = cellm_file_find(f, name, &t)) return rc;
     if (out_host) *out_host = f->map + t.offset_bytes;
     if (out_nbytes) *out_nbytes = (size_t)t.nbytes;
     return CELLM_HIP_OK;
+    CELLM_API_END(cellm::report_exception)
 }
 
 int32_t cellm_hip_upload_cellm_file(cellm_hip_ctx_t* ctx, const cellm_file_t* f, const char* name_prefix,
                                     int64_t* out_count, size_t* out_bytes)
 {
+    CELLM_API_BEGIN
     if (!ctx || !f) return fail(CELLM_HIP_ERR_INVALID_ARG, "null argument");
     const size_t plen = name_prefix ? strlen(name_prefix) : 0;
     int64_t count = 0;
@@ -494,6 +509,7 @@ int32_t cellm_hip_upload_cellm_file(cellm_hip_ctx_t* ctx, const cellm_file_t* f,
     if (out_count) *out_count = count;
     if (out_bytes) *out_bytes = bytes;
     return CELLM_HIP_OK;
+    CELLM_API_END(cellm::report_exception)
 }
 
 }  // extern "C"

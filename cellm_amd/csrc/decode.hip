@@ -10,7 +10,8 @@
 //   rope_half      rotate-half RoPE from a cos/sin table        cpu_kernels.rs:264-277
 //   kv_write_f16   f32 -> f16 (RNE) into the paged cache        kvcache.rs:589-615
 //   rope_kv_write  rope_half on q and k, then kv_write_f16, in one launch
-//   attention      single-token GQA over f16 K/V pages          kvcache.rs:710-789
+//   attention      single-token GQA over f16 K/V pages, with the
+//                  optional attn_scale and soft cap              kvcache.rs:710-789
 //   argmax         first maximum, non-finite -> -inf            llama.rs:1049-1092
 //
 // Where the reference rounds a product and a sum separately, so do these
@@ -237,8 +238,8 @@ __global__ void rope_kv_write_kernel(float* __restrict__ q, float* __restrict__ 
 template <int HD, int G>
 __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
     const float* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
-    const int32_t* __restrict__ pos, PagedKv kv, int layer, int n_kv_heads, float scale, float* __restrict__ part,
-    int nch_max)
+    const int32_t* __restrict__ pos, PagedKv kv, int layer, int n_kv_heads, float scale, float soft_cap,
+    float* __restrict__ part, int nch_max)
 {
     constexpr int KD = HD / 4;                             // Q.K dims per thread
     constexpr int KL = KD / 8;                             // 16-byte K loads per thread
@@ -319,7 +320,9 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
         float d = dot[g];
         d = d + __shfl_xor(d, 1);
         d = d + __shfl_xor(d, 2);
-        sc[g] = valid ? d * scale : -INFINITY;
+        float sg = d * scale;
+        if (soft_cap > 0.0f) sg = tanhf(sg / soft_cap) * soft_cap;  // kvcache.rs:768-770
+        sc[g] = valid ? sg : -INFINITY;
         float m = sc[g];
         m = fmaxf(m, __shfl_xor(m, 4));
         m = fmaxf(m, __shfl_xor(m, 8));
@@ -864,21 +867,21 @@ size_t attention_workspace_bytes(int rows, int n_heads, int n_kv_heads, int head
 hipError_t launch_attention_gqa_f16kv(const float* q, const uint16_t* kcache, const uint16_t* vcache,
                                       const uint32_t* block_tables, int max_blocks, int total_blocks,
                                       const int32_t* pos, int rows, int n_heads, int n_kv_heads, int head_dim,
-                                      int n_layers, int tokens_per_block, int layer, float* out, float* workspace,
-                                      hipStream_t st)
+                                      int n_layers, int tokens_per_block, int layer, float attn_scale,
+                                      float soft_cap, float* out, float* workspace, hipStream_t st)
 {
     const PagedKv kv{block_tables, max_blocks, total_blocks, n_layers, tokens_per_block, n_kv_heads * head_dim};
     const int nch = (max_blocks * tokens_per_block + kAttnChunk - 1) / kAttnChunk;
     if (nch > kAttnMaxChunks) return hipErrorInvalidValue;
-    // scale = 1 / sqrt(head_dim) in f32, as kvcache.rs computes it
-    const float scale = 1.0f / std::sqrt((float)head_dim);
+    // attn_scale None = 1 / sqrt(head_dim) in f32, as kvcache.rs:752 computes it
+    const float scale = attn_scale > 0.0f ? attn_scale : 1.0f / std::sqrt((float)head_dim);
     const dim3 pgrid((unsigned)(rows * n_kv_heads), (unsigned)nch);
     const dim3 cgrid((unsigned)(rows * n_kv_heads));
     const int G = n_heads / n_kv_heads;
     auto go = [&](auto hd, auto g) {
         constexpr int HD = decltype(hd)::value, GG = decltype(g)::value;
         hipLaunchKernelGGL((attn_partial_kernel<HD, GG>), pgrid, dim3(kAttnThreads), 0, st, q, kcache, vcache, pos, kv,
-                           layer, n_kv_heads, scale, workspace, nch);
+                           layer, n_kv_heads, scale, soft_cap, workspace, nch);
         hipLaunchKernelGGL((attn_combine_kernel<HD, GG>), cgrid, dim3(kAttnThreads), 0, st, workspace, pos, kv,
                            n_kv_heads, nch, out);
     };

@@ -59,7 +59,7 @@ hipError_t launch_qgemm_i8_ws(const int8_t* w, const void* S, int sdt, int per_c
                               const float* bias, float* y, int M, int N, int K, float* workspace, hipStream_t st);
 
 // Batched decode on MFMA (2 <= M <= 64, f16 x): int8 needs K % 64 == 0,
-// q4 K % 128 == 0 and group >= 32; 16-byte aligned W and x.
+// q4 K % 128 == 0 and group >= 64; 16-byte aligned W and x.
 bool qgemv_mfma_supported(int wt, int M, int K, int group_size);
 hipError_t launch_qgemv_mfma_i8(const int8_t* w, const void* S, int sdt, int per_channel, const _Float16* x,
                                 const float* bias, float* y, int M, int N, int K, hipStream_t st);
@@ -89,8 +89,8 @@ size_t attention_workspace_bytes(int rows, int n_heads, int n_kv_heads, int head
 hipError_t launch_attention_gqa_f16kv(const float* q, const uint16_t* kcache, const uint16_t* vcache,
                                       const uint32_t* block_tables, int max_blocks, int total_blocks,
                                       const int32_t* pos, int rows, int n_heads, int n_kv_heads, int head_dim,
-                                      int n_layers, int tokens_per_block, int layer, float* out, float* workspace,
-                                      hipStream_t st);
+                                      int n_layers, int tokens_per_block, int layer, float attn_scale,
+                                      float soft_cap, float* out, float* workspace, hipStream_t st);
 hipError_t launch_argmax(const float* logits, int rows, int n, int32_t* idx, float* val, hipStream_t st);
 // Fused decode-step GEMVs (decode.hip): residual add + RMSNorm prologue, int8
 // GEMV of two rows per team, RoPE + K/V write or SiLU * up epilogue.

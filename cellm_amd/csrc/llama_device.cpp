@@ -25,9 +25,11 @@
 
 #include "../../include/cellm_hip.h"
 #include "../../include/cellm_llama_step.h"
+#include "api_guard.hpp"
 
 namespace cellm_step {
-extern thread_local std::string g_err;  // llama_step.cpp: read by cellm_llama_last_error_message
+extern thread_local cellm::ErrorSlot g_err;  // llama_step.cpp: read by cellm_llama_last_error_message
+int32_t report_exception(int32_t code, const char* what);
 }
 
 namespace {
@@ -36,12 +38,12 @@ using cellm_step::g_err;
 
 int32_t fail(int32_t code, const char* fmt, ...)
 {
-    char buf[1024];
+    char buf[sizeof(g_err.msg)];
     va_list ap;
     va_start(ap, fmt);
-    vsnprintf(buf, sizeof(buf), fmt, ap);
+    const int n = vsnprintf(buf, sizeof(buf), fmt, ap);
     va_end(ap);
-    g_err = buf;
+    g_err.store(buf, n < 0 ? 0 : ((size_t)n < sizeof(buf) ? (size_t)n : sizeof(buf) - 1));
     return code;
 }
 
@@ -208,7 +210,7 @@ int32_t enqueue_step(cellm_llama_dev* m, int32_t rows)
                                                  d_bt, MB, c.total_blocks, L, tpb, l, S),
                     "residual + input_layernorm + qkv + rope + kv write");
             LIB_TRY(cellm_hip_attention_gqa_f16kv(H, q, kc, vc, d_bt, MB, c.total_blocks, d_pos, R, c.n_heads,
-                                                  c.n_kv_heads, c.head_dim, L, tpb, l, attn, S),
+                                                  c.n_kv_heads, c.head_dim, L, tpb, l, 0.0f, 0.0f, attn, S),
                     "attention");
             LIB_TRY(cellm_hip_qgemv_i8(H, W[3], Sc[3], CELLM_HIP_DTYPE_F16, hid, attn, CELLM_HIP_DTYPE_F32, nullptr,
                                        proj, R, hid, hid, S),
@@ -236,7 +238,7 @@ int32_t enqueue_step(cellm_llama_dev* m, int32_t rows)
                                             L, tpb, l, S),
                 "rope + kv write");
         LIB_TRY(cellm_hip_attention_gqa_f16kv(H, q, kc, vc, d_bt, MB, c.total_blocks, d_pos, R, c.n_heads,
-                                              c.n_kv_heads, c.head_dim, L, tpb, l, attn, S),
+                                              c.n_kv_heads, c.head_dim, L, tpb, l, 0.0f, 0.0f, attn, S),
                 "attention");
         LIB_TRY(cellm_hip_qgemv_i8(H, W[3], Sc[3], CELLM_HIP_DTYPE_F16, hid, attn, CELLM_HIP_DTYPE_F32, nullptr, proj, R,
                                    hid, hid, S),
@@ -310,6 +312,7 @@ extern "C" {
 
 int32_t cellm_llama_rope_table(float theta, int32_t head_dim, int32_t positions, float* out)
 {
+    CELLM_API_BEGIN
     if (!out || head_dim <= 0 || head_dim % 2 || positions <= 0)
         return fail(CELLM_HIP_ERR_INVALID_ARG, "bad rope table arguments");
     const int32_t half = head_dim / 2;
@@ -322,6 +325,7 @@ int32_t cellm_llama_rope_table(float theta, int32_t head_dim, int32_t positions,
             out[((size_t)p * half + i) * 2 + 1] = std::sin(angle);
         }
     return CELLM_HIP_OK;
+    CELLM_API_END(cellm_step::report_exception)
 }
 
 int32_t cellm_llama_dev_create(const cellm_llama_config_t* cfg, const cellm_llama_layer_t* layers,
@@ -329,8 +333,10 @@ int32_t cellm_llama_dev_create(const cellm_llama_config_t* cfg, const cellm_llam
                                const uint16_t* final_norm_f16, int32_t device, int32_t max_rows, int32_t max_blocks,
                                cellm_llama_dev_t** out)
 {
+    CELLM_API_BEGIN
     return dev_create_impl(cfg, layers, embed_i8, embed_scale_f16, nullptr, nullptr, final_norm_f16, device, max_rows,
                            max_blocks, out);
+    CELLM_API_END(cellm_step::report_exception)
 }
 
 }  // extern "C"
@@ -466,6 +472,7 @@ extern "C" {
 
 void cellm_llama_dev_destroy(cellm_llama_dev_t* m)
 {
+    CELLM_API_BEGIN
     if (!m) return;
     if (m->hip) (void)cellm_hip_synchronize(m->hip);
     for (int r = 0; r < 4; ++r) {
@@ -478,11 +485,13 @@ void cellm_llama_dev_destroy(cellm_llama_dev_t* m)
     cellm_hip_ctx_t* hip = m->hip;
     delete m;
     if (hip) cellm_hip_destroy(hip);
+    CELLM_API_END_VOID
 }
 
 int32_t cellm_llama_dev_create_from_file(const char* path, int32_t device, int32_t max_rows, int32_t max_blocks,
                                          int32_t tokens_per_block, int32_t total_blocks, cellm_llama_dev_t** out)
 {
+    CELLM_API_BEGIN
     if (!path || !out) return fail(CELLM_HIP_ERR_INVALID_ARG, "null argument");
     *out = nullptr;
     cellm_file_t* f = nullptr;
@@ -580,19 +589,23 @@ int32_t cellm_llama_dev_create_from_file(const char* path, int32_t device, int32
     return dev_create_impl(&c, layers.data(), static_cast<const int8_t*>(emb), static_cast<const uint16_t*>(embs),
                            static_cast<const int8_t*>(lm), static_cast<const uint16_t*>(lms),
                            static_cast<const uint16_t*>(fn), device, max_rows, max_blocks, out);
+    CELLM_API_END(cellm_step::report_exception)
 }
 
 int32_t cellm_llama_dev_set_graphs(cellm_llama_dev_t* m, int32_t enable)
 {
+    CELLM_API_BEGIN
     if (!m) return fail(CELLM_HIP_ERR_INVALID_ARG, "null argument");
     for (int32_t r = 0; enable && r < m->max_rows; ++r)
         if (!m->graph_exec[r]) return fail(CELLM_HIP_ERR_UNSUPPORTED, "no captured graph for %d rows", r + 1);
     m->use_graphs = enable != 0;
     return CELLM_HIP_OK;
+    CELLM_API_END(cellm_step::report_exception)
 }
 
 int32_t cellm_llama_dev_kv_upload(cellm_llama_dev_t* m, const uint16_t* k_f16, const uint16_t* v_f16, size_t n_elems)
 {
+    CELLM_API_BEGIN
     if (!m || !k_f16 || !v_f16) return fail(CELLM_HIP_ERR_INVALID_ARG, "null argument");
     if (n_elems != m->kv_elems) return fail(CELLM_HIP_ERR_INVALID_ARG, "K/V have %zu elements, not %zu", n_elems,
                                             m->kv_elems);
@@ -600,10 +613,12 @@ int32_t cellm_llama_dev_kv_upload(cellm_llama_dev_t* m, const uint16_t* k_f16, c
     RT_TRY(hipMemcpy(m->kcache.p, k_f16, n_elems * 2, hipMemcpyHostToDevice), "upload K");
     RT_TRY(hipMemcpy(m->vcache.p, v_f16, n_elems * 2, hipMemcpyHostToDevice), "upload V");
     return CELLM_HIP_OK;
+    CELLM_API_END(cellm_step::report_exception)
 }
 
 int32_t cellm_llama_dev_kv_download(cellm_llama_dev_t* m, uint16_t* k_f16, uint16_t* v_f16, size_t n_elems)
 {
+    CELLM_API_BEGIN
     if (!m || !k_f16 || !v_f16) return fail(CELLM_HIP_ERR_INVALID_ARG, "null argument");
     if (n_elems != m->kv_elems) return fail(CELLM_HIP_ERR_INVALID_ARG, "K/V have %zu elements, not %zu", n_elems,
                                             m->kv_elems);
@@ -612,11 +627,13 @@ int32_t cellm_llama_dev_kv_download(cellm_llama_dev_t* m, uint16_t* k_f16, uint1
     RT_TRY(hipMemcpy(k_f16, m->kcache.p, n_elems * 2, hipMemcpyDeviceToHost), "download K");
     RT_TRY(hipMemcpy(v_f16, m->vcache.p, n_elems * 2, hipMemcpyDeviceToHost), "download V");
     return CELLM_HIP_OK;
+    CELLM_API_END(cellm_step::report_exception)
 }
 
 int32_t cellm_llama_dev_step(cellm_llama_dev_t* m, int32_t rows, const uint32_t* tokens, const int32_t* positions,
                              const uint32_t* block_tables, uint32_t* out_tokens, float* out_logits, float* logits_out)
 {
+    CELLM_API_BEGIN
     if (!m || !tokens || !positions || !block_tables || !out_tokens)
         return fail(CELLM_HIP_ERR_INVALID_ARG, "null argument");
     const cellm_llama_config_t& c = m->cfg;
@@ -659,6 +676,7 @@ int32_t cellm_llama_dev_step(cellm_llama_dev_t* m, int32_t rows, const uint32_t*
         if (out_logits) out_logits[r] = val;
     }
     return CELLM_HIP_OK;
+    CELLM_API_END(cellm_step::report_exception)
 }
 
 }  // extern "C"

@@ -16,9 +16,19 @@
 
 #include "../../include/cellm_hip.h"
 #include "../../include/cellm_llama_step.h"
+#include "api_guard.hpp"
 
 namespace cellm_step {
-thread_local std::string g_err;  // shared with llama_device.cpp
+thread_local cellm::ErrorSlot g_err = {};  // shared with llama_device.cpp
+
+// The CELLM_API_END report of this library (no allocation).
+int32_t report_exception(int32_t code, const char* what)
+{
+    char buf[sizeof(g_err.msg)];
+    const int n = snprintf(buf, sizeof(buf), "internal error: %s", what ? what : "");
+    g_err.store(buf, n < 0 ? 0 : ((size_t)n < sizeof(buf) ? (size_t)n : sizeof(buf) - 1));
+    return code;
+}
 }
 
 namespace {
@@ -27,12 +37,12 @@ using cellm_step::g_err;
 
 int32_t fail(int32_t code, const char* fmt, ...)
 {
-    char buf[1024];
+    char buf[sizeof(g_err.msg)];
     va_list ap;
     va_start(ap, fmt);
-    vsnprintf(buf, sizeof(buf), fmt, ap);
+    const int n = vsnprintf(buf, sizeof(buf), fmt, ap);
     va_end(ap);
-    g_err = buf;
+    g_err.store(buf, n < 0 ? 0 : ((size_t)n < sizeof(buf) ? (size_t)n : sizeof(buf) - 1));
     return code;
 }
 
@@ -160,21 +170,13 @@ int32_t linear(cellm_llama* m, int layer, int j, const float* x, float* y)
 
 extern "C" {
 
-size_t cellm_llama_last_error_message(char* buf, size_t buf_len)
-{
-    const size_t n = g_err.size();
-    if (buf && buf_len) {
-        const size_t c = n < buf_len - 1 ? n : buf_len - 1;
-        memcpy(buf, g_err.data(), c);
-        buf[c] = '\0';
-    }
-    return n;
-}
+size_t cellm_llama_last_error_message(char* buf, size_t buf_len) { return g_err.take(buf, buf_len); }
 
 int32_t cellm_llama_create(const cellm_llama_config_t* cfg, const cellm_llama_layer_t* layers,
                            const int8_t* embed_i8, const uint16_t* embed_scale_f16, const uint16_t* final_norm_f16,
                            int32_t device, cellm_llama_t** out)
 {
+    CELLM_API_BEGIN
     if (!cfg || !layers || !embed_i8 || !embed_scale_f16 || !final_norm_f16 || !out)
         return fail(CELLM_HIP_ERR_INVALID_ARG, "null argument");
     *out = nullptr;
@@ -238,27 +240,33 @@ int32_t cellm_llama_create(const cellm_llama_config_t* cfg, const cellm_llama_la
     }
     *out = m;
     return CELLM_HIP_OK;
+    CELLM_API_END(cellm_step::report_exception)
 }
 
 void cellm_llama_destroy(cellm_llama_t* m)
 {
+    CELLM_API_BEGIN
     if (!m) return;
     if (m->hip) cellm_hip_destroy(m->hip);
     delete m;
+    CELLM_API_END_VOID
 }
 
 int32_t cellm_llama_kv_cache(cellm_llama_t* m, uint16_t** k_f16, uint16_t** v_f16, size_t* n_elems)
 {
+    CELLM_API_BEGIN
     if (!m || !k_f16 || !v_f16 || !n_elems) return fail(CELLM_HIP_ERR_INVALID_ARG, "null argument");
     *k_f16 = m->kcache.data();
     *v_f16 = m->vcache.data();
     *n_elems = m->kcache.size();
     return CELLM_HIP_OK;
+    CELLM_API_END(cellm_step::report_exception)
 }
 
 int32_t cellm_llama_step(cellm_llama_t* m, uint32_t token, size_t pos, const uint32_t* block_table,
                          size_t n_blocks, uint32_t* out_token, float* out_logit, float* logits_out)
 {
+    CELLM_API_BEGIN
     if (!m || !block_table || !out_token) return fail(CELLM_HIP_ERR_INVALID_ARG, "null argument");
     const cellm_llama_config_t& c = m->cfg;
     const size_t hid = (size_t)c.hidden, kvd = m->kv_dim, tpb = (size_t)c.tokens_per_block;
@@ -359,6 +367,7 @@ int32_t cellm_llama_step(cellm_llama_t* m, uint32_t token, size_t pos, const uin
     if (out_logit) *out_logit = logits[best];
     if (logits_out) memcpy(logits_out, logits.data(), vocab * sizeof(float));
     return CELLM_HIP_OK;
+    CELLM_API_END(cellm_step::report_exception)
 }
 
 }  // extern "C"

@@ -21,6 +21,9 @@
 // too long for LDS) use a one-wave-per-row kernel that reads x from memory.
 #include <algorithm>
 #include <atomic>
+#include <mutex>
+#include <utility>
+#include <vector>
 
 #include "common.hpp"
 #include "kernels.hpp"
@@ -567,18 +570,20 @@ __global__ __launch_bounds__(kLutThreads) void q1_lut_kernel(const uint8_t* __re
 }
 
 // CU count of the current device (cached per device)
+// CU count of the current device, cached per device id (any id; guarded by a mutex).
 static int lut_cus()
 {
-    static int cached[64] = {0};
+    static std::mutex mu;
+    static std::vector<std::pair<int, int>> cached;  // (device, CUs)
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) dev = 0;
-    int& c = cached[dev & 63];
-    if (c == 0) {
-        int cus = 0;
-        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 256;
-        c = cus;
-    }
-    return c;
+    const std::lock_guard<std::mutex> lk(mu);
+    for (const auto& e : cached)
+        if (e.first == dev) return e.second;
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 256;
+    cached.emplace_back(dev, cus);
+    return cus;
 }
 
 // LDS of the table kernel: the table, a 64-float slot per wave and each wave's parked row sums

@@ -129,6 +129,15 @@ class HipOps:
         return e.value, b.value
 
     # -- sync: MetalOps::logits_* -----------------------------------------------
+    @staticmethod
+    def _out_f32(out, rows: int, what: str) -> np.ndarray:
+        if out is None:
+            return np.empty(rows, np.float32)
+        if not isinstance(out, np.ndarray) or out.dtype != np.float32 or out.size != rows or \
+                not out.flags["C_CONTIGUOUS"]:
+            raise ValueError(f"{what}: out must be a C-contiguous float32 array of {rows} elements")
+        return out
+
     def logits_i8(self, x: np.ndarray, w_i8: np.ndarray, scales_f16_bits: np.ndarray, vocab: int, hidden: int,
                   cache_key: str, out: np.ndarray | None = None) -> np.ndarray:
         x = np.ascontiguousarray(x, np.float32)
@@ -136,7 +145,7 @@ class HipOps:
         s = np.ascontiguousarray(scales_f16_bits, np.uint16)
         if x.size != hidden or w.size != vocab * hidden or s.size != vocab:
             raise ValueError("logits_i8: shape mismatch")
-        out = np.empty(vocab, np.float32) if out is None else out
+        out = self._out_f32(out, vocab, "logits_i8")
         check(self._lib.cellm_hip_logits_i8(self._h, _np_ptr(x), _np_ptr(w), _np_ptr(s), vocab, hidden,
                                             cache_key.encode(), _np_ptr(out)))
         return out
@@ -148,21 +157,33 @@ class HipOps:
         s = np.ascontiguousarray(scales_f16_bits, np.uint16)
         if x.size != hidden or w.size != vocab * ((hidden + 1) // 2):
             raise ValueError("logits_i4: shape mismatch")
-        out = np.empty(vocab, np.float32) if out is None else out
+        if gs < 1 or vocab < 1 or s.size < vocab * (((hidden - 1) // gs + 1) if hidden else 1):
+            raise ValueError("logits_i4: need gs >= 1 and ceil(hidden / gs) f16 scales per row")
+        out = self._out_f32(out, vocab, "logits_i4")
         check(self._lib.cellm_hip_logits_i4(self._h, _np_ptr(x), _np_ptr(w), _np_ptr(s), s.size, vocab, hidden, gs,
                                             cache_key.encode(), _np_ptr(out)))
         return out
 
     def logits_q4_affine(self, x: np.ndarray, wq: np.ndarray, scales: np.ndarray, biases: np.ndarray, rows: int,
                          cols: int, cache_key: str, out: np.ndarray | None = None) -> np.ndarray:
+        """The LFM affine linear (lfm.rs:985-1066) from host arrays: x [cols],
+        wq u32 [rows, cols/8], scales/biases [rows, ceil(cols/64)] of one dtype
+        (float32, float16, or uint16 holding bf16 bits)."""
         x = np.ascontiguousarray(x, np.float32)
         wq = np.ascontiguousarray(wq, np.uint32)
         scales = np.ascontiguousarray(scales)
-        biases = np.ascontiguousarray(biases, scales.dtype)
+        biases = np.ascontiguousarray(biases)
+        if biases.dtype != scales.dtype:
+            raise TypeError(f"logits_q4_affine: biases dtype {biases.dtype} differs from scales {scales.dtype}")
         dt = _NP_DT.get(scales.dtype, DTYPE_BF16 if scales.dtype == np.uint16 else None)
         if dt is None:
             raise TypeError(f"unsupported scale dtype {scales.dtype}")
-        out = np.empty(rows, np.float32) if out is None else out
+        groups = (cols + 63) // 64
+        if rows < 0 or cols < 0 or cols % 8 != 0 or x.size != cols or wq.size * 8 != rows * cols or \
+                scales.size != rows * groups or biases.size != rows * groups:
+            raise ValueError("logits_q4_affine: shape mismatch (x [cols], wq [rows, cols/8], scales/biases "
+                             "[rows, ceil(cols/64)], cols % 8 == 0)")
+        out = self._out_f32(out, rows, "logits_q4_affine")
         check(self._lib.cellm_hip_logits_q4_affine(self._h, _np_ptr(x), _np_ptr(wq), _np_ptr(scales), _np_ptr(biases),
                                                    dt, rows, cols, cache_key.encode(), _np_ptr(out)))
         return out
@@ -374,12 +395,16 @@ class HipOps:
 
     def encode_attention(self, q, kcache, vcache, block_tables, positions_i32, out, n_heads: int, n_kv_heads: int,
                          head_dim: int, total_blocks: int, n_layers: int, tokens_per_block: int, layer: int,
-                         stream=None) -> None:
+                         attn_scale: float | None = None, soft_cap: float | None = None, stream=None) -> None:
+        """attention_single_token_gqa_f32 (kvcache.rs:710-789) per row; attn_scale
+        None = 1/sqrt(head_dim), soft_cap None = no cap (the reference's Options)."""
         rows = positions_i32.numel()
         check(self._lib.cellm_hip_attention_gqa_f16kv(self._h, _dev_ptr(q), _dev_ptr(kcache), _dev_ptr(vcache),
                                                       _dev_ptr(block_tables), block_tables.shape[-1], total_blocks,
                                                       _dev_ptr(positions_i32), rows, n_heads, n_kv_heads, head_dim,
-                                                      n_layers, tokens_per_block, layer, _dev_ptr(out),
+                                                      n_layers, tokens_per_block, layer,
+                                                      0.0 if attn_scale is None else attn_scale,
+                                                      0.0 if soft_cap is None else soft_cap, _dev_ptr(out),
                                                       _stream_ptr(stream)))
 
     def encode_add_inplace(self, x, y, stream=None) -> None:

@@ -56,9 +56,13 @@ typedef struct cellm_hip_ctx cellm_hip_ctx_t;
 
 /* ---- errors, devices, lifetime ------------------------------------------ */
 
-/* Copies the calling thread's last error message (NUL-terminated, truncated to
- * buf_len) and returns its full length; buf may be NULL to query the length.
- * Replaces cellm_last_error_message (crates/cellm-sdk/include/cellm.h:24-26). */
+/* Takes the calling thread's last error message: copies it NUL-terminated,
+ * truncated to buf_len - 1 bytes, clears it, and returns the number of bytes
+ * written (excluding the NUL).  A NULL buffer or buf_len 0 returns 0 and
+ * leaves the message.  Replaces cellm_last_error_message
+ * (crates/cellm-sdk/include/cellm.h:24-26, crates/cellm-sdk/src/ffi.rs:126-138);
+ * the message is per thread, as cellm.h documents.  Every entry point catches
+ * C++ exceptions and reports them as error codes (ffi.rs:142 catches panics). */
 size_t cellm_hip_last_error_message(char* buf, size_t buf_len);
 
 /* Number of visible HIP devices. */
@@ -104,8 +108,10 @@ int32_t cellm_hip_weight_cache_stats(cellm_hip_ctx_t* ctx, size_t* out_entries, 
 /* int8 per-row-scaled GEMV / GEMM:
  *   y[i, r] = (sum_j W[r, j] * x[i, j]) * scale[per_row ? r : 0]  (+ bias[r] if bias != NULL)
  * scale applied after the sum as in cpu_kernels::matmul_i8_f32
- * (crates/cellm-kernels/src/cpu_kernels.rs:66-133); per-tensor scale when
- * n_scales < n as MetalOps::encode_mv_i8_bias decides (metal.rs:891-904).
+ * (crates/cellm-kernels/src/cpu_kernels.rs:66-133); per-row scales when
+ * n_scales >= n, as MetalOps::encode_mv_i8_bias decides (metal.rs:891-904),
+ * one per-tensor scale when n_scales == 1; other counts are refused
+ * (CELLM_HIP_ERR_INVALID_ARG), where the reference would use scale[0].
  * scale_dtype: F32/F16/BF16; x_dtype: F32/F16/BF16.  m <= 4 runs the decode
  * GEMV; larger m with f16 x and k % 64 == 0 runs the MFMA GEMM. */
 int32_t cellm_hip_qgemv_i8(cellm_hip_ctx_t* ctx, const int8_t* w, const void* scales, int32_t scale_dtype,
@@ -124,7 +130,7 @@ int32_t cellm_hip_qgemv_q4_affine(cellm_hip_ctx_t* ctx, const uint32_t* wq, cons
 /* Fused QKV, one launch for m <= 4 (f16/f32 x, cols % 16 == 0, 16-byte
  * aligned W and x; other shapes run three cellm_hip_qgemv_i8 launches):
  *   q = (Wq . x) * sq (+ bq), k and v likewise with rows_kv rows each.
- * Each projection has its own scales (per row when n_s >= rows, else scale[0])
+ * Each projection has its own scales (per row when n_s >= rows, per tensor when n_s == 1)
  * and optional bias (NULL = none); all scales share scale_dtype.  Replaces
  * MetalOps::encode_qkv_i8 / encode_qkv_i8_bias (crates/cellm-kernels/src/metal.rs:923-945,
  * 1153-1160; kernel mv_qkv_i8 metal.rs:387-439). */
@@ -346,16 +352,19 @@ int32_t cellm_hip_decode_gate_up_silu(cellm_hip_ctx_t* ctx, const float* x_prev,
 /* MetalKvStorage::encode_attention / attention_single_token_gqa_f32
  * (kvcache.rs:710-789, 1377-1439): each row attends over positions
  * 0..positions[r] of `layer`; q and out [rows][n_heads][head_dim] f32, query
- * head h reads kv head h / (n_heads / n_kv_heads).  Needs n_heads %
- * n_kv_heads == 0, at most 8 query heads per kv head, head_dim 64 or 128,
- * max_blocks * tokens_per_block <= 32768.  Split over the sequence in chunks
- * of 64 positions whose softmax partials are combined in a second pass
- * (workspace owned by the context, per stream). */
+ * head h reads kv head h / (n_heads / n_kv_heads).  score = (q . k) * scale,
+ * scale = attn_scale, or 1/sqrt(head_dim) when attn_scale is 0 (the
+ * reference's None); soft_cap > 0 maps each score s to tanh(s / soft_cap) *
+ * soft_cap (Gemma), 0 = none.  Needs n_heads % n_kv_heads == 0, at most 8
+ * query heads per kv head, head_dim 64 or 128, max_blocks * tokens_per_block
+ * <= 32768.  Split over the sequence in chunks of 64 positions whose softmax
+ * partials are combined in a second pass (workspace owned by the context, per
+ * stream). */
 int32_t cellm_hip_attention_gqa_f16kv(cellm_hip_ctx_t* ctx, const float* q, const uint16_t* kcache,
                                       const uint16_t* vcache, const uint32_t* block_tables, int64_t max_blocks,
                                       int64_t total_blocks, const int32_t* positions, int64_t rows, int64_t n_heads,
                                       int64_t n_kv_heads, int64_t head_dim, int64_t n_layers, int64_t tokens_per_block,
-                                      int64_t layer, float* out, void* stream);
+                                      int64_t layer, float attn_scale, float soft_cap, float* out, void* stream);
 
 /* MetalOps::encode_add_f32_inplace: x[i] += y[i]. */
 int32_t cellm_hip_add_f32_inplace(cellm_hip_ctx_t* ctx, float* x, const float* y, int64_t n, void* stream);

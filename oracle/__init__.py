@@ -63,7 +63,7 @@ def _declare(L):
         "oracle_rms_norm_f32": (None, [vp, vp, sz, f32, vp]),
         "oracle_rope_half_f32": (None, [vp, sz, sz, sz, f32]),
         "oracle_softmax_f32": (None, [vp, sz]),
-        "oracle_attention_gqa_f16kv": (None, [vp, vp, vp, sz, vp, sz, sz, sz, vp, vp]),
+        "oracle_attention_gqa_f16kv": (None, [vp, vp, vp, sz, vp, sz, sz, sz, f32, f32, vp, vp]),
         "oracle_silu_mul_f32": (None, [vp, vp, sz]),
         "oracle_argmax_first": (C.c_int64, [vp, sz]),
     }
@@ -307,14 +307,18 @@ def softmax_(x: np.ndarray) -> np.ndarray:
     return x
 
 
-def attention_gqa_f16kv(kcache_bits, vcache_bits, bases, q, n_heads, n_kv_heads, head_dim):
+def attention_gqa_f16kv(kcache_bits, vcache_bits, bases, q, n_heads, n_kv_heads, head_dim, attn_scale=None,
+                        soft_cap=None):
+    """attention_single_token_gqa_f32 (kvcache.rs:710-789); attn_scale / soft_cap
+    None are the reference's None (1/sqrt(head_dim); no cap)."""
     bases = np.ascontiguousarray(bases, np.uint64)
     scores = np.empty(max(len(bases), 1), np.float32)
     out = np.empty(n_heads * head_dim, np.float32)
     lib().oracle_attention_gqa_f16kv(_p(np.ascontiguousarray(kcache_bits, np.uint16)),
                                      _p(np.ascontiguousarray(vcache_bits, np.uint16)), _p(bases), len(bases),
-                                     _p(np.ascontiguousarray(q, np.float32)), n_heads, n_kv_heads, head_dim, _p(scores),
-                                     _p(out))
+                                     _p(np.ascontiguousarray(q, np.float32)), n_heads, n_kv_heads, head_dim,
+                                     0.0 if attn_scale is None else attn_scale, 0.0 if soft_cap is None else soft_cap,
+                                     _p(scores), _p(out))
     return out
 
 

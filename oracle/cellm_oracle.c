@@ -614,14 +614,16 @@ void oracle_softmax_f32(float* x, size_t n)
 
 /* CpuKvStorage::attention_single_token_gqa_f32 (kvcache.rs:710-789) over f16
  * K/V rows addressed by per-token element bases (KvCacheLayout::token_base_elem,
- * crates/cellm-core/src/kv_cache.rs:62-73).  `scores` is scratch of length seq. */
+ * crates/cellm-core/src/kv_cache.rs:62-73).  `scores` is scratch of length seq.
+ * attn_scale: Some(s) when > 0, else None = 1/sqrt(head_dim) (:752);
+ * soft_cap: Some(c) when > 0, s = tanh(s / c) * c per score (:768-770). */
 void oracle_attention_gqa_f16kv(const uint16_t* kcache, const uint16_t* vcache, const size_t* bases, size_t seq,
-                                const float* q, size_t n_heads, size_t n_kv_heads, size_t head_dim, float* scores,
-                                float* out)
+                                const float* q, size_t n_heads, size_t n_kv_heads, size_t head_dim, float attn_scale,
+                                float soft_cap, float* scores, float* out)
 {
     for (size_t i = 0; i < n_heads * head_dim; ++i) out[i] = 0.0f;
     if (seq == 0) return;
-    float scale = 1.0f / sqrtf((float)head_dim);
+    float scale = attn_scale > 0.0f ? attn_scale : 1.0f / sqrtf((float)head_dim);
     size_t group_size = n_heads / n_kv_heads;
     if (group_size < 1) group_size = 1;
     for (size_t h = 0; h < n_heads; ++h) {
@@ -632,7 +634,9 @@ void oracle_attention_gqa_f16kv(const uint16_t* kcache, const uint16_t* vcache, 
             const uint16_t* kt = kcache + bases[t] + kv_h * head_dim;
             float dot = 0.0f;
             for (size_t i = 0; i < head_dim; ++i) dot += qh[i] * oracle_f16_to_f32(kt[i]);
-            scores[t] = dot * scale;
+            float sc = dot * scale;
+            if (soft_cap > 0.0f) sc = tanhf(sc / soft_cap) * soft_cap;
+            scores[t] = sc;
         }
         oracle_softmax_f32(scores, seq);
         float* out_h = out + h * head_dim;

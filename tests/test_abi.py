@@ -60,13 +60,115 @@ def test_error_reporting_without_device():
     rc = lib.cellm_hip_synchronize(None)
     assert rc == _lib.ERR_INVALID_ARG
     assert "null context" in _lib.last_error()
-    # message length query with a NULL buffer
-    n = lib.cellm_hip_last_error_message(None, 0)
-    assert n == len("null context")
-    # truncation keeps a NUL terminator
+
+
+def test_last_error_message_follows_the_reference_ffi():
+    """cellm_last_error_message (crates/cellm-sdk/src/ffi.rs:126-138): a NULL
+    or empty buffer returns 0 and leaves the message; otherwise the message is
+    taken, truncated to buf_len - 1 bytes plus NUL, and the bytes written are
+    returned."""
+    from cellm_amd import _lib
+
+    lib = _lib.load()
+    assert lib.cellm_hip_synchronize(None) == _lib.ERR_INVALID_ARG
+    assert lib.cellm_hip_last_error_message(None, 0) == 0
+    assert lib.cellm_hip_last_error_message(C.create_string_buffer(8), 0) == 0
     buf = C.create_string_buffer(5)
-    lib.cellm_hip_last_error_message(buf, 5)
+    assert lib.cellm_hip_last_error_message(buf, 5) == 4  # "null" + NUL
     assert buf.value == b"null"
+    # taken: a second read finds nothing
+    buf = C.create_string_buffer(64)
+    assert lib.cellm_hip_last_error_message(buf, 64) == 0 and buf.value == b""
+    # a full read returns the whole message
+    assert lib.cellm_hip_synchronize(None) == _lib.ERR_INVALID_ARG
+    assert lib.cellm_hip_last_error_message(buf, 64) == len("null context") and buf.value == b"null context"
+
+
+def test_messages_are_per_thread():
+    """Each thread reads its own last error."""
+    import threading
+
+    from cellm_amd import _lib
+
+    lib = _lib.load()
+    assert lib.cellm_hip_device_count(None) == _lib.ERR_INVALID_ARG
+    seen = {}
+
+    def other():
+        assert lib.cellm_hip_synchronize(None) == _lib.ERR_INVALID_ARG
+        seen["other"] = _lib.last_error()
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert seen["other"] == "null context"
+    assert _lib.last_error() == "null out_count"
+
+
+def test_exception_guard_turns_throws_into_status(tmp_path):
+    """The guard every entry point runs in (cellm_amd/csrc/api_guard.hpp):
+    std::bad_alloc becomes CELLM_HIP_ERR_OUT_OF_MEMORY, any other exception
+    CELLM_HIP_ERR_DEVICE with its message, and nothing propagates (the
+    reference catches panics at its FFI, crates/cellm-sdk/src/ffi.rs:142).
+    Built and run as a small host program."""
+    src = tmp_path / "guard.cpp"
+    src.write_text(r"""
+#include <cstdio>
+#include <stdexcept>
+#include <string>
+#include <vector>
+#include "cellm_hip.h"
+#include "api_guard.hpp"
+static cellm::ErrorSlot slot = {};
+static int32_t report(int32_t code, const char* what) { slot.store(what, strlen(what)); return code; }
+static int32_t oom() { CELLM_API_BEGIN std::vector<char> v((size_t)1 << 62); return v.empty() ? 1 : 0; CELLM_API_END(report) }
+static int32_t rt() { CELLM_API_BEGIN throw std::runtime_error("boom"); CELLM_API_END(report) }
+static int32_t other() { CELLM_API_BEGIN throw 7; CELLM_API_END(report) }
+static void vfn(int* hit) { CELLM_API_BEGIN *hit = 1; throw std::string("x"); CELLM_API_END_VOID }
+int main() {
+    char buf[64];
+    if (oom() != CELLM_HIP_ERR_OUT_OF_MEMORY) return 1;
+    if (rt() != CELLM_HIP_ERR_DEVICE) return 2;
+    slot.take(buf, sizeof buf);
+    if (std::string(buf) != "boom") return 3;
+    if (other() != CELLM_HIP_ERR_DEVICE) return 4;
+    int hit = 0;
+    vfn(&hit);
+    return hit == 1 ? 0 : 5;
+}
+""")
+    exe = tmp_path / "guard"
+    subprocess.run(["g++", "-std=c++17", f"-I{ROOT / 'include'}", f"-I{ROOT / 'cellm_amd' / 'csrc'}", str(src), "-o",
+                    str(exe)], check=True)
+    assert subprocess.run([str(exe)]).returncode == 0
+
+
+def _extern_c_bodies(path):
+    """(name, first body line) of every multi-line extern "C" definition."""
+    lines = path.read_text().split("\n")
+    out, in_c = [], False
+    for i, ln in enumerate(lines):
+        if ln.startswith('extern "C" {'):
+            in_c = True
+        elif ln.startswith('}  // extern "C"'):
+            in_c = False
+        m = re.match(r"^(?:int32_t|void|int64_t|size_t) (cellm_\w+)\(", ln) if in_c else None
+        if m and not ln.rstrip().endswith("}"):
+            j = i
+            while lines[j] != "{":
+                j += 1
+            out.append((m.group(1), lines[j + 1].strip()))
+    return out
+
+
+def test_every_entry_point_is_guarded():
+    """Every multi-line extern "C" body of the library opens with the guard."""
+    srcs = [ROOT / "cellm_amd" / "csrc" / f for f in ("capi.cpp", "cellm_file.cpp", "llama_device.cpp",
+                                                      "llama_step.cpp")]
+    bodies = [b for p in srcs for b in _extern_c_bodies(p)]
+    assert len(bodies) > 40
+    unguarded = [n for n, first in bodies if first != "CELLM_API_BEGIN"]
+    assert not unguarded, unguarded
 
 
 def test_null_out_pointers_rejected():

@@ -160,6 +160,43 @@ def test_attention_gqa_f16kv(ops, nh, nkv, hd, blocks, pos):
         assert rel_err(got[r], ref) <= 1e-5, (r, rel_err(got[r], ref))
 
 
+@pytest.mark.parametrize("nh,nkv,hd,attn_scale,cap,qmag", [
+    (8, 2, 64, 0.0625, None, 1.0),    # explicit attn_scale (kvcache.rs:752)
+    (8, 2, 64, None, 50.0, 40.0),     # soft cap 50 on scores it bends (kvcache.rs:768-770)
+    (4, 1, 128, 0.3, 2.0, 1.0),       # both; a cap that bends most scores
+])
+def test_attention_scale_and_soft_cap(ops, nh, nkv, hd, attn_scale, cap, qmag):
+    L, tpb, rows = 2, 16, 3
+    kvd = nkv * hd
+    total, k, v, bt = paged_setup(L, tpb, nkv, hd, rows, 10, 0xD00000A0 + nh)
+    pos = np.array([0, 70, 159], np.int32)
+    layer = 1
+    q = np.stack([oracle.gen_normal((nh * hd,), 0xD00000B0 + r, 0.0, qmag) for r in range(rows)]).astype(np.float32)
+    out = torch.empty((rows, nh * hd), dtype=torch.float32, device="cuda")
+    ops.encode_attention(dev(q), dev(k), dev(v), dev(bt), dev(pos), out, nh, nkv, hd, total, L, tpb, layer,
+                         attn_scale=attn_scale, soft_cap=cap)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    for r in range(rows):
+        seq = int(pos[r]) + 1
+        bases = np.array([base_of(bt[r], t, layer, L, tpb, kvd) for t in range(seq)], np.uint64)
+        ref = oracle.attention_gqa_f16kv(k, v, bases, q[r], nh, nkv, hd, attn_scale=attn_scale, soft_cap=cap)
+        assert rel_err(got[r], ref) <= 1e-5, (r, rel_err(got[r], ref))
+        if seq > 1:  # the options change the result: the test would see them dropped
+            plain = oracle.attention_gqa_f16kv(k, v, bases, q[r], nh, nkv, hd)
+            assert rel_err(plain, ref) > 1e-3
+
+
+def test_attention_rejects_bad_scale_or_cap(ops):
+    from cellm_amd._lib import CellmHipError
+
+    z = torch.zeros(64, dtype=torch.float32, device="cuda")
+    for kw in ({"attn_scale": -1.0}, {"soft_cap": float("nan")}, {"soft_cap": float("inf")}):
+        with pytest.raises(CellmHipError, match="attn_scale and soft_cap"):
+            ops.encode_attention(z, z, z, torch.zeros((1, 1), dtype=torch.int32, device="cuda"),
+                                 torch.zeros(1, dtype=torch.int32, device="cuda"), z, 1, 1, 64, 1, 1, 16, 0, **kw)
+
+
 def test_attention_rejects_unsupported_head_dim(ops):
     from cellm_amd._lib import CellmHipError
 

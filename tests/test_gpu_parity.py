@@ -200,13 +200,18 @@ def test_i8_bias_and_per_tensor_scale(ops):
     y = _run_i8(ops, w, s, x, bias=bias)
     ref = oracle.qgemv_i8(w, s, x) + bias[None, :]
     assert rel_err(y, ref) <= TOL_F32
-    # per-tensor scale: n_scales < n uses scale[0] (metal.rs:900)
+    # per-tensor scale: one scale for the tensor (metal.rs:900: the buffer does not cover every row)
     s1 = s[:1].copy()
     yt = torch.empty((2, n), dtype=torch.float32, device="cuda")
     ops.encode_qgemv_i8(_t(w), _t(s1), _t(x), yt)
     torch.cuda.synchronize()
     ref1 = oracle.qgemv_i8(w, np.full(n, s1[0], np.float32), x)
     assert rel_err(yt.cpu().numpy(), ref1) <= TOL_F32
+    # 2..n-1 scales are neither: refused instead of silently using scale[0]
+    from cellm_amd import CellmHipError
+
+    with pytest.raises(CellmHipError, match="n_scales=2"):
+        ops.encode_qgemv_i8(_t(w), _t(s[:2].copy()), _t(x), yt)
 
 
 def test_i8_ragged_k(ops):
@@ -219,13 +224,52 @@ def test_i8_ragged_k(ops):
 
 # ------------------------------------------------------------- batched / GEMM ----
 
-@pytest.mark.parametrize("m", [16, 64])
-def test_i8_batched_gemma_lm_head_slice(ops, m):
-    k, n = 1152, 8192  # slice of the 262144-row Gemma lm_head
-    w, s, x = make_i8(n, k, m, cfg=3, x_dtype=np.float16, salt=m)
-    y = _run_i8(ops, w, s, x)
+@pytest.fixture(scope="module")
+def gemma_lm_head():
+    """Config 3's int8 lm_head: W [262144, 1152] (302 MB), fp32 row scales."""
+    k, n = 1152, 262144
+    w, s, _ = make_i8(n, k, 1, cfg=3, x_dtype=np.float16, salt=200)
+    return w, s, _t(w), _t(s)
+
+
+@pytest.mark.parametrize("m", [1, 4])
+def test_i8_gemma_lm_head_full(ops, gemma_lm_head, m):
+    """The bench's config-3 lm_head at full size: M = 1 runs the 8-lane f16-x
+    decode kernel, M = 4 the batched MFMA path (>= 8192 outputs).  Every row
+    against the oracle; the greedy id of each activation row as well."""
+    import torch
+
+    w, s, wd, sd = gemma_lm_head
+    k, n = w.shape[1], w.shape[0]
+    x = oracle.gen_normal((m, k), seed(3, 2, 300 + m), 0.0, 1.0).astype(np.float16)
+    y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    ops.encode_qgemv_i8(wd, sd, _t(x), y)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
     ref = oracle.qgemv_i8(w, s, x)
-    assert rel_err(y, ref) <= TOL_F32  # int8 is exact in f16: f32-accumulation bar
+    assert rel_err(got, ref) <= TOL_F32
+    assert [int(v) for v in got.argmax(1)] == [int(v) for v in ref.argmax(1)]
+
+
+@pytest.mark.parametrize("m", [16, 64])
+def test_i8_gemma_lm_head_full_n_sampled_rows(ops, gemma_lm_head, m):
+    """M = 16 and 64 run over the full 262144 rows; the oracle checks a sample
+    of 6144 rows spread over the whole output (every tile position of the
+    persistent grid's first, middle and last rounds, plus random rows)."""
+    import torch
+
+    w, s, wd, sd = gemma_lm_head
+    k, n = w.shape[1], w.shape[0]
+    x = oracle.gen_normal((m, k), seed(3, 2, 400 + m), 0.0, 1.0).astype(np.float16)
+    y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    ops.encode_qgemv_i8(wd, sd, _t(x), y)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    rng = np.random.default_rng(m)
+    rows = np.unique(np.concatenate([np.arange(2048), np.arange(n // 2 - 1024, n // 2 + 1024), np.arange(n - 1024, n),
+                                     rng.choice(n, 1024, replace=False)]))
+    ref = oracle.qgemv_i8(np.ascontiguousarray(w[rows]), np.ascontiguousarray(s[rows]), x)
+    assert rel_err(got[:, rows], ref) <= TOL_F32
 
 
 @pytest.mark.parametrize("m,k,n", [(64, 1152, 1000), (49, 1024, 4099), (64, 704, 300), (64, 1216, 2000),
@@ -247,21 +291,42 @@ def test_q4_batched_whole_x_in_lds(ops, m, k, n, sb):
     takes the chunked form."""
     wq, s, b, x = make_q4(n, k, m, cfg=3, sb_dtype=sb, salt=m + k)
     y = _run_q4(ops, wq, s, b, x)
-    assert rel_err(y, oracle.qgemv_q4_affine(wq, s, b, x, k)) <= TOL_F16_TILE
-    w16 = oracle.f16_bits_to_f32(oracle.dequant_q4_affine_f16(wq, s, b, k))
-    assert rel_err(y, oracle.gemm_xwT(x, w16)) <= TOL_F32
+    assert rel_err(y, oracle.qgemv_q4_affine(wq, s, b, x, k)) <= TOL_F32
 
 
-@pytest.mark.parametrize("m", [16, 64])
-def test_q4_batched_gemma_mlp(ops, m):
+@pytest.mark.parametrize("m", [1, 4, 16, 64])
+def test_q4_gemma_gate_up_full_config3(ops, m):
+    """Config 3's q4 gate+up 1152 -> 13824 at every M it names, full size.
+    M = 1 takes the 16-lanes-per-row VALU kernel, M = 4 (>= 8192 outputs) and
+    16 the batched MFMA path, M = 64 its whole-X-in-LDS form.  Every path sums
+    exact q*x products in f32 and applies s and b per group: the f32 bar
+    against the reference's (q*s + b)*x order."""
     k, n = 1152, 13824
     wq, s, b, x = make_q4(n, k, m, cfg=3, salt=m)
     y = _run_q4(ops, wq, s, b, x)
-    ref32 = oracle.qgemv_q4_affine(wq, s, b, x, k)
-    assert rel_err(y, ref32) <= TOL_F16_TILE
-    w16 = oracle.f16_bits_to_f32(oracle.dequant_q4_affine_f16(wq, s, b, k))
-    ref16 = oracle.gemm_xwT(x, w16)
-    assert rel_err(y, ref16) <= TOL_F32
+    assert rel_err(y, oracle.qgemv_q4_affine(wq, s, b, x, k)) <= TOL_F32
+
+
+@pytest.mark.parametrize("m,sb,lo,hi", [
+    (4, np.float32, 1e-4, 1e-3),     # f32 scales and biases, as convert_lfm.py writes them (lfm.rs:1003-1004)
+    (16, np.float16, 1e-4, 1e-3),    # f16 scales below 1e-3: s/16 would be an f16 subnormal
+    (64, "bf16", 2e-5, 1e-3),
+    (7, np.float32, 1e-4, 1e-3),
+])
+def test_q4_batched_small_scales(ops, m, sb, lo, hi):
+    """Batched decode with small group scales: the MFMA path multiplies exact
+    q values and applies s, b in f32, so small scales lose nothing."""
+    k, n = 1152, 9000
+    wq, _, b, x = make_q4(n, k, m, cfg=3, sb_dtype=np.float32, salt=m + 100)
+    s = oracle.gen_uniform(b.shape, seed(3, 7, m), lo, hi)
+    b = (b * np.float32(hi / 0.05)).astype(np.float32)  # biases of the same order as the scales
+    if sb == np.float16:
+        s, b = s.astype(np.float16), b.astype(np.float16)
+    elif sb == "bf16":
+        s = (s.view(np.uint32) >> 16).astype(np.uint16)
+        b = (b.view(np.uint32) >> 16).astype(np.uint16)
+    y = _run_q4(ops, wq, s, b, x)
+    assert rel_err(y, oracle.qgemv_q4_affine(wq, s, b, x, k)) <= TOL_F32
 
 
 @pytest.mark.parametrize("m", [2, 3, 7, 33])
@@ -282,9 +347,16 @@ def test_q4_batched_mfma_k_chunks(ops, m, k, n):
     rows take the MFMA path only for >= 8192 outputs."""
     wq, s, b, x = make_q4(n, k, m, cfg=3, salt=m)
     y = _run_q4(ops, wq, s, b, x)
-    assert rel_err(y, oracle.qgemv_q4_affine(wq, s, b, x, k)) <= TOL_F16_TILE
-    w16 = oracle.f16_bits_to_f32(oracle.dequant_q4_affine_f16(wq, s, b, k))
-    assert rel_err(y, oracle.gemm_xwT(x, w16)) <= TOL_F32
+    assert rel_err(y, oracle.qgemv_q4_affine(wq, s, b, x, k)) <= TOL_F32
+
+
+@pytest.mark.parametrize("m,group", [(8, 128), (20, 256), (4, 128)])
+def test_q4_batched_mfma_groups_of_128_and_up(ops, m, group):
+    """Groups of 128 and more: one group per K block, no lane exchange."""
+    k, n = 1024, 8448
+    wq, s, b, x = make_q4(n, k, m, cfg=3, group=group, salt=m + group)
+    y = _run_q4(ops, wq, s, b, x, group=group)
+    assert rel_err(y, oracle.qgemv_q4_affine(wq, s, b, x, k, gs=group)) <= TOL_F32
 
 
 @pytest.mark.parametrize("k,n", [(896, 4864), (4864, 896)])

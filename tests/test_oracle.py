@@ -334,6 +334,99 @@ def test_softmax_attention_argmax():
     assert g[0] == 0.0 and np.isclose(g[1], 2.0 / (1.0 + np.exp(-1.0)))
 
 
+def test_bf16_to_f32_exhaustive():
+    """All 65536 bf16 patterns against torch's bfloat16 -> float32 (a library
+    conversion built independently of the oracle's shift).  NaNs keep sign and
+    payload; ctypes' float return passes through a double, which sets the
+    quiet bit of a signalling NaN, so that bit is compared as set."""
+    import torch
+
+    bits = np.arange(65536, dtype=np.uint16)
+    L = oracle.lib()
+    ours = np.array([L.oracle_bf16_to_f32(int(b)) for b in bits], np.float32).view(np.uint32)
+    ref = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).to(torch.float32).numpy().view(np.uint32)
+    nan = np.isnan(ref.view(np.float32))
+    assert nan.sum() == 2 * 127
+    assert np.array_equal(ours[~nan], ref[~nan])
+    assert np.array_equal(ours[nan], ref[nan] | np.uint32(0x00400000))
+    ours = ours.view(np.float32)
+    # the byte order a wrong shift or a truncating f16 path would break
+    assert ours[0x3F80] == 1.0 and ours[0xBF80] == -1.0 and ours[0x4049] == np.float32(3.140625)
+
+
+def _attention_f64(k, v, q, nh, nkv, hd, scale, cap=None):
+    """Softmax attention in float64 from the widened f16 K/V rows [seq, nkv*hd]."""
+    g = nh // nkv
+    out = np.zeros((nh, hd))
+    for h in range(nh):
+        kv = h // g
+        kh = k[:, kv * hd:(kv + 1) * hd].astype(np.float64)
+        vh = v[:, kv * hd:(kv + 1) * hd].astype(np.float64)
+        sc = kh @ q[h * hd:(h + 1) * hd].astype(np.float64) * scale
+        if cap is not None:
+            sc = np.tanh(sc / cap) * cap
+        w = np.exp(sc - sc.max())
+        out[h] = (w / w.sum()) @ vh
+    return out.reshape(-1)
+
+
+@pytest.mark.parametrize("seq,nh,nkv,hd,attn_scale,cap,qmag", [
+    (37, 4, 2, 64, None, None, 2.0),
+    (300, 15, 5, 64, None, None, 2.0),     # SmolLM2-360M heads
+    (129, 8, 1, 128, 0.0625, None, 2.0),   # explicit attn_scale (Some(s), kvcache.rs:752)
+    (64, 4, 4, 64, None, 50.0, 60.0),      # a soft cap of 50 (kvcache.rs:768-770) on scores it bends
+    (64, 4, 4, 64, 0.3, 2.0, 1.0),         # a cap that bends most scores
+])
+def test_attention_multi_token_fp64_bound(seq, nh, nkv, hd, attn_scale, cap, qmag):
+    """Many positions with unequal scores against float64 softmax attention,
+    within a forward error bound of the f32 arithmetic:
+      |ds| <= scale * gamma_hd * max_t sum|q k_t| + rounding of the scale/cap,
+      |out - ref| <= max|v| * (2|ds| + 2 gamma_seq + 8u), times 2.
+    A wrong 1/sqrt(hd), a missing cap, or a wrong kv-head mapping moves the
+    weights by O(1) and is checked to fail that bound by far."""
+    rng = np.random.default_rng(seq + nh + hd)
+    kvd = nkv * hd
+    k = rng.standard_normal((seq, kvd)).astype(np.float16)
+    v = rng.standard_normal((seq, kvd)).astype(np.float16)
+    q = (qmag * rng.standard_normal(nh * hd)).astype(np.float32)
+    bases = np.arange(seq, dtype=np.uint64) * kvd
+    out = oracle.attention_gqa_f16kv(k.view(np.uint16).ravel(), v.view(np.uint16).ravel(), bases, q, nh, nkv, hd,
+                                     attn_scale=attn_scale, soft_cap=cap)
+    scale = attn_scale if attn_scale is not None else float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+    ref = _attention_f64(k, v, q, nh, nkv, hd, scale, cap)
+    g = nh // nkv
+    qk = max(float(np.max(np.abs(k[:, (h // g) * hd:(h // g + 1) * hd]).astype(np.float64) @
+                      np.abs(q[h * hd:(h + 1) * hd]).astype(np.float64))) for h in range(nh))
+    ds = scale * gamma(hd) * qk + 4 * U * scale * qk + (4 * U * cap if cap else 0.0)
+    bound = 2 * float(np.max(np.abs(v.astype(np.float64)))) * (2 * ds + 2 * gamma(seq) + 8 * U)
+    err = float(np.max(np.abs(out.astype(np.float64) - ref)))
+    assert err <= bound, (err, bound)
+    # the plausible mistakes are far outside the bound
+    wrong = [_attention_f64(k, v, q, nh, nkv, hd, 1.0 / hd, cap),
+             _attention_f64(k, v, q, nh, nkv, hd, scale, None if cap else 1.0)]
+    if nkv > 1:
+        wrong.append(_attention_f64(k, v, q, nh, nkv, hd, scale, cap)[::-1].copy())
+    for w in wrong:
+        assert float(np.max(np.abs(out - w))) > 20 * bound
+
+
+def test_qgemv_i4_sym_rows_equal_matmul_i4():
+    """The batched i4 form is matmul_i4_f32 (cpu_kernels.rs:219-243) per
+    activation row, bit for bit, with f32 x and with f16 x widened exactly;
+    per-row (gs = K) and per-group scales; odd K."""
+    rng = np.random.default_rng(44)
+    for n, k, gs in ((7, 256, 256), (5, 192, 64), (3, 37, 37), (4, 100, 32)):
+        w = rng.integers(0, 256, (n, (k + 1) // 2)).astype(np.uint8)
+        spr = (k + gs - 1) // gs
+        s = rng.uniform(1e-3, 2e-2, n * spr).astype(np.float16).view(np.uint16)
+        for xdt in (np.float32, np.float16):
+            x = rng.standard_normal((3, k)).astype(xdt)
+            y = oracle.qgemv_i4_sym(w, s, gs, x, n, k)
+            for r in range(3):
+                ref = oracle.matmul_i4_f32(w, s, n, k, gs, x[r].astype(np.float32))
+                assert np.array_equal(y[r].view(np.uint32), ref.view(np.uint32)), (n, k, gs, xdt, r)
+
+
 # ------------------------------------------------------- f16, i2, q1_0_g128 ----
 
 def test_f16_gemv_known_answer_and_sequential_order():
