@@ -100,6 +100,7 @@ struct cellm_hip_ctx {
     std::unordered_map<hipStream_t, DeviceBuffer> workspaces;  // split-K partials, one per stream
     std::unordered_map<hipStream_t, DeviceBuffer> aux;         // unfused gate/up: the up rows, one per stream
     std::unordered_map<hipStream_t, DeviceBuffer> attn;        // split-sequence attention partials, one per stream
+    float* attn_static = nullptr;  // this device's static attention scratch (cellm_hip_attention_gqa_f16kv_noalloc)
 };
 
 namespace {
@@ -490,6 +491,13 @@ int32_t cellm_hip_create(int32_t device, cellm_hip_ctx_t** out_ctx)
     if (e != hipSuccess) {
         delete ctx;
         return hip_error(e, "hipStreamCreate");
+    }
+    // the device address of the static attention scratch, with the device current
+    e = attention_static_scratch(&ctx->attn_static);
+    if (e != hipSuccess) {
+        (void)hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return hip_error(e, "hipGetSymbolAddress(attention scratch)");
     }
     *out_ctx = ctx;
     return CELLM_HIP_OK;
@@ -884,6 +892,50 @@ int32_t check_paged(int64_t rows, int64_t max_blocks, int64_t total_blocks, int6
     return CELLM_HIP_OK;
 }
 
+// Shared by cellm_hip_attention_gqa_f16kv (softmax partials in the context's
+// per-stream scratch, grown on demand) and its _noalloc variant (the library's
+// static scratch; nothing is allocated).
+int32_t attention_impl(cellm_hip_ctx* ctx, const float* q, const uint16_t* kcache, const uint16_t* vcache,
+                       const uint32_t* block_tables, int64_t max_blocks, int64_t total_blocks, const int32_t* positions,
+                       int64_t rows, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, int64_t n_layers,
+                       int64_t tokens_per_block, int64_t layer, float attn_scale, float soft_cap, float* out,
+                       hipStream_t st, bool static_scratch)
+{
+    if (int32_t rc = check_paged(rows, max_blocks, total_blocks, n_layers, tokens_per_block, layer)) return rc;
+    if (n_heads < 1 || n_kv_heads < 1 || head_dim < 1 || n_heads > 4096 ||
+        !attention_supported((int)n_heads, (int)n_kv_heads, (int)head_dim, (int)(max_blocks * tokens_per_block)))
+        return set_error(CELLM_HIP_ERR_UNSUPPORTED,
+                         "attention needs n_heads %% n_kv_heads == 0, <= 8 query heads per kv head, head_dim 64 or "
+                         "128 and max_blocks * tokens_per_block <= 32768 (got %lld/%lld/%lld, %lld positions)",
+                         (long long)n_heads, (long long)n_kv_heads, (long long)head_dim,
+                         (long long)(max_blocks * tokens_per_block));
+    if (!(attn_scale >= 0.0f) || !(soft_cap >= 0.0f) || std::isinf(attn_scale) || std::isinf(soft_cap))
+        return set_error(CELLM_HIP_ERR_INVALID_ARG, "attn_scale and soft_cap must be finite and >= 0 (0 = none)");
+    const size_t need = attention_workspace_bytes((int)rows, (int)n_heads, (int)n_kv_heads, (int)head_dim,
+                                                  (int)(max_blocks * tokens_per_block));
+    if (static_scratch && need > kAttnStaticScratchBytes)
+        return set_error(CELLM_HIP_ERR_INVALID_ARG,
+                         "attention_noalloc: %zu bytes of softmax partials (rows x heads x ceil(max_blocks * "
+                         "tokens_per_block / 64) x (head_dim + 2) floats) exceed the static scratch of %zu bytes",
+                         need, kAttnStaticScratchBytes);
+    if (rows == 0) return CELLM_HIP_OK;
+    if (!q || !kcache || !vcache || !block_tables || !positions || !out)
+        return set_error(CELLM_HIP_ERR_INVALID_ARG, "null pointer");
+    if (!aligned16(kcache) || !aligned16(vcache)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "K/V must be 16-byte aligned");
+    float* ws = nullptr;
+    if (static_scratch) {
+        ws = ctx->attn_static;
+        if (!ws) return set_error(CELLM_HIP_ERR_DEVICE, "static attention scratch has no device address");
+    } else if (int32_t rc = get_stream_buffer(ctx, ctx->attn, st, need, &ws)) {
+        return rc;
+    }
+    HIP_TRY(launch_attention_gqa_f16kv(q, kcache, vcache, block_tables, (int)max_blocks, (int)total_blocks, positions,
+                                       (int)rows, (int)n_heads, (int)n_kv_heads, (int)head_dim, (int)n_layers,
+                                       (int)tokens_per_block, (int)layer, attn_scale, soft_cap, out, ws, st),
+            "attention launch");
+    return CELLM_HIP_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1081,32 +1133,27 @@ int32_t cellm_hip_attention_gqa_f16kv(cellm_hip_ctx_t* ctx, const float* q, cons
 {
     CELLM_API_BEGIN
     if (int32_t rc = check_ctx(ctx)) return rc;
-    if (int32_t rc = check_paged(rows, max_blocks, total_blocks, n_layers, tokens_per_block, layer)) return rc;
-    if (n_heads < 1 || n_kv_heads < 1 || head_dim < 1 || n_heads > 4096 ||
-        !attention_supported((int)n_heads, (int)n_kv_heads, (int)head_dim, (int)(max_blocks * tokens_per_block)))
-        return set_error(CELLM_HIP_ERR_UNSUPPORTED,
-                         "attention needs n_heads %% n_kv_heads == 0, <= 8 query heads per kv head, head_dim 64 or "
-                         "128 and max_blocks * tokens_per_block <= 32768 (got %lld/%lld/%lld, %lld positions)",
-                         (long long)n_heads, (long long)n_kv_heads, (long long)head_dim,
-                         (long long)(max_blocks * tokens_per_block));
-    if (!(attn_scale >= 0.0f) || !(soft_cap >= 0.0f) || std::isinf(attn_scale) || std::isinf(soft_cap))
-        return set_error(CELLM_HIP_ERR_INVALID_ARG, "attn_scale and soft_cap must be finite and >= 0 (0 = none)");
-    if (rows == 0) return CELLM_HIP_OK;
-    if (!q || !kcache || !vcache || !block_tables || !positions || !out)
-        return set_error(CELLM_HIP_ERR_INVALID_ARG, "null pointer");
-    if (!aligned16(kcache) || !aligned16(vcache)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "K/V must be 16-byte aligned");
     DeviceGuard g(ctx->device);
     const std::lock_guard<std::recursive_mutex> lk(ctx->mu);  // held until the scratch users are enqueued
-    const hipStream_t st = pick_stream(ctx, stream);
-    float* ws = nullptr;
-    const size_t need = attention_workspace_bytes((int)rows, (int)n_heads, (int)n_kv_heads, (int)head_dim,
-                                                  (int)(max_blocks * tokens_per_block));
-    if (int32_t rc = get_stream_buffer(ctx, ctx->attn, st, need, &ws)) return rc;
-    HIP_TRY(launch_attention_gqa_f16kv(q, kcache, vcache, block_tables, (int)max_blocks, (int)total_blocks, positions,
-                                       (int)rows, (int)n_heads, (int)n_kv_heads, (int)head_dim, (int)n_layers,
-                                       (int)tokens_per_block, (int)layer, attn_scale, soft_cap, out, ws, st),
-            "attention launch");
-    return CELLM_HIP_OK;
+    return attention_impl(ctx, q, kcache, vcache, block_tables, max_blocks, total_blocks, positions, rows, n_heads,
+                          n_kv_heads, head_dim, n_layers, tokens_per_block, layer, attn_scale, soft_cap, out,
+                          pick_stream(ctx, stream), false);
+    CELLM_API_END(report_exception)
+}
+
+int32_t cellm_hip_attention_gqa_f16kv_noalloc(cellm_hip_ctx_t* ctx, const float* q, const uint16_t* kcache,
+                                              const uint16_t* vcache, const uint32_t* block_tables,
+                                              int64_t max_blocks, int64_t total_blocks, const int32_t* positions,
+                                              int64_t rows, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
+                                              int64_t n_layers, int64_t tokens_per_block, int64_t layer,
+                                              float attn_scale, float soft_cap, float* out, void* stream)
+{
+    CELLM_API_BEGIN
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    DeviceGuard g(ctx->device);
+    return attention_impl(ctx, q, kcache, vcache, block_tables, max_blocks, total_blocks, positions, rows, n_heads,
+                          n_kv_heads, head_dim, n_layers, tokens_per_block, layer, attn_scale, soft_cap, out,
+                          pick_stream(ctx, stream), true);
     CELLM_API_END(report_exception)
 }
 

@@ -25,7 +25,10 @@
 //   base(t, layer) = block[t / tpb] * (L * tpb * kvd) + layer * (tpb * kvd) + (t % tpb) * kvd
 #include <algorithm>
 #include <cmath>
+#include <mutex>
 #include <type_traits>
+#include <utility>
+#include <vector>
 
 #include "common.hpp"
 #include "kernels.hpp"
@@ -902,6 +905,35 @@ hipError_t launch_attention_gqa_f16kv(const float* q, const uint16_t* kcache, co
     else
         by_g(std::integral_constant<int, 128>{});
     return hipGetLastError();
+}
+
+// ---- allocation-free attention scratch ---------------------------------------
+// The softmax partials of the split-sequence attention, for callers that cannot
+// allocate (HIP graph capture, serving loops): a fixed device array that every
+// GPU the library runs on holds until the process ends.  Host code never uses
+// the array's name as an address (in host code it is a stand-in, not device
+// memory): the device address comes from hipGetSymbolAddress, once per device.
+static __device__ __align__(256) float scratch[kAttnStaticScratchBytes / sizeof(float)];
+
+hipError_t attention_static_scratch(float** out)
+{
+    static std::mutex mu;
+    static std::vector<std::pair<int, float*>> per_device;  // (device, address of its copy)
+    *out = nullptr;
+    int dev = 0;
+    if (hipError_t e = hipGetDevice(&dev); e != hipSuccess) return e;
+    const std::lock_guard<std::mutex> lk(mu);
+    for (const auto& d : per_device)
+        if (d.first == dev) {
+            *out = d.second;
+            return hipSuccess;
+        }
+    void* p = nullptr;
+    if (hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)); e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    per_device.emplace_back(dev, static_cast<float*>(p));
+    *out = static_cast<float*>(p);
+    return hipSuccess;
 }
 
 // Host-side geometry of the fused decode GEMVs: LPR = 64 lanes per row pair

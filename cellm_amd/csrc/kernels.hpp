@@ -92,6 +92,10 @@ hipError_t launch_attention_gqa_f16kv(const float* q, const uint16_t* kcache, co
                                       int n_layers, int tokens_per_block, int layer, float attn_scale,
                                       float soft_cap, float* out, float* workspace, hipStream_t st);
 hipError_t launch_argmax(const float* logits, int rows, int n, int32_t* idx, float* val, hipStream_t st);
+// Size of the static attention scratch (decode.hip) and the current device's
+// address of it (hipGetSymbolAddress once per device, cached).
+constexpr size_t kAttnStaticScratchBytes = (size_t)8 << 20;
+hipError_t attention_static_scratch(float** out);
 // Fused decode-step GEMVs (decode.hip): residual add + RMSNorm prologue, int8
 // GEMV of two rows per team, RoPE + K/V write or SiLU * up epilogue.
 bool decode_fused_supported(int rows, int H);

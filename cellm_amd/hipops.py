@@ -407,6 +407,20 @@ class HipOps:
                                                       0.0 if soft_cap is None else soft_cap, _dev_ptr(out),
                                                       _stream_ptr(stream)))
 
+    def encode_attention_noalloc(self, q, kcache, vcache, block_tables, positions_i32, out, n_heads: int,
+                                 n_kv_heads: int, head_dim: int, total_blocks: int, n_layers: int,
+                                 tokens_per_block: int, layer: int, attn_scale: float | None = None,
+                                 soft_cap: float | None = None, stream=None) -> None:
+        """encode_attention with its partials in the library's static device
+        scratch (8 MiB per GPU): allocates nothing; overlapping calls on one
+        GPU race."""
+        rows = positions_i32.numel()
+        check(self._lib.cellm_hip_attention_gqa_f16kv_noalloc(
+            self._h, _dev_ptr(q), _dev_ptr(kcache), _dev_ptr(vcache), _dev_ptr(block_tables), block_tables.shape[-1],
+            total_blocks, _dev_ptr(positions_i32), rows, n_heads, n_kv_heads, head_dim, n_layers, tokens_per_block,
+            layer, 0.0 if attn_scale is None else attn_scale, 0.0 if soft_cap is None else soft_cap, _dev_ptr(out),
+            _stream_ptr(stream)))
+
     def encode_add_inplace(self, x, y, stream=None) -> None:
         check(self._lib.cellm_hip_add_f32_inplace(self._h, _dev_ptr(x), _dev_ptr(y), x.numel(), _stream_ptr(stream)))
 

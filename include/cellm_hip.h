@@ -366,6 +366,23 @@ int32_t cellm_hip_attention_gqa_f16kv(cellm_hip_ctx_t* ctx, const float* q, cons
                                       int64_t n_kv_heads, int64_t head_dim, int64_t n_layers, int64_t tokens_per_block,
                                       int64_t layer, float attn_scale, float soft_cap, float* out, void* stream);
 
+/* cellm_hip_attention_gqa_f16kv without any allocation, for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * Same arguments and results; the softmax partials go to a static device
+ * array of 8 MiB that each GPU holds until the process ends, so calls whose
+ * partials need more -- rows * n_heads * ceil(max_blocks * tokens_per_block /
+ * 64) * (head_dim + 2) * 4 bytes -- fail with CELLM_HIP_ERR_INVALID_ARG.
+ * Every call on one GPU shares that array: calls that overlap on one GPU
+ * (other streams, other contexts, other threads) race and must be serialised
+ * by the caller. */
+int32_t cellm_hip_attention_gqa_f16kv_noalloc(cellm_hip_ctx_t* ctx, const float* q, const uint16_t* kcache,
+                                              const uint16_t* vcache, const uint32_t* block_tables,
+                                              int64_t max_blocks, int64_t total_blocks, const int32_t* positions,
+                                              int64_t rows, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim,
+                                              int64_t n_layers, int64_t tokens_per_block, int64_t layer,
+                                              float attn_scale, float soft_cap, float* out, void* stream);
+
 /* MetalOps::encode_add_f32_inplace: x[i] += y[i]. */
 int32_t cellm_hip_add_f32_inplace(cellm_hip_ctx_t* ctx, float* x, const float* y, int64_t n, void* stream);
 
