@@ -264,6 +264,8 @@ def extra_configs(torch, ops, stream, gen, graphs: bool = True):
     res["hbm_copy_512MiB"] = {"us": round(ms * 1e3, 1), "GB/s_read_plus_write": round(2 * nbytes / (ms * 1e-3) / 1e9, 1)}
     del src, dst
 
+    res.update(launch_floor(torch, ops, stream))
+
     # SmolLM2-135M int8, fp32 scale, fp32 x, K=576
     for n in (576, 1536):
         k = 576
@@ -319,6 +321,45 @@ def extra_configs(torch, ops, stream, gen, graphs: bool = True):
         tflops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
         res[f"cfg4_qgemm_m512_{k}x{n}"] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tflops, 1),
                                            "frac_mfma_f16": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
+    return res
+
+
+def launch_floor(torch, ops, stream):
+    """The box's floor for one dependent kernel launch, against which the
+    small decode shapes are judged launch-bound:
+      * eager: 200 back-to-back launches of the smallest int8 GEMV (M=1,
+        16x64, one block) from one cellm_hip_qgemv_batch call, as the bench
+        step issues its projections;
+      * graph: 200 single-block elementwise launches (cellm_hip_add_f32_inplace
+        on 64 floats) captured in a HIP graph and replayed.
+    Both per launch, HIP events on the stream."""
+    res = {}
+    w = torch.zeros((16, 64), dtype=torch.int8, device="cuda")
+    s = torch.ones((16,), dtype=torch.float32, device="cuda")
+    x = torch.zeros((1, 64), dtype=torch.float32, device="cuda")
+    y = torch.empty((1, 16), dtype=torch.float32, device="cuda")
+    arr = op_array([ops.qgemv_op_i8(w, s, x, y) for _ in range(200)])
+    res["launch_floor_eager_us"] = round(time_batch(torch, ops, arr, stream) * 1e3, 3)
+    a = torch.zeros(64, dtype=torch.float32, device="cuda")
+    b = torch.zeros(64, dtype=torch.float32, device="cuda")
+    cap = torch.cuda.Stream()
+    with torch.cuda.stream(cap):
+        ops.encode_add_inplace(a, b, stream=cap.cuda_stream)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=cap):
+        for _ in range(200):
+            ops.encode_add_inplace(a, b, stream=cap.cuda_stream)
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(5):
+        g.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    res["launch_floor_graph_us"] = round(e0.elapsed_time(e1) / 1000 * 1e3, 3)
+    del g
     return res
 
 

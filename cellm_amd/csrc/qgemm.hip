@@ -328,50 +328,6 @@ constexpr int kRegStageBytes = kStageHalves * 2 + kRawStepBytes;    // 40 KB
 constexpr size_t kRegFixedLds = (size_t)kRegStages * kRegStageBytes;
 constexpr size_t kRegExchangeBytes = 8 * 2 * 16 * 64 * 4;  // k-half exchange after the loop (64 KB)
 
-// v_cvt_f32_ubyteN: byte N of a register to f32.  Spelled out because the compiler folds
-// (float)((x >> 8N) & 0xFF) of a masked word back into one v_bfe_u32 per nibble plus a convert.
-template <int N>
-__device__ __forceinline__ float cvt_ubyte(uint32_t x)
-{
-    float f;
-    if constexpr (N == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(f) : "v"(x));
-    else if constexpr (N == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(f) : "v"(x));
-    else if constexpr (N == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(f) : "v"(x));
-    else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(f) : "v"(x));
-    return f;
-}
-
-template <int SBT>
-__device__ __forceinline__ h8_t dequant_word_bytes(uint32_t w, float s, float b)
-{
-    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
-    const float q[8] = {cvt_ubyte<0>(lo), cvt_ubyte<0>(hi), cvt_ubyte<1>(lo), cvt_ubyte<1>(hi),
-                        cvt_ubyte<2>(lo), cvt_ubyte<2>(hi), cvt_ubyte<3>(lo), cvt_ubyte<3>(hi)};
-    float v[8];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float q0 = q[2 * i], q1 = q[2 * i + 1];  // nibbles 2i, 2i + 1
-        if constexpr (SBT == DT_F32) {
-#pragma clang fp contract(off)
-            const float t0 = q0 * s, t1 = q1 * s;
-            v[2 * i] = t0 + b;
-            v[2 * i + 1] = t1 + b;
-        } else {
-            v[2 * i] = __builtin_fmaf(q0, s, b);  // q*s exact: same bits as mul-then-add
-            v[2 * i + 1] = __builtin_fmaf(q1, s, b);
-        }
-    }
-    h8_t h;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        // Keep the f32 rounding (no fused v_fma_mix*_f16 with a single rounding).  Not volatile: a
-        // volatile asm is a scheduling barrier.
-        asm("" : "+v"(v[k]));
-        h[k] = (_Float16)v[k];
-    }
-    return h;
-}
-
 template <int SBT>
 __global__ __launch_bounds__(kRegThreads) void qgemm_q4_regw_kernel(const uint32_t* __restrict__ W,
                                                                    const void* __restrict__ S,

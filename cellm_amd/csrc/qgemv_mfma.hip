@@ -18,27 +18,21 @@
 //   q4:   32 weights (one group), k = kb + 32g .. +32, four k-steps.
 // The MFMA contracts over whatever k each slot carries as long as A and B
 // agree, so X is staged in LDS per 8-k word in the order the unpacked weight
-// pairs come out (int8: 0,2,1,3,4,6,5,7; q4: 0,4,1,5,2,6,3,7).
+// pairs come out (int8: 0,2,1,3,4,6,5,7; q4: natural order).
 //
-// B operands:
+// Dequant into the f16 B operand:
 //   int8: u8 = w ^ 0x80 is exact in f16 as (1152 + w) - 1152 (v_and_or_b32 +
 //         v_pk_add_f16), so products are exact and the result differs from
 //         the reference only by summation order; the row scale is applied
 //         after the sum, as in the reference.
-//   q4:   the exact nibble values q (magic 0x6400 trick, pk_add), never
-//         q*s + b in f16.  Each MFMA k-step covers one quantization group, so
-//         the group's MFMA sum P = sum q x (exact products, f32 sums) is folded
-//         into the accumulator in f32 as  acc += s * P + b * X,  X = sum x over
-//         the group (summed per group while X is staged).  That is the
-//         reference's sum of (q*s + b) * x regrouped, with f32 roundings only,
-//         as the M = 1 VALU kernel computes it.  For group 64 a lane's 32
-//         nibbles span half a group and a K block holds two groups; two
-//         v_permlane32_swap per block trade words 2,3 of the low half-wave with
-//         words 0,1 of the high half (same weight row, lanes l and l + 32) so
-//         that k-steps 0,1 see only group 0 and 2,3 only group 1.
+//   q4:   the converter's tile value RNE_f16(f32(q)*s + b)
+//         (tools/convert/src/main.rs:4435-4436): q*s + b in f32 with the
+//         group's scale and bias as stored (f32 scales: product and sum
+//         rounded apart), then one rounding to f16.  The fp16-tile tolerance
+//         of the MFMA paths applies; the tiles are exactly the ones the
+//         prefill qGEMM and the oracle's f16 dequant produce.
 #include <algorithm>
 #include <mutex>
-#include <type_traits>
 #include <vector>
 
 #include "common.hpp"
@@ -56,7 +50,7 @@ template <int WT>
 __device__ __forceinline__ h8_t permute_word(h8_t v)
 {
     if constexpr (WT == 1) return h8_t{v[0], v[2], v[1], v[3], v[4], v[6], v[5], v[7]};
-    else return h8_t{v[0], v[4], v[1], v[5], v[2], v[6], v[3], v[7]};
+    else return v;  // q4 tiles come out in natural order
 }
 
 // int8 word pair (8 weights) -> f16 x8 in order 0,2,1,3,4,6,5,7 (exact).
@@ -70,61 +64,6 @@ __device__ __forceinline__ h8_t i8x8_to_f16(uint32_t w0, uint32_t w1)
     const h2_t a2 = as_h2(and_or(b1, mlo, magic)) - off;       // (w4, w6)
     const h2_t a3 = as_h2(and_or(b1 >> 8, mlo, magic)) - off;  // (w5, w7)
     return h8_t{a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
-}
-
-// q4 word (8 nibbles) -> the exact values q as f16 x8 in order 0,4,1,5,2,6,3,7.
-__device__ __forceinline__ h8_t q4_exact_f16(uint32_t w)
-{
-    const uint32_t m0f = 0x000F000Fu, magic = 0x64006400u;
-    const h2_t off = {(_Float16)1024.0f, (_Float16)1024.0f};
-    const h2_t q04 = as_h2(and_or(w, m0f, magic)) - off;          // (q0, q4)
-    const h2_t q15 = as_h2(and_or(w >> 4, m0f, magic)) - off;     // (q1, q5)
-    const h2_t q26 = as_h2(and_or(w >> 8, m0f, magic)) - off;     // (q2, q6)
-    const h2_t q37 = as_h2(and_or(w >> 12, m0f, magic)) - off;    // (q3, q7)
-    return h8_t{q04[0], q04[1], q15[0], q15[1], q26[0], q26[1], q37[0], q37[1]};
-}
-
-// Raw bits of two consecutive scale (or bias) elements i, i + 1 (i even, so
-// the pair is aligned): one 32-bit load for f16/bf16, a 64-bit one for f32.
-template <int DT>
-struct RawPair {
-    using type = typename std::conditional<DT == DT_F32, u2_t, uint32_t>::type;
-};
-template <int DT>
-__device__ __forceinline__ typename RawPair<DT>::type load_raw_pair(const void* p, size_t i)
-{
-    return *reinterpret_cast<const typename RawPair<DT>::type*>(reinterpret_cast<const char*>(p) +
-                                                                i * (DT == DT_F32 ? 4 : 2));
-}
-template <int DT>
-__device__ __forceinline__ float raw_pair_f32(typename RawPair<DT>::type r, int j)
-{
-    if constexpr (DT == DT_F32) {
-        // the element goes through a scalar first: hipcc (ROCm 7.2) compiles a
-        // __builtin_bit_cast of a vector element r[1] as a read of r[0]
-        const uint32_t u = j ? r[1] : r[0];
-        return __builtin_bit_cast(float, u);
-    } else {
-        return raw_to_f32<DT>(j ? r >> 16 : r & 0xffffu);
-    }
-}
-
-// Column of the staged X (relative to the K block) that k-step st of slot
-// group g reads.  Without the group-64 exchange: the lane's own chunk,
-// 32 g + 8 st.  With it (see the header): steps 0,1 carry group 0 and 2,3
-// group 1; the low half-wave (g < 2) holds words 0,1 of chunks g and g + 2,
-// the high half words 2,3 of chunks g - 2 and g.
-template <bool G64>
-__device__ __forceinline__ int q4_step_col(int st, int g)
-{
-    if constexpr (!G64) {
-        return 32 * g + 8 * st;
-    } else {
-        const int hg = st >> 1, sub = st & 1;
-        const bool low = g < 2;
-        const int c = (low ? g : g - 2) + 2 * hg;
-        return 32 * c + 8 * (low ? sub : 2 + sub);
-    }
 }
 
 // Persistent streaming kernel.  WT: 0 = q4 affine, 1 = int8.  MS = 16-row
@@ -144,21 +83,17 @@ __device__ __forceinline__ int q4_step_col(int st, int g)
 // CU (8-16 per CU), so no cross-iteration register ring is needed -- the
 // compiler counts outstanding loads exactly only through straight-line code,
 // and a ring that crosses tile boundaries would wait on every load anyway.
-template <int WT, int MS, int NT, int DEPTH, int SBT, bool CHUNKED, int BT = kBlock, bool G64 = false>
+template <int WT, int MS, int NT, int DEPTH, int SBT, bool CHUNKED, int BT = kBlock>
 __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
     const void* __restrict__ W, const void* __restrict__ S, const void* __restrict__ Bz, int per_channel, int gshift,
     const _Float16* __restrict__ X, const float* __restrict__ bias, float* __restrict__ Y, int M, int N, int K, int KC,
     int ntiles)
 {
-    extern __shared__ __align__(16) _Float16 xs[];  // [MS*16][KC + 8], then (q4) sxs
+    extern __shared__ __align__(16) _Float16 xs[];  // [MS*16][KC + 8]
     constexpr int KB = WT == 1 ? 64 : 128;  // K per block: 64 bytes of every row
     constexpr int TSTEPS = KB / 32;         // MFMA k-steps per block
     constexpr int ROWS = (BT / 64) * NT * 16;
-    constexpr int FPB = G64 ? 2 : 1;        // q4: groups (folds) per K block
-    constexpr int SEG = KB / FPB;           // q4: columns per fold
     const int stride = KC + 8;
-    // q4: sxs[KC / SEG][MS * 16] = sum of the staged x over each fold's columns
-    float* sxs = reinterpret_cast<float*>(xs + (size_t)MS * 16 * stride);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int rl = lane & 15, g = lane >> 4;
     const int nkb = K / KB;
@@ -168,9 +103,7 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
     const int row_in_tile = wave * NT * 16 + rl;
 
     // ---- X staging: columns [k0, k0 + kcl) in unpack order, rows >= M zero.
-    // Loads are unconditional (clamped) so they issue back to back.  q4: the
-    // SEG / 8 neighbouring lanes that hold one fold's words also sum them
-    // (f32, a fixed tree) into sxs.
+    // Loads are unconditional (clamped) so they issue back to back.
     auto stage = [&](int k0, int kcl) {
         const int words = kcl >> 3, total = MS * 16 * words;
         for (int base = threadIdx.x; base < total; base += 4 * BT) {
@@ -189,15 +122,6 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
                 if (idx < total)
                     *reinterpret_cast<h8_t*>(xs + (size_t)m * stride + wd * 8) =
                         permute_word<WT>(__builtin_bit_cast(h8_t, v));
-                if constexpr (WT == 0) {
-                    // idx runs over whole folds in lane order (words and BT are multiples of SEG / 8)
-                    const h8_t hv = __builtin_bit_cast(h8_t, v);
-                    float part = 0.0f;
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) part += (float)hv[e];
-                    part = group_sum<SEG / 8>(part);
-                    if (idx < total && (wd & (SEG / 8 - 1)) == 0) sxs[(wd / (SEG / 8)) * (MS * 16) + m] = part;
-                }
             }
         }
     };
@@ -208,15 +132,20 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
 
     // One block's B operands + MFMAs: w[t] is this lane's 16 bytes of row
     // (lane%16) of W tile t at the block's k slot 16*(lane/16) bytes; kx is the
-    // block's first column in the staged X.  q4: s[t][f], b[t][f] are the
-    // row's scale and bias of the block's fold f (f32).
+    // block's first column in the staged X.
     f4_t acc[MS][NT];
-    auto mma_block_i8 = [&](const u4_t(&w)[NT], int kx) {
+    auto mma_block = [&](const u4_t(&w)[NT], const uint32_t(&s)[NT], const uint32_t(&b)[NT], int kx) {
         h8_t bf[NT][TSTEPS];
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            bf[t][0] = i8x8_to_f16(w[t][0], w[t][1]);
-            bf[t][1] = i8x8_to_f16(w[t][2], w[t][3]);
+            if constexpr (WT == 1) {
+                bf[t][0] = i8x8_to_f16(w[t][0], w[t][1]);
+                bf[t][1] = i8x8_to_f16(w[t][2], w[t][3]);
+            } else {
+                const float sc = raw_to_f32<SBT>(s[t]), bi = raw_to_f32<SBT>(b[t]);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) bf[t][q] = dequant_word_bytes<SBT>(w[t][q], sc, bi);
+            }
         }
 #pragma unroll
         for (int st = 0; st < TSTEPS; ++st) {
@@ -227,53 +156,6 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
 #pragma unroll
                 for (int t = 0; t < NT; ++t)
                     acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bf[t][st], acc[i][t], 0, 0, 0);
-            }
-        }
-    };
-    auto mma_block_q4 = [&](const u4_t(&w)[NT], const float(&s)[NT][FPB], const float(&b)[NT][FPB], int kx) {
-        h8_t bf[NT][TSTEPS];
-#pragma unroll
-        for (int t = 0; t < NT; ++t) {
-            u4_t ww = w[t];
-            if constexpr (G64) {
-                const auto p02 = __builtin_amdgcn_permlane32_swap(ww[0], ww[2], false, false);
-                const auto p13 = __builtin_amdgcn_permlane32_swap(ww[1], ww[3], false, false);
-                ww = u4_t{p02[0], p13[0], p02[1], p13[1]};
-            }
-#pragma unroll
-            for (int q = 0; q < TSTEPS; ++q) bf[t][q] = q4_exact_f16(ww[q]);
-        }
-#pragma unroll
-        for (int f = 0; f < FPB; ++f) {
-            f4_t part[MS][NT];
-#pragma unroll
-            for (int i = 0; i < MS; ++i)
-#pragma unroll
-                for (int t = 0; t < NT; ++t) part[i][t] = f4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int j = 0; j < TSTEPS / FPB; ++j) {
-                const int st = f * (TSTEPS / FPB) + j;
-                const int kof = kx + q4_step_col<G64>(st, g);
-#pragma unroll
-                for (int i = 0; i < MS; ++i) {
-                    const h8_t a = *reinterpret_cast<const h8_t*>(xs + (size_t)(i * 16 + rl) * stride + kof);
-#pragma unroll
-                    for (int t = 0; t < NT; ++t)
-                        part[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bf[t][st], part[i][t], 0, 0, 0);
-                }
-            }
-            // acc += s * (sum q x) + b * (sum x), per activation row 4 (lane/16) + e
-            const float* sx = sxs + ((kx + f * SEG) / SEG) * (MS * 16) + 4 * g;
-#pragma unroll
-            for (int i = 0; i < MS; ++i) {
-                const f4_t xsum = *reinterpret_cast<const f4_t*>(sx + i * 16);
-#pragma unroll
-                for (int t = 0; t < NT; ++t)
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float v = acc[i][t][e] + s[t][f] * part[i][t][e];
-                        acc[i][t][e] = v + b[t][f] * xsum[e];
-                    }
             }
         }
     };
@@ -333,12 +215,9 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
             for (int t = 0; t < NT; ++t) acc[i][t] = f4_t{0.f, 0.f, 0.f, 0.f};
 
         for (int p0 = 0; p0 < npairs; p0 += DEPTH) {
-            // the group's weights (and q4 fold scales/biases) in one burst
+            // the group's weights (and q4 group scale/bias) in one burst
             u4_t ld[DEPTH][NT][2];
-            // q4: the row's scale and bias of the block's fold(s): one raw element, or the pair of
-            // consecutive groups of a group-64 block (K % 128 == 0 keeps the pair aligned)
-            using sb_t = typename std::conditional<G64, typename RawPair<SBT>::type, uint32_t>::type;
-            sb_t sr[DEPTH][2][NT], br[DEPTH][2][NT];
+            uint32_t sr[DEPTH][2][NT], br[DEPTH][2][NT];
 #pragma unroll
             for (int d = 0; d < DEPTH; ++d) {
                 if (p0 + d < npairs) {
@@ -351,14 +230,9 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
                         if constexpr (WT == 0) {
 #pragma unroll
                             for (int h = 0; h < 2; ++h) {
-                                const size_t gi = sbrow[t] + ((((p0 + d) * 2 + h) * KB) >> gshift);
-                                if constexpr (G64) {
-                                    sr[d][h][t] = load_raw_pair<SBT>(S, gi);
-                                    br[d][h][t] = load_raw_pair<SBT>(Bz, gi);
-                                } else {
-                                    sr[d][h][t] = load_raw<SBT>(S, gi);
-                                    br[d][h][t] = load_raw<SBT>(Bz, gi);
-                                }
+                                const size_t gi = sbrow[t] + ((((p0 + d) * 2 + h) * KB + 32 * g) >> gshift);
+                                sr[d][h][t] = load_raw<SBT>(S, gi);
+                                br[d][h][t] = load_raw<SBT>(Bz, gi);
                             }
                         }
                     }
@@ -379,61 +253,25 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
                                                                              0xF, 0xF, false);
                         }
                     }
-                    if constexpr (WT == 1) {
-                        mma_block_i8(w0, kx0 + d * 2 * KB);
-                        mma_block_i8(w1, kx0 + d * 2 * KB + KB);
-                    } else {
-#pragma unroll
-                        for (int h = 0; h < 2; ++h) {
-                            float sf[NT][FPB], bf[NT][FPB];
-#pragma unroll
-                            for (int t = 0; t < NT; ++t)
-#pragma unroll
-                                for (int f = 0; f < FPB; ++f) {
-                                    if constexpr (G64) {
-                                        sf[t][f] = raw_pair_f32<SBT>(sr[d][h][t], f);
-                                        bf[t][f] = raw_pair_f32<SBT>(br[d][h][t], f);
-                                    } else {
-                                        sf[t][f] = raw_to_f32<SBT>(sr[d][h][t]);
-                                        bf[t][f] = raw_to_f32<SBT>(br[d][h][t]);
-                                    }
-                                }
-                            mma_block_q4(h == 0 ? w0 : w1, sf, bf, kx0 + d * 2 * KB + h * KB);
-                        }
-                    }
+                    mma_block(w0, sr[d][0], br[d][0], kx0 + d * 2 * KB);
+                    mma_block(w1, sr[d][1], br[d][1], kx0 + d * 2 * KB + KB);
                 }
             }
         }
         if (nkb & 1) {
             // odd last block: 16 rows x 64 bytes, already in the B layout
             u4_t w[NT];
-            uint32_t s[NT][FPB], b[NT][FPB];
+            uint32_t s[NT], b[NT];
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
                 w[t] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(wtail[t] + (size_t)(nkb - 1) * 64));
                 if constexpr (WT == 0) {
-#pragma unroll
-                    for (int f = 0; f < FPB; ++f) {
-                        const size_t gi = sbrow[t] + (((nkb - 1) * KB + f * SEG) >> gshift);
-                        s[t][f] = load_raw<SBT>(S, gi);
-                        b[t][f] = load_raw<SBT>(Bz, gi);
-                    }
+                    const size_t gi = sbrow[t] + (((nkb - 1) * KB + 32 * g) >> gshift);
+                    s[t] = load_raw<SBT>(S, gi);
+                    b[t] = load_raw<SBT>(Bz, gi);
                 }
             }
-            const int kx = chunk_at((nkb - 1) * KB);
-            if constexpr (WT == 1) {
-                mma_block_i8(w, kx);
-            } else {
-                float sf[NT][FPB], bf[NT][FPB];
-#pragma unroll
-                for (int t = 0; t < NT; ++t)
-#pragma unroll
-                    for (int f = 0; f < FPB; ++f) {
-                        sf[t][f] = raw_to_f32<SBT>(s[t][f]);
-                        bf[t][f] = raw_to_f32<SBT>(b[t][f]);
-                    }
-                mma_block_q4(w, sf, bf, kx);
-            }
+            mma_block(w, s, b, chunk_at((nkb - 1) * KB));
         }
 
         // C tile: lane holds activation rows 4*(lane/16)+e, weight row lane%16
@@ -449,7 +287,7 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
                     if (n < N && m < M) {
                         // many rows: up to 64 MB of logits that nothing re-reads soon, stored past the
                         // caches (measured ~3 % faster at M = 64, 5 % slower at M = 4)
-                        const float v = WT == 1 ? acc[i][t][e] * s + bv[t] : acc[i][t][e];
+                        const float v = acc[i][t][e] * s + bv[t];
                         if (M > 8)
                             __builtin_nontemporal_store(v, Y + (size_t)m * N + n);
                         else
@@ -510,19 +348,9 @@ hipError_t allow_big_lds(Kern kern, int bytes)
     return e;
 }
 
-constexpr size_t kWholeXLds = 152 * 1024;  // the one-block-per-CU form holds X up to this size
-constexpr size_t kCuLds = 160 * 1024;      // LDS of one gfx950 CU
+constexpr size_t kWholeXLds = 152 * 1024;  // the BT = 1024 form holds X up to this size
 
-// Dynamic LDS of a kernel that stages KC columns of X: the f16 rows, plus for
-// q4 the per-fold sums of x (f32, one per SEG columns and activation row).
-template <int WT, int MS, bool G64>
-size_t mfma_lds_bytes(int KC)
-{
-    constexpr int SEG = WT == 1 ? 64 : (G64 ? 64 : 128);
-    return (size_t)MS * 16 * (KC + 8) * 2 + (WT == 0 ? (size_t)(KC / SEG) * MS * 16 * 4 : 0);
-}
-
-template <int WT, int MS, int NT, int SBT, bool G64>
+template <int WT, int MS, int NT, int SBT>
 hipError_t launch_mfma_nt(const void* W, const void* S, const void* B, int per_channel, int gshift, const _Float16* X,
                           const float* bias, float* Y, int M, int N, int K, hipStream_t st)
 {
@@ -532,11 +360,11 @@ hipError_t launch_mfma_nt(const void* W, const void* S, const void* B, int per_c
         // int8: 1024 threads, 16 waves of one W tile each (two tiles per wave need more than the 128
         // registers per lane a 1024-thread block leaves, and 8 waves of two tiles stream 12 % slower:
         // measured).  q4 (its dequant needs more registers): 512 threads.
-        const size_t xbytes = (size_t)MS * 16 * (K + 8) * 2, whole = mfma_lds_bytes<WT, MS, G64>(K);
-        if (xbytes > 80 * 1024 && xbytes <= kWholeXLds && whole <= kCuLds) {
+        const size_t whole = (size_t)MS * 16 * (K + 8) * 2;
+        if (whole > 80 * 1024 && whole <= kWholeXLds) {
             constexpr int BT = WT == 1 ? 1024 : 512, DEPTH = 2, ROWS = (BT / 64) * NT * 16;
-            auto kern = qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, false, BT, G64>;
-            if (hipError_t e = allow_big_lds(kern, (int)kCuLds); e != hipSuccess) return e;
+            auto kern = qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, false, BT>;
+            if (hipError_t e = allow_big_lds(kern, (int)kWholeXLds); e != hipSuccess) return e;
             const int ntiles = (N + ROWS - 1) / ROWS;
             int per_cu = 0, cus = 0, dev = 0;
             (void)hipGetDevice(&dev);
@@ -553,20 +381,18 @@ hipError_t launch_mfma_nt(const void* W, const void* S, const void* B, int per_c
     constexpr int DEPTH = 4 / NT;  // block pairs per group: 8 KB of weights per wave
     constexpr int ROWS = (kBlock / 64) * NT * 16;
     // X in LDS: at most 80 KB per block so two blocks share a CU; the whole K
-    // when it fits, else chunks of KC columns (a multiple of the K block pair group)
-    constexpr int KQ = 2 * DEPTH * KB;
-    int KC = std::max(1, (80 * 1024 / (MS * 16 * 2) - 8) / KQ) * KQ;
-    while (KC > KQ && mfma_lds_bytes<WT, MS, G64>(KC) > 80 * 1024) KC -= KQ;
+    // when it fits, else chunks of KC columns (a multiple of the K block)
+    int KC = std::max(1, (80 * 1024 / (MS * 16 * 2) - 8) / (2 * DEPTH * KB)) * (2 * DEPTH * KB);
     if (KC >= K) KC = K;
-    const size_t lds = mfma_lds_bytes<WT, MS, G64>(KC);
+    const size_t lds = (size_t)MS * 16 * (KC + 8) * 2;
     const int ntiles = (N + ROWS - 1) / ROWS;
     if (KC < K) {
-        auto kern = qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, true, kBlock, G64>;
+        auto kern = qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, true>;
         const int grid = std::min(ntiles, resident_blocks(kern, lds));
         hipLaunchKernelGGL(kern, dim3(grid), dim3(kBlock), lds, st, W, S, B, per_channel, gshift, X, bias, Y, M, N, K,
                            KC, ntiles);
     } else {
-        auto kern = qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, false, kBlock, G64>;
+        auto kern = qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, false>;
         const int grid = std::min(ntiles, resident_blocks(kern, lds));
         hipLaunchKernelGGL(kern, dim3(grid), dim3(kBlock), lds, st, W, S, B, per_channel, gshift, X, bias, Y, M, N, K,
                            KC, ntiles);
@@ -574,38 +400,29 @@ hipError_t launch_mfma_nt(const void* W, const void* S, const void* B, int per_c
     return hipGetLastError();
 }
 
-template <int WT, int MS, int SBT, bool G64>
+template <int WT, int MS, int SBT>
 hipError_t launch_mfma_ms(const void* W, const void* S, const void* B, int per_channel, int gshift, const _Float16* X,
                           const float* bias, float* Y, int M, int N, int K, hipStream_t st)
 {
     // two 16-row W tiles per wave when there are rows enough to fill the chip, unless X needs the
     // one-block-per-CU form (one tile per wave there)
-    const size_t xbytes = (size_t)MS * 16 * (K + 8) * 2;
-    const bool whole_x = MS == 4 && xbytes > 80 * 1024 && xbytes <= kWholeXLds &&
-                         mfma_lds_bytes<WT, MS, G64>(K) <= kCuLds;
+    const size_t whole = (size_t)MS * 16 * (K + 8) * 2;
+    const bool whole_x = MS == 4 && whole > 80 * 1024 && whole <= kWholeXLds;
     if (N >= 128 * 512 && !whole_x)
-        return launch_mfma_nt<WT, MS, 2, SBT, G64>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, st);
-    return launch_mfma_nt<WT, MS, 1, SBT, G64>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, st);
+        return launch_mfma_nt<WT, MS, 2, SBT>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, st);
+    return launch_mfma_nt<WT, MS, 1, SBT>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, st);
 }
 
-template <int WT, int SBT, bool G64 = false>
+template <int WT, int SBT>
 hipError_t launch_mfma(const void* W, const void* S, const void* B, int per_channel, int gshift, const _Float16* X,
                        const float* bias, float* Y, int M, int N, int K, hipStream_t st)
 {
     switch ((M + 15) / 16) {
-    case 1: return launch_mfma_ms<WT, 1, SBT, G64>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, st);
-    case 2: return launch_mfma_ms<WT, 2, SBT, G64>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, st);
-    case 3: return launch_mfma_ms<WT, 3, SBT, G64>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, st);
-    default: return launch_mfma_ms<WT, 4, SBT, G64>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, st);
+    case 1: return launch_mfma_ms<WT, 1, SBT>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, st);
+    case 2: return launch_mfma_ms<WT, 2, SBT>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, st);
+    case 3: return launch_mfma_ms<WT, 3, SBT>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, st);
+    default: return launch_mfma_ms<WT, 4, SBT>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, st);
     }
-}
-
-template <int SBT>
-hipError_t launch_mfma_q4(const void* W, const void* S, const void* B, int gshift, const _Float16* X, float* Y, int M,
-                          int N, int K, hipStream_t st)
-{
-    if (gshift == 6) return launch_mfma<0, SBT, true>(W, S, B, 1, gshift, X, nullptr, Y, M, N, K, st);
-    return launch_mfma<0, SBT, false>(W, S, B, 1, gshift, X, nullptr, Y, M, N, K, st);
 }
 
 }  // namespace
@@ -614,8 +431,7 @@ bool qgemv_mfma_supported(int wt, int M, int K, int group_size)
 {
     if (M < 2 || M > 64 || K <= 0) return false;
     if (wt == 1) return K % 64 == 0;
-    // q4: every MFMA k-step must lie in one quantization group (group >= 64)
-    return K % 128 == 0 && group_size >= 64;
+    return K % 128 == 0 && group_size >= 32;
 }
 
 hipError_t launch_qgemv_mfma_i8(const int8_t* w, const void* S, int sdt, int per_channel, const _Float16* x,
@@ -630,9 +446,9 @@ hipError_t launch_qgemv_mfma_q4(const uint32_t* wq, const void* S, const void* B
                                 const _Float16* x, float* y, int M, int N, int K, hipStream_t st)
 {
     const int gshift = __builtin_ctz((unsigned)group_size);
-    if (sbt == DT_F16) return launch_mfma_q4<DT_F16>(wq, S, B, gshift, x, y, M, N, K, st);
-    if (sbt == DT_F32) return launch_mfma_q4<DT_F32>(wq, S, B, gshift, x, y, M, N, K, st);
-    return launch_mfma_q4<DT_BF16>(wq, S, B, gshift, x, y, M, N, K, st);
+    if (sbt == DT_F16) return launch_mfma<0, DT_F16>(wq, S, B, 1, gshift, x, nullptr, y, M, N, K, st);
+    if (sbt == DT_F32) return launch_mfma<0, DT_F32>(wq, S, B, 1, gshift, x, nullptr, y, M, N, K, st);
+    return launch_mfma<0, DT_BF16>(wq, S, B, 1, gshift, x, nullptr, y, M, N, K, st);
 }
 
 }  // namespace cellm
