@@ -1157,6 +1157,19 @@ int32_t cellm_hip_attention_gqa_f16kv_noalloc(cellm_hip_ctx_t* ctx, const float*
     CELLM_API_END(report_exception)
 }
 
+int32_t cellm_hip_silu_mul_f32(cellm_hip_ctx_t* ctx, float* gate, const float* up, int64_t n, void* stream)
+{
+    CELLM_API_BEGIN
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    if (n < 0) return set_error(CELLM_HIP_ERR_INVALID_ARG, "bad length");
+    if (n == 0) return CELLM_HIP_OK;
+    if (!gate || !up) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null pointer");
+    DeviceGuard g(ctx->device);
+    HIP_TRY(launch_silu_mul(gate, up, (size_t)n, pick_stream(ctx, stream)), "silu_mul launch");
+    return CELLM_HIP_OK;
+    CELLM_API_END(report_exception)
+}
+
 int32_t cellm_hip_add_f32_inplace(cellm_hip_ctx_t* ctx, float* x, const float* y, int64_t n, void* stream)
 {
     CELLM_API_BEGIN

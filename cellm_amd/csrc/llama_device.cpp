@@ -115,6 +115,43 @@ struct DevBuf {
     }
 };
 
+// One projection on the device, by the weight format of its .cellm tensor
+// (the dtype dispatch of linear_f16_out_in: llama.rs:743-941, gemma.rs:1358-1499,
+// lfm.rs:924-981):
+//   I8: "i8" [out, in] + f16 "<w>.qscale" [out], scale applied to the row sum;
+//   Q4: "u32" [out, in/8] MLX affine words + f32 "<base>.scales" / "<base>.biases"
+//       [out, ceil(in/64)] (tools/convert_lfm.py:123-136), group 64;
+//   I4: "i4" [out, in], ceil(in/2) bytes per row, low nibble even, + f16
+//       "<w>.qscale" [out]: one scale per row (gs = in, gemma.rs:1466-1471).
+enum ProjKind : int32_t { PK_I8 = 0, PK_Q4 = 1, PK_I4 = 2 };
+
+struct Proj {
+    int32_t kind = PK_I8;
+    const void* w = nullptr;
+    const void* s = nullptr;  // I8/I4: f16 row scales; Q4: f32 group scales
+    const void* b = nullptr;  // Q4: f32 group biases
+};
+
+// Host-side source of one projection (mapped file bytes or caller memory).
+struct HostProj {
+    int32_t kind = PK_I8;
+    const void* w = nullptr;
+    size_t w_bytes = 0;
+    const void* s = nullptr;
+    size_t s_bytes = 0;
+    const void* b = nullptr;
+    size_t b_bytes = 0;
+};
+
+struct HostModel {
+    std::vector<HostProj> p;  // n_layers * 7, in kNames order
+    std::vector<const uint16_t*> n1, n2;
+    const int8_t* embed = nullptr;
+    const uint16_t* embed_scale = nullptr;
+    HostProj lm;  // w == nullptr: tied to the embedding
+    const uint16_t* final_norm = nullptr;
+};
+
 }  // namespace
 
 struct cellm_llama_dev {
@@ -124,17 +161,16 @@ struct cellm_llama_dev {
     cellm_hip_ctx_t* hip = nullptr;
     void* stream = nullptr;
     size_t kvd = 0, kv_elems = 0;
-    // device views of the cached weights, per layer: 7 int8 matrices and their f16 row scales
-    std::vector<const int8_t*> w;
-    std::vector<const uint16_t*> s;
+    // device views of the cached weights: 7 projections per layer, then the lm_head
+    std::vector<Proj> p;
+    Proj lm;  // the tied int8 embedding unless the model has its own lm_head
     std::vector<const float*> attn_norm, mlp_norm;
     const int8_t* embed = nullptr;
     const uint16_t* embed_scale = nullptr;
-    const int8_t* lm_w = nullptr;  // the tied embedding unless the model has its own lm_head
-    const uint16_t* lm_s = nullptr;
     const float* final_norm = nullptr;
-    DevBuf kcache, vcache, rope, x, x2, xn, q, k, v, attn, proj, h, logits, io;
-    bool fused = false;  // fused add+norm+GEMV launches (rows <= 4, hidden % 16 == 0, hidden <= 4096)
+    DevBuf kcache, vcache, rope, x, x2, xn, q, k, v, attn, proj, h, up, logits, io;
+    // fused add+norm+GEMV launches: every projection int8, rows <= 4, hidden % 16 == 0, hidden <= 4096
+    bool fused = false;
     // io: [tokens u32 | positions i32 | block tables u32 | argmax idx i32 | argmax val f32]
     void* host_io = nullptr;  // pinned mirror of io
     size_t io_tokens = 0, io_pos = 0, io_bt = 0, io_idx = 0, io_val = 0, io_bytes = 0;
@@ -173,6 +209,28 @@ void out_in(const cellm_llama_config_t& c, int j, size_t* out, size_t* in)
 }
 
 
+// One projection y[R][out] = W x[R][in] by its weight format.
+int32_t run_proj(cellm_llama_dev* m, const Proj& pr, const float* x, float* y, int64_t R, int64_t out, int64_t in,
+                 const char* what)
+{
+    cellm_hip_ctx_t* H = m->hip;
+    void* S = m->stream;
+    if (pr.kind == PK_I8) {
+        LIB_TRY(cellm_hip_qgemv_i8(H, static_cast<const int8_t*>(pr.w), pr.s, CELLM_HIP_DTYPE_F16, out, x,
+                                   CELLM_HIP_DTYPE_F32, nullptr, y, R, out, in, S),
+                what);
+    } else if (pr.kind == PK_Q4) {
+        LIB_TRY(cellm_hip_qgemv_q4_affine(H, static_cast<const uint32_t*>(pr.w), pr.s, pr.b, CELLM_HIP_DTYPE_F32, 64,
+                                          x, CELLM_HIP_DTYPE_F32, y, R, out, in, S),
+                what);
+    } else {
+        LIB_TRY(cellm_hip_qgemv_i4_sym(H, static_cast<const uint8_t*>(pr.w), static_cast<const uint16_t*>(pr.s), out,
+                                       in, x, CELLM_HIP_DTYPE_F32, y, R, out, in, S),
+                what);
+    }
+    return CELLM_HIP_OK;
+}
+
 // The step's device work for `rows` sessions, enqueued on the runner's stream:
 // inputs are read from io (tokens, positions, block tables), the greedy ids
 // and logits are left in io and m->logits.  Only kernel launches: no
@@ -196,72 +254,84 @@ int32_t enqueue_step(cellm_llama_dev* m, int32_t rows)
     cellm_hip_ctx_t* H = m->hip;
     void* S = m->stream;
     const float eps = c.rms_norm_eps;
+    auto i8w = [](const Proj& pr) { return static_cast<const int8_t*>(pr.w); };
+    auto i8s = [](const Proj& pr) { return static_cast<const uint16_t*>(pr.s); };
 
     LIB_TRY(cellm_hip_embed_i8(H, d_tok, R, m->embed, m->embed_scale, vocab, hid, x, S), "embed");
     if (m->fused) {
         // 5 launches per layer; the residual stream alternates between x and x2
         float* x2 = m->x2.as<float>();
         for (int64_t l = 0; l < L; ++l) {
-            const int8_t* const* W = &m->w[l * 7];
-            const uint16_t* const* Sc = &m->s[l * 7];
-            LIB_TRY(cellm_hip_decode_qkv_rope_kv(H, x, l == 0 ? nullptr : proj, x2, m->attn_norm[l], eps, W[0], Sc[0],
-                                                 W[1], Sc[1], W[2], Sc[2], R, hid, c.n_heads, c.n_kv_heads,
-                                                 c.head_dim, d_pos, m->rope.as<float>(), m->table_positions, q, kc, vc,
-                                                 d_bt, MB, c.total_blocks, L, tpb, l, S),
+            const Proj* P = &m->p[l * 7];
+            LIB_TRY(cellm_hip_decode_qkv_rope_kv(H, x, l == 0 ? nullptr : proj, x2, m->attn_norm[l], eps, i8w(P[0]),
+                                                 i8s(P[0]), i8w(P[1]), i8s(P[1]), i8w(P[2]), i8s(P[2]), R, hid,
+                                                 c.n_heads, c.n_kv_heads, c.head_dim, d_pos, m->rope.as<float>(),
+                                                 m->table_positions, q, kc, vc, d_bt, MB, c.total_blocks, L, tpb, l,
+                                                 S),
                     "residual + input_layernorm + qkv + rope + kv write");
             LIB_TRY(cellm_hip_attention_gqa_f16kv(H, q, kc, vc, d_bt, MB, c.total_blocks, d_pos, R, c.n_heads,
                                                   c.n_kv_heads, c.head_dim, L, tpb, l, 0.0f, 0.0f, attn, S),
                     "attention");
-            LIB_TRY(cellm_hip_qgemv_i8(H, W[3], Sc[3], CELLM_HIP_DTYPE_F16, hid, attn, CELLM_HIP_DTYPE_F32, nullptr,
-                                       proj, R, hid, hid, S),
-                    "o_proj");
-            LIB_TRY(cellm_hip_decode_gate_up_silu(H, x2, proj, x, m->mlp_norm[l], eps, W[4], Sc[4], W[5], Sc[5], R, hid,
-                                                  inter, h, S),
+            if (int32_t rc = run_proj(m, P[3], attn, proj, R, hid, hid, "o_proj")) return rc;
+            LIB_TRY(cellm_hip_decode_gate_up_silu(H, x2, proj, x, m->mlp_norm[l], eps, i8w(P[4]), i8s(P[4]),
+                                                  i8w(P[5]), i8s(P[5]), R, hid, inter, h, S),
                     "residual + post_attention_layernorm + gate/up");
-            LIB_TRY(cellm_hip_qgemv_i8(H, W[6], Sc[6], CELLM_HIP_DTYPE_F16, hid, h, CELLM_HIP_DTYPE_F32, nullptr, proj,
-                                       R, hid, inter, S),
-                    "down_proj");
+            if (int32_t rc = run_proj(m, P[6], h, proj, R, hid, inter, "down_proj")) return rc;
         }
         LIB_TRY(cellm_hip_add_rms_norm(H, x, proj, m->final_norm, CELLM_HIP_DTYPE_F32, R, hid, eps, xn, S),
                 "residual + norm");
     } else {
-    LIB_TRY(cellm_hip_rms_norm(H, x, m->attn_norm[0], CELLM_HIP_DTYPE_F32, R, hid, eps, xn, S), "input_layernorm");
-    for (int64_t l = 0; l < L; ++l) {
-        const int8_t* const* W = &m->w[l * 7];
-        const uint16_t* const* Sc = &m->s[l * 7];
-        // xn = input_layernorm(x), from the previous layer's residual add (or the embedding)
-        LIB_TRY(cellm_hip_qgemv_i8_qkv(H, W[0], Sc[0], hid, nullptr, W[1], Sc[1], kvd, nullptr, W[2], Sc[2], kvd, nullptr,
-                                       CELLM_HIP_DTYPE_F16, xn, CELLM_HIP_DTYPE_F32, q, k, v, R, hid, kvd, hid, S),
-                "qkv");
-        LIB_TRY(cellm_hip_rope_kv_write_f16(H, q, k, v, R, c.n_heads, c.n_kv_heads, c.head_dim, d_pos,
-                                            m->rope.as<float>(), m->table_positions, kc, vc, d_bt, MB, c.total_blocks,
-                                            L, tpb, l, S),
-                "rope + kv write");
-        LIB_TRY(cellm_hip_attention_gqa_f16kv(H, q, kc, vc, d_bt, MB, c.total_blocks, d_pos, R, c.n_heads,
-                                              c.n_kv_heads, c.head_dim, L, tpb, l, 0.0f, 0.0f, attn, S),
-                "attention");
-        LIB_TRY(cellm_hip_qgemv_i8(H, W[3], Sc[3], CELLM_HIP_DTYPE_F16, hid, attn, CELLM_HIP_DTYPE_F32, nullptr, proj, R,
-                                   hid, hid, S),
-                "o_proj");
-        LIB_TRY(cellm_hip_add_rms_norm(H, x, proj, m->mlp_norm[l], CELLM_HIP_DTYPE_F32, R, hid, eps, xn, S),
-                "residual + post_attention_layernorm");
-        LIB_TRY(cellm_hip_qgemv_i8_gate_up_silu(H, W[4], Sc[4], inter, nullptr, W[5], Sc[5], inter, nullptr,
-                                                CELLM_HIP_DTYPE_F16, xn, CELLM_HIP_DTYPE_F32, h, R, inter, hid, S),
-                "gate/up");
-        LIB_TRY(cellm_hip_qgemv_i8(H, W[6], Sc[6], CELLM_HIP_DTYPE_F16, hid, h, CELLM_HIP_DTYPE_F32, nullptr, proj, R,
-                                   hid, inter, S),
-                "down_proj");
-        // residual, then the next layer's input_layernorm (the final norm after the last layer)
-        const float* next_norm = l + 1 < L ? m->attn_norm[l + 1] : m->final_norm;
-        LIB_TRY(cellm_hip_add_rms_norm(H, x, proj, next_norm, CELLM_HIP_DTYPE_F32, R, hid, eps, xn, S),
-                "residual + norm");
+        LIB_TRY(cellm_hip_rms_norm(H, x, m->attn_norm[0], CELLM_HIP_DTYPE_F32, R, hid, eps, xn, S), "input_layernorm");
+        for (int64_t l = 0; l < L; ++l) {
+            const Proj* P = &m->p[l * 7];
+            // xn = input_layernorm(x), from the previous layer's residual add (or the embedding)
+            if (P[0].kind == PK_I8 && P[1].kind == PK_I8 && P[2].kind == PK_I8) {
+                LIB_TRY(cellm_hip_qgemv_i8_qkv(H, i8w(P[0]), i8s(P[0]), hid, nullptr, i8w(P[1]), i8s(P[1]), kvd,
+                                               nullptr, i8w(P[2]), i8s(P[2]), kvd, nullptr, CELLM_HIP_DTYPE_F16, xn,
+                                               CELLM_HIP_DTYPE_F32, q, k, v, R, hid, kvd, hid, S),
+                        "qkv");
+            } else {
+                if (int32_t rc = run_proj(m, P[0], xn, q, R, hid, hid, "q_proj")) return rc;
+                if (int32_t rc = run_proj(m, P[1], xn, k, R, kvd, hid, "k_proj")) return rc;
+                if (int32_t rc = run_proj(m, P[2], xn, v, R, kvd, hid, "v_proj")) return rc;
+            }
+            LIB_TRY(cellm_hip_rope_kv_write_f16(H, q, k, v, R, c.n_heads, c.n_kv_heads, c.head_dim, d_pos,
+                                                m->rope.as<float>(), m->table_positions, kc, vc, d_bt, MB,
+                                                c.total_blocks, L, tpb, l, S),
+                    "rope + kv write");
+            LIB_TRY(cellm_hip_attention_gqa_f16kv(H, q, kc, vc, d_bt, MB, c.total_blocks, d_pos, R, c.n_heads,
+                                                  c.n_kv_heads, c.head_dim, L, tpb, l, 0.0f, 0.0f, attn, S),
+                    "attention");
+            if (int32_t rc = run_proj(m, P[3], attn, proj, R, hid, hid, "o_proj")) return rc;
+            LIB_TRY(cellm_hip_add_rms_norm(H, x, proj, m->mlp_norm[l], CELLM_HIP_DTYPE_F32, R, hid, eps, xn, S),
+                    "residual + post_attention_layernorm");
+            if (P[4].kind == PK_I8 && P[5].kind == PK_I8) {
+                LIB_TRY(cellm_hip_qgemv_i8_gate_up_silu(H, i8w(P[4]), i8s(P[4]), inter, nullptr, i8w(P[5]), i8s(P[5]),
+                                                        inter, nullptr, CELLM_HIP_DTYPE_F16, xn, CELLM_HIP_DTYPE_F32,
+                                                        h, R, inter, hid, S),
+                        "gate/up");
+            } else if (P[4].kind == PK_Q4 && P[5].kind == PK_Q4) {
+                LIB_TRY(cellm_hip_qgemv_q4_affine_gate_up_silu(
+                            H, static_cast<const uint32_t*>(P[4].w), P[4].s, P[4].b,
+                            static_cast<const uint32_t*>(P[5].w), P[5].s, P[5].b, CELLM_HIP_DTYPE_F32, 64, xn,
+                            CELLM_HIP_DTYPE_F32, h, R, inter, hid, S),
+                        "gate/up");
+            } else {
+                float* upb = m->up.as<float>();
+                if (int32_t rc = run_proj(m, P[4], xn, h, R, inter, hid, "gate_proj")) return rc;
+                if (int32_t rc = run_proj(m, P[5], xn, upb, R, inter, hid, "up_proj")) return rc;
+                LIB_TRY(cellm_hip_silu_mul_f32(H, h, upb, R * inter, S), "silu * up");
+            }
+            if (int32_t rc = run_proj(m, P[6], h, proj, R, hid, inter, "down_proj")) return rc;
+            // residual, then the next layer's input_layernorm (the final norm after the last layer)
+            const float* next_norm = l + 1 < L ? m->attn_norm[l + 1] : m->final_norm;
+            LIB_TRY(cellm_hip_add_rms_norm(H, x, proj, next_norm, CELLM_HIP_DTYPE_F32, R, hid, eps, xn, S),
+                    "residual + norm");
+        }
     }
-    }
-    // lm_head (tied embedding or lm_head.weight, llama.rs:522-567) through the int8 GEMV, greedy id on the device
+    // lm_head (tied embedding or lm_head.weight, llama.rs:522-567), greedy id on the device
     float* lg = m->logits.as<float>();
-    LIB_TRY(cellm_hip_qgemv_i8(H, m->lm_w, m->lm_s, CELLM_HIP_DTYPE_F16, vocab, xn, CELLM_HIP_DTYPE_F32, nullptr, lg, R,
-                               vocab, hid, S),
-            "lm_head");
+    if (int32_t rc = run_proj(m, m->lm, xn, lg, R, vocab, hid, "lm_head")) return rc;
     LIB_TRY(cellm_hip_argmax_f32(H, lg, R, vocab, d_idx, d_val, S), "argmax");
     return CELLM_HIP_OK;
 }
@@ -301,10 +371,8 @@ int32_t prepare_graphs(cellm_llama_dev* m)
     return CELLM_HIP_OK;
 }
 
-int32_t dev_create_impl(const cellm_llama_config_t* cfg, const cellm_llama_layer_t* layers, const int8_t* embed_i8,
-                        const uint16_t* embed_scale_f16, const int8_t* lm_i8, const uint16_t* lm_scale_f16,
-                        const uint16_t* final_norm_f16, int32_t device, int32_t max_rows, int32_t max_blocks,
-                        cellm_llama_dev_t** out);
+int32_t dev_create_impl(const cellm_llama_config_t* cfg, const HostModel& hm, int32_t device, int32_t max_rows,
+                        int32_t max_blocks, cellm_llama_dev_t** out);
 
 }  // namespace
 
@@ -334,8 +402,29 @@ int32_t cellm_llama_dev_create(const cellm_llama_config_t* cfg, const cellm_llam
                                cellm_llama_dev_t** out)
 {
     CELLM_API_BEGIN
-    return dev_create_impl(cfg, layers, embed_i8, embed_scale_f16, nullptr, nullptr, final_norm_f16, device, max_rows,
-                           max_blocks, out);
+    if (!cfg || !layers || !embed_i8 || !embed_scale_f16 || !final_norm_f16 || !out)
+        return fail(CELLM_HIP_ERR_INVALID_ARG, "null argument");
+    if (cfg->n_layers <= 0 || cfg->n_layers > 4096) return fail(CELLM_HIP_ERR_INVALID_ARG, "bad n_layers");
+    HostModel hm;
+    for (int32_t l = 0; l < cfg->n_layers; ++l) {
+        for (int j = 0; j < 7; ++j) {
+            size_t o, i;
+            out_in(*cfg, j, &o, &i);
+            HostProj hp;
+            hp.kind = PK_I8;
+            hp.w = layers[l].w[j];
+            hp.w_bytes = o * i;
+            hp.s = layers[l].scale_f16[j];
+            hp.s_bytes = o * 2;
+            hm.p.push_back(hp);
+        }
+        hm.n1.push_back(layers[l].input_layernorm_f16);
+        hm.n2.push_back(layers[l].post_attention_layernorm_f16);
+    }
+    hm.embed = embed_i8;
+    hm.embed_scale = embed_scale_f16;
+    hm.final_norm = final_norm_f16;
+    return dev_create_impl(cfg, hm, device, max_rows, max_blocks, out);
     CELLM_API_END(cellm_step::report_exception)
 }
 
@@ -343,12 +432,10 @@ int32_t cellm_llama_dev_create(const cellm_llama_config_t* cfg, const cellm_llam
 
 namespace {
 
-int32_t dev_create_impl(const cellm_llama_config_t* cfg, const cellm_llama_layer_t* layers, const int8_t* embed_i8,
-                        const uint16_t* embed_scale_f16, const int8_t* lm_i8, const uint16_t* lm_scale_f16,
-                        const uint16_t* final_norm_f16, int32_t device, int32_t max_rows, int32_t max_blocks,
-                        cellm_llama_dev_t** out)
+int32_t dev_create_impl(const cellm_llama_config_t* cfg, const HostModel& hm, int32_t device, int32_t max_rows,
+                        int32_t max_blocks, cellm_llama_dev_t** out)
 {
-    if (!cfg || !layers || !embed_i8 || !embed_scale_f16 || !final_norm_f16 || !out)
+    if (!cfg || !hm.embed || !hm.embed_scale || !hm.final_norm || !out)
         return fail(CELLM_HIP_ERR_INVALID_ARG, "null argument");
     *out = nullptr;
     const cellm_llama_config_t& c = *cfg;
@@ -361,6 +448,9 @@ int32_t dev_create_impl(const cellm_llama_config_t* cfg, const cellm_llama_layer
     if (max_rows < 1 || max_rows > 4) return fail(CELLM_HIP_ERR_INVALID_ARG, "max_rows must be 1..4");
     if (max_blocks < 1 || max_blocks > c.total_blocks)
         return fail(CELLM_HIP_ERR_INVALID_ARG, "max_blocks must be 1..total_blocks");
+    if (hm.p.size() != (size_t)c.n_layers * 7 || hm.n1.size() != (size_t)c.n_layers ||
+        hm.n2.size() != (size_t)c.n_layers)
+        return fail(CELLM_HIP_ERR_INVALID_ARG, "projection list does not match n_layers");
     auto* m = new cellm_llama_dev();
     m->cfg = c;
     m->max_rows = max_rows;
@@ -382,47 +472,51 @@ int32_t dev_create_impl(const cellm_llama_config_t* cfg, const cellm_llama_layer
     if (hipGetDevice(&prev) != hipSuccess || hipSetDevice(device) != hipSuccess)
         return bail(fail(CELLM_HIP_ERR_DEVICE, "hipSetDevice(%d) failed", device));
     const size_t hid = (size_t)c.hidden, L = (size_t)c.n_layers;
-    m->w.resize(L * 7);
-    m->s.resize(L * 7);
+    // the cache keys follow the .cellm tensor names of each format
+    auto upload_proj = [&](const std::string& base, const HostProj& hp, Proj* pr) -> int32_t {
+        if (!hp.w || !hp.s || (hp.kind == PK_Q4 && !hp.b))
+            return fail(CELLM_HIP_ERR_INVALID_ARG, "%s: weight or scale data missing", base.c_str());
+        const void *dw = nullptr, *ds = nullptr, *db = nullptr;
+        if (int32_t r = upload(m, base + ".weight", hp.w, hp.w_bytes, &dw)) return r;
+        if (hp.kind == PK_Q4) {
+            if (int32_t r = upload(m, base + ".scales", hp.s, hp.s_bytes, &ds)) return r;
+            if (int32_t r = upload(m, base + ".biases", hp.b, hp.b_bytes, &db)) return r;
+        } else if (int32_t r = upload(m, base + ".weight.qscale", hp.s, hp.s_bytes, &ds)) {
+            return r;
+        }
+        pr->kind = hp.kind;
+        pr->w = dw;
+        pr->s = ds;
+        pr->b = db;
+        return CELLM_HIP_OK;
+    };
+    m->p.resize(L * 7);
+    bool all_i8 = true;
     for (size_t l = 0; l < L; ++l) {
         const std::string pre = "model.layers." + std::to_string(l) + ".";
         for (int j = 0; j < 7; ++j) {
-            size_t o, i;
-            out_in(c, j, &o, &i);
-            if (!layers[l].w[j] || !layers[l].scale_f16[j])
-                return bail(fail(CELLM_HIP_ERR_INVALID_ARG, "layer %zu tensor %s missing", l, kNames[j]));
-            const void *dw = nullptr, *ds = nullptr;
-            if ((rc = upload(m, pre + kNames[j] + ".weight", layers[l].w[j], o * i, &dw)) ||
-                (rc = upload(m, pre + kNames[j] + ".weight.qscale", layers[l].scale_f16[j], o * 2, &ds)))
-                return bail(rc);
-            m->w[l * 7 + j] = reinterpret_cast<const int8_t*>(dw);
-            m->s[l * 7 + j] = reinterpret_cast<const uint16_t*>(ds);
+            if ((rc = upload_proj(pre + kNames[j], hm.p[l * 7 + j], &m->p[l * 7 + j]))) return bail(rc);
+            all_i8 = all_i8 && hm.p[l * 7 + j].kind == PK_I8;
         }
         const float *a = nullptr, *b = nullptr;
-        if ((rc = upload_norm(m, pre + "input_layernorm.weight", layers[l].input_layernorm_f16, hid, &a)) ||
-            (rc = upload_norm(m, pre + "post_attention_layernorm.weight", layers[l].post_attention_layernorm_f16, hid,
-                              &b)))
+        if (!hm.n1[l] || !hm.n2[l]) return bail(fail(CELLM_HIP_ERR_INVALID_ARG, "layer %zu norm missing", l));
+        if ((rc = upload_norm(m, pre + "input_layernorm.weight", hm.n1[l], hid, &a)) ||
+            (rc = upload_norm(m, pre + "post_attention_layernorm.weight", hm.n2[l], hid, &b)))
             return bail(rc);
         m->attn_norm.push_back(a);
         m->mlp_norm.push_back(b);
     }
     const void *de = nullptr, *des = nullptr;
-    if ((rc = upload(m, "model.embed_tokens.weight", embed_i8, (size_t)c.vocab * hid, &de)) ||
-        (rc = upload(m, "model.embed_tokens.weight.qscale", embed_scale_f16, (size_t)c.vocab * 2, &des)) ||
-        (rc = upload_norm(m, "model.norm.weight", final_norm_f16, hid, &m->final_norm)))
+    if ((rc = upload(m, "model.embed_tokens.weight", hm.embed, (size_t)c.vocab * hid, &de)) ||
+        (rc = upload(m, "model.embed_tokens.weight.qscale", hm.embed_scale, (size_t)c.vocab * 2, &des)) ||
+        (rc = upload_norm(m, "model.norm.weight", hm.final_norm, hid, &m->final_norm)))
         return bail(rc);
     m->embed = reinterpret_cast<const int8_t*>(de);
     m->embed_scale = reinterpret_cast<const uint16_t*>(des);
-    m->lm_w = m->embed;
-    m->lm_s = m->embed_scale;
-    if (lm_i8) {
-        const void *dl = nullptr, *dls = nullptr;
-        if ((rc = upload(m, "lm_head.weight", lm_i8, (size_t)c.vocab * hid, &dl)) ||
-            (rc = upload(m, "lm_head.weight.qscale", lm_scale_f16, (size_t)c.vocab * 2, &dls)))
-            return bail(rc);
-        m->lm_w = reinterpret_cast<const int8_t*>(dl);
-        m->lm_s = reinterpret_cast<const uint16_t*>(dls);
-    }
+    m->lm.kind = PK_I8;
+    m->lm.w = m->embed;
+    m->lm.s = m->embed_scale;
+    if (hm.lm.w && (rc = upload_proj("lm_head", hm.lm, &m->lm))) return bail(rc);
 
     // paged K/V (KvCacheLayout: total_blocks x layers x tokens_per_block x kv_dim), zeroed
     m->kv_elems = (size_t)c.total_blocks * L * c.tokens_per_block * m->kvd;
@@ -435,6 +529,7 @@ int32_t dev_create_impl(const cellm_llama_config_t* cfg, const cellm_llama_layer
         (rc = m->q.alloc(R * hid * 4, "hipMalloc(q)")) || (rc = m->k.alloc(R * m->kvd * 4, "hipMalloc(k)")) ||
         (rc = m->v.alloc(R * m->kvd * 4, "hipMalloc(v)")) || (rc = m->attn.alloc(R * hid * 4, "hipMalloc(attn)")) ||
         (rc = m->proj.alloc(R * hid * 4, "hipMalloc(proj)")) || (rc = m->h.alloc(R * inter * 4, "hipMalloc(h)")) ||
+        (rc = m->up.alloc(R * inter * 4, "hipMalloc(up)")) ||
         (rc = m->logits.alloc(R * (size_t)c.vocab * 4, "hipMalloc(logits)")))
         return bail(rc);
     hipError_t e = hipMemset(m->kcache.p, 0, m->kv_elems * 2);
@@ -446,7 +541,7 @@ int32_t dev_create_impl(const cellm_llama_config_t* cfg, const cellm_llama_layer
         e = hipMemcpy(m->rope.p, table.data(), table.size() * sizeof(float), hipMemcpyHostToDevice);
         if (e != hipSuccess) return bail(from_runtime(e, "upload rope table"));
     }
-    m->fused = (c.hidden % 16) == 0 && c.hidden <= 4096 && c.head_dim % 2 == 0;
+    m->fused = all_i8 && (c.hidden % 16) == 0 && c.hidden <= 4096 && c.head_dim % 2 == 0;
     auto align = [](size_t v) { return (v + 255) & ~(size_t)255; };
     m->io_tokens = 0;
     m->io_pos = align(R * 4);
@@ -538,57 +633,102 @@ int32_t cellm_llama_dev_create_from_file(const char* path, int32_t device, int32
             return fail(CELLM_HIP_ERR_NOT_FOUND,
                         "missing required llama tensors: model.embed_tokens.weight/model.norm.weight");
     }
-    // a tensor of the given dtype and shape ([d0] when d1 < 0), as mapped bytes
-    auto tensor = [&](const std::string& name, const char* dtype, int64_t d0, int64_t d1, const void** p) -> int32_t {
+    // a tensor of the given dtype and shape ([d0] when d1 < 0) holding `nbytes`, as mapped bytes
+    auto tensor = [&](const std::string& name, const char* dtype, int64_t d0, int64_t d1, uint64_t nbytes,
+                      const void** p) -> int32_t {
         cellm_file_tensor_t t;
         if (cellm_file_find(f, name.c_str(), &t) != CELLM_HIP_OK)
             return fail(CELLM_HIP_ERR_NOT_FOUND, "tensor %s missing", name.c_str());
         if (strcmp(t.dtype, dtype) != 0)
             return fail(CELLM_HIP_ERR_UNSUPPORTED, "tensor %s is %s; the device step takes %s", name.c_str(), t.dtype,
                         dtype);
-        const int64_t elem = strcmp(dtype, "f16") == 0 ? 2 : 1;
         const bool shape_ok = d1 < 0 ? (t.ndim == 1 && t.shape[0] == d0)
                                      : (t.ndim == 2 && t.shape[0] == d0 && t.shape[1] == d1);
-        if (!shape_ok || t.nbytes != (uint64_t)(d0 * (d1 < 0 ? 1 : d1) * elem))
+        if (!shape_ok || t.nbytes != nbytes)
             return fail(CELLM_HIP_ERR_INVALID_ARG, "tensor %s has shape/bytes that do not match the config",
                         name.c_str());
         return cellm_file_tensor_bytes(f, name.c_str(), p, nullptr) == CELLM_HIP_OK
                    ? CELLM_HIP_OK
                    : fail(CELLM_HIP_ERR_INVALID_ARG, "tensor %s unreadable", name.c_str());
     };
-    std::vector<cellm_llama_layer_t> layers((size_t)c.n_layers);
+    // One projection [o, i] by the dtype of its weight tensor, as the runners'
+    // linear_f16_out_in dispatch on it (llama.rs:781-941, lfm.rs:924-981,
+    // gemma.rs:1358-1499).
+    auto load_proj = [&](const std::string& w, int64_t o, int64_t i, HostProj* hp) -> int32_t {
+        cellm_file_tensor_t t;
+        if (cellm_file_find(f, w.c_str(), &t) != CELLM_HIP_OK)
+            return fail(CELLM_HIP_ERR_NOT_FOUND, "tensor %s missing", w.c_str());
+        if (strcmp(t.dtype, "i8") == 0) {
+            hp->kind = PK_I8;
+            hp->w_bytes = (size_t)(o * i);
+            hp->s_bytes = (size_t)o * 2;
+            if (int32_t rc = tensor(w, "i8", o, i, hp->w_bytes, &hp->w)) return rc;
+            return tensor(w + ".qscale", "f16", o, -1, hp->s_bytes, &hp->s);
+        }
+        if (strcmp(t.dtype, "u32") == 0) {
+            // MLX affine: [o, i/8] words; f32 scales/biases [o, ceil(i/64)] named by the weight's base
+            // ("<base>.scales" for "<base>.weight", lfm.rs:932-941; tools/convert_lfm.py:123-136)
+            if (i % 8 != 0) return fail(CELLM_HIP_ERR_INVALID_ARG, "%s: in_dim %lld not a multiple of 8", w.c_str(),
+                                        (long long)i);
+            const std::string base = w.size() > 7 && w.compare(w.size() - 7, 7, ".weight") == 0
+                                         ? w.substr(0, w.size() - 7)
+                                         : w;
+            const int64_t groups = (i + 63) / 64;
+            hp->kind = PK_Q4;
+            hp->w_bytes = (size_t)(o * i / 2);
+            hp->s_bytes = hp->b_bytes = (size_t)(o * groups * 4);
+            if (int32_t rc = tensor(w, "u32", o, i / 8, hp->w_bytes, &hp->w)) return rc;
+            if (int32_t rc = tensor(base + ".scales", "f32", o, groups, hp->s_bytes, &hp->s)) return rc;
+            return tensor(base + ".biases", "f32", o, groups, hp->b_bytes, &hp->b);
+        }
+        if (strcmp(t.dtype, "i4") == 0) {
+            // [o, i] with ceil(i/2) bytes per row (i4_packed_nbytes_for_shape), one f16 scale per row
+            hp->kind = PK_I4;
+            hp->w_bytes = (size_t)(o * ((i + 1) / 2));
+            hp->s_bytes = (size_t)o * 2;
+            if (int32_t rc = tensor(w, "i4", o, i, hp->w_bytes, &hp->w)) return rc;
+            return tensor(w + ".qscale", "f16", o, -1, hp->s_bytes, &hp->s);
+        }
+        return fail(CELLM_HIP_ERR_UNSUPPORTED, "tensor %s is %s; the device step takes i8, u32 (MLX affine) or i4",
+                    w.c_str(), t.dtype);
+    };
+    HostModel hm;
+    hm.p.resize((size_t)c.n_layers * 7);
     for (int32_t l = 0; l < c.n_layers; ++l) {
         const std::string pre = prefix + "model.layers." + std::to_string(l) + ".";
         for (int j = 0; j < 7; ++j) {
             size_t o, i;
             out_in(c, j, &o, &i);
-            const std::string w = pre + kNames[j] + ".weight";
-            const void *pw = nullptr, *ps = nullptr;
-            if (int32_t rc = tensor(w, "i8", (int64_t)o, (int64_t)i, &pw)) return rc;
-            if (int32_t rc = tensor(w + ".qscale", "f16", (int64_t)o, -1, &ps)) return rc;
-            layers[l].w[j] = static_cast<const int8_t*>(pw);
-            layers[l].scale_f16[j] = static_cast<const uint16_t*>(ps);
+            if (int32_t rc = load_proj(pre + kNames[j] + ".weight", (int64_t)o, (int64_t)i, &hm.p[(size_t)l * 7 + j]))
+                return rc;
         }
         const void *n1 = nullptr, *n2 = nullptr;
-        if (int32_t rc = tensor(pre + "input_layernorm.weight", "f16", c.hidden, -1, &n1)) return rc;
-        if (int32_t rc = tensor(pre + "post_attention_layernorm.weight", "f16", c.hidden, -1, &n2)) return rc;
-        layers[l].input_layernorm_f16 = static_cast<const uint16_t*>(n1);
-        layers[l].post_attention_layernorm_f16 = static_cast<const uint16_t*>(n2);
+        if (int32_t rc = tensor(pre + "input_layernorm.weight", "f16", c.hidden, -1, (uint64_t)c.hidden * 2, &n1))
+            return rc;
+        if (int32_t rc =
+                tensor(pre + "post_attention_layernorm.weight", "f16", c.hidden, -1, (uint64_t)c.hidden * 2, &n2))
+            return rc;
+        hm.n1.push_back(static_cast<const uint16_t*>(n1));
+        hm.n2.push_back(static_cast<const uint16_t*>(n2));
     }
-    const void *emb = nullptr, *embs = nullptr, *fn = nullptr, *lm = nullptr, *lms = nullptr;
-    if (int32_t rc = tensor(prefix + "model.embed_tokens.weight", "i8", c.vocab, c.hidden, &emb)) return rc;
-    if (int32_t rc = tensor(prefix + "model.embed_tokens.weight.qscale", "f16", c.vocab, -1, &embs)) return rc;
-    if (int32_t rc = tensor(prefix + "model.norm.weight", "f16", c.hidden, -1, &fn)) return rc;
+    const void *emb = nullptr, *embs = nullptr, *fn = nullptr;
+    if (int32_t rc = tensor(prefix + "model.embed_tokens.weight", "i8", c.vocab, c.hidden,
+                            (uint64_t)c.vocab * c.hidden, &emb))
+        return rc;
+    if (int32_t rc = tensor(prefix + "model.embed_tokens.weight.qscale", "f16", c.vocab, -1, (uint64_t)c.vocab * 2,
+                            &embs))
+        return rc;
+    if (int32_t rc = tensor(prefix + "model.norm.weight", "f16", c.hidden, -1, (uint64_t)c.hidden * 2, &fn)) return rc;
     // lm_head.weight when the file has one, else the tied embedding (llama.rs:522-532)
     for (const std::string& name : {prefix + "lm_head.weight", std::string("lm_head.weight")}) {
         if (cellm_file_find(f, name.c_str(), nullptr) != CELLM_HIP_OK) continue;
-        if (int32_t rc = tensor(name, "i8", c.vocab, c.hidden, &lm)) return rc;
-        if (int32_t rc = tensor(name + ".qscale", "f16", c.vocab, -1, &lms)) return rc;
+        if (int32_t rc = load_proj(name, c.vocab, c.hidden, &hm.lm)) return rc;
         break;
     }
-    return dev_create_impl(&c, layers.data(), static_cast<const int8_t*>(emb), static_cast<const uint16_t*>(embs),
-                           static_cast<const int8_t*>(lm), static_cast<const uint16_t*>(lms),
-                           static_cast<const uint16_t*>(fn), device, max_rows, max_blocks, out);
+    hm.embed = static_cast<const int8_t*>(emb);
+    hm.embed_scale = static_cast<const uint16_t*>(embs);
+    hm.final_norm = static_cast<const uint16_t*>(fn);
+    return dev_create_impl(&c, hm, device, max_rows, max_blocks, out);
     CELLM_API_END(cellm_step::report_exception)
 }
 

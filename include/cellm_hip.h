@@ -383,6 +383,11 @@ int32_t cellm_hip_attention_gqa_f16kv_noalloc(cellm_hip_ctx_t* ctx, const float*
                                               int64_t n_layers, int64_t tokens_per_block, int64_t layer,
                                               float attn_scale, float soft_cap, float* out, void* stream);
 
+/* MetalOps::encode_silu_mul_f32_inplace (metal.rs:232-243, the CPU loop of
+ * llama.rs:477-484): gate[i] = silu(gate[i]) * up[i], silu(g) = g / (1 + exp(-g)),
+ * in place on gate. */
+int32_t cellm_hip_silu_mul_f32(cellm_hip_ctx_t* ctx, float* gate, const float* up, int64_t n, void* stream);
+
 /* MetalOps::encode_add_f32_inplace: x[i] += y[i]. */
 int32_t cellm_hip_add_f32_inplace(cellm_hip_ctx_t* ctx, float* x, const float* y, int64_t n, void* stream);
 

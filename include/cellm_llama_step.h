@@ -100,11 +100,22 @@ int32_t cellm_llama_dev_create(const cellm_llama_config_t* cfg, const cellm_llam
 /* The same runner from a .cellm file (LlamaRunner::load, llama.rs:39-75): the
  * model shape from the header (head_dim defaults to hidden / heads), the
  * tensor prefix "" or "language_model." (detect_llama_prefix,
- * llama.rs:1094-1113), int8 projection weights with f16 ".qscale" row scales,
- * f16 norms, the int8 embedding as the lm_head unless the file has an int8
- * lm_head.weight (llama.rs:522-532).  Other dtypes are
- * CELLM_HIP_ERR_UNSUPPORTED.  tokens_per_block / total_blocks size the paged
- * K/V cache; the file is closed before this returns. */
+ * llama.rs:1094-1113), f16 norms, and each projection dispatched on the dtype
+ * of its weight tensor as the runners' linear_f16_out_in does (llama.rs:781-941,
+ * lfm.rs:924-981, gemma.rs:1358-1499):
+ *   "i8"  [out, in] + f16 "<w>.qscale" [out]            -> cellm_hip_qgemv_i8;
+ *   "u32" [out, in/8] MLX affine words + f32 "<base>.scales" / "<base>.biases"
+ *         [out, ceil(in/64)] (tools/convert_lfm.py:123-136)
+ *                                                        -> cellm_hip_qgemv_q4_affine;
+ *   "i4"  [out, in] (ceil(in/2) bytes per row) + f16 "<w>.qscale" [out]
+ *         (one scale per row, gs = in, gemma.rs:1466-1471)
+ *                                                        -> cellm_hip_qgemv_i4_sym.
+ * The int8 embedding is the lm_head unless the file has an lm_head.weight (in
+ * any of the three formats, llama.rs:522-532).  Other dtypes are
+ * CELLM_HIP_ERR_UNSUPPORTED.  A model whose projections are all "i8" runs the
+ * fused decode launches; any other mix runs one launch per projection.
+ * tokens_per_block / total_blocks size the paged K/V cache; the file is
+ * closed before this returns. */
 int32_t cellm_llama_dev_create_from_file(const char* path, int32_t device, int32_t max_rows, int32_t max_blocks,
                                          int32_t tokens_per_block, int32_t total_blocks, cellm_llama_dev_t** out);
 

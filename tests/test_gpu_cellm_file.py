@@ -173,3 +173,150 @@ def test_runner_from_file_rejects_other_dtypes(tmp_path, model):
     write_cellm(p, header(), ts)
     with pytest.raises(CellmHipError, match="q_proj.weight is f16"):
         LlamaDevice.from_file(p, 0, max_rows=ROWS, max_blocks=CTX // TPB, tokens_per_block=TPB)
+
+
+# ---- other projection formats from a file (the runners' dtype dispatch) ----------
+
+def _q4_proj(o, i, sd):
+    """MLX affine u32 words [o, i/8] with f32 scales/biases [o, i/64] whose
+    weights q*s + b are centred and variance-preserving."""
+    wq = oracle.gen_q4_words((o, i // 8), sd)
+    base = 1.0 / (4.6 * np.sqrt(i))
+    s = (oracle.gen_uniform((o, i // 64), sd + 1, 0.5, 1.5) * base).astype(np.float32)
+    b = (-7.5 * s + oracle.gen_normal((o, i // 64), sd + 2, 0.0, 0.1 * base)).astype(np.float32)
+    return wq, s, b
+
+
+def _i4_proj(o, i, sd):
+    """cellm i4: [o, ceil(i/2)] bytes (low nibble even), one f16 scale per row."""
+    w = oracle.gen_i8((o, (i + 1) // 2), sd).view(np.uint8)
+    s = (oracle.gen_uniform((o,), sd + 1, 0.5, 1.5) / (4.6 * np.sqrt(i))).astype(np.float16)
+    return w, s
+
+
+def _mixed_model(kinds):
+    """Layer projections in the given per-projection formats ("u32", "i4",
+    "i8"); int8 embedding (tied unless kinds has an "lm" entry)."""
+    i8_layers, embed, escale, fnorm = make_model()
+    layers = []
+    for l, (ws, ss, n1, n2) in enumerate(i8_layers):
+        projs = []
+        for j, (o, i) in enumerate(shapes()):
+            kind, sd = kinds[j], 0xCF500000 + l * 64 + j * 4
+            if kind == "u32":
+                projs.append(("u32",) + _q4_proj(o, i, sd))
+            elif kind == "i4":
+                projs.append(("i4",) + _i4_proj(o, i, sd))
+            else:
+                projs.append(("i8", ws[j], ss[j]))
+        layers.append((projs, n1, n2))
+    lm = None
+    if "lm" in kinds:
+        lm = ("i4",) + _i4_proj(VOCAB, HID, 0xCF600000) if kinds["lm"] == "i4" else \
+            ("u32",) + _q4_proj(VOCAB, HID, 0xCF600000)
+    return layers, embed, escale, fnorm, lm
+
+
+def _proj_tensors(name, pr):
+    kind = pr[0]
+    if kind == "u32":
+        _, wq, s, b = pr
+        base = name[:-len(".weight")]
+        return [(name, wq, "u32", wq.shape), (base + ".scales", s, "f32", s.shape), (base + ".biases", b, "f32", b.shape)]
+    w, s = pr[1], pr[2]
+    shape = (w.shape[0], 2 * w.shape[1]) if kind == "i4" else w.shape  # i4: logical [out, in]
+    return [(name, w, kind, shape), (name + ".qscale", s, "f16", s.shape)]
+
+
+def _mixed_tensors(mm):
+    layers, embed, escale, fnorm, lm = mm
+    ts = []
+    for l, (projs, n1, n2) in enumerate(layers):
+        pre = f"model.layers.{l}."
+        for j, name in enumerate(NAMES):
+            ts += _proj_tensors(pre + name + ".weight", projs[j])
+        ts.append((pre + "input_layernorm.weight", n1, "f16", n1.shape))
+        ts.append((pre + "post_attention_layernorm.weight", n2, "f16", n2.shape))
+    ts.append(("model.embed_tokens.weight", embed, "i8", embed.shape))
+    ts.append(("model.embed_tokens.weight.qscale", escale, "f16", escale.shape))
+    ts.append(("model.norm.weight", fnorm, "f16", fnorm.shape))
+    if lm is not None:
+        ts += _proj_tensors("lm_head.weight", lm)
+    return ts
+
+
+def _oracle_proj(pr, x, o, i):
+    """The reference's linear for each format: matmul_i8_f32 (cpu_kernels.rs:66-133),
+    the LFM affine GEMV (lfm.rs:985-1066), matmul_i4_f32 with gs = in_dim
+    (cpu_kernels.rs:219-243, gemma.rs:1471)."""
+    if pr[0] == "u32":
+        return oracle.qgemv_q4_affine(pr[1], pr[2], pr[3], x.reshape(1, -1), i)[0]
+    if pr[0] == "i4":
+        return oracle.matmul_i4_f32(pr[1], pr[2].view(np.uint16), o, i, i, x)
+    return oracle.matmul_i8_f32(pr[1], pr[2].view(np.uint16), x)
+
+
+def _oracle_session(mm, kc, vc, token, pos, bt):
+    """LlamaRunner::step_inner (llama.rs:235-647) for one session over the
+    paged f16 cache (updated in place), projections by format."""
+    layers, embed, escale, fnorm, lm = mm
+    t = token % VOCAB
+    x = (embed[t].astype(np.float32) * np.float32(escale[t])).astype(np.float32)
+
+    def base_of(tpos, layer):
+        return int(bt[tpos // TPB]) * (L * TPB * KVD) + layer * (TPB * KVD) + (tpos % TPB) * KVD
+
+    for l, (projs, n1, n2) in enumerate(layers):
+        xn = oracle.rms_norm(x, n1.astype(np.float32), 1e-5)
+        q = _oracle_proj(projs[0], xn, HID, HID)
+        k = _oracle_proj(projs[1], xn, KVD, HID)
+        v = _oracle_proj(projs[2], xn, KVD, HID)
+        oracle.rope_half_(q, NH, HD, pos, 100000.0)
+        oracle.rope_half_(k, NKV, HD, pos, 100000.0)
+        wb = base_of(pos, l)
+        kc[wb:wb + KVD] = k.astype(np.float16).view(np.uint16)
+        vc[wb:wb + KVD] = v.astype(np.float16).view(np.uint16)
+        bases = np.array([base_of(tp, l) for tp in range(pos + 1)], np.uint64)
+        attn = oracle.attention_gqa_f16kv(kc, vc, bases, q, NH, NKV, HD)
+        x = x + _oracle_proj(projs[3], attn, HID, HID)
+        xn = oracle.rms_norm(x, n2.astype(np.float32), 1e-5)
+        g = np.ascontiguousarray(_oracle_proj(projs[4], xn, INTER, HID), np.float32)
+        oracle.silu_mul_(g, _oracle_proj(projs[5], xn, INTER, HID))
+        x = x + _oracle_proj(projs[6], g, HID, INTER)
+    xf = oracle.rms_norm(x, fnorm.astype(np.float32), 1e-5)
+    logits = oracle.llama_lm_head_i8(xf, embed, escale.view(np.uint16)) if lm is None else \
+        _oracle_proj(lm, xf, VOCAB, HID)
+    return oracle.argmax_first(logits), logits
+
+
+@pytest.mark.parametrize("case", ["u32", "i4", "mixed"])
+def test_runner_from_file_other_formats_match_oracle(tmp_path, case):
+    """Row a7: .cellm projections as "u32" MLX affine (+ f32 .scales/.biases,
+    as tools/convert_lfm.py writes them) and as "i4" (+ f16 .qscale), each
+    dispatched to its HIP GEMV; a mixed file also pairs an i8 gate with an i4
+    up (separate GEMVs + the SiLU kernel) and carries an i4 lm_head.  Greedy
+    ids of 4 sessions equal the oracle step's; logits within 1e-3."""
+    from cellm_amd.llama_step import LlamaDevice
+
+    kinds = {"u32": ["u32"] * 7, "i4": ["i4"] * 7,
+             "mixed": ["u32", "i4", "i8", "u32", "i8", "i4", "u32"]}[case]
+    kinds = dict(enumerate(kinds))
+    if case == "mixed":
+        kinds["lm"] = "i4"
+    mm = _mixed_model(kinds)
+    p = tmp_path / f"{case}.cellm"
+    write_cellm(p, header(tied=case != "mixed"), _mixed_tensors(mm))
+    k, v, bts = kv_state()
+    dev = LlamaDevice.from_file(p, 0, max_rows=ROWS, max_blocks=CTX // TPB, tokens_per_block=TPB)
+    try:
+        ids, logits, _, _ = run(dev, k, v, bts)
+    finally:
+        dev.close()
+    kc, vc = k.view(np.uint16).copy(), v.view(np.uint16).copy()
+    tokens = [(100 + 7919 * s) % VOCAB for s in range(ROWS)]
+    pos = [CTX - 1, 300, 64, 0]
+    for s in range(ROWS):
+        rid, rlog = _oracle_session(mm, kc, vc, tokens[s], pos[s], bts[s])
+        assert int(ids[s]) == rid, (case, s)
+        err = float(np.max(np.abs(logits[s] - rlog)) / np.max(np.abs(rlog)))
+        assert err <= 1e-3, (case, s, err)
