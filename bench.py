@@ -57,34 +57,58 @@ def parse():
                     help="time the configs[4] decode step with eager launches only (the same kernels without "
                          "HIP graph replay; for runs under rocprofv3, whose kernel tracer fails on graph launches)")
     ap.add_argument("--no-extra", action="store_true", help="skip the extra configs")
-    ap.add_argument("--pmc-sample", action="store_true",
-                    help="run only a 256 MiB device copy (counter calibration) and 20 lm_head GEMVs, for "
-                         "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes")
+    ap.add_argument("--pmc-sample", nargs="?", const="lm_head_q4", default=None,
+                    choices=["lm_head_q4", "lm_head_i8_m64", "qgemm_896x4864", "qgemm_4864x896"],
+                    help="run only a 256 MiB device copy (counter calibration) and 20 launches of one kernel "
+                         "(default: the q4 lm_head GEMV), for rocprofv3 --pmc passes")
     return ap.parse_args()
 
 
-def pmc_sample(torch, ops, stream, gen):
-    """Workload of the traffic measurement: the plain copy whose counters
-    calibrate FETCH_SIZE / WRITE_SIZE against known bytes, then the dominant
-    kernel on rotating weight copies."""
+def pmc_sample(torch, ops, stream, gen, which: str):
+    """Workload of a counter pass: the plain copy whose counters calibrate
+    FETCH_SIZE / WRITE_SIZE against known bytes, then 20 launches of one
+    kernel (weights on rotating copies for the GEMVs)."""
     nbytes = 256 * 2**20
     src = torch.randn(nbytes // 4, device="cuda", generator=gen)
     dst = torch.empty_like(src)
     for _ in range(3):
         dst.copy_(src)
     torch.cuda.synchronize()
-    k, n = 896, 151936
-    copies = 8
-    ws = [Q4Weights(torch, n, k, gen) for _ in range(copies)]
-    x = torch.randn((1, k), device="cuda", generator=gen).to(torch.float16)
-    y = torch.empty((1, n), dtype=torch.float32, device="cuda")
-    arr = op_array([ops.qgemv_op_q4_affine(ws[i % copies].wq, ws[i % copies].s, ws[i % copies].b, x, y)
-                    for i in range(20)])
-    ops.encode_qgemv_batch(arr, stream=stream.cuda_stream)
+    del src, dst
+    info = {"copy_bytes_read": nbytes, "copy_bytes_written": nbytes, "copy_launches": 3, "workload": which,
+            "launches": 20}
+    if which == "lm_head_q4":
+        k, n, copies = 896, 151936, 8
+        ws = [Q4Weights(torch, n, k, gen) for _ in range(copies)]
+        x = torch.randn((1, k), device="cuda", generator=gen).to(torch.float16)
+        y = torch.empty((1, n), dtype=torch.float32, device="cuda")
+        arr = op_array([ops.qgemv_op_q4_affine(ws[i % copies].wq, ws[i % copies].s, ws[i % copies].b, x, y)
+                        for i in range(20)])
+        ops.encode_qgemv_batch(arr, stream=stream.cuda_stream)
+        info.update({"kernel": "qgemv_q4_flat_kernel (q4 affine 896->151936, M=1)",
+                     "algorithmic_bytes": q4_bytes(1, n, k)})
+    elif which == "lm_head_i8_m64":
+        k, n, m, copies = 1152, 262144, 64, 2
+        w = torch.randint(-127, 128, (copies, n, k), dtype=torch.int8, device="cuda", generator=gen)
+        sc = torch.rand((n,), device="cuda", generator=gen) * 0.019 + 0.001
+        x = torch.randn((m, k), device="cuda", generator=gen).to(torch.float16)
+        y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        arr = op_array([ops.qgemv_op_i8(w[i % copies], sc, x, y) for i in range(20)])
+        ops.encode_qgemv_batch(arr, stream=stream.cuda_stream)
+        info.update({"kernel": "qgemv_mfma_kernel (int8 1152->262144, M=64)",
+                     "algorithmic_bytes": i8_bytes(m, n, k, 2)})
+    else:
+        k, n = (896, 4864) if which == "qgemm_896x4864" else (4864, 896)
+        m = 512
+        w = Q4Weights(torch, n, k, gen)
+        x = torch.randn((m, k), device="cuda", generator=gen).to(torch.float16)
+        y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        for _ in range(20):
+            ops.encode_qgemm_q4_affine(w.wq, w.s, w.b, x, y, stream=stream.cuda_stream)
+        info.update({"kernel": f"qgemm_q4_regw_kernel (M=512, {k}->{n})", "flops": 2 * m * n * k,
+                     "algorithmic_bytes": q4_bytes(m, n, k)})
     torch.cuda.synchronize()
-    print(json.dumps({"pmc_sample": {"copy_bytes_read": nbytes, "copy_bytes_written": nbytes, "copy_launches": 3,
-                                     "gemv": "q4 affine 896->151936, M=1", "gemv_launches": 20,
-                                     "gemv_algorithmic_bytes": q4_bytes(1, n, k)}}))
+    print(json.dumps({"pmc_sample": info}))
 
 
 class Q4Weights:
@@ -158,7 +182,7 @@ def main():
     gen = torch.Generator(device="cuda")
     gen.manual_seed(0xCE11)
     if args.pmc_sample:
-        pmc_sample(torch, ops, stream, gen)
+        pmc_sample(torch, ops, stream, gen, args.pmc_sample)
         ops.close()
         return
 
@@ -474,13 +498,40 @@ def decode_step_cfg5(graphs: bool = True):
     return res
 
 
-def cpu_baseline():
-    """The CPU oracle timed on the host cores on a bounded sample of the step.
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
-    Reference CPU work per decode token for configs[1] (LfmRunner, lfm.rs):
-    the four linear projections hit the f32 dequant cache and run the f32 row
-    GEMV (lfm.rs:1056-1063, 'warm'); the tied lm_head dequantizes on the fly
-    (lfm.rs:700-741).  Timed over a few such passes.
+
+def _median_time(fn, budget_s: float, max_reps: int = 50, min_reps: int = 3) -> tuple[float, int]:
+    """Median seconds per call after one warm-up call, within about budget_s."""
+    fn()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < min_reps or (time.perf_counter() < t_end and len(times) < max_reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2], len(times)
+
+
+def cpu_baseline():
+    """The CPU oracle (a C restatement of the reference CPU kernels, OpenMP over
+    rows as rayon does) on the host cores, on bounded samples of the workloads.
+
+    `value` is configs[1]'s decode pass as the reference runs it per token
+    (LfmRunner, lfm.rs): the four projections hit the f32 dequant cache and run
+    the f32 row GEMV ('warm', lfm.rs:1056-1063); the tied lm_head dequantizes on
+    the fly (lfm.rs:700-741).  `legs` time the other reference paths BASELINE
+    names: the same pass 'cold' (the f32 dequant of each projection included,
+    lfm.rs:1012-1026), matmul_i8_f32 at configs[0] (cpu_kernels.rs:66-133), the
+    configs[2] int8 lm_head row GEMV, and matmul_f32 at configs[3]'s M = 512
+    over the dequantized weight (cpu_kernels.rs:36-63).
     """
     import numpy as np
 
@@ -488,36 +539,70 @@ def cpu_baseline():
 
     threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or (os.cpu_count() or 1)
     rng = np.random.default_rng(0xCE11)
-    lin = []
-    for name, k, n in QWEN_SHAPES[:-1]:
+
+    def q4(n, k):
         wq = rng.integers(0, 2**32, (n, k // 8), dtype=np.uint32)
         s = (np.abs(rng.normal(0.02, 0.005, (n, k // 64)))).astype(np.float32)
         b = rng.normal(0.0, 0.05, (n, k // 64)).astype(np.float32)
-        lin.append((oracle.q4_affine_dequant_f32(wq, s, b, k), rng.normal(size=k).astype(np.float32)))
+        return wq, s, b
+
+    lin_q = [(k, n) + q4(n, k) for _, k, n in QWEN_SHAPES[:-1]]
+    lin = [(oracle.q4_affine_dequant_f32(wq, s, b, k), rng.normal(size=k).astype(np.float32)) for k, n, wq, s, b in lin_q]
     k, n = 896, 151936
-    wq = rng.integers(0, 2**32, (n, k // 8), dtype=np.uint32)
-    s = (np.abs(rng.normal(0.02, 0.005, (n, k // 64)))).astype(np.float32)
-    b = rng.normal(0.0, 0.05, (n, k // 64)).astype(np.float32)
+    wq, s, b = q4(n, k)
     x = rng.normal(size=k).astype(np.float32)
 
-    def one_pass():
+    def warm_pass():
         for w32, xv in lin:
             oracle.matmul_f32(w32, xv.reshape(-1, 1))
         oracle.lfm_lm_head_q4_affine(wq, s, b, x, n, k)
 
-    one_pass()
-    times = []
-    t_end = time.perf_counter() + 10.0
-    while time.perf_counter() < t_end and len(times) < 50:
-        t0 = time.perf_counter()
-        one_pass()
-        times.append(time.perf_counter() - t0)
-    med = sorted(times)[len(times) // 2]
+    def cold_pass():
+        for (kk, _, wq_, s_, b_), (_, xv) in zip(lin_q, lin):
+            oracle.matmul_f32(oracle.q4_affine_dequant_f32(wq_, s_, b_, kk), xv.reshape(-1, 1))
+        oracle.lfm_lm_head_q4_affine(wq, s, b, x, n, k)
+
     step_bytes = sum(q4_bytes(1, n_, k_) for _, k_, n_ in QWEN_SHAPES)
+    med, reps = _median_time(warm_pass, 6.0)
+    legs = {}
+    cmed, creps = _median_time(cold_pass, 4.0, max_reps=20)
+    legs["cfg2_q4_affine_step_cold"] = {"ms": round(cmed * 1e3, 3), "GB/s": round(step_bytes / cmed / 1e9, 3),
+                                        "reps": creps}
+    for n1 in (576, 1536):
+        k1 = 576
+        w8 = rng.integers(-127, 128, (n1, k1), dtype=np.int8)
+        s8 = rng.uniform(1e-3, 2e-2, n1).astype(np.float32)
+        x8 = rng.normal(size=(1, k1)).astype(np.float32)
+        t, r = _median_time(lambda: oracle.qgemv_i8(w8, s8, x8), 1.0)
+        legs[f"cfg1_i8_576x{n1}"] = {"us": round(t * 1e6, 2), "GB/s": round(i8_bytes(1, n1, k1, 4) / t / 1e9, 3),
+                                     "reps": r}
+    kg, ng = 1152, 262144
+    wg = rng.integers(-127, 128, (ng, kg), dtype=np.int8)
+    sg = rng.uniform(1e-3, 2e-2, ng).astype(np.float32)
+    xg = rng.normal(size=(1, kg)).astype(np.float16)
+    t, r = _median_time(lambda: oracle.qgemv_i8(wg, sg, xg), 3.0, max_reps=20)
+    legs["cfg3_i8_lm_head_1152x262144_m1"] = {"ms": round(t * 1e3, 3),
+                                              "GB/s": round(i8_bytes(1, ng, kg, 2) / t / 1e9, 3), "reps": r}
+    del wg
+    for k4, n4 in ((896, 4864), (4864, 896)):
+        wq4, s4, b4 = q4(n4, k4)
+        w32t = np.ascontiguousarray(oracle.q4_affine_dequant_f32(wq4, s4, b4, k4).T)  # [K, N] as matmul_f32 takes b
+        a = rng.normal(size=(512, k4)).astype(np.float32)
+        out = np.zeros((512, n4), np.float32)
+
+        def gemm():
+            out.fill(0.0)
+            oracle.matmul_f32(a, w32t, out)
+
+        t, r = _median_time(gemm, 3.0, max_reps=10)
+        legs[f"cfg4_matmul_f32_m512_{k4}x{n4}"] = {"ms": round(t * 1e3, 3),
+                                                  "GFLOP/s": round(2.0 * 512 * n4 * k4 / t / 1e9, 2), "reps": r}
     return {"value": round(step_bytes / med / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "ms_per_step": round(med * 1e3, 3),
-            "sample": f"{len(times)} decode passes over the 5 configs[1] projections (4 warm f32-cache GEMVs + "
-                      "on-the-fly affine lm_head, lfm.rs:700-741,1056-1063), median; C oracle, OpenMP over rows"}
+            "ms_per_step": round(med * 1e3, 3), "cpu_model": _cpu_model(), "nproc": os.cpu_count(),
+            "sample": f"{reps} decode passes over the 5 configs[1] projections (4 warm f32-cache GEMVs + "
+                      "on-the-fly affine lm_head, lfm.rs:700-741,1056-1063), median; C oracle, OpenMP over rows; "
+                      "legs: medians of the named reference paths at their full sizes",
+            "legs": legs}
 
 
 if __name__ == "__main__":

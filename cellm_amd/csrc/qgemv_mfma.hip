@@ -43,6 +43,10 @@ namespace cellm {
 namespace {
 
 constexpr int kBlock = 256;
+#ifndef CELLM_MFMA_XPAD
+#define CELLM_MFMA_XPAD 8
+#endif
+constexpr int kXPad = CELLM_MFMA_XPAD;  // halves of padding after each staged X row
 constexpr int kRowRor8 = 0x128;  // DPP control: rotate by 8 within each 16-lane row
 
 // Permutation of one 8-element x word into the unpack order.
@@ -89,11 +93,11 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
     const _Float16* __restrict__ X, const float* __restrict__ bias, float* __restrict__ Y, int M, int N, int K, int KC,
     int ntiles)
 {
-    extern __shared__ __align__(16) _Float16 xs[];  // [MS*16][KC + 8]
+    extern __shared__ __align__(16) _Float16 xs[];  // [MS*16][KC + kXPad]
     constexpr int KB = WT == 1 ? 64 : 128;  // K per block: 64 bytes of every row
     constexpr int TSTEPS = KB / 32;         // MFMA k-steps per block
     constexpr int ROWS = (BT / 64) * NT * 16;
-    const int stride = KC + 8;
+    const int stride = KC + kXPad;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int rl = lane & 15, g = lane >> 4;
     const int nkb = K / KB;
@@ -360,7 +364,7 @@ hipError_t launch_mfma_nt(const void* W, const void* S, const void* B, int per_c
         // int8: 1024 threads, 16 waves of one W tile each (two tiles per wave need more than the 128
         // registers per lane a 1024-thread block leaves, and 8 waves of two tiles stream 12 % slower:
         // measured).  q4 (its dequant needs more registers): 512 threads.
-        const size_t whole = (size_t)MS * 16 * (K + 8) * 2;
+        const size_t whole = (size_t)MS * 16 * (K + kXPad) * 2;
         if (whole > 80 * 1024 && whole <= kWholeXLds) {
             constexpr int BT = WT == 1 ? 1024 : 512, DEPTH = 2, ROWS = (BT / 64) * NT * 16;
             auto kern = qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, false, BT>;
@@ -382,9 +386,9 @@ hipError_t launch_mfma_nt(const void* W, const void* S, const void* B, int per_c
     constexpr int ROWS = (kBlock / 64) * NT * 16;
     // X in LDS: at most 80 KB per block so two blocks share a CU; the whole K
     // when it fits, else chunks of KC columns (a multiple of the K block)
-    int KC = std::max(1, (80 * 1024 / (MS * 16 * 2) - 8) / (2 * DEPTH * KB)) * (2 * DEPTH * KB);
+    int KC = std::max(1, (80 * 1024 / (MS * 16 * 2) - kXPad) / (2 * DEPTH * KB)) * (2 * DEPTH * KB);
     if (KC >= K) KC = K;
-    const size_t lds = (size_t)MS * 16 * (KC + 8) * 2;
+    const size_t lds = (size_t)MS * 16 * (KC + kXPad) * 2;
     const int ntiles = (N + ROWS - 1) / ROWS;
     if (KC < K) {
         auto kern = qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, true>;
@@ -406,7 +410,7 @@ hipError_t launch_mfma_ms(const void* W, const void* S, const void* B, int per_c
 {
     // two 16-row W tiles per wave when there are rows enough to fill the chip, unless X needs the
     // one-block-per-CU form (one tile per wave there)
-    const size_t whole = (size_t)MS * 16 * (K + 8) * 2;
+    const size_t whole = (size_t)MS * 16 * (K + kXPad) * 2;
     const bool whole_x = MS == 4 && whole > 80 * 1024 && whole <= kWholeXLds;
     if (N >= 128 * 512 && !whole_x)
         return launch_mfma_nt<WT, MS, 2, SBT>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, st);
