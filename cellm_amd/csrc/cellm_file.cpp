@@ -420,9 +420,14 @@ int32_t cellm_file_open(const char* path, cellm_file_t** out)
         }
         e.offset_bytes = off;
         e.nbytes = nb;
-        if (!f->by_name.emplace(name->str, f->tensors.size()).second)
-            return fail(CELLM_HIP_ERR_INVALID_ARG, "cellm header: duplicate tensor %s", name->str.c_str());
-        f->tensors.push_back(e);
+        // A name seen again replaces the earlier entry (cellm_file.rs:89-92 builds
+        // its index with HashMap::insert, so the last entry wins); every entry,
+        // shadowed or not, has passed the range check above.
+        const auto ins = f->by_name.emplace(name->str, f->tensors.size());
+        if (ins.second)
+            f->tensors.push_back(e);
+        else
+            f->tensors[ins.first->second] = e;
     }
     // one read per 4 KiB page brings the file into the page cache now
     (void)madvise(m, f->size, MADV_WILLNEED);

@@ -79,7 +79,6 @@ def _raw(p, text: bytes, tail: bytes = b"", magic=b"CELLM", version=1, hlen=None
     ("no_tensors", "tensors missing"),
     ("missing_field", "hidden_dim missing"),
     ("range", "out of range"),
-    ("dup", "duplicate tensor"),
     ("bad_shape", "bad shape"),
 ])
 def test_rejects_malformed_files(tmp_path, CellmFile, case, needle):
@@ -108,8 +107,6 @@ def test_rejects_malformed_files(tmp_path, CellmFile, case, needle):
         _raw(p, json.dumps(h).encode())
     elif case == "range":
         _raw(p, json.dumps(dict(good, tensors=[dict(t, nbytes=1 << 20)])).encode(), b"\0" * 128)
-    elif case == "dup":
-        _raw(p, json.dumps(dict(good, tensors=[t, t])).encode(), b"\0" * 128)
     elif case == "bad_shape":
         _raw(p, json.dumps(dict(good, tensors=[dict(t, shape=[-1])])).encode(), b"\0" * 128)
     with pytest.raises(CellmHipError, match=needle):
@@ -126,3 +123,32 @@ def test_missing_path_and_unknown_tensor(tmp_path, CellmFile):
     with CellmFile(p) as f:
         with pytest.raises(CellmHipError, match="unknown tensor"):
             f.tensor_bytes("b")
+
+
+def test_duplicate_name_keeps_last_entry(tmp_path, CellmFile):
+    """cellm_file.rs:89-92 indexes tensors with HashMap::insert: a repeated name
+    resolves to its last entry, and every entry is still range-checked."""
+    from cellm_amd._lib import CellmHipError
+
+    good = llama_header(1, 8, 2, 2, 16, 10)
+    payload = bytes(range(128))
+    first = {"name": "w", "offset_bytes": 0, "nbytes": 8, "shape": [8], "dtype": "i8"}
+    other = {"name": "v", "offset_bytes": 16, "nbytes": 4, "shape": [4], "dtype": "u8"}
+    last = {"name": "w", "offset_bytes": 32, "nbytes": 16, "shape": [4, 4], "dtype": "u8"}
+    base = 10 + 4096  # header padded with spaces to 4096 bytes, so offsets are known up front
+    for t in (first, other, last):
+        t["offset_bytes"] += base
+    p = tmp_path / "dup.cellm"
+    text = json.dumps(dict(good, tensors=[first, other, last])).encode()
+    assert len(text) <= 4096
+    _raw(p, text.ljust(4096), payload)
+    with CellmFile(p) as f:
+        assert [t.name for t in f.tensors] == ["w", "v"]
+        w = f.tensors[0]
+        assert (w.offset_bytes, w.nbytes, list(w.shape), w.dtype) == (base + 32, 16, [4, 4], "u8")
+        np.testing.assert_array_equal(f.tensor_bytes("w"), np.frombuffer(payload[32:48], np.uint8))
+    # a shadowed entry that points past the end still fails the load
+    bad = dict(first, nbytes=1 << 20)
+    _raw(p, json.dumps(dict(good, tensors=[bad, last])).encode().ljust(4096), payload)
+    with pytest.raises(CellmHipError, match="out of range"):
+        CellmFile(p)
