@@ -333,6 +333,7 @@ def extra_configs(torch, ops, stream, gen, graphs: bool = True):
 
     res.update(decode_step_cfg5(graphs))
     res.update(lowbit_gemvs(torch, ops, stream, gen))
+    res.update(i4_gemma_mlp(torch, ops, stream, gen))
 
     # M=512 prefill qGEMM (MFMA)
     m = 512
@@ -420,6 +421,29 @@ def lowbit_gemvs(torch, ops, stream, gen):
         b = wbytes + sbytes + 2 * k + 4 * n
         res[f"lowbit_{fmt}_{k}x{n}"] = {"us": round(ms * 1e3, 2), "GB/s": round(b / (ms * 1e-3) / 1e9, 1),
                                          "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        del w
+    return res
+
+
+def i4_gemma_mlp(torch, ops, stream, gen):
+    """Gemma-3-1B MLP in the reference's symmetric i4 format (gemma.rs:1446-1471:
+    one f16 scale per row, gs = in_dim, f32 activations): gate/up 1152->6912
+    and down 6912->1152 at M in {1, 4}.  Weight copies rotate past 512 MB.
+    Bytes per call: weights + row scales + x + y."""
+    res = {}
+    for k, n in ((1152, 6912), (6912, 1152)):
+        wbytes = n * k // 2
+        copies = max(2, -(-512 * 2**20 // wbytes) + 1)
+        w = torch.randint(0, 256, (copies, n, k // 2), dtype=torch.uint8, device="cuda", generator=gen)
+        s = (torch.rand((n,), device="cuda", generator=gen) * 0.019 + 0.001).to(torch.float16)
+        for m in (1, 4):
+            x = torch.randn((m, k), device="cuda", generator=gen)
+            y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+            arr = op_array([ops.qgemv_op_i4_sym(w[i % copies], s, k, x, y, k) for i in range(100)])
+            ms = time_batch(torch, ops, arr, stream)
+            b = wbytes + 2 * n + 4 * m * k + 4 * m * n
+            res[f"gemma_i4_{k}x{n}_m{m}"] = {"us": round(ms * 1e3, 2), "GB/s": round(b / (ms * 1e-3) / 1e9, 1),
+                                              "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
         del w
     return res
 

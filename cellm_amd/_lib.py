@@ -21,7 +21,7 @@ DTYPE_F32, DTYPE_F16, DTYPE_BF16 = 0, 1, 2
 
 _vp, _sz, _i32, _i64 = C.c_void_p, C.c_size_t, C.c_int32, C.c_int64
 
-OP_QGEMV_I8, OP_QGEMV_Q4_AFFINE, OP_QGEMV_F16, OP_QGEMV_I2, OP_QGEMV_Q1_0_G128 = 0, 1, 2, 3, 4
+OP_QGEMV_I8, OP_QGEMV_Q4_AFFINE, OP_QGEMV_F16, OP_QGEMV_I2, OP_QGEMV_Q1_0_G128, OP_QGEMV_I4_SYM = 0, 1, 2, 3, 4, 5
 
 
 class QgemvOp(C.Structure):

@@ -625,6 +625,9 @@ int32_t cellm_hip_qgemv_q4_affine(cellm_hip_ctx_t* ctx, const uint32_t* wq, cons
     CELLM_API_END(report_exception)
 }
 
+static int32_t qgemv_i4_impl(const uint8_t* w, const uint16_t* scales_f16, int64_t n_scales, int64_t gs,
+                             const void* x, int32_t x_dtype, float* y, int64_t m, int64_t n, int64_t k, hipStream_t st);
+
 int32_t cellm_hip_qgemv_batch(cellm_hip_ctx_t* ctx, const cellm_hip_qgemv_op_t* ops, int64_t n_ops, void* stream)
 {
     CELLM_API_BEGIN
@@ -649,6 +652,9 @@ int32_t cellm_hip_qgemv_batch(cellm_hip_ctx_t* ctx, const cellm_hip_qgemv_op_t* 
                                    o.m, o.n, o.k, st);
         else if (o.kind == CELLM_HIP_OP_QGEMV_Q1_0_G128)
             rc = qgemv_lowbit_impl(LB_Q1, o.w, nullptr, 0, o.x, o.x_dtype, o.y, o.m, o.n, o.k, st);
+        else if (o.kind == CELLM_HIP_OP_QGEMV_I4_SYM)
+            rc = qgemv_i4_impl(static_cast<const uint8_t*>(o.w), static_cast<const uint16_t*>(o.scales), o.n_scales,
+                               o.group, o.x, o.x_dtype, o.y, o.m, o.n, o.k, st);
         else
             rc = set_error(CELLM_HIP_ERR_INVALID_ARG, "op %lld: unknown kind %d", (long long)i, (int)o.kind);
         if (rc) return rc;
@@ -705,12 +711,9 @@ int32_t cellm_hip_qgemv_q4_affine_gate_up_silu(cellm_hip_ctx_t* ctx, const uint3
     CELLM_API_END(report_exception)
 }
 
-int32_t cellm_hip_qgemv_i4_sym(cellm_hip_ctx_t* ctx, const uint8_t* w, const uint16_t* scales_f16, int64_t n_scales,
-                               int64_t gs, const void* x, int32_t x_dtype, float* y, int64_t m, int64_t n, int64_t k,
-                               void* stream)
+static int32_t qgemv_i4_impl(const uint8_t* w, const uint16_t* scales_f16, int64_t n_scales, int64_t gs,
+                             const void* x, int32_t x_dtype, float* y, int64_t m, int64_t n, int64_t k, hipStream_t st)
 {
-    CELLM_API_BEGIN
-    if (int32_t rc = check_ctx(ctx)) return rc;
     if (int32_t rc = check_dims(m, n, k)) return rc;
     if (!valid_dtype(x_dtype)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "bad dtype");
     if (m == 0 || n == 0) return CELLM_HIP_OK;
@@ -721,11 +724,19 @@ int32_t cellm_hip_qgemv_i4_sym(cellm_hip_ctx_t* ctx, const uint8_t* w, const uin
         return set_error(CELLM_HIP_ERR_INVALID_ARG, "scale index (k-1)/gs=%lld out of range spr=%lld",
                          (long long)((k - 1) / gs), (long long)spr);
     if ((k > 0 && (!w || !scales_f16 || !x)) || !y) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null pointer");
-    DeviceGuard g(ctx->device);
-    HIP_TRY(launch_qgemv_i4_sym(w, scales_f16, (int)spr, (int)gs, x, x_dtype, y, (int)m, (int)n, (int)k,
-                                pick_stream(ctx, stream)),
+    HIP_TRY(launch_qgemv_i4_sym(w, scales_f16, (int)spr, (int)gs, x, x_dtype, y, (int)m, (int)n, (int)k, st),
             "qgemv_i4_sym launch");
     return CELLM_HIP_OK;
+}
+
+int32_t cellm_hip_qgemv_i4_sym(cellm_hip_ctx_t* ctx, const uint8_t* w, const uint16_t* scales_f16, int64_t n_scales,
+                               int64_t gs, const void* x, int32_t x_dtype, float* y, int64_t m, int64_t n, int64_t k,
+                               void* stream)
+{
+    CELLM_API_BEGIN
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    DeviceGuard g(ctx->device);
+    return qgemv_i4_impl(w, scales_f16, n_scales, gs, x, x_dtype, y, m, n, k, pick_stream(ctx, stream));
     CELLM_API_END(report_exception)
 }
 

@@ -60,39 +60,6 @@ __global__ __launch_bounds__(kBlock) void dequant_q4_affine_kernel(const uint32_
     }
 }
 
-// Symmetric i4, one wave per output row; element formula of
-// cpu_kernels.rs:234-240: w = (nib - 8) * scale[j / gs] (exact in f32).
-template <int XT>
-__global__ __launch_bounds__(kBlock) void qgemv_i4_sym_kernel(const uint8_t* __restrict__ w,
-                                                              const uint16_t* __restrict__ S, int spr, int gs,
-                                                              const void* __restrict__ x, float* __restrict__ y,
-                                                              int M, int N, int K)
-{
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int n = blockIdx.x * (kBlock / 64) + wave;
-    if (n >= N) return;
-    const int row_stride = (K + 1) >> 1;
-    const uint8_t* row = w + (size_t)n * row_stride;
-    const uint16_t* rs = S + (size_t)n * spr;
-    for (int m = 0; m < M; ++m) {
-        float acc = 0.0f;
-        for (int bi = lane; bi < row_stride; bi += 64) {
-            const uint32_t byte = row[bi];
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const int j = 2 * bi + h;
-                if (j < K) {
-                    const int q = (int)((byte >> (4 * h)) & 0xFu) - 8;
-                    const float s = load_f32<DT_F16>(rs, (size_t)(j / gs));
-                    acc = __builtin_fmaf((float)q * s, load_f32<XT>(x, (size_t)m * K + j), acc);
-                }
-            }
-        }
-        acc = group_sum<64>(acc);
-        if (lane == 0) y[(size_t)m * N + n] = acc;
-    }
-}
-
 __global__ void add_f32_kernel(const float* a, const float* b, float* out, int n)
 {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -128,19 +95,6 @@ hipError_t launch_dequant_q4_affine(const uint32_t* wq, const void* S, const voi
     else if (sbt == DT_F16) { if (f16) CELLM_DQ(DT_F16, 1); else CELLM_DQ(DT_F16, 0); }
     else { if (f16) CELLM_DQ(DT_BF16, 1); else CELLM_DQ(DT_BF16, 0); }
 #undef CELLM_DQ
-    return hipGetLastError();
-}
-
-hipError_t launch_qgemv_i4_sym(const uint8_t* w, const uint16_t* S, int spr, int gs, const void* x, int xdt, float* y,
-                               int M, int N, int K, hipStream_t st)
-{
-    const dim3 grid((N + 3) / 4);
-    if (xdt == DT_F32)
-        hipLaunchKernelGGL((qgemv_i4_sym_kernel<DT_F32>), grid, dim3(kBlock), 0, st, w, S, spr, gs, x, y, M, N, K);
-    else if (xdt == DT_F16)
-        hipLaunchKernelGGL((qgemv_i4_sym_kernel<DT_F16>), grid, dim3(kBlock), 0, st, w, S, spr, gs, x, y, M, N, K);
-    else
-        hipLaunchKernelGGL((qgemv_i4_sym_kernel<DT_BF16>), grid, dim3(kBlock), 0, st, w, S, spr, gs, x, y, M, N, K);
     return hipGetLastError();
 }
 

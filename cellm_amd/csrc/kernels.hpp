@@ -18,7 +18,8 @@ hipError_t launch_qgemv_q4_affine(const uint32_t* wq, const void* S, const void*
                                   int force_generic);
 int qgemv_q4_lds_bytes(int M, int K);
 
-// Symmetric i4 (u8 bytes, low nibble = even element, (nib-8)*scale).
+// Symmetric i4 (u8 bytes, low nibble = even element, (nib-8)*scale); team kernel for K % 32 == 0,
+// per-row or 32-multiple groups, M <= 4; one wave per row otherwise.
 hipError_t launch_qgemv_i4_sym(const uint8_t* w, const uint16_t* S, int spr, int gs, const void* x, int xdt, float* y,
                                int M, int N, int K, hipStream_t st);
 

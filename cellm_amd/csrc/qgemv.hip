@@ -32,6 +32,7 @@
 
 #include "common.hpp"
 #include "kernels.hpp"
+#include "launch_util.hpp"
 
 namespace cellm {
 
@@ -850,6 +851,217 @@ __global__ __launch_bounds__(kBlock) void qgemv_i8_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Symmetric i4: y[m,n] = sum_k (nib[n,k] - 8) * s[n, k / gs] * x[m,k]
+// (cpu_kernels.rs:219-243 matmul_i4_f32, gemma.rs:1446-1471 with gs = in_dim).
+// A row is K/2 bytes, element 2b in the low nibble of byte b and 2b+1 in the
+// high one, so a little-endian u32 holds elements 0..7 in nibble order.  A
+// 16-byte chunk is 32 elements and chunks go to team lanes as in the int8
+// kernel.  x is staged in LDS as f32 (f16 x widened exactly) together with
+// 8 * sum(x) per chunk.  A chunk's dot is sum(nib * x) - 8 * sum(x): the
+// 0x0F0F0F0F-masked word and its 4-bit shift give the nibbles as bytes, and
+// v_cvt_f32_ubyteN turns each into f32 (3 ops per 8 nibbles); nib * x is exact
+// and every sum is f32, so the difference from the reference is its summation
+// order.  One scale per row (gs >= K) scales the row sum once; smaller groups
+// (gs % 32 == 0) scale each chunk sum by its group's scale.
+// ---------------------------------------------------------------------------
+
+// x words of i8_load_x -> LDS: xs [MT][K] f32, cx [MT][K/32] = 8 * sum over the chunk.
+// Units past the first XW per thread are moved in rounds of XW: all loads of a
+// round are issued before any is stored, so a round costs one L2 round trip.
+template <int MT, int XT, int XW>
+__device__ __forceinline__ void i4_stage_x(const u4_t (&xr)[XW], const void* __restrict__ xv, int M, int K,
+                                           float* xs, float* cx)
+{
+    constexpr int unit = XT == DT_F16 ? 8 : 4;
+    constexpr int upc = 32 / unit;  // units per chunk, in adjacent lanes
+    const int units = K / unit;
+    const int total = MT * units;
+    auto put = [&](const u4_t raw, int idx) {
+        const bool valid = idx < total;
+        float s = 0.0f;
+        if constexpr (XT == DT_F16) {
+            const h8_t v = __builtin_bit_cast(h8_t, raw);
+            const f4_t a = {(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+            const f4_t b = {(float)v[4], (float)v[5], (float)v[6], (float)v[7]};
+            s = ((a[0] + a[1]) + (a[2] + a[3])) + ((b[0] + b[1]) + (b[2] + b[3]));
+            if (valid) {
+                *reinterpret_cast<f4_t*>(xs + (size_t)idx * 8) = a;
+                *reinterpret_cast<f4_t*>(xs + (size_t)idx * 8 + 4) = b;
+            }
+        } else {
+            const f4_t a = __builtin_bit_cast(f4_t, raw);
+            s = (a[0] + a[1]) + (a[2] + a[3]);
+            if (valid) *reinterpret_cast<f4_t*>(xs + (size_t)idx * 4) = a;
+        }
+        s = group_sum<upc>(s);
+        if (valid && idx % upc == 0) cx[idx / upc] = 8.0f * s;
+    };
+#pragma unroll
+    for (int j = 0; j < XW; ++j) put(xr[j], (int)threadIdx.x + j * kBlock);
+    for (int b0 = XW * kBlock; b0 < total; b0 += XW * kBlock) {
+        u4_t rr[XW];
+#pragma unroll
+        for (int j = 0; j < XW; ++j) {
+            const int ic = min(b0 + j * kBlock + (int)threadIdx.x, total - 1);
+            const int mi = ic / units;
+            const char* base = reinterpret_cast<const char*>(xv) +
+                               ((size_t)min(mi, M - 1) * K + (size_t)(ic - mi * units) * unit) * (XT == DT_F16 ? 2 : 4);
+            rr[j] = *reinterpret_cast<const u4_t*>(base);
+        }
+#pragma unroll
+        for (int j = 0; j < XW; ++j) put(rr[j], b0 + j * kBlock + (int)threadIdx.x);
+    }
+}
+
+// sum over one chunk of nib * x (32 elements, x at xp)
+__device__ __forceinline__ float i4_chunk_dot(const u4_t w, const float* xp, float d)
+{
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const f4_t xa = *reinterpret_cast<const f4_t*>(xp + 8 * t);
+        const f4_t xb = *reinterpret_cast<const f4_t*>(xp + 8 * t + 4);
+        const uint32_t lo = w[t] & 0x0F0F0F0Fu, hi = (w[t] >> 4) & 0x0F0F0F0Fu;
+        d = __builtin_fmaf(cvt_ubyte<0>(lo), xa[0], d);
+        d = __builtin_fmaf(cvt_ubyte<0>(hi), xa[1], d);
+        d = __builtin_fmaf(cvt_ubyte<1>(lo), xa[2], d);
+        d = __builtin_fmaf(cvt_ubyte<1>(hi), xa[3], d);
+        d = __builtin_fmaf(cvt_ubyte<2>(lo), xb[0], d);
+        d = __builtin_fmaf(cvt_ubyte<2>(hi), xb[1], d);
+        d = __builtin_fmaf(cvt_ubyte<3>(lo), xb[2], d);
+        d = __builtin_fmaf(cvt_ubyte<3>(hi), xb[3], d);
+    }
+    return d;
+}
+
+// cpg = 0: one scale per row (the row's first); else chunk c is scaled by S[n * spr + c / cpg],
+// cpg = gs / 32 chunks per group.
+template <int LPR, int R, int MT, int XT, bool MP>
+__global__ __launch_bounds__(kBlock) void qgemv_i4_kernel(const u4_t* __restrict__ w4, const uint16_t* __restrict__ S,
+                                                          int spr, int cpg, const void* __restrict__ xv,
+                                                          float* __restrict__ y, int M, int N, int K)
+{
+    extern __shared__ __align__(16) uint32_t lds[];
+    const int CPR = K >> 5;
+    const int team = threadIdx.x / LPR;
+    const int lane = threadIdx.x % LPR;
+    const int row0 = (blockIdx.x * (kBlock / LPR) + team) * R;
+    float* xs = reinterpret_cast<float*>(lds);
+    float* cx = xs + (size_t)MT * K;
+
+    constexpr int XW = MT == 1 ? 4 : 8;
+    u4_t xr[XW];
+    i8_load_x<MT, XT, XW>(xv, M, K, xr);
+    u4_t wa[kUnroll][R];
+    load_pass_i8<LPR, R>(w4, row0, lane, N, CPR, wa);
+    const uint16_t* rs[R];
+    uint32_t s0[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        rs[r] = S + (size_t)min(row0 + r, N - 1) * spr;
+        s0[r] = load_raw<DT_F16>(rs[r], 0);
+    }
+    i4_stage_x<MT, XT, XW>(xr, xv, M, K, xs, cx);
+    __syncthreads();
+    if (row0 >= N) return;
+
+    float acc[R][MT];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[r][m] = 0.0f;
+    auto compute = [&](int c0, const u4_t(&wv)[kUnroll][R]) {
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const int c = c0 + u * LPR;
+            if (c < CPR) {
+                if (cpg == 0) {
+#pragma unroll
+                    for (int m = 0; m < MT; ++m) {
+                        const float* xp = xs + (size_t)m * K + (size_t)c * 32;
+                        const float corr = cx[(size_t)m * CPR + c];
+#pragma unroll
+                        for (int r = 0; r < R; ++r) acc[r][m] = i4_chunk_dot(wv[u][r], xp, acc[r][m] - corr);
+                    }
+                } else {
+                    float sg[R];
+#pragma unroll
+                    for (int r = 0; r < R; ++r) sg[r] = raw_to_f32<DT_F16>(load_raw<DT_F16>(rs[r], (size_t)(c / cpg)));
+#pragma unroll
+                    for (int m = 0; m < MT; ++m) {
+                        const float* xp = xs + (size_t)m * K + (size_t)c * 32;
+                        const float corr = cx[(size_t)m * CPR + c];
+#pragma unroll
+                        for (int r = 0; r < R; ++r)
+                            acc[r][m] = __builtin_fmaf(sg[r], i4_chunk_dot(wv[u][r], xp, -corr), acc[r][m]);
+                    }
+                }
+            }
+        }
+    };
+    if constexpr (!MP) {
+        compute(lane, wa);
+    } else {
+        constexpr int P = kUnroll * LPR;
+        u4_t wb[kUnroll][R];
+        for (int c0 = lane; c0 < CPR + lane; c0 += 2 * P) {
+            if (c0 - lane + P < CPR) load_pass_i8<LPR, R>(w4, row0, c0 + P, N, CPR, wb);
+            compute(c0, wa);
+            if (c0 - lane + P >= CPR) break;
+            if (c0 - lane + 2 * P < CPR) load_pass_i8<LPR, R>(w4, row0, c0 + 2 * P, N, CPR, wa);
+            compute(c0 + P, wb);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[r][m] = group_sum<LPR>(acc[r][m]);
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int n = row0 + r;
+            if (n < N) {
+                const float sc = cpg == 0 ? raw_to_f32<DT_F16>(s0[r]) : 1.0f;
+#pragma unroll
+                for (int m = 0; m < MT; ++m)
+                    if (m < M) y[(size_t)m * N + n] = acc[r][m] * sc;
+            }
+        }
+    }
+}
+
+// Any shape, any gs: one wave per output row, one byte per lane and step.
+template <int XT>
+__global__ __launch_bounds__(kBlock) void qgemv_i4_generic_kernel(const uint8_t* __restrict__ w,
+                                                                  const uint16_t* __restrict__ S, int spr, int gs,
+                                                                  const void* __restrict__ x, float* __restrict__ y,
+                                                                  int M, int N, int K)
+{
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int n = blockIdx.x * (kBlock / 64) + wave;
+    if (n >= N) return;
+    const int row_stride = (K + 1) >> 1;
+    const uint8_t* row = w + (size_t)n * row_stride;
+    const uint16_t* rs = S + (size_t)n * spr;
+    for (int m = 0; m < M; ++m) {
+        float acc = 0.0f;
+        for (int bi = lane; bi < row_stride; bi += 64) {
+            const uint32_t byte = row[bi];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int j = 2 * bi + h;
+                if (j < K) {
+                    const int q = (int)((byte >> (4 * h)) & 0xFu) - 8;
+                    const float s = load_f32<DT_F16>(rs, (size_t)(j / gs));
+                    acc = __builtin_fmaf((float)q * s, load_f32<XT>(x, (size_t)m * K + j), acc);
+                }
+            }
+        }
+        acc = group_sum<64>(acc);
+        if (lane == 0) y[(size_t)m * N + n] = acc;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Fused multi-output int8 GEMV: up to three int8 matrices that share x in one
 // launch (QKV, metal.rs:387-439 mv_qkv_i8), or gate and up with the SiLU * up
 // epilogue (llama_graph.rs:320-327: mv_i8 x2 + silu_mul_f32_inplace,
@@ -1202,6 +1414,59 @@ hipError_t launch_i8_fused_xt(int lpr, const I8Segs& t, int total_rows, int sdt,
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+template <int LPR, int R, int MT, int XT>
+hipError_t launch_i4_shape(const uint8_t* w, const uint16_t* S, int spr, int cpg, const void* x, float* y, int M, int N,
+                           int K, hipStream_t st)
+{
+    const int CPR = K >> 5;
+    const int rows_per_block = (kBlock / LPR) * R;
+    const dim3 grid((N + rows_per_block - 1) / rows_per_block);
+    const size_t lds = (size_t)MT * K * 4 + (size_t)MT * CPR * 4;
+    const u4_t* w4 = reinterpret_cast<const u4_t*>(w);
+    if (CPR > kUnroll * LPR) {
+        auto kern = qgemv_i4_kernel<LPR, R, MT, XT, true>;
+        if (lds > 64 * 1024)
+            if (hipError_t e = allow_big_lds(kern, (int)lds); e != hipSuccess) return e;
+        hipLaunchKernelGGL(kern, grid, dim3(kBlock), lds, st, w4, S, spr, cpg, x, y, M, N, K);
+    } else {
+        auto kern = qgemv_i4_kernel<LPR, R, MT, XT, false>;
+        if (lds > 64 * 1024)
+            if (hipError_t e = allow_big_lds(kern, (int)lds); e != hipSuccess) return e;
+        hipLaunchKernelGGL(kern, grid, dim3(kBlock), lds, st, w4, S, spr, cpg, x, y, M, N, K);
+    }
+    return hipGetLastError();
+}
+
+// Team shapes (measured on the Gemma-3-1B MLP shapes): rows of up to 64
+// chunks (K <= 2048) with enough of them take 16-lane teams of two rows, so
+// each x read from LDS serves two rows (1152->6912: 4.5 us against 5.2 us for
+// one row per team); longer rows take 32 lanes at M > 2 (6912->1152, M = 4:
+// 21 us against 28 us with 64) and pick_shape's single-row teams otherwise.
+template <int MT, int XT>
+hipError_t launch_i4_mt(const uint8_t* w, const uint16_t* S, int spr, int cpg, const void* x, float* y, int M, int N,
+                        int K, hipStream_t st)
+{
+    const int CPR = K >> 5;
+    if (CPR <= 64 && N >= 4096) return launch_i4_shape<16, 2, MT, XT>(w, S, spr, cpg, x, y, M, N, K, st);
+    const int lpr = (MT == 4 && CPR > 64) ? 32 : pick_shape(CPR, N, false).lpr;
+    switch (lpr) {
+    case 8: return launch_i4_shape<8, 1, MT, XT>(w, S, spr, cpg, x, y, M, N, K, st);
+    case 16: return launch_i4_shape<16, 1, MT, XT>(w, S, spr, cpg, x, y, M, N, K, st);
+    case 32: return launch_i4_shape<32, 1, MT, XT>(w, S, spr, cpg, x, y, M, N, K, st);
+    default: return launch_i4_shape<64, 1, MT, XT>(w, S, spr, cpg, x, y, M, N, K, st);
+    }
+}
+
+template <int XT>
+hipError_t launch_i4_fast(const uint8_t* w, const uint16_t* S, int spr, int cpg, const void* x, float* y, int M,
+                          int N, int K, hipStream_t st)
+{
+    if (M == 1) return launch_i4_mt<1, XT>(w, S, spr, cpg, x, y, M, N, K, st);
+    if (M == 2) return launch_i4_mt<2, XT>(w, S, spr, cpg, x, y, M, N, K, st);
+    return launch_i4_mt<4, XT>(w, S, spr, cpg, x, y, M, N, K, st);
+}
+
+
 }  // namespace
 
 int qgemv_q4_lds_bytes(int M, int K)
@@ -1378,6 +1643,31 @@ hipError_t launch_qgemv_i8(const int8_t* w, const void* S, int sdt, int per_chan
     else
         hipLaunchKernelGGL((qgemv_i8_generic_kernel<DT_BF16>), grid, dim3(kBlock), 0, st, w, S, sdt, per_channel, x,
                            bias, y, M, N, K);
+    return hipGetLastError();
+}
+
+hipError_t launch_qgemv_i4_sym(const uint8_t* w, const uint16_t* S, int spr, int gs, const void* x, int xdt, float* y,
+                               int M, int N, int K, hipStream_t st)
+{
+    const int MT = M <= 1 ? 1 : (M <= 2 ? 2 : 4);
+    const size_t lds = (size_t)MT * K * 4 + (size_t)MT * (K >> 5) * 4;
+    // one group per row when the row's last element still uses scale 0
+    const bool per_row = K > 0 && (K - 1) / gs == 0;
+    const bool fast = (xdt == DT_F16 || xdt == DT_F32) && M <= 4 && K > 0 && (K % 32) == 0 &&
+                      (per_row || (gs % 32) == 0) && aligned16(w) && aligned16(x) && lds <= 160 * 1024;
+    if (fast) {
+        const int cpg = per_row ? 0 : gs / 32;
+        if (xdt == DT_F16) return launch_i4_fast<DT_F16>(w, S, spr, cpg, x, y, M, N, K, st);
+        return launch_i4_fast<DT_F32>(w, S, spr, cpg, x, y, M, N, K, st);
+    }
+    const dim3 grid((N + 3) / 4);
+    if (xdt == DT_F32)
+        hipLaunchKernelGGL((qgemv_i4_generic_kernel<DT_F32>), grid, dim3(kBlock), 0, st, w, S, spr, gs, x, y, M, N, K);
+    else if (xdt == DT_F16)
+        hipLaunchKernelGGL((qgemv_i4_generic_kernel<DT_F16>), grid, dim3(kBlock), 0, st, w, S, spr, gs, x, y, M, N, K);
+    else
+        hipLaunchKernelGGL((qgemv_i4_generic_kernel<DT_BF16>), grid, dim3(kBlock), 0, st, w, S, spr, gs, x, y, M, N,
+                           K);
     return hipGetLastError();
 }
 

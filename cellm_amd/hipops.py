@@ -273,6 +273,13 @@ class HipOps:
                             x=_dev_ptr(x), bias=None, y=_dev_ptr(y), m=x.numel() // k, n=w_u8.shape[0], k=k)
 
     @staticmethod
+    def qgemv_op_i4_sym(w_u8, scales_f16, gs: int, x, y, k: int) -> "_lib.QgemvOp":
+        """One cellm_hip_qgemv_op_t of kind i4_sym (group carries gs)."""
+        return _lib.QgemvOp(kind=_lib.OP_QGEMV_I4_SYM, sb_dtype=1, x_dtype=_torch_dtype_code(x), group=gs,
+                            w=_dev_ptr(w_u8), scales=_dev_ptr(scales_f16), biases=None, n_scales=scales_f16.numel(),
+                            x=_dev_ptr(x), bias=None, y=_dev_ptr(y), m=x.numel() // k, n=w_u8.shape[0], k=k)
+
+    @staticmethod
     def qgemv_op_q1_0_g128(w_u8, x, y, k: int) -> "_lib.QgemvOp":
         """One cellm_hip_qgemv_op_t of kind q1_0_g128."""
         return _lib.QgemvOp(kind=_lib.OP_QGEMV_Q1_0_G128, sb_dtype=0, x_dtype=_torch_dtype_code(x), group=0,

@@ -169,12 +169,15 @@ int32_t cellm_hip_qgemv_q4_affine_gate_up_silu(cellm_hip_ctx_t* ctx, const uint3
  * kind CELLM_HIP_OP_QGEMV_F16 those of cellm_hip_qgemv_f16 (w only);
  * kind CELLM_HIP_OP_QGEMV_I2 those of cellm_hip_qgemv_i2 (w, scales = f16 row
  * scales, group = scale_mode); kind CELLM_HIP_OP_QGEMV_Q1_0_G128 those of
- * cellm_hip_qgemv_q1_0_g128 (w only).  Unused fields are ignored. */
+ * cellm_hip_qgemv_q1_0_g128 (w only); kind CELLM_HIP_OP_QGEMV_I4_SYM those of
+ * cellm_hip_qgemv_i4_sym (w bytes, scales = f16, n_scales, group = gs).
+ * Unused fields are ignored. */
 #define CELLM_HIP_OP_QGEMV_I8 0
 #define CELLM_HIP_OP_QGEMV_Q4_AFFINE 1
 #define CELLM_HIP_OP_QGEMV_F16 2
 #define CELLM_HIP_OP_QGEMV_I2 3
 #define CELLM_HIP_OP_QGEMV_Q1_0_G128 4
+#define CELLM_HIP_OP_QGEMV_I4_SYM 5
 typedef struct {
     int32_t kind;
     int32_t sb_dtype;

@@ -431,6 +431,53 @@ def test_i4_sym_logits(ops):
     assert rel_err(y, ref) <= TOL_F32
 
 
+def _run_i4(ops, w, s, gs, x):
+    import torch
+
+    n, m, k = w.shape[0], x.shape[0], x.shape[1]
+    y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    ops.encode_qgemv_i4_sym(_t(w), _t(s.view(np.int16)), gs, _t(x), y, k)
+    torch.cuda.synchronize()
+    return y.cpu().numpy()
+
+
+def _i4_case(n, k, m, gs, salt, xdt=np.float32):
+    w = oracle.gen_i8((n, (k + 1) // 2), seed(60 + salt, 0)).view(np.uint8)
+    spr = (k + gs - 1) // gs
+    s = oracle.gen_uniform((n * spr,), seed(60 + salt, 1), 1e-3, 2e-2).astype(np.float16).view(np.uint16)
+    x = oracle.gen_normal((m, k), seed(60 + salt, 2), 0.0, 1.0).astype(xdt)
+    return w, s, x
+
+
+@pytest.mark.parametrize("n,k", [(6912, 1152), (1152, 6912)])
+@pytest.mark.parametrize("m", [1, 2, 4])
+def test_i4_sym_gemma_mlp_per_row(ops, n, k, m):
+    """Gemma-3-1B MLP projections in the reference's i4 format: one f16 scale
+    per row, gs = in_dim (gemma.rs:1446-1471), f32 activations."""
+    w, s, x = _i4_case(n, k, m, k, salt=m + (k == 6912))
+    y = _run_i4(ops, w, s, k, x)
+    assert rel_err(y, oracle.qgemv_i4_sym(w, s, k, x, n, k)) <= TOL_F32
+    if m == 1:
+        assert rel_err(y[0], oracle.matmul_i4_f32(w, s, n, k, k, x[0])) <= TOL_F32
+
+
+@pytest.mark.parametrize("n,k,m,gs,xdt", [
+    (6912, 1152, 1, 1152, np.float16),   # f16 x widened at staging
+    (1152, 6912, 4, 6912, np.float16),
+    (1000, 1024, 3, 32, np.float32),     # one group per chunk
+    (777, 1152, 2, 96, np.float32),      # three chunks per group
+    (513, 4096, 1, 2048, np.float32),    # two groups per row, MP passes
+    (300, 1152, 1, 4096, np.float32),    # gs > k: still one scale per row
+    (200, 1001, 1, 1001, np.float32),    # odd k: one-wave-per-row kernel
+    (200, 1024, 1, 48, np.float32),      # gs % 32 != 0: one-wave-per-row kernel
+    (200, 1152, 5, 1152, np.float32),    # m > 4: one-wave-per-row kernel
+])
+def test_i4_sym_shapes_and_groups(ops, n, k, m, gs, xdt):
+    w, s, x = _i4_case(n, k, m, gs, salt=n % 97 + m, xdt=xdt)
+    y = _run_i4(ops, w, s, gs, x)
+    assert rel_err(y, oracle.qgemv_i4_sym(w, s, gs, x, n, k)) <= TOL_F32
+
+
 # -------------------------------------------------------------- edge cases ----
 
 def test_empty_inputs_are_noops(ops):
@@ -529,14 +576,19 @@ def test_qgemv_batch_matches_single_calls(ops):
     q = [_t(v) if i not in (1, 2) else _sb_tensor(v) for i, v in enumerate(make_q4(1000, 1152, 1, cfg=3, salt=21))]
     e = [_t(v) for v in make_i8(700, 576, 4, x_dtype=np.float16, salt=22)]
     g = [_t(v) if i not in (1, 2) else _sb_tensor(v) for i, v in enumerate(make_q4(300, 896, 16, cfg=3, salt=23))]
-    outs = [torch.empty(shape, dtype=torch.float32, device="cuda") for shape in ((1, 1000), (4, 700), (16, 300))]
+    iw, isc, ix = _i4_case(640, 1152, 2, 1152, salt=24)
+    i4 = [_t(iw), _t(isc.view(np.int16)), _t(ix)]
+    outs = [torch.empty(shape, dtype=torch.float32, device="cuda")
+            for shape in ((1, 1000), (4, 700), (16, 300), (2, 640))]
     refs = [torch.empty_like(o) for o in outs]
     ops.encode_qgemv_q4_affine(q[0], q[1], q[2], q[3], refs[0])
     ops.encode_qgemv_i8(e[0], e[1], e[2], refs[1])
     ops.encode_qgemv_q4_affine(g[0], g[1], g[2], g[3], refs[2])
+    ops.encode_qgemv_i4_sym(i4[0], i4[1], 1152, i4[2], refs[3], 1152)
     ops.encode_qgemv_batch([ops.qgemv_op_q4_affine(q[0], q[1], q[2], q[3], outs[0]),
                             ops.qgemv_op_i8(e[0], e[1], e[2], outs[1]),
-                            ops.qgemv_op_q4_affine(g[0], g[1], g[2], g[3], outs[2])])
+                            ops.qgemv_op_q4_affine(g[0], g[1], g[2], g[3], outs[2]),
+                            ops.qgemv_op_i4_sym(i4[0], i4[1], 1152, i4[2], outs[3], 1152)])
     torch.cuda.synchronize()
     for o, r in zip(outs, refs):
         assert torch.equal(o, r)
