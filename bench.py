@@ -334,6 +334,7 @@ def extra_configs(torch, ops, stream, gen, graphs: bool = True):
     res.update(decode_step_cfg5(graphs))
     res.update(lowbit_gemvs(torch, ops, stream, gen))
     res.update(i4_gemma_mlp(torch, ops, stream, gen))
+    res.update(q4_gate_up_silu(torch, ops, stream, gen))
 
     # M=512 prefill qGEMM (MFMA)
     m = 512
@@ -445,6 +446,70 @@ def i4_gemma_mlp(torch, ops, stream, gen):
             res[f"gemma_i4_{k}x{n}_m{m}"] = {"us": round(ms * 1e3, 2), "GB/s": round(b / (ms * 1e-3) / 1e9, 1),
                                               "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
         del w
+    return res
+
+
+def _graph_us_per_call(torch, record, calls: int, trials: int = 3) -> float:
+    """Capture record() (which enqueues `calls` calls on the capture stream)
+    into one HIP graph, replay it, and return the median us per call."""
+    cap = torch.cuda.Stream()
+    with torch.cuda.stream(cap):
+        record(cap.cuda_stream)  # eager pass: buffers and kernel attributes set up outside the capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=cap):
+        record(cap.cuda_stream)
+    for _ in range(3):
+        g.replay()
+    torch.cuda.synchronize()
+    out = []
+    s = torch.cuda.current_stream()
+    for _ in range(trials):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(s)
+        g.replay()
+        e1.record(s)
+        torch.cuda.synchronize()
+        out.append(e0.elapsed_time(e1) * 1e3 / calls)
+    del g
+    return sorted(out)[len(out) // 2]
+
+
+def q4_gate_up_silu(torch, ops, stream, gen):
+    """MLX q4 gate/up + SiLU (the reference's mv2 + silu_mul pattern) at the
+    Qwen2.5-0.5B (896->4864 x2) and Gemma-3-1B (1152->6912 x2) MLP shapes:
+    one cellm_hip_qgemv_q4_affine_gate_up_silu launch against two q4 GEMVs and
+    the SiLU kernel.  Each variant is captured once per weight pair into a HIP
+    graph (pairs rotate past 512 MB) and replayed; us per gate/up call.  Bytes:
+    both matrices' weights and f16 S/B + x + h."""
+    res = {}
+    for k, n in ((896, 4864), (1152, 6912)):
+        pair = 2 * (n * k // 2 + 4 * n * ((k + 63) // 64))
+        copies = -(-512 * 2**20 // pair) + 1
+        ws = [(Q4Weights(torch, n, k, gen), Q4Weights(torch, n, k, gen)) for _ in range(copies)]
+        for m in (1, 4):
+            x = torch.randn((m, k), device="cuda", generator=gen).to(torch.float16)
+            h = torch.empty((m, n), dtype=torch.float32, device="cuda")
+            u = torch.empty((m, n), dtype=torch.float32, device="cuda")
+
+            def fused(st):
+                for g_, u_ in ws:
+                    ops.encode_gate_up_silu_q4_affine(g_.wq, g_.s, g_.b, u_.wq, u_.s, u_.b, x, h, stream=st)
+
+            def unfused(st):
+                for g_, u_ in ws:
+                    ops.encode_qgemv_q4_affine(g_.wq, g_.s, g_.b, x, h, stream=st)
+                    ops.encode_qgemv_q4_affine(u_.wq, u_.s, u_.b, x, u, stream=st)
+                    ops.encode_silu_mul(h, u, stream=st)
+
+            b = pair + 2 * m * k + 4 * m * n
+            us_f = _graph_us_per_call(torch, fused, copies)
+            us_u = _graph_us_per_call(torch, unfused, copies)
+            res[f"q4_gate_up_silu_{k}x{n}x2_m{m}"] = {
+                "fused_us": round(us_f, 2), "unfused_us": round(us_u, 2),
+                "GB/s": round(b / (us_f * 1e-6) / 1e9, 1), "frac_hbm": round(b / (us_f * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                "launch": "captured HIP graph"}
+        del ws
     return res
 
 

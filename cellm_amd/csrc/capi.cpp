@@ -363,8 +363,17 @@ int32_t gate_up_q4_impl(cellm_hip_ctx* ctx, const uint32_t* wg, const void* sg, 
                         float* h, int64_t m, int64_t n, int64_t k, hipStream_t st)
 {
     if (int32_t rc = check_dims(m, n, k)) return rc;
+    if (int32_t rc = check_group(group)) return rc;
+    if (!valid_dtype(sbt) || !valid_dtype(xdt)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "bad dtype");
     if (m == 0 || n == 0) return CELLM_HIP_OK;
     if (!h) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null output pointer");
+    if (k > 0 && (!wg || !sg || !bg || !wu || !su || !bu || !x))
+        return set_error(CELLM_HIP_ERR_INVALID_ARG, "null input pointer");
+    if (qgemv_q4_gate_up_supported(xdt, (int)m, (int)k, (int)group, x, wg, wu)) {
+        HIP_TRY(launch_qgemv_q4_gate_up_silu(wg, sg, bg, wu, su, bu, sbt, (int)group, x, h, (int)m, (int)n, (int)k, st),
+                "qgemv_q4_gate_up_silu launch");
+        return CELLM_HIP_OK;
+    }
     float* up = nullptr;
     if (int32_t rc = get_stream_buffer(ctx, ctx->aux, st, (size_t)m * n * sizeof(float), &up)) return rc;
     if (int32_t rc = qgemv_q4_impl(ctx, wg, sg, bg, sbt, group, x, xdt, h, m, n, k, st, false)) return rc;

@@ -44,6 +44,13 @@ bool qgemv_i8_fused_supported(int xdt, int M, int K, const void* x, const I8Fuse
 hipError_t launch_qgemv_i8_fused(const I8FusedSeg* segs, int nseg, bool silu, int sdt, const void* x, int xdt, int M,
                                  int K, hipStream_t st);
 
+// MLX q4 gate/up + SiLU in one launch: h[m,n] = silu(gate[m,n]) * up[m,n] (f16 x, M <= 4,
+// K % 32 == 0, group >= 32, 16-byte aligned x and weights, x in 64 KB of LDS).
+bool qgemv_q4_gate_up_supported(int xdt, int M, int K, int group_size, const void* x, const void* wg, const void* wu);
+hipError_t launch_qgemv_q4_gate_up_silu(const uint32_t* wg, const void* Sg, const void* Bg, const uint32_t* wu,
+                                        const void* Su, const void* Bu, int sbt, int group_size, const void* x,
+                                        float* h, int M, int N, int K, hipStream_t st);
+
 // h[i] = silu(g[i]) * u[i] in place on g (dequant.hip), silu(g) = g / (1 + exp(-g)).
 hipError_t launch_silu_mul(float* g, const float* u, size_t count, hipStream_t st);
 

@@ -92,6 +92,27 @@ __device__ __forceinline__ void load_x_words(const _Float16* __restrict__ x, int
     }
 }
 
+// The words of load_x_words -> LDS (stage_word_q4), then any further words of a large M*K.
+template <int XW>
+__device__ __forceinline__ void stage_x_q4(const u4_t (&xr)[XW], const _Float16* __restrict__ x, int M, int K,
+                                           int total, uint32_t* xq, float2* cx)
+{
+#pragma unroll
+    for (int j = 0; j < XW; ++j) {
+        const int idx = (int)threadIdx.x + j * kBlock;
+        stage_word_q4(xr[j], idx, idx < total, xq, cx);
+    }
+    for (int base = XW * kBlock; base < total; base += kBlock) {  // large M*K only
+        const int idx = base + (int)threadIdx.x;
+        const int words = K >> 3;
+        const int m = idx / words;
+        u4_t raw = (idx < total && m < M)
+                       ? *reinterpret_cast<const u4_t*>(x + (size_t)m * K + (size_t)(idx - m * words) * 8)
+                       : u4_t{0u, 0u, 0u, 0u};
+        stage_word_q4(raw, idx, idx < total, xq, cx);
+    }
+}
+
 template <int LPR, int R, int SBT, int U = kUnroll>
 __device__ __forceinline__ void load_pass_q4(const u4_t* __restrict__ wq, const void* __restrict__ S,
                                              const void* __restrict__ B, int row0, int rstride, int c0, int N, int CPR,
@@ -190,20 +211,7 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_f16x_kernel(
     uint32_t sa[kUnroll][R], ba[kUnroll][R];
     load_pass_q4<LPR, R, SBT>(wq, S, B, row0, 1, lane, N, CPR, gpr, gshift, wa, sa, ba);
 
-#pragma unroll
-    for (int j = 0; j < XW; ++j) {
-        const int idx = (int)threadIdx.x + j * kBlock;
-        stage_word_q4(xr[j], idx, idx < total, xq, cx);
-    }
-    for (int base = XW * kBlock; base < total; base += kBlock) {  // large M*K only
-        const int idx = base + (int)threadIdx.x;
-        const int words = K >> 3;
-        const int m = idx / words;
-        u4_t raw = (idx < total && m < M)
-                       ? *reinterpret_cast<const u4_t*>(x + (size_t)m * K + (size_t)(idx - m * words) * 8)
-                       : u4_t{0u, 0u, 0u, 0u};
-        stage_word_q4(raw, idx, idx < total, xq, cx);
-    }
+    stage_x_q4<XW>(xr, x, M, K, total, xq, cx);
     __syncthreads();
     if (row0 >= N) return;
 
@@ -244,6 +252,95 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_f16x_kernel(
                     if (m < M) y[(size_t)m * N + n] = acc[r][m];
             }
         }
+    }
+}
+
+// Gate/up + SiLU for MLX q4 in one launch (the mv2 + silu_mul pattern of the
+// reference's fused graphs: metal.rs:512-541 and 232-243, llama_graph.rs:318-327).
+// A team owns output row n of both matrices: its two rows (gate, up) go through
+// the same loads and dot as qgemv_q4_f16x_kernel's R = 2 rows, and lane 0 writes
+// h[m, n] = (g * (1 / (1 + exp(-g)))) * u, silu_mul_kernel's order.
+template <int LPR, int SBT, int U = kUnroll>
+__device__ __forceinline__ void load_pass_q4_gu(const u4_t* __restrict__ wg, const void* __restrict__ Sg,
+                                                const void* __restrict__ Bg, const u4_t* __restrict__ wu,
+                                                const void* __restrict__ Su, const void* __restrict__ Bu, int n, int c0,
+                                                int N, int CPR, int gpr, int gshift, u4_t (&wv)[U][2],
+                                                uint32_t (&sr)[U][2], uint32_t (&br)[U][2])
+{
+    const int nn = min(n, N - 1);  // clamped like load_pass_q4
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int c = min(c0 + u * LPR, CPR - 1);
+        const size_t gi = (size_t)nn * gpr + ((c << 5) >> gshift);
+        wv[u][0] = __builtin_nontemporal_load(wg + (size_t)nn * CPR + c);
+        sr[u][0] = load_raw<SBT>(Sg, gi);
+        br[u][0] = load_raw<SBT>(Bg, gi);
+        wv[u][1] = __builtin_nontemporal_load(wu + (size_t)nn * CPR + c);
+        sr[u][1] = load_raw<SBT>(Su, gi);
+        br[u][1] = load_raw<SBT>(Bu, gi);
+    }
+}
+
+template <int LPR, int MT, int SBT, bool MP>
+__global__ __launch_bounds__(kBlock) void qgemv_q4_gate_up_silu_kernel(
+    const u4_t* __restrict__ wg, const void* __restrict__ Sg, const void* __restrict__ Bg,
+    const u4_t* __restrict__ wu, const void* __restrict__ Su, const void* __restrict__ Bu,
+    const _Float16* __restrict__ x, float* __restrict__ h, int M, int N, int K, int gshift)
+{
+    extern __shared__ __align__(16) uint32_t lds[];
+    const int CPR = K >> 5;
+    uint32_t* xq = lds;
+    float2* cx = reinterpret_cast<float2*>(lds + (size_t)MT * CPR * 16);
+
+    const int team = threadIdx.x / LPR;
+    const int lane = threadIdx.x % LPR;
+    const int n = blockIdx.x * (kBlock / LPR) + team;
+    const int gpr = (K + (1 << gshift) - 1) >> gshift;
+    const int total = MT * (K >> 3);
+
+    constexpr int XW = MT == 1 ? 4 : 8;
+    u4_t xr[XW];
+    load_x_words<XW>(x, M, K, total, xr);
+    u4_t wa[kUnroll][2];
+    uint32_t sa[kUnroll][2], ba[kUnroll][2];
+    load_pass_q4_gu<LPR, SBT>(wg, Sg, Bg, wu, Su, Bu, n, lane, N, CPR, gpr, gshift, wa, sa, ba);
+    stage_x_q4<XW>(xr, x, M, K, total, xq, cx);
+    __syncthreads();
+    if (n >= N) return;
+
+    float acc[2][MT];
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[r][m] = 0.0f;
+    if constexpr (!MP) {
+        compute_pass_q4<LPR, 2, MT, SBT>(lane, CPR, xq, cx, wa, sa, ba, acc);
+    } else {
+        constexpr int P = kUnroll * LPR;
+        u4_t wb[kUnroll][2];
+        uint32_t sb[kUnroll][2], bb[kUnroll][2];
+        for (int c0 = lane; c0 < CPR + lane; c0 += 2 * P) {
+            if (c0 - lane + P < CPR)
+                load_pass_q4_gu<LPR, SBT>(wg, Sg, Bg, wu, Su, Bu, n, c0 + P, N, CPR, gpr, gshift, wb, sb, bb);
+            compute_pass_q4<LPR, 2, MT, SBT>(c0, CPR, xq, cx, wa, sa, ba, acc);
+            if (c0 - lane + P >= CPR) break;
+            if (c0 - lane + 2 * P < CPR)
+                load_pass_q4_gu<LPR, SBT>(wg, Sg, Bg, wu, Su, Bu, n, c0 + 2 * P, N, CPR, gpr, gshift, wa, sa, ba);
+            compute_pass_q4<LPR, 2, MT, SBT>(c0 + P, CPR, xq, cx, wb, sb, bb, acc);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[r][m] = group_sum<LPR>(acc[r][m]);
+    if (lane == 0) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+            if (m < M) {
+                const float g = acc[0][m];
+                const float sig = 1.0f / (1.0f + expf(-g));
+                h[(size_t)m * N + n] = (g * sig) * acc[1][m];
+            }
     }
 }
 
@@ -1412,6 +1509,44 @@ hipError_t launch_i8_fused_xt(int lpr, const I8Segs& t, int total_rows, int sdt,
     return launch_i8_fused_mt<4, XT, SILU>(lpr, t, total_rows, sdt, x, M, K, st);
 }
 
+template <int LPR, int MT, bool MP>
+hipError_t launch_q4_gu_shape(int sbt, const uint32_t* wg, const void* Sg, const void* Bg, const uint32_t* wu,
+                              const void* Su, const void* Bu, const _Float16* x, float* h, int M, int N, int K,
+                              int gshift, hipStream_t st)
+{
+    const dim3 grid((N + (kBlock / LPR) - 1) / (kBlock / LPR));
+    const size_t lds = (size_t)qgemv_q4_lds_bytes(M, K);
+    const u4_t* g4 = reinterpret_cast<const u4_t*>(wg);
+    const u4_t* u4 = reinterpret_cast<const u4_t*>(wu);
+#define CELLM_GU(SBT_)                                                                                           \
+    hipLaunchKernelGGL((qgemv_q4_gate_up_silu_kernel<LPR, MT, SBT_, MP>), grid, dim3(kBlock), lds, st, g4, Sg, Bg, \
+                       u4, Su, Bu, x, h, M, N, K, gshift)
+    if (sbt == DT_F16) CELLM_GU(DT_F16);
+    else if (sbt == DT_F32) CELLM_GU(DT_F32);
+    else CELLM_GU(DT_BF16);
+#undef CELLM_GU
+    return hipGetLastError();
+}
+
+template <int MT>
+hipError_t launch_q4_gu_mt(int sbt, const uint32_t* wg, const void* Sg, const void* Bg, const uint32_t* wu,
+                           const void* Su, const void* Bu, const _Float16* x, float* h, int M, int N, int K, int gshift,
+                           hipStream_t st)
+{
+    const int CPR = K >> 5;
+    const int lpr = pick_shape(CPR, 2 * N, false).lpr;
+#define CELLM_GU_L(L_)                                                                                               \
+    return CPR > kUnroll * L_ ? launch_q4_gu_shape<L_, MT, true>(sbt, wg, Sg, Bg, wu, Su, Bu, x, h, M, N, K, gshift, st) \
+                              : launch_q4_gu_shape<L_, MT, false>(sbt, wg, Sg, Bg, wu, Su, Bu, x, h, M, N, K, gshift, st)
+    switch (lpr) {
+    case 8: CELLM_GU_L(8);
+    case 16: CELLM_GU_L(16);
+    case 32: CELLM_GU_L(32);
+    default: CELLM_GU_L(64);
+    }
+#undef CELLM_GU_L
+}
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 template <int LPR, int R, int MT, int XT>
@@ -1669,6 +1804,23 @@ hipError_t launch_qgemv_i4_sym(const uint8_t* w, const uint16_t* S, int spr, int
         hipLaunchKernelGGL((qgemv_i4_generic_kernel<DT_BF16>), grid, dim3(kBlock), 0, st, w, S, spr, gs, x, y, M, N,
                            K);
     return hipGetLastError();
+}
+
+bool qgemv_q4_gate_up_supported(int xdt, int M, int K, int group_size, const void* x, const void* wg, const void* wu)
+{
+    return xdt == DT_F16 && M >= 1 && M <= 4 && K > 0 && (K % 32) == 0 && group_size >= 32 && aligned16(x) &&
+           aligned16(wg) && aligned16(wu) && qgemv_q4_lds_bytes(M, K) <= 64 * 1024;
+}
+
+hipError_t launch_qgemv_q4_gate_up_silu(const uint32_t* wg, const void* Sg, const void* Bg, const uint32_t* wu,
+                                        const void* Su, const void* Bu, int sbt, int group_size, const void* x,
+                                        float* h, int M, int N, int K, hipStream_t st)
+{
+    const int gshift = __builtin_ctz((unsigned)group_size);
+    const _Float16* xh = reinterpret_cast<const _Float16*>(x);
+    if (M == 1) return launch_q4_gu_mt<1>(sbt, wg, Sg, Bg, wu, Su, Bu, xh, h, M, N, K, gshift, st);
+    if (M == 2) return launch_q4_gu_mt<2>(sbt, wg, Sg, Bg, wu, Su, Bu, xh, h, M, N, K, gshift, st);
+    return launch_q4_gu_mt<4>(sbt, wg, Sg, Bg, wu, Su, Bu, xh, h, M, N, K, gshift, st);
 }
 
 bool qgemv_i8_fused_supported(int xdt, int M, int K, const void* x, const I8FusedSeg* segs, int nseg)

@@ -428,6 +428,11 @@ class HipOps:
             layer, 0.0 if attn_scale is None else attn_scale, 0.0 if soft_cap is None else soft_cap, _dev_ptr(out),
             _stream_ptr(stream)))
 
+    def encode_silu_mul(self, gate, up, stream=None) -> None:
+        """gate = silu(gate) * up in place (f32), silu_mul_f32_inplace."""
+        check(self._lib.cellm_hip_silu_mul_f32(self._h, _dev_ptr(gate), _dev_ptr(up), gate.numel(),
+                                               _stream_ptr(stream)))
+
     def encode_add_inplace(self, x, y, stream=None) -> None:
         check(self._lib.cellm_hip_add_f32_inplace(self._h, _dev_ptr(x), _dev_ptr(y), x.numel(), _stream_ptr(stream)))
 

@@ -153,9 +153,11 @@ int32_t cellm_hip_qgemv_i8_gate_up_silu(cellm_hip_ctx_t* ctx, const int8_t* wg, 
                                         const float* bu, int32_t scale_dtype, const void* x, int32_t x_dtype, float* h,
                                         int64_t m, int64_t n, int64_t k, void* stream);
 
-/* The same for MLX 4-bit affine gate/up weights (two cellm_hip_qgemv_q4_affine
- * launches, then the SiLU * up kernel); sg/bg and su/bu are the affine
- * scales/biases of each matrix. */
+/* The same for MLX 4-bit affine gate/up weights; sg/bg and su/bu are the affine
+ * scales/biases of each matrix.  One launch computes both rows and the SiLU *
+ * up for m <= 4 with f16 x, k % 32 == 0, group >= 32 and 16-byte aligned x,
+ * wg and wu; other shapes run two cellm_hip_qgemv_q4_affine launches and the
+ * SiLU * up kernel. */
 int32_t cellm_hip_qgemv_q4_affine_gate_up_silu(cellm_hip_ctx_t* ctx, const uint32_t* wg, const void* sg,
                                                const void* bg, const uint32_t* wu, const void* su, const void* bu,
                                                int32_t sb_dtype, int64_t group, const void* x, int32_t x_dtype,

@@ -642,17 +642,27 @@ def test_gate_up_silu_i8(ops, m, xdt):
     assert rel_err(h.cpu().numpy(), ref) <= TOL_F32
 
 
-def test_gate_up_silu_q4(ops):
-    """Qwen2.5-0.5B MLP halves (896 -> 4864 each), q4 affine g64."""
+@pytest.mark.parametrize("k,n,m,sb,group,xdt", [
+    (896, 4864, 1, np.float16, 64, np.float16),    # Qwen2.5-0.5B MLP halves, one launch
+    (896, 4864, 4, np.float16, 64, np.float16),
+    (1152, 6912, 1, np.float32, 64, np.float16),   # Gemma-3-1B MLP halves, f32 S/B as LFM files hold them
+    (1152, 6912, 2, "bf16", 128, np.float16),
+    (4864, 896, 3, np.float16, 32, np.float16),    # long rows: two register passes per lane
+    (896, 1000, 1, np.float16, 64, np.float32),    # f32 x: two GEMVs + SiLU kernel
+    (896, 4864, 5, np.float16, 64, np.float16),    # m > 4: two GEMVs + SiLU kernel
+])
+def test_gate_up_silu_q4(ops, k, n, m, sb, group, xdt):
+    """h = silu(gate) * up over MLX q4 affine gate/up matrices (the mv2 + silu_mul
+    pattern, metal.rs:512-541,232-243), against the oracle's two GEMVs and
+    silu_mul_f32_inplace."""
     import torch
 
-    k, n = 896, 4864
-    wg, sg, bg, x = make_q4(n, k, 1, salt=51)
-    wu, su, bu, _ = make_q4(n, k, 1, salt=52)
-    h = torch.empty((1, n), dtype=torch.float32, device="cuda")
+    wg, sg, bg, x = make_q4(n, k, m, sb_dtype=sb, x_dtype=xdt, group=group, salt=51 + m)
+    wu, su, bu, _ = make_q4(n, k, m, sb_dtype=sb, group=group, salt=52 + m)
+    h = torch.empty((m, n), dtype=torch.float32, device="cuda")
     ops.encode_gate_up_silu_q4_affine(_t(wg), _sb_tensor(sg), _sb_tensor(bg), _t(wu), _sb_tensor(su),
-                                      _sb_tensor(bu), _t(x), h)
+                                      _sb_tensor(bu), _t(x), h, group=group)
     torch.cuda.synchronize()
-    g = np.ascontiguousarray(oracle.qgemv_q4_affine(wg, sg, bg, x, k), np.float32)
-    ref = oracle.silu_mul_(g, oracle.qgemv_q4_affine(wu, su, bu, x, k))
+    g = np.ascontiguousarray(oracle.qgemv_q4_affine(wg, sg, bg, x, k, gs=group), np.float32)
+    ref = oracle.silu_mul_(g, oracle.qgemv_q4_affine(wu, su, bu, x, k, gs=group))
     assert rel_err(h.cpu().numpy(), ref) <= TOL_F32
