@@ -141,6 +141,9 @@ def test_kv_write_f16(ops):
     (14, 2, 64, 34, (0, 100, 200, 543)),    # G 7
     (8, 4, 64, 8, (5, 127, 0, 64)),         # G 2, a short table
     (16, 2, 128, 132, (2099, 1024, 1, 700)),  # G 8: 33 chunks, past the combine's preloaded 16
+    (15, 5, 64, 64, (1023, 960, 15, 511)),   # G 3, 16 chunks: the largest single-launch table
+    (15, 5, 64, 80, (1279, 1024, 3, 640)),   # G 3, 20 chunks: split-sequence launches
+    (4, 2, 128, 20, (319, 0, 64, 200)),      # G 2 at head_dim 128: single launch
 ])
 def test_attention_gqa_f16kv(ops, nh, nkv, hd, blocks, pos):
     L, tpb, rows = 3, 16, 4
