@@ -343,6 +343,31 @@ int32_t enqueue_step(cellm_llama_dev* m, int32_t rows)
 // later step reallocates, and the captured kernel arguments stay valid.  The
 // eager steps run at position 0 on block 0 and the K/V cache is cleared
 // afterwards.
+// A captured step must hold kernel launches only (no copy, memset or host
+// node: those would tie the graph to host buffers or record a clear), each
+// with a function and a non-empty grid.  Checked once per captured graph.
+int32_t check_step_graph(hipGraph_t g, int32_t rows)
+{
+    size_t n = 0;
+    RT_TRY(hipGraphGetNodes(g, nullptr, &n), "hipGraphGetNodes(count)");
+    if (n == 0) return fail(CELLM_HIP_ERR_DEVICE, "captured step for %d rows is empty", rows);
+    std::vector<hipGraphNode_t> nodes(n);
+    RT_TRY(hipGraphGetNodes(g, nodes.data(), &n), "hipGraphGetNodes");
+    for (size_t i = 0; i < n; ++i) {
+        hipGraphNodeType type;
+        RT_TRY(hipGraphNodeGetType(nodes[i], &type), "hipGraphNodeGetType");
+        if (type != hipGraphNodeTypeKernel)
+            return fail(CELLM_HIP_ERR_DEVICE, "captured step for %d rows: node %zu has type %d, not a kernel", rows, i,
+                        (int)type);
+        hipKernelNodeParams kp{};
+        RT_TRY(hipGraphKernelNodeGetParams(nodes[i], &kp), "hipGraphKernelNodeGetParams");
+        if (!kp.func || kp.gridDim.x == 0 || kp.gridDim.y == 0 || kp.gridDim.z == 0 || kp.blockDim.x == 0)
+            return fail(CELLM_HIP_ERR_DEVICE, "captured step for %d rows: kernel node %zu has no function or grid", rows,
+                        i);
+    }
+    return CELLM_HIP_OK;
+}
+
 int32_t prepare_graphs(cellm_llama_dev* m)
 {
     const hipStream_t st = reinterpret_cast<hipStream_t>(m->stream);
@@ -365,6 +390,7 @@ int32_t prepare_graphs(cellm_llama_dev* m)
         }
         if (e != hipSuccess) return from_runtime(e, "hipStreamEndCapture");
         m->graph[r - 1] = g;
+        if (int32_t rc2 = check_step_graph(g, r)) return rc2;
         RT_TRY(hipGraphInstantiate(&m->graph_exec[r - 1], g, nullptr, nullptr, 0), "hipGraphInstantiate");
     }
     m->use_graphs = true;
