@@ -38,6 +38,11 @@ QWEN_SHAPES = [("qkv", 896, 1152), ("o", 896, 896), ("gate_up", 896, 9728), ("do
                ("lm_head", 896, 151936)]
 
 
+def progress(msg: str) -> None:
+    """One line per finished phase on stderr (the JSON line stays alone on stdout)."""
+    print(f"bench: {msg}", file=sys.stderr, flush=True)
+
+
 def q4_bytes(m: int, n: int, k: int) -> int:
     """Algorithmic bytes of one q4-affine g64 call: packed W + f16 S,B + f16 x + f32 y."""
     return n * k // 2 + 4 * n * ((k + 63) // 64) + 2 * m * k + 4 * m * n
@@ -58,7 +63,8 @@ def parse():
                          "HIP graph replay; for runs under rocprofv3, whose kernel tracer fails on graph launches)")
     ap.add_argument("--no-extra", action="store_true", help="skip the extra configs")
     ap.add_argument("--pmc-sample", nargs="?", const="lm_head_q4", default=None,
-                    choices=["lm_head_q4", "lm_head_i8_m64", "qgemm_896x4864", "qgemm_4864x896"],
+                    choices=["lm_head_q4", "lm_head_i8_m64", "qgemm_896x4864", "qgemm_4864x896", "i4_6912x1152",
+                             "q4_gate_up_silu_1152x6912"],
                     help="run only a 256 MiB device copy (counter calibration) and 20 launches of one kernel "
                          "(default: the q4 lm_head GEMV), for rocprofv3 --pmc passes")
     return ap.parse_args()
@@ -97,6 +103,26 @@ def pmc_sample(torch, ops, stream, gen, which: str):
         ops.encode_qgemv_batch(arr, stream=stream.cuda_stream)
         info.update({"kernel": "qgemv_mfma_kernel (int8 1152->262144, M=64)",
                      "algorithmic_bytes": i8_bytes(m, n, k, 2)})
+    elif which == "i4_6912x1152":
+        k, n, copies = 6912, 1152, 8
+        w = torch.randint(0, 256, (copies, n, k // 2), dtype=torch.uint8, device="cuda", generator=gen)
+        sc = (torch.rand((n,), device="cuda", generator=gen) * 0.019 + 0.001).to(torch.float16)
+        x = torch.randn((1, k), device="cuda", generator=gen)
+        y = torch.empty((1, n), dtype=torch.float32, device="cuda")
+        arr = op_array([ops.qgemv_op_i4_sym(w[i % copies], sc, k, x, y, k) for i in range(20)])
+        ops.encode_qgemv_batch(arr, stream=stream.cuda_stream)
+        info.update({"kernel": "qgemv_i4_kernel (symmetric i4 6912->1152, gs = K, M=1, f32 x)",
+                     "algorithmic_bytes": n * k // 2 + 2 * n + 4 * k + 4 * n})
+    elif which == "q4_gate_up_silu_1152x6912":
+        k, n, copies = 1152, 6912, 8
+        ws = [(Q4Weights(torch, n, k, gen), Q4Weights(torch, n, k, gen)) for _ in range(copies)]
+        x = torch.randn((1, k), device="cuda", generator=gen).to(torch.float16)
+        h = torch.empty((1, n), dtype=torch.float32, device="cuda")
+        for i in range(20):
+            g_, u_ = ws[i % copies]
+            ops.encode_gate_up_silu_q4_affine(g_.wq, g_.s, g_.b, u_.wq, u_.s, u_.b, x, h, stream=stream.cuda_stream)
+        info.update({"kernel": "qgemv_q4_gate_up_silu_kernel (q4 affine 1152->6912 x2 + SiLU, M=1)",
+                     "algorithmic_bytes": 2 * (n * k // 2 + 4 * n * ((k + 63) // 64)) + 2 * k + 4 * n})
     else:
         k, n = (896, 4864) if which == "qgemm_896x4864" else (4864, 896)
         m = 512
@@ -242,11 +268,14 @@ def main():
 
     extra = {}
     if not args.no_extra:
+        progress("configs[1] step and per-shape lines done")
         extra = extra_configs(torch, ops, stream, gen, graphs=not args.eager_decode_step)
 
     cpu = None
     if not args.no_cpu:
+        progress("extra lines done")
         cpu = cpu_baseline()
+        progress("cpu baseline done")
 
     out = {
         "metric": BASELINE_METRIC,
@@ -289,6 +318,7 @@ def extra_configs(torch, ops, stream, gen, graphs: bool = True):
     del src, dst
 
     res.update(launch_floor(torch, ops, stream))
+    progress("copy and launch floor done")
 
     # SmolLM2-135M int8, fp32 scale, fp32 x, K=576
     for n in (576, 1536):
@@ -331,10 +361,13 @@ def extra_configs(torch, ops, stream, gen, graphs: bool = True):
                                                    "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     del wset
 
+    progress("configs[0] and configs[2] done")
     res.update(decode_step_cfg5(graphs))
+    progress("configs[4] decode step done")
     res.update(lowbit_gemvs(torch, ops, stream, gen))
     res.update(i4_gemma_mlp(torch, ops, stream, gen))
     res.update(q4_gate_up_silu(torch, ops, stream, gen))
+    progress("low-bit, i4 and fused gate/up lines done")
 
     # M=512 prefill qGEMM (MFMA)
     m = 512
