@@ -19,6 +19,7 @@ import numpy as np
 import pytest
 
 import oracle
+from tests._llama_f64 import f64_step
 
 pytestmark = pytest.mark.gpu
 
@@ -79,6 +80,10 @@ def block_table(s):
 
 def base_of(bt, tpos, layer):
     return int(bt[tpos // TPB]) * (L * TPB * KVD) + layer * (TPB * KVD) + (tpos % TPB) * KVD
+
+
+DIMS = dict(L=L, HID=HID, NH=NH, NKV=NKV, HD=HD, VOCAB=VOCAB, EPS=EPS, THETA=THETA, TPB=TPB)
+F64_TOL = 1e-4  # logits of an f32 step against the float64 step (observed: 7e-6 for the oracle step)
 
 
 def oracle_step(model, kcache, vcache, token, pos, bt):
@@ -169,10 +174,14 @@ def test_decode_step_greedy_ids_match_cpu_reference():
             top2 = np.sort(ref_logits)[-2:]
             margins.append(float(top2[1] - top2[0]))
             rel = float(np.max(np.abs(hip_logits - ref_logits)) / np.max(np.abs(ref_logits)))
-            print(f"session {s}: token {token} -> hip {tok.value} ref {ref_id} "
-                  f"top2 margin {margins[-1]:.4g} logits rel err {rel:.2e}")
-            assert tok.value == ref_id
+            # the runner's CPU helpers (RMSNorm, RoPE, attention, f16 K/V) against an independent float64 step
+            f64_id, f64_logits = f64_step(model, k0.copy(), v0.copy(), token, pos, bt, DIMS)
+            rel64 = float(np.max(np.abs(hip_logits - f64_logits)) / np.max(np.abs(f64_logits)))
+            print(f"session {s}: token {token} -> hip {tok.value} ref {ref_id} f64 {f64_id} "
+                  f"top2 margin {margins[-1]:.4g} logits rel err {rel:.2e} (float64 step {rel64:.2e})")
+            assert tok.value == ref_id == f64_id
             assert rel <= 1e-3
+            assert rel64 <= F64_TOL
         # the step wrote the same K/V row on both sides (f16 RNE of each projection)
         assert np.array_equal(np.flatnonzero(hk != k0), np.flatnonzero(ok != k0))
     finally:
@@ -245,6 +254,7 @@ def test_device_step_batched_sessions_match_cpu_reference():
         k0, v0 = make_kv()
         assert lib.cellm_llama_dev_kv_upload(h, k0.ctypes.data, v0.ctypes.data, k0.size) == 0, err()
         ok, ov = k0.copy(), v0.copy()
+        fk, fv = k0.copy(), v0.copy()
         bts = np.stack([block_table(s) for s in range(SESSIONS)]).astype(np.uint32)
         tokens = np.array([(1000 + 7919 * s) % VOCAB for s in range(SESSIONS)], np.uint32)
         for pos in (CTX - 2, CTX - 1):
@@ -253,12 +263,16 @@ def test_device_step_batched_sessions_match_cpu_reference():
             for s in range(SESSIONS):
                 ref_id, ref_logits = oracle_step(model, ok, ov, int(tokens[s]), pos, bts[s])
                 rel = float(np.max(np.abs(logits[s] - ref_logits)) / np.max(np.abs(ref_logits)))
+                f64_id, f64_logits = f64_step(model, fk, fv, int(tokens[s]), pos, bts[s], DIMS)
+                rel64 = float(np.max(np.abs(logits[s] - f64_logits)) / np.max(np.abs(f64_logits)))
                 top2 = np.sort(ref_logits)[-2:]
-                print(f"pos {pos} session {s}: token {tokens[s]} -> device {out_tok[s]} ref {ref_id} "
-                      f"top2 margin {float(top2[1] - top2[0]):.4g} logits rel err {rel:.2e}")
-                assert out_tok[s] == ref_id
+                print(f"pos {pos} session {s}: token {tokens[s]} -> device {out_tok[s]} ref {ref_id} f64 {f64_id} "
+                      f"top2 margin {float(top2[1] - top2[0]):.4g} logits rel err {rel:.2e} (float64 step "
+                      f"{rel64:.2e})")
+                assert out_tok[s] == ref_id == f64_id
                 assert out_logit[s] == logits[s, out_tok[s]]
                 assert rel <= 1e-3
+                assert rel64 <= F64_TOL
             tokens = out_tok.copy()
         # K/V: the rows of positions CTX-2 and CTX-1 of every session and layer were written, nothing
         # else changed; the written values are within f16 rounding of the reference's (the projections
