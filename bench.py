@@ -63,7 +63,8 @@ def parse():
                          "HIP graph replay; for runs under rocprofv3, whose kernel tracer fails on graph launches)")
     ap.add_argument("--no-extra", action="store_true", help="skip the extra configs")
     ap.add_argument("--pmc-sample", nargs="?", const="lm_head_q4", default=None,
-                    choices=["lm_head_q4", "lm_head_i8_m64", "qgemm_896x4864", "qgemm_4864x896", "i4_6912x1152",
+                    choices=["lm_head_q4", "lm_head_i8_m1", "lm_head_i8_m64", "qgemm_896x4864", "qgemm_4864x896",
+                             "i4_6912x1152",
                              "q4_gate_up_silu_1152x6912"],
                     help="run only a 256 MiB device copy (counter calibration) and 20 launches of one kernel "
                          "(default: the q4 lm_head GEMV), for rocprofv3 --pmc passes")
@@ -93,15 +94,15 @@ def pmc_sample(torch, ops, stream, gen, which: str):
         ops.encode_qgemv_batch(arr, stream=stream.cuda_stream)
         info.update({"kernel": "qgemv_q4_flat_kernel (q4 affine 896->151936, M=1)",
                      "algorithmic_bytes": q4_bytes(1, n, k)})
-    elif which == "lm_head_i8_m64":
-        k, n, m, copies = 1152, 262144, 64, 2
+    elif which in ("lm_head_i8_m1", "lm_head_i8_m64"):
+        k, n, m, copies = 1152, 262144, (1 if which == "lm_head_i8_m1" else 64), 2
         w = torch.randint(-127, 128, (copies, n, k), dtype=torch.int8, device="cuda", generator=gen)
         sc = torch.rand((n,), device="cuda", generator=gen) * 0.019 + 0.001
         x = torch.randn((m, k), device="cuda", generator=gen).to(torch.float16)
         y = torch.empty((m, n), dtype=torch.float32, device="cuda")
         arr = op_array([ops.qgemv_op_i8(w[i % copies], sc, x, y) for i in range(20)])
         ops.encode_qgemv_batch(arr, stream=stream.cuda_stream)
-        info.update({"kernel": "qgemv_mfma_kernel (int8 1152->262144, M=64)",
+        info.update({"kernel": f"{'qgemv_i8_kernel' if m == 1 else 'qgemv_mfma_kernel'} (int8 1152->262144, M={m})",
                      "algorithmic_bytes": i8_bytes(m, n, k, 2)})
     elif which == "i4_6912x1152":
         k, n, copies = 6912, 1152, 8
