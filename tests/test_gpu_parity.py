@@ -419,6 +419,24 @@ def test_qgemm_ragged_m_n(ops, m, k, n, group, sb):
     assert rel_err(y, oracle.gemm_xwT(x, w16)) <= TOL_F32
 
 
+@pytest.mark.parametrize("n,k,m,sb,group", [
+    (4864, 896, 1, np.float16, 64),      # Qwen2.5-0.5B gate, as the LFM runner passes f32 x
+    (896, 4864, 4, np.float16, 64),      # long rows: 64-lane teams
+    (2560, 960, 3, np.float32, 64),      # f32 S/B, as LFM .cellm files hold them
+    (960, 2560, 2, "bf16", 128),
+    (1000, 1024, 1, np.float16, 32),
+    (300, 10240, 2, np.float16, 64),
+    (200, 10240, 4, np.float16, 64),
+])
+def test_q4_affine_f32_activations(ops, n, k, m, sb, group):
+    """MLX q4 affine GEMV with f32 x (linear_i4_out_in, lfm.rs:985-1066), the
+    LFM runner's activations: one wave per row, f32 arithmetic, within 1e-3
+    of the reference order."""
+    wq, s, b, x = make_q4(n, k, m, sb_dtype=sb, x_dtype=np.float32, group=group, salt=70 + m + k % 97)
+    y = _run_q4(ops, wq, s, b, x, group=group)
+    assert rel_err(y, oracle.qgemv_q4_affine(wq, s, b, x, k, gs=group)) <= TOL_F32
+
+
 # ------------------------------------------------------------------- i4 sym ----
 
 def test_i4_sym_logits(ops):
