@@ -385,15 +385,17 @@ def test_q4_prefill_qgemm_m512(ops, k, n):
     assert rel_err(y, ref32) <= TOL_F16_TILE
 
 
+@pytest.mark.parametrize("n", [64, 224])
 @pytest.mark.parametrize("sb", [np.float16, "bf16", np.float32])
-def test_qgemm_tiles_are_the_converter_f16_dequant(ops, sb):
+def test_qgemm_tiles_are_the_converter_f16_dequant(ops, sb, n):
     """X = identity makes Y[m, n] = W_tile[n, m]: one exact product, zeros
     elsewhere, so the GEMM output exposes the f16 tile values bit for bit.
     Row 0 carries the double-rounding case of the oracle pins (q=3,
-    s=1+2^-10, b=-2^-24), where one rounding of q*s+b would differ."""
+    s=1+2^-10, b=-2^-24), where one rounding of q*s+b would differ.  n = 224
+    ends in a ragged 96-column tile."""
     import torch
 
-    k, n = 256, 64
+    k = 256
     wq, s, b, _ = make_q4(n, k, 1, cfg=4, sb_dtype=sb, salt=77)
     if sb == np.float16:
         wq[0, 0] = (wq[0, 0] & ~np.uint32(0xF)) | np.uint32(3)
@@ -411,6 +413,7 @@ def test_qgemm_tiles_are_the_converter_f16_dequant(ops, sb):
     (300, 640, 1000, 128, "bf16"),
     (130, 4864, 200, 64, np.float32),   # split-K through the workspace
     (64, 256, 96, 32, np.float16),
+    (130, 896, 300, 64, np.float16),    # dequant-at-the-MFMA kernel, ragged M and N over 7 k-steps
 ])
 def test_qgemm_ragged_m_n(ops, m, k, n, group, sb):
     wq, s, b, x = make_q4(n, k, m, cfg=4, sb_dtype=sb, group=group, salt=5 + k)
