@@ -64,7 +64,7 @@ def parse():
     ap.add_argument("--no-extra", action="store_true", help="skip the extra configs")
     ap.add_argument("--pmc-sample", nargs="?", const="lm_head_q4", default=None,
                     choices=["lm_head_q4", "lm_head_i8_m1", "lm_head_i8_m64", "qgemm_896x4864", "qgemm_4864x896",
-                             "i4_6912x1152",
+                             "i4_6912x1152", "decode_layer_4",
                              "q4_gate_up_silu_1152x6912"],
                     help="run only a 256 MiB device copy (counter calibration) and 20 launches of one kernel "
                          "(default: the q4 lm_head GEMV), for rocprofv3 --pmc passes")
@@ -104,6 +104,39 @@ def pmc_sample(torch, ops, stream, gen, which: str):
         ops.encode_qgemv_batch(arr, stream=stream.cuda_stream)
         info.update({"kernel": f"{'qgemv_i8_kernel' if m == 1 else 'qgemv_mfma_kernel'} (int8 1152->262144, M={m})",
                      "algorithmic_bytes": i8_bytes(m, n, k, 2)})
+    elif which == "decode_layer_4":
+        # one configs[4] layer for 4 sessions at context 512, eager launches (no runner, no graph): the
+        # fused QKV (+ RMSNorm, RoPE, K/V write), attention, o_proj, fused gate/up, down_proj, 20 times
+        H, NH, NKV, HD, I, L, TPB, CTX, R = 960, 15, 5, 64, 2560, 1, 16, 512, 4
+        kvd, blocks = NKV * HD, CTX // TPB
+        w8 = lambda o, i: torch.randint(-127, 128, (o, i), dtype=torch.int8, device="cuda", generator=gen)
+        sc = lambda o: (torch.rand((o,), device="cuda", generator=gen) * 0.004 + 0.001).to(torch.float16)
+        wq, wk, wv, wo, wg, wu, wd = w8(H, H), w8(kvd, H), w8(kvd, H), w8(H, H), w8(I, H), w8(I, H), w8(H, I)
+        sq, sk, sv, so, sg, su, sd = sc(H), sc(kvd), sc(kvd), sc(H), sc(I), sc(I), sc(H)
+        norm = torch.ones(H, dtype=torch.float32, device="cuda")
+        total = R * blocks
+        kc = torch.randn(total * L * TPB * kvd, device="cuda", generator=gen).to(torch.float16)
+        vc = torch.randn(total * L * TPB * kvd, device="cuda", generator=gen).to(torch.float16)
+        bt = torch.tensor([[b * R + s for b in range(blocks)] for s in range(R)], dtype=torch.int32, device="cuda")
+        pos = torch.full((R,), CTX - 1, dtype=torch.int32, device="cuda")
+        ang = torch.arange(CTX, device="cuda").float()[:, None] * torch.pow(
+            100000.0, -torch.arange(0, HD, 2, device="cuda").float() / HD)[None, :]
+        cs = torch.stack([torch.cos(ang), torch.sin(ang)], dim=-1).contiguous()
+        xa, xb = torch.randn((R, H), device="cuda", generator=gen), torch.zeros((R, H), device="cuda")
+        y = torch.zeros((R, H), device="cuda")
+        q = torch.empty((R, NH * HD), device="cuda")
+        att = torch.empty((R, NH * HD), device="cuda")
+        h = torch.empty((R, I), device="cuda")
+        sp = stream.cuda_stream
+        for _ in range(20):
+            ops.encode_decode_qkv(xa, y, xb, norm, 1e-5, wq, sq, wk, sk, wv, sv, NH, NKV, HD, pos, cs, q, kc, vc, bt,
+                                  total, L, TPB, 0, stream=sp)
+            ops.encode_attention(q, kc, vc, bt, pos, att, NH, NKV, HD, total, L, TPB, 0, stream=sp)
+            ops.encode_qgemv_i8(wo, so, att, y, stream=sp)
+            ops.encode_decode_gate_up(xb, y, xa, norm, 1e-5, wg, sg, wu, su, h, stream=sp)
+            ops.encode_qgemv_i8(wd, sd, h, y, stream=sp)
+        info.update({"kernel": "decode_qkv_kernel, attn_partial/combine, qgemv_i8 (o, down), decode_gate_up_kernel",
+                     "algorithmic_bytes": sum(t.numel() for t in (wq, wk, wv, wo, wg, wu, wd))})
     elif which == "i4_6912x1152":
         k, n, copies = 6912, 1152, 8
         w = torch.randint(0, 256, (copies, n, k // 2), dtype=torch.uint8, device="cuda", generator=gen)

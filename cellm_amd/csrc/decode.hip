@@ -936,9 +936,9 @@ hipError_t attention_static_scratch(float** out)
     return hipSuccess;
 }
 
-// Host-side geometry of the fused decode GEMVs: LPR = 64 lanes per row pair
-// while a row has at least 64 chunks of 16 bytes, fewer otherwise; C chunks
-// per lane; KR registers per thread of the staged row; MT activation rows.
+// Host-side geometry of the fused decode GEMVs (launch_decode): LPR lanes per
+// row pair, 64 for rows of more than 16 chunks of 16 bytes, 16 otherwise; C
+// chunks per lane; KR registers per thread of the staged row; MT activation rows.
 bool decode_fused_supported(int rows, int H)
 {
     return rows >= 1 && rows <= 4 && H >= 16 && H % 16 == 0 && H <= 4 * 4 * kNormThreads;
@@ -988,13 +988,15 @@ hipError_t launch_decode_mt(int rows, int H, const Args& a, int teams_total, hip
     return launch_decode_kr<LPR, C, 4, QKV>(H, a, teams_total, lds, st);
 }
 
-// chunks per row nchunk = H / 16: LPR 64 with C = ceil(nchunk / 64) (up to 8)
+// chunks per row nchunk = H / 16: 16 lanes up to 16 chunks, else 64 lanes with C = ceil(nchunk / 64)
+// (up to 4).  At hidden 960 (60 chunks) 64 lanes of one chunk each beat 32 lanes of two by ~1 % of
+// the configs[4] step: twice the waves, each with half the dot work after its loads land.
 template <bool QKV, class Args>
 hipError_t launch_decode(int rows, int H, const Args& a, int teams_total, hipStream_t st)
 {
     const int nchunk = H >> 4;
     if (nchunk <= 16) return launch_decode_mt<16, 1, QKV>(rows, H, a, teams_total, st);
-    if (nchunk <= 64) return launch_decode_mt<32, 2, QKV>(rows, H, a, teams_total, st);
+    if (nchunk <= 64) return launch_decode_mt<64, 1, QKV>(rows, H, a, teams_total, st);
     if (nchunk <= 128) return launch_decode_mt<64, 2, QKV>(rows, H, a, teams_total, st);
     return launch_decode_mt<64, 4, QKV>(rows, H, a, teams_total, st);
 }
