@@ -10,7 +10,7 @@ from HBM.  `value` = algorithmic bytes of the step / step time (GB/s).
 
 A step is one cellm_hip_qgemv_batch call (the five projections enqueued from C),
 so the host's per-call cost does not gate the small projections.  Extra keys
-report the other BASELINE configs (int8 GEMV, Gemma batched decode, M=512
+report the other BASELINE.json configs (int8 GEMV, Gemma batched decode, M=512
 prefill qGEMM) and the roofline of the dominant kernel (the lm_head GEMV),
 whose per-launch duration is measured with HIP events on the launch stream
 around batch calls of 100 launches (median of three blocks, after 20 ms of
@@ -683,8 +683,8 @@ def cpu_baseline():
     `value` is configs[1]'s decode pass as the reference runs it per token
     (LfmRunner, lfm.rs): the four projections hit the f32 dequant cache and run
     the f32 row GEMV ('warm', lfm.rs:1056-1063); the tied lm_head dequantizes on
-    the fly (lfm.rs:700-741).  `legs` time the other reference paths BASELINE
-    names: the same pass 'cold' (the f32 dequant of each projection included,
+    the fly (lfm.rs:700-741).  `legs` time the other reference CPU paths of the
+    the same pass 'cold' (the f32 dequant of each projection included,
     lfm.rs:1012-1026), matmul_i8_f32 at configs[0] (cpu_kernels.rs:66-133), the
     configs[2] int8 lm_head row GEMV, and matmul_f32 at configs[3]'s M = 512
     over the dequantized weight (cpu_kernels.rs:36-63).
