@@ -394,6 +394,34 @@ def extra_configs(torch, ops, stream, gen, graphs: bool = True):
         res[f"cfg3_q4_gate_up_1152x13824_m{m}"] = {"us": round(ms * 1e3, 2), "GB/s": round(b / (ms * 1e-3) / 1e9, 1),
                                                    "frac_hbm": round(b / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
     del wset
+    # configs[2]'s other projections: int8 fused QKV 1152->1536 and o 1024->1152, q4 down 6912->1152
+    for name, kind, k, n in (("i8_attn_qkv", "i8", 1152, 1536), ("i8_attn_o", "i8", 1024, 1152),
+                             ("q4_mlp_down", "q4", 6912, 1152)):
+        wbytes = n * k if kind == "i8" else n * k // 2 + 4 * n * (k // 64)
+        copies = max(2, -(-512 * 2**20 // wbytes) + 1)
+        if kind == "i8":
+            w8 = torch.randint(-127, 128, (copies, n, k), dtype=torch.int8, device="cuda", generator=gen)
+            s8 = torch.rand((n,), device="cuda", generator=gen) * 0.019 + 0.001
+        else:
+            wset = [Q4Weights(torch, n, k, gen) for _ in range(copies)]
+        for m in (1, 4, 16, 64):
+            x = torch.randn((m, k), device="cuda", generator=gen).to(torch.float16)
+            y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+            if kind == "i8":
+                arr = op_array([ops.qgemv_op_i8(w8[i % copies], s8, x, y) for i in range(100)])
+                bts = i8_bytes(m, n, k, 2)
+            else:
+                arr = op_array([ops.qgemv_op_q4_affine(wset[i % copies].wq, wset[i % copies].s, wset[i % copies].b,
+                                                       x, y) for i in range(100)])
+                bts = q4_bytes(m, n, k)
+            ms = time_batch(torch, ops, arr, stream)
+            res[f"cfg3_{name}_{k}x{n}_m{m}"] = {"us": round(ms * 1e3, 2),
+                                                "GB/s": round(bts / (ms * 1e-3) / 1e9, 1),
+                                                "frac_hbm": round(bts / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        if kind == "i8":
+            del w8
+        else:
+            del wset
 
     progress("configs[0] and configs[2] done")
     res.update(decode_step_cfg5(graphs))

@@ -183,8 +183,11 @@ def test_i8_gemv_smollm_config1(ops, n):
 
 
 @pytest.mark.parametrize("k,n", [(1152, 1536), (1024, 1152)])
-@pytest.mark.parametrize("m", [1, 4])
+@pytest.mark.parametrize("m", [1, 4, 16, 64])
 def test_i8_gemv_gemma_attn_f16x(ops, k, n, m):
+    """Config 3's int8 attention projections (fused QKV 1152 -> 1536, o 1024 ->
+    1152) at every M it names: M <= 4 the VALU GEMV, 16 and 64 the batched
+    MFMA path (int8 exact in f16: exact products, the f32 bar)."""
     w, s, x = make_i8(n, k, m, cfg=3, x_dtype=np.float16, salt=m)
     y = _run_i8(ops, w, s, x)
     ref = oracle.qgemv_i8(w, s, x)
@@ -353,8 +356,18 @@ def test_i8_batched_mfma_small_m_and_k_chunks(ops, m):
         assert rel_err(y, oracle.qgemv_i8(w, s, x)) <= TOL_F32, (m, k)
 
 
-@pytest.mark.parametrize("m,k,n", [(5, 6912, 1152), (17, 6912, 1152), (64, 6912, 1152), (2, 1152, 8200),
-                                   (4, 1152, 8200)])
+@pytest.mark.parametrize("m", [1, 4])
+def test_q4_gemma_down_config3_small_m(ops, m):
+    """Config 3's q4 down projection 6912 -> 1152 at M = 1 and 4: the VALU GEMV
+    (64 lanes per row, two register passes), exact products and f32 sums."""
+    k, n = 6912, 1152
+    wq, s, b, x = make_q4(n, k, m, cfg=3, salt=40 + m)
+    y = _run_q4(ops, wq, s, b, x)
+    assert rel_err(y, oracle.qgemv_q4_affine(wq, s, b, x, k)) <= TOL_F32
+
+
+@pytest.mark.parametrize("m,k,n", [(5, 6912, 1152), (16, 6912, 1152), (17, 6912, 1152), (64, 6912, 1152),
+                                   (2, 1152, 8200), (4, 1152, 8200)])
 def test_q4_batched_mfma_k_chunks(ops, m, k, n):
     """Gemma down projection (several X chunks in LDS) at 5..64 rows; 2..4
     rows take the MFMA path only for >= 8192 outputs."""
