@@ -222,8 +222,11 @@ int32_t qgemv_i8_impl(cellm_hip_ctx* ctx, const int8_t* w, const void* scales, i
     // int8).  At m <= 4 the VALU GEMV wins until there are rows enough to fill
     // the chip with MFMA tiles.
     if (!force_gemm && gemm_ok && (m > 4 || n >= kMfmaMinRows) && qgemv_mfma_supported(1, (int)m, (int)k, 0)) {
+        float* ws = nullptr;
+        const size_t need = qgemv_mfma_workspace_bytes(1, (int)m, (int)n, (int)k);
+        if (int32_t rc = get_workspace(ctx, st, need, &ws)) return rc;
         HIP_TRY(launch_qgemv_mfma_i8(w, scales, sdt, per_channel, reinterpret_cast<const _Float16*>(x), bias, y,
-                                     (int)m, (int)n, (int)k, st),
+                                     (int)m, (int)n, (int)k, ws, need, st),
                 "qgemv_mfma_i8 launch");
         return CELLM_HIP_OK;
     }
@@ -283,8 +286,11 @@ int32_t qgemv_q4_impl(cellm_hip_ctx* ctx, const uint32_t* wq, const void* scales
     // only for long outputs (else the f32-accumulating VALU GEMV is faster)
     if (!force_gemm && (m > 4 || n >= kMfmaMinRows) && gemm_ok &&
         qgemv_mfma_supported(0, (int)m, (int)k, (int)group)) {
+        float* ws = nullptr;
+        const size_t need = qgemv_mfma_workspace_bytes(0, (int)m, (int)n, (int)k);
+        if (int32_t rc = get_workspace(ctx, st, need, &ws)) return rc;
         HIP_TRY(launch_qgemv_mfma_q4(wq, scales, biases, sbt, (int)group, reinterpret_cast<const _Float16*>(x), y,
-                                     (int)m, (int)n, (int)k, st),
+                                     (int)m, (int)n, (int)k, ws, need, st),
                 "qgemv_mfma_q4 launch");
         return CELLM_HIP_OK;
     }

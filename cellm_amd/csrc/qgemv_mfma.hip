@@ -92,7 +92,7 @@ template <int WT, int MS, int NT, int DEPTH, int SBT, bool CHUNKED, int BT = kBl
 __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
     const void* __restrict__ W, const void* __restrict__ S, const void* __restrict__ Bz, int per_channel, int gshift,
     const _Float16* __restrict__ X, const float* __restrict__ bias, float* __restrict__ Y, int M, int N, int K, int KC,
-    int ntiles)
+    int ntiles, int pps, int nsplit, float* __restrict__ part)
 {
     extern __shared__ __align__(16) _Float16 xs[];  // [MS*16][KC + kXPad]
     constexpr int KB = WT == 1 ? 64 : 128;  // K per block: 64 bytes of every row
@@ -107,9 +107,9 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
     const char* wb = reinterpret_cast<const char*>(W);
     const int row_in_tile = wave * NT * 16 + rl;
 
-    // ---- X staging: columns [k0, k0 + kcl) in unpack order, rows >= M zero.
+    // ---- X staging: columns [kb, kb + kcl) in unpack order, rows >= M zero.
     // Loads are unconditional (clamped) so they issue back to back.
-    auto stage = [&](int k0, int kcl) {
+    auto stage = [&](int kb, int kcl) {
         const int words = kcl >> 3, total = MS * 16 * words;
         for (int base = threadIdx.x; base < total; base += 4 * BT) {
             u4_t r[4];
@@ -117,7 +117,7 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
             for (int u = 0; u < 4; ++u) {
                 const int idx = min(base + u * BT, total - 1);
                 const int m = idx / words, wd = idx - m * words;
-                r[u] = *reinterpret_cast<const u4_t*>(X + (size_t)min(m, M - 1) * K + k0 + wd * 8);
+                r[u] = *reinterpret_cast<const u4_t*>(X + (size_t)min(m, M - 1) * K + kb + wd * 8);
             }
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
@@ -164,14 +164,16 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
             }
         }
     };
-    // stage the X chunk that starts at column kcol, if one does; returns the
+    // stage the X chunk that starts at column kcol, if one does (chunks start at
+    // the work item's first column k0 and end at its last, k1); returns the
     // column's offset in the staged X
+    int k0 = 0, k1 = K;
     auto chunk_at = [&](int kcol) {
         if constexpr (CHUNKED) {
-            const int c = kcol / KC, off = kcol - c * KC;
+            const int rel = kcol - k0, c = rel / KC, off = rel - c * KC;
             if (off == 0) {
                 __syncthreads();  // every wave is done with the previous chunk
-                stage(c * KC, min(KC, K - c * KC));
+                stage(k0 + c * KC, min(KC, k1 - (k0 + c * KC)));
                 __syncthreads();
             }
             return off;
@@ -190,7 +192,14 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
     // about a quarter slower.
     const bool low8 = (rl & 8) == 0;
     const int npairs = nkb >> 1;
-    for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    // Work item = (tile, split): split s covers block pairs [s*pps, min(npairs, (s+1)*pps)), the
+    // last split also the odd last K block.  Consecutive items share a split (and its X columns).
+    for (int item = blockIdx.x; item < ntiles * nsplit; item += gridDim.x) {
+        const int split = item / ntiles, tile = item - split * ntiles;
+        const int pb = split * pps, pe = min(npairs, pb + pps);
+        const bool last_split = split == nsplit - 1;
+        k0 = pb * 2 * KB;
+        k1 = last_split ? K : pe * 2 * KB;
         // rows past N read row N-1 and are never stored
         const char* wpair[NT][2];
         const char* wtail[NT];
@@ -219,13 +228,13 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
 #pragma unroll
             for (int t = 0; t < NT; ++t) acc[i][t] = f4_t{0.f, 0.f, 0.f, 0.f};
 
-        for (int p0 = 0; p0 < npairs; p0 += DEPTH) {
+        for (int p0 = pb; p0 < pe; p0 += DEPTH) {
             // the group's weights (and q4 group scale/bias) in one burst
             u4_t ld[DEPTH][NT][2];
             uint32_t sr[DEPTH][2][NT], br[DEPTH][2][NT];
 #pragma unroll
             for (int d = 0; d < DEPTH; ++d) {
-                if (p0 + d < npairs) {
+                if (p0 + d < pe) {
 #pragma unroll
                     for (int t = 0; t < NT; ++t) {
 #pragma unroll
@@ -246,7 +255,7 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
             const int kx0 = chunk_at(p0 * 2 * KB);
 #pragma unroll
             for (int d = 0; d < DEPTH; ++d) {
-                if (p0 + d < npairs) {
+                if (p0 + d < pe) {
                     u4_t w0[NT], w1[NT];
 #pragma unroll
                     for (int t = 0; t < NT; ++t) {
@@ -263,7 +272,7 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
                 }
             }
         }
-        if (nkb & 1) {
+        if ((nkb & 1) && last_split) {
             // odd last block: 16 rows x 64 bytes, already in the B layout
             u4_t w[NT];
             uint32_t s[NT], b[NT];
@@ -280,6 +289,22 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
         }
 
         // C tile: lane holds activation rows 4*(lane/16)+e, weight row lane%16
+        if (part) {
+            // split-K: raw sums to part[split][m][n]; the reduction applies the scale and bias
+            float* pp = part + (size_t)split * M * N;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const int n = tile * ROWS + row_in_tile + t * 16;
+#pragma unroll
+                for (int i = 0; i < MS; ++i)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int m = i * 16 + g * 4 + e;
+                        if (n < N && m < M) pp[(size_t)m * N + n] = acc[i][t][e];
+                    }
+            }
+            continue;
+        }
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             const int n = tile * ROWS + row_in_tile + t * 16;
@@ -332,9 +357,92 @@ int resident_blocks(Kern kern, size_t lds)
 
 constexpr size_t kWholeXLds = 152 * 1024;  // the BT = 1024 form holds X up to this size
 
+// Split-K reduction: y[m,n] = (sum over splits, in split order, of part[s][m][n]) * scale + bias
+// (int8; the scale after the sum, as cpu_kernels.rs:130 applies it), or the plain sum (q4).
+template <int WT, int SBT>
+__global__ __launch_bounds__(256) void mfma_splitk_reduce_kernel(const float* __restrict__ part, int nsplit,
+                                                                 const void* __restrict__ S, int per_channel,
+                                                                 const float* __restrict__ bias,
+                                                                 float* __restrict__ Y, int M, int N)
+{
+    const size_t total = (size_t)M * N, plane = total;
+    if ((N & 3) == 0) {
+        const size_t n4 = total >> 2;
+        for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (size_t)gridDim.x * blockDim.x) {
+            f4_t a = reinterpret_cast<const f4_t*>(part)[i];
+            for (int sp = 1; sp < nsplit; ++sp) a += reinterpret_cast<const f4_t*>(part + sp * plane)[i];
+            if constexpr (WT == 1) {
+                const int n = (int)((4 * i) % (size_t)N);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float s = raw_to_f32<SBT>(load_raw<SBT>(S, per_channel ? (size_t)(n + e) : 0));
+                    a[e] = a[e] * s + (bias ? bias[n + e] : 0.0f);
+                }
+            }
+            reinterpret_cast<f4_t*>(Y)[i] = a;
+        }
+        return;
+    }
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+        float a = part[i];
+        for (int sp = 1; sp < nsplit; ++sp) a += part[sp * plane + i];
+        if constexpr (WT == 1) {
+            const int n = (int)(i % (size_t)N);
+            const float s = raw_to_f32<SBT>(load_raw<SBT>(S, per_channel ? (size_t)n : 0));
+            a = a * s + (bias ? bias[n] : 0.0f);
+        }
+        Y[i] = a;
+    }
+}
+
+int device_cus()
+{
+    static std::mutex mu;
+    static std::vector<std::pair<int, int>> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    std::lock_guard<std::mutex> lk(mu);
+    for (const auto& e : cache)
+        if (e.first == dev) return e.second;
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 256;
+    cache.push_back({dev, cus});
+    return cus;
+}
+
+// Split-K plan of the batched kernel.  Few 64-row W tiles (small N) over a long K leave most CUs
+// idle while each wave walks the whole K; then K is cut into splits of pps block pairs, each
+// (tile, split) is a work item, and a second kernel adds the splits' partial sums.
+struct SplitPlan {
+    int nsplit = 1, pps = 0;
+};
+
+SplitPlan split_plan(int wt, int M, int N, int K)
+{
+    SplitPlan p;
+    const int KB = wt == 1 ? 64 : 128, npairs = (K / KB) >> 1;
+    p.pps = npairs;
+    constexpr int ROWS = (kBlock / 64) * 16;  // one 16-row tile per wave
+    const int ntiles = (N + ROWS - 1) / ROWS, cus = device_cus();
+    // the unsplit kernel's per-wave walk: pairs x 16-row X tiles, a q4 pair (256 k with its dequant)
+    // counted twice; below ~20 the walk is short next to a second launch (measured on MI355X: int8
+    // 1024->1152 at M=16 7.6 us unsplit, 9.2 us split; int8 2560->960 at M=8 14.6 / 9.8 us)
+    const int walk = npairs * ((M + 15) / 16) * (wt == 1 ? 1 : 2);
+    if (M < 2 || npairs < 2 || ntiles * 2 > cus || walk < 20) return p;
+    // about one item per CU, each at least two block pairs: one-pair items measured 1-2 us slower
+    // (q4 4864->896 and 6912->1152, int8 1152->1536, M = 8..64), four-pair items 2 us slower at
+    // 6912->1152, M=64
+    const int want = (cus + ntiles - 1) / ntiles;
+    p.pps = std::max(2, (npairs + want - 1) / want);
+    p.nsplit = (npairs + p.pps - 1) / p.pps;
+    if (p.nsplit < 2) p = SplitPlan{1, npairs};
+    return p;
+}
+
 template <int WT, int MS, int NT, int SBT>
 hipError_t launch_mfma_nt(const void* W, const void* S, const void* B, int per_channel, int gshift, const _Float16* X,
-                          const float* bias, float* Y, int M, int N, int K, hipStream_t st)
+                          const float* bias, float* Y, int M, int N, int K, const SplitPlan& sp, float* ws,
+                          hipStream_t st)
 {
     constexpr int KB = WT == 1 ? 64 : 128;
     if constexpr (MS == 4 && NT == 1) {
@@ -343,20 +451,17 @@ hipError_t launch_mfma_nt(const void* W, const void* S, const void* B, int per_c
         // registers per lane a 1024-thread block leaves, and 8 waves of two tiles stream 12 % slower:
         // measured).  q4 (its dequant needs more registers): 512 threads.
         const size_t whole = (size_t)MS * 16 * (K + kXPad) * 2;
-        if (whole > 80 * 1024 && whole <= kWholeXLds) {
+        if (sp.nsplit == 1 && whole > 80 * 1024 && whole <= kWholeXLds) {
             constexpr int BT = WT == 1 ? 1024 : 512, DEPTH = 2, ROWS = (BT / 64) * NT * 16;
             auto kern = qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, false, BT>;
             if (hipError_t e = allow_big_lds(kern, (int)kWholeXLds); e != hipSuccess) return e;
             const int ntiles = (N + ROWS - 1) / ROWS;
-            int per_cu = 0, cus = 0, dev = 0;
-            (void)hipGetDevice(&dev);
-            if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
-                cus = 1;
+            int per_cu = 0;
             if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, BT, whole) != hipSuccess || per_cu < 1)
                 per_cu = 1;
-            const int grid = std::min(ntiles, per_cu * cus);
+            const int grid = std::min(ntiles, per_cu * device_cus());
             hipLaunchKernelGGL(kern, dim3(grid), dim3(BT), whole, st, W, S, B, per_channel, gshift, X, bias, Y, M, N, K,
-                               K, ntiles);
+                               K, ntiles, (K / KB) >> 1, 1, (float*)nullptr);
             return hipGetLastError();
         }
     }
@@ -366,44 +471,60 @@ hipError_t launch_mfma_nt(const void* W, const void* S, const void* B, int per_c
     // when it fits, else chunks of KC columns (a multiple of the K block)
     int KC = std::max(1, (80 * 1024 / (MS * 16 * 2) - kXPad) / (2 * DEPTH * KB)) * (2 * DEPTH * KB);
     if (KC >= K) KC = K;
-    const size_t lds = (size_t)MS * 16 * (KC + kXPad) * 2;
     const int ntiles = (N + ROWS - 1) / ROWS;
+    float* part = nullptr;
+    if (sp.nsplit > 1) {
+        // one split's columns (plus an odd last block) in one chunk when they fit
+        const int span = sp.pps * 2 * KB + ((K / KB) & 1 ? KB : 0);
+        if ((size_t)MS * 16 * (span + kXPad) * 2 <= 80 * 1024 || span < KC) KC = span;
+        part = ws;
+    }
+    const size_t lds = (size_t)MS * 16 * (KC + kXPad) * 2;
+    const int items = ntiles * sp.nsplit;
     if (KC < K) {
         auto kern = qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, true>;
-        const int grid = std::min(ntiles, resident_blocks(kern, lds));
+        const int grid = std::min(items, resident_blocks(kern, lds));
         hipLaunchKernelGGL(kern, dim3(grid), dim3(kBlock), lds, st, W, S, B, per_channel, gshift, X, bias, Y, M, N, K,
-                           KC, ntiles);
+                           KC, ntiles, sp.pps, sp.nsplit, part);
     } else {
         auto kern = qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, false>;
-        const int grid = std::min(ntiles, resident_blocks(kern, lds));
+        const int grid = std::min(items, resident_blocks(kern, lds));
         hipLaunchKernelGGL(kern, dim3(grid), dim3(kBlock), lds, st, W, S, B, per_channel, gshift, X, bias, Y, M, N, K,
-                           KC, ntiles);
+                           KC, ntiles, sp.pps, sp.nsplit, part);
     }
+    if (hipError_t e = hipGetLastError(); e != hipSuccess || sp.nsplit == 1) return e;
+    const size_t work = (N & 3) == 0 ? (size_t)M * N / 4 : (size_t)M * N;
+    const unsigned blocks = (unsigned)std::min<size_t>((work + 255) / 256, 2048);
+    hipLaunchKernelGGL((mfma_splitk_reduce_kernel<WT, SBT>), dim3(blocks), dim3(256), 0, st, ws, sp.nsplit, S,
+                       per_channel, bias, Y, M, N);
     return hipGetLastError();
 }
 
 template <int WT, int MS, int SBT>
 hipError_t launch_mfma_ms(const void* W, const void* S, const void* B, int per_channel, int gshift, const _Float16* X,
-                          const float* bias, float* Y, int M, int N, int K, hipStream_t st)
+                          const float* bias, float* Y, int M, int N, int K, const SplitPlan& sp, float* ws,
+                          hipStream_t st)
 {
     // two 16-row W tiles per wave when there are rows enough to fill the chip, unless X needs the
     // one-block-per-CU form (one tile per wave there)
     const size_t whole = (size_t)MS * 16 * (K + kXPad) * 2;
     const bool whole_x = MS == 4 && whole > 80 * 1024 && whole <= kWholeXLds;
-    if (N >= 128 * 512 && !whole_x)
-        return launch_mfma_nt<WT, MS, 2, SBT>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, st);
-    return launch_mfma_nt<WT, MS, 1, SBT>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, st);
+    if (sp.nsplit == 1 && N >= 128 * 512 && !whole_x)
+        return launch_mfma_nt<WT, MS, 2, SBT>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, sp, ws, st);
+    return launch_mfma_nt<WT, MS, 1, SBT>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, sp, ws, st);
 }
 
 template <int WT, int SBT>
 hipError_t launch_mfma(const void* W, const void* S, const void* B, int per_channel, int gshift, const _Float16* X,
-                       const float* bias, float* Y, int M, int N, int K, hipStream_t st)
+                       const float* bias, float* Y, int M, int N, int K, float* ws, size_t ws_bytes, hipStream_t st)
 {
+    SplitPlan sp = split_plan(WT, M, N, K);
+    if (sp.nsplit > 1 && (!ws || ws_bytes < (size_t)sp.nsplit * M * N * sizeof(float))) sp = SplitPlan{1, (K / (WT == 1 ? 64 : 128)) >> 1};
     switch ((M + 15) / 16) {
-    case 1: return launch_mfma_ms<WT, 1, SBT>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, st);
-    case 2: return launch_mfma_ms<WT, 2, SBT>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, st);
-    case 3: return launch_mfma_ms<WT, 3, SBT>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, st);
-    default: return launch_mfma_ms<WT, 4, SBT>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, st);
+    case 1: return launch_mfma_ms<WT, 1, SBT>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, sp, ws, st);
+    case 2: return launch_mfma_ms<WT, 2, SBT>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, sp, ws, st);
+    case 3: return launch_mfma_ms<WT, 3, SBT>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, sp, ws, st);
+    default: return launch_mfma_ms<WT, 4, SBT>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, sp, ws, st);
     }
 }
 
@@ -416,21 +537,30 @@ bool qgemv_mfma_supported(int wt, int M, int K, int group_size)
     return K % 128 == 0 && group_size >= 32;
 }
 
-hipError_t launch_qgemv_mfma_i8(const int8_t* w, const void* S, int sdt, int per_channel, const _Float16* x,
-                                const float* bias, float* y, int M, int N, int K, hipStream_t st)
+size_t qgemv_mfma_workspace_bytes(int wt, int M, int N, int K)
 {
-    if (sdt == DT_F16) return launch_mfma<1, DT_F16>(w, S, nullptr, per_channel, 0, x, bias, y, M, N, K, st);
-    if (sdt == DT_F32) return launch_mfma<1, DT_F32>(w, S, nullptr, per_channel, 0, x, bias, y, M, N, K, st);
-    return launch_mfma<1, DT_BF16>(w, S, nullptr, per_channel, 0, x, bias, y, M, N, K, st);
+    if (M < 2 || M > 64 || K <= 0 || N <= 0) return 0;
+    const SplitPlan sp = split_plan(wt, M, N, K);
+    return sp.nsplit > 1 ? (size_t)sp.nsplit * M * N * sizeof(float) : 0;
+}
+
+hipError_t launch_qgemv_mfma_i8(const int8_t* w, const void* S, int sdt, int per_channel, const _Float16* x,
+                                const float* bias, float* y, int M, int N, int K, float* ws, size_t ws_bytes,
+                                hipStream_t st)
+{
+    if (sdt == DT_F16) return launch_mfma<1, DT_F16>(w, S, nullptr, per_channel, 0, x, bias, y, M, N, K, ws, ws_bytes, st);
+    if (sdt == DT_F32) return launch_mfma<1, DT_F32>(w, S, nullptr, per_channel, 0, x, bias, y, M, N, K, ws, ws_bytes, st);
+    return launch_mfma<1, DT_BF16>(w, S, nullptr, per_channel, 0, x, bias, y, M, N, K, ws, ws_bytes, st);
 }
 
 hipError_t launch_qgemv_mfma_q4(const uint32_t* wq, const void* S, const void* B, int sbt, int group_size,
-                                const _Float16* x, float* y, int M, int N, int K, hipStream_t st)
+                                const _Float16* x, float* y, int M, int N, int K, float* ws, size_t ws_bytes,
+                                hipStream_t st)
 {
     const int gshift = __builtin_ctz((unsigned)group_size);
-    if (sbt == DT_F16) return launch_mfma<0, DT_F16>(wq, S, B, 1, gshift, x, nullptr, y, M, N, K, st);
-    if (sbt == DT_F32) return launch_mfma<0, DT_F32>(wq, S, B, 1, gshift, x, nullptr, y, M, N, K, st);
-    return launch_mfma<0, DT_BF16>(wq, S, B, 1, gshift, x, nullptr, y, M, N, K, st);
+    if (sbt == DT_F16) return launch_mfma<0, DT_F16>(wq, S, B, 1, gshift, x, nullptr, y, M, N, K, ws, ws_bytes, st);
+    if (sbt == DT_F32) return launch_mfma<0, DT_F32>(wq, S, B, 1, gshift, x, nullptr, y, M, N, K, ws, ws_bytes, st);
+    return launch_mfma<0, DT_BF16>(wq, S, B, 1, gshift, x, nullptr, y, M, N, K, ws, ws_bytes, st);
 }
 
 }  // namespace cellm

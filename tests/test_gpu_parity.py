@@ -376,6 +376,46 @@ def test_q4_batched_mfma_k_chunks(ops, m, k, n):
     _check_f16_tiles(y, wq, s, b, x, k)
 
 
+@pytest.mark.parametrize("kind,m,k,n,sdt,group", [
+    ("i8", 8, 2560, 960, np.float16, 0), ("i8", 20, 2496, 700, "bf16", 0), ("i8", 64, 4096, 64, np.float32, 0),
+    ("q4", 8, 4864, 896, np.float32, 64), ("q4", 33, 4992, 300, "bf16", 64), ("q4", 64, 6912, 1152, np.float16, 128),
+])
+def test_batched_mfma_split_k(ops, kind, m, k, n, sdt, group):
+    """Few 64-row W tiles over a long K: the batched MFMA kernel splits K over work items
+    and a second kernel adds the partial sums in split order.  K = 2496 and 4992 end on
+    an odd K block (taken by the last split).  Two calls give the same bits."""
+    import torch
+
+    if kind == "i8":
+        w, s, x = make_i8(n, k, m, cfg=3, x_dtype=np.float16, salt=m + k)
+        if sdt == "bf16":
+            s = (s.view(np.uint32) >> 16).astype(np.uint16)
+            sref = (s.astype(np.uint32) << 16).view(np.float32)
+            st = torch.from_numpy(s.view(np.int16)).to("cuda").view(torch.bfloat16)
+        else:
+            s = s.astype(sdt)
+            sref = s.astype(np.float32)
+            st = _t(s)
+        bias = oracle.gen_normal((n,), seed(3, 5, m), 0.0, 1.0)
+        ys = []
+        for _ in range(2):
+            y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+            ops.encode_qgemv_i8(_t(w), st, _t(x), y, bias=_t(bias))
+            torch.cuda.synchronize()
+            ys.append(y.cpu().numpy())
+        assert rel_err(ys[0], oracle.qgemv_i8(w, sref, x) + bias[None, :]) <= TOL_F32
+        # one scale for the tensor
+        y1 = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        ops.encode_qgemv_i8(_t(w), st[:1].contiguous(), _t(x), y1)
+        torch.cuda.synchronize()
+        assert rel_err(y1.cpu().numpy(), oracle.qgemv_i8(w, np.full(n, sref[0], np.float32), x)) <= TOL_F32
+    else:
+        wq, s, b, x = make_q4(n, k, m, cfg=3, sb_dtype=sdt, group=group, salt=m + k)
+        ys = [_run_q4(ops, wq, s, b, x, group=group) for _ in range(2)]
+        _check_f16_tiles(ys[0], wq, s, b, x, k, group)
+    assert np.array_equal(ys[0].view(np.uint32), ys[1].view(np.uint32))
+
+
 @pytest.mark.parametrize("m,group", [(8, 128), (20, 256), (4, 128), (6, 32)])
 def test_q4_batched_mfma_other_groups(ops, m, group):
     """Groups of 32, 128 and 256 on the batched MFMA path."""
