@@ -304,6 +304,11 @@ def main():
     if not args.no_extra:
         progress("configs[1] step and per-shape lines done")
         extra = extra_configs(torch, ops, stream, gen, graphs=not args.eager_decode_step)
+        rd = extra.get("hbm_stream_read_77MB")
+        if rd:
+            # the same bytes read by the probe: the lm_head against the box's own streaming ceiling
+            roofline["measured_read_peak_GBs"] = rd["GB/s"]
+            roofline["frac_of_measured_read_peak"] = round(dom["GB/s"] / rd["GB/s"], 4)
 
     cpu = None
     if not args.no_cpu:
@@ -352,6 +357,7 @@ def extra_configs(torch, ops, stream, gen, graphs: bool = True):
     del src, dst
 
     res.update(launch_floor(torch, ops, stream))
+    res.update(measured_ceilings(torch, stream))
     progress("copy and launch floor done")
 
     # SmolLM2-135M int8, fp32 scale, fp32 x, K=576
@@ -441,7 +447,61 @@ def extra_configs(torch, ops, stream, gen, graphs: bool = True):
         ms = time_calls(torch, fn, 100, stream)
         tflops = 2.0 * m * n * k / (ms * 1e-3) / 1e12
         res[f"cfg4_qgemm_m512_{k}x{n}"] = {"us": round(ms * 1e3, 2), "TFLOP/s": round(tflops, 1),
-                                           "frac_mfma_f16": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
+                                           "frac_mfma_f16": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+                                           "frac_mfma_f16_measured": round(
+                                               tflops / res["mfma_f16_measured"]["TFLOP/s"], 4)}
+    return res
+
+
+def measured_ceilings(torch, stream):
+    """The box's own ceilings beside the published peaks (libcellm_probes.so):
+    dense f16 MFMA throughput (v_mfma_f32_32x32x16_f16 on register operands, four
+    blocks of four waves per CU) and the streaming read rate of a 77,185,280-byte
+    buffer, the q4 lm_head's algorithmic bytes (eight rotating copies, 617 MB,
+    past the 256 MB MALL)."""
+    import ctypes as C
+
+    lib = C.CDLL(str(ROOT / "cellm_amd" / "libcellm_probes.so"))
+    lib.cellm_probe_mfma_f16.argtypes = [C.c_int32, C.c_int32, C.c_void_p, C.c_void_p]
+    lib.cellm_probe_mfma_f16.restype = C.c_int32
+    lib.cellm_probe_mfma_f16_flops.argtypes = [C.c_int32, C.c_int32]
+    lib.cellm_probe_mfma_f16_flops.restype = C.c_double
+    lib.cellm_probe_stream_read.argtypes = [C.c_void_p, C.c_uint64, C.c_void_p, C.c_void_p]
+    lib.cellm_probe_stream_read.restype = C.c_int32
+    sptr = C.c_void_p(stream.cuda_stream)
+    res = {}
+
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    blocks, iters = 4 * cus, 2000
+    sink = torch.empty((blocks,), dtype=torch.float32, device="cuda")
+
+    def mfma(i):
+        assert lib.cellm_probe_mfma_f16(blocks, iters, C.c_void_p(sink.data_ptr()), sptr) == 0
+
+    best = min(time_calls(torch, mfma, 5, stream) for _ in range(3))
+    tflops = lib.cellm_probe_mfma_f16_flops(blocks, iters) / (best * 1e-3) / 1e12
+    res["mfma_f16_measured"] = {"TFLOP/s": round(tflops, 1), "frac_published": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+                                "probe": f"{blocks} blocks x 4 waves, {iters} rounds of 8 independent "
+                                         "v_mfma_f32_32x32x16_f16 chains per wave"}
+
+    nbytes = q4_bytes(1, 151936, 896)
+    nbytes -= nbytes % 16
+    copies = 8
+    bufs = [torch.empty((nbytes // 4,), dtype=torch.int32, device="cuda").fill_(i) for i in range(copies)]
+    isink = torch.empty((1,), dtype=torch.int32, device="cuda")
+
+    def rd(i):
+        assert lib.cellm_probe_stream_read(C.c_void_p(bufs[i % copies].data_ptr()), nbytes,
+                                           C.c_void_p(isink.data_ptr()), sptr) == 0
+
+    for i in range(20):
+        rd(i)
+    ms = sorted(time_calls(torch, rd, 100, stream) for _ in range(3))[1]
+    res["hbm_stream_read_77MB"] = {"us": round(ms * 1e3, 2), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                                   "frac_published": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                   "probe": "non-temporal 16-byte loads, 4 in flight per lane, grid-stride over "
+                                            "one 512-thread block per CU, 8 rotating copies"}
+    del bufs
     return res
 
 

@@ -21,6 +21,7 @@ CSRC = PKG_DIR / "csrc"
 BUILD_DIR = PKG_DIR / "_build"
 LIB_PATH = PKG_DIR / "libcellm_hip.so"
 STEP_LIB_PATH = PKG_DIR / "libcellm_llama_step.so"
+PROBES_LIB_PATH = PKG_DIR / "libcellm_probes.so"
 REPO_ROOT = PKG_DIR.parent
 
 SOURCES = ["qgemv.hip", "qgemv_mfma.hip", "qgemm.hip", "dequant.hip", "decode.hip", "lowbit.hip", "capi.cpp", "cellm_file.cpp"]
@@ -80,7 +81,23 @@ def build_library(verbose: bool = False, jobs: int = 4) -> Path:
         raise RuntimeError("link failed:\n" + res.stderr)
     os.replace(tmp, LIB_PATH)
     build_step_library(verbose)
+    build_probes_library(verbose)
     return LIB_PATH
+
+
+def build_probes_library(verbose: bool = False) -> Path:
+    """bench.py's measurement probes (measured MFMA and streaming-read ceilings): a
+    separate library the hot path never loads."""
+    tmp = PROBES_LIB_PATH.with_suffix(".so.tmp")
+    cmd = [_hipcc(), *_flags(), "-shared", "-x", "hip", str(CSRC / "probes.hip"), "-o", str(tmp)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        noise = [ln for ln in res.stderr.splitlines() if "packed-fp32-ops" not in ln and ln.strip()]
+        raise RuntimeError("probe library build failed:\n" + "\n".join(noise))
+    os.replace(tmp, PROBES_LIB_PATH)
+    return PROBES_LIB_PATH
 
 
 def build_step_library(verbose: bool = False) -> Path:

@@ -231,6 +231,20 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ part, float* __re
                                      int splits, int M, int N)
 {
     const size_t total = (size_t)M * N;
+    if ((N & 3) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0) {
+        // four columns of one row per thread: 16-byte loads of every split's partials
+        const size_t n4 = total >> 2;
+        for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (size_t)gridDim.x * blockDim.x) {
+            f4_t v = reinterpret_cast<const f4_t*>(part)[i];
+            for (int s = 1; s < splits; ++s) v += reinterpret_cast<const f4_t*>(part + (size_t)s * total)[i];
+            if (bias) {
+                const size_t n = (4 * i) % (size_t)N;
+                v += f4_t{bias[n], bias[n + 1], bias[n + 2], bias[n + 3]};
+            }
+            reinterpret_cast<f4_t*>(y)[i] = v;
+        }
+        return;
+    }
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
         float v = part[i];
         for (int s = 1; s < splits; ++s) v += part[(size_t)s * total + i];

@@ -29,6 +29,8 @@
 // difference from the reference is summation order (checked to 1e-3 relative
 // against the reference CPU order in tests/).
 #include <algorithm>
+#include <mutex>
+#include <vector>
 
 #include "common.hpp"
 #include "kernels.hpp"
@@ -1613,10 +1615,21 @@ int qgemv_q4_lds_bytes(int M, int K)
 
 static int persist_grid();
 
+// Blocks for the 16-row-batch lm_head kernels: as many batches per wave as one block per CU needs,
+// and only the waves that takes, so every wave gets the same count (the last round is not a
+// partial one).  At 896->151936: 5 batches for 1900 waves, 238 blocks, measured 2 % faster than 256
+// blocks with 4.6 batches per wave; more waves (2374 of 4 batches, 4748 of 2) were 6-10 % slower.
+static int batch_grid(int NB, int waves_per_block)
+{
+    const int blocks = std::max(1, persist_grid() / 4), per = blocks * waves_per_block;
+    const int bpw = (NB + per - 1) / per, waves = (NB + bpw - 1) / bpw;
+    return std::max(1, (waves + waves_per_block - 1) / waves_per_block);
+}
+
 // The flat-batch kernel parks every row sum of a wave in LDS (64 bytes per batch).
 static bool flat_lds_fits(int N, int K)
 {
-    const int GW = std::max(1, persist_grid() / 4) * (kFlatThreads / 64), nbmax = ((N >> 4) + GW - 1) / GW;
+    const int GW = batch_grid(N >> 4, kFlatThreads / 64) * (kFlatThreads / 64), nbmax = ((N >> 4) + GW - 1) / GW;
     return (size_t)(((K >> 5) * 72 + 15) & ~15) + (size_t)(kFlatThreads / 64) * flat_wave_bytes(K >> 7, nbmax) <=
            64 * 1024;
 }
@@ -1624,23 +1637,25 @@ static bool flat_lds_fits(int N, int K)
 // The ring kernel parks every row sum of a wave in LDS too.
 static bool ring_lds_fits(int N, int K)
 {
-    const int GW = std::max(1, persist_grid() / 4) * (kRingThreads / 64), nbmax = ((N >> 4) + GW - 1) / GW;
+    const int GW = batch_grid(N >> 4, kRingThreads / 64) * (kRingThreads / 64), nbmax = ((N >> 4) + GW - 1) / GW;
     return (size_t)(((K >> 5) * 72 + 15) & ~15) + (size_t)(kRingThreads / 64) * (2048 + 64 * nbmax) <= 64 * 1024;
 }
 
 // Persistent grid: 4 blocks per CU (measured best for the lm_head shape).
 static int persist_grid()
 {
-    static int cached[64] = {0};
+    // keyed by device, under a mutex: contexts on several threads and devices may launch at once
+    static std::mutex mu;
+    static std::vector<std::pair<int, int>> cached;  // (device, 4 * CUs)
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) dev = 0;
-    int& c = cached[dev & 63];
-    if (c == 0) {
-        int cus = 0;
-        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 256;
-        c = 4 * cus;
-    }
-    return c;
+    const std::lock_guard<std::mutex> lk(mu);
+    for (const auto& e : cached)
+        if (e.first == dev) return e.second;
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 256;
+    cached.emplace_back(dev, 4 * cus);
+    return 4 * cus;
 }
 
 hipError_t launch_qgemv_q4_affine(const uint32_t* wq, const void* S, const void* B, int sbt, int group_size,
@@ -1654,7 +1669,7 @@ hipError_t launch_qgemv_q4_affine(const uint32_t* wq, const void* S, const void*
     if (fast && M == 1 && N >= 32768 && (N % 16) == 0 && (K % 128) == 0 && K >= 512 && K <= 1024 &&
         sbrow <= 32 && aligned16(S) && aligned16(B) && flat_lds_fits(N, K)) {
         // long single-row outputs, rows of 16..32 chunks in groups of 4: flat-batch kernel, one block per CU
-        const int grid = std::max(1, persist_grid() / 4);
+        const int grid = batch_grid(N >> 4, kFlatThreads / 64);
         const int J = K >> 7;
         const int GW = grid * (kFlatThreads / 64), nbmax = ((N >> 4) + GW - 1) / GW;
         const size_t lds =
@@ -1686,7 +1701,7 @@ hipError_t launch_qgemv_q4_affine(const uint32_t* wq, const void* S, const void*
     if (fast && M == 1 && N >= 32768 && (N % 16) == 0 && (K >> 5) <= 32 && sbrow <= 32 && aligned16(S) &&
         aligned16(B) && ring_lds_fits(N, K)) {
         // long single-row outputs, whole 16-row batches: batched-row ring kernel, one block per CU
-        const int grid = std::max(1, persist_grid() / 4);
+        const int grid = batch_grid(N >> 4, kRingThreads / 64);
         const int GW = grid * (kRingThreads / 64), nbmax = ((N >> 4) + GW - 1) / GW;
         const size_t lds = (size_t)(((K >> 5) * 72 + 15) & ~15) + (size_t)(kRingThreads / 64) * (2048 + 64 * nbmax);
         const u4_t* w4 = reinterpret_cast<const u4_t*>(wq);

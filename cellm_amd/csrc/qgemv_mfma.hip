@@ -366,7 +366,7 @@ __global__ __launch_bounds__(256) void mfma_splitk_reduce_kernel(const float* __
                                                                  float* __restrict__ Y, int M, int N)
 {
     const size_t total = (size_t)M * N, plane = total;
-    if ((N & 3) == 0) {
+    if ((N & 3) == 0 && (reinterpret_cast<uintptr_t>(Y) & 15) == 0) {
         const size_t n4 = total >> 2;
         for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (size_t)gridDim.x * blockDim.x) {
             f4_t a = reinterpret_cast<const f4_t*>(part)[i];
@@ -493,7 +493,7 @@ hipError_t launch_mfma_nt(const void* W, const void* S, const void* B, int per_c
                            KC, ntiles, sp.pps, sp.nsplit, part);
     }
     if (hipError_t e = hipGetLastError(); e != hipSuccess || sp.nsplit == 1) return e;
-    const size_t work = (N & 3) == 0 ? (size_t)M * N / 4 : (size_t)M * N;
+    const size_t work = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(Y) & 15) == 0 ? (size_t)M * N / 4 : (size_t)M * N;
     const unsigned blocks = (unsigned)std::min<size_t>((work + 255) / 256, 2048);
     hipLaunchKernelGGL((mfma_splitk_reduce_kernel<WT, SBT>), dim3(blocks), dim3(256), 0, st, ws, sp.nsplit, S,
                        per_channel, bias, Y, M, N);
