@@ -113,7 +113,10 @@ int32_t cellm_hip_weight_cache_stats(cellm_hip_ctx_t* ctx, size_t* out_entries, 
  * one per-tensor scale when n_scales == 1; other counts are refused
  * (CELLM_HIP_ERR_INVALID_ARG), where the reference would use scale[0].
  * scale_dtype: F32/F16/BF16; x_dtype: F32/F16/BF16.  m <= 4 runs the decode
- * GEMV; larger m with f16 x and k % 64 == 0 runs the MFMA GEMM. */
+ * GEMV; larger m with f16 x and k % 64 == 0 runs the MFMA GEMM.  With few
+ * output rows over a long k, 2..64 rows split k over work items whose partial
+ * sums go to the context's per-stream workspace (grown on demand, as for the
+ * split-K qGEMM) and a second kernel adds them in a fixed order. */
 int32_t cellm_hip_qgemv_i8(cellm_hip_ctx_t* ctx, const int8_t* w, const void* scales, int32_t scale_dtype,
                            int64_t n_scales, const void* x, int32_t x_dtype, const float* bias, float* y, int64_t m,
                            int64_t n, int64_t k, void* stream);
@@ -122,7 +125,9 @@ int32_t cellm_hip_qgemv_i8(cellm_hip_ctx_t* ctx, const int8_t* w, const void* sc
  *   y[i, r] = sum_j (q[r, j] * S[r, j/group] + B[r, j/group]) * x[i, j]
  * Replaces LfmRunner::linear_i4_out_in (crates/cellm-model/src/lfm.rs:985-1066)
  * and its dequant -> MetalOps::logits_f32 route (lfm.rs:1049-1054).
- * k % 8 == 0; group a power of two >= 8 (MLX uses 64). */
+ * k % 8 == 0; group a power of two >= 8 (MLX uses 64).  2..64 rows with f16 x
+ * run the batched MFMA path, split over k through the per-stream workspace
+ * for few output rows over a long k, as cellm_hip_qgemv_i8. */
 int32_t cellm_hip_qgemv_q4_affine(cellm_hip_ctx_t* ctx, const uint32_t* wq, const void* scales, const void* biases,
                                   int32_t sb_dtype, int64_t group, const void* x, int32_t x_dtype, float* y,
                                   int64_t m, int64_t n, int64_t k, void* stream);
