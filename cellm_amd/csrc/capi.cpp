@@ -179,19 +179,24 @@ int32_t check_n_scales(int64_t n_scales, int64_t n, const char* what)
 // every kernel that uses the buffer is enqueued: calls on one stream then
 // queue their scratch users back to back, and a grow (which waits for the
 // stream, then frees) cannot happen between a get and its launches.
+// zero_prefix: bytes at the start of a freshly allocated buffer that are cleared
+// on this stream before first use (the attention's group counters, which its
+// kernels then return to zero themselves).
 int32_t get_stream_buffer(cellm_hip_ctx* ctx, std::unordered_map<hipStream_t, DeviceBuffer>& map, hipStream_t st,
-                          size_t need, float** out)
+                          size_t need, float** out, size_t zero_prefix = 0)
 {
     *out = nullptr;
     if (need == 0) return CELLM_HIP_OK;
     std::lock_guard<std::recursive_mutex> lk(ctx->mu);
     DeviceBuffer& b = map[st];
-    if (b.bytes < need) {
+    const bool grow = b.bytes < need;
+    if (grow) {
         // The old buffer may still be read by queued work on this stream.
         HIP_TRY(hipStreamSynchronize(st), "hipStreamSynchronize(workspace grow)");
     }
     int32_t rc = ensure_buffer(b, need);
     if (rc) return rc;
+    if (grow && zero_prefix) HIP_TRY(hipMemsetAsync(b.ptr, 0, std::min(zero_prefix, need), st), "hipMemsetAsync(counters)");
     *out = reinterpret_cast<float*>(b.ptr);
     return CELLM_HIP_OK;
 }
@@ -952,7 +957,7 @@ int32_t attention_impl(cellm_hip_ctx* ctx, const float* q, const uint16_t* kcach
     if (static_scratch) {
         ws = ctx->attn_static;
         if (!ws) return set_error(CELLM_HIP_ERR_DEVICE, "static attention scratch has no device address");
-    } else if (int32_t rc = get_stream_buffer(ctx, ctx->attn, st, need, &ws)) {
+    } else if (int32_t rc = get_stream_buffer(ctx, ctx->attn, st, need, &ws, attention_counter_bytes())) {
         return rc;
     }
     HIP_TRY(launch_attention_gqa_f16kv(q, kcache, vcache, block_tables, (int)max_blocks, (int)total_blocks, positions,

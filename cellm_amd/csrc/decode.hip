@@ -44,6 +44,31 @@ constexpr int kAttnChunk = 64;        // positions per partial-attention block
 constexpr int kAttnThreads = 256;
 constexpr int kAttnGMax = 8;          // query heads per kv head
 constexpr int kAttnMaxChunks = 512;   // positions per sequence <= 32768
+// One-launch attention: a counter per (row, kv head) group at the start of the
+// workspace, zero between calls (the group's last block resets it).
+constexpr int kAttnCounters = 16384;
+constexpr size_t kAttnCounterBytes = (size_t)kAttnCounters * sizeof(uint32_t);
+
+// Agent-coherent (sc1) store and load: the one-launch attention hands a group's
+// partials to its last block through these, with a wait for the stores before
+// the arrival count, instead of an agent-scope fence (an L2 write-back per
+// block on this part).
+template <bool COH>
+__device__ __forceinline__ void st_part(float* p, float v)
+{
+    if constexpr (COH)
+        __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+        *p = v;
+}
+template <bool COH>
+__device__ __forceinline__ float ld_part(const float* p)
+{
+    if constexpr (COH)
+        return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else
+        return *p;
+}
 
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 
@@ -231,6 +256,65 @@ __global__ void rope_kv_write_kernel(float* __restrict__ q, float* __restrict__ 
     }
 }
 
+// Combine of one (row, kv head) group's nch chunk partials p (layout of
+// attn_partial_kernel) into its G heads' outputs o[g][HD]:
+//   o[g][i] = (sum_c acc_c[i] e^(m_c - M)) / (sum_c l_c e^(m_c - M)),  M = max_c m_c
+// The chunk maxima and sums go to LDS, together with each thread's first
+// kCombinePre partials of its first output (one memory latency for up to
+// kCombinePre chunks); wave w then weighs the chunks of heads w and w + 4.
+// Chunks are added in chunk order whichever block runs it.
+template <int HD, int G, bool COH>
+__device__ __forceinline__ void attn_combine_group(const float* __restrict__ p, int nch, float* __restrict__ o,
+                                                   float (&cm)[G][kAttnMaxChunks], float (&cl)[G][kAttnMaxChunks],
+                                                   float (&invl)[G])
+{
+    constexpr int kCombinePre = 16;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const size_t cstride = (size_t)G * (HD + 2);
+    // this thread's first output and its first partials
+    const int i0 = min(t, G * HD - 1);
+    const float* pc0 = p + (size_t)(i0 / HD) * (HD + 2) + i0 % HD;
+    float pre[kCombinePre];
+#pragma unroll
+    for (int c = 0; c < kCombinePre; ++c) pre[c] = ld_part<COH>(pc0 + (size_t)min(c, nch - 1) * cstride);
+    for (int j = t; j < G * nch; j += kAttnThreads) {
+        const int g = j % G, c = j / G;
+        cm[g][c] = ld_part<COH>(p + c * cstride + (size_t)g * (HD + 2) + HD);
+        cl[g][c] = ld_part<COH>(p + c * cstride + (size_t)g * (HD + 2) + HD + 1);
+    }
+    __syncthreads();
+    for (int g = wave; g < G; g += 4) {
+        float m = -INFINITY;
+        for (int c = lane; c < nch; c += 64) m = fmaxf(m, cm[g][c]);
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+        float l = 0.0f;
+        for (int c = lane; c < nch; c += 64) {
+            const float w = expf(cm[g][c] - m);
+            cm[g][c] = w;
+            l = l + cl[g][c] * w;
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) l = l + __shfl_xor(l, off);
+        if (lane == 0) invl[g] = l > 0.0f ? 1.0f / l : 0.0f;
+    }
+    __syncthreads();
+    for (int i = t; i < G * HD; i += kAttnThreads) {
+        const int g = i / HD, d = i % HD;
+        const float* pc = p + (size_t)g * (HD + 2) + d;
+        float acc = 0.0f;
+        int c = 0;
+        if (i == t) {
+#pragma unroll
+            for (; c < kCombinePre; ++c)
+                if (c < nch) acc = acc + pre[c] * cm[g][c];
+        }
+#pragma unroll 8
+        for (; c < nch; ++c) acc = acc + ld_part<COH>(pc + c * cstride) * cm[g][c];
+        o[(size_t)g * HD + d] = acc * invl[g];
+    }
+}
+
 // Partial attention over positions [64c, 64c+64) for one (row, kv head) and
 // its G query heads; part layout [row][kvh][chunk][G][HD + 2]: HD weighted-V
 // sums, the chunk max and the chunk sum of exp(score - max).  Every K and V
@@ -238,11 +322,16 @@ __global__ void rope_kv_write_kernel(float* __restrict__ q, float* __restrict__ 
 //   Q.K: thread t -> position t / 4, dims (t % 4) * HD/4 .. + HD/4 (16-B loads)
 //   P.V: thread t -> dims (t % 64) * HD/64 .. + HD/64, positions 16 (t / 64) .. + 16
 // so wave w owns positions 16w .. 16w + 15 in both phases.
-template <int HD, int G>
+//
+// FUSED: one launch.  The partials go out with agent-coherent stores; after
+// waiting for them the block counts its arrival in its group's counter, and the
+// group's last block to arrive (whichever chunk) combines the group with
+// agent-coherent loads into `out` and resets the counter to zero.
+template <int HD, int G, bool FUSED = false>
 __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
     const float* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
     const int32_t* __restrict__ pos, PagedKv kv, int layer, int n_kv_heads, float scale, float soft_cap,
-    float* __restrict__ part, int nch_max)
+    float* __restrict__ part, int nch_max, uint32_t* __restrict__ counters = nullptr, float* __restrict__ out = nullptr)
 {
     constexpr int KD = HD / 4;                             // Q.K dims per thread
     constexpr int KL = KD / 8;                             // 16-byte K loads per thread
@@ -377,80 +466,52 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
         for (int d = 0; d < VD; ++d) accs[wave][g * HD + lane * VD + d] = acc[g][d];
     }
     __syncthreads();
-    float* out = part + ((((size_t)r * n_kv_heads + kvh) * nch_max + ch) * G) * (HD + 2);
+    float* const grp = part + (((size_t)r * n_kv_heads + kvh) * nch_max) * G * (HD + 2);
+    float* const pout = grp + (size_t)ch * G * (HD + 2);
     for (int i = t; i < G * HD; i += kAttnThreads)
-        out[(size_t)(i / HD) * (HD + 2) + i % HD] = (accs[0][i] + accs[1][i]) + (accs[2][i] + accs[3][i]);
+        st_part<FUSED>(pout + (size_t)(i / HD) * (HD + 2) + i % HD,
+                       (accs[0][i] + accs[1][i]) + (accs[2][i] + accs[3][i]));
     if (t < G) {
-        out[(size_t)t * (HD + 2) + HD] = fmaxf(fmaxf(wmax[0][t], wmax[1][t]), fmaxf(wmax[2][t], wmax[3][t]));
-        out[(size_t)t * (HD + 2) + HD + 1] = (wsum[0][t] + wsum[1][t]) + (wsum[2][t] + wsum[3][t]);
+        st_part<FUSED>(pout + (size_t)t * (HD + 2) + HD,
+                       fmaxf(fmaxf(wmax[0][t], wmax[1][t]), fmaxf(wmax[2][t], wmax[3][t])));
+        st_part<FUSED>(pout + (size_t)t * (HD + 2) + HD + 1, (wsum[0][t] + wsum[1][t]) + (wsum[2][t] + wsum[3][t]));
+    }
+    if constexpr (FUSED) {
+        __shared__ float cm[G][kAttnMaxChunks];
+        __shared__ float cl[G][kAttnMaxChunks];
+        __shared__ float invl[G];
+        __shared__ int last;
+        // this block's partials are performed at the coherence point before it counts itself
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        const int nch = (seq + kAttnChunk - 1) / kAttnChunk;  // blocks of the group that reach here
+        if (t == 0)
+            last = __hip_atomic_fetch_add(counters + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                   (uint32_t)(nch - 1);
+        __syncthreads();
+        if (!last) return;
+        attn_combine_group<HD, G, true>(grp, nch, out + ((size_t)r * n_heads + (size_t)kvh * G) * HD, cm, cl, invl);
+        if (t == 0) __hip_atomic_store(counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
-// One block per (row, kv head): its G query heads.
-//   out[h][i] = (sum_c acc_c[i] e^(m_c - M)) / (sum_c l_c e^(m_c - M)),  M = max_c m_c
-// The chunk maxima and sums go to LDS, together with each thread's first
-// kCombinePre partials of its first output (one memory latency for up to
-// kCombinePre chunks); wave w then weighs the chunks of heads w and w + 4.
+// One block per (row, kv head): its G query heads (the two-launch form).
 template <int HD, int G>
 __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(const float* __restrict__ part,
                                                                    const int32_t* __restrict__ pos, PagedKv kv,
                                                                    int n_kv_heads, int nch_max,
                                                                    float* __restrict__ out)
 {
-    constexpr int kCombinePre = 16;
-    const int n_heads = G * n_kv_heads;
     __shared__ float cm[G][kAttnMaxChunks];  // chunk maxima, then the weights e^(m_c - M)
     __shared__ float cl[G][kAttnMaxChunks];  // chunk exp-sums
     __shared__ float invl[G];
+    const int n_heads = G * n_kv_heads;
     const int r = blockIdx.x / n_kv_heads, kvh = blockIdx.x % n_kv_heads;
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int seq = min(pos[r] + 1, kv.max_blocks * kv.tpb);
     const int nch = seq > 0 ? (seq + kAttnChunk - 1) / kAttnChunk : 0;
     if (nch == 0) return;
-    const size_t cstride = (size_t)G * (HD + 2);
-    const float* p = part + ((size_t)r * n_kv_heads + kvh) * nch_max * cstride;
-    // this thread's first output and its first partials
-    const int i0 = min(t, G * HD - 1);
-    const float* pc0 = p + (size_t)(i0 / HD) * (HD + 2) + i0 % HD;
-    float pre[kCombinePre];
-#pragma unroll
-    for (int c = 0; c < kCombinePre; ++c) pre[c] = pc0[(size_t)min(c, nch - 1) * cstride];
-    for (int j = t; j < G * nch; j += kAttnThreads) {
-        const int g = j % G, c = j / G;
-        cm[g][c] = p[c * cstride + (size_t)g * (HD + 2) + HD];
-        cl[g][c] = p[c * cstride + (size_t)g * (HD + 2) + HD + 1];
-    }
-    __syncthreads();
-    for (int g = wave; g < G; g += 4) {
-        float m = -INFINITY;
-        for (int c = lane; c < nch; c += 64) m = fmaxf(m, cm[g][c]);
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-        float l = 0.0f;
-        for (int c = lane; c < nch; c += 64) {
-            const float w = expf(cm[g][c] - m);
-            cm[g][c] = w;
-            l = l + cl[g][c] * w;
-        }
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) l = l + __shfl_xor(l, off);
-        if (lane == 0) invl[g] = l > 0.0f ? 1.0f / l : 0.0f;
-    }
-    __syncthreads();
-    for (int i = t; i < G * HD; i += kAttnThreads) {
-        const int g = i / HD, d = i % HD;
-        const float* pc = p + (size_t)g * (HD + 2) + d;
-        float acc = 0.0f;
-        int c = 0;
-        if (i == t) {
-#pragma unroll
-            for (; c < kCombinePre; ++c)
-                if (c < nch) acc = acc + pre[c] * cm[g][c];
-        }
-#pragma unroll 8
-        for (; c < nch; ++c) acc = acc + pc[c * cstride] * cm[g][c];
-        out[((size_t)r * n_heads + (size_t)kvh * G + g) * HD + d] = acc * invl[g];
-    }
+    const float* p = part + ((size_t)r * n_kv_heads + kvh) * nch_max * (size_t)G * (HD + 2);
+    attn_combine_group<HD, G, false>(p, nch, out + ((size_t)r * n_heads + (size_t)kvh * G) * HD, cm, cl, invl);
 }
 
 // ---- fused decode-step GEMVs ------------------------------------------------
@@ -864,8 +925,10 @@ bool attention_supported(int n_heads, int n_kv_heads, int head_dim, int max_seq)
 size_t attention_workspace_bytes(int rows, int n_heads, int n_kv_heads, int head_dim, int max_seq)
 {
     const int nch = (max_seq + kAttnChunk - 1) / kAttnChunk;
-    return (size_t)rows * n_heads * nch * (head_dim + 2) * sizeof(float);
+    return kAttnCounterBytes + (size_t)rows * n_heads * nch * (head_dim + 2) * sizeof(float);
 }
+
+size_t attention_counter_bytes() { return kAttnCounterBytes; }
 
 hipError_t launch_attention_gqa_f16kv(const float* q, const uint16_t* kcache, const uint16_t* vcache,
                                       const uint32_t* block_tables, int max_blocks, int total_blocks,
@@ -881,11 +944,20 @@ hipError_t launch_attention_gqa_f16kv(const float* q, const uint16_t* kcache, co
     const dim3 pgrid((unsigned)(rows * n_kv_heads), (unsigned)nch);
     const dim3 cgrid((unsigned)(rows * n_kv_heads));
     const int G = n_heads / n_kv_heads;
+    // workspace: the group counters (zero between calls), then the partials
+    uint32_t* counters = reinterpret_cast<uint32_t*>(workspace);
+    float* part = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + kAttnCounterBytes);
+    const bool one_launch = rows * n_kv_heads <= kAttnCounters;
     auto go = [&](auto hd, auto g) {
         constexpr int HD = decltype(hd)::value, GG = decltype(g)::value;
+        if (one_launch) {
+            hipLaunchKernelGGL((attn_partial_kernel<HD, GG, true>), pgrid, dim3(kAttnThreads), 0, st, q, kcache,
+                               vcache, pos, kv, layer, n_kv_heads, scale, soft_cap, part, nch, counters, out);
+            return;
+        }
         hipLaunchKernelGGL((attn_partial_kernel<HD, GG>), pgrid, dim3(kAttnThreads), 0, st, q, kcache, vcache, pos, kv,
-                           layer, n_kv_heads, scale, soft_cap, workspace, nch);
-        hipLaunchKernelGGL((attn_combine_kernel<HD, GG>), cgrid, dim3(kAttnThreads), 0, st, workspace, pos, kv,
+                           layer, n_kv_heads, scale, soft_cap, part, nch, nullptr, nullptr);
+        hipLaunchKernelGGL((attn_combine_kernel<HD, GG>), cgrid, dim3(kAttnThreads), 0, st, part, pos, kv,
                            n_kv_heads, nch, out);
     };
     auto by_g = [&](auto hd) {
@@ -931,6 +1003,8 @@ hipError_t attention_static_scratch(float** out)
     void* p = nullptr;
     if (hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)); e != hipSuccess) return e;
     if (!p) return hipErrorInvalidSymbol;
+    // the group counters at its start must read zero before the first call (the calls keep them so)
+    if (hipError_t e = hipMemset(p, 0, kAttnCounterBytes); e != hipSuccess) return e;
     per_device.emplace_back(dev, static_cast<float*>(p));
     *out = static_cast<float*>(p);
     return hipSuccess;

@@ -100,6 +100,9 @@ hipError_t launch_kv_write_f16(const float* k, const float* v, int rows, int kv_
                                int total_blocks, int n_layers, int tokens_per_block, int layer, hipStream_t st);
 bool attention_supported(int n_heads, int n_kv_heads, int head_dim, int max_seq);
 size_t attention_workspace_bytes(int rows, int n_heads, int n_kv_heads, int head_dim, int max_seq);
+// Bytes at the start of an attention workspace that hold its group counters:
+// zero when the workspace is first used, and zero again after every call.
+size_t attention_counter_bytes();
 hipError_t launch_attention_gqa_f16kv(const float* q, const uint16_t* kcache, const uint16_t* vcache,
                                       const uint32_t* block_tables, int max_blocks, int total_blocks,
                                       const int32_t* pos, int rows, int n_heads, int n_kv_heads, int head_dim,
