@@ -360,7 +360,7 @@ constexpr size_t kWholeXLds = 152 * 1024;  // the BT = 1024 form holds X up to t
 // Split-K reduction: y[m,n] = (sum over splits, in split order, of part[s][m][n]) * scale + bias
 // (int8; the scale after the sum, as cpu_kernels.rs:130 applies it), or the plain sum (q4).
 template <int WT, int SBT>
-__global__ __launch_bounds__(256) void mfma_splitk_reduce_kernel(const float* __restrict__ part, int nsplit,
+__global__ __launch_bounds__(64) void mfma_splitk_reduce_kernel(const float* __restrict__ part, int nsplit,
                                                                  const void* __restrict__ S, int per_channel,
                                                                  const float* __restrict__ bias,
                                                                  float* __restrict__ Y, int M, int N)
@@ -369,8 +369,19 @@ __global__ __launch_bounds__(256) void mfma_splitk_reduce_kernel(const float* __
     if ((N & 3) == 0 && (reinterpret_cast<uintptr_t>(Y) & 15) == 0) {
         const size_t n4 = total >> 2;
         for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (size_t)gridDim.x * blockDim.x) {
-            f4_t a = reinterpret_cast<const f4_t*>(part)[i];
-            for (int sp = 1; sp < nsplit; ++sp) a += reinterpret_cast<const f4_t*>(part + sp * plane)[i];
+            const f4_t* p4 = reinterpret_cast<const f4_t*>(part) + i;
+            f4_t a = p4[0];
+            int sp = 1;
+            // four splits' loads in flight at a time, added in split order
+            for (; sp + 3 < nsplit; sp += 4) {
+                const f4_t b0 = p4[(size_t)sp * (plane >> 2)], b1 = p4[(size_t)(sp + 1) * (plane >> 2)];
+                const f4_t b2 = p4[(size_t)(sp + 2) * (plane >> 2)], b3 = p4[(size_t)(sp + 3) * (plane >> 2)];
+                a += b0;
+                a += b1;
+                a += b2;
+                a += b3;
+            }
+            for (; sp < nsplit; ++sp) a += p4[(size_t)sp * (plane >> 2)];
             if constexpr (WT == 1) {
                 const int n = (int)((4 * i) % (size_t)N);
 #pragma unroll
@@ -493,9 +504,10 @@ hipError_t launch_mfma_nt(const void* W, const void* S, const void* B, int per_c
                            KC, ntiles, sp.pps, sp.nsplit, part);
     }
     if (hipError_t e = hipGetLastError(); e != hipSuccess || sp.nsplit == 1) return e;
+    // one-wave blocks: a few thousand threads at most, spread over as many CUs as there are waves
     const size_t work = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(Y) & 15) == 0 ? (size_t)M * N / 4 : (size_t)M * N;
-    const unsigned blocks = (unsigned)std::min<size_t>((work + 255) / 256, 2048);
-    hipLaunchKernelGGL((mfma_splitk_reduce_kernel<WT, SBT>), dim3(blocks), dim3(256), 0, st, ws, sp.nsplit, S,
+    const unsigned blocks = (unsigned)std::min<size_t>((work + 63) / 64, 8192);
+    hipLaunchKernelGGL((mfma_splitk_reduce_kernel<WT, SBT>), dim3(blocks), dim3(64), 0, st, ws, sp.nsplit, S,
                        per_channel, bias, Y, M, N);
     return hipGetLastError();
 }
