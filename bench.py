@@ -204,6 +204,22 @@ def time_batch(torch, ops, arr, stream, reps: int = 5, warm_s: float = 0.02, tri
     return sorted(out)[len(out) // 2]
 
 
+def isolated_launch_us(torch, ops, arr, stream, reps: int = 20) -> float:
+    """Median of `reps` single launches, each alone on an idle GPU: HIP events
+    around one op of `arr` (its own weight copy), with a synchronisation before
+    and after (the latency one projection adds when nothing is queued)."""
+    out = []
+    for i in range(reps):
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        ops.encode_qgemv_batch(op_array([arr[i % len(arr)]]), stream=stream.cuda_stream)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        out.append(e0.elapsed_time(e1) * 1e3)
+    return round(sorted(out)[len(out) // 2], 2)
+
+
 def time_calls(torch, fn, reps: int, stream):
     """Mean ms per call of fn(i) over `reps` back-to-back calls (used for the
     qGEMM, whose kernels far outlast the host launch cost)."""
@@ -284,7 +300,8 @@ def main():
         ms = time_batch(torch, ops, arr, stream)
         gbs = q4_bytes(1, n, k) / (ms * 1e-3) / 1e9
         per_shape[f"{name}_{k}x{n}"] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
-                                        "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+                                        "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                                        "isolated_us": isolated_launch_us(torch, ops, arr, stream)}
     dom = per_shape["lm_head_896x151936"]
     traffic = None
     tfile = ROOT / "profiles" / "traffic_q4_gemv_lm_head.json"
