@@ -163,6 +163,42 @@ def test_attention_gqa_f16kv(ops, nh, nkv, hd, blocks, pos):
         assert rel_err(got[r], ref) <= 1e-5, (r, rel_err(got[r], ref))
 
 
+def test_attention_one_launch_and_two_launch_forms(ops):
+    """Up to 16384 (row, kv head) groups run in one launch (the group's last
+    chunk block combines through coherent stores/loads and a self-resetting
+    counter); more groups take the two-launch form.  257 rows x 64 kv heads
+    (16448 groups) run the two-launch form, then the first 256 rows (16384
+    groups) the one-launch form, twice.  Every row has 65..80 positions (two
+    chunks).  Sampled rows match the oracle; the rows both forms share are equal
+    bit for bit, as are the two one-launch calls."""
+    nh, nkv, hd, L, tpb, layer, bpr = 64, 64, 64, 1, 16, 0, 5
+    kvd = nkv * hd
+    rows = 257
+    total = rows * bpr + 3
+    rng = np.random.default_rng(0xD0000500)
+    k = rng.standard_normal(total * L * tpb * kvd, dtype=np.float32).astype(np.float16).view(np.uint16)
+    v = rng.standard_normal(total * L * tpb * kvd, dtype=np.float32).astype(np.float16).view(np.uint16)
+    bt = np.array([[b * rows + r + 3 for b in range(bpr)] for r in range(rows)], np.uint32)
+    pos = (64 + (np.arange(rows) * 7) % 16).astype(np.int32)
+    q = rng.standard_normal((rows, nh * hd), dtype=np.float32)
+    kd, vd, qd = dev(k), dev(v), dev(q)
+    outs = []
+    for r_used in (rows, rows - 1, rows - 1):
+        out = torch.empty((r_used, nh * hd), dtype=torch.float32, device="cuda")
+        ops.encode_attention(qd[:r_used].contiguous(), kd, vd, dev(np.ascontiguousarray(bt[:r_used])),
+                             dev(np.ascontiguousarray(pos[:r_used])), out, nh, nkv, hd, total, L, tpb, layer)
+        torch.cuda.synchronize()
+        outs.append(out.cpu().numpy())
+    for r in (0, 1, 100, 200, rows - 2, rows - 1):
+        bases = np.array([base_of(bt[r], t, layer, L, tpb, kvd) for t in range(int(pos[r]) + 1)], np.uint64)
+        ref = oracle.attention_gqa_f16kv(k, v, bases, q[r], nh, nkv, hd)
+        assert rel_err(outs[0][r], ref) <= 1e-5, r
+        if r < rows - 1:
+            assert rel_err(outs[1][r], ref) <= 1e-5, r
+    np.testing.assert_array_equal(outs[1].view(np.uint32), outs[0][:rows - 1].view(np.uint32))
+    np.testing.assert_array_equal(outs[2].view(np.uint32), outs[1].view(np.uint32))
+
+
 @pytest.mark.parametrize("nh,nkv,hd,attn_scale,cap,qmag", [
     (8, 2, 64, 0.0625, None, 1.0),    # explicit attn_scale (kvcache.rs:752)
     (8, 2, 64, None, 50.0, 40.0),     # soft cap 50 on scores it bends (kvcache.rs:768-770)
