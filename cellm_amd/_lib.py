@@ -60,6 +60,8 @@ SIGNATURES = {
     "cellm_hip_logits_i4": (_i32, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _sz, C.c_char_p, _vp]),
     "cellm_hip_logits_q4_affine": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _sz, _sz, C.c_char_p, _vp]),
     "cellm_hip_embed_i8": (_i32, [_vp, _vp, _i64, _vp, _vp, _i64, _i64, _vp, _vp]),
+    "cellm_hip_embed_f16": (_i32, [_vp, _vp, _i64, _vp, _i64, _i64, _vp, _vp]),
+    "cellm_hip_embed_i4": (_i32, [_vp, _vp, _i64, _vp, _vp, _i64, _i64, _vp, _vp]),
     "cellm_hip_rms_norm": (_i32, [_vp, _vp, _vp, _i32, _i64, _i64, C.c_float, _vp, _vp]),
     "cellm_hip_qgemv_f16": (_i32, [_vp, _vp, _vp, _i32, _vp, _i64, _i64, _i64, _vp]),
     "cellm_hip_qgemv_i2": (_i32, [_vp, _vp, _vp, _i32, _vp, _i32, _vp, _i64, _i64, _i64, _vp]),

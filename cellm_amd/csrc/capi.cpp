@@ -988,6 +988,39 @@ int32_t cellm_hip_embed_i8(cellm_hip_ctx_t* ctx, const uint32_t* tokens, int64_t
     CELLM_API_END(report_exception)
 }
 
+int32_t cellm_hip_embed_f16(cellm_hip_ctx_t* ctx, const uint32_t* tokens, int64_t rows, const uint16_t* embed_f16,
+                            int64_t vocab, int64_t hidden, float* out, void* stream)
+{
+    CELLM_API_BEGIN
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    if (int32_t rc = check_dims(rows, vocab, hidden)) return rc;
+    if (rows == 0 || hidden == 0) return CELLM_HIP_OK;
+    if (vocab < 1) return set_error(CELLM_HIP_ERR_INVALID_ARG, "vocab must be >= 1");
+    if (!tokens || !embed_f16 || !out) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null pointer");
+    DeviceGuard g(ctx->device);
+    HIP_TRY(launch_embed_f16(tokens, (int)rows, embed_f16, (int)vocab, (int)hidden, out, pick_stream(ctx, stream)),
+            "embed_f16 launch");
+    return CELLM_HIP_OK;
+    CELLM_API_END(report_exception)
+}
+
+int32_t cellm_hip_embed_i4(cellm_hip_ctx_t* ctx, const uint32_t* tokens, int64_t rows, const uint8_t* embed_i4,
+                           const uint16_t* scales_f16, int64_t vocab, int64_t hidden, float* out, void* stream)
+{
+    CELLM_API_BEGIN
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    if (int32_t rc = check_dims(rows, vocab, hidden)) return rc;
+    if (rows == 0 || hidden == 0) return CELLM_HIP_OK;
+    if (vocab < 1) return set_error(CELLM_HIP_ERR_INVALID_ARG, "vocab must be >= 1");
+    if (!tokens || !embed_i4 || !scales_f16 || !out) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null pointer");
+    DeviceGuard g(ctx->device);
+    HIP_TRY(launch_embed_i4(tokens, (int)rows, embed_i4, scales_f16, (int)vocab, (int)hidden, out,
+                            pick_stream(ctx, stream)),
+            "embed_i4 launch");
+    return CELLM_HIP_OK;
+    CELLM_API_END(report_exception)
+}
+
 int32_t cellm_hip_rms_norm(cellm_hip_ctx_t* ctx, const float* x, const void* weight, int32_t weight_dtype,
                            int64_t rows, int64_t n, float eps, float* out, void* stream)
 {

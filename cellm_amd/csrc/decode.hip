@@ -82,6 +82,31 @@ __global__ void embed_i8_kernel(const uint32_t* __restrict__ tokens, const int8_
         x[(size_t)r * hidden + i] = (float)emb[t * hidden + i] * s;
 }
 
+// embed_token's f16 and i4 branches (llama.rs:687-693, 703-718): one row per token.
+__global__ void embed_f16_kernel(const uint32_t* __restrict__ tokens, const uint16_t* __restrict__ emb, int vocab,
+                                 int hidden, float* __restrict__ x)
+{
+    const int r = blockIdx.y;
+    const size_t t = tokens[r] % (uint32_t)vocab;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < hidden; i += gridDim.x * blockDim.x)
+        x[(size_t)r * hidden + i] = h2f(emb[t * hidden + i]);
+}
+
+// (nibble - 8) * scale, low nibble = even element, ceil(hidden / 2) bytes per row
+__global__ void embed_i4_kernel(const uint32_t* __restrict__ tokens, const uint8_t* __restrict__ emb,
+                                const uint16_t* __restrict__ scale, int vocab, int hidden, float* __restrict__ x)
+{
+    const int r = blockIdx.y;
+    const size_t t = tokens[r] % (uint32_t)vocab;
+    const float s = h2f(scale[t]);
+    const uint8_t* row = emb + t * (size_t)((hidden + 1) / 2);
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < hidden; i += gridDim.x * blockDim.x) {
+        const uint32_t b = row[i >> 1];
+        const int q = (int)((i & 1) ? (b >> 4) : (b & 0xFu)) - 8;
+        x[(size_t)r * hidden + i] = (float)q * s;
+    }
+}
+
 template <int WDT>
 __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(const float* __restrict__ x, const void* __restrict__ w,
                                                                float* __restrict__ out, int n, float eps)
@@ -853,6 +878,22 @@ hipError_t launch_embed_i8(const uint32_t* tokens, int rows, const int8_t* emb, 
 {
     const dim3 grid((unsigned)std::min((hidden + 255) / 256, 64), (unsigned)rows);
     hipLaunchKernelGGL(embed_i8_kernel, grid, dim3(256), 0, st, tokens, emb, scale, vocab, hidden, x);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed_f16(const uint32_t* tokens, int rows, const uint16_t* emb, int vocab, int hidden, float* x,
+                            hipStream_t st)
+{
+    const dim3 grid((unsigned)std::min((hidden + 255) / 256, 64), (unsigned)rows);
+    hipLaunchKernelGGL(embed_f16_kernel, grid, dim3(256), 0, st, tokens, emb, vocab, hidden, x);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed_i4(const uint32_t* tokens, int rows, const uint8_t* emb, const uint16_t* scale, int vocab,
+                           int hidden, float* x, hipStream_t st)
+{
+    const dim3 grid((unsigned)std::min((hidden + 255) / 256, 64), (unsigned)rows);
+    hipLaunchKernelGGL(embed_i4_kernel, grid, dim3(256), 0, st, tokens, emb, scale, vocab, hidden, x);
     return hipGetLastError();
 }
 

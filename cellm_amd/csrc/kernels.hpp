@@ -85,6 +85,10 @@ hipError_t launch_qgemv_mfma_q4(const uint32_t* wq, const void* S, const void* B
 // uint32); K/V caches are f16 pages laid out as KvCacheLayout::token_base_elem.
 hipError_t launch_embed_i8(const uint32_t* tokens, int rows, const int8_t* emb, const uint16_t* scale, int vocab,
                            int hidden, float* x, hipStream_t st);
+hipError_t launch_embed_f16(const uint32_t* tokens, int rows, const uint16_t* emb, int vocab, int hidden, float* x,
+                            hipStream_t st);
+hipError_t launch_embed_i4(const uint32_t* tokens, int rows, const uint8_t* emb, const uint16_t* scale, int vocab,
+                           int hidden, float* x, hipStream_t st);
 hipError_t launch_rms_norm(const float* x, const void* w, int wdt, int rows, int n, float eps, float* out,
                            hipStream_t st);
 hipError_t launch_add_rms_norm(float* x, const float* y, const void* w, int wdt, int rows, int n, float eps,

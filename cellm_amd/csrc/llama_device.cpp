@@ -122,13 +122,16 @@ struct DevBuf {
 //   Q4: "u32" [out, in/8] MLX affine words + f32 "<base>.scales" / "<base>.biases"
 //       [out, ceil(in/64)] (tools/convert_lfm.py:123-136), group 64;
 //   I4: "i4" [out, in], ceil(in/2) bytes per row, low nibble even, + f16
-//       "<w>.qscale" [out]: one scale per row (gs = in, gemma.rs:1466-1471).
-enum ProjKind : int32_t { PK_I8 = 0, PK_Q4 = 1, PK_I4 = 2 };
+//       "<w>.qscale" [out]: one scale per row (gs = in, gemma.rs:1466-1471);
+//   F16: "f16" [out, in], no scale (llama.rs:898 matmul_f16_f32).
+// The embedding takes one of I8, I4 or F16 (embed_token, llama.rs:676-726), and
+// the tied lm_head is the embedding in the same format (llama.rs:576-646).
+enum ProjKind : int32_t { PK_I8 = 0, PK_Q4 = 1, PK_I4 = 2, PK_F16 = 3 };
 
 struct Proj {
     int32_t kind = PK_I8;
     const void* w = nullptr;
-    const void* s = nullptr;  // I8/I4: f16 row scales; Q4: f32 group scales
+    const void* s = nullptr;  // I8/I4: f16 row scales; Q4: f32 group scales; F16: none
     const void* b = nullptr;  // Q4: f32 group biases
 };
 
@@ -146,9 +149,8 @@ struct HostProj {
 struct HostModel {
     std::vector<HostProj> p;  // n_layers * 7, in kNames order
     std::vector<const uint16_t*> n1, n2;
-    const int8_t* embed = nullptr;
-    const uint16_t* embed_scale = nullptr;
-    HostProj lm;  // w == nullptr: tied to the embedding
+    HostProj embed;  // kind I8, I4 or F16; s: f16 row scales (none for F16)
+    HostProj lm;     // w == nullptr: tied to the embedding
     const uint16_t* final_norm = nullptr;
 };
 
@@ -163,10 +165,9 @@ struct cellm_llama_dev {
     size_t kvd = 0, kv_elems = 0;
     // device views of the cached weights: 7 projections per layer, then the lm_head
     std::vector<Proj> p;
-    Proj lm;  // the tied int8 embedding unless the model has its own lm_head
+    Proj lm;     // the tied embedding unless the model has its own lm_head
+    Proj embed;  // kind I8, I4 or F16
     std::vector<const float*> attn_norm, mlp_norm;
-    const int8_t* embed = nullptr;
-    const uint16_t* embed_scale = nullptr;
     const float* final_norm = nullptr;
     DevBuf kcache, vcache, rope, x, x2, xn, q, k, v, attn, proj, h, up, logits, io;
     // fused add+norm+GEMV launches: every projection int8, rows <= 4, hidden % 16 == 0, hidden <= 4096
@@ -223,9 +224,12 @@ int32_t run_proj(cellm_llama_dev* m, const Proj& pr, const float* x, float* y, i
         LIB_TRY(cellm_hip_qgemv_q4_affine(H, static_cast<const uint32_t*>(pr.w), pr.s, pr.b, CELLM_HIP_DTYPE_F32, 64,
                                           x, CELLM_HIP_DTYPE_F32, y, R, out, in, S),
                 what);
-    } else {
+    } else if (pr.kind == PK_I4) {
         LIB_TRY(cellm_hip_qgemv_i4_sym(H, static_cast<const uint8_t*>(pr.w), static_cast<const uint16_t*>(pr.s), out,
                                        in, x, CELLM_HIP_DTYPE_F32, y, R, out, in, S),
+                what);
+    } else {
+        LIB_TRY(cellm_hip_qgemv_f16(H, static_cast<const uint16_t*>(pr.w), x, CELLM_HIP_DTYPE_F32, y, R, out, in, S),
                 what);
     }
     return CELLM_HIP_OK;
@@ -257,7 +261,17 @@ int32_t enqueue_step(cellm_llama_dev* m, int32_t rows)
     auto i8w = [](const Proj& pr) { return static_cast<const int8_t*>(pr.w); };
     auto i8s = [](const Proj& pr) { return static_cast<const uint16_t*>(pr.s); };
 
-    LIB_TRY(cellm_hip_embed_i8(H, d_tok, R, m->embed, m->embed_scale, vocab, hid, x, S), "embed");
+    const Proj& E = m->embed;
+    if (E.kind == PK_I8)
+        LIB_TRY(cellm_hip_embed_i8(H, d_tok, R, static_cast<const int8_t*>(E.w), static_cast<const uint16_t*>(E.s),
+                                   vocab, hid, x, S),
+                "embed");
+    else if (E.kind == PK_I4)
+        LIB_TRY(cellm_hip_embed_i4(H, d_tok, R, static_cast<const uint8_t*>(E.w), static_cast<const uint16_t*>(E.s),
+                                   vocab, hid, x, S),
+                "embed");
+    else
+        LIB_TRY(cellm_hip_embed_f16(H, d_tok, R, static_cast<const uint16_t*>(E.w), vocab, hid, x, S), "embed");
     if (m->fused) {
         // 5 launches per layer; the residual stream alternates between x and x2
         float* x2 = m->x2.as<float>();
@@ -447,8 +461,11 @@ int32_t cellm_llama_dev_create(const cellm_llama_config_t* cfg, const cellm_llam
         hm.n1.push_back(layers[l].input_layernorm_f16);
         hm.n2.push_back(layers[l].post_attention_layernorm_f16);
     }
-    hm.embed = embed_i8;
-    hm.embed_scale = embed_scale_f16;
+    hm.embed.kind = PK_I8;
+    hm.embed.w = embed_i8;
+    hm.embed.w_bytes = (size_t)cfg->vocab * (size_t)cfg->hidden;
+    hm.embed.s = embed_scale_f16;
+    hm.embed.s_bytes = (size_t)cfg->vocab * 2;
     hm.final_norm = final_norm_f16;
     return dev_create_impl(cfg, hm, device, max_rows, max_blocks, out);
     CELLM_API_END(cellm_step::report_exception)
@@ -461,8 +478,10 @@ namespace {
 int32_t dev_create_impl(const cellm_llama_config_t* cfg, const HostModel& hm, int32_t device, int32_t max_rows,
                         int32_t max_blocks, cellm_llama_dev_t** out)
 {
-    if (!cfg || !hm.embed || !hm.embed_scale || !hm.final_norm || !out)
+    if (!cfg || !hm.embed.w || (hm.embed.kind != PK_F16 && !hm.embed.s) || !hm.final_norm || !out)
         return fail(CELLM_HIP_ERR_INVALID_ARG, "null argument");
+    if (hm.embed.kind != PK_I8 && hm.embed.kind != PK_I4 && hm.embed.kind != PK_F16)
+        return fail(CELLM_HIP_ERR_UNSUPPORTED, "embedding format %d is not i8, i4 or f16", hm.embed.kind);
     *out = nullptr;
     const cellm_llama_config_t& c = *cfg;
     if (c.n_layers <= 0 || c.hidden <= 0 || c.n_heads <= 0 || c.n_kv_heads <= 0 || c.head_dim <= 0 ||
@@ -500,15 +519,15 @@ int32_t dev_create_impl(const cellm_llama_config_t* cfg, const HostModel& hm, in
     const size_t hid = (size_t)c.hidden, L = (size_t)c.n_layers;
     // the cache keys follow the .cellm tensor names of each format
     auto upload_proj = [&](const std::string& base, const HostProj& hp, Proj* pr) -> int32_t {
-        if (!hp.w || !hp.s || (hp.kind == PK_Q4 && !hp.b))
+        if (!hp.w || (hp.kind != PK_F16 && !hp.s) || (hp.kind == PK_Q4 && !hp.b))
             return fail(CELLM_HIP_ERR_INVALID_ARG, "%s: weight or scale data missing", base.c_str());
         const void *dw = nullptr, *ds = nullptr, *db = nullptr;
         if (int32_t r = upload(m, base + ".weight", hp.w, hp.w_bytes, &dw)) return r;
         if (hp.kind == PK_Q4) {
             if (int32_t r = upload(m, base + ".scales", hp.s, hp.s_bytes, &ds)) return r;
             if (int32_t r = upload(m, base + ".biases", hp.b, hp.b_bytes, &db)) return r;
-        } else if (int32_t r = upload(m, base + ".weight.qscale", hp.s, hp.s_bytes, &ds)) {
-            return r;
+        } else if (hp.kind != PK_F16) {
+            if (int32_t r = upload(m, base + ".weight.qscale", hp.s, hp.s_bytes, &ds)) return r;
         }
         pr->kind = hp.kind;
         pr->w = dw;
@@ -532,16 +551,10 @@ int32_t dev_create_impl(const cellm_llama_config_t* cfg, const HostModel& hm, in
         m->attn_norm.push_back(a);
         m->mlp_norm.push_back(b);
     }
-    const void *de = nullptr, *des = nullptr;
-    if ((rc = upload(m, "model.embed_tokens.weight", hm.embed, (size_t)c.vocab * hid, &de)) ||
-        (rc = upload(m, "model.embed_tokens.weight.qscale", hm.embed_scale, (size_t)c.vocab * 2, &des)) ||
+    if ((rc = upload_proj("model.embed_tokens", hm.embed, &m->embed)) ||
         (rc = upload_norm(m, "model.norm.weight", hm.final_norm, hid, &m->final_norm)))
         return bail(rc);
-    m->embed = reinterpret_cast<const int8_t*>(de);
-    m->embed_scale = reinterpret_cast<const uint16_t*>(des);
-    m->lm.kind = PK_I8;
-    m->lm.w = m->embed;
-    m->lm.s = m->embed_scale;
+    m->lm = m->embed;  // tied: the lm_head reads the embedding in its own format
     if (hm.lm.w && (rc = upload_proj("lm_head", hm.lm, &m->lm))) return bail(rc);
 
     // paged K/V (KvCacheLayout: total_blocks x layers x tokens_per_block x kv_dim), zeroed
@@ -715,8 +728,13 @@ int32_t cellm_llama_dev_create_from_file(const char* path, int32_t device, int32
             if (int32_t rc = tensor(w, "i4", o, i, hp->w_bytes, &hp->w)) return rc;
             return tensor(w + ".qscale", "f16", o, -1, hp->s_bytes, &hp->s);
         }
-        return fail(CELLM_HIP_ERR_UNSUPPORTED, "tensor %s is %s; the device step takes i8, u32 (MLX affine) or i4",
-                    w.c_str(), t.dtype);
+        if (strcmp(t.dtype, "f16") == 0) {
+            hp->kind = PK_F16;
+            hp->w_bytes = (size_t)(o * i) * 2;
+            return tensor(w, "f16", o, i, hp->w_bytes, &hp->w);
+        }
+        return fail(CELLM_HIP_ERR_UNSUPPORTED,
+                    "tensor %s is %s; the device step takes i8, u32 (MLX affine), i4 or f16", w.c_str(), t.dtype);
     };
     HostModel hm;
     hm.p.resize((size_t)c.n_layers * 7);
@@ -737,13 +755,24 @@ int32_t cellm_llama_dev_create_from_file(const char* path, int32_t device, int32
         hm.n1.push_back(static_cast<const uint16_t*>(n1));
         hm.n2.push_back(static_cast<const uint16_t*>(n2));
     }
-    const void *emb = nullptr, *embs = nullptr, *fn = nullptr;
-    if (int32_t rc = tensor(prefix + "model.embed_tokens.weight", "i8", c.vocab, c.hidden,
-                            (uint64_t)c.vocab * c.hidden, &emb))
-        return rc;
-    if (int32_t rc = tensor(prefix + "model.embed_tokens.weight.qscale", "f16", c.vocab, -1, (uint64_t)c.vocab * 2,
-                            &embs))
-        return rc;
+    // the embedding as embed_token takes it: i8 or i4 with a per-row f16 .qscale, or f16 (llama.rs:676-726)
+    {
+        const std::string e = prefix + "model.embed_tokens.weight";
+        cellm_file_tensor_t t;
+        if (cellm_file_find(f, e.c_str(), &t) != CELLM_HIP_OK)
+            return fail(CELLM_HIP_ERR_NOT_FOUND, "tensor %s missing", e.c_str());
+        if (strcmp(t.dtype, "f16") == 0) {
+            hm.embed.kind = PK_F16;
+            hm.embed.w_bytes = (size_t)c.vocab * c.hidden * 2;
+            if (int32_t rc = tensor(e, "f16", c.vocab, c.hidden, hm.embed.w_bytes, &hm.embed.w)) return rc;
+        } else if (strcmp(t.dtype, "i8") == 0 || strcmp(t.dtype, "i4") == 0) {
+            if (int32_t rc = load_proj(e, c.vocab, c.hidden, &hm.embed)) return rc;
+        } else {
+            return fail(CELLM_HIP_ERR_UNSUPPORTED, "unsupported embed dtype for model.embed_tokens.weight: %s",
+                        t.dtype);
+        }
+    }
+    const void* fn = nullptr;
     if (int32_t rc = tensor(prefix + "model.norm.weight", "f16", c.hidden, -1, (uint64_t)c.hidden * 2, &fn)) return rc;
     // lm_head.weight when the file has one, else the tied embedding (llama.rs:522-532)
     for (const std::string& name : {prefix + "lm_head.weight", std::string("lm_head.weight")}) {
@@ -751,8 +780,6 @@ int32_t cellm_llama_dev_create_from_file(const char* path, int32_t device, int32
         if (int32_t rc = load_proj(name, c.vocab, c.hidden, &hm.lm)) return rc;
         break;
     }
-    hm.embed = static_cast<const int8_t*>(emb);
-    hm.embed_scale = static_cast<const uint16_t*>(embs);
     hm.final_norm = static_cast<const uint16_t*>(fn);
     return dev_create_impl(&c, hm, device, max_rows, max_blocks, out);
     CELLM_API_END(cellm_step::report_exception)

@@ -347,6 +347,20 @@ class HipOps:
         check(self._lib.cellm_hip_embed_i8(self._h, _dev_ptr(tokens_u32), tokens_u32.numel(), _dev_ptr(embed_i8),
                                            _dev_ptr(scales_f16), vocab, hidden, _dev_ptr(out), _stream_ptr(stream)))
 
+    def encode_embed_f16(self, tokens_u32, embed_f16, out, stream=None) -> None:
+        """embed_token's f16 branch (llama.rs:687-693); embed_f16 f16 [vocab, hidden]."""
+        vocab, hidden = embed_f16.shape
+        check(self._lib.cellm_hip_embed_f16(self._h, _dev_ptr(tokens_u32), tokens_u32.numel(), _dev_ptr(embed_f16),
+                                            vocab, hidden, _dev_ptr(out), _stream_ptr(stream)))
+
+    def encode_embed_i4(self, tokens_u32, embed_i4, scales_f16, hidden: int, out, stream=None) -> None:
+        """embed_token's i4 branch (llama.rs:703-718); embed_i4 uint8 [vocab, ceil(hidden/2)]."""
+        vocab = embed_i4.shape[0]
+        if embed_i4.shape[1] != (hidden + 1) // 2:
+            raise ValueError(f"embed_i4 rows hold {embed_i4.shape[1]} bytes, hidden {hidden} needs {(hidden + 1) // 2}")
+        check(self._lib.cellm_hip_embed_i4(self._h, _dev_ptr(tokens_u32), tokens_u32.numel(), _dev_ptr(embed_i4),
+                                           _dev_ptr(scales_f16), vocab, hidden, _dev_ptr(out), _stream_ptr(stream)))
+
     def encode_rms_norm(self, x, weight, out, eps: float, stream=None) -> None:
         n = weight.numel()
         check(self._lib.cellm_hip_rms_norm(self._h, _dev_ptr(x), _dev_ptr(weight), _torch_dtype_code(weight),

@@ -294,6 +294,17 @@ int32_t cellm_hip_logits_q4_affine(cellm_hip_ctx_t* ctx, const float* x, const u
 int32_t cellm_hip_embed_i8(cellm_hip_ctx_t* ctx, const uint32_t* tokens, int64_t rows, const int8_t* embed_i8,
                            const uint16_t* scales_f16, int64_t vocab, int64_t hidden, float* out, void* stream);
 
+/* embed_token, f16 branch (llama.rs:687-693): out[r] = f32(embed_f16[t]),
+ * t = tokens[r] % vocab (f16 bits [vocab, hidden]). */
+int32_t cellm_hip_embed_f16(cellm_hip_ctx_t* ctx, const uint32_t* tokens, int64_t rows, const uint16_t* embed_f16,
+                            int64_t vocab, int64_t hidden, float* out, void* stream);
+
+/* embed_token, i4 branch (llama.rs:703-718): out[r][i] = f32(nibble - 8) *
+ * f32(scales_f16[t]), rows of ceil(hidden / 2) bytes with element 2j in the low
+ * nibble of byte j, t = tokens[r] % vocab. */
+int32_t cellm_hip_embed_i4(cellm_hip_ctx_t* ctx, const uint32_t* tokens, int64_t rows, const uint8_t* embed_i4,
+                           const uint16_t* scales_f16, int64_t vocab, int64_t hidden, float* out, void* stream);
+
 /* MetalOps::encode_rms_norm_f16w (metal.rs) / rms_norm_f32 (cpu_kernels.rs:17-34)
  * per row: out = x * (1 / sqrt(mean(x^2) + eps)) * weight; weight f32/f16/bf16 [n]. */
 int32_t cellm_hip_rms_norm(cellm_hip_ctx_t* ctx, const float* x, const void* weight, int32_t weight_dtype,

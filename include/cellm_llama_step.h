@@ -109,10 +109,13 @@ int32_t cellm_llama_dev_create(const cellm_llama_config_t* cfg, const cellm_llam
  *                                                        -> cellm_hip_qgemv_q4_affine;
  *   "i4"  [out, in] (ceil(in/2) bytes per row) + f16 "<w>.qscale" [out]
  *         (one scale per row, gs = in, gemma.rs:1466-1471)
- *                                                        -> cellm_hip_qgemv_i4_sym.
- * The int8 embedding is the lm_head unless the file has an lm_head.weight (in
- * any of the three formats, llama.rs:522-532).  Other dtypes are
- * CELLM_HIP_ERR_UNSUPPORTED.  A model whose projections are all "i8" runs the
+ *                                                        -> cellm_hip_qgemv_i4_sym;
+ *   "f16" [out, in] (llama.rs:898)                       -> cellm_hip_qgemv_f16.
+ * model.embed_tokens.weight is "i8" or "i4" (+ f16 .qscale per row) or "f16"
+ * (embed_token, llama.rs:676-726) -> cellm_hip_embed_i8 / _i4 / _f16, and is
+ * the lm_head, read through the GEMV of its format, unless the file has an
+ * lm_head.weight (in any of the four formats, llama.rs:522-646).  Other dtypes
+ * are CELLM_HIP_ERR_UNSUPPORTED.  A model whose projections are all "i8" runs the
  * fused decode launches; any other mix runs one launch per projection.
  * tokens_per_block / total_blocks size the paged K/V cache; the file is
  * closed before this returns. */

@@ -49,6 +49,8 @@ def _declare(L):
         "oracle_matmul_i8_f32": (None, [vp, vp, sz, sz, vp, vp]),
         "oracle_qgemv_i8": (None, [vp, vp, i32, vp, i32, sz, sz, sz, vp]),
         "oracle_llama_lm_head_i8": (None, [vp, vp, vp, sz, sz, vp]),
+        "oracle_embed": (None, [i32, vp, sz, vp, vp, sz, sz, vp]),
+        "oracle_llama_lm_head_f16_i4": (None, [i32, vp, vp, vp, sz, sz, vp]),
         "oracle_matmul_i4_f32": (None, [vp, vp, sz, sz, sz, sz, vp, vp]),
         "oracle_qgemv_i4_sym": (None, [vp, vp, sz, sz, vp, i32, sz, sz, sz, vp]),
         "oracle_qgemv_f16": (None, [vp, vp, i32, sz, sz, sz, vp]),
@@ -170,6 +172,31 @@ def llama_lm_head_i8(x: np.ndarray, w: np.ndarray, scales_f16_bits: np.ndarray) 
 
 
 # --- a2: symmetric i4 ----------------------------------------------------------
+
+EMBED_KINDS = {"f16": 0, "i8": 1, "i4": 2}
+
+
+def embed(kind: str, tokens, w: np.ndarray, scales_f16_bits: np.ndarray | None, vocab: int, hidden: int) -> np.ndarray:
+    """LlamaRunner::embed_token (llama.rs:676-726) for each token: kind "f16"
+    (w f16 bits [vocab, hidden]), "i8" (int8 [vocab, hidden]) or "i4" (uint8
+    [vocab, ceil(hidden/2)]), the last two with f16 row scales."""
+    t = np.ascontiguousarray(tokens, np.uint32)
+    out = np.empty((t.size, hidden), np.float32)
+    sp = None if scales_f16_bits is None else _p(np.ascontiguousarray(scales_f16_bits, np.uint16))
+    lib().oracle_embed(EMBED_KINDS[kind], _p(t), t.size, _p(np.ascontiguousarray(w)), sp, vocab, hidden, _p(out))
+    return out
+
+
+def llama_lm_head_f16_i4(kind: str, x: np.ndarray, w: np.ndarray, scales_f16_bits: np.ndarray | None,
+                         vocab: int, hidden: int) -> np.ndarray:
+    """The serial lm_head loop of llama.rs:576-646 over an f16 ("f16") or i4
+    ("i4", per-row f16 scale) source; non-finite logits -> -inf."""
+    out = np.empty(vocab, np.float32)
+    sp = None if scales_f16_bits is None else _p(np.ascontiguousarray(scales_f16_bits, np.uint16))
+    lib().oracle_llama_lm_head_f16_i4(0 if kind == "f16" else 1, _p(np.ascontiguousarray(x, np.float32)),
+                                      _p(np.ascontiguousarray(w)), sp, vocab, hidden, _p(out))
+    return out
+
 
 def matmul_i4_f32(w_u8: np.ndarray, scales_f16_bits: np.ndarray, m: int, k: int, gs: int, x: np.ndarray) -> np.ndarray:
     w_u8 = np.ascontiguousarray(w_u8, np.uint8)

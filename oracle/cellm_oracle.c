@@ -255,6 +255,66 @@ void oracle_llama_lm_head_i8(const float* x, const int8_t* w, const uint16_t* sc
 /* a2: cellm symmetric i4 (u8 bytes, low nibble = even element).            */
 /* ------------------------------------------------------------------------ */
 
+/* LlamaRunner::embed_token (crates/cellm-model/src/llama.rs:676-726), one
+ * row per token, t = token % vocab (:684):
+ *   "f16": out[i] = f16::from_bits(row[i]).to_f32()                (:687-693)
+ *   "i8":  out[i] = (row[i] as f32) * scale[t]                      (:694-702)
+ *   "i4":  out[i] = ((nibble as i8 - 8) as f32) * scale[t], low nibble even,
+ *          ceil(hidden/2) bytes per row                              (:703-718) */
+void oracle_embed(int kind, const uint32_t* tokens, size_t rows, const void* w, const uint16_t* scales_f16,
+                  size_t vocab, size_t hidden, float* out)
+{
+    for (size_t r = 0; r < rows; ++r) {
+        const size_t t = (size_t)tokens[r] % vocab;
+        float* o = out + r * hidden;
+        if (kind == 0) {
+            const uint16_t* row = (const uint16_t*)w + t * hidden;
+            for (size_t i = 0; i < hidden; ++i) o[i] = oracle_f16_to_f32(row[i]);
+        } else if (kind == 1) {
+            const int8_t* row = (const int8_t*)w + t * hidden;
+            const float scale = oracle_f16_to_f32(scales_f16[t]);
+            for (size_t i = 0; i < hidden; ++i) o[i] = (float)row[i] * scale;
+        } else {
+            const size_t stride = (hidden + 1) / 2;
+            const uint8_t* row = (const uint8_t*)w + t * stride;
+            const float scale = oracle_f16_to_f32(scales_f16[t]);
+            for (size_t i = 0; i < hidden; ++i) {
+                const uint8_t b = row[i / 2];
+                const int v = (i % 2 == 0) ? (int)(b & 0x0F) - 8 : (int)(b >> 4) - 8;
+                o[i] = (float)v * scale;
+            }
+        }
+    }
+}
+
+/* The CPU lm_head loop of LlamaRunner::step_inner for an f16 or i4 source
+ * (llama.rs:576-646; the i8 one is oracle_llama_lm_head_i8), serial over the
+ * vocabulary, non-finite logits -> -inf (:641-643):
+ *   f16: acc += x[i] * f16_to_f32(row[i])                           (:602-608)
+ *   i4:  acc += x[i] * val * scale, left to right: (x[i] * val) * scale (:619-634) */
+void oracle_llama_lm_head_f16_i4(int kind, const float* x, const void* w, const uint16_t* scales_f16, size_t vocab,
+                                 size_t hidden, float* out)
+{
+    for (size_t vid = 0; vid < vocab; ++vid) {
+        float acc = 0.0f;
+        if (kind == 0) {
+            const uint16_t* row = (const uint16_t*)w + vid * hidden;
+            for (size_t i = 0; i < hidden; ++i) acc += x[i] * oracle_f16_to_f32(row[i]);
+        } else {
+            const size_t stride = (hidden + 1) / 2;
+            const uint8_t* row = (const uint8_t*)w + vid * stride;
+            const float scale = oracle_f16_to_f32(scales_f16[vid]);
+            for (size_t i = 0; i < hidden; ++i) {
+                const uint8_t b = row[i / 2];
+                const float val = (float)((i % 2 == 0) ? (int)(b & 0x0F) - 8 : (int)(b >> 4) - 8);
+                acc += x[i] * val * scale;
+            }
+        }
+        if (!isfinite(acc)) acc = -INFINITY;
+        out[vid] = acc;
+    }
+}
+
 /* cpu_kernels::matmul_i4_f32 (cpu_kernels.rs:219-243):
  * row_stride = ceil(k/2), spr = len(scales)/m,
  * dot += (q as f32) * scale * b[j]   i.e. ((q*scale)*x) then add. */

@@ -168,10 +168,14 @@ def test_runner_from_file_rejects_other_dtypes(tmp_path, model):
     from cellm_amd.llama_step import LlamaDevice
 
     ts = file_tensors(model)
-    ts = [(n, a, "f16" if n == "model.layers.0.self_attn.q_proj.weight" else d, s) for n, a, d, s in ts]
+    ts = [(n, a, "bf16" if n == "model.layers.0.self_attn.q_proj.weight" else d, s) for n, a, d, s in ts]
     p = tmp_path / "bad.cellm"
     write_cellm(p, header(), ts)
-    with pytest.raises(CellmHipError, match="q_proj.weight is f16"):
+    with pytest.raises(CellmHipError, match="q_proj.weight is bf16"):
+        LlamaDevice.from_file(p, 0, max_rows=ROWS, max_blocks=CTX // TPB, tokens_per_block=TPB)
+    ts = [(n, a, "bf16" if n == "model.embed_tokens.weight" else d, s) for n, a, d, s in file_tensors(model)]
+    write_cellm(p, header(), ts)
+    with pytest.raises(CellmHipError, match="unsupported embed dtype"):
         LlamaDevice.from_file(p, 0, max_rows=ROWS, max_blocks=CTX // TPB, tokens_per_block=TPB)
 
 
@@ -194,9 +198,27 @@ def _i4_proj(o, i, sd):
     return w, s
 
 
+def _f16_proj(o, i, sd):
+    """f16 [o, i] weights with unit-variance outputs for unit inputs."""
+    return (oracle.gen_normal((o, i), sd, 0.0, 1.0 / np.sqrt(i))).astype(np.float16), None
+
+
+def _embed_of(kind, embed, escale):
+    """The int8 test embedding in the given format: "i8" as is, "i4" as the
+    nibbles q + 8 of a fresh i4 table with per-row scales, "f16" as fresh
+    unit-normal rows."""
+    if kind == "i8":
+        return "i8", embed, escale
+    if kind == "i4":
+        w, s = _i4_proj(VOCAB, HID, 0xCF700000)
+        return "i4", w, (s * np.float16(4.6 * np.sqrt(HID) / 7.0)).astype(np.float16)
+    return "f16", oracle.gen_normal((VOCAB, HID), 0xCF700002, 0.0, 1.0).astype(np.float16), None
+
+
 def _mixed_model(kinds):
     """Layer projections in the given per-projection formats ("u32", "i4",
-    "i8"); int8 embedding (tied unless kinds has an "lm" entry)."""
+    "i8", "f16"); the embedding in kinds.get("embed", "i8") (tied unless kinds
+    has an "lm" entry)."""
     i8_layers, embed, escale, fnorm = make_model()
     layers = []
     for l, (ws, ss, n1, n2) in enumerate(i8_layers):
@@ -207,6 +229,8 @@ def _mixed_model(kinds):
                 projs.append(("u32",) + _q4_proj(o, i, sd))
             elif kind == "i4":
                 projs.append(("i4",) + _i4_proj(o, i, sd))
+            elif kind == "f16":
+                projs.append(("f16",) + _f16_proj(o, i, sd))
             else:
                 projs.append(("i8", ws[j], ss[j]))
         layers.append((projs, n1, n2))
@@ -214,7 +238,7 @@ def _mixed_model(kinds):
     if "lm" in kinds:
         lm = ("i4",) + _i4_proj(VOCAB, HID, 0xCF600000) if kinds["lm"] == "i4" else \
             ("u32",) + _q4_proj(VOCAB, HID, 0xCF600000)
-    return layers, embed, escale, fnorm, lm
+    return layers, _embed_of(kinds.get("embed", "i8"), embed, escale), fnorm, lm
 
 
 def _proj_tensors(name, pr):
@@ -224,12 +248,14 @@ def _proj_tensors(name, pr):
         base = name[:-len(".weight")]
         return [(name, wq, "u32", wq.shape), (base + ".scales", s, "f32", s.shape), (base + ".biases", b, "f32", b.shape)]
     w, s = pr[1], pr[2]
+    if kind == "f16":
+        return [(name, w, "f16", w.shape)]
     shape = (w.shape[0], 2 * w.shape[1]) if kind == "i4" else w.shape  # i4: logical [out, in]
     return [(name, w, kind, shape), (name + ".qscale", s, "f16", s.shape)]
 
 
 def _mixed_tensors(mm):
-    layers, embed, escale, fnorm, lm = mm
+    layers, emb, fnorm, lm = mm
     ts = []
     for l, (projs, n1, n2) in enumerate(layers):
         pre = f"model.layers.{l}."
@@ -237,8 +263,7 @@ def _mixed_tensors(mm):
             ts += _proj_tensors(pre + name + ".weight", projs[j])
         ts.append((pre + "input_layernorm.weight", n1, "f16", n1.shape))
         ts.append((pre + "post_attention_layernorm.weight", n2, "f16", n2.shape))
-    ts.append(("model.embed_tokens.weight", embed, "i8", embed.shape))
-    ts.append(("model.embed_tokens.weight.qscale", escale, "f16", escale.shape))
+    ts += _proj_tensors("model.embed_tokens.weight", emb)
     ts.append(("model.norm.weight", fnorm, "f16", fnorm.shape))
     if lm is not None:
         ts += _proj_tensors("lm_head.weight", lm)
@@ -248,7 +273,9 @@ def _mixed_tensors(mm):
 def _oracle_proj(pr, x, o, i):
     """The reference's linear for each format: matmul_i8_f32 (cpu_kernels.rs:66-133),
     the LFM affine GEMV (lfm.rs:985-1066), matmul_i4_f32 with gs = in_dim
-    (cpu_kernels.rs:219-243, gemma.rs:1471)."""
+    (cpu_kernels.rs:219-243, gemma.rs:1471), matmul_f16_f32 (cpu_kernels.rs:135-214)."""
+    if pr[0] == "f16":
+        return oracle.qgemv_f16(pr[1].view(np.uint16), x.reshape(1, -1))[0]
     if pr[0] == "u32":
         return oracle.qgemv_q4_affine(pr[1], pr[2], pr[3], x.reshape(1, -1), i)[0]
     if pr[0] == "i4":
@@ -259,9 +286,10 @@ def _oracle_proj(pr, x, o, i):
 def _oracle_session(mm, kc, vc, token, pos, bt):
     """LlamaRunner::step_inner (llama.rs:235-647) for one session over the
     paged f16 cache (updated in place), projections by format."""
-    layers, embed, escale, fnorm, lm = mm
-    t = token % VOCAB
-    x = (embed[t].astype(np.float32) * np.float32(escale[t])).astype(np.float32)
+    layers, emb, fnorm, lm = mm
+    ekind, ew, es = emb
+    x = oracle.embed(ekind, [token], ew.view(np.uint16) if ekind == "f16" else ew,
+                     None if es is None else es.view(np.uint16), VOCAB, HID)[0]
 
     def base_of(tpos, layer):
         return int(bt[tpos // TPB]) * (L * TPB * KVD) + layer * (TPB * KVD) + (tpos % TPB) * KVD
@@ -284,25 +312,35 @@ def _oracle_session(mm, kc, vc, token, pos, bt):
         oracle.silu_mul_(g, _oracle_proj(projs[5], xn, INTER, HID))
         x = x + _oracle_proj(projs[6], g, HID, INTER)
     xf = oracle.rms_norm(x, fnorm.astype(np.float32), 1e-5)
-    logits = oracle.llama_lm_head_i8(xf, embed, escale.view(np.uint16)) if lm is None else \
-        _oracle_proj(lm, xf, VOCAB, HID)
+    if lm is not None:
+        logits = _oracle_proj(lm, xf, VOCAB, HID)
+    elif ekind == "i8":  # the tied lm_head reads the embedding in its own format (llama.rs:576-646)
+        logits = oracle.llama_lm_head_i8(xf, ew, es.view(np.uint16))
+    else:
+        logits = oracle.llama_lm_head_f16_i4(ekind, xf, ew.view(np.uint16) if ekind == "f16" else ew,
+                                             None if es is None else es.view(np.uint16), VOCAB, HID)
     return oracle.argmax_first(logits), logits
 
 
-@pytest.mark.parametrize("case", ["u32", "i4", "mixed"])
+@pytest.mark.parametrize("case", ["u32", "i4", "mixed", "f16", "i8_embed_i4", "mixed_embed_f16"])
 def test_runner_from_file_other_formats_match_oracle(tmp_path, case):
-    """Row a7: .cellm projections as "u32" MLX affine (+ f32 .scales/.biases,
-    as tools/convert_lfm.py writes them) and as "i4" (+ f16 .qscale), each
-    dispatched to its HIP GEMV; a mixed file also pairs an i8 gate with an i4
-    up (separate GEMVs + the SiLU kernel) and carries an i4 lm_head.  Greedy
+    """The runners' dtype dispatch from a .cellm file: projections as "u32"
+    MLX affine (+ f32 .scales/.biases, as tools/convert_lfm.py writes them),
+    "i4" (+ f16 .qscale) or "f16", each dispatched to its HIP GEMV; a mixed
+    file also pairs an i8 gate with an i4 up (separate GEMVs + the SiLU
+    kernel) and carries an i4 lm_head.  The embedding as "i8", "i4" or "f16"
+    (embed_token, llama.rs:676-726) is also the tied lm_head in its own format
+    ("i8_embed_i4" keeps the fused int8 launches with an i4 embedding).  Greedy
     ids of 4 sessions equal the oracle step's; logits within 1e-3."""
     from cellm_amd.llama_step import LlamaDevice
 
-    kinds = {"u32": ["u32"] * 7, "i4": ["i4"] * 7,
-             "mixed": ["u32", "i4", "i8", "u32", "i8", "i4", "u32"]}[case]
+    kinds = {"u32": ["u32"] * 7, "i4": ["i4"] * 7, "f16": ["f16"] * 7, "i8_embed_i4": ["i8"] * 7,
+             "mixed": ["u32", "i4", "i8", "u32", "i8", "i4", "u32"],
+             "mixed_embed_f16": ["f16", "i8", "i4", "f16", "u32", "f16", "i8"]}[case]
     kinds = dict(enumerate(kinds))
     if case == "mixed":
         kinds["lm"] = "i4"
+    kinds["embed"] = {"f16": "f16", "mixed_embed_f16": "f16", "i8_embed_i4": "i4"}.get(case, "i8")
     mm = _mixed_model(kinds)
     p = tmp_path / f"{case}.cellm"
     write_cellm(p, header(tied=case != "mixed"), _mixed_tensors(mm))

@@ -69,6 +69,26 @@ def test_embed_i8(ops):
     np.testing.assert_array_equal(out.cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("hid", [960, 7])
+def test_embed_f16_and_i4_bit_exact(ops, hid):
+    """embed_token's f16 and i4 branches (llama.rs:687-693, 703-718) against
+    the oracle, bit for bit; an odd hidden size for i4 rows of ceil(hid/2)
+    bytes; tokens wrap modulo the vocabulary."""
+    vocab = 1000
+    rng = np.random.default_rng(0xD0000003 + hid)
+    ef = rng.standard_normal((vocab, hid)).astype(np.float16)
+    e4 = rng.integers(0, 256, (vocab, (hid + 1) // 2)).astype(np.uint8)
+    sc = (rng.uniform(0.5, 1.5, vocab) / 7).astype(np.float16).view(np.uint16)
+    toks = np.array([3, 999, 1000 + 5, 0], np.uint32)
+    out = torch.empty((4, hid), dtype=torch.float32, device="cuda")
+    ops.encode_embed_f16(dev(toks), dev(ef.view(np.uint16)), out)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy(), oracle.embed("f16", toks, ef.view(np.uint16), None, vocab, hid))
+    ops.encode_embed_i4(dev(toks), dev(e4), dev(sc), hid, out)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy(), oracle.embed("i4", toks, e4, sc, vocab, hid))
+
+
 @pytest.mark.parametrize("wdt", ["f32", "f16"])
 @pytest.mark.parametrize("n", [960, 1152, 7])
 def test_rms_norm(ops, n, wdt):

@@ -149,6 +149,75 @@ def test_llama_lm_head_i8_per_element_scale_and_nonfinite():
     assert np.all(np.isneginf(y))
 
 
+def test_embed_f16_i8_i4_known_answers_and_wrap():
+    """llama.rs:676-726: f16 rows widen exactly (every f16 pattern against
+    numpy); i8 rows are f32(w) * scale; i4 byte 0x8F -> [7, 0] (low nibble
+    even, q = nib - 8) times the row scale, ceil(hidden/2) bytes per row for
+    an odd hidden; the token wraps modulo the vocabulary (:684)."""
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16).reshape(1, -1)
+    got = oracle.embed("f16", [0], bits, None, 1, 65536)[0]
+    want = bits[0].view(np.float16).astype(np.float32)
+    finite = np.isfinite(want)
+    assert np.array_equal(got[finite].view(np.uint32), want[finite].view(np.uint32))
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    rng = np.random.default_rng(41)
+    v, h = 5, 7
+    w8 = rng.integers(-127, 128, (v, h)).astype(np.int8)
+    s = rng.uniform(1e-3, 2e-2, v).astype(np.float16)
+    got = oracle.embed("i8", [3, v + 1], w8, s.view(np.uint16), v, h)
+    assert np.array_equal(got[0], w8[3].astype(np.float32) * np.float32(s[3]))
+    assert np.array_equal(got[1], w8[1].astype(np.float32) * np.float32(s[1]))
+    w4 = np.zeros((v, (h + 1) // 2), np.uint8)
+    w4[2, 0], w4[2, 3] = 0x8F, 0xE1  # elements 0, 1 = 7, 0; element 6 = 1 - 8 (its high nibble has no element)
+    got = oracle.embed("i4", [2], w4, s.view(np.uint16), v, h)[0]
+    sc = np.float32(s[2])
+    want = np.array([7, 0, -8, -8, -8, -8, -7], np.float32) * sc
+    assert np.array_equal(got, want)
+    # every byte value, both nibbles, against numpy's own unpacking
+    w4 = np.arange(256, dtype=np.uint8).reshape(1, 256)
+    got = oracle.embed("i4", [0], w4, np.array([0x3C00], np.uint16), 1, 512)[0]
+    want = np.empty(512, np.float32)
+    want[0::2] = (w4[0] & 0xF).astype(np.int32) - 8
+    want[1::2] = (w4[0] >> 4).astype(np.int32) - 8
+    assert np.array_equal(got, want)
+
+
+def test_llama_lm_head_f16_i4_order_bounds_and_nonfinite():
+    """llama.rs:576-646 for f16 and i4 sources: strict left-to-right sums of
+    x * f32(w) and (x * val) * scale; integer data with a power-of-two scale
+    is exact; random data within gamma_K of an fp64 dot; non-finite -> -inf."""
+    rng = np.random.default_rng(42)
+    v, h = 6, 96
+    wf = rng.standard_normal((v, h)).astype(np.float16)
+    x = rng.standard_normal(h).astype(np.float32)
+    y = oracle.llama_lm_head_f16_i4("f16", x, wf.view(np.uint16), None, v, h)
+    for r in range(v):
+        assert y[r] == seq_sum_f32(x * wf[r].astype(np.float32))
+        exact = float(np.dot(x.astype(np.float64), wf[r].astype(np.float64)))
+        bound = gamma(h) * float(np.sum(np.abs(x.astype(np.float64) * wf[r].astype(np.float64))))
+        assert abs(float(y[r]) - exact) <= bound
+    w4 = rng.integers(0, 256, (v, (h + 1) // 2)).astype(np.uint8)
+    s = rng.uniform(1e-3, 2e-2, v).astype(np.float16)
+    y = oracle.llama_lm_head_f16_i4("i4", x, w4, s.view(np.uint16), v, h)
+    q = np.empty((v, h), np.float32)
+    q[:, 0::2] = (w4 & 0xF).astype(np.int32) - 8
+    q[:, 1::2] = (w4 >> 4).astype(np.int32) - 8
+    for r in range(v):
+        assert y[r] == seq_sum_f32((x * q[r]) * np.float32(s[r]))
+        exact = float(np.dot(x.astype(np.float64), q[r].astype(np.float64))) * float(np.float32(s[r]))
+        bound = 2 * gamma(h + 2) * float(np.sum(np.abs(x.astype(np.float64) * q[r]))) * float(np.float32(s[r]))
+        assert abs(float(y[r]) - exact) <= bound
+    # integer x, power-of-two scale: every partial sum exact
+    xi = rng.integers(-4, 5, h).astype(np.float32)
+    s2 = np.full(v, 0.25, np.float16)
+    y = oracle.llama_lm_head_f16_i4("i4", xi, w4, s2.view(np.uint16), v, h)
+    assert np.array_equal(y, (q.astype(np.int64) @ xi.astype(np.int64)).astype(np.float32) * np.float32(0.25))
+    x[5] = np.inf
+    wf[0, 5], wf[1, 5], wf[2, 5] = 1.0, -1.0, 0.0
+    y = oracle.llama_lm_head_f16_i4("f16", x, wf.view(np.uint16), None, v, h)
+    assert np.all(np.isneginf(y[:3]))
+
+
 # ------------------------------------------------------------- a2: i4 sym ----
 
 def test_i4_known_answer_and_order():
