@@ -138,7 +138,7 @@ def gen_normal(shape, seed: int, mu: float, sigma: float, positive_only: bool = 
     return out
 
 
-# --- a1 / a8: int8 -----------------------------------------------------------
+# --- int8 GEMV and the Llama int8 lm_head -----------------------------------
 
 def matmul_i8_f32(w: np.ndarray, scales_f16_bits: np.ndarray, x: np.ndarray) -> np.ndarray:
     """cpu_kernels::matmul_i8_f32 (x86 branch), f16 scales."""
@@ -152,7 +152,7 @@ def matmul_i8_f32(w: np.ndarray, scales_f16_bits: np.ndarray, x: np.ndarray) -> 
 
 
 def qgemv_i8(w: np.ndarray, scales: np.ndarray, x: np.ndarray) -> np.ndarray:
-    """Batched a1: x [M,K] (f32 or f16), scales [N] (f32, f16, or uint16 = bf16 bits)."""
+    """Batched int8 GEMV: x [M,K] (f32 or f16), scales [N] (f32, f16, or uint16 = bf16 bits)."""
     n, k = w.shape
     x2 = np.ascontiguousarray(x.reshape(-1, k))
     m = x2.shape[0]
@@ -171,7 +171,7 @@ def llama_lm_head_i8(x: np.ndarray, w: np.ndarray, scales_f16_bits: np.ndarray) 
     return out
 
 
-# --- a2: symmetric i4 ----------------------------------------------------------
+# --- Llama embedding and f16 / i4 lm_head sources -----------------------------
 
 EMBED_KINDS = {"f16": 0, "i8": 1, "i4": 2}
 
@@ -197,6 +197,8 @@ def llama_lm_head_f16_i4(kind: str, x: np.ndarray, w: np.ndarray, scales_f16_bit
                                       _p(np.ascontiguousarray(w)), sp, vocab, hidden, _p(out))
     return out
 
+
+# --- symmetric i4 ----------------------------------------------------------------
 
 def matmul_i4_f32(w_u8: np.ndarray, scales_f16_bits: np.ndarray, m: int, k: int, gs: int, x: np.ndarray) -> np.ndarray:
     w_u8 = np.ascontiguousarray(w_u8, np.uint8)
@@ -246,7 +248,7 @@ def qgemv_q1_0_g128(w_u8: np.ndarray, x: np.ndarray, k: int) -> np.ndarray:
     return y
 
 
-# --- a3/a4/a5: MLX affine -------------------------------------------------------
+# --- MLX affine GEMV, lm_head and f16 dequant -----------------------------------
 
 def q4_affine_dequant_f32(wq: np.ndarray, scales: np.ndarray, biases: np.ndarray, k: int, gs: int = 64) -> np.ndarray:
     n = wq.shape[0]
@@ -291,7 +293,7 @@ def dequant_q4_affine_f16(wq, scales, biases, k: int, gs: int = 64) -> np.ndarra
     return out
 
 
-# --- a6: dense ------------------------------------------------------------------
+# --- dense f32 -------------------------------------------------------------------
 
 def matmul_f32(a: np.ndarray, b: np.ndarray, out: np.ndarray | None = None) -> np.ndarray:
     m, k = a.shape
@@ -313,7 +315,7 @@ def gemm_xwT(x: np.ndarray, w_f32: np.ndarray) -> np.ndarray:
     return y
 
 
-# --- a9 helpers -------------------------------------------------------------------
+# --- decode-step helpers ----------------------------------------------------------
 
 def rms_norm(x, w, eps):
     out = np.empty_like(x, dtype=np.float32)

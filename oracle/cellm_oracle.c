@@ -197,7 +197,7 @@ void oracle_gen_normal(float* out, size_t n, uint64_t seed, float mu, float sigm
 }
 
 /* ------------------------------------------------------------------------ */
-/* a1: int8 per-output-row scaled GEMV.                                     */
+/* int8 per-output-row scaled GEMV.                                         */
 /* ------------------------------------------------------------------------ */
 
 /* cpu_kernels::matmul_i8_f32, x86 branch (crates/cellm-kernels/src/cpu_kernels.rs:66-80,124-131):
@@ -215,7 +215,7 @@ void oracle_matmul_i8_f32(const int8_t* a_i8, const uint16_t* a_scales_f16, size
     }
 }
 
-/* Batched form of a1 for M activation rows and the config dtypes: the scale
+/* Batched form of the int8 GEMV for M activation rows and the config dtypes: the scale
  * (f32/f16/bf16) and x (f32/f16) are widened exactly to f32, then each output
  * y[mi, n] is the reference row GEMV above on activation row mi.
  * This is what the reference computes when called once per row (one session
@@ -235,7 +235,7 @@ void oracle_qgemv_i8(const int8_t* w, const void* scales, int scale_dtype, const
     }
 }
 
-/* a8: Llama CPU lm_head over i8 weights (crates/cellm-model/src/llama.rs:602-643):
+/* Llama CPU lm_head over i8 weights (crates/cellm-model/src/llama.rs:602-643):
  * serial over vocab, scale applied per element: acc += x[i] * ((w as f32) * scale);
  * non-finite -> -inf. */
 void oracle_llama_lm_head_i8(const float* x, const int8_t* w, const uint16_t* scales_f16, size_t vocab,
@@ -252,7 +252,7 @@ void oracle_llama_lm_head_i8(const float* x, const int8_t* w, const uint16_t* sc
 }
 
 /* ------------------------------------------------------------------------ */
-/* a2: cellm symmetric i4 (u8 bytes, low nibble = even element).            */
+/* cellm symmetric i4 (u8 bytes, low nibble = even element).                */
 /* ------------------------------------------------------------------------ */
 
 /* LlamaRunner::embed_token (crates/cellm-model/src/llama.rs:676-726), one
@@ -339,7 +339,7 @@ void oracle_matmul_i4_f32(const uint8_t* a_i4, const uint16_t* a_scales_f16, siz
     }
 }
 
-/* Batched/dtype form of a2: x widened from f32/f16, M activation rows. */
+/* Batched/dtype form of the symmetric i4 GEMV: x widened from f32/f16, M activation rows. */
 void oracle_qgemv_i4_sym(const uint8_t* w, const uint16_t* scales_f16, size_t n_scales, size_t gs,
                          const void* x, int x_dtype, size_t M, size_t N, size_t K, float* y)
 {
@@ -458,7 +458,7 @@ void oracle_qgemv_q1_0_g128(const uint8_t* w, const void* x, int x_dtype, size_t
 }
 
 /* ------------------------------------------------------------------------ */
-/* a3/a4: MLX 4-bit affine (u32 words, 8 nibbles, per-64-group scale+bias). */
+/* MLX 4-bit affine (u32 words, 8 nibbles, per-64-group scale+bias).        */
 /* ------------------------------------------------------------------------ */
 
 /* Dequant of LfmRunner::linear_i4_out_in (crates/cellm-model/src/lfm.rs:1006-1025):
@@ -488,9 +488,9 @@ void oracle_q4_affine_dequant_f32(const uint32_t* wq, const void* scales, const 
     }
 }
 
-/* Full a3 GEMV: dequant as above, then the cached-f32 dot
+/* Full affine GEMV: dequant as above, then the cached-f32 dot
  * (lfm.rs:1056-1063): acc += w[j] * x[j], j ascending.
- * a4 (the affine lm_head, lfm.rs:715-737) evaluates the same per-element
+ * The affine lm_head ( lfm.rs:715-737) evaluates the same per-element
  * formula q*s+b and the same ascending-j sum, so it yields identical bits. */
 void oracle_qgemv_q4_affine(const uint32_t* wq, const void* scales, const void* biases, int sb_dtype,
                             const void* x, int x_dtype, size_t M, size_t N, size_t K, size_t G, float* y)
@@ -519,7 +519,7 @@ void oracle_qgemv_q4_affine(const uint32_t* wq, const void* scales, const void* 
     }
 }
 
-/* a4 as written in the reference (lfm.rs:700-741): group loop, j loop, the
+/* The affine lm_head as written in the reference (lfm.rs:700-741): group loop, j loop, the
  * on-the-fly dequant and out-of-range defaults (scale 1.0, bias 0.0).  Kept
  * separate so a test can show it equals oracle_qgemv_q4_affine bit for bit. */
 void oracle_lfm_lm_head_q4_affine(const uint32_t* wq, size_t nwords, const float* scales, const float* biases,
@@ -554,7 +554,7 @@ void oracle_lfm_lm_head_q4_affine(const uint32_t* wq, size_t nwords, const float
     }
 }
 
-/* a5: dequant_u32_affine_to_f16 (tools/convert/src/main.rs:4349-4444):
+/* dequant_u32_affine_to_f16 (tools/convert/src/main.rs:4349-4444):
  * in_dim = packed_in*8, groups = ceil(in_dim/gs), g = min(i/gs, groups-1),
  * fp = (q as f32) * scale + bias (two roundings), h = f16::from_f32(fp) (RNE). */
 void oracle_dequant_q4_affine_f16(const uint32_t* wq, const void* scales, const void* biases, int sb_dtype,
@@ -579,7 +579,7 @@ void oracle_dequant_q4_affine_f16(const uint32_t* wq, const void* scales, const 
 }
 
 /* ------------------------------------------------------------------------ */
-/* a6: dense f32 matmul (cpu_kernels.rs:36-63).                             */
+/* dense f32 matmul (cpu_kernels.rs:36-63).                                 */
 /* ------------------------------------------------------------------------ */
 
 /* n == 1: row dot; else out[i, j] += a[i,k] * b[k,j] in i-k-j order.  The
@@ -610,9 +610,9 @@ void oracle_matmul_f32(const float* a, size_t m, size_t k, const float* b, size_
 }
 
 /* Prefill reference for the qGEMM: Y[M,N] = X[M,K] . dequant(W)^T, each
- * element summed over k ascending from zero (a6 over the a3 or a5 dequant).
+ * element summed over k ascending from zero (the dense matmul over the affine f32 or f16 dequant).
  * w_f32 is the dequantized weight [N,K] (row-major out x in); x widened from
- * f32/f16.  The per-element order equals a6's i-k-j loop with a zeroed out. */
+ * f32/f16.  The per-element order equals the dense matmul's i-k-j loop with a zeroed out. */
 void oracle_gemm_xwT_f32(const void* x, int x_dtype, const float* w_f32, size_t M, size_t N, size_t K, float* y)
 {
 #pragma omp parallel for schedule(static)
@@ -627,7 +627,7 @@ void oracle_gemm_xwT_f32(const void* x, int x_dtype, const float* w_f32, size_t 
 }
 
 /* ------------------------------------------------------------------------ */
-/* a9: pieces of LlamaRunner::step_inner used around the projections.       */
+/* pieces of LlamaRunner::step_inner used around the projections.           */
 /* ------------------------------------------------------------------------ */
 
 /* rms_norm_f32 (cpu_kernels.rs:17-34). */

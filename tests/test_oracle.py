@@ -85,7 +85,7 @@ def test_lcg_deterministic_and_in_range():
     assert s.min() > 0 and abs(float(s.mean()) - 0.02) < 5e-4
 
 
-# ------------------------------------------------------ a1: int8 per-row ----
+# ---------------------------------------------------------- int8 per-row ----
 
 def test_i8_closed_form_exact_integers():
     """Integer x in [-4,4], power-of-two scales, K <= 4096: every partial sum is
@@ -218,7 +218,7 @@ def test_llama_lm_head_f16_i4_order_bounds_and_nonfinite():
     assert np.all(np.isneginf(y[:3]))
 
 
-# ------------------------------------------------------------- a2: i4 sym ----
+# ----------------------------------------------------------------- i4 sym ----
 
 def test_i4_known_answer_and_order():
     """byte 0x8F -> elements [7, 0] (low nibble even, q = nib - 8)."""
@@ -241,7 +241,7 @@ def test_i4_known_answer_and_order():
         assert y[r] == seq_sum_f32((q[r] * sc) * x)
 
 
-# --------------------------------------------------------- a3/a4/a5: affine ----
+# --------------------------------------------------------------- affine ----
 
 def _unpack(wq: np.ndarray) -> np.ndarray:
     return ((wq[..., None] >> (4 * np.arange(8, dtype=np.uint32))) & 0xF).reshape(wq.shape[0], -1)
@@ -288,7 +288,7 @@ def test_affine_gemv_sequential_bit_exact_and_lm_head_equal():
     for i in range(m):
         for r in range(n):
             assert y[i, r] == seq_sum_f32(w[r] * x[i].astype(np.float32))
-    # a4 (lfm.rs:700-741) with f32 scale/bias files gives the same bits as a3
+    # the affine lm_head (lfm.rs:700-741) with f32 scale/bias files gives the same bits as the GEMV
     s32, b32 = s.astype(np.float32), b.astype(np.float32)
     lm = oracle.lfm_lm_head_q4_affine(wq, s32, b32, x[0].astype(np.float32), n, k)
     assert np.array_equal(lm, oracle.qgemv_q4_affine(wq, s32, b32, x[0:1].astype(np.float32), k)[0])
@@ -333,7 +333,7 @@ def test_dequant_f16_rne_and_double_rounding():
     assert h1 == double and h1 != single
 
 
-# --------------------------------------------------------------- a6: dense ----
+# ------------------------------------------------------------------- dense ----
 
 def test_matmul_f32_accumulates_into_out_sequentially():
     rng = np.random.default_rng(11)
@@ -362,7 +362,7 @@ def test_gemm_xwT_equals_matmul_over_transposed_weight():
     assert np.array_equal(y, ref)
 
 
-# ------------------------------------------------- a9: decode-step helpers ----
+# ----------------------------------------------------- decode-step helpers ----
 
 def test_rms_norm_closed_form():
     x = np.full(64, 3.0, np.float32)
