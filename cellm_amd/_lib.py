@@ -67,6 +67,7 @@ SIGNATURES = {
     "cellm_hip_qgemv_i2": (_i32, [_vp, _vp, _vp, _i32, _vp, _i32, _vp, _i64, _i64, _i64, _vp]),
     "cellm_hip_qgemv_q1_0_g128": (_i32, [_vp, _vp, _vp, _i32, _vp, _i64, _i64, _i64, _vp]),
     "cellm_hip_upload_cellm_file": (_i32, [_vp, _vp, C.c_char_p, _vp, _vp]),
+    "cellm_hip_linear_file": (_i32, [_vp, _vp, C.c_char_p, _i32, _vp, _vp, _i64, _i64, _i64, _vp]),
     "cellm_hip_decode_qkv_rope_kv": (_i32, [_vp, _vp, _vp, _vp, _vp, C.c_float, _vp, _vp, _vp, _vp, _vp, _vp, _i64,
                                             _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64,
                                             _i64, _i64, _i64, _vp]),

@@ -3,8 +3,10 @@ cellm_file_*), the host side of CellmFile (crates/cellm-model/src/cellm_file.rs)
 
 `CellmFile(path)` maps and validates a file; `.config` holds the model fields
 of the header, `.tensors` the tensor index in header order, `.tensor_bytes`
-returns a zero-copy numpy view of the mapped bytes, and `.upload(ops)` puts
-the tensors into a HipOps context's name-keyed device weight cache.
+returns a zero-copy numpy view of the mapped bytes, `.upload(ops)` puts
+the tensors into a HipOps context's name-keyed device weight cache, and
+`.linear(ops, name, family, x, y)` runs one projection by the dtype of its
+weight tensor under a runner family's dispatch rules.
 """
 from __future__ import annotations
 
@@ -37,6 +39,9 @@ class TensorInfo:
     offset_bytes: int
     nbytes: int
 
+
+# runner families of cellm_hip_linear_file (CELLM_HIP_FAMILY_*)
+FAMILIES = {"llama": 0, "qwen": 1, "gemma": 2, "lfm": 3}
 
 _bound = None
 
@@ -128,6 +133,23 @@ class CellmFile:
         _check(ops._lib.cellm_hip_upload_cellm_file(ops._h, self._h, name_prefix.encode() if name_prefix else None,
                                                     C.byref(count), C.byref(nbytes)), "cellm_hip_upload_cellm_file")
         return count.value, nbytes.value
+
+    def linear(self, ops, weight_name: str, family: str, x, y, stream=None) -> None:
+        """y[m, out] = W x[m, in] with W the tensor `weight_name`, dispatched on its dtype as the
+        family's ("llama", "qwen", "gemma", "lfm") linear_f16_out_in does (cellm_hip_linear_file);
+        x and y are float32 device tensors of shape [m, in] and [m, out]; enqueued on `stream`.
+        The first call for a tensor uploads it into ops' weight cache."""
+        from .hipops import _dev_ptr, _stream_ptr
+        import torch
+
+        if family not in FAMILIES:
+            raise ValueError(f"family must be one of {sorted(FAMILIES)}")
+        if x.dtype != torch.float32 or y.dtype != torch.float32 or x.dim() != 2 or y.dim() != 2 \
+                or x.shape[0] != y.shape[0]:
+            raise ValueError("x and y must be float32 [m, in] and [m, out] device tensors")
+        _check(ops._lib.cellm_hip_linear_file(ops._h, self._h, weight_name.encode(), FAMILIES[family], _dev_ptr(x),
+                                              _dev_ptr(y), x.shape[0], y.shape[1], x.shape[1], _stream_ptr(stream)),
+               f"cellm_hip_linear_file({weight_name})")
 
     def close(self) -> None:
         if getattr(self, "_h", None):

@@ -23,6 +23,7 @@
 #include <cerrno>
 #include <cmath>
 #include <cstdarg>
+#include <cstdint>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -514,6 +515,152 @@ int32_t cellm_hip_upload_cellm_file(cellm_hip_ctx_t* ctx, const cellm_file_t* f,
     if (out_count) *out_count = count;
     if (out_bytes) *out_bytes = bytes;
     return CELLM_HIP_OK;
+    CELLM_API_END(cellm::report_exception)
+}
+
+
+// One projection by the dtype of its .cellm weight tensor, with the rules of
+// the runner family's linear_f16_out_in.  The tensors it reads go into the
+// context's weight cache under their file names on first use (blocking
+// upload), as the Metal ops cache weights by name; later calls only enqueue.
+int32_t cellm_hip_linear_file(cellm_hip_ctx_t* ctx, const cellm_file_t* f, const char* weight_name, int32_t family,
+                              const float* x, float* y, int64_t m, int64_t out_dim, int64_t in_dim, void* stream)
+{
+    CELLM_API_BEGIN
+    if (!ctx || !f || !weight_name) return fail(CELLM_HIP_ERR_INVALID_ARG, "null argument");
+    if (family < CELLM_HIP_FAMILY_LLAMA || family > CELLM_HIP_FAMILY_LFM)
+        return fail(CELLM_HIP_ERR_INVALID_ARG, "unknown runner family %d", family);
+    if (m < 0 || out_dim < 1 || in_dim < 1 || out_dim > INT32_MAX || in_dim > INT32_MAX)
+        return fail(CELLM_HIP_ERR_INVALID_ARG, "bad dimensions m=%lld out=%lld in=%lld", (long long)m,
+                    (long long)out_dim, (long long)in_dim);
+    if (m > 0 && (!x || !y)) return fail(CELLM_HIP_ERR_INVALID_ARG, "null x or y");
+    const std::string name = weight_name;
+    const long long o = out_dim, i = in_dim;
+    auto find = [&](const std::string& n) -> const cellm_file_tensor_t* {
+        auto it = f->by_name.find(n);
+        return it == f->by_name.end() ? nullptr : &f->tensors[it->second];
+    };
+    auto on_device = [&](const cellm_file_tensor_t* t, const void** dev) -> int32_t {
+        return cellm_hip_weight_upload(ctx, t->name, f->map + t->offset_bytes, (size_t)t->nbytes, dev);
+    };
+    // "<w>.qscale" as f16 row scales of at least one per row; `exact` requires exactly one per row
+    auto qscale = [&](bool exact, const void** dev, int64_t* count) -> int32_t {
+        const cellm_file_tensor_t* s = find(name + ".qscale");
+        if (!s) return fail(CELLM_HIP_ERR_NOT_FOUND, "unknown tensor %s.qscale", weight_name);
+        *count = (int64_t)(s->nbytes / 2);
+        if (exact && *count != out_dim)
+            return fail(CELLM_HIP_ERR_INVALID_ARG, "weight %s qscale len mismatch: %lld expected %lld", weight_name,
+                        (long long)*count, o);
+        if (*count < out_dim)
+            return fail(CELLM_HIP_ERR_INVALID_ARG, "weight %s qscale holds %lld scales for %lld rows", weight_name,
+                        (long long)*count, o);
+        return on_device(s, dev);
+    };
+    auto len_check = [&](const cellm_file_tensor_t* t, uint64_t want, long long elems, long long want_elems) {
+        return t->nbytes == want ? CELLM_HIP_OK
+                                 : fail(CELLM_HIP_ERR_INVALID_ARG, "weight %s len mismatch: %lld expected %lld",
+                                        weight_name, elems, want_elems);
+    };
+    const cellm_file_tensor_t* t = find(name);
+    const int fam = family;
+    if (!t) {
+        if (fam == CELLM_HIP_FAMILY_QWEN)  // qwen.rs:1035-1036
+            return fail(CELLM_HIP_ERR_NOT_FOUND, "linear_f16_out_in: unknown tensor '%s'", weight_name);
+        return fail(CELLM_HIP_ERR_NOT_FOUND, "unknown tensor %s", weight_name);
+    }
+    const std::string dt = t->dtype;
+    if (fam == CELLM_HIP_FAMILY_LLAMA || fam == CELLM_HIP_FAMILY_GEMMA) {
+        // [out, in] check of llama.rs:764-776 / gemma.rs:1366-1391
+        std::string shape = "[";
+        for (int32_t d = 0; d < t->ndim; ++d) shape += (d ? ", " : "") + std::to_string(t->shape[d]);
+        shape += "]";
+        if (t->ndim != 2) return fail(CELLM_HIP_ERR_INVALID_ARG, "weight %s expected 2D, got %s", weight_name, shape.c_str());
+        if (t->shape[0] != out_dim || t->shape[1] != in_dim)
+            return fail(CELLM_HIP_ERR_INVALID_ARG, "weight %s shape mismatch: %s expected [%lld,%lld]", weight_name,
+                        shape.c_str(), o, i);
+    }
+    const void *w = nullptr, *s = nullptr, *b = nullptr;
+    int64_t ns = 0;
+    if (fam == CELLM_HIP_FAMILY_LFM) {
+        // lfm.rs:924-981: "u32" with "<base>.scales" and "<base>.biases" is the MLX affine GEMV (group 64,
+        // f32 scales and biases); any other tensor is read as f16
+        const std::string base = name.size() > 7 && name.compare(name.size() - 7, 7, ".weight") == 0
+                                     ? name.substr(0, name.size() - 7)
+                                     : name;
+        const cellm_file_tensor_t *ts = find(base + ".scales"), *tb = find(base + ".biases");
+        if (dt == "u32" && ts && tb) {
+            const uint64_t groups = (uint64_t)(i + 63) / 64;
+            if (i % 8 != 0 || t->nbytes != (uint64_t)o * i / 2 || ts->nbytes != (uint64_t)o * groups * 4 ||
+                tb->nbytes != (uint64_t)o * groups * 4)
+                return fail(CELLM_HIP_ERR_INVALID_ARG,
+                            "%s: u32 words / f32 scales / biases do not match [%lld, %lld] in groups of 64",
+                            weight_name, o, i);
+            if (int32_t rc = on_device(t, &w)) return rc;
+            if (int32_t rc = on_device(ts, &s)) return rc;
+            if (int32_t rc = on_device(tb, &b)) return rc;
+            return cellm_hip_qgemv_q4_affine(ctx, static_cast<const uint32_t*>(w), s, b, CELLM_HIP_DTYPE_F32, 64, x,
+                                             CELLM_HIP_DTYPE_F32, y, m, out_dim, in_dim, stream);
+        }
+        if (t->nbytes % 2 != 0) return fail(CELLM_HIP_ERR_INVALID_ARG, "tensor %s nbytes not even", weight_name);
+        if (t->nbytes != (uint64_t)o * i * 2)
+            return fail(CELLM_HIP_ERR_INVALID_ARG,
+                        "linear_f16_out_in: weight shape mismatch for %s: got %llu elements, expected %lld (%lldx%lld "
+                        "f16)",
+                        weight_name, (unsigned long long)(t->nbytes / 2), o * i, o, i);
+        if (int32_t rc = on_device(t, &w)) return rc;
+        return cellm_hip_qgemv_f16(ctx, static_cast<const uint16_t*>(w), x, CELLM_HIP_DTYPE_F32, y, m, out_dim,
+                                   in_dim, stream);
+    }
+    if (dt == "f16") {
+        if (int32_t rc = len_check(t, (uint64_t)o * i * 2, (long long)(t->nbytes / 2), o * i)) return rc;
+        if (int32_t rc = on_device(t, &w)) return rc;
+        return cellm_hip_qgemv_f16(ctx, static_cast<const uint16_t*>(w), x, CELLM_HIP_DTYPE_F32, y, m, out_dim,
+                                   in_dim, stream);
+    }
+    if (dt == "i8") {
+        // matmul_i8_f32: the row scale applied to the row sum
+        if (int32_t rc = len_check(t, (uint64_t)o * i, (long long)t->nbytes, o * i)) return rc;
+        if (int32_t rc = qscale(fam != CELLM_HIP_FAMILY_QWEN, &s, &ns)) return rc;
+        if (int32_t rc = on_device(t, &w)) return rc;
+        return cellm_hip_qgemv_i8(ctx, static_cast<const int8_t*>(w), s, CELLM_HIP_DTYPE_F16, out_dim, x,
+                                  CELLM_HIP_DTYPE_F32, nullptr, y, m, out_dim, in_dim, stream);
+    }
+    if (dt == "i4") {
+        // matmul_i4_f32 with gs = in_dim (llama.rs:932, gemma.rs:1471), or one scale per group of
+        // in_dim / (scales per row) when there are more scales than rows (qwen.rs:1076-1077)
+        const uint64_t row_bytes = (uint64_t)(i + 1) / 2;
+        if (int32_t rc = len_check(t, (uint64_t)o * row_bytes, (long long)t->nbytes, o * (long long)row_bytes))
+            return rc;
+        if (int32_t rc = qscale(fam == CELLM_HIP_FAMILY_GEMMA, &s, &ns)) return rc;
+        const int64_t gs = (fam == CELLM_HIP_FAMILY_QWEN && ns > out_dim) ? in_dim / (ns / out_dim) : in_dim;
+        if (gs < 1) return fail(CELLM_HIP_ERR_INVALID_ARG, "weight %s: more scale groups than columns", weight_name);
+        if (int32_t rc = on_device(t, &w)) return rc;
+        return cellm_hip_qgemv_i4_sym(ctx, static_cast<const uint8_t*>(w), static_cast<const uint16_t*>(s), ns, gs,
+                                      x, CELLM_HIP_DTYPE_F32, y, m, out_dim, in_dim, stream);
+    }
+    if (dt == "i2" && fam != CELLM_HIP_FAMILY_LLAMA) {
+        // Qwen's dot_i2_scaled_row scales the row sum (qwen.rs:1591-1606); Gemma's each element
+        // (gemma.rs:1673-1687)
+        if (int32_t rc = len_check(t, (uint64_t)o * ((i + 3) / 4), (long long)t->nbytes, o * ((i + 3) / 4)))
+            return rc;
+        if (int32_t rc = qscale(false, &s, &ns)) return rc;
+        if (int32_t rc = on_device(t, &w)) return rc;
+        return cellm_hip_qgemv_i2(ctx, static_cast<const uint8_t*>(w), static_cast<const uint16_t*>(s),
+                                  fam == CELLM_HIP_FAMILY_GEMMA ? 1 : 0, x, CELLM_HIP_DTYPE_F32, y, m, out_dim, in_dim,
+                                  stream);
+    }
+    if (dt == "q1_0_g128" && fam == CELLM_HIP_FAMILY_QWEN) {
+        // dot_row (qwen.rs:1004-1022): in_dim / 128 blocks of 18 bytes per row
+        if (i % 128 != 0) return fail(CELLM_HIP_ERR_INVALID_ARG, "weight %s: q1_0_g128 needs in %% 128 == 0", weight_name);
+        if (int32_t rc = len_check(t, (uint64_t)o * (i / 128) * 18, (long long)t->nbytes, o * (i / 128) * 18))
+            return rc;
+        if (int32_t rc = on_device(t, &w)) return rc;
+        return cellm_hip_qgemv_q1_0_g128(ctx, static_cast<const uint8_t*>(w), x, CELLM_HIP_DTYPE_F32, y, m, out_dim,
+                                         in_dim, stream);
+    }
+    if (fam == CELLM_HIP_FAMILY_QWEN)  // qwen.rs:1101
+        return fail(CELLM_HIP_ERR_UNSUPPORTED, "linear fallback unsupported dtype %s", dt.c_str());
+    return fail(CELLM_HIP_ERR_UNSUPPORTED, "unsupported weight dtype for %s: %s", weight_name, dt.c_str());
     CELLM_API_END(cellm::report_exception)
 }
 

@@ -486,6 +486,36 @@ int32_t cellm_file_tensor_bytes(const cellm_file_t* f, const char* name, const v
 int32_t cellm_hip_upload_cellm_file(cellm_hip_ctx_t* ctx, const cellm_file_t* f, const char* name_prefix,
                                     int64_t* out_count, size_t* out_bytes);
 
+/* One projection y[m, out] = W x[m, in] (x, y: f32 device arrays) by the dtype
+ * of the .cellm tensor `weight_name` (an exact name, as the runners'
+ * *_by_exact_name lookups take it), with the rules of one runner family's
+ * linear_f16_out_in:
+ *   LLAMA (llama.rs:743-941): 2-D [out, in] check; "f16"; "i8" + f16 .qscale,
+ *         one per row; "i4" + .qscale, gs = in (the row's first scale).
+ *   QWEN  (qwen.rs:1033-1105): "f16"; "i8"; "i4" with gs = in / (scales per
+ *         row) when .qscale holds more than one scale per row;
+ *         "q1_0_g128" (dot_row, :1004-1022); "i2" with the row scale applied
+ *         to the sum (:1591-1606).
+ *   GEMMA (gemma.rs:1358-1499): [out, in] check; "f16"; "i8"; "i4" with
+ *         exactly one scale per row; "i2" with the scale applied per element
+ *         (:1673-1687).
+ *   LFM   (lfm.rs:924-981): "u32" with "<base>.scales" and "<base>.biases"
+ *         (f32, groups of 64) -> MLX affine GEMV; any other tensor is read as
+ *         f16.
+ * Each arm runs the GEMV entry point of its format (cellm_hip_qgemv_*) on
+ * `stream`.  The tensors it reads are uploaded into the context's weight
+ * cache under their file names on the first call (blocking), as MetalOps
+ * caches weights by name (metal.rs:1045-1050); two files with equal tensor
+ * names therefore need two contexts.  Other dtypes and malformed tensors
+ * return CELLM_HIP_ERR_UNSUPPORTED / CELLM_HIP_ERR_INVALID_ARG with the
+ * reference's messages. */
+#define CELLM_HIP_FAMILY_LLAMA 0
+#define CELLM_HIP_FAMILY_QWEN 1
+#define CELLM_HIP_FAMILY_GEMMA 2
+#define CELLM_HIP_FAMILY_LFM 3
+int32_t cellm_hip_linear_file(cellm_hip_ctx_t* ctx, const cellm_file_t* f, const char* weight_name, int32_t family,
+                              const float* x, float* y, int64_t m, int64_t out_dim, int64_t in_dim, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
