@@ -123,16 +123,28 @@ struct DevBuf {
 //       [out, ceil(in/64)] (tools/convert_lfm.py:123-136), group 64;
 //   I4: "i4" [out, in], ceil(in/2) bytes per row, low nibble even, + f16
 //       "<w>.qscale" [out]: one scale per row (gs = in, gemma.rs:1466-1471);
-//   F16: "f16" [out, in], no scale (llama.rs:898 matmul_f16_f32).
+//   F16: "f16" [out, in], no scale (llama.rs:898 matmul_f16_f32);
+//   I2, Q1 (Qwen files only): "i2" [out, in] in ceil(in/4) bytes per row + f16
+//       "<w>.qscale" [out], the scale on the row sum (qwen.rs:1087-1096,
+//       1591-1606); "q1_0_g128" [out, in] in in/128 blocks of 18 bytes
+//       (qwen.rs:1004-1022).
 // The embedding takes one of I8, I4 or F16 (embed_token, llama.rs:676-726), and
 // the tied lm_head is the embedding in the same format (llama.rs:576-646).
-enum ProjKind : int32_t { PK_I8 = 0, PK_Q4 = 1, PK_I4 = 2, PK_F16 = 3 };
+enum ProjKind : int32_t { PK_I8 = 0, PK_Q4 = 1, PK_I4 = 2, PK_F16 = 3, PK_I2 = 4, PK_Q1 = 5 };
+
+// Runner family: LLAMA follows LlamaRunner (llama.rs); QWEN the Qwen2 layers
+// of QwenRunner and its fused Metal step (qwen.rs:309-630, 1255-1470): the same
+// layer with optional f16 biases on every projection, added after it, and
+// Qwen's weight formats.
+enum Family : int32_t { FAM_LLAMA = 0, FAM_QWEN = 1 };
 
 struct Proj {
     int32_t kind = PK_I8;
     const void* w = nullptr;
-    const void* s = nullptr;  // I8/I4: f16 row scales; Q4: f32 group scales; F16: none
+    const void* s = nullptr;  // I8/I4/I2: f16 row scales; Q4: f32 group scales; F16/Q1: none
     const void* b = nullptr;  // Q4: f32 group biases
+    int64_t ns = 0, gs = 0;   // I4: scales in .qscale and the group size they cover
+    const float* bias = nullptr;  // projection bias as f32, repeated for max_rows rows; nullptr: none
 };
 
 // Host-side source of one projection (mapped file bytes or caller memory).
@@ -144,6 +156,9 @@ struct HostProj {
     size_t s_bytes = 0;
     const void* b = nullptr;
     size_t b_bytes = 0;
+    int64_t ns = 0, gs = 0;              // I4: 0 = one scale per row, gs = in
+    const uint16_t* bias_f16 = nullptr;  // [bias_n = out] f16, or nullptr
+    size_t bias_n = 0;
 };
 
 struct HostModel {
@@ -216,22 +231,35 @@ int32_t run_proj(cellm_llama_dev* m, const Proj& pr, const float* x, float* y, i
 {
     cellm_hip_ctx_t* H = m->hip;
     void* S = m->stream;
-    if (pr.kind == PK_I8) {
+    if (pr.kind == PK_I8) {  // the bias rides in the GEMV's epilogue
         LIB_TRY(cellm_hip_qgemv_i8(H, static_cast<const int8_t*>(pr.w), pr.s, CELLM_HIP_DTYPE_F16, out, x,
-                                   CELLM_HIP_DTYPE_F32, nullptr, y, R, out, in, S),
+                                   CELLM_HIP_DTYPE_F32, pr.bias, y, R, out, in, S),
                 what);
-    } else if (pr.kind == PK_Q4) {
+        return CELLM_HIP_OK;
+    }
+    if (pr.kind == PK_Q4) {
         LIB_TRY(cellm_hip_qgemv_q4_affine(H, static_cast<const uint32_t*>(pr.w), pr.s, pr.b, CELLM_HIP_DTYPE_F32, 64,
                                           x, CELLM_HIP_DTYPE_F32, y, R, out, in, S),
                 what);
     } else if (pr.kind == PK_I4) {
-        LIB_TRY(cellm_hip_qgemv_i4_sym(H, static_cast<const uint8_t*>(pr.w), static_cast<const uint16_t*>(pr.s), out,
-                                       in, x, CELLM_HIP_DTYPE_F32, y, R, out, in, S),
+        LIB_TRY(cellm_hip_qgemv_i4_sym(H, static_cast<const uint8_t*>(pr.w), static_cast<const uint16_t*>(pr.s),
+                                       pr.ns ? pr.ns : out, pr.gs ? pr.gs : in, x, CELLM_HIP_DTYPE_F32, y, R, out, in,
+                                       S),
+                what);
+    } else if (pr.kind == PK_I2) {
+        LIB_TRY(cellm_hip_qgemv_i2(H, static_cast<const uint8_t*>(pr.w), static_cast<const uint16_t*>(pr.s), 0, x,
+                                   CELLM_HIP_DTYPE_F32, y, R, out, in, S),
+                what);
+    } else if (pr.kind == PK_Q1) {
+        LIB_TRY(cellm_hip_qgemv_q1_0_g128(H, static_cast<const uint8_t*>(pr.w), x, CELLM_HIP_DTYPE_F32, y, R, out, in,
+                                          S),
                 what);
     } else {
         LIB_TRY(cellm_hip_qgemv_f16(H, static_cast<const uint16_t*>(pr.w), x, CELLM_HIP_DTYPE_F32, y, R, out, in, S),
                 what);
     }
+    // add_projection_bias_if_present (qwen.rs:1132-1139); the bias holds max_rows copies
+    if (pr.bias) LIB_TRY(cellm_hip_add_f32_inplace(H, y, pr.bias, R * out, S), what);
     return CELLM_HIP_OK;
 }
 
@@ -300,9 +328,9 @@ int32_t enqueue_step(cellm_llama_dev* m, int32_t rows)
             const Proj* P = &m->p[l * 7];
             // xn = input_layernorm(x), from the previous layer's residual add (or the embedding)
             if (P[0].kind == PK_I8 && P[1].kind == PK_I8 && P[2].kind == PK_I8) {
-                LIB_TRY(cellm_hip_qgemv_i8_qkv(H, i8w(P[0]), i8s(P[0]), hid, nullptr, i8w(P[1]), i8s(P[1]), kvd,
-                                               nullptr, i8w(P[2]), i8s(P[2]), kvd, nullptr, CELLM_HIP_DTYPE_F16, xn,
-                                               CELLM_HIP_DTYPE_F32, q, k, v, R, hid, kvd, hid, S),
+                LIB_TRY(cellm_hip_qgemv_i8_qkv(H, i8w(P[0]), i8s(P[0]), hid, P[0].bias, i8w(P[1]), i8s(P[1]), kvd,
+                                               P[1].bias, i8w(P[2]), i8s(P[2]), kvd, P[2].bias, CELLM_HIP_DTYPE_F16,
+                                               xn, CELLM_HIP_DTYPE_F32, q, k, v, R, hid, kvd, hid, S),
                         "qkv");
             } else {
                 if (int32_t rc = run_proj(m, P[0], xn, q, R, hid, hid, "q_proj")) return rc;
@@ -320,11 +348,11 @@ int32_t enqueue_step(cellm_llama_dev* m, int32_t rows)
             LIB_TRY(cellm_hip_add_rms_norm(H, x, proj, m->mlp_norm[l], CELLM_HIP_DTYPE_F32, R, hid, eps, xn, S),
                     "residual + post_attention_layernorm");
             if (P[4].kind == PK_I8 && P[5].kind == PK_I8) {
-                LIB_TRY(cellm_hip_qgemv_i8_gate_up_silu(H, i8w(P[4]), i8s(P[4]), inter, nullptr, i8w(P[5]), i8s(P[5]),
-                                                        inter, nullptr, CELLM_HIP_DTYPE_F16, xn, CELLM_HIP_DTYPE_F32,
-                                                        h, R, inter, hid, S),
+                LIB_TRY(cellm_hip_qgemv_i8_gate_up_silu(H, i8w(P[4]), i8s(P[4]), inter, P[4].bias, i8w(P[5]),
+                                                        i8s(P[5]), inter, P[5].bias, CELLM_HIP_DTYPE_F16, xn,
+                                                        CELLM_HIP_DTYPE_F32, h, R, inter, hid, S),
                         "gate/up");
-            } else if (P[4].kind == PK_Q4 && P[5].kind == PK_Q4) {
+            } else if (P[4].kind == PK_Q4 && P[5].kind == PK_Q4 && !P[4].bias && !P[5].bias) {
                 LIB_TRY(cellm_hip_qgemv_q4_affine_gate_up_silu(
                             H, static_cast<const uint32_t*>(P[4].w), P[4].s, P[4].b,
                             static_cast<const uint32_t*>(P[5].w), P[5].s, P[5].b, CELLM_HIP_DTYPE_F32, 64, xn,
@@ -519,20 +547,34 @@ int32_t dev_create_impl(const cellm_llama_config_t* cfg, const HostModel& hm, in
     const size_t hid = (size_t)c.hidden, L = (size_t)c.n_layers;
     // the cache keys follow the .cellm tensor names of each format
     auto upload_proj = [&](const std::string& base, const HostProj& hp, Proj* pr) -> int32_t {
-        if (!hp.w || (hp.kind != PK_F16 && !hp.s) || (hp.kind == PK_Q4 && !hp.b))
+        const bool scaled = hp.kind != PK_F16 && hp.kind != PK_Q1;
+        if (!hp.w || (scaled && !hp.s) || (hp.kind == PK_Q4 && !hp.b))
             return fail(CELLM_HIP_ERR_INVALID_ARG, "%s: weight or scale data missing", base.c_str());
         const void *dw = nullptr, *ds = nullptr, *db = nullptr;
         if (int32_t r = upload(m, base + ".weight", hp.w, hp.w_bytes, &dw)) return r;
         if (hp.kind == PK_Q4) {
             if (int32_t r = upload(m, base + ".scales", hp.s, hp.s_bytes, &ds)) return r;
             if (int32_t r = upload(m, base + ".biases", hp.b, hp.b_bytes, &db)) return r;
-        } else if (hp.kind != PK_F16) {
+        } else if (scaled) {
             if (int32_t r = upload(m, base + ".weight.qscale", hp.s, hp.s_bytes, &ds)) return r;
         }
         pr->kind = hp.kind;
         pr->w = dw;
         pr->s = ds;
         pr->b = db;
+        pr->ns = hp.ns;
+        pr->gs = hp.gs;
+        pr->bias = nullptr;
+        if (hp.bias_f16) {
+            // widened to f32 once at upload (qwen.rs:232-239) and repeated for each of the max_rows rows, so one
+            // elementwise add covers a whole batch
+            std::vector<float> rep((size_t)max_rows * hp.bias_n);
+            for (int32_t r = 0; r < max_rows; ++r)
+                for (size_t j = 0; j < hp.bias_n; ++j) rep[(size_t)r * hp.bias_n + j] = h2f(hp.bias_f16[j]);
+            const void* d = nullptr;
+            if (int32_t r = upload(m, base + ".bias", rep.data(), rep.size() * sizeof(float), &d)) return r;
+            pr->bias = static_cast<const float*>(d);
+        }
         return CELLM_HIP_OK;
     };
     m->p.resize(L * 7);
@@ -541,7 +583,7 @@ int32_t dev_create_impl(const cellm_llama_config_t* cfg, const HostModel& hm, in
         const std::string pre = "model.layers." + std::to_string(l) + ".";
         for (int j = 0; j < 7; ++j) {
             if ((rc = upload_proj(pre + kNames[j], hm.p[l * 7 + j], &m->p[l * 7 + j]))) return bail(rc);
-            all_i8 = all_i8 && hm.p[l * 7 + j].kind == PK_I8;
+            all_i8 = all_i8 && hm.p[l * 7 + j].kind == PK_I8 && !hm.p[l * 7 + j].bias_f16;
         }
         const float *a = nullptr, *b = nullptr;
         if (!hm.n1[l] || !hm.n2[l]) return bail(fail(CELLM_HIP_ERR_INVALID_ARG, "layer %zu norm missing", l));
@@ -655,15 +697,24 @@ int32_t cellm_llama_dev_create_from_file(const char* path, int32_t device, int32
     c.tokens_per_block = tokens_per_block;
     c.total_blocks = total_blocks;
 
-    // detect_llama_prefix (llama.rs:1094-1113)
-    std::string prefix;
-    {
+    // The runner family from the header's model_type, as the SDK picks a runner
+    // (crates/cellm-sdk/src/lib.rs:125-135): "qwen*" runs the Qwen2 layer, anything else the Llama one.
+    const std::string model_type = fc.model_type;
+    const int32_t family = model_type.compare(0, 4, "qwen") == 0 ? FAM_QWEN : FAM_LLAMA;
+    if (family == FAM_QWEN && model_type.find("qwen3_5") != std::string::npos)
+        return fail(CELLM_HIP_ERR_UNSUPPORTED,
+                    "model_type %s (linear-attention layers, offset norms) is not supported by the device step",
+                    model_type.c_str());
+    auto has = [&](const std::string& n) { return cellm_file_find(f, n.c_str(), nullptr) == CELLM_HIP_OK; };
+    // Tensor names are base + "layers.N.…", base + "norm.weight", base + "embed_tokens.weight".
+    std::string base;
+    if (family == FAM_LLAMA) {
+        // detect_llama_prefix (llama.rs:1094-1113)
         bool found = false;
         for (const char* p : {"", "language_model."}) {
-            const std::string e = std::string(p) + "model.embed_tokens.weight", n = std::string(p) + "model.norm.weight";
-            if (cellm_file_find(f, e.c_str(), nullptr) == CELLM_HIP_OK &&
-                cellm_file_find(f, n.c_str(), nullptr) == CELLM_HIP_OK) {
-                prefix = p;
+            const std::string b = std::string(p) + "model.";
+            if (has(b + "embed_tokens.weight") && has(b + "norm.weight")) {
+                base = b;
                 found = true;
                 break;
             }
@@ -671,6 +722,23 @@ int32_t cellm_llama_dev_create_from_file(const char* path, int32_t device, int32
         if (!found)
             return fail(CELLM_HIP_ERR_NOT_FOUND,
                         "missing required llama tensors: model.embed_tokens.weight/model.norm.weight");
+    } else {
+        // the prefix order of QwenRunner::step_inner (qwen.rs:339-342)
+        bool found = false;
+        for (const char* p : {"model.language_model.", "language_model.model.", "model."}) {
+            if (has(std::string(p) + "embed_tokens.weight")) {
+                base = p;
+                found = true;
+                break;
+            }
+        }
+        if (!found) base = "";
+        // per-head q/k RMSNorms (qwen.rs:433-468) sit between the projections and RoPE: not in this step
+        for (int32_t l = 0; l < c.n_layers; ++l)
+            for (const char* nm : {"self_attn.q_norm.weight", "self_attn.k_norm.weight"})
+                if (has(base + "layers." + std::to_string(l) + "." + nm))
+                    return fail(CELLM_HIP_ERR_UNSUPPORTED, "%slayers.%d.%s: q/k norms are not supported by the "
+                                "device step", base.c_str(), l, nm);
     }
     // a tensor of the given dtype and shape ([d0] when d1 < 0) holding `nbytes`, as mapped bytes
     auto tensor = [&](const std::string& name, const char* dtype, int64_t d0, int64_t d1, uint64_t nbytes,
@@ -693,7 +761,7 @@ int32_t cellm_llama_dev_create_from_file(const char* path, int32_t device, int32
     // One projection [o, i] by the dtype of its weight tensor, as the runners'
     // linear_f16_out_in dispatch on it (llama.rs:781-941, lfm.rs:924-981,
     // gemma.rs:1358-1499).
-    auto load_proj = [&](const std::string& w, int64_t o, int64_t i, HostProj* hp) -> int32_t {
+    auto load_proj = [&](const std::string& w, int64_t o, int64_t i, HostProj* hp, bool rows_only) -> int32_t {
         cellm_file_tensor_t t;
         if (cellm_file_find(f, w.c_str(), &t) != CELLM_HIP_OK)
             return fail(CELLM_HIP_ERR_NOT_FOUND, "tensor %s missing", w.c_str());
@@ -721,30 +789,74 @@ int32_t cellm_llama_dev_create_from_file(const char* path, int32_t device, int32
             return tensor(base + ".biases", "f32", o, groups, hp->b_bytes, &hp->b);
         }
         if (strcmp(t.dtype, "i4") == 0) {
-            // [o, i] with ceil(i/2) bytes per row (i4_packed_nbytes_for_shape), one f16 scale per row
+            // [o, i] with ceil(i/2) bytes per row (i4_packed_nbytes_for_shape) and f16 .qscale.  Per row
+            // (rows_only, the embedding and lm_head loops read scales[row]) or as matmul_i4_f32 reads
+            // them for a projection: spr = count / o scales per row, gs = i for Llama (llama.rs:932, the
+            // row's first scale) and i / spr for Qwen when spr > 1 (qwen.rs:1076-1077).
             hp->kind = PK_I4;
             hp->w_bytes = (size_t)(o * ((i + 1) / 2));
-            hp->s_bytes = (size_t)o * 2;
             if (int32_t rc = tensor(w, "i4", o, i, hp->w_bytes, &hp->w)) return rc;
-            return tensor(w + ".qscale", "f16", o, -1, hp->s_bytes, &hp->s);
+            cellm_file_tensor_t st;
+            const std::string sn = w + ".qscale";
+            if (cellm_file_find(f, sn.c_str(), &st) != CELLM_HIP_OK)
+                return fail(CELLM_HIP_ERR_NOT_FOUND, "tensor %s missing", sn.c_str());
+            const int64_t count = (int64_t)(st.nbytes / 2);
+            if (strcmp(st.dtype, "f16") != 0 || count < o || count % o != 0 || (rows_only && count != o))
+                return fail(CELLM_HIP_ERR_INVALID_ARG, "tensor %s: %lld f16 scales for %lld rows", sn.c_str(),
+                            (long long)count, (long long)o);
+            const int64_t spr = count / o;
+            hp->ns = count;
+            hp->gs = (family == FAM_QWEN && spr > 1) ? i / spr : i;
+            if (hp->gs < 1 || (i - 1) / hp->gs >= spr)
+                return fail(CELLM_HIP_ERR_INVALID_ARG, "tensor %s: %lld scales per row do not cover %lld columns",
+                            sn.c_str(), (long long)spr, (long long)i);
+            hp->s_bytes = (size_t)count * 2;
+            return cellm_file_tensor_bytes(f, sn.c_str(), &hp->s, nullptr) == CELLM_HIP_OK
+                       ? CELLM_HIP_OK
+                       : fail(CELLM_HIP_ERR_INVALID_ARG, "tensor %s unreadable", sn.c_str());
         }
         if (strcmp(t.dtype, "f16") == 0) {
             hp->kind = PK_F16;
             hp->w_bytes = (size_t)(o * i) * 2;
             return tensor(w, "f16", o, i, hp->w_bytes, &hp->w);
         }
-        return fail(CELLM_HIP_ERR_UNSUPPORTED,
-                    "tensor %s is %s; the device step takes i8, u32 (MLX affine), i4 or f16", w.c_str(), t.dtype);
+        if (family == FAM_QWEN && strcmp(t.dtype, "i2") == 0) {
+            // ceil(i/4) bytes per row, one f16 scale per row on the row sum (qwen.rs:1087-1096)
+            hp->kind = PK_I2;
+            hp->w_bytes = (size_t)(o * ((i + 3) / 4));
+            hp->s_bytes = (size_t)o * 2;
+            if (int32_t rc = tensor(w, "i2", o, i, hp->w_bytes, &hp->w)) return rc;
+            return tensor(w + ".qscale", "f16", o, -1, hp->s_bytes, &hp->s);
+        }
+        if (family == FAM_QWEN && strcmp(t.dtype, "q1_0_g128") == 0) {
+            // i / 128 blocks of 18 bytes per row (qwen.rs:1004-1022)
+            if (i % 128 != 0)
+                return fail(CELLM_HIP_ERR_INVALID_ARG, "%s: q1_0_g128 needs in %% 128 == 0", w.c_str());
+            hp->kind = PK_Q1;
+            hp->w_bytes = (size_t)(o * (i / 128) * 18);
+            return tensor(w, "q1_0_g128", o, i, hp->w_bytes, &hp->w);
+        }
+        return fail(CELLM_HIP_ERR_UNSUPPORTED, "tensor %s is %s; the device step takes i8, u32 (MLX affine), i4%s",
+                    w.c_str(), t.dtype, family == FAM_QWEN ? ", f16, i2 or q1_0_g128" : " or f16");
     };
     HostModel hm;
     hm.p.resize((size_t)c.n_layers * 7);
     for (int32_t l = 0; l < c.n_layers; ++l) {
-        const std::string pre = prefix + "model.layers." + std::to_string(l) + ".";
+        const std::string pre = base + "layers." + std::to_string(l) + ".";
         for (int j = 0; j < 7; ++j) {
             size_t o, i;
             out_in(c, j, &o, &i);
-            if (int32_t rc = load_proj(pre + kNames[j] + ".weight", (int64_t)o, (int64_t)i, &hm.p[(size_t)l * 7 + j]))
-                return rc;
+            HostProj& hp = hm.p[(size_t)l * 7 + j];
+            if (int32_t rc = load_proj(pre + kNames[j] + ".weight", (int64_t)o, (int64_t)i, &hp, false)) return rc;
+            // Qwen: "<stem>.bias" [out] f16 when present, added after the projection (qwen.rs:1132-1139,
+            // 1361-1363, 1420, 1436-1437, 1457)
+            const std::string bn = pre + kNames[j] + ".bias";
+            if (family == FAM_QWEN && has(bn)) {
+                const void* bp = nullptr;
+                if (int32_t rc = tensor(bn, "f16", (int64_t)o, -1, (uint64_t)o * 2, &bp)) return rc;
+                hp.bias_f16 = static_cast<const uint16_t*>(bp);
+                hp.bias_n = o;
+            }
         }
         const void *n1 = nullptr, *n2 = nullptr;
         if (int32_t rc = tensor(pre + "input_layernorm.weight", "f16", c.hidden, -1, (uint64_t)c.hidden * 2, &n1))
@@ -755,9 +867,10 @@ int32_t cellm_llama_dev_create_from_file(const char* path, int32_t device, int32
         hm.n1.push_back(static_cast<const uint16_t*>(n1));
         hm.n2.push_back(static_cast<const uint16_t*>(n2));
     }
-    // the embedding as embed_token takes it: i8 or i4 with a per-row f16 .qscale, or f16 (llama.rs:676-726)
+    // the embedding as embed_token takes it: i8 or i4 with a per-row f16 .qscale, or f16 (llama.rs:676-726,
+    // qwen.rs:850-918 without its q1_0_g128 and i2 rows)
     {
-        const std::string e = prefix + "model.embed_tokens.weight";
+        const std::string e = base + "embed_tokens.weight";
         cellm_file_tensor_t t;
         if (cellm_file_find(f, e.c_str(), &t) != CELLM_HIP_OK)
             return fail(CELLM_HIP_ERR_NOT_FOUND, "tensor %s missing", e.c_str());
@@ -766,18 +879,25 @@ int32_t cellm_llama_dev_create_from_file(const char* path, int32_t device, int32
             hm.embed.w_bytes = (size_t)c.vocab * c.hidden * 2;
             if (int32_t rc = tensor(e, "f16", c.vocab, c.hidden, hm.embed.w_bytes, &hm.embed.w)) return rc;
         } else if (strcmp(t.dtype, "i8") == 0 || strcmp(t.dtype, "i4") == 0) {
-            if (int32_t rc = load_proj(e, c.vocab, c.hidden, &hm.embed)) return rc;
+            if (int32_t rc = load_proj(e, c.vocab, c.hidden, &hm.embed, true)) return rc;
         } else {
             return fail(CELLM_HIP_ERR_UNSUPPORTED, "unsupported embed dtype for model.embed_tokens.weight: %s",
                         t.dtype);
         }
     }
     const void* fn = nullptr;
-    if (int32_t rc = tensor(prefix + "model.norm.weight", "f16", c.hidden, -1, (uint64_t)c.hidden * 2, &fn)) return rc;
-    // lm_head.weight when the file has one, else the tied embedding (llama.rs:522-532)
-    for (const std::string& name : {prefix + "lm_head.weight", std::string("lm_head.weight")}) {
-        if (cellm_file_find(f, name.c_str(), nullptr) != CELLM_HIP_OK) continue;
-        if (int32_t rc = load_proj(name, c.vocab, c.hidden, &hm.lm)) return rc;
+    if (int32_t rc = tensor(base + "norm.weight", "f16", c.hidden, -1, (uint64_t)c.hidden * 2, &fn)) return rc;
+    // lm_head.weight when the file has one, else the tied embedding (llama.rs:522-532; Qwen resolves the name
+    // through its prefixes, qwen.rs:577 and :1560-1570)
+    const std::string llama_prefix = family == FAM_LLAMA ? base.substr(0, base.size() - 6) : std::string();
+    const std::vector<std::string> lm_names =
+        family == FAM_LLAMA ? std::vector<std::string>{llama_prefix + "lm_head.weight", "lm_head.weight"}
+                            : std::vector<std::string>{"lm_head.weight", "model.lm_head.weight",
+                                                       "language_model.model.lm_head.weight",
+                                                       "model.language_model.lm_head.weight"};
+    for (const std::string& name : lm_names) {
+        if (!has(name)) continue;
+        if (int32_t rc = load_proj(name, c.vocab, c.hidden, &hm.lm, true)) return rc;
         break;
     }
     hm.final_norm = static_cast<const uint16_t*>(fn);

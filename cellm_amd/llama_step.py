@@ -143,11 +143,12 @@ class LlamaDevice:
     @classmethod
     def from_file(cls, path, device: int = 0, max_rows: int = 4, max_blocks: int = 64, tokens_per_block: int = 16,
                   total_blocks: int | None = None) -> "LlamaDevice":
-        """A runner over a .cellm Llama model (cellm_llama_dev_create_from_file): projections stored as
-        "i8" (+ .qscale), "u32" MLX affine (+ f32 .scales/.biases), "i4" (+ .qscale) or "f16"; the
-        embedding (and tied lm_head) as "i8" / "i4" (+ .qscale) or "f16"; the shape comes from the
-        file's header, the paged K/V cache from the arguments (total_blocks defaults to
-        max_rows * max_blocks)."""
+        """A runner over a .cellm Llama or Qwen2 model (cellm_llama_dev_create_from_file; the header's
+        model_type "qwen*" selects the Qwen2 layer with its optional projection biases): projections
+        stored as "i8" (+ .qscale), "u32" MLX affine (+ f32 .scales/.biases), "i4" (+ .qscale) or
+        "f16", and for Qwen also "i2" (+ .qscale) and "q1_0_g128"; the embedding (and tied lm_head) as
+        "i8" / "i4" (+ .qscale) or "f16"; the shape comes from the file's header, the paged K/V cache
+        from the arguments (total_blocks defaults to max_rows * max_blocks)."""
         from .cellm_file import CellmFile
 
         with CellmFile(path) as f:

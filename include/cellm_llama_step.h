@@ -98,27 +98,39 @@ int32_t cellm_llama_dev_create(const cellm_llama_config_t* cfg, const cellm_llam
                                cellm_llama_dev_t** out);
 
 /* The same runner from a .cellm file (LlamaRunner::load, llama.rs:39-75): the
- * model shape from the header (head_dim defaults to hidden / heads), the
- * tensor prefix "" or "language_model." (detect_llama_prefix,
- * llama.rs:1094-1113), f16 norms, and each projection dispatched on the dtype
- * of its weight tensor as the runners' linear_f16_out_in does (llama.rs:781-941,
- * lfm.rs:924-981, gemma.rs:1358-1499):
+ * model shape from the header (head_dim defaults to hidden / heads), f16
+ * norms, and each projection dispatched on the dtype of its weight tensor as
+ * the runners' linear_f16_out_in does (llama.rs:781-941, lfm.rs:924-981,
+ * gemma.rs:1358-1499):
  *   "i8"  [out, in] + f16 "<w>.qscale" [out]            -> cellm_hip_qgemv_i8;
  *   "u32" [out, in/8] MLX affine words + f32 "<base>.scales" / "<base>.biases"
  *         [out, ceil(in/64)] (tools/convert_lfm.py:123-136)
  *                                                        -> cellm_hip_qgemv_q4_affine;
- *   "i4"  [out, in] (ceil(in/2) bytes per row) + f16 "<w>.qscale" [out]
- *         (one scale per row, gs = in, gemma.rs:1466-1471)
+ *   "i4"  [out, in] (ceil(in/2) bytes per row) + f16 "<w>.qscale", one or more
+ *         scales per row; Llama reads each row's first (gs = in, llama.rs:932)
  *                                                        -> cellm_hip_qgemv_i4_sym;
  *   "f16" [out, in] (llama.rs:898)                       -> cellm_hip_qgemv_f16.
- * model.embed_tokens.weight is "i8" or "i4" (+ f16 .qscale per row) or "f16"
- * (embed_token, llama.rs:676-726) -> cellm_hip_embed_i8 / _i4 / _f16, and is
- * the lm_head, read through the GEMV of its format, unless the file has an
- * lm_head.weight (in any of the four formats, llama.rs:522-646).  Other dtypes
- * are CELLM_HIP_ERR_UNSUPPORTED.  A model whose projections are all "i8" runs the
- * fused decode launches; any other mix runs one launch per projection.
- * tokens_per_block / total_blocks size the paged K/V cache; the file is
- * closed before this returns. */
+ * The header's model_type picks the layer (crates/cellm-sdk/src/lib.rs:125-135):
+ *   "qwen*": the Qwen2 layer of QwenRunner and its fused Metal step
+ *     (qwen.rs:309-630, 1255-1470): tensor prefix "model.language_model.",
+ *     "language_model.model.", "model." or "" (qwen.rs:339-342); an optional
+ *     f16 "<stem>.bias" [out] on any projection, added after it
+ *     (qwen.rs:1132-1139); i4 with s scales per row in groups of in / s
+ *     (qwen.rs:1076-1077); also "i2" [out, in] + f16 .qscale [out], the scale
+ *     on the row sum (qwen.rs:1087-1096) -> cellm_hip_qgemv_i2, and
+ *     "q1_0_g128" (qwen.rs:1004-1022) -> cellm_hip_qgemv_q1_0_g128.  q/k norms
+ *     (Qwen3) and model_type qwen3_5 are CELLM_HIP_ERR_UNSUPPORTED.
+ *   anything else: the Llama layer, prefix "" or "language_model." before
+ *     "model." (detect_llama_prefix, llama.rs:1094-1113).
+ * The embedding is "i8" or "i4" (+ f16 .qscale, one per row) or "f16"
+ * (embed_token, llama.rs:676-726, qwen.rs:850-918) -> cellm_hip_embed_i8 /
+ * _i4 / _f16, and is the lm_head, read through the GEMV of its format, unless
+ * the file has an lm_head.weight (llama.rs:522-646, qwen.rs:575-630).  Other
+ * dtypes are CELLM_HIP_ERR_UNSUPPORTED.  A model whose projections are all
+ * "i8" without biases runs the fused decode launches; any other mix runs one
+ * launch per projection (the int8 QKV and gate/up pairs as one launch each,
+ * biases in their epilogue).  tokens_per_block / total_blocks size the paged
+ * K/V cache; the file is closed before this returns. */
 int32_t cellm_llama_dev_create_from_file(const char* path, int32_t device, int32_t max_rows, int32_t max_blocks,
                                          int32_t tokens_per_block, int32_t total_blocks, cellm_llama_dev_t** out);
 
