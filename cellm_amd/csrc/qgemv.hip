@@ -1445,12 +1445,17 @@ hipError_t launch_i8_xt(const int8_t* w, const void* S, int sdt, int per_channel
     const dim3 grid((N + rows_per_block - 1) / rows_per_block);
     const u4_t* w4 = reinterpret_cast<const u4_t*>(w);
     const size_t lds = XT == DT_F16 ? (size_t)MT * CPR * 8 * 4 + (size_t)MT * CPR * 4 : (size_t)MT * K * 4;
-    if (CPR > kUnroll * LPR)
-        hipLaunchKernelGGL((qgemv_i8_kernel<LPR, R, MT, XT, true>), grid, dim3(kBlock), lds, st, w4, S, sdt,
-                           per_channel, x, bias, y, M, N, K);
-    else
-        hipLaunchKernelGGL((qgemv_i8_kernel<LPR, R, MT, XT, false>), grid, dim3(kBlock), lds, st, w4, S, sdt,
-                           per_channel, x, bias, y, M, N, K);
+    if (CPR > kUnroll * LPR) {
+        auto kern = qgemv_i8_kernel<LPR, R, MT, XT, true>;
+        if (lds > 64 * 1024)
+            if (hipError_t e = allow_big_lds(kern, (int)lds); e != hipSuccess) return e;
+        hipLaunchKernelGGL(kern, grid, dim3(kBlock), lds, st, w4, S, sdt, per_channel, x, bias, y, M, N, K);
+    } else {
+        auto kern = qgemv_i8_kernel<LPR, R, MT, XT, false>;
+        if (lds > 64 * 1024)
+            if (hipError_t e = allow_big_lds(kern, (int)lds); e != hipSuccess) return e;
+        hipLaunchKernelGGL(kern, grid, dim3(kBlock), lds, st, w4, S, sdt, per_channel, x, bias, y, M, N, K);
+    }
     return hipGetLastError();
 }
 
@@ -1775,8 +1780,9 @@ hipError_t launch_qgemv_i8(const int8_t* w, const void* S, int sdt, int per_chan
 {
     const int MT = M <= 1 ? 1 : (M <= 2 ? 2 : 4);
     const size_t lds = xdt == DT_F16 ? (size_t)MT * (K >> 4) * 36 : (size_t)MT * K * 4;
+    // x past 64 KB of LDS (f32 x of long rows at M > 1) takes the per-kernel limit raised to 160 KB
     const bool fast = !force_generic && (xdt == DT_F16 || xdt == DT_F32) && M <= 4 && (K % 16) == 0 &&
-                      aligned16(w) && aligned16(x) && lds <= 64 * 1024;
+                      aligned16(w) && aligned16(x) && lds <= 160 * 1024;
     if (fast) {
         const GemvShape sh = pick_shape(K >> 4, N, false);
         if (M == 1) return launch_i8_lpr<1, 1>(sh.lpr, xdt, w, S, sdt, per_channel, x, bias, y, M, N, K, st);

@@ -227,6 +227,18 @@ def test_i8_bias_and_per_tensor_scale(ops):
         ops.encode_qgemv_i8(_t(w), _t(s[:2].copy()), _t(x), yt)
 
 
+@pytest.mark.parametrize("k,m", [(6912, 4), (4864, 4), (10240, 3), (6912, 2)])
+def test_i8_gemv_f32x_long_rows(ops, k, m):
+    """f32 activations of long rows at M > 1 (the device runner's down_proj at Gemma-3-1B and Qwen2.5
+    widths): x takes more than 64 KB of LDS, so the team kernel runs with the per-kernel limit
+    raised (up to 160 KB: K <= 10240 at four rows)."""
+    n = 1152
+    w, s, x = make_i8(n, k, m, cfg=5, x_dtype=np.float32, salt=k + m)
+    y = _run_i8(ops, w, s, x)
+    ref = oracle.qgemv_i8(w, s, x)
+    assert rel_err(y, ref) <= TOL_F32
+
+
 def test_i8_ragged_k(ops):
     k, n = 40, 19  # k % 16 != 0 -> generic kernel
     w, s, x = make_i8(n, k, 1, salt=9)
