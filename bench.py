@@ -459,6 +459,8 @@ def extra_configs(torch, ops, stream, gen, graphs: bool = True):
     progress("configs[0] and configs[2] done")
     res.update(decode_step_cfg5(graphs))
     progress("configs[4] decode step done")
+    res.update(decode_step_cfg2_qwen(graphs))
+    progress("configs[4] decode step done")
     res.update(lowbit_gemvs(torch, ops, stream, gen))
     res.update(i4_gemma_mlp(torch, ops, stream, gen))
     res.update(q4_gate_up_silu(torch, ops, stream, gen))
@@ -766,6 +768,92 @@ def decode_step_cfg5(graphs: bool = True):
                 entry["eager_us_per_step"] = round(us, 1)
         res[f"cfg5_llama360m_i8_decode_step_{rows}sessions"] = entry
     dev.close()
+    return res
+
+
+def decode_step_cfg2_qwen(graphs: bool = True):
+    """configs[1]'s projections inside a model: a random-init Qwen2.5-0.5B-shape decode step on the
+    device runner (cellm_llama_dev_create_from_file, model_type "qwen2"): 24 layers, hidden 896, 14/2
+    heads of 64, intermediate 4864, vocabulary 151936; every projection and the untied lm_head MLX
+    4-bit affine (u32 words, f32 scales and biases per group of 64, the .cellm layout
+    tools/convert_lfm.py writes), f16 q/k/v biases, int8 embedding; 1 and 4 sessions at context 512
+    of seeded f16 K/V.  The file is written to a temporary directory and removed.  Timed as the
+    configs[4] step; bytes per step: every weight, scale and bias once plus each session's K/V."""
+    import tempfile
+
+    import numpy as np
+
+    from cellm_amd.cellm_file import llama_header, write_cellm
+    from cellm_amd.llama_step import LlamaDevice
+
+    L, H, NH, NKV, HD, I, V = 24, 896, 14, 2, 64, 4864, 151936
+    sessions, ctx, tpb = 4, 512, 16
+    kvd = NKV * HD
+    rng = np.random.default_rng(0xC2)
+    names = ("self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj", "mlp.gate_proj",
+             "mlp.up_proj", "mlp.down_proj")
+    shapes = [(H, H), (kvd, H), (kvd, H), (H, H), (I, H), (I, H), (H, I)]
+
+    def q4(name, o, i):
+        # zero-mean weights of std ~1/sqrt(i): q*s + b with s ~ U(0.5,1.5)/(4.6 sqrt(i)), b ~ -7.5 s
+        wq = rng.integers(0, 2**32, (o, i // 8), dtype=np.uint32)
+        sc = (rng.uniform(0.5, 1.5, (o, i // 64)) / (4.6 * np.sqrt(i))).astype(np.float32)
+        bi = (-7.5 * sc).astype(np.float32)
+        base = name[:-len(".weight")]
+        return [(name, wq, "u32", wq.shape), (base + ".scales", sc, "f32", sc.shape), (base + ".biases", bi, "f32", bi.shape)]
+
+    ts, wbytes = [], 0
+    for l in range(L):
+        pre = f"model.layers.{l}."
+        for j, (o, i) in enumerate(shapes):
+            ts += q4(pre + names[j] + ".weight", o, i)
+            if j < 3:
+                ts.append((pre + names[j] + ".bias", rng.standard_normal(o).astype(np.float16), "f16", (o,)))
+        for nm in ("input_layernorm.weight", "post_attention_layernorm.weight"):
+            ts.append((pre + nm, (1.0 + 0.1 * rng.standard_normal(H)).astype(np.float16), "f16", (H,)))
+    ts.append(("model.embed_tokens.weight", rng.integers(-127, 128, (V, H), dtype=np.int8), "i8", (V, H)))
+    ts.append(("model.embed_tokens.weight.qscale", (rng.uniform(0.5, 1.5, V) / 127.0).astype(np.float16), "f16", (V,)))
+    ts.append(("model.norm.weight", (1.0 + 0.1 * rng.standard_normal(H)).astype(np.float16), "f16", (H,)))
+    ts += q4("lm_head.weight", V, H)
+    # bytes a step reads: every projection and lm_head tensor, biases and norms, one embedding row per session
+    wbytes = sum(a.nbytes for n, a, _, _ in ts if not n.startswith("model.embed_tokens"))
+    res = {}
+    with tempfile.TemporaryDirectory() as tmp:
+        path = Path(tmp) / "qwen25_05b_q4.cellm"
+        write_cellm(path, llama_header(L, H, NH, NKV, I, V, eps=1e-6, theta=1000000.0, model_type="qwen2",
+                                       tie_word_embeddings=False), ts)
+        del ts
+        dev = LlamaDevice.from_file(path, 0, max_rows=sessions, max_blocks=ctx // tpb, tokens_per_block=tpb)
+    try:
+        kv = dev.shape.kv_elems()
+        dev.kv_upload(rng.standard_normal(kv, dtype=np.float32).astype(np.float16),
+                      rng.standard_normal(kv, dtype=np.float32).astype(np.float16))
+        bts = np.array([[b * sessions + s for b in range(ctx // tpb)] for s in range(sessions)], np.uint32)
+        for rows in (sessions, 1):
+            tokens = np.array([(1000 + 7919 * s) % V for s in range(rows)], np.uint32)
+            pos = np.full(rows, ctx - 1, np.int32)
+            step_bytes = wbytes + rows * (H + 2) + rows * ctx * L * kvd * 2 * 2
+            entry = {"sessions": rows, "context": ctx, "bytes_per_step": step_bytes,
+                     "weights": "u32 MLX affine g64, f32 scales/biases; f16 q/k/v biases; int8 embedding",
+                     "launch": "captured HIP graph" if graphs else "eager launches"}
+            for replay in ((True, False) if graphs else (False,)):
+                dev.set_graphs(replay)
+                for _ in range(3):
+                    dev.step(tokens, pos, bts[:rows])
+                n = 50
+                t0 = time.perf_counter()
+                for _ in range(n):
+                    dev.step(tokens, pos, bts[:rows])
+                us = (time.perf_counter() - t0) / n * 1e6
+                if replay or not graphs:
+                    entry.update({"us_per_step": round(us, 1), "tokens_per_s": round(rows * 1e6 / us, 1),
+                                  "GB/s": round(step_bytes / (us * 1e-6) / 1e9, 1),
+                                  "frac_hbm": round(step_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+                else:
+                    entry["eager_us_per_step"] = round(us, 1)
+            res[f"cfg2_qwen25_05b_q4_decode_step_{rows}sessions"] = entry
+    finally:
+        dev.close()
     return res
 
 

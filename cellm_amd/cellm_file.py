@@ -6,11 +6,14 @@ of the header, `.tensors` the tensor index in header order, `.tensor_bytes`
 returns a zero-copy numpy view of the mapped bytes, `.upload(ops)` puts
 the tensors into a HipOps context's name-keyed device weight cache, and
 `.linear(ops, name, family, x, y)` runs one projection by the dtype of its
-weight tensor under a runner family's dispatch rules.
+weight tensor under a runner family's dispatch rules.  `write_cellm` writes a
+file in the same layout (synthetic models for tests and bench.py).
 """
 from __future__ import annotations
 
 import ctypes as C
+import json
+import struct
 from dataclasses import dataclass
 
 import numpy as np
@@ -164,3 +167,60 @@ class CellmFile:
 
     def __del__(self):
         self.close()
+
+
+def write_cellm(path, header: dict, tensors, version: int = 1, magic: bytes = b"CELLM") -> dict:
+    """Writes a .cellm file in the layout the reference's writers use (tools/convert_lfm.py:15-90):
+    the magic, a version byte, the u32 little-endian header length, the JSON header (the given
+    fields plus the tensor index), then each tensor at an absolute, 64-byte aligned offset, in
+    name order.  tensors: (name, array, dtype string, shape) with the array's bytes written as
+    they are; returns the header written.  Tensors are written one at a time (no copy of the
+    whole model is held)."""
+    items = sorted(tensors, key=lambda t: t[0])
+    sizes = {name: int(np.asarray(a).nbytes) for name, a, _, _ in items}
+
+    def layout(hlen):
+        off = (10 + hlen + 63) & ~63
+        offs = {}
+        for name, _, _, _ in items:
+            off = (off + 63) & ~63
+            offs[name] = off
+            off += sizes[name]
+        return offs
+
+    def build(offs):
+        h = dict(header)
+        h["tensors"] = [{"name": n, "offset_bytes": offs[n], "nbytes": sizes[n], "shape": list(shape),
+                         "dtype": dt} for n, _, dt, shape in items]
+        return h, json.dumps(h).encode()
+
+    offs = layout(0)
+    for _ in range(4):  # offsets depend on the header length and vice versa: iterate to a fixed point
+        h, text = build(offs)
+        new = layout(len(text))
+        if new == offs:
+            break
+        offs = new
+    h, text = build(offs)
+    with open(path, "wb") as f:
+        f.write(magic)
+        f.write(struct.pack("<B", version))
+        f.write(struct.pack("<I", len(text)))
+        f.write(text)
+        for name, a, _, _ in items:
+            pos = f.tell()
+            f.write(b"\0" * (offs[name] - pos))
+            f.write(np.ascontiguousarray(a).tobytes())
+    return h
+
+
+def llama_header(n_layers, hidden, heads, kv_heads, inter, vocab, eps=1e-5, theta=100000.0, head_dim=None,
+                 **extra) -> dict:
+    """The model fields of a .cellm header (CellmHeader, crates/cellm-model/src/cellm_file.rs:20-48) for a
+    Llama-layout model; `extra` adds or overrides fields (model_type, tie_word_embeddings, ...)."""
+    h = {"model_type": "llama", "vocab_size": vocab, "hidden_dim": hidden, "intermediate_size": inter,
+         "num_layers": n_layers, "num_heads": heads, "num_kv_heads": kv_heads, "head_dim": head_dim,
+         "rms_norm_eps": eps, "rope_theta": theta, "bos_token_id": 1, "eos_token_id": 2,
+         "tie_word_embeddings": True, "source_quantization": None}
+    h.update(extra)
+    return h

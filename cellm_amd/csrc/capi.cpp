@@ -381,7 +381,8 @@ int32_t gate_up_q4_impl(cellm_hip_ctx* ctx, const uint32_t* wg, const void* sg, 
     if (k > 0 && (!wg || !sg || !bg || !wu || !su || !bu || !x))
         return set_error(CELLM_HIP_ERR_INVALID_ARG, "null input pointer");
     if (qgemv_q4_gate_up_supported(xdt, (int)m, (int)k, (int)group, x, wg, wu)) {
-        HIP_TRY(launch_qgemv_q4_gate_up_silu(wg, sg, bg, wu, su, bu, sbt, (int)group, x, h, (int)m, (int)n, (int)k, st),
+        HIP_TRY(launch_qgemv_q4_gate_up_silu(wg, sg, bg, wu, su, bu, sbt, (int)group, x, xdt, h, (int)m, (int)n, (int)k,
+                                             st),
                 "qgemv_q4_gate_up_silu launch");
         return CELLM_HIP_OK;
     }

@@ -49,7 +49,7 @@ hipError_t launch_qgemv_i8_fused(const I8FusedSeg* segs, int nseg, bool silu, in
 bool qgemv_q4_gate_up_supported(int xdt, int M, int K, int group_size, const void* x, const void* wg, const void* wu);
 hipError_t launch_qgemv_q4_gate_up_silu(const uint32_t* wg, const void* Sg, const void* Bg, const uint32_t* wu,
                                         const void* Su, const void* Bu, int sbt, int group_size, const void* x,
-                                        float* h, int M, int N, int K, hipStream_t st);
+                                        int xdt, float* h, int M, int N, int K, hipStream_t st);
 
 // h[i] = silu(g[i]) * u[i] in place on g (dequant.hip), silu(g) = g / (1 + exp(-g)).
 hipError_t launch_silu_mul(float* g, const float* u, size_t count, hipStream_t st);

@@ -79,6 +79,67 @@ __device__ __forceinline__ void stage_word_q4(u4_t raw, int idx, bool valid, uin
     if (valid && (idx & 3) == 0) cx[idx >> 2] = make_float2(1024.0f * corr, xs);
 }
 
+// f32 activations (the LFM runner's and the .cellm u32 runner's x) as two f16 parts,
+// x = hi + lo with hi = RNE_f16(x) and lo = RNE_f16(x - hi): a nibble value times either
+// part is exact in f32, so the dot over both parts keeps x to about 22 bits where one
+// f16 rounding would keep 11.  Eight f32 values -> the hi pairs at xq, the lo pairs at
+// xq_lo (the layout of stage_word_q4), cx = (1024 * the pairs' sum over both parts, sum of
+// the f32 x) per chunk.
+__device__ __forceinline__ void stage_word_q4_x32(f4_t a, f4_t b, int idx, bool valid, uint32_t* xq, uint32_t* xq_lo,
+                                                  float2* cx)
+{
+    const float xv[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    h8_t hi, lo;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        hi[i] = (_Float16)xv[i];
+        lo[i] = (_Float16)(xv[i] - (float)hi[i]);
+    }
+    const _Float16 inv16 = (_Float16)0.0625f;
+    float corr = 0.0f;
+    auto pack = [&](const h8_t& v, uint32_t* dst) {
+        const h2_t p0 = {v[0], v[4]}, p1 = {v[1] * inv16, v[5] * inv16};
+        const h2_t p2 = {v[2], v[6]}, p3 = {v[3] * inv16, v[7] * inv16};
+        corr += ((float)p0[0] + (float)p0[1]) + ((float)p1[0] + (float)p1[1]) + ((float)p2[0] + (float)p2[1]) +
+                ((float)p3[0] + (float)p3[1]);
+        if (valid) *reinterpret_cast<u4_t*>(dst + (size_t)idx * 4) = u4_t{as_u32(p0), as_u32(p1), as_u32(p2), as_u32(p3)};
+    };
+    pack(hi, xq);
+    pack(lo, xq_lo);
+    float xs = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xs += xv[i];
+    corr = group_sum<4>(corr);
+    xs = group_sum<4>(xs);
+    if (valid && (idx & 3) == 0) cx[idx >> 2] = make_float2(1024.0f * corr, xs);
+}
+
+// All MT * K / 8 words of f32 x -> LDS through stage_word_q4_x32, two 16-byte loads per word, in
+// rounds of XW words per thread whose loads all issue before the round's first store (clamped,
+// branch-free: padding rows and words past `total` read valid data whose results are never stored).
+template <int XW>
+__device__ __forceinline__ void stage_x_q4_x32(const float* __restrict__ x, int M, int K, int total, uint32_t* xq,
+                                               uint32_t* xq_lo, float2* cx)
+{
+    const int words = K >> 3;
+    for (int base = 0; base < total; base += XW * kBlock) {
+        f4_t ra[XW], rb[XW];
+#pragma unroll
+        for (int j = 0; j < XW; ++j) {
+            const int idx = min(base + j * kBlock + (int)threadIdx.x, total - 1);
+            const int m = idx / words;
+            const f4_t* p = reinterpret_cast<const f4_t*>(x + (size_t)min(m, M - 1) * K + (size_t)(idx - m * words) * 8);
+            ra[j] = p[0];
+            rb[j] = p[1];
+        }
+#pragma unroll
+        for (int j = 0; j < XW; ++j) {
+            const int idx = base + j * kBlock + (int)threadIdx.x;
+            stage_word_q4_x32(ra[j], rb[j], idx, idx < total, xq, xq_lo, cx);
+        }
+    }
+}
+
 template <int XW>
 __device__ __forceinline__ void load_x_words(const _Float16* __restrict__ x, int M, int K, int total, u4_t (&xr)[XW])
 {
@@ -139,10 +200,11 @@ __device__ __forceinline__ void load_pass_q4(const u4_t* __restrict__ wq, const 
     }
 }
 
-template <int LPR, int R, int MT, int SBT, int U = kUnroll>
+template <int LPR, int R, int MT, int SBT, int U = kUnroll, bool XS = false>
 __device__ __forceinline__ void compute_pass_q4(int c0, int CPR, const uint32_t* xq, const float2* cx,
                                                 const u4_t (&wv)[U][R], const uint32_t (&sr)[U][R],
-                                                const uint32_t (&br)[U][R], float (&acc)[R][MT])
+                                                const uint32_t (&br)[U][R], float (&acc)[R][MT],
+                                                const uint32_t* xq_lo = nullptr)
 {
     const uint32_t m0f = 0x000F000Fu, m1f = 0x00F000F0u, magic = 0x64006400u;
 #pragma unroll
@@ -179,6 +241,19 @@ __device__ __forceinline__ void compute_pass_q4(int c0, int CPR, const uint32_t*
                     h = w[3] >> 8;
                     d = dot2(and_or(h, m0f, magic), xd[2], d);
                     d = dot2(and_or(h, m1f, magic), xd[3], d);
+                    if constexpr (XS) {
+                        // the low f16 parts of f32 x, same nibbles (the correction in cc.x covers both)
+                        const u4_t* lp = reinterpret_cast<const u4_t*>(xq_lo + ((size_t)m * CPR + c) * 16);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const u4_t xl = lp[e];
+                            d = dot2(and_or(w[e], m0f, magic), xl[0], d);
+                            d = dot2(and_or(w[e], m1f, magic), xl[1], d);
+                            h = w[e] >> 8;
+                            d = dot2(and_or(h, m0f, magic), xl[2], d);
+                            d = dot2(and_or(h, m1f, magic), xl[3], d);
+                        }
+                    }
                     acc[r][m] += raw_to_f32<SBT>(sr[u][r]) * d + raw_to_f32<SBT>(br[u][r]) * cc.y;
                 }
             }
@@ -188,16 +263,18 @@ __device__ __forceinline__ void compute_pass_q4(int c0, int CPR, const uint32_t*
 
 // MP: rows need more than one pass of kUnroll chunks per lane; the next pass
 // is prefetched into a second register set (ping-pong) before the current one
-// is consumed.
-template <int LPR, int R, int MT, int SBT, bool MP>
+// is consumed.  XS: x is f32, staged as hi and lo f16 parts (stage_word_q4_x32)
+// and dotted with both; else x is f16.
+template <int LPR, int R, int MT, int SBT, bool MP, bool XS = false>
 __global__ __launch_bounds__(kBlock) void qgemv_q4_f16x_kernel(
     const u4_t* __restrict__ wq, const void* __restrict__ S, const void* __restrict__ B,
-    const _Float16* __restrict__ x, float* __restrict__ y, int M, int N, int K, int gshift)
+    const void* __restrict__ xv, float* __restrict__ y, int M, int N, int K, int gshift)
 {
     extern __shared__ __align__(16) uint32_t lds[];
     const int CPR = K >> 5;
     uint32_t* xq = lds;
-    float2* cx = reinterpret_cast<float2*>(lds + (size_t)MT * CPR * 16);
+    uint32_t* xq_lo = XS ? lds + (size_t)MT * CPR * 16 : nullptr;
+    float2* cx = reinterpret_cast<float2*>(lds + (size_t)(XS ? 2 : 1) * MT * CPR * 16);
 
     const int team = threadIdx.x / LPR;
     const int lane = threadIdx.x % LPR;
@@ -206,14 +283,19 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_f16x_kernel(
     const int total = MT * (K >> 3);
 
     constexpr int XW = MT == 1 ? 4 : 8;
-    u4_t xr[XW];
-    load_x_words<XW>(x, M, K, total, xr);
-
     u4_t wa[kUnroll][R];
     uint32_t sa[kUnroll][R], ba[kUnroll][R];
-    load_pass_q4<LPR, R, SBT>(wq, S, B, row0, 1, lane, N, CPR, gpr, gshift, wa, sa, ba);
-
-    stage_x_q4<XW>(xr, x, M, K, total, xq, cx);
+    if constexpr (XS) {
+        // the weights first: x is a cache hit after the first blocks, the weights are not
+        load_pass_q4<LPR, R, SBT>(wq, S, B, row0, 1, lane, N, CPR, gpr, gshift, wa, sa, ba);
+        stage_x_q4_x32<XW / 2>(reinterpret_cast<const float*>(xv), M, K, total, xq, xq_lo, cx);
+    } else {
+        const _Float16* x = reinterpret_cast<const _Float16*>(xv);
+        u4_t xr[XW];
+        load_x_words<XW>(x, M, K, total, xr);
+        load_pass_q4<LPR, R, SBT>(wq, S, B, row0, 1, lane, N, CPR, gpr, gshift, wa, sa, ba);
+        stage_x_q4<XW>(xr, x, M, K, total, xq, cx);
+    }
     __syncthreads();
     if (row0 >= N) return;
 
@@ -224,18 +306,18 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_f16x_kernel(
         for (int m = 0; m < MT; ++m) acc[r][m] = 0.0f;
 
     if constexpr (!MP) {
-        compute_pass_q4<LPR, R, MT, SBT>(lane, CPR, xq, cx, wa, sa, ba, acc);
+        compute_pass_q4<LPR, R, MT, SBT, kUnroll, XS>(lane, CPR, xq, cx, wa, sa, ba, acc, xq_lo);
     } else {
         constexpr int P = kUnroll * LPR;
         u4_t wb[kUnroll][R];
         uint32_t sb[kUnroll][R], bb[kUnroll][R];
         for (int c0 = lane; c0 < CPR + lane; c0 += 2 * P) {
             if (c0 - lane + P < CPR) load_pass_q4<LPR, R, SBT>(wq, S, B, row0, 1, c0 + P, N, CPR, gpr, gshift, wb, sb, bb);
-            compute_pass_q4<LPR, R, MT, SBT>(c0, CPR, xq, cx, wa, sa, ba, acc);
+            compute_pass_q4<LPR, R, MT, SBT, kUnroll, XS>(c0, CPR, xq, cx, wa, sa, ba, acc, xq_lo);
             if (c0 - lane + P >= CPR) break;
             if (c0 - lane + 2 * P < CPR)
                 load_pass_q4<LPR, R, SBT>(wq, S, B, row0, 1, c0 + 2 * P, N, CPR, gpr, gshift, wa, sa, ba);
-            compute_pass_q4<LPR, R, MT, SBT>(c0 + P, CPR, xq, cx, wb, sb, bb, acc);
+            compute_pass_q4<LPR, R, MT, SBT, kUnroll, XS>(c0 + P, CPR, xq, cx, wb, sb, bb, acc, xq_lo);
         }
     }
 
@@ -283,16 +365,17 @@ __device__ __forceinline__ void load_pass_q4_gu(const u4_t* __restrict__ wg, con
     }
 }
 
-template <int LPR, int MT, int SBT, bool MP>
+template <int LPR, int MT, int SBT, bool MP, bool XS = false>
 __global__ __launch_bounds__(kBlock) void qgemv_q4_gate_up_silu_kernel(
     const u4_t* __restrict__ wg, const void* __restrict__ Sg, const void* __restrict__ Bg,
     const u4_t* __restrict__ wu, const void* __restrict__ Su, const void* __restrict__ Bu,
-    const _Float16* __restrict__ x, float* __restrict__ h, int M, int N, int K, int gshift)
+    const void* __restrict__ xv, float* __restrict__ h, int M, int N, int K, int gshift)
 {
     extern __shared__ __align__(16) uint32_t lds[];
     const int CPR = K >> 5;
     uint32_t* xq = lds;
-    float2* cx = reinterpret_cast<float2*>(lds + (size_t)MT * CPR * 16);
+    uint32_t* xq_lo = XS ? lds + (size_t)MT * CPR * 16 : nullptr;
+    float2* cx = reinterpret_cast<float2*>(lds + (size_t)(XS ? 2 : 1) * MT * CPR * 16);
 
     const int team = threadIdx.x / LPR;
     const int lane = threadIdx.x % LPR;
@@ -301,12 +384,19 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_gate_up_silu_kernel(
     const int total = MT * (K >> 3);
 
     constexpr int XW = MT == 1 ? 4 : 8;
-    u4_t xr[XW];
-    load_x_words<XW>(x, M, K, total, xr);
     u4_t wa[kUnroll][2];
     uint32_t sa[kUnroll][2], ba[kUnroll][2];
-    load_pass_q4_gu<LPR, SBT>(wg, Sg, Bg, wu, Su, Bu, n, lane, N, CPR, gpr, gshift, wa, sa, ba);
-    stage_x_q4<XW>(xr, x, M, K, total, xq, cx);
+    if constexpr (XS) {
+        // f32 x as hi + lo f16 parts (stage_word_q4_x32); the weights first
+        load_pass_q4_gu<LPR, SBT>(wg, Sg, Bg, wu, Su, Bu, n, lane, N, CPR, gpr, gshift, wa, sa, ba);
+        stage_x_q4_x32<XW / 2>(reinterpret_cast<const float*>(xv), M, K, total, xq, xq_lo, cx);
+    } else {
+        const _Float16* x = reinterpret_cast<const _Float16*>(xv);
+        u4_t xr[XW];
+        load_x_words<XW>(x, M, K, total, xr);
+        load_pass_q4_gu<LPR, SBT>(wg, Sg, Bg, wu, Su, Bu, n, lane, N, CPR, gpr, gshift, wa, sa, ba);
+        stage_x_q4<XW>(xr, x, M, K, total, xq, cx);
+    }
     __syncthreads();
     if (n >= N) return;
 
@@ -316,7 +406,7 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_gate_up_silu_kernel(
 #pragma unroll
         for (int m = 0; m < MT; ++m) acc[r][m] = 0.0f;
     if constexpr (!MP) {
-        compute_pass_q4<LPR, 2, MT, SBT>(lane, CPR, xq, cx, wa, sa, ba, acc);
+        compute_pass_q4<LPR, 2, MT, SBT, kUnroll, XS>(lane, CPR, xq, cx, wa, sa, ba, acc, xq_lo);
     } else {
         constexpr int P = kUnroll * LPR;
         u4_t wb[kUnroll][2];
@@ -324,11 +414,11 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_gate_up_silu_kernel(
         for (int c0 = lane; c0 < CPR + lane; c0 += 2 * P) {
             if (c0 - lane + P < CPR)
                 load_pass_q4_gu<LPR, SBT>(wg, Sg, Bg, wu, Su, Bu, n, c0 + P, N, CPR, gpr, gshift, wb, sb, bb);
-            compute_pass_q4<LPR, 2, MT, SBT>(c0, CPR, xq, cx, wa, sa, ba, acc);
+            compute_pass_q4<LPR, 2, MT, SBT, kUnroll, XS>(c0, CPR, xq, cx, wa, sa, ba, acc, xq_lo);
             if (c0 - lane + P >= CPR) break;
             if (c0 - lane + 2 * P < CPR)
                 load_pass_q4_gu<LPR, SBT>(wg, Sg, Bg, wu, Su, Bu, n, c0 + 2 * P, N, CPR, gpr, gshift, wa, sa, ba);
-            compute_pass_q4<LPR, 2, MT, SBT>(c0 + P, CPR, xq, cx, wb, sb, bb, acc);
+            compute_pass_q4<LPR, 2, MT, SBT, kUnroll, XS>(c0 + P, CPR, xq, cx, wb, sb, bb, acc, xq_lo);
         }
     }
 #pragma unroll
@@ -1395,44 +1485,44 @@ GemvShape pick_shape(int cpr, int n_rows, bool q4)
     return {best, 1};
 }
 
-template <int LPR, int R, int MT, bool MP>
-hipError_t launch_q4_f16x_sbt(int sbt, const uint32_t* wq, const void* S, const void* B, const _Float16* x, float* y,
+template <int LPR, int R, int MT, bool MP, bool XS>
+hipError_t launch_q4_f16x_sbt(int sbt, const uint32_t* wq, const void* S, const void* B, const void* x, float* y,
                               int M, int N, int K, int gshift, hipStream_t st)
 {
     const int CPR = K >> 5;
-    const size_t lds = (size_t)MT * CPR * 16 * 4 + (size_t)MT * CPR * 8;
+    const size_t lds = (size_t)(XS ? 2 : 1) * MT * CPR * 16 * 4 + (size_t)MT * CPR * 8;
     const int rows_per_block = (kBlock / LPR) * R;
     const dim3 grid((N + rows_per_block - 1) / rows_per_block);
     const u4_t* w4 = reinterpret_cast<const u4_t*>(wq);
-    if (sbt == DT_F16)
-        hipLaunchKernelGGL((qgemv_q4_f16x_kernel<LPR, R, MT, DT_F16, MP>), grid, dim3(kBlock), lds, st, w4, S, B, x, y,
-                           M, N, K, gshift);
-    else if (sbt == DT_F32)
-        hipLaunchKernelGGL((qgemv_q4_f16x_kernel<LPR, R, MT, DT_F32, MP>), grid, dim3(kBlock), lds, st, w4, S, B, x, y,
-                           M, N, K, gshift);
-    else
-        hipLaunchKernelGGL((qgemv_q4_f16x_kernel<LPR, R, MT, DT_BF16, MP>), grid, dim3(kBlock), lds, st, w4, S, B, x,
-                           y, M, N, K, gshift);
-    return hipGetLastError();
+    auto go = [&](auto kern) {
+        if (lds > 64 * 1024)
+            if (hipError_t e = allow_big_lds(kern, (int)lds); e != hipSuccess) return e;
+        hipLaunchKernelGGL(kern, grid, dim3(kBlock), lds, st, w4, S, B, x, y, M, N, K, gshift);
+        return hipGetLastError();
+    };
+    if (sbt == DT_F16) return go(qgemv_q4_f16x_kernel<LPR, R, MT, DT_F16, MP, XS>);
+    if (sbt == DT_F32) return go(qgemv_q4_f16x_kernel<LPR, R, MT, DT_F32, MP, XS>);
+    return go(qgemv_q4_f16x_kernel<LPR, R, MT, DT_BF16, MP, XS>);
 }
 
-template <int LPR, int R, int MT>
-hipError_t launch_q4_f16x_mp(int sbt, const uint32_t* wq, const void* S, const void* B, const _Float16* x, float* y,
+template <int LPR, int R, int MT, bool XS>
+hipError_t launch_q4_f16x_mp(int sbt, const uint32_t* wq, const void* S, const void* B, const void* x, float* y,
                              int M, int N, int K, int gshift, hipStream_t st)
 {
-    if ((K >> 5) > kUnroll * LPR) return launch_q4_f16x_sbt<LPR, R, MT, true>(sbt, wq, S, B, x, y, M, N, K, gshift, st);
-    return launch_q4_f16x_sbt<LPR, R, MT, false>(sbt, wq, S, B, x, y, M, N, K, gshift, st);
+    if ((K >> 5) > kUnroll * LPR)
+        return launch_q4_f16x_sbt<LPR, R, MT, true, XS>(sbt, wq, S, B, x, y, M, N, K, gshift, st);
+    return launch_q4_f16x_sbt<LPR, R, MT, false, XS>(sbt, wq, S, B, x, y, M, N, K, gshift, st);
 }
 
-template <int R, int MT>
-hipError_t launch_q4_f16x_lpr(int lpr, int sbt, const uint32_t* wq, const void* S, const void* B, const _Float16* x,
+template <int R, int MT, bool XS = false>
+hipError_t launch_q4_f16x_lpr(int lpr, int sbt, const uint32_t* wq, const void* S, const void* B, const void* x,
                               float* y, int M, int N, int K, int gshift, hipStream_t st)
 {
     switch (lpr) {
-    case 8: return launch_q4_f16x_mp<8, R, MT>(sbt, wq, S, B, x, y, M, N, K, gshift, st);
-    case 16: return launch_q4_f16x_mp<16, R, MT>(sbt, wq, S, B, x, y, M, N, K, gshift, st);
-    case 32: return launch_q4_f16x_mp<32, R, MT>(sbt, wq, S, B, x, y, M, N, K, gshift, st);
-    default: return launch_q4_f16x_mp<64, R, MT>(sbt, wq, S, B, x, y, M, N, K, gshift, st);
+    case 8: return launch_q4_f16x_mp<8, R, MT, XS>(sbt, wq, S, B, x, y, M, N, K, gshift, st);
+    case 16: return launch_q4_f16x_mp<16, R, MT, XS>(sbt, wq, S, B, x, y, M, N, K, gshift, st);
+    case 32: return launch_q4_f16x_mp<32, R, MT, XS>(sbt, wq, S, B, x, y, M, N, K, gshift, st);
+    default: return launch_q4_f16x_mp<64, R, MT, XS>(sbt, wq, S, B, x, y, M, N, K, gshift, st);
     }
 }
 
@@ -1516,35 +1606,36 @@ hipError_t launch_i8_fused_xt(int lpr, const I8Segs& t, int total_rows, int sdt,
     return launch_i8_fused_mt<4, XT, SILU>(lpr, t, total_rows, sdt, x, M, K, st);
 }
 
-template <int LPR, int MT, bool MP>
+template <int LPR, int MT, bool MP, bool XS>
 hipError_t launch_q4_gu_shape(int sbt, const uint32_t* wg, const void* Sg, const void* Bg, const uint32_t* wu,
-                              const void* Su, const void* Bu, const _Float16* x, float* h, int M, int N, int K,
+                              const void* Su, const void* Bu, const void* x, float* h, int M, int N, int K,
                               int gshift, hipStream_t st)
 {
     const dim3 grid((N + (kBlock / LPR) - 1) / (kBlock / LPR));
-    const size_t lds = (size_t)qgemv_q4_lds_bytes(M, K);
+    const size_t lds = (size_t)qgemv_q4_lds_bytes(M, K) + (XS ? (size_t)MT * (K >> 5) * 64 : 0);
     const u4_t* g4 = reinterpret_cast<const u4_t*>(wg);
     const u4_t* u4 = reinterpret_cast<const u4_t*>(wu);
-#define CELLM_GU(SBT_)                                                                                           \
-    hipLaunchKernelGGL((qgemv_q4_gate_up_silu_kernel<LPR, MT, SBT_, MP>), grid, dim3(kBlock), lds, st, g4, Sg, Bg, \
-                       u4, Su, Bu, x, h, M, N, K, gshift)
-    if (sbt == DT_F16) CELLM_GU(DT_F16);
-    else if (sbt == DT_F32) CELLM_GU(DT_F32);
-    else CELLM_GU(DT_BF16);
-#undef CELLM_GU
-    return hipGetLastError();
+    auto go = [&](auto kern) {
+        if (lds > 64 * 1024)
+            if (hipError_t e = allow_big_lds(kern, (int)lds); e != hipSuccess) return e;
+        hipLaunchKernelGGL(kern, grid, dim3(kBlock), lds, st, g4, Sg, Bg, u4, Su, Bu, x, h, M, N, K, gshift);
+        return hipGetLastError();
+    };
+    if (sbt == DT_F16) return go(qgemv_q4_gate_up_silu_kernel<LPR, MT, DT_F16, MP, XS>);
+    if (sbt == DT_F32) return go(qgemv_q4_gate_up_silu_kernel<LPR, MT, DT_F32, MP, XS>);
+    return go(qgemv_q4_gate_up_silu_kernel<LPR, MT, DT_BF16, MP, XS>);
 }
 
-template <int MT>
+template <int MT, bool XS>
 hipError_t launch_q4_gu_mt(int sbt, const uint32_t* wg, const void* Sg, const void* Bg, const uint32_t* wu,
-                           const void* Su, const void* Bu, const _Float16* x, float* h, int M, int N, int K, int gshift,
+                           const void* Su, const void* Bu, const void* x, float* h, int M, int N, int K, int gshift,
                            hipStream_t st)
 {
     const int CPR = K >> 5;
     const int lpr = pick_shape(CPR, 2 * N, false).lpr;
 #define CELLM_GU_L(L_)                                                                                               \
-    return CPR > kUnroll * L_ ? launch_q4_gu_shape<L_, MT, true>(sbt, wg, Sg, Bg, wu, Su, Bu, x, h, M, N, K, gshift, st) \
-                              : launch_q4_gu_shape<L_, MT, false>(sbt, wg, Sg, Bg, wu, Su, Bu, x, h, M, N, K, gshift, st)
+    return CPR > kUnroll * L_ ? launch_q4_gu_shape<L_, MT, true, XS>(sbt, wg, Sg, Bg, wu, Su, Bu, x, h, M, N, K, gshift, st) \
+                              : launch_q4_gu_shape<L_, MT, false, XS>(sbt, wg, Sg, Bg, wu, Su, Bu, x, h, M, N, K, gshift, st)
     switch (lpr) {
     case 8: CELLM_GU_L(8);
     case 16: CELLM_GU_L(16);
@@ -1754,6 +1845,16 @@ hipError_t launch_qgemv_q4_affine(const uint32_t* wq, const void* S, const void*
         if (M == 2) return launch_q4_f16x_lpr<1, 2>(sh.lpr, sbt, wq, S, B, xh, y, M, N, K, gshift, st);
         return launch_q4_f16x_lpr<1, 4>(sh.lpr, sbt, wq, S, B, xh, y, M, N, K, gshift, st);
     }
+    // f32 x (the LFM runner's activations): the same team kernel over hi + lo f16 parts of x
+    const int MT = M <= 1 ? 1 : (M <= 2 ? 2 : 4);
+    const size_t lds32 = (size_t)2 * MT * (K >> 5) * 64 + (size_t)MT * (K >> 5) * 8;
+    if (!force_generic && xdt == DT_F32 && M <= 4 && (K % 32) == 0 && group_size >= 32 && aligned16(wq) &&
+        aligned16(x) && lds32 <= 160 * 1024) {
+        const GemvShape sh = pick_shape(K >> 5, N, true);
+        if (M == 1) return launch_q4_f16x_lpr<1, 1, true>(sh.lpr, sbt, wq, S, B, x, y, M, N, K, gshift, st);
+        if (M == 2) return launch_q4_f16x_lpr<1, 2, true>(sh.lpr, sbt, wq, S, B, x, y, M, N, K, gshift, st);
+        return launch_q4_f16x_lpr<1, 4, true>(sh.lpr, sbt, wq, S, B, x, y, M, N, K, gshift, st);
+    }
     const dim3 grid((N + 3) / 4);
 #define CELLM_Q4_GENERIC(XT_, SBT_)                                                                              \
     hipLaunchKernelGGL((qgemv_q4_generic_kernel<XT_, SBT_>), grid, dim3(kBlock), 0, st, wq, S, B, x, y, M, N, K, \
@@ -1829,19 +1930,28 @@ hipError_t launch_qgemv_i4_sym(const uint8_t* w, const uint16_t* S, int spr, int
 
 bool qgemv_q4_gate_up_supported(int xdt, int M, int K, int group_size, const void* x, const void* wg, const void* wu)
 {
-    return xdt == DT_F16 && M >= 1 && M <= 4 && K > 0 && (K % 32) == 0 && group_size >= 32 && aligned16(x) &&
-           aligned16(wg) && aligned16(wu) && qgemv_q4_lds_bytes(M, K) <= 64 * 1024;
+    // f32 x (staged as hi + lo f16 parts) takes twice the x space, up to the raised 160 KB
+    const bool f32x = xdt == DT_F32;
+    return (xdt == DT_F16 || f32x) && M >= 1 && M <= 4 && K > 0 && (K % 32) == 0 && group_size >= 32 &&
+           aligned16(x) && aligned16(wg) && aligned16(wu) &&
+           (f32x ? (size_t)qgemv_q4_lds_bytes(M, K) + (size_t)(M <= 1 ? 1 : (M <= 2 ? 2 : 4)) * (K >> 5) * 64 <=
+                       160 * 1024
+                 : qgemv_q4_lds_bytes(M, K) <= 64 * 1024);
 }
 
 hipError_t launch_qgemv_q4_gate_up_silu(const uint32_t* wg, const void* Sg, const void* Bg, const uint32_t* wu,
                                         const void* Su, const void* Bu, int sbt, int group_size, const void* x,
-                                        float* h, int M, int N, int K, hipStream_t st)
+                                        int xdt, float* h, int M, int N, int K, hipStream_t st)
 {
     const int gshift = __builtin_ctz((unsigned)group_size);
-    const _Float16* xh = reinterpret_cast<const _Float16*>(x);
-    if (M == 1) return launch_q4_gu_mt<1>(sbt, wg, Sg, Bg, wu, Su, Bu, xh, h, M, N, K, gshift, st);
-    if (M == 2) return launch_q4_gu_mt<2>(sbt, wg, Sg, Bg, wu, Su, Bu, xh, h, M, N, K, gshift, st);
-    return launch_q4_gu_mt<4>(sbt, wg, Sg, Bg, wu, Su, Bu, xh, h, M, N, K, gshift, st);
+    if (xdt == DT_F32) {
+        if (M == 1) return launch_q4_gu_mt<1, true>(sbt, wg, Sg, Bg, wu, Su, Bu, x, h, M, N, K, gshift, st);
+        if (M == 2) return launch_q4_gu_mt<2, true>(sbt, wg, Sg, Bg, wu, Su, Bu, x, h, M, N, K, gshift, st);
+        return launch_q4_gu_mt<4, true>(sbt, wg, Sg, Bg, wu, Su, Bu, x, h, M, N, K, gshift, st);
+    }
+    if (M == 1) return launch_q4_gu_mt<1, false>(sbt, wg, Sg, Bg, wu, Su, Bu, x, h, M, N, K, gshift, st);
+    if (M == 2) return launch_q4_gu_mt<2, false>(sbt, wg, Sg, Bg, wu, Su, Bu, x, h, M, N, K, gshift, st);
+    return launch_q4_gu_mt<4, false>(sbt, wg, Sg, Bg, wu, Su, Bu, x, h, M, N, K, gshift, st);
 }
 
 bool qgemv_i8_fused_supported(int xdt, int M, int K, const void* x, const I8FusedSeg* segs, int nseg)

@@ -495,14 +495,23 @@ def test_qgemm_ragged_m_n(ops, m, k, n, group, sb):
     (1000, 1024, 1, np.float16, 32),
     (300, 10240, 2, np.float16, 64),
     (200, 10240, 4, np.float16, 64),
+    (151936, 896, 1, np.float16, 64),    # the affine lm_head (lfm.rs:700-741) with its f32 x_final
+    (333, 96, 1, np.float16, 32),        # one chunk per row, most lanes idle
 ])
 def test_q4_affine_f32_activations(ops, n, k, m, sb, group):
     """MLX q4 affine GEMV with f32 x (linear_i4_out_in, lfm.rs:985-1066), the
-    LFM runner's activations: one wave per row, f32 arithmetic, within 1e-3
-    of the reference order."""
+    LFM runner's activations: the team kernel over x split into hi + lo f16
+    parts (products with either part exact in f32), within 1e-3 of the
+    reference order.  The split keeps x to about 22 bits: the error also stays
+    under 3e-5, which one f16 rounding of x (about 2e-4 here) would not."""
     wq, s, b, x = make_q4(n, k, m, sb_dtype=sb, x_dtype=np.float32, group=group, salt=70 + m + k % 97)
     y = _run_q4(ops, wq, s, b, x, group=group)
-    assert rel_err(y, oracle.qgemv_q4_affine(wq, s, b, x, k, gs=group)) <= TOL_F32
+    ref = oracle.qgemv_q4_affine(wq, s, b, x, k, gs=group)
+    assert rel_err(y, ref) <= TOL_F32
+    assert rel_err(y, ref) <= 3e-5
+    # the same weights with x rounded once to f16 land much further from the f32 reference
+    xr = x.astype(np.float16).astype(np.float32)
+    assert rel_err(oracle.qgemv_q4_affine(wq, s, b, xr, k, gs=group), ref) > 3e-5
 
 
 # ------------------------------------------------------------------- i4 sym ----
@@ -734,7 +743,9 @@ def test_gate_up_silu_i8(ops, m, xdt):
     (1152, 6912, 1, np.float32, 64, np.float16),   # Gemma-3-1B MLP halves, f32 S/B as LFM files hold them
     (1152, 6912, 2, "bf16", 128, np.float16),
     (4864, 896, 3, np.float16, 32, np.float16),    # long rows: two register passes per lane
-    (896, 1000, 1, np.float16, 64, np.float32),    # f32 x: two GEMVs + SiLU kernel
+    (896, 1000, 1, np.float16, 64, np.float32),    # f32 x (the LFM runner's): one launch over hi + lo f16 parts
+    (896, 4864, 4, np.float32, 64, np.float32),    # Qwen2.5-0.5B MLP halves from a .cellm u32 file, f32 x
+    (4864, 896, 3, np.float16, 64, np.float32),    # f32 x of long rows: past 64 KB of LDS
     (896, 4864, 5, np.float16, 64, np.float16),    # m > 4: two GEMVs + SiLU kernel
 ])
 def test_gate_up_silu_q4(ops, k, n, m, sb, group, xdt):
