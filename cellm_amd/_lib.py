@@ -48,6 +48,8 @@ SIGNATURES = {
     "cellm_hip_qgemv_batch": (_i32, [_vp, C.POINTER(QgemvOp), _i64, _vp]),
     "cellm_hip_qgemv_i8_qkv": (_i32, [_vp, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i32, _vp,
                                       _i32, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
+    "cellm_hip_qgemv_q4_affine_qkv": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32,
+                                             _i64, _vp, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
     "cellm_hip_qgemv_i8_gate_up_silu": (_i32, [_vp, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i32, _vp, _i32, _vp,
                                                _i64, _i64, _i64, _vp]),
     "cellm_hip_qgemv_q4_affine_gate_up_silu": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _vp, _i32, _vp,

@@ -704,6 +704,51 @@ int32_t cellm_hip_qgemv_i8_qkv(cellm_hip_ctx_t* ctx, const int8_t* wq, const voi
     CELLM_API_END(report_exception)
 }
 
+int32_t cellm_hip_qgemv_q4_affine_qkv(cellm_hip_ctx_t* ctx, const uint32_t* wq, const void* sq, const void* bq,
+                                      const float* biasq, const uint32_t* wk, const void* sk, const void* bk,
+                                      const float* biask, const uint32_t* wv, const void* sv, const void* bv,
+                                      const float* biasv, int32_t sb_dtype, int64_t group, const void* x,
+                                      int32_t x_dtype, float* q, float* k_out, float* v, int64_t m, int64_t rows_q,
+                                      int64_t rows_kv, int64_t cols, void* stream)
+{
+    CELLM_API_BEGIN
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    DeviceGuard g(ctx->device);
+    const std::lock_guard<std::recursive_mutex> lk(ctx->mu);  // held until the scratch users are enqueued
+    hipStream_t st = pick_stream(ctx, stream);
+    const uint32_t* w[3] = {wq, wk, wv};
+    const void* s[3] = {sq, sk, sv};
+    const void* b[3] = {bq, bk, bv};
+    const float* pb[3] = {biasq, biask, biasv};
+    float* y[3] = {q, k_out, v};
+    const int64_t rows[3] = {rows_q, rows_kv, rows_kv};
+    for (int i = 0; i < 3; ++i)
+        if (int32_t rc = check_dims(m, rows[i], cols)) return rc;
+    if (int32_t rc = check_group(group)) return rc;
+    if (!valid_dtype(sb_dtype) || !valid_dtype(x_dtype)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "bad dtype");
+    if (m == 0 || rows[0] + rows[1] + rows[2] == 0) return CELLM_HIP_OK;
+    for (int i = 0; i < 3; ++i)
+        if (rows[i] > 0 && ((cols > 0 && (!w[i] || !s[i] || !b[i] || !x)) || !y[i]))
+            return set_error(CELLM_HIP_ERR_INVALID_ARG, "null pointer in projection %d", i);
+    Q4FusedSeg segs[3];
+    for (int i = 0; i < 3; ++i) segs[i] = Q4FusedSeg{w[i], s[i], b[i], pb[i], y[i], (int)rows[i]};
+    if (cols > 0 && qgemv_q4_segs_supported(x_dtype, (int)m, (int)cols, (int)group, x, segs, 3)) {
+        HIP_TRY(launch_qgemv_q4_segs(segs, 3, sb_dtype, (int)group, x, x_dtype, (int)m, (int)cols, st),
+                "qgemv_q4_qkv launch");
+        return CELLM_HIP_OK;
+    }
+    // other shapes: one GEMV per projection, then its bias
+    for (int i = 0; i < 3; ++i) {
+        if (rows[i] == 0) continue;
+        if (int32_t rc = qgemv_q4_impl(ctx, w[i], s[i], b[i], sb_dtype, group, x, x_dtype, y[i], m, rows[i], cols, st,
+                                       false))
+            return rc;
+        if (pb[i]) HIP_TRY(launch_add_bias_rows(y[i], pb[i], (int)m, (int)rows[i], st), "add_bias launch");
+    }
+    return CELLM_HIP_OK;
+    CELLM_API_END(report_exception)
+}
+
 int32_t cellm_hip_qgemv_i8_gate_up_silu(cellm_hip_ctx_t* ctx, const int8_t* wg, const void* sg, int64_t n_sg,
                                         const float* bg, const int8_t* wu, const void* su, int64_t n_su,
                                         const float* bu, int32_t scale_dtype, const void* x, int32_t x_dtype, float* h,

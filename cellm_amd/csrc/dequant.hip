@@ -98,6 +98,21 @@ hipError_t launch_dequant_q4_affine(const uint32_t* wq, const void* S, const voi
     return hipGetLastError();
 }
 
+__global__ void add_bias_rows_kernel(float* __restrict__ y, const float* __restrict__ bias, int M, int N)
+{
+    const size_t total = (size_t)M * N;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x)
+        y[i] += bias[i % (size_t)N];
+}
+
+hipError_t launch_add_bias_rows(float* y, const float* bias, int M, int N, hipStream_t st)
+{
+    const size_t total = (size_t)M * N;
+    const unsigned blocks = (unsigned)std::min<size_t>((total + 255) / 256, 4096);
+    hipLaunchKernelGGL(add_bias_rows_kernel, dim3(blocks), dim3(256), 0, st, y, bias, M, N);
+    return hipGetLastError();
+}
+
 hipError_t launch_silu_mul(float* g, const float* u, size_t count, hipStream_t st)
 {
     if (count == 0) return hipSuccess;

@@ -53,6 +53,23 @@ hipError_t launch_qgemv_q4_gate_up_silu(const uint32_t* wg, const void* Sg, cons
 
 // h[i] = silu(g[i]) * u[i] in place on g (dequant.hip), silu(g) = g / (1 + exp(-g)).
 hipError_t launch_silu_mul(float* g, const float* u, size_t count, hipStream_t st);
+// y[m, n] += bias[n] over M rows of N (the projection-bias fallback of the multi-segment q4 GEMV)
+hipError_t launch_add_bias_rows(float* y, const float* bias, int M, int N, hipStream_t st);
+
+// Up to three MLX q4 matrices sharing x in one launch (f16 or f32 x, M <= 4, K % 32 == 0,
+// group >= 32, 16-byte aligned x and W), each with its own scales S, group biases B,
+// optional f32 projection bias [n] and output y [M][n].
+struct Q4FusedSeg {
+    const uint32_t* w;
+    const void* S;
+    const void* B;
+    const float* bias;
+    float* y;
+    int n;
+};
+bool qgemv_q4_segs_supported(int xdt, int M, int K, int group_size, const void* x, const Q4FusedSeg* segs, int nseg);
+hipError_t launch_qgemv_q4_segs(const Q4FusedSeg* segs, int nseg, int sbt, int group_size, const void* x, int xdt,
+                                int M, int K, hipStream_t st);
 
 // Prefill / batched qGEMM on MFMA: Y[M,N] = X[M,K] . dequant(W)[N,K]^T with
 // W tiles dequantized to f16 in LDS and f32 accumulation.  Requires K % 64 == 0

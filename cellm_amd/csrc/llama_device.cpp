@@ -332,6 +332,14 @@ int32_t enqueue_step(cellm_llama_dev* m, int32_t rows)
                                                P[1].bias, i8w(P[2]), i8s(P[2]), kvd, P[2].bias, CELLM_HIP_DTYPE_F16,
                                                xn, CELLM_HIP_DTYPE_F32, q, k, v, R, hid, kvd, hid, S),
                         "qkv");
+            } else if (P[0].kind == PK_Q4 && P[1].kind == PK_Q4 && P[2].kind == PK_Q4) {
+                // the three MLX affine projections in one launch, biases in its epilogue
+                LIB_TRY(cellm_hip_qgemv_q4_affine_qkv(H, static_cast<const uint32_t*>(P[0].w), P[0].s, P[0].b,
+                                                      P[0].bias, static_cast<const uint32_t*>(P[1].w), P[1].s, P[1].b,
+                                                      P[1].bias, static_cast<const uint32_t*>(P[2].w), P[2].s, P[2].b,
+                                                      P[2].bias, CELLM_HIP_DTYPE_F32, 64, xn, CELLM_HIP_DTYPE_F32, q,
+                                                      k, v, R, hid, kvd, hid, S),
+                        "qkv");
             } else {
                 if (int32_t rc = run_proj(m, P[0], xn, q, R, hid, hid, "q_proj")) return rc;
                 if (int32_t rc = run_proj(m, P[1], xn, k, R, kvd, hid, "k_proj")) return rc;

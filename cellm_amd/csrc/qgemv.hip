@@ -436,6 +436,95 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_gate_up_silu_kernel(
     }
 }
 
+// Up to three MLX q4 matrices that share x in one launch (the q, k and v
+// projections of the u32 runners), each with its own scales, group biases,
+// optional projection bias (f32 [n], added after the row sum, as
+// add_projection_bias_if_present does, qwen.rs:1132-1139) and output.  A team
+// owns one row of the concatenation [seg0 rows; seg1 rows; seg2 rows]; the rows
+// past the end repeat the last row and are not stored.  XS: f32 x as hi + lo
+// f16 parts (stage_word_q4_x32).
+struct Q4Seg {
+    const u4_t* w;
+    const void* S;
+    const void* B;
+    const float* bias;
+    float* y;
+    int n;
+};
+struct Q4Segs {
+    Q4Seg g0, g1, g2;
+};
+
+template <int LPR, int MT, int SBT, bool MP, bool XS>
+__global__ __launch_bounds__(kBlock) void qgemv_q4_segs_kernel(Q4Segs segs, const void* __restrict__ xv, int M,
+                                                              int total_rows, int K, int gshift)
+{
+    extern __shared__ __align__(16) uint32_t lds[];
+    const int CPR = K >> 5;
+    uint32_t* xq = lds;
+    uint32_t* xq_lo = XS ? lds + (size_t)MT * CPR * 16 : nullptr;
+    float2* cx = reinterpret_cast<float2*>(lds + (size_t)(XS ? 2 : 1) * MT * CPR * 16);
+    const int team = threadIdx.x / LPR;
+    const int lane = threadIdx.x % LPR;
+    const int row = blockIdx.x * (kBlock / LPR) + team;
+    const int gpr = (K + (1 << gshift) - 1) >> gshift;
+    const int total = MT * (K >> 3);
+
+    int v = min(row, total_rows - 1);
+    Q4Seg sg = segs.g0;
+    if (v >= segs.g0.n) {
+        v -= segs.g0.n;
+        sg = segs.g1;
+        if (v >= segs.g1.n) {
+            v -= segs.g1.n;
+            sg = segs.g2;
+        }
+    }
+    constexpr int XW = MT == 1 ? 4 : 8;
+    u4_t wa[kUnroll][1];
+    uint32_t sa[kUnroll][1], ba[kUnroll][1];
+    if constexpr (XS) {
+        load_pass_q4<LPR, 1, SBT>(sg.w, sg.S, sg.B, v, 1, lane, sg.n, CPR, gpr, gshift, wa, sa, ba);
+        stage_x_q4_x32<XW / 2>(reinterpret_cast<const float*>(xv), M, K, total, xq, xq_lo, cx);
+    } else {
+        const _Float16* x = reinterpret_cast<const _Float16*>(xv);
+        u4_t xr[XW];
+        load_x_words<XW>(x, M, K, total, xr);
+        load_pass_q4<LPR, 1, SBT>(sg.w, sg.S, sg.B, v, 1, lane, sg.n, CPR, gpr, gshift, wa, sa, ba);
+        stage_x_q4<XW>(xr, x, M, K, total, xq, cx);
+    }
+    __syncthreads();
+    if (row >= total_rows) return;
+
+    float acc[1][MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc[0][m] = 0.0f;
+    if constexpr (!MP) {
+        compute_pass_q4<LPR, 1, MT, SBT, kUnroll, XS>(lane, CPR, xq, cx, wa, sa, ba, acc, xq_lo);
+    } else {
+        constexpr int P = kUnroll * LPR;
+        u4_t wb[kUnroll][1];
+        uint32_t sb[kUnroll][1], bb[kUnroll][1];
+        for (int c0 = lane; c0 < CPR + lane; c0 += 2 * P) {
+            if (c0 - lane + P < CPR)
+                load_pass_q4<LPR, 1, SBT>(sg.w, sg.S, sg.B, v, 1, c0 + P, sg.n, CPR, gpr, gshift, wb, sb, bb);
+            compute_pass_q4<LPR, 1, MT, SBT, kUnroll, XS>(c0, CPR, xq, cx, wa, sa, ba, acc, xq_lo);
+            if (c0 - lane + P >= CPR) break;
+            if (c0 - lane + 2 * P < CPR)
+                load_pass_q4<LPR, 1, SBT>(sg.w, sg.S, sg.B, v, 1, c0 + 2 * P, sg.n, CPR, gpr, gshift, wa, sa, ba);
+            compute_pass_q4<LPR, 1, MT, SBT, kUnroll, XS>(c0 + P, CPR, xq, cx, wb, sb, bb, acc, xq_lo);
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc[0][m] = group_sum<LPR>(acc[0][m]);
+    if (lane == 0) {
+        const float bv = sg.bias ? sg.bias[v] : 0.0f;
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+            if (m < M) sg.y[(size_t)m * sg.n + v] = sg.bias ? acc[0][m] + bv : acc[0][m];
+    }
+}
+
 // Persistent single-row (M = 1) variant for long outputs (lm_head): a block
 // stages x once, then walks tiles tile, tile+grid, ... of ROWS rows.  The next
 // tile's weights are loaded while the current one is computed (two register
@@ -1952,6 +2041,82 @@ hipError_t launch_qgemv_q4_gate_up_silu(const uint32_t* wg, const void* Sg, cons
     if (M == 1) return launch_q4_gu_mt<1, false>(sbt, wg, Sg, Bg, wu, Su, Bu, x, h, M, N, K, gshift, st);
     if (M == 2) return launch_q4_gu_mt<2, false>(sbt, wg, Sg, Bg, wu, Su, Bu, x, h, M, N, K, gshift, st);
     return launch_q4_gu_mt<4, false>(sbt, wg, Sg, Bg, wu, Su, Bu, x, h, M, N, K, gshift, st);
+}
+
+bool qgemv_q4_segs_supported(int xdt, int M, int K, int group_size, const void* x, const Q4FusedSeg* segs, int nseg)
+{
+    if (!(xdt == DT_F16 || xdt == DT_F32) || M < 1 || M > 4 || K <= 0 || (K % 32) != 0 || group_size < 32 ||
+        !aligned16(x))
+        return false;
+    const size_t lds = (size_t)qgemv_q4_lds_bytes(M, K) + (xdt == DT_F32 ? (size_t)(M <= 1 ? 1 : (M <= 2 ? 2 : 4)) * (K >> 5) * 64 : 0);
+    if (lds > (xdt == DT_F32 ? 160 : 64) * 1024) return false;
+    for (int i = 0; i < nseg; ++i)
+        if (!aligned16(segs[i].w)) return false;
+    return true;
+}
+
+namespace {
+
+template <int LPR, int MT, bool MP, bool XS>
+hipError_t launch_q4_segs_shape(const Q4Segs& t, int total_rows, int sbt, const void* x, int M, int K, int gshift,
+                                hipStream_t st)
+{
+    const dim3 grid((total_rows + (kBlock / LPR) - 1) / (kBlock / LPR));
+    const size_t lds = (size_t)qgemv_q4_lds_bytes(M, K) + (XS ? (size_t)MT * (K >> 5) * 64 : 0);
+    auto go = [&](auto kern) {
+        if (lds > 64 * 1024)
+            if (hipError_t e = allow_big_lds(kern, (int)lds); e != hipSuccess) return e;
+        hipLaunchKernelGGL(kern, grid, dim3(kBlock), lds, st, t, x, M, total_rows, K, gshift);
+        return hipGetLastError();
+    };
+    if (sbt == DT_F16) return go(qgemv_q4_segs_kernel<LPR, MT, DT_F16, MP, XS>);
+    if (sbt == DT_F32) return go(qgemv_q4_segs_kernel<LPR, MT, DT_F32, MP, XS>);
+    return go(qgemv_q4_segs_kernel<LPR, MT, DT_BF16, MP, XS>);
+}
+
+template <int MT, bool XS>
+hipError_t launch_q4_segs_mt(const Q4Segs& t, int total_rows, int sbt, const void* x, int M, int K, int gshift,
+                             hipStream_t st)
+{
+    const int CPR = K >> 5;
+    const int lpr = pick_shape(CPR, total_rows, true).lpr;
+#define CELLM_SEGS_L(L_)                                                                                   \
+    return CPR > kUnroll * L_ ? launch_q4_segs_shape<L_, MT, true, XS>(t, total_rows, sbt, x, M, K, gshift, st) \
+                              : launch_q4_segs_shape<L_, MT, false, XS>(t, total_rows, sbt, x, M, K, gshift, st)
+    switch (lpr) {
+    case 8: CELLM_SEGS_L(8);
+    case 16: CELLM_SEGS_L(16);
+    case 32: CELLM_SEGS_L(32);
+    default: CELLM_SEGS_L(64);
+    }
+#undef CELLM_SEGS_L
+}
+
+}  // namespace
+
+hipError_t launch_qgemv_q4_segs(const Q4FusedSeg* segs, int nseg, int sbt, int group_size, const void* x, int xdt,
+                                int M, int K, hipStream_t st)
+{
+    Q4Seg g[3] = {};
+    int total = 0;
+    for (int i = 0; i < 3; ++i) {
+        if (i < nseg)
+            g[i] = Q4Seg{reinterpret_cast<const u4_t*>(segs[i].w), segs[i].S, segs[i].B, segs[i].bias, segs[i].y,
+                         segs[i].n};
+        else
+            g[i] = g[0], g[i].n = 0;
+        total += g[i].n;
+    }
+    const Q4Segs t{g[0], g[1], g[2]};
+    const int gshift = __builtin_ctz((unsigned)group_size);
+    if (xdt == DT_F32) {
+        if (M == 1) return launch_q4_segs_mt<1, true>(t, total, sbt, x, M, K, gshift, st);
+        if (M == 2) return launch_q4_segs_mt<2, true>(t, total, sbt, x, M, K, gshift, st);
+        return launch_q4_segs_mt<4, true>(t, total, sbt, x, M, K, gshift, st);
+    }
+    if (M == 1) return launch_q4_segs_mt<1, false>(t, total, sbt, x, M, K, gshift, st);
+    if (M == 2) return launch_q4_segs_mt<2, false>(t, total, sbt, x, M, K, gshift, st);
+    return launch_q4_segs_mt<4, false>(t, total, sbt, x, M, K, gshift, st);
 }
 
 bool qgemv_i8_fused_supported(int xdt, int M, int K, const void* x, const I8FusedSeg* segs, int nseg)

@@ -220,6 +220,21 @@ class HipOps:
             _torch_dtype_code(x), _dev_ptr(q), _dev_ptr(k_out), _dev_ptr(v), m, rows_q, rows_kv, cols,
             _stream_ptr(stream)))
 
+    def encode_qkv_q4_affine(self, wq, sq, bq, wk, sk, bk, wv, sv, bv, x, q, k_out, v, biasq=None, biask=None,
+                             biasv=None, group: int = 64, stream=None) -> None:
+        """Three MLX q4 affine projections of one x (f16 or f32) in one launch, each with an
+        optional f32 projection bias added after the row sum (cellm_hip_qgemv_q4_affine_qkv)."""
+        rows_q, cols = wq.shape[0], wq.shape[1] * 8
+        rows_kv = wk.shape[0]
+        m = x.numel() // cols
+        if not (sq.dtype == sk.dtype == sv.dtype == bq.dtype == bk.dtype == bv.dtype):
+            raise TypeError("q/k/v scales and group biases must share a dtype")
+        check(self._lib.cellm_hip_qgemv_q4_affine_qkv(
+            self._h, _dev_ptr(wq), _dev_ptr(sq), _dev_ptr(bq), _dev_ptr(biasq), _dev_ptr(wk), _dev_ptr(sk),
+            _dev_ptr(bk), _dev_ptr(biask), _dev_ptr(wv), _dev_ptr(sv), _dev_ptr(bv), _dev_ptr(biasv),
+            _torch_dtype_code(sq), group, _dev_ptr(x), _torch_dtype_code(x), _dev_ptr(q), _dev_ptr(k_out),
+            _dev_ptr(v), m, rows_q, rows_kv, cols, _stream_ptr(stream)))
+
     def encode_gate_up_silu_i8(self, wg, sg, wu, su, x, h, bg=None, bu=None, stream=None) -> None:
         """h = silu(Wg.x * sg (+bg)) * (Wu.x * su (+bu)); int8 gate/up."""
         n, k = wg.shape

@@ -145,6 +145,22 @@ int32_t cellm_hip_qgemv_i8_qkv(cellm_hip_ctx_t* ctx, const int8_t* wq, const voi
                                int32_t x_dtype, float* q, float* k_out, float* v, int64_t m, int64_t rows_q,
                                int64_t rows_kv, int64_t cols, void* stream);
 
+/* The q, k and v projections of MLX 4-bit affine weights sharing x, in one
+ * launch for m <= 4 (f16 or f32 x, cols % 32 == 0, group >= 32, 16-byte
+ * aligned x and W); other shapes run one GEMV per projection.  sq/bq ... are
+ * each matrix's scales and group biases in sb_dtype (cellm_hip_qgemv_q4_affine);
+ * biasq/biask/biasv (f32 [rows], or NULL) are added after each row sum, as
+ * add_projection_bias_if_present does (qwen.rs:1132-1139).  No reference
+ * counterpart as one call: the u32 runners call linear_f16_out_in once per
+ * projection (lfm.rs:924-981); this is the q4 form of
+ * cellm_hip_qgemv_i8_qkv. */
+int32_t cellm_hip_qgemv_q4_affine_qkv(cellm_hip_ctx_t* ctx, const uint32_t* wq, const void* sq, const void* bq,
+                                      const float* biasq, const uint32_t* wk, const void* sk, const void* bk,
+                                      const float* biask, const uint32_t* wv, const void* sv, const void* bv,
+                                      const float* biasv, int32_t sb_dtype, int64_t group, const void* x,
+                                      int32_t x_dtype, float* q, float* k_out, float* v, int64_t m, int64_t rows_q,
+                                      int64_t rows_kv, int64_t cols, void* stream);
+
 /* Gate and up projections with the SiLU * up epilogue:
  *   h = silu((Wg . x) * sg (+ bg)) * ((Wu . x) * su (+ bu)),  silu(g) = g / (1 + exp(-g)).
  * One launch for m <= 4 under the conditions of cellm_hip_qgemv_i8_qkv; other

@@ -737,6 +737,39 @@ def test_gate_up_silu_i8(ops, m, xdt):
     assert rel_err(h.cpu().numpy(), ref) <= TOL_F32
 
 
+@pytest.mark.parametrize("k,rq,rkv,m,sb,xdt,biased", [
+    (896, 896, 128, 1, np.float16, np.float16, True),    # Qwen2.5-0.5B q/k/v, f16 x
+    (896, 896, 128, 4, np.float32, np.float32, True),    # from a .cellm u32 file: f32 S/B and x
+    (1152, 1024, 256, 2, "bf16", np.float32, False),     # Gemma-3-1B shapes, no bias
+    (4864, 300, 100, 3, np.float16, np.float32, True),   # long rows (two register passes), ragged rows
+    (896, 896, 128, 5, np.float16, np.float32, True),    # m > 4: one GEMV per projection + bias kernel
+])
+def test_qkv_q4_affine(ops, k, rq, rkv, m, sb, xdt, biased):
+    """Three MLX q4 projections of one x in one launch with projection biases after the row
+    sums (cellm_hip_qgemv_q4_affine_qkv), against the oracle's three GEMVs plus the bias
+    (lfm.rs:985-1066, qwen.rs:1132-1139); f32 x within 3e-5 (hi + lo f16 parts)."""
+    import torch
+
+    mats = [make_q4(r, k, m, sb_dtype=sb, x_dtype=xdt, salt=90 + i + m) for i, r in enumerate((rq, rkv, rkv))]
+    x = mats[0][3]
+    biases = [oracle.gen_normal((r,), seed(3, 9, i), 0.0, 1.0) if biased else None
+              for i, r in enumerate((rq, rkv, rkv))]
+    outs = [torch.empty((m, r), dtype=torch.float32, device="cuda") for r in (rq, rkv, rkv)]
+    args = []
+    for wq, s, b, _ in mats:
+        args += [_t(wq), _sb_tensor(s), _sb_tensor(b)]
+    ops.encode_qkv_q4_affine(*args, _t(x), *outs, *[None if bb is None else _t(bb) for bb in biases])
+    torch.cuda.synchronize()
+    for (wq, s, b, _), bb, y in zip(mats, biases, outs):
+        ref = oracle.qgemv_q4_affine(wq, s, b, x, k)
+        if bb is not None:
+            ref = (ref + bb[None, :]).astype(np.float32)
+        err = rel_err(y.cpu().numpy(), ref)
+        assert err <= TOL_F32
+        if xdt == np.float32:
+            assert err <= 3e-5
+
+
 @pytest.mark.parametrize("k,n,m,sb,group,xdt", [
     (896, 4864, 1, np.float16, 64, np.float16),    # Qwen2.5-0.5B MLP halves, one launch
     (896, 4864, 4, np.float16, 64, np.float16),
