@@ -539,6 +539,166 @@ __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(const float*
     attn_combine_group<HD, G, false>(p, nch, out + ((size_t)r * n_heads + (size_t)kvh * G) * HD, cm, cl, invl);
 }
 
+// Whole-sequence attention in one block per (row, query head), for caches of
+// at most S * 256 positions.  16 waves; wave w owns positions
+// 256 s + 16 w .. + 15 of each sub-chunk s, with attn_partial_kernel's
+// per-wave mapping (Q.K: 4 lanes per position, P.V: HD/64 dims per lane).
+// Every K and V load of the sequence is issued before any arithmetic and the
+// softmax max and sum are reduced across the block in LDS, so the head's
+// output is the block's only global write:
+//   o = (sum_p e^(s_p - M) v_p) / (sum_p e^(s_p - M)),  M = max_p s_p
+// (kvcache.rs:710-789, with the one maximum over the sequence the reference
+// takes).  The G heads of a kv head read its K and V once each, through L2.
+// The waves' P.V sums are added in a fixed order (waves 8..15 onto 0..7, then
+// the eight in index order), so a call is deterministic.  A row with no
+// position (pos < 0) writes nothing, as in the chunked kernels.
+constexpr int kAttnBlockWaves = 16;
+constexpr int kAttnBlockThreads = kAttnBlockWaves * 64;
+constexpr int kAttnBlockSub = kAttnBlockWaves * 16;  // positions per sub-chunk
+
+template <int HD, int S>
+__global__ __launch_bounds__(kAttnBlockThreads) void attn_head_kernel(
+    const float* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
+    const int32_t* __restrict__ pos, PagedKv kv, int layer, int n_heads, int group, float scale, float soft_cap,
+    float* __restrict__ out)
+{
+    constexpr int NW = kAttnBlockWaves, CAP = S * kAttnBlockSub;
+    constexpr int KD = HD / 4;  // Q.K dims per lane
+    constexpr int KL = KD / 8;  // 16-byte K loads per lane and sub-chunk
+    constexpr int VD = HD / 64; // P.V dims per lane
+    using vword_t = typename std::conditional<VD == 1, uint16_t, uint32_t>::type;
+    __shared__ float qs[HD];
+    __shared__ float ps[CAP];
+    __shared__ long long bases[CAP];
+    __shared__ float wmax[NW], wsum[NW];
+    __shared__ float accs[NW / 2][HD];
+    const int r = blockIdx.x / n_heads, h = blockIdx.x % n_heads, kvh = h / group;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    // position, q and the page entries: independent loads, issued together
+    const int p_r = pos[r];
+    const float qv = q[((size_t)r * n_heads + h) * HD + min(t, HD - 1)];
+    const int tp = min(t, CAP - 1), blk_i = tp / kv.tpb;
+    const uint32_t blk = kv.bt[(size_t)r * kv.max_blocks + min(blk_i, kv.max_blocks - 1)];
+    const int seq = min(p_r + 1, kv.max_blocks * kv.tpb);  // the launcher keeps max_blocks * tpb <= CAP
+    if (seq <= 0) return;  // the same for the whole block
+    if (t < HD) qs[t] = qv;
+    if (t < CAP)
+        bases[t] = (t < seq && blk_i < kv.max_blocks && blk < (uint32_t)kv.total_blocks)
+                       ? ((long long)blk * kv.n_layers + layer) * (long long)kv.tpb * kv.kvd +
+                             (long long)(t % kv.tpb) * kv.kvd
+                       : -1;
+    __syncthreads();
+
+    // every K and V load (a missing page or a position past the sequence reads
+    // element 0 and is zeroed)
+    const int kq = lane & 3;
+    u4_t kraw[S][KL];
+    bool kok[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        const long long kb = bases[s * kAttnBlockSub + wave * 16 + (lane >> 2)];
+        kok[s] = kb >= 0;
+        const u4_t* ksrc = reinterpret_cast<const u4_t*>(kc + (kb >= 0 ? kb + (long long)kvh * HD + kq * KD : 0));
+#pragma unroll
+        for (int j = 0; j < KL; ++j) kraw[s][j] = ksrc[j];
+    }
+    vword_t vraw[S][16];
+    uint32_t vok[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        vok[s] = 0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const long long vb = bases[s * kAttnBlockSub + wave * 16 + i];
+            vok[s] |= (vb >= 0 ? 1u : 0u) << i;
+            vraw[s][i] =
+                *reinterpret_cast<const vword_t*>(vc + (vb >= 0 ? vb + (long long)kvh * HD + lane * VD : 0));
+        }
+    }
+
+    // scores of this lane's positions, the wave maximum, then the block maximum
+    float sc[S], mloc = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        float dot = 0.0f;
+#pragma unroll
+        for (int j = 0; j < KL; ++j) {
+            const h8_t kh = __builtin_bit_cast(h8_t, kok[s] ? kraw[s][j] : u4_t{0, 0, 0, 0});
+#pragma unroll
+            for (int e = 0; e < 8; ++e) dot = dot + qs[kq * KD + j * 8 + e] * (float)kh[e];
+        }
+        const bool valid = s * kAttnBlockSub + wave * 16 + (lane >> 2) < seq;
+        dot = dot + __shfl_xor(dot, 1);
+        dot = dot + __shfl_xor(dot, 2);
+        float sg = dot * scale;
+        if (soft_cap > 0.0f) sg = tanhf(sg / soft_cap) * soft_cap;  // kvcache.rs:768-770
+        sc[s] = valid ? sg : -INFINITY;
+        mloc = fmaxf(mloc, sc[s]);
+    }
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 4));
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 8));
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+    if (lane == 0) wmax[wave] = mloc;
+    __syncthreads();
+    // weights e^(s - M) into LDS (one lane of each position), and the wave sums
+    float m = wmax[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) m = fmaxf(m, wmax[w]);
+    float l = 0.0f;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        const bool valid = s * kAttnBlockSub + wave * 16 + (lane >> 2) < seq;
+        const float e = valid ? expf(sc[s] - m) : 0.0f;
+        if (kq == 0) ps[s * kAttnBlockSub + wave * 16 + (lane >> 2)] = e;
+        l = l + e;
+    }
+    l = l + __shfl_xor(l, 4);
+    l = l + __shfl_xor(l, 8);
+    l = l + __shfl_xor(l, 16);
+    l = l + __shfl_xor(l, 32);
+    if (lane == 0) wsum[wave] = l;
+    __syncthreads();
+
+    // weighted V over this wave's positions
+    float acc[VD];
+#pragma unroll
+    for (int d = 0; d < VD; ++d) acc[d] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const vword_t w = (vok[s] >> i) & 1u ? vraw[s][i] : vword_t(0);
+            const float pg = ps[s * kAttnBlockSub + wave * 16 + i];
+            if constexpr (VD == 1) {
+                acc[0] = acc[0] + pg * h2f(w);
+            } else {
+                acc[0] = acc[0] + pg * h2f((uint16_t)(w & 0xffffu));
+                acc[1] = acc[1] + pg * h2f((uint16_t)(w >> 16));
+            }
+        }
+    // across the waves: 8..15 onto 0..7, then the eight in order
+    if (wave >= NW / 2) {
+#pragma unroll
+        for (int d = 0; d < VD; ++d) accs[wave - NW / 2][lane * VD + d] = acc[d];
+    }
+    __syncthreads();
+    if (wave < NW / 2) {
+#pragma unroll
+        for (int d = 0; d < VD; ++d) accs[wave][lane * VD + d] = acc[d] + accs[wave][lane * VD + d];
+    }
+    __syncthreads();
+    if (t < HD) {
+        float lt = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) lt = lt + wsum[w];
+        float a = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NW / 2; ++j) a = a + accs[j][t];
+        out[((size_t)r * n_heads + h) * HD + t] = a * (lt > 0.0f ? 1.0f / lt : 0.0f);
+    }
+}
+
 // ---- fused decode-step GEMVs ------------------------------------------------
 // One launch replaces "residual add + RMSNorm, int8 GEMV(s), epilogue op":
 //   decode_qkv_kernel:     xn = rms_norm(x_prev + y) * w;  q, k, v = W xn;
@@ -989,8 +1149,21 @@ hipError_t launch_attention_gqa_f16kv(const float* q, const uint16_t* kcache, co
     uint32_t* counters = reinterpret_cast<uint32_t*>(workspace);
     float* part = reinterpret_cast<float*>(reinterpret_cast<char*>(workspace) + kAttnCounterBytes);
     const bool one_launch = rows * n_kv_heads <= kAttnCounters;
+    const int cap = max_blocks * tokens_per_block;
+    const dim3 hgrid((unsigned)(rows * n_heads));
     auto go = [&](auto hd, auto g) {
         constexpr int HD = decltype(hd)::value, GG = decltype(g)::value;
+        // caches of up to 512 positions: the whole sequence in one block per query head
+        if (cap <= kAttnBlockSub) {
+            hipLaunchKernelGGL((attn_head_kernel<HD, 1>), hgrid, dim3(kAttnBlockThreads), 0, st, q, kcache, vcache,
+                               pos, kv, layer, n_heads, GG, scale, soft_cap, out);
+            return;
+        }
+        if (cap <= 2 * kAttnBlockSub) {
+            hipLaunchKernelGGL((attn_head_kernel<HD, 2>), hgrid, dim3(kAttnBlockThreads), 0, st, q, kcache, vcache,
+                               pos, kv, layer, n_heads, GG, scale, soft_cap, out);
+            return;
+        }
         if (one_launch) {
             hipLaunchKernelGGL((attn_partial_kernel<HD, GG, true>), pgrid, dim3(kAttnThreads), 0, st, q, kcache,
                                vcache, pos, kv, layer, n_kv_heads, scale, soft_cap, part, nch, counters, out);

@@ -5,7 +5,8 @@ paged GQA attention, residual add, greedy argmax) against the CPU oracle.
   cellm_llama_rope_table, the same glibc f32 math the oracle's rope uses).
 - RMSNorm: the sum of squares is a tree here and sequential in the reference:
   relative error <= 1e-6.
-- attention: softmax with the device expf, split-sequence partials combined
+- attention: softmax with the device expf; tables of up to 512 positions in
+  one block per query head, longer ones as split-sequence partials combined
   with rescaling: relative error <= 1e-5 of max|out|.
 """
 from __future__ import annotations
@@ -164,6 +165,11 @@ def test_kv_write_f16(ops):
     (15, 5, 64, 64, (1023, 960, 15, 511)),   # G 3, 16 chunks: the largest single-launch table
     (15, 5, 64, 80, (1279, 1024, 3, 640)),   # G 3, 20 chunks: split-sequence launches
     (4, 2, 128, 20, (319, 0, 64, 200)),      # G 2 at head_dim 128: single launch
+    # tables of up to 512 positions: one block per query head over the whole sequence
+    (14, 2, 64, 32, (511, 300, 0, 255)),    # G 7, 512 positions: two sub-chunks, full
+    (8, 8, 128, 16, (255, 128, 17, 0)),     # G 1 at head_dim 128, 256 positions: one sub-chunk
+    (16, 2, 128, 32, (511, 256, 257, 3)),   # G 8 at head_dim 128, sub-chunk edges
+    (15, 5, 64, 33, (527, 511, 512, 0)),    # 528 positions: back to the chunked kernels
 ])
 def test_attention_gqa_f16kv(ops, nh, nkv, hd, blocks, pos):
     L, tpb, rows = 3, 16, 4
@@ -189,7 +195,8 @@ def test_attention_one_launch_and_two_launch_forms(ops):
     counter); more groups take the two-launch form.  257 rows x 64 kv heads
     (16448 groups) run the two-launch form, then the first 256 rows (16384
     groups) the one-launch form, twice.  Every row has 65..80 positions (two
-    chunks).  Sampled rows match the oracle; the rows both forms share are equal
+    chunks) in a table of 33 pages (528 positions: tables of up to 512 take
+    the one-block-per-head kernel instead).  Sampled rows match the oracle; the rows both forms share are equal
     bit for bit, as are the two one-launch calls."""
     nh, nkv, hd, L, tpb, layer, bpr = 64, 64, 64, 1, 16, 0, 5
     kvd = nkv * hd
@@ -198,7 +205,7 @@ def test_attention_one_launch_and_two_launch_forms(ops):
     rng = np.random.default_rng(0xD0000500)
     k = rng.standard_normal(total * L * tpb * kvd, dtype=np.float32).astype(np.float16).view(np.uint16)
     v = rng.standard_normal(total * L * tpb * kvd, dtype=np.float32).astype(np.float16).view(np.uint16)
-    bt = np.array([[b * rows + r + 3 for b in range(bpr)] for r in range(rows)], np.uint32)
+    bt = np.array([[b * rows + r + 3 for b in range(bpr)] + [3] * (33 - bpr) for r in range(rows)], np.uint32)
     pos = (64 + (np.arange(rows) * 7) % 16).astype(np.int32)
     q = rng.standard_normal((rows, nh * hd), dtype=np.float32)
     kd, vd, qd = dev(k), dev(v), dev(q)

@@ -56,7 +56,7 @@ def test_noalloc_matches_allocating_entry_point_twice(ops):
     positions): each equals the allocating entry point bit for bit, and the
     oracle within the attention bar."""
     big = _case(15, 5, 64, 4, 34, (0, 31, 300, 543), 0xD0000300)
-    small = _case(8, 2, 128, 2, 5, (79, 7), 0xD0000400)
+    small = _case(8, 2, 128, 2, 33, (79, 7), 0xD0000400)  # 528-position tables: the partials path
     for c in (big, small):
         rows, width = c["q"].shape
         out_na = torch.full((rows, width), float("nan"), dtype=torch.float32, device="cuda")
