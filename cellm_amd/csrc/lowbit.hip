@@ -569,7 +569,6 @@ __global__ __launch_bounds__(kLutThreads) void q1_lut_kernel(const uint8_t* __re
     }
 }
 
-// CU count of the current device (cached per device)
 // CU count of the current device, cached per device id (any id; guarded by a mutex).
 static int lut_cus()
 {

@@ -394,12 +394,14 @@ int32_t cellm_hip_decode_gate_up_silu(cellm_hip_ctx_t* ctx, const float* x_prev,
  * reference's None); soft_cap > 0 maps each score s to tanh(s / soft_cap) *
  * soft_cap (Gemma), 0 = none.  Needs n_heads % n_kv_heads == 0, at most 8
  * query heads per kv head, head_dim 64 or 128, max_blocks * tokens_per_block
- * <= 32768.  Split over the sequence in chunks of 64 positions, one block
- * each; the last chunk block of each (row, kv head) to finish combines the
- * group's softmax partials in the same launch (workspace owned by the
- * context, per stream: 64 KB of group counters, zeroed when the workspace is
- * allocated and left at zero by every call, then the partials).  More than
- * 16384 (row, kv head) groups take a second combine launch. */
+ * <= 32768.  Tables of up to 512 positions (max_blocks * tokens_per_block)
+ * run one block per (row, query head) over the whole sequence, with no
+ * workspace use.  Longer tables are split over the sequence in chunks of 64
+ * positions, one block each; the last chunk block of each (row, kv head) to
+ * finish combines the group's softmax partials in the same launch (workspace
+ * owned by the context, per stream: 64 KB of group counters, zeroed when the
+ * workspace is allocated and left at zero by every call, then the partials).
+ * More than 16384 (row, kv head) groups take a second combine launch. */
 int32_t cellm_hip_attention_gqa_f16kv(cellm_hip_ctx_t* ctx, const float* q, const uint16_t* kcache,
                                       const uint16_t* vcache, const uint32_t* block_tables, int64_t max_blocks,
                                       int64_t total_blocks, const int32_t* positions, int64_t rows, int64_t n_heads,
@@ -409,8 +411,9 @@ int32_t cellm_hip_attention_gqa_f16kv(cellm_hip_ctx_t* ctx, const float* q, cons
 /* cellm_hip_attention_gqa_f16kv without any allocation, for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc).  No counterpart in the reference.
- * Same arguments and results; the group counters and softmax partials go to
- * a static device array of 8 MiB that each GPU holds until the process ends,
+ * Same arguments and results; the group counters and softmax partials of
+ * the split form (tables of more than 512 positions) go to a static device
+ * array of 8 MiB that each GPU holds until the process ends,
  * so calls that need more -- 65536 + rows * n_heads * ceil(max_blocks *
  * tokens_per_block / 64) * (head_dim + 2) * 4 bytes -- fail with
  * CELLM_HIP_ERR_INVALID_ARG.
