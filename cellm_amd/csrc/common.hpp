@@ -84,6 +84,25 @@ __device__ __forceinline__ float group_sum(float v)
     return v;
 }
 
+// group_sum<4> and group_sum<2> on DPP quad permutes: the same additions in the
+// same order (the xor-2 partner, then the xor-1 partner), as VALU operations
+// instead of LDS permute round trips.  Every lane of the quad must be active.
+__device__ __forceinline__ float dpp_xor1(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float dpp_xor2(float v)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float quad_sum(float v)
+{
+    v += dpp_xor2(v);
+    v += dpp_xor1(v);
+    return v;
+}
+__device__ __forceinline__ float pair_sum(float v) { return v + dpp_xor1(v); }
+
 
 // ---- MLX affine dequant of one u32 word of nibbles to f16, as the converter
 // rounds it (tools/convert/src/main.rs:4435-4436): RNE_f16(f32(q) * s + b),

@@ -750,6 +750,9 @@ __device__ __forceinline__ void stage_add_norm(const float* __restrict__ x_prev,
 #pragma unroll
                 for (int e = 0; e < 4; ++e) v[m][u][e] = v[m][u][e] + yv[m][u][e];
     }
+    // the rows' sums of squares, then their wave reductions interleaved (a store
+    // between them, as block 0's residual write once was, serialises the rows'
+    // shuffle chains)
     float s[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
@@ -758,13 +761,27 @@ __device__ __forceinline__ void stage_add_norm(const float* __restrict__ x_prev,
         for (int u = 0; u < KR; ++u) {
             const int g = t + u * kNormThreads;
             if (g < H4 && m < rows) {
-                if (blockIdx.x == 0) reinterpret_cast<f4_t*>(x_out + (size_t)m * H)[g] = v[m][u];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) s[m] = s[m] + v[m][u][e] * v[m][u][e];
             }
         }
-        s[m] = group_sum<64>(s[m]);
-        if ((t & 63) == 0) red[t >> 6][m] = s[m];
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) s[m] = s[m] + __shfl_xor(s[m], off, 64);
+    if ((t & 63) == 0) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m) red[t >> 6][m] = s[m];
+    }
+    if (blockIdx.x == 0) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int u = 0; u < KR; ++u) {
+                const int g = t + u * kNormThreads;
+                if (g < H4 && m < rows) reinterpret_cast<f4_t*>(x_out + (size_t)m * H)[g] = v[m][u];
+            }
     }
     __syncthreads();
 #pragma unroll

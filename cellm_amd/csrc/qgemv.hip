@@ -74,8 +74,8 @@ __device__ __forceinline__ void stage_word_q4(u4_t raw, int idx, bool valid, uin
 #pragma unroll
     for (int i = 0; i < 8; ++i) xs += (float)v[i];
     if (valid) *reinterpret_cast<u4_t*>(xq + (size_t)idx * 4) = u4_t{as_u32(p0), as_u32(p1), as_u32(p2), as_u32(p3)};
-    corr = group_sum<4>(corr);
-    xs = group_sum<4>(xs);
+    corr = quad_sum(corr);
+    xs = quad_sum(xs);
     if (valid && (idx & 3) == 0) cx[idx >> 2] = make_float2(1024.0f * corr, xs);
 }
 
@@ -109,8 +109,8 @@ __device__ __forceinline__ void stage_word_q4_x32(f4_t a, f4_t b, int idx, bool 
     float xs = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) xs += xv[i];
-    corr = group_sum<4>(corr);
-    xs = group_sum<4>(xs);
+    corr = quad_sum(corr);
+    xs = quad_sum(xs);
     if (valid && (idx & 3) == 0) cx[idx >> 2] = make_float2(1024.0f * corr, xs);
 }
 
@@ -876,7 +876,7 @@ __device__ __forceinline__ void stage_unit_i8(u4_t raw, int idx, bool valid, uin
 #pragma unroll
     for (int i = 0; i < 8; ++i) s += (float)v[i];
     if (valid) *reinterpret_cast<u4_t*>(xq + (size_t)idx * 4) = u4_t{as_u32(p0), as_u32(p1), as_u32(p2), as_u32(p3)};
-    s = group_sum<2>(s);
+    s = pair_sum(s);
     if (valid && (idx & 1) == 0) cx[idx >> 1] = 1152.0f * s;
 }
 
