@@ -102,6 +102,20 @@ __device__ __forceinline__ float quad_sum(float v)
     return v;
 }
 __device__ __forceinline__ float pair_sum(float v) { return v + dpp_xor1(v); }
+// the xor-4 partner: lanes 0-3 of each 8 read 4 up (row_shl:4), lanes 4-7 read 4 down (row_shr:4)
+__device__ __forceinline__ float dpp_xor4(float v)
+{
+    const int b = __builtin_bit_cast(int, v);
+    const int up = __builtin_amdgcn_update_dpp(0, b, 0x104, 0xF, 0xF, false);
+    const int down = __builtin_amdgcn_update_dpp(0, b, 0x114, 0xF, 0xF, false);
+    return __builtin_bit_cast(float, (threadIdx.x & 4) ? down : up);
+}
+// group_sum<8> in the same order (xor 4, then 2, then 1)
+__device__ __forceinline__ float oct_sum(float v)
+{
+    v += dpp_xor4(v);
+    return quad_sum(v);
+}
 
 
 // ---- MLX affine dequant of one u32 word of nibbles to f16, as the converter

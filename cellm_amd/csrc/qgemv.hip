@@ -1171,7 +1171,10 @@ __device__ __forceinline__ void i4_stage_x(const u4_t (&xr)[XW], const void* __r
             s = (a[0] + a[1]) + (a[2] + a[3]);
             if (valid) *reinterpret_cast<f4_t*>(xs + (size_t)idx * 4) = a;
         }
-        s = group_sum<upc>(s);
+        if constexpr (upc == 8)
+            s = oct_sum(s);
+        else
+            s = quad_sum(s);
         if (valid && idx % upc == 0) cx[idx / upc] = 8.0f * s;
     };
 #pragma unroll
