@@ -1765,15 +1765,17 @@ hipError_t launch_i4_shape(const uint8_t* w, const uint16_t* S, int spr, int cpg
 // Team shapes (measured on the Gemma-3-1B MLP shapes): rows of up to 64
 // chunks (K <= 2048) with enough of them take 16-lane teams of two rows, so
 // each x read from LDS serves two rows (1152->6912: 4.5 us against 5.2 us for
-// one row per team); longer rows take 32 lanes at M > 2 (6912->1152, M = 4:
-// 21 us against 28 us with 64) and pick_shape's single-row teams otherwise.
+// one row per team); longer rows at M = 4 take 64-lane teams of two rows
+// (6912->1152: 14.0 us, against 19.4 us for 32-lane teams of one row and 16.8
+// us for 64-lane teams of four), and pick_shape's single-row teams otherwise.
 template <int MT, int XT>
 hipError_t launch_i4_mt(const uint8_t* w, const uint16_t* S, int spr, int cpg, const void* x, float* y, int M, int N,
                         int K, hipStream_t st)
 {
     const int CPR = K >> 5;
     if (CPR <= 64 && N >= 4096) return launch_i4_shape<16, 2, MT, XT>(w, S, spr, cpg, x, y, M, N, K, st);
-    const int lpr = (MT == 4 && CPR > 64) ? 32 : pick_shape(CPR, N, false).lpr;
+    if (MT == 4 && CPR > 64) return launch_i4_shape<64, 2, MT, XT>(w, S, spr, cpg, x, y, M, N, K, st);
+    const int lpr = pick_shape(CPR, N, false).lpr;
     switch (lpr) {
     case 8: return launch_i4_shape<8, 1, MT, XT>(w, S, spr, cpg, x, y, M, N, K, st);
     case 16: return launch_i4_shape<16, 1, MT, XT>(w, S, spr, cpg, x, y, M, N, K, st);
