@@ -75,18 +75,10 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c)
     return __builtin_amdgcn_fdot2(as_h2(a), as_h2(b), c, false);
 }
 
-// Sum over aligned groups of W lanes (W a power of two <= 64).
-template <int W>
-__device__ __forceinline__ float group_sum(float v)
-{
-#pragma unroll
-    for (int off = W / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, W);
-    return v;
-}
-
-// group_sum<4> and group_sum<2> on DPP quad permutes: the same additions in the
-// same order (the xor-2 partner, then the xor-1 partner), as VALU operations
-// instead of LDS permute round trips.  Every lane of the quad must be active.
+// Butterfly partners on DPP (VALU moves within a 16-lane row, no LDS permute
+// round trip): lane i gets the value of lane i ^ 1, i ^ 2, i ^ 4 or i ^ 8.  xor 1
+// and 2 are quad permutes; xor 4 and 8 pick a row shift up or down by the lane
+// bit.  Every lane read must be active.
 __device__ __forceinline__ float dpp_xor1(float v)
 {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
@@ -95,27 +87,41 @@ __device__ __forceinline__ float dpp_xor2(float v)
 {
     return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
 }
-__device__ __forceinline__ float quad_sum(float v)
-{
-    v += dpp_xor2(v);
-    v += dpp_xor1(v);
-    return v;
-}
-__device__ __forceinline__ float pair_sum(float v) { return v + dpp_xor1(v); }
-// the xor-4 partner: lanes 0-3 of each 8 read 4 up (row_shl:4), lanes 4-7 read 4 down (row_shr:4)
-__device__ __forceinline__ float dpp_xor4(float v)
+// lanes with bit `B` clear read B lanes up (row_shl:B), the others B lanes down (row_shr:B)
+template <int B>
+__device__ __forceinline__ float dpp_xor_row(float v)
 {
     const int b = __builtin_bit_cast(int, v);
-    const int up = __builtin_amdgcn_update_dpp(0, b, 0x104, 0xF, 0xF, false);
-    const int down = __builtin_amdgcn_update_dpp(0, b, 0x114, 0xF, 0xF, false);
-    return __builtin_bit_cast(float, (threadIdx.x & 4) ? down : up);
+    const int up = __builtin_amdgcn_update_dpp(0, b, 0x100 + B, 0xF, 0xF, false);
+    const int down = __builtin_amdgcn_update_dpp(0, b, 0x110 + B, 0xF, 0xF, false);
+    return __builtin_bit_cast(float, (threadIdx.x & B) ? down : up);
 }
-// group_sum<8> in the same order (xor 4, then 2, then 1)
-__device__ __forceinline__ float oct_sum(float v)
+template <int OFF>
+__device__ __forceinline__ float lane_xor(float v, int width)
 {
-    v += dpp_xor4(v);
-    return quad_sum(v);
+    if constexpr (OFF == 1) return dpp_xor1(v);
+    else if constexpr (OFF == 2) return dpp_xor2(v);
+    else if constexpr (OFF == 4 || OFF == 8) return dpp_xor_row<OFF>(v);
+    else return __shfl_xor(v, OFF, width);
 }
+
+// Sum over aligned groups of W lanes (W a power of two <= 64): the butterfly
+// v += partner(v ^ off) for off = W/2 .. 1, with offsets below 16 on DPP.
+// Every lane of a group must be active.
+template <int W>
+__device__ __forceinline__ float group_sum(float v)
+{
+    if constexpr (W >= 64) v += lane_xor<32>(v, W);
+    if constexpr (W >= 32) v += lane_xor<16>(v, W);
+    if constexpr (W >= 16) v += lane_xor<8>(v, W);
+    if constexpr (W >= 8) v += lane_xor<4>(v, W);
+    if constexpr (W >= 4) v += lane_xor<2>(v, W);
+    if constexpr (W >= 2) v += lane_xor<1>(v, W);
+    return v;
+}
+__device__ __forceinline__ float quad_sum(float v) { return group_sum<4>(v); }
+__device__ __forceinline__ float pair_sum(float v) { return group_sum<2>(v); }
+__device__ __forceinline__ float oct_sum(float v) { return group_sum<8>(v); }
 
 
 // ---- MLX affine dequant of one u32 word of nibbles to f16, as the converter

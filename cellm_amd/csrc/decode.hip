@@ -435,16 +435,16 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         float d = dot[g];
-        d = d + __shfl_xor(d, 1);
-        d = d + __shfl_xor(d, 2);
+        d = d + lane_xor<1>(d, 64);
+        d = d + lane_xor<2>(d, 64);
         float sg = d * scale;
         if (soft_cap > 0.0f) sg = tanhf(sg / soft_cap) * soft_cap;  // kvcache.rs:768-770
         sc[g] = valid ? sg : -INFINITY;
         float m = sc[g];
-        m = fmaxf(m, __shfl_xor(m, 4));
-        m = fmaxf(m, __shfl_xor(m, 8));
-        m = fmaxf(m, __shfl_xor(m, 16));
-        m = fmaxf(m, __shfl_xor(m, 32));
+        m = fmaxf(m, lane_xor<4>(m, 64));
+        m = fmaxf(m, lane_xor<8>(m, 64));
+        m = fmaxf(m, lane_xor<16>(m, 64));
+        m = fmaxf(m, lane_xor<32>(m, 64));
         if (lane == 0) wmax[wave][g] = m;
     }
     __syncthreads();
@@ -454,10 +454,10 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
         const float e = valid ? expf(sc[g] - m) : 0.0f;
         if (kq == 0) ps[g][kp] = e;
         float l = e;
-        l = l + __shfl_xor(l, 4);
-        l = l + __shfl_xor(l, 8);
-        l = l + __shfl_xor(l, 16);
-        l = l + __shfl_xor(l, 32);
+        l = l + lane_xor<4>(l, 64);
+        l = l + lane_xor<8>(l, 64);
+        l = l + lane_xor<16>(l, 64);
+        l = l + lane_xor<32>(l, 64);
         if (lane == 0) wsum[wave][g] = l;
     }
     __syncthreads();
@@ -628,17 +628,17 @@ __global__ __launch_bounds__(kAttnBlockThreads) void attn_head_kernel(
             for (int e = 0; e < 8; ++e) dot = dot + qs[kq * KD + j * 8 + e] * (float)kh[e];
         }
         const bool valid = s * kAttnBlockSub + wave * 16 + (lane >> 2) < seq;
-        dot = dot + __shfl_xor(dot, 1);
-        dot = dot + __shfl_xor(dot, 2);
+        dot = dot + lane_xor<1>(dot, 64);
+        dot = dot + lane_xor<2>(dot, 64);
         float sg = dot * scale;
         if (soft_cap > 0.0f) sg = tanhf(sg / soft_cap) * soft_cap;  // kvcache.rs:768-770
         sc[s] = valid ? sg : -INFINITY;
         mloc = fmaxf(mloc, sc[s]);
     }
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 4));
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 8));
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+    mloc = fmaxf(mloc, lane_xor<4>(mloc, 64));
+    mloc = fmaxf(mloc, lane_xor<8>(mloc, 64));
+    mloc = fmaxf(mloc, lane_xor<16>(mloc, 64));
+    mloc = fmaxf(mloc, lane_xor<32>(mloc, 64));
     if (lane == 0) wmax[wave] = mloc;
     __syncthreads();
     // weights e^(s - M) into LDS (one lane of each position), and the wave sums
@@ -653,10 +653,10 @@ __global__ __launch_bounds__(kAttnBlockThreads) void attn_head_kernel(
         if (kq == 0) ps[s * kAttnBlockSub + wave * 16 + (lane >> 2)] = e;
         l = l + e;
     }
-    l = l + __shfl_xor(l, 4);
-    l = l + __shfl_xor(l, 8);
-    l = l + __shfl_xor(l, 16);
-    l = l + __shfl_xor(l, 32);
+    l = l + lane_xor<4>(l, 64);
+    l = l + lane_xor<8>(l, 64);
+    l = l + lane_xor<16>(l, 64);
+    l = l + lane_xor<32>(l, 64);
     if (lane == 0) wsum[wave] = l;
     __syncthreads();
 
@@ -767,9 +767,7 @@ __device__ __forceinline__ void stage_add_norm(const float* __restrict__ x_prev,
         }
     }
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1)
-#pragma unroll
-        for (int m = 0; m < MT; ++m) s[m] = s[m] + __shfl_xor(s[m], off, 64);
+    for (int m = 0; m < MT; ++m) s[m] = group_sum<64>(s[m]);
     if ((t & 63) == 0) {
 #pragma unroll
         for (int m = 0; m < MT; ++m) red[t >> 6][m] = s[m];

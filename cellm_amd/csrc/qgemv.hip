@@ -709,10 +709,10 @@ __global__ __launch_bounds__(kRingThreads) void qgemv_q4_ring_kernel(const u4_t*
 #pragma unroll
         for (int i = 0; i < 4; ++i) a4[i] = (b16 ? v[i + 4] : v[i]) + __shfl_xor(b16 ? v[i] : v[i + 4], 16, 32);
 #pragma unroll
-        for (int i = 0; i < 2; ++i) a2[i] = (b8 ? a4[i + 2] : a4[i]) + __shfl_xor(b8 ? a4[i] : a4[i + 2], 8, 32);
-        a1 = (b4 ? a2[1] : a2[0]) + __shfl_xor(b4 ? a2[0] : a2[1], 4, 32);
-        a1 += __shfl_xor(a1, 2, 32);
-        a1 += __shfl_xor(a1, 1, 32);
+        for (int i = 0; i < 2; ++i) a2[i] = (b8 ? a4[i + 2] : a4[i]) + lane_xor<8>(b8 ? a4[i] : a4[i + 2], 32);
+        a1 = (b4 ? a2[1] : a2[0]) + lane_xor<4>(b4 ? a2[0] : a2[1], 32);
+        a1 += lane_xor<2>(a1, 32);
+        a1 += lane_xor<1>(a1, 32);
         // the lane now holds step s = 4*b16 + 2*b8 + b4 of the batch
         const int s = (b16 ? 4 : 0) + (b8 ? 2 : 0) + (b4 ? 1 : 0);
         if ((c & 3) == 0) park[16 * bi + 2 * s + h] = a1;
@@ -846,8 +846,8 @@ __global__ __launch_bounds__(kFlatThreads) void qgemv_q4_flat_kernel(const u4_t*
         float s = 0.0f;
 #pragma unroll
         for (int t = 0; t < J; ++t) s += red[rr * RS + q + 4 * t];
-        s += __shfl_xor(s, 1);
-        s += __shfl_xor(s, 2);
+        s += lane_xor<1>(s, 64);
+        s += lane_xor<2>(s, 64);
         if (q == 0) park[16 * bi + rr] = s;
         __builtin_amdgcn_wave_barrier();
     };
