@@ -96,18 +96,36 @@ __device__ __forceinline__ float dpp_xor_row(float v)
     const int down = __builtin_amdgcn_update_dpp(0, b, 0x110 + B, 0xF, 0xF, false);
     return __builtin_bit_cast(float, (threadIdx.x & B) ? down : up);
 }
+// xor 16 and 32 with the gfx950 lane swaps: v_permlane16_swap exchanges the odd
+// 16-lane rows of its first operand with the even rows of its second, and
+// v_permlane32_swap the upper half of the first with the lower half of the
+// second; with v in both, the partner's value is in the first result for lanes
+// with the bit set and in the second for the others.
+template <int B>
+__device__ __forceinline__ float swap_xor(float v)
+{
+    const int b = __builtin_bit_cast(int, v);
+    if constexpr (B == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+        return __builtin_bit_cast(float, (threadIdx.x & 16) ? r[0] : r[1]);
+    } else {
+        const auto r = __builtin_amdgcn_permlane32_swap(b, b, false, false);
+        return __builtin_bit_cast(float, (threadIdx.x & 32) ? r[0] : r[1]);
+    }
+}
 template <int OFF>
 __device__ __forceinline__ float lane_xor(float v, int width)
 {
+    (void)width;  // every partner lies inside the aligned group of `width` lanes
     if constexpr (OFF == 1) return dpp_xor1(v);
     else if constexpr (OFF == 2) return dpp_xor2(v);
     else if constexpr (OFF == 4 || OFF == 8) return dpp_xor_row<OFF>(v);
-    else return __shfl_xor(v, OFF, width);
+    else return swap_xor<OFF>(v);
 }
 
 // Sum over aligned groups of W lanes (W a power of two <= 64): the butterfly
-// v += partner(v ^ off) for off = W/2 .. 1, with offsets below 16 on DPP.
-// Every lane of a group must be active.
+// v += partner(v ^ off) for off = W/2 .. 1, every step a VALU lane move (DPP
+// below 16, the lane swaps at 16 and 32).  Every lane of a group must be active.
 template <int W>
 __device__ __forceinline__ float group_sum(float v)
 {
