@@ -30,6 +30,7 @@
 // against the reference CPU order in tests/).
 #include <algorithm>
 #include <mutex>
+#include <type_traits>
 #include <vector>
 
 #include "common.hpp"
@@ -807,13 +808,16 @@ __global__ __launch_bounds__(kFlatThreads) void qgemv_q4_flat_kernel(const u4_t*
     }
     const uint32_t m0f = 0x000F000Fu, m1f = 0x00F000F0u, magic = 0x64006400u;
     const int rr = lane >> 2, q = lane & 3;
-    auto batch = [&](int bi, int slot) {
+    // NEXT: issue the following batch's loads (every batch but a wave's last, so that no load is
+    // left in flight past the loop: the stores after it reuse those registers and would wait for it)
+    auto batch = [&](int bi, int slot, auto next) {
+        constexpr bool NEXT = decltype(next)::value;
         // this batch's scale/bias rows -> LDS (loaded a batch ago); next batch's load.  Lanes past the
         // rows write the spare last 16 bytes of the S slot (free whenever such lanes exist): a store
         // under a branch made the compiler wait for every load in flight.
         *reinterpret_cast<u4_t*>(sbw + (lane < sbrow ? lane * 16 : (lane < 2 * sbrow ? 512 + (lane - sbrow) * 16 : 496))) =
             sbr;
-        load_sb(bi + 1);
+        if constexpr (NEXT) load_sb(bi + 1);
         __builtin_amdgcn_wave_barrier();
 #pragma unroll
         for (int j = 0; j < J; ++j) {
@@ -821,7 +825,7 @@ __global__ __launch_bounds__(kFlatThreads) void qgemv_q4_flat_kernel(const u4_t*
             // the next batch's load leave ahead of this chunk's dot instead of after it
             u4_t w = wr[slot][j];
             asm("" : "+v"(w));
-            load_w(bi + D, slot, j);
+            if constexpr (NEXT) load_w(bi + D, slot, j);
             float sc, bb;
             if constexpr (SBT == DT_F32) {
                 sc = *reinterpret_cast<const float*>(sbw + soff[j]);
@@ -852,10 +856,14 @@ __global__ __launch_bounds__(kFlatThreads) void qgemv_q4_flat_kernel(const u4_t*
         __builtin_amdgcn_wave_barrier();
     };
     static_assert(D == 1 || D == 2, "one or two batches in flight");
-    for (int bi = 0; bi < nb; bi += D) {
-        batch(bi, 0);
-        if constexpr (D == 2) {
-            if (bi + 1 < nb) batch(bi + 1, 1);
+    using with_next = std::integral_constant<bool, true>;
+    if constexpr (D == 1) {
+        for (int bi = 0; bi + 1 < nb; ++bi) batch(bi, 0, with_next{});
+        if (nb > 0) batch(nb - 1, 0, std::integral_constant<bool, false>{});
+    } else {
+        for (int bi = 0; bi < nb; bi += D) {
+            batch(bi, 0, with_next{});
+            if (bi + 1 < nb) batch(bi + 1, 1, with_next{});
         }
     }
     for (int i = lane; i < 16 * nb; i += 64) y[16 * (gw + GW * (i >> 4)) + (i & 15)] = park[i];
