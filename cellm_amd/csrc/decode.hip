@@ -541,8 +541,10 @@ __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(const float*
 
 // Whole-sequence attention in one block per (row, query head), for caches of
 // at most S * 256 positions.  16 waves; wave w owns positions
-// 256 s + 16 w .. + 15 of each sub-chunk s, with attn_partial_kernel's
-// per-wave mapping (Q.K: 4 lanes per position, P.V: HD/64 dims per lane).
+// 256 s + 16 w .. + 15 of each sub-chunk s: Q.K with 4 lanes per position
+// (attn_partial_kernel's mapping), P.V with 32 lanes per position and HD/32
+// dims per lane, the two half-waves on alternate positions (one 4- or 8-byte
+// V load per lane covers two positions), added across halves at the end.
 // Every K and V load of the sequence is issued before any arithmetic and the
 // softmax max and sum are reduced across the block in LDS, so the head's
 // output is the block's only global write:
@@ -565,8 +567,8 @@ __global__ __launch_bounds__(kAttnBlockThreads) void attn_head_kernel(
     constexpr int NW = kAttnBlockWaves, CAP = S * kAttnBlockSub;
     constexpr int KD = HD / 4;  // Q.K dims per lane
     constexpr int KL = KD / 8;  // 16-byte K loads per lane and sub-chunk
-    constexpr int VD = HD / 64; // P.V dims per lane
-    using vword_t = typename std::conditional<VD == 1, uint16_t, uint32_t>::type;
+    constexpr int VD = HD / 32; // P.V dims per lane: 32 lanes per position, two positions per load
+    using vword_t = typename std::conditional<VD == 2, uint32_t, u2_t>::type;
     __shared__ float qs[HD];
     __shared__ float ps[CAP];
     __shared__ long long bases[CAP];
@@ -602,17 +604,19 @@ __global__ __launch_bounds__(kAttnBlockThreads) void attn_head_kernel(
 #pragma unroll
         for (int j = 0; j < KL; ++j) kraw[s][j] = ksrc[j];
     }
-    vword_t vraw[S][16];
+    // V: lane l reads dims VD (l % 32) .. + VD - 1 of position 2i + l / 32 of the wave's 16
+    const int vh = lane >> 5, vl = lane & 31;
+    vword_t vraw[S][8];
     uint32_t vok[S];
 #pragma unroll
     for (int s = 0; s < S; ++s) {
         vok[s] = 0;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const long long vb = bases[s * kAttnBlockSub + wave * 16 + i];
+        for (int i = 0; i < 8; ++i) {
+            const long long vb = bases[s * kAttnBlockSub + wave * 16 + 2 * i + vh];
             vok[s] |= (vb >= 0 ? 1u : 0u) << i;
             vraw[s][i] =
-                *reinterpret_cast<const vword_t*>(vc + (vb >= 0 ? vb + (long long)kvh * HD + lane * VD : 0));
+                *reinterpret_cast<const vword_t*>(vc + (vb >= 0 ? vb + (long long)kvh * HD + vl * VD : 0));
         }
     }
 
@@ -667,25 +671,34 @@ __global__ __launch_bounds__(kAttnBlockThreads) void attn_head_kernel(
 #pragma unroll
     for (int s = 0; s < S; ++s)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const vword_t w = (vok[s] >> i) & 1u ? vraw[s][i] : vword_t(0);
-            const float pg = ps[s * kAttnBlockSub + wave * 16 + i];
-            if constexpr (VD == 1) {
-                acc[0] = acc[0] + pg * h2f(w);
-            } else {
+        for (int i = 0; i < 8; ++i) {
+            const float pg = ps[s * kAttnBlockSub + wave * 16 + 2 * i + vh];
+            const bool ok = (vok[s] >> i) & 1u;
+            if constexpr (VD == 2) {
+                const uint32_t w = ok ? vraw[s][i] : 0u;
                 acc[0] = acc[0] + pg * h2f((uint16_t)(w & 0xffffu));
                 acc[1] = acc[1] + pg * h2f((uint16_t)(w >> 16));
+            } else {
+                const u2_t w = ok ? vraw[s][i] : u2_t{0u, 0u};
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    acc[2 * e] = acc[2 * e] + pg * h2f((uint16_t)(w[e] & 0xffffu));
+                    acc[2 * e + 1] = acc[2 * e + 1] + pg * h2f((uint16_t)(w[e] >> 16));
+                }
             }
         }
-    // across the waves: 8..15 onto 0..7, then the eight in order
-    if (wave >= NW / 2) {
+    // the two half-waves hold the even and odd positions: add across them
 #pragma unroll
-        for (int d = 0; d < VD; ++d) accs[wave - NW / 2][lane * VD + d] = acc[d];
+    for (int d = 0; d < VD; ++d) acc[d] = acc[d] + lane_xor<32>(acc[d], 64);
+    // across the waves: 8..15 onto 0..7, then the eight in order
+    if (wave >= NW / 2 && vh == 0) {
+#pragma unroll
+        for (int d = 0; d < VD; ++d) accs[wave - NW / 2][vl * VD + d] = acc[d];
     }
     __syncthreads();
-    if (wave < NW / 2) {
+    if (wave < NW / 2 && vh == 0) {
 #pragma unroll
-        for (int d = 0; d < VD; ++d) accs[wave][lane * VD + d] = acc[d] + accs[wave][lane * VD + d];
+        for (int d = 0; d < VD; ++d) accs[wave][vl * VD + d] = acc[d] + accs[wave][vl * VD + d];
     }
     __syncthreads();
     if (t < HD) {
