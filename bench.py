@@ -33,6 +33,8 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, published
 BASELINE_METRIC = "int4/int8 qGEMV µs & HBM GB/s (% peak); M=512 qGEMM TFLOP/s (% MFMA)"
+WARM_MIN_S = 0.05              # least warm-up time before the timed steps (see main)
+CACHE_BYTES = 512 * 2**20      # every timed loop rotates through more weight bytes than this (2x the MALL)
 
 QWEN_SHAPES = [("qkv", 896, 1152), ("o", 896, 896), ("gate_up", 896, 9728), ("down", 4864, 896),
                ("lm_head", 896, 151936)]
@@ -181,6 +183,18 @@ def pmc_sample(torch, ops, stream, gen, which: str):
     print(json.dumps({"pmc_sample": info}))
 
 
+def q4_copies(torch, n: int, k: int, gen, min_bytes: int = CACHE_BYTES):
+    """R copies of one q4 g64 weight (f16 S/B) with R * bytes > min_bytes, allocated as three
+    tensors; returns R and the list of (wq, s, b) views."""
+    g = (k + 63) // 64
+    wbytes = n * k // 2 + 4 * n * g
+    r = max(2, -(-min_bytes // wbytes) + 1)
+    wq = torch.randint(-2**31, 2**31 - 1, (r, n, k // 8), dtype=torch.int32, device="cuda", generator=gen)
+    s = (torch.randn((r, n, g), device="cuda", generator=gen) * 0.005 + 0.02).abs_().to(torch.float16)
+    b = (torch.randn((r, n, g), device="cuda", generator=gen) * 0.05).to(torch.float16)
+    return r, [(wq[i], s[i], b[i]) for i in range(r)]
+
+
 class Q4Weights:
     def __init__(self, torch, n: int, k: int, gen):
         self.n, self.k = n, k
@@ -287,9 +301,18 @@ def main():
     def step(i):
         ops.encode_qgemv_batch(step_arrays[i % copies], stream=sptr)
 
-    for i in range(args.warmup):
-        step(i)
+    # Warm-up: the W steps asked for, and at least one pass over every weight copy and WARM_MIN_S
+    # seconds of steps.  Right after the weights are written, the first steps of a fresh process
+    # read 40-55 us where every later one reads ~29 us (first touch of each copy's pages, clocks
+    # still rising): W = 5 steps touch only 5 of the copies.  The extra steps are reported.
+    warm_steps, t_warm = 0, time.perf_counter()
+    while warm_steps < max(args.warmup, copies) or time.perf_counter() - t_warm < WARM_MIN_S:
+        step(warm_steps)
+        warm_steps += 1
+        if warm_steps % 64 == 0:
+            torch.cuda.synchronize()  # keep the queue short
     torch.cuda.synchronize()
+    warm_s = time.perf_counter() - t_warm
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     ev0.record(stream)
@@ -302,16 +325,25 @@ def main():
     ms_per_step = ms_total / args.steps
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
 
-    # ---- per-shape latency (rotating copies) and the dominant kernel's roofline --
+    del step_arrays, sets
+    torch.cuda.empty_cache()
+
+    # ---- per-shape latency and the dominant kernel's roofline ---------------------
+    # Each shape rotates through its own R weight copies with R * W > CACHE_BYTES (one op per copy
+    # in the timed batch), so every launch reads its weights from HBM.
     per_shape = {}
     for j, (name, k, n) in enumerate(QWEN_SHAPES):
-        arr = op_array([ops.qgemv_op_q4_affine(sets[i % copies][j].wq, sets[i % copies][j].s, sets[i % copies][j].b,
-                                               xs[j], ys[j]) for i in range(100)])
-        ms = time_batch(torch, ops, arr, stream)
+        r_copies, wset = q4_copies(torch, n, k, gen)
+        arr = op_array([ops.qgemv_op_q4_affine(*wset[i % r_copies], xs[j], ys[j]) for i in range(max(100, r_copies))])
+        ms = time_batch(torch, ops, arr, stream, reps=1 if len(arr) > 100 else 5)
         gbs = q4_bytes(1, n, k) / (ms * 1e-3) / 1e9
         per_shape[f"{name}_{k}x{n}"] = {"us": round(ms * 1e3, 3), "GB/s": round(gbs, 1),
                                         "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
-                                        "isolated_us": isolated_launch_us(torch, ops, arr, stream)}
+                                        "isolated_us": isolated_launch_us(torch, ops, arr, stream),
+                                        "weight_copies": r_copies,
+                                        "bytes_rotated": r_copies * (n * k // 2 + 4 * n * ((k + 63) // 64))}
+        del arr, wset
+        torch.cuda.empty_cache()
     dom = per_shape["lm_head_896x151936"]
     traffic = None
     tfile = ROOT / "profiles" / "traffic_q4_gemv_lm_head.json"
@@ -324,8 +356,6 @@ def main():
                 "frac": round(dom["GB/s"] / HBM_PEAK_GBS, 4), "traffic": traffic,
                 "kernel": "qgemv_q4_flat_kernel (896->151936 lm_head, M=1)",
                 "algorithmic_bytes": q4_bytes(1, 151936, 896)}
-    del sets
-    torch.cuda.empty_cache()
 
     extra = {}
     if not args.no_extra:
@@ -360,6 +390,7 @@ def main():
                                "896->1152, 896->896, 896->9728, 4864->896, 896->151936",
                    "weight_copies_rotated": copies, "bytes_per_step": step_bytes,
                    "timing": "HIP events on the launch stream; a step is one cellm_hip_qgemv_batch call",
+                   "warmup_steps_run": warm_steps, "warmup_s": round(warm_s, 3),
                    "frac_hbm_peak": round(value / HBM_PEAK_GBS, 4), "wall_s": round(wall, 3)},
         "per_shape": per_shape,
         "roofline": roofline,

@@ -54,6 +54,12 @@ SIGNATURES = {
                                                _i64, _i64, _i64, _vp]),
     "cellm_hip_qgemv_q4_affine_gate_up_silu": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _vp, _i32, _vp,
                                                       _i64, _i64, _i64, _vp]),
+    "cellm_hip_qgemv_i8_gate_up_gelu": (_i32, [_vp, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i32, _vp, _i32, _vp,
+                                               _i64, _i64, _i64, _vp]),
+    "cellm_hip_qgemv_q4_affine_gate_up_gelu": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _vp, _i32, _vp,
+                                                      _i64, _i64, _i64, _vp]),
+    "cellm_hip_qgemv_i4_gate_up_gelu": (_i32, [_vp, _vp, _vp, _i64, _vp, _vp, _i64, _i64, _vp, _i32, _vp, _i64, _i64,
+                                               _i64, _vp]),
     "cellm_hip_qgemv_i4_sym": (_i32, [_vp, _vp, _vp, _i64, _i64, _vp, _i32, _vp, _i64, _i64, _i64, _vp]),
     "cellm_hip_qgemm_q4_affine": (_i32, [_vp, _vp, _vp, _vp, _i32, _i64, _vp, _vp, _i64, _i64, _i64, _vp]),
     "cellm_hip_qgemm_i8": (_i32, [_vp, _vp, _vp, _i32, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
@@ -77,6 +83,8 @@ SIGNATURES = {
                                              _i64, _vp, _vp]),
     "cellm_hip_add_rms_norm": (_i32, [_vp, _vp, _vp, _vp, _i32, _i64, _i64, C.c_float, _vp, _vp]),
     "cellm_hip_rope_half_f32": (_i32, [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp]),
+    "cellm_hip_rope_interleaved_f32": (_i32, [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp]),
+    "cellm_hip_set_rope_interleaved": (_i32, [_vp, _i32]),
     "cellm_hip_rope_kv_write_f16": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp,
                                            _i64, _i64, _i64, _i64, _i64, _vp]),
     "cellm_hip_kv_write_f16": (_i32, [_vp, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64,
@@ -86,6 +94,7 @@ SIGNATURES = {
     "cellm_hip_attention_gqa_f16kv_noalloc": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i64,
                                                      _i64, _i64, _i64, C.c_float, C.c_float, _vp, _vp]),
     "cellm_hip_silu_mul_f32": (_i32, [_vp, _vp, _vp, _i64, _vp]),
+    "cellm_hip_gelu_tanh_mul_f32": (_i32, [_vp, _vp, _vp, _i64, _vp]),
     "cellm_hip_add_f32_inplace": (_i32, [_vp, _vp, _vp, _i64, _vp]),
     "cellm_hip_argmax_f32": (_i32, [_vp, _vp, _i64, _i64, _vp, _vp, _vp]),
 }

@@ -195,13 +195,17 @@ def write_cellm(path, header: dict, tensors, version: int = 1, magic: bytes = b"
         return h, json.dumps(h).encode()
 
     offs = layout(0)
-    for _ in range(4):  # offsets depend on the header length and vice versa: iterate to a fixed point
+    for _ in range(8):  # offsets depend on the header length and vice versa: iterate to a fixed point
         h, text = build(offs)
         new = layout(len(text))
         if new == offs:
             break
         offs = new
     h, text = build(offs)
+    if layout(len(text)) != offs:
+        # a header whose length moved a tensor after the last pass would put the data at other offsets
+        # than the header states: refuse instead of writing a corrupt file
+        raise ValueError("write_cellm: header offsets did not converge")
     with open(path, "wb") as f:
         f.write(magic)
         f.write(struct.pack("<B", version))

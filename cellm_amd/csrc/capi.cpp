@@ -12,6 +12,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <atomic>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -101,6 +102,7 @@ struct cellm_hip_ctx {
     std::unordered_map<hipStream_t, DeviceBuffer> aux;         // unfused gate/up: the up rows, one per stream
     std::unordered_map<hipStream_t, DeviceBuffer> attn;        // split-sequence attention partials, one per stream
     float* attn_static = nullptr;  // this device's static attention scratch (cellm_hip_attention_gqa_f16kv_noalloc)
+    std::atomic<int> rope_interleaved{0};  // RoPE pairs of the fused decode ops (cellm_hip_set_rope_interleaved)
 };
 
 namespace {
@@ -266,7 +268,7 @@ int32_t qgemv_lowbit_impl(int fmt, const void* w, const uint16_t* scales_f16, in
     if (fmt == LB_F16 && (reinterpret_cast<uintptr_t>(w) & 1))
         return set_error(CELLM_HIP_ERR_INVALID_ARG, "f16 weights must be 2-byte aligned");
     if (k == 0) {
-        HIP_TRY(hipMemsetAsync(y, 0, (size_t)m * n * sizeof(float), st), "hipMemsetAsync(y)");
+        HIP_TRY(launch_fill_f32(y, 0.0f, (size_t)m * n, st), "zero fill of y");
         return CELLM_HIP_OK;
     }
     HIP_TRY(launch_qgemv_lowbit(fmt, w, scales_f16, scale_mode, x, xdt, y, (int)m, (int)n, (int)k, st),
@@ -335,7 +337,7 @@ int32_t qkv_i8_impl(cellm_hip_ctx* ctx, const int8_t* const w[3], const void* co
     for (int i = 0; i < 3; ++i)
         segs[i] = I8FusedSeg{w[i], s[i], b[i], y[i], (int)rows[i], n_s[i] >= rows[i] ? 1 : 0};
     if (k > 0 && qgemv_i8_fused_supported(xdt, (int)m, (int)k, x, segs, 3)) {
-        HIP_TRY(launch_qgemv_i8_fused(segs, 3, false, sdt, x, xdt, (int)m, (int)k, st), "qgemv_i8_qkv launch");
+        HIP_TRY(launch_qgemv_i8_fused(segs, 3, false, ACT_SILU, sdt, x, xdt, (int)m, (int)k, st), "qgemv_i8_qkv launch");
         return CELLM_HIP_OK;
     }
     for (int i = 0; i < 3; ++i)
@@ -347,7 +349,7 @@ int32_t qkv_i8_impl(cellm_hip_ctx* ctx, const int8_t* const w[3], const void* co
 
 int32_t gate_up_i8_impl(cellm_hip_ctx* ctx, const int8_t* wg, const void* sg, int64_t n_sg, const float* bg,
                         const int8_t* wu, const void* su, int64_t n_su, const float* bu, int32_t sdt, const void* x,
-                        int32_t xdt, float* h, int64_t m, int64_t n, int64_t k, hipStream_t st)
+                        int32_t xdt, float* h, int64_t m, int64_t n, int64_t k, int act, hipStream_t st)
 {
     if (int32_t rc = check_dims(m, n, k)) return rc;
     if (!valid_dtype(sdt) || !valid_dtype(xdt)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "bad dtype");
@@ -358,20 +360,20 @@ int32_t gate_up_i8_impl(cellm_hip_ctx* ctx, const int8_t* wg, const void* sg, in
     I8FusedSeg segs[2] = {I8FusedSeg{wg, sg, bg, h, (int)n, n_sg >= n ? 1 : 0},
                           I8FusedSeg{wu, su, bu, nullptr, (int)n, n_su >= n ? 1 : 0}};
     if (k > 0 && qgemv_i8_fused_supported(xdt, (int)m, (int)k, x, segs, 2)) {
-        HIP_TRY(launch_qgemv_i8_fused(segs, 2, true, sdt, x, xdt, (int)m, (int)k, st), "qgemv_i8_gate_up_silu launch");
+        HIP_TRY(launch_qgemv_i8_fused(segs, 2, true, act, sdt, x, xdt, (int)m, (int)k, st), "qgemv_i8 gate/up launch");
         return CELLM_HIP_OK;
     }
     float* up = nullptr;
     if (int32_t rc = get_stream_buffer(ctx, ctx->aux, st, (size_t)m * n * sizeof(float), &up)) return rc;
     if (int32_t rc = qgemv_i8_impl(ctx, wg, sg, sdt, n_sg, x, xdt, bg, h, m, n, k, st, false)) return rc;
     if (int32_t rc = qgemv_i8_impl(ctx, wu, su, sdt, n_su, x, xdt, bu, up, m, n, k, st, false)) return rc;
-    HIP_TRY(launch_silu_mul(h, up, (size_t)m * n, st), "silu_mul launch");
+    HIP_TRY(launch_act_mul(act, h, up, (size_t)m * n, st), "activation * up launch");
     return CELLM_HIP_OK;
 }
 
 int32_t gate_up_q4_impl(cellm_hip_ctx* ctx, const uint32_t* wg, const void* sg, const void* bg, const uint32_t* wu,
                         const void* su, const void* bu, int32_t sbt, int64_t group, const void* x, int32_t xdt,
-                        float* h, int64_t m, int64_t n, int64_t k, hipStream_t st)
+                        float* h, int64_t m, int64_t n, int64_t k, int act, hipStream_t st)
 {
     if (int32_t rc = check_dims(m, n, k)) return rc;
     if (int32_t rc = check_group(group)) return rc;
@@ -382,15 +384,15 @@ int32_t gate_up_q4_impl(cellm_hip_ctx* ctx, const uint32_t* wg, const void* sg, 
         return set_error(CELLM_HIP_ERR_INVALID_ARG, "null input pointer");
     if (qgemv_q4_gate_up_supported(xdt, (int)m, (int)k, (int)group, x, wg, wu)) {
         HIP_TRY(launch_qgemv_q4_gate_up_silu(wg, sg, bg, wu, su, bu, sbt, (int)group, x, xdt, h, (int)m, (int)n, (int)k,
-                                             st),
-                "qgemv_q4_gate_up_silu launch");
+                                             act, st),
+                "qgemv_q4 gate/up launch");
         return CELLM_HIP_OK;
     }
     float* up = nullptr;
     if (int32_t rc = get_stream_buffer(ctx, ctx->aux, st, (size_t)m * n * sizeof(float), &up)) return rc;
     if (int32_t rc = qgemv_q4_impl(ctx, wg, sg, bg, sbt, group, x, xdt, h, m, n, k, st, false)) return rc;
     if (int32_t rc = qgemv_q4_impl(ctx, wu, su, bu, sbt, group, x, xdt, up, m, n, k, st, false)) return rc;
-    HIP_TRY(launch_silu_mul(h, up, (size_t)m * n, st), "silu_mul launch");
+    HIP_TRY(launch_act_mul(act, h, up, (size_t)m * n, st), "activation * up launch");
     return CELLM_HIP_OK;
 }
 
@@ -513,12 +515,12 @@ int32_t cellm_hip_create(int32_t device, cellm_hip_ctx_t** out_ctx)
         delete ctx;
         return hip_error(e, "hipStreamCreate");
     }
-    // the device address of the static attention scratch, with the device current
-    e = attention_static_scratch(&ctx->attn_static);
-    if (e != hipSuccess) {
-        (void)hipStreamDestroy(ctx->stream);
-        delete ctx;
-        return hip_error(e, "hipGetSymbolAddress(attention scratch)");
+    // The device address of the static attention scratch, with the device current.  Only
+    // cellm_hip_attention_gqa_f16kv_noalloc needs it: a failure here leaves it null, and that
+    // entry point tries again on its first call and reports the error itself.
+    if (attention_static_scratch(&ctx->attn_static) != hipSuccess) {
+        ctx->attn_static = nullptr;
+        (void)hipGetLastError();
     }
     *out_ctx = ctx;
     return CELLM_HIP_OK;
@@ -758,8 +760,22 @@ int32_t cellm_hip_qgemv_i8_gate_up_silu(cellm_hip_ctx_t* ctx, const int8_t* wg, 
     if (int32_t rc = check_ctx(ctx)) return rc;
     DeviceGuard g(ctx->device);
     const std::lock_guard<std::recursive_mutex> lk(ctx->mu);  // held until the scratch users are enqueued
-    return gate_up_i8_impl(ctx, wg, sg, n_sg, bg, wu, su, n_su, bu, scale_dtype, x, x_dtype, h, m, n, k,
+    return gate_up_i8_impl(ctx, wg, sg, n_sg, bg, wu, su, n_su, bu, scale_dtype, x, x_dtype, h, m, n, k, ACT_SILU,
                            pick_stream(ctx, stream));
+    CELLM_API_END(report_exception)
+}
+
+int32_t cellm_hip_qgemv_i8_gate_up_gelu(cellm_hip_ctx_t* ctx, const int8_t* wg, const void* sg, int64_t n_sg,
+                                        const float* bg, const int8_t* wu, const void* su, int64_t n_su,
+                                        const float* bu, int32_t scale_dtype, const void* x, int32_t x_dtype, float* h,
+                                        int64_t m, int64_t n, int64_t k, void* stream)
+{
+    CELLM_API_BEGIN
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    DeviceGuard g(ctx->device);
+    const std::lock_guard<std::recursive_mutex> lk(ctx->mu);  // held until the scratch users are enqueued
+    return gate_up_i8_impl(ctx, wg, sg, n_sg, bg, wu, su, n_su, bu, scale_dtype, x, x_dtype, h, m, n, k,
+                           ACT_GELU_TANH, pick_stream(ctx, stream));
     CELLM_API_END(report_exception)
 }
 
@@ -772,7 +788,21 @@ int32_t cellm_hip_qgemv_q4_affine_gate_up_silu(cellm_hip_ctx_t* ctx, const uint3
     if (int32_t rc = check_ctx(ctx)) return rc;
     DeviceGuard g(ctx->device);
     const std::lock_guard<std::recursive_mutex> lk(ctx->mu);  // held until the scratch users are enqueued
-    return gate_up_q4_impl(ctx, wg, sg, bg, wu, su, bu, sb_dtype, group, x, x_dtype, h, m, n, k,
+    return gate_up_q4_impl(ctx, wg, sg, bg, wu, su, bu, sb_dtype, group, x, x_dtype, h, m, n, k, ACT_SILU,
+                           pick_stream(ctx, stream));
+    CELLM_API_END(report_exception)
+}
+
+int32_t cellm_hip_qgemv_q4_affine_gate_up_gelu(cellm_hip_ctx_t* ctx, const uint32_t* wg, const void* sg,
+                                               const void* bg, const uint32_t* wu, const void* su, const void* bu,
+                                               int32_t sb_dtype, int64_t group, const void* x, int32_t x_dtype,
+                                               float* h, int64_t m, int64_t n, int64_t k, void* stream)
+{
+    CELLM_API_BEGIN
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    DeviceGuard g(ctx->device);
+    const std::lock_guard<std::recursive_mutex> lk(ctx->mu);  // held until the scratch users are enqueued
+    return gate_up_q4_impl(ctx, wg, sg, bg, wu, su, bu, sb_dtype, group, x, x_dtype, h, m, n, k, ACT_GELU_TANH,
                            pick_stream(ctx, stream));
     CELLM_API_END(report_exception)
 }
@@ -793,6 +823,30 @@ static int32_t qgemv_i4_impl(const uint8_t* w, const uint16_t* scales_f16, int64
     HIP_TRY(launch_qgemv_i4_sym(w, scales_f16, (int)spr, (int)gs, x, x_dtype, y, (int)m, (int)n, (int)k, st),
             "qgemv_i4_sym launch");
     return CELLM_HIP_OK;
+}
+
+// Gemma's MLP over symmetric i4 gate/up weights (gemma.rs:838-846 with the i4 branch of
+// linear_f16_out_in, gemma.rs:1446-1471): the two i4 GEMVs, then gelu_tanh(g) * u.
+int32_t cellm_hip_qgemv_i4_gate_up_gelu(cellm_hip_ctx_t* ctx, const uint8_t* wg, const uint16_t* sg, int64_t n_sg,
+                                        const uint8_t* wu, const uint16_t* su, int64_t n_su, int64_t gs,
+                                        const void* x, int32_t x_dtype, float* h, int64_t m, int64_t n, int64_t k,
+                                        void* stream)
+{
+    CELLM_API_BEGIN
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    if (int32_t rc = check_dims(m, n, k)) return rc;
+    if (m == 0 || n == 0) return CELLM_HIP_OK;
+    if (!h) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null output pointer");
+    DeviceGuard g(ctx->device);
+    const std::lock_guard<std::recursive_mutex> lk(ctx->mu);  // held until the scratch users are enqueued
+    hipStream_t st = pick_stream(ctx, stream);
+    float* up = nullptr;
+    if (int32_t rc = get_stream_buffer(ctx, ctx->aux, st, (size_t)m * n * sizeof(float), &up)) return rc;
+    if (int32_t rc = qgemv_i4_impl(wg, sg, n_sg, gs, x, x_dtype, h, m, n, k, st)) return rc;
+    if (int32_t rc = qgemv_i4_impl(wu, su, n_su, gs, x, x_dtype, up, m, n, k, st)) return rc;
+    HIP_TRY(launch_act_mul(ACT_GELU_TANH, h, up, (size_t)m * n, st), "gelu_tanh_mul launch");
+    return CELLM_HIP_OK;
+    CELLM_API_END(report_exception)
 }
 
 int32_t cellm_hip_qgemv_i4_sym(cellm_hip_ctx_t* ctx, const uint8_t* w, const uint16_t* scales_f16, int64_t n_scales,
@@ -1001,6 +1055,10 @@ int32_t attention_impl(cellm_hip_ctx* ctx, const float* q, const uint16_t* kcach
     if (!aligned16(kcache) || !aligned16(vcache)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "K/V must be 16-byte aligned");
     float* ws = nullptr;
     if (static_scratch) {
+        if (!ctx->attn_static) {
+            std::lock_guard<std::recursive_mutex> lk(ctx->mu);
+            if (!ctx->attn_static) HIP_TRY(attention_static_scratch(&ctx->attn_static), "hipGetSymbolAddress(attention scratch)");
+        }
         ws = ctx->attn_static;
         if (!ws) return set_error(CELLM_HIP_ERR_DEVICE, "static attention scratch has no device address");
     } else if (int32_t rc = get_stream_buffer(ctx, ctx->attn, st, need, &ws, attention_counter_bytes())) {
@@ -1112,9 +1170,40 @@ int32_t cellm_hip_rope_half_f32(cellm_hip_ctx_t* ctx, float* x, int64_t rows, in
     if (rows * n_heads * head_dim > INT32_MAX) return set_error(CELLM_HIP_ERR_INVALID_ARG, "tensor too large");
     if (!x || !positions || !cos_sin) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null pointer");
     DeviceGuard g(ctx->device);
-    HIP_TRY(launch_rope_half(x, (int)rows, (int)n_heads, (int)head_dim, positions, cos_sin, (int)table_positions,
+    HIP_TRY(launch_rope_half(x, (int)rows, (int)n_heads, (int)head_dim, positions, cos_sin, (int)table_positions, 0,
                              pick_stream(ctx, stream)),
             "rope_half launch");
+    return CELLM_HIP_OK;
+    CELLM_API_END(report_exception)
+}
+
+int32_t cellm_hip_rope_interleaved_f32(cellm_hip_ctx_t* ctx, float* x, int64_t rows, int64_t n_heads, int64_t head_dim,
+                                       const int32_t* positions, const float* cos_sin, int64_t table_positions,
+                                       void* stream)
+{
+    CELLM_API_BEGIN
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    if (int32_t rc = check_dims(rows, n_heads, head_dim)) return rc;
+    if (rows == 0 || n_heads == 0 || head_dim == 0) return CELLM_HIP_OK;
+    if (head_dim % 2 != 0) return set_error(CELLM_HIP_ERR_INVALID_ARG, "head_dim must be even");
+    if (table_positions < 1 || table_positions > INT32_MAX)
+        return set_error(CELLM_HIP_ERR_INVALID_ARG, "table_positions must be >= 1");
+    if (rows * n_heads * head_dim > INT32_MAX) return set_error(CELLM_HIP_ERR_INVALID_ARG, "tensor too large");
+    if (!x || !positions || !cos_sin) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null pointer");
+    DeviceGuard g(ctx->device);
+    HIP_TRY(launch_rope_half(x, (int)rows, (int)n_heads, (int)head_dim, positions, cos_sin, (int)table_positions, 1,
+                             pick_stream(ctx, stream)),
+            "rope_interleaved launch");
+    return CELLM_HIP_OK;
+    CELLM_API_END(report_exception)
+}
+
+int32_t cellm_hip_set_rope_interleaved(cellm_hip_ctx_t* ctx, int32_t interleaved)
+{
+    CELLM_API_BEGIN
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    if (interleaved != 0 && interleaved != 1) return set_error(CELLM_HIP_ERR_INVALID_ARG, "interleaved must be 0 or 1");
+    ctx->rope_interleaved.store(interleaved);
     return CELLM_HIP_OK;
     CELLM_API_END(report_exception)
 }
@@ -1162,7 +1251,7 @@ int32_t cellm_hip_rope_kv_write_f16(cellm_hip_ctx_t* ctx, float* q, float* k, co
     HIP_TRY(launch_rope_kv_write_f16(q, k, v, (int)rows, (int)n_heads, (int)n_kv_heads, (int)head_dim, positions,
                                      cos_sin, (int)table_positions, kcache, vcache, block_tables, (int)max_blocks,
                                      (int)total_blocks, (int)n_layers, (int)tokens_per_block, (int)layer,
-                                     pick_stream(ctx, stream)),
+                                     ctx->rope_interleaved.load(), pick_stream(ctx, stream)),
             "rope_kv_write launch");
     return CELLM_HIP_OK;
     CELLM_API_END(report_exception)
@@ -1203,7 +1292,7 @@ int32_t cellm_hip_decode_qkv_rope_kv(cellm_hip_ctx_t* ctx, const float* x_prev, 
     HIP_TRY(launch_decode_qkv(x_prev, y, x_out, norm_w, eps, w, sc, (int)rows, (int)hidden, (int)n_heads,
                               (int)n_kv_heads, (int)head_dim, positions, cos_sin, (int)table_positions, q_out, kcache,
                               vcache, block_tables, (int)max_blocks, (int)total_blocks, (int)n_layers,
-                              (int)tokens_per_block, (int)layer, pick_stream(ctx, stream)),
+                              (int)tokens_per_block, (int)layer, ctx->rope_interleaved.load(), pick_stream(ctx, stream)),
             "decode_qkv launch");
     return CELLM_HIP_OK;
     CELLM_API_END(report_exception)
@@ -1276,6 +1365,19 @@ int32_t cellm_hip_silu_mul_f32(cellm_hip_ctx_t* ctx, float* gate, const float* u
     if (!gate || !up) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null pointer");
     DeviceGuard g(ctx->device);
     HIP_TRY(launch_silu_mul(gate, up, (size_t)n, pick_stream(ctx, stream)), "silu_mul launch");
+    return CELLM_HIP_OK;
+    CELLM_API_END(report_exception)
+}
+
+int32_t cellm_hip_gelu_tanh_mul_f32(cellm_hip_ctx_t* ctx, float* gate, const float* up, int64_t n, void* stream)
+{
+    CELLM_API_BEGIN
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    if (n < 0) return set_error(CELLM_HIP_ERR_INVALID_ARG, "bad length");
+    if (n == 0) return CELLM_HIP_OK;
+    if (!gate || !up) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null pointer");
+    DeviceGuard g(ctx->device);
+    HIP_TRY(launch_act_mul(ACT_GELU_TANH, gate, up, (size_t)n, pick_stream(ctx, stream)), "gelu_tanh_mul launch");
     return CELLM_HIP_OK;
     CELLM_API_END(report_exception)
 }

@@ -137,10 +137,44 @@ __device__ __forceinline__ float group_sum(float v)
     if constexpr (W >= 2) v += lane_xor<1>(v, W);
     return v;
 }
+// Maximum over aligned groups of W lanes (the butterfly of group_sum with fmaxf).
+template <int W>
+__device__ __forceinline__ float group_max(float v)
+{
+    if constexpr (W >= 64) v = fmaxf(v, lane_xor<32>(v, W));
+    if constexpr (W >= 32) v = fmaxf(v, lane_xor<16>(v, W));
+    if constexpr (W >= 16) v = fmaxf(v, lane_xor<8>(v, W));
+    if constexpr (W >= 8) v = fmaxf(v, lane_xor<4>(v, W));
+    if constexpr (W >= 4) v = fmaxf(v, lane_xor<2>(v, W));
+    if constexpr (W >= 2) v = fmaxf(v, lane_xor<1>(v, W));
+    return v;
+}
 __device__ __forceinline__ float quad_sum(float v) { return group_sum<4>(v); }
 __device__ __forceinline__ float pair_sum(float v) { return group_sum<2>(v); }
 __device__ __forceinline__ float oct_sum(float v) { return group_sum<8>(v); }
 
+
+// ---- gate/up activation epilogues -------------------------------------------
+// ACT_SILU: silu(g) * u with silu(g) = g * (1 / (1 + exp(-g))), the order of
+// silu_mul_f32_inplace (metal.rs:232-243) and llama.rs:477-484.
+// ACT_GELU_TANH: gelu_tanh(g) * u with gelu_tanh(x) = 0.5 x (1 + tanh(k (x + c x^3))),
+// k = 0.7978846, c = 0.044715, evaluated in the reference's order
+// (crates/cellm-model/src/gemma.rs:1689-1693, applied at :844-846;
+// gelu_tanh_mul_f32_inplace, metal.rs:245-257): c*x*x*x as ((c*x)*x)*x, every
+// product and sum rounded in f32 (no contraction).
+enum Act : int32_t { ACT_SILU = 0, ACT_GELU_TANH = 1 };
+
+__device__ __forceinline__ float act_mul(int act, float g, float u)
+{
+#pragma clang fp contract(off)
+    if (act == ACT_GELU_TANH) {
+        const float k = 0.7978846f, c = 0.044715f;
+        const float inner = k * (g + ((c * g) * g) * g);
+        return ((0.5f * g) * (1.0f + tanhf(inner))) * u;
+    }
+    const float sig = 1.0f / (1.0f + expf(-g));
+    return (g * sig) * u;
+}
 
 // ---- MLX affine dequant of one u32 word of nibbles to f16, as the converter
 // rounds it (tools/convert/src/main.rs:4435-4436): RNE_f16(f32(q) * s + b),

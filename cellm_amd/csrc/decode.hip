@@ -191,8 +191,16 @@ __global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(float* __res
 }
 
 // One thread per (row, head, i < half).  cs[p][i] = (cos, sin) of position p.
+// The two elements pair i of a head rotates: i and i + half (rotate-half,
+// rope_non_interleaved_inplace_f32, cpu_kernels.rs:264-277) or 2i and 2i + 1
+// (rope_interleaved_inplace_f32, cpu_kernels.rs:279-292).  Both use the angle
+// pos * theta^(-2i / head_dim) of pair i.
+__device__ __forceinline__ int rope_lo(int i, int half, int il) { return il ? 2 * i : i; }
+__device__ __forceinline__ int rope_hi(int i, int half, int il) { return il ? 2 * i + 1 : half + i; }
+
 __global__ void rope_half_kernel(float* __restrict__ x, int rows, int n_heads, int head_dim,
-                                 const int32_t* __restrict__ pos, const float2* __restrict__ cs, int table_positions)
+                                 const int32_t* __restrict__ pos, const float2* __restrict__ cs, int table_positions,
+                                 int il)
 {
     const int half = head_dim >> 1;
     const int total = rows * n_heads * half;
@@ -202,9 +210,10 @@ __global__ void rope_half_kernel(float* __restrict__ x, int rows, int n_heads, i
         const int p = min(max(pos[r], 0), table_positions - 1);
         const float2 c = cs[(size_t)p * half + i];
         float* head = x + (size_t)rh * head_dim;
-        const float x0 = head[i], x1 = head[half + i];
-        head[i] = x0 * c.x - x1 * c.y;
-        head[half + i] = x1 * c.x + x0 * c.y;
+        const int i0 = rope_lo(i, half, il), i1 = rope_hi(i, half, il);
+        const float x0 = head[i0], x1 = head[i1];
+        head[i0] = x0 * c.x - x1 * c.y;
+        head[i1] = x1 * c.x + x0 * c.y;
     }
 }
 
@@ -246,7 +255,7 @@ __global__ void rope_kv_write_kernel(float* __restrict__ q, float* __restrict__ 
                                      int rows, int n_heads, int n_kv_heads, int head_dim,
                                      const int32_t* __restrict__ pos, const float2* __restrict__ cs,
                                      int table_positions, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
-                                     PagedKv kv, int layer)
+                                     PagedKv kv, int layer, int il)
 {
     const int half = head_dim >> 1;
     const int nq = n_heads * half, per_row = nq + n_kv_heads * half;
@@ -256,27 +265,29 @@ __global__ void rope_kv_write_kernel(float* __restrict__ q, float* __restrict__ 
         const int p = min(max(pos[r], 0), table_positions - 1);
         if (j < nq) {
             const int i = j % half;
+            const int i0 = rope_lo(i, half, il), i1 = rope_hi(i, half, il);
             const float2 c = cs[(size_t)p * half + i];
             float* head = q + ((size_t)r * n_heads + j / half) * head_dim;
-            const float x0 = head[i], x1 = head[half + i];
-            head[i] = x0 * c.x - x1 * c.y;
-            head[half + i] = x1 * c.x + x0 * c.y;
+            const float x0 = head[i0], x1 = head[i1];
+            head[i0] = x0 * c.x - x1 * c.y;
+            head[i1] = x1 * c.x + x0 * c.y;
         } else {
             const int jk = j - nq, kh = jk / half, i = jk % half;
+            const int i0 = rope_lo(i, half, il), i1 = rope_hi(i, half, il);
             const float2 c = cs[(size_t)p * half + i];
             const size_t off = ((size_t)r * n_kv_heads + kh) * head_dim;
-            const float x0 = k[off + i], x1 = k[off + half + i];
+            const float x0 = k[off + i0], x1 = k[off + i1];
             const float k0 = x0 * c.x - x1 * c.y;
             const float k1 = x1 * c.x + x0 * c.y;
-            k[off + i] = k0;
-            k[off + half + i] = k1;
+            k[off + i0] = k0;
+            k[off + i1] = k1;
             const long long b = pos[r] >= 0 ? kv.base(r, pos[r], layer) : -1;
             if (b < 0) continue;
             const size_t e = (size_t)b + (size_t)kh * head_dim;
-            kc[e + i] = __builtin_bit_cast(uint16_t, (_Float16)k0);
-            kc[e + half + i] = __builtin_bit_cast(uint16_t, (_Float16)k1);
-            vc[e + i] = __builtin_bit_cast(uint16_t, (_Float16)v[off + i]);
-            vc[e + half + i] = __builtin_bit_cast(uint16_t, (_Float16)v[off + half + i]);
+            kc[e + i0] = __builtin_bit_cast(uint16_t, (_Float16)k0);
+            kc[e + i1] = __builtin_bit_cast(uint16_t, (_Float16)k1);
+            vc[e + i0] = __builtin_bit_cast(uint16_t, (_Float16)v[off + i0]);
+            vc[e + i1] = __builtin_bit_cast(uint16_t, (_Float16)v[off + i1]);
         }
     }
 }
@@ -877,10 +888,12 @@ struct DecodeQkvArgs {
     uint16_t* vc;
     PagedKv kv;
     int layer;
+    int il;  // RoPE pairs: 0 rotate-half (i, i + half), 1 interleaved (2i, 2i + 1)
 };
 
-// Team -> one (head, i < head_dim/2) pair: rows i and i + head_dim/2 of a q,
-// k or v head, the two operands of one RoPE rotation.
+// Team -> one (head, i < head_dim/2) pair: rows i and i + head_dim/2 (rotate-half)
+// or 2i and 2i + 1 (interleaved) of a q, k or v head, the two operands of one
+// RoPE rotation.
 template <int LPR, int C, int MT, int KR, bool HASY>
 __global__ __launch_bounds__(256) void decode_qkv_kernel(DecodeQkvArgs a)
 {
@@ -894,7 +907,8 @@ __global__ __launch_bounds__(256) void decode_qkv_kernel(DecodeQkvArgs a)
     const int hh = p / half, i = p - hh * half;
     const int which = hh < a.n_heads ? 0 : (hh < a.n_heads + a.n_kv_heads ? 1 : 2);
     const int head = which == 0 ? hh : (which == 1 ? hh - a.n_heads : hh - a.n_heads - a.n_kv_heads);
-    const int r0 = head * a.head_dim + i, r1 = r0 + half;
+    const int i0 = rope_lo(i, half, a.il), i1 = rope_hi(i, half, a.il);
+    const int r0 = head * a.head_dim + i0, r1 = head * a.head_dim + i1;
     const int8_t* wm = which == 0 ? a.w[0] : (which == 1 ? a.w[1] : a.w[2]);
     const uint16_t* sm = which == 0 ? a.s[0] : (which == 1 ? a.s[1] : a.s[2]);
     u4_t w0[C], w1[C];
@@ -922,19 +936,19 @@ __global__ __launch_bounds__(256) void decode_qkv_kernel(DecodeQkvArgs a)
         const float2 c = a.cs[(size_t)min(max(pr, 0), a.table_positions - 1) * half + i];
         if (which == 0) {
             float* q = a.q_out + ((size_t)m * a.n_heads + head) * a.head_dim;
-            q[i] = v0 * c.x - v1 * c.y;
-            q[half + i] = v1 * c.x + v0 * c.y;
+            q[i0] = v0 * c.x - v1 * c.y;
+            q[i1] = v1 * c.x + v0 * c.y;
             continue;
         }
         const long long b = pr >= 0 ? a.kv.base(m, pr, a.layer) : -1;
         if (b < 0) continue;
         const size_t e = (size_t)b + (size_t)head * a.head_dim;
         if (which == 1) {
-            a.kc[e + i] = __builtin_bit_cast(uint16_t, (_Float16)(v0 * c.x - v1 * c.y));
-            a.kc[e + half + i] = __builtin_bit_cast(uint16_t, (_Float16)(v1 * c.x + v0 * c.y));
+            a.kc[e + i0] = __builtin_bit_cast(uint16_t, (_Float16)(v0 * c.x - v1 * c.y));
+            a.kc[e + i1] = __builtin_bit_cast(uint16_t, (_Float16)(v1 * c.x + v0 * c.y));
         } else {
-            a.vc[e + i] = __builtin_bit_cast(uint16_t, (_Float16)v0);
-            a.vc[e + half + i] = __builtin_bit_cast(uint16_t, (_Float16)v1);
+            a.vc[e + i0] = __builtin_bit_cast(uint16_t, (_Float16)v0);
+            a.vc[e + i1] = __builtin_bit_cast(uint16_t, (_Float16)v1);
         }
     }
 }
@@ -1113,24 +1127,24 @@ hipError_t launch_add_rms_norm(float* x, const float* y, const void* w, int wdt,
 hipError_t launch_rope_kv_write_f16(float* q, float* k, const float* v, int rows, int n_heads, int n_kv_heads,
                                     int head_dim, const int32_t* pos, const float* cos_sin, int table_positions,
                                     uint16_t* kcache, uint16_t* vcache, const uint32_t* block_tables, int max_blocks,
-                                    int total_blocks, int n_layers, int tokens_per_block, int layer, hipStream_t st)
+                                    int total_blocks, int n_layers, int tokens_per_block, int layer, int interleaved, hipStream_t st)
 {
     const PagedKv kv{block_tables, max_blocks, total_blocks, n_layers, tokens_per_block, n_kv_heads * head_dim};
     const int total = rows * (n_heads + n_kv_heads) * (head_dim / 2);
     const int blocks = std::max(1, std::min((total + 255) / 256, 1024));
     hipLaunchKernelGGL(rope_kv_write_kernel, dim3(blocks), dim3(256), 0, st, q, k, v, rows, n_heads, n_kv_heads,
                        head_dim, pos, reinterpret_cast<const float2*>(cos_sin), table_positions, kcache, vcache, kv,
-                       layer);
+                       layer, interleaved ? 1 : 0);
     return hipGetLastError();
 }
 
 hipError_t launch_rope_half(float* x, int rows, int n_heads, int head_dim, const int32_t* pos, const float* cos_sin,
-                            int table_positions, hipStream_t st)
+                            int table_positions, int interleaved, hipStream_t st)
 {
     const int total = rows * n_heads * (head_dim / 2);
     const int blocks = std::max(1, std::min((total + 255) / 256, 1024));
     hipLaunchKernelGGL(rope_half_kernel, dim3(blocks), dim3(256), 0, st, x, rows, n_heads, head_dim, pos,
-                       reinterpret_cast<const float2*>(cos_sin), table_positions);
+                       reinterpret_cast<const float2*>(cos_sin), table_positions, interleaved ? 1 : 0);
     return hipGetLastError();
 }
 
@@ -1324,7 +1338,7 @@ hipError_t launch_decode_qkv(const float* x_prev, const float* y, float* x_out, 
                              int n_kv_heads, int head_dim, const int32_t* pos, const float* cos_sin,
                              int table_positions, float* q_out, uint16_t* kcache, uint16_t* vcache,
                              const uint32_t* block_tables, int max_blocks, int total_blocks, int n_layers,
-                             int tokens_per_block, int layer, hipStream_t st)
+                             int tokens_per_block, int layer, int interleaved, hipStream_t st)
 {
     DecodeQkvArgs a{};
     a.x_prev = x_prev;
@@ -1349,6 +1363,7 @@ hipError_t launch_decode_qkv(const float* x_prev, const float* y, float* x_out, 
     a.vc = vcache;
     a.kv = PagedKv{block_tables, max_blocks, total_blocks, n_layers, tokens_per_block, n_kv_heads * head_dim};
     a.layer = layer;
+    a.il = interleaved ? 1 : 0;
     const int pairs = (n_heads + 2 * n_kv_heads) * (head_dim / 2);
     if (H > 64 * 16 * 4) return hipErrorInvalidValue;
     return launch_decode<true>(rows, H, a, pairs, st);

@@ -60,6 +60,11 @@ __global__ __launch_bounds__(kBlock) void dequant_q4_affine_kernel(const uint32_
     }
 }
 
+__global__ void fill_f32_kernel(float* __restrict__ y, float v, size_t n)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) y[i] = v;
+}
+
 __global__ void add_f32_kernel(const float* a, const float* b, float* out, int n)
 {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -75,6 +80,14 @@ __global__ void silu_mul_kernel(float* __restrict__ g, const float* __restrict__
         const float sig = 1.0f / (1.0f + expf(-x));
         g[i] = (x * sig) * u[i];
     }
+}
+
+// g[i] = gelu_tanh(g[i]) * u[i]: gelu_tanh_mul_f32_inplace (metal.rs:245-257) and the CPU
+// loop of gemma.rs:844-846 over gelu_tanh_f32 (gemma.rs:1689-1693), in act_mul's order
+__global__ void gelu_tanh_mul_kernel(float* __restrict__ g, const float* __restrict__ u, size_t n)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        g[i] = act_mul(ACT_GELU_TANH, g[i], u[i]);
 }
 
 }  // namespace
@@ -113,12 +126,30 @@ hipError_t launch_add_bias_rows(float* y, const float* bias, int M, int N, hipSt
     return hipGetLastError();
 }
 
+hipError_t launch_act_mul(int act, float* g, const float* u, size_t count, hipStream_t st)
+{
+    if (act == ACT_SILU) return launch_silu_mul(g, u, count, st);
+    if (count == 0) return hipSuccess;
+    const size_t blocks = std::min<size_t>((count + 255) / 256, 4096);
+    hipLaunchKernelGGL(gelu_tanh_mul_kernel, dim3((unsigned)blocks), dim3(256), 0, st, g, u, count);
+    return hipGetLastError();
+}
+
 hipError_t launch_silu_mul(float* g, const float* u, size_t count, hipStream_t st)
 {
     if (count == 0) return hipSuccess;
     size_t blocks = (count + 255) / 256;
     if (blocks > 4096) blocks = 4096;
     hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)blocks), dim3(256), 0, st, g, u, count);
+    return hipGetLastError();
+}
+
+// A kernel, not hipMemsetAsync: a caller capturing the stream into a HIP graph gets a kernel node.
+hipError_t launch_fill_f32(float* y, float v, size_t count, hipStream_t st)
+{
+    if (count == 0) return hipSuccess;
+    const size_t blocks = std::min<size_t>((count + 255) / 256, 4096);
+    hipLaunchKernelGGL(fill_f32_kernel, dim3((unsigned)blocks), dim3(256), 0, st, y, v, count);
     return hipGetLastError();
 }
 

@@ -41,17 +41,19 @@ struct I8FusedSeg {
     int per_channel;
 };
 bool qgemv_i8_fused_supported(int xdt, int M, int K, const void* x, const I8FusedSeg* segs, int nseg);
-hipError_t launch_qgemv_i8_fused(const I8FusedSeg* segs, int nseg, bool silu, int sdt, const void* x, int xdt, int M,
-                                 int K, hipStream_t st);
+hipError_t launch_qgemv_i8_fused(const I8FusedSeg* segs, int nseg, bool silu, int act, int sdt, const void* x, int xdt,
+                                 int M, int K, hipStream_t st);
 
 // MLX q4 gate/up + SiLU in one launch: h[m,n] = silu(gate[m,n]) * up[m,n] (f16 x, M <= 4,
 // K % 32 == 0, group >= 32, 16-byte aligned x and weights, x in 64 KB of LDS).
 bool qgemv_q4_gate_up_supported(int xdt, int M, int K, int group_size, const void* x, const void* wg, const void* wu);
 hipError_t launch_qgemv_q4_gate_up_silu(const uint32_t* wg, const void* Sg, const void* Bg, const uint32_t* wu,
                                         const void* Su, const void* Bu, int sbt, int group_size, const void* x,
-                                        int xdt, float* h, int M, int N, int K, hipStream_t st);
+                                        int xdt, float* h, int M, int N, int K, int act, hipStream_t st);
 
 // h[i] = silu(g[i]) * u[i] in place on g (dequant.hip), silu(g) = g / (1 + exp(-g)).
+// gate[i] = act(gate[i]) * up[i] for act ACT_SILU / ACT_GELU_TANH (common.hpp act_mul)
+hipError_t launch_act_mul(int act, float* g, const float* u, size_t count, hipStream_t st);
 hipError_t launch_silu_mul(float* g, const float* u, size_t count, hipStream_t st);
 // y[m, n] += bias[n] over M rows of N (the projection-bias fallback of the multi-segment q4 GEMV)
 hipError_t launch_add_bias_rows(float* y, const float* bias, int M, int N, hipStream_t st);
@@ -113,9 +115,9 @@ hipError_t launch_add_rms_norm(float* x, const float* y, const void* w, int wdt,
 hipError_t launch_rope_kv_write_f16(float* q, float* k, const float* v, int rows, int n_heads, int n_kv_heads,
                                     int head_dim, const int32_t* pos, const float* cos_sin, int table_positions,
                                     uint16_t* kcache, uint16_t* vcache, const uint32_t* block_tables, int max_blocks,
-                                    int total_blocks, int n_layers, int tokens_per_block, int layer, hipStream_t st);
+                                    int total_blocks, int n_layers, int tokens_per_block, int layer, int interleaved, hipStream_t st);
 hipError_t launch_rope_half(float* x, int rows, int n_heads, int head_dim, const int32_t* pos, const float* cos_sin,
-                            int table_positions, hipStream_t st);
+                            int table_positions, int interleaved, hipStream_t st);
 hipError_t launch_kv_write_f16(const float* k, const float* v, int rows, int kv_dim, const int32_t* pos,
                                uint16_t* kcache, uint16_t* vcache, const uint32_t* block_tables, int max_blocks,
                                int total_blocks, int n_layers, int tokens_per_block, int layer, hipStream_t st);
@@ -143,7 +145,7 @@ hipError_t launch_decode_qkv(const float* x_prev, const float* y, float* x_out, 
                              int n_kv_heads, int head_dim, const int32_t* pos, const float* cos_sin,
                              int table_positions, float* q_out, uint16_t* kcache, uint16_t* vcache,
                              const uint32_t* block_tables, int max_blocks, int total_blocks, int n_layers,
-                             int tokens_per_block, int layer, hipStream_t st);
+                             int tokens_per_block, int layer, int interleaved, hipStream_t st);
 hipError_t launch_decode_gate_up(const float* x_prev, const float* y, float* x_out, const float* norm_w, float eps,
                                  const int8_t* wg, const uint16_t* sg, const int8_t* wu, const uint16_t* su, int rows,
                                  int H, int N, float* h, hipStream_t st);
@@ -156,6 +158,8 @@ hipError_t launch_qgemv_lowbit(int fmt, const void* w, const uint16_t* S, int sc
                                float* y, int M, int N, int K, hipStream_t st);
 
 // Device smoke test kernel: out[i] = a[i] + b[i].
+// y[0..count) = v (used where a result is all zeros, e.g. K == 0)
+hipError_t launch_fill_f32(float* y, float v, size_t count, hipStream_t st);
 hipError_t launch_add_f32(const float* a, const float* b, float* out, int n, hipStream_t st);
 
 }  // namespace cellm

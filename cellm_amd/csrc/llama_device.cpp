@@ -17,6 +17,8 @@
 #include <hip/hip_runtime_api.h>
 
 #include <cmath>
+#include <cstdlib>
+#include <cctype>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -30,6 +32,7 @@
 namespace cellm_step {
 extern thread_local cellm::ErrorSlot g_err;  // llama_step.cpp: read by cellm_llama_last_error_message
 int32_t report_exception(int32_t code, const char* what);
+bool llama_rope_interleaved_from_env();      // llama_step.cpp
 }
 
 namespace {
@@ -167,6 +170,7 @@ struct HostModel {
     HostProj embed;  // kind I8, I4 or F16; s: f16 row scales (none for F16)
     HostProj lm;     // w == nullptr: tied to the embedding
     const uint16_t* final_norm = nullptr;
+    bool rope_interleaved = false;  // RoPE pairs (2i, 2i + 1) instead of (i, i + head_dim/2)
 };
 
 }  // namespace
@@ -503,6 +507,7 @@ int32_t cellm_llama_dev_create(const cellm_llama_config_t* cfg, const cellm_llam
     hm.embed.s = embed_scale_f16;
     hm.embed.s_bytes = (size_t)cfg->vocab * 2;
     hm.final_norm = final_norm_f16;
+    hm.rope_interleaved = cellm_step::llama_rope_interleaved_from_env();
     return dev_create_impl(cfg, hm, device, max_rows, max_blocks, out);
     CELLM_API_END(cellm_step::report_exception)
 }
@@ -549,6 +554,8 @@ int32_t dev_create_impl(const cellm_llama_config_t* cfg, const HostModel& hm, in
         return bail(from_hip_lib(rc, "cellm_hip_create"));
     }
     if ((rc = cellm_hip_get_stream(m->hip, &m->stream))) return bail(from_hip_lib(rc, "cellm_hip_get_stream"));
+    if ((rc = cellm_hip_set_rope_interleaved(m->hip, hm.rope_interleaved ? 1 : 0)))
+        return bail(from_hip_lib(rc, "cellm_hip_set_rope_interleaved"));
     int prev = 0;
     if (hipGetDevice(&prev) != hipSuccess || hipSetDevice(device) != hipSuccess)
         return bail(fail(CELLM_HIP_ERR_DEVICE, "hipSetDevice(%d) failed", device));
@@ -848,6 +855,7 @@ int32_t cellm_llama_dev_create_from_file(const char* path, int32_t device, int32
                     w.c_str(), t.dtype, family == FAM_QWEN ? ", f16, i2 or q1_0_g128" : " or f16");
     };
     HostModel hm;
+    hm.rope_interleaved = family == FAM_LLAMA && cellm_step::llama_rope_interleaved_from_env();
     hm.p.resize((size_t)c.n_layers * 7);
     for (int32_t l = 0; l < c.n_layers; ++l) {
         const std::string pre = base + "layers." + std::to_string(l) + ".";

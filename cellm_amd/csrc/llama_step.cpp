@@ -7,7 +7,9 @@
 // f16 KV cache and attention are CPU code restated from the reference; this
 // file is compiled with -ffp-contract=off so every f32 operation rounds as
 // Rust's does.
+#include <cctype>
 #include <cmath>
+#include <cstdlib>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -20,6 +22,22 @@
 
 namespace cellm_step {
 thread_local cellm::ErrorSlot g_err = {};  // shared with llama_device.cpp
+
+// LlamaRunner's RoPE layout switch (llama.rs:80-82): CELLM_LLAMA_ROPE_INTERLEAVED set to "1" or
+// "true" in any case selects rope_interleaved_inplace_f32 for q and k (llama.rs:391-396); unset or
+// anything else keeps rotate-half.  Read once when a runner is created, as the reference does.
+bool llama_rope_interleaved_from_env()
+{
+    const char* v = std::getenv("CELLM_LLAMA_ROPE_INTERLEAVED");
+    if (!v) return false;
+    if (std::strcmp(v, "1") == 0) return true;
+    const char* t = "true";
+    for (size_t i = 0;; ++i) {
+        const char a = (char)std::tolower((unsigned char)v[i]);
+        if (a != t[i]) return false;
+        if (a == '\0') return true;
+    }
+}
 
 // The CELLM_API_END report of this library (no allocation).
 int32_t report_exception(int32_t code, const char* what)
@@ -109,8 +127,10 @@ void rms_norm(const float* x, const float* w, size_t n, float eps, float* out)
 }
 
 // rope_non_interleaved_inplace_f32 with rotary_dim = head_dim (cpu_kernels.rs:264-277),
-// the default layout (llama.rs:394-396)
-void rope_half(float* x, size_t n_heads, size_t head_dim, size_t pos, float theta)
+// the default layout (llama.rs:394-396), or with `interleaved`
+// rope_interleaved_inplace_f32 (cpu_kernels.rs:279-292, llama.rs:391-393): the same
+// angle for pair i, applied to elements (2i, 2i + 1) instead of (i, i + half)
+void rope(float* x, size_t n_heads, size_t head_dim, size_t pos, float theta, bool interleaved)
 {
     const size_t half = head_dim / 2;
     for (size_t h = 0; h < n_heads; ++h) {
@@ -119,9 +139,10 @@ void rope_half(float* x, size_t n_heads, size_t head_dim, size_t pos, float thet
             const float inv_freq = std::pow(theta, -(2.0f * (float)i) / (float)head_dim);
             const float angle = (float)pos * inv_freq;
             const float s = std::sin(angle), c = std::cos(angle);
-            const float x0 = head[i], x1 = head[half + i];
-            head[i] = x0 * c - x1 * s;
-            head[half + i] = x1 * c + x0 * s;
+            const size_t i0 = interleaved ? 2 * i : i, i1 = interleaved ? 2 * i + 1 : half + i;
+            const float x0 = head[i0], x1 = head[i1];
+            head[i0] = x0 * c - x1 * s;
+            head[i1] = x1 * c + x0 * s;
         }
     }
 }
@@ -130,6 +151,7 @@ void rope_half(float* x, size_t n_heads, size_t head_dim, size_t pos, float thet
 
 struct cellm_llama {
     cellm_llama_config_t cfg{};
+    bool rope_interleaved = false;  // CELLM_LLAMA_ROPE_INTERLEAVED at creation
     cellm_hip_ctx_t* hip = nullptr;
     std::vector<std::vector<int8_t>> w;       // kept host-side: logits_i8 takes host slices
     std::vector<std::vector<uint16_t>> s;
@@ -189,6 +211,7 @@ int32_t cellm_llama_create(const cellm_llama_config_t* cfg, const cellm_llama_la
     if (c.n_heads % c.n_kv_heads != 0) return fail(CELLM_HIP_ERR_INVALID_ARG, "n_heads % n_kv_heads != 0");
     auto* m = new cellm_llama();
     m->cfg = c;
+    m->rope_interleaved = cellm_step::llama_rope_interleaved_from_env();
     m->kv_dim = (size_t)c.n_kv_heads * c.head_dim;
     int32_t rc = cellm_hip_create(device, &m->hip);
     if (rc) {
@@ -295,8 +318,8 @@ int32_t cellm_llama_step(cellm_llama_t* m, uint32_t token, size_t pos, const uin
         if ((rc = linear(m, (int)l, 0, xn.data(), q.data())) || (rc = linear(m, (int)l, 1, xn.data(), k.data())) ||
             (rc = linear(m, (int)l, 2, xn.data(), v.data())))
             return rc;
-        rope_half(q.data(), nh, hd, pos, c.rope_theta);
-        rope_half(k.data(), nkv, hd, pos, c.rope_theta);
+        rope(q.data(), nh, hd, pos, c.rope_theta, m->rope_interleaved);
+        rope(k.data(), nkv, hd, pos, c.rope_theta, m->rope_interleaved);
         // write_token_f32: f32 -> f16 RNE (crates/cellm-cache/src/kvcache.rs:589-615)
         const size_t wb = base_of(pos, l);
         for (size_t i = 0; i < kvd; ++i) {

@@ -81,15 +81,17 @@ __device__ __forceinline__ void stage_word_q4(u4_t raw, int idx, bool valid, uin
 }
 
 // f32 activations (the LFM runner's and the .cellm u32 runner's x) as two f16 parts,
-// x = hi + lo with hi = RNE_f16(x) and lo = RNE_f16(x - hi): a nibble value times either
-// part is exact in f32, so the dot over both parts keeps x to about 22 bits where one
-// f16 rounding would keep 11.  Eight f32 values -> the hi pairs at xq, the lo pairs at
-// xq_lo (the layout of stage_word_q4), cx = (1024 * the pairs' sum over both parts, sum of
-// the f32 x) per chunk.
-__device__ __forceinline__ void stage_word_q4_x32(f4_t a, f4_t b, int idx, bool valid, uint32_t* xq, uint32_t* xq_lo,
-                                                  float2* cx)
+// x' = hi + lo with hi = RNE_f16(x') and lo = RNE_f16(x' - hi), where x' = x * 2^sh is the
+// row scaled by x32_row_shifts: a nibble value times either part is exact in f32, so the
+// dot over both parts keeps x to about 22 bits where one f16 rounding would keep 11.
+// Eight f32 values -> the hi pairs at xq, the lo pairs at xq_lo (the layout of
+// stage_word_q4), cx = (1024 * the pairs' sum over both parts, sum of the scaled x) per chunk.
+__device__ __forceinline__ void stage_word_q4_x32(f4_t a, f4_t b, int sh, int idx, bool valid, uint32_t* xq,
+                                                  uint32_t* xq_lo, float2* cx)
 {
-    const float xv[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    float xv[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xv[i] = __builtin_ldexpf(xv[i], sh);
     h8_t hi, lo;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -118,9 +120,51 @@ __device__ __forceinline__ void stage_word_q4_x32(f4_t a, f4_t b, int idx, bool 
 // All MT * K / 8 words of f32 x -> LDS through stage_word_q4_x32, two 16-byte loads per word, in
 // rounds of XW words per thread whose loads all issue before the round's first store (clamped,
 // branch-free: padding rows and words past `total` read valid data whose results are never stored).
-template <int XW>
+// Per-row exponent shifts for f32 x.  Row m is staged as x * 2^sh[m], sh[m] chosen from the
+// row's largest |x| so that the largest staged value lies in [2^13, 2^14): hi never overflows f16
+// (|x| > 65504 alone would give hi = inf, lo = -inf and a NaN row sum), and a row of small values
+// stays clear of f16 subnormals, where hi and lo (and lo / 16 in the pair layout) lose bits.
+// Every product and partial sum of the row's dot then carries the exact factor 2^sh[m], and the
+// kernels return ldexp(acc, -sh[m]): bit for bit the unscaled result wherever that one kept its
+// values in f16 normal range.  A row of zeros or with an infinite value keeps sh = 0 (NaN is
+// ignored by fmaxf and propagates through the dot as it would unscaled).
+template <int MT>
+__device__ __forceinline__ void x32_row_shifts(const float* __restrict__ x, int M, int K, int (&sh)[MT])
+{
+    __shared__ float red[kBlock / 64][MT];
+    const int q = K >> 2;  // 16-byte words per row (K % 32 == 0, x 16-byte aligned)
+    float mx[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        mx[m] = 0.0f;
+        if (m < M) {
+            const f4_t* row = reinterpret_cast<const f4_t*>(x + (size_t)m * K);
+            for (int i = threadIdx.x; i < q; i += kBlock) {
+                const f4_t v = row[i];
+                mx[m] = fmaxf(mx[m], fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+            }
+        }
+        mx[m] = group_max<64>(mx[m]);
+    }
+    if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+        for (int m = 0; m < MT; ++m) red[threadIdx.x >> 6][m] = mx[m];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        float v = red[0][m];
+#pragma unroll
+        for (int w = 1; w < kBlock / 64; ++w) v = fmaxf(v, red[w][m]);
+        int e = 0;
+        (void)__builtin_frexpf(v, &e);
+        sh[m] = (v > 0.0f && v <= 3.402823466e38f) ? 14 - e : 0;
+    }
+}
+
+template <int XW, int MT>
 __device__ __forceinline__ void stage_x_q4_x32(const float* __restrict__ x, int M, int K, int total, uint32_t* xq,
-                                               uint32_t* xq_lo, float2* cx)
+                                               uint32_t* xq_lo, float2* cx, const int (&sh)[MT])
 {
     const int words = K >> 3;
     for (int base = 0; base < total; base += XW * kBlock) {
@@ -136,7 +180,11 @@ __device__ __forceinline__ void stage_x_q4_x32(const float* __restrict__ x, int 
 #pragma unroll
         for (int j = 0; j < XW; ++j) {
             const int idx = base + j * kBlock + (int)threadIdx.x;
-            stage_word_q4_x32(ra[j], rb[j], idx, idx < total, xq, xq_lo, cx);
+            const int m = min(idx / words, MT - 1);
+            int shm = sh[0];
+#pragma unroll
+            for (int r = 1; r < MT; ++r) shm = m == r ? sh[r] : shm;  // constant indices: no scratch
+            stage_word_q4_x32(ra[j], rb[j], shm, idx, idx < total, xq, xq_lo, cx);
         }
     }
 }
@@ -284,12 +332,14 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_f16x_kernel(
     const int total = MT * (K >> 3);
 
     constexpr int XW = MT == 1 ? 4 : 8;
+    int xsh[MT] = {};  // f32 x: per-row exponent shift (x32_row_shifts); 0 for f16 x
     u4_t wa[kUnroll][R];
     uint32_t sa[kUnroll][R], ba[kUnroll][R];
     if constexpr (XS) {
         // the weights first: x is a cache hit after the first blocks, the weights are not
         load_pass_q4<LPR, R, SBT>(wq, S, B, row0, 1, lane, N, CPR, gpr, gshift, wa, sa, ba);
-        stage_x_q4_x32<XW / 2>(reinterpret_cast<const float*>(xv), M, K, total, xq, xq_lo, cx);
+        x32_row_shifts<MT>(reinterpret_cast<const float*>(xv), M, K, xsh);
+        stage_x_q4_x32<XW / 2>(reinterpret_cast<const float*>(xv), M, K, total, xq, xq_lo, cx, xsh);
     } else {
         const _Float16* x = reinterpret_cast<const _Float16*>(xv);
         u4_t xr[XW];
@@ -325,7 +375,10 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_f16x_kernel(
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
-        for (int m = 0; m < MT; ++m) acc[r][m] = group_sum<LPR>(acc[r][m]);
+        for (int m = 0; m < MT; ++m) {
+            acc[r][m] = group_sum<LPR>(acc[r][m]);
+            if constexpr (XS) acc[r][m] = __builtin_ldexpf(acc[r][m], -xsh[m]);
+        }
 
     if (lane == 0) {
 #pragma unroll
@@ -340,11 +393,12 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_f16x_kernel(
     }
 }
 
-// Gate/up + SiLU for MLX q4 in one launch (the mv2 + silu_mul pattern of the
-// reference's fused graphs: metal.rs:512-541 and 232-243, llama_graph.rs:318-327).
-// A team owns output row n of both matrices: its two rows (gate, up) go through
-// the same loads and dot as qgemv_q4_f16x_kernel's R = 2 rows, and lane 0 writes
-// h[m, n] = (g * (1 / (1 + exp(-g)))) * u, silu_mul_kernel's order.
+// Gate/up + SiLU (or tanh GELU) for MLX q4 in one launch (the mv2 + silu_mul
+// pattern of the reference's fused graphs: metal.rs:512-541 and 232-243,
+// llama_graph.rs:318-327; Gemma's gelu_tanh * up, gemma.rs:844-846).  A team owns
+// output row n of both matrices: its two rows (gate, up) go through the same
+// loads and dot as qgemv_q4_f16x_kernel's R = 2 rows, and lane 0 writes
+// h[m, n] = act_mul(act, g, u).
 template <int LPR, int SBT, int U = kUnroll>
 __device__ __forceinline__ void load_pass_q4_gu(const u4_t* __restrict__ wg, const void* __restrict__ Sg,
                                                 const void* __restrict__ Bg, const u4_t* __restrict__ wu,
@@ -370,7 +424,7 @@ template <int LPR, int MT, int SBT, bool MP, bool XS = false>
 __global__ __launch_bounds__(kBlock) void qgemv_q4_gate_up_silu_kernel(
     const u4_t* __restrict__ wg, const void* __restrict__ Sg, const void* __restrict__ Bg,
     const u4_t* __restrict__ wu, const void* __restrict__ Su, const void* __restrict__ Bu,
-    const void* __restrict__ xv, float* __restrict__ h, int M, int N, int K, int gshift)
+    const void* __restrict__ xv, float* __restrict__ h, int M, int N, int K, int gshift, int act)
 {
     extern __shared__ __align__(16) uint32_t lds[];
     const int CPR = K >> 5;
@@ -385,12 +439,14 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_gate_up_silu_kernel(
     const int total = MT * (K >> 3);
 
     constexpr int XW = MT == 1 ? 4 : 8;
+    int xsh[MT] = {};  // f32 x: per-row exponent shift (x32_row_shifts); 0 for f16 x
     u4_t wa[kUnroll][2];
     uint32_t sa[kUnroll][2], ba[kUnroll][2];
     if constexpr (XS) {
         // f32 x as hi + lo f16 parts (stage_word_q4_x32); the weights first
         load_pass_q4_gu<LPR, SBT>(wg, Sg, Bg, wu, Su, Bu, n, lane, N, CPR, gpr, gshift, wa, sa, ba);
-        stage_x_q4_x32<XW / 2>(reinterpret_cast<const float*>(xv), M, K, total, xq, xq_lo, cx);
+        x32_row_shifts<MT>(reinterpret_cast<const float*>(xv), M, K, xsh);
+        stage_x_q4_x32<XW / 2>(reinterpret_cast<const float*>(xv), M, K, total, xq, xq_lo, cx, xsh);
     } else {
         const _Float16* x = reinterpret_cast<const _Float16*>(xv);
         u4_t xr[XW];
@@ -425,15 +481,14 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_gate_up_silu_kernel(
 #pragma unroll
     for (int r = 0; r < 2; ++r)
 #pragma unroll
-        for (int m = 0; m < MT; ++m) acc[r][m] = group_sum<LPR>(acc[r][m]);
+        for (int m = 0; m < MT; ++m) {
+            acc[r][m] = group_sum<LPR>(acc[r][m]);
+            if constexpr (XS) acc[r][m] = __builtin_ldexpf(acc[r][m], -xsh[m]);
+        }
     if (lane == 0) {
 #pragma unroll
         for (int m = 0; m < MT; ++m)
-            if (m < M) {
-                const float g = acc[0][m];
-                const float sig = 1.0f / (1.0f + expf(-g));
-                h[(size_t)m * N + n] = (g * sig) * acc[1][m];
-            }
+            if (m < M) h[(size_t)m * N + n] = act_mul(act, acc[0][m], acc[1][m]);
     }
 }
 
@@ -482,11 +537,13 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_segs_kernel(Q4Segs segs, cons
         }
     }
     constexpr int XW = MT == 1 ? 4 : 8;
+    int xsh[MT] = {};  // f32 x: per-row exponent shift (x32_row_shifts); 0 for f16 x
     u4_t wa[kUnroll][1];
     uint32_t sa[kUnroll][1], ba[kUnroll][1];
     if constexpr (XS) {
         load_pass_q4<LPR, 1, SBT>(sg.w, sg.S, sg.B, v, 1, lane, sg.n, CPR, gpr, gshift, wa, sa, ba);
-        stage_x_q4_x32<XW / 2>(reinterpret_cast<const float*>(xv), M, K, total, xq, xq_lo, cx);
+        x32_row_shifts<MT>(reinterpret_cast<const float*>(xv), M, K, xsh);
+        stage_x_q4_x32<XW / 2>(reinterpret_cast<const float*>(xv), M, K, total, xq, xq_lo, cx, xsh);
     } else {
         const _Float16* x = reinterpret_cast<const _Float16*>(xv);
         u4_t xr[XW];
@@ -517,7 +574,10 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_segs_kernel(Q4Segs segs, cons
         }
     }
 #pragma unroll
-    for (int m = 0; m < MT; ++m) acc[0][m] = group_sum<LPR>(acc[0][m]);
+    for (int m = 0; m < MT; ++m) {
+        acc[0][m] = group_sum<LPR>(acc[0][m]);
+        if constexpr (XS) acc[0][m] = __builtin_ldexpf(acc[0][m], -xsh[m]);
+    }
     if (lane == 0) {
         const float bv = sg.bias ? sg.bias[v] : 0.0f;
 #pragma unroll
@@ -1359,13 +1419,15 @@ __global__ __launch_bounds__(kBlock) void qgemv_i4_generic_kernel(const uint8_t*
 //     [seg0 rows; seg1 rows; seg2 rows], each row reading its own matrix,
 //     scale, bias and output;
 //   * SILU: row n of seg0 (gate) and row n of seg1 (up);
-//     h[n] = silu(g) * u with g, u the scaled (and biased) row results and
-//     silu(g) = g / (1 + exp(-g)), written to seg0's output.
+//     h[n] = act(g) * u with g, u the scaled (and biased) row results and
+//     act silu(g) = g / (1 + exp(-g)) or the tanh GELU (act_mul, segs.act),
+//     written to seg0's output.
 // ---------------------------------------------------------------------------
 using I8Seg = I8FusedSeg;
 
 struct I8Segs {
     I8Seg g0, g1, g2;
+    int act;  // gate/up epilogue (SILU = true): ACT_SILU or ACT_GELU_TANH
 };
 
 __device__ __forceinline__ I8Seg seg_of(const I8Segs& t, int i)
@@ -1477,11 +1539,7 @@ __global__ __launch_bounds__(kBlock) void qgemv_i8_fused_kernel(I8Segs segs, int
         const int n = segs.g0.n;
 #pragma unroll
         for (int m = 0; m < MT; ++m)
-            if (m < M) {
-                const float g = val[0][m];
-                const float sig = 1.0f / (1.0f + expf(-g));
-                h[(size_t)m * n + first] = (g * sig) * val[1][m];
-            }
+            if (m < M) h[(size_t)m * n + first] = act_mul(segs.act, val[0][m], val[1][m]);
     } else {
 #pragma unroll
         for (int r = 0; r < R; ++r) {
@@ -1709,7 +1767,7 @@ hipError_t launch_i8_fused_xt(int lpr, const I8Segs& t, int total_rows, int sdt,
 template <int LPR, int MT, bool MP, bool XS>
 hipError_t launch_q4_gu_shape(int sbt, const uint32_t* wg, const void* Sg, const void* Bg, const uint32_t* wu,
                               const void* Su, const void* Bu, const void* x, float* h, int M, int N, int K,
-                              int gshift, hipStream_t st)
+                              int gshift, int act, hipStream_t st)
 {
     const dim3 grid((N + (kBlock / LPR) - 1) / (kBlock / LPR));
     const size_t lds = (size_t)qgemv_q4_lds_bytes(M, K) + (XS ? (size_t)MT * (K >> 5) * 64 : 0);
@@ -1718,7 +1776,7 @@ hipError_t launch_q4_gu_shape(int sbt, const uint32_t* wg, const void* Sg, const
     auto go = [&](auto kern) {
         if (lds > 64 * 1024)
             if (hipError_t e = allow_big_lds(kern, (int)lds); e != hipSuccess) return e;
-        hipLaunchKernelGGL(kern, grid, dim3(kBlock), lds, st, g4, Sg, Bg, u4, Su, Bu, x, h, M, N, K, gshift);
+        hipLaunchKernelGGL(kern, grid, dim3(kBlock), lds, st, g4, Sg, Bg, u4, Su, Bu, x, h, M, N, K, gshift, act);
         return hipGetLastError();
     };
     if (sbt == DT_F16) return go(qgemv_q4_gate_up_silu_kernel<LPR, MT, DT_F16, MP, XS>);
@@ -1729,13 +1787,14 @@ hipError_t launch_q4_gu_shape(int sbt, const uint32_t* wg, const void* Sg, const
 template <int MT, bool XS>
 hipError_t launch_q4_gu_mt(int sbt, const uint32_t* wg, const void* Sg, const void* Bg, const uint32_t* wu,
                            const void* Su, const void* Bu, const void* x, float* h, int M, int N, int K, int gshift,
-                           hipStream_t st)
+                           int act, hipStream_t st)
 {
     const int CPR = K >> 5;
     const int lpr = pick_shape(CPR, 2 * N, false).lpr;
 #define CELLM_GU_L(L_)                                                                                               \
-    return CPR > kUnroll * L_ ? launch_q4_gu_shape<L_, MT, true, XS>(sbt, wg, Sg, Bg, wu, Su, Bu, x, h, M, N, K, gshift, st) \
-                              : launch_q4_gu_shape<L_, MT, false, XS>(sbt, wg, Sg, Bg, wu, Su, Bu, x, h, M, N, K, gshift, st)
+    return CPR > kUnroll * L_                                                                                      \
+               ? launch_q4_gu_shape<L_, MT, true, XS>(sbt, wg, Sg, Bg, wu, Su, Bu, x, h, M, N, K, gshift, act, st)  \
+               : launch_q4_gu_shape<L_, MT, false, XS>(sbt, wg, Sg, Bg, wu, Su, Bu, x, h, M, N, K, gshift, act, st)
     switch (lpr) {
     case 8: CELLM_GU_L(8);
     case 16: CELLM_GU_L(16);
@@ -2043,17 +2102,17 @@ bool qgemv_q4_gate_up_supported(int xdt, int M, int K, int group_size, const voi
 
 hipError_t launch_qgemv_q4_gate_up_silu(const uint32_t* wg, const void* Sg, const void* Bg, const uint32_t* wu,
                                         const void* Su, const void* Bu, int sbt, int group_size, const void* x,
-                                        int xdt, float* h, int M, int N, int K, hipStream_t st)
+                                        int xdt, float* h, int M, int N, int K, int act, hipStream_t st)
 {
     const int gshift = __builtin_ctz((unsigned)group_size);
     if (xdt == DT_F32) {
-        if (M == 1) return launch_q4_gu_mt<1, true>(sbt, wg, Sg, Bg, wu, Su, Bu, x, h, M, N, K, gshift, st);
-        if (M == 2) return launch_q4_gu_mt<2, true>(sbt, wg, Sg, Bg, wu, Su, Bu, x, h, M, N, K, gshift, st);
-        return launch_q4_gu_mt<4, true>(sbt, wg, Sg, Bg, wu, Su, Bu, x, h, M, N, K, gshift, st);
+        if (M == 1) return launch_q4_gu_mt<1, true>(sbt, wg, Sg, Bg, wu, Su, Bu, x, h, M, N, K, gshift, act, st);
+        if (M == 2) return launch_q4_gu_mt<2, true>(sbt, wg, Sg, Bg, wu, Su, Bu, x, h, M, N, K, gshift, act, st);
+        return launch_q4_gu_mt<4, true>(sbt, wg, Sg, Bg, wu, Su, Bu, x, h, M, N, K, gshift, act, st);
     }
-    if (M == 1) return launch_q4_gu_mt<1, false>(sbt, wg, Sg, Bg, wu, Su, Bu, x, h, M, N, K, gshift, st);
-    if (M == 2) return launch_q4_gu_mt<2, false>(sbt, wg, Sg, Bg, wu, Su, Bu, x, h, M, N, K, gshift, st);
-    return launch_q4_gu_mt<4, false>(sbt, wg, Sg, Bg, wu, Su, Bu, x, h, M, N, K, gshift, st);
+    if (M == 1) return launch_q4_gu_mt<1, false>(sbt, wg, Sg, Bg, wu, Su, Bu, x, h, M, N, K, gshift, act, st);
+    if (M == 2) return launch_q4_gu_mt<2, false>(sbt, wg, Sg, Bg, wu, Su, Bu, x, h, M, N, K, gshift, act, st);
+    return launch_q4_gu_mt<4, false>(sbt, wg, Sg, Bg, wu, Su, Bu, x, h, M, N, K, gshift, act, st);
 }
 
 bool qgemv_q4_segs_supported(int xdt, int M, int K, int group_size, const void* x, const Q4FusedSeg* segs, int nseg)
@@ -2143,10 +2202,11 @@ bool qgemv_i8_fused_supported(int xdt, int M, int K, const void* x, const I8Fuse
     return true;
 }
 
-hipError_t launch_qgemv_i8_fused(const I8FusedSeg* segs, int nseg, bool silu, int sdt, const void* x, int xdt, int M,
-                                 int K, hipStream_t st)
+hipError_t launch_qgemv_i8_fused(const I8FusedSeg* segs, int nseg, bool silu, int act, int sdt, const void* x, int xdt,
+                                 int M, int K, hipStream_t st)
 {
     I8Segs t;
+    t.act = act;
     t.g0 = segs[0];
     t.g1 = nseg > 1 ? segs[1] : segs[0];
     t.g2 = nseg > 2 ? segs[2] : segs[0];

@@ -255,6 +255,34 @@ class HipOps:
             _torch_dtype_code(sg), group, _dev_ptr(x), _torch_dtype_code(x), _dev_ptr(h), m, n, k,
             _stream_ptr(stream)))
 
+    def encode_gate_up_gelu_i8(self, wg, sg, wu, su, x, h, bg=None, bu=None, stream=None) -> None:
+        """h = gelu_tanh(Wg.x * sg (+bg)) * (Wu.x * su (+bu)); int8 gate/up (Gemma's MLP)."""
+        n, k = wg.shape
+        m = x.numel() // k
+        if sg.dtype != su.dtype:
+            raise TypeError("gate/up scales must share a dtype")
+        check(self._lib.cellm_hip_qgemv_i8_gate_up_gelu(
+            self._h, _dev_ptr(wg), _dev_ptr(sg), sg.numel(), _dev_ptr(bg), _dev_ptr(wu), _dev_ptr(su), su.numel(),
+            _dev_ptr(bu), _torch_dtype_code(sg), _dev_ptr(x), _torch_dtype_code(x), _dev_ptr(h), m, n, k,
+            _stream_ptr(stream)))
+
+    def encode_gate_up_gelu_q4_affine(self, wg, sg, bg, wu, su, bu, x, h, group: int = 64, stream=None) -> None:
+        """h = gelu_tanh(dequant(Wg).x) * (dequant(Wu).x); MLX 4-bit affine gate/up."""
+        n, k = wg.shape[0], wg.shape[1] * 8
+        m = x.numel() // k
+        check(self._lib.cellm_hip_qgemv_q4_affine_gate_up_gelu(
+            self._h, _dev_ptr(wg), _dev_ptr(sg), _dev_ptr(bg), _dev_ptr(wu), _dev_ptr(su), _dev_ptr(bu),
+            _torch_dtype_code(sg), group, _dev_ptr(x), _torch_dtype_code(x), _dev_ptr(h), m, n, k,
+            _stream_ptr(stream)))
+
+    def encode_gate_up_gelu_i4_sym(self, wg, sg_f16, wu, su_f16, gs: int, x, h, k: int, stream=None) -> None:
+        """h = gelu_tanh(i4(Wg).x) * (i4(Wu).x); symmetric i4 gate/up [n, ceil(k/2)] bytes, f16 scales."""
+        n = wg.shape[0]
+        m = x.numel() // k
+        check(self._lib.cellm_hip_qgemv_i4_gate_up_gelu(
+            self._h, _dev_ptr(wg), _dev_ptr(sg_f16), sg_f16.numel(), _dev_ptr(wu), _dev_ptr(su_f16), su_f16.numel(),
+            gs, _dev_ptr(x), _torch_dtype_code(x), _dev_ptr(h), m, n, k, _stream_ptr(stream)))
+
     @staticmethod
     def qgemv_op_i8(w, scales, x, y, bias=None) -> "_lib.QgemvOp":
         """One cellm_hip_qgemv_op_t of kind int8 (arguments as encode_qgemv_i8)."""
@@ -421,6 +449,16 @@ class HipOps:
                                                 _dev_ptr(positions_i32), _dev_ptr(cos_sin), cos_sin.shape[0],
                                                 _stream_ptr(stream)))
 
+    def encode_rope_interleaved(self, x, n_heads: int, head_dim: int, positions_i32, cos_sin, stream=None) -> None:
+        rows = positions_i32.numel()
+        check(self._lib.cellm_hip_rope_interleaved_f32(self._h, _dev_ptr(x), rows, n_heads, head_dim,
+                                                       _dev_ptr(positions_i32), _dev_ptr(cos_sin), cos_sin.shape[0],
+                                                       _stream_ptr(stream)))
+
+    def set_rope_interleaved(self, interleaved: bool) -> None:
+        """RoPE pair layout of encode_rope_kv_write / encode_decode_qkv on this context."""
+        check(self._lib.cellm_hip_set_rope_interleaved(self._h, 1 if interleaved else 0))
+
     def encode_kv_write(self, k, v, positions_i32, kcache, vcache, block_tables, total_blocks: int, n_layers: int,
                         tokens_per_block: int, layer: int, stream=None) -> None:
         rows = positions_i32.numel()
@@ -461,6 +499,11 @@ class HipOps:
         """gate = silu(gate) * up in place (f32), silu_mul_f32_inplace."""
         check(self._lib.cellm_hip_silu_mul_f32(self._h, _dev_ptr(gate), _dev_ptr(up), gate.numel(),
                                                _stream_ptr(stream)))
+
+    def encode_gelu_tanh_mul(self, gate, up, stream=None) -> None:
+        """gate = gelu_tanh(gate) * up in place (f32), gelu_tanh_mul_f32_inplace."""
+        check(self._lib.cellm_hip_gelu_tanh_mul_f32(self._h, _dev_ptr(gate), _dev_ptr(up), gate.numel(),
+                                                    _stream_ptr(stream)))
 
     def encode_add_inplace(self, x, y, stream=None) -> None:
         check(self._lib.cellm_hip_add_f32_inplace(self._h, _dev_ptr(x), _dev_ptr(y), x.numel(), _stream_ptr(stream)))

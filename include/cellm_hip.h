@@ -127,7 +127,13 @@ int32_t cellm_hip_qgemv_i8(cellm_hip_ctx_t* ctx, const int8_t* w, const void* sc
  * and its dequant -> MetalOps::logits_f32 route (lfm.rs:1049-1054).
  * k % 8 == 0; group a power of two >= 8 (MLX uses 64).  2..64 rows with f16 x
  * run the batched MFMA path, split over k through the per-stream workspace
- * for few output rows over a long k, as cellm_hip_qgemv_i8. */
+ * for few output rows over a long k, as cellm_hip_qgemv_i8.
+ * f32 x (m <= 4) is multiplied as two f16 parts, hi = RNE_f16(x') and
+ * lo = RNE_f16(x' - hi), of each row scaled by a power of two x' = x * 2^e
+ * that puts the row's largest |x| in [2^13, 2^14): any finite f32 x keeps
+ * about 22 bits (relative to its row's largest value), and the result is
+ * scaled back exactly.  This holds for the fused gate/up and QKV entry
+ * points below too. */
 int32_t cellm_hip_qgemv_q4_affine(cellm_hip_ctx_t* ctx, const uint32_t* wq, const void* scales, const void* biases,
                                   int32_t sb_dtype, int64_t group, const void* x, int32_t x_dtype, float* y,
                                   int64_t m, int64_t n, int64_t k, void* stream);
@@ -183,6 +189,28 @@ int32_t cellm_hip_qgemv_q4_affine_gate_up_silu(cellm_hip_ctx_t* ctx, const uint3
                                                const void* bg, const uint32_t* wu, const void* su, const void* bu,
                                                int32_t sb_dtype, int64_t group, const void* x, int32_t x_dtype,
                                                float* h, int64_t m, int64_t n, int64_t k, void* stream);
+
+/* Gemma's MLP activation in place of SiLU (crates/cellm-model/src/gemma.rs:844-846,
+ * gemma_graph.rs:435-436):
+ *   h = gelu_tanh(g) * u,  gelu_tanh(g) = 0.5 g (1 + tanh(0.7978846 (g + 0.044715 g^3)))
+ * in the order of gelu_tanh_f32 (gemma.rs:1689-1693), g and u as in the SiLU
+ * entry points above, with the same arguments, launch shapes and fallbacks. */
+int32_t cellm_hip_qgemv_i8_gate_up_gelu(cellm_hip_ctx_t* ctx, const int8_t* wg, const void* sg, int64_t n_sg,
+                                        const float* bg, const int8_t* wu, const void* su, int64_t n_su,
+                                        const float* bu, int32_t scale_dtype, const void* x, int32_t x_dtype, float* h,
+                                        int64_t m, int64_t n, int64_t k, void* stream);
+int32_t cellm_hip_qgemv_q4_affine_gate_up_gelu(cellm_hip_ctx_t* ctx, const uint32_t* wg, const void* sg,
+                                               const void* bg, const uint32_t* wu, const void* su, const void* bu,
+                                               int32_t sb_dtype, int64_t group, const void* x, int32_t x_dtype,
+                                               float* h, int64_t m, int64_t n, int64_t k, void* stream);
+
+/* The same over symmetric i4 gate/up weights (gemma.rs:1446-1471 runs the i4
+ * branch of linear_f16_out_in for each): two cellm_hip_qgemv_i4_sym launches
+ * (arguments as there, one gs for both) and the GELU * up kernel. */
+int32_t cellm_hip_qgemv_i4_gate_up_gelu(cellm_hip_ctx_t* ctx, const uint8_t* wg, const uint16_t* sg, int64_t n_sg,
+                                        const uint8_t* wu, const uint16_t* su, int64_t n_su, int64_t gs,
+                                        const void* x, int32_t x_dtype, float* h, int64_t m, int64_t n, int64_t k,
+                                        void* stream);
 
 /* One projection of a batch (cellm_hip_qgemv_batch).  kind
  * CELLM_HIP_OP_QGEMV_I8 takes the arguments of cellm_hip_qgemv_i8 (w int8,
@@ -341,6 +369,19 @@ int32_t cellm_hip_add_rms_norm(cellm_hip_ctx_t* ctx, float* x, const float* y, c
 int32_t cellm_hip_rope_half_f32(cellm_hip_ctx_t* ctx, float* x, int64_t rows, int64_t n_heads, int64_t head_dim,
                                 const int32_t* positions, const float* cos_sin, int64_t table_positions, void* stream);
 
+/* rope_interleaved_inplace_f32 (cpu_kernels.rs:279-292): the same rotation of
+ * the pairs (2i, 2i + 1) of each head instead of (i, i + head_dim/2), with the
+ * same table (the angle of pair i is pos * theta^(-2i/head_dim) in both). */
+int32_t cellm_hip_rope_interleaved_f32(cellm_hip_ctx_t* ctx, float* x, int64_t rows, int64_t n_heads, int64_t head_dim,
+                                       const int32_t* positions, const float* cos_sin, int64_t table_positions,
+                                       void* stream);
+
+/* The RoPE layout of the context's fused decode ops (cellm_hip_rope_kv_write_f16
+ * and cellm_hip_decode_qkv_rope_kv): 0 rotate-half (the default), 1 interleaved.
+ * The reference's Llama runner picks it once, from CELLM_LLAMA_ROPE_INTERLEAVED
+ * (crates/cellm-model/src/llama.rs:80-82, used at :391-396). */
+int32_t cellm_hip_set_rope_interleaved(cellm_hip_ctx_t* ctx, int32_t interleaved);
+
 /* MetalKvStorage::encode_write_token_f32 / write_token_f32 (kvcache.rs:589-615):
  * k, v [rows][kv_dim] f32 -> f16 (RNE) at each row's position in `layer`. */
 int32_t cellm_hip_kv_write_f16(cellm_hip_ctx_t* ctx, const float* k, const float* v, int64_t rows, int64_t kv_dim,
@@ -353,7 +394,8 @@ int32_t cellm_hip_kv_write_f16(cellm_hip_ctx_t* ctx, const float* k, const float
  * [rows][n_heads][head_dim] and k [rows][n_kv_heads][head_dim], then the
  * rotated k and v written as f16 at each row's position in `layer`.  Same
  * results as cellm_hip_rope_half_f32 on q and on k followed by
- * cellm_hip_kv_write_f16. */
+ * cellm_hip_kv_write_f16 (cellm_hip_rope_interleaved_f32 when the context's
+ * layout is interleaved, cellm_hip_set_rope_interleaved). */
 int32_t cellm_hip_rope_kv_write_f16(cellm_hip_ctx_t* ctx, float* q, float* k, const float* v, int64_t rows,
                                     int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, const int32_t* positions,
                                     const float* cos_sin, int64_t table_positions, uint16_t* kcache, uint16_t* vcache,
@@ -368,7 +410,7 @@ int32_t cellm_hip_rope_kv_write_f16(cellm_hip_ctx_t* ctx, float* q, float* k, co
  * each row's position in `layer` of the paged cache.  int8 weights [out][hidden]
  * with f16 row scales.  x_out must be a different buffer from x_prev and y.
  * rows 1..4, hidden % 16 == 0 and <= 4096; otherwise CELLM_HIP_ERR_UNSUPPORTED
- * (use the separate calls). */
+ * (use the separate calls).  RoPE pairs follow cellm_hip_set_rope_interleaved. */
 int32_t cellm_hip_decode_qkv_rope_kv(cellm_hip_ctx_t* ctx, const float* x_prev, const float* y, float* x_out,
                                      const float* norm_w, float eps, const int8_t* wq, const uint16_t* sq,
                                      const int8_t* wk, const uint16_t* sk, const int8_t* wv, const uint16_t* sv,
@@ -431,6 +473,11 @@ int32_t cellm_hip_attention_gqa_f16kv_noalloc(cellm_hip_ctx_t* ctx, const float*
  * llama.rs:477-484): gate[i] = silu(gate[i]) * up[i], silu(g) = g / (1 + exp(-g)),
  * in place on gate. */
 int32_t cellm_hip_silu_mul_f32(cellm_hip_ctx_t* ctx, float* gate, const float* up, int64_t n, void* stream);
+
+/* MetalOps::encode_gelu_tanh_mul_f32_inplace (metal.rs:245-257, 966-982; the CPU
+ * loop of gemma.rs:844-846): gate[i] = gelu_tanh(gate[i]) * up[i], gelu_tanh as
+ * cellm_hip_qgemv_i8_gate_up_gelu. */
+int32_t cellm_hip_gelu_tanh_mul_f32(cellm_hip_ctx_t* ctx, float* gate, const float* up, int64_t n, void* stream);
 
 /* MetalOps::encode_add_f32_inplace: x[i] += y[i]. */
 int32_t cellm_hip_add_f32_inplace(cellm_hip_ctx_t* ctx, float* x, const float* y, int64_t n, void* stream);

@@ -64,6 +64,8 @@ def _declare(L):
         "oracle_gemm_xwT_f32": (None, [vp, i32, vp, sz, sz, sz, vp]),
         "oracle_rms_norm_f32": (None, [vp, vp, sz, f32, vp]),
         "oracle_rope_half_f32": (None, [vp, sz, sz, sz, f32]),
+        "oracle_rope_interleaved_f32": (None, [vp, sz, sz, sz, f32]),
+        "oracle_gelu_tanh_mul_f32": (None, [vp, vp, sz]),
         "oracle_softmax_f32": (None, [vp, sz]),
         "oracle_attention_gqa_f16kv": (None, [vp, vp, vp, sz, vp, sz, sz, sz, f32, f32, vp, vp]),
         "oracle_silu_mul_f32": (None, [vp, vp, sz]),
@@ -330,6 +332,13 @@ def rope_half_(x: np.ndarray, n_heads: int, head_dim: int, pos: int, theta: floa
     return x
 
 
+def rope_interleaved_(x: np.ndarray, n_heads: int, head_dim: int, pos: int, theta: float) -> np.ndarray:
+    """rope_interleaved_inplace_f32 (cpu_kernels.rs:279-292), in place."""
+    assert x.dtype == np.float32 and x.flags["C_CONTIGUOUS"]
+    lib().oracle_rope_interleaved_f32(_p(x), n_heads, head_dim, pos, theta)
+    return x
+
+
 def softmax_(x: np.ndarray) -> np.ndarray:
     assert x.dtype == np.float32 and x.flags["C_CONTIGUOUS"]
     lib().oracle_softmax_f32(_p(x), x.size)
@@ -354,6 +363,13 @@ def attention_gqa_f16kv(kcache_bits, vcache_bits, bases, q, n_heads, n_kv_heads,
 def silu_mul_(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
     assert gate.dtype == np.float32 and gate.flags["C_CONTIGUOUS"]
     lib().oracle_silu_mul_f32(_p(gate), _p(np.ascontiguousarray(up, np.float32)), gate.size)
+    return gate
+
+
+def gelu_tanh_mul_(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    """gate = gelu_tanh_f32(gate) * up in place (gemma.rs:844-846, 1689-1693)."""
+    assert gate.dtype == np.float32 and gate.flags["C_CONTIGUOUS"]
+    lib().oracle_gelu_tanh_mul_f32(_p(gate), _p(np.ascontiguousarray(up, np.float32)), gate.size)
     return gate
 
 

@@ -15,9 +15,12 @@
  * Parity pins (tests/test_oracle.py): every function below is checked against
  * closed forms, IEEE conversions from numpy, exhaustive nibble/byte sweeps,
  * fp64 error bounds and brute-force tiny cases.  The config-5 decode-step
- * helpers at the bottom (rms_norm, RoPE, attention, softmax, SiLU) are pinned
- * by closed forms (RoPE at pos 0 is the identity, rotation preserves the norm,
- * softmax of equal scores is uniform, attention over one token returns v).
+ * helpers at the bottom (rms_norm, RoPE in both layouts, attention, softmax,
+ * SiLU, tanh GELU) are pinned by closed forms (RoPE at pos 0 is the identity,
+ * rotation preserves the norm of each pair and the two layouts are one
+ * permutation apart, softmax of equal scores is uniform, attention over one
+ * token returns v, gelu(0) = 0 and gelu(x) - gelu(-x) = x, the tanh GELU
+ * within its published distance of the erf GELU).
  * Their glibc expf/sinf/cosf/powf calls are not bit-pinned across machines;
  * that is why the decode step is compared by greedy token id.
  *
@@ -658,6 +661,25 @@ void oracle_rope_half_f32(float* x, size_t n_heads, size_t head_dim, size_t pos,
     }
 }
 
+/* rope_interleaved_inplace_f32 (cpu_kernels.rs:279-292): the pairs (2i, 2i + 1)
+ * of each head, with the angle of pair i as in the rotate-half form above. */
+void oracle_rope_interleaved_f32(float* x, size_t n_heads, size_t head_dim, size_t pos, float theta)
+{
+    size_t half = head_dim / 2;
+    for (size_t h = 0; h < n_heads; ++h) {
+        float* head = x + h * head_dim;
+        for (size_t i = 0; i < half; ++i) {
+            float inv_freq = powf(theta, -(2.0f * (float)i) / (float)head_dim);
+            float angle = (float)pos * inv_freq;
+            float s = sinf(angle), c = cosf(angle);
+            float x0 = head[2 * i];
+            float x1 = head[2 * i + 1];
+            head[2 * i] = x0 * c - x1 * s;
+            head[2 * i + 1] = x1 * c + x0 * s;
+        }
+    }
+}
+
 /* softmax_f32_inplace_cpu_local (crates/cellm-cache/src/kvcache.rs:1206-1227). */
 void oracle_softmax_f32(float* x, size_t n)
 {
@@ -717,6 +739,21 @@ void oracle_silu_mul_f32(float* gate, const float* up, size_t n)
         gate[i] = g * s;
     }
     for (size_t i = 0; i < n; ++i) gate[i] *= up[i];
+}
+
+/* gelu_tanh_f32 (crates/cellm-model/src/gemma.rs:1689-1693) times up, in place on
+ * gate, as the Gemma MLP loop (gemma.rs:844-846): k = 0.797_884_6f32,
+ * c = 0.044_715f32, 0.5 * x * (1 + tanh(k * (x + c * x * x * x))) with Rust's
+ * left-to-right products, then * up[i]. */
+void oracle_gelu_tanh_mul_f32(float* gate, const float* up, size_t n)
+{
+    const float k = 0.7978846f;
+    const float c = 0.044715f;
+    for (size_t i = 0; i < n; ++i) {
+        float x = gate[i];
+        float g = 0.5f * x * (1.0f + tanhf(k * (x + c * x * x * x)));
+        gate[i] = g * up[i];
+    }
 }
 
 /* topk_from_logits(..)[0] for top_k = 1 (llama.rs:1049-1078): first index of

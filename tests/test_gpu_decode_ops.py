@@ -121,6 +121,22 @@ def test_rope_half_bit_exact(ops, steplib, heads, hd):
         np.testing.assert_array_equal(got[r], ref)
 
 
+@pytest.mark.parametrize("heads,hd", [(15, 64), (4, 256)])
+def test_rope_interleaved_bit_exact(ops, steplib, heads, hd):
+    """cellm_hip_rope_interleaved_f32 against rope_interleaved_inplace_f32 (cpu_kernels.rs:279-292)
+    bit for bit, from the same table as the rotate-half form."""
+    positions = np.array([0, 1, 511, 2047], np.int32)
+    theta = 10000.0
+    table = rope_table(steplib, theta, hd, 2048)
+    x = np.stack([oracle.gen_normal((heads * hd,), 0xD0000038 + i, 0.0, 1.0) for i in range(4)]).astype(np.float32)
+    xd = dev(x.copy())
+    ops.encode_rope_interleaved(xd, heads, hd, dev(positions), dev(table))
+    torch.cuda.synchronize()
+    got = xd.cpu().numpy()
+    for r, p in enumerate(positions):
+        np.testing.assert_array_equal(got[r], oracle.rope_interleaved_(x[r].copy(), heads, hd, int(p), theta))
+
+
 def paged_setup(L, tpb, nkv, hd, rows, blocks_per_row, seed):
     total = rows * blocks_per_row + 3
     kvd = nkv * hd
@@ -326,10 +342,12 @@ def test_add_rms_norm(ops, wdt, n):
         assert rel_err(got[r], oracle.rms_norm(a[r] + b[r], w.astype(np.float32), 1e-5)) <= 1e-6
 
 
+@pytest.mark.parametrize("interleaved", [False, True])
 @pytest.mark.parametrize("nh,nkv,hd", [(15, 5, 64), (16, 2, 128)])
-def test_rope_kv_write_matches_rope_then_write(ops, steplib, nh, nkv, hd):
+def test_rope_kv_write_matches_rope_then_write(ops, steplib, nh, nkv, hd, interleaved):
     """One launch = rope on q, rope on k, then the K/V write: q and k bit-exact
-    against the oracle's RoPE, the cache rows bit-exact against f16(k), f16(v),
+    against the oracle's RoPE (rotate-half, or interleaved after
+    cellm_hip_set_rope_interleaved), the cache rows bit-exact against f16(k), f16(v),
     every other cache element untouched; a negative position writes nothing."""
     L, tpb, rows, layer, theta = 3, 16, 4, 1, 10000.0
     kvd = nkv * hd
@@ -341,14 +359,19 @@ def test_rope_kv_write_matches_rope_then_write(ops, steplib, nh, nkv, hd):
     v = np.stack([oracle.gen_normal((kvd,), 0xD0000110 + r, 0.0, 1.0) for r in range(rows)]).astype(np.float32)
     qd, kd, vd = dev(q.copy()), dev(k.copy()), dev(v.copy())
     kc, vc = dev(k0.copy()), dev(v0.copy())
-    ops.encode_rope_kv_write(qd, kd, vd, nh, nkv, hd, dev(pos), dev(table), kc, vc, dev(bt), total, L, tpb, layer)
-    torch.cuda.synchronize()
+    ops.set_rope_interleaved(interleaved)
+    try:
+        ops.encode_rope_kv_write(qd, kd, vd, nh, nkv, hd, dev(pos), dev(table), kc, vc, dev(bt), total, L, tpb, layer)
+        torch.cuda.synchronize()
+    finally:
+        ops.set_rope_interleaved(False)
+    rope = oracle.rope_interleaved_ if interleaved else oracle.rope_half_
     gq, gk = qd.cpu().numpy(), kd.cpu().numpy()
     k_ref, v_ref = k0.copy(), v0.copy()
     for r in range(rows):
         p = max(int(pos[r]), 0)
-        np.testing.assert_array_equal(gq[r], oracle.rope_half_(q[r].copy(), nh, hd, p, theta))
-        kr = oracle.rope_half_(k[r].copy(), nkv, hd, p, theta)
+        np.testing.assert_array_equal(gq[r], rope(q[r].copy(), nh, hd, p, theta))
+        kr = rope(k[r].copy(), nkv, hd, p, theta)
         np.testing.assert_array_equal(gk[r], kr)
         if pos[r] >= 0:
             b = base_of(bt[r], int(pos[r]), layer, L, tpb, kvd)
@@ -366,12 +389,21 @@ def _i8_layer(out_dims, k, seed):
     return ws, ss
 
 
-@pytest.mark.parametrize("rows,with_y", [(4, True), (1, True), (3, False)])
-def test_decode_qkv_matches_separate_ops(ops, steplib, rows, with_y):
+@pytest.mark.parametrize("rows,with_y,interleaved", [(4, True, False), (1, True, False), (3, False, False),
+                                                    (4, True, True)])
+def test_decode_qkv_matches_separate_ops(ops, steplib, rows, with_y, interleaved):
     """cellm_hip_decode_qkv_rope_kv against add_rms_norm + three int8 GEMVs +
-    rope_kv_write: the residual exactly, q within 1e-5 (the GEMV sums its row
-    in another order), the written K/V rows within f16 rounding, no other
-    cache element touched."""
+    rope_kv_write, both with the context's RoPE layout: the residual exactly, q
+    within 1e-5 (the GEMV sums its row in another order), the written K/V rows
+    within f16 rounding, no other cache element touched."""
+    ops.set_rope_interleaved(interleaved)
+    try:
+        _decode_qkv_case(ops, steplib, rows, with_y)
+    finally:
+        ops.set_rope_interleaved(False)
+
+
+def _decode_qkv_case(ops, steplib, rows, with_y):
     H, nh, nkv, hd, L, tpb, layer = 960, 15, 5, 64, 3, 16, 2
     kvd = nkv * hd
     total, k0, v0, bt = paged_setup(L, tpb, nkv, hd, rows, 8, 0xD0000200)

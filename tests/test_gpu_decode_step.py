@@ -86,8 +86,9 @@ DIMS = dict(L=L, HID=HID, NH=NH, NKV=NKV, HD=HD, VOCAB=VOCAB, EPS=EPS, THETA=THE
 F64_TOL = 1e-4  # logits of an f32 step against the float64 step (observed: 7e-6 for the oracle step)
 
 
-def oracle_step(model, kcache, vcache, token, pos, bt):
+def oracle_step(model, kcache, vcache, token, pos, bt, interleaved=False):
     layers, embed, escale, fnorm = model
+    rope = oracle.rope_interleaved_ if interleaved else oracle.rope_half_
     t = token % VOCAB
     x = (embed[t].astype(np.float32) * np.float32(oracle.f16_bits_to_f32(escale[t:t + 1])[0])).astype(np.float32)
     bases = np.array([base_of(bt, tp, 0) for tp in range(pos + 1)], np.uint64)
@@ -97,8 +98,8 @@ def oracle_step(model, kcache, vcache, token, pos, bt):
         q = oracle.matmul_i8_f32(ws[0], ss[0], xn)
         k = oracle.matmul_i8_f32(ws[1], ss[1], xn)
         v = oracle.matmul_i8_f32(ws[2], ss[2], xn)
-        oracle.rope_half_(q, NH, HD, pos, THETA)
-        oracle.rope_half_(k, NKV, HD, pos, THETA)
+        rope(q, NH, HD, pos, THETA)
+        rope(k, NKV, HD, pos, THETA)
         wb = base_of(bt, pos, l)
         kcache[wb:wb + KVD] = k.astype(np.float16).view(np.uint16)
         vcache[wb:wb + KVD] = v.astype(np.float16).view(np.uint16)
@@ -290,6 +291,37 @@ def test_device_step_batched_sessions_match_cpu_reference():
             np.testing.assert_array_equal(got[~written], init[~written])
             d = np.abs(oracle.f16_bits_to_f32(got[written]) - oracle.f16_bits_to_f32(ref[written]))
             assert float(d.max()) <= 1e-2 * float(np.abs(oracle.f16_bits_to_f32(ref[written])).max())
+    finally:
+        lib.cellm_llama_dev_destroy(h)
+
+
+def test_device_step_interleaved_rope_from_env(monkeypatch):
+    """CELLM_LLAMA_ROPE_INTERLEAVED=1 at creation (llama.rs:80-82) switches the device runner's
+    q/k rotation to rope_interleaved_inplace_f32 (llama.rs:391-393): greedy ids of the 4 sessions
+    equal the CPU reference step with the interleaved RoPE, and its logits sit far from the
+    rotate-half step's."""
+    lib = dev_lib()
+    model = make_model()
+    monkeypatch.setenv("CELLM_LLAMA_ROPE_INTERLEAVED", "True")
+    h = dev_create(lib, model, SESSIONS)
+    monkeypatch.delenv("CELLM_LLAMA_ROPE_INTERLEAVED")
+    try:
+        k0, v0 = make_kv()
+        assert lib.cellm_llama_dev_kv_upload(h, k0.ctypes.data, v0.ctypes.data, k0.size) == 0, lib_err(lib)
+        bts = np.stack([block_table(s) for s in range(SESSIONS)]).astype(np.uint32)
+        tokens = np.array([(1000 + 7919 * s) % VOCAB for s in range(SESSIONS)], np.uint32)
+        positions = np.full(SESSIONS, CTX - 1, np.int32)
+        out_tok, _, logits = dev_step(lib, h, tokens, positions, bts)
+        for s in range(SESSIONS):
+            ref_id, ref_logits = oracle_step(model, k0.copy(), v0.copy(), int(tokens[s]), CTX - 1, bts[s],
+                                             interleaved=True)
+            rel = float(np.max(np.abs(logits[s] - ref_logits)) / np.max(np.abs(ref_logits)))
+            print(f"session {s}: device {out_tok[s]} ref {ref_id} logits rel err {rel:.2e}")
+            assert out_tok[s] == ref_id
+            assert rel <= 1e-3
+            if s == 0:
+                _, half_logits = oracle_step(model, k0.copy(), v0.copy(), int(tokens[s]), CTX - 1, bts[s])
+                assert float(np.max(np.abs(logits[s] - half_logits)) / np.max(np.abs(half_logits))) > 1e-2
     finally:
         lib.cellm_llama_dev_destroy(h)
 

@@ -514,6 +514,45 @@ def test_q4_affine_f32_activations(ops, n, k, m, sb, group):
     assert rel_err(oracle.qgemv_q4_affine(wq, s, b, xr, k, gs=group), ref) > 3e-5
 
 
+@pytest.mark.parametrize("entry", ["gemv", "gate_up_silu", "qkv"])
+def test_q4_affine_f32_activation_range(ops, entry):
+    """f32 x far from N(0,1) through the three hi + lo f16 kernels (lfm.rs:985-1066 takes any
+    f32 x): one row scaled past f16's largest value (|x| up to ~4e5 > 65504, where an
+    unscaled split gives hi = inf and a NaN row), one at ~1e-5 and one at ~1e-12 (below
+    f16's normal range, where hi, lo and lo/16 lose bits), and a row of zeros.  Each
+    row is checked on its own against the f32 oracle, to the 3e-5 of the N(0,1) case."""
+    import torch
+
+    k, n, m = 896, 1000, 4
+    row_scale = np.array([1e5, 1e-5, 1e-12, 0.0], np.float32)
+    mats = [make_q4(n, k, m, x_dtype=np.float32, salt=77 + i) for i in range(3)]
+    x = np.ascontiguousarray(mats[0][3] * row_scale[:, None], np.float32)
+    assert np.max(np.abs(x[0])) > 65504.0
+    refs = [oracle.qgemv_q4_affine(wq, s, b, x, k) for wq, s, b, _ in mats]
+    if entry == "gemv":
+        wq, s, b, _ = mats[0]
+        outs, want = [_run_q4(ops, wq, s, b, x)], refs[:1]
+    elif entry == "gate_up_silu":
+        (wg, sg, bg, _), (wu, su, bu, _) = mats[0], mats[1]
+        h = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        ops.encode_gate_up_silu_q4_affine(_t(wg), _t(sg), _t(bg), _t(wu), _t(su), _t(bu), _t(x), h)
+        torch.cuda.synchronize()
+        outs, want = [h.cpu().numpy()], [oracle.silu_mul_(np.ascontiguousarray(refs[0]), refs[1])]
+    else:
+        ys = [torch.empty((m, n), dtype=torch.float32, device="cuda") for _ in range(3)]
+        args = []
+        for wq, s, b, _ in mats:
+            args += [_t(wq), _t(s), _t(b)]
+        ops.encode_qkv_q4_affine(*args, _t(x), *ys)
+        torch.cuda.synchronize()
+        outs, want = [y.cpu().numpy() for y in ys], refs
+    for y, ref in zip(outs, want):
+        assert np.all(np.isfinite(y))
+        for r in range(m):
+            assert rel_err(y[r], ref[r]) <= 3e-5, (entry, r, rel_err(y[r], ref[r]))
+        assert not np.any(y[3])  # x = 0: exactly zero
+
+
 # ------------------------------------------------------------------- i4 sym ----
 
 def test_i4_sym_logits(ops):
@@ -796,3 +835,94 @@ def test_gate_up_silu_q4(ops, k, n, m, sb, group, xdt):
     g = np.ascontiguousarray(oracle.qgemv_q4_affine(wg, sg, bg, x, k, gs=group), np.float32)
     ref = oracle.silu_mul_(g, oracle.qgemv_q4_affine(wu, su, bu, x, k, gs=group))
     assert rel_err(h.cpu().numpy(), ref) <= TOL_F32
+
+
+# ------------------------------------------------------------ GELU * up ----
+# Gemma's MLP activation (gemma.rs:844-846 over gelu_tanh_f32, gemma.rs:1689-1693; Metal
+# gelu_tanh_mul_f32_inplace, metal.rs:245-257) at the Gemma-3-1B MLP shape 1152 -> 6912.
+
+def test_gelu_tanh_mul_elementwise(ops):
+    """cellm_hip_gelu_tanh_mul_f32 against the oracle: the device tanhf and glibc's differ by an
+    ulp or two, so the bar is normwise 1e-6 (1 + tanh cancels for large negative g, where both
+    results are ~1e-7 in absolute terms)."""
+    import torch
+
+    n = 6912 * 4
+    g = np.concatenate([np.linspace(-12.0, 12.0, 4001), oracle.gen_normal((n - 4001,), seed(3, 12), 0.0, 3.0)])
+    g = g.astype(np.float32)
+    u = oracle.gen_normal((n,), seed(3, 13), 0.0, 1.0)
+    gd = _t(g.copy())
+    ops.encode_gelu_tanh_mul(gd, _t(u))
+    torch.cuda.synchronize()
+    ref = oracle.gelu_tanh_mul_(g.copy(), u)
+    assert rel_err(gd.cpu().numpy(), ref) <= 1e-6
+    # not the SiLU: the two activations differ at this size
+    assert rel_err(oracle.silu_mul_(g.copy(), u), ref) > 1e-2
+
+
+@pytest.mark.parametrize("m,xdt", [(1, np.float16), (4, np.float16), (2, np.float32), (8, np.float16)])
+def test_gate_up_gelu_i8(ops, m, xdt):
+    """int8 gate/up with the tanh GELU epilogue (cellm_hip_qgemv_i8_gate_up_gelu): one launch for
+    m <= 4, the two GEMVs and the elementwise kernel at m = 8; against the oracle's two
+    matmul_i8_f32 rows and gelu_tanh_mul."""
+    import torch
+
+    k, n = 1152, 6912
+    wg, sg, x = make_i8(n, k, m, cfg=3, scale_dtype=np.float16, x_dtype=xdt, salt=141)
+    wu, su, _ = make_i8(n, k, m, cfg=3, scale_dtype=np.float16, salt=142)
+    h = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    ops.encode_gate_up_gelu_i8(_t(wg), _t(sg), _t(wu), _t(su), _t(x), h)
+    torch.cuda.synchronize()
+    g = np.ascontiguousarray(oracle.qgemv_i8(wg, sg, x), np.float32)
+    u = oracle.qgemv_i8(wu, su, x)
+    ref = oracle.gelu_tanh_mul_(g.copy(), u)
+    got = h.cpu().numpy()
+    assert rel_err(got, ref) <= TOL_F32
+    # the GELU, not the SiLU: where |g| < 2 the two activations differ by far more than the error
+    silu = oracle.silu_mul_(g.copy(), u)
+    near = np.abs(g) < 2.0
+    assert near.sum() > 10
+    assert np.max(np.abs(got - silu)[near]) > 100 * np.max(np.abs(got - ref)[near])
+
+
+@pytest.mark.parametrize("m,sb,xdt", [(1, np.float16, np.float16), (4, np.float32, np.float16),
+                                      (2, np.float16, np.float32), (5, np.float16, np.float16)])
+def test_gate_up_gelu_q4(ops, m, sb, xdt):
+    """MLX q4 gate/up with the tanh GELU epilogue (cellm_hip_qgemv_q4_affine_gate_up_gelu), Gemma
+    MLP halves 1152 -> 6912: one launch for m <= 4 (f16 or f32 x), two GEMVs and the elementwise
+    kernel at m = 5."""
+    import torch
+
+    k, n = 1152, 6912
+    wg, sg, bg, x = make_q4(n, k, m, sb_dtype=sb, x_dtype=xdt, salt=151 + m)
+    wu, su, bu, _ = make_q4(n, k, m, sb_dtype=sb, salt=152 + m)
+    h = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    ops.encode_gate_up_gelu_q4_affine(_t(wg), _sb_tensor(sg), _sb_tensor(bg), _t(wu), _sb_tensor(su),
+                                      _sb_tensor(bu), _t(x), h)
+    torch.cuda.synchronize()
+    g = np.ascontiguousarray(oracle.qgemv_q4_affine(wg, sg, bg, x, k), np.float32)
+    ref = oracle.gelu_tanh_mul_(g, oracle.qgemv_q4_affine(wu, su, bu, x, k))
+    assert rel_err(h.cpu().numpy(), ref) <= TOL_F32
+
+
+@pytest.mark.parametrize("m", [1, 4])
+def test_gate_up_gelu_i4(ops, m):
+    """Symmetric i4 gate/up (gs = in_dim, gemma.rs:1446-1471) with the tanh GELU
+    (cellm_hip_qgemv_i4_gate_up_gelu), f32 x, 1152 -> 6912, against the oracle's two
+    matmul_i4_f32 rows and gelu_tanh_mul."""
+    import torch
+
+    k, n, gs = 1152, 6912, 1152
+    wg = oracle.gen_i8((n, k // 2), seed(6, 20, m)).view(np.uint8)
+    wu = oracle.gen_i8((n, k // 2), seed(6, 21, m)).view(np.uint8)
+    sg = oracle.gen_uniform((n,), seed(6, 22, m), 1e-3, 2e-2).astype(np.float16)
+    su = oracle.gen_uniform((n,), seed(6, 23, m), 1e-3, 2e-2).astype(np.float16)
+    x = oracle.gen_normal((m, k), seed(6, 24, m), 0.0, 1.0)
+    h = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    ops.encode_gate_up_gelu_i4_sym(_t(wg), _t(sg.view(np.int16)), _t(wu), _t(su.view(np.int16)), gs, _t(x), h, k)
+    torch.cuda.synchronize()
+    got = h.cpu().numpy()
+    for r in range(m):
+        g = np.ascontiguousarray(oracle.matmul_i4_f32(wg, sg.view(np.uint16), n, k, gs, x[r]), np.float32)
+        ref = oracle.gelu_tanh_mul_(g, oracle.matmul_i4_f32(wu, su.view(np.uint16), n, k, gs, x[r]))
+        assert rel_err(got[r], ref) <= TOL_F32

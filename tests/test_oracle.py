@@ -386,6 +386,56 @@ def test_rope_identity_at_zero_and_rotation():
     assert np.allclose(z, [np.cos(1.0), np.sin(1.0)], atol=1e-6)
 
 
+def test_rope_interleaved_identity_rotation_and_permutation():
+    """rope_interleaved_inplace_f32 (cpu_kernels.rs:279-292): identity at pos 0, each (2i, 2i+1)
+    pair keeps its norm, a 2-element head at pos 1 turns by 1 rad, and the interleaved form equals
+    the rotate-half form on the permuted head (x[2i] -> i, x[2i+1] -> half + i) bit for bit, so
+    the two layouts share every angle and product."""
+    rng = np.random.default_rng(14)
+    nh, hd = 4, 64
+    x = rng.standard_normal(nh * hd).astype(np.float32)
+    assert np.array_equal(oracle.rope_interleaved_(x.copy(), nh, hd, 0, 10000.0), x)
+    y = oracle.rope_interleaved_(x.copy(), nh, hd, 37, 10000.0)
+    assert np.allclose(np.hypot(x[0::2], x[1::2]), np.hypot(y[0::2], y[1::2]), rtol=1e-5)
+    z = oracle.rope_interleaved_(np.array([1.0, 0.0], np.float32), 1, 2, 1, 10000.0)
+    assert np.allclose(z, [np.cos(1.0), np.sin(1.0)], atol=1e-6)
+    perm = np.concatenate([np.arange(0, hd, 2), np.arange(1, hd, 2)])  # half-layout position j <- x[perm[j]]
+    for pos in (1, 37, 511):
+        xh = np.ascontiguousarray(x.reshape(nh, hd)[:, perm].reshape(-1))
+        yh = oracle.rope_half_(xh, nh, hd, pos, 10000.0).reshape(nh, hd)
+        back = np.empty((nh, hd), np.float32)
+        back[:, perm] = yh
+        yi = oracle.rope_interleaved_(x.copy(), nh, hd, pos, 10000.0)
+        assert np.array_equal(back.reshape(-1), yi)
+    # and the layouts differ: rotate-half on the unpermuted head is another result
+    assert not np.array_equal(oracle.rope_half_(x.copy(), nh, hd, 37, 10000.0), y)
+
+
+def test_gelu_tanh_closed_forms_and_erf_distance():
+    """gelu_tanh_f32 * up (gemma.rs:844-846, 1689-1693): gelu(0) = 0; the odd part
+    gelu(x) - gelu(-x) = x (the 0.5 and the 1 + tanh); gelu(x) -> x and -> 0 far out; multiplying
+    by up = 2 doubles it exactly; against the float64 formula with k = sqrt(2/pi) computed here,
+    within f32 rounding; and within 5e-4 of the erf GELU x * Phi(x) over [-8, 8], the tanh form's
+    known distance, which a wrong k (0.79: 2.8e-3), c (0.05: 3.0e-3) or a missing cubic (3.4e-2)
+    exceeds."""
+    import math
+
+    x = np.linspace(-8.0, 8.0, 40001).astype(np.float32)
+    one = np.ones_like(x)
+    g = oracle.gelu_tanh_mul_(x.copy(), one)
+    assert g[len(x) // 2] == 0.0 and x[len(x) // 2] == 0.0
+    gn = oracle.gelu_tanh_mul_((-x).copy(), one)
+    assert np.max(np.abs((g - gn) - x)) <= 1e-6 * 8
+    big = oracle.gelu_tanh_mul_(np.array([12.0, -12.0], np.float32), np.ones(2, np.float32))
+    assert big[0] == np.float32(12.0) and abs(big[1]) <= 1e-30
+    assert np.array_equal(oracle.gelu_tanh_mul_(x.copy(), 2 * one), 2 * g)
+    xd = x.astype(np.float64)
+    t = 0.5 * xd * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (xd + 0.044715 * xd ** 3)))
+    assert np.max(np.abs(g - t)) <= 1e-6
+    erf_gelu = np.array([0.5 * v * (1.0 + math.erf(v / math.sqrt(2.0))) for v in xd])
+    assert np.max(np.abs(g - erf_gelu)) <= 5e-4
+
+
 def test_softmax_attention_argmax():
     s = oracle.softmax_(np.full(8, 2.5, np.float32))
     assert np.allclose(s, 1 / 8)
