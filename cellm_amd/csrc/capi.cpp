@@ -101,6 +101,7 @@ struct cellm_hip_ctx {
     std::unordered_map<hipStream_t, DeviceBuffer> workspaces;  // split-K partials, one per stream
     std::unordered_map<hipStream_t, DeviceBuffer> aux;         // unfused gate/up: the up rows, one per stream
     std::unordered_map<hipStream_t, DeviceBuffer> attn;        // split-sequence attention partials, one per stream
+    std::unordered_map<hipStream_t, DeviceBuffer> argmax;      // argmax row counters + chunk partials, one per stream
     float* attn_static = nullptr;  // this device's static attention scratch (cellm_hip_attention_gqa_f16kv_noalloc)
     std::atomic<int> rope_interleaved{0};  // RoPE pairs of the fused decode ops (cellm_hip_set_rope_interleaved)
 };
@@ -533,7 +534,7 @@ void cellm_hip_destroy(cellm_hip_ctx_t* ctx)
     if (!ctx) return;
     DeviceGuard g(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
-    for (auto* map : {&ctx->workspaces, &ctx->aux, &ctx->attn})
+    for (auto* map : {&ctx->workspaces, &ctx->aux, &ctx->attn, &ctx->argmax})
         for (auto& kv : *map) {
             (void)hipStreamSynchronize(kv.first);
             if (kv.second.ptr) (void)hipFree(kv.second.ptr);
@@ -1404,8 +1405,17 @@ int32_t cellm_hip_argmax_f32(cellm_hip_ctx_t* ctx, const float* logits, int64_t 
     if (rows == 0) return CELLM_HIP_OK;
     if (n == 0) return set_error(CELLM_HIP_ERR_INVALID_ARG, "empty logits");
     if (!logits || !out_index || !out_value) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null pointer");
+    if (rows > 65535) return set_error(CELLM_HIP_ERR_INVALID_ARG, "rows=%lld > 65535", (long long)rows);
     DeviceGuard g(ctx->device);
-    HIP_TRY(launch_argmax(logits, (int)rows, (int)n, out_index, out_value, pick_stream(ctx, stream)), "argmax launch");
+    const std::lock_guard<std::recursive_mutex> lk(ctx->mu);  // held until the scratch user is enqueued
+    hipStream_t st = pick_stream(ctx, stream);
+    // rows longer than one chunk: per-stream scratch, its row counters cleared when it is allocated
+    // and returned to zero by every launch
+    float* scratch = nullptr;
+    if (int32_t rc = get_stream_buffer(ctx, ctx->argmax, st, argmax_scratch_bytes((int)rows, (int)n), &scratch,
+                                       argmax_counter_bytes((int)rows)))
+        return rc;
+    HIP_TRY(launch_argmax(logits, (int)rows, (int)n, out_index, out_value, scratch, st), "argmax launch");
     return CELLM_HIP_OK;
     CELLM_API_END(report_exception)
 }

@@ -1012,65 +1012,91 @@ __device__ __forceinline__ void argmax_take(float v, int i, float& best, int& bi
     }
 }
 
-// One block per row.  Each thread visits its elements in increasing index
-// order; with 16-byte rows it first loads up to kArgmaxUnroll float4 at once
-// (one memory latency for a 64K-entry row), addresses clamped in range.
-constexpr int kArgmaxThreads = 1024;
+// Chunk blocks per row: block (c, r) takes elements [c * kArgmaxChunk, (c + 1) * kArgmaxChunk) of
+// row r, every thread loading all of its kArgmaxUnroll float4 before it compares any (one memory
+// latency per block), and reduces them to the chunk's first maximum.  With one chunk the block
+// writes the row's result; otherwise it publishes (value, index) with agent-coherent stores,
+// performed before it counts itself on the row's counter, and the row's last block combines the
+// chunks in chunk order and returns the counter to zero.  Each thread visits its elements in
+// increasing index order and every reduction keeps the lower index among equal values, so the
+// result is the first maximum (topk_from_logits(..)[0], llama.rs:1049-1078).
+constexpr int kArgmaxThreads = 256;
 constexpr int kArgmaxUnroll = 16;
+constexpr int kArgmaxChunk = kArgmaxThreads * 4 * kArgmaxUnroll;  // 16384 elements, 64 KB
+
+__device__ __forceinline__ void argmax_pick(float ov, int oi, float& best, int& bi)
+{
+    if (ov > best || (ov == best && oi < bi)) {
+        best = ov;
+        bi = oi;
+    }
+}
 
 __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __restrict__ logits, int n,
-                                                                int32_t* __restrict__ idx, float* __restrict__ val)
+                                                                int32_t* __restrict__ idx, float* __restrict__ val,
+                                                                uint32_t* __restrict__ cnt, float2* __restrict__ part)
 {
     __shared__ float sv[kArgmaxThreads / 64];
     __shared__ int si[kArgmaxThreads / 64];
-    const int r = blockIdx.x, t = threadIdx.x;
+    __shared__ int last;
+    const int c = blockIdx.x, r = blockIdx.y, t = threadIdx.x, nch = gridDim.x;
     const float* z = logits + (size_t)r * n;
+    const int beg = c * kArgmaxChunk, end = min(n, beg + kArgmaxChunk);
     float best = -INFINITY;
     int bi = 0x7fffffff;
-    if ((n & 3) == 0 && (reinterpret_cast<uintptr_t>(z) & 15) == 0) {
+    if ((n & 3) == 0 && (reinterpret_cast<uintptr_t>(logits) & 15) == 0) {
         const float4* z4 = reinterpret_cast<const float4*>(z);
-        const int n4 = n >> 2;
-        for (int j0 = t; j0 < n4; j0 += kArgmaxUnroll * kArgmaxThreads) {
-            float4 a[kArgmaxUnroll];
+        const int j0 = beg >> 2, j1 = end >> 2;
+        float4 a[kArgmaxUnroll];
 #pragma unroll
-            for (int u = 0; u < kArgmaxUnroll; ++u) a[u] = z4[min(j0 + u * kArgmaxThreads, n4 - 1)];
+        for (int u = 0; u < kArgmaxUnroll; ++u) a[u] = z4[min(j0 + u * kArgmaxThreads + t, j1 - 1)];
 #pragma unroll
-            for (int u = 0; u < kArgmaxUnroll; ++u) {
-                const int j = j0 + u * kArgmaxThreads;
-                if (j < n4) {
-                    argmax_take(a[u].x, 4 * j, best, bi);
-                    argmax_take(a[u].y, 4 * j + 1, best, bi);
-                    argmax_take(a[u].z, 4 * j + 2, best, bi);
-                    argmax_take(a[u].w, 4 * j + 3, best, bi);
-                }
+        for (int u = 0; u < kArgmaxUnroll; ++u) {
+            const int j = j0 + u * kArgmaxThreads + t;
+            if (j < j1) {
+                argmax_take(a[u].x, 4 * j, best, bi);
+                argmax_take(a[u].y, 4 * j + 1, best, bi);
+                argmax_take(a[u].z, 4 * j + 2, best, bi);
+                argmax_take(a[u].w, 4 * j + 3, best, bi);
             }
         }
     } else {
-        for (int i = t; i < n; i += kArgmaxThreads) argmax_take(z[i], i, best, bi);
+        for (int i = beg + t; i < end; i += kArgmaxThreads) argmax_take(z[i], i, best, bi);
     }
-    // (value, index) max with the lowest index among equal values: the first maximum
-    for (int off = 32; off > 0; off >>= 1) {
-        const float ov = __shfl_xor(best, off);
-        const int oi = __shfl_xor(bi, off);
-        if (ov > best || (ov == best && oi < bi)) {
-            best = ov;
-            bi = oi;
-        }
-    }
+    for (int off = 32; off > 0; off >>= 1) argmax_pick(__shfl_xor(best, off), __shfl_xor(bi, off), best, bi);
     if ((t & 63) == 0) {
         sv[t >> 6] = best;
         si[t >> 6] = bi;
     }
     __syncthreads();
     if (t == 0) {
-        for (int w = 1; w < kArgmaxThreads / 64; ++w)
-            if (sv[w] > best || (sv[w] == best && si[w] < bi)) {
-                best = sv[w];
-                bi = si[w];
-            }
-        idx[r] = bi == 0x7fffffff ? 0 : bi;
-        val[r] = best;
+        for (int w = 1; w < kArgmaxThreads / 64; ++w) argmax_pick(sv[w], si[w], best, bi);
+        if (nch == 1) {
+            idx[r] = bi == 0x7fffffff ? 0 : bi;
+            val[r] = best;
+        } else {
+            float2* p = part + (size_t)r * nch + c;
+            __hip_atomic_store(&p->x, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&p->y, __builtin_bit_cast(float, bi), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // performed before the count
+            last = __hip_atomic_fetch_add(cnt + r, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                   (uint32_t)(nch - 1);
+        }
     }
+    if (nch == 1) return;
+    __syncthreads();
+    if (!last || t != 0) return;
+    __hip_atomic_store(cnt + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    best = -INFINITY;
+    bi = 0x7fffffff;
+    for (int k = 0; k < nch; ++k) {
+        const float2* p = part + (size_t)r * nch + k;
+        argmax_pick(__hip_atomic_load(&p->x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                    __builtin_bit_cast(int, __hip_atomic_load(&p->y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)),
+                    best, bi);
+    }
+    idx[r] = bi == 0x7fffffff ? 0 : bi;
+    val[r] = best;
 }
 
 }  // namespace
@@ -1378,9 +1404,25 @@ hipError_t launch_decode_gate_up(const float* x_prev, const float* y, float* x_o
     return launch_decode<false>(rows, H, a, N, st);
 }
 
-hipError_t launch_argmax(const float* logits, int rows, int n, int32_t* idx, float* val, hipStream_t st)
+int argmax_chunks(int n) { return std::max(1, (n + kArgmaxChunk - 1) / kArgmaxChunk); }
+
+size_t argmax_counter_bytes(int rows) { return (((size_t)rows * sizeof(uint32_t)) + 255) & ~(size_t)255; }
+
+size_t argmax_scratch_bytes(int rows, int n)
 {
-    hipLaunchKernelGGL(argmax_kernel, dim3(rows), dim3(kArgmaxThreads), 0, st, logits, n, idx, val);
+    const int nch = argmax_chunks(n);
+    return nch == 1 ? 0 : argmax_counter_bytes(rows) + (size_t)rows * nch * sizeof(float2);
+}
+
+hipError_t launch_argmax(const float* logits, int rows, int n, int32_t* idx, float* val, void* scratch, hipStream_t st)
+{
+    const int nch = argmax_chunks(n);
+    if (nch > 1 && !scratch) return hipErrorInvalidValue;
+    uint32_t* cnt = reinterpret_cast<uint32_t*>(scratch);
+    float2* part = nch > 1 ? reinterpret_cast<float2*>(reinterpret_cast<unsigned char*>(scratch) +
+                                                        argmax_counter_bytes(rows))
+                           : nullptr;
+    hipLaunchKernelGGL(argmax_kernel, dim3(nch, rows), dim3(kArgmaxThreads), 0, st, logits, n, idx, val, cnt, part);
     return hipGetLastError();
 }
 

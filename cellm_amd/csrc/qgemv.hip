@@ -80,16 +80,30 @@ __device__ __forceinline__ void stage_word_q4(u4_t raw, int idx, bool valid, uin
     if (valid && (idx & 3) == 0) cx[idx >> 2] = make_float2(1024.0f * corr, xs);
 }
 
-// f32 activations (the LFM runner's and the .cellm u32 runner's x) as two f16 parts,
-// x' = hi + lo with hi = RNE_f16(x') and lo = RNE_f16(x' - hi), where x' = x * 2^sh is the
-// row scaled by x32_row_shifts: a nibble value times either part is exact in f32, so the
-// dot over both parts keeps x to about 22 bits where one f16 rounding would keep 11.
-// Eight f32 values -> the hi pairs at xq, the lo pairs at xq_lo (the layout of
-// stage_word_q4), cx = (1024 * the pairs' sum over both parts, sum of the scaled x) per chunk.
-__device__ __forceinline__ void stage_word_q4_x32(f4_t a, f4_t b, int sh, int idx, bool valid, uint32_t* xq,
-                                                  uint32_t* xq_lo, float2* cx)
+// f32 activations (the LFM runner's and the .cellm u32 runner's x) as two f16 parts.  Each
+// 32-element chunk (4 words, in 4 adjacent lanes) is scaled by a power of two, x' = x * 2^sh, sh
+// chosen from the chunk's largest |x| so that it lies in [2^13, 2^14): hi = RNE_f16(x') never
+// overflows (|x| > 65504 alone would give hi = inf, lo = -inf and a NaN row sum) and small values
+// stay clear of f16 subnormals, where hi, lo and lo / 16 lose bits.  Then x' = hi + lo with
+// lo = RNE_f16(x' - hi): a nibble value times either part is exact in f32, so the dot over both
+// parts keeps x to about 22 bits where one f16 rounding would keep 11.  Every product and partial
+// sum of the chunk carries the exact factor 2^sh, and p2 = 2^-sh takes it out of the chunk's
+// contribution (compute_pass_q4): bit for bit the unscaled sum wherever that stays in f16 normal
+// range.  A chunk of zeros or with an infinite value keeps sh = 0 (fmaxf ignores NaN, which then
+// propagates through the dot as it would unscaled).
+// Eight f32 values -> the hi pairs at xq, the lo pairs at xq_lo (the layout of stage_word_q4),
+// cx = (1024 * the pairs' sum over both parts, sum of the scaled x) and p2 per chunk.
+__device__ __forceinline__ void stage_word_q4_x32(f4_t a, f4_t b, int idx, bool valid, uint32_t* xq, uint32_t* xq_lo,
+                                                  float2* cx, float* p2)
 {
     float xv[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    float mx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(xv[i]));
+    mx = group_max<4>(mx);
+    int e = 0;
+    (void)__builtin_frexpf(mx, &e);
+    const int sh = (mx > 0.0f && mx <= 3.402823466e38f) ? min(14 - e, 126) : 0;
 #pragma unroll
     for (int i = 0; i < 8; ++i) xv[i] = __builtin_ldexpf(xv[i], sh);
     h8_t hi, lo;
@@ -101,11 +115,11 @@ __device__ __forceinline__ void stage_word_q4_x32(f4_t a, f4_t b, int sh, int id
     const _Float16 inv16 = (_Float16)0.0625f;
     float corr = 0.0f;
     auto pack = [&](const h8_t& v, uint32_t* dst) {
-        const h2_t p0 = {v[0], v[4]}, p1 = {v[1] * inv16, v[5] * inv16};
-        const h2_t p2 = {v[2], v[6]}, p3 = {v[3] * inv16, v[7] * inv16};
-        corr += ((float)p0[0] + (float)p0[1]) + ((float)p1[0] + (float)p1[1]) + ((float)p2[0] + (float)p2[1]) +
-                ((float)p3[0] + (float)p3[1]);
-        if (valid) *reinterpret_cast<u4_t*>(dst + (size_t)idx * 4) = u4_t{as_u32(p0), as_u32(p1), as_u32(p2), as_u32(p3)};
+        const h2_t q0 = {v[0], v[4]}, q1 = {v[1] * inv16, v[5] * inv16};
+        const h2_t q2 = {v[2], v[6]}, q3 = {v[3] * inv16, v[7] * inv16};
+        corr += ((float)q0[0] + (float)q0[1]) + ((float)q1[0] + (float)q1[1]) + ((float)q2[0] + (float)q2[1]) +
+                ((float)q3[0] + (float)q3[1]);
+        if (valid) *reinterpret_cast<u4_t*>(dst + (size_t)idx * 4) = u4_t{as_u32(q0), as_u32(q1), as_u32(q2), as_u32(q3)};
     };
     pack(hi, xq);
     pack(lo, xq_lo);
@@ -114,57 +128,18 @@ __device__ __forceinline__ void stage_word_q4_x32(f4_t a, f4_t b, int sh, int id
     for (int i = 0; i < 8; ++i) xs += xv[i];
     corr = quad_sum(corr);
     xs = quad_sum(xs);
-    if (valid && (idx & 3) == 0) cx[idx >> 2] = make_float2(1024.0f * corr, xs);
+    if (valid && (idx & 3) == 0) {
+        cx[idx >> 2] = make_float2(1024.0f * corr, xs);
+        p2[idx >> 2] = __builtin_ldexpf(1.0f, -sh);
+    }
 }
 
 // All MT * K / 8 words of f32 x -> LDS through stage_word_q4_x32, two 16-byte loads per word, in
 // rounds of XW words per thread whose loads all issue before the round's first store (clamped,
 // branch-free: padding rows and words past `total` read valid data whose results are never stored).
-// Per-row exponent shifts for f32 x.  Row m is staged as x * 2^sh[m], sh[m] chosen from the
-// row's largest |x| so that the largest staged value lies in [2^13, 2^14): hi never overflows f16
-// (|x| > 65504 alone would give hi = inf, lo = -inf and a NaN row sum), and a row of small values
-// stays clear of f16 subnormals, where hi and lo (and lo / 16 in the pair layout) lose bits.
-// Every product and partial sum of the row's dot then carries the exact factor 2^sh[m], and the
-// kernels return ldexp(acc, -sh[m]): bit for bit the unscaled result wherever that one kept its
-// values in f16 normal range.  A row of zeros or with an infinite value keeps sh = 0 (NaN is
-// ignored by fmaxf and propagates through the dot as it would unscaled).
-template <int MT>
-__device__ __forceinline__ void x32_row_shifts(const float* __restrict__ x, int M, int K, int (&sh)[MT])
-{
-    __shared__ float red[kBlock / 64][MT];
-    const int q = K >> 2;  // 16-byte words per row (K % 32 == 0, x 16-byte aligned)
-    float mx[MT];
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-        mx[m] = 0.0f;
-        if (m < M) {
-            const f4_t* row = reinterpret_cast<const f4_t*>(x + (size_t)m * K);
-            for (int i = threadIdx.x; i < q; i += kBlock) {
-                const f4_t v = row[i];
-                mx[m] = fmaxf(mx[m], fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
-            }
-        }
-        mx[m] = group_max<64>(mx[m]);
-    }
-    if ((threadIdx.x & 63) == 0) {
-#pragma unroll
-        for (int m = 0; m < MT; ++m) red[threadIdx.x >> 6][m] = mx[m];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-        float v = red[0][m];
-#pragma unroll
-        for (int w = 1; w < kBlock / 64; ++w) v = fmaxf(v, red[w][m]);
-        int e = 0;
-        (void)__builtin_frexpf(v, &e);
-        sh[m] = (v > 0.0f && v <= 3.402823466e38f) ? 14 - e : 0;
-    }
-}
-
-template <int XW, int MT>
+template <int XW>
 __device__ __forceinline__ void stage_x_q4_x32(const float* __restrict__ x, int M, int K, int total, uint32_t* xq,
-                                               uint32_t* xq_lo, float2* cx, const int (&sh)[MT])
+                                               uint32_t* xq_lo, float2* cx, float* p2)
 {
     const int words = K >> 3;
     for (int base = 0; base < total; base += XW * kBlock) {
@@ -180,11 +155,7 @@ __device__ __forceinline__ void stage_x_q4_x32(const float* __restrict__ x, int 
 #pragma unroll
         for (int j = 0; j < XW; ++j) {
             const int idx = base + j * kBlock + (int)threadIdx.x;
-            const int m = min(idx / words, MT - 1);
-            int shm = sh[0];
-#pragma unroll
-            for (int r = 1; r < MT; ++r) shm = m == r ? sh[r] : shm;  // constant indices: no scratch
-            stage_word_q4_x32(ra[j], rb[j], shm, idx, idx < total, xq, xq_lo, cx);
+            stage_word_q4_x32(ra[j], rb[j], idx, idx < total, xq, xq_lo, cx, p2);
         }
     }
 }
@@ -253,7 +224,7 @@ template <int LPR, int R, int MT, int SBT, int U = kUnroll, bool XS = false>
 __device__ __forceinline__ void compute_pass_q4(int c0, int CPR, const uint32_t* xq, const float2* cx,
                                                 const u4_t (&wv)[U][R], const uint32_t (&sr)[U][R],
                                                 const uint32_t (&br)[U][R], float (&acc)[R][MT],
-                                                const uint32_t* xq_lo = nullptr)
+                                                const uint32_t* xq_lo = nullptr, const float* p2 = nullptr)
 {
     const uint32_t m0f = 0x000F000Fu, m1f = 0x00F000F0u, magic = 0x64006400u;
 #pragma unroll
@@ -303,7 +274,11 @@ __device__ __forceinline__ void compute_pass_q4(int c0, int CPR, const uint32_t*
                             d = dot2(and_or(h, m1f, magic), xl[3], d);
                         }
                     }
-                    acc[r][m] += raw_to_f32<SBT>(sr[u][r]) * d + raw_to_f32<SBT>(br[u][r]) * cc.y;
+                    if constexpr (XS)  // the chunk's x carried 2^sh: p2 = 2^-sh takes it out exactly
+                        acc[r][m] += (raw_to_f32<SBT>(sr[u][r]) * d + raw_to_f32<SBT>(br[u][r]) * cc.y) *
+                                     p2[(size_t)m * CPR + c];
+                    else
+                        acc[r][m] += raw_to_f32<SBT>(sr[u][r]) * d + raw_to_f32<SBT>(br[u][r]) * cc.y;
                 }
             }
         }
@@ -324,6 +299,7 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_f16x_kernel(
     uint32_t* xq = lds;
     uint32_t* xq_lo = XS ? lds + (size_t)MT * CPR * 16 : nullptr;
     float2* cx = reinterpret_cast<float2*>(lds + (size_t)(XS ? 2 : 1) * MT * CPR * 16);
+    float* p2 = XS ? reinterpret_cast<float*>(cx + (size_t)MT * CPR) : nullptr;  // f32 x: 2^-sh per chunk
 
     const int team = threadIdx.x / LPR;
     const int lane = threadIdx.x % LPR;
@@ -332,14 +308,12 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_f16x_kernel(
     const int total = MT * (K >> 3);
 
     constexpr int XW = MT == 1 ? 4 : 8;
-    int xsh[MT] = {};  // f32 x: per-row exponent shift (x32_row_shifts); 0 for f16 x
     u4_t wa[kUnroll][R];
     uint32_t sa[kUnroll][R], ba[kUnroll][R];
     if constexpr (XS) {
         // the weights first: x is a cache hit after the first blocks, the weights are not
         load_pass_q4<LPR, R, SBT>(wq, S, B, row0, 1, lane, N, CPR, gpr, gshift, wa, sa, ba);
-        x32_row_shifts<MT>(reinterpret_cast<const float*>(xv), M, K, xsh);
-        stage_x_q4_x32<XW / 2>(reinterpret_cast<const float*>(xv), M, K, total, xq, xq_lo, cx, xsh);
+        stage_x_q4_x32<XW / 2>(reinterpret_cast<const float*>(xv), M, K, total, xq, xq_lo, cx, p2);
     } else {
         const _Float16* x = reinterpret_cast<const _Float16*>(xv);
         u4_t xr[XW];
@@ -357,18 +331,18 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_f16x_kernel(
         for (int m = 0; m < MT; ++m) acc[r][m] = 0.0f;
 
     if constexpr (!MP) {
-        compute_pass_q4<LPR, R, MT, SBT, kUnroll, XS>(lane, CPR, xq, cx, wa, sa, ba, acc, xq_lo);
+        compute_pass_q4<LPR, R, MT, SBT, kUnroll, XS>(lane, CPR, xq, cx, wa, sa, ba, acc, xq_lo, p2);
     } else {
         constexpr int P = kUnroll * LPR;
         u4_t wb[kUnroll][R];
         uint32_t sb[kUnroll][R], bb[kUnroll][R];
         for (int c0 = lane; c0 < CPR + lane; c0 += 2 * P) {
             if (c0 - lane + P < CPR) load_pass_q4<LPR, R, SBT>(wq, S, B, row0, 1, c0 + P, N, CPR, gpr, gshift, wb, sb, bb);
-            compute_pass_q4<LPR, R, MT, SBT, kUnroll, XS>(c0, CPR, xq, cx, wa, sa, ba, acc, xq_lo);
+            compute_pass_q4<LPR, R, MT, SBT, kUnroll, XS>(c0, CPR, xq, cx, wa, sa, ba, acc, xq_lo, p2);
             if (c0 - lane + P >= CPR) break;
             if (c0 - lane + 2 * P < CPR)
                 load_pass_q4<LPR, R, SBT>(wq, S, B, row0, 1, c0 + 2 * P, N, CPR, gpr, gshift, wa, sa, ba);
-            compute_pass_q4<LPR, R, MT, SBT, kUnroll, XS>(c0 + P, CPR, xq, cx, wb, sb, bb, acc, xq_lo);
+            compute_pass_q4<LPR, R, MT, SBT, kUnroll, XS>(c0 + P, CPR, xq, cx, wb, sb, bb, acc, xq_lo, p2);
         }
     }
 
@@ -377,7 +351,6 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_f16x_kernel(
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
             acc[r][m] = group_sum<LPR>(acc[r][m]);
-            if constexpr (XS) acc[r][m] = __builtin_ldexpf(acc[r][m], -xsh[m]);
         }
 
     if (lane == 0) {
@@ -431,6 +404,7 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_gate_up_silu_kernel(
     uint32_t* xq = lds;
     uint32_t* xq_lo = XS ? lds + (size_t)MT * CPR * 16 : nullptr;
     float2* cx = reinterpret_cast<float2*>(lds + (size_t)(XS ? 2 : 1) * MT * CPR * 16);
+    float* p2 = XS ? reinterpret_cast<float*>(cx + (size_t)MT * CPR) : nullptr;  // f32 x: 2^-sh per chunk
 
     const int team = threadIdx.x / LPR;
     const int lane = threadIdx.x % LPR;
@@ -439,14 +413,12 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_gate_up_silu_kernel(
     const int total = MT * (K >> 3);
 
     constexpr int XW = MT == 1 ? 4 : 8;
-    int xsh[MT] = {};  // f32 x: per-row exponent shift (x32_row_shifts); 0 for f16 x
     u4_t wa[kUnroll][2];
     uint32_t sa[kUnroll][2], ba[kUnroll][2];
     if constexpr (XS) {
         // f32 x as hi + lo f16 parts (stage_word_q4_x32); the weights first
         load_pass_q4_gu<LPR, SBT>(wg, Sg, Bg, wu, Su, Bu, n, lane, N, CPR, gpr, gshift, wa, sa, ba);
-        x32_row_shifts<MT>(reinterpret_cast<const float*>(xv), M, K, xsh);
-        stage_x_q4_x32<XW / 2>(reinterpret_cast<const float*>(xv), M, K, total, xq, xq_lo, cx, xsh);
+        stage_x_q4_x32<XW / 2>(reinterpret_cast<const float*>(xv), M, K, total, xq, xq_lo, cx, p2);
     } else {
         const _Float16* x = reinterpret_cast<const _Float16*>(xv);
         u4_t xr[XW];
@@ -463,7 +435,7 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_gate_up_silu_kernel(
 #pragma unroll
         for (int m = 0; m < MT; ++m) acc[r][m] = 0.0f;
     if constexpr (!MP) {
-        compute_pass_q4<LPR, 2, MT, SBT, kUnroll, XS>(lane, CPR, xq, cx, wa, sa, ba, acc, xq_lo);
+        compute_pass_q4<LPR, 2, MT, SBT, kUnroll, XS>(lane, CPR, xq, cx, wa, sa, ba, acc, xq_lo, p2);
     } else {
         constexpr int P = kUnroll * LPR;
         u4_t wb[kUnroll][2];
@@ -471,11 +443,11 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_gate_up_silu_kernel(
         for (int c0 = lane; c0 < CPR + lane; c0 += 2 * P) {
             if (c0 - lane + P < CPR)
                 load_pass_q4_gu<LPR, SBT>(wg, Sg, Bg, wu, Su, Bu, n, c0 + P, N, CPR, gpr, gshift, wb, sb, bb);
-            compute_pass_q4<LPR, 2, MT, SBT, kUnroll, XS>(c0, CPR, xq, cx, wa, sa, ba, acc, xq_lo);
+            compute_pass_q4<LPR, 2, MT, SBT, kUnroll, XS>(c0, CPR, xq, cx, wa, sa, ba, acc, xq_lo, p2);
             if (c0 - lane + P >= CPR) break;
             if (c0 - lane + 2 * P < CPR)
                 load_pass_q4_gu<LPR, SBT>(wg, Sg, Bg, wu, Su, Bu, n, c0 + 2 * P, N, CPR, gpr, gshift, wa, sa, ba);
-            compute_pass_q4<LPR, 2, MT, SBT, kUnroll, XS>(c0 + P, CPR, xq, cx, wb, sb, bb, acc, xq_lo);
+            compute_pass_q4<LPR, 2, MT, SBT, kUnroll, XS>(c0 + P, CPR, xq, cx, wb, sb, bb, acc, xq_lo, p2);
         }
     }
 #pragma unroll
@@ -483,7 +455,6 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_gate_up_silu_kernel(
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
             acc[r][m] = group_sum<LPR>(acc[r][m]);
-            if constexpr (XS) acc[r][m] = __builtin_ldexpf(acc[r][m], -xsh[m]);
         }
     if (lane == 0) {
 #pragma unroll
@@ -520,6 +491,7 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_segs_kernel(Q4Segs segs, cons
     uint32_t* xq = lds;
     uint32_t* xq_lo = XS ? lds + (size_t)MT * CPR * 16 : nullptr;
     float2* cx = reinterpret_cast<float2*>(lds + (size_t)(XS ? 2 : 1) * MT * CPR * 16);
+    float* p2 = XS ? reinterpret_cast<float*>(cx + (size_t)MT * CPR) : nullptr;  // f32 x: 2^-sh per chunk
     const int team = threadIdx.x / LPR;
     const int lane = threadIdx.x % LPR;
     const int row = blockIdx.x * (kBlock / LPR) + team;
@@ -537,13 +509,11 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_segs_kernel(Q4Segs segs, cons
         }
     }
     constexpr int XW = MT == 1 ? 4 : 8;
-    int xsh[MT] = {};  // f32 x: per-row exponent shift (x32_row_shifts); 0 for f16 x
     u4_t wa[kUnroll][1];
     uint32_t sa[kUnroll][1], ba[kUnroll][1];
     if constexpr (XS) {
         load_pass_q4<LPR, 1, SBT>(sg.w, sg.S, sg.B, v, 1, lane, sg.n, CPR, gpr, gshift, wa, sa, ba);
-        x32_row_shifts<MT>(reinterpret_cast<const float*>(xv), M, K, xsh);
-        stage_x_q4_x32<XW / 2>(reinterpret_cast<const float*>(xv), M, K, total, xq, xq_lo, cx, xsh);
+        stage_x_q4_x32<XW / 2>(reinterpret_cast<const float*>(xv), M, K, total, xq, xq_lo, cx, p2);
     } else {
         const _Float16* x = reinterpret_cast<const _Float16*>(xv);
         u4_t xr[XW];
@@ -558,7 +528,7 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_segs_kernel(Q4Segs segs, cons
 #pragma unroll
     for (int m = 0; m < MT; ++m) acc[0][m] = 0.0f;
     if constexpr (!MP) {
-        compute_pass_q4<LPR, 1, MT, SBT, kUnroll, XS>(lane, CPR, xq, cx, wa, sa, ba, acc, xq_lo);
+        compute_pass_q4<LPR, 1, MT, SBT, kUnroll, XS>(lane, CPR, xq, cx, wa, sa, ba, acc, xq_lo, p2);
     } else {
         constexpr int P = kUnroll * LPR;
         u4_t wb[kUnroll][1];
@@ -566,17 +536,16 @@ __global__ __launch_bounds__(kBlock) void qgemv_q4_segs_kernel(Q4Segs segs, cons
         for (int c0 = lane; c0 < CPR + lane; c0 += 2 * P) {
             if (c0 - lane + P < CPR)
                 load_pass_q4<LPR, 1, SBT>(sg.w, sg.S, sg.B, v, 1, c0 + P, sg.n, CPR, gpr, gshift, wb, sb, bb);
-            compute_pass_q4<LPR, 1, MT, SBT, kUnroll, XS>(c0, CPR, xq, cx, wa, sa, ba, acc, xq_lo);
+            compute_pass_q4<LPR, 1, MT, SBT, kUnroll, XS>(c0, CPR, xq, cx, wa, sa, ba, acc, xq_lo, p2);
             if (c0 - lane + P >= CPR) break;
             if (c0 - lane + 2 * P < CPR)
                 load_pass_q4<LPR, 1, SBT>(sg.w, sg.S, sg.B, v, 1, c0 + 2 * P, sg.n, CPR, gpr, gshift, wa, sa, ba);
-            compute_pass_q4<LPR, 1, MT, SBT, kUnroll, XS>(c0 + P, CPR, xq, cx, wb, sb, bb, acc, xq_lo);
+            compute_pass_q4<LPR, 1, MT, SBT, kUnroll, XS>(c0 + P, CPR, xq, cx, wb, sb, bb, acc, xq_lo, p2);
         }
     }
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
         acc[0][m] = group_sum<LPR>(acc[0][m]);
-        if constexpr (XS) acc[0][m] = __builtin_ldexpf(acc[0][m], -xsh[m]);
     }
     if (lane == 0) {
         const float bv = sg.bias ? sg.bias[v] : 0.0f;
@@ -1648,7 +1617,7 @@ hipError_t launch_q4_f16x_sbt(int sbt, const uint32_t* wq, const void* S, const 
                               int M, int N, int K, int gshift, hipStream_t st)
 {
     const int CPR = K >> 5;
-    const size_t lds = (size_t)(XS ? 2 : 1) * MT * CPR * 16 * 4 + (size_t)MT * CPR * 8;
+    const size_t lds = (size_t)(XS ? 2 : 1) * MT * CPR * 16 * 4 + (size_t)MT * CPR * (XS ? 12 : 8);
     const int rows_per_block = (kBlock / LPR) * R;
     const dim3 grid((N + rows_per_block - 1) / rows_per_block);
     const u4_t* w4 = reinterpret_cast<const u4_t*>(wq);
@@ -1770,7 +1739,7 @@ hipError_t launch_q4_gu_shape(int sbt, const uint32_t* wg, const void* Sg, const
                               int gshift, int act, hipStream_t st)
 {
     const dim3 grid((N + (kBlock / LPR) - 1) / (kBlock / LPR));
-    const size_t lds = (size_t)qgemv_q4_lds_bytes(M, K) + (XS ? (size_t)MT * (K >> 5) * 64 : 0);
+    const size_t lds = (size_t)qgemv_q4_lds_bytes(M, K) + (XS ? (size_t)MT * (K >> 5) * 68 : 0);
     const u4_t* g4 = reinterpret_cast<const u4_t*>(wg);
     const u4_t* u4 = reinterpret_cast<const u4_t*>(wu);
     auto go = [&](auto kern) {
@@ -2008,7 +1977,7 @@ hipError_t launch_qgemv_q4_affine(const uint32_t* wq, const void* S, const void*
     }
     // f32 x (the LFM runner's activations): the same team kernel over hi + lo f16 parts of x
     const int MT = M <= 1 ? 1 : (M <= 2 ? 2 : 4);
-    const size_t lds32 = (size_t)2 * MT * (K >> 5) * 64 + (size_t)MT * (K >> 5) * 8;
+    const size_t lds32 = (size_t)2 * MT * (K >> 5) * 64 + (size_t)MT * (K >> 5) * 12;
     if (!force_generic && xdt == DT_F32 && M <= 4 && (K % 32) == 0 && group_size >= 32 && aligned16(wq) &&
         aligned16(x) && lds32 <= 160 * 1024) {
         const GemvShape sh = pick_shape(K >> 5, N, true);
@@ -2095,7 +2064,7 @@ bool qgemv_q4_gate_up_supported(int xdt, int M, int K, int group_size, const voi
     const bool f32x = xdt == DT_F32;
     return (xdt == DT_F16 || f32x) && M >= 1 && M <= 4 && K > 0 && (K % 32) == 0 && group_size >= 32 &&
            aligned16(x) && aligned16(wg) && aligned16(wu) &&
-           (f32x ? (size_t)qgemv_q4_lds_bytes(M, K) + (size_t)(M <= 1 ? 1 : (M <= 2 ? 2 : 4)) * (K >> 5) * 64 <=
+           (f32x ? (size_t)qgemv_q4_lds_bytes(M, K) + (size_t)(M <= 1 ? 1 : (M <= 2 ? 2 : 4)) * (K >> 5) * 68 <=
                        160 * 1024
                  : qgemv_q4_lds_bytes(M, K) <= 64 * 1024);
 }
@@ -2120,7 +2089,7 @@ bool qgemv_q4_segs_supported(int xdt, int M, int K, int group_size, const void* 
     if (!(xdt == DT_F16 || xdt == DT_F32) || M < 1 || M > 4 || K <= 0 || (K % 32) != 0 || group_size < 32 ||
         !aligned16(x))
         return false;
-    const size_t lds = (size_t)qgemv_q4_lds_bytes(M, K) + (xdt == DT_F32 ? (size_t)(M <= 1 ? 1 : (M <= 2 ? 2 : 4)) * (K >> 5) * 64 : 0);
+    const size_t lds = (size_t)qgemv_q4_lds_bytes(M, K) + (xdt == DT_F32 ? (size_t)(M <= 1 ? 1 : (M <= 2 ? 2 : 4)) * (K >> 5) * 68 : 0);
     if (lds > (xdt == DT_F32 ? 160 : 64) * 1024) return false;
     for (int i = 0; i < nseg; ++i)
         if (!aligned16(segs[i].w)) return false;
@@ -2134,7 +2103,7 @@ hipError_t launch_q4_segs_shape(const Q4Segs& t, int total_rows, int sbt, const 
                                 hipStream_t st)
 {
     const dim3 grid((total_rows + (kBlock / LPR) - 1) / (kBlock / LPR));
-    const size_t lds = (size_t)qgemv_q4_lds_bytes(M, K) + (XS ? (size_t)MT * (K >> 5) * 64 : 0);
+    const size_t lds = (size_t)qgemv_q4_lds_bytes(M, K) + (XS ? (size_t)MT * (K >> 5) * 68 : 0);
     auto go = [&](auto kern) {
         if (lds > 64 * 1024)
             if (hipError_t e = allow_big_lds(kern, (int)lds); e != hipSuccess) return e;

@@ -483,7 +483,11 @@ int32_t cellm_hip_gelu_tanh_mul_f32(cellm_hip_ctx_t* ctx, float* gate, const flo
 int32_t cellm_hip_add_f32_inplace(cellm_hip_ctx_t* ctx, float* x, const float* y, int64_t n, void* stream);
 
 /* topk_from_logits(..)[0] (llama.rs:1049-1078) after the non-finite -> -inf
- * sanitize (llama.rs:1081-1092), per row: the first index of the maximum. */
+ * sanitize (llama.rs:1081-1092), per row: the first index of the maximum.
+ * One launch of 16384-element chunk blocks per row (rows <= 65535); rows of
+ * more than one chunk hand their chunk maxima to the row's last block through
+ * the context's per-stream scratch (a few bytes per chunk, allocated on the
+ * first call that needs more, counters left at zero by every call). */
 int32_t cellm_hip_argmax_f32(cellm_hip_ctx_t* ctx, const float* logits, int64_t rows, int64_t n, int32_t* out_index,
                              float* out_value, void* stream);
 

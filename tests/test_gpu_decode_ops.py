@@ -288,23 +288,33 @@ def test_attention_rejects_unsupported_head_dim(ops):
                              torch.zeros(1, dtype=torch.int32, device="cuda"), z, 1, 1, 96, 1, 1, 16, 0)
 
 
-@pytest.mark.parametrize("n", [49152, 49151, 131072])
+@pytest.mark.parametrize("n", [49152, 49151, 131072, 151936, 262144, 16385, 1000])
 def test_argmax_first_and_non_finite(ops, n):
-    rows = np.stack([oracle.gen_normal((n,), 0xD0000090 + r, 0.0, 1.0) for r in range(4)]).astype(np.float32)
-    rows[1, 100] = rows[1, 40000] = 50.0          # a tie: the first index wins
-    rows[2, 7] = np.nan                           # NaN -> -inf
-    rows[2, 9] = np.inf                           # +inf -> -inf too (not finite)
-    rows[3, :] = -np.inf                          # all -inf: index 0
-    idx = torch.empty(4, dtype=torch.int32, device="cuda")
-    val = torch.empty(4, dtype=torch.float32, device="cuda")
-    ops.encode_argmax(dev(rows), idx, val)
-    torch.cuda.synchronize()
-    got = idx.cpu().numpy()
-    for r in range(4):
-        z = rows[r].copy()
-        z[~np.isfinite(z)] = -np.inf
-        assert got[r] == oracle.argmax_first(z), r
-    assert got[1] == 100
+    """First maximum per row over chunk blocks of 16384 elements combined in one launch: ties inside a
+    chunk and across chunks keep the first index; NaN and +-inf count as -inf; an all -inf row
+    gives index 0; the maximum in the ragged last chunk; three calls in a row (the row counters
+    return to zero) with the same results and values."""
+    rows = np.stack([oracle.gen_normal((n,), 0xD0000090 + r, 0.0, 1.0) for r in range(5)]).astype(np.float32)
+    rows[1, 100] = rows[1, min(40000, n - 1)] = 50.0   # a tie (across chunks when n > 40000): the first index wins
+    rows[2, 7] = np.nan                                 # NaN -> -inf
+    rows[2, 9] = np.inf                                 # +inf -> -inf too (not finite)
+    rows[3, :] = -np.inf                                # all -inf: index 0
+    rows[4, n - 1] = 60.0                               # in the last (ragged) chunk
+    rows[4, n - 2] = 60.0                               # ... tied with its neighbour: n - 2 wins
+    idx = torch.empty(5, dtype=torch.int32, device="cuda")
+    val = torch.empty(5, dtype=torch.float32, device="cuda")
+    d = dev(rows)
+    for _ in range(3):
+        idx.fill_(-7)
+        ops.encode_argmax(d, idx, val)
+        torch.cuda.synchronize()
+        got, gv = idx.cpu().numpy(), val.cpu().numpy()
+        for r in range(5):
+            z = rows[r].copy()
+            z[~np.isfinite(z)] = -np.inf
+            assert got[r] == oracle.argmax_first(z), r
+            assert gv[r] == z[got[r]], r
+        assert got[1] == 100 and got[4] == n - 2
 
 
 def test_add_inplace(ops):
