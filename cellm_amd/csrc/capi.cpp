@@ -229,7 +229,7 @@ int32_t qgemv_i8_impl(cellm_hip_ctx* ctx, const int8_t* w, const void* scales, i
     // 2..64 activation rows: weights streamed once into MFMA operands (exact for
     // int8).  At m <= 4 the VALU GEMV wins until there are rows enough to fill
     // the chip with MFMA tiles.
-    if (!force_gemm && gemm_ok && (m > 4 || n >= kMfmaMinRows) && qgemv_mfma_supported(1, (int)m, (int)k, 0)) {
+    if (!force_gemm && gemm_ok && (m > 4 || n >= kMfmaMinRows) && qgemv_mfma_supported(1, (int)m, (int)n, (int)k, 0)) {
         float* ws = nullptr;
         const size_t need = qgemv_mfma_workspace_bytes(1, (int)m, (int)n, (int)k);
         if (int32_t rc = get_workspace(ctx, st, need, &ws)) return rc;
@@ -293,7 +293,7 @@ int32_t qgemv_q4_impl(cellm_hip_ctx* ctx, const uint32_t* wq, const void* scales
     // 2..64 activation rows: f16 MFMA tiles dequantized in registers; at m <= 4
     // only for long outputs (else the f32-accumulating VALU GEMV is faster)
     if (!force_gemm && (m > 4 || n >= kMfmaMinRows) && gemm_ok &&
-        qgemv_mfma_supported(0, (int)m, (int)k, (int)group)) {
+        qgemv_mfma_supported(0, (int)m, (int)n, (int)k, (int)group)) {
         float* ws = nullptr;
         const size_t need = qgemv_mfma_workspace_bytes(0, (int)m, (int)n, (int)k);
         if (int32_t rc = get_workspace(ctx, st, need, &ws)) return rc;

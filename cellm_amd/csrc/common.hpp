@@ -149,6 +149,21 @@ __device__ __forceinline__ float group_max(float v)
     if constexpr (W >= 2) v = fmaxf(v, lane_xor<1>(v, W));
     return v;
 }
+// Raw buffer resource over [base, base + bytes), bytes < 2^31.  A buffer store whose byte
+// offset falls outside it is dropped by the hardware, so a masked store is one instruction
+// with an out-of-range offset (kBufferDrop) in the lanes that must not write -- no branch,
+// and the same number of memory instructions on every path.
+constexpr uint32_t kBufferDrop = 0x80000000u;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(void* base, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(base, (short)0, (int)bytes, 0x00020000);
+}
+// NT: non-temporal (streaming) store
+template <bool NT>
+__device__ __forceinline__ void buffer_store_f32(float v, __amdgpu_buffer_rsrc_t r, uint32_t byte_off)
+{
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, (int)byte_off, 0, NT ? 2 : 0);
+}
 __device__ __forceinline__ float quad_sum(float v) { return group_sum<4>(v); }
 __device__ __forceinline__ float pair_sum(float v) { return group_sum<2>(v); }
 __device__ __forceinline__ float oct_sum(float v) { return group_sum<8>(v); }

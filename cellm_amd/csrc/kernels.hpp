@@ -85,12 +85,13 @@ hipError_t launch_qgemm_q4_affine_ws(const uint32_t* wq, const void* S, const vo
 hipError_t launch_qgemm_i8_ws(const int8_t* w, const void* S, int sdt, int per_channel, const _Float16* x,
                               const float* bias, float* y, int M, int N, int K, float* workspace, hipStream_t st);
 
-// Batched decode on MFMA (2 <= M <= 64, f16 x): int8 needs K % 64 == 0,
-// q4 K % 128 == 0 and group >= 64; 16-byte aligned W and x.
+// Batched decode on MFMA (2 <= M <= 64, f16 x): int8 needs K % 64 == 0 and
+// K >= 128, q4 K % 128 == 0, K >= 256 and group >= 32; 16-byte aligned W and x;
+// ceil16(M) * N * 4 < 2^31.
 // Small N over a long K splits K over work items (partial sums in `ws`, then a
 // reduction kernel); qgemv_mfma_workspace_bytes is the size that needs, 0 when
 // the shape runs unsplit.  Without enough workspace the shape runs unsplit.
-bool qgemv_mfma_supported(int wt, int M, int K, int group_size);
+bool qgemv_mfma_supported(int wt, int M, int N, int K, int group_size);
 size_t qgemv_mfma_workspace_bytes(int wt, int M, int N, int K);
 hipError_t launch_qgemv_mfma_i8(const int8_t* w, const void* S, int sdt, int per_channel, const _Float16* x,
                                 const float* bias, float* y, int M, int N, int K, float* ws, size_t ws_bytes,

@@ -33,6 +33,7 @@
 //         prefill qGEMM and the oracle's f16 dequant produce.
 #include <algorithm>
 #include <mutex>
+#include <type_traits>
 #include <vector>
 
 #include "common.hpp"
@@ -88,7 +89,7 @@ __device__ __forceinline__ h8_t i8x8_to_f16(uint32_t w0, uint32_t w1)
 // CU (8-16 per CU), so no cross-iteration register ring is needed -- the
 // compiler counts outstanding loads exactly only through straight-line code,
 // and a ring that crosses tile boundaries would wait on every load anyway.
-template <int WT, int MS, int NT, int DEPTH, int SBT, bool CHUNKED, int BT = kBlock>
+template <int WT, int MS, int NT, int DEPTH, int SBT, bool CHUNKED, bool SPLIT, int BT = kBlock>
 __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
     const void* __restrict__ W, const void* __restrict__ S, const void* __restrict__ Bz, int per_channel, int gshift,
     const _Float16* __restrict__ X, const float* __restrict__ bias, float* __restrict__ Y, int M, int N, int K, int KC,
@@ -130,11 +131,6 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
             }
         }
     };
-    if constexpr (!CHUNKED) {
-        stage(0, K);
-        __syncthreads();
-    }
-
     // One block's B operands + MFMAs: w[t] is this lane's 16 bytes of row
     // (lane%16) of W tile t at the block's k slot 16*(lane/16) bytes; kx is the
     // block's first column in the staged X.
@@ -192,20 +188,23 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
     // about a quarter slower.
     const bool low8 = (rl & 8) == 0;
     const int npairs = nkb >> 1;
+    const int nitems = ntiles * nsplit;
     // Work item = (tile, split): split s covers block pairs [s*pps, min(npairs, (s+1)*pps)), the
     // last split also the odd last K block.  Consecutive items share a split (and its X columns).
-    for (int item = blockIdx.x; item < ntiles * nsplit; item += gridDim.x) {
-        const int split = item / ntiles, tile = item - split * ntiles;
-        const int pb = split * pps, pe = min(npairs, pb + pps);
-        const bool last_split = split == nsplit - 1;
+    int split = 0, tile = 0, pb = 0, pe = 0;
+    bool last_split = true;
+    const char* wpair[NT][2];
+    const char* wtail[NT];
+    size_t sbrow[NT];  // the tile row this lane loads (rows past N: N - 1)
+    auto setup = [&](int item) {
+        split = item / ntiles;
+        tile = item - split * ntiles;
+        pb = split * pps;
+        pe = min(npairs, pb + pps);
+        last_split = split == nsplit - 1;
         k0 = pb * 2 * KB;
         k1 = last_split ? K : pe * 2 * KB;
         // rows past N read row N-1 and are never stored
-        const char* wpair[NT][2];
-        const char* wtail[NT];
-        size_t sbrow[NT];
-        uint32_t sc_raw[NT];
-        float bv[NT];
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
             const int base = tile * ROWS + wave * NT * 16 + t * 16;
@@ -215,117 +214,171 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
                 wpair[t][h] = wb + (size_t)min(base + (rl & 7) + 8 * h, N - 1) * row_bytes + 16 * g +
                               64 * ((rl >> 3) ^ h);
             wtail[t] = wb + (size_t)r * row_bytes + 16 * g;
-            sbrow[t] = (size_t)r * gpr;
-            sc_raw[t] = 0;
-            bv[t] = 0.0f;
-            if constexpr (WT == 1) {
-                sc_raw[t] = load_raw<SBT>(S, per_channel ? (size_t)r : 0);
-                if (bias) bv[t] = bias[r];
-            }
+            sbrow[t] = (size_t)r;
         }
-#pragma unroll
-        for (int i = 0; i < MS; ++i)
-#pragma unroll
-            for (int t = 0; t < NT; ++t) acc[i][t] = f4_t{0.f, 0.f, 0.f, 0.f};
-
-        for (int p0 = pb; p0 < pe; p0 += DEPTH) {
-            // the group's weights (and q4 group scale/bias) in one burst
-            u4_t ld[DEPTH][NT][2];
-            uint32_t sr[DEPTH][2][NT], br[DEPTH][2][NT];
-#pragma unroll
-            for (int d = 0; d < DEPTH; ++d) {
-                if (p0 + d < pe) {
-#pragma unroll
-                    for (int t = 0; t < NT; ++t) {
-#pragma unroll
-                        for (int h = 0; h < 2; ++h)
-                            ld[d][t][h] = __builtin_nontemporal_load(
-                                reinterpret_cast<const u4_t*>(wpair[t][h] + (size_t)(p0 + d) * 128));
-                        if constexpr (WT == 0) {
-#pragma unroll
-                            for (int h = 0; h < 2; ++h) {
-                                const size_t gi = sbrow[t] + ((((p0 + d) * 2 + h) * KB + 32 * g) >> gshift);
-                                sr[d][h][t] = load_raw<SBT>(S, gi);
-                                br[d][h][t] = load_raw<SBT>(Bz, gi);
-                            }
-                        }
-                    }
-                }
-            }
-            const int kx0 = chunk_at(p0 * 2 * KB);
-#pragma unroll
-            for (int d = 0; d < DEPTH; ++d) {
-                if (p0 + d < pe) {
-                    u4_t w0[NT], w1[NT];
-#pragma unroll
-                    for (int t = 0; t < NT; ++t) {
-                        const u4_t a = ld[d][t][0], b = ld[d][t][1];
-#pragma unroll
-                        for (int j = 0; j < 4; ++j) {
-                            w0[t][j] = low8 ? a[j] : b[j];
-                            w1[t][j] = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(low8 ? b[j] : a[j]), kRowRor8,
-                                                                             0xF, 0xF, false);
-                        }
-                    }
-                    mma_block(w0, sr[d][0], br[d][0], kx0 + d * 2 * KB);
-                    mma_block(w1, sr[d][1], br[d][1], kx0 + d * 2 * KB + KB);
-                }
-            }
-        }
-        if ((nkb & 1) && last_split) {
-            // odd last block: 16 rows x 64 bytes, already in the B layout
-            u4_t w[NT];
-            uint32_t s[NT], b[NT];
+    };
+    // int8 row scale and bias of the current item, loaded unconditionally (without a bias the
+    // load reads X and the value is replaced by 0) so that no branch changes the count of
+    // memory operations in flight
+    uint32_t sc_raw[NT];
+    float bv[NT];
+    auto load_scale = [&]() {
+        if constexpr (WT == 1) {
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                w[t] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(wtail[t] + (size_t)(nkb - 1) * 64));
+                const size_t r = sbrow[t];
+                sc_raw[t] = load_raw<SBT>(S, per_channel ? r : 0);
+                const float b = *(bias ? bias + r : reinterpret_cast<const float*>(X));
+                bv[t] = bias ? b : 0.0f;
+            }
+        }
+    };
+    // one group's weights (and q4 group scale/bias) in one burst; pairs past the item's end load
+    // its last pair again (never used), so every group issues the same loads and the compiler's
+    // wait counts stay exact
+    u4_t ld[DEPTH][NT][2];
+    uint32_t sr[DEPTH][2][NT], br[DEPTH][2][NT];
+    auto issue = [&](int p0) {
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) {
+            const int p = min(p0 + d, pe - 1);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    ld[d][t][h] =
+                        __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(wpair[t][h] + (size_t)p * 128));
                 if constexpr (WT == 0) {
-                    const size_t gi = sbrow[t] + (((nkb - 1) * KB + 32 * g) >> gshift);
-                    s[t] = load_raw<SBT>(S, gi);
-                    b[t] = load_raw<SBT>(Bz, gi);
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const size_t gi = sbrow[t] * gpr + (((p * 2 + h) * KB + 32 * g) >> gshift);
+                        sr[d][h][t] = load_raw<SBT>(S, gi);
+                        br[d][h][t] = load_raw<SBT>(Bz, gi);
+                    }
                 }
             }
-            mma_block(w, s, b, chunk_at((nkb - 1) * KB));
         }
-
-        // C tile: lane holds activation rows 4*(lane/16)+e, weight row lane%16
-        if (part) {
-            // split-K: raw sums to part[split][m][n]; the reduction applies the scale and bias
-            float* pp = part + (size_t)split * M * N;
+    };
+    // the group's MFMAs
+    auto consume = [&](int p0) {
+        const int kx0 = chunk_at(p0 * 2 * KB);
 #pragma unroll
-            for (int t = 0; t < NT; ++t) {
-                const int n = tile * ROWS + row_in_tile + t * 16;
+        for (int d = 0; d < DEPTH; ++d) {
+            if (p0 + d < pe) {
+                u4_t w0[NT], w1[NT];
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    const u4_t a = ld[d][t][0], b = ld[d][t][1];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        w0[t][j] = low8 ? a[j] : b[j];
+                        w1[t][j] = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(low8 ? b[j] : a[j]), kRowRor8, 0xF,
+                                                                         0xF, false);
+                    }
+                }
+                mma_block(w0, sr[d][0], br[d][0], kx0 + d * 2 * KB);
+                mma_block(w1, sr[d][1], br[d][1], kx0 + d * 2 * KB + KB);
+            }
+        }
+    };
+
+    // The next item's first group is issued before this item's C tile is stored: gfx9 counts
+    // loads and stores on one in-order counter, so stores issued first would hold that group's
+    // wait until they had reached memory (the 1152 -> 262144 int8 lm_head at M = 64 ran 93 us
+    // with its stores, ~71 us without them).  Every path issues the same memory operations
+    // (items have at least one block pair; stores are buffer stores that drop out-of-range
+    // lanes; loads are unconditional), so the compiler's waits count exactly.
+    const uint32_t ybytes = (uint32_t)M * (uint32_t)N * 4u;
+    const auto yr = buffer_rsrc(Y, ybytes);
+    // C tile of the finished item: lane holds activation rows 4*(lane/16)+e, weight row lane%16.
+    // Columns past N get an offset past 2^31, rows past M one past M*N*4: both are dropped.
+    auto store_tile = [&](int n0, int cur_split, const float(&scl)[NT], const float(&bvc)[NT]) {
+        uint32_t col[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) col[t] = n0 + t * 16 < N ? (uint32_t)(n0 + t * 16) : 0x20000000u;
+        auto put = [&](auto nt, __amdgpu_buffer_rsrc_t r, bool raw) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
 #pragma unroll
                 for (int i = 0; i < MS; ++i)
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        const int m = i * 16 + g * 4 + e;
-                        if (n < N && m < M) pp[(size_t)m * N + n] = acc[i][t][e];
+                        const uint32_t m = i * 16 + g * 4 + e;
+                        const float v = raw ? acc[i][t][e] : acc[i][t][e] * scl[t] + bvc[t];
+                        buffer_store_f32<decltype(nt)::value>(v, r, (m * (uint32_t)N + col[t]) * 4u);
                     }
+        };
+        if constexpr (SPLIT)
+            // split-K: raw sums to part[split][m][n]; the reduction applies the scale and bias
+            put(std::false_type{}, buffer_rsrc(part + (size_t)cur_split * M * N, ybytes), true);
+        else
+            // more than 16 rows: up to 64 MB of logits that nothing re-reads soon, stored past the
+            // caches (measured ~3 % faster at M = 64, 5 % slower at M = 4)
+            put(std::integral_constant<bool, (MS > 1)>{}, yr, false);
+    };
+
+    // the odd last K block (16 rows x 64 bytes, already in the B layout), loaded with the item's
+    // first group
+    u4_t tw[NT];
+    uint32_t ts[NT], tb[NT];
+    auto issue_tail = [&]() {
+        if ((nkb & 1) && last_split) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                tw[t] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(wtail[t] + (size_t)(nkb - 1) * 64));
+                if constexpr (WT == 0) {
+                    const size_t gi = sbrow[t] * gpr + (((nkb - 1) * KB + 32 * g) >> gshift);
+                    ts[t] = load_raw<SBT>(S, gi);
+                    tb[t] = load_raw<SBT>(Bz, gi);
+                }
             }
-            continue;
         }
+    };
+
+    int item = blockIdx.x;
+    if (item >= nitems) return;
+    setup(item);
+    issue(pb);
+    issue_tail();
+    // as many dropped stores as a C tile, so the first item's group has the same operations
+    // behind it as every later one
+#pragma unroll
+    for (int u = 0; u < MS * NT * 4; ++u) buffer_store_f32<false>(0.0f, yr, kBufferDrop + 256u * u);  // distinct: not merged
+    if constexpr (!CHUNKED) {
+        // X staged while the first weights are in flight
+        stage(0, K);
+        __syncthreads();
+    }
+    int n0 = 0, cur_split = 0;
+    float scl[NT], bvc[NT];
+    for (;;) {
+        load_scale();
+#pragma unroll
+        for (int i = 0; i < MS; ++i)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) acc[i][t] = f4_t{0.f, 0.f, 0.f, 0.f};
+        consume(pb);
+        for (int p0 = pb + DEPTH; p0 < pe; p0 += DEPTH) {
+            issue(p0);
+            consume(p0);
+        }
+        if ((nkb & 1) && last_split) mma_block(tw, ts, tb, chunk_at((nkb - 1) * KB));
+
+        n0 = tile * ROWS + row_in_tile;
+        cur_split = split;
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            const int n = tile * ROWS + row_in_tile + t * 16;
-            const float s = WT == 1 ? raw_to_f32<SBT>(sc_raw[t]) : 1.0f;
-#pragma unroll
-            for (int i = 0; i < MS; ++i)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int m = i * 16 + g * 4 + e;
-                    if (n < N && m < M) {
-                        // many rows: up to 64 MB of logits that nothing re-reads soon, stored past the
-                        // caches (measured ~3 % faster at M = 64, 5 % slower at M = 4)
-                        const float v = acc[i][t][e] * s + bv[t];
-                        if (M > 8)
-                            __builtin_nontemporal_store(v, Y + (size_t)m * N + n);
-                        else
-                            Y[(size_t)m * N + n] = v;
-                    }
-                }
+            scl[t] = WT == 1 ? raw_to_f32<SBT>(sc_raw[t]) : 1.0f;
+            bvc[t] = WT == 1 ? bv[t] : 0.0f;
         }
+        item += gridDim.x;
+        if (item >= nitems) break;
+        setup(item);
+        issue(pb);
+        issue_tail();
+        store_tile(n0, cur_split, scl, bvc);
     }
+    store_tile(n0, cur_split, scl, bvc);
 }
 
 // Blocks of one instantiation that fit a CU at this LDS size, times the CU
@@ -463,8 +516,14 @@ hipError_t launch_mfma_nt(const void* W, const void* S, const void* B, int per_c
         // measured).  q4 (its dequant needs more registers): 512 threads.
         const size_t whole = (size_t)MS * 16 * (K + kXPad) * 2;
         if (sp.nsplit == 1 && whole > 80 * 1024 && whole <= kWholeXLds) {
-            constexpr int BT = WT == 1 ? 1024 : 512, DEPTH = 2, ROWS = (BT / 64) * NT * 16;
-            auto kern = qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, false, BT>;
+#ifndef CELLM_WX_NT
+#define CELLM_WX_NT 1
+#define CELLM_WX_DEPTH 2
+#define CELLM_WX_BT 1024
+#endif
+            constexpr int XNT = WT == 1 ? CELLM_WX_NT : 1;
+            constexpr int BT = WT == 1 ? CELLM_WX_BT : 512, DEPTH = WT == 1 ? CELLM_WX_DEPTH : 2, ROWS = (BT / 64) * XNT * 16;
+            auto kern = qgemv_mfma_kernel<WT, MS, XNT, DEPTH, SBT, false, false, BT>;
             if (hipError_t e = allow_big_lds(kern, (int)kWholeXLds); e != hipSuccess) return e;
             const int ntiles = (N + ROWS - 1) / ROWS;
             int per_cu = 0;
@@ -492,16 +551,17 @@ hipError_t launch_mfma_nt(const void* W, const void* S, const void* B, int per_c
     }
     const size_t lds = (size_t)MS * 16 * (KC + kXPad) * 2;
     const int items = ntiles * sp.nsplit;
+    auto launch = [&](auto kern) {
+        const int grid = std::min(items, resident_blocks(kern, lds));
+        hipLaunchKernelGGL(kern, dim3(grid), dim3(kBlock), lds, st, W, S, B, per_channel, gshift, X, bias, Y, M, N, K,
+                           KC, ntiles, sp.pps, sp.nsplit, part);
+    };
     if (KC < K) {
-        auto kern = qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, true>;
-        const int grid = std::min(items, resident_blocks(kern, lds));
-        hipLaunchKernelGGL(kern, dim3(grid), dim3(kBlock), lds, st, W, S, B, per_channel, gshift, X, bias, Y, M, N, K,
-                           KC, ntiles, sp.pps, sp.nsplit, part);
+        if (part) launch(qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, true, true>);
+        else launch(qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, true, false>);
     } else {
-        auto kern = qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, false>;
-        const int grid = std::min(items, resident_blocks(kern, lds));
-        hipLaunchKernelGGL(kern, dim3(grid), dim3(kBlock), lds, st, W, S, B, per_channel, gshift, X, bias, Y, M, N, K,
-                           KC, ntiles, sp.pps, sp.nsplit, part);
+        if (part) launch(qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, false, true>);
+        else launch(qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, false, false>);
     }
     if (hipError_t e = hipGetLastError(); e != hipSuccess || sp.nsplit == 1) return e;
     // one-wave blocks: a few thousand threads at most, spread over as many CUs as there are waves
@@ -542,11 +602,15 @@ hipError_t launch_mfma(const void* W, const void* S, const void* B, int per_chan
 
 }  // namespace
 
-bool qgemv_mfma_supported(int wt, int M, int K, int group_size)
+bool qgemv_mfma_supported(int wt, int M, int N, int K, int group_size)
 {
-    if (M < 2 || M > 64 || K <= 0) return false;
-    if (wt == 1) return K % 64 == 0;
-    return K % 128 == 0 && group_size >= 32;
+    if (M < 2 || M > 64 || N <= 0) return false;
+    // every 16-row X tile's output offsets fit the 2^31-byte buffer range of the stores
+    if ((size_t)((M + 15) & ~15) * (size_t)N * 4 > 0x7FFFFFFFu) return false;
+    // at least one 128-byte block pair per row (the kernel issues a work item's first pair
+    // unconditionally)
+    if (wt == 1) return K % 64 == 0 && K >= 128;
+    return K % 128 == 0 && K >= 256 && group_size >= 32;
 }
 
 size_t qgemv_mfma_workspace_bytes(int wt, int M, int N, int K)
