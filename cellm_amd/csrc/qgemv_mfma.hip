@@ -16,12 +16,11 @@
 // 16-byte chunk of its row per K block:
 //   int8: 16 weights, k = kb + 16g .. +16, two MFMA k-steps (t = 0,1: 8 each);
 //   q4:   32 weights (one group), k = kb + 32g .. +32, four k-steps.
-// The MFMA contracts over whatever k each slot carries as long as A and B
-// agree, so X is staged in LDS per 8-k word in the order the unpacked weight
-// pairs come out (int8: 0,2,1,3,4,6,5,7; q4: natural order).
+// Both unpacks produce the weights of each 8-k word in natural order, so X is
+// copied into LDS as it lies in memory.
 //
 // Dequant into the f16 B operand:
-//   int8: u8 = w ^ 0x80 is exact in f16 as (1152 + w) - 1152 (v_and_or_b32 +
+//   int8: u8 = w ^ 0x80 is exact in f16 as (1152 + w) - 1152 (v_perm_b32 +
 //         v_pk_add_f16), so products are exact and the result differs from
 //         the reference only by summation order; the row scale is applied
 //         after the sum, as in the reference.
@@ -51,24 +50,17 @@ constexpr int kBlock = 256;
 constexpr int kXPad = CELLM_MFMA_XPAD;  // halves of padding after each staged X row
 constexpr int kRowRor8 = 0x128;  // DPP control: rotate by 8 within each 16-lane row
 
-// Permutation of one 8-element x word into the unpack order.
-template <int WT>
-__device__ __forceinline__ h8_t permute_word(h8_t v)
-{
-    if constexpr (WT == 1) return h8_t{v[0], v[2], v[1], v[3], v[4], v[6], v[5], v[7]};
-    else return v;  // q4 tiles come out in natural order
-}
-
-// int8 word pair (8 weights) -> f16 x8 in order 0,2,1,3,4,6,5,7 (exact).
+// int8 word pair (8 weights) -> f16 x8 in natural order (exact): byte permutes place
+// 0x64 above each biased byte, giving f16 1024 + (w + 128), and 1152 is subtracted.
 __device__ __forceinline__ h8_t i8x8_to_f16(uint32_t w0, uint32_t w1)
 {
-    const uint32_t mlo = 0x00FF00FFu, magic = 0x64006400u;
+    const uint32_t hi = 0x64646464u;
     const h2_t off = {(_Float16)1152.0f, (_Float16)1152.0f};
     const uint32_t b0 = w0 ^ 0x80808080u, b1 = w1 ^ 0x80808080u;
-    const h2_t a0 = as_h2(and_or(b0, mlo, magic)) - off;       // (w0, w2)
-    const h2_t a1 = as_h2(and_or(b0 >> 8, mlo, magic)) - off;  // (w1, w3)
-    const h2_t a2 = as_h2(and_or(b1, mlo, magic)) - off;       // (w4, w6)
-    const h2_t a3 = as_h2(and_or(b1 >> 8, mlo, magic)) - off;  // (w5, w7)
+    const h2_t a0 = as_h2(__builtin_amdgcn_perm(hi, b0, 0x04010400u)) - off;  // (w0, w1)
+    const h2_t a1 = as_h2(__builtin_amdgcn_perm(hi, b0, 0x04030402u)) - off;  // (w2, w3)
+    const h2_t a2 = as_h2(__builtin_amdgcn_perm(hi, b1, 0x04010400u)) - off;  // (w4, w5)
+    const h2_t a3 = as_h2(__builtin_amdgcn_perm(hi, b1, 0x04030402u)) - off;  // (w6, w7)
     return h8_t{a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
 }
 
@@ -89,7 +81,7 @@ __device__ __forceinline__ h8_t i8x8_to_f16(uint32_t w0, uint32_t w1)
 // CU (8-16 per CU), so no cross-iteration register ring is needed -- the
 // compiler counts outstanding loads exactly only through straight-line code,
 // and a ring that crosses tile boundaries would wait on every load anyway.
-template <int WT, int MS, int NT, int DEPTH, int SBT, bool CHUNKED, bool SPLIT, int BT = kBlock>
+template <int WT, int MS, int NT, int DEPTH, int SBT, bool CHUNKED, bool SPLIT, int BT = kBlock, int WK = 1>
 __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
     const void* __restrict__ W, const void* __restrict__ S, const void* __restrict__ Bz, int per_channel, int gshift,
     const _Float16* __restrict__ X, const float* __restrict__ bias, float* __restrict__ Y, int M, int N, int K, int KC,
@@ -98,7 +90,9 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
     extern __shared__ __align__(16) _Float16 xs[];  // [MS*16][KC + kXPad]
     constexpr int KB = WT == 1 ? 64 : 128;  // K per block: 64 bytes of every row
     constexpr int TSTEPS = KB / 32;         // MFMA k-steps per block
-    constexpr int ROWS = (BT / 64) * NT * 16;
+    static_assert(!(CHUNKED && WK > 1), "waves splitting an item's K need the item's X whole");
+    constexpr int WR = BT / 64 / WK;  // row groups; WK waves share each one's rows, splitting K
+    constexpr int ROWS = WR * NT * 16;
     const int stride = KC + kXPad;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int rl = lane & 15, g = lane >> 4;
@@ -106,29 +100,20 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
     const int gpr = (K + (1 << gshift) - 1) >> gshift;
     const size_t row_bytes = WT == 1 ? (size_t)K : (size_t)K / 2;
     const char* wb = reinterpret_cast<const char*>(W);
-    const int row_in_tile = wave * NT * 16 + rl;
+    const int wr = wave % WR, wk = wave / WR;
+    const int row_in_tile = wr * NT * 16 + rl;
 
-    // ---- X staging: columns [kb, kb + kcl) in unpack order, rows >= M zero.
-    // Loads are unconditional (clamped) so they issue back to back.
+    // ---- X staging: columns [kb, kb + kcl) of the M rows, copied global -> LDS by
+    // global_load_lds_dwordx4 (no registers; 16 bytes per lane, lane i at the wave's LDS base +
+    // 16 i).  Chunk j of the padded layout is row j / (stride/8), word j % (stride/8); padding
+    // words and rows M..MS*16-1 (zeroed once, below) are not written.  The caller waits vmcnt(0)
+    // before the barrier that publishes the tile.
     auto stage = [&](int kb, int kcl) {
-        const int words = kcl >> 3, total = MS * 16 * words;
-        for (int base = threadIdx.x; base < total; base += 4 * BT) {
-            u4_t r[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int idx = min(base + u * BT, total - 1);
-                const int m = idx / words, wd = idx - m * words;
-                r[u] = *reinterpret_cast<const u4_t*>(X + (size_t)min(m, M - 1) * K + kb + wd * 8);
-            }
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int idx = base + u * BT;
-                const int m = idx / words, wd = idx - m * words;
-                const u4_t v = m < M ? r[u] : u4_t{0u, 0u, 0u, 0u};
-                if (idx < total)
-                    *reinterpret_cast<h8_t*>(xs + (size_t)m * stride + wd * 8) =
-                        permute_word<WT>(__builtin_bit_cast(h8_t, v));
-            }
+        const int words = kcl >> 3, rowc = stride >> 3, total = M * rowc;
+        for (int j0 = wave * 64; j0 < total; j0 += BT) {
+            const int j = j0 + lane, m = j / rowc, c = j - m * rowc;
+            if (j < total && c < words)
+                __builtin_amdgcn_global_load_lds(X + (size_t)m * K + kb + c * 8, xs + (size_t)j0 * 8, 16, 0, 0);
         }
     };
     // One block's B operands + MFMAs: w[t] is this lane's 16 bytes of row
@@ -170,6 +155,7 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
             if (off == 0) {
                 __syncthreads();  // every wave is done with the previous chunk
                 stage(k0 + c * KC, min(KC, k1 - (k0 + c * KC)));
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
                 __syncthreads();
             }
             return off;
@@ -191,7 +177,7 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
     const int nitems = ntiles * nsplit;
     // Work item = (tile, split): split s covers block pairs [s*pps, min(npairs, (s+1)*pps)), the
     // last split also the odd last K block.  Consecutive items share a split (and its X columns).
-    int split = 0, tile = 0, pb = 0, pe = 0;
+    int split = 0, tile = 0, pb = 0, pe = 0, wpb = 0, wpe = 0;  // item pairs; this wave's share
     bool last_split = true;
     const char* wpair[NT][2];
     const char* wtail[NT];
@@ -202,12 +188,15 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
         pb = split * pps;
         pe = min(npairs, pb + pps);
         last_split = split == nsplit - 1;
+        const int q = (pe - pb + WK - 1) / WK;
+        wpb = min(pe, pb + wk * q);
+        wpe = min(pe, wpb + q);
         k0 = pb * 2 * KB;
         k1 = last_split ? K : pe * 2 * KB;
         // rows past N read row N-1 and are never stored
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            const int base = tile * ROWS + wave * NT * 16 + t * 16;
+            const int base = tile * ROWS + wr * NT * 16 + t * 16;
             const int r = min(base + rl, N - 1);
 #pragma unroll
             for (int h = 0; h < 2; ++h)
@@ -241,7 +230,7 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
     auto issue = [&](int p0) {
 #pragma unroll
         for (int d = 0; d < DEPTH; ++d) {
-            const int p = min(p0 + d, pe - 1);
+            const int p = max(pb, min(p0 + d, wpe - 1));
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
 #pragma unroll
@@ -264,7 +253,7 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
         const int kx0 = chunk_at(p0 * 2 * KB);
 #pragma unroll
         for (int d = 0; d < DEPTH; ++d) {
-            if (p0 + d < pe) {
+            if (p0 + d < wpe) {
                 u4_t w0[NT], w1[NT];
 #pragma unroll
                 for (int t = 0; t < NT; ++t) {
@@ -295,7 +284,7 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
     auto store_tile = [&](int n0, int cur_split, const float(&scl)[NT], const float(&bvc)[NT]) {
         uint32_t col[NT];
 #pragma unroll
-        for (int t = 0; t < NT; ++t) col[t] = n0 + t * 16 < N ? (uint32_t)(n0 + t * 16) : 0x20000000u;
+        for (int t = 0; t < NT; ++t) col[t] = wk == 0 && n0 + t * 16 < N ? (uint32_t)(n0 + t * 16) : 0x20000000u;
         auto put = [&](auto nt, __amdgpu_buffer_rsrc_t r, bool raw) {
 #pragma unroll
             for (int t = 0; t < NT; ++t)
@@ -309,7 +298,7 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
                     }
         };
         if constexpr (SPLIT)
-            // split-K: raw sums to part[split][m][n]; the reduction applies the scale and bias
+            // split-K: raw sums to part[split][m][n]; the reduction kernel applies the scale and bias
             put(std::false_type{}, buffer_rsrc(part + (size_t)cur_split * M * N, ybytes), true);
         else
             // more than 16 rows: up to 64 MB of logits that nothing re-reads soon, stored past the
@@ -322,7 +311,7 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
     u4_t tw[NT];
     uint32_t ts[NT], tb[NT];
     auto issue_tail = [&]() {
-        if ((nkb & 1) && last_split) {
+        if ((nkb & 1) && last_split && wk == WK - 1) {
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
                 tw[t] = __builtin_nontemporal_load(reinterpret_cast<const u4_t*>(wtail[t] + (size_t)(nkb - 1) * 64));
@@ -335,18 +324,49 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
         }
     };
 
+    // K split over the WK waves of a row group: waves 1..WK-1 hand their sums to wave 0 through
+    // LDS after the X tile; wave 0 adds them in wave order.
+    f4_t* red = reinterpret_cast<f4_t*>(xs + (size_t)MS * 16 * stride);
+    auto reduce_waves = [&]() {
+        if constexpr (WK > 1) {
+            if (wk > 0) {
+#pragma unroll
+                for (int i = 0; i < MS; ++i)
+#pragma unroll
+                    for (int t = 0; t < NT; ++t) red[(((wk - 1) * WR + wr) * MS * NT + i * NT + t) * 64 + lane] = acc[i][t];
+            }
+            __syncthreads();
+            if (wk == 0) {
+                for (int j = 1; j < WK; ++j)
+#pragma unroll
+                    for (int i = 0; i < MS; ++i)
+#pragma unroll
+                        for (int t = 0; t < NT; ++t) acc[i][t] += red[(((j - 1) * WR + wr) * MS * NT + i * NT + t) * 64 + lane];
+            }
+            __syncthreads();  // the slots are free for the next item
+        }
+    };
+
     int item = blockIdx.x;
     if (item >= nitems) return;
     setup(item);
-    issue(pb);
+    issue(wpb);
     issue_tail();
     // as many dropped stores as a C tile, so the first item's group has the same operations
     // behind it as every later one
+    auto dummy_stores = [&]() {
 #pragma unroll
-    for (int u = 0; u < MS * NT * 4; ++u) buffer_store_f32<false>(0.0f, yr, kBufferDrop + 256u * u);  // distinct: not merged
+        for (int u = 0; u < MS * NT * 4; ++u)
+            buffer_store_f32<false>(0.0f, yr, kBufferDrop + 256u * u);  // distinct offsets: not merged
+    };
+    dummy_stores();
+    // the padding rows of the last X tile: zero for every chunk
+    for (int i = threadIdx.x; i < (MS * 16 - M) * (stride >> 3); i += BT)
+        reinterpret_cast<u4_t*>(xs + (size_t)M * stride)[i] = u4_t{0u, 0u, 0u, 0u};
     if constexpr (!CHUNKED) {
         // X staged while the first weights are in flight
         stage(0, K);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
     }
     int n0 = 0, cur_split = 0;
@@ -357,12 +377,13 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
         for (int i = 0; i < MS; ++i)
 #pragma unroll
             for (int t = 0; t < NT; ++t) acc[i][t] = f4_t{0.f, 0.f, 0.f, 0.f};
-        consume(pb);
-        for (int p0 = pb + DEPTH; p0 < pe; p0 += DEPTH) {
+        consume(wpb);
+        for (int p0 = wpb + DEPTH; p0 < wpe; p0 += DEPTH) {
             issue(p0);
             consume(p0);
         }
-        if ((nkb & 1) && last_split) mma_block(tw, ts, tb, chunk_at((nkb - 1) * KB));
+        if ((nkb & 1) && last_split && wk == WK - 1) mma_block(tw, ts, tb, chunk_at((nkb - 1) * KB));
+        reduce_waves();
 
         n0 = tile * ROWS + row_in_tile;
         cur_split = split;
@@ -374,7 +395,7 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
         item += gridDim.x;
         if (item >= nitems) break;
         setup(item);
-        issue(pb);
+        issue(wpb);
         issue_tail();
         store_tile(n0, cur_split, scl, bvc);
     }
@@ -503,6 +524,7 @@ SplitPlan split_plan(int wt, int M, int N, int K)
     return p;
 }
 
+
 template <int WT, int MS, int NT, int SBT>
 hipError_t launch_mfma_nt(const void* W, const void* S, const void* B, int per_channel, int gshift, const _Float16* X,
                           const float* bias, float* Y, int M, int N, int K, const SplitPlan& sp, float* ws,
@@ -550,21 +572,45 @@ hipError_t launch_mfma_nt(const void* W, const void* S, const void* B, int per_c
         part = ws;
     }
     const size_t lds = (size_t)MS * 16 * (KC + kXPad) * 2;
-    const int items = ntiles * sp.nsplit;
-    auto launch = [&](auto kern) {
-        const int grid = std::min(items, resident_blocks(kern, lds));
-        hipLaunchKernelGGL(kern, dim3(grid), dim3(kBlock), lds, st, W, S, B, per_channel, gshift, X, bias, Y, M, N, K,
-                           KC, ntiles, sp.pps, sp.nsplit, part);
+    auto launch = [&](auto kern, int rows, size_t lds_bytes) {
+        const int nt = (N + rows - 1) / rows, items = nt * sp.nsplit;
+        const int grid = std::min(items, resident_blocks(kern, lds_bytes));
+        hipLaunchKernelGGL(kern, dim3(grid), dim3(kBlock), lds_bytes, st, W, S, B, per_channel, gshift, X, bias, Y, M,
+                           N, K, KC, nt, sp.pps, sp.nsplit, part);
     };
-    if (KC < K) {
-        if (part) launch(qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, true, true>);
-        else launch(qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, true, false>);
+    if (part) {
+        // split plans run one tile per wave (launch_mfma_ms)
+        if constexpr (NT == 1) {
+            if (KC < K) launch(qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, true, true>, ROWS, lds);
+            else launch(qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, false, true>, ROWS, lds);
+        }
+    } else if (KC < K) {
+        launch(qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, true, false>, ROWS, lds);
     } else {
-        if (part) launch(qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, false, true>);
-        else launch(qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, false, false>);
+        // Few tiles over a K that takes a wave several load groups: the block's waves share one
+        // tile row group and split its K (WK = 4 or 2), adding their sums through LDS.
+        const int npairs = (K / KB) >> 1, groups = (npairs + DEPTH - 1) / DEPTH;
+        int wk = 1;
+        if constexpr (NT == 1) {
+            for (int cand : {4, 2})
+                if (groups > 1 && npairs >= cand && (N + (4 / cand) * 16 - 1) / ((4 / cand) * 16) <= 2 * device_cus()) {
+                    wk = cand;
+                    break;
+                }
+        }
+        const size_t red = (size_t)(wk - 1) * (4 / wk) * MS * NT * 64 * 16;
+        if constexpr (NT == 1) {
+            if (wk == 4) launch(qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, false, false, kBlock, 4>, 16, lds + red);
+            if (wk == 2) launch(qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, false, false, kBlock, 2>, 32, lds + red);
+        }
+        if (wk == 1) launch(qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, false, false>, ROWS, lds);
     }
     if (hipError_t e = hipGetLastError(); e != hipSuccess || sp.nsplit == 1) return e;
-    // one-wave blocks: a few thousand threads at most, spread over as many CUs as there are waves
+    // A second launch adds the splits.  Adding them inside the GEMV instead (device-coherent
+    // partial stores, an arrival counter per tile and the last block summing in split order)
+    // measured slower on MI355X: int8 1152->1536 at M = 64 15.8 vs 9.6 us per call, q4
+    // 6912->1152 at M = 16 14.6 vs 11.1 us and at M = 64 35.5 vs 13.4 us.
+    // One-wave blocks: a few thousand threads at most, spread over as many CUs as there are waves.
     const size_t work = (N & 3) == 0 && (reinterpret_cast<uintptr_t>(Y) & 15) == 0 ? (size_t)M * N / 4 : (size_t)M * N;
     const unsigned blocks = (unsigned)std::min<size_t>((work + 63) / 64, 8192);
     hipLaunchKernelGGL((mfma_splitk_reduce_kernel<WT, SBT>), dim3(blocks), dim3(64), 0, st, ws, sp.nsplit, S,
@@ -591,7 +637,8 @@ hipError_t launch_mfma(const void* W, const void* S, const void* B, int per_chan
                        const float* bias, float* Y, int M, int N, int K, float* ws, size_t ws_bytes, hipStream_t st)
 {
     SplitPlan sp = split_plan(WT, M, N, K);
-    if (sp.nsplit > 1 && (!ws || ws_bytes < (size_t)sp.nsplit * M * N * sizeof(float))) sp = SplitPlan{1, (K / (WT == 1 ? 64 : 128)) >> 1};
+    if (sp.nsplit > 1 && (!ws || ws_bytes < (size_t)sp.nsplit * M * N * sizeof(float)))
+        sp = SplitPlan{1, (K / (WT == 1 ? 64 : 128)) >> 1};
     switch ((M + 15) / 16) {
     case 1: return launch_mfma_ms<WT, 1, SBT>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, sp, ws, st);
     case 2: return launch_mfma_ms<WT, 2, SBT>(W, S, B, per_channel, gshift, X, bias, Y, M, N, K, sp, ws, st);
