@@ -87,7 +87,11 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
     const _Float16* __restrict__ X, const float* __restrict__ bias, float* __restrict__ Y, int M, int N, int K, int KC,
     int ntiles, int pps, int nsplit, float* __restrict__ part)
 {
-    extern __shared__ __align__(16) _Float16 xs[];  // [MS*16][KC + kXPad]
+    // X rows in LDS: with one X tile (M <= 16) just the M rows, the A operand of the others
+    // selected to zero (a long K at small M then still fits whole); else MS*16 rows, the
+    // padding zeroed
+    extern __shared__ __align__(16) _Float16 xs[];  // [xrows][KC + kXPad]
+    const int xrows = MS == 1 ? M : MS * 16;
     constexpr int KB = WT == 1 ? 64 : 128;  // K per block: 64 bytes of every row
     constexpr int TSTEPS = KB / 32;         // MFMA k-steps per block
     static_assert(!(CHUNKED && WK > 1), "waves splitting an item's K need the item's X whole");
@@ -138,7 +142,13 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
             const int kof = kx + g * (KB / 4) + st * 8;
 #pragma unroll
             for (int i = 0; i < MS; ++i) {
-                const h8_t a = *reinterpret_cast<const h8_t*>(xs + (size_t)(i * 16 + rl) * stride + kof);
+                h8_t a;
+                if constexpr (MS == 1) {
+                    const h8_t v = *reinterpret_cast<const h8_t*>(xs + (size_t)min(rl, M - 1) * stride + kof);
+                    a = rl < M ? v : h8_t{};
+                } else {
+                    a = *reinterpret_cast<const h8_t*>(xs + (size_t)(i * 16 + rl) * stride + kof);
+                }
 #pragma unroll
                 for (int t = 0; t < NT; ++t)
                     acc[i][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bf[t][st], acc[i][t], 0, 0, 0);
@@ -326,7 +336,7 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
 
     // K split over the WK waves of a row group: waves 1..WK-1 hand their sums to wave 0 through
     // LDS after the X tile; wave 0 adds them in wave order.
-    f4_t* red = reinterpret_cast<f4_t*>(xs + (size_t)MS * 16 * stride);
+    f4_t* red = reinterpret_cast<f4_t*>(xs + (size_t)xrows * stride);
     auto reduce_waves = [&]() {
         if constexpr (WK > 1) {
             if (wk > 0) {
@@ -360,8 +370,8 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
             buffer_store_f32<false>(0.0f, yr, kBufferDrop + 256u * u);  // distinct offsets: not merged
     };
     dummy_stores();
-    // the padding rows of the last X tile: zero for every chunk
-    for (int i = threadIdx.x; i < (MS * 16 - M) * (stride >> 3); i += BT)
+    // the padding rows of the last X tile (MS > 1): zero for every chunk
+    for (int i = threadIdx.x; i < (xrows - M) * (stride >> 3); i += BT)
         reinterpret_cast<u4_t*>(xs + (size_t)M * stride)[i] = u4_t{0u, 0u, 0u, 0u};
     if constexpr (!CHUNKED) {
         // X staged while the first weights are in flight
@@ -536,7 +546,7 @@ hipError_t launch_mfma_nt(const void* W, const void* S, const void* B, int per_c
         // int8: 1024 threads, 16 waves of one W tile each (two tiles per wave need more than the 128
         // registers per lane a 1024-thread block leaves, and 8 waves of two tiles stream 12 % slower:
         // measured).  q4 (its dequant needs more registers): 512 threads.
-        const size_t whole = (size_t)MS * 16 * (K + kXPad) * 2;
+        const size_t whole = (size_t)MS * 16 * (K + kXPad) * 2;  // MS == 4: padded rows
         if (sp.nsplit == 1 && whole > 80 * 1024 && whole <= kWholeXLds) {
 #ifndef CELLM_WX_NT
 #define CELLM_WX_NT 1
@@ -561,17 +571,18 @@ hipError_t launch_mfma_nt(const void* W, const void* S, const void* B, int per_c
     constexpr int ROWS = (kBlock / 64) * NT * 16;
     // X in LDS: at most 80 KB per block so two blocks share a CU; the whole K
     // when it fits, else chunks of KC columns (a multiple of the K block)
-    int KC = std::max(1, (80 * 1024 / (MS * 16 * 2) - kXPad) / (2 * DEPTH * KB)) * (2 * DEPTH * KB);
+    const int xrows = MS == 1 ? M : MS * 16;  // the kernel's X rows in LDS
+    int KC = std::max(1, (80 * 1024 / (xrows * 2) - kXPad) / (2 * DEPTH * KB)) * (2 * DEPTH * KB);
     if (KC >= K) KC = K;
     const int ntiles = (N + ROWS - 1) / ROWS;
     float* part = nullptr;
     if (sp.nsplit > 1) {
         // one split's columns (plus an odd last block) in one chunk when they fit
         const int span = sp.pps * 2 * KB + ((K / KB) & 1 ? KB : 0);
-        if ((size_t)MS * 16 * (span + kXPad) * 2 <= 80 * 1024 || span < KC) KC = span;
+        if ((size_t)xrows * (span + kXPad) * 2 <= 80 * 1024 || span < KC) KC = span;
         part = ws;
     }
-    const size_t lds = (size_t)MS * 16 * (KC + kXPad) * 2;
+    const size_t lds = (size_t)xrows * (KC + kXPad) * 2;
     auto launch = [&](auto kern, int rows, size_t lds_bytes) {
         const int nt = (N + rows - 1) / rows, items = nt * sp.nsplit;
         const int grid = std::min(items, resident_blocks(kern, lds_bytes));
