@@ -67,7 +67,9 @@ def parse():
     ap.add_argument("--pmc-sample", nargs="?", const="lm_head_q4", default=None,
                     choices=["lm_head_q4", "lm_head_i8_m1", "lm_head_i8_m64", "qgemm_896x4864", "qgemm_4864x896",
                              "i4_6912x1152", "decode_layer_4",
-                             "q4_gate_up_silu_1152x6912", "q4_down_6912x1152_m1", "q4_down_6912x1152_m4"],
+                             "q4_gate_up_silu_1152x6912", "q4_down_6912x1152_m1", "q4_down_6912x1152_m4",
+                             "q4_down_6912x1152_m16", "q4_down_6912x1152_m64", "q4_gate_up_1152x13824_m4",
+                             "q4_gate_up_1152x13824_m16", "q4_gate_up_1152x13824_m64"],
                     help="run only a 256 MiB device copy (counter calibration) and 20 launches of one kernel "
                          "(default: the q4 lm_head GEMV), for rocprofv3 --pmc passes")
     return ap.parse_args()
@@ -149,15 +151,16 @@ def pmc_sample(torch, ops, stream, gen, which: str):
         ops.encode_qgemv_batch(arr, stream=stream.cuda_stream)
         info.update({"kernel": "qgemv_i4_kernel (symmetric i4 6912->1152, gs = K, M=1, f32 x)",
                      "algorithmic_bytes": n * k // 2 + 2 * n + 4 * k + 4 * n})
-    elif which in ("q4_down_6912x1152_m1", "q4_down_6912x1152_m4"):
-        k, n, copies, m = 6912, 1152, 8, int(which[-1])
+    elif which.startswith(("q4_down_6912x1152_m", "q4_gate_up_1152x13824_m")):
+        k, n = (6912, 1152) if "down" in which else (1152, 13824)
+        copies, m = 8, int(which.rsplit("_m", 1)[1])
         ws = [Q4Weights(torch, n, k, gen) for _ in range(copies)]
         x = torch.randn((m, k), device="cuda", generator=gen).to(torch.float16)
         y = torch.empty((m, n), dtype=torch.float32, device="cuda")
         arr = op_array([ops.qgemv_op_q4_affine(ws[i % copies].wq, ws[i % copies].s, ws[i % copies].b, x, y)
                         for i in range(20)])
         ops.encode_qgemv_batch(arr, stream=stream.cuda_stream)
-        info.update({"kernel": f"qgemv_q4_f16x_kernel (q4 affine 6912->1152, M={m})",
+        info.update({"kernel": f"q4 affine {k}->{n}, M={m} (VALU GEMV at M <= 4 and N < 8192, else MFMA)",
                      "algorithmic_bytes": q4_bytes(m, n, k)})
     elif which == "q4_gate_up_silu_1152x6912":
         k, n, copies = 1152, 6912, 8
