@@ -24,7 +24,7 @@ STEP_LIB_PATH = PKG_DIR / "libcellm_llama_step.so"
 PROBES_LIB_PATH = PKG_DIR / "libcellm_probes.so"
 REPO_ROOT = PKG_DIR.parent
 
-SOURCES = ["qgemv.hip", "qgemv_mfma.hip", "qgemm.hip", "dequant.hip", "decode.hip", "lowbit.hip", "capi.cpp", "cellm_file.cpp"]
+SOURCES = ["qgemv.hip", "qgemv_mfma.hip", "qgemv_f32x_mfma.hip", "qgemm.hip", "dequant.hip", "decode.hip", "lowbit.hip", "capi.cpp", "cellm_file.cpp"]
 HEADERS = ["common.hpp", "kernels.hpp"]
 ARCH = os.environ.get("CELLM_HIP_ARCH", "gfx950")
 

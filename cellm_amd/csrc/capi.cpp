@@ -208,6 +208,9 @@ int32_t get_stream_buffer(cellm_hip_ctx* ctx, std::unordered_map<hipStream_t, De
 // 2..4 activation rows (measured on MI355X: 1152->13824 q4 at m=4 7.6 vs 10.3 us;
 // 960->2560 int8 at m=4 7.2 vs 4.6 us).
 constexpr int64_t kMfmaMinRows = 8192;
+// Output rows from which the f32-x q4 GEMV runs on MFMA (the VALU kernels do the dot twice,
+// once per f16 part of x; the MFMA form reads each weight once and is HBM-bound).
+constexpr int64_t kF32xMfmaMinRows = 32768;
 
 int32_t get_workspace(cellm_hip_ctx* ctx, hipStream_t st, size_t need, float** out)
 {
@@ -290,6 +293,14 @@ int32_t qgemv_q4_impl(cellm_hip_ctx* ctx, const uint32_t* wq, const void* scales
     if (k > 0 && (!wq || !scales || !biases || !x)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null input pointer");
     if (!y) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null output pointer");
     const bool gemm_ok = xdt == DT_F16 && k > 0 && (k % 64) == 0 && group >= 32 && aligned16(wq) && aligned16(x);
+    // f32 x over a long output (the affine lm_head, lfm.rs:700-741): exact nibbles on MFMA
+    if (!force_gemm && xdt == DT_F32 && n >= kF32xMfmaMinRows && aligned16(wq) && aligned16(x) &&
+        qgemv_q4_f32x_mfma_supported((int)m, (int)n, (int)k, (int)group)) {
+        HIP_TRY(launch_qgemv_q4_f32x_mfma(wq, scales, biases, sbt, static_cast<const float*>(x), y, (int)m, (int)n,
+                                          (int)k, st),
+                "qgemv_q4_f32x_mfma launch");
+        return CELLM_HIP_OK;
+    }
     // 2..64 activation rows: f16 MFMA tiles dequantized in registers; at m <= 4
     // only for long outputs (else the f32-accumulating VALU GEMV is faster)
     if (!force_gemm && (m > 4 || n >= kMfmaMinRows) && gemm_ok &&

@@ -93,6 +93,13 @@ hipError_t launch_qgemm_i8_ws(const int8_t* w, const void* S, int sdt, int per_c
 // the shape runs unsplit.  Without enough workspace the shape runs unsplit.
 bool qgemv_mfma_supported(int wt, int M, int N, int K, int group_size);
 size_t qgemv_mfma_workspace_bytes(int wt, int M, int N, int K);
+
+// q4 affine with f32 x on MFMA (1 <= M <= 4, N % 16 == 0, K % 128 == 0, K <= 1024,
+// group 64; 16-byte aligned W and x): nibbles as exact f16 integers, x as hi + lo f16
+// parts scaled per (row, group) by a power of two, scale and bias folded per group.
+bool qgemv_q4_f32x_mfma_supported(int M, int N, int K, int group_size);
+hipError_t launch_qgemv_q4_f32x_mfma(const uint32_t* wq, const void* S, const void* B, int sbt, const float* x,
+                                     float* y, int M, int N, int K, hipStream_t st);
 hipError_t launch_qgemv_mfma_i8(const int8_t* w, const void* S, int sdt, int per_channel, const _Float16* x,
                                 const float* bias, float* y, int M, int N, int K, float* ws, size_t ws_bytes,
                                 hipStream_t st);

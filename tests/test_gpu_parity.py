@@ -514,6 +514,46 @@ def test_q4_affine_f32_activations(ops, n, k, m, sb, group):
     assert rel_err(oracle.qgemv_q4_affine(wq, s, b, xr, k, gs=group), ref) > 3e-5
 
 
+@pytest.mark.parametrize("n,k,m,sb", [
+    (32768, 896, 1, np.float16),
+    (32768, 896, 2, np.float16),
+    (32768, 896, 3, "bf16"),
+    (32768, 896, 4, np.float16),
+    (32768, 128, 2, np.float32),         # one 128-k block: no block pair, only the odd block
+    (35008, 1024, 4, np.float32),        # the longest K; N not a multiple of 64 tiles
+    (40000, 384, 3, np.float16),         # three blocks: a pair and an odd one
+    (151936, 896, 4, np.float32),        # the Qwen-shape affine lm_head at four sessions, f32 S/B
+])
+def test_q4_affine_f32_activations_long_output_mfma(ops, n, k, m, sb):
+    """The long-output f32-x path (lfm.rs:700-741's x_final on the affine lm_head): nibbles as exact
+    f16 integers on MFMA, x as hi + lo f16 parts scaled per (row, group of 64), the group's scale
+    and bias folded after the group's sum.  Every row within 3e-5 of the f32 reference order, which
+    one f16 rounding of x would miss."""
+    wq, s, b, x = make_q4(n, k, m, sb_dtype=sb, x_dtype=np.float32, group=64, salt=90 + m + k % 89)
+    y = _run_q4(ops, wq, s, b, x, group=64)
+    ref = oracle.qgemv_q4_affine(wq, s, b, x, k, gs=64)
+    for r in range(m):
+        assert rel_err(y[r], ref[r]) <= 3e-5, (r, rel_err(y[r], ref[r]))
+    xr = x.astype(np.float16).astype(np.float32)
+    assert rel_err(oracle.qgemv_q4_affine(wq, s, b, xr, k, gs=64), ref) > 3e-5
+
+
+def test_q4_affine_f32_activation_range_long_output_mfma(ops):
+    """The MFMA f32-x path over x far from N(0,1): rows past f16's largest value, at ~1e-5 and
+    ~1e-12, and zero; each row against the f32 oracle to 3e-5, the zero row exactly zero."""
+    k, n, m = 896, 32768, 4
+    row_scale = np.array([1e5, 1e-5, 1e-12, 0.0], np.float32)
+    wq, s, b, x0 = make_q4(n, k, m, x_dtype=np.float32, salt=81)
+    x = np.ascontiguousarray(x0 * row_scale[:, None], np.float32)
+    assert np.max(np.abs(x[0])) > 65504.0
+    y = _run_q4(ops, wq, s, b, x)
+    ref = oracle.qgemv_q4_affine(wq, s, b, x, k)
+    assert np.all(np.isfinite(y))
+    for r in range(m):
+        assert rel_err(y[r], ref[r]) <= 3e-5, (r, rel_err(y[r], ref[r]))
+    assert not np.any(y[3])
+
+
 @pytest.mark.parametrize("entry", ["gemv", "gate_up_silu", "qkv"])
 def test_q4_affine_f32_activation_range(ops, entry):
     """f32 x far from N(0,1) through the three hi + lo f16 kernels (lfm.rs:985-1066 takes any
