@@ -5,23 +5,29 @@
 //   y[m,n] = sum_k (q[n,k] s[n,g(k)] + b[n,g(k)]) x[m,k].
 // Per group of 64 k the scale and bias factor out of the dot product:
 //   y[m,n] = sum_g ( s[n,g] * sum_{k in g} q[n,k] x[m,k]  +  b[n,g] * sum_{k in g} x[m,k] ).
-// Here the inner sums run on v_mfma_f32_16x16x32_f16 with the nibbles as exact f16
-// integers (B) and x as two f16 parts, hi = RNE_f16(x') and lo = RNE_f16(x' - hi), in
-// A rows m and M + m, where x' = x * 2^sh with one power of two per (row, group) chosen
-// from the group's largest |x| (so every finite x stays inside f16's normal range).
-// q * part is exact in f32, so the group sum carries x to about 22 bits, as the f32-x
-// VALU kernels do; the fold  y += s * (2^-sh * acc) + b * sum(x)  runs once per group.
+// The inner sums run on v_mfma_i32_16x16x64_i8: the nibbles are the B bytes as they are,
+// and each x row becomes three signed 8-bit digits.  x' = rint(x * 2^sh), one power of two
+// per row chosen from the row's largest |x| so that |x'| <= 2^20, and
+//   x' = d0 * 2^14 + d1 * 2^7 + d2,   |d0|, |d1|, |d2| <= 64,
+// in A rows m, M + m and 2M + m.  Each group's integer sum is exact; it is folded in f32 as
+// Y_d += s * acc_d (plus b * sum(x) on the d0 rows, pre-divided by 2^(14 - sh), a power of
+// two), and y = 2^-sh * (2^14 Y_0 + 2^7 Y_1 + Y_2).  x is carried to 2^-20 of the row's
+// largest |x| (the f32-x VALU kernels carry each element to about 22 bits through two f16
+// parts); the reference order is matched to well within 3e-5 normwise.
 //
 // MFMA k-slots and groups: a lane (row n = lane%16, slot group g = lane/16) loads 16
 // bytes of its row per 128-k block, k = 32g .. 32g+31, i.e. words w0..w3 of 8 nibbles.
-// One 16x16x32 k-step contracts the four lanes' words, which would mix the block's two
-// groups; v_permlane32_swap of (w0, w1) and of (w2, w3) moves the words between lane
-// halves so that each k-step holds one group:
+// A 64-k step over the four lanes' data would mix the block's two groups;
+// v_permlane32_swap of (w0, w1) and of (w2, w3) moves words between the lane halves so
+// that each step holds one group:
 //   R0 = swap(w0,w1).first : g = 0,1,2,3 -> k 0, 32, 8, 40 (+0..7)     group 0 of the block
 //   R1 = swap(w0,w1).second: g = 0,1,2,3 -> k 64, 96, 72, 104           group 1
 //   R2 = swap(w2,w3).first : k 16, 48, 24, 56                           group 0
 //   R3 = swap(w2,w3).second: k 80, 112, 88, 120                         group 1
-// The A fragment of lane (row, g) for a k-step reads those 8 k of its X row from LDS.
+// A lane's B operand for a group is (nibbles 0,2,4,6 | 1,3,5,7) of its first word, then of
+// its second; X is staged in LDS in exactly that order per (row, block, group, lane group),
+// so the A operand is one 16-byte LDS read.  (The MFMA contracts A and B over the same
+// register positions, whatever k those hold.)
 #include <algorithm>
 #include <mutex>
 #include <vector>
@@ -34,25 +40,13 @@ namespace cellm {
 
 namespace {
 
-constexpr int kFxThreads = 256;  // four waves
+// eight waves per block (measured 4 % faster than four and than sixteen at 896->151936)
+constexpr int kFxThreads = 512;
+constexpr int kFxWaves = kFxThreads / 64;
 constexpr int kFxMaxK = 1024;
 constexpr int kFxMaxGroups = kFxMaxK / 64;
-constexpr int kFxAPad = 8;        // halves after each staged X row
+constexpr int kFxAPad = 16;       // bytes after each staged digit row (rows then start 4 banks apart)
 constexpr int kFxWaveLds = 2048;  // per wave: the tile's (scale, bias) table, then its output tile
-
-// 8 nibbles of a word as exact f16 integers, in the order q0 q2 q4 q6 q1 q3 q5 q7
-// (0x64 placed above each nibble byte gives f16 1024 + q; 1024 is then subtracted).
-__device__ __forceinline__ h8_t q4_word_exact(uint32_t w)
-{
-    const uint32_t hi64 = 0x64646464u;
-    const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
-    const h2_t off = {(_Float16)1024.0f, (_Float16)1024.0f};
-    const h2_t a0 = as_h2(__builtin_amdgcn_perm(hi64, lo, 0x04010400u)) - off;  // q0 q2
-    const h2_t a1 = as_h2(__builtin_amdgcn_perm(hi64, lo, 0x04030402u)) - off;  // q4 q6
-    const h2_t a2 = as_h2(__builtin_amdgcn_perm(hi64, hi, 0x04010400u)) - off;  // q1 q3
-    const h2_t a3 = as_h2(__builtin_amdgcn_perm(hi64, hi, 0x04030402u)) - off;  // q5 q7
-    return h8_t{a0[0], a0[1], a1[0], a1[1], a2[0], a2[1], a3[0], a3[1]};
-}
 
 // A tile's loads: its 16 W rows over the whole K as full 128-byte row segments (two
 // 128-k blocks; load h covers rows 8h..8h+7, lane (rl, g) taking row (rl & 7) + 8h at byte
@@ -65,7 +59,7 @@ struct FxTile {
     uint32_t s[4], b[4];
 };
 
-// Four waves per block; wave w of block b takes tiles b*4 + w, += gridDim.x*4, a tile being
+// Eight waves per block; wave w of block b takes tiles b*8 + w, += gridDim.x*8, a tile being
 // 16 rows of W over the whole K (NB blocks of 128).  Each wave keeps its next tile's loads in
 // flight while it computes the current one: two register sets, the loop unrolled by two so
 // neither is copied, and a tile past the end loaded through a buffer offset out of range
@@ -79,18 +73,18 @@ __global__ __launch_bounds__(kFxThreads) void qgemv_q4_f32x_mfma_kernel(const ui
 {
     constexpr int K = NB * 128, G = K / 64, NP = NB / 2, astride = K + kFxAPad;
     extern __shared__ __align__(16) unsigned char smem[];
-    _Float16* A = reinterpret_cast<_Float16*>(smem);                              // [16][astride]
-    float* P2 = reinterpret_cast<float*>(smem + (size_t)16 * astride * 2);        // [kFxMaxGroups][16]: 2^-sh
-    float* SX = P2 + kFxMaxGroups * 16;                                           // [kFxMaxGroups][16]: sum x
-    unsigned char* wave_lds = reinterpret_cast<unsigned char*>(SX + kFxMaxGroups * 16);
+    int8_t* A = reinterpret_cast<int8_t*>(smem);                          // [16 digit rows][astride] bytes
+    float* SX = reinterpret_cast<float*>(smem + (size_t)16 * astride);   // [kFxMaxGroups][16]: d0 rows' sum x
+    float* P2 = SX + kFxMaxGroups * 16;                                   // [4]: 2^-sh per x row
+    uint32_t* RMAX = reinterpret_cast<uint32_t*>(P2 + 4);                 // [4]: bits of the row's max |x|
+    unsigned char* wave_lds = reinterpret_cast<unsigned char*>(RMAX + 4);
     // the wave index as a uniform (scalar) value, so the tile loop is a scalar loop
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int rl = lane & 15, g = lane >> 4;
-    const int ntiles = N >> 4, stride = gridDim.x * 4;
+    const int ntiles = N >> 4, stride = gridDim.x * kFxWaves;
     constexpr uint32_t row_bytes = K / 2;
     const auto wr = buffer_rsrc(const_cast<uint32_t*>(W), (uint32_t)ntiles * 16u * row_bytes);
     const bool low8 = (rl & 8) == 0;
-    const int offg = (g & 1) * 32 + (g >> 1) * 8;  // this lane's k within a group-pure k-step
 
     auto load_tile = [&](FxTile<NB>& t, int tile) {
         const bool live = tile < ntiles;
@@ -114,95 +108,104 @@ __global__ __launch_bounds__(kFxThreads) void qgemv_q4_f32x_mfma_kernel(const ui
         }
     };
 
-    int tile = blockIdx.x * 4 + wave;
+    int tile = blockIdx.x * kFxWaves + wave;
     FxTile<NB> ta, tb;
     load_tile(ta, tile);  // in flight while X is staged
 
-    // ---- X: rows 0..M-1 hi parts, M..2M-1 lo parts, 2M..15 zero; per (row, group) 2^-sh
-    // and the group's sum of x (zero for lo and padding rows).
-    for (int i = threadIdx.x; i < (16 - 2 * M) * (astride >> 3); i += kFxThreads)
-        reinterpret_cast<u4_t*>(A + (size_t)2 * M * astride)[i] = u4_t{0u, 0u, 0u, 0u};
-    for (int i = threadIdx.x; i < kFxMaxGroups * 16; i += kFxThreads) {
-        if ((i & 15) >= 2 * M) {
-            P2[i] = 0.0f;
-            SX[i] = 0.0f;
+    // ---- X as digit rows.  Item i = ((m * NB + b) * 2 + h) * 4 + g is the 16 k that lane group
+    // g supplies for group h of block b: two words of 8 k at kb = 128b + 64h + {0,32,8,40}[g]
+    // and kb + 16, each in the order 0,2,4,6,1,3,5,7.  One item per thread (M * K / 16 <= 256).
+    for (int i = threadIdx.x; i < (16 - 3 * M) * (astride >> 4); i += kFxThreads)
+        reinterpret_cast<u4_t*>(A + (size_t)3 * M * astride)[i] = u4_t{0u, 0u, 0u, 0u};
+    for (int i = threadIdx.x; i < kFxMaxGroups * 16; i += kFxThreads) SX[i] = 0.0f;
+    if (threadIdx.x < 4) RMAX[threadIdx.x] = 0u;
+    const int items = M * (K / 16), it = min((int)threadIdx.x, items - 1);
+    const int im = it / (K / 16), ir = it - im * (K / 16);
+    const int ib = ir >> 3, ih = (ir >> 2) & 1, ig = ir & 3;
+    const int kb = 128 * ib + 64 * ih + (ig & 1) * 32 + (ig >> 1) * 8;
+    float xv[16];
+    {
+        const f4_t* r0 = reinterpret_cast<const f4_t*>(X + (size_t)im * K + kb);
+        const f4_t* r1 = reinterpret_cast<const f4_t*>(X + (size_t)im * K + kb + 16);
+        const f4_t a0 = r0[0], a1 = r0[1], c0 = r1[0], c1 = r1[1];
+        constexpr int order[8] = {0, 2, 4, 6, 1, 3, 5, 7};
+        const float w0[8] = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+        const float w1[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            xv[j] = w0[order[j]];
+            xv[8 + j] = w1[order[j]];
         }
     }
-    {
-        constexpr int words = K / 8;
-        const int total = M * words;  // a multiple of 8: K % 64 == 0
-        for (int base = 0; base < total; base += kFxThreads) {
-            const int i = base + threadIdx.x, ic = min(i, total - 1);
-            const int m = ic / words, c = ic - m * words;
-            const f4_t* src = reinterpret_cast<const f4_t*>(X + (size_t)m * K + 8 * c);
-            const f4_t v0 = src[0], v1 = src[1];
-            float xv[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-            float mx = 0.0f, xs = 0.0f;
+    float mx = 0.0f, xs = 0.0f;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                mx = fmaxf(mx, fabsf(xv[j]));
-                xs += xv[j];
-            }
-            // eight consecutive lanes hold one group of 64 (aligned: words per row % 8 == 0)
-            mx = group_max<8>(mx);
-            xs = group_sum<8>(xs);
-            int e = 0;
-            (void)__builtin_frexpf(mx, &e);
-            const int sh = (mx > 0.0f && mx <= 3.402823466e38f) ? min(14 - e, 126) : 0;
-            h8_t hi, lo;
-            constexpr int order[8] = {0, 2, 4, 6, 1, 3, 5, 7};  // q4_word_exact's order
+    for (int j = 0; j < 16; ++j) {
+        mx = fmaxf(mx, fabsf(xv[j]));
+        xs += xv[j];
+    }
+    xs = group_sum<4>(xs);  // the group's 64 k: four consecutive items (items % 4 == 0)
+    __syncthreads();        // RMAX cleared
+    if ((int)threadIdx.x < items) atomicMax(&RMAX[im], __builtin_bit_cast(uint32_t, mx));  // |x| >= 0: bits order as values
+    __syncthreads();
+    if ((int)threadIdx.x < items) {
+        const float rmax = __builtin_bit_cast(float, RMAX[im]);
+        int e = 0;
+        (void)__builtin_frexpf(rmax, &e);
+        const int sh = (rmax > 0.0f && rmax <= 3.402823466e38f) ? min(20 - e, 140) : 0;
+        uint32_t dw[3][4];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float xp = __builtin_ldexpf(xv[order[j]], sh);
-                hi[j] = (_Float16)xp;
-                lo[j] = (_Float16)(xp - (float)hi[j]);
+        for (int q = 0; q < 4; ++q) {
+            uint32_t b0 = 0, b1 = 0, b2 = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float xp = rintf(__builtin_ldexpf(xv[4 * q + j], sh));  // |xp| <= 2^20
+                const float d0 = rintf(xp * 0.00006103515625f);             // / 2^14
+                const float r = xp - d0 * 16384.0f;                          // |r| <= 2^13
+                const float d1 = rintf(r * 0.0078125f);                      // / 2^7
+                const float d2 = r - d1 * 128.0f;
+                b0 |= ((uint32_t)(int)d0 & 0xFFu) << (8 * j);
+                b1 |= ((uint32_t)(int)d1 & 0xFFu) << (8 * j);
+                b2 |= ((uint32_t)(int)d2 & 0xFFu) << (8 * j);
             }
-            if (i < total) {
-                *reinterpret_cast<h8_t*>(A + (size_t)m * astride + 8 * c) = hi;
-                *reinterpret_cast<h8_t*>(A + (size_t)(M + m) * astride + 8 * c) = lo;
-                if ((c & 7) == 0) {
-                    const int grp = c >> 3;
-                    const float p2 = __builtin_ldexpf(1.0f, -sh);
-                    P2[grp * 16 + m] = p2;
-                    P2[grp * 16 + M + m] = p2;
-                    SX[grp * 16 + m] = xs;
-                    SX[grp * 16 + M + m] = 0.0f;
-                }
-            }
+            dw[0][q] = b0;
+            dw[1][q] = b1;
+            dw[2][q] = b2;
         }
+#pragma unroll
+        for (int d = 0; d < 3; ++d)
+            *reinterpret_cast<u4_t*>(A + (size_t)(d * M + im) * astride + 16 * ir) = u4_t{dw[d][0], dw[d][1], dw[d][2], dw[d][3]};
+        if (ig == 0) SX[(2 * ib + ih) * 16 + im] = __builtin_ldexpf(xs, sh - 14);  // exact: a power of two
+        if (ir == 0) P2[im] = __builtin_ldexpf(1.0f, -sh);
     }
     __syncthreads();
     if (tile >= ntiles) return;
 
-    float2* sbw = reinterpret_cast<float2*>(wave_lds + wave * kFxWaveLds);  // [16 rows][16 groups]
+    float2* sbw = reinterpret_cast<float2*>(wave_lds + wave * kFxWaveLds);  // [16 groups][16 rows]: no bank conflicts
     float* otw = reinterpret_cast<float*>(wave_lds + wave * kFxWaveLds);    // [16][16], after the folds
 
     auto compute = [&](const FxTile<NB>& t, int n0) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) sbw[rl * 16 + 4 * g + j] = make_float2(raw_to_f32<SBT>(t.s[j]), raw_to_f32<SBT>(t.b[j]));
+        for (int j = 0; j < 4; ++j) sbw[(4 * g + j) * 16 + rl] = make_float2(raw_to_f32<SBT>(t.s[j]), raw_to_f32<SBT>(t.b[j]));
         f4_t y = {0.f, 0.f, 0.f, 0.f};
-        auto fold = [&](const f4_t& acc, int grp) {
-            const f4_t pv = *reinterpret_cast<const f4_t*>(P2 + grp * 16 + 4 * g);
+        // one group's integer sums of rows 4g..4g+3 (digit rows) for column rl
+        auto fold = [&](const i4_t& acc, int grp) {
             const f4_t sx = *reinterpret_cast<const f4_t*>(SX + grp * 16 + 4 * g);
-            const float2 sb = sbw[rl * 16 + grp];
+            const float2 sb = sbw[grp * 16 + rl];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) y[e] = fmaf(acc[e] * pv[e], sb.x, fmaf(sb.y, sx[e], y[e]));
+            for (int e = 0; e < 4; ++e) y[e] = fmaf((float)acc[e], sb.x, fmaf(sb.y, sx[e], y[e]));
         };
         auto do_block = [&](const u4_t& w, int b) {
             const auto s01 = __builtin_amdgcn_permlane32_swap(w[0], w[1], false, false);
             const auto s23 = __builtin_amdgcn_permlane32_swap(w[2], w[3], false, false);
-            const _Float16* arow = A + (size_t)rl * astride + 128 * b + offg;
-            const h8_t a0 = *reinterpret_cast<const h8_t*>(arow);
-            const h8_t a2 = *reinterpret_cast<const h8_t*>(arow + 16);
-            const h8_t a1 = *reinterpret_cast<const h8_t*>(arow + 64);
-            const h8_t a3 = *reinterpret_cast<const h8_t*>(arow + 80);
-            const f4_t z = {0.f, 0.f, 0.f, 0.f};
-            f4_t ce = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, q4_word_exact(s01[0]), z, 0, 0, 0);
-            ce = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, q4_word_exact(s23[0]), ce, 0, 0, 0);
-            f4_t co = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, q4_word_exact(s01[1]), z, 0, 0, 0);
-            co = __builtin_amdgcn_mfma_f32_16x16x32_f16(a3, q4_word_exact(s23[1]), co, 0, 0, 0);
-            fold(ce, 2 * b);
-            fold(co, 2 * b + 1);
+            const uint32_t m4 = 0x0F0F0F0Fu;
+            const i4_t b0 = {(int)(s01[0] & m4), (int)((s01[0] >> 4) & m4), (int)(s23[0] & m4), (int)((s23[0] >> 4) & m4)};
+            const i4_t b1 = {(int)(s01[1] & m4), (int)((s01[1] >> 4) & m4), (int)(s23[1] & m4), (int)((s23[1] >> 4) & m4)};
+            const int8_t* arow = A + (size_t)rl * astride + 128 * b + 16 * g;
+            const i4_t a0 = *reinterpret_cast<const i4_t*>(arow);
+            const i4_t a1 = *reinterpret_cast<const i4_t*>(arow + 64);
+            const i4_t z = {0, 0, 0, 0};
+            fold(__builtin_amdgcn_mfma_i32_16x16x64_i8(a0, b0, z, 0, 0, 0), 2 * b);
+            fold(__builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, z, 0, 0, 0), 2 * b + 1);
         };
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
@@ -218,12 +221,14 @@ __global__ __launch_bounds__(kFxThreads) void qgemv_q4_f32x_mfma_kernel(const ui
         }
         if constexpr (NB & 1) do_block(t.tail, NB - 1);
 
-        // rows m (hi) and M + m (lo) of column n0 + rl: through the wave's LDS tile
+        // digit rows m, M + m and 2M + m of column n0 + rl: through the wave's LDS tile
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the table reads above are done
 #pragma unroll
         for (int e = 0; e < 4; ++e) otw[(4 * g + e) * 16 + rl] = y[e];
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        if (g < M) Y[(size_t)g * N + n0 + rl] = otw[g * 16 + rl] + otw[(M + g) * 16 + rl];
+        if (g < M)
+            Y[(size_t)g * N + n0 + rl] =
+                P2[g] * (16384.0f * otw[g * 16 + rl] + (128.0f * otw[(M + g) * 16 + rl] + otw[(2 * M + g) * 16 + rl]));
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // before the next tile's table writes
     };
 
@@ -259,15 +264,15 @@ hipError_t launch_fx_nb(const uint32_t* wq, const void* S, const void* B, const 
                         hipStream_t st)
 {
     auto kern = qgemv_q4_f32x_mfma_kernel<SBT, NB>;
-    const size_t lds = (size_t)16 * (NB * 128 + kFxAPad) * 2 + (size_t)2 * kFxMaxGroups * 16 * 4 + 4 * kFxWaveLds;
+    const size_t lds = (size_t)16 * (NB * 128 + kFxAPad) + (size_t)kFxMaxGroups * 16 * 4 + 32 + kFxWaves * kFxWaveLds;
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kFxThreads, lds) != hipSuccess || per_cu < 1)
         per_cu = 1;
     // as few rounds of tiles as the resident waves allow, spread evenly: every wave then takes
     // that many tiles or one fewer
-    const int ntiles = N / 16, waves = per_cu * fx_device_cus() * 4;
+    const int ntiles = N / 16, waves = per_cu * fx_device_cus() * kFxWaves;
     const int rounds = (ntiles + waves - 1) / waves;
-    const int grid = std::max(1, ((ntiles + rounds - 1) / rounds + 3) / 4);
+    const int grid = std::max(1, ((ntiles + rounds - 1) / rounds + kFxWaves - 1) / kFxWaves);
     hipLaunchKernelGGL(kern, dim3(grid), dim3(kFxThreads), lds, st, wq, S, B, x, y, M, N);
     return hipGetLastError();
 }
