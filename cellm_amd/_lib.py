@@ -81,6 +81,12 @@ SIGNATURES = {
                                             _i64, _i64, _i64, _vp]),
     "cellm_hip_decode_gate_up_silu": (_i32, [_vp, _vp, _vp, _vp, _vp, C.c_float, _vp, _vp, _vp, _vp, _i64, _i64,
                                              _i64, _vp, _vp]),
+    "cellm_hip_decode_q4_affine_qkv_rope_kv": (_i32, [_vp, _vp, _vp, _vp, _vp, C.c_float, _vp, _vp, _vp, _vp, _vp, _vp,
+                                                     _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64, _i64, _i64,
+                                                     _i64, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64,
+                                                     _i64, _i64, _i64, _vp]),
+    "cellm_hip_decode_q4_affine_gate_up_silu": (_i32, [_vp, _vp, _vp, _vp, _vp, C.c_float, _vp, _vp, _vp, _vp, _vp,
+                                                      _vp, _i32, _i64, _i64, _i64, _i64, _vp, _vp]),
     "cellm_hip_add_rms_norm": (_i32, [_vp, _vp, _vp, _vp, _i32, _i64, _i64, C.c_float, _vp, _vp]),
     "cellm_hip_rope_half_f32": (_i32, [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp]),
     "cellm_hip_rope_interleaved_f32": (_i32, [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _i64, _vp]),

@@ -1336,6 +1336,96 @@ int32_t cellm_hip_decode_gate_up_silu(cellm_hip_ctx_t* ctx, const float* x_prev,
     CELLM_API_END(report_exception)
 }
 
+namespace {
+
+// Shared checks of the two fused q4 decode entry points.
+int32_t check_decode_q4(const float* x_prev, const float* y, const float* x_out, const float* norm_w,
+                        int32_t sb_dtype, int64_t group, int64_t rows, int64_t hidden, const char* what)
+{
+    if (sb_dtype != CELLM_HIP_DTYPE_F32)
+        return set_error(CELLM_HIP_ERR_UNSUPPORTED, "%s: scales and biases must be f32 (got dtype %d)", what,
+                         (int)sb_dtype);
+    if (rows < 1 || hidden > 4096 || group < 1 || group > hidden ||
+        !decode_q4_fused_supported((int)rows, (int)hidden, (int)group))
+        return set_error(CELLM_HIP_ERR_UNSUPPORTED, "%s needs 1..4 rows, hidden %% 32 == 0, <= 4096 and a power-of-two "
+                                                    "group >= 32 (got rows=%lld hidden=%lld group=%lld)",
+                         what, (long long)rows, (long long)hidden, (long long)group);
+    if (!x_prev || !x_out || !norm_w) return set_error(CELLM_HIP_ERR_INVALID_ARG, "%s: null pointer", what);
+    if (x_out == x_prev || x_out == y)
+        return set_error(CELLM_HIP_ERR_INVALID_ARG, "x_out must not alias x_prev or y (other blocks still read them)");
+    if (!aligned16(x_prev) || (y && !aligned16(y)) || !aligned16(x_out) || !aligned16(norm_w))
+        return set_error(CELLM_HIP_ERR_INVALID_ARG, "%s: x_prev, y, x_out and norm_w must be 16-byte aligned", what);
+    return CELLM_HIP_OK;
+}
+
+}  // namespace
+
+int32_t cellm_hip_decode_q4_affine_qkv_rope_kv(
+    cellm_hip_ctx_t* ctx, const float* x_prev, const float* y, float* x_out, const float* norm_w, float eps,
+    const uint32_t* wq, const void* sq, const void* bq, const float* biasq, const uint32_t* wk, const void* sk,
+    const void* bk, const float* biask, const uint32_t* wv, const void* sv, const void* bv, const float* biasv,
+    int32_t sb_dtype, int64_t group, int64_t rows, int64_t hidden, int64_t n_heads, int64_t n_kv_heads,
+    int64_t head_dim, const int32_t* positions, const float* cos_sin, int64_t table_positions, float* q_out,
+    uint16_t* kcache, uint16_t* vcache, const uint32_t* block_tables, int64_t max_blocks, int64_t total_blocks,
+    int64_t n_layers, int64_t tokens_per_block, int64_t layer, void* stream)
+{
+    CELLM_API_BEGIN
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    if (int32_t rc = check_paged(rows, max_blocks, total_blocks, n_layers, tokens_per_block, layer)) return rc;
+    if (rows == 0) return CELLM_HIP_OK;
+    if (int32_t rc = check_decode_q4(x_prev, y, x_out, norm_w, sb_dtype, group, rows, hidden, "fused q4 decode QKV"))
+        return rc;
+    if (n_heads < 1 || n_kv_heads < 1 || head_dim < 2 || head_dim % 2 != 0 || n_heads > 4096 || n_kv_heads > 4096 ||
+        head_dim > 4096)
+        return set_error(CELLM_HIP_ERR_INVALID_ARG, "bad head geometry %lld/%lld/%lld", (long long)n_heads,
+                         (long long)n_kv_heads, (long long)head_dim);
+    if (table_positions < 1 || table_positions > INT32_MAX)
+        return set_error(CELLM_HIP_ERR_INVALID_ARG, "table_positions must be >= 1");
+    if (!wq || !sq || !bq || !wk || !sk || !bk || !wv || !sv || !bv || !positions || !cos_sin || !q_out || !kcache ||
+        !vcache || !block_tables)
+        return set_error(CELLM_HIP_ERR_INVALID_ARG, "null pointer");
+    if (!aligned16(wq) || !aligned16(wk) || !aligned16(wv))
+        return set_error(CELLM_HIP_ERR_INVALID_ARG, "weights must be 16-byte aligned");
+    DeviceGuard g(ctx->device);
+    const uint32_t* w[3] = {wq, wk, wv};
+    const float* s[3] = {static_cast<const float*>(sq), static_cast<const float*>(sk), static_cast<const float*>(sv)};
+    const float* b[3] = {static_cast<const float*>(bq), static_cast<const float*>(bk), static_cast<const float*>(bv)};
+    const float* bias[3] = {biasq, biask, biasv};
+    HIP_TRY(launch_decode_q4_qkv(x_prev, y, x_out, norm_w, eps, w, s, b, bias, (int)group, (int)rows, (int)hidden,
+                                 (int)n_heads, (int)n_kv_heads, (int)head_dim, positions, cos_sin,
+                                 (int)table_positions, q_out, kcache, vcache, block_tables, (int)max_blocks,
+                                 (int)total_blocks, (int)n_layers, (int)tokens_per_block, (int)layer,
+                                 ctx->rope_interleaved.load(), pick_stream(ctx, stream)),
+            "decode_q4_qkv launch");
+    return CELLM_HIP_OK;
+    CELLM_API_END(report_exception)
+}
+
+int32_t cellm_hip_decode_q4_affine_gate_up_silu(cellm_hip_ctx_t* ctx, const float* x_prev, const float* y,
+                                                float* x_out, const float* norm_w, float eps, const uint32_t* wg,
+                                                const void* sg, const void* bg, const uint32_t* wu, const void* su,
+                                                const void* bu, int32_t sb_dtype, int64_t group, int64_t rows,
+                                                int64_t hidden, int64_t inter, float* h, void* stream)
+{
+    CELLM_API_BEGIN
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    if (rows == 0) return CELLM_HIP_OK;
+    if (int32_t rc =
+            check_decode_q4(x_prev, y, x_out, norm_w, sb_dtype, group, rows, hidden, "fused q4 decode gate/up"))
+        return rc;
+    if (inter < 1 || inter > INT32_MAX) return set_error(CELLM_HIP_ERR_INVALID_ARG, "bad intermediate size");
+    if (!wg || !sg || !bg || !wu || !su || !bu || !h) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null pointer");
+    if (!aligned16(wg) || !aligned16(wu)) return set_error(CELLM_HIP_ERR_INVALID_ARG, "weights must be 16-byte aligned");
+    DeviceGuard g(ctx->device);
+    HIP_TRY(launch_decode_q4_gate_up(x_prev, y, x_out, norm_w, eps, wg, static_cast<const float*>(sg),
+                                     static_cast<const float*>(bg), wu, static_cast<const float*>(su),
+                                     static_cast<const float*>(bu), (int)group, (int)rows, (int)hidden, (int)inter,
+                                     ACT_SILU, h, pick_stream(ctx, stream)),
+            "decode_q4_gate_up launch");
+    return CELLM_HIP_OK;
+    CELLM_API_END(report_exception)
+}
+
 int32_t cellm_hip_attention_gqa_f16kv(cellm_hip_ctx_t* ctx, const float* q, const uint16_t* kcache,
                                       const uint16_t* vcache, const uint32_t* block_tables, int64_t max_blocks,
                                       int64_t total_blocks, const int32_t* positions, int64_t rows, int64_t n_heads,

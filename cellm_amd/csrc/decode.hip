@@ -745,11 +745,13 @@ __host__ __device__ __forceinline__ int xpad(int k) { return k + (k >> 4) * 4; }
 // writes x_prev + y to x_out (HASY false: x_prev as is).  Thread t handles the
 // float4 groups t, t + 256, ... (KR of them: KR * 1024 >= H); its sum of
 // squares runs over its groups in order, then the same wave and block tree as
-// add_rms_norm_kernel.
-template <int MT, int KR, bool HASY>
+// add_rms_norm_kernel.  CSUM (H % 32 == 0): also the sums of the normalised
+// values over each 32-element chunk, xsum[m][H / 32] (the eight groups of a
+// chunk sit in eight adjacent lanes).
+template <int MT, int KR, bool HASY, bool CSUM = false>
 __device__ __forceinline__ void stage_add_norm(const float* __restrict__ x_prev, const float* __restrict__ y,
                                                float* __restrict__ x_out, const float* __restrict__ w, int rows,
-                                               int H, float eps, float* xs, float (*red)[MT])
+                                               int H, float eps, float* xs, float (*red)[MT], float* xsum = nullptr)
 {
     const int t = threadIdx.x;
     const int xst = xpad(H), H4 = H >> 2;
@@ -817,11 +819,14 @@ __device__ __forceinline__ void stage_add_norm(const float* __restrict__ x_prev,
 #pragma unroll
         for (int u = 0; u < KR; ++u) {
             const int g = t + u * kNormThreads;
-            if (g < H4) {
-                f4_t o;
+            f4_t o;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) o[e] = v[m][u][e] * inv * wv[u][e];
-                *reinterpret_cast<f4_t*>(xs + m * xst + xpad(4 * g)) = o;  // 4 | 16: a group never straddles padding
+            for (int e = 0; e < 4; ++e) o[e] = v[m][u][e] * inv * wv[u][e];
+            if (g < H4) *reinterpret_cast<f4_t*>(xs + m * xst + xpad(4 * g)) = o;  // a group never straddles padding
+            if constexpr (CSUM) {
+                // H4 % 8 == 0: the eight groups of a chunk are all in range or all out
+                const float cs = group_sum<8>((o[0] + o[1]) + (o[2] + o[3]));
+                if (g < H4 && (t & 7) == 0) xsum[m * (H >> 5) + (g >> 3)] = cs;
             }
         }
     }
@@ -1000,6 +1005,231 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(DecodeGateUpArgs a)
         const float g = acc0[m] * sg, u = acc1[m] * su;
         const float sig = 1.0f / (1.0f + expf(-g));
         a.h[(size_t)m * a.N + n] = (g * sig) * u;
+    }
+}
+
+// ---- fused decode-step GEMVs over MLX q4 affine weights ---------------------
+// The q4 counterparts of the two kernels above, for the u32 runners (the Qwen2
+// step, qwen.rs:1255-1470, whose projections are linear_i4_out_in,
+// lfm.rs:985-1066, over f32 activations).  Same prologue (stage_add_norm, with
+// the 32-element chunk sums of xn) and team layout (LPR lanes, two output rows,
+// C 16-byte chunks of each per lane, loaded before the prologue).  A chunk is
+// 32 nibbles of one row: four u32 words, element 8j + e = nibble e of word j.
+// The dot is plain f32: the nibbles widened by v_cvt_f32_ubyteN meet xn in FMA
+// chains, and one group scale and bias cover the whole chunk (group >= 32):
+//   y[n] = sum_c ( S[n][g(c)] * sum_{k in c} q[n][k] xn[k] + B[n][g(c)] * xsum[c] )
+// which is sum_k (q S + B) xn in another summation order.
+
+// This lane's C chunks of two rows (w0/w1: row starts in 16-byte chunks; g0/g1:
+// the rows' first scale/bias index), chunk index clamped; f32 scales and biases.
+template <int C>
+__device__ __forceinline__ void load_rows_q4(const u4_t* __restrict__ w0, const float* __restrict__ S0,
+                                             const float* __restrict__ B0, size_t g0, const u4_t* __restrict__ w1,
+                                             const float* __restrict__ S1, const float* __restrict__ B1, size_t g1,
+                                             int lane, int LPR, int cpr, int gshift, u4_t (&a)[C], u4_t (&b)[C],
+                                             float (&sb)[C][4])
+{
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        const int ch = min(lane + c * LPR, cpr - 1);
+        const int gi = (ch << 5) >> gshift;
+        a[c] = __builtin_nontemporal_load(w0 + ch);
+        b[c] = __builtin_nontemporal_load(w1 + ch);
+        sb[c][0] = S0[g0 + gi];
+        sb[c][1] = B0[g0 + gi];
+        sb[c][2] = S1[g1 + gi];
+        sb[c][3] = B1[g1 + gi];
+    }
+}
+
+// acc0/acc1[m] += this lane's chunks of rows 0/1 against xn[m] (xs: stage_add_norm's layout)
+template <int MT, int C>
+__device__ __forceinline__ void dot_rows_q4(const u4_t (&a)[C], const u4_t (&b)[C], const float (&sb)[C][4], int lane,
+                                            int LPR, int cpr, const float* xs, int xst, const float* xsum, int rows,
+                                            float (&acc0)[MT], float (&acc1)[MT])
+{
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        const int ch = lane + c * LPR;
+        if (ch >= cpr) break;
+        float d0[MT], d1[MT];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) d0[m] = d1[m] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t alo = a[c][j] & 0x0F0F0F0Fu, ahi = (a[c][j] >> 4) & 0x0F0F0F0Fu;
+            const uint32_t blo = b[c][j] & 0x0F0F0F0Fu, bhi = (b[c][j] >> 4) & 0x0F0F0F0Fu;
+            const float qa[8] = {cvt_ubyte<0>(alo), cvt_ubyte<0>(ahi), cvt_ubyte<1>(alo), cvt_ubyte<1>(ahi),
+                                 cvt_ubyte<2>(alo), cvt_ubyte<2>(ahi), cvt_ubyte<3>(alo), cvt_ubyte<3>(ahi)};
+            const float qb[8] = {cvt_ubyte<0>(blo), cvt_ubyte<0>(bhi), cvt_ubyte<1>(blo), cvt_ubyte<1>(bhi),
+                                 cvt_ubyte<2>(blo), cvt_ubyte<2>(bhi), cvt_ubyte<3>(blo), cvt_ubyte<3>(bhi)};
+            // elements 32 ch + 8 j + 0..7 sit at xpad(...) = 40 ch + 8 j + (j >= 2 ? 4 : 0) + 0..7
+            const int xo = 40 * ch + 8 * j + (j >= 2 ? 4 : 0);
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                if (m >= rows) break;
+                const f4_t* xp = reinterpret_cast<const f4_t*>(xs + m * xst + xo);
+                const f4_t x0 = xp[0], x1 = xp[1];
+                const float xv[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    d0[m] = __builtin_fmaf(qa[e], xv[e], d0[m]);
+                    d1[m] = __builtin_fmaf(qb[e], xv[e], d1[m]);
+                }
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            if (m >= rows) break;
+            const float xc = xsum[m * cpr + ch];
+            acc0[m] += sb[c][0] * d0[m] + sb[c][1] * xc;
+            acc1[m] += sb[c][2] * d1[m] + sb[c][3] * xc;
+        }
+    }
+}
+
+struct DecodeQ4QkvArgs {
+    const float* x_prev;
+    const float* y;
+    float* x_out;
+    const float* norm_w;
+    float eps;
+    const u4_t* w[3];  // q, k, v: u32 words [rows_out][H / 8] as 16-byte chunks
+    const float* s[3];  // scales and biases [rows_out][H / group]
+    const float* b[3];
+    const float* bias[3];  // projection biases [rows_out] or null
+    int rows, H, n_heads, n_kv_heads, head_dim, gshift;
+    const int32_t* pos;
+    const float2* cs;
+    int table_positions;
+    float* q_out;
+    uint16_t* kc;
+    uint16_t* vc;
+    PagedKv kv;
+    int layer;
+    int il;
+};
+
+// Team -> one RoPE pair (rows i0, i1 of a q, k or v head), as decode_qkv_kernel;
+// the projection bias is added to the row sums before the rotation
+// (add_projection_bias_if_present, qwen.rs:1132-1139, then RoPE).
+template <int LPR, int C, int MT, int KR, bool HASY>
+__global__ __launch_bounds__(256) void decode_q4_qkv_kernel(DecodeQ4QkvArgs a)
+{
+    extern __shared__ __align__(16) float xs[];
+    __shared__ float red[kNormThreads / 64][MT];
+    const int H = a.H, half = a.head_dim >> 1, cpr = H >> 5;
+    const int gpr = (H + (1 << a.gshift) - 1) >> a.gshift;
+    const int team = threadIdx.x / LPR, lane = threadIdx.x % LPR;
+    const int pairs = (a.n_heads + 2 * a.n_kv_heads) * half;
+    const int p_raw = blockIdx.x * (256 / LPR) + team;
+    const int p = min(p_raw, pairs - 1);
+    const int hh = p / half, i = p - hh * half;
+    const int which = hh < a.n_heads ? 0 : (hh < a.n_heads + a.n_kv_heads ? 1 : 2);
+    const int head = which == 0 ? hh : (which == 1 ? hh - a.n_heads : hh - a.n_heads - a.n_kv_heads);
+    const int i0 = rope_lo(i, half, a.il), i1 = rope_hi(i, half, a.il);
+    const int r0 = head * a.head_dim + i0, r1 = head * a.head_dim + i1;
+    const u4_t* wm = which == 0 ? a.w[0] : (which == 1 ? a.w[1] : a.w[2]);
+    const float* sm = which == 0 ? a.s[0] : (which == 1 ? a.s[1] : a.s[2]);
+    const float* bm = which == 0 ? a.b[0] : (which == 1 ? a.b[1] : a.b[2]);
+    u4_t w0[C], w1[C];
+    float sb[C][4];
+    load_rows_q4<C>(wm + (size_t)r0 * cpr, sm, bm, (size_t)r0 * gpr, wm + (size_t)r1 * cpr, sm, bm,
+                    (size_t)r1 * gpr, lane, LPR, cpr, a.gshift, w0, w1, sb);
+
+    float* xsum = xs + MT * xpad(H);
+    stage_add_norm<MT, KR, HASY, true>(a.x_prev, a.y, a.x_out, a.norm_w, a.rows, H, a.eps, xs, red, xsum);
+
+    float acc0[MT], acc1[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc0[m] = acc1[m] = 0.0f;
+    dot_rows_q4<MT, C>(w0, w1, sb, lane, LPR, cpr, xs, xpad(H), xsum, a.rows, acc0, acc1);
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        acc0[m] = group_sum<LPR>(acc0[m]);
+        acc1[m] = group_sum<LPR>(acc1[m]);
+    }
+    if (p_raw >= pairs) return;
+    const float* pb = which == 0 ? a.bias[0] : (which == 1 ? a.bias[1] : a.bias[2]);
+    // lane m writes session m: y (+ bias), then RoPE and the cache write as decode_qkv_kernel
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        if (m != lane || m >= a.rows) continue;
+        float v0 = acc0[m], v1 = acc1[m];
+        if (pb) {
+            v0 = v0 + pb[r0];
+            v1 = v1 + pb[r1];
+        }
+        const int pr = a.pos[m];
+        const float2 c = a.cs[(size_t)min(max(pr, 0), a.table_positions - 1) * half + i];
+        if (which == 0) {
+            float* q = a.q_out + ((size_t)m * a.n_heads + head) * a.head_dim;
+            q[i0] = v0 * c.x - v1 * c.y;
+            q[i1] = v1 * c.x + v0 * c.y;
+            continue;
+        }
+        const long long b = pr >= 0 ? a.kv.base(m, pr, a.layer) : -1;
+        if (b < 0) continue;
+        const size_t e = (size_t)b + (size_t)head * a.head_dim;
+        if (which == 1) {
+            a.kc[e + i0] = __builtin_bit_cast(uint16_t, (_Float16)(v0 * c.x - v1 * c.y));
+            a.kc[e + i1] = __builtin_bit_cast(uint16_t, (_Float16)(v1 * c.x + v0 * c.y));
+        } else {
+            a.vc[e + i0] = __builtin_bit_cast(uint16_t, (_Float16)v0);
+            a.vc[e + i1] = __builtin_bit_cast(uint16_t, (_Float16)v1);
+        }
+    }
+}
+
+struct DecodeQ4GateUpArgs {
+    const float* x_prev;
+    const float* y;
+    float* x_out;
+    const float* norm_w;
+    float eps;
+    const u4_t* wg;
+    const float* sg;
+    const float* bg;
+    const u4_t* wu;
+    const float* su;
+    const float* bu;
+    int rows, H, N, gshift, act;
+    float* h;  // [rows][N]
+};
+
+// Team -> row n of gate and of up; h = act_mul(act, g, u).
+template <int LPR, int C, int MT, int KR, bool HASY>
+__global__ __launch_bounds__(256) void decode_q4_gate_up_kernel(DecodeQ4GateUpArgs a)
+{
+    extern __shared__ __align__(16) float xs[];
+    __shared__ float red[kNormThreads / 64][MT];
+    const int H = a.H, cpr = H >> 5;
+    const int gpr = (H + (1 << a.gshift) - 1) >> a.gshift;
+    const int team = threadIdx.x / LPR, lane = threadIdx.x % LPR;
+    const int n_raw = blockIdx.x * (256 / LPR) + team;
+    const int n = min(n_raw, a.N - 1);
+    u4_t w0[C], w1[C];
+    float sb[C][4];
+    load_rows_q4<C>(a.wg + (size_t)n * cpr, a.sg, a.bg, (size_t)n * gpr, a.wu + (size_t)n * cpr, a.su, a.bu,
+                    (size_t)n * gpr, lane, LPR, cpr, a.gshift, w0, w1, sb);
+
+    float* xsum = xs + MT * xpad(H);
+    stage_add_norm<MT, KR, HASY, true>(a.x_prev, a.y, a.x_out, a.norm_w, a.rows, H, a.eps, xs, red, xsum);
+
+    float acc0[MT], acc1[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc0[m] = acc1[m] = 0.0f;
+    dot_rows_q4<MT, C>(w0, w1, sb, lane, LPR, cpr, xs, xpad(H), xsum, a.rows, acc0, acc1);
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        acc0[m] = group_sum<LPR>(acc0[m]);
+        acc1[m] = group_sum<LPR>(acc1[m]);
+    }
+    if (n_raw >= a.N) return;
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        if (m != lane || m >= a.rows) continue;
+        a.h[(size_t)m * a.N + n] = act_mul(a.act, acc0[m], acc1[m]);
     }
 }
 
@@ -1402,6 +1632,114 @@ hipError_t launch_decode_gate_up(const float* x_prev, const float* y, float* x_o
     DecodeGateUpArgs a{x_prev, y, x_out, norm_w, eps, wg, sg, wu, su, rows, H, N, h};
     if (H > 64 * 16 * 4) return hipErrorInvalidValue;
     return launch_decode<false>(rows, H, a, N, st);
+}
+
+bool decode_q4_fused_supported(int rows, int H, int group)
+{
+    return rows >= 1 && rows <= 4 && H >= 32 && H % 32 == 0 && H <= 4096 && group >= 32 && group <= H &&
+           (group & (group - 1)) == 0;
+}
+
+namespace {
+
+size_t decode_q4_lds_bytes(int MT, int H) { return (size_t)MT * (xpad(H) + (H >> 5)) * sizeof(float); }
+
+template <int LPR, int C, int MT, int KR, bool QKV, class Args>
+hipError_t launch_decode_q4_fixed(const Args& a, int teams_total, hipStream_t st)
+{
+    const dim3 grid((unsigned)((teams_total + 256 / LPR - 1) / (256 / LPR)));
+    const size_t lds = decode_q4_lds_bytes(MT, a.H);
+    if constexpr (QKV) {
+        if (a.y)
+            hipLaunchKernelGGL((decode_q4_qkv_kernel<LPR, C, MT, KR, true>), grid, dim3(256), lds, st, a);
+        else
+            hipLaunchKernelGGL((decode_q4_qkv_kernel<LPR, C, MT, KR, false>), grid, dim3(256), lds, st, a);
+    } else {
+        if (a.y)
+            hipLaunchKernelGGL((decode_q4_gate_up_kernel<LPR, C, MT, KR, true>), grid, dim3(256), lds, st, a);
+        else
+            hipLaunchKernelGGL((decode_q4_gate_up_kernel<LPR, C, MT, KR, false>), grid, dim3(256), lds, st, a);
+    }
+    return hipGetLastError();
+}
+
+template <int LPR, int C, int KR, bool QKV, class Args>
+hipError_t launch_decode_q4_mt(const Args& a, int teams_total, hipStream_t st)
+{
+    if (a.rows <= 1) return launch_decode_q4_fixed<LPR, C, 1, KR, QKV>(a, teams_total, st);
+    if (a.rows <= 2) return launch_decode_q4_fixed<LPR, C, 2, KR, QKV>(a, teams_total, st);
+    return launch_decode_q4_fixed<LPR, C, 4, KR, QKV>(a, teams_total, st);
+}
+
+// chunks per row cpr = H / 32, one chunk per lane up to 64 (teams of 16, 32 or 64 lanes), two up to 128;
+// KR float4 groups per thread in the prologue (KR * 1024 >= H follows from the same bounds)
+template <bool QKV, class Args>
+hipError_t launch_decode_q4(const Args& a, int teams_total, hipStream_t st)
+{
+    const int cpr = a.H >> 5;
+    if (cpr <= 16) return launch_decode_q4_mt<16, 1, 1, QKV>(a, teams_total, st);
+    if (cpr <= 32) return launch_decode_q4_mt<32, 1, 1, QKV>(a, teams_total, st);
+    if (cpr <= 64) return launch_decode_q4_mt<64, 1, 2, QKV>(a, teams_total, st);
+    return launch_decode_q4_mt<64, 2, 4, QKV>(a, teams_total, st);
+}
+
+int log2_exact(int v)
+{
+    int s = 0;
+    while ((1 << s) < v) ++s;
+    return s;
+}
+
+}  // namespace
+
+hipError_t launch_decode_q4_qkv(const float* x_prev, const float* y, float* x_out, const float* norm_w, float eps,
+                                const uint32_t* const w[3], const float* const s[3], const float* const b[3],
+                                const float* const bias[3], int group, int rows, int H, int n_heads, int n_kv_heads,
+                                int head_dim, const int32_t* pos, const float* cos_sin, int table_positions,
+                                float* q_out, uint16_t* kcache, uint16_t* vcache, const uint32_t* block_tables,
+                                int max_blocks, int total_blocks, int n_layers, int tokens_per_block, int layer,
+                                int interleaved, hipStream_t st)
+{
+    if (!decode_q4_fused_supported(rows, H, group)) return hipErrorInvalidValue;
+    DecodeQ4QkvArgs a{};
+    a.x_prev = x_prev;
+    a.y = y;
+    a.x_out = x_out;
+    a.norm_w = norm_w;
+    a.eps = eps;
+    for (int j = 0; j < 3; ++j) {
+        a.w[j] = reinterpret_cast<const u4_t*>(w[j]);
+        a.s[j] = s[j];
+        a.b[j] = b[j];
+        a.bias[j] = bias[j];
+    }
+    a.rows = rows;
+    a.H = H;
+    a.n_heads = n_heads;
+    a.n_kv_heads = n_kv_heads;
+    a.head_dim = head_dim;
+    a.gshift = log2_exact(group);
+    a.pos = pos;
+    a.cs = reinterpret_cast<const float2*>(cos_sin);
+    a.table_positions = table_positions;
+    a.q_out = q_out;
+    a.kc = kcache;
+    a.vc = vcache;
+    a.kv = PagedKv{block_tables, max_blocks, total_blocks, n_layers, tokens_per_block, n_kv_heads * head_dim};
+    a.layer = layer;
+    a.il = interleaved ? 1 : 0;
+    return launch_decode_q4<true>(a, (n_heads + 2 * n_kv_heads) * (head_dim / 2), st);
+}
+
+hipError_t launch_decode_q4_gate_up(const float* x_prev, const float* y, float* x_out, const float* norm_w, float eps,
+                                    const uint32_t* wg, const float* sg, const float* bg, const uint32_t* wu,
+                                    const float* su, const float* bu, int group, int rows, int H, int N, int act,
+                                    float* h, hipStream_t st)
+{
+    if (!decode_q4_fused_supported(rows, H, group)) return hipErrorInvalidValue;
+    DecodeQ4GateUpArgs a{x_prev, y, x_out, norm_w, eps, reinterpret_cast<const u4_t*>(wg), sg, bg,
+                         reinterpret_cast<const u4_t*>(wu), su, bu, rows, H, N, log2_exact(group), act, h};
+    return launch_decode_q4<false>(a, N, st);
 }
 
 int argmax_chunks(int n) { return std::max(1, (n + kArgmaxChunk - 1) / kArgmaxChunk); }

@@ -162,6 +162,21 @@ hipError_t launch_decode_qkv(const float* x_prev, const float* y, float* x_out, 
 hipError_t launch_decode_gate_up(const float* x_prev, const float* y, float* x_out, const float* norm_w, float eps,
                                  const int8_t* wg, const uint16_t* sg, const int8_t* wu, const uint16_t* su, int rows,
                                  int H, int N, float* h, hipStream_t st);
+// The same two launches over MLX q4 affine weights (u32 words, f32 scales and
+// biases, group a power of two >= 32) with an f32 dot: rows 1..4, H % 32 == 0,
+// H <= 4096; q/k/v projection biases optional (null entries).
+bool decode_q4_fused_supported(int rows, int H, int group);
+hipError_t launch_decode_q4_qkv(const float* x_prev, const float* y, float* x_out, const float* norm_w, float eps,
+                                const uint32_t* const w[3], const float* const s[3], const float* const b[3],
+                                const float* const bias[3], int group, int rows, int H, int n_heads, int n_kv_heads,
+                                int head_dim, const int32_t* pos, const float* cos_sin, int table_positions,
+                                float* q_out, uint16_t* kcache, uint16_t* vcache, const uint32_t* block_tables,
+                                int max_blocks, int total_blocks, int n_layers, int tokens_per_block, int layer,
+                                int interleaved, hipStream_t st);
+hipError_t launch_decode_q4_gate_up(const float* x_prev, const float* y, float* x_out, const float* norm_w, float eps,
+                                    const uint32_t* wg, const float* sg, const float* bg, const uint32_t* wu,
+                                    const float* su, const float* bu, int group, int rows, int H, int N, int act,
+                                    float* h, hipStream_t st);
 
 // Remaining .cellm weight formats (lowbit.hip): f16 rows, i2 (2-bit per-row
 // symmetric, scale_mode 0 = scale at the end, 1 = per element), q1_0_g128.

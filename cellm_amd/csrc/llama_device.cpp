@@ -191,6 +191,8 @@ struct cellm_llama_dev {
     DevBuf kcache, vcache, rope, x, x2, xn, q, k, v, attn, proj, h, up, logits, io;
     // fused add+norm+GEMV launches: every projection int8, rows <= 4, hidden % 16 == 0, hidden <= 4096
     bool fused = false;
+    // the same over MLX q4 affine q/k/v (projection biases allowed) and gate/up (no biases), hidden % 32 == 0
+    bool fused_q4 = false;
     // io: [tokens u32 | positions i32 | block tables u32 | argmax idx i32 | argmax val f32]
     void* host_io = nullptr;  // pinned mirror of io
     size_t io_tokens = 0, io_pos = 0, io_bt = 0, io_idx = 0, io_val = 0, io_bytes = 0;
@@ -304,24 +306,40 @@ int32_t enqueue_step(cellm_llama_dev* m, int32_t rows)
                 "embed");
     else
         LIB_TRY(cellm_hip_embed_f16(H, d_tok, R, static_cast<const uint16_t*>(E.w), vocab, hid, x, S), "embed");
-    if (m->fused) {
+    if (m->fused || m->fused_q4) {
         // 5 launches per layer; the residual stream alternates between x and x2
         float* x2 = m->x2.as<float>();
+        auto u32w = [](const Proj& pr) { return static_cast<const uint32_t*>(pr.w); };
         for (int64_t l = 0; l < L; ++l) {
             const Proj* P = &m->p[l * 7];
-            LIB_TRY(cellm_hip_decode_qkv_rope_kv(H, x, l == 0 ? nullptr : proj, x2, m->attn_norm[l], eps, i8w(P[0]),
-                                                 i8s(P[0]), i8w(P[1]), i8s(P[1]), i8w(P[2]), i8s(P[2]), R, hid,
-                                                 c.n_heads, c.n_kv_heads, c.head_dim, d_pos, m->rope.as<float>(),
-                                                 m->table_positions, q, kc, vc, d_bt, MB, c.total_blocks, L, tpb, l,
-                                                 S),
-                    "residual + input_layernorm + qkv + rope + kv write");
+            const float* yl = l == 0 ? nullptr : proj;
+            if (m->fused)
+                LIB_TRY(cellm_hip_decode_qkv_rope_kv(H, x, yl, x2, m->attn_norm[l], eps, i8w(P[0]), i8s(P[0]),
+                                                     i8w(P[1]), i8s(P[1]), i8w(P[2]), i8s(P[2]), R, hid, c.n_heads,
+                                                     c.n_kv_heads, c.head_dim, d_pos, m->rope.as<float>(),
+                                                     m->table_positions, q, kc, vc, d_bt, MB, c.total_blocks, L, tpb,
+                                                     l, S),
+                        "residual + input_layernorm + qkv + rope + kv write");
+            else
+                LIB_TRY(cellm_hip_decode_q4_affine_qkv_rope_kv(
+                            H, x, yl, x2, m->attn_norm[l], eps, u32w(P[0]), P[0].s, P[0].b, P[0].bias, u32w(P[1]),
+                            P[1].s, P[1].b, P[1].bias, u32w(P[2]), P[2].s, P[2].b, P[2].bias, CELLM_HIP_DTYPE_F32, 64,
+                            R, hid, c.n_heads, c.n_kv_heads, c.head_dim, d_pos, m->rope.as<float>(),
+                            m->table_positions, q, kc, vc, d_bt, MB, c.total_blocks, L, tpb, l, S),
+                        "residual + input_layernorm + q4 qkv + bias + rope + kv write");
             LIB_TRY(cellm_hip_attention_gqa_f16kv(H, q, kc, vc, d_bt, MB, c.total_blocks, d_pos, R, c.n_heads,
                                                   c.n_kv_heads, c.head_dim, L, tpb, l, 0.0f, 0.0f, attn, S),
                     "attention");
             if (int32_t rc = run_proj(m, P[3], attn, proj, R, hid, hid, "o_proj")) return rc;
-            LIB_TRY(cellm_hip_decode_gate_up_silu(H, x2, proj, x, m->mlp_norm[l], eps, i8w(P[4]), i8s(P[4]),
-                                                  i8w(P[5]), i8s(P[5]), R, hid, inter, h, S),
-                    "residual + post_attention_layernorm + gate/up");
+            if (m->fused)
+                LIB_TRY(cellm_hip_decode_gate_up_silu(H, x2, proj, x, m->mlp_norm[l], eps, i8w(P[4]), i8s(P[4]),
+                                                      i8w(P[5]), i8s(P[5]), R, hid, inter, h, S),
+                        "residual + post_attention_layernorm + gate/up");
+            else
+                LIB_TRY(cellm_hip_decode_q4_affine_gate_up_silu(H, x2, proj, x, m->mlp_norm[l], eps, u32w(P[4]),
+                                                                P[4].s, P[4].b, u32w(P[5]), P[5].s, P[5].b,
+                                                                CELLM_HIP_DTYPE_F32, 64, R, hid, inter, h, S),
+                        "residual + post_attention_layernorm + q4 gate/up");
             if (int32_t rc = run_proj(m, P[6], h, proj, R, hid, inter, "down_proj")) return rc;
         }
         LIB_TRY(cellm_hip_add_rms_norm(H, x, proj, m->final_norm, CELLM_HIP_DTYPE_F32, R, hid, eps, xn, S),
@@ -593,12 +611,15 @@ int32_t dev_create_impl(const cellm_llama_config_t* cfg, const HostModel& hm, in
         return CELLM_HIP_OK;
     };
     m->p.resize(L * 7);
-    bool all_i8 = true;
+    bool all_i8 = true, q4_fusable = true;
     for (size_t l = 0; l < L; ++l) {
         const std::string pre = "model.layers." + std::to_string(l) + ".";
         for (int j = 0; j < 7; ++j) {
             if ((rc = upload_proj(pre + kNames[j], hm.p[l * 7 + j], &m->p[l * 7 + j]))) return bail(rc);
             all_i8 = all_i8 && hm.p[l * 7 + j].kind == PK_I8 && !hm.p[l * 7 + j].bias_f16;
+            // q/k/v (j < 3) and gate/up (j = 4, 5) in the fused q4 launches; gate/up without biases
+            if (j != 3 && j != 6)
+                q4_fusable = q4_fusable && hm.p[l * 7 + j].kind == PK_Q4 && (j < 3 || !hm.p[l * 7 + j].bias_f16);
         }
         const float *a = nullptr, *b = nullptr;
         if (!hm.n1[l] || !hm.n2[l]) return bail(fail(CELLM_HIP_ERR_INVALID_ARG, "layer %zu norm missing", l));
@@ -638,6 +659,8 @@ int32_t dev_create_impl(const cellm_llama_config_t* cfg, const HostModel& hm, in
         if (e != hipSuccess) return bail(from_runtime(e, "upload rope table"));
     }
     m->fused = all_i8 && (c.hidden % 16) == 0 && c.hidden <= 4096 && c.head_dim % 2 == 0;
+    m->fused_q4 = !m->fused && q4_fusable && (c.hidden % 32) == 0 && c.hidden >= 64 && c.hidden <= 4096 &&
+                  c.head_dim % 2 == 0;
     auto align = [](size_t v) { return (v + 255) & ~(size_t)255; };
     m->io_tokens = 0;
     m->io_pos = align(R * 4);

@@ -443,6 +443,30 @@ class HipOps:
             self._h, _dev_ptr(x_prev), _dev_ptr(y), _dev_ptr(x_out), _dev_ptr(norm_w), eps, _dev_ptr(wg),
             _dev_ptr(sg), _dev_ptr(wu), _dev_ptr(su), rows, hidden, wg.shape[0], _dev_ptr(h), _stream_ptr(stream)))
 
+    def encode_decode_q4_qkv(self, x_prev, y, x_out, norm_w, eps: float, wq, sq, bq, biasq, wk, sk, bk, biask, wv, sv,
+                             bv, biasv, group: int, n_heads: int, n_kv_heads: int, head_dim: int, positions_i32,
+                             cos_sin, q_out, kcache, vcache, block_tables, total_blocks: int, n_layers: int,
+                             tokens_per_block: int, layer: int, stream=None) -> None:
+        """cellm_hip_decode_q4_affine_qkv_rope_kv: u32 weights, f32 scales/biases [out][hidden/group]."""
+        rows, hidden = positions_i32.numel(), norm_w.numel()
+        check(self._lib.cellm_hip_decode_q4_affine_qkv_rope_kv(
+            self._h, _dev_ptr(x_prev), _dev_ptr(y), _dev_ptr(x_out), _dev_ptr(norm_w), eps, _dev_ptr(wq),
+            _dev_ptr(sq), _dev_ptr(bq), _dev_ptr(biasq), _dev_ptr(wk), _dev_ptr(sk), _dev_ptr(bk), _dev_ptr(biask),
+            _dev_ptr(wv), _dev_ptr(sv), _dev_ptr(bv), _dev_ptr(biasv), _torch_dtype_code(sq), group, rows, hidden,
+            n_heads, n_kv_heads, head_dim, _dev_ptr(positions_i32), _dev_ptr(cos_sin), cos_sin.shape[0],
+            _dev_ptr(q_out), _dev_ptr(kcache), _dev_ptr(vcache), _dev_ptr(block_tables), block_tables.shape[-1],
+            total_blocks, n_layers, tokens_per_block, layer, _stream_ptr(stream)))
+
+    def encode_decode_q4_gate_up(self, x_prev, y, x_out, norm_w, eps: float, wg, sg, bg, wu, su, bu, group: int, h,
+                                 stream=None) -> None:
+        """cellm_hip_decode_q4_affine_gate_up_silu: u32 weights, f32 scales/biases [inter][hidden/group]."""
+        hidden = norm_w.numel()
+        rows = x_prev.numel() // hidden
+        check(self._lib.cellm_hip_decode_q4_affine_gate_up_silu(
+            self._h, _dev_ptr(x_prev), _dev_ptr(y), _dev_ptr(x_out), _dev_ptr(norm_w), eps, _dev_ptr(wg),
+            _dev_ptr(sg), _dev_ptr(bg), _dev_ptr(wu), _dev_ptr(su), _dev_ptr(bu), _torch_dtype_code(sg), group,
+            rows, hidden, wg.shape[0], _dev_ptr(h), _stream_ptr(stream)))
+
     def encode_rope_half(self, x, n_heads: int, head_dim: int, positions_i32, cos_sin, stream=None) -> None:
         rows = positions_i32.numel()
         check(self._lib.cellm_hip_rope_half_f32(self._h, _dev_ptr(x), rows, n_heads, head_dim,

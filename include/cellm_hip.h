@@ -432,6 +432,32 @@ int32_t cellm_hip_decode_gate_up_silu(cellm_hip_ctx_t* ctx, const float* x_prev,
                                       const int8_t* wu, const uint16_t* su, int64_t rows, int64_t hidden,
                                       int64_t inter, float* h, void* stream);
 
+/* The two entry points above for MLX 4-bit affine weights (the u32 layers of
+ * the Qwen2 decode step, qwen.rs:1355-1453: input_layernorm, the q/k/v
+ * projections with their biases, RoPE and the K/V write; then
+ * post_attention_layernorm, gate/up and SiLU * up).  Weights as in
+ * cellm_hip_qgemv_q4_affine_qkv / _gate_up_silu: u32 words [out][hidden / 8],
+ * scales and biases [out][hidden / group]; here f32 (sb_dtype
+ * CELLM_HIP_DTYPE_F32) with group a power of two >= 32.  biasq/biask/biasv are
+ * the f32 projection biases [out] or NULL; they are added to the row sums
+ * before RoPE (add_projection_bias_if_present, qwen.rs:1132-1139).  The dot
+ * runs in f32 over the normalised activations (no f16 rounding of x).  x_prev,
+ * y, x_out and norm_w 16-byte aligned; rows 1..4, hidden % 32 == 0 and
+ * <= 4096; otherwise CELLM_HIP_ERR_UNSUPPORTED (use the separate calls). */
+int32_t cellm_hip_decode_q4_affine_qkv_rope_kv(
+    cellm_hip_ctx_t* ctx, const float* x_prev, const float* y, float* x_out, const float* norm_w, float eps,
+    const uint32_t* wq, const void* sq, const void* bq, const float* biasq, const uint32_t* wk, const void* sk,
+    const void* bk, const float* biask, const uint32_t* wv, const void* sv, const void* bv, const float* biasv,
+    int32_t sb_dtype, int64_t group, int64_t rows, int64_t hidden, int64_t n_heads, int64_t n_kv_heads,
+    int64_t head_dim, const int32_t* positions, const float* cos_sin, int64_t table_positions, float* q_out,
+    uint16_t* kcache, uint16_t* vcache, const uint32_t* block_tables, int64_t max_blocks, int64_t total_blocks,
+    int64_t n_layers, int64_t tokens_per_block, int64_t layer, void* stream);
+int32_t cellm_hip_decode_q4_affine_gate_up_silu(cellm_hip_ctx_t* ctx, const float* x_prev, const float* y,
+                                                float* x_out, const float* norm_w, float eps, const uint32_t* wg,
+                                                const void* sg, const void* bg, const uint32_t* wu, const void* su,
+                                                const void* bu, int32_t sb_dtype, int64_t group, int64_t rows,
+                                                int64_t hidden, int64_t inter, float* h, void* stream);
+
 /* MetalKvStorage::encode_attention / attention_single_token_gqa_f32
  * (kvcache.rs:710-789, 1377-1439): each row attends over positions
  * 0..positions[r] of `layer`; q and out [rows][n_heads][head_dim] f32, query

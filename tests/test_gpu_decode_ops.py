@@ -480,6 +480,156 @@ def test_decode_gate_up_matches_separate_ops(ops, rows):
     assert rel_err(h2.cpu().numpy(), h.cpu().numpy()) <= 1e-5
 
 
+def _q4_mats(out_dims, k, seed, group=64):
+    """MLX q4 affine matrices with f32 group scales/biases (the u32 runners' layout)."""
+    ws, ss, bs = [], [], []
+    for j, n in enumerate(out_dims):
+        ws.append(oracle.gen_q4_words((n, k // 8), seed + 3 * j))
+        ss.append(oracle.gen_normal((n, k // group), seed + 3 * j + 1, 0.02, 0.005, positive_only=True))
+        bs.append(oracle.gen_normal((n, k // group), seed + 3 * j + 2, 0.0, 0.05))
+    return ws, ss, bs
+
+
+# hidden 896: Qwen2.5-0.5B (28 chunks per row, teams of 32 lanes); 256 (teams of 16);
+# 1536 (48 chunks, teams of 64, two float4 groups per thread in the prologue);
+# 2560 (80 chunks: two per lane, four float4 groups per thread)
+@pytest.mark.parametrize("H,nh,nkv,hd,rows,with_y,interleaved,bias", [
+    (896, 14, 2, 64, 4, True, False, True),
+    (896, 14, 2, 64, 1, False, False, True),
+    (896, 14, 2, 64, 3, True, True, False),
+    (256, 4, 2, 64, 2, True, False, True),
+    (1536, 12, 2, 128, 4, True, False, True),
+    (2560, 20, 4, 128, 4, True, False, False),
+    (2560, 20, 4, 128, 1, True, True, True),
+])
+def test_decode_q4_qkv_matches_separate_ops(ops, steplib, H, nh, nkv, hd, rows, with_y, interleaved, bias):
+    """cellm_hip_decode_q4_affine_qkv_rope_kv against add_rms_norm + the q4 QKV
+    GEMV (f32 x) + rope_kv_write, and its q against the oracle (RMSNorm, the q4
+    affine GEMV, the projection bias and rotate-half/interleaved RoPE): the
+    residual exactly, q within 1e-5, written K/V within f16 rounding, no other
+    cache element touched."""
+    ops.set_rope_interleaved(interleaved)
+    try:
+        _decode_q4_qkv_case(ops, steplib, H, nh, nkv, hd, rows, with_y, interleaved, bias)
+    finally:
+        ops.set_rope_interleaved(False)
+
+
+def _decode_q4_qkv_case(ops, steplib, H, nh, nkv, hd, rows, with_y, interleaved, bias):
+    L, tpb, layer, theta = 3, 16, 1, 1000000.0
+    kvd = nkv * hd
+    total, k0, v0, bt = paged_setup(L, tpb, nkv, hd, rows, 8, 0xD0000500)
+    pos = np.array([127, 0, 64, 17][:rows], np.int32)
+    table = rope_table(steplib, theta, hd, 8 * tpb)
+    xp = np.stack([oracle.gen_normal((H,), 0xD0000510 + r, 0.0, 1.0) for r in range(rows)]).astype(np.float32)
+    y = np.stack([oracle.gen_normal((H,), 0xD0000520 + r, 0.0, 0.5) for r in range(rows)]).astype(np.float32)
+    nw = (1.0 + 0.1 * oracle.lcg_fill(H, 0xD0000530, 1.0)).astype(np.float32)
+    (wq, wk, wv), (sq, sk, sv), (bq, bk, bv) = _q4_mats([nh * hd, kvd, kvd], H, 0xD0000540)
+    pb = [oracle.gen_normal((n,), 0xD0000550 + j, 0.0, 0.3).astype(np.float32) if bias else None
+          for j, n in enumerate((nh * hd, kvd, kvd))]
+    d = [dev(a) for a in (wq, sq, bq, wk, sk, bk, wv, sv, bv)]
+    dpb = [dev(b) if b is not None else None for b in pb]
+    # separate ops
+    x_sep = dev(xp.copy())
+    xn = torch.empty((rows, H), dtype=torch.float32, device="cuda")
+    if with_y:
+        ops.encode_add_rms_norm(x_sep, dev(y), dev(nw), xn, 1e-6)
+    else:
+        ops.encode_rms_norm(x_sep, dev(nw), xn, 1e-6)
+    q = torch.empty((rows, nh * hd), dtype=torch.float32, device="cuda")
+    k = torch.empty((rows, kvd), dtype=torch.float32, device="cuda")
+    v = torch.empty((rows, kvd), dtype=torch.float32, device="cuda")
+    ops.encode_qkv_q4_affine(*d, xn, q, k, v, biasq=dpb[0], biask=dpb[1], biasv=dpb[2])
+    kc1, vc1 = dev(k0.copy()), dev(v0.copy())
+    ops.encode_rope_kv_write(q, k, v, nh, nkv, hd, dev(pos), dev(table), kc1, vc1, dev(bt), total, L, tpb, layer)
+    # fused
+    x_out = torch.full((rows, H), np.nan, dtype=torch.float32, device="cuda")
+    q2 = torch.full_like(q, np.nan)
+    kc2, vc2 = dev(k0.copy()), dev(v0.copy())
+    ops.encode_decode_q4_qkv(dev(xp), dev(y) if with_y else None, x_out, dev(nw), 1e-6, d[0], d[1], d[2], dpb[0],
+                             d[3], d[4], d[5], dpb[1], d[6], d[7], d[8], dpb[2], 64, nh, nkv, hd, dev(pos),
+                             dev(table), q2, kc2, vc2, dev(bt), total, L, tpb, layer)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(x_out.cpu().numpy(), x_sep.cpu().numpy())
+    assert rel_err(q2.cpu().numpy(), q.cpu().numpy()) <= 1e-5
+    # q against the oracle: x_prev + y, RMSNorm, the affine GEMV in the reference order, bias, RoPE
+    xr = xp + y if with_y else xp
+    q_ref = np.empty((rows, nh * hd), np.float32)
+    for r in range(rows):
+        xn_r = oracle.rms_norm(xr[r], nw, 1e-6)
+        qr = oracle.qgemv_q4_affine(wq, sq, bq, xn_r, H)[0]
+        if bias:
+            qr = (qr + pb[0]).astype(np.float32)
+        qr = np.ascontiguousarray(qr)
+        (oracle.rope_interleaved_ if interleaved else oracle.rope_half_)(qr, nh, hd, int(pos[r]), theta)
+        q_ref[r] = qr
+    assert rel_err(q2.cpu().numpy(), q_ref) <= 2e-5
+    for got, ref, init in ((kc2, kc1, k0), (vc2, vc1, v0)):
+        g = got.cpu().numpy().view(np.uint16)
+        r = ref.cpu().numpy().view(np.uint16)
+        changed = r != init
+        assert changed.sum() > 0
+        np.testing.assert_array_equal(g[~changed], init[~changed])
+        gf, rf = oracle.f16_bits_to_f32(g[changed]), oracle.f16_bits_to_f32(r[changed])
+        assert np.max(np.abs(gf - rf)) <= 2e-3 * np.max(np.abs(rf))
+
+
+@pytest.mark.parametrize("H,N,rows,with_y", [(896, 4864, 4, True), (896, 4864, 1, True), (896, 4864, 2, False),
+                                             (256, 704, 3, True), (1536, 8960, 4, True), (2560, 1000, 4, True)])
+def test_decode_q4_gate_up_matches_separate_ops(ops, H, N, rows, with_y):
+    """cellm_hip_decode_q4_affine_gate_up_silu against add_rms_norm + the q4
+    gate/up+SiLU GEMV (f32 x), and h against the oracle (RMSNorm, two q4 affine
+    GEMVs, silu * up): the residual exactly, h within 1e-5 / 2e-5."""
+    xp = np.stack([oracle.gen_normal((H,), 0xD0000600 + r, 0.0, 1.0) for r in range(rows)]).astype(np.float32)
+    y = np.stack([oracle.gen_normal((H,), 0xD0000610 + r, 0.0, 0.5) for r in range(rows)]).astype(np.float32)
+    nw = (1.0 + 0.1 * oracle.lcg_fill(H, 0xD0000620, 1.0)).astype(np.float32)
+    (wg, wu), (sg, su), (bg, bu) = _q4_mats([N, N], H, 0xD0000630)
+    d = [dev(a) for a in (wg, sg, bg, wu, su, bu)]
+    x_sep = dev(xp.copy())
+    xn = torch.empty((rows, H), dtype=torch.float32, device="cuda")
+    if with_y:
+        ops.encode_add_rms_norm(x_sep, dev(y), dev(nw), xn, 1e-6)
+    else:
+        ops.encode_rms_norm(x_sep, dev(nw), xn, 1e-6)
+    h = torch.empty((rows, N), dtype=torch.float32, device="cuda")
+    ops.encode_gate_up_silu_q4_affine(*d, xn, h)
+    x_out = torch.full((rows, H), np.nan, dtype=torch.float32, device="cuda")
+    h2 = torch.full_like(h, np.nan)
+    ops.encode_decode_q4_gate_up(dev(xp), dev(y) if with_y else None, x_out, dev(nw), 1e-6, *d, 64, h2)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(x_out.cpu().numpy(), x_sep.cpu().numpy())
+    assert rel_err(h2.cpu().numpy(), h.cpu().numpy()) <= 1e-5
+    xr = xp + y if with_y else xp
+    xn_ref = np.stack([oracle.rms_norm(xr[r], nw, 1e-6) for r in range(rows)])
+    g = oracle.qgemv_q4_affine(wg, sg, bg, xn_ref, H)
+    u = oracle.qgemv_q4_affine(wu, su, bu, xn_ref, H)
+    h_ref = oracle.silu_mul_(np.ascontiguousarray(g), u)
+    assert rel_err(h2.cpu().numpy(), h_ref) <= 2e-5
+
+
+def test_decode_q4_fused_rejects_unsupported(ops):
+    from cellm_amd._lib import CellmHipError
+
+    H, N = 896, 64
+    x = torch.zeros((1, H), dtype=torch.float32, device="cuda")
+    nw = torch.ones(H, dtype=torch.float32, device="cuda")
+    w = torch.zeros((N, H // 8), dtype=torch.int32, device="cuda")
+    s = torch.ones((N, H // 64), dtype=torch.float32, device="cuda")
+    h = torch.zeros((1, N), dtype=torch.float32, device="cuda")
+    with pytest.raises(CellmHipError, match="alias"):
+        ops.encode_decode_q4_gate_up(x, None, x, nw, 1e-5, w, s, s, w, s, s, 64, h)
+    with pytest.raises(CellmHipError, match="f32"):
+        ops.encode_decode_q4_gate_up(x, None, x.clone(), nw, 1e-5, w, s.half(), s.half(), w, s.half(), s.half(), 64, h)
+    with pytest.raises(CellmHipError, match="power-of-two"):
+        ops.encode_decode_q4_gate_up(x, None, x.clone(), nw, 1e-5, w, s, s, w, s, s, 96, h)
+    xb = torch.zeros((1, 4128), dtype=torch.float32, device="cuda")
+    wb = torch.zeros((N, 4128 // 8), dtype=torch.int32, device="cuda")
+    sb = torch.ones((N, 4128 // 32), dtype=torch.float32, device="cuda")
+    with pytest.raises(CellmHipError, match="4096"):
+        ops.encode_decode_q4_gate_up(xb, None, xb.clone(), torch.ones(4128, dtype=torch.float32, device="cuda"), 1e-5,
+                                     wb, sb, sb, wb, sb, sb, 32, h)
+
+
 def test_decode_fused_rejects_aliasing_and_unsupported(ops):
     from cellm_amd._lib import CellmHipError
 
