@@ -301,6 +301,15 @@ int32_t qgemv_q4_impl(cellm_hip_ctx* ctx, const uint32_t* wq, const void* scales
                 "qgemv_q4_f32x_mfma launch");
         return CELLM_HIP_OK;
     }
+    // f32 x at m <= 4 with f32 scales and biases (the u32 runners' o_proj and down_proj): x copied to
+    // LDS as f32 once per block, an f32 dot (the hi + lo f16 kernels stage and dot x twice)
+    if (!force_gemm && xdt == DT_F32 && sbt == DT_F32 && aligned16(wq) && aligned16(x) &&
+        qgemv_q4_x32_supported((int)m, (int)n, (int)k, (int)group)) {
+        HIP_TRY(launch_qgemv_q4_x32(wq, static_cast<const float*>(scales), static_cast<const float*>(biases),
+                                    static_cast<const float*>(x), y, (int)m, (int)n, (int)k, (int)group, st),
+                "qgemv_q4_x32 launch");
+        return CELLM_HIP_OK;
+    }
     // 2..64 activation rows: f16 MFMA tiles dequantized in registers; at m <= 4
     // only for long outputs (else the f32-accumulating VALU GEMV is faster)
     if (!force_gemm && (m > 4 || n >= kMfmaMinRows) && gemm_ok &&

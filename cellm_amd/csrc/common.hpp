@@ -150,6 +150,68 @@ __device__ __forceinline__ float group_max(float v)
     if constexpr (W >= 2) v = fmaxf(v, lane_xor<1>(v, W));
     return v;
 }
+// Sums of V values over aligned teams of W lanes, transposed (V <= W, both powers
+// of two): log2(V) halving steps, each at offset O = W/2, W/4, ..., leave every
+// lane with one value, and plain butterfly steps finish the sum over the team.
+// In a halving step a lane keeps the low half of its values when its lane bit O
+// is clear and the high half when set, adding the partner's copy of that half:
+// one lane swap per pair of values at O = 16 and 32 (the swap hands each side
+// the half it keeps), two DPP adds and a select below.  Lane l ends with the
+// team total of value index  sum_s bit(l, W >> (s + 1)) * V / 2^(s + 1)
+// (team_sum_t_index), against one full butterfly per value otherwise.
+template <int O>
+__device__ __forceinline__ float half_step(float lo, float hi)
+{
+    if constexpr (O >= 16) {
+        const int a = __builtin_bit_cast(int, lo), b = __builtin_bit_cast(int, hi);
+        const auto r = O == 32 ? __builtin_amdgcn_permlane32_swap(a, b, false, false)
+                               : __builtin_amdgcn_permlane16_swap(a, b, false, false);
+        // ROCm 7.2's compiler folds r[0] + r[1] of one lane swap into r[0] + r[0] (checked in
+        // the gfx950 assembly); an empty asm on both results keeps them apart
+        uint32_t x = r[0], y = r[1];
+        asm("" : "+v"(x), "+v"(y));
+        return __builtin_bit_cast(float, x) + __builtin_bit_cast(float, y);
+    } else {
+        float l, h;
+        if constexpr (O == 8 || O == 4) {
+            l = lo + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, lo), 0x100 + O,
+                                                                          0xF, 0xF, false));  // lane + O
+            h = hi + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, hi), 0x110 + O,
+                                                                          0xF, 0xF, false));  // lane - O
+        } else if constexpr (O == 2) {
+            l = lo + dpp_xor2(lo);
+            h = hi + dpp_xor2(hi);
+        } else {
+            l = lo + dpp_xor1(lo);
+            h = hi + dpp_xor1(hi);
+        }
+        return (threadIdx.x & O) ? h : l;
+    }
+}
+template <int W, int V>
+__device__ __forceinline__ float team_sum_t(const float (&a)[V])
+{
+    static_assert(V >= 1 && V <= W && (V & (V - 1)) == 0 && (W & (W - 1)) == 0, "V <= W, powers of two");
+    if constexpr (V == 1) {
+        return group_sum<W>(a[0]);
+    } else {
+        float b[V / 2];
+#pragma unroll
+        for (int i = 0; i < V / 2; ++i) b[i] = half_step<W / 2>(a[i], a[V / 2 + i]);
+        return team_sum_t<W / 2, V / 2>(b);
+    }
+}
+// The value index team_sum_t<W, V> leaves in lane `lane` (lanes of one team that
+// differ only below bit W / V hold the same total).
+template <int W, int V>
+__device__ __forceinline__ int team_sum_t_index(int lane)
+{
+    int idx = 0;
+#pragma unroll
+    for (int o = W / 2, v = V / 2; v >= 1; o >>= 1, v >>= 1) idx += (lane & o) ? v : 0;
+    return idx;
+}
+
 // Raw buffer resource over [base, base + bytes), bytes < 2^31.  A buffer store whose byte
 // offset falls outside it is dropped by the hardware, so a masked store is one instruction
 // with an out-of-range offset (kBufferDrop) in the lanes that must not write -- no branch,

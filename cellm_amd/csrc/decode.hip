@@ -741,44 +741,57 @@ __global__ __launch_bounds__(kAttnBlockThreads) void attn_head_kernel(
 
 __host__ __device__ __forceinline__ int xpad(int k) { return k + (k >> 4) * 4; }
 
-// x rows [rows][H] -> LDS xs[MT][xpad(H)] = rms_norm(x_prev + y) * w; block 0
-// writes x_prev + y to x_out (HASY false: x_prev as is).  Thread t handles the
-// float4 groups t, t + 256, ... (KR of them: KR * 1024 >= H); its sum of
-// squares runs over its groups in order, then the same wave and block tree as
-// add_rms_norm_kernel.  CSUM (H % 32 == 0): also the sums of the normalised
-// values over each 32-element chunk, xsum[m][H / 32] (the eight groups of a
-// chunk sit in eight adjacent lanes).
-template <int MT, int KR, bool HASY, bool CSUM = false>
-__device__ __forceinline__ void stage_add_norm(const float* __restrict__ x_prev, const float* __restrict__ y,
-                                               float* __restrict__ x_out, const float* __restrict__ w, int rows,
-                                               int H, float eps, float* xs, float (*red)[MT], float* xsum = nullptr)
-{
-    const int t = threadIdx.x;
-    const int xst = xpad(H), H4 = H >> 2;
-    // every load first (addresses clamped in range, no branch between them), then the adds
+// The prologue's inputs: thread t's float4 groups t, t + 256, ... (KR of them:
+// KR * 1024 >= H) of every row of x_prev (and y) and of the norm weights.
+// Loaded first (addresses clamped in range, no branch between them), before
+// the weights of the kernel's dot: loads retire in issue order, so the
+// prologue then waits for these alone and runs while the weights are in flight.
+template <int MT, int KR>
+struct NormIn {
     f4_t v[MT][KR], yv[MT][KR], wv[KR];
+};
+
+template <int MT, int KR, bool HASY>
+__device__ __forceinline__ void load_add_norm(const float* __restrict__ x_prev, const float* __restrict__ y,
+                                              const float* __restrict__ w, int rows, int H, NormIn<MT, KR>& in)
+{
+    const int t = threadIdx.x, H4 = H >> 2;
 #pragma unroll
     for (int u = 0; u < KR; ++u) {
         const int g = min(t + u * kNormThreads, H4 - 1);
-        wv[u] = reinterpret_cast<const f4_t*>(w)[g];
+        in.wv[u] = reinterpret_cast<const f4_t*>(w)[g];
 #pragma unroll
         for (int m = 0; m < MT; ++m) {
             const int mm = min(m, rows - 1);
-            v[m][u] = reinterpret_cast<const f4_t*>(x_prev + (size_t)mm * H)[g];
-            if constexpr (HASY) yv[m][u] = reinterpret_cast<const f4_t*>(y + (size_t)mm * H)[g];
+            in.v[m][u] = reinterpret_cast<const f4_t*>(x_prev + (size_t)mm * H)[g];
+            if constexpr (HASY) in.yv[m][u] = reinterpret_cast<const f4_t*>(y + (size_t)mm * H)[g];
         }
     }
+}
+
+// x rows [rows][H] -> LDS xs[MT][xpad(H)] = rms_norm(x_prev + y) * w from the
+// loads of load_add_norm; block 0 writes x_prev + y to x_out (HASY false:
+// x_prev as is).  Each thread's sum of squares runs over its groups in order,
+// then the same wave and block tree as add_rms_norm_kernel.  CSUM
+// (H % 32 == 0): also the sums of the normalised values over each 32-element
+// chunk, xsum[m][H / 32] (the eight groups of a chunk sit in eight adjacent lanes).
+template <int MT, int KR, bool HASY, bool CSUM = false>
+__device__ __forceinline__ void stage_add_norm(NormIn<MT, KR>& in, float* __restrict__ x_out, int rows, int H,
+                                               float eps, float* xs, float (*red)[MT], float* xsum = nullptr)
+{
+    const int t = threadIdx.x;
+    const int xst = xpad(H), H4 = H >> 2;
+    auto& v = in.v;
     if constexpr (HASY) {
 #pragma unroll
         for (int m = 0; m < MT; ++m)
 #pragma unroll
             for (int u = 0; u < KR; ++u)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) v[m][u][e] = v[m][u][e] + yv[m][u][e];
+                for (int e = 0; e < 4; ++e) v[m][u][e] = v[m][u][e] + in.yv[m][u][e];
     }
-    // the rows' sums of squares, then their wave reductions interleaved (a store
-    // between them, as block 0's residual write once was, serialises the rows'
-    // shuffle chains)
+    // the rows' sums of squares (padding rows m >= rows sum nothing), reduced over the
+    // wave transposed (lane l ends with row team_sum_t_index<64, MT>(l)), then over the waves
     float s[MT];
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
@@ -792,11 +805,9 @@ __device__ __forceinline__ void stage_add_norm(const float* __restrict__ x_prev,
             }
         }
     }
-#pragma unroll
-    for (int m = 0; m < MT; ++m) s[m] = group_sum<64>(s[m]);
-    if ((t & 63) == 0) {
-#pragma unroll
-        for (int m = 0; m < MT; ++m) red[t >> 6][m] = s[m];
+    {
+        const float sw = team_sum_t<64, MT>(s);
+        if ((t & (64 / MT - 1)) == 0) red[t >> 6][team_sum_t_index<64, MT>(t & 63)] = sw;
     }
     if (blockIdx.x == 0) {
 #pragma unroll
@@ -808,26 +819,35 @@ __device__ __forceinline__ void stage_add_norm(const float* __restrict__ x_prev,
             }
     }
     __syncthreads();
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-        if (m >= rows) break;
+    // lane m of every wave computes row m's 1 / rms; every lane reads the MT values back
+    float inv[MT];
+    {
         float tot = 0.0f;
 #pragma unroll
-        for (int i = 0; i < kNormThreads / 64; ++i) tot = tot + red[i][m];
+        for (int i = 0; i < kNormThreads / 64; ++i) tot = tot + red[i][t & (MT - 1)];
         const float mean = tot / (float)H;
-        const float inv = 1.0f / sqrtf(mean + eps);
+        const float il = 1.0f / sqrtf(mean + eps);
 #pragma unroll
-        for (int u = 0; u < KR; ++u) {
-            const int g = t + u * kNormThreads;
+        for (int m = 0; m < MT; ++m)
+            inv[m] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, il), m));
+    }
+#pragma unroll
+    for (int u = 0; u < KR; ++u) {
+        const int g = t + u * kNormThreads;
+        float cs[MT];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
             f4_t o;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = v[m][u][e] * inv * wv[u][e];
+            for (int e = 0; e < 4; ++e) o[e] = v[m][u][e] * inv[m] * in.wv[u][e];
             if (g < H4) *reinterpret_cast<f4_t*>(xs + m * xst + xpad(4 * g)) = o;  // a group never straddles padding
-            if constexpr (CSUM) {
-                // H4 % 8 == 0: the eight groups of a chunk are all in range or all out
-                const float cs = group_sum<8>((o[0] + o[1]) + (o[2] + o[3]));
-                if (g < H4 && (t & 7) == 0) xsum[m * (H >> 5) + (g >> 3)] = cs;
-            }
+            cs[m] = (o[0] + o[1]) + (o[2] + o[3]);
+        }
+        if constexpr (CSUM) {
+            // H4 % 8 == 0: the eight groups of a chunk are all in range or all out; the MT chunk
+            // sums reduced over the eight lanes transposed (MT <= 8)
+            const float c = team_sum_t<8, MT>(cs);
+            if (g < H4 && (t & (8 / MT - 1)) == 0) xsum[team_sum_t_index<8, MT>(t & 7) * (H >> 5) + (g >> 3)] = c;
         }
     }
     __syncthreads();
@@ -916,11 +936,13 @@ __global__ __launch_bounds__(256) void decode_qkv_kernel(DecodeQkvArgs a)
     const int r0 = head * a.head_dim + i0, r1 = head * a.head_dim + i1;
     const int8_t* wm = which == 0 ? a.w[0] : (which == 1 ? a.w[1] : a.w[2]);
     const uint16_t* sm = which == 0 ? a.s[0] : (which == 1 ? a.s[1] : a.s[2]);
+    NormIn<MT, KR> nin;
+    load_add_norm<MT, KR, HASY>(a.x_prev, a.y, a.norm_w, a.rows, H, nin);
     u4_t w0[C], w1[C];
     load_rows_i8<C>(wm + (size_t)r0 * H, wm + (size_t)r1 * H, lane, LPR, nchunk, w0, w1);
     const float s0 = h2f(sm[r0]), s1 = h2f(sm[r1]);
 
-    stage_add_norm<MT, KR, HASY>(a.x_prev, a.y, a.x_out, a.norm_w, a.rows, H, a.eps, xs, red);
+    stage_add_norm<MT, KR, HASY>(nin, a.x_out, a.rows, H, a.eps, xs, red);
 
     float acc0[MT], acc1[MT];
 #pragma unroll
@@ -983,11 +1005,13 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(DecodeGateUpArgs a)
     const int team = threadIdx.x / LPR, lane = threadIdx.x % LPR;
     const int n_raw = blockIdx.x * (256 / LPR) + team;
     const int n = min(n_raw, a.N - 1);
+    NormIn<MT, KR> nin;
+    load_add_norm<MT, KR, HASY>(a.x_prev, a.y, a.norm_w, a.rows, H, nin);
     u4_t w0[C], w1[C];
     load_rows_i8<C>(a.wg + (size_t)n * H, a.wu + (size_t)n * H, lane, LPR, nchunk, w0, w1);
     const float sg = h2f(a.sg[n]), su = h2f(a.su[n]);
 
-    stage_add_norm<MT, KR, HASY>(a.x_prev, a.y, a.x_out, a.norm_w, a.rows, H, a.eps, xs, red);
+    stage_add_norm<MT, KR, HASY>(nin, a.x_out, a.rows, H, a.eps, xs, red);
 
     float acc0[MT], acc1[MT];
 #pragma unroll
@@ -1012,81 +1036,18 @@ __global__ __launch_bounds__(256) void decode_gate_up_kernel(DecodeGateUpArgs a)
 // The q4 counterparts of the two kernels above, for the u32 runners (the Qwen2
 // step, qwen.rs:1255-1470, whose projections are linear_i4_out_in,
 // lfm.rs:985-1066, over f32 activations).  Same prologue (stage_add_norm, with
-// the 32-element chunk sums of xn) and team layout (LPR lanes, two output rows,
-// C 16-byte chunks of each per lane, loaded before the prologue).  A chunk is
-// 32 nibbles of one row: four u32 words, element 8j + e = nibble e of word j.
-// The dot is plain f32: the nibbles widened by v_cvt_f32_ubyteN meet xn in FMA
+// the 32-element chunk sums of xn).  A team of LPR lanes owns RP units of two
+// output rows (a RoPE pair, or row n of gate and of up); each lane holds C
+// 16-byte chunks of every row, loaded before the prologue.  A chunk is 32
+// nibbles of one row: four u32 words, element 8j + e = nibble e of word j.  The
+// dot is plain f32: the nibbles widened by v_cvt_f32_ubyteN meet xn in FMA
 // chains, and one group scale and bias cover the whole chunk (group >= 32):
 //   y[n] = sum_c ( S[n][g(c)] * sum_{k in c} q[n][k] xn[k] + B[n][g(c)] * xsum[c] )
-// which is sum_k (q S + B) xn in another summation order.
-
-// This lane's C chunks of two rows (w0/w1: row starts in 16-byte chunks; g0/g1:
-// the rows' first scale/bias index), chunk index clamped; f32 scales and biases.
-template <int C>
-__device__ __forceinline__ void load_rows_q4(const u4_t* __restrict__ w0, const float* __restrict__ S0,
-                                             const float* __restrict__ B0, size_t g0, const u4_t* __restrict__ w1,
-                                             const float* __restrict__ S1, const float* __restrict__ B1, size_t g1,
-                                             int lane, int LPR, int cpr, int gshift, u4_t (&a)[C], u4_t (&b)[C],
-                                             float (&sb)[C][4])
-{
-#pragma unroll
-    for (int c = 0; c < C; ++c) {
-        const int ch = min(lane + c * LPR, cpr - 1);
-        const int gi = (ch << 5) >> gshift;
-        a[c] = __builtin_nontemporal_load(w0 + ch);
-        b[c] = __builtin_nontemporal_load(w1 + ch);
-        sb[c][0] = S0[g0 + gi];
-        sb[c][1] = B0[g0 + gi];
-        sb[c][2] = S1[g1 + gi];
-        sb[c][3] = B1[g1 + gi];
-    }
-}
-
-// acc0/acc1[m] += this lane's chunks of rows 0/1 against xn[m] (xs: stage_add_norm's layout)
-template <int MT, int C>
-__device__ __forceinline__ void dot_rows_q4(const u4_t (&a)[C], const u4_t (&b)[C], const float (&sb)[C][4], int lane,
-                                            int LPR, int cpr, const float* xs, int xst, const float* xsum, int rows,
-                                            float (&acc0)[MT], float (&acc1)[MT])
-{
-#pragma unroll
-    for (int c = 0; c < C; ++c) {
-        const int ch = lane + c * LPR;
-        if (ch >= cpr) break;
-        float d0[MT], d1[MT];
-#pragma unroll
-        for (int m = 0; m < MT; ++m) d0[m] = d1[m] = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t alo = a[c][j] & 0x0F0F0F0Fu, ahi = (a[c][j] >> 4) & 0x0F0F0F0Fu;
-            const uint32_t blo = b[c][j] & 0x0F0F0F0Fu, bhi = (b[c][j] >> 4) & 0x0F0F0F0Fu;
-            const float qa[8] = {cvt_ubyte<0>(alo), cvt_ubyte<0>(ahi), cvt_ubyte<1>(alo), cvt_ubyte<1>(ahi),
-                                 cvt_ubyte<2>(alo), cvt_ubyte<2>(ahi), cvt_ubyte<3>(alo), cvt_ubyte<3>(ahi)};
-            const float qb[8] = {cvt_ubyte<0>(blo), cvt_ubyte<0>(bhi), cvt_ubyte<1>(blo), cvt_ubyte<1>(bhi),
-                                 cvt_ubyte<2>(blo), cvt_ubyte<2>(bhi), cvt_ubyte<3>(blo), cvt_ubyte<3>(bhi)};
-            // elements 32 ch + 8 j + 0..7 sit at xpad(...) = 40 ch + 8 j + (j >= 2 ? 4 : 0) + 0..7
-            const int xo = 40 * ch + 8 * j + (j >= 2 ? 4 : 0);
-#pragma unroll
-            for (int m = 0; m < MT; ++m) {
-                if (m >= rows) break;
-                const f4_t* xp = reinterpret_cast<const f4_t*>(xs + m * xst + xo);
-                const f4_t x0 = xp[0], x1 = xp[1];
-                const float xv[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    d0[m] = __builtin_fmaf(qa[e], xv[e], d0[m]);
-                    d1[m] = __builtin_fmaf(qb[e], xv[e], d1[m]);
-                }
-            }
-        }
-#pragma unroll
-        for (int m = 0; m < MT; ++m) {
-            if (m >= rows) break;
-            const float xc = xsum[m * cpr + ch];
-            acc0[m] += sb[c][0] * d0[m] + sb[c][1] * xc;
-            acc1[m] += sb[c][2] * d1[m] + sb[c][3] * xc;
-        }
-    }
-}
+// which is sum_k (q S + B) xn in another summation order.  All MT activation
+// rows are computed (padding rows repeat the last one and are never stored), so
+// the dot has no per-row branch.  The RP * 2 * MT row sums of a lane are summed
+// over the team transposed (team_sum_t); a lane then pairs the two rows of its
+// (unit, session) value and runs the epilogue once.
 
 struct DecodeQ4QkvArgs {
     const float* x_prev;
@@ -1110,77 +1071,6 @@ struct DecodeQ4QkvArgs {
     int il;
 };
 
-// Team -> one RoPE pair (rows i0, i1 of a q, k or v head), as decode_qkv_kernel;
-// the projection bias is added to the row sums before the rotation
-// (add_projection_bias_if_present, qwen.rs:1132-1139, then RoPE).
-template <int LPR, int C, int MT, int KR, bool HASY>
-__global__ __launch_bounds__(256) void decode_q4_qkv_kernel(DecodeQ4QkvArgs a)
-{
-    extern __shared__ __align__(16) float xs[];
-    __shared__ float red[kNormThreads / 64][MT];
-    const int H = a.H, half = a.head_dim >> 1, cpr = H >> 5;
-    const int gpr = (H + (1 << a.gshift) - 1) >> a.gshift;
-    const int team = threadIdx.x / LPR, lane = threadIdx.x % LPR;
-    const int pairs = (a.n_heads + 2 * a.n_kv_heads) * half;
-    const int p_raw = blockIdx.x * (256 / LPR) + team;
-    const int p = min(p_raw, pairs - 1);
-    const int hh = p / half, i = p - hh * half;
-    const int which = hh < a.n_heads ? 0 : (hh < a.n_heads + a.n_kv_heads ? 1 : 2);
-    const int head = which == 0 ? hh : (which == 1 ? hh - a.n_heads : hh - a.n_heads - a.n_kv_heads);
-    const int i0 = rope_lo(i, half, a.il), i1 = rope_hi(i, half, a.il);
-    const int r0 = head * a.head_dim + i0, r1 = head * a.head_dim + i1;
-    const u4_t* wm = which == 0 ? a.w[0] : (which == 1 ? a.w[1] : a.w[2]);
-    const float* sm = which == 0 ? a.s[0] : (which == 1 ? a.s[1] : a.s[2]);
-    const float* bm = which == 0 ? a.b[0] : (which == 1 ? a.b[1] : a.b[2]);
-    u4_t w0[C], w1[C];
-    float sb[C][4];
-    load_rows_q4<C>(wm + (size_t)r0 * cpr, sm, bm, (size_t)r0 * gpr, wm + (size_t)r1 * cpr, sm, bm,
-                    (size_t)r1 * gpr, lane, LPR, cpr, a.gshift, w0, w1, sb);
-
-    float* xsum = xs + MT * xpad(H);
-    stage_add_norm<MT, KR, HASY, true>(a.x_prev, a.y, a.x_out, a.norm_w, a.rows, H, a.eps, xs, red, xsum);
-
-    float acc0[MT], acc1[MT];
-#pragma unroll
-    for (int m = 0; m < MT; ++m) acc0[m] = acc1[m] = 0.0f;
-    dot_rows_q4<MT, C>(w0, w1, sb, lane, LPR, cpr, xs, xpad(H), xsum, a.rows, acc0, acc1);
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-        acc0[m] = group_sum<LPR>(acc0[m]);
-        acc1[m] = group_sum<LPR>(acc1[m]);
-    }
-    if (p_raw >= pairs) return;
-    const float* pb = which == 0 ? a.bias[0] : (which == 1 ? a.bias[1] : a.bias[2]);
-    // lane m writes session m: y (+ bias), then RoPE and the cache write as decode_qkv_kernel
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-        if (m != lane || m >= a.rows) continue;
-        float v0 = acc0[m], v1 = acc1[m];
-        if (pb) {
-            v0 = v0 + pb[r0];
-            v1 = v1 + pb[r1];
-        }
-        const int pr = a.pos[m];
-        const float2 c = a.cs[(size_t)min(max(pr, 0), a.table_positions - 1) * half + i];
-        if (which == 0) {
-            float* q = a.q_out + ((size_t)m * a.n_heads + head) * a.head_dim;
-            q[i0] = v0 * c.x - v1 * c.y;
-            q[i1] = v1 * c.x + v0 * c.y;
-            continue;
-        }
-        const long long b = pr >= 0 ? a.kv.base(m, pr, a.layer) : -1;
-        if (b < 0) continue;
-        const size_t e = (size_t)b + (size_t)head * a.head_dim;
-        if (which == 1) {
-            a.kc[e + i0] = __builtin_bit_cast(uint16_t, (_Float16)(v0 * c.x - v1 * c.y));
-            a.kc[e + i1] = __builtin_bit_cast(uint16_t, (_Float16)(v1 * c.x + v0 * c.y));
-        } else {
-            a.vc[e + i0] = __builtin_bit_cast(uint16_t, (_Float16)v0);
-            a.vc[e + i1] = __builtin_bit_cast(uint16_t, (_Float16)v1);
-        }
-    }
-}
-
 struct DecodeQ4GateUpArgs {
     const float* x_prev;
     const float* y;
@@ -1197,62 +1087,347 @@ struct DecodeQ4GateUpArgs {
     float* h;  // [rows][N]
 };
 
-// Team -> row n of gate and of up; h = act_mul(act, g, u).
-template <int LPR, int C, int MT, int KR, bool HASY>
-__global__ __launch_bounds__(256) void decode_q4_gate_up_kernel(DecodeQ4GateUpArgs a)
+// Unit -> its two rows.  QKV: pair p < units of (q heads, k heads, v heads) x
+// head_dim / 2, rows i0 and i1 of one head (rope_lo / rope_hi).  Gate/up: row
+// n of each matrix.
+struct Q4Unit {
+    const u4_t* w0;
+    const u4_t* w1;
+    const float* s0;
+    const float* b0;
+    const float* s1;
+    const float* b1;
+    size_t g0, g1;  // first scale/bias index of each row
+    int which, head, i, i0, i1, r0, r1;
+};
+
+__device__ __forceinline__ Q4Unit q4_unit(const DecodeQ4QkvArgs& a, int p, int cpr, int gpr)
 {
+    Q4Unit u;
+    const int half = a.head_dim >> 1;
+    const int hh = p / half;
+    u.i = p - hh * half;
+    u.which = hh < a.n_heads ? 0 : (hh < a.n_heads + a.n_kv_heads ? 1 : 2);
+    u.head = u.which == 0 ? hh : (u.which == 1 ? hh - a.n_heads : hh - a.n_heads - a.n_kv_heads);
+    u.i0 = rope_lo(u.i, half, a.il);
+    u.i1 = rope_hi(u.i, half, a.il);
+    u.r0 = u.head * a.head_dim + u.i0;
+    u.r1 = u.head * a.head_dim + u.i1;
+    const u4_t* wm = u.which == 0 ? a.w[0] : (u.which == 1 ? a.w[1] : a.w[2]);
+    u.s0 = u.s1 = u.which == 0 ? a.s[0] : (u.which == 1 ? a.s[1] : a.s[2]);
+    u.b0 = u.b1 = u.which == 0 ? a.b[0] : (u.which == 1 ? a.b[1] : a.b[2]);
+    u.w0 = wm + (size_t)u.r0 * cpr;
+    u.w1 = wm + (size_t)u.r1 * cpr;
+    u.g0 = (size_t)u.r0 * gpr;
+    u.g1 = (size_t)u.r1 * gpr;
+    return u;
+}
+
+__device__ __forceinline__ Q4Unit q4_unit(const DecodeQ4GateUpArgs& a, int n, int cpr, int gpr)
+{
+    Q4Unit u{};
+    u.w0 = a.wg + (size_t)n * cpr;
+    u.w1 = a.wu + (size_t)n * cpr;
+    u.s0 = a.sg;
+    u.b0 = a.bg;
+    u.s1 = a.su;
+    u.b1 = a.bu;
+    u.g0 = u.g1 = (size_t)n * gpr;
+    u.r0 = u.r1 = n;
+    return u;
+}
+
+template <class Args>
+__host__ __device__ __forceinline__ int q4_units(const Args& a)
+{
+    if constexpr (std::is_same<Args, DecodeQ4QkvArgs>::value)
+        return (a.n_heads + 2 * a.n_kv_heads) * (a.head_dim >> 1);
+    else
+        return a.N;
+}
+
+// (unit, session m) epilogue with the unit's two row sums v0, v1
+__device__ __forceinline__ void q4_epilogue(const DecodeQ4QkvArgs& a, const Q4Unit& u, int m, float v0, float v1)
+{
+    const float* pb = u.which == 0 ? a.bias[0] : (u.which == 1 ? a.bias[1] : a.bias[2]);
+    if (pb) {  // add_projection_bias_if_present, then RoPE
+        v0 = v0 + pb[u.r0];
+        v1 = v1 + pb[u.r1];
+    }
+    const int half = a.head_dim >> 1;
+    const int pr = a.pos[m];
+    const float2 c = a.cs[(size_t)min(max(pr, 0), a.table_positions - 1) * half + u.i];
+    if (u.which == 0) {
+        float* q = a.q_out + ((size_t)m * a.n_heads + u.head) * a.head_dim;
+        q[u.i0] = v0 * c.x - v1 * c.y;
+        q[u.i1] = v1 * c.x + v0 * c.y;
+        return;
+    }
+    const long long b = pr >= 0 ? a.kv.base(m, pr, a.layer) : -1;
+    if (b < 0) return;
+    const size_t e = (size_t)b + (size_t)u.head * a.head_dim;
+    if (u.which == 1) {
+        a.kc[e + u.i0] = __builtin_bit_cast(uint16_t, (_Float16)(v0 * c.x - v1 * c.y));
+        a.kc[e + u.i1] = __builtin_bit_cast(uint16_t, (_Float16)(v1 * c.x + v0 * c.y));
+    } else {
+        a.vc[e + u.i0] = __builtin_bit_cast(uint16_t, (_Float16)v0);
+        a.vc[e + u.i1] = __builtin_bit_cast(uint16_t, (_Float16)v1);
+    }
+}
+
+__device__ __forceinline__ void q4_epilogue(const DecodeQ4GateUpArgs& a, const Q4Unit& u, int m, float v0, float v1)
+{
+    a.h[(size_t)m * a.N + u.r0] = act_mul(a.act, v0, v1);
+}
+
+template <int LPR, int C, int RP, int MT, int KR, bool HASY, class Args>
+__global__ __launch_bounds__(256) void decode_q4_kernel(Args a)
+{
+    constexpr int V = RP * 2 * MT;  // row sums per lane: [unit p][row r][session m]
+    static_assert(V <= LPR, "one transposed value per lane");
     extern __shared__ __align__(16) float xs[];
     __shared__ float red[kNormThreads / 64][MT];
     const int H = a.H, cpr = H >> 5;
     const int gpr = (H + (1 << a.gshift) - 1) >> a.gshift;
     const int team = threadIdx.x / LPR, lane = threadIdx.x % LPR;
-    const int n_raw = blockIdx.x * (256 / LPR) + team;
-    const int n = min(n_raw, a.N - 1);
-    u4_t w0[C], w1[C];
-    float sb[C][4];
-    load_rows_q4<C>(a.wg + (size_t)n * cpr, a.sg, a.bg, (size_t)n * gpr, a.wu + (size_t)n * cpr, a.su, a.bu,
-                    (size_t)n * gpr, lane, LPR, cpr, a.gshift, w0, w1, sb);
+    const int units = q4_units(a);
+    const int unit0 = (blockIdx.x * (256 / LPR) + team) * RP;
+
+    NormIn<MT, KR> nin;
+    load_add_norm<MT, KR, HASY>(a.x_prev, a.y, a.norm_w, a.rows, H, nin);
+    u4_t w[C][RP][2];
+    float sb[C][RP][2][2];
+#pragma unroll
+    for (int p = 0; p < RP; ++p) {
+        const Q4Unit u = q4_unit(a, min(unit0 + p, units - 1), cpr, gpr);
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+            const int ch = min(lane + c * LPR, cpr - 1);
+            const int gi = (ch << 5) >> a.gshift;
+            w[c][p][0] = __builtin_nontemporal_load(u.w0 + ch);
+            w[c][p][1] = __builtin_nontemporal_load(u.w1 + ch);
+            sb[c][p][0][0] = u.s0[u.g0 + gi];
+            sb[c][p][0][1] = u.b0[u.g0 + gi];
+            sb[c][p][1][0] = u.s1[u.g1 + gi];
+            sb[c][p][1][1] = u.b1[u.g1 + gi];
+        }
+    }
 
     float* xsum = xs + MT * xpad(H);
-    stage_add_norm<MT, KR, HASY, true>(a.x_prev, a.y, a.x_out, a.norm_w, a.rows, H, a.eps, xs, red, xsum);
+    stage_add_norm<MT, KR, HASY, true>(nin, a.x_out, a.rows, H, a.eps, xs, red, xsum);
 
-    float acc0[MT], acc1[MT];
+    float acc[V];
 #pragma unroll
-    for (int m = 0; m < MT; ++m) acc0[m] = acc1[m] = 0.0f;
-    dot_rows_q4<MT, C>(w0, w1, sb, lane, LPR, cpr, xs, xpad(H), xsum, a.rows, acc0, acc1);
+    for (int i = 0; i < V; ++i) acc[i] = 0.0f;
+    const int xst = xpad(H);
 #pragma unroll
-    for (int m = 0; m < MT; ++m) {
-        acc0[m] = group_sum<LPR>(acc0[m]);
-        acc1[m] = group_sum<LPR>(acc1[m]);
+    for (int c = 0; c < C; ++c) {
+        const int ch = lane + c * LPR;
+        if (ch >= cpr) break;
+        float d[V];
+#pragma unroll
+        for (int i = 0; i < V; ++i) d[i] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float q[RP][2][8];
+#pragma unroll
+            for (int p = 0; p < RP; ++p)
+#pragma unroll
+                for (int r = 0; r < 2; ++r) {
+                    const uint32_t wd = w[c][p][r][j];
+                    const uint32_t lo = wd & 0x0F0F0F0Fu, hi = (wd >> 4) & 0x0F0F0F0Fu;
+                    q[p][r][0] = cvt_ubyte<0>(lo);
+                    q[p][r][1] = cvt_ubyte<0>(hi);
+                    q[p][r][2] = cvt_ubyte<1>(lo);
+                    q[p][r][3] = cvt_ubyte<1>(hi);
+                    q[p][r][4] = cvt_ubyte<2>(lo);
+                    q[p][r][5] = cvt_ubyte<2>(hi);
+                    q[p][r][6] = cvt_ubyte<3>(lo);
+                    q[p][r][7] = cvt_ubyte<3>(hi);
+                }
+            // elements 32 ch + 8 j + 0..7 sit at xpad(...) = 40 ch + 8 j + (j >= 2 ? 4 : 0) + 0..7
+            const int xo = 40 * ch + 8 * j + (j >= 2 ? 4 : 0);
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                const f4_t* xp = reinterpret_cast<const f4_t*>(xs + m * xst + xo);
+                const f4_t x0 = xp[0], x1 = xp[1];
+                const float xv[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+#pragma unroll
+                for (int p = 0; p < RP; ++p)
+#pragma unroll
+                    for (int r = 0; r < 2; ++r)
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            float& dd = d[(p * 2 + r) * MT + m];
+                            dd = __builtin_fmaf(q[p][r][e], xv[e], dd);
+                        }
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            const float xc = xsum[m * cpr + ch];
+#pragma unroll
+            for (int p = 0; p < RP; ++p)
+#pragma unroll
+                for (int r = 0; r < 2; ++r) {
+                    const int vi = (p * 2 + r) * MT + m;
+                    acc[vi] += sb[c][p][r][0] * d[vi] + sb[c][p][r][1] * xc;
+                }
+        }
     }
-    if (n_raw >= a.N) return;
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-        if (m != lane || m >= a.rows) continue;
-        a.h[(size_t)m * a.N + n] = act_mul(a.act, acc0[m], acc1[m]);
-    }
+    // lane -> value index (p * 2 + r) * MT + m; the row-1 partner of a row-0 lane is
+    // LPR / (2 RP) lanes up (the halving step that split on r)
+    const float tot = team_sum_t<LPR, V>(acc);
+    constexpr int RO = LPR / (2 * RP);
+    float other;
+    if constexpr (RO >= 16)
+        other = swap_xor<RO>(tot);
+    else
+        other = lane_xor<RO>(tot, LPR);
+    const int vi = team_sum_t_index<LPR, V>(lane);
+    const int p = vi / (2 * MT), r = (vi / MT) & 1, m = vi % MT;
+    if (r != 0 || (lane & (LPR / V - 1)) != 0 || m >= a.rows || unit0 + p >= units) return;
+    q4_epilogue(a, q4_unit(a, unit0 + p, cpr, gpr), m, tot, other);
 }
 
-__device__ __forceinline__ void argmax_take(float v, int i, float& best, int& bi)
+// ---- MLX q4 affine GEMV over f32 activations (M <= 4), f32 dot ---------------
+// y[m][n] = sum_k (q[n][k] S[n][k/g] + B[n][k/g]) x[m][k] for the u32 runners'
+// projections that take no prologue (o_proj, down_proj: linear_i4_out_in,
+// lfm.rs:985-1066).  x is copied to LDS as f32 (the layout of stage_add_norm,
+// with the 32-element chunk sums), and the dot is dot_rows_q4's: no f16
+// rounding of x, so nothing to scale per chunk.  A team of LPR lanes owns R
+// consecutive rows, C chunks of each per lane (one pass: C * LPR >= K / 32).
+
+// x [M][K] -> xs[MT][xpad(K)], xsum[MT][K / 32]; padding rows m >= M repeat row
+// M - 1 (never stored).  Rounds of XU float4 groups per thread, all loads of a
+// round issued before its stores; a chunk's eight groups sit in eight adjacent lanes.
+template <int MT, int XU>
+__device__ __forceinline__ void stage_x32(const float* __restrict__ x, int M, int K, float* xs, float* xsum)
 {
-    if (!isfinite(v)) v = -INFINITY;          // llama.rs:1081-1092
-    if (v > best || bi == 0x7fffffff) {       // strictly greater keeps the first maximum
-        best = v;
-        bi = i;
+    const int t = threadIdx.x, K4 = K >> 2, total = MT * K4, xst = xpad(K), cpr = K >> 5;
+    for (int base = 0; base < total; base += XU * kNormThreads) {
+        f4_t v[XU];
+#pragma unroll
+        for (int u = 0; u < XU; ++u) {
+            const int g = min(base + u * kNormThreads + t, total - 1);
+            const int m = g / K4;
+            v[u] = reinterpret_cast<const f4_t*>(x)[(size_t)min(m, M - 1) * K4 + (g - m * K4)];
+        }
+#pragma unroll
+        for (int u = 0; u < XU; ++u) {
+            const int g = base + u * kNormThreads + t;
+            const int m = g / K4, k4 = g - m * K4;
+            if (g < total) *reinterpret_cast<f4_t*>(xs + m * xst + xpad(4 * k4)) = v[u];
+            // total % 8 == 0 (K4 % 8 == 0): a chunk's groups are all in range or all out
+            const float cs = group_sum<8>((v[u][0] + v[u][1]) + (v[u][2] + v[u][3]));
+            if (g < total && (t & 7) == 0) xsum[m * cpr + (k4 >> 3)] = cs;
+        }
     }
+    __syncthreads();
+}
+
+template <int LPR, int C, int R, int MT, int XU>
+__global__ __launch_bounds__(256) void qgemv_q4_x32_kernel(const u4_t* __restrict__ wq, const float* __restrict__ S,
+                                                           const float* __restrict__ B, const float* __restrict__ x,
+                                                           float* __restrict__ y, int M, int N, int K, int gshift)
+{
+    extern __shared__ __align__(16) float xs[];
+    const int cpr = K >> 5, gpr = (K + (1 << gshift) - 1) >> gshift;
+    const int team = threadIdx.x / LPR, lane = threadIdx.x % LPR;
+    const int row0 = (blockIdx.x * (256 / LPR) + team) * R;
+    u4_t w[C][R];
+    float sb[C][R][2];
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        const int ch = min(lane + c * LPR, cpr - 1);
+        const int gi = (ch << 5) >> gshift;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const int n = min(row0 + r, N - 1);
+            w[c][r] = __builtin_nontemporal_load(wq + (size_t)n * cpr + ch);
+            sb[c][r][0] = S[(size_t)n * gpr + gi];
+            sb[c][r][1] = B[(size_t)n * gpr + gi];
+        }
+    }
+    float* xsum = xs + MT * xpad(K);
+    stage_x32<MT, XU>(x, M, K, xs, xsum);
+
+    float acc[R][MT];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[r][m] = 0.0f;
+    const int xst = xpad(K);
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        const int ch = lane + c * LPR;
+        if (ch >= cpr) break;
+        float d[R][MT];
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int m = 0; m < MT; ++m) d[r][m] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float q[R][8];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const uint32_t lo = w[c][r][j] & 0x0F0F0F0Fu, hi = (w[c][r][j] >> 4) & 0x0F0F0F0Fu;
+                q[r][0] = cvt_ubyte<0>(lo);
+                q[r][1] = cvt_ubyte<0>(hi);
+                q[r][2] = cvt_ubyte<1>(lo);
+                q[r][3] = cvt_ubyte<1>(hi);
+                q[r][4] = cvt_ubyte<2>(lo);
+                q[r][5] = cvt_ubyte<2>(hi);
+                q[r][6] = cvt_ubyte<3>(lo);
+                q[r][7] = cvt_ubyte<3>(hi);
+            }
+            const int xo = 40 * ch + 8 * j + (j >= 2 ? 4 : 0);
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                if (m >= M) break;
+                const f4_t* xp = reinterpret_cast<const f4_t*>(xs + m * xst + xo);
+                const f4_t x0 = xp[0], x1 = xp[1];
+                const float xv[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) d[r][m] = __builtin_fmaf(q[r][e], xv[e], d[r][m]);
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            if (m >= M) break;
+            const float xc = xsum[m * cpr + ch];
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[r][m] += sb[c][r][0] * d[r][m] + sb[c][r][1] * xc;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[r][m] = group_sum<LPR>(acc[r][m]);
+    // lane r * MT + m stores (row0 + r, m)
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int m = 0; m < MT; ++m)
+            if (lane == r * MT + m && m < M && row0 + r < N) y[(size_t)m * N + row0 + r] = acc[r][m];
 }
 
 // Chunk blocks per row: block (c, r) takes elements [c * kArgmaxChunk, (c + 1) * kArgmaxChunk) of
 // row r, every thread loading all of its kArgmaxUnroll float4 before it compares any (one memory
-// latency per block), and reduces them to the chunk's first maximum.  With one chunk the block
-// writes the row's result; otherwise it publishes (value, index) with agent-coherent stores,
-// performed before it counts itself on the row's counter, and the row's last block combines the
-// chunks in chunk order and returns the counter to zero.  Each thread visits its elements in
-// increasing index order and every reduction keeps the lower index among equal values, so the
-// result is the first maximum (topk_from_logits(..)[0], llama.rs:1049-1078).
+// latency per block).  A thread takes the largest of its values (non-finite ones count as -inf,
+// llama.rs:1081-1092) and then the lowest index holding it: two short independent passes instead
+// of one compare chain.  Waves and the block reduce (value, index) pairs keeping the lower index
+// among equal values.  With one chunk the block writes the row's result; otherwise it publishes
+// (value, index) with agent-coherent stores, performed before it counts itself on the row's
+// counter, and the row's last block combines the chunks (wave 0, one partial per lane) and returns
+// the counter to zero.  Every reduction keeps the lower index among equal values, so the result is
+// the first maximum in any combining order (topk_from_logits(..)[0], llama.rs:1049-1078).
 constexpr int kArgmaxThreads = 256;
-constexpr int kArgmaxUnroll = 16;
-constexpr int kArgmaxChunk = kArgmaxThreads * 4 * kArgmaxUnroll;  // 16384 elements, 64 KB
+constexpr int kArgmaxUnroll = 4;
+constexpr int kArgmaxChunk = kArgmaxThreads * 4 * kArgmaxUnroll;  // 4096 elements, 16 KB
 
 __device__ __forceinline__ void argmax_pick(float ov, int oi, float& best, int& bi)
 {
@@ -1260,6 +1435,11 @@ __device__ __forceinline__ void argmax_pick(float ov, int oi, float& best, int& 
         best = ov;
         bi = oi;
     }
+}
+
+__device__ __forceinline__ void argmax_wave(float& best, int& bi)
+{
+    for (int off = 32; off > 0; off >>= 1) argmax_pick(__shfl_xor(best, off), __shfl_xor(bi, off), best, bi);
 }
 
 __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __restrict__ logits, int n,
@@ -1277,23 +1457,43 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __r
     if ((n & 3) == 0 && (reinterpret_cast<uintptr_t>(logits) & 15) == 0) {
         const float4* z4 = reinterpret_cast<const float4*>(z);
         const int j0 = beg >> 2, j1 = end >> 2;
-        float4 a[kArgmaxUnroll];
-#pragma unroll
-        for (int u = 0; u < kArgmaxUnroll; ++u) a[u] = z4[min(j0 + u * kArgmaxThreads + t, j1 - 1)];
+        float v[kArgmaxUnroll][4];
 #pragma unroll
         for (int u = 0; u < kArgmaxUnroll; ++u) {
+            const float4 a = z4[min(j0 + u * kArgmaxThreads + t, j1 - 1)];
+            v[u][0] = a.x;
+            v[u][1] = a.y;
+            v[u][2] = a.z;
+            v[u][3] = a.w;
+        }
+#pragma unroll
+        for (int u = 0; u < kArgmaxUnroll; ++u) {
+            const bool in = j0 + u * kArgmaxThreads + t < j1;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[u][e] = in && isfinite(v[u][e]) ? v[u][e] : -INFINITY;
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < kArgmaxUnroll; ++u)
+            mx = fmaxf(mx, fmaxf(fmaxf(v[u][0], v[u][1]), fmaxf(v[u][2], v[u][3])));
+        // the lowest in-range index holding mx (an all -inf thread: its first in-range element)
+#pragma unroll
+        for (int u = kArgmaxUnroll - 1; u >= 0; --u) {
             const int j = j0 + u * kArgmaxThreads + t;
             if (j < j1) {
-                argmax_take(a[u].x, 4 * j, best, bi);
-                argmax_take(a[u].y, 4 * j + 1, best, bi);
-                argmax_take(a[u].z, 4 * j + 2, best, bi);
-                argmax_take(a[u].w, 4 * j + 3, best, bi);
+#pragma unroll
+                for (int e = 3; e >= 0; --e) bi = v[u][e] == mx ? 4 * j + e : bi;
             }
         }
+        best = mx;
     } else {
-        for (int i = beg + t; i < end; i += kArgmaxThreads) argmax_take(z[i], i, best, bi);
+        for (int i = beg + t; i < end; i += kArgmaxThreads) {
+            float x = z[i];
+            if (!isfinite(x)) x = -INFINITY;
+            argmax_pick(x, i, best, bi);  // ties keep the lower index: the first element counts even at -inf
+        }
     }
-    for (int off = 32; off > 0; off >>= 1) argmax_pick(__shfl_xor(best, off), __shfl_xor(bi, off), best, bi);
+    argmax_wave(best, bi);
     if ((t & 63) == 0) {
         sv[t >> 6] = best;
         si[t >> 6] = bi;
@@ -1315,18 +1515,22 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __r
     }
     if (nch == 1) return;
     __syncthreads();
-    if (!last || t != 0) return;
-    __hip_atomic_store(cnt + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (!last || t >= 64) return;
+    // wave 0: lane l takes partials l, l + 64, ... of the row
     best = -INFINITY;
     bi = 0x7fffffff;
-    for (int k = 0; k < nch; ++k) {
+    for (int k = t; k < nch; k += 64) {
         const float2* p = part + (size_t)r * nch + k;
         argmax_pick(__hip_atomic_load(&p->x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
                     __builtin_bit_cast(int, __hip_atomic_load(&p->y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)),
                     best, bi);
     }
-    idx[r] = bi == 0x7fffffff ? 0 : bi;
-    val[r] = best;
+    argmax_wave(best, bi);
+    if (t == 0) {
+        __hip_atomic_store(cnt + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        idx[r] = bi == 0x7fffffff ? 0 : bi;
+        val[r] = best;
+    }
 }
 
 }  // namespace
@@ -1644,43 +1848,47 @@ namespace {
 
 size_t decode_q4_lds_bytes(int MT, int H) { return (size_t)MT * (xpad(H) + (H >> 5)) * sizeof(float); }
 
-template <int LPR, int C, int MT, int KR, bool QKV, class Args>
-hipError_t launch_decode_q4_fixed(const Args& a, int teams_total, hipStream_t st)
+#ifndef CELLM_DQ4_RP_QKV
+#define CELLM_DQ4_RP_QKV 1
+#endif
+#ifndef CELLM_DQ4_RP_GU
+#define CELLM_DQ4_RP_GU 2
+#endif
+
+template <int LPR, int C, int MT, int KR, class Args>
+hipError_t launch_decode_q4_fixed(const Args& a, hipStream_t st)
 {
-    const dim3 grid((unsigned)((teams_total + 256 / LPR - 1) / (256 / LPR)));
+    constexpr bool QKV = std::is_same<Args, DecodeQ4QkvArgs>::value;
+    constexpr int RPW = QKV ? CELLM_DQ4_RP_QKV : CELLM_DQ4_RP_GU;  // units per team wanted
+    constexpr int RP = RPW * 2 * MT <= LPR ? RPW : (LPR / (2 * MT) >= 1 ? LPR / (2 * MT) : 1);
+    const int per_block = (256 / LPR) * RP;
+    const dim3 grid((unsigned)((q4_units(a) + per_block - 1) / per_block));
     const size_t lds = decode_q4_lds_bytes(MT, a.H);
-    if constexpr (QKV) {
-        if (a.y)
-            hipLaunchKernelGGL((decode_q4_qkv_kernel<LPR, C, MT, KR, true>), grid, dim3(256), lds, st, a);
-        else
-            hipLaunchKernelGGL((decode_q4_qkv_kernel<LPR, C, MT, KR, false>), grid, dim3(256), lds, st, a);
-    } else {
-        if (a.y)
-            hipLaunchKernelGGL((decode_q4_gate_up_kernel<LPR, C, MT, KR, true>), grid, dim3(256), lds, st, a);
-        else
-            hipLaunchKernelGGL((decode_q4_gate_up_kernel<LPR, C, MT, KR, false>), grid, dim3(256), lds, st, a);
-    }
+    if (a.y)
+        hipLaunchKernelGGL((decode_q4_kernel<LPR, C, RP, MT, KR, true, Args>), grid, dim3(256), lds, st, a);
+    else
+        hipLaunchKernelGGL((decode_q4_kernel<LPR, C, RP, MT, KR, false, Args>), grid, dim3(256), lds, st, a);
     return hipGetLastError();
 }
 
-template <int LPR, int C, int KR, bool QKV, class Args>
-hipError_t launch_decode_q4_mt(const Args& a, int teams_total, hipStream_t st)
+template <int LPR, int C, int KR, class Args>
+hipError_t launch_decode_q4_mt(const Args& a, hipStream_t st)
 {
-    if (a.rows <= 1) return launch_decode_q4_fixed<LPR, C, 1, KR, QKV>(a, teams_total, st);
-    if (a.rows <= 2) return launch_decode_q4_fixed<LPR, C, 2, KR, QKV>(a, teams_total, st);
-    return launch_decode_q4_fixed<LPR, C, 4, KR, QKV>(a, teams_total, st);
+    if (a.rows <= 1) return launch_decode_q4_fixed<LPR, C, 1, KR>(a, st);
+    if (a.rows <= 2) return launch_decode_q4_fixed<LPR, C, 2, KR>(a, st);
+    return launch_decode_q4_fixed<LPR, C, 4, KR>(a, st);
 }
 
 // chunks per row cpr = H / 32, one chunk per lane up to 64 (teams of 16, 32 or 64 lanes), two up to 128;
 // KR float4 groups per thread in the prologue (KR * 1024 >= H follows from the same bounds)
-template <bool QKV, class Args>
-hipError_t launch_decode_q4(const Args& a, int teams_total, hipStream_t st)
+template <class Args>
+hipError_t launch_decode_q4(const Args& a, hipStream_t st)
 {
     const int cpr = a.H >> 5;
-    if (cpr <= 16) return launch_decode_q4_mt<16, 1, 1, QKV>(a, teams_total, st);
-    if (cpr <= 32) return launch_decode_q4_mt<32, 1, 1, QKV>(a, teams_total, st);
-    if (cpr <= 64) return launch_decode_q4_mt<64, 1, 2, QKV>(a, teams_total, st);
-    return launch_decode_q4_mt<64, 2, 4, QKV>(a, teams_total, st);
+    if (cpr <= 16) return launch_decode_q4_mt<16, 1, 1>(a, st);
+    if (cpr <= 32) return launch_decode_q4_mt<32, 1, 1>(a, st);
+    if (cpr <= 64) return launch_decode_q4_mt<64, 1, 2>(a, st);
+    return launch_decode_q4_mt<64, 2, 4>(a, st);
 }
 
 int log2_exact(int v)
@@ -1728,7 +1936,7 @@ hipError_t launch_decode_q4_qkv(const float* x_prev, const float* y, float* x_ou
     a.kv = PagedKv{block_tables, max_blocks, total_blocks, n_layers, tokens_per_block, n_kv_heads * head_dim};
     a.layer = layer;
     a.il = interleaved ? 1 : 0;
-    return launch_decode_q4<true>(a, (n_heads + 2 * n_kv_heads) * (head_dim / 2), st);
+    return launch_decode_q4(a, st);
 }
 
 hipError_t launch_decode_q4_gate_up(const float* x_prev, const float* y, float* x_out, const float* norm_w, float eps,
@@ -1739,7 +1947,61 @@ hipError_t launch_decode_q4_gate_up(const float* x_prev, const float* y, float* 
     if (!decode_q4_fused_supported(rows, H, group)) return hipErrorInvalidValue;
     DecodeQ4GateUpArgs a{x_prev, y, x_out, norm_w, eps, reinterpret_cast<const u4_t*>(wg), sg, bg,
                          reinterpret_cast<const u4_t*>(wu), su, bu, rows, H, N, log2_exact(group), act, h};
-    return launch_decode_q4<false>(a, N, st);
+    return launch_decode_q4(a, st);
+}
+
+// Long rows at 2..4 activation rows stay on the hi + lo f16 kernels (measured on MI355X, 4864 -> 896:
+// 6.8 / 10.0 us here against 6.5 / 9.3 us at M = 2 / 4); up to K = 2048 this kernel is as fast or
+// faster at every M (896 -> 896: 2.95 / 3.17 / 4.62 against 3.25 / 4.07 / 4.59 us at M = 1 / 2 / 4).
+bool qgemv_q4_x32_supported(int M, int N, int K, int group)
+{
+    return M >= 1 && M <= 4 && N >= 1 && K >= 32 && K % 32 == 0 && group >= 32 && group <= K &&
+           (group & (group - 1)) == 0 && (size_t)4 * (xpad(K) + (K >> 5)) * sizeof(float) <= 160 * 1024 &&
+           (K >> 5) <= 4 * 64 && (M == 1 || K <= 2048);
+}
+
+namespace {
+
+template <int LPR, int C, int R, int MT>
+hipError_t launch_q4_x32_fixed(const uint32_t* wq, const float* S, const float* B, const float* x, float* y, int M,
+                               int N, int K, int gshift, hipStream_t st)
+{
+    const int rows_per_block = (256 / LPR) * R;
+    const dim3 grid((unsigned)((N + rows_per_block - 1) / rows_per_block));
+    const size_t lds = (size_t)MT * (xpad(K) + (K >> 5)) * sizeof(float);
+    const int groups = MT * (K >> 2);
+    if (groups <= 2 * kNormThreads)
+        hipLaunchKernelGGL((qgemv_q4_x32_kernel<LPR, C, R, MT, 2>), grid, dim3(256), lds, st,
+                           reinterpret_cast<const u4_t*>(wq), S, B, x, y, M, N, K, gshift);
+    else
+        hipLaunchKernelGGL((qgemv_q4_x32_kernel<LPR, C, R, MT, 8>), grid, dim3(256), lds, st,
+                           reinterpret_cast<const u4_t*>(wq), S, B, x, y, M, N, K, gshift);
+    return hipGetLastError();
+}
+
+template <int LPR, int C, int R>
+hipError_t launch_q4_x32_mt(const uint32_t* wq, const float* S, const float* B, const float* x, float* y, int M,
+                            int N, int K, int gshift, hipStream_t st)
+{
+    if (M <= 1) return launch_q4_x32_fixed<LPR, C, R, 1>(wq, S, B, x, y, M, N, K, gshift, st);
+    if (M <= 2) return launch_q4_x32_fixed<LPR, C, R, 2>(wq, S, B, x, y, M, N, K, gshift, st);
+    return launch_q4_x32_fixed<LPR, C, R, 4>(wq, S, B, x, y, M, N, K, gshift, st);
+}
+
+}  // namespace
+
+hipError_t launch_qgemv_q4_x32(const uint32_t* wq, const float* S, const float* B, const float* x, float* y, int M,
+                               int N, int K, int group, hipStream_t st)
+{
+    if (!qgemv_q4_x32_supported(M, N, K, group)) return hipErrorInvalidValue;
+    const int cpr = K >> 5, gshift = log2_exact(group);
+    constexpr int R = 1;  // one row per team: at K <= 1536 faster than two or four (more blocks)
+    if (cpr <= 16) return launch_q4_x32_mt<16, 1, R>(wq, S, B, x, y, M, N, K, gshift, st);
+    if (cpr <= 32) return launch_q4_x32_mt<32, 1, R>(wq, S, B, x, y, M, N, K, gshift, st);
+    if (cpr <= 64) return launch_q4_x32_mt<64, 1, R>(wq, S, B, x, y, M, N, K, gshift, st);
+    if (cpr <= 128) return launch_q4_x32_mt<64, 2, R>(wq, S, B, x, y, M, N, K, gshift, st);
+    if (cpr <= 192) return launch_q4_x32_mt<64, 3, R>(wq, S, B, x, y, M, N, K, gshift, st);
+    return launch_q4_x32_mt<64, 4, R>(wq, S, B, x, y, M, N, K, gshift, st);
 }
 
 int argmax_chunks(int n) { return std::max(1, (n + kArgmaxChunk - 1) / kArgmaxChunk); }

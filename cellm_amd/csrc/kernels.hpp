@@ -166,6 +166,12 @@ hipError_t launch_decode_gate_up(const float* x_prev, const float* y, float* x_o
 // biases, group a power of two >= 32) with an f32 dot: rows 1..4, H % 32 == 0,
 // H <= 4096; q/k/v projection biases optional (null entries).
 bool decode_q4_fused_supported(int rows, int H, int group);
+// Plain MLX q4 affine GEMV over f32 x at M <= 4 with f32 scales/biases (decode.hip): x in LDS as f32,
+// f32 dot; K % 32 == 0, four rows of x within 160 KB of LDS (K <= 7936), K <= 2048 unless M == 1,
+// group a power of two >= 32.
+bool qgemv_q4_x32_supported(int M, int N, int K, int group);
+hipError_t launch_qgemv_q4_x32(const uint32_t* wq, const float* S, const float* B, const float* x, float* y, int M,
+                               int N, int K, int group, hipStream_t st);
 hipError_t launch_decode_q4_qkv(const float* x_prev, const float* y, float* x_out, const float* norm_w, float eps,
                                 const uint32_t* const w[3], const float* const s[3], const float* const b[3],
                                 const float* const bias[3], int group, int rows, int H, int n_heads, int n_kv_heads,
