@@ -723,21 +723,16 @@ __global__ __launch_bounds__(kAttnBlockThreads) void attn_head_kernel(
     }
 }
 
-// ---- fused decode-step GEMVs ------------------------------------------------
-// One launch replaces "residual add + RMSNorm, int8 GEMV(s), epilogue op":
-//   decode_qkv_kernel:     xn = rms_norm(x_prev + y) * w;  q, k, v = W xn;
-//                          RoPE on q and k; k and v into the paged cache
-//   decode_gate_up_kernel: xn = rms_norm(x_prev + y) * w;  h = silu(Wg xn) * (Wu xn)
-// Every block stages the whole normalised row(s) in LDS (each needs all of
-// xn); block 0 also writes x_prev + y to x_out, the next residual stream, a
-// different buffer from x_prev so that no block reads a row another has
-// already overwritten.  The add and the scaling are those of
-// add_rms_norm_kernel; the sum of squares is a tree of another shape (each
-// thread sums 4 neighbouring elements first).  A team of LPR
-// lanes computes two output rows; each lane owns C 16-byte chunks of both,
-// loaded before the prologue so that their memory latency overlaps it.  x is
-// stored with 4 floats of padding after every 16 (lanes read it at a stride of
-// 16 floats, which would put 4 lanes on each bank group).
+// ---- fused decode-step GEMVs: the shared prologue --------------------------------
+// decode_i8_kernel and decode_q4_kernel (below) replace "residual add +
+// RMSNorm, GEMV(s), epilogue op" with one launch.  Every block stages the whole
+// normalised row(s) in LDS (each needs all of xn); block 0 also writes
+// x_prev + y to x_out, the next residual stream, a different buffer from
+// x_prev so that no block reads a row another has already overwritten.  The
+// add and the scaling are those of add_rms_norm_kernel; the sum of squares is
+// a tree of another shape (each thread sums 4 neighbouring elements first).
+// xn is stored with 4 floats of padding after every 16 (lanes read it at a
+// stride of 16 or 32 floats, which would put several lanes on each bank group).
 
 __host__ __device__ __forceinline__ int xpad(int k) { return k + (k >> 4) * 4; }
 
@@ -853,49 +848,6 @@ __device__ __forceinline__ void stage_add_norm(NormIn<MT, KR>& in, float* __rest
     __syncthreads();
 }
 
-// This lane's C chunks of rows r0 and r1 (row bytes H), chunk index clamped.
-template <int C>
-__device__ __forceinline__ void load_rows_i8(const int8_t* __restrict__ w0, const int8_t* __restrict__ w1, int lane,
-                                             int LPR, int nchunk, u4_t (&a)[C], u4_t (&b)[C])
-{
-#pragma unroll
-    for (int c = 0; c < C; ++c) {
-        const int ch = min(lane + c * LPR, nchunk - 1);
-        a[c] = reinterpret_cast<const u4_t*>(w0)[ch];
-        b[c] = reinterpret_cast<const u4_t*>(w1)[ch];
-    }
-}
-
-// acc0/acc1[m] += sum over this lane's chunks of w * xn[m]
-template <int MT, int C>
-__device__ __forceinline__ void dot_rows_i8(const u4_t (&a)[C], const u4_t (&b)[C], int lane, int LPR, int nchunk,
-                                            const float* xs, int xst, int rows, float (&acc0)[MT],
-                                            float (&acc1)[MT])
-{
-#pragma unroll
-    for (int c = 0; c < C; ++c) {
-        const int ch = lane + c * LPR;
-        if (ch >= nchunk) break;
-#pragma unroll
-        for (int m = 0; m < MT; ++m) {
-            if (m >= rows) break;
-            const f4_t* xp = reinterpret_cast<const f4_t*>(xs + m * xst + ch * 20);
-            const f4_t xq[4] = {xp[0], xp[1], xp[2], xp[3]};
-            float d0 = acc0[m], d1 = acc1[m];
-#pragma unroll
-            for (int wd = 0; wd < 4; ++wd)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float xe = xq[wd][e];
-                    d0 = __builtin_fmaf((float)(int8_t)(a[c][wd] >> (8 * e)), xe, d0);
-                    d1 = __builtin_fmaf((float)(int8_t)(b[c][wd] >> (8 * e)), xe, d1);
-                }
-            acc0[m] = d0;
-            acc1[m] = d1;
-        }
-    }
-}
-
 struct DecodeQkvArgs {
     const float* x_prev;
     const float* y;
@@ -916,70 +868,6 @@ struct DecodeQkvArgs {
     int il;  // RoPE pairs: 0 rotate-half (i, i + half), 1 interleaved (2i, 2i + 1)
 };
 
-// Team -> one (head, i < head_dim/2) pair: rows i and i + head_dim/2 (rotate-half)
-// or 2i and 2i + 1 (interleaved) of a q, k or v head, the two operands of one
-// RoPE rotation.
-template <int LPR, int C, int MT, int KR, bool HASY>
-__global__ __launch_bounds__(256) void decode_qkv_kernel(DecodeQkvArgs a)
-{
-    extern __shared__ __align__(16) float xs[];
-    __shared__ float red[kNormThreads / 64][MT];
-    const int H = a.H, half = a.head_dim >> 1, nchunk = H >> 4;
-    const int team = threadIdx.x / LPR, lane = threadIdx.x % LPR;
-    const int pairs = (a.n_heads + 2 * a.n_kv_heads) * half;
-    const int p = min((int)(blockIdx.x * (256 / LPR) + team), pairs - 1);
-    const bool active = (int)(blockIdx.x * (256 / LPR) + team) < pairs;
-    const int hh = p / half, i = p - hh * half;
-    const int which = hh < a.n_heads ? 0 : (hh < a.n_heads + a.n_kv_heads ? 1 : 2);
-    const int head = which == 0 ? hh : (which == 1 ? hh - a.n_heads : hh - a.n_heads - a.n_kv_heads);
-    const int i0 = rope_lo(i, half, a.il), i1 = rope_hi(i, half, a.il);
-    const int r0 = head * a.head_dim + i0, r1 = head * a.head_dim + i1;
-    const int8_t* wm = which == 0 ? a.w[0] : (which == 1 ? a.w[1] : a.w[2]);
-    const uint16_t* sm = which == 0 ? a.s[0] : (which == 1 ? a.s[1] : a.s[2]);
-    NormIn<MT, KR> nin;
-    load_add_norm<MT, KR, HASY>(a.x_prev, a.y, a.norm_w, a.rows, H, nin);
-    u4_t w0[C], w1[C];
-    load_rows_i8<C>(wm + (size_t)r0 * H, wm + (size_t)r1 * H, lane, LPR, nchunk, w0, w1);
-    const float s0 = h2f(sm[r0]), s1 = h2f(sm[r1]);
-
-    stage_add_norm<MT, KR, HASY>(nin, a.x_out, a.rows, H, a.eps, xs, red);
-
-    float acc0[MT], acc1[MT];
-#pragma unroll
-    for (int m = 0; m < MT; ++m) acc0[m] = acc1[m] = 0.0f;
-    dot_rows_i8<MT, C>(w0, w1, lane, LPR, nchunk, xs, xpad(H), a.rows, acc0, acc1);
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-        acc0[m] = group_sum<LPR>(acc0[m]);
-        acc1[m] = group_sum<LPR>(acc1[m]);
-    }
-    if (!active) return;
-    // lane m writes session m: y = acc * scale (matmul_i8_f32), then the epilogue op
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-        if (m != lane || m >= a.rows) continue;
-        const float v0 = acc0[m] * s0, v1 = acc1[m] * s1;
-        const int pr = a.pos[m];
-        const float2 c = a.cs[(size_t)min(max(pr, 0), a.table_positions - 1) * half + i];
-        if (which == 0) {
-            float* q = a.q_out + ((size_t)m * a.n_heads + head) * a.head_dim;
-            q[i0] = v0 * c.x - v1 * c.y;
-            q[i1] = v1 * c.x + v0 * c.y;
-            continue;
-        }
-        const long long b = pr >= 0 ? a.kv.base(m, pr, a.layer) : -1;
-        if (b < 0) continue;
-        const size_t e = (size_t)b + (size_t)head * a.head_dim;
-        if (which == 1) {
-            a.kc[e + i0] = __builtin_bit_cast(uint16_t, (_Float16)(v0 * c.x - v1 * c.y));
-            a.kc[e + i1] = __builtin_bit_cast(uint16_t, (_Float16)(v1 * c.x + v0 * c.y));
-        } else {
-            a.vc[e + i0] = __builtin_bit_cast(uint16_t, (_Float16)v0);
-            a.vc[e + i1] = __builtin_bit_cast(uint16_t, (_Float16)v1);
-        }
-    }
-}
-
 struct DecodeGateUpArgs {
     const float* x_prev;
     const float* y;
@@ -993,44 +881,6 @@ struct DecodeGateUpArgs {
     int rows, H, N;
     float* h;  // [rows][N]
 };
-
-// Team -> row n of gate and of up; h = silu(g) * u as silu_mul_f32_inplace
-// (metal.rs:235-245): (g * (1 / (1 + exp(-g)))) * u.
-template <int LPR, int C, int MT, int KR, bool HASY>
-__global__ __launch_bounds__(256) void decode_gate_up_kernel(DecodeGateUpArgs a)
-{
-    extern __shared__ __align__(16) float xs[];
-    __shared__ float red[kNormThreads / 64][MT];
-    const int H = a.H, nchunk = H >> 4;
-    const int team = threadIdx.x / LPR, lane = threadIdx.x % LPR;
-    const int n_raw = blockIdx.x * (256 / LPR) + team;
-    const int n = min(n_raw, a.N - 1);
-    NormIn<MT, KR> nin;
-    load_add_norm<MT, KR, HASY>(a.x_prev, a.y, a.norm_w, a.rows, H, nin);
-    u4_t w0[C], w1[C];
-    load_rows_i8<C>(a.wg + (size_t)n * H, a.wu + (size_t)n * H, lane, LPR, nchunk, w0, w1);
-    const float sg = h2f(a.sg[n]), su = h2f(a.su[n]);
-
-    stage_add_norm<MT, KR, HASY>(nin, a.x_out, a.rows, H, a.eps, xs, red);
-
-    float acc0[MT], acc1[MT];
-#pragma unroll
-    for (int m = 0; m < MT; ++m) acc0[m] = acc1[m] = 0.0f;
-    dot_rows_i8<MT, C>(w0, w1, lane, LPR, nchunk, xs, xpad(H), a.rows, acc0, acc1);
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-        acc0[m] = group_sum<LPR>(acc0[m]);
-        acc1[m] = group_sum<LPR>(acc1[m]);
-    }
-    if (n_raw >= a.N) return;
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-        if (m != lane || m >= a.rows) continue;
-        const float g = acc0[m] * sg, u = acc1[m] * su;
-        const float sig = 1.0f / (1.0f + expf(-g));
-        a.h[(size_t)m * a.N + n] = (g * sig) * u;
-    }
-}
 
 // ---- fused decode-step GEMVs over MLX q4 affine weights ---------------------
 // The q4 counterparts of the two kernels above, for the u32 runners (the Qwen2
@@ -1146,6 +996,34 @@ __host__ __device__ __forceinline__ int q4_units(const Args& a)
         return a.N;
 }
 
+// RoPE on the pair (v0, v1) of head `head`, rows i0 / i1 (pair i of the table row
+// at session m's position), then q into q_out or k / v into the paged cache as f16:
+// the arithmetic of rope_kv_write_kernel.  Shared by the int8 and q4 QKV kernels.
+template <class A>
+__device__ __forceinline__ void rope_kv_epilogue(const A& a, int which, int head, int i, int i0, int i1, int m,
+                                                 float v0, float v1)
+{
+    const int half = a.head_dim >> 1;
+    const int pr = a.pos[m];
+    const float2 c = a.cs[(size_t)min(max(pr, 0), a.table_positions - 1) * half + i];
+    if (which == 0) {
+        float* q = a.q_out + ((size_t)m * a.n_heads + head) * a.head_dim;
+        q[i0] = v0 * c.x - v1 * c.y;
+        q[i1] = v1 * c.x + v0 * c.y;
+        return;
+    }
+    const long long b = pr >= 0 ? a.kv.base(m, pr, a.layer) : -1;
+    if (b < 0) return;
+    const size_t e = (size_t)b + (size_t)head * a.head_dim;
+    if (which == 1) {
+        a.kc[e + i0] = __builtin_bit_cast(uint16_t, (_Float16)(v0 * c.x - v1 * c.y));
+        a.kc[e + i1] = __builtin_bit_cast(uint16_t, (_Float16)(v1 * c.x + v0 * c.y));
+    } else {
+        a.vc[e + i0] = __builtin_bit_cast(uint16_t, (_Float16)v0);
+        a.vc[e + i1] = __builtin_bit_cast(uint16_t, (_Float16)v1);
+    }
+}
+
 // (unit, session m) epilogue with the unit's two row sums v0, v1
 __device__ __forceinline__ void q4_epilogue(const DecodeQ4QkvArgs& a, const Q4Unit& u, int m, float v0, float v1)
 {
@@ -1154,25 +1032,7 @@ __device__ __forceinline__ void q4_epilogue(const DecodeQ4QkvArgs& a, const Q4Un
         v0 = v0 + pb[u.r0];
         v1 = v1 + pb[u.r1];
     }
-    const int half = a.head_dim >> 1;
-    const int pr = a.pos[m];
-    const float2 c = a.cs[(size_t)min(max(pr, 0), a.table_positions - 1) * half + u.i];
-    if (u.which == 0) {
-        float* q = a.q_out + ((size_t)m * a.n_heads + u.head) * a.head_dim;
-        q[u.i0] = v0 * c.x - v1 * c.y;
-        q[u.i1] = v1 * c.x + v0 * c.y;
-        return;
-    }
-    const long long b = pr >= 0 ? a.kv.base(m, pr, a.layer) : -1;
-    if (b < 0) return;
-    const size_t e = (size_t)b + (size_t)u.head * a.head_dim;
-    if (u.which == 1) {
-        a.kc[e + u.i0] = __builtin_bit_cast(uint16_t, (_Float16)(v0 * c.x - v1 * c.y));
-        a.kc[e + u.i1] = __builtin_bit_cast(uint16_t, (_Float16)(v1 * c.x + v0 * c.y));
-    } else {
-        a.vc[e + u.i0] = __builtin_bit_cast(uint16_t, (_Float16)v0);
-        a.vc[e + u.i1] = __builtin_bit_cast(uint16_t, (_Float16)v1);
-    }
+    rope_kv_epilogue(a, u.which, u.head, u.i, u.i0, u.i1, m, v0, v1);
 }
 
 __device__ __forceinline__ void q4_epilogue(const DecodeQ4GateUpArgs& a, const Q4Unit& u, int m, float v0, float v1)
@@ -1288,6 +1148,154 @@ __global__ __launch_bounds__(256) void decode_q4_kernel(Args a)
     const int p = vi / (2 * MT), r = (vi / MT) & 1, m = vi % MT;
     if (r != 0 || (lane & (LPR / V - 1)) != 0 || m >= a.rows || unit0 + p >= units) return;
     q4_epilogue(a, q4_unit(a, unit0 + p, cpr, gpr), m, tot, other);
+}
+
+// ---- fused decode-step GEMVs over int8 weights -------------------------------
+// One launch replaces "residual add + RMSNorm, int8 GEMV(s), epilogue op" for
+// the int8 Llama step (llama_graph.rs:245-327):
+//   QKV:     xn = rms_norm(x_prev + y) * w;  q, k, v = W xn;  RoPE on q and k;
+//            k and v into the paged cache
+//   gate/up: xn = rms_norm(x_prev + y) * w;  h = silu(Wg xn) * (Wu xn)
+// The layout of decode_q4_kernel: every block stages the normalised rows
+// (stage_add_norm; block 0 also writes x_prev + y to x_out, a different buffer
+// from x_prev, so that no block reads a row another has already overwritten),
+// a team of LPR lanes owns RP units of two rows, a lane C 16-byte chunks
+// (16 int8) of each, loaded after the prologue's inputs and before its work.
+// The dot is f32 FMA over the widened bytes; the row sums are summed over the
+// team transposed and scaled by the f16 row scale (matmul_i8_f32: the sum,
+// then the scale) in the epilogue.
+
+struct I8Unit {
+    const u4_t* w0;
+    const u4_t* w1;
+    const uint16_t* s0;
+    const uint16_t* s1;
+    int which, head, i, i0, i1, r0, r1;
+};
+
+__device__ __forceinline__ I8Unit i8_unit(const DecodeQkvArgs& a, int p, int cpr)
+{
+    I8Unit u;
+    const int half = a.head_dim >> 1;
+    const int hh = p / half;
+    u.i = p - hh * half;
+    u.which = hh < a.n_heads ? 0 : (hh < a.n_heads + a.n_kv_heads ? 1 : 2);
+    u.head = u.which == 0 ? hh : (u.which == 1 ? hh - a.n_heads : hh - a.n_heads - a.n_kv_heads);
+    u.i0 = rope_lo(u.i, half, a.il);
+    u.i1 = rope_hi(u.i, half, a.il);
+    u.r0 = u.head * a.head_dim + u.i0;
+    u.r1 = u.head * a.head_dim + u.i1;
+    const u4_t* wm = reinterpret_cast<const u4_t*>(u.which == 0 ? a.w[0] : (u.which == 1 ? a.w[1] : a.w[2]));
+    u.s0 = u.s1 = u.which == 0 ? a.s[0] : (u.which == 1 ? a.s[1] : a.s[2]);
+    u.w0 = wm + (size_t)u.r0 * cpr;
+    u.w1 = wm + (size_t)u.r1 * cpr;
+    return u;
+}
+
+__device__ __forceinline__ I8Unit i8_unit(const DecodeGateUpArgs& a, int n, int cpr)
+{
+    I8Unit u{};
+    u.w0 = reinterpret_cast<const u4_t*>(a.wg) + (size_t)n * cpr;
+    u.w1 = reinterpret_cast<const u4_t*>(a.wu) + (size_t)n * cpr;
+    u.s0 = a.sg;
+    u.s1 = a.su;
+    u.r0 = u.r1 = n;
+    return u;
+}
+
+template <class Args>
+__host__ __device__ __forceinline__ int i8_units(const Args& a)
+{
+    if constexpr (std::is_same<Args, DecodeQkvArgs>::value)
+        return (a.n_heads + 2 * a.n_kv_heads) * (a.head_dim >> 1);
+    else
+        return a.N;
+}
+
+__device__ __forceinline__ void i8_epilogue(const DecodeQkvArgs& a, const I8Unit& u, int m, float v0, float v1)
+{
+    rope_kv_epilogue(a, u.which, u.head, u.i, u.i0, u.i1, m, v0, v1);
+}
+
+// h = silu(g) * u as silu_mul_f32_inplace (metal.rs:235-245): (g * (1 / (1 + exp(-g)))) * u
+__device__ __forceinline__ void i8_epilogue(const DecodeGateUpArgs& a, const I8Unit& u, int m, float v0, float v1)
+{
+    a.h[(size_t)m * a.N + u.r0] = act_mul(ACT_SILU, v0, v1);
+}
+
+template <int LPR, int C, int RP, int MT, int KR, bool HASY, class Args>
+__global__ __launch_bounds__(256) void decode_i8_kernel(Args a)
+{
+    constexpr int V = RP * 2 * MT;  // row sums per lane: [unit p][row r][session m]
+    static_assert(V <= LPR, "one transposed value per lane");
+    extern __shared__ __align__(16) float xs[];
+    __shared__ float red[kNormThreads / 64][MT];
+    const int H = a.H, cpr = H >> 4;
+    const int team = threadIdx.x / LPR, lane = threadIdx.x % LPR;
+    const int units = i8_units(a);
+    const int unit0 = (blockIdx.x * (256 / LPR) + team) * RP;
+
+    NormIn<MT, KR> nin;
+    load_add_norm<MT, KR, HASY>(a.x_prev, a.y, a.norm_w, a.rows, H, nin);
+    u4_t w[C][RP][2];
+#pragma unroll
+    for (int p = 0; p < RP; ++p) {
+        const I8Unit u = i8_unit(a, min(unit0 + p, units - 1), cpr);
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+            const int ch = min(lane + c * LPR, cpr - 1);
+            w[c][p][0] = u.w0[ch];
+            w[c][p][1] = u.w1[ch];
+        }
+    }
+
+    stage_add_norm<MT, KR, HASY>(nin, a.x_out, a.rows, H, a.eps, xs, red);
+
+    float acc[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = 0.0f;
+    const int xst = xpad(H);
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+        const int ch = lane + c * LPR;
+        if (ch >= cpr) break;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float q[RP][2][4];
+#pragma unroll
+            for (int p = 0; p < RP; ++p)
+#pragma unroll
+                for (int r = 0; r < 2; ++r)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) q[p][r][e] = (float)(int8_t)(w[c][p][r][j] >> (8 * e));
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                // elements 16 ch + 4 j + 0..3 sit at xpad(...) = 20 ch + 4 j + 0..3
+                const f4_t xv = *reinterpret_cast<const f4_t*>(xs + m * xst + 20 * ch + 4 * j);
+#pragma unroll
+                for (int p = 0; p < RP; ++p)
+#pragma unroll
+                    for (int r = 0; r < 2; ++r)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            float& dd = acc[(p * 2 + r) * MT + m];
+                            dd = __builtin_fmaf(q[p][r][e], xv[e], dd);
+                        }
+            }
+        }
+    }
+    const float tot = team_sum_t<LPR, V>(acc);
+    constexpr int RO = LPR / (2 * RP);
+    float other;
+    if constexpr (RO >= 16)
+        other = swap_xor<RO>(tot);
+    else
+        other = lane_xor<RO>(tot, LPR);
+    const int vi = team_sum_t_index<LPR, V>(lane);
+    const int p = vi / (2 * MT), r = (vi / MT) & 1, m = vi % MT;
+    if (r != 0 || (lane & (LPR / V - 1)) != 0 || m >= a.rows || unit0 + p >= units) return;
+    const I8Unit u = i8_unit(a, unit0 + p, cpr);
+    i8_epilogue(a, u, m, tot * h2f(u.s0[u.r0]), other * h2f(u.s1[u.r1]));
 }
 
 // ---- MLX q4 affine GEMV over f32 activations (M <= 4), f32 dot ---------------
@@ -1742,53 +1750,57 @@ size_t decode_fused_lds_bytes(int rows, int H)
 
 namespace {
 
-template <int LPR, int C, int MT, int KR, bool QKV, class Args>
-hipError_t launch_decode_fixed(const Args& a, int teams_total, size_t lds, hipStream_t st)
+#ifndef CELLM_DI8_RP_QKV
+#define CELLM_DI8_RP_QKV 1
+#endif
+#ifndef CELLM_DI8_RP_GU
+#define CELLM_DI8_RP_GU 2
+#endif
+
+template <int LPR, int C, int MT, int KR, class Args>
+hipError_t launch_decode_fixed(const Args& a, size_t lds, hipStream_t st)
 {
-    const dim3 grid((unsigned)((teams_total + 256 / LPR - 1) / (256 / LPR)));
-    if constexpr (QKV) {
-        if (a.y)
-            hipLaunchKernelGGL((decode_qkv_kernel<LPR, C, MT, KR, true>), grid, dim3(256), lds, st, a);
-        else
-            hipLaunchKernelGGL((decode_qkv_kernel<LPR, C, MT, KR, false>), grid, dim3(256), lds, st, a);
-    } else {
-        if (a.y)
-            hipLaunchKernelGGL((decode_gate_up_kernel<LPR, C, MT, KR, true>), grid, dim3(256), lds, st, a);
-        else
-            hipLaunchKernelGGL((decode_gate_up_kernel<LPR, C, MT, KR, false>), grid, dim3(256), lds, st, a);
-    }
+    constexpr bool QKV = std::is_same<Args, DecodeQkvArgs>::value;
+    constexpr int RPW = QKV ? CELLM_DI8_RP_QKV : CELLM_DI8_RP_GU;  // units per team wanted
+    constexpr int RP = RPW * 2 * MT <= LPR ? RPW : (LPR / (2 * MT) >= 1 ? LPR / (2 * MT) : 1);
+    const int per_block = (256 / LPR) * RP;
+    const dim3 grid((unsigned)((i8_units(a) + per_block - 1) / per_block));
+    if (a.y)
+        hipLaunchKernelGGL((decode_i8_kernel<LPR, C, RP, MT, KR, true, Args>), grid, dim3(256), lds, st, a);
+    else
+        hipLaunchKernelGGL((decode_i8_kernel<LPR, C, RP, MT, KR, false, Args>), grid, dim3(256), lds, st, a);
     return hipGetLastError();
 }
 
-template <int LPR, int C, int MT, bool QKV, class Args>
-hipError_t launch_decode_kr(int H, const Args& a, int teams_total, size_t lds, hipStream_t st)
+template <int LPR, int C, int MT, class Args>
+hipError_t launch_decode_kr(int H, const Args& a, size_t lds, hipStream_t st)
 {
     const int kr = (H / 4 + kNormThreads - 1) / kNormThreads;  // float4 groups per thread
-    if (kr <= 1) return launch_decode_fixed<LPR, C, MT, 1, QKV>(a, teams_total, lds, st);
-    if (kr <= 2) return launch_decode_fixed<LPR, C, MT, 2, QKV>(a, teams_total, lds, st);
-    return launch_decode_fixed<LPR, C, MT, 4, QKV>(a, teams_total, lds, st);
+    if (kr <= 1) return launch_decode_fixed<LPR, C, MT, 1>(a, lds, st);
+    if (kr <= 2) return launch_decode_fixed<LPR, C, MT, 2>(a, lds, st);
+    return launch_decode_fixed<LPR, C, MT, 4>(a, lds, st);
 }
 
-template <int LPR, int C, bool QKV, class Args>
-hipError_t launch_decode_mt(int rows, int H, const Args& a, int teams_total, hipStream_t st)
+template <int LPR, int C, class Args>
+hipError_t launch_decode_mt(int rows, int H, const Args& a, hipStream_t st)
 {
     const size_t lds = decode_fused_lds_bytes(rows, H);
-    if (rows <= 1) return launch_decode_kr<LPR, C, 1, QKV>(H, a, teams_total, lds, st);
-    if (rows <= 2) return launch_decode_kr<LPR, C, 2, QKV>(H, a, teams_total, lds, st);
-    return launch_decode_kr<LPR, C, 4, QKV>(H, a, teams_total, lds, st);
+    if (rows <= 1) return launch_decode_kr<LPR, C, 1>(H, a, lds, st);
+    if (rows <= 2) return launch_decode_kr<LPR, C, 2>(H, a, lds, st);
+    return launch_decode_kr<LPR, C, 4>(H, a, lds, st);
 }
 
 // chunks per row nchunk = H / 16: 16 lanes up to 16 chunks, else 64 lanes with C = ceil(nchunk / 64)
 // (up to 4).  At hidden 960 (60 chunks) 64 lanes of one chunk each beat 32 lanes of two by ~1 % of
 // the configs[4] step: twice the waves, each with half the dot work after its loads land.
-template <bool QKV, class Args>
-hipError_t launch_decode(int rows, int H, const Args& a, int teams_total, hipStream_t st)
+template <class Args>
+hipError_t launch_decode(int rows, int H, const Args& a, hipStream_t st)
 {
     const int nchunk = H >> 4;
-    if (nchunk <= 16) return launch_decode_mt<16, 1, QKV>(rows, H, a, teams_total, st);
-    if (nchunk <= 64) return launch_decode_mt<64, 1, QKV>(rows, H, a, teams_total, st);
-    if (nchunk <= 128) return launch_decode_mt<64, 2, QKV>(rows, H, a, teams_total, st);
-    return launch_decode_mt<64, 4, QKV>(rows, H, a, teams_total, st);
+    if (nchunk <= 16) return launch_decode_mt<16, 1>(rows, H, a, st);
+    if (nchunk <= 64) return launch_decode_mt<64, 1>(rows, H, a, st);
+    if (nchunk <= 128) return launch_decode_mt<64, 2>(rows, H, a, st);
+    return launch_decode_mt<64, 4>(rows, H, a, st);
 }
 
 }  // namespace
@@ -1824,9 +1836,8 @@ hipError_t launch_decode_qkv(const float* x_prev, const float* y, float* x_out, 
     a.kv = PagedKv{block_tables, max_blocks, total_blocks, n_layers, tokens_per_block, n_kv_heads * head_dim};
     a.layer = layer;
     a.il = interleaved ? 1 : 0;
-    const int pairs = (n_heads + 2 * n_kv_heads) * (head_dim / 2);
     if (H > 64 * 16 * 4) return hipErrorInvalidValue;
-    return launch_decode<true>(rows, H, a, pairs, st);
+    return launch_decode(rows, H, a, st);
 }
 
 hipError_t launch_decode_gate_up(const float* x_prev, const float* y, float* x_out, const float* norm_w, float eps,
@@ -1835,7 +1846,7 @@ hipError_t launch_decode_gate_up(const float* x_prev, const float* y, float* x_o
 {
     DecodeGateUpArgs a{x_prev, y, x_out, norm_w, eps, wg, sg, wu, su, rows, H, N, h};
     if (H > 64 * 16 * 4) return hipErrorInvalidValue;
-    return launch_decode<false>(rows, H, a, N, st);
+    return launch_decode(rows, H, a, st);
 }
 
 bool decode_q4_fused_supported(int rows, int H, int group)
