@@ -1309,21 +1309,21 @@ __global__ __launch_bounds__(256) void decode_i8_kernel(Args a)
 // x [M][K] -> xs[MT][xpad(K)], xsum[MT][K / 32]; padding rows m >= M repeat row
 // M - 1 (never stored).  Rounds of XU float4 groups per thread, all loads of a
 // round issued before its stores; a chunk's eight groups sit in eight adjacent lanes.
-template <int MT, int XU>
+template <int MT, int XU, int NT = kNormThreads>
 __device__ __forceinline__ void stage_x32(const float* __restrict__ x, int M, int K, float* xs, float* xsum)
 {
     const int t = threadIdx.x, K4 = K >> 2, total = MT * K4, xst = xpad(K), cpr = K >> 5;
-    for (int base = 0; base < total; base += XU * kNormThreads) {
+    for (int base = 0; base < total; base += XU * NT) {
         f4_t v[XU];
 #pragma unroll
         for (int u = 0; u < XU; ++u) {
-            const int g = min(base + u * kNormThreads + t, total - 1);
+            const int g = min(base + u * NT + t, total - 1);
             const int m = g / K4;
             v[u] = reinterpret_cast<const f4_t*>(x)[(size_t)min(m, M - 1) * K4 + (g - m * K4)];
         }
 #pragma unroll
         for (int u = 0; u < XU; ++u) {
-            const int g = base + u * kNormThreads + t;
+            const int g = base + u * NT + t;
             const int m = g / K4, k4 = g - m * K4;
             if (g < total) *reinterpret_cast<f4_t*>(xs + m * xst + xpad(4 * k4)) = v[u];
             // total % 8 == 0 (K4 % 8 == 0): a chunk's groups are all in range or all out
@@ -1421,6 +1421,74 @@ __global__ __launch_bounds__(256) void qgemv_q4_x32_kernel(const u4_t* __restric
 #pragma unroll
         for (int m = 0; m < MT; ++m)
             if (lane == r * MT + m && m < M && row0 + r < N) y[(size_t)m * N + row0 + r] = acc[r][m];
+}
+
+// Long rows (K > 2048) at 2..4 activation rows: one block of KS * RB waves
+// stages x once (every thread one round of loads) and splits each of its RB
+// rows over KS waves, wave (ks, rb) taking chunks [ks * cps, (ks + 1) * cps),
+// one per lane (cps <= 64).  Each wave sums its rows transposed
+// (team_sum_t<64, MT>), the partials meet in LDS, and one lane per (row,
+// session) adds the KS partials in slice order and stores.  Every wave gets
+// a 1/KS share of the row's dot, so the block's VALU work spreads over KS
+// times more waves than one-wave-per-row teams.
+template <int KS, int RB, int MT, int XU>
+__global__ __launch_bounds__(KS * RB * 64) void qgemv_q4_x32s_kernel(
+    const u4_t* __restrict__ wq, const float* __restrict__ S, const float* __restrict__ B, const float* __restrict__ x,
+    float* __restrict__ y, int M, int N, int K, int gshift)
+{
+    constexpr int NT = KS * RB * 64;
+    extern __shared__ __align__(16) float xs[];
+    __shared__ float part[KS][RB][MT];
+    const int cpr = K >> 5, gpr = (K + (1 << gshift) - 1) >> gshift, cps = (cpr + KS - 1) / KS;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int ks = wave / RB, rb = wave % RB;
+    const int n = min((int)blockIdx.x * RB + rb, N - 1);
+    const int ch_raw = ks * cps + lane;
+    const bool live = lane < cps && ch_raw < cpr;
+    const int ch = min(ch_raw, cpr - 1);
+    const int gi = (ch << 5) >> gshift;
+    const u4_t wv = __builtin_nontemporal_load(wq + (size_t)n * cpr + ch);
+    const float sc = S[(size_t)n * gpr + gi], bc = B[(size_t)n * gpr + gi];
+    float* xsum = xs + MT * xpad(K);
+    stage_x32<MT, XU, NT>(x, M, K, xs, xsum);
+
+    float acc[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
+    if (live) {
+        float d[MT];
+#pragma unroll
+        for (int m = 0; m < MT; ++m) d[m] = 0.0f;
+        const int xst = xpad(K);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t lo = wv[j] & 0x0F0F0F0Fu, hi = (wv[j] >> 4) & 0x0F0F0F0Fu;
+            const float q[8] = {cvt_ubyte<0>(lo), cvt_ubyte<0>(hi), cvt_ubyte<1>(lo), cvt_ubyte<1>(hi),
+                                cvt_ubyte<2>(lo), cvt_ubyte<2>(hi), cvt_ubyte<3>(lo), cvt_ubyte<3>(hi)};
+            const int xo = 40 * ch + 8 * j + (j >= 2 ? 4 : 0);
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                const f4_t* xp = reinterpret_cast<const f4_t*>(xs + m * xst + xo);
+                const f4_t x0 = xp[0], x1 = xp[1];
+                const float xv[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) d[m] = __builtin_fmaf(q[e], xv[e], d[m]);
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < MT; ++m) acc[m] = sc * d[m] + bc * xsum[m * cpr + ch];
+    }
+    const float tot = team_sum_t<64, MT>(acc);
+    if ((lane & (64 / MT - 1)) == 0) part[ks][rb][team_sum_t_index<64, MT>(lane)] = tot;
+    __syncthreads();
+    if (threadIdx.x < RB * MT) {
+        const int r = threadIdx.x / MT, m = threadIdx.x % MT;
+        const int row = (int)blockIdx.x * RB + r;
+        float v = part[0][r][m];
+#pragma unroll
+        for (int k = 1; k < KS; ++k) v = v + part[k][r][m];
+        if (m < M && row < N) y[(size_t)m * N + row] = v;
+    }
 }
 
 // Chunk blocks per row: block (c, r) takes elements [c * kArgmaxChunk, (c + 1) * kArgmaxChunk) of
@@ -2000,6 +2068,60 @@ hipError_t launch_q4_x32_mt(const uint32_t* wq, const float* S, const float* B, 
 }
 
 }  // namespace
+
+namespace {
+
+template <int KS, int RB, int MT>
+hipError_t launch_q4_x32s_fixed(const uint32_t* wq, const float* S, const float* B, const float* x, float* y, int M,
+                                int N, int K, int gshift, hipStream_t st)
+{
+    constexpr int NT = KS * RB * 64;
+    const dim3 grid((unsigned)((N + RB - 1) / RB));
+    const size_t lds = (size_t)MT * (xpad(K) + (K >> 5)) * sizeof(float);
+    const auto* w4 = reinterpret_cast<const u4_t*>(wq);
+    const int rounds = (MT * (K >> 2) + NT - 1) / NT;  // float4 loads per thread
+    if (rounds <= 4)
+        hipLaunchKernelGGL((qgemv_q4_x32s_kernel<KS, RB, MT, 4>), grid, dim3(NT), lds, st, w4, S, B, x, y, M, N, K,
+                           gshift);
+    else
+        hipLaunchKernelGGL((qgemv_q4_x32s_kernel<KS, RB, MT, 8>), grid, dim3(NT), lds, st, w4, S, B, x, y, M, N, K,
+                           gshift);
+    return hipGetLastError();
+}
+
+template <int KS, int RB>
+hipError_t launch_q4_x32s_mt(const uint32_t* wq, const float* S, const float* B, const float* x, float* y, int M,
+                             int N, int K, int gshift, hipStream_t st)
+{
+    if (M <= 1) return launch_q4_x32s_fixed<KS, RB, 1>(wq, S, B, x, y, M, N, K, gshift, st);
+    if (M <= 2) return launch_q4_x32s_fixed<KS, RB, 2>(wq, S, B, x, y, M, N, K, gshift, st);
+    return launch_q4_x32s_fixed<KS, RB, 4>(wq, S, B, x, y, M, N, K, gshift, st);
+}
+
+}  // namespace
+
+// Waves per row and rows per block of qgemv_q4_x32s_kernel.  4864 -> 896 at 4 rows on MI355X:
+// 3 x 4 (768 threads) 6.2 us, 4 x 4 7.2 us, 4 x 2 and 3 x 2 12.7-12.9 us; the hi + lo f16 kernel 9.3 us.
+#ifndef CELLM_X32S_KS
+#define CELLM_X32S_KS 3
+#endif
+#ifndef CELLM_X32S_RB
+#define CELLM_X32S_RB 4
+#endif
+bool qgemv_q4_x32s_supported(int M, int N, int K, int group)
+{
+    const int cpr = K >> 5;
+    return M >= 1 && M <= 4 && N >= 1 && K >= 32 && K % 32 == 0 && group >= 32 && group <= K &&
+           (group & (group - 1)) == 0 && (size_t)4 * (xpad(K) + (K >> 5)) * sizeof(float) <= 160 * 1024 &&
+           (cpr + CELLM_X32S_KS - 1) / CELLM_X32S_KS <= 64;
+}
+
+hipError_t launch_qgemv_q4_x32s(const uint32_t* wq, const float* S, const float* B, const float* x, float* y, int M,
+                                int N, int K, int group, hipStream_t st)
+{
+    if (!qgemv_q4_x32s_supported(M, N, K, group)) return hipErrorInvalidValue;
+    return launch_q4_x32s_mt<CELLM_X32S_KS, CELLM_X32S_RB>(wq, S, B, x, y, M, N, K, log2_exact(group), st);
+}
 
 hipError_t launch_qgemv_q4_x32(const uint32_t* wq, const float* S, const float* B, const float* x, float* y, int M,
                                int N, int K, int group, hipStream_t st)
