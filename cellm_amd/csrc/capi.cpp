@@ -310,8 +310,8 @@ int32_t qgemv_q4_impl(cellm_hip_ctx* ctx, const uint32_t* wq, const void* scales
                 "qgemv_q4_x32 launch");
         return CELLM_HIP_OK;
     }
-    // the same at 2..4 rows over long rows (the down projection): each row split over the waves of a block
-    if (!force_gemm && xdt == DT_F32 && sbt == DT_F32 && m >= 2 && aligned16(wq) && aligned16(x) &&
+    // the same over rows longer than 2048 (the down projection): each row split over the waves of a block
+    if (!force_gemm && xdt == DT_F32 && sbt == DT_F32 && aligned16(wq) && aligned16(x) &&
         qgemv_q4_x32s_supported((int)m, (int)n, (int)k, (int)group)) {
         HIP_TRY(launch_qgemv_q4_x32s(wq, static_cast<const float*>(scales), static_cast<const float*>(biases),
                                      static_cast<const float*>(x), y, (int)m, (int)n, (int)k, (int)group, st),

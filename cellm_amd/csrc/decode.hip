@@ -1423,7 +1423,7 @@ __global__ __launch_bounds__(256) void qgemv_q4_x32_kernel(const u4_t* __restric
             if (lane == r * MT + m && m < M && row0 + r < N) y[(size_t)m * N + row0 + r] = acc[r][m];
 }
 
-// Long rows (K > 2048) at 2..4 activation rows: one block of KS * RB waves
+// Long rows (K > 2048, 1..4 activation rows): one block of KS * RB waves
 // stages x once (every thread one round of loads) and splits each of its RB
 // rows over KS waves, wave (ks, rb) taking chunks [ks * cps, (ks + 1) * cps),
 // one per lane (cps <= 64).  Each wave sums its rows transposed
@@ -2029,14 +2029,15 @@ hipError_t launch_decode_q4_gate_up(const float* x_prev, const float* y, float* 
     return launch_decode_q4(a, st);
 }
 
-// Long rows at 2..4 activation rows stay on the hi + lo f16 kernels (measured on MI355X, 4864 -> 896:
-// 6.8 / 10.0 us here against 6.5 / 9.3 us at M = 2 / 4); up to K = 2048 this kernel is as fast or
-// faster at every M (896 -> 896: 2.95 / 3.17 / 4.62 against 3.25 / 4.07 / 4.59 us at M = 1 / 2 / 4).
+// Rows of up to 2048 (64 chunks): one team per row.  Longer rows go to qgemv_q4_x32s_kernel, which
+// splits each row over three waves (measured on MI355X, 4864 -> 896 at M = 1 / 2 / 4: 3.9 / 4.3 / 6.2 us
+// there, 4.6 / 6.8 / 10.0 us here and 4.7 / 6.5 / 9.3 us on the hi + lo f16 kernels); 896 -> 896 here:
+// 2.95 / 3.17 / 4.62 us against 3.25 / 4.07 / 4.59 us on the hi + lo f16 kernels.
 bool qgemv_q4_x32_supported(int M, int N, int K, int group)
 {
     return M >= 1 && M <= 4 && N >= 1 && K >= 32 && K % 32 == 0 && group >= 32 && group <= K &&
            (group & (group - 1)) == 0 && (size_t)4 * (xpad(K) + (K >> 5)) * sizeof(float) <= 160 * 1024 &&
-           (K >> 5) <= 4 * 64 && (M == 1 || K <= 2048);
+           K <= 2048;
 }
 
 namespace {
@@ -2111,7 +2112,7 @@ hipError_t launch_q4_x32s_mt(const uint32_t* wq, const float* S, const float* B,
 bool qgemv_q4_x32s_supported(int M, int N, int K, int group)
 {
     const int cpr = K >> 5;
-    return M >= 1 && M <= 4 && N >= 1 && K >= 32 && K % 32 == 0 && group >= 32 && group <= K &&
+    return M >= 1 && M <= 4 && N >= 1 && K > 2048 && K >= 32 && K % 32 == 0 && group >= 32 && group <= K &&
            (group & (group - 1)) == 0 && (size_t)4 * (xpad(K) + (K >> 5)) * sizeof(float) <= 160 * 1024 &&
            (cpr + CELLM_X32S_KS - 1) / CELLM_X32S_KS <= 64;
 }
@@ -2131,10 +2132,7 @@ hipError_t launch_qgemv_q4_x32(const uint32_t* wq, const float* S, const float* 
     constexpr int R = 1;  // one row per team: at K <= 1536 faster than two or four (more blocks)
     if (cpr <= 16) return launch_q4_x32_mt<16, 1, R>(wq, S, B, x, y, M, N, K, gshift, st);
     if (cpr <= 32) return launch_q4_x32_mt<32, 1, R>(wq, S, B, x, y, M, N, K, gshift, st);
-    if (cpr <= 64) return launch_q4_x32_mt<64, 1, R>(wq, S, B, x, y, M, N, K, gshift, st);
-    if (cpr <= 128) return launch_q4_x32_mt<64, 2, R>(wq, S, B, x, y, M, N, K, gshift, st);
-    if (cpr <= 192) return launch_q4_x32_mt<64, 3, R>(wq, S, B, x, y, M, N, K, gshift, st);
-    return launch_q4_x32_mt<64, 4, R>(wq, S, B, x, y, M, N, K, gshift, st);
+    return launch_q4_x32_mt<64, 1, R>(wq, S, B, x, y, M, N, K, gshift, st);  // K <= 2048: 64 chunks
 }
 
 int argmax_chunks(int n) { return std::max(1, (n + kArgmaxChunk - 1) / kArgmaxChunk); }

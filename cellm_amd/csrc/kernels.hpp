@@ -167,10 +167,10 @@ hipError_t launch_decode_gate_up(const float* x_prev, const float* y, float* x_o
 // H <= 4096; q/k/v projection biases optional (null entries).
 bool decode_q4_fused_supported(int rows, int H, int group);
 // Plain MLX q4 affine GEMV over f32 x at M <= 4 with f32 scales/biases (decode.hip): x in LDS as f32,
-// f32 dot; K % 32 == 0, four rows of x within 160 KB of LDS (K <= 7936), K <= 2048 unless M == 1,
-// group a power of two >= 32.
+// f32 dot; K % 32 == 0 and K <= 2048, group a power of two >= 32.
 bool qgemv_q4_x32_supported(int M, int N, int K, int group);
-// The same over long rows (K up to the LDS bound): each row split over the waves of one block.
+// The same over longer rows (2048 < K, four rows of x within 160 KB of LDS: K <= 7936): each row
+// split over the waves of one block.
 bool qgemv_q4_x32s_supported(int M, int N, int K, int group);
 hipError_t launch_qgemv_q4_x32s(const uint32_t* wq, const float* S, const float* B, const float* x, float* y, int M,
                                 int N, int K, int group, hipStream_t st);
