@@ -538,6 +538,43 @@ def test_q4_affine_f32_activations_long_output_mfma(ops, n, k, m, sb):
     assert rel_err(oracle.qgemv_q4_affine(wq, s, b, xr, k, gs=64), ref) > 3e-5
 
 
+@pytest.mark.parametrize("n,k,m,group", [
+    (896, 896, 1, 64), (896, 896, 2, 64), (896, 896, 4, 64),   # Qwen2 o_proj: one team per row
+    (1000, 1024, 3, 32),
+    (333, 96, 1, 32),                   # three chunks per row: teams of 16 lanes, most idle
+    (700, 2048, 4, 128),                # the longest row on one team (64 chunks)
+    (896, 4864, 1, 64), (896, 4864, 2, 64), (896, 4864, 4, 64),  # Qwen2 down_proj: rows split over 3 waves
+    (300, 2080, 2, 32),                 # just past 2048: 22 chunks per wave
+    (129, 6144, 3, 64),                 # 64 chunks per wave, a ragged last block of rows
+])
+def test_q4_affine_f32_dot_paths(ops, n, k, m, group):
+    """f32 x with f32 scales and biases at 1..4 rows (the u32 runners' o_proj and down_proj,
+    linear_i4_out_in, lfm.rs:985-1066): x in LDS as f32 and an f32 FMA dot over the widened
+    nibbles, one team per row up to K = 2048, longer rows split over three waves.  No f16 rounding
+    of x anywhere: every row within 1e-5 of the f32 reference order."""
+    wq, s, b, x = make_q4(n, k, m, sb_dtype=np.float32, x_dtype=np.float32, group=group, salt=200 + m + k % 83)
+    y = _run_q4(ops, wq, s, b, x, group=group)
+    ref = oracle.qgemv_q4_affine(wq, s, b, x, k, gs=group)
+    for r in range(m):
+        assert rel_err(y[r], ref[r]) <= 1e-5, (r, rel_err(y[r], ref[r]))
+
+
+@pytest.mark.parametrize("k", [896, 4864])
+def test_q4_affine_f32_dot_range(ops, k):
+    """The f32-dot paths over x far from N(0,1) (rows at ~1e5, ~1e-5, ~1e-12 and zero): f32
+    throughout, so each row stays within 1e-5 of the f32 oracle and the zero row is exactly zero."""
+    n, m = 700, 4
+    row_scale = np.array([1e5, 1e-5, 1e-12, 0.0], np.float32)
+    wq, s, b, x0 = make_q4(n, k, m, sb_dtype=np.float32, x_dtype=np.float32, salt=230 + k % 7)
+    x = np.ascontiguousarray(x0 * row_scale[:, None], np.float32)
+    y = _run_q4(ops, wq, s, b, x)
+    ref = oracle.qgemv_q4_affine(wq, s, b, x, k)
+    assert np.all(np.isfinite(y))
+    for r in range(m):
+        assert rel_err(y[r], ref[r]) <= 1e-5, (r, rel_err(y[r], ref[r]))
+    assert not np.any(y[3])
+
+
 def test_q4_affine_f32_activation_range_long_output_mfma(ops):
     """The MFMA f32-x path over x far from N(0,1): rows past f16's largest value, at ~1e-5 and
     ~1e-12, and zero; each row against the f32 oracle to 3e-5, the zero row exactly zero."""
