@@ -66,7 +66,7 @@ def parse():
     ap.add_argument("--no-extra", action="store_true", help="skip the extra configs")
     ap.add_argument("--pmc-sample", nargs="?", const="lm_head_q4", default=None,
                     choices=["lm_head_q4", "lm_head_i8_m1", "lm_head_i8_m64", "qgemm_896x4864", "qgemm_4864x896",
-                             "i4_6912x1152", "decode_layer_4",
+                             "i4_6912x1152", "decode_layer_4", "decode_layer_q4_4",
                              "q4_gate_up_silu_1152x6912", "q4_down_6912x1152_m1", "q4_down_6912x1152_m4",
                              "q4_down_6912x1152_m16", "q4_down_6912x1152_m64", "q4_gate_up_1152x13824_m4",
                              "q4_gate_up_1152x13824_m16", "q4_gate_up_1152x13824_m64"],
@@ -139,8 +139,50 @@ def pmc_sample(torch, ops, stream, gen, which: str):
             ops.encode_qgemv_i8(wo, so, att, y, stream=sp)
             ops.encode_decode_gate_up(xb, y, xa, norm, 1e-5, wg, sg, wu, su, h, stream=sp)
             ops.encode_qgemv_i8(wd, sd, h, y, stream=sp)
-        info.update({"kernel": "decode_qkv_kernel, attn_partial/combine, qgemv_i8 (o, down), decode_gate_up_kernel",
+        info.update({"kernel": "decode_i8_kernel (QKV, gate/up), attn_head_kernel, qgemv_i8_kernel (o, down)",
                      "algorithmic_bytes": sum(t.numel() for t in (wq, wk, wv, wo, wg, wu, wd))})
+    elif which == "decode_layer_q4_4":
+        # one configs[1]-shape Qwen2 layer for 4 sessions at context 512, eager launches: the fused q4 QKV
+        # (+ RMSNorm, biases, RoPE, K/V write), attention, o_proj, fused q4 gate/up, down_proj (f32 x,
+        # MLX q4 g64 with f32 scales and biases, as the u32 runners hold them), 20 times
+        H, NH, NKV, HD, I, L, TPB, CTX, R = 896, 14, 2, 64, 4864, 1, 16, 512, 4
+        kvd, blocks = NKV * HD, CTX // TPB
+
+        def q4w(o, i):
+            wq_ = torch.randint(-2**31, 2**31 - 1, (o, i // 8), dtype=torch.int32, device="cuda", generator=gen)
+            s_ = (torch.rand((o, i // 64), device="cuda", generator=gen) + 0.5) / (4.6 * i ** 0.5)
+            return wq_, s_, -7.5 * s_
+
+        (wq, sq, bq), (wk, sk, bk), (wv, sv, bv) = q4w(H, H), q4w(kvd, H), q4w(kvd, H)
+        (wo, so, bo), (wg, sg, bg), (wu, su, bu), (wd, sd, bd) = q4w(H, H), q4w(I, H), q4w(I, H), q4w(H, I)
+        pq, pk, pv = (torch.randn(n, device="cuda", generator=gen) * 0.1 for n in (H, kvd, kvd))
+        norm = torch.ones(H, dtype=torch.float32, device="cuda")
+        total = R * blocks
+        kc = torch.randn(total * L * TPB * kvd, device="cuda", generator=gen).to(torch.float16)
+        vc = torch.randn(total * L * TPB * kvd, device="cuda", generator=gen).to(torch.float16)
+        bt = torch.tensor([[b * R + s for b in range(blocks)] for s in range(R)], dtype=torch.int32, device="cuda")
+        pos = torch.full((R,), CTX - 1, dtype=torch.int32, device="cuda")
+        ang = torch.arange(CTX, device="cuda").float()[:, None] * torch.pow(
+            1000000.0, -torch.arange(0, HD, 2, device="cuda").float() / HD)[None, :]
+        cs = torch.stack([torch.cos(ang), torch.sin(ang)], dim=-1).contiguous()
+        xa, xb = torch.randn((R, H), device="cuda", generator=gen), torch.zeros((R, H), device="cuda")
+        y = torch.zeros((R, H), device="cuda")
+        q = torch.empty((R, NH * HD), device="cuda")
+        att = torch.empty((R, NH * HD), device="cuda")
+        h = torch.empty((R, I), device="cuda")
+        sp = stream.cuda_stream
+        for _ in range(20):
+            ops.encode_decode_q4_qkv(xa, y, xb, norm, 1e-6, wq, sq, bq, pq, wk, sk, bk, pk, wv, sv, bv, pv, 64, NH,
+                                     NKV, HD, pos, cs, q, kc, vc, bt, total, L, TPB, 0, stream=sp)
+            ops.encode_attention(q, kc, vc, bt, pos, att, NH, NKV, HD, total, L, TPB, 0, stream=sp)
+            ops.encode_qgemv_q4_affine(wo, so, bo, att, y, stream=sp)
+            ops.encode_decode_q4_gate_up(xb, y, xa, norm, 1e-6, wg, sg, bg, wu, su, bu, 64, h, stream=sp)
+            ops.encode_qgemv_q4_affine(wd, sd, bd, h, y, stream=sp)
+        info.update({"kernel": "decode_q4_kernel (QKV, gate/up), attn_head_kernel, qgemv_q4_x32_kernel (o), "
+                               "qgemv_q4_x32s_kernel (down)",
+                     # packed W + f32 S,B per group of 64 + f32 x + f32 y per projection
+                     "algorithmic_bytes": sum(o * i // 2 + 8 * o * (i // 64) + 4 * R * i + 4 * R * o for o, i in
+                                              ((H, H), (kvd, H), (kvd, H), (H, H), (I, H), (I, H), (H, I)))})
     elif which == "i4_6912x1152":
         k, n, copies = 6912, 1152, 8
         w = torch.randint(0, 256, (copies, n, k // 2), dtype=torch.uint8, device="cuda", generator=gen)
