@@ -128,11 +128,13 @@ int32_t cellm_hip_qgemv_i8(cellm_hip_ctx_t* ctx, const int8_t* w, const void* sc
  * k % 8 == 0; group a power of two >= 8 (MLX uses 64).  2..64 rows with f16 x
  * run the batched MFMA path, split over k through the per-stream workspace
  * for few output rows over a long k, as cellm_hip_qgemv_i8.
- * f32 x (m <= 4) is multiplied as two f16 parts, hi = RNE_f16(x') and
- * lo = RNE_f16(x' - hi), of each 32-element chunk scaled by a power of two
- * x' = x * 2^e that puts the chunk's largest |x| in [2^13, 2^14): any finite
- * f32 x keeps about 22 bits, and the result is scaled back exactly.  This
- * holds for the fused gate/up and QKV entry points below too.  Long outputs
+ * f32 x (m <= 4) with f32 scales and biases runs an f32 dot (x kept in f32,
+ * the nibbles widened exactly).  With f16/bf16 scales it is multiplied as two
+ * f16 parts, hi = RNE_f16(x') and lo = RNE_f16(x' - hi), of each 32-element
+ * chunk scaled by a power of two x' = x * 2^e that puts the chunk's largest
+ * |x| in [2^13, 2^14): any finite f32 x keeps about 22 bits, and the result is
+ * scaled back exactly.  The split holds for the fused gate/up and QKV entry
+ * points below too.  Long outputs
  * (n >= 32768, n % 16 == 0, k % 128 == 0, k <= 1024, group 64, 16-byte
  * aligned wq and x: the affine lm_head) run on int8 MFMA instead: each row
  * is rounded to integers x' = rint(x * 2^e) with |x'| <= 2^20 for the row's
