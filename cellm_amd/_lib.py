@@ -103,6 +103,9 @@ SIGNATURES = {
     "cellm_hip_gelu_tanh_mul_f32": (_i32, [_vp, _vp, _vp, _i64, _vp]),
     "cellm_hip_add_f32_inplace": (_i32, [_vp, _vp, _vp, _i64, _vp]),
     "cellm_hip_argmax_f32": (_i32, [_vp, _vp, _i64, _i64, _vp, _vp, _vp]),
+    "cellm_hip_argmax_f32_keys": (_i32, [_vp, _vp, _i64, _i64, _vp, _vp]),
+    "cellm_hip_argmax_key_index": (_i32, [C.c_uint64]),
+    "cellm_hip_argmax_key_value": (C.c_float, [C.c_uint64]),
 }
 
 _lib = None

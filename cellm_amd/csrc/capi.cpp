@@ -1538,4 +1538,29 @@ int32_t cellm_hip_argmax_f32(cellm_hip_ctx_t* ctx, const float* logits, int64_t 
     CELLM_API_END(report_exception)
 }
 
+int32_t cellm_hip_argmax_key_index(uint64_t key) { return (int32_t)(0xffffffffu - (uint32_t)key); }
+
+float cellm_hip_argmax_key_value(uint64_t key)
+{
+    const uint32_t o = (uint32_t)(key >> 32);
+    return __builtin_bit_cast(float, (o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
+}
+
+int32_t cellm_hip_argmax_f32_keys(cellm_hip_ctx_t* ctx, const float* logits, int64_t rows, int64_t n,
+                                  uint64_t* out_keys, void* stream)
+{
+    CELLM_API_BEGIN
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    if (int32_t rc = check_dims(rows, n, 1)) return rc;
+    if (rows == 0) return CELLM_HIP_OK;
+    if (n == 0) return set_error(CELLM_HIP_ERR_INVALID_ARG, "empty logits");
+    if (!logits || !out_keys) return set_error(CELLM_HIP_ERR_INVALID_ARG, "null pointer");
+    if (rows > 65535) return set_error(CELLM_HIP_ERR_INVALID_ARG, "rows=%lld > 65535", (long long)rows);
+    if (reinterpret_cast<uintptr_t>(out_keys) & 7) return set_error(CELLM_HIP_ERR_INVALID_ARG, "keys not 8-byte aligned");
+    DeviceGuard g(ctx->device);
+    HIP_TRY(launch_argmax_keys(logits, (int)rows, (int)n, out_keys, pick_stream(ctx, stream)), "argmax launch");
+    return CELLM_HIP_OK;
+    CELLM_API_END(report_exception)
+}
+
 }  // extern "C"

@@ -1518,19 +1518,16 @@ __device__ __forceinline__ void argmax_wave(float& best, int& bi)
     for (int off = 32; off > 0; off >>= 1) argmax_pick(__shfl_xor(best, off), __shfl_xor(bi, off), best, bi);
 }
 
-__global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __restrict__ logits, int n,
-                                                                int32_t* __restrict__ idx, float* __restrict__ val,
-                                                                uint32_t* __restrict__ cnt, float2* __restrict__ part)
+// The first maximum of chunk c of row z (n elements): valid in thread 0 on return; sv/si are the
+// block's wave slots.
+__device__ __forceinline__ void argmax_chunk(const float* __restrict__ z, int n, int c, float (&sv)[kArgmaxThreads / 64],
+                                             int (&si)[kArgmaxThreads / 64], float& best, int& bi)
 {
-    __shared__ float sv[kArgmaxThreads / 64];
-    __shared__ int si[kArgmaxThreads / 64];
-    __shared__ int last;
-    const int c = blockIdx.x, r = blockIdx.y, t = threadIdx.x, nch = gridDim.x;
-    const float* z = logits + (size_t)r * n;
+    const int t = threadIdx.x;
     const int beg = c * kArgmaxChunk, end = min(n, beg + kArgmaxChunk);
-    float best = -INFINITY;
-    int bi = 0x7fffffff;
-    if ((n & 3) == 0 && (reinterpret_cast<uintptr_t>(logits) & 15) == 0) {
+    best = -INFINITY;
+    bi = 0x7fffffff;
+    if ((n & 3) == 0 && (reinterpret_cast<uintptr_t>(z) & 15) == 0) {
         const float4* z4 = reinterpret_cast<const float4*>(z);
         const int j0 = beg >> 2, j1 = end >> 2;
         float v[kArgmaxUnroll][4];
@@ -1575,8 +1572,22 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __r
         si[t >> 6] = bi;
     }
     __syncthreads();
-    if (t == 0) {
+    if (t == 0)
         for (int w = 1; w < kArgmaxThreads / 64; ++w) argmax_pick(sv[w], si[w], best, bi);
+}
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __restrict__ logits, int n,
+                                                                int32_t* __restrict__ idx, float* __restrict__ val,
+                                                                uint32_t* __restrict__ cnt, float2* __restrict__ part)
+{
+    __shared__ float sv[kArgmaxThreads / 64];
+    __shared__ int si[kArgmaxThreads / 64];
+    __shared__ int last;
+    const int c = blockIdx.x, r = blockIdx.y, t = threadIdx.x, nch = gridDim.x;
+    float best;
+    int bi;
+    argmax_chunk(logits + (size_t)r * n, n, c, sv, si, best, bi);
+    if (t == 0) {
         if (nch == 1) {
             idx[r] = bi == 0x7fffffff ? 0 : bi;
             val[r] = best;
@@ -1607,6 +1618,31 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_kernel(const float* __r
         idx[r] = bi == 0x7fffffff ? 0 : bi;
         val[r] = best;
     }
+}
+
+// Packed form of a row's first maximum: the value's bits mapped to an unsigned order (-0 taken as
+// +0, so equal values compare equal) in the high word, 0xffffffff - index in the low word.  The
+// largest key is the largest value at its lowest index, so one 64-bit atomic max per chunk block
+// merges the chunks in any order into the row's first maximum, with no partials, counter or
+// combining block.
+__device__ __forceinline__ uint64_t argmax_key(float v, int i)
+{
+    const uint32_t u = __float_as_uint(v == 0.0f ? 0.0f : v);
+    const uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)o << 32) | (uint64_t)(0xffffffffu - (uint32_t)i);
+}
+
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_key_kernel(const float* __restrict__ logits, int n,
+                                                                    uint64_t* __restrict__ keys)
+{
+    __shared__ float sv[kArgmaxThreads / 64];
+    __shared__ int si[kArgmaxThreads / 64];
+    const int c = blockIdx.x, r = blockIdx.y;
+    float best;
+    int bi;
+    argmax_chunk(logits + (size_t)r * n, n, c, sv, si, best, bi);
+    if (threadIdx.x == 0)
+        (void)__hip_atomic_fetch_max(keys + r, argmax_key(best, bi), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace
@@ -2143,6 +2179,12 @@ size_t argmax_scratch_bytes(int rows, int n)
 {
     const int nch = argmax_chunks(n);
     return nch == 1 ? 0 : argmax_counter_bytes(rows) + (size_t)rows * nch * sizeof(float2);
+}
+
+hipError_t launch_argmax_keys(const float* logits, int rows, int n, uint64_t* keys, hipStream_t st)
+{
+    hipLaunchKernelGGL(argmax_key_kernel, dim3(argmax_chunks(n), rows), dim3(kArgmaxThreads), 0, st, logits, n, keys);
+    return hipGetLastError();
 }
 
 hipError_t launch_argmax(const float* logits, int rows, int n, int32_t* idx, float* val, void* scratch, hipStream_t st)

@@ -145,6 +145,10 @@ hipError_t launch_attention_gqa_f16kv(const float* q, const uint16_t* kcache, co
 size_t argmax_scratch_bytes(int rows, int n);
 size_t argmax_counter_bytes(int rows);
 hipError_t launch_argmax(const float* logits, int rows, int n, int32_t* idx, float* val, void* scratch, hipStream_t st);
+// The same first maximum per row as a packed key (value order in the high word, 0xffffffff - index
+// in the low word) merged into keys[r] by one 64-bit atomic max per chunk block: keys start at zero;
+// no scratch.
+hipError_t launch_argmax_keys(const float* logits, int rows, int n, uint64_t* keys, hipStream_t st);
 // Size of the static attention scratch (decode.hip) and the current device's
 // address of it (hipGetSymbolAddress once per device, cached).
 constexpr size_t kAttnStaticScratchBytes = (size_t)8 << 20;

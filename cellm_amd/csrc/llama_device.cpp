@@ -193,9 +193,9 @@ struct cellm_llama_dev {
     bool fused = false;
     // the same over MLX q4 affine q/k/v (projection biases allowed) and gate/up (no biases), hidden % 32 == 0
     bool fused_q4 = false;
-    // io: [tokens u32 | positions i32 | block tables u32 | argmax idx i32 | argmax val f32]
+    // io: [tokens u32 | positions i32 | block tables u32 | greedy keys u64 (zero when uploaded)]
     void* host_io = nullptr;  // pinned mirror of io
-    size_t io_tokens = 0, io_pos = 0, io_bt = 0, io_idx = 0, io_val = 0, io_bytes = 0;
+    size_t io_tokens = 0, io_pos = 0, io_bt = 0, io_keys = 0, io_bytes = 0;
     // one captured graph per row count (index rows - 1): the step's launches
     // from the embedding to the argmax, replayed with one hipGraphLaunch
     hipGraph_t graph[4] = {};
@@ -281,8 +281,7 @@ int32_t enqueue_step(cellm_llama_dev* m, int32_t rows)
     const uint32_t* d_tok = reinterpret_cast<const uint32_t*>(dio + m->io_tokens);
     const int32_t* d_pos = reinterpret_cast<const int32_t*>(dio + m->io_pos);
     const uint32_t* d_bt = reinterpret_cast<const uint32_t*>(dio + m->io_bt);
-    int32_t* d_idx = reinterpret_cast<int32_t*>(dio + m->io_idx);
-    float* d_val = reinterpret_cast<float*>(dio + m->io_val);
+    uint64_t* d_keys = reinterpret_cast<uint64_t*>(dio + m->io_keys);
 
     const int64_t R = rows, hid = c.hidden, kvd = (int64_t)m->kvd, inter = c.intermediate, vocab = c.vocab;
     const int64_t L = c.n_layers;
@@ -404,7 +403,8 @@ int32_t enqueue_step(cellm_llama_dev* m, int32_t rows)
     // lm_head (tied embedding or lm_head.weight, llama.rs:522-567), greedy id on the device
     float* lg = m->logits.as<float>();
     if (int32_t rc = run_proj(m, m->lm, xn, lg, R, vocab, hid, "lm_head")) return rc;
-    LIB_TRY(cellm_hip_argmax_f32(H, lg, R, vocab, d_idx, d_val, S), "argmax");
+    // greedy id as a packed key per row (the upload of the step inputs zeroes the keys)
+    LIB_TRY(cellm_hip_argmax_f32_keys(H, lg, R, vocab, d_keys, S), "argmax");
     return CELLM_HIP_OK;
 }
 
@@ -665,9 +665,8 @@ int32_t dev_create_impl(const cellm_llama_config_t* cfg, const HostModel& hm, in
     m->io_tokens = 0;
     m->io_pos = align(R * 4);
     m->io_bt = m->io_pos + align(R * 4);
-    m->io_idx = m->io_bt + align(R * (size_t)max_blocks * 4);
-    m->io_val = m->io_idx + align(R * 4);
-    m->io_bytes = m->io_val + align(R * 4);
+    m->io_keys = m->io_bt + align(R * (size_t)max_blocks * 4);
+    m->io_bytes = m->io_keys + align(R * 8);
     if ((rc = m->io.alloc(m->io_bytes, "hipMalloc(step io)"))) return bail(rc);
     e = hipHostMalloc(&m->host_io, m->io_bytes, hipHostMallocDefault);
     if (e != hipSuccess) {
@@ -1006,7 +1005,8 @@ int32_t cellm_llama_dev_step(cellm_llama_dev_t* m, int32_t rows, const uint32_t*
     memcpy(hio + m->io_tokens, tokens, (size_t)rows * 4);
     memcpy(hio + m->io_pos, positions, (size_t)rows * 4);
     memcpy(hio + m->io_bt, block_tables, (size_t)rows * MB * 4);
-    RT_TRY(hipMemcpyAsync(m->io.p, m->host_io, m->io_idx, hipMemcpyHostToDevice, st), "upload step inputs");
+    memset(hio + m->io_keys, 0, m->io_bytes - m->io_keys);  // the argmax merges into zero keys
+    RT_TRY(hipMemcpyAsync(m->io.p, m->host_io, m->io_bytes, hipMemcpyHostToDevice, st), "upload step inputs");
     if (m->use_graphs) {
         RT_TRY(hipGraphLaunch(m->graph_exec[rows - 1], st), "hipGraphLaunch(step)");
     } else if (int32_t rc = enqueue_step(m, rows)) {
@@ -1014,18 +1014,16 @@ int32_t cellm_llama_dev_step(cellm_llama_dev_t* m, int32_t rows, const uint32_t*
     }
     unsigned char* dio = m->io.as<unsigned char>();
     const float* lg = m->logits.as<float>();
-    RT_TRY(hipMemcpyAsync(hio + m->io_idx, dio + m->io_idx, m->io_bytes - m->io_idx, hipMemcpyDeviceToHost, st),
+    RT_TRY(hipMemcpyAsync(hio + m->io_keys, dio + m->io_keys, m->io_bytes - m->io_keys, hipMemcpyDeviceToHost, st),
            "download ids");
     if (logits_out)
         RT_TRY(hipMemcpyAsync(logits_out, lg, (size_t)rows * c.vocab * 4, hipMemcpyDeviceToHost, st), "download logits");
     RT_TRY(hipStreamSynchronize(st), "step");
     for (int32_t r = 0; r < rows; ++r) {
-        int32_t id;
-        float val;
-        memcpy(&id, hio + m->io_idx + (size_t)r * 4, 4);
-        memcpy(&val, hio + m->io_val + (size_t)r * 4, 4);
-        out_tokens[r] = (uint32_t)id;
-        if (out_logits) out_logits[r] = val;
+        uint64_t key;
+        memcpy(&key, hio + m->io_keys + (size_t)r * 8, 8);
+        out_tokens[r] = (uint32_t)cellm_hip_argmax_key_index(key);
+        if (out_logits) out_logits[r] = cellm_hip_argmax_key_value(key);
     }
     return CELLM_HIP_OK;
     CELLM_API_END(cellm_step::report_exception)

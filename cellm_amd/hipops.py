@@ -54,6 +54,18 @@ def _stream_ptr(stream):
     return C.c_void_p(stream.cuda_stream)
 
 
+def argmax_key_index(key: int) -> int:
+    """Index of a cellm_hip_argmax_f32_keys key (the low word holds 0xffffffff - index)."""
+    return 0xFFFFFFFF - (int(key) & 0xFFFFFFFF)
+
+
+def argmax_key_value(key: int) -> float:
+    """Value of a cellm_hip_argmax_f32_keys key (the high word holds the f32 bits in unsigned order)."""
+    o = (int(key) >> 32) & 0xFFFFFFFF
+    u = (o & 0x7FFFFFFF) if o & 0x80000000 else (~o & 0xFFFFFFFF)
+    return float(np.array([u], np.uint32).view(np.float32)[0])
+
+
 def device_count() -> int:
     lib = _lib.load()
     n = C.c_int32(0)
@@ -536,3 +548,10 @@ class HipOps:
         rows = out_index_i32.numel()
         check(self._lib.cellm_hip_argmax_f32(self._h, _dev_ptr(logits), rows, logits.numel() // rows,
                                              _dev_ptr(out_index_i32), _dev_ptr(out_value), _stream_ptr(stream)))
+
+    def encode_argmax_keys(self, logits, out_keys_i64, stream=None) -> None:
+        """First maximum per row merged into packed keys (int64 tensor, zero before the first call);
+        decode with argmax_key_index / argmax_key_value."""
+        rows = out_keys_i64.numel()
+        check(self._lib.cellm_hip_argmax_f32_keys(self._h, _dev_ptr(logits), rows, logits.numel() // rows,
+                                                  _dev_ptr(out_keys_i64), _stream_ptr(stream)))

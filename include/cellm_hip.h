@@ -516,12 +516,27 @@ int32_t cellm_hip_add_f32_inplace(cellm_hip_ctx_t* ctx, float* x, const float* y
 
 /* topk_from_logits(..)[0] (llama.rs:1049-1078) after the non-finite -> -inf
  * sanitize (llama.rs:1081-1092), per row: the first index of the maximum.
- * One launch of 16384-element chunk blocks per row (rows <= 65535); rows of
+ * One launch of 4096-element chunk blocks per row (rows <= 65535); rows of
  * more than one chunk hand their chunk maxima to the row's last block through
  * the context's per-stream scratch (a few bytes per chunk, allocated on the
  * first call that needs more, counters left at zero by every call). */
 int32_t cellm_hip_argmax_f32(cellm_hip_ctx_t* ctx, const float* logits, int64_t rows, int64_t n, int32_t* out_index,
                              float* out_value, void* stream);
+
+/* The same first maximum (topk_from_logits(..)[0], llama.rs:1049-1092) as a
+ * packed key per row, for callers that read the result on the host anyway
+ * (the greedy decode loop, llama.rs:1049-1078): out_keys[r] = max(out_keys[r],
+ * key of the row's first maximum), one 64-bit atomic max per 4096-element
+ * chunk, so no scratch, counter or combining block.  out_keys must hold zero
+ * before the call (a zero key is below every key; e.g. clear it with the
+ * step's uploaded inputs) and be 8-byte aligned; a repeated call on the same
+ * logits leaves the keys as they are.  Key: high word = the value's bits in
+ * unsigned order (non-finite values taken as -inf, -0 as +0), low word =
+ * 0xffffffff - index; the two calls below decode a key (host only, no device). */
+int32_t cellm_hip_argmax_f32_keys(cellm_hip_ctx_t* ctx, const float* logits, int64_t rows, int64_t n,
+                                  uint64_t* out_keys, void* stream);
+int32_t cellm_hip_argmax_key_index(uint64_t key);
+float cellm_hip_argmax_key_value(uint64_t key);
 
 /* ---- .cellm model files -----------------------------------------------------
  * CellmFile (crates/cellm-model/src/cellm_file.rs:58-146): "CELLM", version 1,

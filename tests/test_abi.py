@@ -214,3 +214,31 @@ def test_step_library_exports_its_header():
 def test_every_header_is_checked():
     headers = {p.name for p in (ROOT / "include").glob("*.h")}
     assert headers == {"cellm_hip.h", "cellm_llama_step.h"}, headers
+
+
+def test_argmax_key_decoding():
+    """cellm_hip_argmax_f32_keys keys decode as documented (high word: f32 bits in unsigned order,
+    non-negative values with the sign bit set, negative ones inverted; low word: 0xffffffff - index),
+    in the library and in the Python helper alike; the order of such keys is the order of the
+    values, then of the lower index."""
+    from cellm_amd import _lib
+    from cellm_amd.hipops import argmax_key_index, argmax_key_value
+
+    lib = _lib.load()
+    cases = [  # (key, value, index)
+        ((0xBF800000 << 32) | 0xFFFFFFFA, 1.0, 5),              # 1.0 = 0x3f800000 | sign bit
+        ((0x3FFFFFFF << 32) | 0xFFFFFFFF, -2.0, 0),             # -2.0 = 0xc0000000, inverted
+        ((0x007FFFFF << 32) | 0x00000000, float("-inf"), 0xFFFFFFFF),  # -inf = 0xff800000, inverted
+        ((0x80000000 << 32) | 0xFFFF0000, 0.0, 0xFFFF),         # +0 (and -0, taken as +0)
+        ((0xFF7FFFFF << 32) | 0xFFFFFF00, 3.4028234663852886e38, 0xFF),  # largest finite f32
+    ]
+    for key, val, idx in cases:
+        want_idx = idx - (1 << 32) if idx >= 1 << 31 else idx
+        assert lib.cellm_hip_argmax_key_index(key) == want_idx
+        assert lib.cellm_hip_argmax_key_value(key) == val
+        assert argmax_key_index(key) == idx
+        assert argmax_key_value(key) == val
+    # ordering: values ascending give keys ascending; at equal values the lower index gives the larger key
+    ordered = sorted(cases[:4], key=lambda c: c[0])
+    assert [c[1] for c in ordered] == sorted(c[1] for c in cases[:4])
+    assert ((0xBF800000 << 32) | (0xFFFFFFFF - 3)) > ((0xBF800000 << 32) | (0xFFFFFFFF - 4))

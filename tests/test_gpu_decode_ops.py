@@ -317,6 +317,53 @@ def test_argmax_first_and_non_finite(ops, n):
         assert got[1] == 100 and got[4] == n - 2
 
 
+@pytest.mark.parametrize("n", [49152, 49151, 151936, 262144, 4097, 1000])
+def test_argmax_keys_first_and_non_finite(ops, n):
+    """The packed-key argmax (one 64-bit atomic max per 4096-element chunk) gives the oracle's first
+    maximum: ties inside and across chunks keep the first index, NaN and +-inf count as -inf, an
+    all -inf row gives index 0, -0 and +0 are equal (the first of them wins), the maximum in the
+    ragged last chunk; a second call on the same keys leaves them unchanged."""
+    rows = np.stack([oracle.gen_normal((n,), 0xD00000B0 + r, 0.0, 1.0) for r in range(6)]).astype(np.float32)
+    rows[1, 100] = rows[1, min(40000, n - 1)] = 50.0
+    rows[2, 7] = np.nan
+    rows[2, 9] = np.inf
+    rows[3, :] = -np.inf
+    rows[4, n - 1] = 60.0
+    rows[4, n - 2] = 60.0
+    rows[5, :] = -np.abs(rows[5, :]) - 1.0
+    rows[5, 3] = -0.0
+    rows[5, min(5000, n - 1)] = 0.0                    # +0 after -0: equal, index 3 wins
+    keys = torch.zeros(6, dtype=torch.int64, device="cuda")
+    d = dev(rows)
+    from cellm_amd.hipops import argmax_key_index, argmax_key_value
+    for call in range(3):
+        if call != 2:
+            keys.zero_()
+        ops.encode_argmax_keys(d, keys)
+        torch.cuda.synchronize()
+        got = [int(k) & 0xFFFFFFFFFFFFFFFF for k in keys.cpu().numpy()]
+        for r in range(6):
+            z = rows[r].copy()
+            z[~np.isfinite(z)] = -np.inf
+            i = argmax_key_index(got[r])
+            assert i == oracle.argmax_first(z), (r, i)
+            assert argmax_key_value(got[r]) == z[i], r
+        assert argmax_key_index(got[1]) == 100 and argmax_key_index(got[4]) == n - 2
+        assert argmax_key_index(got[5]) == 3
+
+
+def test_argmax_keys_refusals(ops):
+    """Keys that are not 8-byte aligned and empty rows are refused before any launch."""
+    from cellm_amd._lib import CellmHipError
+    d = torch.zeros((2, 64), dtype=torch.float32, device="cuda")
+    k = torch.zeros(3, dtype=torch.int64, device="cuda")
+    rc = ops._lib.cellm_hip_argmax_f32_keys(ops._h, C.c_void_p(d.data_ptr()), 2, 64, C.c_void_p(k.data_ptr() + 4),
+                                            None)
+    assert rc != 0
+    with pytest.raises(CellmHipError):
+        ops.encode_argmax_keys(torch.zeros((2, 0), dtype=torch.float32, device="cuda"), k[:2])
+
+
 def test_add_inplace(ops):
     a = oracle.gen_normal((5000,), 0xD00000A0, 0.0, 1.0).astype(np.float32)
     b = oracle.gen_normal((5000,), 0xD00000A1, 0.0, 1.0).astype(np.float32)
