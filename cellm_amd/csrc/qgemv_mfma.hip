@@ -598,21 +598,34 @@ hipError_t launch_mfma_nt(const void* W, const void* S, const void* B, int per_c
     } else if (KC < K) {
         launch(qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, true, false>, ROWS, lds);
     } else {
-        // Few tiles over a K that takes a wave several load groups: the block's waves share one
-        // tile row group and split its K (WK = 4 or 2), adding their sums through LDS.
+        // Few tiles over a K that takes a wave several load groups, or fewer 64-row tiles than CUs:
+        // the block's waves share one tile row group and split its K (WK = 4 or 2), adding their sums
+        // through LDS.  A wave's load group is no deeper than its share of the block pairs: a group
+        // deeper than the share re-reads its last pair for every missing one (measured on MI355X at
+        // M = 8..32: q4 1024->4096 7.8 -> 4.9 us, 896->4864 6.7 -> 5.5 us, int8 1024->1152 5.0 -> 4.6
+        // us; the same split with 4-pair groups was slower than no split).
         const int npairs = (K / KB) >> 1, groups = (npairs + DEPTH - 1) / DEPTH;
         int wk = 1;
         if constexpr (NT == 1) {
+            const int cus = device_cus();
             for (int cand : {4, 2})
-                if (groups > 1 && npairs >= cand && (N + (4 / cand) * 16 - 1) / ((4 / cand) * 16) <= 2 * device_cus()) {
+                if ((groups > 1 || ntiles < cus) && npairs >= cand &&
+                    (N + (4 / cand) * 16 - 1) / ((4 / cand) * 16) <= 2 * cus) {
                     wk = cand;
                     break;
                 }
         }
         const size_t red = (size_t)(wk - 1) * (4 / wk) * MS * NT * 64 * 16;
         if constexpr (NT == 1) {
-            if (wk == 4) launch(qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, false, false, kBlock, 4>, 16, lds + red);
-            if (wk == 2) launch(qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, false, false, kBlock, 2>, 32, lds + red);
+            const int share = (npairs + wk - 1) / wk;  // block pairs per wave
+            if (wk == 4) {
+                if (share <= 1) launch(qgemv_mfma_kernel<WT, MS, NT, 1, SBT, false, false, kBlock, 4>, 16, lds + red);
+                else if (share <= 2) launch(qgemv_mfma_kernel<WT, MS, NT, 2, SBT, false, false, kBlock, 4>, 16, lds + red);
+                else launch(qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, false, false, kBlock, 4>, 16, lds + red);
+            } else if (wk == 2) {
+                if (share <= 2) launch(qgemv_mfma_kernel<WT, MS, NT, 2, SBT, false, false, kBlock, 2>, 32, lds + red);
+                else launch(qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, false, false, kBlock, 2>, 32, lds + red);
+            }
         }
         if (wk == 1) launch(qgemv_mfma_kernel<WT, MS, NT, DEPTH, SBT, false, false>, ROWS, lds);
     }
