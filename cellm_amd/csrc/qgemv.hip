@@ -987,6 +987,11 @@ __device__ __forceinline__ void compute_pass_i8_f16x(int c0, int CPR, const uint
     }
 }
 
+// f32 x in LDS: 4 floats of padding after every 16 (K % 16 == 0, so each row starts padded too).  A
+// lane's 16-float chunk then starts 80 bytes after its neighbour's, and the 16-byte reads of 8
+// lanes fall on 32 distinct banks (unpadded, 64 bytes apart, they met 4-way conflicts).
+__host__ __device__ constexpr int i8_xpad(int e) { return e + (e >> 4) * 4; }
+
 template <int LPR, int R, int MT>
 __device__ __forceinline__ void compute_pass_i8_f32x(int c0, int CPR, int K, const float* xs,
                                                      const u4_t (&wv)[kUnroll][R], float (&acc)[R][MT])
@@ -997,7 +1002,7 @@ __device__ __forceinline__ void compute_pass_i8_f32x(int c0, int CPR, int K, con
         if (c < CPR) {
 #pragma unroll
             for (int m = 0; m < MT; ++m) {
-                const f4_t* xp = reinterpret_cast<const f4_t*>(xs + (size_t)m * K + (size_t)c * 16);
+                const f4_t* xp = reinterpret_cast<const f4_t*>(xs + i8_xpad(m * K + c * 16));
                 const f4_t x0 = xp[0], x1 = xp[1], x2 = xp[2], x3 = xp[3];
                 const float xv[16] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3],
                                       x2[0], x2[1], x2[2], x2[3], x3[0], x3[1], x3[2], x3[3]};
@@ -1063,17 +1068,18 @@ __device__ __forceinline__ void i8_stage_x(const u4_t (&xr)[XW], const void* __r
             stage_unit_i8(raw, idx, idx < total, xq, cx);
         }
     } else {
+        // f32 x: element e of the [MT][K] rows at e + 4 (e / 16) (i8_xpad)
 #pragma unroll
         for (int j = 0; j < XW; ++j) {
             const int idx = (int)threadIdx.x + j * kBlock;
-            if (idx < total) *reinterpret_cast<u4_t*>(xq + (size_t)idx * 4) = xr[j];
+            if (idx < total) *reinterpret_cast<u4_t*>(xq + i8_xpad(idx * 4)) = xr[j];
         }
         for (int b0 = XW * kBlock; b0 < total; b0 += kBlock) {
             const int idx = b0 + (int)threadIdx.x;
             const int m = idx / units;
             const float* xf = reinterpret_cast<const float*>(xv);
             if (idx < total)
-                *reinterpret_cast<u4_t*>(xq + (size_t)idx * 4) =
+                *reinterpret_cast<u4_t*>(xq + i8_xpad(idx * 4)) =
                     m < M ? *reinterpret_cast<const u4_t*>(xf + (size_t)m * K + (size_t)(idx - m * units) * 4)
                           : u4_t{0u, 0u, 0u, 0u};
         }
@@ -1140,28 +1146,25 @@ __global__ __launch_bounds__(kBlock) void qgemv_i8_kernel(
         }
     }
 
+    // the team's R * MT sums reduced transposed: lane l ends with value team_sum_t_index(l), and
+    // one lane per value applies the row's scale (and bias) and stores
+    static_assert(R == 1 || R == 2, "one or two rows per team");
+    constexpr int V = R * MT;
+    float a[V];
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
-        for (int m = 0; m < MT; ++m) acc[r][m] = group_sum<LPR>(acc[r][m]);
-
-    if (lane == 0) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const int n = row0 + r;
-            if (n < N) {
-                const float s = sdt == DT_F32 ? raw_to_f32<DT_F32>(sraw[r])
-                              : sdt == DT_F16 ? raw_to_f32<DT_F16>(sraw[r])
-                                              : raw_to_f32<DT_BF16>(sraw[r]);
-#pragma unroll
-                for (int m = 0; m < MT; ++m)
-                    if (m < M) {
-                        float v = acc[r][m] * s;
-                        if (bias) v += bv[r];
-                        y[(size_t)m * N + n] = v;
-                    }
-            }
-        }
+        for (int m = 0; m < MT; ++m) a[r * MT + m] = acc[r][m];
+    const float tot = team_sum_t<LPR, V>(a);
+    const int vi = team_sum_t_index<LPR, V>(lane), r = vi / MT, m = vi % MT, n = row0 + r;
+    if ((lane & (LPR / V - 1)) == 0 && m < M && n < N) {
+        const uint32_t sr = R == 1 || r == 0 ? sraw[0] : sraw[R - 1];
+        const float s = sdt == DT_F32 ? raw_to_f32<DT_F32>(sr)
+                      : sdt == DT_F16 ? raw_to_f32<DT_F16>(sr)
+                                      : raw_to_f32<DT_BF16>(sr);
+        float v = tot * s;
+        if (bias) v += R == 1 || r == 0 ? bv[0] : bv[R - 1];
+        y[(size_t)m * N + n] = v;
     }
 }
 
@@ -1661,7 +1664,7 @@ hipError_t launch_i8_xt(const int8_t* w, const void* S, int sdt, int per_channel
     const int rows_per_block = (kBlock / LPR) * R;
     const dim3 grid((N + rows_per_block - 1) / rows_per_block);
     const u4_t* w4 = reinterpret_cast<const u4_t*>(w);
-    const size_t lds = XT == DT_F16 ? (size_t)MT * CPR * 8 * 4 + (size_t)MT * CPR * 4 : (size_t)MT * K * 4;
+    const size_t lds = XT == DT_F16 ? (size_t)MT * CPR * 8 * 4 + (size_t)MT * CPR * 4 : (size_t)i8_xpad(MT * K) * 4;
     if (CPR > kUnroll * LPR) {
         auto kern = qgemv_i8_kernel<LPR, R, MT, XT, true>;
         if (lds > 64 * 1024)
@@ -1702,7 +1705,7 @@ hipError_t launch_i8_fused_lpr(const I8Segs& t, int total_rows, int sdt, const v
     const int CPR = K >> 4;
     const int rows_per_block = (kBlock / LPR) * (SILU ? 1 : 2);
     const dim3 grid((total_rows + rows_per_block - 1) / rows_per_block);
-    const size_t lds = XT == DT_F16 ? (size_t)MT * CPR * 8 * 4 + (size_t)MT * CPR * 4 : (size_t)MT * K * 4;
+    const size_t lds = XT == DT_F16 ? (size_t)MT * CPR * 8 * 4 + (size_t)MT * CPR * 4 : (size_t)i8_xpad(MT * K) * 4;
     if (CPR > kUnroll * LPR)
         hipLaunchKernelGGL((qgemv_i8_fused_kernel<LPR, MT, XT, true, SILU>), grid, dim3(kBlock), lds, st, t, sdt, x, M,
                            total_rows, K);
@@ -2010,7 +2013,7 @@ hipError_t launch_qgemv_i8(const int8_t* w, const void* S, int sdt, int per_chan
                            const float* bias, float* y, int M, int N, int K, hipStream_t st, int force_generic)
 {
     const int MT = M <= 1 ? 1 : (M <= 2 ? 2 : 4);
-    const size_t lds = xdt == DT_F16 ? (size_t)MT * (K >> 4) * 36 : (size_t)MT * K * 4;
+    const size_t lds = xdt == DT_F16 ? (size_t)MT * (K >> 4) * 36 : (size_t)i8_xpad(MT * K) * 4;
     // x past 64 KB of LDS (f32 x of long rows at M > 1) takes the per-kernel limit raised to 160 KB
     const bool fast = !force_generic && (xdt == DT_F16 || xdt == DT_F32) && M <= 4 && (K % 16) == 0 &&
                       aligned16(w) && aligned16(x) && lds <= 160 * 1024;
@@ -2164,7 +2167,7 @@ bool qgemv_i8_fused_supported(int xdt, int M, int K, const void* x, const I8Fuse
 {
     if (!(xdt == DT_F16 || xdt == DT_F32) || M < 1 || M > 4 || K <= 0 || (K % 16) != 0 || !aligned16(x)) return false;
     const int MT = M <= 1 ? 1 : (M <= 2 ? 2 : 4);
-    const size_t lds = xdt == DT_F16 ? (size_t)MT * (K >> 4) * 36 : (size_t)MT * K * 4;
+    const size_t lds = xdt == DT_F16 ? (size_t)MT * (K >> 4) * 36 : (size_t)i8_xpad(MT * K) * 4;
     if (lds > 64 * 1024) return false;
     for (int i = 0; i < nseg; ++i)
         if (!aligned16(segs[i].w)) return false;
