@@ -208,6 +208,10 @@ int32_t get_stream_buffer(cellm_hip_ctx* ctx, std::unordered_map<hipStream_t, De
 // 2..4 activation rows (measured on MI355X: 1152->13824 q4 at m=4 7.6 vs 10.3 us;
 // 960->2560 int8 at m=4 7.2 vs 4.6 us).
 constexpr int64_t kMfmaMinRows = 8192;
+#ifndef CELLM_I8FX_MIN_M
+#define CELLM_I8FX_MIN_M 3
+#endif
+constexpr int64_t kI8F32xMfmaMinM = CELLM_I8FX_MIN_M;  // rows from which the int8 f32-x MFMA path runs
 // Output rows from which the f32-x q4 GEMV runs on MFMA (the VALU kernels do the dot twice,
 // once per f16 part of x; the MFMA form reads each weight once and is HBM-bound).
 constexpr int64_t kF32xMfmaMinRows = 32768;
@@ -251,6 +255,15 @@ int32_t qgemv_i8_impl(cellm_hip_ctx* ctx, const int8_t* w, const void* scales, i
         return CELLM_HIP_OK;
     }
     if (force_gemm) return set_error(CELLM_HIP_ERR_UNSUPPORTED, "qgemm_i8 needs f16 x, k %% 64 == 0, 16-byte alignment");
+    // f32 x over a long output at several rows (the Llama lm_head of a multi-session step,
+    // llama.rs:602-643): exact integer sums on int8 MFMA over three x digits per row
+    if (xdt == DT_F32 && m >= kI8F32xMfmaMinM && n >= kF32xMfmaMinRows && aligned16(w) && aligned16(x) &&
+        qgemv_i8_f32x_mfma_supported((int)m, (int)n, (int)k)) {
+        HIP_TRY(launch_qgemv_i8_f32x_mfma(w, scales, sdt, per_channel, bias, static_cast<const float*>(x), y, (int)m,
+                                          (int)n, (int)k, st),
+                "qgemv_i8_f32x_mfma launch");
+        return CELLM_HIP_OK;
+    }
     HIP_TRY(launch_qgemv_i8(w, scales, sdt, per_channel, x, xdt, bias, y, (int)m, (int)n, (int)k, st, k == 0),
             "qgemv_i8 launch");
     return CELLM_HIP_OK;

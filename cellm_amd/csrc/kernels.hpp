@@ -98,6 +98,11 @@ size_t qgemv_mfma_workspace_bytes(int wt, int M, int N, int K);
 // group 64; 16-byte aligned W and x): nibbles as exact f16 integers, x as hi + lo f16
 // parts scaled per (row, group) by a power of two, scale and bias folded per group.
 bool qgemv_q4_f32x_mfma_supported(int M, int N, int K, int group_size);
+// int8 rows over f32 x on int8 MFMA (x as three 8-bit digits per row, one power of two per row; the
+// row scale after the exact integer sums): M <= 4, N % 16 == 0, K % 64 == 0, 128 <= K <= 1024.
+bool qgemv_i8_f32x_mfma_supported(int M, int N, int K);
+hipError_t launch_qgemv_i8_f32x_mfma(const int8_t* w, const void* S, int sdt, int per_channel, const float* bias,
+                                     const float* x, float* y, int M, int N, int K, hipStream_t st);
 hipError_t launch_qgemv_q4_f32x_mfma(const uint32_t* wq, const void* S, const void* B, int sbt, const float* x,
                                      float* y, int M, int N, int K, hipStream_t st);
 hipError_t launch_qgemv_mfma_i8(const int8_t* w, const void* S, int sdt, int per_channel, const _Float16* x,

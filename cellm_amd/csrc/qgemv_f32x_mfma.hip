@@ -244,6 +244,175 @@ __global__ __launch_bounds__(kFxThreads) void qgemv_q4_f32x_mfma_kernel(const ui
     }
 }
 
+// ---- int8 rows, f32 x: y[m,n] = (sum_k w[n,k] x[m,k]) * s[n] (+ bias[n])
+// (crates/cellm-kernels/src/cpu_kernels.rs:66-133, matmul_i8_f32 per row; the Llama lm_head loop
+// llama.rs:602-643 at several sessions).  The same three-digit x rows as above, and the int8
+// weights are the B bytes as they are: a lane (column n = lane%16, slot group g = lane/16) holds
+// 16 bytes of its row per 64-k block, k = 64b + 16g .. +15 in natural order, and A is staged in
+// that order.  No group scale splits the sum, so each digit row accumulates over the whole K in
+// one i32 accumulator: |d| <= 64, |w| <= 127, K <= 1024 keep every partial sum below 2^23, so it
+// converts to f32 exactly, and the row scale is applied once, after the sum, as the reference
+// does.  y = s * 2^-sh * (2^14 Y_0 + 2^7 Y_1 + Y_2).
+constexpr int kI8FxMaxK = 1024;
+
+template <int NB>
+struct I8FxTile {
+    u4_t w[NB / 2 > 0 ? NB / 2 : 1][2];
+    u4_t tail;
+    uint32_t s;
+    float bias;
+};
+
+template <int SBT, int NB>
+__global__ __launch_bounds__(kFxThreads) void qgemv_i8_f32x_mfma_kernel(const int8_t* __restrict__ W,
+                                                                        const void* __restrict__ S, int per_channel,
+                                                                        const float* __restrict__ bias,
+                                                                        const float* __restrict__ X,
+                                                                        float* __restrict__ Y, int M, int N)
+{
+    constexpr int K = NB * 64, NP = NB / 2, astride = K + kFxAPad;
+    extern __shared__ __align__(16) unsigned char smem[];
+    int8_t* A = reinterpret_cast<int8_t*>(smem);                         // [16 digit rows][astride] bytes
+    float* P2 = reinterpret_cast<float*>(smem + (size_t)16 * astride);  // [4]: 2^-sh per x row
+    uint32_t* RMAX = reinterpret_cast<uint32_t*>(P2 + 4);                // [4]: bits of the row's max |x|
+    float* wave_out = reinterpret_cast<float*>(RMAX + 4);                // [waves][16][16]: a tile's digit sums
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int rl = lane & 15, g = lane >> 4;
+    const int ntiles = N >> 4, stride = gridDim.x * kFxWaves;
+    constexpr uint32_t row_bytes = K;
+    const auto wr = buffer_rsrc(const_cast<int8_t*>(W), (uint32_t)ntiles * 16u * row_bytes);
+    const bool low8 = (rl & 8) == 0;
+
+    // a tile's loads: 16 rows as full 128-byte row segments (two 64-k blocks; load h covers rows
+    // 8h..8h+7, lane (rl, g) taking row (rl & 7) + 8h at byte 16g + 64((rl >> 3) ^ h)), the odd
+    // last block, the row's scale and bias; a tile past the end loads through an out-of-range
+    // buffer offset (zeros, no traffic) so every iteration issues the same loads
+    auto load_tile = [&](I8FxTile<NB>& t, int tile) {
+        const bool live = tile < ntiles;
+        const int n0 = min(tile, ntiles - 1) * 16;
+#pragma unroll
+        for (int p = 0; p < NP; ++p)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t off = (uint32_t)(n0 + (rl & 7) + 8 * h) * row_bytes + 128 * p + 16 * g + 64 * ((rl >> 3) ^ h);
+                t.w[p][h] = __builtin_bit_cast(u4_t, __builtin_amdgcn_raw_buffer_load_b128(wr, live ? off : kBufferDrop, 0, 2));
+            }
+        if constexpr (NB & 1) {
+            const uint32_t off = (uint32_t)(n0 + rl) * row_bytes + 64 * (NB - 1) + 16 * g;
+            t.tail = __builtin_bit_cast(u4_t, __builtin_amdgcn_raw_buffer_load_b128(wr, live ? off : kBufferDrop, 0, 2));
+        }
+        t.s = load_raw<SBT>(S, per_channel ? (size_t)(n0 + rl) : 0);
+        const float b = *(bias ? bias + n0 + rl : X);  // unconditional load (X when there is no bias)
+        t.bias = bias ? b : 0.0f;
+    };
+
+    int tile = blockIdx.x * kFxWaves + wave;
+    I8FxTile<NB> ta, tb;
+    load_tile(ta, tile);  // in flight while X is staged
+
+    // ---- X as digit rows in natural k order: item i = m * (K / 16) + r is 16 k of row m
+    for (int i = threadIdx.x; i < (16 - 3 * M) * (astride >> 4); i += kFxThreads)
+        reinterpret_cast<u4_t*>(A + (size_t)3 * M * astride)[i] = u4_t{0u, 0u, 0u, 0u};
+    if (threadIdx.x < 4) RMAX[threadIdx.x] = 0u;
+    const int items = M * (K / 16), it = min((int)threadIdx.x, items - 1);
+    const int im = it / (K / 16), ir = it - im * (K / 16);
+    float xv[16];
+    {
+        const f4_t* r0 = reinterpret_cast<const f4_t*>(X + (size_t)im * K + 16 * ir);
+        const f4_t a0 = r0[0], a1 = r0[1], a2 = r0[2], a3 = r0[3];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            xv[j] = a0[j];
+            xv[4 + j] = a1[j];
+            xv[8 + j] = a2[j];
+            xv[12 + j] = a3[j];
+        }
+    }
+    float mx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) mx = fmaxf(mx, fabsf(xv[j]));
+    __syncthreads();  // RMAX cleared
+    if ((int)threadIdx.x < items) atomicMax(&RMAX[im], __builtin_bit_cast(uint32_t, mx));  // |x| >= 0: bits order as values
+    __syncthreads();
+    if ((int)threadIdx.x < items) {
+        const float rmax = __builtin_bit_cast(float, RMAX[im]);
+        int e = 0;
+        (void)__builtin_frexpf(rmax, &e);
+        const int sh = (rmax > 0.0f && rmax <= 3.402823466e38f) ? min(20 - e, 140) : 0;
+        uint32_t dw[3][4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            uint32_t b0 = 0, b1 = 0, b2 = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float xp = rintf(__builtin_ldexpf(xv[4 * q + j], sh));  // |xp| <= 2^20
+                const float d0 = rintf(xp * 0.00006103515625f);             // / 2^14
+                const float r = xp - d0 * 16384.0f;                          // |r| <= 2^13
+                const float d1 = rintf(r * 0.0078125f);                      // / 2^7
+                const float d2 = r - d1 * 128.0f;
+                b0 |= ((uint32_t)(int)d0 & 0xFFu) << (8 * j);
+                b1 |= ((uint32_t)(int)d1 & 0xFFu) << (8 * j);
+                b2 |= ((uint32_t)(int)d2 & 0xFFu) << (8 * j);
+            }
+            dw[0][q] = b0;
+            dw[1][q] = b1;
+            dw[2][q] = b2;
+        }
+#pragma unroll
+        for (int d = 0; d < 3; ++d)
+            *reinterpret_cast<u4_t*>(A + (size_t)(d * M + im) * astride + 16 * ir) = u4_t{dw[d][0], dw[d][1], dw[d][2], dw[d][3]};
+        if (ir == 0) P2[im] = __builtin_ldexpf(1.0f, -sh);
+    }
+    __syncthreads();
+    if (tile >= ntiles) return;
+
+    float* otw = wave_out + wave * 256;  // [16 digit rows][16 columns]
+    const int8_t* arow = A + (size_t)rl * astride + 16 * g;
+
+    auto compute = [&](const I8FxTile<NB>& t, int n0) {
+        i4_t acc = {0, 0, 0, 0};
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            u4_t w0, w1;
+            const u4_t a = t.w[p][0], b = t.w[p][1];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                w0[j] = low8 ? a[j] : b[j];
+                w1[j] = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(low8 ? b[j] : a[j]), 0x128, 0xF, 0xF, false);
+            }
+            const i4_t x0 = *reinterpret_cast<const i4_t*>(arow + 128 * p);
+            const i4_t x1 = *reinterpret_cast<const i4_t*>(arow + 128 * p + 64);
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(x0, __builtin_bit_cast(i4_t, w0), acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(x1, __builtin_bit_cast(i4_t, w1), acc, 0, 0, 0);
+        }
+        if constexpr (NB & 1) {
+            const i4_t x0 = *reinterpret_cast<const i4_t*>(arow + 64 * (NB - 1));
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(x0, __builtin_bit_cast(i4_t, t.tail), acc, 0, 0, 0);
+        }
+        // lane (rl, g) holds digit rows 4g..4g+3 of column n0 + rl; the three digits of x row m
+        // meet through the wave's LDS tile
+#pragma unroll
+        for (int e = 0; e < 4; ++e) otw[(4 * g + e) * 16 + rl] = (float)acc[e];  // exact: |acc| < 2^23
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (g < M) {
+            const float v = P2[g] * (16384.0f * otw[g * 16 + rl] + (128.0f * otw[(M + g) * 16 + rl] + otw[(2 * M + g) * 16 + rl]));
+            Y[(size_t)g * N + n0 + rl] = v * raw_to_f32<SBT>(t.s) + t.bias;
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // before the next tile's writes
+    };
+
+    for (;;) {
+        load_tile(tb, tile + stride);
+        compute(ta, tile * 16);
+        tile += stride;
+        if (tile >= ntiles) break;
+        load_tile(ta, tile + stride);
+        compute(tb, tile * 16);
+        tile += stride;
+        if (tile >= ntiles) break;
+    }
+}
+
 int fx_device_cus()
 {
     static std::mutex mu;
@@ -293,6 +462,45 @@ hipError_t launch_fx(const uint32_t* wq, const void* S, const void* B, const flo
     }
 }
 
+template <int SBT, int NB>
+hipError_t launch_i8fx_nb(const int8_t* w, const void* S, int per_channel, const float* bias, const float* x, float* y,
+                          int M, int N, hipStream_t st)
+{
+    auto kern = qgemv_i8_f32x_mfma_kernel<SBT, NB>;
+    const size_t lds = (size_t)16 * (NB * 64 + kFxAPad) + 32 + (size_t)kFxWaves * 256 * 4;
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kFxThreads, lds) != hipSuccess || per_cu < 1)
+        per_cu = 1;
+    const int ntiles = N / 16, waves = per_cu * fx_device_cus() * kFxWaves;
+    const int rounds = (ntiles + waves - 1) / waves;
+    const int grid = std::max(1, ((ntiles + rounds - 1) / rounds + kFxWaves - 1) / kFxWaves);
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(kFxThreads), lds, st, w, S, per_channel, bias, x, y, M, N);
+    return hipGetLastError();
+}
+
+template <int SBT>
+hipError_t launch_i8fx(const int8_t* w, const void* S, int per_channel, const float* bias, const float* x, float* y,
+                       int M, int N, int K, hipStream_t st)
+{
+    switch (K / 64) {
+    case 2: return launch_i8fx_nb<SBT, 2>(w, S, per_channel, bias, x, y, M, N, st);
+    case 3: return launch_i8fx_nb<SBT, 3>(w, S, per_channel, bias, x, y, M, N, st);
+    case 4: return launch_i8fx_nb<SBT, 4>(w, S, per_channel, bias, x, y, M, N, st);
+    case 5: return launch_i8fx_nb<SBT, 5>(w, S, per_channel, bias, x, y, M, N, st);
+    case 6: return launch_i8fx_nb<SBT, 6>(w, S, per_channel, bias, x, y, M, N, st);
+    case 7: return launch_i8fx_nb<SBT, 7>(w, S, per_channel, bias, x, y, M, N, st);
+    case 8: return launch_i8fx_nb<SBT, 8>(w, S, per_channel, bias, x, y, M, N, st);
+    case 9: return launch_i8fx_nb<SBT, 9>(w, S, per_channel, bias, x, y, M, N, st);
+    case 10: return launch_i8fx_nb<SBT, 10>(w, S, per_channel, bias, x, y, M, N, st);
+    case 11: return launch_i8fx_nb<SBT, 11>(w, S, per_channel, bias, x, y, M, N, st);
+    case 12: return launch_i8fx_nb<SBT, 12>(w, S, per_channel, bias, x, y, M, N, st);
+    case 13: return launch_i8fx_nb<SBT, 13>(w, S, per_channel, bias, x, y, M, N, st);
+    case 14: return launch_i8fx_nb<SBT, 14>(w, S, per_channel, bias, x, y, M, N, st);
+    case 15: return launch_i8fx_nb<SBT, 15>(w, S, per_channel, bias, x, y, M, N, st);
+    default: return launch_i8fx_nb<SBT, 16>(w, S, per_channel, bias, x, y, M, N, st);
+    }
+}
+
 }  // namespace
 
 bool qgemv_q4_f32x_mfma_supported(int M, int N, int K, int group_size)
@@ -308,6 +516,22 @@ hipError_t launch_qgemv_q4_f32x_mfma(const uint32_t* wq, const void* S, const vo
     if (sbt == DT_F16) return launch_fx<DT_F16>(wq, S, B, x, y, M, N, K, st);
     if (sbt == DT_F32) return launch_fx<DT_F32>(wq, S, B, x, y, M, N, K, st);
     return launch_fx<DT_BF16>(wq, S, B, x, y, M, N, K, st);
+}
+
+bool qgemv_i8_f32x_mfma_supported(int M, int N, int K)
+{
+    // one X item per thread (M * K / 16 <= 512 threads) and the weights' buffer range below 2^31
+    return M >= 1 && M <= 4 && N >= 16 && N % 16 == 0 && K >= 128 && K <= kI8FxMaxK && K % 64 == 0 &&
+           (size_t)N * K < ((size_t)1 << 31);
+}
+
+hipError_t launch_qgemv_i8_f32x_mfma(const int8_t* w, const void* S, int sdt, int per_channel, const float* bias,
+                                     const float* x, float* y, int M, int N, int K, hipStream_t st)
+{
+    if (!qgemv_i8_f32x_mfma_supported(M, N, K)) return hipErrorInvalidValue;
+    if (sdt == DT_F16) return launch_i8fx<DT_F16>(w, S, per_channel, bias, x, y, M, N, K, st);
+    if (sdt == DT_F32) return launch_i8fx<DT_F32>(w, S, per_channel, bias, x, y, M, N, K, st);
+    return launch_i8fx<DT_BF16>(w, S, per_channel, bias, x, y, M, N, K, st);
 }
 
 }  // namespace cellm

@@ -116,7 +116,13 @@ int32_t cellm_hip_weight_cache_stats(cellm_hip_ctx_t* ctx, size_t* out_entries, 
  * GEMV; larger m with f16 x and k % 64 == 0 runs the MFMA GEMM.  With few
  * output rows over a long k, 2..64 rows split k over work items whose partial
  * sums go to the context's per-stream workspace (grown on demand, as for the
- * split-K qGEMM) and a second kernel adds them in a fixed order. */
+ * split-K qGEMM) and a second kernel adds them in a fixed order.  f32 x at
+ * 3..4 rows over a long output (n >= 32768, n % 16 == 0, k % 64 == 0,
+ * 128 <= k <= 1024, 16-byte aligned w and x: a multi-session lm_head) runs on
+ * int8 MFMA: each x row becomes x' = rint(x * 2^e) with |x'| <= 2^20 for the
+ * row's power of two, split into three signed 8-bit digits; the integer sums
+ * over k are exact and the row scale follows them, so x keeps 2^-20 of its
+ * row's largest |x| (within 3e-5 normwise of the f32 reference order). */
 int32_t cellm_hip_qgemv_i8(cellm_hip_ctx_t* ctx, const int8_t* w, const void* scales, int32_t scale_dtype,
                            int64_t n_scales, const void* x, int32_t x_dtype, const float* bias, float* y, int64_t m,
                            int64_t n, int64_t k, void* stream);

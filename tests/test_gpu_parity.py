@@ -239,6 +239,49 @@ def test_i8_gemv_f32x_long_rows(ops, k, m):
     assert rel_err(y, ref) <= TOL_F32
 
 
+@pytest.mark.parametrize("n,k,m,sdt", [
+    (49152, 960, 4, np.float16),    # the configs[4] lm_head at four sessions (f16 row scales)
+    (49152, 960, 2, np.float32),
+    (32768, 128, 3, np.float32),    # two 64-k blocks: one block pair
+    (32768, 192, 4, np.float16),    # three blocks: a pair and an odd one
+    (40000, 1024, 2, np.float32),   # the longest K; N not a multiple of 64
+    (32768, 576, 4, np.float32),
+])
+def test_i8_f32x_long_output_mfma(ops, n, k, m, sdt):
+    """f32 activations at 2..4 rows over a long output (the Llama lm_head of a multi-session step,
+    llama.rs:602-643): int8 weights as the B bytes of int8 MFMA, each x row as three signed 8-bit
+    digits under one power of two per row, exact integer sums over the whole K, the row scale
+    after the sum.  Every row within 3e-5 of the f32 reference order, which one f16 rounding of x
+    would miss."""
+    w, s, x = make_i8(n, k, m, cfg=5, scale_dtype=sdt, x_dtype=np.float32, salt=300 + m + k % 97)
+    y = _run_i8(ops, w, s, x)
+    ref = oracle.qgemv_i8(w, s, x)
+    for r in range(m):
+        assert rel_err(y[r], ref[r]) <= 3e-5, (r, rel_err(y[r], ref[r]))
+    xr = x.astype(np.float16).astype(np.float32)
+    assert rel_err(oracle.qgemv_i8(w, s, xr), ref) > 3e-5
+    # with a bias: added after the scale, as the team kernel does
+    bias = oracle.gen_normal((n,), 0xD0000300 + k, 0.0, 1.0).astype(np.float32)
+    yb = _run_i8(ops, w, s, x, bias=bias)
+    for r in range(m):
+        assert rel_err(yb[r], ref[r] + bias) <= 3e-5, r
+
+
+def test_i8_f32x_long_output_mfma_range(ops):
+    """The int8 f32-x MFMA path over x far from N(0,1): rows at ~1e5, ~1e-5 and ~1e-12 and a zero
+    row; each row against the f32 oracle to 3e-5, the zero row exactly zero."""
+    n, k, m = 32768, 960, 4
+    row_scale = np.array([1e5, 1e-5, 1e-12, 0.0], np.float32)
+    w, s, x0 = make_i8(n, k, m, cfg=5, x_dtype=np.float32, salt=331)
+    x = np.ascontiguousarray(x0 * row_scale[:, None], np.float32)
+    y = _run_i8(ops, w, s, x)
+    ref = oracle.qgemv_i8(w, s, x)
+    assert np.all(np.isfinite(y))
+    for r in range(3):
+        assert rel_err(y[r], ref[r]) <= 3e-5, (r, rel_err(y[r], ref[r]))
+    assert not np.any(y[3])
+
+
 def test_i8_ragged_k(ops):
     k, n = 40, 19  # k % 16 != 0 -> generic kernel
     w, s, x = make_i8(n, k, 1, salt=9)
