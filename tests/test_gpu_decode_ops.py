@@ -205,6 +205,34 @@ def test_attention_gqa_f16kv(ops, nh, nkv, hd, blocks, pos):
         assert rel_err(got[r], ref) <= 1e-5, (r, rel_err(got[r], ref))
 
 
+@pytest.mark.parametrize("tpb,blocks,pos", [
+    (8, 64, (511, 300, 7, 0)),      # pages of 8: a wave's 16 positions span two pages
+    (12, 42, (503, 255, 12, 11)),   # pages of 12: page edges inside the waves' 16-position groups
+    (32, 16, (511, 31, 32, 256)),   # pages of 32: two waves' positions per page
+    (64, 8, (511, 64, 63, 400)),
+    (16, 16, (255, 16, 15, 0)),     # one sub-chunk
+])
+def test_attention_per_head_page_sizes(ops, tpb, blocks, pos):
+    """The per-query-head kernel (tables of up to 512 positions) at page sizes other than 16
+    positions, including pages whose edges fall inside a wave's 16 positions: each position's
+    element base comes from its own page entry.  Every row against the oracle."""
+    nh, nkv, hd, L, rows = 15, 5, 64, 2, 4
+    kvd = nkv * hd
+    total, k, v, bt = paged_setup(L, tpb, nkv, hd, rows, blocks, 0xD00000C0 + tpb)
+    pos = np.array(pos, np.int32)
+    layer = 1
+    q = np.stack([oracle.gen_normal((nh * hd,), 0xD00000D0 + r, 0.0, 1.0) for r in range(rows)]).astype(np.float32)
+    out = torch.empty((rows, nh * hd), dtype=torch.float32, device="cuda")
+    ops.encode_attention(dev(q), dev(k), dev(v), dev(bt), dev(pos), out, nh, nkv, hd, total, L, tpb, layer)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    for r in range(rows):
+        seq = int(pos[r]) + 1
+        bases = np.array([base_of(bt[r], t, layer, L, tpb, kvd) for t in range(seq)], np.uint64)
+        ref = oracle.attention_gqa_f16kv(k, v, bases, q[r], nh, nkv, hd)
+        assert rel_err(got[r], ref) <= 1e-5, (r, rel_err(got[r], ref))
+
+
 def test_attention_one_launch_and_two_launch_forms(ops):
     """Up to 16384 (row, kv head) groups run in one launch (the group's last
     chunk block combines through coherent stores/loads and a self-resetting
