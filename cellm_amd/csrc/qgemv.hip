@@ -1086,8 +1086,9 @@ __device__ __forceinline__ void i8_stage_x(const u4_t (&xr)[XW], const void* __r
     }
 }
 
-// XT: DT_F16 (dot2 path) or DT_F32 (exact int8->f32 conversion + f32 FMA).
-template <int LPR, int R, int MT, int XT, bool MP>
+// XT: DT_F16 (dot2 path) or DT_F32 (exact int8->f32 conversion + f32 FMA).  BX: 12 x words per
+// thread instead of 8 in the first staging round (4 rows of f32 x over K up to 3072 in one round).
+template <int LPR, int R, int MT, int XT, bool MP, bool BX = false>
 __global__ __launch_bounds__(kBlock) void qgemv_i8_kernel(
     const u4_t* __restrict__ w8, const void* __restrict__ S, int sdt, int per_channel,
     const void* __restrict__ xv, const float* __restrict__ bias, float* __restrict__ y, int M, int N, int K)
@@ -1099,7 +1100,7 @@ __global__ __launch_bounds__(kBlock) void qgemv_i8_kernel(
     const int row0 = (blockIdx.x * (kBlock / LPR) + team) * R;
 
     // (1) activations: f16 in 8-element units, f32 in 4-element units
-    constexpr int XW = MT == 1 ? 4 : 8;
+    constexpr int XW = MT == 1 ? 4 : (BX ? 12 : 8);
     u4_t xr[XW];
     i8_load_x<MT, XT, XW>(xv, M, K, xr);
     // (2) weights for the first pass and this team's per-row scale / bias
@@ -1665,18 +1666,23 @@ hipError_t launch_i8_xt(const int8_t* w, const void* S, int sdt, int per_channel
     const dim3 grid((N + rows_per_block - 1) / rows_per_block);
     const u4_t* w4 = reinterpret_cast<const u4_t*>(w);
     const size_t lds = XT == DT_F16 ? (size_t)MT * CPR * 8 * 4 + (size_t)MT * CPR * 4 : (size_t)i8_xpad(MT * K) * 4;
-    if (CPR > kUnroll * LPR) {
-        auto kern = qgemv_i8_kernel<LPR, R, MT, XT, true>;
+    auto go = [&](auto kern) {
         if (lds > 64 * 1024)
             if (hipError_t e = allow_big_lds(kern, (int)lds); e != hipSuccess) return e;
         hipLaunchKernelGGL(kern, grid, dim3(kBlock), lds, st, w4, S, sdt, per_channel, x, bias, y, M, N, K);
-    } else {
-        auto kern = qgemv_i8_kernel<LPR, R, MT, XT, false>;
-        if (lds > 64 * 1024)
-            if (hipError_t e = allow_big_lds(kern, (int)lds); e != hipSuccess) return e;
-        hipLaunchKernelGGL(kern, grid, dim3(kBlock), lds, st, w4, S, sdt, per_channel, x, bias, y, M, N, K);
+        return hipGetLastError();
+    };
+    // 4 rows of f32 x past one round of 8 words per thread (K > 2048): 12 words, one round up to
+    // K = 3072 (2560->960 at 4 rows 4.57 -> 4.32 us on MI355X; shorter rows run slower with 12,
+    // the extra words being clamped re-reads)
+    if constexpr (MT == 4 && XT == DT_F32) {
+        if ((size_t)MT * (K / 4) > (size_t)kBlock * 8) {
+            if (CPR > kUnroll * LPR) return go(qgemv_i8_kernel<LPR, R, MT, XT, true, true>);
+            return go(qgemv_i8_kernel<LPR, R, MT, XT, false, true>);
+        }
     }
-    return hipGetLastError();
+    if (CPR > kUnroll * LPR) return go(qgemv_i8_kernel<LPR, R, MT, XT, true>);
+    return go(qgemv_i8_kernel<LPR, R, MT, XT, false>);
 }
 
 template <int LPR, int R, int MT>
