@@ -1854,11 +1854,14 @@ size_t decode_fused_lds_bytes(int rows, int H)
 
 namespace {
 
+// Units (a QKV row, or a gate row with its up row) per 64-lane team.  Measured on the configs[4]
+// step at 4 sessions (one box, graph replay): gate/up with 1 / 2 / 4 / 8 units 0.882 / 0.854 /
+// 0.835 / 0.893 ms; QKV with 2 units 0.879 against 0.854 with 1.
 #ifndef CELLM_DI8_RP_QKV
 #define CELLM_DI8_RP_QKV 1
 #endif
 #ifndef CELLM_DI8_RP_GU
-#define CELLM_DI8_RP_GU 2
+#define CELLM_DI8_RP_GU 4
 #endif
 
 template <int LPR, int C, int MT, int KR, class Args>
@@ -1963,6 +1966,8 @@ namespace {
 
 size_t decode_q4_lds_bytes(int MT, int H) { return (size_t)MT * (xpad(H) + (H >> 5)) * sizeof(float); }
 
+// q4 gate/up: 2 units per team (4 and 8 measured 0.786-0.790 against 0.764-0.767 ms on the
+// Qwen2-shape step at 4 sessions)
 #ifndef CELLM_DQ4_RP_QKV
 #define CELLM_DQ4_RP_QKV 1
 #endif
