@@ -1149,7 +1149,7 @@ __global__ __launch_bounds__(kBlock) void qgemv_i8_kernel(
 
     // the team's R * MT sums reduced transposed: lane l ends with value team_sum_t_index(l), and
     // one lane per value applies the row's scale (and bias) and stores
-    static_assert(R == 1 || R == 2, "one or two rows per team");
+    static_assert(R * MT <= LPR, "one value per lane at most");
     constexpr int V = R * MT;
     float a[V];
 #pragma unroll
@@ -1159,12 +1159,18 @@ __global__ __launch_bounds__(kBlock) void qgemv_i8_kernel(
     const float tot = team_sum_t<LPR, V>(a);
     const int vi = team_sum_t_index<LPR, V>(lane), r = vi / MT, m = vi % MT, n = row0 + r;
     if ((lane & (LPR / V - 1)) == 0 && m < M && n < N) {
-        const uint32_t sr = R == 1 || r == 0 ? sraw[0] : sraw[R - 1];
+        uint32_t sr = sraw[0];
+        float bvr = bv[0];
+#pragma unroll
+        for (int k = 1; k < R; ++k) {
+            sr = r == k ? sraw[k] : sr;
+            bvr = r == k ? bv[k] : bvr;
+        }
         const float s = sdt == DT_F32 ? raw_to_f32<DT_F32>(sr)
                       : sdt == DT_F16 ? raw_to_f32<DT_F16>(sr)
                                       : raw_to_f32<DT_BF16>(sr);
         float v = tot * s;
-        if (bias) v += R == 1 || r == 0 ? bv[0] : bv[R - 1];
+        if (bias) v += bvr;
         y[(size_t)m * N + n] = v;
     }
 }
@@ -1593,6 +1599,21 @@ struct GemvShape {
     int lpr;
     int rows;
 };
+
+int gemv_device_cus()
+{
+    static std::mutex mu;
+    static std::vector<std::pair<int, int>> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    std::lock_guard<std::mutex> lk(mu);
+    for (const auto& e : cache)
+        if (e.first == dev) return e.second;
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 256;
+    cache.push_back({dev, cus});
+    return cus;
+}
 
 GemvShape pick_shape(int cpr, int n_rows, bool q4)
 {
@@ -2027,6 +2048,11 @@ hipError_t launch_qgemv_i8(const int8_t* w, const void* S, int sdt, int per_chan
         const GemvShape sh = pick_shape(K >> 4, N, false);
         if (M == 1) return launch_i8_lpr<1, 1>(sh.lpr, xdt, w, S, sdt, per_channel, x, bias, y, M, N, K, st);
         if (M == 2) return launch_i8_lpr<1, 2>(sh.lpr, xdt, w, S, sdt, per_channel, x, bias, y, M, N, K, st);
+        // f32 x whose LDS leaves one block per CU (over 80 KB) and more four-row blocks than CUs:
+        // two rows per team halve the blocks into one round (6912->1152 at 4 rows 18.4 -> 11.2 us
+        // on MI355X; where two blocks fit a CU, two rows per team measured slower)
+        if (xdt == DT_F32 && lds > 80 * 1024 && (N + 3) / 4 > gemv_device_cus())
+            return launch_i8_lpr<2, 4>(sh.lpr, xdt, w, S, sdt, per_channel, x, bias, y, M, N, K, st);
         return launch_i8_lpr<1, 4>(sh.lpr, xdt, w, S, sdt, per_channel, x, bias, y, M, N, K, st);
     }
     const dim3 grid((N + 3) / 4);
