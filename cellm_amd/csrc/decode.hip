@@ -1312,23 +1312,23 @@ __global__ __launch_bounds__(256) void decode_i8_kernel(Args a)
 template <int MT, int XU, int NT = kNormThreads>
 __device__ __forceinline__ void stage_x32(const float* __restrict__ x, int M, int K, float* xs, float* xsum)
 {
-    const int t = threadIdx.x, K4 = K >> 2, total = MT * K4, xst = xpad(K), cpr = K >> 5;
+    const int t = threadIdx.x, K4 = K >> 2, total = MT * K4;
     for (int base = 0; base < total; base += XU * NT) {
         f4_t v[XU];
 #pragma unroll
         for (int u = 0; u < XU; ++u) {
-            const int g = min(base + u * NT + t, total - 1);
-            const int m = g / K4;
-            v[u] = reinterpret_cast<const f4_t*>(x)[(size_t)min(m, M - 1) * K4 + (g - m * K4)];
+            // x rows are contiguous: group g at x + 4 g (padding rows read the last real group)
+            v[u] = reinterpret_cast<const f4_t*>(x)[min(base + u * NT + t, min(total, M * K4) - 1)];
         }
 #pragma unroll
         for (int u = 0; u < XU; ++u) {
+            // row m = g / K4, group k4: LDS m * xpad(K) + xpad(4 k4) = xpad(4 g) and chunk m * cpr +
+            // k4 / 8 = g / 8 (K % 32 == 0), so no division
             const int g = base + u * NT + t;
-            const int m = g / K4, k4 = g - m * K4;
-            if (g < total) *reinterpret_cast<f4_t*>(xs + m * xst + xpad(4 * k4)) = v[u];
+            if (g < total) *reinterpret_cast<f4_t*>(xs + xpad(4 * g)) = v[u];
             // total % 8 == 0 (K4 % 8 == 0): a chunk's groups are all in range or all out
             const float cs = group_sum<8>((v[u][0] + v[u][1]) + (v[u][2] + v[u][3]));
-            if (g < total && (t & 7) == 0) xsum[m * cpr + (k4 >> 3)] = cs;
+            if (g < total && (t & 7) == 0) xsum[g >> 3] = cs;
         }
     }
     __syncthreads();

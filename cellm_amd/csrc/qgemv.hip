@@ -146,9 +146,10 @@ __device__ __forceinline__ void stage_x_q4_x32(const float* __restrict__ x, int 
         f4_t ra[XW], rb[XW];
 #pragma unroll
         for (int j = 0; j < XW; ++j) {
-            const int idx = min(base + j * kBlock + (int)threadIdx.x, total - 1);
-            const int m = idx / words;
-            const f4_t* p = reinterpret_cast<const f4_t*>(x + (size_t)min(m, M - 1) * K + (size_t)(idx - m * words) * 8);
+            // x rows are contiguous: word idx of row idx / words sits at x + 8 idx (rows past M
+            // read the last real word; their results are never stored)
+            const int idx = min(base + j * kBlock + (int)threadIdx.x, M * words - 1);
+            const f4_t* p = reinterpret_cast<const f4_t*>(x + (size_t)idx * 8);
             ra[j] = p[0];
             rb[j] = p[1];
         }
@@ -168,10 +169,9 @@ __device__ __forceinline__ void load_x_words(const _Float16* __restrict__ x, int
     for (int j = 0; j < XW; ++j) {
         // clamped, branch-free: padding rows m >= M and words past `total`
         // read valid data whose results are never stored
-        const int idx = min((int)threadIdx.x + j * kBlock, total - 1);
-        const int m = idx / words;
-        const int mc = min(m, M - 1);
-        xr[j] = *reinterpret_cast<const u4_t*>(x + (size_t)mc * K + (size_t)(idx - m * words) * 8);
+        // (x rows are contiguous: word idx sits at x + 8 idx, no division)
+        const int idx = min((int)threadIdx.x + j * kBlock, min(total, M * words) - 1);
+        xr[j] = *reinterpret_cast<const u4_t*>(x + (size_t)idx * 8);
     }
 }
 
@@ -188,10 +188,8 @@ __device__ __forceinline__ void stage_x_q4(const u4_t (&xr)[XW], const _Float16*
     for (int base = XW * kBlock; base < total; base += kBlock) {  // large M*K only
         const int idx = base + (int)threadIdx.x;
         const int words = K >> 3;
-        const int m = idx / words;
-        u4_t raw = (idx < total && m < M)
-                       ? *reinterpret_cast<const u4_t*>(x + (size_t)m * K + (size_t)(idx - m * words) * 8)
-                       : u4_t{0u, 0u, 0u, 0u};
+        u4_t raw = (idx < total && idx < M * words) ? *reinterpret_cast<const u4_t*>(x + (size_t)idx * 8)
+                                                    : u4_t{0u, 0u, 0u, 0u};
         stage_word_q4(raw, idx, idx < total, xq, cx);
     }
 }
@@ -1033,11 +1031,10 @@ __device__ __forceinline__ void i8_load_x(const void* __restrict__ xv, int M, in
     const int total = MT * units;
 #pragma unroll
     for (int j = 0; j < XW; ++j) {
-        const int idx = min((int)threadIdx.x + j * kBlock, total - 1);
-        const int m = idx / units;
-        const int mc = min(m, M - 1);
-        const char* base = reinterpret_cast<const char*>(xv) + ((size_t)mc * K + (size_t)(idx - m * units) * unit) *
-                                                                   (XT == DT_F16 ? 2 : 4);
+        // x rows are contiguous: unit idx sits at element unit * idx (no division; padding rows read
+        // the last real unit, and their results are never stored)
+        const int idx = min((int)threadIdx.x + j * kBlock, min(total, M * units) - 1);
+        const char* base = reinterpret_cast<const char*>(xv) + (size_t)idx * unit * (XT == DT_F16 ? 2 : 4);
         xr[j] = *reinterpret_cast<const u4_t*>(base);
     }
 }
@@ -1060,11 +1057,9 @@ __device__ __forceinline__ void i8_stage_x(const u4_t (&xr)[XW], const void* __r
         }
         for (int b0 = XW * kBlock; b0 < total; b0 += kBlock) {
             const int idx = b0 + (int)threadIdx.x;
-            const int m = idx / units;
             const _Float16* xh = reinterpret_cast<const _Float16*>(xv);
-            u4_t raw = (idx < total && m < M)
-                           ? *reinterpret_cast<const u4_t*>(xh + (size_t)m * K + (size_t)(idx - m * units) * 8)
-                           : u4_t{0u, 0u, 0u, 0u};
+            u4_t raw = (idx < total && idx < M * units) ? *reinterpret_cast<const u4_t*>(xh + (size_t)idx * 8)
+                                                        : u4_t{0u, 0u, 0u, 0u};
             stage_unit_i8(raw, idx, idx < total, xq, cx);
         }
     } else {
@@ -1076,12 +1071,10 @@ __device__ __forceinline__ void i8_stage_x(const u4_t (&xr)[XW], const void* __r
         }
         for (int b0 = XW * kBlock; b0 < total; b0 += kBlock) {
             const int idx = b0 + (int)threadIdx.x;
-            const int m = idx / units;
             const float* xf = reinterpret_cast<const float*>(xv);
             if (idx < total)
                 *reinterpret_cast<u4_t*>(xq + i8_xpad(idx * 4)) =
-                    m < M ? *reinterpret_cast<const u4_t*>(xf + (size_t)m * K + (size_t)(idx - m * units) * 4)
-                          : u4_t{0u, 0u, 0u, 0u};
+                    idx < M * units ? *reinterpret_cast<const u4_t*>(xf + (size_t)idx * 4) : u4_t{0u, 0u, 0u, 0u};
         }
     }
 }
