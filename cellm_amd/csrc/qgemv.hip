@@ -1223,10 +1223,9 @@ __device__ __forceinline__ void i4_stage_x(const u4_t (&xr)[XW], const void* __r
         u4_t rr[XW];
 #pragma unroll
         for (int j = 0; j < XW; ++j) {
-            const int ic = min(b0 + j * kBlock + (int)threadIdx.x, total - 1);
-            const int mi = ic / units;
-            const char* base = reinterpret_cast<const char*>(xv) +
-                               ((size_t)min(mi, M - 1) * K + (size_t)(ic - mi * units) * unit) * (XT == DT_F16 ? 2 : 4);
+            // contiguous rows: unit ic at element unit * ic (padding rows read the last real unit)
+            const int ic = min(b0 + j * kBlock + (int)threadIdx.x, min(total, M * units) - 1);
+            const char* base = reinterpret_cast<const char*>(xv) + (size_t)ic * unit * (XT == DT_F16 ? 2 : 4);
             rr[j] = *reinterpret_cast<const u4_t*>(base);
         }
 #pragma unroll

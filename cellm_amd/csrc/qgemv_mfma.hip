@@ -114,10 +114,20 @@ __global__ __launch_bounds__(BT) void qgemv_mfma_kernel(
     // before the barrier that publishes the tile.
     auto stage = [&](int kb, int kcl) {
         const int words = kcl >> 3, rowc = stride >> 3, total = M * rowc;
+        // this lane's first (row, chunk) by one division, then stepped BT chunks at a time (BT =
+        // step_q rows + step_r chunks, step_r < rowc): no division per DMA
+        const int step_q = BT / rowc, step_r = BT - step_q * rowc;
+        int j = wave * 64 + lane, m = j / rowc, c = j - m * rowc;
         for (int j0 = wave * 64; j0 < total; j0 += BT) {
-            const int j = j0 + lane, m = j / rowc, c = j - m * rowc;
             if (j < total && c < words)
                 __builtin_amdgcn_global_load_lds(X + (size_t)m * K + kb + c * 8, xs + (size_t)j0 * 8, 16, 0, 0);
+            j += BT;
+            m += step_q;
+            c += step_r;
+            if (c >= rowc) {
+                c -= rowc;
+                ++m;
+            }
         }
     };
     // One block's B operands + MFMAs: w[t] is this lane's 16 bytes of row
