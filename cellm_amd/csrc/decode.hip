@@ -996,46 +996,77 @@ __host__ __device__ __forceinline__ int q4_units(const Args& a)
         return a.N;
 }
 
-// RoPE on the pair (v0, v1) of head `head`, rows i0 / i1 (pair i of the table row
-// at session m's position), then q into q_out or k / v into the paged cache as f16:
-// the arithmetic of rope_kv_write_kernel.  Shared by the int8 and q4 QKV kernels.
+// The epilogue's loads for one (unit, session), issued with a kernel's prologue: a lane's
+// epilogue unit and session are fixed by its lane (team_sum_t_index), so its position, RoPE row
+// and page base (QKV), its projection biases (q4 QKV) and its row scales (int8) need not wait for
+// the dot.  QKV: the position is loaded first (*_epi_pos), the RoPE row and the page base after
+// the prologue's own loads are issued (rope_prefetch).
+struct EpiPre {
+    int pr = 0;        // the session's position
+    float2 c{};        // cos / sin of the RoPE pair at pr
+    long long b = -1;  // K/V element base of (session, pr), or -1
+    float s0 = 0.0f, s1 = 0.0f;  // int8 row scales, or q4 projection biases of the unit's two rows
+};
+
 template <class A>
-__device__ __forceinline__ void rope_kv_epilogue(const A& a, int which, int head, int i, int i0, int i1, int m,
-                                                 float v0, float v1)
+__device__ __forceinline__ void rope_prefetch(const A& a, int which, int i, int m, EpiPre& e)
 {
     const int half = a.head_dim >> 1;
-    const int pr = a.pos[m];
-    const float2 c = a.cs[(size_t)min(max(pr, 0), a.table_positions - 1) * half + i];
+    e.c = a.cs[(size_t)min(max(e.pr, 0), a.table_positions - 1) * half + i];
+    e.b = (which != 0 && e.pr >= 0) ? a.kv.base(m, e.pr, a.layer) : -1;
+}
+
+// RoPE on the pair (v0, v1) of head `head`, rows i0 / i1, with the prefetched table row (pair i
+// at session m's position), then q into q_out or k / v into the paged cache as f16 (the
+// arithmetic of rope_kv_write_kernel).  Shared by the int8 and q4 QKV kernels.
+template <class A>
+__device__ __forceinline__ void rope_kv_store(const A& a, int which, int head, int i0, int i1, int m, const EpiPre& e,
+                                              float v0, float v1)
+{
+    const float2 c = e.c;
     if (which == 0) {
         float* q = a.q_out + ((size_t)m * a.n_heads + head) * a.head_dim;
         q[i0] = v0 * c.x - v1 * c.y;
         q[i1] = v1 * c.x + v0 * c.y;
         return;
     }
-    const long long b = pr >= 0 ? a.kv.base(m, pr, a.layer) : -1;
-    if (b < 0) return;
-    const size_t e = (size_t)b + (size_t)head * a.head_dim;
+    if (e.b < 0) return;
+    const size_t el = (size_t)e.b + (size_t)head * a.head_dim;
     if (which == 1) {
-        a.kc[e + i0] = __builtin_bit_cast(uint16_t, (_Float16)(v0 * c.x - v1 * c.y));
-        a.kc[e + i1] = __builtin_bit_cast(uint16_t, (_Float16)(v1 * c.x + v0 * c.y));
+        a.kc[el + i0] = __builtin_bit_cast(uint16_t, (_Float16)(v0 * c.x - v1 * c.y));
+        a.kc[el + i1] = __builtin_bit_cast(uint16_t, (_Float16)(v1 * c.x + v0 * c.y));
     } else {
-        a.vc[e + i0] = __builtin_bit_cast(uint16_t, (_Float16)v0);
-        a.vc[e + i1] = __builtin_bit_cast(uint16_t, (_Float16)v1);
+        a.vc[el + i0] = __builtin_bit_cast(uint16_t, (_Float16)v0);
+        a.vc[el + i1] = __builtin_bit_cast(uint16_t, (_Float16)v1);
     }
 }
 
 // (unit, session m) epilogue with the unit's two row sums v0, v1
-__device__ __forceinline__ void q4_epilogue(const DecodeQ4QkvArgs& a, const Q4Unit& u, int m, float v0, float v1)
+// (unit, session m) epilogue of the q4 kernel over its prefetched values (EpiPre: position,
+// RoPE row, page base, projection biases)
+__device__ __forceinline__ void q4_epi_pos(const DecodeQ4QkvArgs& a, int m, EpiPre& e) { e.pr = a.pos[m]; }
+__device__ __forceinline__ void q4_epi_pos(const DecodeQ4GateUpArgs&, int, EpiPre&) {}
+__device__ __forceinline__ void q4_epi_prefetch(const DecodeQ4QkvArgs& a, const Q4Unit& u, int m, EpiPre& e)
+{
+    const float* pb = u.which == 0 ? a.bias[0] : (u.which == 1 ? a.bias[1] : a.bias[2]);
+    const float z = 0.0f;
+    e.s0 = *(pb ? pb + u.r0 : &z);
+    e.s1 = *(pb ? pb + u.r1 : &z);
+    rope_prefetch(a, u.which, u.i, m, e);
+}
+__device__ __forceinline__ void q4_epi_prefetch(const DecodeQ4GateUpArgs&, const Q4Unit&, int, EpiPre&) {}
+__device__ __forceinline__ void q4_epilogue(const DecodeQ4QkvArgs& a, const Q4Unit& u, int m, const EpiPre& e,
+                                            float v0, float v1)
 {
     const float* pb = u.which == 0 ? a.bias[0] : (u.which == 1 ? a.bias[1] : a.bias[2]);
     if (pb) {  // add_projection_bias_if_present, then RoPE
-        v0 = v0 + pb[u.r0];
-        v1 = v1 + pb[u.r1];
+        v0 = v0 + e.s0;
+        v1 = v1 + e.s1;
     }
-    rope_kv_epilogue(a, u.which, u.head, u.i, u.i0, u.i1, m, v0, v1);
+    rope_kv_store(a, u.which, u.head, u.i0, u.i1, m, e, v0, v1);
 }
-
-__device__ __forceinline__ void q4_epilogue(const DecodeQ4GateUpArgs& a, const Q4Unit& u, int m, float v0, float v1)
+__device__ __forceinline__ void q4_epilogue(const DecodeQ4GateUpArgs& a, const Q4Unit& u, int m, const EpiPre&,
+                                            float v0, float v1)
 {
     a.h[(size_t)m * a.N + u.r0] = act_mul(a.act, v0, v1);
 }
@@ -1147,7 +1178,13 @@ __global__ __launch_bounds__(256) void decode_q4_kernel(Args a)
     const int vi = team_sum_t_index<LPR, V>(lane);
     const int p = vi / (2 * MT), r = (vi / MT) & 1, m = vi % MT;
     if (r != 0 || (lane & (LPR / V - 1)) != 0 || m >= a.rows || unit0 + p >= units) return;
-    q4_epilogue(a, q4_unit(a, unit0 + p, cpr, gpr), m, tot, other);
+    // the q4 kernels load the epilogue's values here, after the dot (issued with the prologue they
+    // measured 2-6 us slower per Qwen2-shape step)
+    const Q4Unit u = q4_unit(a, unit0 + p, cpr, gpr);
+    EpiPre epre;
+    q4_epi_pos(a, m, epre);
+    q4_epi_prefetch(a, u, m, epre);
+    q4_epilogue(a, u, m, epre, tot, other);
 }
 
 // ---- fused decode-step GEMVs over int8 weights -------------------------------
@@ -1212,13 +1249,29 @@ __host__ __device__ __forceinline__ int i8_units(const Args& a)
         return a.N;
 }
 
-__device__ __forceinline__ void i8_epilogue(const DecodeQkvArgs& a, const I8Unit& u, int m, float v0, float v1)
+__device__ __forceinline__ void i8_epi_pos(const DecodeQkvArgs& a, int m, EpiPre& e) { e.pr = a.pos[m]; }
+__device__ __forceinline__ void i8_epi_pos(const DecodeGateUpArgs&, int, EpiPre&) {}
+__device__ __forceinline__ void i8_epi_prefetch(const DecodeQkvArgs& a, const I8Unit& u, int m, EpiPre& e)
 {
-    rope_kv_epilogue(a, u.which, u.head, u.i, u.i0, u.i1, m, v0, v1);
+    e.s0 = h2f(u.s0[u.r0]);
+    e.s1 = h2f(u.s1[u.r1]);
+    rope_prefetch(a, u.which, u.i, m, e);
+}
+__device__ __forceinline__ void i8_epi_prefetch(const DecodeGateUpArgs&, const I8Unit& u, int, EpiPre& e)
+{
+    e.s0 = h2f(u.s0[u.r0]);
+    e.s1 = h2f(u.s1[u.r1]);
+}
+
+__device__ __forceinline__ void i8_epilogue(const DecodeQkvArgs& a, const I8Unit& u, int m, const EpiPre& e, float v0,
+                                            float v1)
+{
+    rope_kv_store(a, u.which, u.head, u.i0, u.i1, m, e, v0, v1);
 }
 
 // h = silu(g) * u as silu_mul_f32_inplace (metal.rs:235-245): (g * (1 / (1 + exp(-g)))) * u
-__device__ __forceinline__ void i8_epilogue(const DecodeGateUpArgs& a, const I8Unit& u, int m, float v0, float v1)
+__device__ __forceinline__ void i8_epilogue(const DecodeGateUpArgs& a, const I8Unit& u, int m, const EpiPre&, float v0,
+                                            float v1)
 {
     a.h[(size_t)m * a.N + u.r0] = act_mul(ACT_SILU, v0, v1);
 }
@@ -1234,6 +1287,11 @@ __global__ __launch_bounds__(256) void decode_i8_kernel(Args a)
     const int team = threadIdx.x / LPR, lane = threadIdx.x % LPR;
     const int units = i8_units(a);
     const int unit0 = (blockIdx.x * (256 / LPR) + team) * RP;
+    // this lane's epilogue (unit ep, session em): its position first, its row scales, RoPE row and
+    // page base after the prologue's loads (EpiPre)
+    const int evi = team_sum_t_index<LPR, V>(lane), ep = evi / (2 * MT), em = min(evi % MT, a.rows - 1);
+    EpiPre epre;
+    i8_epi_pos(a, em, epre);
 
     NormIn<MT, KR> nin;
     load_add_norm<MT, KR, HASY>(a.x_prev, a.y, a.norm_w, a.rows, H, nin);
@@ -1248,6 +1306,7 @@ __global__ __launch_bounds__(256) void decode_i8_kernel(Args a)
             w[c][p][1] = u.w1[ch];
         }
     }
+    i8_epi_prefetch(a, i8_unit(a, min(unit0 + ep, units - 1), cpr), em, epre);
 
     stage_add_norm<MT, KR, HASY>(nin, a.x_out, a.rows, H, a.eps, xs, red);
 
@@ -1295,7 +1354,7 @@ __global__ __launch_bounds__(256) void decode_i8_kernel(Args a)
     const int p = vi / (2 * MT), r = (vi / MT) & 1, m = vi % MT;
     if (r != 0 || (lane & (LPR / V - 1)) != 0 || m >= a.rows || unit0 + p >= units) return;
     const I8Unit u = i8_unit(a, unit0 + p, cpr);
-    i8_epilogue(a, u, m, tot * h2f(u.s0[u.r0]), other * h2f(u.s1[u.r1]));
+    i8_epilogue(a, u, m, epre, tot * epre.s0, other * epre.s1);
 }
 
 // ---- MLX q4 affine GEMV over f32 activations (M <= 4), f32 dot ---------------
