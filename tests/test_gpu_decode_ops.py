@@ -488,11 +488,17 @@ def test_decode_qkv_matches_separate_ops(ops, steplib, rows, with_y, interleaved
         ops.set_rope_interleaved(False)
 
 
-def _decode_qkv_case(ops, steplib, rows, with_y):
+def test_decode_qkv_negative_position(ops, steplib):
+    """A session at position -1 in the fused int8 QKV launch: its q as the separate ops give it, no
+    K/V element written for it (the page base the epilogue reads early is -1)."""
+    _decode_qkv_case(ops, steplib, 4, True, positions=(127, -1, 64, 17))
+
+
+def _decode_qkv_case(ops, steplib, rows, with_y, positions=(127, 0, 64, 17)):
     H, nh, nkv, hd, L, tpb, layer = 960, 15, 5, 64, 3, 16, 2
     kvd = nkv * hd
     total, k0, v0, bt = paged_setup(L, tpb, nkv, hd, rows, 8, 0xD0000200)
-    pos = np.array([127, 0, 64, 17][:rows], np.int32)
+    pos = np.array(positions[:rows], np.int32)
     table = rope_table(steplib, 100000.0, hd, 8 * tpb)
     xp = np.stack([oracle.gen_normal((H,), 0xD0000210 + r, 0.0, 1.0) for r in range(rows)]).astype(np.float32)
     y = np.stack([oracle.gen_normal((H,), 0xD0000220 + r, 0.0, 0.5) for r in range(rows)]).astype(np.float32)
