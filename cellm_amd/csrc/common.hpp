@@ -227,6 +227,22 @@ __device__ __forceinline__ void buffer_store_f32(float v, __amdgpu_buffer_rsrc_t
 {
     __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, (int)byte_off, 0, NT ? 2 : 0);
 }
+// Sum of the nsplit split-K partials p4[s * stride], s = 0, 1, ..., added in split order (a fixed
+// order: deterministic), with eight splits' 16-byte loads in flight at a time (slots past the last
+// split re-read it and are not added).
+__device__ __forceinline__ f4_t sum_splits_f4(const f4_t* __restrict__ p4, size_t stride, int nsplit)
+{
+    f4_t a = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s0 = 0; s0 < nsplit; s0 += 8) {
+        f4_t b[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) b[j] = p4[(size_t)min(s0 + j, nsplit - 1) * stride];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (s0 + j < nsplit) a = s0 + j == 0 ? b[j] : a + b[j];
+    }
+    return a;
+}
 __device__ __forceinline__ float quad_sum(float v) { return group_sum<4>(v); }
 __device__ __forceinline__ float pair_sum(float v) { return group_sum<2>(v); }
 __device__ __forceinline__ float oct_sum(float v) { return group_sum<8>(v); }

@@ -235,19 +235,7 @@ __global__ void splitk_reduce_kernel(const float* __restrict__ part, float* __re
         // four columns of one row per thread: 16-byte loads of every split's partials
         const size_t n4 = total >> 2;
         for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (size_t)gridDim.x * blockDim.x) {
-            const f4_t* p4 = reinterpret_cast<const f4_t*>(part) + i;
-            f4_t v = p4[0];
-            int s = 1;
-            // four splits' loads in flight at a time, added in split order
-            for (; s + 3 < splits; s += 4) {
-                const f4_t b0 = p4[(size_t)s * n4], b1 = p4[(size_t)(s + 1) * n4];
-                const f4_t b2 = p4[(size_t)(s + 2) * n4], b3 = p4[(size_t)(s + 3) * n4];
-                v += b0;
-                v += b1;
-                v += b2;
-                v += b3;
-            }
-            for (; s < splits; ++s) v += p4[(size_t)s * n4];
+            f4_t v = sum_splits_f4(reinterpret_cast<const f4_t*>(part) + i, n4, splits);
             if (bias) {
                 const size_t n = (4 * i) % (size_t)N;
                 v += f4_t{bias[n], bias[n + 1], bias[n + 2], bias[n + 3]};

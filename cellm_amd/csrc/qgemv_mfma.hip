@@ -463,19 +463,7 @@ __global__ __launch_bounds__(64) void mfma_splitk_reduce_kernel(const float* __r
     if ((N & 3) == 0 && (reinterpret_cast<uintptr_t>(Y) & 15) == 0) {
         const size_t n4 = total >> 2;
         for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (size_t)gridDim.x * blockDim.x) {
-            const f4_t* p4 = reinterpret_cast<const f4_t*>(part) + i;
-            f4_t a = p4[0];
-            int sp = 1;
-            // four splits' loads in flight at a time, added in split order
-            for (; sp + 3 < nsplit; sp += 4) {
-                const f4_t b0 = p4[(size_t)sp * (plane >> 2)], b1 = p4[(size_t)(sp + 1) * (plane >> 2)];
-                const f4_t b2 = p4[(size_t)(sp + 2) * (plane >> 2)], b3 = p4[(size_t)(sp + 3) * (plane >> 2)];
-                a += b0;
-                a += b1;
-                a += b2;
-                a += b3;
-            }
-            for (; sp < nsplit; ++sp) a += p4[(size_t)sp * (plane >> 2)];
+            f4_t a = sum_splits_f4(reinterpret_cast<const f4_t*>(part) + i, plane >> 2, nsplit);
             if constexpr (WT == 1) {
                 const int n = (int)((4 * i) % (size_t)N);
 #pragma unroll
