@@ -97,6 +97,8 @@ SIGNATURES = {
                                       _vp]),
     "cellm_hip_attention_gqa_f16kv": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _i64,
                                              _i64, _i64, C.c_float, C.c_float, _vp, _vp]),
+    "cellm_hip_attention_gqa_f16kv_window": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i64,
+                                                    _i64, _i64, _i64, C.c_float, C.c_float, _i64, _vp, _vp]),
     "cellm_hip_attention_gqa_f16kv_noalloc": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _i64, _i64, _i64,
                                                      _i64, _i64, _i64, C.c_float, C.c_float, _vp, _vp]),
     "cellm_hip_silu_mul_f32": (_i32, [_vp, _vp, _vp, _i64, _vp]),

@@ -1072,8 +1072,9 @@ int32_t attention_impl(cellm_hip_ctx* ctx, const float* q, const uint16_t* kcach
                        const uint32_t* block_tables, int64_t max_blocks, int64_t total_blocks, const int32_t* positions,
                        int64_t rows, int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, int64_t n_layers,
                        int64_t tokens_per_block, int64_t layer, float attn_scale, float soft_cap, float* out,
-                       hipStream_t st, bool static_scratch)
+                       hipStream_t st, bool static_scratch, int64_t window = 0)
 {
+    if (window < 0 || window > INT32_MAX) return set_error(CELLM_HIP_ERR_INVALID_ARG, "bad window %lld", (long long)window);
     if (int32_t rc = check_paged(rows, max_blocks, total_blocks, n_layers, tokens_per_block, layer)) return rc;
     if (n_heads < 1 || n_kv_heads < 1 || head_dim < 1 || n_heads > 4096 ||
         !attention_supported((int)n_heads, (int)n_kv_heads, (int)head_dim, (int)(max_blocks * tokens_per_block)))
@@ -1108,7 +1109,8 @@ int32_t attention_impl(cellm_hip_ctx* ctx, const float* q, const uint16_t* kcach
     }
     HIP_TRY(launch_attention_gqa_f16kv(q, kcache, vcache, block_tables, (int)max_blocks, (int)total_blocks, positions,
                                        (int)rows, (int)n_heads, (int)n_kv_heads, (int)head_dim, (int)n_layers,
-                                       (int)tokens_per_block, (int)layer, attn_scale, soft_cap, out, ws, st),
+                                       (int)tokens_per_block, (int)layer, attn_scale, soft_cap, out, ws, st,
+                                       (int)window),
             "attention launch");
     return CELLM_HIP_OK;
 }
@@ -1469,6 +1471,23 @@ int32_t cellm_hip_attention_gqa_f16kv(cellm_hip_ctx_t* ctx, const float* q, cons
     return attention_impl(ctx, q, kcache, vcache, block_tables, max_blocks, total_blocks, positions, rows, n_heads,
                           n_kv_heads, head_dim, n_layers, tokens_per_block, layer, attn_scale, soft_cap, out,
                           pick_stream(ctx, stream), false);
+    CELLM_API_END(report_exception)
+}
+
+int32_t cellm_hip_attention_gqa_f16kv_window(cellm_hip_ctx_t* ctx, const float* q, const uint16_t* kcache,
+                                             const uint16_t* vcache, const uint32_t* block_tables, int64_t max_blocks,
+                                             int64_t total_blocks, const int32_t* positions, int64_t rows,
+                                             int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, int64_t n_layers,
+                                             int64_t tokens_per_block, int64_t layer, float attn_scale, float soft_cap,
+                                             int64_t window, float* out, void* stream)
+{
+    CELLM_API_BEGIN
+    if (int32_t rc = check_ctx(ctx)) return rc;
+    DeviceGuard g(ctx->device);
+    const std::lock_guard<std::recursive_mutex> lk(ctx->mu);  // held until the scratch users are enqueued
+    return attention_impl(ctx, q, kcache, vcache, block_tables, max_blocks, total_blocks, positions, rows, n_heads,
+                          n_kv_heads, head_dim, n_layers, tokens_per_block, layer, attn_scale, soft_cap, out,
+                          pick_stream(ctx, stream), false, window);
     CELLM_API_END(report_exception)
 }
 

@@ -363,10 +363,16 @@ __device__ __forceinline__ void attn_combine_group(const float* __restrict__ p, 
 // waiting for them the block counts its arrival in its group's counter, and the
 // group's last block to arrive (whichever chunk) combines the group with
 // agent-coherent loads into `out` and resets the counter to zero.
+// First position a row attends to: with a sliding window of `window`
+// positions (window > 0) the last `window` of its `seq`, else all of them
+// (gemma.rs:747-751: start = seq.saturating_sub(sliding_window) on sliding
+// layers, 0 on full-attention layers).
+__device__ __forceinline__ int window_start(int seq, int window) { return window > 0 ? max(seq - window, 0) : 0; }
+
 template <int HD, int G, bool FUSED = false>
 __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
     const float* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
-    const int32_t* __restrict__ pos, PagedKv kv, int layer, int n_kv_heads, float scale, float soft_cap,
+    const int32_t* __restrict__ pos, PagedKv kv, int layer, int n_kv_heads, float scale, float soft_cap, int window,
     float* __restrict__ part, int nch_max, uint32_t* __restrict__ counters = nullptr, float* __restrict__ out = nullptr)
 {
     constexpr int KD = HD / 4;                             // Q.K dims per thread
@@ -394,13 +400,14 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
     const int tt = t0 + lane, blk_i = tt / kv.tpb;
     const uint32_t blk = kv.bt[(size_t)r * kv.max_blocks + min(blk_i, kv.max_blocks - 1)];
     const int seq = min(p_r + 1, kv.max_blocks * kv.tpb);
-    if (t0 >= seq) return;  // the same for the whole block
+    const int s0 = window_start(seq, window), c0 = s0 / kAttnChunk;
+    if (t0 >= seq || ch < c0) return;  // the same for the whole block
     const int nt = min(kAttnChunk, seq - t0);
 #pragma unroll
     for (int j = 0; j < QL; ++j)
         if (t + j * kAttnThreads < G * HD) qs[t + j * kAttnThreads] = qv[j];
     if (t < kAttnChunk)
-        bases[t] = (t < nt && blk_i < kv.max_blocks && blk < (uint32_t)kv.total_blocks)
+        bases[t] = (t < nt && tt >= s0 && blk_i < kv.max_blocks && blk < (uint32_t)kv.total_blocks)
                        ? ((long long)blk * kv.n_layers + layer) * (long long)kv.tpb * kv.kvd +
                              (long long)(tt % kv.tpb) * kv.kvd
                        : -1;
@@ -441,7 +448,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
             for (int g = 0; g < G; ++g) dot[g] = dot[g] + qs[g * HD + d] * kf;
         }
     }
-    const bool valid = kp < nt;
+    const bool valid = kp < nt && t0 + kp >= s0;
     float sc[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -520,13 +527,14 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
         // this block's partials are performed at the coherence point before it counts itself
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        const int nch = (seq + kAttnChunk - 1) / kAttnChunk;  // blocks of the group that reach here
+        const int nch = (seq + kAttnChunk - 1) / kAttnChunk - c0;  // blocks of the group that reach here
         if (t == 0)
             last = __hip_atomic_fetch_add(counters + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                    (uint32_t)(nch - 1);
         __syncthreads();
         if (!last) return;
-        attn_combine_group<HD, G, true>(grp, nch, out + ((size_t)r * n_heads + (size_t)kvh * G) * HD, cm, cl, invl);
+        attn_combine_group<HD, G, true>(grp + (size_t)c0 * G * (HD + 2), nch,
+                                        out + ((size_t)r * n_heads + (size_t)kvh * G) * HD, cm, cl, invl);
         if (t == 0) __hip_atomic_store(counters + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
@@ -535,7 +543,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_partial_kernel(
 template <int HD, int G>
 __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(const float* __restrict__ part,
                                                                    const int32_t* __restrict__ pos, PagedKv kv,
-                                                                   int n_kv_heads, int nch_max,
+                                                                   int n_kv_heads, int nch_max, int window,
                                                                    float* __restrict__ out)
 {
     __shared__ float cm[G][kAttnMaxChunks];  // chunk maxima, then the weights e^(m_c - M)
@@ -544,9 +552,10 @@ __global__ __launch_bounds__(kAttnThreads) void attn_combine_kernel(const float*
     const int n_heads = G * n_kv_heads;
     const int r = blockIdx.x / n_kv_heads, kvh = blockIdx.x % n_kv_heads;
     const int seq = min(pos[r] + 1, kv.max_blocks * kv.tpb);
-    const int nch = seq > 0 ? (seq + kAttnChunk - 1) / kAttnChunk : 0;
-    if (nch == 0) return;
-    const float* p = part + ((size_t)r * n_kv_heads + kvh) * nch_max * (size_t)G * (HD + 2);
+    if (seq <= 0) return;
+    const int c0 = window_start(seq, window) / kAttnChunk;  // the first chunk the window reaches
+    const int nch = (seq + kAttnChunk - 1) / kAttnChunk - c0;
+    const float* p = part + (((size_t)r * n_kv_heads + kvh) * nch_max + c0) * (size_t)G * (HD + 2);
     attn_combine_group<HD, G, false>(p, nch, out + ((size_t)r * n_heads + (size_t)kvh * G) * HD, cm, cl, invl);
 }
 
@@ -573,7 +582,7 @@ template <int HD, int S>
 __global__ __launch_bounds__(kAttnBlockThreads) void attn_head_kernel(
     const float* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
     const int32_t* __restrict__ pos, PagedKv kv, int layer, int n_heads, int group, float scale, float soft_cap,
-    float* __restrict__ out)
+    int window, float* __restrict__ out)
 {
     constexpr int NW = kAttnBlockWaves, CAP = S * kAttnBlockSub;
     constexpr int KD = HD / 4;  // Q.K dims per lane
@@ -594,9 +603,10 @@ __global__ __launch_bounds__(kAttnBlockThreads) void attn_head_kernel(
     const uint32_t blk = kv.bt[(size_t)r * kv.max_blocks + min(blk_i, kv.max_blocks - 1)];
     const int seq = min(p_r + 1, kv.max_blocks * kv.tpb);  // the launcher keeps max_blocks * tpb <= CAP
     if (seq <= 0) return;  // the same for the whole block
+    const int s0 = window_start(seq, window);
     if (t < HD) qs[t] = qv;
     if (t < CAP)
-        bases[t] = (t < seq && blk_i < kv.max_blocks && blk < (uint32_t)kv.total_blocks)
+        bases[t] = (t >= s0 && t < seq && blk_i < kv.max_blocks && blk < (uint32_t)kv.total_blocks)
                        ? ((long long)blk * kv.n_layers + layer) * (long long)kv.tpb * kv.kvd +
                              (long long)(t % kv.tpb) * kv.kvd
                        : -1;
@@ -642,7 +652,8 @@ __global__ __launch_bounds__(kAttnBlockThreads) void attn_head_kernel(
 #pragma unroll
             for (int e = 0; e < 8; ++e) dot = dot + qs[kq * KD + j * 8 + e] * (float)kh[e];
         }
-        const bool valid = s * kAttnBlockSub + wave * 16 + (lane >> 2) < seq;
+        const int pp = s * kAttnBlockSub + wave * 16 + (lane >> 2);
+        const bool valid = pp >= s0 && pp < seq;
         dot = dot + lane_xor<1>(dot, 64);
         dot = dot + lane_xor<2>(dot, 64);
         float sg = dot * scale;
@@ -663,7 +674,8 @@ __global__ __launch_bounds__(kAttnBlockThreads) void attn_head_kernel(
     float l = 0.0f;
 #pragma unroll
     for (int s = 0; s < S; ++s) {
-        const bool valid = s * kAttnBlockSub + wave * 16 + (lane >> 2) < seq;
+        const int pp = s * kAttnBlockSub + wave * 16 + (lane >> 2);
+        const bool valid = pp >= s0 && pp < seq;
         const float e = valid ? expf(sc[s] - m) : 0.0f;
         if (kq == 0) ps[s * kAttnBlockSub + wave * 16 + (lane >> 2)] = e;
         l = l + e;
@@ -1808,7 +1820,7 @@ hipError_t launch_attention_gqa_f16kv(const float* q, const uint16_t* kcache, co
                                       const uint32_t* block_tables, int max_blocks, int total_blocks,
                                       const int32_t* pos, int rows, int n_heads, int n_kv_heads, int head_dim,
                                       int n_layers, int tokens_per_block, int layer, float attn_scale,
-                                      float soft_cap, float* out, float* workspace, hipStream_t st)
+                                      float soft_cap, float* out, float* workspace, hipStream_t st, int window)
 {
     const PagedKv kv{block_tables, max_blocks, total_blocks, n_layers, tokens_per_block, n_kv_heads * head_dim};
     const int nch = (max_blocks * tokens_per_block + kAttnChunk - 1) / kAttnChunk;
@@ -1829,23 +1841,23 @@ hipError_t launch_attention_gqa_f16kv(const float* q, const uint16_t* kcache, co
         // caches of up to 512 positions: the whole sequence in one block per query head
         if (cap <= kAttnBlockSub) {
             hipLaunchKernelGGL((attn_head_kernel<HD, 1>), hgrid, dim3(kAttnBlockThreads), 0, st, q, kcache, vcache,
-                               pos, kv, layer, n_heads, GG, scale, soft_cap, out);
+                               pos, kv, layer, n_heads, GG, scale, soft_cap, window, out);
             return;
         }
         if (cap <= 2 * kAttnBlockSub) {
             hipLaunchKernelGGL((attn_head_kernel<HD, 2>), hgrid, dim3(kAttnBlockThreads), 0, st, q, kcache, vcache,
-                               pos, kv, layer, n_heads, GG, scale, soft_cap, out);
+                               pos, kv, layer, n_heads, GG, scale, soft_cap, window, out);
             return;
         }
         if (one_launch) {
             hipLaunchKernelGGL((attn_partial_kernel<HD, GG, true>), pgrid, dim3(kAttnThreads), 0, st, q, kcache,
-                               vcache, pos, kv, layer, n_kv_heads, scale, soft_cap, part, nch, counters, out);
+                               vcache, pos, kv, layer, n_kv_heads, scale, soft_cap, window, part, nch, counters, out);
             return;
         }
         hipLaunchKernelGGL((attn_partial_kernel<HD, GG>), pgrid, dim3(kAttnThreads), 0, st, q, kcache, vcache, pos, kv,
-                           layer, n_kv_heads, scale, soft_cap, part, nch, nullptr, nullptr);
+                           layer, n_kv_heads, scale, soft_cap, window, part, nch, nullptr, nullptr);
         hipLaunchKernelGGL((attn_combine_kernel<HD, GG>), cgrid, dim3(kAttnThreads), 0, st, part, pos, kv,
-                           n_kv_heads, nch, out);
+                           n_kv_heads, nch, window, out);
     };
     auto by_g = [&](auto hd) {
         switch (G) {

@@ -143,7 +143,8 @@ hipError_t launch_attention_gqa_f16kv(const float* q, const uint16_t* kcache, co
                                       const uint32_t* block_tables, int max_blocks, int total_blocks,
                                       const int32_t* pos, int rows, int n_heads, int n_kv_heads, int head_dim,
                                       int n_layers, int tokens_per_block, int layer, float attn_scale,
-                                      float soft_cap, float* out, float* workspace, hipStream_t st);
+                                      float soft_cap, float* out, float* workspace, hipStream_t st,
+                                      int window = 0);  // window > 0: each row attends to its last `window` positions
 // First maximum per row (non-finite -> -inf): chunk blocks of 4096 elements in one launch; rows past
 // one chunk need scratch of argmax_scratch_bytes whose first argmax_counter_bytes (the per-row
 // counters) are zero before the first call and are left at zero by every call.

@@ -505,10 +505,20 @@ class HipOps:
 
     def encode_attention(self, q, kcache, vcache, block_tables, positions_i32, out, n_heads: int, n_kv_heads: int,
                          head_dim: int, total_blocks: int, n_layers: int, tokens_per_block: int, layer: int,
-                         attn_scale: float | None = None, soft_cap: float | None = None, stream=None) -> None:
+                         attn_scale: float | None = None, soft_cap: float | None = None, stream=None,
+                         window: int | None = None) -> None:
         """attention_single_token_gqa_f32 (kvcache.rs:710-789) per row; attn_scale
-        None = 1/sqrt(head_dim), soft_cap None = no cap (the reference's Options)."""
+        None = 1/sqrt(head_dim), soft_cap None = no cap (the reference's Options).
+        window: a Gemma sliding layer's window (gemma.rs:747-751), each row then
+        attends to its last `window` positions only; 0 = every position."""
         rows = positions_i32.numel()
+        if window is not None:
+            check(self._lib.cellm_hip_attention_gqa_f16kv_window(
+                self._h, _dev_ptr(q), _dev_ptr(kcache), _dev_ptr(vcache), _dev_ptr(block_tables),
+                block_tables.shape[-1], total_blocks, _dev_ptr(positions_i32), rows, n_heads, n_kv_heads, head_dim,
+                n_layers, tokens_per_block, layer, 0.0 if attn_scale is None else attn_scale,
+                0.0 if soft_cap is None else soft_cap, window, _dev_ptr(out), _stream_ptr(stream)))
+            return
         check(self._lib.cellm_hip_attention_gqa_f16kv(self._h, _dev_ptr(q), _dev_ptr(kcache), _dev_ptr(vcache),
                                                       _dev_ptr(block_tables), block_tables.shape[-1], total_blocks,
                                                       _dev_ptr(positions_i32), rows, n_heads, n_kv_heads, head_dim,

@@ -488,6 +488,20 @@ int32_t cellm_hip_attention_gqa_f16kv(cellm_hip_ctx_t* ctx, const float* q, cons
                                       int64_t n_kv_heads, int64_t head_dim, int64_t n_layers, int64_t tokens_per_block,
                                       int64_t layer, float attn_scale, float soft_cap, float* out, void* stream);
 
+/* Sliding-window attention of Gemma-3/4 sliding layers (gemma.rs:747-780:
+ * the gather starts at seq.saturating_sub(sliding_window), seq = the row's
+ * position + 1; the pattern of gemma.rs:570-585 picks the layers): as
+ * cellm_hip_attention_gqa_f16kv, but each row attends only to its last
+ * `window` positions, max(0, positions[r] + 1 - window) .. positions[r].
+ * window 0 attends to every position (the full-attention layers); window < 0
+ * is CELLM_HIP_ERR_INVALID_ARG.  Same limits and workspace. */
+int32_t cellm_hip_attention_gqa_f16kv_window(cellm_hip_ctx_t* ctx, const float* q, const uint16_t* kcache,
+                                             const uint16_t* vcache, const uint32_t* block_tables, int64_t max_blocks,
+                                             int64_t total_blocks, const int32_t* positions, int64_t rows,
+                                             int64_t n_heads, int64_t n_kv_heads, int64_t head_dim, int64_t n_layers,
+                                             int64_t tokens_per_block, int64_t layer, float attn_scale, float soft_cap,
+                                             int64_t window, float* out, void* stream);
+
 /* cellm_hip_attention_gqa_f16kv without any allocation, for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc).  No counterpart in the reference.

@@ -233,6 +233,79 @@ def test_attention_per_head_page_sizes(ops, tpb, blocks, pos):
         assert rel_err(got[r], ref) <= 1e-5, (r, rel_err(got[r], ref))
 
 
+@pytest.mark.parametrize("nh,nkv,hd,blocks,window,pos", [
+    (15, 5, 64, 32, 100, (511, 99, 100, 0)),        # per-head kernel, one sub-chunk group: window edges
+    (14, 2, 64, 64, 512, (1023, 600, 511, 513)),    # per-head kernel over 1024 positions, Gemma-3's window
+    (8, 2, 128, 80, 512, (1279, 700, 512, 5)),      # chunked one-launch form: window starts inside a chunk
+    (8, 4, 64, 80, 64, (1279, 1215, 64, 63)),       # chunked: window start on a chunk edge
+    (15, 5, 64, 32, 1, (511, 37, 1, 0)),            # window 1, per-head kernel
+    (8, 2, 64, 80, 1, (1279, 640, 63, 64)),         # window 1, chunked form
+])
+def test_attention_sliding_window(ops, nh, nkv, hd, blocks, window, pos):
+    """Sliding-window layers (gemma.rs:747-780): each row attends to positions
+    max(0, pos + 1 - window) .. pos, the reference's gather bases from
+    seq.saturating_sub(window).  Every row against the oracle over exactly
+    those bases; at window 1 the softmax has one term, so every query head's
+    output is the current position's V of its kv head (the f16 values, exactly);
+    window 0 through the same entry equals the full-attention entry bit for bit."""
+    L, tpb, rows, layer = 2, 16, 4, 1
+    kvd = nkv * hd
+    total, k, v, bt = paged_setup(L, tpb, nkv, hd, rows, blocks, 0xD0000600 + blocks + window)
+    pos = np.array(pos, np.int32)
+    q = np.stack([oracle.gen_normal((nh * hd,), 0xD0000610 + r, 0.0, 1.0) for r in range(rows)]).astype(np.float32)
+    args = (dev(q), dev(k), dev(v), dev(bt), dev(pos))
+    out = torch.empty((rows, nh * hd), dtype=torch.float32, device="cuda")
+    ops.encode_attention(*args, out, nh, nkv, hd, total, L, tpb, layer, window=window)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    for r in range(rows):
+        seq = int(pos[r]) + 1
+        bases = np.array([base_of(bt[r], t, layer, L, tpb, kvd) for t in range(max(0, seq - window), seq)], np.uint64)
+        ref = oracle.attention_gqa_f16kv(k, v, bases, q[r], nh, nkv, hd)
+        assert rel_err(got[r], ref) <= 1e-5, (r, rel_err(got[r], ref))
+        if window == 1:
+            b = base_of(bt[r], seq - 1, layer, L, tpb, kvd)
+            vrow = v[b:b + kvd].view(np.float16).astype(np.float32).reshape(nkv, hd)
+            np.testing.assert_array_equal(got[r].reshape(nh, hd), vrow[np.arange(nh) // (nh // nkv)])
+    full = torch.empty_like(out)
+    ops.encode_attention(*args, full, nh, nkv, hd, total, L, tpb, layer)
+    ops.encode_attention(*args, out, nh, nkv, hd, total, L, tpb, layer, window=0)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy().view(np.uint32), full.cpu().numpy().view(np.uint32))
+    from cellm_amd._lib import CellmHipError
+    with pytest.raises(CellmHipError, match="bad window"):
+        ops.encode_attention(*args, out, nh, nkv, hd, total, L, tpb, layer, window=-1)
+
+
+def test_attention_sliding_window_two_launch_form(ops):
+    """The two-launch form (more than 16384 (row, kv head) groups) with a window
+    of 10: rows whose window starts in the first chunk and rows whose window
+    starts in the second, against the oracle on sampled rows."""
+    nh, nkv, hd, L, tpb, layer, bpr, window = 64, 64, 64, 1, 16, 0, 5, 10
+    kvd = nkv * hd
+    rows = 257
+    total = rows * bpr + 3
+    rng = np.random.default_rng(0xD0000700)
+    k = rng.standard_normal(total * L * tpb * kvd, dtype=np.float32).astype(np.float16).view(np.uint16)
+    v = rng.standard_normal(total * L * tpb * kvd, dtype=np.float32).astype(np.float16).view(np.uint16)
+    bt = np.array([[b * rows + r + 3 for b in range(bpr)] + [3] * (33 - bpr) for r in range(rows)], np.uint32)
+    pos = (64 + (np.arange(rows) * 7) % 16).astype(np.int32)
+    q = rng.standard_normal((rows, nh * hd), dtype=np.float32)
+    out = torch.empty((rows, nh * hd), dtype=torch.float32, device="cuda")
+    ops.encode_attention(dev(q), dev(k), dev(v), dev(bt), dev(pos), out, nh, nkv, hd, total, L, tpb, layer,
+                         window=window)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    starts = set()
+    for r in (0, 1, 2, 9, 100, 200, rows - 1):
+        seq = int(pos[r]) + 1
+        starts.add((seq - window) // 64)
+        bases = np.array([base_of(bt[r], t, layer, L, tpb, kvd) for t in range(seq - window, seq)], np.uint64)
+        ref = oracle.attention_gqa_f16kv(k, v, bases, q[r], nh, nkv, hd)
+        assert rel_err(got[r], ref) <= 1e-5, r
+    assert starts == {0, 1}
+
+
 def test_attention_one_launch_and_two_launch_forms(ops):
     """Up to 16384 (row, kv head) groups run in one launch (the group's last
     chunk block combines through coherent stores/loads and a self-resetting
